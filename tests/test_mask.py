@@ -1,0 +1,232 @@
+"""Host geometry: the product's build_mask against the reference's own outputs,
+the closed forms, and a loop-based rebuild from the definitions.
+
+Ports tests/test_smat.py:43-173 (structure, block layout, planted identity,
+counting) and adds the bit-exact index checks the reference's tests do not
+make (golden C_indices from the reference's build_mask)."""
+import hashlib
+
+import numpy as np
+import pytest
+
+from oracle import mask_ref
+from smat_attention_amd.mask import (build_mask, d_max_geometric, estimate_cost,
+                                     incidence_audit, materialise, next_prime,
+                                     planted_hyperplane_normals, shatter_witness)
+
+
+def _sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+# --------------------------------------------------------------------------
+# bit-exact against the reference's build_mask
+# --------------------------------------------------------------------------
+
+def test_golden_indices_bit_exact(golden, golden_arrays):
+    for c in golden:
+        s = build_mask(c["T"], c["d"], chunk=c["chunk"], n_P=c["n_P"])
+        assert s.kind == c["kind"], c["key"]
+        for k in ("n", "T_R", "q", "dim", "N0", "n_dirs", "B", "n_planted", "k",
+                  "uniform_deg", "nnz", "I_tok"):
+            got = s.I_prof if k == "nnz" else getattr(s, k)
+            assert got == c[k], (c["key"], k, got, c[k])
+        assert [int(x) for x in s.planted_cols] == c["planted_cols"], c["key"]
+        assert _sha(s.C_indices.astype(np.int32)) == c["C_indices_sha256"], c["key"]
+        assert _sha(s.C_indptr.astype(np.int64)) == c["C_indptr_sha256"], c["key"]
+        if c["key"] in golden_arrays:
+            np.testing.assert_array_equal(s.C_indices, golden_arrays[c["key"]])
+
+
+def test_published_rows_scalars(ref_tables):
+    """Every (T, d) row of the published sweeps and the counting table."""
+    for table in ("prefill_h200", "prefill_a100", "theory_counting"):
+        for row in ref_tables[table]:
+            try:
+                s = build_mask(row["T"], row["d"], chunk=row["chunk"], _probe=True)
+            except ValueError:
+                # the probe refuses T_R < 2B (those rows were built with a
+                # warning); check the oracle's closed forms instead
+                n = row["chunk"] * (row["T"] // (2 * row["chunk"]))
+                q = mask_ref.field_size(n, row["d"])
+                dim = row["d"] - 1
+                assert q == row["q"] and q ** dim == row["N0"], row
+                assert row["B"] == q * (q ** dim - 1) // (q - 1), row
+                assert row["deg"] == q ** (dim - 1) and row["I_prof"] == row["B"] * row["deg"]
+                continue
+            assert s.q == row["q"] and s.B == row["B"] and s.N0 == row["N0"], row
+            assert s.uniform_deg == row["deg"], row
+            assert s.B * s.uniform_deg == row["I_prof"], row
+            if "n" in row:
+                assert s.n == row["n"] and s.T_R == row["T_R"], row
+            # I_tok = sum_j nu(prof(j)) = n_X * D for the full family (closed form)
+            D = (s.q ** s.dim - 1) // (s.q - 1) if s.d >= 2 else 1
+            assert (s.n - s.n_P) * D == row["I_tok"], row
+
+
+def test_theory_structure_checksums(ref_tables):
+    """nnz and density of the materialised mask (results/theory_structure.csv)."""
+    for row in ref_tables["theory_structure"]:
+        s = build_mask(row["T"], row["d"], chunk=row["chunk"])
+        M = materialise(s, np.int8)
+        assert (s.n, s.T_R, s.q, s.B, s.N0) == (row["n"], row["T_R"], row["q"],
+                                                row["B"], row["N0"]), row
+        assert int(M.sum(dtype=np.int64)) == row["nnz"], row
+        assert abs(M.sum(dtype=np.int64) / row["T"] ** 2 - row["density"]) < 1e-12
+
+
+# --------------------------------------------------------------------------
+# against the loop-based rebuild from the definitions
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T,d,chunk,n_P", [
+    (512, 2, 64, 0), (1024, 3, 64, 0), (2048, 3, 64, 16), (2048, 4, 64, 0),
+    (1024, 2, 128, 0), (4096, 3, 128, 0), (8192, 4, 128, 0)])
+def test_incidence_matches_definition(T, d, chunk, n_P):
+    s = build_mask(T, d, chunk=chunk, n_P=n_P)
+    geo = mask_ref.geometry(T, d, chunk=chunk, n_P=n_P)
+    assert (s.q, s.N0, s.B, s.uniform_deg) == (geo["q"], geo["N0"], geo["B"], geo["deg"])
+    rows = s.C_indices.reshape(s.B, s.uniform_deg)
+    assert [list(map(int, r)) for r in rows] == geo["rows"]
+    assert list(map(int, s.planted_cols)) == geo["planted_cols"]
+
+
+@pytest.mark.parametrize("T,d,chunk,n_P,endpoint", [
+    (256, 1, 64, 0, False), (512, 2, 64, 0, False), (512, 3, 64, 0, False),
+    (640, 3, 64, 16, False), (256, 8, 8, 0, True), (300, 8, 8, 0, True)])
+def test_dense_mask_matches_definition(T, d, chunk, n_P, endpoint):
+    s = build_mask(T, d, chunk=chunk, n_P=n_P)
+    geo = (mask_ref.endpoint_geometry(T, d) if endpoint
+           else mask_ref.geometry(T, d, chunk=chunk, n_P=n_P))
+    if endpoint:
+        assert s.kind == "endpoint"
+        assert [list(map(int, s.C_indices[s.C_indptr[h]:s.C_indptr[h + 1]]))
+                for h in range(s.B)] == geo["rows"]
+    M = materialise(s, np.int8)
+    ref = np.array(mask_ref.dense_mask(T, geo, endpoint=endpoint), dtype=np.int8)
+    np.testing.assert_array_equal(M, ref)
+
+
+# --------------------------------------------------------------------------
+# structure (test_smat.py:43-89)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T,d", [(256, 1), (512, 2), (1024, 2), (1024, 3),
+                                 (2048, 3), (2048, 4)])
+def test_structure(T, d):
+    s = build_mask(T, d, chunk=64)
+    M = materialise(s)
+    L = np.tril(np.ones((T, T)))
+    assert np.all(np.triu(M, 1) == 0)
+    assert np.all(np.diag(M) == 1)
+    assert np.all((M == 0) | (M == 1))
+    assert np.all(M <= L)
+    floor = (s.n * (s.n + 1) + s.T_R * (s.T_R + 1)) / 2
+    assert M.sum() >= floor
+
+
+@pytest.mark.parametrize("T", [256, 512, 1000])
+def test_d1_is_causal_triangle(T):
+    s = build_mask(T, 1, chunk=64)
+    np.testing.assert_array_equal(materialise(s), np.tril(np.ones((T, T))))
+
+
+def test_landmark_rows_see_their_prefix():
+    s = build_mask(1024, 3, chunk=64)
+    M = materialise(s)
+    np.testing.assert_array_equal(M[:s.n, :s.n].sum(1), np.arange(1, s.n + 1))
+
+
+def test_range_checks():
+    with pytest.raises(ValueError):
+        build_mask(1024, 11, chunk=64)
+    with pytest.raises(ValueError):
+        build_mask(4, 1)
+    assert build_mask(1024, 10, chunk=64).kind == "endpoint"
+    for T in (4096, 65536):
+        assert d_max_geometric(T, chunk=128) < T.bit_length() - 1
+    with pytest.raises(MemoryError):
+        build_mask(65536, 4, chunk=128, max_I_prof=1000)
+
+
+def test_q_uses_double_precision_pow():
+    # 32768 ** (1/3) = 31.999999999999996 in IEEE double; ceil gives 32
+    assert float(32768) ** (1.0 / 3) < 32
+    s = build_mask(65536, 3, chunk=128)          # n = 32768
+    assert s.q == 37 and next_prime(32) == 37
+    # n = 29^3: a prime cube root must give q = 29 itself
+    assert build_mask(2 * 24389, 3, chunk=1, _probe=True).q == 29
+
+
+# --------------------------------------------------------------------------
+# block layout, planted identity, counting (test_smat.py:92-173)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T,d,nP", [(1024, 2, 0), (2048, 3, 0), (2048, 4, 0), (2048, 3, 16)])
+def test_block_layout(T, d, nP):
+    s = build_mask(T, d, chunk=64, n_P=nP)
+    M = materialise(s)
+    n, T_R = s.n, s.T_R
+    np.testing.assert_array_equal(M[:n, :n], np.tril(np.ones((n, n))))
+    assert np.all(M[:n, n:] == 0)
+    np.testing.assert_array_equal(M[n:, n:], np.tril(np.ones((T_R, T_R))))
+    if nP:
+        assert np.all(M[n:, :nP] == 1)
+    C = s.dense_C()
+    prof = s.prof_of_column()
+    R = np.zeros((T_R, s.B))
+    R[np.arange(T_R), np.arange(T_R) % s.B] = 1
+    S = np.zeros((s.n_X, s.N0))
+    S[np.arange(s.n_X), prof] = 1
+    np.testing.assert_array_equal(M[n:, s.n_P:n], R @ C @ S.T)
+
+
+@pytest.mark.parametrize("T,d", [(1024, 2), (2048, 3), (4096, 4), (16384, 5)])
+def test_planted(T, d):
+    s = build_mask(T, d, chunk=64)
+    a = incidence_audit(s)
+    assert a["planted_identity"] and a["B_ge_2_pow_d_minus_1"]
+    hs = planted_hyperplane_normals(d)
+    assert all(np.any(a_ != 0) for a_, _ in hs)
+    assert len({(tuple(a_), b) for a_, b in hs}) == len(hs)
+    cols, ok, _ = shatter_witness(s)
+    assert ok and len(cols) == d
+
+
+@pytest.mark.parametrize("T,d", [(4096, 2), (16384, 2), (4096, 3), (16384, 3),
+                                 (65536, 3), (16384, 4), (65536, 4)])
+def test_incidence_audit(T, d):
+    s = build_mask(T, d, chunk=128)
+    a = incidence_audit(s)
+    assert a["exact"] and a["nu_is_D"] and a["full_hyperplane_family"]
+    # every member satisfies its hyperplane equation: rebuild <a_e, x> = b from
+    # the planted normals for the first 2^(d-1) rows
+    q, dim = s.q, s.dim
+    rows = s.C_indices.reshape(s.B, -1)
+    for R, (avec, b) in enumerate(planted_hyperplane_normals(d)):
+        pts = np.array([mask_ref.point(int(x), q, dim) for x in rows[R]])
+        assert np.all((pts @ avec) % q == b)
+
+
+@pytest.mark.parametrize("d", [2, 3, 4, 5])
+def test_closed_forms(d):
+    for T in [2 ** k for k in range(14, 20)]:
+        s = build_mask(T, d, chunk=128, _probe=True)
+        q = s.q
+        assert s.B * s.uniform_deg == q ** (d - 1) * (q ** (d - 1) - 1) // (q - 1)
+        assert s.B == q * (q ** (d - 1) - 1) // (q - 1)
+        assert s.N0 == q ** (d - 1)
+
+
+def test_endpoint_walsh_rows():
+    s = build_mask(1024, 10, chunk=64)
+    a = np.arange(s.N0)
+    Cw = (np.bitwise_count(a[:, None] & a[None, :]) % 2) == 0
+    np.testing.assert_array_equal(s.dense_C().astype(bool), Cw)
+    assert s.uniform_deg == 0 and incidence_audit(s)["exact"]
+
+
+def test_estimate_cost():
+    e = estimate_cost(131072, 3, 128, 128)
+    assert e["feasible"] and e["I_prof"] == 70602 and e["B"] == 1722
+    assert not estimate_cost(64, 5, 8, 8)["feasible"]
