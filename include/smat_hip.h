@@ -1,0 +1,167 @@
+/*
+ * smat_hip.h -- C ABI of libsmat_hip.so, the MI355X (gfx950) kernels of the
+ * SMat chunkwise schedule.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers; the library never allocates or frees.
+ *     Entry points that need scratch memory take a caller-provided workspace
+ *     whose size a matching *_workspace_bytes() query returns.
+ *   - A matrix argument is (pointer, batch stride, row stride) in ELEMENTS;
+ *     its columns are contiguous.  Strides are int64_t.
+ *   - `dtype` names the element type of the feature inputs (Phi, Psi, Vb):
+ *     SMAT_BF16, SMAT_F16 or SMAT_F32.  Pooled tables, chunk states and
+ *     outputs are fp32 (the reference accumulates and returns fp32 for these
+ *     inputs, src/smat/attention.py:124-127).
+ *   - `stream` is a hipStream_t (NULL: the null stream).  Work is enqueued
+ *     only; nothing synchronises the host.
+ *   - Return value: SMAT_OK, or a negative code; smat_last_error() then
+ *     returns a message naming the entry point and the offending argument.
+ *
+ * Sizes supported by the MFMA kernels: r <= 128 (feature rank) and
+ * p <= 144 (value width + 1); chunk C <= 256.  Larger shapes return
+ * SMAT_EUNSUPPORTED rather than running.
+ */
+#ifndef SMAT_HIP_H
+#define SMAT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMAT_OK 0
+#define SMAT_EINVAL (-1)
+#define SMAT_EUNSUPPORTED (-2)
+#define SMAT_ELAUNCH (-3)
+
+#define SMAT_BF16 0
+#define SMAT_F16 1
+#define SMAT_F32 2
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* smat_last_error(void);
+
+/* Library version and the target it was built for, e.g. "0.1 gfx950". */
+const char* smat_version(void);
+
+/*
+ * Fused within-chunk pass, one output block per chunk:
+ *   out_b = Phi_b Sin_b + (tril(Phi_b Psi_b^T)) Vb_b
+ * Phi_b, Psi_b: (C, r) of dtype; Vb_b: (C, p) of dtype; Sin_b: (r, p) fp32;
+ * out_b: (C, p) fp32, for b in [0, nbc).  The score tile is rounded to dtype
+ * before the product with Vb, as the reference does.
+ * Replaces chunk_local, src/smat/kernels/triton_fwd.py:118-152 (kernel
+ * :48-115), called at src/smat/attention.py:183,185.
+ */
+int smat_chunk_local(int dtype, const void* phi, const void* psi, const void* vb,
+                     const float* sin, float* out, int64_t nbc, int C, int r, int p,
+                     int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
+                     int64_t v_sb, int64_t v_st, int64_t s_sb, int64_t s_sr,
+                     int64_t o_sb, int64_t o_st, void* stream);
+
+/*
+ * Chunk summaries D_c = Psi_c^T Vb_c (fp32, (nb, nc, r, p) contiguous) for the
+ * chunks of width C of a (nb, T, .) sequence; a ragged last chunk is
+ * zero-padded.  Replaces the torch GEMM of src/smat/attention.py:162.
+ */
+int smat_chunk_states(int dtype, const void* psi, const void* vb, float* D,
+                      int nb, int T, int C, int r, int p,
+                      int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
+                      void* stream);
+
+/*
+ * Segmented shifted exclusive scan over chunks, one reset at chunk nc0:
+ *   Sin[c] = sum_{c' in seg(c), c' < c} D[c']   (seg: [0,nc0) and [nc0,nc))
+ * D, Sin: (nb, nc, rp) fp32 contiguous; Sin may not alias D.  A shifted scan,
+ * never cumsum-minus-self (src/smat/attention.py:163-179).
+ */
+int smat_segment_scan(const float* D, float* Sin, int nb, int nc, int nc0, int64_t rp,
+                      void* stream);
+
+/*
+ * Profile pooling  F_x = sum_{j in [n_P, n), (j - n_P) mod N0 = x} Psi_j^T Vb_j
+ * (fp32, F: (nb, N0, r, p) contiguous).  If F_glob is not NULL and n_P > 0 it
+ * also receives the global-channel term sum_{j < n_P} Psi_j^T Vb_j, (nb, r, p).
+ * Replaces pool, src/smat/kernels/triton_fwd.py:281-311 (kernel :226-267),
+ * and the rank-one term of src/smat/attention.py:422-425.  Few, long
+ * progressions (small N0, e.g. d = 1 where N0 = 1) are split over several
+ * workgroups and summed in a fixed order; that needs
+ * smat_pool_workspace_bytes(...) bytes of workspace (0: none needed).
+ */
+int64_t smat_pool_workspace_bytes(int nb, int n_P, int n, int N0, int r, int p);
+int smat_pool(int dtype, const void* psi, const void* vb, float* F, float* F_glob,
+              int nb, int n_P, int n, int N0, int r, int p,
+              int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
+              void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Incidence  U_h = sum_{x in H_h} F_x (+ F_glob when not NULL), fp32.
+ * F: (nb, N0, rp) contiguous; U: (nb, B, rp) contiguous.  Row h's points are
+ * idx[h*deg .. h*deg+deg) when indptr is NULL (uniform degree), otherwise
+ * idx[indptr[h] .. indptr[h+1]).  idx_is_64: 1 if idx holds int64, 0 int32.
+ * Replaces incidence, src/smat/kernels/triton_fwd.py:191-216 (kernel
+ * :162-188), and the ragged CSR loop of src/smat/attention.py:268-274.
+ */
+int smat_incidence(const float* F, const float* F_glob, const void* idx, int idx_is_64,
+                   const int64_t* indptr, int deg, float* U, int nb, int N0, int B,
+                   int64_t rp, void* stream);
+
+/*
+ * Type-major query  Y[i] = Phi_rec[i] U_{i mod B}, i in [0, T_R), fp32 out
+ * (nb, T_R, p) with row stride y_st.  Phi_rec has dtype; U: (nb, B, r, p).
+ * Replaces query_by_type, src/smat/attention.py:310-330.
+ */
+int smat_query(int dtype, const void* phi_rec, const float* U, float* Y,
+               int nb, int T_R, int B, int r, int p,
+               int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st, void* stream);
+
+/*
+ * Normalise  out[t, c] = (H[t, c] + Y[t-n, c]) / (H[t, p-1] + Y[t-n, p-1]) * g[t]
+ * for c < p-1; the Y term only for t >= n (Y may be NULL), g optional (NULL).
+ * H: (nb, T, p) fp32; out: (nb, T, p-1) fp32; g: (nb, T) fp32.
+ * Replaces the cat + divide + gate of src/smat/attention.py:446-453.
+ */
+int smat_normalise(const float* H, const float* Y, const float* g, float* out,
+                   int nb, int T, int n, int p,
+                   int64_t h_sb, int64_t h_st, int64_t y_sb, int64_t y_st,
+                   int64_t o_sb, int64_t o_st, int64_t g_sb, void* stream);
+
+/*
+ * Whole forward schedule of smat_attention (src/smat/attention.py:391-455) for
+ * a geometric mask: pool -> incidence (+ global channel) -> query ->
+ * chunk states -> segmented scan -> chunk-local pass -> normalise.
+ * idx/indptr/deg describe C as for smat_incidence; B, N0, n, n_P from the spec.
+ * out: (nb, T, p-1) fp32 with row stride o_st; g optional.  H_out, if not
+ * NULL, receives the unnormalised H (nb, T, p) fp32 contiguous.
+ * workspace: smat_forward_workspace_bytes(...) bytes, 256-byte aligned.
+ */
+int64_t smat_forward_workspace_bytes(int nb, int T, int n, int N0, int B, int n_P,
+                                     int C, int r, int p);
+int smat_forward(int dtype, const void* phi, const void* psi, const void* vb,
+                 const void* idx, int idx_is_64, const int64_t* indptr, int deg,
+                 float* out, float* H_out, const float* g,
+                 int nb, int T, int n, int n_P, int N0, int B, int C, int r, int p,
+                 int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
+                 int64_t v_sb, int64_t v_st, int64_t o_sb, int64_t o_st, int64_t g_sb,
+                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * One cached-decode step for nb sequences (SmatDecoder.step,
+ * src/smat/attention.py:522-528):
+ *   S_out = S_in + Psi_t Vb_t^T;  o = Phi_t (S_out + U[type]);  out = o[:p-1] / o[p-1]
+ * S_in, S_out: (nb, r, p) fp32, distinct buffers (the caller swaps them
+ * between steps); U: (nb, B, r, p) fp32; the row type is step mod B.
+ * Phi_t, Psi_t: (nb, r) and Vb_t: (nb, p) of dtype with batch strides;
+ * out: (nb, p-1) fp32.  o_full, if not NULL, receives o (nb, p) fp32.
+ */
+int smat_decode_step(int dtype, const void* phi_t, const void* psi_t, const void* vb_t,
+                     const float* S_in, float* S_out, const float* U, float* out,
+                     float* o_full, int nb, int B, int r, int p, int64_t step,
+                     int64_t q_sb, int64_t k_sb, int64_t v_sb, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SMAT_HIP_H */

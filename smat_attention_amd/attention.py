@@ -1,0 +1,409 @@
+"""SMat attention's chunkwise schedule on MI355X: the Python surface.
+
+Mirrors ``src/smat/attention.py`` (``__all__`` at attention.py:42-48), so a
+caller switches by changing the import.  Everything runs on the GPU through
+the HIP kernels of :mod:`smat_attention_amd.kernels.hip_fwd`; there is no
+torch fallback, and a call that the kernels cannot serve raises.
+
+Everything operates on kernel features ``Phi = phi(Q)``, ``Psi = h phi(K)``,
+``Vb = [V, 1]`` (``p = d_v + 1`` columns), and the output is
+``H[..., :-1] / H[..., -1:]`` with
+
+    H = [[L_n, 0], [G, L_{T_R}]] Phi Psi^T Vb,      G = R C S^T,
+
+computed as two passes summed before the single division:
+
+  long range   F = S^T (Psi (x) Vb)   pool by profile      (pool)
+               U = C F                 incidence            (incidence)
+               Y = R (Phi_rec U)       type-major query     (query)
+  causal       one chunked scan over all T with a single reset at n.
+
+Reference differences, all deliberate:
+  * ``backend="torch"`` / ``"walsh"`` select torch code in the reference; here
+    they raise -- this package has one implementation, the kernels.
+  * fp64 inputs raise (the reference keeps fp64 on torch, attention.py:109-121,
+    so the kernels never see it there either).
+  * ``featurise`` returns ``Vb`` as a view with 16-byte aligned rows (same
+    values, padded row stride), the layout the kernels load fastest.
+"""
+from __future__ import annotations
+
+from contextlib import nullcontext
+from typing import Callable, Dict, Optional
+
+import numpy as np
+import torch
+
+from .kernels import hip_fwd as _hip
+from .mask import MaskSpec
+
+__all__ = [
+    "make_phi", "featurise", "to_device",
+    "segmented_causal_scan", "pool_profiles", "apply_incidence",
+    "query_by_type", "zeta_transform", "walsh_incidence",
+    "smat_attention", "dense_masked_kernel_attention", "SmatDecoder",
+    "have_triton", "have_hip",
+]
+
+_KERNEL_BACKENDS = ("auto", "hip", "triton")
+
+
+def have_hip() -> bool:
+    """True when the HIP library is built and a GPU is visible."""
+    return _hip.available()
+
+
+def have_triton() -> bool:
+    """Name kept from the reference (attention.py:54-55); means :func:`have_hip`."""
+    return have_hip()
+
+
+def _backend(name: str, who: str) -> None:
+    if name not in _KERNEL_BACKENDS:
+        raise ValueError(f"{who}: backend {name!r} is not available; this package runs "
+                         f"only its HIP kernels ({', '.join(_KERNEL_BACKENDS)})")
+
+
+def _acc(x: torch.Tensor, acc_dtype, who: str) -> torch.dtype:
+    """The kernels accumulate and return fp32 (attention.py:109-127)."""
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"{who}: inputs must be bfloat16, float16 or float32, got {x.dtype}")
+    if acc_dtype not in (None, torch.float32):
+        raise TypeError(f"{who}: the kernels accumulate in float32, got acc_dtype={acc_dtype}")
+    if not x.is_cuda:
+        raise ValueError(f"{who}: inputs must be on the GPU, got {x.device}")
+    return torch.float32
+
+
+# ---------------------------------------------------------------------------
+# feature map (attention.py:82-106)
+# ---------------------------------------------------------------------------
+
+def make_phi(d_qk: int, r: int, *, kind: str = "elu1", device="cpu",
+             dtype=torch.float32, seed: int = 0) -> Callable:
+    """A positive rank-``r`` feature map with ``W ~ randn(r, d_qk)/sqrt(d_qk)``.
+
+    ``W`` comes from a seeded CPU generator in float64 and is then cast, as in
+    attention.py:82-96, so the same seed gives the same map on any device.
+    """
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    W = (torch.randn(r, d_qk, generator=gen, dtype=torch.float64)
+         / np.sqrt(d_qk)).to(device=device, dtype=dtype)
+    if kind == "elu1":
+        return lambda x: torch.nn.functional.elu(x @ W.T) + 1.0
+    if kind == "relu":
+        return lambda x: torch.nn.functional.relu(x @ W.T) + 1e-3
+    raise ValueError(f"unknown feature map {kind!r}")
+
+
+def featurise(Q, K, V, phi, *, g=None, h=None):
+    """``(Q, K, V) -> (Phi, Psi, Vb)`` with the key gate folded into ``Psi``.
+
+    ``Vb = [V, 1]`` is returned as a view whose rows start on 16-byte
+    boundaries (row stride rounded up to 8 elements).
+    """
+    Phi = phi(Q)
+    Psi = phi(K)
+    if h is not None:
+        Psi = Psi * h.unsqueeze(-1)
+    d_v = V.shape[-1]
+    p = d_v + 1
+    pad = -(-p // 8) * 8
+    buf = torch.empty(*V.shape[:-1], pad, device=V.device, dtype=V.dtype)
+    buf[..., :d_v] = V
+    buf[..., d_v:] = 1
+    return Phi, Psi, buf[..., :p]
+
+
+# ---------------------------------------------------------------------------
+# device staging (attention.py:542-571)
+# ---------------------------------------------------------------------------
+
+def to_device(spec: MaskSpec, device, *, want_direct: bool = False) -> MaskSpec:
+    """Stage the incidence on ``device``.
+
+    Same attributes as the reference (``C_indptr_t``, ``C_indices_t`` int64,
+    ``plane_pts_t`` the ``(B, deg)`` view when the degree is uniform), plus the
+    int32 copies the kernels read.  Every index is range-checked on the host
+    here, so the kernels can trust the tables.
+    """
+    ind = np.asarray(spec.C_indices)
+    ptr_ = np.asarray(spec.C_indptr)
+    if ind.size and (ind.min() < 0 or ind.max() >= spec.N0):
+        raise ValueError("C_indices out of range [0, N0)")
+    if ptr_[0] != 0 or ptr_[-1] != ind.size or np.any(np.diff(ptr_) < 0):
+        raise ValueError("C_indptr is not a valid CSR row pointer")
+    spec.C_indptr_t = torch.from_numpy(ptr_.astype(np.int64)).to(device)
+    spec.C_indices_t = torch.from_numpy(ind.astype(np.int64)).to(device)
+    spec.C_indices_i32_t = torch.from_numpy(ind.astype(np.int32)).to(device)
+    for t in (spec.C_indices_t, spec.C_indices_i32_t):
+        t._smat_checked_N0 = spec.N0
+    if spec.uniform_deg:
+        spec.plane_pts_t = spec.C_indices_t.view(spec.B, spec.uniform_deg)
+        spec.plane_pts_t._smat_checked_N0 = spec.N0
+    else:
+        spec.plane_pts_t = None
+    if want_direct:
+        if not spec.uniform_deg:
+            raise ValueError("the direct backend needs a uniform row degree; "
+                             "the endpoint mask is ragged")
+        spec.type_cols_t = torch.from_numpy(_type_columns(spec)).to(device)
+    spec._smat_device = torch.device(device)
+    return spec
+
+
+def _type_columns(spec: MaskSpec) -> np.ndarray:
+    """``(B, kappa)`` landmark columns per row type, padded with ``n_X``.
+
+    Profile ``x`` owns the columns ``x, x + N0, ...`` of the landmark block, so
+    a row type's columns are those progressions for its ``deg`` points.
+    """
+    n_X, N0 = spec.n_X, spec.N0
+    g = -(-n_X // N0)
+    pts = spec.C_indices.reshape(spec.B, -1).astype(np.int64)
+    cols = pts[:, :, None] + np.arange(g, dtype=np.int64)[None, None, :] * N0
+    return np.where(cols < n_X, cols, n_X).reshape(spec.B, -1).astype(np.int32)
+
+
+def _staged(spec: MaskSpec, device) -> MaskSpec:
+    dev = torch.device(device)
+    have = getattr(spec, "_smat_device", None)
+    if getattr(spec, "C_indices_i32_t", None) is None or have is None or have != dev:
+        to_device(spec, dev)
+    return spec
+
+
+def _incidence_args(spec: MaskSpec):
+    """``(idx, indptr, deg)`` for the incidence kernel: the uniform ``(B, deg)``
+    table when there is one, else CSR."""
+    if spec.uniform_deg:
+        return spec.C_indices_i32_t, None, int(spec.uniform_deg)
+    return spec.C_indices_i32_t, spec.C_indptr_t, 0
+
+
+# ---------------------------------------------------------------------------
+# the stages (attention.py:134-330)
+# ---------------------------------------------------------------------------
+
+def segmented_causal_scan(Phi, Psi, Vb, n: int, chunk: int = 128,
+                          acc_dtype=None, backend: str = "auto"):
+    """``[[L_n, 0], [0, L_{T_R}]] Phi Psi^T Vb`` as one chunked scan with one reset.
+
+    Chunk summaries ``D``, then a shifted exclusive scan per segment (never
+    cumsum-minus-self, attention.py:163-179), then the fused chunk-local pass.
+    Returns fp32 ``(nb, T, p)``.
+    """
+    who = "segmented_causal_scan"
+    _backend(backend, who)
+    _acc(Phi, acc_dtype, who)
+    nb, T, r = Phi.shape
+    p = Vb.shape[-1]
+    C = min(chunk, T)
+    if n % C:
+        raise ValueError(f"segment boundary n={n} is not a multiple of chunk={C}")
+    nc = -(-T // C)
+    D = _hip.chunk_states(Psi, Vb, C)
+    Sin = _hip.segment_scan(D, n // C)
+    pad = nc * C - T
+    if pad:
+        Phi = torch.nn.functional.pad(Phi, (0, 0, 0, pad))
+        Psi = torch.nn.functional.pad(Psi, (0, 0, 0, pad))
+        Vb = torch.nn.functional.pad(Vb, (0, 0, 0, pad))
+    out = _hip.chunk_local(Phi.reshape(nb, nc, C, r), Psi.reshape(nb, nc, C, r),
+                           Vb.reshape(nb, nc, C, p), Sin)
+    return out.reshape(nb, nc * C, p)[:, :T]
+
+
+def pool_profiles(Psi, Vb, spec: MaskSpec, acc_dtype=None, backend: str = "auto"):
+    """``F_x = sum_{prof(j)=x} Psi_j Vb_j^T``: fp32 ``(nb, N0, r, p)``."""
+    who = "pool_profiles"
+    _backend(backend, who)
+    _acc(Psi, acc_dtype, who)
+    return _hip.pool(Psi, Vb, spec.n_P, spec.n, spec.N0)
+
+
+def apply_incidence(F, spec: MaskSpec, *, backend: str = "auto", gather_chunk: int = 0):
+    """``U_h = sum_{x in H_h} F_x``: fp32 ``(nb, B, r, p)``.
+
+    Uniform-degree masks use the ``(B, deg)`` table, ragged ones (the endpoint
+    mask) the CSR rows; both through the same gather-reduce kernel.
+    ``gather_chunk`` tuned the reference's torch gather and is ignored.
+    """
+    who = "apply_incidence"
+    if backend == "walsh":
+        raise ValueError(f"{who}: the Walsh butterfly is not part of this build; the "
+                         f"gather-reduce kernel applies C for every mask kind")
+    _backend(backend, who)
+    if not F.is_cuda:
+        raise ValueError(f"{who}: F must be on the GPU")
+    _staged(spec, F.device)
+    nb, N0, r, p = F.shape
+    Ff = F.contiguous().float()
+    idx, indptr, deg = _incidence_args(spec)
+    U = torch.empty(nb, spec.B, r, p, device=F.device, dtype=torch.float32)
+    _hip.call("smat_incidence", Ff.data_ptr(), None, idx.data_ptr(), 0, _hip.ptr(indptr), deg,
+              U.data_ptr(), nb, N0, spec.B, r * p, _hip.stream_of(Ff))
+    return U
+
+
+def query_by_type(Phi_rec, U, spec: MaskSpec):
+    """``Y_{R_h} = Phi_{R_h} U_h``, ``rho(i) = i mod B``: fp32 ``(nb, T_R, p)``."""
+    if U.shape[1] != spec.B:
+        raise ValueError(f"query_by_type: U has {U.shape[1]} types, spec.B = {spec.B}")
+    return _hip.query(Phi_rec, U)
+
+
+def zeta_transform(F):
+    """Subset sums over the endpoint's landmark block (attention.py:369-384).
+
+    The endpoint mask (``d = floor(log2 T)``) is not part of this build's
+    kernel set; see the package documentation.
+    """
+    raise NotImplementedError("zeta_transform: the endpoint mask's landmark block has no "
+                              "HIP kernel in this build")
+
+
+def walsh_incidence(F):
+    """The Walsh butterfly route of attention.py:288-307; not in this build --
+    :func:`apply_incidence` applies the endpoint's ragged ``C`` by gather."""
+    raise NotImplementedError("walsh_incidence: use apply_incidence (CSR gather kernel)")
+
+
+# ---------------------------------------------------------------------------
+# full forward (attention.py:391-455)
+# ---------------------------------------------------------------------------
+
+def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
+                   acc_dtype=None, timer=None, long_range: str = "pooled",
+                   scan_backend: str = "auto", incidence_backend: str = "auto",
+                   return_parts: bool = False, workspace: Optional[torch.Tensor] = None):
+    """Algorithm 1 of the reference (attention.py:391-455) on the GPU.
+
+    Long range (pool by profile, incidence, type-major query) and the causal
+    segmented scan are summed before the single division.  Returns fp32
+    ``(nb, T, d_v)``; with ``return_parts`` also ``{"U", "Y_lr", "H"}``.
+    ``timer(name)`` (a context-manager factory) brackets the phases
+    ``lr_pool``, ``lr_incidence``, ``lr_query``, ``scan`` and ``normalise``.
+    Without a timer or parts the whole schedule is one library call;
+    ``workspace`` (uint8, on the device) may be passed to reuse its scratch.
+    """
+    who = "smat_attention"
+    _backend(scan_backend, who)
+    _backend(incidence_backend, who)
+    if long_range != "pooled":
+        raise NotImplementedError(f"{who}: long_range={long_range!r}; this build implements "
+                                  f"the pooled schedule")
+    _acc(Phi, acc_dtype, who)
+    if Psi.dtype != Phi.dtype or Vb.dtype != Phi.dtype:
+        raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
+    if spec.kind != "geometric":
+        raise NotImplementedError(f"{who}: the {spec.kind} mask's landmark block (zeta "
+                                  f"transform) has no HIP kernel in this build")
+    nb, T, r = Phi.shape
+    if T != spec.T:
+        raise ValueError(f"{who}: T={T} but the mask was built for T={spec.T}")
+    C = min(chunk, T)
+    n = spec.n
+    if n % C:
+        raise ValueError(f"segment boundary n={n} is not a multiple of chunk={C}")
+    _staged(spec, Phi.device)
+    idx, indptr, deg = _incidence_args(spec)
+
+    if timer is None and not return_parts:
+        return _hip.forward(Phi, Psi, Vb, idx, deg, n=n, n_P=spec.n_P, N0=spec.N0, B=spec.B,
+                            chunk=C, indptr=indptr, g=g, workspace=workspace)
+
+    tm = timer or (lambda name: nullcontext())
+    parts: Dict[str, torch.Tensor] = {}
+    p = Vb.shape[-1]
+    with tm("lr_pool"):
+        F_glob = (torch.empty(nb, r, p, device=Phi.device, dtype=torch.float32)
+                  if spec.n_P else None)
+        F = _hip.pool(Psi, Vb, spec.n_P, n, spec.N0, F_glob=F_glob)
+    with tm("lr_incidence"):
+        Ff = F.contiguous()
+        U = torch.empty(nb, spec.B, r, p, device=Phi.device, dtype=torch.float32)
+        profiled = n > spec.n_P
+        _hip.call("smat_incidence", Ff.data_ptr(), _hip.ptr(F_glob), idx.data_ptr(), 0,
+                  _hip.ptr(indptr) if profiled else None, deg if profiled else 0,
+                  U.data_ptr(), nb, spec.N0, spec.B, r * p, _hip.stream_of(Ff))
+    with tm("lr_query"):
+        Y_lr = _hip.query(Phi[:, n:], U)
+    with tm("scan"):
+        H = segmented_causal_scan(Phi, Psi, Vb, n=n, chunk=C)
+    with tm("normalise"):
+        out = _hip.normalise(H, n, Y_lr, g)
+    if return_parts:
+        Hfull = H.clone()
+        Hfull[:, n:] += Y_lr
+        parts.update(U=U, Y_lr=Y_lr, H=Hfull)
+        return out, parts
+    return out
+
+
+def dense_masked_kernel_attention(Phi, Psi, Vb, M):
+    """``O(T^2)`` definition (attention.py:485-489).  Verification only: it is
+    not a kernel path and computes with plain (non-batched-view) products."""
+    A = (Phi @ Psi.transpose(-1, -2).contiguous()) * M
+    H = A @ Vb
+    return H[..., :-1] / H[..., -1:]
+
+
+# ---------------------------------------------------------------------------
+# streaming decode (attention.py:496-535)
+# ---------------------------------------------------------------------------
+
+class SmatDecoder:
+    """Exact autoregressive decoding at ``O(rp)`` per token, flat in ``T``.
+
+    Every landmark key precedes every recent query, so the type table
+    ``U = C S^T (Psi (x) Vb)`` over the prefix is fixed after prefill (built
+    here by the pool and incidence kernels); each step adds ``psi vb^T`` to the
+    running state ``S`` and reads ``U[i mod B]`` (attention.py:496-528).  The
+    state is double-buffered on the device; :attr:`S` is the current one.
+    """
+
+    def __init__(self, Psi_prefix, Vb_prefix, spec: MaskSpec, *, acc_dtype=None,
+                 incidence_backend: str = "auto"):
+        who = "SmatDecoder"
+        _backend(incidence_backend, who)
+        _acc(Psi_prefix, acc_dtype, who)
+        self.spec = spec
+        self.acc = torch.float32
+        nb, _, r = Psi_prefix.shape
+        p = Vb_prefix.shape[-1]
+        self.nb, self.r, self.p = nb, r, p
+        dev = Psi_prefix.device
+        _staged(spec, dev)
+        F_glob = torch.empty(nb, r, p, device=dev, dtype=torch.float32) if spec.n_P else None
+        F = _hip.pool(Psi_prefix, Vb_prefix, spec.n_P, spec.n, spec.N0, F_glob=F_glob)
+        idx, indptr, deg = _incidence_args(spec)
+        self.U = torch.empty(nb, spec.B, r, p, device=dev, dtype=torch.float32)
+        profiled = spec.n > spec.n_P
+        _hip.call("smat_incidence", F.data_ptr(), _hip.ptr(F_glob), idx.data_ptr(), 0,
+                  _hip.ptr(indptr) if profiled else None, deg if profiled else 0,
+                  self.U.data_ptr(), nb, spec.N0, spec.B, r * p, _hip.stream_of(F))
+        del F
+        self._S = [torch.zeros(nb, r, p, device=dev, dtype=torch.float32),
+                   torch.empty(nb, r, p, device=dev, dtype=torch.float32)]
+        self._cur = 0
+        self.i = 0
+
+    @property
+    def S(self) -> torch.Tensor:
+        return self._S[self._cur]
+
+    def step(self, Phi_t, Psi_t, Vb_t, *, out=None):
+        """One token.  ``Phi_t, Psi_t: (nb, r)``, ``Vb_t: (nb, p)``; returns fp32 ``(nb, p-1)``."""
+        S_in, S_out = self._S[self._cur], self._S[1 - self._cur]
+        o = _hip.decode_step(Phi_t, Psi_t, Vb_t, S_in, S_out, self.U, self.i, out=out)
+        self._cur = 1 - self._cur
+        self.i += 1
+        return o
+
+    def cache_words(self) -> int:
+        return int(self.S.numel() + self.U.numel())
+
+    @staticmethod
+    def kv_cache_words(nb: int, T: int, d_v: int) -> int:
+        return int(nb * 2 * T * d_v)

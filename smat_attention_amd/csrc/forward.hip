@@ -1,0 +1,204 @@
+// The whole forward schedule of smat_attention (src/smat/attention.py:391-455)
+// for a geometric mask, as one C call that enqueues the kernels on one stream:
+//
+//   pool (+ global channel)  ->  incidence  ->  type-major query  ->
+//   chunk summaries  ->  segmented shifted scan  ->  chunk-local pass  ->
+//   normalise (long-range term added for recent rows, optional gate)
+//
+// The two passes are summed before the single division, as in the reference.
+// Scratch lives in the caller's workspace; this file also holds the error
+// state and version string of the library.
+#include <stdio.h>
+#include <string.h>
+
+#include "smat_host.hpp"
+
+namespace smat {
+
+static thread_local char g_err[512] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+// defined in the other translation units
+int pool_dispatch(int dtype, const void* psi, const void* vb, float* F, float* F_glob, int nb,
+                  int n_P, int n, int N0, int r, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                  int64_t v_st, float* partials, int64_t partial_bytes, hipStream_t stream);
+int64_t pool_workspace_bytes(int nb, int n_P, int n, int N0, int r, int p, bool glob);
+int chunk_states_dispatch(int dtype, const void* psi, const void* vb, float* D, int nb, int T,
+                          int C, int K, int n, int r, int p, int64_t k_sb, int64_t k_st,
+                          int64_t v_sb, int64_t v_st, float* partials, int64_t partial_bytes,
+                          hipStream_t stream, int* ngroups_out, int* ng0_out);
+int segment_scan_dispatch(const float* D, float* Sin, int nb, int nc, int nc0, int64_t rp,
+                          hipStream_t stream);
+int chunk_local_dispatch(int dtype, const void* phi, const void* psi, const void* vb,
+                         const float* sin, float* out, int64_t nbc, int C, int r, int p,
+                         int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                         int64_t v_st, int64_t s_sb, int64_t s_sr, int64_t o_sb, int64_t o_st,
+                         hipStream_t stream);
+int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int idx_is_64,
+                       const int64_t* indptr, int deg, float* U, int nb, int N0, int B, int64_t rp,
+                       hipStream_t stream);
+int query_dispatch(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R, int B,
+                   int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
+                   hipStream_t stream);
+int normalise_dispatch(const float* H, const float* Y, const float* g, float* out, int nb, int T,
+                       int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb, int64_t y_st,
+                       int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream);
+
+// Workspace carve-up, each region 256-byte aligned.
+struct FwdLayout {
+  int64_t F, Fg, U, Y, D, Sin, H, part, total;
+};
+
+static inline int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+static FwdLayout fwd_layout(int nb, int T, int n, int N0, int B, int n_P, int C, int r, int p,
+                            bool want_H_scratch) {
+  FwdLayout L{};
+  const int64_t rp = (int64_t)r * p;
+  const int nc = (T + C - 1) / C;
+  const int T_R = T - n;
+  int64_t off = 0;
+  L.F = off;   off += al256((int64_t)nb * N0 * rp * 4);
+  L.Fg = off;  off += n_P > 0 ? al256((int64_t)nb * rp * 4) : 0;
+  L.U = off;   off += al256((int64_t)nb * B * rp * 4);
+  L.Y = off;   off += al256((int64_t)nb * T_R * p * 4);
+  L.D = off;   off += al256((int64_t)nb * nc * rp * 4);
+  L.Sin = off; off += al256((int64_t)nb * nc * rp * 4);
+  L.H = off;   off += want_H_scratch ? al256((int64_t)nb * nc * C * p * 4) : 0;
+  L.part = off; off += al256(pool_workspace_bytes(nb, n_P, n, N0, r, p, n_P > 0));
+  L.total = off;
+  return L;
+}
+
+}  // namespace smat
+
+extern "C" const char* smat_last_error(void) { return smat::g_err; }
+
+extern "C" const char* smat_version(void) { return "0.1 gfx950"; }
+
+extern "C" int64_t smat_forward_workspace_bytes(int nb, int T, int n, int N0, int B, int n_P,
+                                                int C, int r, int p) {
+  if (nb <= 0 || T <= 0 || C <= 0 || N0 <= 0 || B <= 0 || r <= 0 || p <= 0) return 0;
+  return smat::fwd_layout(nb, T, n, N0, B, n_P, C, r, p, true).total;
+}
+
+extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const void* vb,
+                            const void* idx, int idx_is_64, const int64_t* indptr, int deg,
+                            float* out, float* H_out, const float* g, int nb, int T, int n,
+                            int n_P, int N0, int B, int C, int r, int p, int64_t q_sb,
+                            int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
+                            int64_t o_sb, int64_t o_st, int64_t g_sb, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(phi && psi && vb && idx && out && workspace, SMAT_EINVAL,
+               "smat_forward: null pointer");
+  SMAT_REQUIRE(dtype == SMAT_BF16 || dtype == SMAT_F16 || dtype == SMAT_F32, SMAT_EINVAL,
+               "smat_forward: unknown dtype %d", dtype);
+  SMAT_REQUIRE(nb >= 1 && T >= 1 && C >= 1 && C <= kMaxC, SMAT_EINVAL,
+               "smat_forward: bad sizes (nb=%d T=%d C=%d)", nb, T, C);
+  SMAT_REQUIRE(n >= 0 && n <= T && n % C == 0, SMAT_EINVAL,
+               "smat_forward: landmark count n=%d must be a multiple of chunk=%d in [0, T]", n, C);
+  SMAT_REQUIRE(n_P >= 0 && n_P <= n && N0 >= 1 && B >= 1, SMAT_EINVAL,
+               "smat_forward: bad mask sizes (n_P=%d N0=%d B=%d)", n_P, N0, B);
+  SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 2 && p <= kMaxP, SMAT_EUNSUPPORTED,
+               "smat_forward: r=%d p=%d beyond r<=%d, 2<=p<=%d", r, p, kMaxR, kMaxP);
+  SMAT_REQUIRE(q_st >= r && k_st >= r && v_st >= p && o_st >= p - 1, SMAT_EINVAL,
+               "smat_forward: a row stride is shorter than its row");
+  SMAT_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, SMAT_EINVAL,
+               "smat_forward: workspace must be 256-byte aligned");
+  const FwdLayout L = fwd_layout(nb, T, n, N0, B, n_P, C, r, p, H_out == nullptr);
+  SMAT_REQUIRE(workspace_bytes >= L.total, SMAT_EINVAL,
+               "smat_forward: workspace of %lld bytes needed, %lld given", (long long)L.total,
+               (long long)workspace_bytes);
+
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  float* F = (float*)(ws + L.F);
+  float* Fg = n_P > 0 ? (float*)(ws + L.Fg) : nullptr;
+  float* U = (float*)(ws + L.U);
+  float* Y = (float*)(ws + L.Y);
+  float* D = (float*)(ws + L.D);
+  float* Sin = (float*)(ws + L.Sin);
+  float* part = (float*)(ws + L.part);
+  const int64_t part_bytes = L.total - L.part;
+  const int64_t rp = (int64_t)r * p;
+  const int nc = (T + C - 1) / C;
+  const int T_R = T - n;
+  // H in (nb, nc*C, p) fp32: the caller's H_out is (nb, T, p), which is the
+  // same layout for every row the chunk pass writes (rows >= T are skipped).
+  float* H = H_out ? H_out : (float*)(ws + L.H);
+  int rc;
+
+  // ---- long range: S^T, then C, then R ---------------------------------
+  if (T_R > 0) {
+    // With no profiled landmark columns (n == n_P) every U_h is the global
+    // channel alone (or zero): the incidence runs with an empty row.
+    const bool profiled = n > n_P;
+    rc = pool_dispatch(dtype, psi, vb, F, Fg, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st, part,
+                       part_bytes, st);
+    if (rc) return rc;
+    rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
+                            profiled ? deg : 0, U, nb, N0, B, rp, st);
+    if (rc) return rc;
+  }
+  if (T_R > 0) {
+    const char* phi_rec = (const char*)phi + (int64_t)n * q_st * elem_bytes(dtype);
+    rc = query_dispatch(dtype, phi_rec, U, Y, nb, T_R, B, r, p, q_sb, q_st, (int64_t)T_R * p, p,
+                        st);
+    if (rc) return rc;
+  }
+
+  // ---- causal: chunk summaries, segmented scan, chunk-local pass ----------
+  rc = chunk_states_dispatch(dtype, psi, vb, D, nb, T, C, 1, n, r, p, k_sb, k_st, v_sb, v_st,
+                             nullptr, 0, st, nullptr, nullptr);
+  if (rc) return rc;
+  rc = segment_scan_dispatch(D, Sin, nb, nc, n / C, rp, st);
+  if (rc) return rc;
+  // Chunk b of sequence s covers rows [b*C, b*C + C).  When every sequence is
+  // a whole number of chunks laid out back to back, all nb*nc chunks form one
+  // batch; otherwise each sequence runs its full chunks and its ragged tail
+  // chunk (rows [nfull*C, T), zero-padded like the reference) separately.
+  const int nfull = T / C;
+  const int64_t h_sb = H_out ? (int64_t)T * p : (int64_t)nc * C * p;
+  const int eb = elem_bytes(dtype);
+  if (T % C == 0 && q_sb == (int64_t)T * q_st && k_sb == (int64_t)T * k_st &&
+      v_sb == (int64_t)T * v_st) {
+    rc = chunk_local_dispatch(dtype, phi, psi, vb, Sin, H, (int64_t)nb * nc, C, r, p, C * q_st,
+                              q_st, C * k_st, k_st, C * v_st, v_st, rp, p, (int64_t)C * p, p, st);
+    if (rc) return rc;
+  } else {
+    for (int s = 0; s < nb; ++s) {
+      const char* phs = (const char*)phi + s * q_sb * eb;
+      const char* pss = (const char*)psi + s * k_sb * eb;
+      const char* vbs = (const char*)vb + s * v_sb * eb;
+      float* Hs = H + s * h_sb;
+      const float* Ss = Sin + (int64_t)s * nc * rp;
+      if (nfull > 0) {
+        rc = chunk_local_dispatch(dtype, phs, pss, vbs, Ss, Hs, nfull, C, r, p, C * q_st, q_st,
+                                  C * k_st, k_st, C * v_st, v_st, rp, p, (int64_t)C * p, p, st);
+        if (rc) return rc;
+      }
+      if (nfull < nc) {
+        const int Ct = T - nfull * C;
+        const int64_t t0 = (int64_t)nfull * C;
+        rc = chunk_local_dispatch(dtype, phs + t0 * q_st * eb, pss + t0 * k_st * eb,
+                                  vbs + t0 * v_st * eb, Ss + (int64_t)nfull * rp, Hs + t0 * p, 1,
+                                  Ct, r, p, 0, q_st, 0, k_st, 0, v_st, 0, p, 0, p, st);
+        if (rc) return rc;
+      }
+    }
+  }
+
+  // ---- normalise ---------------------------------------------------------
+  return normalise_dispatch(H, T_R > 0 ? Y : nullptr, g, out, nb, T, n, p, h_sb, p,
+                            (int64_t)T_R * p, p, o_sb, o_st, g_sb, st);
+}

@@ -1,0 +1,356 @@
+// Gram sums  G = sum_{t in set} Psi_t^T Vb_t  (r x p, fp32) over token sets
+// that are arithmetic progressions {start + s*stride : s < count}.
+//
+// One kernel serves every place the schedule pools keys against values:
+//   * chunk summaries D_c (src/smat/attention.py:162): stride 1, one chunk;
+//   * profile pooling F_x (src/smat/attention.py:199-236, the Triton pool
+//     kernel src/smat/kernels/triton_fwd.py:226-311): prof(j) = (j - n_P)
+//     mod N0 is round-robin, so profile x is the progression n_P + x + s*N0;
+//   * the global-channel rank-one term (src/smat/attention.py:422-425):
+//     tokens [0, n_P), stride 1;
+//   * the decoder's prefix pooling (src/smat/attention.py:515-519).
+//
+// MFMA layout: M = a (feature, r), N = c (value column, p), K = tokens.  Both
+// operands need 8 consecutive TOKENS per lane, so each 32-token block of Psi
+// and Vb is staged in LDS transposed (Psi^T[a][t], Vb^T[c][t]); wave w owns
+// the 16-row tiles 2w and 2w+1 of G and every column tile.
+#include "smat_host.hpp"
+
+namespace smat {
+
+namespace gr {
+constexpr int kThreads = 256;
+constexpr int kBT = 32;                 // tokens per staged block (one MFMA k-block)
+constexpr int kTPad = kBT + 8;          // LDS row length (tokens) of the transposed tiles
+constexpr int kRows = 128;              // r <= 128
+constexpr int kCols = 144;              // p <= 144
+constexpr int kNCT = kCols / 16;
+}  // namespace gr
+
+// How item i of batch b maps to a token progression.
+struct GramItems {
+  int mode;        // 0: chunk groups, 1: profiles (+ optional global channel)
+  // mode 0: chunks of width C over T tokens; segment 0 has nc0 chunks; a group
+  // is K consecutive chunks inside one segment.
+  int T, C, K, nc0, nc, ng0;
+  // mode 1: profiles x < N0 over [n_P, n); item N0 is the global channel.
+  int n_P, n, N0;
+  // split-K: each progression is cut into nsplit runs of `per` terms (a
+  // multiple of the 32-token block); run s writes partial s, and a second
+  // kernel sums the partials in run order, so the result is deterministic.
+  int nsplit, per;
+};
+
+__device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& start,
+                                          int64_t& stride, int& count) {
+  if (it.mode == 0) {
+    int c0, c1;
+    if (i < it.ng0) {
+      c0 = i * it.K;
+      c1 = min(c0 + it.K, it.nc0);
+    } else {
+      c0 = it.nc0 + (i - it.ng0) * it.K;
+      c1 = min(c0 + it.K, it.nc);
+    }
+    start = (int64_t)c0 * it.C;
+    stride = 1;
+    const int64_t end = min((int64_t)c1 * it.C, (int64_t)it.T);
+    count = (int)max((int64_t)0, end - start);
+  } else {
+    if (i < it.N0) {
+      const int nX = it.n - it.n_P;
+      start = it.n_P + i;
+      stride = it.N0;
+      count = (i < nX) ? (nX - i + it.N0 - 1) / it.N0 : 0;
+    } else {
+      start = 0;
+      stride = 1;
+      count = it.n_P;
+    }
+  }
+}
+
+template <typename In>
+__global__ __launch_bounds__(gr::kThreads) void gram_kernel(
+    const In* __restrict__ psi, const In* __restrict__ vb, float* __restrict__ G,
+    float* __restrict__ G_last, GramItems it, int r, int p, int64_t k_sb, int64_t k_st,
+    int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si, int64_t gl_sb) {
+  using namespace gr;
+  typedef typename Traits<In>::frag Frag;
+  __shared__ __attribute__((aligned(16))) In psiT[kRows * kTPad];
+  __shared__ __attribute__((aligned(16))) In vbT[kCols * kTPad];
+
+  const int item = blockIdx.x / it.nsplit;
+  const int sp = blockIdx.x - item * it.nsplit;
+  const int64_t b = blockIdx.y;
+  const int lane = lane_id(), w = wave_id();
+  const int row16 = lane & 15, grp = lane >> 4;
+  const int nrt = (r + 15) >> 4;     // 16-row tiles of G
+  const int nct = (p + 15) >> 4;
+
+  int64_t start, stride;
+  int count;
+  gram_item(it, item, start, stride, count);
+  if (it.nsplit > 1) {           // this run: terms [sp*per, min((sp+1)*per, count))
+    const int lo = sp * it.per;
+    const int hi = min(count, lo + it.per);
+    start += (int64_t)lo * stride;
+    count = max(0, hi - lo);
+  }
+
+  const In* psib = psi + b * k_sb;
+  const In* vbb = vb + b * v_sb;
+
+  f32x4 acc[2][kNCT];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ct = 0; ct < kNCT; ++ct) acc[t][ct] = zero4();
+
+  const int nrows = nrt * 16, ncols = nct * 16;
+  for (int s0 = 0; s0 < count; s0 += kBT) {
+    // stage Psi^T[a][tt] and Vb^T[c][tt] for tokens s0 + tt
+    for (int idx = threadIdx.x; idx < kBT * nrows; idx += kThreads) {
+      const int tt = idx / nrows, a = idx - tt * nrows;
+      const int s = s0 + tt;
+      psiT[a * kTPad + tt] = (s < count && a < r) ? psib[(start + (int64_t)s * stride) * k_st + a]
+                                                  : from_f32<In>(0.f);
+    }
+    for (int idx = threadIdx.x; idx < kBT * ncols; idx += kThreads) {
+      const int tt = idx / ncols, c = idx - tt * ncols;
+      const int s = s0 + tt;
+      vbT[c * kTPad + tt] = (s < count && c < p) ? vbb[(start + (int64_t)s * stride) * v_st + c]
+                                                 : from_f32<In>(0.f);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int rt = 2 * w + t;
+      if (rt >= nrt) continue;
+      const Frag a = *reinterpret_cast<const Frag*>(psiT + (rt * 16 + row16) * kTPad + 8 * grp);
+#pragma unroll
+      for (int ct = 0; ct < kNCT; ++ct) {
+        if (ct >= nct) continue;
+        const Frag bf = *reinterpret_cast<const Frag*>(vbT + (ct * 16 + row16) * kTPad + 8 * grp);
+        acc[t][ct] = mma(acc[t][ct], a, bf);
+      }
+    }
+    __syncthreads();
+  }
+
+  // nsplit > 1: G is the partial buffer (nb, nitems, nsplit, r, p) and G_last
+  // is unused; otherwise item nitems-1 goes to G_last when that is given.
+  const int nitems = gridDim.x / it.nsplit;
+  float* Gb;
+  if (it.nsplit > 1)
+    Gb = G + ((b * nitems + item) * it.nsplit + sp) * (int64_t)r * p;
+  else
+    Gb = (G_last != nullptr && item == nitems - 1) ? G_last + b * gl_sb : G + b * g_sb + item * g_si;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int rt = 2 * w + t;
+    if (rt >= nrt) continue;
+#pragma unroll
+    for (int ct = 0; ct < kNCT; ++ct) {
+      if (ct >= nct) continue;
+      const int c = ct * 16 + row16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int a = rt * 16 + 4 * grp + i;
+        if (a < r && c < p) Gb[(int64_t)a * p + c] = acc[t][ct][i];
+      }
+    }
+  }
+}
+
+// Sum the nsplit partials of every (b, item) in run order into G / G_last.
+__global__ __launch_bounds__(256) void gram_reduce_kernel(const float* __restrict__ part,
+                                                          float* __restrict__ G,
+                                                          float* __restrict__ G_last, int nitems,
+                                                          int nsplit, int64_t rp, int64_t g_sb,
+                                                          int64_t g_si, int64_t gl_sb) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int item = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  if (e >= rp) return;
+  const float* src = part + (b * nitems + item) * (int64_t)nsplit * rp + e;
+  float acc = 0.f;
+  for (int s = 0; s < nsplit; ++s) acc += src[(int64_t)s * rp];
+  float* dst = (G_last != nullptr && item == nitems - 1) ? G_last + b * gl_sb
+                                                          : G + b * g_sb + item * g_si;
+  dst[e] = acc;
+}
+
+template <typename In>
+static int launch_gram(const void* psi, const void* vb, float* G, float* G_last,
+                       const GramItems& it, int nitems, int nb, int r, int p, int64_t k_sb,
+                       int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                       int64_t gl_sb, float* partials, hipStream_t stream, const char* who) {
+  const int64_t gx = (int64_t)nitems * it.nsplit;
+  if (gx >= (1ll << 31) || nb >= 65536) {
+    set_error("%s: problem too large", who);
+    return SMAT_EUNSUPPORTED;
+  }
+  if (it.nsplit > 1) {
+    hipLaunchKernelGGL(gram_kernel<In>, dim3((unsigned)gx, (unsigned)nb), dim3(gr::kThreads), 0,
+                       stream, (const In*)psi, (const In*)vb, partials, nullptr, it, r, p, k_sb,
+                       k_st, v_sb, v_st, 0, 0, 0);
+    int st = launch_status(who);
+    if (st != SMAT_OK) return st;
+    const int64_t rp = (int64_t)r * p;
+    hipLaunchKernelGGL(gram_reduce_kernel, dim3((unsigned)((rp + 255) / 256), nitems, nb),
+                       dim3(256), 0, stream, partials, G, G_last, nitems, it.nsplit, rp, g_sb,
+                       g_si, gl_sb);
+    return launch_status(who);
+  }
+  hipLaunchKernelGGL(gram_kernel<In>, dim3((unsigned)gx, (unsigned)nb), dim3(gr::kThreads), 0,
+                     stream, (const In*)psi, (const In*)vb, G, G_last, it, r, p, k_sb, k_st,
+                     v_sb, v_st, g_sb, g_si, gl_sb);
+  return launch_status(who);
+}
+
+// Choose the split of the longest progression so that a launch has enough
+// workgroups to fill the GPU; returns bytes of partials needed (0: no split).
+static int64_t plan_split(GramItems& it, int nitems, int nb, int max_count, int r, int p) {
+  const int64_t wgs = (int64_t)nitems * nb;
+  int nsplit = 1;
+  if (wgs < 2048 && max_count > 8 * gr::kBT) {
+    const int by_work = (max_count + 4 * gr::kBT - 1) / (4 * gr::kBT);   // >= 128 terms a run
+    const int by_fill = (int)((2048 + wgs - 1) / wgs);
+    nsplit = max(1, min(by_work, by_fill));
+  }
+  int per = (max_count + nsplit - 1) / nsplit;
+  per = (per + gr::kBT - 1) / gr::kBT * gr::kBT;
+  if (per > 0) nsplit = (max_count + per - 1) / per;
+  if (nsplit < 1) nsplit = 1;
+  it.nsplit = nsplit;
+  it.per = per;
+  return nsplit > 1 ? (int64_t)nb * nitems * nsplit * r * p * 4 : 0;
+}
+
+int gram_dispatch(int dtype, const void* psi, const void* vb, float* G, float* G_last,
+                  const GramItems& it, int nitems, int nb, int r, int p, int64_t k_sb,
+                  int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                  int64_t gl_sb, float* partials, hipStream_t stream, const char* who) {
+  if (nitems == 0 || nb == 0) return SMAT_OK;
+  if (it.nsplit > 1 && partials == nullptr) {
+    set_error("%s: split-K needs a workspace", who);
+    return SMAT_EINVAL;
+  }
+  switch (dtype) {
+    case SMAT_BF16:
+      return launch_gram<bf16>(psi, vb, G, G_last, it, nitems, nb, r, p, k_sb, k_st, v_sb, v_st,
+                               g_sb, g_si, gl_sb, partials, stream, who);
+    case SMAT_F16:
+      return launch_gram<f16>(psi, vb, G, G_last, it, nitems, nb, r, p, k_sb, k_st, v_sb, v_st,
+                              g_sb, g_si, gl_sb, partials, stream, who);
+    case SMAT_F32:
+      return launch_gram<float>(psi, vb, G, G_last, it, nitems, nb, r, p, k_sb, k_st, v_sb,
+                                v_st, g_sb, g_si, gl_sb, partials, stream, who);
+  }
+  set_error("%s: unknown dtype %d", who, dtype);
+  return SMAT_EINVAL;
+}
+
+// Chunk summaries for chunks of width C (K = 1) or groups of K chunks.
+int chunk_states_dispatch(int dtype, const void* psi, const void* vb, float* D, int nb, int T,
+                          int C, int K, int n, int r, int p, int64_t k_sb, int64_t k_st,
+                          int64_t v_sb, int64_t v_st, float* partials, int64_t partial_bytes,
+                          hipStream_t stream, int* ngroups_out, int* ng0_out) {
+  GramItems it{};
+  it.mode = 0;
+  it.T = T;
+  it.C = C;
+  it.K = K;
+  it.nc = (T + C - 1) / C;
+  it.nc0 = n / C;
+  it.ng0 = (it.nc0 + K - 1) / K;
+  const int ng = it.ng0 + (it.nc - it.nc0 + K - 1) / K;
+  if (ngroups_out) *ngroups_out = ng;
+  if (ng0_out) *ng0_out = it.ng0;
+  const int64_t need = plan_split(it, ng, nb, K * C, r, p);
+  if (need > partial_bytes) {   // not enough scratch: run unsplit
+    it.nsplit = 1;
+    it.per = K * C;
+  }
+  const int64_t rp = (int64_t)r * p;
+  return gram_dispatch(dtype, psi, vb, D, nullptr, it, ng, nb, r, p, k_sb, k_st, v_sb, v_st,
+                       (int64_t)ng * rp, rp, 0, partials, stream, "smat_chunk_states");
+}
+
+static GramItems pool_items(int n_P, int n, int N0, bool glob, int nb, int r, int p,
+                            int64_t* need) {
+  GramItems it{};
+  it.mode = 1;
+  it.n_P = n_P;
+  it.n = n;
+  it.N0 = N0;
+  const int nX = n - n_P;
+  int maxc = (nX + N0 - 1) / N0;
+  if (glob) maxc = maxc > n_P ? maxc : n_P;
+  *need = plan_split(it, N0 + (glob ? 1 : 0), nb, maxc, r, p);
+  return it;
+}
+
+int64_t pool_workspace_bytes(int nb, int n_P, int n, int N0, int r, int p, bool glob) {
+  int64_t need = 0;
+  pool_items(n_P, n, N0, glob, nb, r, p, &need);
+  return need;
+}
+
+int pool_dispatch(int dtype, const void* psi, const void* vb, float* F, float* F_glob, int nb,
+                  int n_P, int n, int N0, int r, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                  int64_t v_st, float* partials, int64_t partial_bytes, hipStream_t stream) {
+  const bool glob = (F_glob != nullptr && n_P > 0);
+  int64_t need = 0;
+  GramItems it = pool_items(n_P, n, N0, glob, nb, r, p, &need);
+  if (need > partial_bytes) {
+    set_error("smat_pool: workspace of %lld bytes needed, %lld given", (long long)need,
+              (long long)partial_bytes);
+    return SMAT_EINVAL;
+  }
+  const int64_t rp = (int64_t)r * p;
+  return gram_dispatch(dtype, psi, vb, F, glob ? F_glob : nullptr, it, N0 + (glob ? 1 : 0), nb, r,
+                       p, k_sb, k_st, v_sb, v_st, (int64_t)N0 * rp, rp, rp, partials, stream,
+                       "smat_pool");
+}
+
+}  // namespace smat
+
+extern "C" int smat_chunk_states(int dtype, const void* psi, const void* vb, float* D, int nb,
+                                 int T, int C, int r, int p, int64_t k_sb, int64_t k_st,
+                                 int64_t v_sb, int64_t v_st, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(psi && vb && D, SMAT_EINVAL, "smat_chunk_states: null pointer");
+  SMAT_REQUIRE(nb >= 0 && T >= 0 && C >= 1 && C <= kMaxC, SMAT_EINVAL,
+               "smat_chunk_states: bad sizes (C=%d)", C);
+  SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 1 && p <= kMaxP, SMAT_EUNSUPPORTED,
+               "smat_chunk_states: r=%d p=%d beyond r<=%d, p<=%d", r, p, kMaxR, kMaxP);
+  SMAT_REQUIRE(k_st >= r && v_st >= p, SMAT_EINVAL, "smat_chunk_states: row stride too short");
+  return chunk_states_dispatch(dtype, psi, vb, D, nb, T, C, 1, 0, r, p, k_sb, k_st, v_sb, v_st,
+                               nullptr, 0, (hipStream_t)stream, nullptr, nullptr);
+}
+
+extern "C" int64_t smat_pool_workspace_bytes(int nb, int n_P, int n, int N0, int r, int p) {
+  if (nb <= 0 || N0 < 1 || n_P < 0 || n < n_P) return 0;
+  return smat::pool_workspace_bytes(nb, n_P, n, N0, r, p, n_P > 0);
+}
+
+extern "C" int smat_pool(int dtype, const void* psi, const void* vb, float* F, float* F_glob,
+                         int nb, int n_P, int n, int N0, int r, int p, int64_t k_sb, int64_t k_st,
+                         int64_t v_sb, int64_t v_st, void* workspace, int64_t workspace_bytes,
+                         void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(psi && vb && F, SMAT_EINVAL, "smat_pool: null pointer");
+  SMAT_REQUIRE(nb >= 0 && N0 >= 1 && n_P >= 0 && n >= n_P, SMAT_EINVAL,
+               "smat_pool: need N0 >= 1 and 0 <= n_P <= n (N0=%d n_P=%d n=%d)", N0, n_P, n);
+  SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 1 && p <= kMaxP, SMAT_EUNSUPPORTED,
+               "smat_pool: r=%d p=%d beyond r<=%d, p<=%d", r, p, kMaxR, kMaxP);
+  SMAT_REQUIRE(k_st >= r && v_st >= p, SMAT_EINVAL, "smat_pool: row stride too short");
+  SMAT_REQUIRE(workspace == nullptr || aligned16(workspace), SMAT_EINVAL,
+               "smat_pool: workspace must be 16-byte aligned");
+  return pool_dispatch(dtype, psi, vb, F, F_glob, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st,
+                       (float*)workspace, workspace ? workspace_bytes : 0, (hipStream_t)stream);
+}

@@ -1,0 +1,100 @@
+// Bandwidth kernels around the chunk pass:
+//   * the segmented shifted exclusive scan of chunk summaries
+//     (src/smat/attention.py:163-179);
+//   * the final normalisation H[..., :-1] / H[..., -1:] with the long-range
+//     term added for recent rows and the optional output gate
+//     (src/smat/attention.py:446-453).
+#include "smat_host.hpp"
+
+namespace smat {
+
+// One thread per state element; it walks its segment's chunks in order, so
+// Sin[c] is the running sum BEFORE adding D[c] (a shifted scan: D[c] never
+// reaches its own Sin[c], and no subtraction ever happens).
+__global__ __launch_bounds__(256) void segment_scan_kernel(const float* __restrict__ D,
+                                                           float* __restrict__ Sin, int nc,
+                                                           int nc0, int64_t rp) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const int seg = blockIdx.z;
+  if (e >= rp) return;
+  const int c_lo = seg == 0 ? 0 : nc0;
+  const int c_hi = seg == 0 ? nc0 : nc;
+  const float* Db = D + b * nc * rp + e;
+  float* Sb = Sin + b * nc * rp + e;
+  float run = 0.f;
+  for (int c = c_lo; c < c_hi; ++c) {
+    const float d = Db[(int64_t)c * rp];
+    Sb[(int64_t)c * rp] = run;
+    run += d;
+  }
+}
+
+int segment_scan_dispatch(const float* D, float* Sin, int nb, int nc, int nc0, int64_t rp,
+                          hipStream_t stream) {
+  if (nb == 0 || nc == 0 || rp == 0) return SMAT_OK;
+  // nc0 == 0 or nc0 == nc: one segment.  Segment 1 is [nc0, nc).
+  dim3 grid((unsigned)((rp + 255) / 256), (unsigned)nb, 2);
+  hipLaunchKernelGGL(segment_scan_kernel, grid, dim3(256), 0, stream, D, Sin, nc, nc0, rp);
+  return launch_status("smat_segment_scan");
+}
+
+// One wave per output row: the normaliser is read once, every column divided.
+__global__ __launch_bounds__(256) void normalise_kernel(
+    const float* __restrict__ H, const float* __restrict__ Y, const float* __restrict__ g,
+    float* __restrict__ out, int T, int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb,
+    int64_t y_st, int64_t o_sb, int64_t o_st, int64_t g_sb) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  const int64_t b = blockIdx.y;
+  const int lane = lane_id();
+  if (row >= T) return;
+  const float* h = H + b * h_sb + row * h_st;
+  const float* y = (Y != nullptr && row >= n) ? Y + b * y_sb + (row - n) * y_st : nullptr;
+  float den = h[p - 1];
+  if (y) den += y[p - 1];
+  const float gate = g ? g[b * g_sb + row] : 1.f;
+  float* o = out + b * o_sb + row * o_st;
+  for (int c = lane; c < p - 1; c += 64) {
+    float num = h[c];
+    if (y) num += y[c];
+    float v = num / den;
+    if (g) v *= gate;
+    o[c] = v;
+  }
+}
+
+int normalise_dispatch(const float* H, const float* Y, const float* g, float* out, int nb, int T,
+                       int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb, int64_t y_st,
+                       int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream) {
+  if (nb == 0 || T == 0) return SMAT_OK;
+  dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
+  hipLaunchKernelGGL(normalise_kernel, grid, dim3(256), 0, stream, H, Y, g, out, T, n, p, h_sb,
+                     h_st, y_sb, y_st, o_sb, o_st, g_sb);
+  return launch_status("smat_normalise");
+}
+
+}  // namespace smat
+
+extern "C" int smat_segment_scan(const float* D, float* Sin, int nb, int nc, int nc0, int64_t rp,
+                                 void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(D && Sin && D != Sin, SMAT_EINVAL, "smat_segment_scan: null or aliased D/Sin");
+  SMAT_REQUIRE(nb >= 0 && nc >= 0 && nc0 >= 0 && nc0 <= nc && rp >= 0, SMAT_EINVAL,
+               "smat_segment_scan: need 0 <= nc0 <= nc (nc=%d nc0=%d)", nc, nc0);
+  return segment_scan_dispatch(D, Sin, nb, nc, nc0, rp, (hipStream_t)stream);
+}
+
+extern "C" int smat_normalise(const float* H, const float* Y, const float* g, float* out, int nb,
+                              int T, int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb,
+                              int64_t y_st, int64_t o_sb, int64_t o_st, int64_t g_sb,
+                              void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(H && out, SMAT_EINVAL, "smat_normalise: null pointer");
+  SMAT_REQUIRE(nb >= 0 && T >= 0 && n >= 0 && n <= T && p >= 2, SMAT_EINVAL,
+               "smat_normalise: bad sizes (T=%d n=%d p=%d)", T, n, p);
+  SMAT_REQUIRE(h_st >= p && o_st >= p - 1, SMAT_EINVAL, "smat_normalise: row stride too short");
+  return normalise_dispatch(H, Y, g, out, nb, T, n, p, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb,
+                            (hipStream_t)stream);
+}

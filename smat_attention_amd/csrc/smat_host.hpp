@@ -1,0 +1,52 @@
+// Host-side helpers shared by the C-ABI entry points: argument checks, the
+// per-thread error message, and dtype dispatch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/smat_hip.h"
+#include "smat_common.hpp"
+
+namespace smat {
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+// Checked at every entry point before any launch.
+#define SMAT_REQUIRE(cond, code, ...)            \
+  do {                                           \
+    if (!(cond)) {                               \
+      ::smat::set_error(__VA_ARGS__);            \
+      return (code);                             \
+    }                                            \
+  } while (0)
+
+inline int launch_status(const char* who) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", who, hipGetErrorString(e));
+    return SMAT_ELAUNCH;
+  }
+  return SMAT_OK;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// True when rows of `elem_bytes`-sized elements starting at p with row stride
+// `ld` (elements) and batch stride `sb` can be read in 16-byte groups.
+inline bool rows_vec_ok(const void* p, int64_t sb, int64_t ld, int elem_bytes) {
+  const int64_t per16 = 16 / elem_bytes;
+  return aligned16(p) && (ld % per16 == 0) && (sb % per16 == 0);
+}
+
+inline int elem_bytes(int dtype) { return dtype == SMAT_F32 ? 4 : 2; }
+
+// Upper bounds of the MFMA tilings.
+constexpr int kMaxR = 128;
+constexpr int kMaxP = 144;
+constexpr int kMaxC = 256;
+
+}  // namespace smat

@@ -1,0 +1,302 @@
+"""The forward kernels behind the ``kernels/`` dispatch, on HIP (gfx950).
+
+Drop-in for ``src/smat/kernels/triton_fwd.py``: the same five names with the
+same arguments, shapes and return dtypes --
+
+    available()                          triton_fwd.py:38-39
+    chunk_local(Phi_c, Psi_c, Vb_c, Sin) triton_fwd.py:118-152
+    incidence(F, plane_pts, B)           triton_fwd.py:191-216
+    pool_ok(N0, gmax, P)                 triton_fwd.py:270-278
+    pool(Psi, Vb, n_P, n, N0)            triton_fwd.py:281-311
+
+-- plus the schedule stages the reference leaves to torch (chunk summaries,
+segmented scan, type-major query, normalisation), the whole forward as one
+call, and the decode step.  Inputs are borrowed; outputs are allocated here
+with torch's caching allocator and filled by libsmat_hip.so on torch's
+current stream.  Every failure raises; nothing falls back.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import DTYPE_CODE, HipKernelError, HipUnavailable, call, ptr, stream_of
+
+MAX_R = 128
+MAX_P = 144
+MAX_C = 256
+
+__all__ = [
+    "available", "chunk_local", "incidence", "pool_ok", "pool",
+    "chunk_states", "segment_scan", "query", "normalise", "forward",
+    "forward_workspace_bytes", "decode_step", "validate_table",
+    "HipKernelError", "HipUnavailable", "MAX_R", "MAX_P", "MAX_C",
+]
+
+
+def available() -> bool:
+    """True when libsmat_hip.so loads and a GPU is visible."""
+    if not torch.cuda.is_available():
+        return False
+    try:
+        _lib.load()
+    except HipUnavailable:
+        return False
+    return True
+
+
+# ---------------------------------------------------------------------------
+# argument plumbing
+# ---------------------------------------------------------------------------
+
+def _code(t: torch.Tensor, who: str) -> int:
+    try:
+        return DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise TypeError(f"{who}: dtype {t.dtype} is not one of bfloat16, float16, "
+                        f"float32") from None
+
+
+def _on_gpu(who: str, *ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError(f"{who}: tensors must be on the GPU (got {t.device})")
+
+
+def _rows3(t: torch.Tensor):
+    """``t`` as a (batch, rows, cols) tensor with unit column stride, plus its
+    batch and row strides in elements.  Copies only when no such view exists."""
+    if t.stride(-1) != 1:
+        t = t.contiguous()
+    return t, t.stride(0), t.stride(1)
+
+
+def _fp32_rows(t: torch.Tensor) -> torch.Tensor:
+    t = t if t.dtype == torch.float32 else t.float()
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def validate_table(plane_pts: torch.Tensor, N0: int) -> None:
+    """Check once that every point index lies in ``[0, N0)`` (the kernels trust it).
+
+    The check is remembered on the tensor object, so a table staged by
+    :func:`smat_attention_amd.attention.to_device` (which checks on the host)
+    or already validated costs nothing.
+    """
+    if getattr(plane_pts, "_smat_checked_N0", None) == N0:
+        return
+    if plane_pts.numel():
+        lo, hi = int(plane_pts.min()), int(plane_pts.max())
+        if lo < 0 or hi >= N0:
+            raise ValueError(f"incidence table entries must lie in [0, {N0}), got "
+                             f"[{lo}, {hi}]")
+    plane_pts._smat_checked_N0 = N0
+
+
+# ---------------------------------------------------------------------------
+# the reference's five functions
+# ---------------------------------------------------------------------------
+
+def chunk_local(Phi_c, Psi_c, Vb_c, Sin):
+    """``Phi_b Sin_b + (Phi_b Psi_b^T . L_C) Vb_b`` for every chunk, fused.
+
+    Shapes ``(nb, nc, C, r)``, ``(nb, nc, C, r)``, ``(nb, nc, C, p)``,
+    ``(nb, nc, r, p)`` -> fp32 ``(nb, nc, C, p)``.
+    """
+    who = "chunk_local"
+    _on_gpu(who, Phi_c, Psi_c, Vb_c, Sin)
+    nb, nc, C, R = Phi_c.shape
+    P = Vb_c.shape[-1]
+    if Psi_c.dtype != Phi_c.dtype or Vb_c.dtype != Phi_c.dtype:
+        raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
+    code = _code(Phi_c, who)
+    q, q_sb, q_st = _rows3(Phi_c.reshape(nb * nc, C, R))
+    k, k_sb, k_st = _rows3(Psi_c.reshape(nb * nc, C, R))
+    v, v_sb, v_st = _rows3(Vb_c.reshape(nb * nc, C, P))
+    s, s_sb, s_sr = _rows3(_fp32_rows(Sin).reshape(nb * nc, R, P))
+    out = torch.empty(nb * nc, C, P, device=q.device, dtype=torch.float32)
+    call("smat_chunk_local", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), s.data_ptr(),
+         out.data_ptr(), nb * nc, C, R, P, q_sb, q_st, k_sb, k_st, v_sb, v_st, s_sb, s_sr,
+         out.stride(0), out.stride(1), stream_of(q))
+    return out.reshape(nb, nc, C, P)
+
+
+def incidence(F, plane_pts, B: int):
+    """``U_h = sum_{x in H_h} F_x``: ``F (nb, N0, r, p) -> U (nb, B, r, p)`` fp32,
+    ``plane_pts (B, deg)`` int64 or int32."""
+    who = "incidence"
+    _on_gpu(who, F, plane_pts)
+    nb, N0, R, P = F.shape
+    if plane_pts.dim() != 2 or plane_pts.shape[0] != B:
+        raise ValueError(f"{who}: plane_pts must be (B={B}, deg), got {tuple(plane_pts.shape)}")
+    if plane_pts.dtype not in (torch.int64, torch.int32):
+        raise TypeError(f"{who}: plane_pts must be int64 or int32")
+    plane_pts = plane_pts.contiguous()
+    validate_table(plane_pts, N0)
+    Ff = F.contiguous().float()
+    U = torch.empty(nb, B, R, P, device=F.device, dtype=torch.float32)
+    call("smat_incidence", Ff.data_ptr(), None, plane_pts.data_ptr(),
+         int(plane_pts.dtype == torch.int64), None, int(plane_pts.shape[1]), U.data_ptr(),
+         nb, N0, B, R * P, stream_of(Ff))
+    return U
+
+
+def pool_ok(N0: int, gmax: int, P: int) -> bool:
+    """Whether the pooling kernel takes this shape.
+
+    The reference gates its kernel to ``N0 >= 64`` because a short grid loses
+    to one torch GEMM there; this kernel splits long progressions over several
+    workgroups instead, so it runs at every ``N0`` and only ``P`` is bounded.
+    """
+    return available() and 1 <= P <= MAX_P and N0 >= 1 and gmax >= 0
+
+
+def pool(Psi, Vb, n_P: int, n: int, N0: int, *, F_glob: Optional[torch.Tensor] = None):
+    """``F_x = sum_{prof(j)=x} Psi_j Vb_j^T``: ``(nb, T, r), (nb, T, p) -> (nb, N0, r, p)`` fp32.
+
+    ``F_glob`` (optional, fp32 ``(nb, r, p)``) receives the global-channel
+    term ``sum_{j < n_P} Psi_j Vb_j^T`` in the same launch.
+    """
+    who = "pool"
+    _on_gpu(who, Psi, Vb)
+    nb, T, R = Psi.shape
+    P = Vb.shape[-1]
+    if Vb.dtype != Psi.dtype:
+        raise TypeError(f"{who}: Psi and Vb must share a dtype")
+    if not (0 <= n_P <= n <= T):
+        raise ValueError(f"{who}: need 0 <= n_P <= n <= T, got n_P={n_P} n={n} T={T}")
+    code = _code(Psi, who)
+    k, k_sb, k_st = _rows3(Psi)
+    v, v_sb, v_st = _rows3(Vb)
+    F = torch.empty(nb, N0, R, P, device=Psi.device, dtype=torch.float32)
+    if F_glob is not None:
+        if F_glob.shape != (nb, R, P) or F_glob.dtype != torch.float32 or not F_glob.is_contiguous():
+            raise ValueError(f"{who}: F_glob must be contiguous fp32 ({nb}, {R}, {P})")
+    wsb = _lib.query("smat_pool_workspace_bytes", nb, n_P, n, N0, R, P)
+    ws = torch.empty(max(wsb, 1), device=Psi.device, dtype=torch.uint8) if wsb else None
+    call("smat_pool", code, k.data_ptr(), v.data_ptr(), F.data_ptr(), ptr(F_glob), nb, n_P, n,
+         N0, R, P, k_sb, k_st, v_sb, v_st, ptr(ws), wsb, stream_of(k))
+    return F
+
+
+# ---------------------------------------------------------------------------
+# schedule stages the reference runs in torch
+# ---------------------------------------------------------------------------
+
+def chunk_states(Psi, Vb, C: int):
+    """``D_c = Psi_c^T Vb_c`` for the chunks of width ``C``: fp32 ``(nb, nc, r, p)``."""
+    who = "chunk_states"
+    _on_gpu(who, Psi, Vb)
+    nb, T, R = Psi.shape
+    P = Vb.shape[-1]
+    code = _code(Psi, who)
+    k, k_sb, k_st = _rows3(Psi)
+    v, v_sb, v_st = _rows3(Vb)
+    nc = -(-T // C)
+    D = torch.empty(nb, nc, R, P, device=Psi.device, dtype=torch.float32)
+    call("smat_chunk_states", code, k.data_ptr(), v.data_ptr(), D.data_ptr(), nb, T, C, R, P,
+         k_sb, k_st, v_sb, v_st, stream_of(k))
+    return D
+
+
+def segment_scan(D, nc0: int):
+    """Shifted exclusive scan of ``D (nb, nc, r, p)`` with one reset at chunk ``nc0``."""
+    who = "segment_scan"
+    _on_gpu(who, D)
+    nb, nc, R, P = D.shape
+    Dc = D.contiguous().float()
+    Sin = torch.empty_like(Dc)
+    call("smat_segment_scan", Dc.data_ptr(), Sin.data_ptr(), nb, nc, nc0, R * P, stream_of(Dc))
+    return Sin
+
+
+def query(Phi_rec, U):
+    """``Y[i] = Phi_rec[i] U_{i mod B}``: fp32 ``(nb, T_R, p)``."""
+    who = "query"
+    _on_gpu(who, Phi_rec, U)
+    nb, T_R, R = Phi_rec.shape
+    B, P = U.shape[1], U.shape[-1]
+    code = _code(Phi_rec, who)
+    q, q_sb, q_st = _rows3(Phi_rec)
+    Uc = U.contiguous().float()
+    Y = torch.empty(nb, T_R, P, device=U.device, dtype=torch.float32)
+    call("smat_query", code, q.data_ptr(), Uc.data_ptr(), Y.data_ptr(), nb, T_R, B, R, P,
+         q_sb, q_st, Y.stride(0), Y.stride(1), stream_of(Uc))
+    return Y
+
+
+def normalise(H, n: int, Y=None, g=None):
+    """``(H + [0; Y])[..., :-1] / (H + [0; Y])[..., -1:]``, times ``g`` when given."""
+    who = "normalise"
+    _on_gpu(who, H, Y, g)
+    nb, T, P = H.shape
+    Hc = _fp32_rows(H)
+    Yc = _fp32_rows(Y) if Y is not None else None
+    gc = g.float().contiguous() if g is not None else None
+    out = torch.empty(nb, T, P - 1, device=H.device, dtype=torch.float32)
+    call("smat_normalise", Hc.data_ptr(), ptr(Yc), ptr(gc), out.data_ptr(), nb, T, n, P,
+         Hc.stride(0), Hc.stride(1), Yc.stride(0) if Yc is not None else 0,
+         Yc.stride(1) if Yc is not None else 0, out.stride(0), out.stride(1),
+         gc.stride(0) if gc is not None else 0, stream_of(Hc))
+    return out
+
+
+def forward_workspace_bytes(nb, T, n, N0, B, n_P, C, r, p) -> int:
+    return _lib.query("smat_forward_workspace_bytes", nb, T, n, N0, B, n_P, C, r, p)
+
+
+def forward(Phi, Psi, Vb, idx, deg: int, *, n: int, n_P: int, N0: int, B: int, chunk: int,
+            indptr=None, g=None, out=None, H_out=None, workspace=None):
+    """The whole forward schedule in one call; returns fp32 ``(nb, T, p-1)``."""
+    who = "forward"
+    _on_gpu(who, Phi, Psi, Vb, idx, indptr, g, out, H_out)
+    nb, T, R = Phi.shape
+    P = Vb.shape[-1]
+    if Psi.dtype != Phi.dtype or Vb.dtype != Phi.dtype:
+        raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
+    code = _code(Phi, who)
+    q, q_sb, q_st = _rows3(Phi)
+    k, k_sb, k_st = _rows3(Psi)
+    v, v_sb, v_st = _rows3(Vb)
+    if out is None:
+        out = torch.empty(nb, T, P - 1, device=Phi.device, dtype=torch.float32)
+    if H_out is not None and (H_out.shape != (nb, T, P) or not H_out.is_contiguous()
+                              or H_out.dtype != torch.float32):
+        raise ValueError(f"{who}: H_out must be contiguous fp32 ({nb}, {T}, {P})")
+    gc = g.float().contiguous() if g is not None else None
+    need = forward_workspace_bytes(nb, T, n, N0, B, n_P, chunk, R, P)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need + 256, device=Phi.device, dtype=torch.uint8)
+    base = workspace.data_ptr()
+    aligned = (base + 255) & ~255
+    avail = workspace.numel() - (aligned - base)
+    call("smat_forward", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), idx.data_ptr(),
+         int(idx.dtype == torch.int64), ptr(indptr), deg, out.data_ptr(), ptr(H_out), ptr(gc),
+         nb, T, n, n_P, N0, B, chunk, R, P, q_sb, q_st, k_sb, k_st, v_sb, v_st,
+         out.stride(0), out.stride(1), gc.stride(0) if gc is not None else 0,
+         aligned, avail, stream_of(q))
+    return out
+
+
+def decode_step(Phi_t, Psi_t, Vb_t, S_in, S_out, U, step: int, *, out=None, o_full=None):
+    """One decode step for a batch; returns fp32 ``(nb, p-1)`` and writes ``S_out``."""
+    who = "decode_step"
+    _on_gpu(who, Phi_t, Psi_t, Vb_t, S_in, S_out, U)
+    nb, R = Phi_t.shape
+    P = Vb_t.shape[-1]
+    B = U.shape[1]
+    code = _code(Phi_t, who)
+    for t in (Phi_t, Psi_t, Vb_t):
+        if t.stride(-1) != 1:
+            raise ValueError(f"{who}: feature rows must be contiguous")
+    for t in (S_in, S_out, U):
+        if not t.is_contiguous() or t.dtype != torch.float32:
+            raise ValueError(f"{who}: S and U must be contiguous fp32")
+    if out is None:
+        out = torch.empty(nb, P - 1, device=Phi_t.device, dtype=torch.float32)
+    call("smat_decode_step", code, Phi_t.data_ptr(), Psi_t.data_ptr(), Vb_t.data_ptr(),
+         S_in.data_ptr(), S_out.data_ptr(), U.data_ptr(), out.data_ptr(), ptr(o_full), nb, B, R,
+         P, int(step), Phi_t.stride(0), Psi_t.stride(0), Vb_t.stride(0), stream_of(U))
+    return out

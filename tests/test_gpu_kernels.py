@@ -1,0 +1,299 @@
+"""HIP kernels vs the CPU oracle on identical seeded inputs (GPU only).
+
+Each drop-in function is compared with the oracle's restatement of the
+reference's torch branch (oracle/schedule.py); the whole schedule is compared
+with the fp64 oracle.  Tolerances:
+  * fp32 inputs: max|got - ref| / max|ref| < 1e-5 against fp64 on the same values
+    (the bar stated for fp32), except where noted;
+  * bf16 inputs: O within 2e-2 absolute and log-normaliser within 1e-3
+    absolute of the reference torch path (the bar stated for bf16);
+  * pooled tables / chunk summaries from bf16 inputs are exact products summed
+    in fp32, so they are held to 1e-5 relative against fp64 as well.
+"""
+import math
+
+import pytest
+import torch
+
+import oracle.schedule as O
+from smat_attention_amd import attention as A
+from smat_attention_amd.kernels import hip_fwd as K
+from smat_attention_amd.mask import build_mask
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _rel(got, ref):
+    got, ref = got.double().cpu(), ref.double().cpu()
+    return ((got - ref).abs().max() / ref.abs().max().clamp_min(1e-300)).item()
+
+
+def _feats(nb, T, hd, dt, seed=0, k_scale=1.0, q_scale=1.0, v_scale=1.0, r=None):
+    r = r or hd
+    Q, Kk, V = O.seeded_qkv(nb, T, hd, hd, seed=seed, dtype=torch.float32,
+                            q_scale=q_scale, k_scale=k_scale, v_scale=v_scale)
+    phi = O.make_phi(hd, r, dtype=torch.float32, seed=0)
+    Phi, Psi, Vb = O.featurise(Q, Kk, V, phi)
+    return Phi.to(dt), Psi.to(dt), Vb.to(dt)
+
+
+# ---------------------------------------------------------------------------
+# drop-in kernels
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("C,r,p", [(128, 128, 129), (128, 64, 65), (64, 32, 33), (256, 64, 65)])
+def test_chunk_local(dt, C, r, p):
+    _say("chunk_local", dt, C, r, p)
+    nb, nc = 2, 3
+    g = torch.Generator().manual_seed(1)
+    Phi = (torch.rand(nb, nc, C, r, generator=g) + 0.5).to(dt)
+    Psi = (torch.rand(nb, nc, C, r, generator=g) + 0.5).to(dt)
+    Vb = torch.randn(nb, nc, C, p, generator=g).to(dt)
+    Sin = torch.randn(nb, nc, r, p, generator=g) * 10
+    got = K.chunk_local(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), Sin.to(DEV))
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32 and got.shape == (nb, nc, C, p)
+    if dt == torch.float32:
+        ref = O.chunk_local(Phi.double(), Psi.double(), Vb.double(), Sin.double())
+        assert _rel(got, ref) < 1e-5
+    else:
+        # the reference's own path: score tile rounded to the input dtype
+        ref = O.chunk_local(Phi, Psi, Vb, Sin, torch.float32)
+        assert _rel(got, ref) < 1e-2
+        # and the exact product on the same inputs, up to that rounding
+        ref64 = O.chunk_local(Phi.double(), Psi.double(), Vb.double(), Sin.double())
+        assert _rel(got, ref64) < 3e-2
+
+
+def test_chunk_local_ragged_and_strided_vb():
+    _say("chunk_local ragged C=100, padded Vb rows")
+    nb, nc, C, r, p = 2, 2, 100, 64, 65
+    g = torch.Generator().manual_seed(2)
+    Phi = torch.rand(nb, nc, C, r, generator=g) + 0.5
+    Psi = torch.rand(nb, nc, C, r, generator=g) + 0.5
+    Vb = torch.randn(nb, nc, C, p, generator=g)
+    Sin = torch.randn(nb, nc, r, p, generator=g)
+    buf = torch.zeros(nb, nc, C, 72, device=DEV)
+    buf[..., :p] = Vb.to(DEV)
+    got = K.chunk_local(Phi.to(DEV), Psi.to(DEV), buf[..., :p], Sin.to(DEV))
+    ref = O.chunk_local(Phi.double(), Psi.double(), Vb.double(), Sin.double())
+    assert _rel(got, ref) < 1e-5
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,d,n_P", [(4096, 2, 0), (4096, 3, 0), (8192, 3, 0), (2048, 3, 16),
+                                     (4096, 1, 0)])
+def test_pool(dt, T, d, n_P):
+    _say("pool", dt, T, d, n_P)
+    spec = build_mask(T, d, chunk=128, n_P=n_P)
+    Phi, Psi, Vb = _feats(2, T, 32, dt, seed=3)
+    Fg = torch.empty(2, 32, 33, device=DEV) if n_P else None
+    F = K.pool(Psi.to(DEV), Vb.to(DEV), spec.n_P, spec.n, spec.N0, F_glob=Fg)
+    ref = O.pool_profiles(Psi.double(), Vb.double(), spec)
+    assert F.shape == ref.shape and F.dtype == torch.float32
+    assert _rel(F, ref) < 1e-5
+    if n_P:
+        gref = Psi[:, :n_P].double().transpose(-1, -2) @ Vb[:, :n_P].double()
+        assert _rel(Fg, gref) < 1e-5
+    assert K.pool_ok(spec.N0, -(-(spec.n - spec.n_P) // spec.N0), 33)
+
+
+@pytest.mark.parametrize("T,d", [(4096, 2), (4096, 3), (8192, 4), (1024, 3)])
+def test_incidence(T, d):
+    _say("incidence", T, d)
+    spec = A.to_device(build_mask(T, d, chunk=128), DEV)
+    g = torch.Generator().manual_seed(4)
+    F = torch.randn(2, spec.N0, 32, 33, generator=g)
+    U = K.incidence(F.to(DEV), spec.plane_pts_t, spec.B)
+    ref = O.apply_incidence(F.double(), spec)
+    assert _rel(U, ref) < 1e-6
+    # int32 table and the schedule-level wrapper give the same answer
+    U2 = A.apply_incidence(F.to(DEV), spec)
+    assert torch.equal(U, U2)
+
+
+def test_incidence_ragged_endpoint_csr():
+    _say("incidence ragged (endpoint mask, CSR)")
+    spec = A.to_device(build_mask(256, 8, chunk=8), DEV)
+    assert spec.kind == "endpoint" and not spec.uniform_deg
+    g = torch.Generator().manual_seed(5)
+    F = torch.randn(2, spec.N0, 16, 17, generator=g)
+    U = A.apply_incidence(F.to(DEV), spec)
+    ref = O.apply_incidence_csr(F.double(), spec)
+    assert _rel(U, ref) < 1e-6
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,d,r,p", [(4096, 3, 32, 33), (8192, 2, 64, 65), (4096, 1, 128, 129),
+                                     (32768, 3, 128, 129)])
+def test_query(dt, T, d, r, p):
+    _say("query", dt, T, d, r, p)
+    spec = build_mask(T, d, chunk=128)
+    g = torch.Generator().manual_seed(6)
+    Phi = (torch.rand(2, spec.T_R, r, generator=g) + 0.5).to(dt)
+    U = torch.randn(2, spec.B, r, p, generator=g)
+    Y = K.query(Phi.to(DEV), U.to(DEV))
+    ref = O.query_by_type(Phi.double(), U.double(), spec)
+    # 16-bit Phi is exact; U enters as hi + lo 16-bit parts (~2^-16 relative)
+    assert _rel(Y, ref) < (1e-5 if dt == torch.float32 else 2e-5)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_chunk_states_and_segment_scan(dt):
+    _say("chunk_states + segment_scan", dt)
+    nb, T, C, r, p, n = 2, 2048 + 77, 128, 64, 65, 1024
+    Phi, Psi, Vb = _feats(nb, T, 64, dt, seed=7)
+    D = K.chunk_states(Psi.to(DEV), Vb.to(DEV), C)
+    pad = (-T) % C
+    Psi_p = torch.nn.functional.pad(Psi.double(), (0, 0, 0, pad))
+    Vb_p = torch.nn.functional.pad(Vb.double(), (0, 0, 0, pad))
+    nc = (T + pad) // C
+    Dref, Sref = O.chunk_states(Psi_p.reshape(nb, nc, C, r), Vb_p.reshape(nb, nc, C, p), n, C,
+                                torch.float64)
+    assert _rel(D, Dref) < 1e-5
+    Sin = K.segment_scan(D, n // C)
+    assert _rel(Sin, Sref) < 1e-5
+    # the reset: the first chunk of each segment sees a zero state, exactly
+    assert torch.count_nonzero(Sin[:, 0]).item() == 0
+    assert torch.count_nonzero(Sin[:, n // C]).item() == 0
+
+
+# ---------------------------------------------------------------------------
+# the whole schedule
+# ---------------------------------------------------------------------------
+
+def _check_forward(spec, Phi, Psi, Vb, *, dt, g=None, label=""):
+    Pd, Sd, Wd = (x.to(DEV) for x in (Phi, Psi, Vb))
+    gd = g.to(DEV) if g is not None else None
+    out, parts = A.smat_attention(Pd, Sd, Wd, spec, g=gd, return_parts=True)
+    fused = A.smat_attention(Pd, Sd, Wd, spec, g=gd)
+    torch.cuda.synchronize()
+    ref64, p64 = O.smat_attention(Phi.double(), Psi.double(), Vb.double(), spec, g=g,
+                                  return_parts=True)
+    lse = torch.log(parts["H"][..., -1].double().cpu())
+    lse64 = torch.log(p64["H"][..., -1])
+    e_fused = (fused - out).abs().max().item()
+    if dt == torch.float32:
+        rel = _rel(out, ref64)
+        _say(label, f"fp32 rel {rel:.2e}, lse {((lse - lse64).abs().max().item()):.2e}")
+        assert rel < 1e-5
+        assert (lse - lse64).abs().max().item() < 1e-5
+    else:
+        refbf, pbf = O.smat_attention(Phi, Psi, Vb, spec, g=g, return_parts=True)
+        lsebf = torch.log(pbf["H"][..., -1].double())
+        e_o = (out.double().cpu() - refbf.double()).abs().max().item()
+        e_l = (lse - lsebf).abs().max().item()
+        e_o64 = (out.double().cpu() - ref64).abs().max().item()
+        e_l64 = (lse - lse64).abs().max().item()
+        _say(label, f"vs torch path: O {e_o:.2e} lse {e_l:.2e}; vs fp64: O {e_o64:.2e} "
+                    f"lse {e_l64:.2e}")
+        assert e_o < 2e-2 and e_l < 1e-3
+        assert e_o64 < 2e-2 and e_l64 < 1e-3
+    assert e_fused <= 1e-6 * max(1.0, out.abs().max().item())
+    return out
+
+
+def test_forward_plumbing_config_fp32():
+    """nb=4 (B=1, H=4), T=1024, d=2, head_dim=64, fp32, q,k,v ~ N(0,1) seed 0."""
+    _say("forward T=1024 d=2 nb=4 hd=64 fp32")
+    spec = build_mask(1024, 2, chunk=128)
+    Phi, Psi, Vb = _feats(4, 1024, 64, torch.float32, seed=0)
+    _check_forward(spec, Phi, Psi, Vb, dt=torch.float32, label="T=1024 d=2")
+    # and against the O(T^2) definition under the materialised mask
+    M = torch.from_numpy(__import__("smat_attention_amd.mask", fromlist=["x"]).materialise(spec))
+    dense = O.dense_masked_kernel_attention(Phi.double(), Psi.double(), Vb.double(), M)
+    got = A.smat_attention(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), spec)
+    assert _rel(got, dense) < 1e-5
+
+
+@pytest.mark.parametrize("T,d,n_P", [(2048, 3, 0), (2048, 3, 16), (4096, 4, 0), (2000, 3, 0),
+                                     (1024, 1, 0), (4096, 2, 0)])
+def test_forward_fp32_small(T, d, n_P):
+    _say("forward fp32", T, d, n_P)
+    spec = build_mask(T, d, chunk=128, n_P=n_P)
+    Phi, Psi, Vb = _feats(2, T, 32, torch.float32, seed=11)
+    g = torch.rand(2, T, generator=torch.Generator().manual_seed(12)) + 0.5
+    _check_forward(spec, Phi, Psi, Vb, dt=torch.float32, g=g, label=f"T={T} d={d}")
+
+
+def test_forward_single_gpu_d2_bf16():
+    """nb=32 (B=4, H=8), T=8192, d=2, head_dim=64, bf16, q,k,v ~ N(0,1)/sqrt(64)."""
+    _say("forward T=8192 d=2 nb=32 hd=64 bf16")
+    spec = build_mask(8192, 2, chunk=128)
+    Phi, Psi, Vb = _feats(32, 8192, 64, torch.bfloat16, seed=0, q_scale=1 / 8, k_scale=1 / 8,
+                          v_scale=1 / 8)
+    _check_forward(spec, Phi, Psi, Vb, dt=torch.bfloat16, label="T=8192 d=2")
+
+
+def test_forward_long_prefill_d3_bf16_T32768():
+    """B=1, H=8, head_dim=128, d=3, T=32768, bf16, k scaled 1/sqrt(128); heads 0-1 vs the oracle."""
+    _say("forward T=32768 d=3 nb=8 hd=128 bf16")
+    T = 32768
+    spec = build_mask(T, 3, chunk=128)
+    Phi, Psi, Vb = _feats(8, T, 128, torch.bfloat16, seed=0, k_scale=128 ** -0.5)
+    out = A.smat_attention(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), spec)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _check_forward(spec, Phi[:2], Psi[:2], Vb[:2], dt=torch.bfloat16, label="T=32768 d=3 heads 0-1")
+    sub = A.smat_attention(Phi[:2].to(DEV), Psi[:2].to(DEV), Vb[:2].to(DEV), spec)
+    assert torch.equal(sub, out[:2])     # heads are independent and deterministic
+
+
+def test_exact_non_influence():
+    """A landmark payload outside a recent row's mask leaves that row bit-identical
+    (the reference's test_smat.py:292-324, on the GPU path)."""
+    _say("non-influence T=2048 d=3 fp32")
+    T, d = 2048, 3
+    spec = build_mask(T, d, chunk=128)
+    Phi, Psi, Vb = _feats(1, T, 32, torch.float32, seed=13)
+    base = A.smat_attention(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), spec).cpu()
+    M = __import__("smat_attention_amd.mask", fromlist=["x"]).materialise(spec)
+    j = spec.planted_cols[0]
+    Vb2 = Vb.clone()
+    Vb2[:, j, :-1] += 1e3
+    pert = A.smat_attention(Phi.to(DEV), Psi.to(DEV), Vb2.to(DEV), spec).cpu()
+    rows_out = [i for i in range(spec.n, T) if M[i, j] == 0]
+    rows_in = [i for i in range(spec.n, T) if M[i, j] == 1]
+    assert rows_out and rows_in
+    assert torch.equal(pert[:, rows_out], base[:, rows_out])
+    assert not torch.equal(pert[:, rows_in], base[:, rows_in])
+
+
+def test_fp64_is_refused():
+    _say("fp64 refused")
+    spec = build_mask(1024, 2, chunk=128)
+    x = torch.rand(1, 1024, 8, device=DEV, dtype=torch.float64)
+    with pytest.raises(TypeError):
+        A.smat_attention(x, x, torch.rand(1, 1024, 9, device=DEV, dtype=torch.float64), spec)
+
+
+# ---------------------------------------------------------------------------
+# decode
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,d", [(2048, 3), (4096, 2), (1024, 1)])
+def test_decode_matches_prefill(dt, T, d):
+    _say("decode", dt, T, d)
+    spec = build_mask(T, d, chunk=128)
+    Phi, Psi, Vb = _feats(3, T, 32, dt, seed=14)
+    Pd, Sd, Wd = (x.to(DEV) for x in (Phi, Psi, Vb))
+    pre = A.smat_attention(Pd, Sd, Wd, spec).cpu()
+    n = spec.n
+    dec = A.SmatDecoder(Sd[:, :n], Wd[:, :n], spec)
+    steps = min(300, spec.T_R)
+    outs = [dec.step(Pd[:, n + i], Sd[:, n + i], Wd[:, n + i]) for i in range(steps)]
+    got = torch.stack(outs, 1).cpu()
+    ref64 = O.smat_attention(Phi.double(), Psi.double(), Vb.double(), spec)[:, n:n + steps]
+    if dt == torch.float32:
+        assert _rel(got, ref64) < 1e-5
+        assert _rel(got, pre[:, n:n + steps]) < 1e-5
+    else:
+        assert (got.double() - ref64).abs().max().item() < 2e-2
+    assert dec.cache_words() == 3 * (spec.B + 1) * 32 * 33
