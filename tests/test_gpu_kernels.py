@@ -193,8 +193,11 @@ def _check_forward(spec, Phi, Psi, Vb, *, dt, g=None, label=""):
         e_l64 = (lse - lse64).abs().max().item()
         _say(label, f"vs torch path: O {e_o:.2e} lse {e_l:.2e}; vs fp64: O {e_o64:.2e} "
                     f"lse {e_l64:.2e}")
+        # the bar: the reference's torch path on the same bf16 inputs
         assert e_o < 2e-2 and e_l < 1e-3
-        assert e_o64 < 2e-2 and e_l64 < 1e-3
+        # the exact schedule on the same values differs by the reference's own
+        # rounding of the score tile to bf16 (up to 2^-8 on a one-term row)
+        assert e_o64 < 2e-2 and e_l64 < 1e-2
     assert e_fused <= 1e-6 * max(1.0, out.abs().max().item())
     return out
 
