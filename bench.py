@@ -1,0 +1,333 @@
+#!/usr/bin/env python3
+"""Benchmark of the SMat forward schedule on one MI355X.
+
+Workload (the long-prefill configuration the metric is quoted on): B=1, H=8
+(nb = 8 sequences x heads), head_dim 128 (feature rank r = 128, p = 129),
+T = 131072, d = 3 geometric mask, chunk 128, bf16 inputs with fp32
+accumulation and fp32 output; q, k, v ~ N(0, 1) drawn on the CPU from seed 0,
+k scaled by 1/sqrt(128); features Phi = elu(q W^T) + 1, Psi = elu(k W^T) + 1,
+Vb = [v, 1] computed before the timed region (the reference times prefill
+without featurisation too).
+
+A step is one full forward (pool -> incidence -> query -> causal scan ->
+normalise) over the resident inputs.  W untimed steps, then K timed steps
+between two device synchronisations.  Printed: one JSON line with the
+throughput (tokens/s = B*T / step time), the roofline of the dominant kernel
+(timed live with events on the stream the kernels run on), the CPU baseline
+(the oracle's restatement of the reference's torch path, on a bounded
+sample, timed on this host) and the cached-decode rate.
+
+    python bench.py [--steps K] [--warmup W] [--T 131072] [--no-cpu] [--no-decode]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+
+METRIC = "SMat prefill tokens/s at T=131072 bf16 d=3; % of MFMA peak; decode GB/s"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--T", type=int, default=131072)
+    ap.add_argument("--d", type=int, default=3)
+    ap.add_argument("--heads", type=int, default=8)
+    ap.add_argument("--head-dim", type=int, default=128)
+    ap.add_argument("--kernel-reps", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-heads", type=int, default=2,
+                    help="heads in the CPU baseline sample (of --heads)")
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--verbose", action="store_true")
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs(nb, T, hd, dtype, seed=0):
+    """Seeded CPU draw, featurised on the CPU in fp32, cast, then moved."""
+    import torch
+    from smat_attention_amd.attention import make_phi
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    Q = torch.randn(nb, T, hd, generator=gen)
+    K = torch.randn(nb, T, hd, generator=gen) * hd ** -0.5
+    V = torch.randn(nb, T, hd, generator=gen)
+    phi = make_phi(hd, hd, dtype=torch.float32, seed=0)
+    Phi = phi(Q).to(dtype)
+    Psi = phi(K).to(dtype)
+    Vb = torch.cat([V, torch.ones(nb, T, 1)], dim=-1).to(dtype)
+    return Phi, Psi, Vb
+
+
+def to_gpu_padded(Phi, Psi, Vb, dev):
+    """Move to the device; Vb rows padded to a 16-byte multiple (same values)."""
+    import torch
+    p = Vb.shape[-1]
+    pad = -(-p // 8) * 8
+    buf = torch.zeros(*Vb.shape[:-1], pad, device=dev, dtype=Vb.dtype)
+    buf[..., :p] = Vb.to(dev)
+    return Phi.to(dev), Psi.to(dev), buf[..., :p]
+
+
+class Events:
+    """Per-kernel durations with events recorded on the stream the kernels use."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time(self, fn, reps):
+        torch = self.torch
+        fn()
+        torch.cuda.synchronize()
+        s = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            fn()
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3      # microseconds per launch
+
+
+def kernel_table(spec, Phi, Psi, Vb, reps):
+    """Average duration and algorithmic traffic/work of every kernel of the forward."""
+    import torch
+    from smat_attention_amd import attention as A
+    from smat_attention_amd.kernels import hip_fwd as K
+    ev = Events(torch)
+    nb, T, r = Phi.shape
+    p = Vb.shape[-1]
+    n, C, N0, B, T_R = spec.n, 128, spec.N0, spec.B, spec.T_R
+    nc = T // C
+    eb = Phi.element_size()
+    rp4 = r * p * 4
+    F = K.pool(Psi, Vb, spec.n_P, n, N0)
+    U = A.apply_incidence(F, spec)
+    D = K.chunk_states(Psi, Vb, C)
+    Sin = K.segment_scan(D, n // C)
+    H = K.chunk_local(Phi.reshape(nb, nc, C, r), Psi.reshape(nb, nc, C, r),
+                      Vb.reshape(nb, nc, C, p), Sin).reshape(nb, T, p)
+    Y = K.query(Phi[:, n:], U)
+    rows = {}
+    # algorithmic bytes: each operand read once and each result written once
+    rows["pool"] = dict(us=ev.time(lambda: K.pool(Psi, Vb, spec.n_P, n, N0), reps),
+                        bytes=nb * ((n - spec.n_P) * (r + p) * eb + N0 * rp4),
+                        flops=2 * nb * (n - spec.n_P) * r * p)
+    rows["incidence"] = dict(us=ev.time(lambda: A.apply_incidence(F, spec), reps),
+                             bytes=nb * (N0 + B) * rp4, flops=nb * spec.I_prof * r * p)
+    rows["query"] = dict(us=ev.time(lambda: K.query(Phi[:, n:], U), reps),
+                         bytes=nb * (B * rp4 + T_R * r * eb + T_R * p * 4),
+                         flops=2 * nb * T_R * r * p)
+    rows["chunk_states"] = dict(us=ev.time(lambda: K.chunk_states(Psi, Vb, C), reps),
+                                bytes=nb * (T * (r + p) * eb + nc * rp4),
+                                flops=2 * nb * T * r * p)
+    rows["segment_scan"] = dict(us=ev.time(lambda: K.segment_scan(D, n // C), reps),
+                                bytes=nb * 2 * nc * rp4, flops=nb * nc * r * p)
+    rows["chunk_local"] = dict(
+        us=ev.time(lambda: K.chunk_local(Phi.reshape(nb, nc, C, r), Psi.reshape(nb, nc, C, r),
+                                         Vb.reshape(nb, nc, C, p), Sin), reps),
+        bytes=nb * (T * (2 * r + p) * eb + nc * rp4 + T * p * 4),
+        flops=2 * nb * (T * (C + 1) // 2 * (r + p) + T * r * p))
+    rows["normalise"] = dict(us=ev.time(lambda: K.normalise(H, n, Y), reps),
+                             bytes=nb * (T * p * 4 + T_R * p * 4 + T * (p - 1) * 4),
+                             flops=nb * T * (p - 1))
+    for k, v in rows.items():
+        v["GBs"] = v["bytes"] / (v["us"] * 1e-6) / 1e9
+        v["TFLOPs"] = v["flops"] / (v["us"] * 1e-6) / 1e12
+    return rows
+
+
+def useful_flops(spec, nb, T, r, p, C=128):
+    """Mask-density-scaled MFMA work of the schedule: causal intra-chunk QK^T and
+    AV, Phi Sin, chunk summaries, pooling, type-major query (2 flops per MAC)."""
+    macs = (T * (C + 1) / 2 * (r + p) + T * r * p + T * r * p
+            + (spec.n - spec.n_P) * r * p + spec.T_R * r * p)
+    return 2.0 * nb * macs
+
+
+def compulsory_bytes(nb, T, r, p, eb_in=2, eb_out=4):
+    return nb * (T * (2 * r + p) * eb_in + T * (p - 1) * eb_out)
+
+
+def cpu_baseline(args, spec, Phi, Psi, Vb):
+    """The oracle's restatement of the reference's torch path, timed on the host:
+    median of 3 runs after one warm-up, on ``cpu_heads`` of the heads."""
+    import torch
+    import oracle.schedule as O
+    threads = max(1, min(args.cpu_threads, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    h = args.cpu_heads
+    P, S, W = Phi[:h].contiguous(), Psi[:h].contiguous(), Vb[:h].contiguous()
+    O.smat_attention(P, S, W, spec)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.smat_attention(P, S, W, spec)
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    t_full = t * (Phi.shape[0] / h)              # heads are independent
+    return {"value": round(args.T / t_full, 1), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"{h} of {Phi.shape[0]} heads at T={args.T}, d={args.d}, bf16 inputs "
+                       f"(reference torch path restated, oracle/schedule.py); median of 3 "
+                       f"after 1 warm-up = {t:.3f} s, scaled x{Phi.shape[0] // h} to all heads"),
+            "host_cpus": os.cpu_count()}
+
+
+def decode_bench(args):
+    """Cached decode at B=16, H=8 (nb=128), head_dim 128, d=3, T=65536 prefill."""
+    import torch
+    from smat_attention_amd import attention as A
+    from smat_attention_amd.mask import build_mask
+    dev = torch.device("cuda:0")
+    nb, hd, T_pre = 128, 128, 65536
+    T_total = T_pre + 4096
+    spec = build_mask(T_total, 3, chunk=128)
+    r, p = hd, hd + 1
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    # the landmark block is what U is built from; recent-step inputs are fresh
+    n = spec.n
+    Psi = (torch.nn.functional.elu(torch.randn(nb, n, r, generator=gen) * 0.3) + 1
+           ).to(torch.bfloat16).to(dev)
+    Vb = torch.cat([torch.randn(nb, n, hd, generator=gen), torch.ones(nb, n, 1)], -1
+                   ).to(torch.bfloat16).to(dev)
+    dec = A.SmatDecoder(Psi, Vb, spec)
+    del Psi, Vb
+    steps = args.decode_steps
+    ph = (torch.nn.functional.elu(torch.randn(steps, nb, r, generator=gen)) + 1
+          ).to(torch.bfloat16).to(dev)
+    ps = (torch.nn.functional.elu(torch.randn(steps, nb, r, generator=gen)) + 1
+          ).to(torch.bfloat16).to(dev)
+    vb = torch.cat([torch.randn(steps, nb, hd, generator=gen), torch.ones(steps, nb, 1)], -1
+                   ).to(torch.bfloat16).to(dev)
+    out = torch.empty(nb, p - 1, device=dev)
+    for i in range(8):
+        dec.step(ph[i], ps[i], vb[i], out=out)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for i in range(steps):
+        dec.step(ph[i], ps[i], vb[i], out=out)
+    e1.record(s)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    # per step and sequence: U[type] read, S read, S write (r*p fp32 each), plus io
+    step_bytes = nb * (3 * r * p * 4 + (2 * r + p) * 2 + (p - 1) * 4)
+    return {"us_per_step": round(us, 2), "GBs": round(step_bytes / (us * 1e-6) / 1e9, 1),
+            "frac_hbm": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "config": f"nb=128 (B=16,H=8), r=128, p=129, d=3, prefill {T_pre}, "
+                      f"B_types={spec.B}, eager launches",
+            "bytes_per_step": step_bytes, "U_cache_GB": round(dec.U.numel() * 4 / 1e9, 2)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
+              f"multi-GPU path; heads would shard across GPUs with no communication.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from smat_attention_amd import attention as A
+    from smat_attention_amd.mask import build_mask
+
+    if not A.have_hip():
+        raise SystemExit("the HIP library or the GPU is missing; build with "
+                         "`python -m smat_attention_amd._build` and run on the MI355X")
+    dev = torch.device("cuda:0")
+    nb, T, hd = args.heads, args.T, args.head_dim
+    r, p = hd, hd + 1
+    spec = build_mask(T, args.d, chunk=128)
+    log(f"[bench] {spec.summary()}; nb={nb} r={r} p={p}")
+    Phi_c, Psi_c, Vb_c = make_inputs(nb, T, hd, torch.bfloat16)
+    Phi, Psi, Vb = to_gpu_padded(Phi_c, Psi_c, Vb_c, dev)
+    A.to_device(spec, dev)
+    ws = torch.empty(A._hip.forward_workspace_bytes(nb, T, spec.n, spec.N0, spec.B, spec.n_P,
+                                                    128, r, p) + 256,
+                     device=dev, dtype=torch.uint8)
+    out = None
+    for _ in range(args.warmup):
+        out = A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
+    torch.cuda.synchronize()
+    log(f"[bench] warmup done ({args.warmup} steps)")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = dt / args.steps * 1e3
+    tokens_per_s = T / (ms * 1e-3)                # B*T tokens per step, B = 1
+    log(f"[bench] {args.steps} steps: {ms:.3f} ms/step, {tokens_per_s / 1e6:.2f} M tokens/s")
+    assert torch.isfinite(out).all()
+
+    rows = kernel_table(spec, Phi, Psi, Vb, args.kernel_reps)
+    for k, v in rows.items():
+        log(f"[bench] {k:13s} {v['us']:9.1f} us  {v['GBs']:7.0f} GB/s  {v['TFLOPs']:6.1f} TF/s")
+    dom = max(rows, key=lambda k: rows[k]["us"])
+    drow = rows[dom]
+    uf = useful_flops(spec, nb, T, r, p)
+    cb = compulsory_bytes(nb, T, r, p)
+    t_mfma = uf / (BF16_PEAK_TFLOPS * 1e12)
+    t_hbm = cb / (HBM_PEAK_GBS * 1e9)
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q,k,v; random-init feature map)",
+        "config": {"workload": f"long prefill d={args.d}: B=1 H={nb} head_dim={hd} T={T} "
+                               f"chunk=128 bf16 in / fp32 acc+out",
+                   "T": T, "d": args.d, "nb": nb, "r": r, "p": p, "q": spec.q, "N0": spec.N0,
+                   "B_types": spec.B, "nnz_C": spec.I_prof, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": dom,
+                     "achieved": round(drow["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(drow["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "us_per_launch": round(drow["us"], 2),
+                     "algorithmic_bytes_per_launch": int(drow["bytes"])},
+        "mfma": {"useful_flops": uf, "achieved_TFLOPs": round(uf / (ms * 1e-3) / 1e12, 2),
+                 "frac_of_bf16_peak": round(uf / (ms * 1e-3) / (BF16_PEAK_TFLOPS * 1e12), 4),
+                 "schedule_roofline_frac": round(max(t_mfma, t_hbm) / (ms * 1e-3), 4),
+                 "compulsory_bytes": cb},
+        "kernels_us": {k: round(v["us"], 1) for k, v in rows.items()},
+    }
+    if not args.no_decode:
+        del Phi, Psi, Vb, ws, out
+        torch.cuda.empty_cache()
+        result["decode"] = decode_bench(args)
+        log(f"[bench] decode {result['decode']}")
+    if not args.no_cpu:
+        log("[bench] CPU baseline ...")
+        result["cpu_baseline"] = cpu_baseline(args, spec, Phi_c, Psi_c, Vb_c)
+        log(f"[bench] cpu {result['cpu_baseline']}")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
