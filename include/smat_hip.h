@@ -108,6 +108,17 @@ int smat_incidence(const float* F, const float* F_glob, const void* idx, int idx
                    int64_t rp, void* stream);
 
 /*
+ * Incidence for the d = 3 geometric mask with the lines generated in-kernel:
+ * row h is the line <a_e, x> = b of F_q^2 given by code[h] = e*q + b, where
+ * a_0 = (0, 1), a_e = (1, e-1) for e >= 1, and point x = x0*q + x1.  Same
+ * result as smat_incidence on that mask's table (up to fp32 summation order)
+ * without reading the table.  F, U, F_glob as for smat_incidence; N0 = q*q.
+ * Returns SMAT_EUNSUPPORTED when the F panel does not fit on chip.
+ */
+int smat_incidence_plane(const float* F, const float* F_glob, const int* code, int q,
+                         float* U, int nb, int N0, int B, int64_t rp, void* stream);
+
+/*
  * Type-major query  Y[i] = Phi_rec[i] U_{i mod B}, i in [0, T_R), fp32 out
  * (nb, T_R, p) with row stride y_st.  Phi_rec has dtype; U: (nb, B, r, p).
  * Replaces query_by_type, src/smat/attention.py:310-330.
@@ -132,6 +143,8 @@ int smat_normalise(const float* H, const float* Y, const float* g, float* out,
  * a geometric mask: pool -> incidence (+ global channel) -> query ->
  * chunk states -> segmented scan -> chunk-local pass -> normalise.
  * idx/indptr/deg describe C as for smat_incidence; B, N0, n, n_P from the spec.
+ * plane_code/q, when plane_code is not NULL, select smat_incidence_plane's
+ * generated lines instead of the table (d = 3 masks).
  * out: (nb, T, p-1) fp32 with row stride o_st; g optional.  H_out, if not
  * NULL, receives the unnormalised H (nb, T, p) fp32 contiguous.
  * workspace: smat_forward_workspace_bytes(...) bytes, 256-byte aligned.
@@ -140,6 +153,7 @@ int64_t smat_forward_workspace_bytes(int nb, int T, int n, int N0, int B, int n_
                                      int C, int r, int p);
 int smat_forward(int dtype, const void* phi, const void* psi, const void* vb,
                  const void* idx, int idx_is_64, const int64_t* indptr, int deg,
+                 const int* plane_code, int q,
                  float* out, float* H_out, const float* g,
                  int nb, int T, int n, int n_P, int N0, int B, int C, int r, int p,
                  int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,

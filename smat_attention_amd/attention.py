@@ -136,7 +136,11 @@ def to_device(spec: MaskSpec, device, *, want_direct: bool = False) -> MaskSpec:
     spec.C_indptr_t = torch.from_numpy(ptr_.astype(np.int64)).to(device)
     spec.C_indices_t = torch.from_numpy(ind.astype(np.int64)).to(device)
     spec.C_indices_i32_t = torch.from_numpy(ind.astype(np.int32)).to(device)
-    for t in (spec.C_indices_t, spec.C_indices_i32_t):
+    spec.C_indices_par_t = (torch.from_numpy(parity_interleaved_table(spec)).to(device)
+                            if spec.uniform_deg else spec.C_indices_i32_t)
+    codes = plane_line_codes(spec)
+    spec.plane_code_t = torch.from_numpy(codes).to(device) if codes is not None else None
+    for t in (spec.C_indices_t, spec.C_indices_i32_t, spec.C_indices_par_t):
         t._smat_checked_N0 = spec.N0
     if spec.uniform_deg:
         spec.plane_pts_t = spec.C_indices_t.view(spec.B, spec.uniform_deg)
@@ -150,6 +154,52 @@ def to_device(spec: MaskSpec, device, *, want_direct: bool = False) -> MaskSpec:
         spec.type_cols_t = torch.from_numpy(_type_columns(spec)).to(device)
     spec._smat_device = torch.device(device)
     return spec
+
+
+def plane_line_codes(spec: MaskSpec) -> Optional[np.ndarray]:
+    """``(B,)`` int32 codes ``e*q + b`` naming each row type's line of ``F_q^2``
+    (d = 3), for the incidence kernel that generates the points itself; None for
+    other masks.  Line ``e = 0`` is ``x1 = b``; line ``e >= 1`` is
+    ``x0 + (e-1) x1 = b (mod q)``, with point ``x = x0*q + x1``.  Every code is
+    checked here: the generated point set must equal the row of ``C``."""
+    if spec.kind != "geometric" or spec.d != 3 or not spec.uniform_deg:
+        return None
+    q, B = spec.q, spec.B
+    rows = np.sort(np.asarray(spec.C_indices, dtype=np.int64).reshape(B, q), axis=1)
+    x0, x1 = rows // q, rows % q
+    vertical = np.all(x1 == x1[:, :1], axis=1)          # e = 0: constant x1
+    # e >= 1: x0 + m x1 = b with m from two points of the row (x1 distinct there)
+    dx0 = (x0[:, 1] - x0[:, 0]) % q
+    dx1 = (x1[:, 0] - x1[:, 1]) % q
+    inv = np.array([pow(int(v), q - 2, q) if v else 0 for v in dx1], dtype=np.int64)
+    m = (dx0 * inv) % q
+    b = (x0[:, 0] + m * x1[:, 0]) % q
+    e = np.where(vertical, 0, m + 1)
+    b = np.where(vertical, x1[:, 0], b)
+    code = (e * q + b).astype(np.int64)
+    # regenerate every line and compare with the table
+    t = np.arange(q, dtype=np.int64)[None, :]
+    gen_vert = t * q + b[:, None]
+    gen_sl = ((b[:, None] - (e[:, None] - 1) * t) % q) * q + t
+    gen = np.sort(np.where(vertical[:, None], gen_vert, gen_sl), axis=1)
+    if not np.array_equal(gen, rows):
+        return None
+    return code.astype(np.int32)
+
+
+def parity_interleaved_table(spec: MaskSpec) -> np.ndarray:
+    """The ``(B*deg,)`` int32 point table with each row's points reordered for the
+    LDS incidence kernel: even point indices first on even rows, odd first on odd
+    rows (ascending within a parity).  The kernel reads the rows of two adjacent
+    hyperplanes in one LDS cycle; opposite parities put them in opposite bank
+    halves.  The same points per row, so the same U up to fp32 summation order."""
+    deg = spec.uniform_deg
+    pts = np.asarray(spec.C_indices, dtype=np.int64).reshape(spec.B, deg)
+    odd = (pts & 1).astype(np.int64)
+    first = (np.arange(spec.B) & 1)[:, None]                  # parity taken first
+    key = (odd != first).astype(np.int64) * (2 * spec.N0) + pts
+    order = np.argsort(key, axis=1, kind="stable")
+    return np.take_along_axis(pts, order, axis=1).reshape(-1).astype(np.int32)
 
 
 def _type_columns(spec: MaskSpec) -> np.ndarray:
@@ -175,9 +225,9 @@ def _staged(spec: MaskSpec, device) -> MaskSpec:
 
 def _incidence_args(spec: MaskSpec):
     """``(idx, indptr, deg)`` for the incidence kernel: the uniform ``(B, deg)``
-    table when there is one, else CSR."""
+    table (rows parity-interleaved) when there is one, else CSR."""
     if spec.uniform_deg:
-        return spec.C_indices_i32_t, None, int(spec.uniform_deg)
+        return spec.C_indices_par_t, None, int(spec.uniform_deg)
     return spec.C_indices_i32_t, spec.C_indptr_t, 0
 
 
@@ -237,13 +287,30 @@ def apply_incidence(F, spec: MaskSpec, *, backend: str = "auto", gather_chunk: i
     if not F.is_cuda:
         raise ValueError(f"{who}: F must be on the GPU")
     _staged(spec, F.device)
+    return _incidence(F, spec, None)
+
+
+def _incidence(F, spec: MaskSpec, F_glob):
+    """``C F`` (+ the global channel) through the fastest kernel the mask allows."""
     nb, N0, r, p = F.shape
     Ff = F.contiguous().float()
-    idx, indptr, deg = _incidence_args(spec)
     U = torch.empty(nb, spec.B, r, p, device=F.device, dtype=torch.float32)
-    _hip.call("smat_incidence", Ff.data_ptr(), None, idx.data_ptr(), 0, _hip.ptr(indptr), deg,
+    profiled = spec.n > spec.n_P
+    if profiled and getattr(spec, "plane_code_t", None) is not None and _plane_ok(spec, r * p):
+        _hip.call("smat_incidence_plane", Ff.data_ptr(), _hip.ptr(F_glob),
+                  spec.plane_code_t.data_ptr(), spec.q, U.data_ptr(), nb, N0, spec.B, r * p,
+                  _hip.stream_of(Ff))
+        return U
+    idx, indptr, deg = _incidence_args(spec)
+    _hip.call("smat_incidence", Ff.data_ptr(), _hip.ptr(F_glob), idx.data_ptr(), 0,
+              _hip.ptr(indptr) if profiled else None, deg if profiled else 0,
               U.data_ptr(), nb, N0, spec.B, r * p, _hip.stream_of(Ff))
     return U
+
+
+def _plane_ok(spec: MaskSpec, rp: int) -> bool:
+    """The generated-line kernel needs rp % 4 == 0 and an N0 x 4 float panel on chip."""
+    return rp % 4 == 0 and spec.N0 * 16 <= 150 * 1024
 
 
 def query_by_type(Phi_rec, U, spec: MaskSpec):
@@ -310,8 +377,10 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
     idx, indptr, deg = _incidence_args(spec)
 
     if timer is None and not return_parts:
+        pc = spec.plane_code_t if _plane_ok(spec, r * Vb.shape[-1]) else None
         return _hip.forward(Phi, Psi, Vb, idx, deg, n=n, n_P=spec.n_P, N0=spec.N0, B=spec.B,
-                            chunk=C, indptr=indptr, g=g, workspace=workspace)
+                            chunk=C, indptr=indptr, plane_code=pc, field_q=spec.q, g=g,
+                            workspace=workspace)
 
     tm = timer or (lambda name: nullcontext())
     parts: Dict[str, torch.Tensor] = {}
@@ -321,12 +390,7 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
                   if spec.n_P else None)
         F = _hip.pool(Psi, Vb, spec.n_P, n, spec.N0, F_glob=F_glob)
     with tm("lr_incidence"):
-        Ff = F.contiguous()
-        U = torch.empty(nb, spec.B, r, p, device=Phi.device, dtype=torch.float32)
-        profiled = n > spec.n_P
-        _hip.call("smat_incidence", Ff.data_ptr(), _hip.ptr(F_glob), idx.data_ptr(), 0,
-                  _hip.ptr(indptr) if profiled else None, deg if profiled else 0,
-                  U.data_ptr(), nb, spec.N0, spec.B, r * p, _hip.stream_of(Ff))
+        U = _incidence(F, spec, F_glob)
     with tm("lr_query"):
         Y_lr = _hip.query(Phi[:, n:], U)
     with tm("scan"):
@@ -377,12 +441,7 @@ class SmatDecoder:
         _staged(spec, dev)
         F_glob = torch.empty(nb, r, p, device=dev, dtype=torch.float32) if spec.n_P else None
         F = _hip.pool(Psi_prefix, Vb_prefix, spec.n_P, spec.n, spec.N0, F_glob=F_glob)
-        idx, indptr, deg = _incidence_args(spec)
-        self.U = torch.empty(nb, spec.B, r, p, device=dev, dtype=torch.float32)
-        profiled = spec.n > spec.n_P
-        _hip.call("smat_incidence", F.data_ptr(), _hip.ptr(F_glob), idx.data_ptr(), 0,
-                  _hip.ptr(indptr) if profiled else None, deg if profiled else 0,
-                  self.U.data_ptr(), nb, spec.N0, spec.B, r * p, _hip.stream_of(F))
+        self.U = _incidence(F, spec, F_glob)
         del F
         self._S = [torch.zeros(nb, r, p, device=dev, dtype=torch.float32),
                    torch.empty(nb, r, p, device=dev, dtype=torch.float32)]

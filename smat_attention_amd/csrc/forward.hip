@@ -45,6 +45,8 @@ int chunk_local_dispatch(int dtype, const void* phi, const void* psi, const void
 int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int idx_is_64,
                        const int64_t* indptr, int deg, float* U, int nb, int N0, int B, int64_t rp,
                        hipStream_t stream);
+int incidence_plane_dispatch(const float* F, const float* F_glob, const int* code, int q,
+                             float* U, int nb, int N0, int B, int64_t rp, hipStream_t stream);
 int query_dispatch(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R, int B,
                    int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
                    hipStream_t stream);
@@ -92,6 +94,7 @@ extern "C" int64_t smat_forward_workspace_bytes(int nb, int T, int n, int N0, in
 
 extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const void* vb,
                             const void* idx, int idx_is_64, const int64_t* indptr, int deg,
+                            const int* plane_code, int q,
                             float* out, float* H_out, const float* g, int nb, int T, int n,
                             int n_P, int N0, int B, int C, int r, int p, int64_t q_sb,
                             int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
@@ -146,8 +149,11 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     rc = pool_dispatch(dtype, psi, vb, F, Fg, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st, part,
                        part_bytes, st);
     if (rc) return rc;
-    rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
-                            profiled ? deg : 0, U, nb, N0, B, rp, st);
+    if (plane_code && profiled)
+      rc = incidence_plane_dispatch(F, Fg, plane_code, q, U, nb, N0, B, rp, st);
+    else
+      rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
+                              profiled ? deg : 0, U, nb, N0, B, rp, st);
     if (rc) return rc;
   }
   if (T_R > 0) {

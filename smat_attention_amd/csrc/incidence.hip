@@ -2,19 +2,25 @@
 // (src/smat/attention.py:239-285; the Triton kernel it replaces is
 // src/smat/kernels/triton_fwd.py:162-216).
 //
-// Pure gather-reduce over fp32 rows of rp = r*p floats.  The design target is
-// that every F element crosses HBM once even though each point lies on D
-// hyperplanes (D = q+1 for d = 3) and is therefore read D times:
+// A gather-reduce over fp32 rows of rp = r*p floats.  Each point lies on D
+// hyperplanes (D = q+1 for d = 3), so the adds read nnz(C)*rp floats while
+// only N0*rp distinct ones exist; the kernels are built around where those
+// re-reads are served from.
 //
-//   * work is cut into (batch, element slice) GROUPS; a group's F panel is
-//     N0 x kSlice floats (1.7 MB at N0 = 1681) and fits one XCD's 4 MB L2;
-//   * workgroups are dispatched round-robin over the 8 XCDs (workgroup L runs
-//     on XCD L mod 8), so the flat id is remapped to give each XCD a
-//     contiguous run of groups: all the hyperplanes of a group then read the
-//     panel from the same L2;
-//   * one wave per hyperplane and slice; each lane owns 4 consecutive floats
-//     (16-byte loads) and sums its deg rows in registers, in the row order of
-//     the table, exactly like the reference's fp32 accumulation.
+// incidence_lds_kernel (the default): one workgroup per (batch, slice of E
+//   floats).  The N0 x E panel of F is staged once in LDS (E = 16: 108 KB at
+//   N0 = 1681), then every hyperplane of the batch is summed out of LDS by four
+//   lanes.  F crosses HBM once; the re-reads hit LDS, whose bandwidth is twice
+//   the vector L1's.
+// incidence_l2_kernel (fallback: panels too large for LDS, rp % 4 != 0): one
+//   wave per (hyperplane, 256-float slice), the panel re-read from L2.  Flat
+//   ids are remapped so each XCD (workgroup L runs on XCD L mod 8) walks a
+//   contiguous run of (batch, slice) groups and the panel stays in that XCD's
+//   L2; each lane keeps 8 loads in flight.
+//
+// Both sum a hyperplane's points in the order of the table they are given.
+#include <stdlib.h>
+
 #include "smat_host.hpp"
 
 namespace smat {
@@ -22,20 +28,250 @@ namespace smat {
 namespace inc {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kSlice = 256;               // floats per wave per hyperplane (64 lanes x 4)
+constexpr int kSlice = 256;               // L2 kernel: floats per wave per hyperplane
 constexpr int kPlanesPerWave = 2;
 constexpr int kPlanesPerWG = kWaves * kPlanesPerWave;
 constexpr int kXCD = 8;
+constexpr int kUnroll = 8;                // loads in flight per lane (L2 kernel)
+constexpr int kLdsBudget = 150 * 1024;    // bytes of LDS for the F panel
 }  // namespace inc
 
-template <typename Idx, bool Vec>
-__global__ __launch_bounds__(inc::kThreads) void incidence_kernel(
+__device__ __forceinline__ void add4(float4& a, const float4& v) {
+  a.x += v.x;
+  a.y += v.y;
+  a.z += v.z;
+  a.w += v.w;
+}
+
+// ---------------------------------------------------------------------------
+// LDS panel kernel
+// ---------------------------------------------------------------------------
+
+// Four consecutive lanes own one hyperplane, lane k of the four the floats
+// [4k, 4k+4) of the 16-float slice, so eight lanes (one 128-byte LDS cycle)
+// read the 64-byte rows of two points.  Rows are 64 B apart, so the two reads
+// are conflict-free exactly when the two points differ in parity; tables
+// prepared by the host (parity_interleaved_table in attention.py) order each
+// hyperplane's points even-first or odd-first, alternating between
+// hyperplanes, which makes that the common case.  Any table is accepted.
+template <typename Idx, int E, int DMAX>
+__global__ __launch_bounds__(inc::kThreads) void incidence_lds_kernel(
     const float* __restrict__ F, const float* __restrict__ Fg, const Idx* __restrict__ idx,
-    const int64_t* __restrict__ indptr, int deg, float* __restrict__ U, int nb, int N0, int B,
-    int64_t rp, int nslices, int nhg, int64_t total_wg, int64_t per_xcd) {
+    const int64_t* __restrict__ indptr, int deg, float* __restrict__ U, int N0, int B, int64_t rp,
+    int nslices, int64_t total, int64_t per_xcd) {
   using namespace inc;
-  // XCD-aware remap: flat id L runs on XCD L % 8; give XCD x the work items
-  // [x * per_xcd, (x+1) * per_xcd).
+  constexpr int Q = E / 4;          // float4 per point (= lanes per hyperplane)
+  constexpr int kLines = kThreads / Q;
+  extern __shared__ float4 panel[];
+
+  const int64_t L = blockIdx.x;
+  const int64_t work = (L % kXCD) * per_xcd + L / kXCD;
+  if (work >= total) return;
+  const int64_t b = work / nslices;
+  const int slice = (int)(work - b * nslices);
+  const int64_t e0 = (int64_t)slice * E;
+
+  const float* Fb = F + b * (int64_t)N0 * rp + e0;
+  for (int i = threadIdx.x; i < N0 * Q; i += kThreads) {
+    const int x = i / Q, k = i - x * Q;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (e0 + 4 * k < rp) v = *reinterpret_cast<const float4*>(Fb + (int64_t)x * rp + 4 * k);
+    panel[i] = v;
+  }
+
+  const int k = threadIdx.x % Q;                  // float4 of the slice
+  const bool live = e0 + 4 * k < rp;
+  float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (Fg && live) g = *reinterpret_cast<const float4*>(Fg + b * rp + e0 + 4 * k);
+  float* Ub = U + b * (int64_t)B * rp + e0 + 4 * k;
+
+  if (indptr == nullptr && deg <= DMAX) {
+    // Uniform degree: a hyperplane's whole index row is loaded into registers
+    // in one burst, and the next hyperplane's row while this one is summed,
+    // so index latency overlaps the LDS work.
+    int cur[DMAX], nxt[DMAX];
+    int h = threadIdx.x / Q;
+#pragma unroll
+    for (int u = 0; u < DMAX; ++u)
+      cur[u] = (h < B && u < deg) ? (int)idx[(int64_t)h * deg + u] : 0;
+    __syncthreads();                              // panel staged
+    for (; h < B; h += kLines) {
+      const int hn = h + kLines;
+#pragma unroll
+      for (int u = 0; u < DMAX; ++u)
+        nxt[u] = (hn < B && u < deg) ? (int)idx[(int64_t)hn * deg + u] : 0;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < DMAX; ++u)
+        if (u < deg) add4(acc, panel[cur[u] * Q + k]);
+      if (live) {
+        if (Fg) add4(acc, g);
+        *reinterpret_cast<float4*>(Ub + (int64_t)h * rp) = acc;
+      }
+#pragma unroll
+      for (int u = 0; u < DMAX; ++u) cur[u] = nxt[u];
+    }
+    return;
+  }
+  __syncthreads();                                // panel staged
+  for (int h = threadIdx.x / Q; h < B; h += kLines) {
+    int64_t lo, hi;
+    if (indptr) {
+      lo = indptr[h];
+      hi = indptr[h + 1];
+    } else {
+      lo = (int64_t)h * deg;
+      hi = lo + deg;
+    }
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    int64_t t = lo;
+    for (; t + 8 <= hi; t += 8) {
+      int x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = (int)idx[t + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) add4(acc, panel[x[u] * Q + k]);
+    }
+    for (; t < hi; ++t) add4(acc, panel[(int)idx[t] * Q + k]);
+    if (live) {
+      if (Fg) add4(acc, g);
+      *reinterpret_cast<float4*>(Ub + (int64_t)h * rp) = acc;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LDS panel kernel, lines of the affine plane (d = 3) generated in-kernel
+// ---------------------------------------------------------------------------
+
+// For d = 3 every row type is a line <a_e, x> = b of F_q^2, with a_e = (0, 1)
+// for e = 0 and a_e = (1, e-1) otherwise, and point x = x0*q + x1.  Its q
+// points are generated from code[h] = e*q + b instead of being read from the
+// table: no index traffic at all.  Line e = 0: x1 = b, x0 = 0..q-1; line
+// (1, m): x0 = b - m*x1 mod q for x1 = 0..q-1.  Points are summed in that
+// order.
+//
+// One lane owns one line and all E floats of the slice, so the point
+// arithmetic is paid once per E adds.  The panel stores point x's four
+// 16-byte chunks rotated by x>>1 (chunk k at slot (k + (x>>1)) & 3): the
+// 16-byte bank group of (x, k) is then 4*(x&1) + ((k + (x>>1)) & 3), i.e. a
+// bijection of x mod 8.  Consecutive lanes own lines b, b+1, ... of one
+// direction, whose points at any step have consecutive x0 and hence, q being
+// odd, distinct x mod 8: the eight lanes an LDS cycle serves hit eight
+// different bank groups.
+template <int E>
+__global__ __launch_bounds__(1024) void incidence_plane_kernel(
+    const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
+    int q, float* __restrict__ U, int N0, int B, int64_t rp, int nslices, int64_t total,
+    int64_t per_xcd) {
+  using namespace inc;
+  constexpr int kT = 1024;          // 16 waves: four per SIMD to cover LDS latency
+  constexpr int Q = E / 4;          // float4 per point
+  constexpr int kU = 4;             // points in flight per lane
+  extern __shared__ float4 panel[];
+
+  const int64_t L = blockIdx.x;
+  const int64_t work = (L % kXCD) * per_xcd + L / kXCD;
+  if (work >= total) return;
+  const int64_t b = work / nslices;
+  const int slice = (int)(work - b * nslices);
+  const int64_t e0 = (int64_t)slice * E;
+
+  const float* Fb = F + b * (int64_t)N0 * rp + e0;
+  for (int i = threadIdx.x; i < N0 * Q; i += kT) {
+    const int x = i / Q, k = i - x * Q;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (e0 + 4 * k < rp) v = *reinterpret_cast<const float4*>(Fb + (int64_t)x * rp + 4 * k);
+    panel[x * Q + ((k + (x >> 1)) & (Q - 1))] = v;
+  }
+  __syncthreads();
+
+  float* Ub = U + b * (int64_t)B * rp + e0;
+  for (int h = threadIdx.x; h < B; h += kT) {
+    const int c = code[h];
+    const int e = c / q, off = c - e * q;
+    const int m = e == 0 ? 0 : e - 1;
+    float4 acc[Q];
+#pragma unroll
+    for (int k = 0; k < Q; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    int x0 = e == 0 ? 0 : off, x1 = e == 0 ? off : 0;
+    int t = 0;
+    for (; t + kU <= q; t += kU) {
+      int xs[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        xs[u] = x0 * q + x1;
+        if (e == 0) {
+          ++x0;
+        } else {
+          ++x1;
+          x0 -= m;
+          if (x0 < 0) x0 += q;
+        }
+      }
+      float4 v[kU][Q];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int k = 0; k < Q; ++k) v[u][k] = panel[xs[u] * Q + ((k + (xs[u] >> 1)) & (Q - 1))];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int k = 0; k < Q; ++k) add4(acc[k], v[u][k]);
+    }
+    for (; t < q; ++t) {
+      const int x = x0 * q + x1;
+#pragma unroll
+      for (int k = 0; k < Q; ++k) add4(acc[k], panel[x * Q + ((k + (x >> 1)) & (Q - 1))]);
+      if (e == 0) {
+        ++x0;
+      } else {
+        ++x1;
+        x0 -= m;
+        if (x0 < 0) x0 += q;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < Q; ++k) {
+      if (e0 + 4 * k < rp) {
+        if (Fg) add4(acc[k], *reinterpret_cast<const float4*>(Fg + b * rp + e0 + 4 * k));
+        *reinterpret_cast<float4*>(Ub + (int64_t)h * rp + 4 * k) = acc[k];
+      }
+    }
+  }
+}
+
+template <int E>
+static int launch_plane(const float* F, const float* F_glob, const int* code, int q, float* U,
+                        int nb, int N0, int B, int64_t rp, hipStream_t stream) {
+  using namespace inc;
+  const int nslices = (int)((rp + E - 1) / E);
+  const int64_t total = (int64_t)nb * nslices;
+  const int64_t per_xcd = (total + kXCD - 1) / kXCD;
+  const int64_t grid = per_xcd * kXCD;
+  const size_t smem = (size_t)N0 * E * 4;
+  auto kern = incidence_plane_kernel<E>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        inc::kLdsBudget);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(1024), smem, stream, F, F_glob, code, q,
+                     U, N0, B, rp, nslices, total, per_xcd);
+  return launch_status("smat_incidence_plane");
+}
+
+// ---------------------------------------------------------------------------
+// L2 kernel
+// ---------------------------------------------------------------------------
+
+template <typename Idx, bool Vec>
+__global__ __launch_bounds__(inc::kThreads) void incidence_l2_kernel(
+    const float* __restrict__ F, const float* __restrict__ Fg, const Idx* __restrict__ idx,
+    const int64_t* __restrict__ indptr, int deg, float* __restrict__ U, int N0, int B, int64_t rp,
+    int nslices, int nhg, int64_t total_wg, int64_t per_xcd) {
+  using namespace inc;
   const int64_t L = blockIdx.x;
   const int64_t work = (L % kXCD) * per_xcd + L / kXCD;
   if (work >= total_wg) return;
@@ -51,9 +287,9 @@ __global__ __launch_bounds__(inc::kThreads) void incidence_kernel(
   float* Ub = U + b * (int64_t)B * rp;
 
 #pragma unroll
-  for (int k = 0; k < kPlanesPerWave; ++k) {
-    const int h = hg * kPlanesPerWG + w * kPlanesPerWave + k;
-    if (h >= B) break;
+  for (int kp = 0; kp < kPlanesPerWave; ++kp) {
+    const int h = hg * kPlanesPerWG + w * kPlanesPerWave + kp;
+    if (h >= B) continue;
     int64_t lo, hi;
     if (indptr) {
       lo = indptr[h];
@@ -65,21 +301,17 @@ __global__ __launch_bounds__(inc::kThreads) void incidence_kernel(
     if (Vec) {
       if (e0 < rp) {   // rp % 4 == 0 on this path, so the 4 floats are in range
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int64_t t = lo; t < hi; ++t) {
-          const int64_t x = (int64_t)idx[t];
-          const float4 v = *reinterpret_cast<const float4*>(Fb + x * rp + e0);
-          acc.x += v.x;
-          acc.y += v.y;
-          acc.z += v.z;
-          acc.w += v.w;
+        int64_t t = lo;
+        for (; t + kUnroll <= hi; t += kUnroll) {
+          float4 v[kUnroll];
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u)
+            v[u] = *reinterpret_cast<const float4*>(Fb + (int64_t)idx[t + u] * rp + e0);
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u) add4(acc, v[u]);
         }
-        if (Fgb) {
-          const float4 v = *reinterpret_cast<const float4*>(Fgb + e0);
-          acc.x += v.x;
-          acc.y += v.y;
-          acc.z += v.z;
-          acc.w += v.w;
-        }
+        for (; t < hi; ++t) add4(acc, *reinterpret_cast<const float4*>(Fb + (int64_t)idx[t] * rp + e0));
+        if (Fgb) add4(acc, *reinterpret_cast<const float4*>(Fgb + e0));
         *reinterpret_cast<float4*>(Ub + (int64_t)h * rp + e0) = acc;
       }
     } else {
@@ -102,11 +334,72 @@ __global__ __launch_bounds__(inc::kThreads) void incidence_kernel(
   }
 }
 
+// Widest slice whose padded panel fits the LDS budget (0: none fits).
+static int lds_slice_width(int N0) {
+  for (int E : {16, 8, 4}) {
+    const int64_t bytes = (int64_t)N0 * E * 4;
+    if (bytes <= inc::kLdsBudget) return E;
+  }
+  return 0;
+}
+
+template <typename Idx, int E, int DMAX>
+static int launch_lds(const float* F, const float* F_glob, const void* idx, const int64_t* indptr,
+                      int deg, float* U, int nb, int N0, int B, int64_t rp, hipStream_t stream) {
+  using namespace inc;
+  const int nslices = (int)((rp + E - 1) / E);
+  const int64_t total = (int64_t)nb * nslices;
+  const int64_t per_xcd = (total + kXCD - 1) / kXCD;
+  const int64_t grid = per_xcd * kXCD;
+  const size_t smem = (size_t)N0 * E * 4;
+  auto kern = incidence_lds_kernel<Idx, E, DMAX>;
+  static bool attr_set = false;     // the LDS ceiling is per kernel; raise it once
+  if (!attr_set) {
+    hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        inc::kLdsBudget);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), smem, stream, F, F_glob,
+                     (const Idx*)idx, indptr, deg, U, N0, B, rp, nslices, total, per_xcd);
+  return launch_status("smat_incidence");
+}
+
+template <typename Idx, int E>
+static int launch_lds_deg(const float* F, const float* F_glob, const void* idx,
+                          const int64_t* indptr, int deg, float* U, int nb, int N0, int B,
+                          int64_t rp, hipStream_t stream) {
+  if (indptr == nullptr && deg <= 32)
+    return launch_lds<Idx, E, 32>(F, F_glob, idx, indptr, deg, U, nb, N0, B, rp, stream);
+  if (indptr == nullptr && deg <= 48)
+    return launch_lds<Idx, E, 48>(F, F_glob, idx, indptr, deg, U, nb, N0, B, rp, stream);
+  return launch_lds<Idx, E, 80>(F, F_glob, idx, indptr, deg, U, nb, N0, B, rp, stream);
+}
+
+static int incidence_mode_env() {
+  static int mode = -1;
+  if (mode < 0) {
+    const char* s = getenv("SMAT_INCIDENCE");
+    mode = (s && s[0] == 'l' && s[1] == '2') ? 1 : 0;   // "l2": force the L2 kernel
+  }
+  return mode;
+}
+
 int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int idx_is_64,
                        const int64_t* indptr, int deg, float* U, int nb, int N0, int B, int64_t rp,
                        hipStream_t stream) {
   using namespace inc;
   if (nb == 0 || B == 0 || rp == 0) return SMAT_OK;
+  const bool aligned = (rp % 4 == 0) && aligned16(F) && aligned16(U) &&
+                       (!F_glob || aligned16(F_glob));
+  const int E = lds_slice_width(N0);
+  if (aligned && E > 0 && incidence_mode_env() == 0) {
+#define SMAT_LDS(IDX)                                                                       \
+  (E == 16 ? launch_lds_deg<IDX, 16>(F, F_glob, idx, indptr, deg, U, nb, N0, B, rp, stream) \
+   : E == 8 ? launch_lds_deg<IDX, 8>(F, F_glob, idx, indptr, deg, U, nb, N0, B, rp, stream) \
+            : launch_lds_deg<IDX, 4>(F, F_glob, idx, indptr, deg, U, nb, N0, B, rp, stream))
+    return idx_is_64 ? SMAT_LDS(int64_t) : SMAT_LDS(int32_t);
+#undef SMAT_LDS
+  }
   const int nslices = (int)((rp + kSlice - 1) / kSlice);
   const int nhg = (B + kPlanesPerWG - 1) / kPlanesPerWG;
   const int64_t total = (int64_t)nb * nslices * nhg;
@@ -116,18 +409,33 @@ int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int
     set_error("smat_incidence: problem too large (%lld workgroups)", (long long)grid);
     return SMAT_EUNSUPPORTED;
   }
-  const bool vec = (rp % 4 == 0) && aligned16(F) && aligned16(U) && (!F_glob || aligned16(F_glob));
 #define SMAT_INC_LAUNCH(IDX, VEC)                                                              \
-  hipLaunchKernelGGL((incidence_kernel<IDX, VEC>), dim3((unsigned)grid), dim3(kThreads), 0,    \
-                     stream, F, F_glob, (const IDX*)idx, indptr, deg, U, nb, N0, B, rp,        \
-                     nslices, nhg, total, per_xcd)
+  hipLaunchKernelGGL((incidence_l2_kernel<IDX, VEC>), dim3((unsigned)grid), dim3(kThreads), 0, \
+                     stream, F, F_glob, (const IDX*)idx, indptr, deg, U, N0, B, rp, nslices,   \
+                     nhg, total, per_xcd)
   if (idx_is_64) {
-    if (vec) SMAT_INC_LAUNCH(int64_t, true); else SMAT_INC_LAUNCH(int64_t, false);
+    if (aligned) SMAT_INC_LAUNCH(int64_t, true); else SMAT_INC_LAUNCH(int64_t, false);
   } else {
-    if (vec) SMAT_INC_LAUNCH(int32_t, true); else SMAT_INC_LAUNCH(int32_t, false);
+    if (aligned) SMAT_INC_LAUNCH(int32_t, true); else SMAT_INC_LAUNCH(int32_t, false);
   }
 #undef SMAT_INC_LAUNCH
   return launch_status("smat_incidence");
+}
+
+int incidence_plane_dispatch(const float* F, const float* F_glob, const int* code, int q,
+                             float* U, int nb, int N0, int B, int64_t rp, hipStream_t stream) {
+  if (nb == 0 || B == 0 || rp == 0) return SMAT_OK;
+  const int E = lds_slice_width(N0);
+  const bool aligned = (rp % 4 == 0) && aligned16(F) && aligned16(U) &&
+                       (!F_glob || aligned16(F_glob));
+  if (!aligned || E == 0 || (int64_t)q * q != N0) {
+    set_error("smat_incidence_plane: needs rp %% 4 == 0, aligned tables, N0 = q^2 and a panel "
+              "that fits LDS (q=%d N0=%d rp=%lld)", q, N0, (long long)rp);
+    return SMAT_EUNSUPPORTED;
+  }
+  if (E == 16) return launch_plane<16>(F, F_glob, code, q, U, nb, N0, B, rp, stream);
+  if (E == 8) return launch_plane<8>(F, F_glob, code, q, U, nb, N0, B, rp, stream);
+  return launch_plane<4>(F, F_glob, code, q, U, nb, N0, B, rp, stream);
 }
 
 }  // namespace smat
@@ -142,4 +450,14 @@ extern "C" int smat_incidence(const float* F, const float* F_glob, const void* i
   SMAT_REQUIRE(indptr || deg >= 0, SMAT_EINVAL, "smat_incidence: need indptr or deg >= 0");
   return incidence_dispatch(F, F_glob, idx, idx_is_64, indptr, deg, U, nb, N0, B, rp,
                             (hipStream_t)stream);
+}
+
+extern "C" int smat_incidence_plane(const float* F, const float* F_glob, const int* code, int q,
+                                    float* U, int nb, int N0, int B, int64_t rp, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(F && code && U, SMAT_EINVAL, "smat_incidence_plane: null pointer");
+  SMAT_REQUIRE(nb >= 0 && q >= 2 && B >= 0 && rp >= 0, SMAT_EINVAL,
+               "smat_incidence_plane: bad sizes");
+  return incidence_plane_dispatch(F, F_glob, code, q, U, nb, N0, B, rp, (hipStream_t)stream);
 }

@@ -46,11 +46,12 @@ SIGNATURES = {
     "smat_pool": (_i, [_i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,
                        _i64, _i64, _i64, _i64, _p, _i64, _p]),
     "smat_incidence": (_i, [_p, _p, _p, _i, _p, _i, _p, _i, _i, _i, _i64, _p]),
+    "smat_incidence_plane": (_i, [_p, _p, _p, _i, _p, _i, _i, _i, _i64, _p]),
     "smat_query": (_i, [_i, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64, _p]),
     "smat_normalise": (_i, [_p, _p, _p, _p, _i, _i, _i, _i,
                             _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "smat_forward_workspace_bytes": (_i64, [_i, _i, _i, _i, _i, _i, _i, _i, _i]),
-    "smat_forward": (_i, [_i, _p, _p, _p, _p, _i, _p, _i, _p, _p, _p,
+    "smat_forward": (_i, [_i, _p, _p, _p, _p, _i, _p, _i, _p, _i, _p, _p, _p,
                           _i, _i, _i, _i, _i, _i, _i, _i, _i,
                           _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                           _p, _i64, _p]),

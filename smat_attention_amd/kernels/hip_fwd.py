@@ -29,7 +29,7 @@ MAX_P = 144
 MAX_C = 256
 
 __all__ = [
-    "available", "chunk_local", "incidence", "pool_ok", "pool",
+    "available", "chunk_local", "incidence", "pool_ok", "pool", "incidence_plane",
     "chunk_states", "segment_scan", "query", "normalise", "forward",
     "forward_workspace_bytes", "decode_step", "validate_table",
     "HipKernelError", "HipUnavailable", "MAX_R", "MAX_P", "MAX_C",
@@ -121,6 +121,20 @@ def chunk_local(Phi_c, Psi_c, Vb_c, Sin):
          out.data_ptr(), nb * nc, C, R, P, q_sb, q_st, k_sb, k_st, v_sb, v_st, s_sb, s_sr,
          out.stride(0), out.stride(1), stream_of(q))
     return out.reshape(nb, nc, C, P)
+
+
+def incidence_plane(F, plane_code, q: int, *, F_glob=None):
+    """``U_h = sum_{x in H_h} F_x`` for d = 3 with the lines generated from
+    ``plane_code`` (int32 ``(B,)``, ``e*q + b``) instead of a point table."""
+    who = "incidence_plane"
+    _on_gpu(who, F, plane_code, F_glob)
+    nb, N0, R, P = F.shape
+    B = plane_code.shape[0]
+    Ff = F.contiguous().float()
+    U = torch.empty(nb, B, R, P, device=F.device, dtype=torch.float32)
+    call("smat_incidence_plane", Ff.data_ptr(), ptr(F_glob), plane_code.data_ptr(), q,
+         U.data_ptr(), nb, N0, B, R * P, stream_of(Ff))
+    return U
 
 
 def incidence(F, plane_pts, B: int):
@@ -248,7 +262,8 @@ def forward_workspace_bytes(nb, T, n, N0, B, n_P, C, r, p) -> int:
 
 
 def forward(Phi, Psi, Vb, idx, deg: int, *, n: int, n_P: int, N0: int, B: int, chunk: int,
-            indptr=None, g=None, out=None, H_out=None, workspace=None):
+            indptr=None, plane_code=None, field_q: int = 0, g=None, out=None, H_out=None,
+            workspace=None):
     """The whole forward schedule in one call; returns fp32 ``(nb, T, p-1)``."""
     who = "forward"
     _on_gpu(who, Phi, Psi, Vb, idx, indptr, g, out, H_out)
@@ -273,7 +288,8 @@ def forward(Phi, Psi, Vb, idx, deg: int, *, n: int, n_P: int, N0: int, B: int, c
     aligned = (base + 255) & ~255
     avail = workspace.numel() - (aligned - base)
     call("smat_forward", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), idx.data_ptr(),
-         int(idx.dtype == torch.int64), ptr(indptr), deg, out.data_ptr(), ptr(H_out), ptr(gc),
+         int(idx.dtype == torch.int64), ptr(indptr), deg, ptr(plane_code), field_q,
+         out.data_ptr(), ptr(H_out), ptr(gc),
          nb, T, n, n_P, N0, B, chunk, R, P, q_sb, q_st, k_sb, k_st, v_sb, v_st,
          out.stride(0), out.stride(1), gc.stride(0) if gc is not None else 0,
          aligned, avail, stream_of(q))

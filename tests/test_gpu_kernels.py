@@ -113,9 +113,24 @@ def test_incidence(T, d):
     U = K.incidence(F.to(DEV), spec.plane_pts_t, spec.B)
     ref = O.apply_incidence(F.double(), spec)
     assert _rel(U, ref) < 1e-6
-    # int32 table and the schedule-level wrapper give the same answer
+    # the schedule-level wrapper reads the parity-interleaved int32 table: the
+    # same points per row, summed in another order
     U2 = A.apply_incidence(F.to(DEV), spec)
-    assert torch.equal(U, U2)
+    assert _rel(U2, ref) < 1e-6
+
+
+@pytest.mark.parametrize("T,n_P", [(2048, 0), (32768, 0), (131072, 0), (2048, 16)])
+def test_incidence_generated_lines(T, n_P):
+    _say("incidence, d=3 lines generated in-kernel", T, n_P)
+    spec = A.to_device(build_mask(T, 3, chunk=128, n_P=n_P), DEV)
+    assert spec.plane_code_t is not None
+    g = torch.Generator().manual_seed(8)
+    nb, r, p = (1, 128, 129) if T >= 32768 else (2, 32, 33)
+    F = torch.randn(nb, spec.N0, r, p, generator=g)
+    Fg = torch.randn(nb, r, p, generator=g)
+    U = K.incidence_plane(F.to(DEV), spec.plane_code_t, spec.q, F_glob=Fg.to(DEV))
+    ref = O.apply_incidence(F.double(), spec) + Fg.double().unsqueeze(1)
+    assert _rel(U, ref) < 1e-6
 
 
 def test_incidence_ragged_endpoint_csr():

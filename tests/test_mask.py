@@ -230,3 +230,47 @@ def test_estimate_cost():
     e = estimate_cost(131072, 3, 128, 128)
     assert e["feasible"] and e["I_prof"] == 70602 and e["B"] == 1722
     assert not estimate_cost(64, 5, 8, 8)["feasible"]
+
+
+def test_parity_interleaved_table_keeps_rows_and_alternates():
+    """The kernel-side table reorders points within each row only, even-first on
+    even rows and odd-first on odd rows."""
+    from smat_attention_amd.attention import parity_interleaved_table
+    spec = build_mask(131072, 3, chunk=128)
+    par = parity_interleaved_table(spec).reshape(spec.B, spec.uniform_deg)
+    ref = spec.C_indices.reshape(spec.B, spec.uniform_deg)
+    assert np.array_equal(np.sort(par, axis=1), np.sort(ref, axis=1))
+    for h in (0, 1, 2, 3, 1721):
+        row = par[h]
+        first = h & 1
+        par_bits = row & 1
+        n_first = int((par_bits == first).sum())
+        assert np.all(par_bits[:n_first] == first) and np.all(par_bits[n_first:] != first)
+        assert np.all(np.diff(row[:n_first]) > 0) and np.all(np.diff(row[n_first:]) > 0)
+
+
+@pytest.mark.parametrize("T", [2048, 4096, 32768, 131072, 524288, 69632])
+def test_plane_line_codes_regenerate_every_row(T):
+    """d = 3: each row of C is the line named by its code (checked set-wise
+    inside plane_line_codes; here also against the loop-built oracle rows)."""
+    from smat_attention_amd.attention import plane_line_codes
+    spec = build_mask(T, 3, chunk=128)
+    code = plane_line_codes(spec)
+    assert code is not None and code.shape == (spec.B,)
+    q = spec.q
+    e, b = code // q, code % q
+    if T <= 4096:
+        geo = mask_ref.geometry(T, 3, chunk=128)
+        for h in range(spec.B):
+            if e[h] == 0:
+                pts = {x0 * q + int(b[h]) for x0 in range(q)}
+            else:
+                m = int(e[h]) - 1
+                pts = {((int(b[h]) - m * x1) % q) * q + x1 for x1 in range(q)}
+            assert pts == set(geo["rows"][h])
+
+
+def test_plane_line_codes_absent_for_other_masks():
+    from smat_attention_amd.attention import plane_line_codes
+    assert plane_line_codes(build_mask(4096, 2, chunk=128)) is None
+    assert plane_line_codes(build_mask(8192, 4, chunk=128)) is None
