@@ -80,6 +80,25 @@ int smat_segment_scan(const float* D, float* Sin, int nb, int nc, int nc0, int64
                       void* stream);
 
 /*
+ * The causal pass fused: segmented chunked scan with one reset at n (chunk
+ * C <= 128), then either (write_H = 1) H = [[L_n,0],[0,L_{T_R}]] Phi Psi^T Vb
+ * into out (nb, T, p) fp32, or (write_H = 0) the normalised output
+ *   out[t, c] = (H[t, c] + Y[t-n, c]) / (H[t, p-1] + Y[t-n, p-1]) * g[t]
+ * into out (nb, T, p-1) fp32, the Y term only for t >= n (Y may be NULL, rows
+ * y_st apart), g optional.  Reads Phi, Psi, Vb once; H never reaches memory in
+ * the normalised mode.  Replaces segmented_causal_scan
+ * (src/smat/attention.py:134-192) plus the cat/normalise of :446-453.
+ * workspace: smat_causal_scan_workspace_bytes(...) bytes, 256-byte aligned.
+ */
+int64_t smat_causal_scan_workspace_bytes(int nb, int T, int C, int r, int p);
+int smat_causal_scan(int dtype, const void* phi, const void* psi, const void* vb,
+                     const float* Y, const float* g, float* out, int nb, int T, int n, int C,
+                     int r, int p, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
+                     int64_t v_sb, int64_t v_st, int64_t y_sb, int64_t y_st,
+                     int64_t o_sb, int64_t o_st, int64_t g_sb, int write_H,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Profile pooling  F_x = sum_{j in [n_P, n), (j - n_P) mod N0 = x} Psi_j^T Vb_j
  * (fp32, F: (nb, N0, r, p) contiguous).  If F_glob is not NULL and n_P > 0 it
  * also receives the global-channel term sum_{j < n_P} Psi_j^T Vb_j, (nb, r, p).

@@ -239,9 +239,11 @@ def segmented_causal_scan(Phi, Psi, Vb, n: int, chunk: int = 128,
                           acc_dtype=None, backend: str = "auto"):
     """``[[L_n, 0], [0, L_{T_R}]] Phi Psi^T Vb`` as one chunked scan with one reset.
 
-    Chunk summaries ``D``, then a shifted exclusive scan per segment (never
-    cumsum-minus-self, attention.py:163-179), then the fused chunk-local pass.
-    Returns fp32 ``(nb, T, p)``.
+    Chunks of up to 128 rows go through the fused scan kernel (state carried in
+    registers across chunks, seeded per group of chunks by a shifted exclusive
+    scan, never cumsum-minus-self, attention.py:163-179); wider chunks run the
+    chunk summaries, the per-segment scan and the chunk-local pass as separate
+    kernels.  Returns fp32 ``(nb, T, p)``.
     """
     who = "segmented_causal_scan"
     _backend(backend, who)
@@ -251,6 +253,9 @@ def segmented_causal_scan(Phi, Psi, Vb, n: int, chunk: int = 128,
     C = min(chunk, T)
     if n % C:
         raise ValueError(f"segment boundary n={n} is not a multiple of chunk={C}")
+    if C <= 128:
+        return _hip.causal_scan(Phi, Psi, Vb, n, C, write_H=True)
+    # wide chunks: summaries, scan and chunk-local pass as separate kernels
     nc = -(-T // C)
     D = _hip.chunk_states(Psi, Vb, C)
     Sin = _hip.segment_scan(D, n // C)

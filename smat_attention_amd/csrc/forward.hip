@@ -54,27 +54,43 @@ int normalise_dispatch(const float* H, const float* Y, const float* g, float* ou
                        int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb, int64_t y_st,
                        int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream);
 
-// Workspace carve-up, each region 256-byte aligned.
+int64_t causal_scan_workspace_bytes(int nb, int T, int C, int r, int p);
+int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void* vb,
+                         const float* Y, const float* gate, float* out, int nb, int T, int n,
+                         int C, int r, int p, int64_t q_sb, int64_t q_st, int64_t k_sb,
+                         int64_t k_st, int64_t v_sb, int64_t v_st, int64_t y_sb, int64_t y_st,
+                         int64_t o_sb, int64_t o_st, int64_t g_sb, int write_H, void* ws,
+                         int64_t ws_bytes, hipStream_t stream);
+
+// Workspace carve-up, each region 256-byte aligned.  The fused causal pass
+// (chunk <= 128, no H requested) needs only its group states; the staged one
+// keeps the per-chunk summaries, their scan and H.
 struct FwdLayout {
-  int64_t F, Fg, U, Y, D, Sin, H, part, total;
+  int64_t F, Fg, U, Y, D, Sin, H, part, scan, total;
+  bool fused;
 };
 
 static inline int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
 static FwdLayout fwd_layout(int nb, int T, int n, int N0, int B, int n_P, int C, int r, int p,
-                            bool want_H_scratch) {
+                            bool want_H) {
   FwdLayout L{};
   const int64_t rp = (int64_t)r * p;
   const int nc = (T + C - 1) / C;
   const int T_R = T - n;
+  L.fused = (C <= 128) && !want_H;
   int64_t off = 0;
   L.F = off;   off += al256((int64_t)nb * N0 * rp * 4);
   L.Fg = off;  off += n_P > 0 ? al256((int64_t)nb * rp * 4) : 0;
   L.U = off;   off += al256((int64_t)nb * B * rp * 4);
   L.Y = off;   off += al256((int64_t)nb * T_R * p * 4);
-  L.D = off;   off += al256((int64_t)nb * nc * rp * 4);
-  L.Sin = off; off += al256((int64_t)nb * nc * rp * 4);
-  L.H = off;   off += want_H_scratch ? al256((int64_t)nb * nc * C * p * 4) : 0;
+  if (L.fused) {
+    L.scan = off; off += al256(causal_scan_workspace_bytes(nb, T, C, r, p));
+  } else {
+    L.D = off;   off += al256((int64_t)nb * nc * rp * 4);
+    L.Sin = off; off += al256((int64_t)nb * nc * rp * 4);
+    L.H = off;   off += al256((int64_t)nb * nc * C * p * 4);
+  }
   L.part = off; off += al256(pool_workspace_bytes(nb, n_P, n, N0, r, p, n_P > 0));
   L.total = off;
   return L;
@@ -89,7 +105,9 @@ extern "C" const char* smat_version(void) { return "0.1 gfx950"; }
 extern "C" int64_t smat_forward_workspace_bytes(int nb, int T, int n, int N0, int B, int n_P,
                                                 int C, int r, int p) {
   if (nb <= 0 || T <= 0 || C <= 0 || N0 <= 0 || B <= 0 || r <= 0 || p <= 0) return 0;
-  return smat::fwd_layout(nb, T, n, N0, B, n_P, C, r, p, true).total;
+  const smat::FwdLayout a = smat::fwd_layout(nb, T, n, N0, B, n_P, C, r, p, false);
+  const smat::FwdLayout b = smat::fwd_layout(nb, T, n, N0, B, n_P, C, r, p, true);
+  return a.total > b.total ? a.total : b.total;
 }
 
 extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const void* vb,
@@ -118,7 +136,7 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
                "smat_forward: a row stride is shorter than its row");
   SMAT_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, SMAT_EINVAL,
                "smat_forward: workspace must be 256-byte aligned");
-  const FwdLayout L = fwd_layout(nb, T, n, N0, B, n_P, C, r, p, H_out == nullptr);
+  const FwdLayout L = fwd_layout(nb, T, n, N0, B, n_P, C, r, p, H_out != nullptr);
   SMAT_REQUIRE(workspace_bytes >= L.total, SMAT_EINVAL,
                "smat_forward: workspace of %lld bytes needed, %lld given", (long long)L.total,
                (long long)workspace_bytes);
@@ -129,16 +147,11 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
   float* Fg = n_P > 0 ? (float*)(ws + L.Fg) : nullptr;
   float* U = (float*)(ws + L.U);
   float* Y = (float*)(ws + L.Y);
-  float* D = (float*)(ws + L.D);
-  float* Sin = (float*)(ws + L.Sin);
   float* part = (float*)(ws + L.part);
   const int64_t part_bytes = L.total - L.part;
   const int64_t rp = (int64_t)r * p;
   const int nc = (T + C - 1) / C;
   const int T_R = T - n;
-  // H in (nb, nc*C, p) fp32: the caller's H_out is (nb, T, p), which is the
-  // same layout for every row the chunk pass writes (rows >= T are skipped).
-  float* H = H_out ? H_out : (float*)(ws + L.H);
   int rc;
 
   // ---- long range: S^T, then C, then R ---------------------------------
@@ -163,7 +176,19 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     if (rc) return rc;
   }
 
-  // ---- causal: chunk summaries, segmented scan, chunk-local pass ----------
+  // ---- causal pass ------------------------------------------------------
+  if (L.fused) {
+    // one kernel: segmented scan, + Y on recent rows, normalise, gate
+    return causal_scan_dispatch(dtype, phi, psi, vb, T_R > 0 ? Y : nullptr, g, out, nb, T, n, C,
+                                r, p, q_sb, q_st, k_sb, k_st, v_sb, v_st, (int64_t)T_R * p, p,
+                                o_sb, o_st, g_sb, 0, ws + L.scan, L.part - L.scan, st);
+  }
+  // staged: chunk summaries, segmented scan, chunk-local pass into H, normalise
+  float* D = (float*)(ws + L.D);
+  float* Sin = (float*)(ws + L.Sin);
+  // H in (nb, nc*C, p) fp32: the caller's H_out is (nb, T, p), which is the
+  // same layout for every row the chunk pass writes (rows >= T are skipped).
+  float* H = H_out ? H_out : (float*)(ws + L.H);
   rc = chunk_states_dispatch(dtype, psi, vb, D, nb, T, C, 1, n, r, p, k_sb, k_st, v_sb, v_st,
                              nullptr, 0, st, nullptr, nullptr);
   if (rc) return rc;
@@ -203,8 +228,6 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
       }
     }
   }
-
-  // ---- normalise ---------------------------------------------------------
   return normalise_dispatch(H, T_R > 0 ? Y : nullptr, g, out, nb, T, n, p, h_sb, p,
                             (int64_t)T_R * p, p, o_sb, o_st, g_sb, st);
 }

@@ -1,0 +1,460 @@
+// The causal pass of the schedule fused end to end: the segmented chunked
+// scan of src/smat/attention.py:134-192 (one reset at n), the long-range term
+// added to recent rows and the normalisation of :446-453, in one kernel that
+// reads Phi, Psi, Vb (and Y) once and writes the output once.
+//
+// Chunks are grouped K at a time inside a segment.  A prepass (the Gram
+// kernel over each group's tokens, then the shifted exclusive scan over
+// groups) gives every group its incoming state; one workgroup then walks the
+// group's chunks in order with the r x p state S held in fp32 MFMA
+// accumulators:
+//
+//   for each chunk:  out = Phi S + tril(Phi Psi^T) Vb      (as chunk_local)
+//                    S  += Psi^T Vb                        (as the Gram kernel)
+//                    normalise out (+ Y on recent rows, x g) and store
+//
+// The in-chunk products reuse chunk_local's layout (wave w owns 16-row tiles
+// w and 7-w; S^T = Psi Phi^T feeds the S Vb product straight from the
+// accumulators).  The state update reuses the Gram kernel's (wave w owns rows
+// 32w..32w+31 of S).  After each chunk the waves write S^T to LDS, split into
+// hi/lo 16-bit parts for 16-bit inputs, as the B operand of the next chunk's
+// Phi S.  Psi and Vb are staged once per 64-token block and feed both the
+// intra-chunk product and the update.
+#include "smat_host.hpp"
+
+namespace smat {
+
+namespace sf {
+constexpr int kThreads = 256;
+constexpr int kC = 128;                  // rows per chunk handled (chunk <= 128)
+constexpr int kRK = 4;                   // r <= 128
+constexpr int kNCT = 9;                  // p <= 144
+constexpr int kCols = kNCT * 16;
+constexpr int kRPad = kRK * 32 + 8;      // row length of r-indexed LDS rows
+
+// tokens per staged block: 64 for 16-bit inputs, 32 for fp32 (LDS budget)
+template <typename In> constexpr int bn() { return sizeof(In) == 4 ? 32 : 64; }
+template <typename In> constexpr int npad() { return bn<In>() + 8; }
+
+template <typename In>
+constexpr int state_bytes() {
+  return Traits<In>::split ? 2 * kCols * kRPad * (int)sizeof(In) : kCols * kRPad * 4;
+}
+template <typename In>
+constexpr int block_bytes() {
+  // psiS [bn][kRPad], psiT [128][npad], vbT [kCols][npad]
+  return (bn<In>() * kRPad + 128 * npad<In>() + kCols * npad<In>()) * (int)sizeof(In);
+}
+}  // namespace sf
+
+struct ScanArgs {
+  int T, n, C, K, nc, nc0, ng0, r, p;
+  int64_t q_sb, q_st, k_sb, k_st, v_sb, v_st;
+  int64_t y_sb, y_st;   // Y rows are recent rows t - n
+  int64_t o_sb, o_st;
+  int64_t g_sb;
+  int write_H;          // 1: out is H (nb, T, p) unnormalised, no Y / gate
+};
+
+template <typename In>
+__global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
+    const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
+    const float* __restrict__ Sg, const float* __restrict__ Y, const float* __restrict__ gate,
+    float* __restrict__ out, ScanArgs a, int vec_q, int vec_k) {
+  using namespace sf;
+  typedef typename Traits<In>::frag Frag;
+  constexpr int kBN = bn<In>();
+  constexpr int kNPad = npad<In>();
+  __shared__ __attribute__((aligned(16))) char smem[state_bytes<In>() + block_bytes<In>()];
+  In* sT_hi = reinterpret_cast<In*>(smem);                 // S^T [c][a] (hi, or fp32 whole)
+  In* sT_lo = sT_hi + kCols * kRPad;
+  float* sT32 = reinterpret_cast<float*>(smem);
+  In* psiS = reinterpret_cast<In*>(smem + state_bytes<In>());   // [kBN][kRPad]
+  In* psiT = psiS + kBN * kRPad;                                 // [128][kNPad]
+  In* vbT = psiT + 128 * kNPad;                                  // [kCols][kNPad]
+
+  const int grp = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int lane = lane_id(), w = wave_id();
+  const int row16 = lane & 15, g4 = lane >> 4;
+  const int r = a.r, p = a.p, C = a.C;
+  const int rk = (r + 31) >> 5;
+  const int nct = (p + 15) >> 4;
+  const int nrt = (r + 15) >> 4;
+
+  // chunks of this group
+  int c0, c1;
+  if (grp < a.ng0) {
+    c0 = grp * a.K;
+    c1 = min(c0 + a.K, a.nc0);
+  } else {
+    c0 = a.nc0 + (grp - a.ng0) * a.K;
+    c1 = min(c0 + a.K, a.nc);
+  }
+
+  const In* phib = phi + b * a.q_sb;
+  const In* psib = psi + b * a.k_sb;
+  const In* vbb = vb + b * a.v_sb;
+
+  // ---- incoming state: this wave's rows of S in accumulators, S^T in LDS ----
+  f32x4 accS[2][kNCT];
+  {
+    const float* Sb = Sg + ((int64_t)b * gridDim.x + grp) * (int64_t)r * p;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int rt = 2 * w + t;
+#pragma unroll
+      for (int ct = 0; ct < kNCT; ++ct) {
+        const int c = ct * 16 + row16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int ar = rt * 16 + 4 * g4 + i;
+          accS[t][ct][i] = (rt < nrt && ct < nct && ar < r && c < p) ? Sb[(int64_t)ar * p + c] : 0.f;
+        }
+      }
+    }
+  }
+
+  int mrow[2];
+  mrow[0] = 16 * w;
+  mrow[1] = 16 * (7 - w);
+
+  for (int ch = c0; ch < c1; ++ch) {
+    const int64_t t0 = (int64_t)ch * C;                  // first token of the chunk
+    const int Cv = (int)min((int64_t)C, (int64_t)a.T - t0);   // valid rows (ragged tail)
+
+    // ---- publish S^T (state before this chunk) ----
+    __syncthreads();        // previous chunk's readers of sT are done
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int rt = 2 * w + t;
+#pragma unroll
+      for (int ct = 0; ct < kNCT; ++ct) {
+        const int c = ct * 16 + row16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int ar = rt * 16 + 4 * g4 + i;       // < 128 always; zeros beyond r/p
+          const float v = accS[t][ct][i];
+          if constexpr (Traits<In>::split) {
+            In h, l;
+            split2<In>(v, h, l);
+            sT_hi[c * kRPad + ar] = h;
+            sT_lo[c * kRPad + ar] = l;
+          } else {
+            sT32[c * kRPad + ar] = v;
+          }
+        }
+      }
+    }
+
+    // ---- this wave's Phi rows ----
+    Frag phiA[2][kRK];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int m = mrow[t] + row16;
+#pragma unroll
+      for (int kb = 0; kb < kRK; ++kb) {
+        const int k0 = 32 * kb + 8 * g4;
+        const int nv = (kb < rk && m < Cv) ? min(8, r - k0) : 0;
+        phiA[t][kb] = load8<In>(phib + (t0 + m) * a.q_st + k0, nv, vec_q);
+      }
+    }
+    __syncthreads();        // sT complete
+
+    // ---- inter-chunk term: Phi S ----
+    f32x4 acc[2][kNCT];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int ct = 0; ct < kNCT; ++ct) acc[t][ct] = zero4();
+#pragma unroll
+    for (int kb = 0; kb < kRK; ++kb) {
+      if (kb >= rk) continue;
+#pragma unroll
+      for (int ct = 0; ct < kNCT; ++ct) {
+        if (ct >= nct) continue;
+        const int off = (ct * 16 + row16) * kRPad + 32 * kb + 8 * g4;
+        if constexpr (Traits<In>::split) {
+          const Frag bh = *reinterpret_cast<const Frag*>(sT_hi + off);
+          const Frag bl = *reinterpret_cast<const Frag*>(sT_lo + off);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            acc[t][ct] = mma(acc[t][ct], phiA[t][kb], bh);
+            acc[t][ct] = mma(acc[t][ct], phiA[t][kb], bl);
+          }
+        } else {
+          const Frag bf = *reinterpret_cast<const Frag*>(sT32 + off);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) acc[t][ct] = mma(acc[t][ct], phiA[t][kb], bf);
+        }
+      }
+    }
+
+    // ---- token blocks: intra-chunk product and the state update ----
+    const int kgroups = rk * 4;
+    const int ncols = nct * 16;
+    for (int n0 = 0; n0 < Cv; n0 += kBN) {
+      __syncthreads();      // previous block's readers are done
+      for (int idx = threadIdx.x; idx < kBN * kgroups; idx += kThreads) {
+        const int nn = idx / kgroups, g8 = idx - nn * kgroups;
+        const int nr = n0 + nn;
+        const int nv = (nr < Cv) ? min(8, r - 8 * g8) : 0;
+        const Frag v = load8<In>(psib + (t0 + nr) * a.k_st + 8 * g8, nv, vec_k);
+        *reinterpret_cast<Frag*>(psiS + nn * kRPad + 8 * g8) = v;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) psiT[(8 * g8 + j) * kNPad + nn] = v[j];
+      }
+      for (int idx = threadIdx.x; idx < kBN * ncols; idx += kThreads) {
+        const int nn = idx / ncols, c = idx - nn * ncols;
+        const int nr = n0 + nn;
+        vbT[c * kNPad + nn] = (nr < Cv && c < p) ? vbb[(t0 + nr) * a.v_st + c] : from_f32<In>(0.f);
+      }
+      __syncthreads();
+
+      // intra-chunk: rows of this wave against tokens [n0, n0+64)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int mr0 = mrow[t];
+#pragma unroll
+        for (int np = 0; np < kBN / 32; ++np) {
+          const int nb0 = n0 + 32 * np;
+          if (nb0 > mr0 + 15 || nb0 >= Cv) continue;
+          f32x4 s[2];
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            s[nt] = zero4();
+            const int nt0 = nb0 + 16 * nt;
+            if (nt0 <= mr0 + 15 && nt0 < Cv) {
+#pragma unroll
+              for (int kb = 0; kb < kRK; ++kb) {
+                if (kb >= rk) continue;
+                const Frag av = *reinterpret_cast<const Frag*>(
+                    psiS + (32 * np + 16 * nt + row16) * kRPad + 32 * kb + 8 * g4);
+                s[nt] = mma(s[nt], av, phiA[t][kb]);
+              }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (nt0 + 4 * g4 + i > mr0 + row16) s[nt][i] = 0.f;
+          }
+          Frag sa;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            sa[j] = from_f32<In>(s[0][j]);
+            sa[j + 4] = from_f32<In>(s[1][j]);
+          }
+#pragma unroll
+          for (int ct = 0; ct < kNCT; ++ct) {
+            if (ct >= nct) continue;
+            const In* vr = vbT + (ct * 16 + row16) * kNPad + 32 * np + 4 * g4;
+            Frag vf;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              vf[j] = vr[j];
+              vf[j + 4] = vr[16 + j];
+            }
+            acc[t][ct] = mma(acc[t][ct], sa, vf);
+          }
+        }
+      }
+
+      // state update: S += Psi_blk^T Vb_blk (this wave's rows of S)
+#pragma unroll
+      for (int kk = 0; kk < kBN / 32; ++kk) {
+        if (n0 + 32 * kk >= Cv) continue;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int rt = 2 * w + t;
+          if (rt >= nrt) continue;
+          const Frag av = *reinterpret_cast<const Frag*>(psiT + (rt * 16 + row16) * kNPad +
+                                                         32 * kk + 8 * g4);
+#pragma unroll
+          for (int ct = 0; ct < kNCT; ++ct) {
+            if (ct >= nct) continue;
+            const Frag bv = *reinterpret_cast<const Frag*>(vbT + (ct * 16 + row16) * kNPad +
+                                                           32 * kk + 8 * g4);
+            accS[t][ct] = mma(accS[t][ct], av, bv);
+          }
+        }
+      }
+    }
+
+    // ---- normalise and store the chunk's rows ----
+    const int pn = p - 1;                         // the normaliser column
+    const int ctn = pn >> 4, ln = pn & 15;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float yv[kNCT][4];
+      float den[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = mrow[t] + 4 * g4 + i;
+        const int64_t row = t0 + m;
+        const bool live = m < Cv;
+        const bool rec = live && !a.write_H && Y != nullptr && row >= a.n;
+        const float* yrow = rec ? Y + b * a.y_sb + (row - a.n) * a.y_st : nullptr;
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct) {
+          const int c = ct * 16 + row16;
+          yv[ct][i] = (yrow && ct < nct && c < p) ? yrow[c] : 0.f;
+        }
+        // the normaliser of row m sits in lane (g4, ln) of column tile ctn
+        float hn = 0.f;
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct)
+          if (ct == ctn) hn = acc[t][ct][i] + yv[ct][i];
+        den[i] = __shfl(hn, g4 * 16 + ln, 64);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = mrow[t] + 4 * g4 + i;
+        if (m >= Cv) continue;
+        const int64_t row = t0 + m;
+        float* orow = out + b * a.o_sb + row * a.o_st;
+        if (a.write_H) {
+#pragma unroll
+          for (int ct = 0; ct < kNCT; ++ct) {
+            const int c = ct * 16 + row16;
+            if (ct < nct && c < p) orow[c] = acc[t][ct][i];
+          }
+        } else {
+          const float gv = gate ? gate[b * a.g_sb + row] : 1.f;
+#pragma unroll
+          for (int ct = 0; ct < kNCT; ++ct) {
+            const int c = ct * 16 + row16;
+            if (ct < nct && c < pn) {
+              float v = (acc[t][ct][i] + yv[ct][i]) / den[i];
+              if (gate) v *= gv;
+              orow[c] = v;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+template <typename In>
+static int launch_scan_fused(const void* phi, const void* psi, const void* vb, const float* Sg,
+                             const float* Y, const float* gate, float* out, int nb, int ng,
+                             const ScanArgs& a, hipStream_t stream) {
+  const int eb = sizeof(In);
+  const int vq = rows_vec_ok(phi, a.q_sb, a.q_st, eb);
+  const int vk = rows_vec_ok(psi, a.k_sb, a.k_st, eb);
+  hipLaunchKernelGGL(scan_fused_kernel<In>, dim3((unsigned)ng, (unsigned)nb), dim3(sf::kThreads),
+                     0, stream, (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a,
+                     vq, vk);
+  return launch_status("smat_causal_scan");
+}
+
+int chunk_states_dispatch(int dtype, const void* psi, const void* vb, float* D, int nb, int T,
+                          int C, int K, int n, int r, int p, int64_t k_sb, int64_t k_st,
+                          int64_t v_sb, int64_t v_st, float* partials, int64_t partial_bytes,
+                          hipStream_t stream, int* ngroups_out, int* ng0_out);
+int segment_scan_dispatch(const float* D, float* Sin, int nb, int nc, int nc0, int64_t rp,
+                          hipStream_t stream);
+
+// Group size: enough workgroups to fill the GPU (one per CU at a time), and
+// no more than needed so the prepass stays small.
+static int scan_group_chunks(int nb, int nc) {
+  int K = 8;
+  while (K > 1 && (int64_t)nb * ((nc + K - 1) / K) < 1024) K >>= 1;
+  return K;
+}
+
+int64_t causal_scan_workspace_bytes(int nb, int T, int C, int r, int p) {
+  const int nc = (T + C - 1) / C;
+  const int K = scan_group_chunks(nb, nc);
+  const int ng = (nc + K - 1) / K + 1;             // +1: the segment split may add a group
+  return 2 * (((int64_t)nb * ng * r * p * 4 + 255) & ~(int64_t)255);
+}
+
+int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void* vb,
+                         const float* Y, const float* gate, float* out, int nb, int T, int n,
+                         int C, int r, int p, int64_t q_sb, int64_t q_st, int64_t k_sb,
+                         int64_t k_st, int64_t v_sb, int64_t v_st, int64_t y_sb, int64_t y_st,
+                         int64_t o_sb, int64_t o_st, int64_t g_sb, int write_H, void* ws,
+                         int64_t ws_bytes, hipStream_t stream) {
+  if (nb == 0 || T == 0) return SMAT_OK;
+  const int nc = (T + C - 1) / C;
+  const int K = scan_group_chunks(nb, nc);
+  const int64_t need = causal_scan_workspace_bytes(nb, T, C, r, p);
+  if (ws_bytes < need) {
+    set_error("smat_causal_scan: workspace of %lld bytes needed, %lld given", (long long)need,
+              (long long)ws_bytes);
+    return SMAT_EINVAL;
+  }
+  float* G = (float*)ws;
+  float* Sg = (float*)((char*)ws + need / 2);
+  int ng = 0, ng0 = 0;
+  int rc = chunk_states_dispatch(dtype, psi, vb, G, nb, T, C, K, n, r, p, k_sb, k_st, v_sb, v_st,
+                                 nullptr, 0, stream, &ng, &ng0);
+  if (rc) return rc;
+  rc = segment_scan_dispatch(G, Sg, nb, ng, ng0, (int64_t)r * p, stream);
+  if (rc) return rc;
+  ScanArgs a{};
+  a.T = T;
+  a.n = n;
+  a.C = C;
+  a.K = K;
+  a.nc = nc;
+  a.nc0 = n / C;
+  a.ng0 = ng0;
+  a.r = r;
+  a.p = p;
+  a.q_sb = q_sb;
+  a.q_st = q_st;
+  a.k_sb = k_sb;
+  a.k_st = k_st;
+  a.v_sb = v_sb;
+  a.v_st = v_st;
+  a.y_sb = y_sb;
+  a.y_st = y_st;
+  a.o_sb = o_sb;
+  a.o_st = o_st;
+  a.g_sb = g_sb;
+  a.write_H = write_H;
+  switch (dtype) {
+    case SMAT_BF16:
+      return launch_scan_fused<bf16>(phi, psi, vb, Sg, Y, gate, out, nb, ng, a, stream);
+    case SMAT_F16:
+      return launch_scan_fused<f16>(phi, psi, vb, Sg, Y, gate, out, nb, ng, a, stream);
+    case SMAT_F32:
+      return launch_scan_fused<float>(phi, psi, vb, Sg, Y, gate, out, nb, ng, a, stream);
+  }
+  set_error("smat_causal_scan: unknown dtype %d", dtype);
+  return SMAT_EINVAL;
+}
+
+}  // namespace smat
+
+extern "C" int64_t smat_causal_scan_workspace_bytes(int nb, int T, int C, int r, int p) {
+  if (nb <= 0 || T <= 0 || C <= 0 || r <= 0 || p <= 0) return 0;
+  return smat::causal_scan_workspace_bytes(nb, T, C, r, p);
+}
+
+extern "C" int smat_causal_scan(int dtype, const void* phi, const void* psi, const void* vb,
+                                const float* Y, const float* gate, float* out, int nb, int T,
+                                int n, int C, int r, int p, int64_t q_sb, int64_t q_st,
+                                int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
+                                int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
+                                int64_t g_sb, int write_H, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(phi && psi && vb && out && workspace, SMAT_EINVAL,
+               "smat_causal_scan: null pointer");
+  SMAT_REQUIRE(nb >= 0 && T >= 0 && C >= 1 && C <= sf::kC, SMAT_EUNSUPPORTED,
+               "smat_causal_scan: chunk C=%d not in [1, %d]", C, sf::kC);
+  SMAT_REQUIRE(n >= 0 && n <= T && n % C == 0, SMAT_EINVAL,
+               "smat_causal_scan: n=%d must be a multiple of C=%d in [0, T]", n, C);
+  SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 2 && p <= kMaxP, SMAT_EUNSUPPORTED,
+               "smat_causal_scan: r=%d p=%d beyond r<=%d, 2<=p<=%d", r, p, kMaxR, kMaxP);
+  SMAT_REQUIRE(q_st >= r && k_st >= r && v_st >= p && o_st >= (write_H ? p : p - 1), SMAT_EINVAL,
+               "smat_causal_scan: a row stride is shorter than its row");
+  SMAT_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, SMAT_EINVAL,
+               "smat_causal_scan: workspace must be 256-byte aligned");
+  return causal_scan_dispatch(dtype, phi, psi, vb, Y, gate, out, nb, T, n, C, r, p, q_sb, q_st,
+                              k_sb, k_st, v_sb, v_st, y_sb, y_st, o_sb, o_st, g_sb, write_H,
+                              workspace, workspace_bytes, (hipStream_t)stream);
+}

@@ -30,7 +30,7 @@ MAX_C = 256
 
 __all__ = [
     "available", "chunk_local", "incidence", "pool_ok", "pool", "incidence_plane",
-    "chunk_states", "segment_scan", "query", "normalise", "forward",
+    "chunk_states", "segment_scan", "causal_scan", "query", "normalise", "forward",
     "forward_workspace_bytes", "decode_step", "validate_table",
     "HipKernelError", "HipUnavailable", "MAX_R", "MAX_P", "MAX_C",
 ]
@@ -213,6 +213,36 @@ def chunk_states(Psi, Vb, C: int):
     call("smat_chunk_states", code, k.data_ptr(), v.data_ptr(), D.data_ptr(), nb, T, C, R, P,
          k_sb, k_st, v_sb, v_st, stream_of(k))
     return D
+
+
+def causal_scan(Phi, Psi, Vb, n: int, chunk: int, *, Y=None, g=None, write_H: bool = False,
+                out=None):
+    """The fused causal pass (chunk <= 128).  ``write_H``: fp32 ``(nb, T, p)`` H of
+    the segmented scan; else the normalised fp32 ``(nb, T, p-1)`` output with
+    ``Y`` (``(nb, T-n, p)``) added on recent rows and the gate ``g`` applied."""
+    who = "causal_scan"
+    _on_gpu(who, Phi, Psi, Vb, Y, g, out)
+    nb, T, R = Phi.shape
+    P = Vb.shape[-1]
+    if Psi.dtype != Phi.dtype or Vb.dtype != Phi.dtype:
+        raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
+    code = _code(Phi, who)
+    q, q_sb, q_st = _rows3(Phi)
+    k, k_sb, k_st = _rows3(Psi)
+    v, v_sb, v_st = _rows3(Vb)
+    Yc = _fp32_rows(Y) if Y is not None else None
+    gc = g.float().contiguous() if g is not None else None
+    if out is None:
+        out = torch.empty(nb, T, P if write_H else P - 1, device=Phi.device, dtype=torch.float32)
+    wsb = _lib.query("smat_causal_scan_workspace_bytes", nb, T, chunk, R, P)
+    ws = torch.empty(wsb + 256, device=Phi.device, dtype=torch.uint8)
+    base = (ws.data_ptr() + 255) & ~255
+    call("smat_causal_scan", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), ptr(Yc), ptr(gc),
+         out.data_ptr(), nb, T, n, chunk, R, P, q_sb, q_st, k_sb, k_st, v_sb, v_st,
+         Yc.stride(0) if Yc is not None else 0, Yc.stride(1) if Yc is not None else 0,
+         out.stride(0), out.stride(1), gc.stride(0) if gc is not None else 0, int(write_H),
+         base, wsb, stream_of(q))
+    return out
 
 
 def segment_scan(D, nc0: int):

@@ -54,8 +54,8 @@ def test_unsupported_sizes_are_rejected():
                   0, 256, 0, 256, 0, 65, 0, 65, 0, 65, None)
     assert e.value.code == -2 and "r=256" in str(e.value)
     with pytest.raises(HipKernelError, match="unknown dtype"):
-        _lib.call("smat_forward", 7, fake, fake, fake, fake, 0, None, 1, fake, None, None,
-                  1, 256, 128, 0, 4, 4, 128, 16, 17, 0, 16, 0, 16, 0, 17, 0, 16, 0,
+        _lib.call("smat_forward", 7, fake, fake, fake, fake, 0, None, 1, None, 0, fake, None,
+                  None, 1, 256, 128, 0, 4, 4, 128, 16, 17, 0, 16, 0, 16, 0, 17, 0, 16, 0,
                   fake, 1 << 30, None)
 
 

@@ -179,6 +179,32 @@ def test_chunk_states_and_segment_scan(dt):
     assert torch.count_nonzero(Sin[:, n // C]).item() == 0
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,n,C,hd", [(2048, 1024, 128, 64), (2048 + 77, 1024, 128, 32),
+                                      (4096, 2048, 64, 32), (1000, 0, 128, 32),
+                                      (8192, 4096, 128, 128), (300, 256, 128, 16)])
+def test_causal_scan_fused(dt, T, n, C, hd):
+    _say("causal scan fused", dt, T, n, C, hd)
+    Phi, Psi, Vb = _feats(2, T, hd, dt, seed=9)
+    H = K.causal_scan(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), n, C, write_H=True)
+    if dt == torch.float32:
+        ref = O.segmented_causal_scan(Phi.double(), Psi.double(), Vb.double(), n, chunk=C)
+        assert _rel(H, ref) < 1e-5
+    else:
+        ref = O.segmented_causal_scan(Phi, Psi, Vb, n, chunk=C)
+        assert _rel(H, ref) < 1e-2
+    # normalised mode with a long-range term on the recent rows and a gate
+    g = torch.Generator().manual_seed(10)
+    Y = torch.rand(2, T - n, Vb.shape[-1], generator=g)
+    gate = torch.rand(2, T, generator=g) + 0.5
+    out = K.causal_scan(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), n, C, Y=Y.to(DEV), g=gate.to(DEV))
+    Hr = ref.double().clone()
+    Hr[:, n:] += Y.double()
+    want = Hr[..., :-1] / Hr[..., -1:] * gate.double().unsqueeze(-1)
+    tol = 1e-5 if dt == torch.float32 else 2e-2
+    assert (out.double().cpu() - want).abs().max().item() < tol * max(1.0, want.abs().max().item())
+
+
 # ---------------------------------------------------------------------------
 # the whole schedule
 # ---------------------------------------------------------------------------
