@@ -70,7 +70,7 @@ __device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& s
   }
 }
 
-template <typename In>
+template <typename In, bool VEC>
 __global__ __launch_bounds__(gr::kThreads) void gram_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, float* __restrict__ G,
     float* __restrict__ G_last, GramItems it, int r, int p, int64_t k_sb, int64_t k_st,
@@ -109,20 +109,34 @@ __global__ __launch_bounds__(gr::kThreads) void gram_kernel(
 
   const int nrows = nrt * 16, ncols = nct * 16;
   for (int s0 = 0; s0 < count; s0 += kBT) {
-    // stage Psi^T[a][tt] and Vb^T[c][tt] for tokens s0 + tt
-    for (int idx = threadIdx.x; idx < kBT * nrows; idx += kThreads) {
-      const int tt = idx / nrows, a = idx - tt * nrows;
-      const int s = s0 + tt;
-      psiT[a * kTPad + tt] = (s < count && a < r) ? psib[(start + (int64_t)s * stride) * k_st + a]
-                                                  : from_f32<In>(0.f);
+    // stage Psi^T[a][tt] and Vb^T[c][tt] for tokens s0 + tt, 8 x 8 tiles
+    {
+      const int tpsi = (kBT / 8) * (nrows / 8);
+      const int tvb = (kBT / 8) * (ncols / 8);
+      for (int tile = threadIdx.x; tile < tpsi + tvb; tile += kThreads) {
+        const bool is_psi = tile < tpsi;
+        const int tix = is_psi ? tile : tile - tpsi;
+        const int per_row = is_psi ? nrows / 8 : ncols / 8;
+        const int tt = (tix / per_row) * 8, c0 = (tix % per_row) * 8;
+        const In* rowp[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int sidx = s0 + tt + u;
+          const int64_t tok = start + (int64_t)sidx * stride;
+          rowp[u] = sidx < count ? (is_psi ? psib + tok * k_st : vbb + tok * v_st) : nullptr;
+        }
+        Tile8<In> tl;
+        const int64_t tok0 = start + (int64_t)s0 * stride;    // valid: s0 < count
+        if (is_psi) {
+          tile8_load<In, VEC>(tl, rowp, psib + tok0 * k_st, c0, r);
+          tile8_store_T<In>(tl, psiT, kTPad, c0, tt);
+        } else {
+          tile8_load<In, VEC>(tl, rowp, vbb + tok0 * v_st, c0, p);
+          tile8_store_T<In>(tl, vbT, kTPad, c0, tt);
+        }
+      }
     }
-    for (int idx = threadIdx.x; idx < kBT * ncols; idx += kThreads) {
-      const int tt = idx / ncols, c = idx - tt * ncols;
-      const int s = s0 + tt;
-      vbT[c * kTPad + tt] = (s < count && c < p) ? vbb[(start + (int64_t)s * stride) * v_st + c]
-                                                 : from_f32<In>(0.f);
-    }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int rt = 2 * w + t;
@@ -135,7 +149,7 @@ __global__ __launch_bounds__(gr::kThreads) void gram_kernel(
         acc[t][ct] = mma(acc[t][ct], a, bf);
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 
   // nsplit > 1: G is the partial buffer (nb, nitems, nsplit, r, p) and G_last
@@ -187,14 +201,21 @@ static int launch_gram(const void* psi, const void* vb, float* G, float* G_last,
                        int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
                        int64_t gl_sb, float* partials, hipStream_t stream, const char* who) {
   const int64_t gx = (int64_t)nitems * it.nsplit;
+  const int vk = rows_vec_ok(psi, k_sb, k_st, sizeof(In));
+  const int vv = rows_vec_ok(vb, v_sb, v_st, sizeof(In));
   if (gx >= (1ll << 31) || nb >= 65536) {
     set_error("%s: problem too large", who);
     return SMAT_EUNSUPPORTED;
   }
   if (it.nsplit > 1) {
-    hipLaunchKernelGGL(gram_kernel<In>, dim3((unsigned)gx, (unsigned)nb), dim3(gr::kThreads), 0,
-                       stream, (const In*)psi, (const In*)vb, partials, nullptr, it, r, p, k_sb,
-                       k_st, v_sb, v_st, 0, 0, 0);
+    if (vk && vv)
+      hipLaunchKernelGGL((gram_kernel<In, true>), dim3((unsigned)gx, (unsigned)nb),
+                         dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, partials,
+                         nullptr, it, r, p, k_sb, k_st, v_sb, v_st, 0, 0, 0);
+    else
+      hipLaunchKernelGGL((gram_kernel<In, false>), dim3((unsigned)gx, (unsigned)nb),
+                         dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, partials,
+                         nullptr, it, r, p, k_sb, k_st, v_sb, v_st, 0, 0, 0);
     int st = launch_status(who);
     if (st != SMAT_OK) return st;
     const int64_t rp = (int64_t)r * p;
@@ -203,9 +224,14 @@ static int launch_gram(const void* psi, const void* vb, float* G, float* G_last,
                        g_si, gl_sb);
     return launch_status(who);
   }
-  hipLaunchKernelGGL(gram_kernel<In>, dim3((unsigned)gx, (unsigned)nb), dim3(gr::kThreads), 0,
-                     stream, (const In*)psi, (const In*)vb, G, G_last, it, r, p, k_sb, k_st,
-                     v_sb, v_st, g_sb, g_si, gl_sb);
+  if (vk && vv)
+    hipLaunchKernelGGL((gram_kernel<In, true>), dim3((unsigned)gx, (unsigned)nb),
+                       dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, G, G_last,
+                       it, r, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb);
+  else
+    hipLaunchKernelGGL((gram_kernel<In, false>), dim3((unsigned)gx, (unsigned)nb),
+                       dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, G, G_last,
+                       it, r, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb);
   return launch_status(who);
 }
 

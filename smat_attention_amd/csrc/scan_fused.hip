@@ -56,11 +56,11 @@ struct ScanArgs {
   int write_H;          // 1: out is H (nb, T, p) unnormalised, no Y / gate
 };
 
-template <typename In>
+template <typename In, bool VEC>
 __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
     const float* __restrict__ Sg, const float* __restrict__ Y, const float* __restrict__ gate,
-    float* __restrict__ out, ScanArgs a, int vec_q, int vec_k) {
+    float* __restrict__ out, ScanArgs a) {
   using namespace sf;
   typedef typename Traits<In>::frag Frag;
   constexpr int kBN = bn<In>();
@@ -96,6 +96,58 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
   const In* psib = psi + b * a.k_sb;
   const In* vbb = vb + b * a.v_sb;
 
+  // ---- staging of one token block: 8 x 8 tiles of Psi (to psiS and psiT)
+  // and of Vb (to vbT); a thread owns tiles tid and tid + kThreads ----
+  const int kgroups = rk * 4;
+  const int ncols = nct * 16;
+  const int tpsi = (kBN / 8) * kgroups;
+  const int ttot = tpsi + (kBN / 8) * (ncols / 8);
+  struct Pf {
+    Tile8<In> tl[2];
+    int tt[2], c0[2];
+    bool psi[2], live[2];
+  } pf;
+  auto stage_issue = [&](Pf& f, int chk, int nb0) {
+    const int64_t tk0 = (int64_t)chk * C;
+    const int cv = (int)min((int64_t)C, (int64_t)a.T - tk0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int tile = threadIdx.x + j * kThreads;
+      f.live[j] = tile < ttot;
+      if (!f.live[j]) continue;
+      const bool is_psi = tile < tpsi;
+      const int tix = is_psi ? tile : tile - tpsi;
+      const int per_row = is_psi ? kgroups : ncols / 8;
+      f.psi[j] = is_psi;
+      f.tt[j] = (tix / per_row) * 8;
+      f.c0[j] = (tix % per_row) * 8;
+      const In* rowp[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int nr = nb0 + f.tt[j] + u;
+        rowp[u] = nr < cv ? (is_psi ? psib + (tk0 + nr) * a.k_st : vbb + (tk0 + nr) * a.v_st)
+                          : nullptr;
+      }
+      if (is_psi)
+        tile8_load<In, VEC>(f.tl[j], rowp, psib + tk0 * a.k_st, f.c0[j], r);
+      else
+        tile8_load<In, VEC>(f.tl[j], rowp, vbb + tk0 * a.v_st, f.c0[j], p);
+    }
+  };
+  auto stage_commit = [&](const Pf& f, In* dS, In* dT, In* dV) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (!f.live[j]) continue;
+      if (f.psi[j]) {
+        tile8_store<In>(f.tl[j], dS, kRPad, f.c0[j], f.tt[j]);
+        tile8_store_T<In>(f.tl[j], dT, kNPad, f.c0[j], f.tt[j]);
+      } else {
+        tile8_store_T<In>(f.tl[j], dV, kNPad, f.c0[j], f.tt[j]);
+      }
+    }
+  };
+  if (c0 < c1) stage_issue(pf, c0, 0);
+
   // ---- incoming state: this wave's rows of S in accumulators, S^T in LDS ----
   f32x4 accS[2][kNCT];
   {
@@ -124,25 +176,28 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
     const int Cv = (int)min((int64_t)C, (int64_t)a.T - t0);   // valid rows (ragged tail)
 
     // ---- publish S^T (state before this chunk) ----
-    __syncthreads();        // previous chunk's readers of sT are done
+    // lane (g4, row16) holds S[rt*16 + 4*g4 + i][ct*16 + row16], i = 0..3:
+    // four consecutive rows of one column, one 8-byte (fp32: 16-byte) store.
+    lds_barrier();        // previous chunk's readers of sT are done
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int rt = 2 * w + t;
 #pragma unroll
       for (int ct = 0; ct < kNCT; ++ct) {
-        const int c = ct * 16 + row16;
+        const int off = (ct * 16 + row16) * kRPad + rt * 16 + 4 * g4;
+        if constexpr (Traits<In>::split) {
+          typename Traits<In>::half_frag h4, l4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int ar = rt * 16 + 4 * g4 + i;       // < 128 always; zeros beyond r/p
-          const float v = accS[t][ct][i];
-          if constexpr (Traits<In>::split) {
+          for (int i = 0; i < 4; ++i) {
             In h, l;
-            split2<In>(v, h, l);
-            sT_hi[c * kRPad + ar] = h;
-            sT_lo[c * kRPad + ar] = l;
-          } else {
-            sT32[c * kRPad + ar] = v;
+            split2<In>(accS[t][ct][i], h, l);
+            h4[i] = h;
+            l4[i] = l;
           }
+          *reinterpret_cast<typename Traits<In>::half_frag*>(sT_hi + off) = h4;
+          *reinterpret_cast<typename Traits<In>::half_frag*>(sT_lo + off) = l4;
+        } else {
+          *reinterpret_cast<f32x4*>(sT32 + off) = accS[t][ct];
         }
       }
     }
@@ -156,10 +211,10 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
       for (int kb = 0; kb < kRK; ++kb) {
         const int k0 = 32 * kb + 8 * g4;
         const int nv = (kb < rk && m < Cv) ? min(8, r - k0) : 0;
-        phiA[t][kb] = load8<In>(phib + (t0 + m) * a.q_st + k0, nv, vec_q);
+        phiA[t][kb] = load8v<In, VEC>(phib + (t0 + m) * a.q_st + k0, phib + t0 * a.q_st, nv);
       }
     }
-    __syncthreads();        // sT complete
+    lds_barrier();        // sT complete
 
     // ---- inter-chunk term: Phi S ----
     f32x4 acc[2][kNCT];
@@ -191,25 +246,19 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
     }
 
     // ---- token blocks: intra-chunk product and the state update ----
-    const int kgroups = rk * 4;
-    const int ncols = nct * 16;
     for (int n0 = 0; n0 < Cv; n0 += kBN) {
-      __syncthreads();      // previous block's readers are done
-      for (int idx = threadIdx.x; idx < kBN * kgroups; idx += kThreads) {
-        const int nn = idx / kgroups, g8 = idx - nn * kgroups;
-        const int nr = n0 + nn;
-        const int nv = (nr < Cv) ? min(8, r - 8 * g8) : 0;
-        const Frag v = load8<In>(psib + (t0 + nr) * a.k_st + 8 * g8, nv, vec_k);
-        *reinterpret_cast<Frag*>(psiS + nn * kRPad + 8 * g8) = v;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) psiT[(8 * g8 + j) * kNPad + nn] = v[j];
+      lds_barrier();      // previous block's readers are done
+      stage_commit(pf, psiS, psiT, vbT);
+      lds_barrier();
+      // the next block's loads fly while this block is multiplied
+      {
+        int nch = ch, nn0 = n0 + kBN;
+        if (nn0 >= Cv) {
+          nch = ch + 1;
+          nn0 = 0;
+        }
+        if (nch < c1) stage_issue(pf, nch, nn0);
       }
-      for (int idx = threadIdx.x; idx < kBN * ncols; idx += kThreads) {
-        const int nn = idx / ncols, c = idx - nn * ncols;
-        const int nr = n0 + nn;
-        vbT[c * kNPad + nn] = (nr < Cv && c < p) ? vbb[(t0 + nr) * a.v_st + c] : from_f32<In>(0.f);
-      }
-      __syncthreads();
 
       // intra-chunk: rows of this wave against tokens [n0, n0+64)
 #pragma unroll
@@ -319,11 +368,12 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
           }
         } else {
           const float gv = gate ? gate[b * a.g_sb + row] : 1.f;
+          const float inv = 1.f / den[i];        // one division per row
 #pragma unroll
           for (int ct = 0; ct < kNCT; ++ct) {
             const int c = ct * 16 + row16;
             if (ct < nct && c < pn) {
-              float v = (acc[t][ct][i] + yv[ct][i]) / den[i];
+              float v = (acc[t][ct][i] + yv[ct][i]) * inv;
               if (gate) v *= gv;
               orow[c] = v;
             }
@@ -339,11 +389,15 @@ static int launch_scan_fused(const void* phi, const void* psi, const void* vb, c
                              const float* Y, const float* gate, float* out, int nb, int ng,
                              const ScanArgs& a, hipStream_t stream) {
   const int eb = sizeof(In);
-  const int vq = rows_vec_ok(phi, a.q_sb, a.q_st, eb);
-  const int vk = rows_vec_ok(psi, a.k_sb, a.k_st, eb);
-  hipLaunchKernelGGL(scan_fused_kernel<In>, dim3((unsigned)ng, (unsigned)nb), dim3(sf::kThreads),
-                     0, stream, (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a,
-                     vq, vk);
+  const bool vec = rows_vec_ok(phi, a.q_sb, a.q_st, eb) && rows_vec_ok(psi, a.k_sb, a.k_st, eb) &&
+                   rows_vec_ok(vb, a.v_sb, a.v_st, eb);
+  dim3 grid((unsigned)ng, (unsigned)nb);
+  if (vec)
+    hipLaunchKernelGGL((scan_fused_kernel<In, true>), grid, dim3(sf::kThreads), 0, stream,
+                       (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a);
+  else
+    hipLaunchKernelGGL((scan_fused_kernel<In, false>), grid, dim3(sf::kThreads), 0, stream,
+                       (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a);
   return launch_status("smat_causal_scan");
 }
 

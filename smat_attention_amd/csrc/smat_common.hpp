@@ -102,3 +102,116 @@ __device__ __forceinline__ typename Traits<In>::frag load8(const In* p, int nval
 }
 
 }  // namespace smat
+
+namespace smat {
+
+// ---------------------------------------------------------------------------
+// Staging a token-major tile into LDS transposed (feature-major), 8 x 8 at a
+// time: a thread loads 8 token rows x 8 consecutive columns with 16-byte (or
+// 32-byte for fp32) reads, transposes the 8 x 8 block in registers and writes
+// 8 column runs of 8 tokens with 16-byte (32-byte) LDS stores.  This replaces
+// per-element global loads and per-element transposed LDS writes.
+// ---------------------------------------------------------------------------
+
+template <typename In>
+struct Tile8 {
+  typename Traits<In>::frag row[8];   // row[t] = columns c0..c0+7 of token t
+};
+
+// Load rows tok(0..7) x columns [c0, c0+8) of a row-major matrix; `rowp[t]` is
+// the row start of token t (nullptr: a padding token, loaded as zeros).
+// Columns >= ncols load as zeros.
+//
+// VEC (rows 16-byte aligned, row stride a multiple of 16 bytes): branch-free.
+// Every row is read with one 16-byte (fp32: 32-byte) load -- a padding row,
+// or a tile starting at or past column ncols, from `safe` (the start of any
+// valid row of the same matrix) -- and the padding rows and columns are then
+// zeroed with selects.  A live read covers [c0, c0+8) with c0 < ncols and c0 a
+// multiple of 8, so it ends at or before round_up(ncols, 8) <= the row stride:
+// no read leaves its row, hence none leaves the allocation.  Branches around loads make the
+// compiler wait for every outstanding load where they join, which would
+// serialise the staging; this form keeps all eight loads in flight.
+// !VEC: element-wise loads with zero fill.
+template <typename In, bool VEC>
+__device__ __forceinline__ void tile8_load(Tile8<In>& tl, const In* const* rowp, const In* safe,
+                                           int c0, int ncols) {
+  typedef typename Traits<In>::frag F;
+  const int nv = ncols - c0;
+  if constexpr (VEC) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      // A tile wholly past the last column (nv <= 0) or a padding row reads
+      // `safe` at column 0 instead: c0 + 8 may exceed the row stride there.
+      const bool live = rowp[t] != nullptr && nv > 0;
+      const In* src = live ? rowp[t] + c0 : safe;
+      F v = *reinterpret_cast<const F*>(src);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (live && j < nv) ? v[j] : from_f32<In>(0.f);
+      tl.row[t] = v;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        tl.row[t][j] = (rowp[t] != nullptr && j < nv) ? rowp[t][c0 + j] : from_f32<In>(0.f);
+    }
+  }
+}
+
+// Eight consecutive elements at p; elements j >= nvalid read as zero.  VEC as
+// for tile8_load: one vector load from p when the row is valid, else from
+// `safe`, then selects.
+template <typename In, bool VEC>
+__device__ __forceinline__ typename Traits<In>::frag load8v(const In* p, const In* safe,
+                                                            int nvalid) {
+  typedef typename Traits<In>::frag F;
+  F v;
+  if constexpr (VEC) {
+    v = *reinterpret_cast<const F*>(nvalid > 0 ? p : safe);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (j < nvalid) ? v[j] : from_f32<In>(0.f);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (j < nvalid) ? p[j] : from_f32<In>(0.f);
+  }
+  return v;
+}
+
+// Write the transpose: dst[(c0 + j) * ld + t0 .. + 8] = column j of the tile.
+template <typename In>
+__device__ __forceinline__ void tile8_store_T(const Tile8<In>& tl, In* dst, int ld, int c0,
+                                              int t0) {
+  typedef typename Traits<In>::frag F;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    F col;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) col[t] = tl.row[t][j];
+    *reinterpret_cast<F*>(dst + (c0 + j) * ld + t0) = col;
+  }
+}
+
+// Write the tile as is: dst[(t0 + t) * ld + c0 .. + 8] = row t.
+template <typename In>
+__device__ __forceinline__ void tile8_store(const Tile8<In>& tl, In* dst, int ld, int c0, int t0) {
+  typedef typename Traits<In>::frag F;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) *reinterpret_cast<F*>(dst + (t0 + t) * ld + c0) = tl.row[t];
+}
+
+}  // namespace smat
+
+namespace smat {
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load and store of the wave (vmcnt(0)), which would
+// drain the prefetches the kernels keep in flight across a barrier; here the
+// wave waits for its own LDS operations (lgkmcnt(0)) and then meets the
+// others, which is all that LDS producer/consumer hand-offs need.  Global data
+// loaded into registers is still waited for by the compiler at its first use.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+}  // namespace smat

@@ -285,8 +285,12 @@ def test_forward_long_prefill_d3_bf16_T32768():
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
     _check_forward(spec, Phi[:2], Psi[:2], Vb[:2], dt=torch.bfloat16, label="T=32768 d=3 heads 0-1")
+    # heads are independent: a 2-head launch matches the 8-head one (the scan's
+    # chunk grouping depends on the batch, so only up to fp32 summation order)
     sub = A.smat_attention(Phi[:2].to(DEV), Psi[:2].to(DEV), Vb[:2].to(DEV), spec)
-    assert torch.equal(sub, out[:2])     # heads are independent and deterministic
+    assert _rel(sub, out[:2]) < 1e-6
+    again = A.smat_attention(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), spec)
+    assert torch.equal(again, out)       # and a repeated launch is bit-identical
 
 
 def test_exact_non_influence():
