@@ -128,16 +128,24 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
         rowp[u] = nr < cv ? (is_psi ? psib + (tk0 + nr) * a.k_st : vbb + (tk0 + nr) * a.v_st)
                           : nullptr;
       }
-      if (is_psi)
-        tile8_load<In, VEC>(f.tl[j], rowp, psib + tk0 * a.k_st, f.c0[j], r);
-      else
-        tile8_load<In, VEC>(f.tl[j], rowp, vbb + tk0 * a.v_st, f.c0[j], p);
+      if constexpr (VEC) {
+        if (is_psi)
+          tile8_issue<In>(f.tl[j], rowp, psib + tk0 * a.k_st, f.c0[j], r);
+        else
+          tile8_issue<In>(f.tl[j], rowp, vbb + tk0 * a.v_st, f.c0[j], p);
+      } else {
+        if (is_psi)
+          tile8_load<In, false>(f.tl[j], rowp, psib + tk0 * a.k_st, f.c0[j], r);
+        else
+          tile8_load<In, false>(f.tl[j], rowp, vbb + tk0 * a.v_st, f.c0[j], p);
+      }
     }
   };
-  auto stage_commit = [&](const Pf& f, In* dS, In* dT, In* dV) {
+  auto stage_commit = [&](Pf& f, In* dS, In* dT, In* dV) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       if (!f.live[j]) continue;
+      if constexpr (VEC) tile8_finish<In>(f.tl[j]);
       if (f.psi[j]) {
         tile8_store<In>(f.tl[j], dS, kRPad, f.c0[j], f.tt[j]);
         tile8_store_T<In>(f.tl[j], dT, kNPad, f.c0[j], f.tt[j]);
@@ -161,7 +169,9 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int ar = rt * 16 + 4 * g4 + i;
-          accS[t][ct][i] = (rt < nrt && ct < nct && ar < r && c < p) ? Sb[(int64_t)ar * p + c] : 0.f;
+          const bool ok = ar < r && c < p;            // (rt < nrt, ct < nct follow)
+          const float v = Sb[ok ? (int64_t)ar * p + c : 0];   // branch-free
+          accS[t][ct][i] = ok ? v : 0.f;
         }
       }
     }
@@ -212,6 +222,26 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
         const int k0 = 32 * kb + 8 * g4;
         const int nv = (kb < rk && m < Cv) ? min(8, r - k0) : 0;
         phiA[t][kb] = load8v<In, VEC>(phib + (t0 + m) * a.q_st + k0, phib + t0 * a.q_st, nv);
+      }
+    }
+    // ---- this chunk's long-range rows (recent rows only), loaded now so the
+    // latency overlaps the products; branch-free from a clamped address ----
+    float yv[2][kNCT][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = mrow[t] + 4 * g4 + i;
+        const int64_t row = t0 + m;
+        const bool rec = m < Cv && !a.write_H && Y != nullptr && row >= a.n;
+        const float* yrow = rec ? Y + b * a.y_sb + (row - a.n) * a.y_st : Y;
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct) {
+          const int c = ct * 16 + row16;
+          const bool ok = rec && c < p;
+          const float v = (Y != nullptr) ? yrow[ok ? c : 0] : 0.f;
+          yv[t][ct][i] = ok ? v : 0.f;
+        }
       }
     }
     lds_barrier();        // sT complete
@@ -333,25 +363,14 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
     const int ctn = pn >> 4, ln = pn & 15;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      float yv[kNCT][4];
       float den[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int m = mrow[t] + 4 * g4 + i;
-        const int64_t row = t0 + m;
-        const bool live = m < Cv;
-        const bool rec = live && !a.write_H && Y != nullptr && row >= a.n;
-        const float* yrow = rec ? Y + b * a.y_sb + (row - a.n) * a.y_st : nullptr;
-#pragma unroll
-        for (int ct = 0; ct < kNCT; ++ct) {
-          const int c = ct * 16 + row16;
-          yv[ct][i] = (yrow && ct < nct && c < p) ? yrow[c] : 0.f;
-        }
         // the normaliser of row m sits in lane (g4, ln) of column tile ctn
         float hn = 0.f;
 #pragma unroll
         for (int ct = 0; ct < kNCT; ++ct)
-          if (ct == ctn) hn = acc[t][ct][i] + yv[ct][i];
+          if (ct == ctn) hn = acc[t][ct][i] + yv[t][ct][i];
         den[i] = __shfl(hn, g4 * 16 + ln, 64);
       }
 #pragma unroll
@@ -373,7 +392,7 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
           for (int ct = 0; ct < kNCT; ++ct) {
             const int c = ct * 16 + row16;
             if (ct < nct && c < pn) {
-              float v = (acc[t][ct][i] + yv[ct][i]) * inv;
+              float v = (acc[t][ct][i] + yv[t][ct][i]) * inv;
               if (gate) v *= gv;
               orow[c] = v;
             }

@@ -116,7 +116,38 @@ namespace smat {
 template <typename In>
 struct Tile8 {
   typename Traits<In>::frag row[8];   // row[t] = columns c0..c0+7 of token t
+  unsigned live;                      // bit t: row t holds data (tile8_issue)
+  int nv;                             // valid columns (tile8_issue)
 };
+
+// Split form of tile8_load<In, true> for prefetching: tile8_issue only starts
+// the eight vector loads (nothing reads their results, so nothing waits for
+// them); tile8_finish, called when the data is needed, zeroes padding rows and
+// columns.  Same addresses, same bounds argument as tile8_load.
+template <typename In>
+__device__ __forceinline__ void tile8_issue(Tile8<In>& tl, const In* const* rowp, const In* safe,
+                                            int c0, int ncols) {
+  typedef typename Traits<In>::frag F;
+  tl.nv = ncols - c0;
+  tl.live = 0;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const bool live = rowp[t] != nullptr && tl.nv > 0;
+    tl.live |= live ? (1u << t) : 0u;
+    tl.row[t] = *reinterpret_cast<const F*>(live ? rowp[t] + c0 : safe);
+  }
+}
+
+template <typename In>
+__device__ __forceinline__ void tile8_finish(Tile8<In>& tl) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const bool live = (tl.live >> t) & 1u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      tl.row[t][j] = (live && j < tl.nv) ? tl.row[t][j] : from_f32<In>(0.f);
+  }
+}
 
 // Load rows tok(0..7) x columns [c0, c0+8) of a row-major matrix; `rowp[t]` is
 // the row start of token t (nullptr: a padding token, loaded as zeros).
