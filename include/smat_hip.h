@@ -158,6 +158,42 @@ int smat_normalise(const float* H, const float* Y, const float* g, float* out,
                    int64_t o_sb, int64_t o_st, int64_t g_sb, void* stream);
 
 /*
+ * Reverse segmented exclusive scan (backward pass): Sout[c] = sum of D[c']
+ * over c' > c in the same segment ([0, nc0) or [nc0, nc)).  The state that
+ * flows backwards through the chunks in the gradient of the causal scan.
+ */
+int smat_segment_scan_reverse(const float* D, float* Sout, int nb, int nc, int nc0, int64_t rp,
+                              void* stream);
+
+/*
+ * Backward of out = H[..., :p-1] / H[..., p-1:] * g (g optional):
+ * dH[t, c] = dout[t, c] g[t] / H[t, p-1] for c < p-1,
+ * dH[t, p-1] = -sum_c dH[t, c] H[t, c] / H[t, p-1], and dg[t] (if dg is not
+ * NULL) = sum_c dout[t, c] H[t, c] / H[t, p-1].  dout (nb, T, p-1), H and dH
+ * (nb, T, p), each with its own (batch, row) strides, all fp32; dg (nb, T).
+ */
+int smat_normalise_backward(const float* dout, const float* H, const float* g, float* dH,
+                            float* dg, int nb, int T, int p, int64_t o_sb, int64_t o_st,
+                            int64_t h_sb, int64_t h_st, int64_t d_sb, int64_t d_st,
+                            int64_t g_sb, void* stream);
+
+/*
+ * Strided batched GEMM on fp32 MFMA (backward pass building block):
+ *   C[i] = A[i] . B[i]  (beta = 0)  or  C[i] += A[i] . B[i]  (beta = 1),
+ * A[i]: M x K, B[i]: K x N, C[i]: M x N fp32, for i = (i1, i2) in
+ * [0, n1) x [0, n2); element (m, k) of A[i] is A[i1*a1 + i2*a2 + m*am + k*ak],
+ * likewise B with (b1, b2, bk, bn) and C with (c1, c2, cm, cn).  A and B may
+ * be bf16, fp16 or fp32 (dtype_a, dtype_b), widened to fp32.  mask: 0 none,
+ * 1 keep entries with m >= n (zero the rest), 2 keep m <= n.  n1*n2 < 65536.
+ * The products of the backward pass the reference takes from torch autograd
+ * and from the fused kernels of src/smat/kernels/triton_bwd.py:49-237.
+ */
+int smat_bgemm(int dtype_a, int dtype_b, const void* A, const void* B, float* C, int M, int N,
+               int K, int n1, int n2, int64_t a1, int64_t a2, int64_t am, int64_t ak, int64_t b1,
+               int64_t b2, int64_t bk, int64_t bn, int64_t c1, int64_t c2, int64_t cm,
+               int64_t cn, int beta, int mask, void* stream);
+
+/*
  * Whole forward schedule of smat_attention (src/smat/attention.py:391-455) for
  * a geometric mask: pool -> incidence (+ global channel) -> query ->
  * chunk states -> segmented scan -> chunk-local pass -> normalise.

@@ -348,7 +348,8 @@ def walsh_incidence(F):
 def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
                    acc_dtype=None, timer=None, long_range: str = "pooled",
                    scan_backend: str = "auto", incidence_backend: str = "auto",
-                   return_parts: bool = False, workspace: Optional[torch.Tensor] = None):
+                   return_parts: bool = False, workspace: Optional[torch.Tensor] = None,
+                   _no_grad_fn: bool = False):
     """Algorithm 1 of the reference (attention.py:391-455) on the GPU.
 
     Long range (pool by profile, incidence, type-major query) and the causal
@@ -358,6 +359,9 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
     ``lr_pool``, ``lr_incidence``, ``lr_query``, ``scan`` and ``normalise``.
     Without a timer or parts the whole schedule is one library call;
     ``workspace`` (uint8, on the device) may be passed to reuse its scratch.
+    When an input requires grad (and grad mode is on) the call is recorded as
+    one autograd node whose backward runs on the HIP kernels
+    (:class:`smat_attention_amd.kernels.hip_bwd.SmatAttentionFunction`).
     """
     who = "smat_attention"
     _backend(scan_backend, who)
@@ -380,6 +384,15 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
         raise ValueError(f"segment boundary n={n} is not a multiple of chunk={C}")
     _staged(spec, Phi.device)
     idx, indptr, deg = _incidence_args(spec)
+
+    wants_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (Phi, Psi, Vb, g))
+    if wants_grad and not _no_grad_fn:
+        if return_parts or timer is not None:
+            raise NotImplementedError(f"{who}: return_parts/timer are forward-only; call "
+                                      f"under torch.no_grad() or on detached inputs")
+        from .kernels.hip_bwd import SmatAttentionFunction
+        return SmatAttentionFunction.apply(Phi, Psi, Vb, g, spec, C)
 
     if timer is None and not return_parts:
         pc = spec.plane_code_t if _plane_ok(spec, r * Vb.shape[-1]) else None

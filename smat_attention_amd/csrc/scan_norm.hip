@@ -30,6 +30,62 @@ __global__ __launch_bounds__(256) void segment_scan_kernel(const float* __restri
   }
 }
 
+// The mirror image for the backward pass: Sout[c] = sum of D[c'] over the
+// later chunks c' > c of the same segment (the state flowing backwards).
+__global__ __launch_bounds__(256) void segment_scan_rev_kernel(const float* __restrict__ D,
+                                                               float* __restrict__ Sout, int nc,
+                                                               int nc0, int64_t rp) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const int seg = blockIdx.z;
+  if (e >= rp) return;
+  const int c_lo = seg == 0 ? 0 : nc0;
+  const int c_hi = seg == 0 ? nc0 : nc;
+  const float* Db = D + b * nc * rp + e;
+  float* Sb = Sout + b * nc * rp + e;
+  float run = 0.f;
+  for (int c = c_hi - 1; c >= c_lo; --c) {
+    const float d = Db[(int64_t)c * rp];
+    Sb[(int64_t)c * rp] = run;
+    run += d;
+  }
+}
+
+// Backward of out = H[:, :p-1] / H[:, p-1] * g, one wave per row:
+//   dH_c = dout_c g / den (c < p-1),  dH_{p-1} = -sum_c dH_c H_c / den,
+//   dg = sum_c dout_c H_c / den.
+__global__ __launch_bounds__(256) void normalise_bwd_kernel(
+    const float* __restrict__ dout, const float* __restrict__ H, const float* __restrict__ g,
+    float* __restrict__ dH, float* __restrict__ dg, int T, int p, int64_t o_sb, int64_t o_st,
+    int64_t h_sb, int64_t h_st, int64_t d_sb, int64_t d_st, int64_t g_sb) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  const int64_t b = blockIdx.y;
+  const int lane = lane_id();
+  if (row >= T) return;
+  const float* h = H + b * h_sb + row * h_st;
+  const float* d = dout + b * o_sb + row * o_st;
+  float* dh = dH + b * d_sb + row * d_st;
+  const float den = h[p - 1];
+  const float inv = 1.f / den;
+  const float gate = g ? g[b * g_sb + row] : 1.f;
+  float sh = 0.f, sg = 0.f;
+  for (int c = lane; c < p - 1; c += 64) {
+    const float o = h[c] * inv;
+    const float dc = d[c] * gate * inv;
+    dh[c] = dc;
+    sh += dc * o;
+    sg += d[c] * o;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    sh += __shfl_down(sh, off, 64);
+    sg += __shfl_down(sg, off, 64);
+  }
+  if (lane == 0) {
+    dh[p - 1] = -sh;
+    if (dg) dg[b * T + row] = sg;
+  }
+}
+
 int segment_scan_dispatch(const float* D, float* Sin, int nb, int nc, int nc0, int64_t rp,
                           hipStream_t stream) {
   if (nb == 0 || nc == 0 || rp == 0) return SMAT_OK;
@@ -97,4 +153,35 @@ extern "C" int smat_normalise(const float* H, const float* Y, const float* g, fl
   SMAT_REQUIRE(h_st >= p && o_st >= p - 1, SMAT_EINVAL, "smat_normalise: row stride too short");
   return normalise_dispatch(H, Y, g, out, nb, T, n, p, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb,
                             (hipStream_t)stream);
+}
+
+extern "C" int smat_segment_scan_reverse(const float* D, float* Sout, int nb, int nc, int nc0,
+                                         int64_t rp, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(D && Sout && D != Sout, SMAT_EINVAL,
+               "smat_segment_scan_reverse: null or aliased D/Sout");
+  SMAT_REQUIRE(nb >= 0 && nc >= 0 && nc0 >= 0 && nc0 <= nc && rp >= 0, SMAT_EINVAL,
+               "smat_segment_scan_reverse: need 0 <= nc0 <= nc (nc=%d nc0=%d)", nc, nc0);
+  if (nb == 0 || nc == 0 || rp == 0) return SMAT_OK;
+  dim3 grid((unsigned)((rp + 255) / 256), (unsigned)nb, 2);
+  hipLaunchKernelGGL(segment_scan_rev_kernel, grid, dim3(256), 0, (hipStream_t)stream, D, Sout, nc,
+                     nc0, rp);
+  return launch_status("smat_segment_scan_reverse");
+}
+
+extern "C" int smat_normalise_backward(const float* dout, const float* H, const float* g,
+                                       float* dH, float* dg, int nb, int T, int p, int64_t o_sb,
+                                       int64_t o_st, int64_t h_sb, int64_t h_st, int64_t d_sb,
+                                       int64_t d_st, int64_t g_sb, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(dout && H && dH, SMAT_EINVAL, "smat_normalise_backward: null pointer");
+  SMAT_REQUIRE(nb >= 0 && T >= 0 && p >= 2 && h_st >= p && d_st >= p && o_st >= p - 1,
+               SMAT_EINVAL, "smat_normalise_backward: bad sizes");
+  if (nb == 0 || T == 0) return SMAT_OK;
+  dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
+  hipLaunchKernelGGL(normalise_bwd_kernel, grid, dim3(256), 0, (hipStream_t)stream, dout, H, g, dH,
+                     dg, T, p, o_sb, o_st, h_sb, h_st, d_sb, d_st, g_sb);
+  return launch_status("smat_normalise_backward");
 }

@@ -5,3 +5,4 @@
 an alias so code written against the reference's module path keeps working.
 """
 from . import hip_fwd  # noqa: F401
+from . import hip_bwd  # noqa: F401

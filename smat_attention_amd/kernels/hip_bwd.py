@@ -1,0 +1,272 @@
+"""Gradients of the SMat schedule on HIP (gfx950).
+
+Counterpart of ``src/smat/kernels/triton_bwd.py``.  The reference wraps its
+three forward kernels in autograd Functions and patches them into the kernel
+table (``patch()``, triton_bwd.py:334-346), leaving the rest of the schedule
+(chunk summaries, cumsum, query, normalise) to torch autograd; its fused
+backward kernels also stop at ``r, p <= 128`` (triton_bwd.py:166-167).  Here
+the whole schedule is one autograd Function whose backward runs on the HIP
+kernels for any ``r <= 128, p <= 144``:
+
+    out = H[:, :-1] / H[:, -1] * g,     H = H_causal + [0; Y],
+    H_causal  per chunk b:  Phi_b S_b + tril(Phi_b Psi_b^T) Vb_b
+    Y_i = Phi_i U_{i mod B},   U_h = sum_{x in H_h} F_x (+ F_glob),
+    F_x = sum_{j: prof(j) = x} Psi_j Vb_j^T
+
+    dH            normalise backward
+    causal        dA = tril(dH_b Vb_b^T),  A = tril(Phi_b Psi_b^T),
+                  Q_b = sum over later chunks of the segment of Phi^T dH,
+                  dPhi_b = dH_b S_b^T + dA Psi_b
+                  dPsi_b = Vb_b Q_b^T + dA^T Phi_b
+                  dVb_b  = Psi_b Q_b + A^T dH_b
+    long range    dPhi_i += dY_i U_h^T,  dU_h = sum_{i in R_h} Phi_i^T dY_i,
+                  dF = C^T dU (incidence over the transposed table),
+                  dPsi_j += dF_x Vb_j,  dVb_j += dF_x^T Psi_j   (j in profile x)
+
+Every product runs on ``smat_bgemm`` (fp32 MFMA, fp32 accumulation), so the
+gradients are fp32 products summed in fp32 from the stored inputs; they are
+returned in the input dtype, as the reference does.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import DTYPE_CODE, call, ptr, stream_of
+from . import hip_fwd as _hip
+
+__all__ = ["smat_attention_grad", "SmatAttentionFunction", "transposed_incidence",
+           "patch", "unpatch", "patched"]
+
+def _code(t):
+    return DTYPE_CODE[t.dtype]
+
+
+def _bgemm(A, B, C, *, M, N, K, n1, n2, a, b, c, beta=0, mask=0, a_off=0, b_off=0, c_off=0):
+    """C[i] (+)= A[i] B[i] with element strides a = (a1, a2, am, ak), b = (b1, b2, bk, bn),
+    c = (c1, c2, cm, cn); *_off are element offsets added to the base pointers."""
+    if M <= 0 or N <= 0 or n1 <= 0 or n2 <= 0:
+        return
+    # host-side bounds check: the last element each operand addresses must lie
+    # inside its tensor's storage (all strides here are non-negative)
+    for name, t, off, (s1, s2, sr, sc), rows, cols in (
+            ("A", A, a_off, a, M, K), ("B", B, b_off, b, K, N), ("C", C, c_off, c, M, N)):
+        if rows <= 0 or cols <= 0:
+            continue
+        last = off + (n1 - 1) * s1 + (n2 - 1) * s2 + (rows - 1) * sr + (cols - 1) * sc
+        avail = t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+        if min(s1, s2, sr, sc, off) < 0 or last >= avail:
+            raise ValueError(f"smat_bgemm operand {name}: element {last} addressed, "
+                             f"{avail} available")
+    ea, eb = A.element_size(), B.element_size()
+    call("smat_bgemm", _code(A), _code(B), A.data_ptr() + a_off * ea, B.data_ptr() + b_off * eb,
+         C.data_ptr() + c_off * 4, M, N, K, n1, n2, *a, *b, *c, beta, mask, stream_of(C))
+
+
+def transposed_incidence(spec, device):
+    """CSR (indptr, idx) of C^T: for every point x, the row types h whose
+    hyperplane contains x (ascending h); cached on the spec."""
+    key = ("_smat_CT", str(device))
+    hit = getattr(spec, "_smat_CT", None)
+    if hit is not None and hit[0] == key:
+        return hit[1], hit[2]
+    ptr_ = np.asarray(spec.C_indptr, dtype=np.int64)
+    ind = np.asarray(spec.C_indices, dtype=np.int64)
+    rows = np.repeat(np.arange(spec.B, dtype=np.int64), np.diff(ptr_))
+    order = np.lexsort((rows, ind))
+    counts = np.bincount(ind, minlength=spec.N0)
+    indptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    idx = rows[order].astype(np.int32)
+    t_ptr = torch.from_numpy(indptr).to(device)
+    t_idx = torch.from_numpy(idx).to(device)
+    t_idx._smat_checked_N0 = spec.B
+    spec._smat_CT = (key, t_ptr, t_idx)
+    return t_ptr, t_idx
+
+
+def _incidence_rows(src, idx, indptr, n_out, nb, n_in, rp):
+    """out[b, y] = sum_{t in row y} src[b, idx[t]] over (n_in)-row fp32 panels."""
+    out = torch.empty(nb, n_out, rp, device=src.device, dtype=torch.float32)
+    call("smat_incidence", src.data_ptr(), None, idx.data_ptr(), 0, ptr(indptr), 0,
+         out.data_ptr(), nb, n_in, n_out, rp, stream_of(src))
+    return out
+
+
+def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=None,
+                        need_dg: bool = False):
+    """``(dPhi, dPsi, dVb, dg)`` of ``out = smat_attention(Phi, Psi, Vb, spec, g=g)``
+    given the forward's ``U`` (nb, B, r, p) and ``H`` (nb, T, p, long-range
+    term included), fp32 gradients."""
+    nb, T, r = Phi.shape
+    p = Vb.shape[-1]
+    C = min(chunk, T)
+    n, n_P, N0, B = spec.n, spec.n_P, spec.N0, spec.B
+    T_R = T - n
+    dev = Phi.device
+    nc = -(-T // C)
+    Tp = nc * C
+
+    # ---- normalise --------------------------------------------------------
+    dout = dout.float().contiguous()
+    H = H.float().contiguous()
+    dH = torch.zeros(nb, Tp, p, device=dev, dtype=torch.float32)      # rows >= T stay 0
+    dg = torch.empty(nb, T, device=dev, dtype=torch.float32) if need_dg else None
+    gc = g.float().contiguous() if g is not None else None
+    call("smat_normalise_backward", dout.data_ptr(), H.data_ptr(), ptr(gc), dH.data_ptr(),
+         ptr(dg), nb, T, p, dout.stride(0), dout.stride(1), H.stride(0), H.stride(1),
+         dH.stride(0), dH.stride(1), gc.stride(0) if gc is not None else 0, stream_of(dH))
+
+    # inputs padded to whole chunks (zeros contribute nothing)
+    def padded(x):
+        x = x.contiguous()
+        if Tp == T:
+            return x
+        out = torch.zeros(nb, Tp, x.shape[-1], device=dev, dtype=x.dtype)
+        out[:, :T] = x
+        return out
+
+    Ph, Ps, Vv = padded(Phi), padded(Psi), padded(Vb)
+
+    dPhi = torch.empty(nb, Tp, r, device=dev, dtype=torch.float32)
+    dPsi = torch.empty(nb, Tp, r, device=dev, dtype=torch.float32)
+    dVb = torch.empty(nb, Tp, p, device=dev, dtype=torch.float32)
+
+    # ---- causal: states, reverse states, per-chunk products ---------------
+    D = _hip.chunk_states(Ps, Vv, C)                    # (nb, nc, r, p)
+    Sin = _hip.segment_scan(D, n // C)
+    Dr = torch.empty(nb, nc, r, p, device=dev, dtype=torch.float32)
+    rp = r * p
+    # Dr_b = Phi_b^T dH_b
+    _bgemm(Ph, dH, Dr, M=r, N=p, K=C, n1=nb, n2=nc,
+           a=(Tp * r, C * r, 1, r), b=(Tp * p, C * p, p, 1), c=(nc * rp, rp, p, 1))
+    Q = torch.empty_like(Dr)
+    call("smat_segment_scan_reverse", Dr.data_ptr(), Q.data_ptr(), nb, nc, n // C, rp,
+         stream_of(Q))
+    del Dr
+    A = torch.empty(nb, nc, C, C, device=dev, dtype=torch.float32)
+    dA = torch.empty_like(A)
+    CC = C * C
+    # A = tril(Phi_b Psi_b^T), dA = tril(dH_b Vb_b^T)
+    _bgemm(Ph, Ps, A, M=C, N=C, K=r, n1=nb, n2=nc,
+           a=(Tp * r, C * r, r, 1), b=(Tp * r, C * r, 1, r), c=(nc * CC, CC, C, 1), mask=1)
+    _bgemm(dH, Vv, dA, M=C, N=C, K=p, n1=nb, n2=nc,
+           a=(Tp * p, C * p, p, 1), b=(Tp * p, C * p, 1, p), c=(nc * CC, CC, C, 1), mask=1)
+    cr, cp_ = (Tp * r, C * r, r, 1), (Tp * p, C * p, p, 1)
+    # dPhi = dH S^T + dA Psi
+    _bgemm(dH, Sin, dPhi, M=C, N=r, K=p, n1=nb, n2=nc,
+           a=cp_, b=(nc * rp, rp, 1, p), c=cr)
+    _bgemm(dA, Ps, dPhi, M=C, N=r, K=C, n1=nb, n2=nc,
+           a=(nc * CC, CC, C, 1), b=cr, c=cr, beta=1)
+    # dPsi = Vb Q^T + dA^T Phi
+    _bgemm(Vv, Q, dPsi, M=C, N=r, K=p, n1=nb, n2=nc,
+           a=cp_, b=(nc * rp, rp, 1, p), c=cr)
+    _bgemm(dA, Ph, dPsi, M=C, N=r, K=C, n1=nb, n2=nc,
+           a=(nc * CC, CC, 1, C), b=cr, c=cr, beta=1)
+    # dVb = Psi Q + A^T dH
+    _bgemm(Ps, Q, dVb, M=C, N=p, K=r, n1=nb, n2=nc,
+           a=cr, b=(nc * rp, rp, p, 1), c=cp_)
+    _bgemm(A, dH, dVb, M=C, N=p, K=C, n1=nb, n2=nc,
+           a=(nc * CC, CC, 1, C), b=cp_, c=cp_, beta=1)
+    del A, dA, Sin, Q, D
+
+    # ---- long range --------------------------------------------------------
+    if T_R > 0:
+        Uc = U.float().contiguous()
+        dU = torch.empty(nb, B, r, p, device=dev, dtype=torch.float32)
+        full, rem = divmod(T_R, B)
+        Brp = B * rp
+        # rows of type h: n + h + k*B; first `full` rounds for every type, then
+        # one more row for types h < rem
+        if full:
+            _bgemm(dH, Uc, dPhi, M=full, N=r, K=p, n1=nb, n2=B,
+                   a=(Tp * p, p, B * p, 1), b=(Brp, rp, 1, p), c=(Tp * r, r, B * r, 1),
+                   beta=1, a_off=n * p, c_off=n * r)
+            _bgemm(Ph, dH, dU, M=r, N=p, K=full, n1=nb, n2=B,
+                   a=(Tp * r, r, 1, B * r), b=(Tp * p, p, B * p, 1), c=(Brp, rp, p, 1),
+                   a_off=n * r, b_off=n * p)
+        else:
+            dU.zero_()
+        if rem:
+            t0 = n + full * B
+            _bgemm(dH, Uc, dPhi, M=1, N=r, K=p, n1=nb, n2=rem,
+                   a=(Tp * p, p, 0, 1), b=(Brp, rp, 1, p), c=(Tp * r, r, 0, 1),
+                   beta=1, a_off=t0 * p, c_off=t0 * r)
+            _bgemm(Ph, dH, dU, M=r, N=p, K=1, n1=nb, n2=rem,
+                   a=(Tp * r, r, 1, 0), b=(Tp * p, p, 0, 1), c=(Brp, rp, p, 1),
+                   beta=1 if full else 0, a_off=t0 * r, b_off=t0 * p)
+            if not full and rem < B:
+                dU[:, rem:] = 0
+        # dF = C^T dU (and the global channel's sum over all types)
+        t_ptr, t_idx = transposed_incidence(spec, dev)
+        dF = _incidence_rows(dU, t_idx, t_ptr, N0, nb, B, rp)
+        nX = n - n_P
+        gq, grem = divmod(nX, N0)
+        Nrp = N0 * rp
+        # pool backward over profile x's tokens n_P + x + s*N0
+        for lo, hi, cnt in ((0, grem, gq + 1), (grem, N0, gq)):
+            if hi <= lo or cnt <= 0:
+                continue
+            tok0 = n_P + lo
+            _bgemm(Vv, dF, dPsi, M=cnt, N=r, K=p, n1=nb, n2=hi - lo,
+                   a=(Tp * p, p, N0 * p, 1), b=(Nrp, rp, 1, p), c=(Tp * r, r, N0 * r, 1),
+                   beta=1, a_off=tok0 * p, b_off=lo * rp, c_off=tok0 * r)
+            _bgemm(Ps, dF, dVb, M=cnt, N=p, K=r, n1=nb, n2=hi - lo,
+                   a=(Tp * r, r, N0 * r, 1), b=(Nrp, rp, p, 1), c=(Tp * p, p, N0 * p, 1),
+                   beta=1, a_off=tok0 * r, b_off=lo * rp, c_off=tok0 * p)
+        if n_P:
+            allrows = torch.arange(B, device=dev, dtype=torch.int32)
+            allrows._smat_checked_N0 = B
+            aptr = torch.tensor([0, B], device=dev, dtype=torch.int64)
+            dFg = _incidence_rows(dU, allrows, aptr, 1, nb, B, rp)
+            _bgemm(Vv, dFg, dPsi, M=n_P, N=r, K=p, n1=nb, n2=1,
+                   a=(Tp * p, 0, p, 1), b=(rp, 0, 1, p), c=(Tp * r, 0, r, 1), beta=1)
+            _bgemm(Ps, dFg, dVb, M=n_P, N=p, K=r, n1=nb, n2=1,
+                   a=(Tp * r, 0, r, 1), b=(rp, 0, p, 1), c=(Tp * p, 0, p, 1), beta=1)
+    return dPhi[:, :T], dPsi[:, :T], dVb[:, :T], dg
+
+
+class SmatAttentionFunction(torch.autograd.Function):
+    """``smat_attention`` (pooled schedule, geometric mask) with its HIP backward."""
+
+    @staticmethod
+    def forward(ctx, Phi, Psi, Vb, g, spec, chunk):
+        from .. import attention as A
+        out, parts = A.smat_attention(Phi.detach(), Psi.detach(), Vb.detach(), spec,
+                                      chunk=chunk, g=None if g is None else g.detach(),
+                                      return_parts=True, _no_grad_fn=True)
+        ctx.save_for_backward(Phi, Psi, Vb, g, parts["U"], parts["H"])
+        ctx.spec, ctx.chunk = spec, chunk
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        Phi, Psi, Vb, g, U, H = ctx.saved_tensors
+        need_dg = g is not None and ctx.needs_input_grad[3]
+        dPhi, dPsi, dVb, dg = smat_attention_grad(Phi, Psi, Vb, ctx.spec, U, H, dout,
+                                                  chunk=ctx.chunk, g=g, need_dg=need_dg)
+        return (dPhi.to(Phi.dtype) if ctx.needs_input_grad[0] else None,
+                dPsi.to(Psi.dtype) if ctx.needs_input_grad[1] else None,
+                dVb.to(Vb.dtype) if ctx.needs_input_grad[2] else None,
+                dg.to(g.dtype) if need_dg else None, None, None)
+
+
+# The reference's patch()/unpatch() make its kernel path differentiable
+# (triton_bwd.py:334-346); without them backend="auto" silently drops the
+# kernels' gradients.  Here smat_attention is differentiable whenever an input
+# requires grad, so these only record the request, for callers that use them.
+_PATCHED = [False]
+
+
+def patch():
+    _PATCHED[0] = True
+
+
+def unpatch():
+    _PATCHED[0] = False
+
+
+def patched() -> bool:
+    return _PATCHED[0]
