@@ -109,7 +109,11 @@ class Events:
 
 
 def kernel_table(spec, Phi, Psi, Vb, reps):
-    """Average duration and algorithmic traffic/work of every kernel of the forward."""
+    """Average duration and algorithmic traffic/work of each stage of the fused
+    forward, timed with events on torch's current stream (the kernels' stream):
+    pool, incidence, type-major query, and the fused causal pass (chunk-group
+    Gram prepass + group scan + the scan kernel that also adds Y, normalises
+    and writes the output)."""
     import torch
     from smat_attention_amd import attention as A
     from smat_attention_amd.kernels import hip_fwd as K
@@ -117,16 +121,12 @@ def kernel_table(spec, Phi, Psi, Vb, reps):
     nb, T, r = Phi.shape
     p = Vb.shape[-1]
     n, C, N0, B, T_R = spec.n, 128, spec.N0, spec.B, spec.T_R
-    nc = T // C
     eb = Phi.element_size()
     rp4 = r * p * 4
     F = K.pool(Psi, Vb, spec.n_P, n, N0)
     U = A.apply_incidence(F, spec)
-    D = K.chunk_states(Psi, Vb, C)
-    Sin = K.segment_scan(D, n // C)
-    H = K.chunk_local(Phi.reshape(nb, nc, C, r), Psi.reshape(nb, nc, C, r),
-                      Vb.reshape(nb, nc, C, p), Sin).reshape(nb, T, p)
     Y = K.query(Phi[:, n:], U)
+    out = torch.empty(nb, T, p - 1, device=Phi.device)
     rows = {}
     # algorithmic bytes: each operand read once and each result written once
     rows["pool"] = dict(us=ev.time(lambda: K.pool(Psi, Vb, spec.n_P, n, N0), reps),
@@ -137,19 +137,10 @@ def kernel_table(spec, Phi, Psi, Vb, reps):
     rows["query"] = dict(us=ev.time(lambda: K.query(Phi[:, n:], U), reps),
                          bytes=nb * (B * rp4 + T_R * r * eb + T_R * p * 4),
                          flops=2 * nb * T_R * r * p)
-    rows["chunk_states"] = dict(us=ev.time(lambda: K.chunk_states(Psi, Vb, C), reps),
-                                bytes=nb * (T * (r + p) * eb + nc * rp4),
-                                flops=2 * nb * T * r * p)
-    rows["segment_scan"] = dict(us=ev.time(lambda: K.segment_scan(D, n // C), reps),
-                                bytes=nb * 2 * nc * rp4, flops=nb * nc * r * p)
-    rows["chunk_local"] = dict(
-        us=ev.time(lambda: K.chunk_local(Phi.reshape(nb, nc, C, r), Psi.reshape(nb, nc, C, r),
-                                         Vb.reshape(nb, nc, C, p), Sin), reps),
-        bytes=nb * (T * (2 * r + p) * eb + nc * rp4 + T * p * 4),
-        flops=2 * nb * (T * (C + 1) // 2 * (r + p) + T * r * p))
-    rows["normalise"] = dict(us=ev.time(lambda: K.normalise(H, n, Y), reps),
-                             bytes=nb * (T * p * 4 + T_R * p * 4 + T * (p - 1) * 4),
-                             flops=nb * T * (p - 1))
+    rows["causal_scan"] = dict(
+        us=ev.time(lambda: K.causal_scan(Phi, Psi, Vb, n, C, Y=Y, out=out), reps),
+        bytes=nb * (T * (2 * r + p) * eb + T_R * p * 4 + T * (p - 1) * 4),
+        flops=2 * nb * (T * (C + 1) / 2 * (r + p) + 2 * T * r * p))
     for k, v in rows.items():
         v["GBs"] = v["bytes"] / (v["us"] * 1e-6) / 1e9
         v["TFLOPs"] = v["flops"] / (v["us"] * 1e-6) / 1e12
@@ -230,13 +221,33 @@ def decode_bench(args):
         dec.step(ph[i], ps[i], vb[i], out=out)
     e1.record(s)
     e1.synchronize()
-    us = e0.elapsed_time(e1) / steps * 1e3
+    us_eager = e0.elapsed_time(e1) / steps * 1e3
+    # the same steps captured once into a HIP graph and replayed: no host
+    # launch cost between steps (an even step count returns the double-buffered
+    # state to the buffer it started in)
+    gsteps = steps - (steps % 2)
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(s)
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(gsteps):
+                dec.step(ph[i], ps[i], vb[i], out=out)
+    s.wait_stream(cap)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0.record(s)
+    graph.replay()
+    e1.record(s)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) / gsteps * 1e3
     # per step and sequence: U[type] read, S read, S write (r*p fp32 each), plus io
     step_bytes = nb * (3 * r * p * 4 + (2 * r + p) * 2 + (p - 1) * 4)
     return {"us_per_step": round(us, 2), "GBs": round(step_bytes / (us * 1e-6) / 1e9, 1),
             "frac_hbm": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "us_per_step_eager": round(us_eager, 2),
             "config": f"nb=128 (B=16,H=8), r=128, p=129, d=3, prefill {T_pre}, "
-                      f"B_types={spec.B}, eager launches",
+                      f"B_types={spec.B}, {gsteps} steps replayed from one HIP graph",
             "bytes_per_step": step_bytes, "U_cache_GB": round(dec.U.numel() * 4 / 1e9, 2)}
 
 

@@ -3,21 +3,23 @@
 //   S' = S + psi vb^T;   o = phi (S' + U[step mod B]);   out = o[:p-1] / o[p-1]
 //
 // A bandwidth kernel: per sequence it reads S and U_h (r*p fp32 each) and
-// writes S' once.  Workgroups own 32-column groups of one sequence; 8 thread
-// rows split the features and reduce through LDS.  Every group also needs the
-// normaliser column, which only one group advances, so the state is
-// double-buffered (S in, S' out): no group ever reads a column another group
-// has already advanced.
+// writes S' once.  The state is double-buffered (S in, S' out) so a step never
+// reads what it writes; the caller swaps the buffers.
 #include "smat_host.hpp"
 
 namespace smat {
 
 namespace dc {
-constexpr int kThreads = 256;
-constexpr int kCols = 32;
-constexpr int kParts = kThreads / kCols;   // 8 feature partitions
+constexpr int kThreads = 1024;
+constexpr int kCols = 144;                // p <= 144 columns, one thread column each
+constexpr int kParts = kThreads / kCols;  // 7 feature partitions (1008 threads busy)
 }  // namespace dc
 
+// One workgroup per sequence: thread (part, c) owns column c of the rows
+// a = part, part + 7, ...; it advances S there (S_out = S_in + psi vb^T) and
+// accumulates phi_a (S_out + U_h)[a][c].  The 7 partial sums of each column
+// meet in LDS, which also hands every column the normaliser o[p-1] -- one read
+// of S, U_h and one write of S per sequence, nothing recomputed.
 template <typename In>
 __global__ __launch_bounds__(dc::kThreads) void decode_step_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
@@ -26,14 +28,11 @@ __global__ __launch_bounds__(dc::kThreads) void decode_step_kernel(
     int64_t q_sb, int64_t k_sb, int64_t v_sb) {
   using namespace dc;
   __shared__ float sphi[kMaxR], spsi[kMaxR], svb[kMaxP];
-  __shared__ float red[kParts][kCols + 1];
-  __shared__ float den_s;
-  __shared__ float wsum[kThreads / 64];
+  __shared__ float red[kParts][kCols];
 
-  const int64_t b = blockIdx.y;
-  const int c0 = blockIdx.x * kCols;
+  const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
-  const int cl = tid % kCols, part = tid / kCols;
+  const int c = tid % kCols, part = tid / kCols;
   const int h = (int)(step % B);
 
   if (tid < r) {
@@ -48,45 +47,46 @@ __global__ __launch_bounds__(dc::kThreads) void decode_step_kernel(
   float* Sob = S_out + b * rp;
   const float* Ub = U + (b * B + h) * rp;
 
-  const int c = c0 + cl;
   float acc = 0.f;
-  if (c < p) {
+  if (part < kParts && c < p) {
     const float vc = svb[c];
-    for (int a = part; a < r; a += kParts) {
+    int a = part;
+    // rows in groups of 4: eight loads issued before the first use
+    for (; a + 3 * kParts < r; a += 4 * kParts) {
+      float sv[4], uv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t o = (int64_t)(a + u * kParts) * p + c;
+        sv[u] = Sb[o];
+        uv[u] = Ub[o];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int au = a + u * kParts;
+        const float s = sv[u] + spsi[au] * vc;
+        Sob[(int64_t)au * p + c] = s;
+        acc += sphi[au] * (s + uv[u]);
+      }
+    }
+    for (; a < r; a += kParts) {
       const int64_t o = (int64_t)a * p + c;
       const float s = Sb[o] + spsi[a] * vc;
       Sob[o] = s;
       acc += sphi[a] * (s + Ub[o]);
     }
   }
-  red[part][cl] = acc;
+  if (part < kParts) red[part][c] = acc;
   __syncthreads();
 
-  // The normaliser o[p-1], computed the same way by every column group (so
-  // all groups divide by the same value) from the incoming state.
-  {
-    float v = 0.f;
-    for (int a = tid; a < r; a += kThreads) {
-      const int64_t o = (int64_t)a * p + (p - 1);
-      v += sphi[a] * ((Sb[o] + spsi[a] * svb[p - 1]) + Ub[o]);
+  if (tid < p) {
+    float o = 0.f, den = 0.f;
+#pragma unroll
+    for (int i = 0; i < kParts; ++i) {
+      o += red[i][tid];
+      den += red[i][p - 1];
     }
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
-    if ((tid & 63) == 0) wsum[tid >> 6] = v;
-    __syncthreads();
-    if (tid == 0) {
-      float t = 0.f;
-      for (int i = 0; i < kThreads / 64; ++i) t += wsum[i];
-      den_s = t;
-    }
-  }
-  __syncthreads();
-
-  if (tid < kCols && c0 + tid < p) {
-    float o = 0.f;
-    for (int i = 0; i < kParts; ++i) o += red[i][tid];
-    const int cc = c0 + tid;
-    if (o_full) o_full[b * p + cc] = o;
-    if (cc < p - 1) out[b * (p - 1) + cc] = o / den_s;
+    if (o_full) o_full[b * p + tid] = o;
+    if (tid < p - 1) out[b * (p - 1) + tid] = o / den;
   }
 }
 
@@ -95,10 +95,9 @@ static int launch_decode(const void* phi, const void* psi, const void* vb, const
                          float* S_out, const float* U, float* out, float* o_full, int nb, int B,
                          int r, int p, int64_t step, int64_t q_sb, int64_t k_sb, int64_t v_sb,
                          hipStream_t stream) {
-  dim3 grid((unsigned)((p + dc::kCols - 1) / dc::kCols), (unsigned)nb);
-  hipLaunchKernelGGL(decode_step_kernel<In>, grid, dim3(dc::kThreads), 0, stream, (const In*)phi,
-                     (const In*)psi, (const In*)vb, S_in, S_out, U, out, o_full, B, r, p, step,
-                     q_sb, k_sb, v_sb);
+  hipLaunchKernelGGL(decode_step_kernel<In>, dim3((unsigned)nb), dim3(dc::kThreads), 0, stream,
+                     (const In*)phi, (const In*)psi, (const In*)vb, S_in, S_out, U, out, o_full,
+                     B, r, p, step, q_sb, k_sb, v_sb);
   return launch_status("smat_decode_step");
 }
 
