@@ -34,6 +34,7 @@ constexpr int kPlanesPerWG = kWaves * kPlanesPerWave;
 constexpr int kXCD = 8;
 constexpr int kUnroll = 8;                // loads in flight per lane (L2 kernel)
 constexpr int kLdsBudget = 150 * 1024;    // bytes of LDS for the F panel
+constexpr int kPlaneLdsBudget = 160 * 1024;   // the plane kernel's panel + line table
 }  // namespace inc
 
 __device__ __forceinline__ void add4(float4& a, const float4& v) {
@@ -144,31 +145,41 @@ __global__ __launch_bounds__(inc::kThreads) void incidence_lds_kernel(
 // LDS panel kernel, lines of the affine plane (d = 3) generated in-kernel
 // ---------------------------------------------------------------------------
 
-// For d = 3 every row type is a line <a_e, x> = b of F_q^2, with a_e = (0, 1)
-// for e = 0 and a_e = (1, e-1) otherwise, and point x = x0*q + x1.  Its q
-// points are generated from code[h] = e*q + b instead of being read from the
-// table: no index traffic at all.  Line e = 0: x1 = b, x0 = 0..q-1; line
-// (1, m): x0 = b - m*x1 mod q for x1 = 0..q-1.  Points are summed in that
-// order.
+// For d = 3 every row type is a line <a_e, x> = b of F_q^2 (a_0 = (0, 1),
+// a_e = (1, e-1) for e >= 1), point x = x0*q + x1.  Its q points follow from
+// the line code e*q + b, so no index table is read: a line with e >= 1 has one
+// point in each column x1 (x0 = b - m*x1 mod q, m = e-1), the line e = 0 is
+// the column x1 = b.
 //
-// One lane owns one line and all E floats of the slice, so the point
-// arithmetic is paid once per E adds.  The panel stores point x's four
-// 16-byte chunks rotated by x>>1 (chunk k at slot (k + (x>>1)) & 3): the
-// 16-byte bank group of (x, k) is then 4*(x&1) + ((k + (x>>1)) & 3), i.e. a
-// bijection of x mod 8.  Consecutive lanes own lines b, b+1, ... of one
-// direction, whose points at any step have consecutive x0 and hence, q being
-// odd, distinct x mod 8: the eight lanes an LDS cycle serves hit eight
-// different bank groups.
-template <int E>
-__global__ __launch_bounds__(1024) void incidence_plane_kernel(
+// The N0 x E slice of F is staged in LDS column by column: entry W*x1 + i holds
+// point (i mod q, x1) for i in [0, W), W = q + 15, so each column's first 15
+// points appear twice.  The E floats of an entry are split into Q = E/4
+// 16-byte chunks kept in Q separate planes of PLANE entries (chunk k of entry P
+// at float4 index k*PLANE + P), so a lane's Q reads of one entry share one
+// address and differ by an immediate offset.  Sixteen consecutive lanes own
+// the lines b0 .. b0+15 of one direction.  At step x1 = t they need
+// x0 = s + j (mod q), j = 0..15, s = b0 - m*t mod q: the entries W*t + s + j,
+// sixteen CONSECUTIVE entries (the duplicates absorb the wrap), i.e. 256
+// contiguous bytes of a plane: one ds_read_b128 of sixteen lanes touches each
+// of the 64 banks once.  Lines e = 0 walk their column from a lane-dependent
+// start, entry W*b + j + t, so neighbouring lanes are W + 1 entries apart --
+// an odd stride for odd q, again sixteen distinct bank groups.  Points are
+// summed in x1 order (e >= 1) or from the lane's start around the column
+// (e = 0).
+template <int E, int PLANE, int MINB>
+__global__ __launch_bounds__(1024, MINB) void incidence_plane_kernel(
     const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
     int q, float* __restrict__ U, int N0, int B, int64_t rp, int nslices, int64_t total,
     int64_t per_xcd) {
   using namespace inc;
-  constexpr int kT = 1024;          // 16 waves: four per SIMD to cover LDS latency
-  constexpr int Q = E / 4;          // float4 per point
-  constexpr int kU = 4;             // points in flight per lane
-  extern __shared__ float4 panel[];
+  constexpr int kT = 1024;
+  constexpr int Q = E / 4;          // 16-byte chunks per entry = planes
+  constexpr int kU = 4;             // steps in flight per lane
+  extern __shared__ float4 smem[];
+  const int W = q + 15;
+  const int nlines = q * (q + 1);
+  float4* panel = smem;
+  short* line_type = reinterpret_cast<short*>(smem + (size_t)Q * PLANE);
 
   const int64_t L = blockIdx.x;
   const int64_t work = (L % kXCD) * per_xcd + L / kXCD;
@@ -177,71 +188,90 @@ __global__ __launch_bounds__(1024) void incidence_plane_kernel(
   const int slice = (int)(work - b * nslices);
   const int64_t e0 = (int64_t)slice * E;
 
+  // line code -> row type (the inverse of code[])
+  for (int c = threadIdx.x; c < nlines; c += kT) line_type[c] = -1;
   const float* Fb = F + b * (int64_t)N0 * rp + e0;
-  for (int i = threadIdx.x; i < N0 * Q; i += kT) {
-    const int x = i / Q, k = i - x * Q;
+  for (int idx = threadIdx.x; idx < N0 * Q; idx += kT) {
+    const int x = idx / Q, k = idx - x * Q;
+    const int x0 = x / q, x1 = x - x0 * q;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (e0 + 4 * k < rp) v = *reinterpret_cast<const float4*>(Fb + (int64_t)x * rp + 4 * k);
-    panel[x * Q + ((k + (x >> 1)) & (Q - 1))] = v;
+    for (int i = x0; i < W; i += q) panel[k * PLANE + W * x1 + i] = v;
+  }
+  __syncthreads();
+  for (int h = threadIdx.x; h < B; h += kT) {
+    const int c = code[h];
+    if (c >= 0 && c < nlines) line_type[c] = (short)h;
   }
   __syncthreads();
 
   float* Ub = U + b * (int64_t)B * rp + e0;
-  for (int h = threadIdx.x; h < B; h += kT) {
-    const int c = code[h];
-    const int e = c / q, off = c - e * q;
+  const float* Fgb = Fg ? Fg + b * rp + e0 : nullptr;
+  const int gpd = (q + 15) >> 4;                 // 16-lane groups per direction
+  const int ngroups = gpd * (q + 1);
+  const int j = threadIdx.x & 15;
+  for (int G = threadIdx.x >> 4; G < ngroups; G += kT / 16) {
+    const int e = G / gpd;
+    const int b0 = (G - e * gpd) * 16;
+    const int bl = b0 + j;
+    const int bb = bl < q ? bl : q - 1;          // idle lanes shadow the last line
     const int m = e == 0 ? 0 : e - 1;
+    const int stride = e == 0 ? 1 : W;
+    int pt = e == 0 ? W * bb + j : j;            // entry of step t, less s
+    int s = e == 0 ? 0 : b0;
     float4 acc[Q];
 #pragma unroll
     for (int k = 0; k < Q; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    int x0 = e == 0 ? 0 : off, x1 = e == 0 ? off : 0;
     int t = 0;
     for (; t + kU <= q; t += kU) {
-      int xs[kU];
+      const float4* row[kU];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
-        xs[u] = x0 * q + x1;
-        if (e == 0) {
-          ++x0;
-        } else {
-          ++x1;
-          x0 -= m;
-          if (x0 < 0) x0 += q;
-        }
+        row[u] = panel + pt + s;
+        pt += stride;
+        s -= m;
+        s += s < 0 ? q : 0;
       }
       float4 v[kU][Q];
 #pragma unroll
       for (int u = 0; u < kU; ++u)
 #pragma unroll
-        for (int k = 0; k < Q; ++k) v[u][k] = panel[xs[u] * Q + ((k + (xs[u] >> 1)) & (Q - 1))];
+        for (int k = 0; k < Q; ++k) v[u][k] = row[u][k * PLANE];
 #pragma unroll
       for (int u = 0; u < kU; ++u)
 #pragma unroll
         for (int k = 0; k < Q; ++k) add4(acc[k], v[u][k]);
     }
     for (; t < q; ++t) {
-      const int x = x0 * q + x1;
+      const float4* row = panel + pt + s;
+      pt += stride;
+      s -= m;
+      s += s < 0 ? q : 0;
 #pragma unroll
-      for (int k = 0; k < Q; ++k) add4(acc[k], panel[x * Q + ((k + (x >> 1)) & (Q - 1))]);
-      if (e == 0) {
-        ++x0;
-      } else {
-        ++x1;
-        x0 -= m;
-        if (x0 < 0) x0 += q;
-      }
+      for (int k = 0; k < Q; ++k) add4(acc[k], row[k * PLANE]);
     }
+    if (bl < q) {
+      const int h = line_type[e * q + bl];
+      if (h >= 0) {
 #pragma unroll
-    for (int k = 0; k < Q; ++k) {
-      if (e0 + 4 * k < rp) {
-        if (Fg) add4(acc[k], *reinterpret_cast<const float4*>(Fg + b * rp + e0 + 4 * k));
-        *reinterpret_cast<float4*>(Ub + (int64_t)h * rp + 4 * k) = acc[k];
+        for (int k = 0; k < Q; ++k) {
+          if (e0 + 4 * k < rp) {
+            if (Fgb) add4(acc[k], *reinterpret_cast<const float4*>(Fgb + 4 * k));
+            *reinterpret_cast<float4*>(Ub + (int64_t)h * rp + 4 * k) = acc[k];
+          }
+        }
       }
     }
   }
 }
 
-template <int E>
+// LDS bytes of the plane kernel: Q planes of PLANE entries and the line table.
+static int64_t plane_lds_bytes(int q, int E, int plane) {
+  (void)E;
+  return (int64_t)(E / 4) * plane * 16 + (((int64_t)q * (q + 1) * 2 + 15) & ~(int64_t)15);
+}
+
+template <int E, int PLANE, int MINB>
 static int launch_plane(const float* F, const float* F_glob, const int* code, int q, float* U,
                         int nb, int N0, int B, int64_t rp, hipStream_t stream) {
   using namespace inc;
@@ -249,12 +279,12 @@ static int launch_plane(const float* F, const float* F_glob, const int* code, in
   const int64_t total = (int64_t)nb * nslices;
   const int64_t per_xcd = (total + kXCD - 1) / kXCD;
   const int64_t grid = per_xcd * kXCD;
-  const size_t smem = (size_t)N0 * E * 4;
-  auto kern = incidence_plane_kernel<E>;
+  const size_t smem = (size_t)plane_lds_bytes(q, E, PLANE);
+  auto kern = incidence_plane_kernel<E, PLANE, MINB>;
   static bool attr_set = false;
   if (!attr_set) {
-    hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        inc::kLdsBudget);
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kPlaneLdsBudget);
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(1024), smem, stream, F, F_glob, code, q,
@@ -425,17 +455,27 @@ int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int
 int incidence_plane_dispatch(const float* F, const float* F_glob, const int* code, int q,
                              float* U, int nb, int N0, int B, int64_t rp, hipStream_t stream) {
   if (nb == 0 || B == 0 || rp == 0) return SMAT_OK;
-  const int E = lds_slice_width(N0);
   const bool aligned = (rp % 4 == 0) && aligned16(F) && aligned16(U) &&
                        (!F_glob || aligned16(F_glob));
-  if (!aligned || E == 0 || (int64_t)q * q != N0) {
-    set_error("smat_incidence_plane: needs rp %% 4 == 0, aligned tables, N0 = q^2 and a panel "
-              "that fits LDS (q=%d N0=%d rp=%lld)", q, N0, (long long)rp);
+  if (!aligned || (int64_t)q * q != N0 || q > 181) {
+    set_error("smat_incidence_plane: needs rp %% 4 == 0, aligned tables and N0 = q^2 "
+              "(q=%d N0=%d rp=%lld)", q, N0, (long long)rp);
     return SMAT_EUNSUPPORTED;
   }
-  if (E == 16) return launch_plane<16>(F, F_glob, code, q, U, nb, N0, B, rp, stream);
-  if (E == 8) return launch_plane<8>(F, F_glob, code, q, U, nb, N0, B, rp, stream);
-  return launch_plane<4>(F, F_glob, code, q, U, nb, N0, B, rp, stream);
+  // Two workgroups per CU at E = 8 (one stages its panel while the other sums)
+  // measured ahead of one at E = 16; wider panels fall back to one per CU.
+  const int64_t entries = (int64_t)q * (q + 15);
+  const int64_t budget = inc::kPlaneLdsBudget;
+#define SMAT_PLANE_TRY(E_, PL_, MB_)                                                   \
+  if (entries <= PL_ && MB_ * plane_lds_bytes(q, E_, PL_) <= budget)                   \
+    return launch_plane<E_, PL_, MB_>(F, F_glob, code, q, U, nb, N0, B, rp, stream);
+  SMAT_PLANE_TRY(8, 2304, 2)
+  SMAT_PLANE_TRY(16, 2304, 1)
+  SMAT_PLANE_TRY(8, 4608, 1)
+  SMAT_PLANE_TRY(4, 9216, 1)
+#undef SMAT_PLANE_TRY
+  set_error("smat_incidence_plane: the F panel of q=%d does not fit LDS", q);
+  return SMAT_EUNSUPPORTED;
 }
 
 }  // namespace smat
