@@ -71,6 +71,8 @@ struct FwdLayout {
 };
 
 static inline int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+// Row stride of the long-range term Y: 16-byte rows for vector access.
+static inline int64_t y_stride(int p) { return (p + 3) & ~3; }
 
 static FwdLayout fwd_layout(int nb, int T, int n, int N0, int B, int n_P, int C, int r, int p,
                             bool want_H) {
@@ -83,7 +85,7 @@ static FwdLayout fwd_layout(int nb, int T, int n, int N0, int B, int n_P, int C,
   L.F = off;   off += al256((int64_t)nb * N0 * rp * 4);
   L.Fg = off;  off += n_P > 0 ? al256((int64_t)nb * rp * 4) : 0;
   L.U = off;   off += al256((int64_t)nb * B * rp * 4);
-  L.Y = off;   off += al256((int64_t)nb * T_R * p * 4);
+  L.Y = off;   off += al256((int64_t)nb * T_R * y_stride(p) * 4);
   if (L.fused) {
     L.scan = off; off += al256(causal_scan_workspace_bytes(nb, T, C, r, p));
   } else {
@@ -152,6 +154,7 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
   const int64_t rp = (int64_t)r * p;
   const int nc = (T + C - 1) / C;
   const int T_R = T - n;
+  const int64_t yst = y_stride(p);
   int rc;
 
   // ---- long range: S^T, then C, then R ---------------------------------
@@ -171,8 +174,8 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
   }
   if (T_R > 0) {
     const char* phi_rec = (const char*)phi + (int64_t)n * q_st * elem_bytes(dtype);
-    rc = query_dispatch(dtype, phi_rec, U, Y, nb, T_R, B, r, p, q_sb, q_st, (int64_t)T_R * p, p,
-                        st);
+    rc = query_dispatch(dtype, phi_rec, U, Y, nb, T_R, B, r, p, q_sb, q_st, (int64_t)T_R * yst,
+                        yst, st);
     if (rc) return rc;
   }
 
@@ -180,7 +183,7 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
   if (L.fused) {
     // one kernel: segmented scan, + Y on recent rows, normalise, gate
     return causal_scan_dispatch(dtype, phi, psi, vb, T_R > 0 ? Y : nullptr, g, out, nb, T, n, C,
-                                r, p, q_sb, q_st, k_sb, k_st, v_sb, v_st, (int64_t)T_R * p, p,
+                                r, p, q_sb, q_st, k_sb, k_st, v_sb, v_st, (int64_t)T_R * yst, yst,
                                 o_sb, o_st, g_sb, 0, ws + L.scan, L.part - L.scan, st);
   }
   // staged: chunk summaries, segmented scan, chunk-local pass into H, normalise
@@ -229,5 +232,5 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     }
   }
   return normalise_dispatch(H, T_R > 0 ? Y : nullptr, g, out, nb, T, n, p, h_sb, p,
-                            (int64_t)T_R * p, p, o_sb, o_st, g_sb, st);
+                            (int64_t)T_R * yst, yst, o_sb, o_st, g_sb, st);
 }

@@ -47,15 +47,6 @@ constexpr int block_bytes() {
 }
 }  // namespace sf
 
-struct ScanArgs {
-  int T, n, C, K, nc, nc0, ng0, r, p;
-  int64_t q_sb, q_st, k_sb, k_st, v_sb, v_st;
-  int64_t y_sb, y_st;   // Y rows are recent rows t - n
-  int64_t o_sb, o_st;
-  int64_t g_sb;
-  int write_H;          // 1: out is H (nb, T, p) unnormalised, no Y / gate
-};
-
 template <typename In, bool VEC>
 __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
@@ -426,6 +417,11 @@ int chunk_states_dispatch(int dtype, const void* psi, const void* vb, float* D, 
                           hipStream_t stream, int* ngroups_out, int* ng0_out);
 int segment_scan_dispatch(const float* D, float* Sin, int nb, int nc, int nc0, int64_t rp,
                           hipStream_t stream);
+bool scan_stream_ok(int dtype, const void* phi, const void* psi, const void* vb, const float* Y,
+                    const float* out, const ScanArgs& a);
+int scan_stream_launch(int dtype, const void* phi, const void* psi, const void* vb,
+                       const float* Sg, const float* Y, const float* gate, float* out, int nb,
+                       int ng, const ScanArgs& a, hipStream_t stream);
 
 // Group size: enough workgroups to fill the GPU (one per CU at a time), and
 // no more than needed so the prepass stays small.
@@ -487,6 +483,8 @@ int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void
   a.o_st = o_st;
   a.g_sb = g_sb;
   a.write_H = write_H;
+  if (scan_stream_ok(dtype, phi, psi, vb, Y, out, a))
+    return scan_stream_launch(dtype, phi, psi, vb, Sg, Y, gate, out, nb, ng, a, stream);
   switch (dtype) {
     case SMAT_BF16:
       return launch_scan_fused<bf16>(phi, psi, vb, Sg, Y, gate, out, nb, ng, a, stream);

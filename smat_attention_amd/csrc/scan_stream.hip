@@ -1,0 +1,489 @@
+// The causal pass of the schedule for the common head shape -- 16-bit inputs,
+// r = 128 features, p = 129 value columns (head_dim 128 plus the ones column),
+// T and n multiples of 64 -- streamed through LDS.  Same contract as the
+// normalising mode of scan_fused_kernel (src/smat/attention.py:134-192 and
+// :446-453): segmented chunked scan with one reset at n, the long-range term
+// Y added to recent rows, division by the normaliser column, optional gate.
+//
+//   * One workgroup of eight waves walks one group of chunks; the group's
+//     incoming state comes from the same prepass (Gram sums per group, shifted
+//     exclusive scan over groups) as scan_fused_kernel.
+//   * Tokens advance 64 per step.  The Phi, Psi and Vb rows of the next step
+//     are copied HBM -> LDS by global_load_lds_dwordx4 while the current step
+//     computes: double-buffered, no registers and no VALU spent on staging.
+//   * Wave w owns value columns 16w .. 16w+15.  It keeps S[:, cols] (128 x 16,
+//     fp32) in MFMA accumulators and produces the transposed output
+//         O^T[cols][t] = S^T Phi^T + Vb^T A^T ,
+//     because (k-slot bijection) the accumulator tiles of S[a][c], split into
+//     hi + lo 16-bit parts, are exactly the A operand of S^T Phi^T -- S never
+//     goes through LDS -- and the O^T accumulator layout gives each lane four
+//     consecutive columns of one row: 16-byte output stores.
+//   * Columns 128..143 (the normaliser column and padding) are a ninth
+//     column tile whose state every wave keeps; waves 0..3 each produce the
+//     normaliser of one 16-row tile and share it through LDS.
+//   * The within-step scores A^T = Psi Phi^T (the causal 16 x 16 tiles of the
+//     64 x 64 block) are computed once, split over the waves, masked, rounded
+//     to the input dtype as the reference does, and shared through LDS.
+//   * Psi and Vb feed the MFMAs along the token axis through the gfx950
+//     transposing LDS read ds_read_b64_tr_b16: within each 16-lane group,
+//     lane i receives element (i & 3) of the 8 bytes addressed by lane
+//     4j + (i >> 2) as its element j.
+//
+// LDS layout.  Phi and Psi tiles are 64 rows of 256 bytes (sixteen 16-byte
+// chunks); chunk k of row t is stored at slot k ^ swz16(t), which spreads
+// both the sixteen rows of a row-wise fragment read and the four rows x 32
+// bytes of a transposing read over distinct bank groups.  Vb tiles are 64
+// rows of 288 bytes (18 chunks, columns 0..143), unswizzled: consecutive rows
+// are 32 bytes apart in bank space already.  The score share is 64 rows of
+// 128 bytes with chunk k of row t at k ^ swz8(t).
+#include <stdlib.h>
+
+#include <type_traits>
+
+#include "smat_host.hpp"
+
+namespace smat {
+
+namespace ss {
+constexpr int kThreads = 512;
+constexpr int kStep = 64;                      // tokens per step
+constexpr int kRowChunks = 16;                 // 16-byte chunks per Phi/Psi row
+constexpr int kVbChunks = 18;                  // per Vb row in LDS (144 columns)
+constexpr int kTileChunks = kStep * kRowChunks;    // 1024
+constexpr int kVbTileChunks = kStep * kVbChunks;   // 1152
+constexpr int kPhiLoads = kTileChunks / 64;        // wave-wide DMA loads per tile: 16
+constexpr int kVbLoads = kVbTileChunks / 64;       // 18
+constexpr int kLoads = 2 * kPhiLoads + kVbLoads;   // 50 per step, over eight waves
+}  // namespace ss
+
+#define SMAT_LDS __attribute__((address_space(3)))
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int swz16(int t) { return ((t & 7) << 1) | ((t >> 3) & 1); }
+__device__ __forceinline__ int swz8(int t) { return (t >> 1) & 7; }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// 8 bytes of a swizzled 256-byte row (t, chunk k, half h).
+template <typename In>
+__device__ __forceinline__ typename Traits<In>::half_frag row_half(const uint4* tile, int t, int k,
+                                                                    int h) {
+  const char* p = reinterpret_cast<const char*>(tile + t * ss::kRowChunks + (k ^ swz16(t))) + 8 * h;
+  return *reinterpret_cast<const typename Traits<In>::half_frag*>(p);
+}
+// 16 bytes (one chunk) of a swizzled 256-byte row.
+template <typename In>
+__device__ __forceinline__ typename Traits<In>::frag row_chunk(const uint4* tile, int t, int k) {
+  return *reinterpret_cast<const typename Traits<In>::frag*>(tile + t * ss::kRowChunks +
+                                                              (k ^ swz16(t)));
+}
+
+template <typename In>
+__device__ __forceinline__ typename Traits<In>::half_frag tr_read(const char* addr) {
+  short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (SMAT_LDS short4v*)(SMAT_LDS char*)(addr));
+  return __builtin_bit_cast(typename Traits<In>::half_frag, v);
+}
+
+template <typename In>
+__device__ __forceinline__ typename Traits<In>::frag join(typename Traits<In>::half_frag lo,
+                                                          typename Traits<In>::half_frag hi) {
+  typename Traits<In>::frag f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[j] = lo[j];
+    f[4 + j] = hi[j];
+  }
+  return f;
+}
+
+// A fragment of Psi^T (rows a = 16*at + lane%16, k-slots = tokens
+// 32*ks + 8*grp + j) from a swizzled Psi tile, by two transposing reads.
+template <typename In>
+__device__ __forceinline__ typename Traits<In>::frag psi_tr(const uint4* tile, int at, int ks,
+                                                            int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  typename Traits<In>::half_frag h2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = 32 * ks + 8 * g + 4 * h + (r16 >> 2);
+    const int k = 2 * at + ((r16 & 3) >> 1);
+    const char* p =
+        reinterpret_cast<const char*>(tile + row * ss::kRowChunks + (k ^ swz16(row))) +
+        8 * (r16 & 1);
+    h2[h] = tr_read<In>(p);
+  }
+  return join<In>(h2[0], h2[1]);
+}
+
+// Fragment of Vb along tokens (column 16*ct + lane%16, k-slots = tokens
+// 32*ks + 8*grp + j): the B operand of the state update and the A operand
+// (Vb^T) of the within-step product.
+template <typename In>
+__device__ __forceinline__ typename Traits<In>::frag vb_tr(const uint4* tile, int ct, int ks,
+                                                           int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  typename Traits<In>::half_frag h2[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = 32 * ks + 8 * g + 4 * h + (r16 >> 2);
+    const char* p = reinterpret_cast<const char*>(tile) + row * (ss::kVbChunks * 16) +
+                    (16 * ct + 4 * (r16 & 3)) * 2;
+    h2[h] = tr_read<In>(p);
+  }
+  return join<In>(h2[0], h2[1]);
+}
+
+// Issue the DMA of one step's Phi, Psi and Vb rows [ts, ts + 64) into one
+// buffer.  Load I of the 50 goes to wave I % 8: waves 0 and 1 issue seven,
+// the others six.  Each load moves 64 x 16 bytes to 1 KB of consecutive LDS;
+// which global chunk a lane fetches implements the swizzle.
+template <typename In>
+__device__ __forceinline__ void issue_step(uint4* dphi, uint4* dpsi, uint4* dvb, const In* phib,
+                                           const In* psib, const In* vbb, int64_t ts,
+                                           const ScanArgs& a, int w, int lane) {
+#pragma unroll
+  for (int u = 0; u < 7; ++u) {
+    const int I = w + 8 * u;
+    if (I < ss::kLoads) {
+      const In* src;
+      uint4* dst;
+      if (I < 2 * ss::kPhiLoads) {
+        const bool is_phi = I < ss::kPhiLoads;
+        const int li = is_phi ? I : I - ss::kPhiLoads;
+        const int row = 4 * li + (lane >> 4);
+        const int k = (lane & 15) ^ swz16(row);
+        src = (is_phi ? phib + (ts + row) * a.q_st : psib + (ts + row) * a.k_st) + 8 * k;
+        dst = (is_phi ? dphi : dpsi) + 64 * li;
+      } else {
+        const int li = I - 2 * ss::kPhiLoads;
+        const int L = 64 * li + lane;
+        const int row = L / ss::kVbChunks;
+        const int k = L - row * ss::kVbChunks;
+        // chunks past the row (columns >= row stride) carry no data the
+        // kernel keeps; read the row's first chunk instead of the next row
+        const int col = 8 * k + 8 <= a.v_st ? 8 * k : 0;
+        src = vbb + (ts + row) * a.v_st + col;
+        dst = dvb + 64 * li;
+      }
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                       (SMAT_LDS void*)(SMAT_LDS char*)(dst), 16, 0, 0);
+    }
+  }
+}
+
+struct YRegs {
+  float4 y[4];      // Y[t][16w + 4g .. +3] for the step's four row tiles
+  float y8[4];      // Y[t][p - 1]
+  float gv[4];      // gate
+};
+
+// Twelve loads, always issued (dummy in-bounds addresses when a term is
+// absent), so the compiler's waits on them count a fixed number of loads.
+__device__ __forceinline__ void issue_y(YRegs& R, const float* Yb, const float* gb,
+                                       const float* dummy, int64_t ts, const ScanArgs& a, int w,
+                                       int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  const bool rec = Yb != nullptr && ts >= a.n;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const float* yrow = rec ? Yb + (ts - a.n + 16 * tt + r16) * a.y_st : dummy;
+    R.y[tt] = *reinterpret_cast<const float4*>(rec ? yrow + 16 * w + 4 * g : dummy);
+    R.y8[tt] = rec ? yrow[a.p - 1] : 0.f;
+    R.gv[tt] = gb ? gb[ts + 16 * tt + r16] : 1.f;
+  }
+}
+
+__device__ __forceinline__ f32x4 mma16(f32x4 c, bf16x4 a, bf16x4 b) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a),
+                                                   __builtin_bit_cast(s4, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma16(f32x4 c, f16x4 a, f16x4 b) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+template <typename In>
+__global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
+    const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
+    const float* __restrict__ Sg, const float* __restrict__ Y, const float* __restrict__ gate,
+    float* __restrict__ out, ScanArgs a) {
+  using namespace ss;
+  typedef typename Traits<In>::frag Frag;
+  typedef typename Traits<In>::half_frag Half;
+  __shared__ __attribute__((aligned(16))) uint4 phi0[kTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 psi0[kTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 vb0[kVbTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 phi1[kTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 psi1[kTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 vb1[kVbTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 share[kStep * 8];
+  // normaliser partials: normp[t][w] = wave w's share of H[t][p-1]
+  __shared__ __attribute__((aligned(16))) float normp[kStep * 8];
+
+  const int grp = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  // The wave index in a scalar register: every condition on it below is a
+  // scalar branch.  (Under a vector condition the compiler masks EXEC around
+  // an MFMA without branching past it, and MFMAs execute regardless of EXEC.)
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int lane = lane_id();
+  const int r16 = lane & 15, g = lane >> 4;
+
+  int c0, c1;
+  if (grp < a.ng0) {
+    c0 = grp * a.K;
+    c1 = min(c0 + a.K, a.nc0);
+  } else {
+    c0 = a.nc0 + (grp - a.ng0) * a.K;
+    c1 = min(c0 + a.K, a.nc);
+  }
+  const int64_t tk0 = (int64_t)c0 * a.C;
+  const int64_t tk1 = min((int64_t)c1 * a.C, (int64_t)a.T);
+  const int nsteps = (int)((tk1 - tk0) / kStep);
+
+  const In* phib = phi + b * a.q_sb;
+  const In* psib = psi + b * a.k_sb;
+  const In* vbb = vb + b * a.v_sb;
+  const float* Yb = Y ? Y + b * a.y_sb : nullptr;
+  const float* gb = gate ? gate + b * a.g_sb : nullptr;
+  float* outb = out + b * a.o_sb;
+  const float* Sb = Sg + ((int64_t)b * gridDim.x + grp) * (int64_t)128 * a.p;
+
+  if (nsteps > 0) issue_step<In>(phi0, psi0, vb0, phib, psib, vbb, tk0, a, w, lane);
+
+  // incoming state: S[a][16w + lane%16] for all a, and the normaliser column
+  // block S[a][128 + lane%16] for this wave's rows a in [16w, 16w + 16)
+  const int cn = a.p - 1 - 128;            // normaliser's row in the ninth tile
+  f32x4 accS[8], accS8;
+#pragma unroll
+  for (int at = 0; at < 8; ++at)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) accS[at][i] = Sb[(int64_t)(16 * at + 4 * g + i) * a.p + 16 * w + r16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c8 = 128 + r16;
+    const float v8 = Sb[(int64_t)(16 * w + 4 * g + i) * a.p + (c8 < a.p ? c8 : 0)];
+    accS8[i] = c8 < a.p ? v8 : 0.f;
+  }
+  // Consume the state loads here, so that no wait for them (which would also
+  // wait for the step DMA issued after them) is placed inside the loop.
+#pragma unroll
+  for (int at = 0; at < 8; ++at) asm volatile("" : "+v"(accS[at]));
+  asm volatile("" : "+v"(accS8));
+
+  auto step = [&](auto BUFC, int s) {
+    constexpr int BUF = decltype(BUFC)::value;
+    const uint4* tphi = BUF ? phi1 : phi0;
+    const uint4* tpsi = BUF ? psi1 : psi0;
+    const uint4* tvb = BUF ? vb1 : vb0;
+    const int64_t ts = tk0 + (int64_t)s * kStep;
+    // An opaque copy of the lane index per step: the LDS addresses derived
+    // from it are recomputed inside the step instead of being hoisted out of
+    // the loop, where the ~60 distinct swizzled addresses would pin as many
+    // registers for the whole kernel.
+    int lane = lane_id();
+    asm volatile("" : "+v"(lane));
+    const int r16 = lane & 15, g = lane >> 4;
+    if (s + 1 < nsteps) {
+      issue_step<In>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib, vbb,
+                     ts + kStep, a, w, lane);
+      if (w < 2)
+        wait_vmcnt<7>();
+      else
+        wait_vmcnt<6>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();      // every wave's DMA of this step has landed
+    YRegs yr;
+    issue_y(yr, Yb, gb, Sb, ts, a, w, lane);
+
+    // (a) this wave's share of the causal score tiles A^T = Psi Phi^T
+    //     entries 0..9: (ut, tt) with ut <= tt; 10, 11: zero tiles (1,0), (3,2)
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) {
+      const int e = w + 8 * rep;
+      if (e < 12) {
+        int ut, tt;
+        if (e < 10) {
+          tt = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
+          ut = e - (tt * (tt + 1)) / 2;
+        } else {
+          ut = e == 10 ? 1 : 3;
+          tt = e == 10 ? 0 : 2;
+        }
+        f32x4 acc = zero4();
+        if (e < 10) {
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk)
+            acc = mma(acc, row_chunk<In>(tpsi, 16 * ut + r16, 4 * kk + g),
+                      row_chunk<In>(tphi, 16 * tt + r16, 4 * kk + g));
+        }
+        // acc[i] = A^T[t' = 16ut + 4g + i][t = 16tt + r16] = A[t][t']
+        Half hv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool keep = ut < tt || 4 * g + i <= r16;
+          hv[i] = from_f32<In>(keep ? acc[i] : 0.f);
+        }
+        const int t = 16 * tt + r16;
+        const int k = 2 * ut + (g >> 1);
+        char* p = reinterpret_cast<char*>(share + t * 8 + (k ^ swz8(t))) + 8 * (g & 1);
+        *reinterpret_cast<Half*>(p) = hv;
+      }
+    }
+
+    // (b) O^T = S^T Phi^T with the state before this step; the normaliser
+    //     column's share of this wave's 16 state rows
+    f32x4 accO[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) accO[tt] = zero4();
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      Frag shi, slo;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        In h0, l0, h1, l1;
+        split2<In>(accS[2 * kk][i], h0, l0);
+        split2<In>(accS[2 * kk + 1][i], h1, l1);
+        shi[i] = h0;
+        slo[i] = l0;
+        shi[4 + i] = h1;
+        slo[4 + i] = l1;
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int t = 16 * tt + r16;
+        const Frag bf = join<In>(row_half<In>(tphi, t, 4 * kk + (g >> 1), g & 1),
+                                 row_half<In>(tphi, t, 4 * kk + 2 + (g >> 1), g & 1));
+        accO[tt] = mma(accO[tt], shi, bf);
+        accO[tt] = mma(accO[tt], slo, bf);
+      }
+    }
+    float own = 0.f;                       // wave w < 4: its row tile's value, finished in (d)
+    {
+      Half s8hi, s8lo;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        In h0, l0;
+        split2<In>(accS8[i], h0, l0);
+        s8hi[i] = h0;
+        s8lo[i] = l0;
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int t = 16 * tt + r16;
+        const Half bf = row_half<In>(tphi, t, 2 * w + (g >> 1), g & 1);
+        f32x4 pn = mma16(zero4(), s8hi, bf);
+        pn = mma16(pn, s8lo, bf);
+        if (g == (cn >> 2)) {
+          if (tt == w)
+            own = pn[cn & 3];
+          else
+            normp[t * 8 + w] = pn[cn & 3];
+        }
+      }
+    }
+
+    // (c) S += Psi^T Vb over the step's 64 tokens
+    Frag vbw[2], vb8[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      vbw[ks] = vb_tr<In>(tvb, w, ks, lane);
+      vb8[ks] = vb_tr<In>(tvb, 8, ks, lane);
+#pragma unroll
+      for (int at = 0; at < 8; ++at) {
+        const Frag pa = psi_tr<In>(tpsi, at, ks, lane);
+        accS[at] = mma(accS[at], pa, vbw[ks]);
+        if (at == w) accS8 = mma(accS8, pa, vb8[ks]);
+      }
+    }
+    lds_barrier();       // the score share is complete
+
+    // (d) O^T += Vb^T A^T within the step; waves 0..3 add the row sums of A
+    //     (the ones column) to their row tile's normaliser
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int t = 16 * tt + r16;
+      f32x4 p8 = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (ks <= (tt >> 1)) {
+          const Frag bf = *reinterpret_cast<const Frag*>(share + t * 8 + ((4 * ks + g) ^ swz8(t)));
+          accO[tt] = mma(accO[tt], vbw[ks], bf);
+          if (tt == w) p8 = mma(p8, vb8[ks], bf);
+        }
+      }
+      if (tt == w && g == (cn >> 2)) normp[t * 8 + w] = own + p8[cn & 3];
+    }
+    lds_barrier();
+
+    // (e) long-range term, normalise, store four columns per lane per row tile
+    const bool rec = Yb != nullptr && ts >= a.n;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int t = 16 * tt + r16;
+      const float4 n0 = *reinterpret_cast<const float4*>(normp + t * 8);
+      const float4 n1 = *reinterpret_cast<const float4*>(normp + t * 8 + 4);
+      float den = ((n0.x + n0.y) + (n0.z + n0.w)) + ((n1.x + n1.y) + (n1.z + n1.w));
+      float4 o;
+      o.x = accO[tt][0];
+      o.y = accO[tt][1];
+      o.z = accO[tt][2];
+      o.w = accO[tt][3];
+      if (rec) {
+        den += yr.y8[tt];
+        o.x += yr.y[tt].x;
+        o.y += yr.y[tt].y;
+        o.z += yr.y[tt].z;
+        o.w += yr.y[tt].w;
+      }
+      const float inv = yr.gv[tt] / den;
+      o.x *= inv;
+      o.y *= inv;
+      o.z *= inv;
+      o.w *= inv;
+      *reinterpret_cast<float4*>(outb + (ts + t) * a.o_st + 16 * w + 4 * g) = o;
+    }
+  };
+
+  for (int s = 0; s < nsteps; s += 2) {
+    step(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+  }
+}
+
+// The shapes this kernel serves; everything else runs scan_fused_kernel.
+bool scan_stream_ok(int dtype, const void* phi, const void* psi, const void* vb, const float* Y,
+                    const float* out, const ScanArgs& a) {
+  if (dtype != SMAT_BF16 && dtype != SMAT_F16) return false;
+  if (a.write_H || a.r != 128 || a.p != 129) return false;
+  if (a.C % ss::kStep || a.T % ss::kStep || a.n % ss::kStep) return false;
+  if (!rows_vec_ok(phi, a.q_sb, a.q_st, 2) || !rows_vec_ok(psi, a.k_sb, a.k_st, 2) ||
+      !rows_vec_ok(vb, a.v_sb, a.v_st, 2) || a.v_st < 136)
+    return false;
+  if (!rows_vec_ok(out, a.o_sb, a.o_st, 4)) return false;
+  if (Y && !rows_vec_ok(Y, a.y_sb, a.y_st, 4)) return false;
+  const char* env = getenv("SMAT_SCAN");
+  if (env && env[0] == 'f') return false;        // SMAT_SCAN=fused: the general kernel
+  return true;
+}
+
+int scan_stream_launch(int dtype, const void* phi, const void* psi, const void* vb,
+                       const float* Sg, const float* Y, const float* gate, float* out, int nb,
+                       int ng, const ScanArgs& a, hipStream_t stream) {
+  dim3 grid((unsigned)ng, (unsigned)nb);
+  if (dtype == SMAT_BF16)
+    hipLaunchKernelGGL(scan_stream_kernel<bf16>, grid, dim3(ss::kThreads), 0, stream,
+                       (const bf16*)phi, (const bf16*)psi, (const bf16*)vb, Sg, Y, gate, out, a);
+  else
+    hipLaunchKernelGGL(scan_stream_kernel<f16>, grid, dim3(ss::kThreads), 0, stream,
+                       (const f16*)phi, (const f16*)psi, (const f16*)vb, Sg, Y, gate, out, a);
+  return launch_status("smat_causal_scan");
+}
+
+}  // namespace smat

@@ -45,6 +45,18 @@ inline bool rows_vec_ok(const void* p, int64_t sb, int64_t ld, int elem_bytes) {
 inline int elem_bytes(int dtype) { return dtype == SMAT_F32 ? 4 : 2; }
 
 // Upper bounds of the MFMA tilings.
+// Arguments of the causal-pass kernels (scan_fused.hip, scan_stream.hip): chunks
+// of C tokens grouped K at a time inside each segment; ng0 groups cover the
+// first segment [0, n).
+struct ScanArgs {
+  int T, n, C, K, nc, nc0, ng0, r, p;
+  int64_t q_sb, q_st, k_sb, k_st, v_sb, v_st;
+  int64_t y_sb, y_st;   // Y rows are recent rows t - n
+  int64_t o_sb, o_st;
+  int64_t g_sb;
+  int write_H;          // 1: out is H (nb, T, p) unnormalised, no Y / gate
+};
+
 constexpr int kMaxR = 128;
 constexpr int kMaxP = 144;
 constexpr int kMaxC = 256;

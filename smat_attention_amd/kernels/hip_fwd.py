@@ -257,7 +257,11 @@ def segment_scan(D, nc0: int):
 
 
 def query(Phi_rec, U):
-    """``Y[i] = Phi_rec[i] U_{i mod B}``: fp32 ``(nb, T_R, p)``."""
+    """``Y[i] = Phi_rec[i] U_{i mod B}``: fp32 ``(nb, T_R, p)``.
+
+    The result is a view whose rows are padded to a multiple of 4 floats, so
+    the causal pass can read it with 16-byte loads.
+    """
     who = "query"
     _on_gpu(who, Phi_rec, U)
     nb, T_R, R = Phi_rec.shape
@@ -265,7 +269,7 @@ def query(Phi_rec, U):
     code = _code(Phi_rec, who)
     q, q_sb, q_st = _rows3(Phi_rec)
     Uc = U.contiguous().float()
-    Y = torch.empty(nb, T_R, P, device=U.device, dtype=torch.float32)
+    Y = torch.empty(nb, T_R, (P + 3) // 4 * 4, device=U.device, dtype=torch.float32)[..., :P]
     call("smat_query", code, q.data_ptr(), Uc.data_ptr(), Y.data_ptr(), nb, T_R, B, R, P,
          q_sb, q_st, Y.stride(0), Y.stride(1), stream_of(Uc))
     return Y
