@@ -28,48 +28,6 @@ constexpr int kNCT = kCols / 16;
 }  // namespace gr
 
 // How item i of batch b maps to a token progression.
-struct GramItems {
-  int mode;        // 0: chunk groups, 1: profiles (+ optional global channel)
-  // mode 0: chunks of width C over T tokens; segment 0 has nc0 chunks; a group
-  // is K consecutive chunks inside one segment.
-  int T, C, K, nc0, nc, ng0;
-  // mode 1: profiles x < N0 over [n_P, n); item N0 is the global channel.
-  int n_P, n, N0;
-  // split-K: each progression is cut into nsplit runs of `per` terms (a
-  // multiple of the 32-token block); run s writes partial s, and a second
-  // kernel sums the partials in run order, so the result is deterministic.
-  int nsplit, per;
-};
-
-__device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& start,
-                                          int64_t& stride, int& count) {
-  if (it.mode == 0) {
-    int c0, c1;
-    if (i < it.ng0) {
-      c0 = i * it.K;
-      c1 = min(c0 + it.K, it.nc0);
-    } else {
-      c0 = it.nc0 + (i - it.ng0) * it.K;
-      c1 = min(c0 + it.K, it.nc);
-    }
-    start = (int64_t)c0 * it.C;
-    stride = 1;
-    const int64_t end = min((int64_t)c1 * it.C, (int64_t)it.T);
-    count = (int)max((int64_t)0, end - start);
-  } else {
-    if (i < it.N0) {
-      const int nX = it.n - it.n_P;
-      start = it.n_P + i;
-      stride = it.N0;
-      count = (i < nX) ? (nX - i + it.N0 - 1) / it.N0 : 0;
-    } else {
-      start = 0;
-      stride = 1;
-      count = it.n_P;
-    }
-  }
-}
-
 template <typename In, bool VEC>
 __global__ __launch_bounds__(gr::kThreads) void gram_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, float* __restrict__ G,
@@ -254,11 +212,22 @@ static int64_t plan_split(GramItems& it, int nitems, int nb, int max_count, int 
   return nsplit > 1 ? (int64_t)nb * nitems * nsplit * r * p * 4 : 0;
 }
 
+bool gram_stream_ok(int dtype, const void* psi, const void* vb, int r, int p, int64_t k_sb,
+                    int64_t k_st, int64_t v_sb, int64_t v_st, const GramItems& it, int nitems,
+                    int nb);
+int gram_stream_launch(int dtype, const void* psi, const void* vb, float* G, float* G_last,
+                       const GramItems& it, int nitems, int nb, int p, int64_t k_sb,
+                       int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                       int64_t gl_sb, hipStream_t stream, const char* who);
+
 int gram_dispatch(int dtype, const void* psi, const void* vb, float* G, float* G_last,
                   const GramItems& it, int nitems, int nb, int r, int p, int64_t k_sb,
                   int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
                   int64_t gl_sb, float* partials, hipStream_t stream, const char* who) {
   if (nitems == 0 || nb == 0) return SMAT_OK;
+  if (gram_stream_ok(dtype, psi, vb, r, p, k_sb, k_st, v_sb, v_st, it, nitems, nb))
+    return gram_stream_launch(dtype, psi, vb, G, G_last, it, nitems, nb, p, k_sb, k_st, v_sb, v_st,
+                              g_sb, g_si, gl_sb, stream, who);
   if (it.nsplit > 1 && partials == nullptr) {
     set_error("%s: split-K needs a workspace", who);
     return SMAT_EINVAL;

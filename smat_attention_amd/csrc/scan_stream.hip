@@ -457,6 +457,168 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Gram sums G = sum_t Psi_t^T Vb_t over a token progression (the chunk-group
+// prepass of the causal pass, and the profile pool), same machinery: rows
+// of 64 tokens at a time copied HBM -> LDS by DMA (double-buffered), read
+// along tokens by transposing LDS reads, wave w accumulating G[:, 16w ..
+// 16w+15] and rows [16w, 16w+16) of the ninth column tile.  Rows past the end
+// of a progression are fetched from its first token (in bounds) and zeroed in
+// the Vb fragment, so they add nothing.
+// ---------------------------------------------------------------------------
+
+// Issue one step's DMA: Psi (16 loads) and Vb (18) for rows
+// tok(row) = start + stride * (base + row), row < 64; waves 0, 1 issue five
+// loads, the others four.
+template <typename In>
+__device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* psib,
+                                           const In* vbb, int64_t start, int64_t stride,
+                                           int base, int count, int64_t k_st, int64_t v_st,
+                                           int w, int lane) {
+  constexpr int kL = ss::kPhiLoads + ss::kVbLoads;     // 34
+#pragma unroll
+  for (int u = 0; u < 5; ++u) {
+    const int I = w + 8 * u;
+    if (I < kL) {
+      const In* src;
+      uint4* dst;
+      if (I < ss::kPhiLoads) {
+        const int row = 4 * I + (lane >> 4);
+        const int k = (lane & 15) ^ swz16(row);
+        const int64_t tok = start + (base + row < count ? stride * (base + row) : 0);
+        src = psib + tok * k_st + 8 * k;
+        dst = dpsi + 64 * I;
+      } else {
+        const int li = I - ss::kPhiLoads;
+        const int L = 64 * li + lane;
+        const int row = L / ss::kVbChunks;
+        const int k = L - row * ss::kVbChunks;
+        const int col = 8 * k + 8 <= v_st ? 8 * k : 0;
+        const int64_t tok = start + (base + row < count ? stride * (base + row) : 0);
+        src = vbb + tok * v_st + col;
+        dst = dvb + 64 * li;
+      }
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+                                       (SMAT_LDS void*)(SMAT_LDS char*)(dst), 16, 0, 0);
+    }
+  }
+}
+
+template <typename In>
+__global__ __launch_bounds__(ss::kThreads, 2) void gram_stream_kernel(
+    const In* __restrict__ psi, const In* __restrict__ vb, float* __restrict__ G,
+    float* __restrict__ G_last, GramItems it, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
+    int64_t v_st, int64_t g_sb, int64_t g_si, int64_t gl_sb) {
+  using namespace ss;
+  typedef typename Traits<In>::frag Frag;
+  __shared__ __attribute__((aligned(16))) uint4 psi0[kTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 vb0[kVbTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 psi1[kTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 vb1[kVbTileChunks];
+
+  const int item = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  int64_t start, stride;
+  int count;
+  gram_item(it, item, start, stride, count);
+  const In* psib = psi + b * k_sb;
+  const In* vbb = vb + b * v_sb;
+  float* Gout = (it.mode == 1 && item == it.N0) ? G_last + b * gl_sb : G + b * g_sb + item * g_si;
+  const int nsteps = (count + kStep - 1) / kStep;
+
+  f32x4 accS[8], accS8 = zero4();
+#pragma unroll
+  for (int at = 0; at < 8; ++at) accS[at] = zero4();
+  if (nsteps > 0)
+    issue_gram<In>(psi0, vb0, psib, vbb, start, stride, 0, count, k_st, v_st, w, lane_id());
+
+  auto step = [&](auto BUFC, int s) {
+    constexpr int BUF = decltype(BUFC)::value;
+    const uint4* tpsi = BUF ? psi1 : psi0;
+    const uint4* tvb = BUF ? vb1 : vb0;
+    int lane = lane_id();
+    asm volatile("" : "+v"(lane));
+    const int g = lane >> 4;
+    if (s + 1 < nsteps) {
+      issue_gram<In>(BUF ? psi0 : psi1, BUF ? vb0 : vb1, psib, vbb, start, stride,
+                     (s + 1) * kStep, count, k_st, v_st, w, lane);
+      if (w < 2)
+        wait_vmcnt<5>();
+      else
+        wait_vmcnt<4>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();
+    const int nvalid = count - s * kStep;        // rows of this step holding tokens
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      Frag vbw = vb_tr<In>(tvb, w, ks, lane);
+      Frag vb8 = vb_tr<In>(tvb, 8, ks, lane);
+      if (nvalid < kStep) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const bool ok = 32 * ks + 8 * g + e < nvalid;
+          vbw[e] = ok ? vbw[e] : from_f32<In>(0.f);
+          vb8[e] = ok ? vb8[e] : from_f32<In>(0.f);
+        }
+      }
+#pragma unroll
+      for (int at = 0; at < 8; ++at) {
+        const Frag pa = psi_tr<In>(tpsi, at, ks, lane);
+        accS[at] = mma(accS[at], pa, vbw);
+        if (at == w) accS8 = mma(accS8, pa, vb8);
+      }
+    }
+    lds_barrier();     // this buffer is free for the DMA issued next step
+  };
+  for (int s = 0; s < nsteps; s += 2) {
+    step(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+  }
+
+  const int lane = lane_id();
+  const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int at = 0; at < 8; ++at)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Gout[(int64_t)(16 * at + 4 * g + i) * p + 16 * w + r16] = accS[at][i];
+  if (128 + r16 < p) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Gout[(int64_t)(16 * w + 4 * g + i) * p + 128 + r16] = accS8[i];
+  }
+}
+
+bool gram_stream_ok(int dtype, const void* psi, const void* vb, int r, int p, int64_t k_sb,
+                    int64_t k_st, int64_t v_sb, int64_t v_st, const GramItems& it, int nitems,
+                    int nb) {
+  if (dtype != SMAT_BF16 && dtype != SMAT_F16) return false;
+  if (r != 128 || p != 129 || it.nsplit > 1) return false;
+  if ((int64_t)nitems * nb < 256) return false;        // few, long items: the split-K kernel
+  if (!rows_vec_ok(psi, k_sb, k_st, 2) || !rows_vec_ok(vb, v_sb, v_st, 2) || v_st < 136)
+    return false;
+  const char* env = getenv("SMAT_GRAM");
+  if (env && env[0] == 'o') return false;              // SMAT_GRAM=old: the general kernel
+  return true;
+}
+
+int gram_stream_launch(int dtype, const void* psi, const void* vb, float* G, float* G_last,
+                       const GramItems& it, int nitems, int nb, int p, int64_t k_sb,
+                       int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                       int64_t gl_sb, hipStream_t stream, const char* who) {
+  dim3 grid((unsigned)nitems, (unsigned)nb);
+  if (dtype == SMAT_BF16)
+    hipLaunchKernelGGL(gram_stream_kernel<bf16>, grid, dim3(ss::kThreads), 0, stream,
+                       (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
+                       v_st, g_sb, g_si, gl_sb);
+  else
+    hipLaunchKernelGGL(gram_stream_kernel<f16>, grid, dim3(ss::kThreads), 0, stream,
+                       (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
+                       v_st, g_sb, g_si, gl_sb);
+  return launch_status(who);
+}
+
 // The shapes this kernel serves; everything else runs scan_fused_kernel.
 bool scan_stream_ok(int dtype, const void* phi, const void* psi, const void* vb, const float* Y,
                     const float* out, const ScanArgs& a) {

@@ -57,6 +57,49 @@ struct ScanArgs {
   int write_H;          // 1: out is H (nb, T, p) unnormalised, no Y / gate
 };
 
+// Token progressions summed by the Gram kernels (gram.hip, scan_stream.hip).
+struct GramItems {
+  int mode;        // 0: chunk groups, 1: profiles (+ optional global channel)
+  // mode 0: chunks of width C over T tokens; segment 0 has nc0 chunks; a group
+  // is K consecutive chunks inside one segment.
+  int T, C, K, nc0, nc, ng0;
+  // mode 1: profiles x < N0 over [n_P, n); item N0 is the global channel.
+  int n_P, n, N0;
+  // split-K: each progression is cut into nsplit runs of `per` terms (a
+  // multiple of the 32-token block); run s writes partial s, and a second
+  // kernel sums the partials in run order, so the result is deterministic.
+  int nsplit, per;
+};
+
+__device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& start,
+                                          int64_t& stride, int& count) {
+  if (it.mode == 0) {
+    int c0, c1;
+    if (i < it.ng0) {
+      c0 = i * it.K;
+      c1 = min(c0 + it.K, it.nc0);
+    } else {
+      c0 = it.nc0 + (i - it.ng0) * it.K;
+      c1 = min(c0 + it.K, it.nc);
+    }
+    start = (int64_t)c0 * it.C;
+    stride = 1;
+    const int64_t end = min((int64_t)c1 * it.C, (int64_t)it.T);
+    count = (int)max((int64_t)0, end - start);
+  } else {
+    if (i < it.N0) {
+      const int nX = it.n - it.n_P;
+      start = it.n_P + i;
+      stride = it.N0;
+      count = (i < nX) ? (nX - i + it.N0 - 1) / it.N0 : 0;
+    } else {
+      start = 0;
+      stride = 1;
+      count = it.n_P;
+    }
+  }
+}
+
 constexpr int kMaxR = 128;
 constexpr int kMaxP = 144;
 constexpr int kMaxC = 256;

@@ -159,6 +159,31 @@ def test_query(dt, T, d, r, p):
     assert _rel(Y, ref) < (1e-5 if dt == torch.float32 else 2e-5)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,d,n_P", [(4096, 3, 0), (8192, 2, 0), (2048, 3, 16), (32768, 3, 0)])
+def test_pool_streaming_head_dim_128(dt, T, d, n_P, monkeypatch):
+    """The DMA-streamed Gram kernel (16-bit, r = 128, p = 129) on the profile
+    pool, incl. the global channel, against fp64 and the general kernel."""
+    _say("pool streaming", dt, T, d, n_P)
+    spec = build_mask(T, d, chunk=128, n_P=n_P)
+    nb = 4
+    Phi, Psi, Vb = _feats(nb, T, 128, dt, seed=31)
+    Vp = torch.zeros(nb, T, 136, dtype=dt)
+    Vp[..., :129] = Vb
+    Sd, Vd = Psi.to(DEV), Vp.to(DEV)[..., :129]
+    Fg = torch.empty(nb, 128, 129, device=DEV) if n_P else None
+    F = K.pool(Sd, Vd, spec.n_P, spec.n, spec.N0, F_glob=Fg)
+    monkeypatch.setenv("SMAT_GRAM", "old")
+    Fg_old = torch.empty(nb, 128, 129, device=DEV) if n_P else None
+    F_old = K.pool(Sd, Vd, spec.n_P, spec.n, spec.N0, F_glob=Fg_old)
+    monkeypatch.delenv("SMAT_GRAM")
+    ref = O.pool_profiles(Psi.double(), Vb.double(), spec)
+    assert _rel(F, ref) < 1e-5 and _rel(F_old, ref) < 1e-5
+    if n_P:
+        gref = Psi[:, :n_P].double().transpose(-1, -2) @ Vb[:, :n_P].double()
+        assert _rel(Fg, gref) < 1e-5
+
+
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 def test_chunk_states_and_segment_scan(dt):
     _say("chunk_states + segment_scan", dt)
