@@ -9,6 +9,11 @@
 // gathered straight into A fragments (8 consecutive features per lane).  U is
 // fp32; for 16-bit inputs each U fragment is split into hi + lo 16-bit parts
 // (two MFMAs, ~16 mantissa bits), for fp32 inputs it goes to fp32 MFMA whole.
+#include <stdlib.h>
+
+#include <algorithm>
+#include <type_traits>
+
 #include "smat_host.hpp"
 
 namespace smat {
@@ -117,6 +122,169 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Head-dim-128 variant (16-bit inputs, r = 128, p = 129): persistent
+// workgroups of nine waves walk the (sequence, row type) items.  Each item's
+// U_h (66 KB fp32) and its <= 48 Phi rows (12 KB) are copied HBM -> LDS with
+// global_load_lds_dwordx4, double-buffered: the next item streams in while
+// the current one is multiplied.  The product is taken transposed,
+// Y^T = U_h^T Phi^T: wave w owns column tile w, its A operand is U_h^T read
+// from LDS and split hi/lo, its B operand the Phi rows (row chunks swizzled by
+// row so sixteen rows read without bank conflicts), and each lane ends with
+// four consecutive columns of one row -- 16-byte stores into Y rows padded to
+// 4 floats.
+// ---------------------------------------------------------------------------
+
+namespace qs {
+constexpr int kWaves = 9;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kR = 128, kP = 129;
+constexpr int kUChunks = kR * kP / 4;                     // 16-byte chunks of U_h: 4128
+constexpr int kULoads = (kUChunks + 63) / 64;             // wave-wide DMA loads: 65
+constexpr int kMT = 3;                                    // row tiles: <= 48 rows per type
+constexpr int kPhiLoads = 16 * kMT * 16 / 64;             // 48 rows x 16 chunks: 12
+constexpr int kLoads = kULoads + kPhiLoads;               // 77 per item
+constexpr int kUFloats = kULoads * 256;                   // 16640 (LDS image incl. tail)
+}  // namespace qs
+
+template <typename In>
+__device__ __forceinline__ void query_issue(float* ubuf, uint4* pbuf, const float* U,
+                                            const In* phi, int64_t item, int T_R, int B,
+                                            int64_t q_sb, int64_t q_st, int w, int lane) {
+  using namespace qs;
+  const int64_t b = item / B;
+  const int h = (int)(item - b * B);
+  const int cnt = (T_R - h + B - 1) / B;
+  const float* Uh = U + item * (int64_t)(kR * kP);
+  const In* phib = phi + b * q_sb;
+#pragma unroll
+  for (int u = 0; u < (kLoads + kWaves - 1) / kWaves; ++u) {
+    const int I = w + kWaves * u;
+    if (I < kLoads) {
+      const void* src;
+      void* dst;
+      if (I < kULoads) {
+        const int c = 64 * I + lane;
+        src = Uh + 4 * (c < kUChunks ? c : 0);
+        dst = ubuf + 256 * I;
+      } else {
+        const int li = I - kULoads;
+        const int row = 4 * li + (lane >> 4);
+        const int k = (lane & 15) ^ (row & 15);
+        const int rr = row < cnt ? row : 0;
+        src = phib + ((int64_t)h + (int64_t)rr * B) * q_st + 8 * k;
+        dst = pbuf + 64 * li;
+      }
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(
+                                                __attribute__((address_space(3))) char*)(dst),
+                                       16, 0, 0);
+    }
+  }
+}
+
+template <typename In>
+__global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
+    const In* __restrict__ phi, const float* __restrict__ U, float* __restrict__ Y, int T_R,
+    int B, int64_t nitems, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st) {
+  using namespace qs;
+  typedef typename Traits<In>::frag Frag;
+  __shared__ __attribute__((aligned(16))) float u0[kUFloats];
+  __shared__ __attribute__((aligned(16))) float u1[kUFloats];
+  __shared__ __attribute__((aligned(16))) uint4 p0[kPhiLoads * 64];
+  __shared__ __attribute__((aligned(16))) uint4 p1[kPhiLoads * 64];
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int64_t G = gridDim.x;
+  int64_t item = blockIdx.x;
+  if (item < nitems) query_issue<In>(u0, p0, U, phi, item, T_R, B, q_sb, q_st, w, lane_id());
+
+  auto step = [&](auto BUFC) {
+    constexpr int BUF = decltype(BUFC)::value;
+    const float* us = BUF ? u1 : u0;
+    const uint4* ps = BUF ? p1 : p0;
+    int lane = lane_id();
+    asm volatile("" : "+v"(lane));
+    const int r16 = lane & 15, g = lane >> 4;
+    const int64_t next = item + G;
+    if (next < nitems) {
+      query_issue<In>(BUF ? u0 : u1, BUF ? p0 : p1, U, phi, next, T_R, B, q_sb, q_st, w, lane);
+      if (w < kLoads % kWaves)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads / kWaves + 1) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads / kWaves) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    lds_barrier();
+
+    const int64_t b = item / B;
+    const int h = (int)(item - b * B);
+    const int cnt = (T_R - h + B - 1) / B;
+    const int c = 16 * w + r16;
+    f32x4 acc[kMT];
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) acc[t] = zero4();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      Frag ah, al;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float uv = c < kP ? us[(32 * kb + 8 * g + e) * kP + c] : 0.f;
+        In hh, ll;
+        split2<In>(uv, hh, ll);
+        ah[e] = hh;
+        al[e] = ll;
+      }
+#pragma unroll
+      for (int t = 0; t < kMT; ++t) {
+        const int row = 16 * t + r16;
+        const Frag pb = *reinterpret_cast<const Frag*>(ps + row * 16 + ((4 * kb + g) ^ (row & 15)));
+        acc[t] = mma(acc[t], ah, pb);
+        acc[t] = mma(acc[t], al, pb);
+      }
+    }
+    float* Yb = Y + b * y_sb;
+    const int c0 = 16 * w + 4 * g;
+#pragma unroll
+    for (int t = 0; t < kMT; ++t) {
+      const int k = 16 * t + r16;
+      if (k < cnt) {
+        float* yrow = Yb + ((int64_t)h + (int64_t)k * B) * y_st;
+        if (c0 + 3 < kP) {
+          *reinterpret_cast<float4*>(yrow + c0) = make_float4(acc[t][0], acc[t][1], acc[t][2],
+                                                              acc[t][3]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (c0 + i < kP) yrow[c0 + i] = acc[t][i];
+        }
+      }
+    }
+    lds_barrier();     // this buffer is free for the DMA issued next step
+    item = next;
+  };
+  while (item < nitems) {
+    step(std::integral_constant<int, 0>{});
+    if (item < nitems) step(std::integral_constant<int, 1>{});
+  }
+}
+
+template <typename In>
+static int launch_query(const void* phi, const float* U, float* Y, int nb, int T_R, int B, int r,
+                        int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
+                        hipStream_t stream);
+
+static bool query_stream_ok(int dtype, const void* phi, const float* U, const float* Y, int T_R,
+                            int B, int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                            int64_t y_st) {
+  if (dtype != SMAT_BF16 && dtype != SMAT_F16) return false;
+  if (r != qs::kR || p != qs::kP) return false;
+  if ((T_R + B - 1) / B > 16 * qs::kMT) return false;        // <= 48 rows per type
+  if (!rows_vec_ok(phi, q_sb, q_st, 2) || !aligned16(U) || !rows_vec_ok(Y, y_sb, y_st, 4))
+    return false;
+  const char* env = getenv("SMAT_QUERY");
+  return !(env && env[0] == 'o');                             // SMAT_QUERY=old
+}
+
 template <typename In>
 static int launch_query(const void* phi, const float* U, float* Y, int nb, int T_R, int B, int r,
                         int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
@@ -138,6 +306,20 @@ int query_dispatch(int dtype, const void* phi, const float* U, float* Y, int nb,
                    int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
                    hipStream_t stream) {
   if (nb == 0 || T_R == 0 || B == 0) return SMAT_OK;
+  if (query_stream_ok(dtype, phi, U, Y, T_R, B, r, p, q_sb, q_st, y_sb, y_st)) {
+    int dev = 0, ncu = 256;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    const int64_t nitems = (int64_t)nb * B;
+    const unsigned grid = (unsigned)std::min<int64_t>(nitems, (int64_t)ncu);
+    if (dtype == SMAT_BF16)
+      hipLaunchKernelGGL(query_stream_kernel<bf16>, dim3(grid), dim3(qs::kThreads), 0, stream,
+                         (const bf16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st);
+    else
+      hipLaunchKernelGGL(query_stream_kernel<f16>, dim3(grid), dim3(qs::kThreads), 0, stream,
+                         (const f16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st);
+    return launch_status("smat_query");
+  }
   switch (dtype) {
     case SMAT_BF16:
       return launch_query<bf16>(phi, U, Y, nb, T_R, B, r, p, q_sb, q_st, y_sb, y_st, stream);
