@@ -21,6 +21,9 @@
 // Both sum a hyperplane's points in the order of the table they are given.
 #include <stdlib.h>
 
+#include <algorithm>
+#include <type_traits>
+
 #include "smat_host.hpp"
 
 namespace smat {
@@ -207,18 +210,21 @@ __global__ __launch_bounds__(1024, MINB) void incidence_plane_kernel(
 
   float* Ub = U + b * (int64_t)B * rp + e0;
   const float* Fgb = Fg ? Fg + b * rp + e0 : nullptr;
-  const int gpd = (q + 15) >> 4;                 // 16-lane groups per direction
-  const int ngroups = gpd * (q + 1);
-  const int j = threadIdx.x & 15;
-  for (int G = threadIdx.x >> 4; G < ngroups; G += kT / 16) {
-    const int e = G / gpd;
-    const int b0 = (G - e * gpd) * 16;
-    const int bl = b0 + j;
-    const int bb = bl < q ? bl : q - 1;          // idle lanes shadow the last line
-    const int m = e == 0 ? 0 : e - 1;
-    const int stride = e == 0 ? 1 : W;
-    int pt = e == 0 ? W * bb + j : j;            // entry of step t, less s
-    int s = e == 0 ? 0 : b0;
+  // Lane L owns line (e, b) = divmod(L, q): no idle lanes.  Within a run of
+  // consecutive b of one direction the entries read at a step are consecutive
+  // (mod q); a run that wraps, or a sixteen-lane group that straddles two
+  // directions, costs a two-way bank conflict at worst.
+  const int nlines_all = q * (q + 1);
+  for (int L = threadIdx.x; L < nlines_all; L += kT) {
+    const int e = L / q;
+    const int bl = L - e * q;
+    // e >= 1: entry W*t + (b - m t mod q).  e = 0 (the column x1 = b): entry
+    // W*b + (b + t mod q), i.e. m = q - 1 = -1 mod q and no column stride,
+    // so neighbouring lanes are W + 1 entries apart (odd): distinct banks.
+    const int m = e == 0 ? q - 1 : e - 1;
+    const int stride = e == 0 ? 0 : W;
+    int pt = e == 0 ? W * bl : 0;                // entry of step t, less s
+    int s = bl;
     float4 acc[Q];
 #pragma unroll
     for (int k = 0; k < Q; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(1024, MINB) void incidence_plane_kernel(
 #pragma unroll
       for (int k = 0; k < Q; ++k) add4(acc[k], row[k * PLANE]);
     }
-    if (bl < q) {
+    {
       const int h = line_type[e * q + bl];
       if (h >= 0) {
 #pragma unroll
