@@ -229,6 +229,42 @@ int smat_decode_step(int dtype, const void* phi_t, const void* psi_t, const void
                      float* o_full, int nb, int B, int r, int p, int64_t step,
                      int64_t q_sb, int64_t k_sb, int64_t v_sb, void* stream);
 
+/*
+ * Unpooled long-range sums  U_h = sum_{j in cols_h} Psi_{n_P+j}^T Vb_{n_P+j}
+ * (fp32, U: (nb, B, r, p) contiguous), one row type per list: cols (B, kappa)
+ * int32 landmark columns, row h holding its counts[h] columns first.
+ * Replaces direct_long_range, src/smat/attention.py:333-362 (the reference
+ * pads each list with n_X; this table is the same lists, compacted).
+ */
+int smat_direct(int dtype, const void* psi, const void* vb, const int32_t* cols,
+                const int32_t* counts, int kappa, float* U, int nb, int B, int n_P,
+                int r, int p, int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
+                void* stream);
+
+/*
+ * Subset-sum (zeta) transform over N = 2^k profiles:
+ *   Z_a = sum_{x subset of a} F_x,   F, Z: (nb, N, rp) fp32, Z may equal F.
+ * Replaces zeta_transform, src/smat/attention.py:369-384.
+ */
+int smat_zeta(const float* F, float* Z, int nb, int N, int64_t rp, void* stream);
+
+/*
+ * Walsh incidence of the endpoint mask, C[h, a] = 1{popcount(h & a) even}:
+ *   U = (sum_x F_x + H F) / 2, H the N x N Walsh matrix, N = 2^k;
+ * F, U: (nb, N, rp) fp32, U may equal F.  Replaces walsh_incidence,
+ * src/smat/attention.py:288-307.
+ */
+int smat_walsh(const float* F, float* U, int nb, int N, int64_t rp, void* stream);
+
+/*
+ * U_h <- U_h - sum_x F_x for every row type h (in place; F: (nb, N0, rp),
+ * U: (nb, B, rp) fp32).  The negated complement Ubar = F_tot - U of the
+ * subtractive schedule, src/smat/attention.py:458-482: querying the result
+ * gives -Y_ex, which the normalisation adds.
+ */
+int smat_incidence_complement(const float* F, float* U, int nb, int N0, int B, int64_t rp,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

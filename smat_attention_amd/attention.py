@@ -40,12 +40,15 @@ from .mask import MaskSpec
 __all__ = [
     "make_phi", "featurise", "to_device",
     "segmented_causal_scan", "pool_profiles", "apply_incidence",
-    "query_by_type", "zeta_transform", "walsh_incidence",
+    "query_by_type", "zeta_transform", "walsh_incidence", "direct_long_range",
     "smat_attention", "dense_masked_kernel_attention", "SmatDecoder",
     "have_triton", "have_hip",
 ]
 
 _KERNEL_BACKENDS = ("auto", "hip", "triton")
+# apply_incidence realisations (attention.py:239-285): "torch" is the gather
+# (here the gather-reduce kernel), "walsh" the endpoint butterfly
+_INCIDENCE_BACKENDS = _KERNEL_BACKENDS + ("torch", "walsh")
 
 
 def have_hip() -> bool:
@@ -151,7 +154,14 @@ def to_device(spec: MaskSpec, device, *, want_direct: bool = False) -> MaskSpec:
         if not spec.uniform_deg:
             raise ValueError("the direct backend needs a uniform row degree; "
                              "the endpoint mask is ragged")
-        spec.type_cols_t = torch.from_numpy(_type_columns(spec)).to(device)
+        cols = _type_columns(spec)
+        spec.type_cols_t = torch.from_numpy(cols).to(device)
+        # the same lists with the n_X padding moved to the end of each row
+        valid = cols < spec.n_X
+        order = np.argsort(~valid, axis=1, kind="stable")
+        spec.type_cols_c_t = torch.from_numpy(
+            np.take_along_axis(cols, order, axis=1).astype(np.int32)).to(device)
+        spec.type_counts_t = torch.from_numpy(valid.sum(1).astype(np.int32)).to(device)
     spec._smat_device = torch.device(device)
     return spec
 
@@ -278,19 +288,23 @@ def pool_profiles(Psi, Vb, spec: MaskSpec, acc_dtype=None, backend: str = "auto"
 
 
 def apply_incidence(F, spec: MaskSpec, *, backend: str = "auto", gather_chunk: int = 0):
-    """``U_h = sum_{x in H_h} F_x``: fp32 ``(nb, B, r, p)``.
+    """``U_h = sum_{x in H_h} F_x``: fp32 ``(nb, B, r, p)`` (attention.py:239-285).
 
-    Uniform-degree masks use the ``(B, deg)`` table, ragged ones (the endpoint
-    mask) the CSR rows; both through the same gather-reduce kernel.
+    As in the reference, the endpoint mask takes the Walsh butterfly under
+    ``"auto"``/``"walsh"``; every other case is the gather-reduce kernel
+    (``"triton"`` requires a uniform degree, as the reference's kernel does).
     ``gather_chunk`` tuned the reference's torch gather and is ignored.
     """
     who = "apply_incidence"
-    if backend == "walsh":
-        raise ValueError(f"{who}: the Walsh butterfly is not part of this build; the "
-                         f"gather-reduce kernel applies C for every mask kind")
-    _backend(backend, who)
+    if backend not in _INCIDENCE_BACKENDS:
+        raise ValueError(f"{who}: unknown backend {backend!r}")
     if not F.is_cuda:
         raise ValueError(f"{who}: F must be on the GPU")
+    if spec.kind == "endpoint" and backend in ("auto", "walsh"):
+        return walsh_incidence(F)
+    if backend == "triton" and not spec.uniform_deg:
+        raise ValueError("the triton incidence kernel needs a uniform row degree; this mask "
+                         "is ragged (use walsh or torch)")
     _staged(spec, F.device)
     return _incidence(F, spec, None)
 
@@ -326,19 +340,33 @@ def query_by_type(Phi_rec, U, spec: MaskSpec):
 
 
 def zeta_transform(F):
-    """Subset sums over the endpoint's landmark block (attention.py:369-384).
-
-    The endpoint mask (``d = floor(log2 T)``) is not part of this build's
-    kernel set; see the package documentation.
-    """
-    raise NotImplementedError("zeta_transform: the endpoint mask's landmark block has no "
-                              "HIP kernel in this build")
+    """``(Z_k F)_a = sum_{x subset of a} F_x`` over ``N = 2^k`` profiles
+    (attention.py:369-384): a k-stage butterfly in LDS, fp32 out of place."""
+    nb, N = F.shape[0], F.shape[1]
+    if N & (N - 1):
+        raise AssertionError("zeta needs a power-of-two profile count")
+    return _hip.zeta(F)
 
 
 def walsh_incidence(F):
-    """The Walsh butterfly route of attention.py:288-307; not in this build --
-    :func:`apply_incidence` applies the endpoint's ragged ``C`` by gather."""
-    raise NotImplementedError("walsh_incidence: use apply_incidence (CSR gather kernel)")
+    """``C = (J + H)/2`` applied by a Walsh butterfly (attention.py:288-307):
+    the endpoint mask's ``C[h, a] = 1{popcount(h & a) even}``, fp32."""
+    nb, N = F.shape[0], F.shape[1]
+    if N & (N - 1):
+        raise AssertionError("Walsh route needs a power-of-two profile count")
+    return _hip.walsh(F)
+
+
+def direct_long_range(Psi, Vb, spec: MaskSpec, acc_dtype=None, type_chunk: int = 64):
+    """The unpooled backend (attention.py:333-362): ``U_h`` summed straight from
+    the landmark columns of row type ``h``, one Gram sum per type on the GPU.
+    Needs ``to_device(spec, ..., want_direct=True)`` like the reference;
+    ``type_chunk`` bounded the reference's gather and is ignored."""
+    who = "direct_long_range"
+    _acc(Psi, acc_dtype, who)
+    if getattr(spec, "type_cols_c_t", None) is None:
+        raise ValueError("the direct backend needs to_device(..., want_direct=True)")
+    return _hip.direct(Psi, Vb, spec.type_cols_c_t, spec.type_counts_t, spec.n_P)
 
 
 # ---------------------------------------------------------------------------
@@ -353,66 +381,97 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
     """Algorithm 1 of the reference (attention.py:391-455) on the GPU.
 
     Long range (pool by profile, incidence, type-major query) and the causal
-    segmented scan are summed before the single division.  Returns fp32
-    ``(nb, T, d_v)``; with ``return_parts`` also ``{"U", "Y_lr", "H"}``.
+    segmented scan are summed before the single division.  ``long_range`` is
+    ``"pooled"``, ``"direct"`` (the unpooled comparison) or ``"subtractive"``
+    (one unbroken scan minus the excluded mass, attention.py:458-482); the
+    endpoint mask's landmark block goes through the zeta transform.  Returns
+    fp32 ``(nb, T, d_v)``; with ``return_parts`` also the reference's parts.
     ``timer(name)`` (a context-manager factory) brackets the phases
-    ``lr_pool``, ``lr_incidence``, ``lr_query``, ``scan`` and ``normalise``.
-    Without a timer or parts the whole schedule is one library call;
-    ``workspace`` (uint8, on the device) may be passed to reuse its scratch.
-    When an input requires grad (and grad mode is on) the call is recorded as
-    one autograd node whose backward runs on the HIP kernels
+    ``lr_pool``, ``lr_incidence``, ``lr_query``, ``zeta``, ``scan`` and
+    ``normalise``.  The pooled schedule of a geometric mask without a timer or
+    parts is one library call; ``workspace`` (uint8, on the device) may be
+    passed to reuse its scratch.  When an input requires grad (and grad mode
+    is on) that schedule is recorded as one autograd node whose backward runs
+    on the HIP kernels
     (:class:`smat_attention_amd.kernels.hip_bwd.SmatAttentionFunction`).
     """
     who = "smat_attention"
     _backend(scan_backend, who)
-    _backend(incidence_backend, who)
-    if long_range != "pooled":
-        raise NotImplementedError(f"{who}: long_range={long_range!r}; this build implements "
-                                  f"the pooled schedule")
+    if incidence_backend not in _INCIDENCE_BACKENDS:
+        raise ValueError(f"{who}: unknown incidence_backend {incidence_backend!r}")
+    if long_range not in ("pooled", "direct", "subtractive"):
+        raise ValueError(f"{who}: long_range must be pooled, direct or subtractive, "
+                         f"got {long_range!r}")
     _acc(Phi, acc_dtype, who)
     if Psi.dtype != Phi.dtype or Vb.dtype != Phi.dtype:
         raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
-    if spec.kind != "geometric":
-        raise NotImplementedError(f"{who}: the {spec.kind} mask's landmark block (zeta "
-                                  f"transform) has no HIP kernel in this build")
     nb, T, r = Phi.shape
     if T != spec.T:
         raise ValueError(f"{who}: T={T} but the mask was built for T={spec.T}")
     C = min(chunk, T)
     n = spec.n
-    if n % C:
+    endpoint = spec.kind == "endpoint"
+    segmented = long_range != "subtractive" and not endpoint
+    if segmented and n % C:
         raise ValueError(f"segment boundary n={n} is not a multiple of chunk={C}")
     _staged(spec, Phi.device)
-    idx, indptr, deg = _incidence_args(spec)
+    plain = long_range == "pooled" and not endpoint
 
     wants_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (Phi, Psi, Vb, g))
     if wants_grad and not _no_grad_fn:
+        if not plain:
+            raise NotImplementedError(f"{who}: gradients are implemented for the pooled "
+                                      f"schedule of a geometric mask")
         if return_parts or timer is not None:
             raise NotImplementedError(f"{who}: return_parts/timer are forward-only; call "
                                       f"under torch.no_grad() or on detached inputs")
         from .kernels.hip_bwd import SmatAttentionFunction
         return SmatAttentionFunction.apply(Phi, Psi, Vb, g, spec, C)
 
-    if timer is None and not return_parts:
+    if plain and timer is None and not return_parts:
+        idx, indptr, deg = _incidence_args(spec)
         pc = spec.plane_code_t if _plane_ok(spec, r * Vb.shape[-1]) else None
         return _hip.forward(Phi, Psi, Vb, idx, deg, n=n, n_P=spec.n_P, N0=spec.N0, B=spec.B,
                             chunk=C, indptr=indptr, plane_code=pc, field_q=spec.q, g=g,
                             workspace=workspace)
 
     tm = timer or (lambda name: nullcontext())
+    if long_range == "subtractive":
+        return _subtractive(Phi, Psi, Vb, spec, C, g, tm, return_parts, incidence_backend)
     parts: Dict[str, torch.Tensor] = {}
     p = Vb.shape[-1]
+    F = None
     with tm("lr_pool"):
         F_glob = (torch.empty(nb, r, p, device=Phi.device, dtype=torch.float32)
                   if spec.n_P else None)
-        F = _hip.pool(Psi, Vb, spec.n_P, n, spec.N0, F_glob=F_glob)
+        if long_range == "pooled" or endpoint:
+            F = _hip.pool(Psi, Vb, spec.n_P, n, spec.N0, F_glob=F_glob)
+        elif F_glob is not None:        # direct: only the global channel's rank-one term
+            _hip.pool(Psi, Vb, spec.n_P, spec.n_P, 1, F_glob=F_glob)
     with tm("lr_incidence"):
-        U = _incidence(F, spec, F_glob)
+        if long_range == "direct":
+            U = direct_long_range(Psi, Vb, spec)
+            if F_glob is not None:
+                U += F_glob.unsqueeze(1)
+        elif endpoint and incidence_backend in ("auto", "walsh"):
+            U = walsh_incidence(F)
+        else:
+            U = _incidence(F, spec, F_glob)
     with tm("lr_query"):
         Y_lr = _hip.query(Phi[:, n:], U)
-    with tm("scan"):
-        H = segmented_causal_scan(Phi, Psi, Vb, n=n, chunk=C)
+    if endpoint:
+        with tm("zeta"):
+            if F is None:
+                F = _hip.pool(Psi, Vb, 0, n, spec.N0)
+            top = _hip.query(Phi[:, :n], _hip.zeta(F, out=F))   # row t reads Z_t
+        with tm("scan"):
+            loc = segmented_causal_scan(Phi[:, n:], Psi[:, n:], Vb[:, n:], n=0, chunk=C)
+        H = torch.cat([top, loc], dim=1)
+        parts["zeta"] = top
+    else:
+        with tm("scan"):
+            H = segmented_causal_scan(Phi, Psi, Vb, n=n, chunk=C)
     with tm("normalise"):
         out = _hip.normalise(H, n, Y_lr, g)
     if return_parts:
@@ -420,6 +479,33 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
         Hfull[:, n:] += Y_lr
         parts.update(U=U, Y_lr=Y_lr, H=Hfull)
         return out, parts
+    return out
+
+
+def _subtractive(Phi, Psi, Vb, spec, C, g, tm, return_parts, incidence_backend):
+    """Remark 3.10 (attention.py:458-482): one unbroken causal scan minus the
+    excluded long-range mass ``Ybar = R (F_tot - U)``.  The complement kernel
+    forms ``U - F_tot`` in place, so the query returns ``-Y_ex`` and the
+    normalisation adds it."""
+    n = spec.n
+    with tm("lr_pool"):
+        F = _hip.pool(Psi, Vb, spec.n_P, n, spec.N0)
+    with tm("lr_incidence"):
+        if spec.kind == "endpoint" and incidence_backend in ("auto", "walsh"):
+            U = walsh_incidence(F)
+        else:
+            U = _incidence(F, spec, None)
+        _hip.incidence_complement(F, U)
+    with tm("lr_query"):
+        Y_neg = _hip.query(Phi[:, n:], U)
+    with tm("scan"):
+        H = segmented_causal_scan(Phi, Psi, Vb, n=0, chunk=C)
+    with tm("normalise"):
+        out = _hip.normalise(H, n, Y_neg, g)
+    if return_parts:
+        Hfull = H.clone()
+        Hfull[:, n:] += Y_neg
+        return out, {"H": Hfull, "Y_ex": -Y_neg}
     return out
 
 
@@ -448,7 +534,8 @@ class SmatDecoder:
     def __init__(self, Psi_prefix, Vb_prefix, spec: MaskSpec, *, acc_dtype=None,
                  incidence_backend: str = "auto"):
         who = "SmatDecoder"
-        _backend(incidence_backend, who)
+        if incidence_backend not in _INCIDENCE_BACKENDS:
+            raise ValueError(f"{who}: unknown incidence_backend {incidence_backend!r}")
         _acc(Psi_prefix, acc_dtype, who)
         self.spec = spec
         self.acc = torch.float32
@@ -459,7 +546,10 @@ class SmatDecoder:
         _staged(spec, dev)
         F_glob = torch.empty(nb, r, p, device=dev, dtype=torch.float32) if spec.n_P else None
         F = _hip.pool(Psi_prefix, Vb_prefix, spec.n_P, spec.n, spec.N0, F_glob=F_glob)
-        self.U = _incidence(F, spec, F_glob)
+        if spec.kind == "endpoint" and incidence_backend in ("auto", "walsh"):
+            self.U = walsh_incidence(F)
+        else:
+            self.U = _incidence(F, spec, F_glob)
         del F
         self._S = [torch.zeros(nb, r, p, device=dev, dtype=torch.float32),
                    torch.empty(nb, r, p, device=dev, dtype=torch.float32)]

@@ -80,11 +80,11 @@ __global__ __launch_bounds__(gr::kThreads) void gram_kernel(
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int sidx = s0 + tt + u;
-          const int64_t tok = start + (int64_t)sidx * stride;
+          const int64_t tok = sidx < count ? gram_token(it, item, start, stride, sidx) : 0;
           rowp[u] = sidx < count ? (is_psi ? psib + tok * k_st : vbb + tok * v_st) : nullptr;
         }
         Tile8<In> tl;
-        const int64_t tok0 = start + (int64_t)s0 * stride;    // valid: s0 < count
+        const int64_t tok0 = gram_token(it, item, start, stride, s0);    // valid: s0 < count
         if (is_psi) {
           tile8_load<In, VEC>(tl, rowp, psib + tok0 * k_st, c0, r);
           tile8_store_T<In>(tl, psiT, kTPad, c0, tt);
@@ -310,6 +310,25 @@ int pool_dispatch(int dtype, const void* psi, const void* vb, float* F, float* F
                        "smat_pool");
 }
 
+// Unpooled long-range sums U_h = sum_{j in cols_h} Psi_{n_P+j}^T Vb_{n_P+j}: one
+// item per row type over its compacted column list.
+int direct_dispatch(int dtype, const void* psi, const void* vb, const int32_t* cols,
+                    const int32_t* counts, int kappa, float* U, int nb, int B, int n_P, int r,
+                    int p, int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
+                    hipStream_t stream) {
+  GramItems it{};
+  it.mode = 2;
+  it.n_P = n_P;
+  it.cols = cols;
+  it.counts = counts;
+  it.kappa = kappa;
+  it.nsplit = 1;
+  it.per = 1 << 30;
+  const int64_t rp = (int64_t)r * p;
+  return gram_dispatch(dtype, psi, vb, U, nullptr, it, B, nb, r, p, k_sb, k_st, v_sb, v_st,
+                       (int64_t)B * rp, rp, 0, nullptr, stream, "smat_direct");
+}
+
 }  // namespace smat
 
 extern "C" int smat_chunk_states(int dtype, const void* psi, const void* vb, float* D, int nb,
@@ -348,4 +367,20 @@ extern "C" int smat_pool(int dtype, const void* psi, const void* vb, float* F, f
                "smat_pool: workspace must be 16-byte aligned");
   return pool_dispatch(dtype, psi, vb, F, F_glob, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st,
                        (float*)workspace, workspace ? workspace_bytes : 0, (hipStream_t)stream);
+}
+
+extern "C" int smat_direct(int dtype, const void* psi, const void* vb, const int32_t* cols,
+                           const int32_t* counts, int kappa, float* U, int nb, int B, int n_P,
+                           int r, int p, int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
+                           void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(psi && vb && cols && counts && U, SMAT_EINVAL, "smat_direct: null pointer");
+  SMAT_REQUIRE(nb >= 0 && B >= 0 && kappa >= 0 && n_P >= 0, SMAT_EINVAL,
+               "smat_direct: bad sizes");
+  SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 1 && p <= kMaxP, SMAT_EUNSUPPORTED,
+               "smat_direct: r=%d p=%d beyond r<=%d, p<=%d", r, p, kMaxR, kMaxP);
+  SMAT_REQUIRE(k_st >= r && v_st >= p, SMAT_EINVAL, "smat_direct: row stride too short");
+  return direct_dispatch(dtype, psi, vb, cols, counts, kappa, U, nb, B, n_P, r, p, k_sb, k_st,
+                         v_sb, v_st, (hipStream_t)stream);
 }

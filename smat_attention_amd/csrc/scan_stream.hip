@@ -472,9 +472,9 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 // loads, the others four.
 template <typename In>
 __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* psib,
-                                           const In* vbb, int64_t start, int64_t stride,
-                                           int base, int count, int64_t k_st, int64_t v_st,
-                                           int w, int lane) {
+                                           const In* vbb, const GramItems& it, int item,
+                                           int64_t start, int64_t stride, int base, int count,
+                                           int64_t k_st, int64_t v_st, int w, int lane) {
   constexpr int kL = ss::kPhiLoads + ss::kVbLoads;     // 34
 #pragma unroll
   for (int u = 0; u < 5; ++u) {
@@ -485,7 +485,7 @@ __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* ps
       if (I < ss::kPhiLoads) {
         const int row = 4 * I + (lane >> 4);
         const int k = (lane & 15) ^ swz16(row);
-        const int64_t tok = start + (base + row < count ? stride * (base + row) : 0);
+        const int64_t tok = gram_token(it, item, start, stride, base + row < count ? base + row : 0);
         src = psib + tok * k_st + 8 * k;
         dst = dpsi + 64 * I;
       } else {
@@ -494,7 +494,7 @@ __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* ps
         const int row = L / ss::kVbChunks;
         const int k = L - row * ss::kVbChunks;
         const int col = 8 * k + 8 <= v_st ? 8 * k : 0;
-        const int64_t tok = start + (base + row < count ? stride * (base + row) : 0);
+        const int64_t tok = gram_token(it, item, start, stride, base + row < count ? base + row : 0);
         src = vbb + tok * v_st + col;
         dst = dvb + 64 * li;
       }
@@ -531,7 +531,8 @@ __global__ __launch_bounds__(ss::kThreads, 2) void gram_stream_kernel(
 #pragma unroll
   for (int at = 0; at < 8; ++at) accS[at] = zero4();
   if (nsteps > 0)
-    issue_gram<In>(psi0, vb0, psib, vbb, start, stride, 0, count, k_st, v_st, w, lane_id());
+    issue_gram<In>(psi0, vb0, psib, vbb, it, item, start, stride, 0, count, k_st, v_st, w,
+                   lane_id());
 
   auto step = [&](auto BUFC, int s) {
     constexpr int BUF = decltype(BUFC)::value;
@@ -541,7 +542,7 @@ __global__ __launch_bounds__(ss::kThreads, 2) void gram_stream_kernel(
     asm volatile("" : "+v"(lane));
     const int g = lane >> 4;
     if (s + 1 < nsteps) {
-      issue_gram<In>(BUF ? psi0 : psi1, BUF ? vb0 : vb1, psib, vbb, start, stride,
+      issue_gram<In>(BUF ? psi0 : psi1, BUF ? vb0 : vb1, psib, vbb, it, item, start, stride,
                      (s + 1) * kStep, count, k_st, v_st, w, lane);
       if (w < 2)
         wait_vmcnt<5>();

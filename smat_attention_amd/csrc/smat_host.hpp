@@ -69,6 +69,11 @@ struct GramItems {
   // multiple of the 32-token block); run s writes partial s, and a second
   // kernel sums the partials in run order, so the result is deterministic.
   int nsplit, per;
+  // mode 2: item i sums the landmark columns cols[i*kappa .. i*kappa + counts[i])
+  // (tokens n_P + col): the unpooled (direct) long-range sums of row types.
+  const int32_t* cols;
+  const int32_t* counts;
+  int kappa;
 };
 
 __device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& start,
@@ -86,6 +91,10 @@ __device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& s
     stride = 1;
     const int64_t end = min((int64_t)c1 * it.C, (int64_t)it.T);
     count = (int)max((int64_t)0, end - start);
+  } else if (it.mode == 2) {
+    start = it.n_P;
+    stride = 1;
+    count = it.counts[i];
   } else {
     if (i < it.N0) {
       const int nX = it.n - it.n_P;
@@ -98,6 +107,13 @@ __device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& s
       count = it.n_P;
     }
   }
+}
+
+// Token of term `idx` of item `item` (start, stride from gram_item).
+__device__ __forceinline__ int64_t gram_token(const GramItems& it, int item, int64_t start,
+                                              int64_t stride, int idx) {
+  if (it.mode == 2) return start + it.cols[(int64_t)item * it.kappa + idx];
+  return start + (int64_t)idx * stride;
 }
 
 constexpr int kMaxR = 128;

@@ -64,6 +64,11 @@ SIGNATURES = {
                           _i, _i, _i, _i, _i, _i, _i, _i, _i,
                           _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                           _p, _i64, _p]),
+    "smat_direct": (_i, [_i, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64,
+                         _p]),
+    "smat_zeta": (_i, [_p, _p, _i, _i, _i64, _p]),
+    "smat_walsh": (_i, [_p, _p, _i, _i, _i64, _p]),
+    "smat_incidence_complement": (_i, [_p, _p, _i, _i, _i, _i64, _p]),
     "smat_decode_step": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64,
                               _i64, _i64, _i64, _p]),
 }

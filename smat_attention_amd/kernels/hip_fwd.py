@@ -31,7 +31,8 @@ MAX_C = 256
 __all__ = [
     "available", "chunk_local", "incidence", "pool_ok", "pool", "incidence_plane",
     "chunk_states", "segment_scan", "causal_scan", "query", "normalise", "forward",
-    "forward_workspace_bytes", "decode_step", "validate_table",
+    "forward_workspace_bytes", "decode_step", "validate_table", "direct", "zeta", "walsh",
+    "incidence_complement",
     "HipKernelError", "HipUnavailable", "MAX_R", "MAX_P", "MAX_C",
 ]
 
@@ -243,6 +244,65 @@ def causal_scan(Phi, Psi, Vb, n: int, chunk: int, *, Y=None, g=None, write_H: bo
          out.stride(0), out.stride(1), gc.stride(0) if gc is not None else 0, int(write_H),
          base, wsb, stream_of(q))
     return out
+
+
+def direct(Psi, Vb, cols, counts, n_P: int):
+    """Unpooled ``U_h = sum_{j in cols_h} Psi_{n_P+j}^T Vb_{n_P+j}``: fp32 ``(nb, B, r, p)``.
+
+    ``cols`` (``(B, kappa)`` int32) lists each row type's landmark columns,
+    ``counts[h]`` of them first; ``counts`` is ``(B,)`` int32.
+    """
+    who = "direct"
+    _on_gpu(who, Psi, Vb, cols, counts)
+    if cols.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise TypeError(f"{who}: cols and counts must be int32")
+    nb, T, R = Psi.shape
+    P = Vb.shape[-1]
+    B, kappa = cols.shape
+    code = _code(Psi, who)
+    k, k_sb, k_st = _rows3(Psi)
+    v, v_sb, v_st = _rows3(Vb)
+    cc, cn = cols.contiguous(), counts.contiguous()
+    U = torch.empty(nb, B, R, P, device=Psi.device, dtype=torch.float32)
+    call("smat_direct", code, k.data_ptr(), v.data_ptr(), cc.data_ptr(), cn.data_ptr(), kappa,
+         U.data_ptr(), nb, B, n_P, R, P, k_sb, k_st, v_sb, v_st, stream_of(k))
+    return U
+
+
+def _butterfly(name, F, out):
+    _on_gpu(name, F, out)
+    nb, N = F.shape[0], F.shape[1]
+    Fc = F.contiguous().float()
+    rp = Fc[0, 0].numel() if N else 0
+    if out is None:
+        out = torch.empty_like(Fc)
+    elif out.shape != Fc.shape or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError(f"{name}: out must be contiguous fp32 of F's shape")
+    call(f"smat_{name}", Fc.data_ptr(), out.data_ptr(), nb, N, rp, stream_of(Fc))
+    return out
+
+
+def zeta(F, *, out=None):
+    """Subset sums ``Z_a = sum_{x subset of a} F_x`` over ``N = 2^k`` profiles (fp32)."""
+    return _butterfly("zeta", F, out)
+
+
+def walsh(F, *, out=None):
+    """Endpoint incidence ``U = (sum_x F_x + H F) / 2`` over ``N = 2^k`` profiles (fp32)."""
+    return _butterfly("walsh", F, out)
+
+
+def incidence_complement(F, U):
+    """In place ``U_h <- U_h - sum_x F_x`` (the negated complement ``-(F_tot - U)``)."""
+    who = "incidence_complement"
+    _on_gpu(who, F, U)
+    if not (F.is_contiguous() and U.is_contiguous()) or F.dtype != torch.float32 or \
+            U.dtype != torch.float32:
+        raise ValueError(f"{who}: F and U must be contiguous fp32")
+    nb, N0, B = F.shape[0], F.shape[1], U.shape[1]
+    rp = F[0, 0].numel()
+    call("smat_incidence_complement", F.data_ptr(), U.data_ptr(), nb, N0, B, rp, stream_of(F))
+    return U
 
 
 def segment_scan(D, nc0: int):

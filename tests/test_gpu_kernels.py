@@ -414,3 +414,68 @@ def test_decode_matches_prefill(dt, T, d):
     else:
         assert (got.double() - ref64).abs().max().item() < 2e-2
     assert dec.cache_words() == 3 * (spec.B + 1) * 32 * 33
+
+
+# ---------------------------------------------------------------------------
+# the other schedules: endpoint (zeta + Walsh), direct, subtractive
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,rp", [(128, 32 * 33), (512, 64 * 65), (4096, 16 * 17), (32768, 8)])
+def test_zeta_and_walsh_butterflies(N, rp):
+    _say("zeta/walsh", N, rp)
+    g = torch.Generator().manual_seed(41)
+    F = torch.randn(2, N, rp, generator=g)
+    Fd = F.to(DEV)
+    Z = A.zeta_transform(Fd.view(2, N, rp, 1))
+    W = A.walsh_incidence(Fd.view(2, N, rp, 1))
+    Zr = O.zeta_transform(F.double().view(2, N, rp, 1))
+    Wr = O.walsh_incidence(F.double().view(2, N, rp, 1))
+    assert _rel(Z, Zr) < 1e-5 and _rel(W, Wr) < 1e-5
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,hd", [(256, 32), (300, 32), (1024, 64), (2048, 128)])
+def test_forward_endpoint(dt, T, hd):
+    """d = floor(log2 T): zeta transform over the landmark block, Walsh incidence."""
+    spec = build_mask(T, T.bit_length() - 1, chunk=8)
+    assert spec.kind == "endpoint"
+    Phi, Psi, Vb = _feats(2, T, hd, dt, seed=42, k_scale=0.5)
+    _check_forward(spec, Phi, Psi, Vb, dt=dt, label=f"endpoint T={T} hd={hd}")
+
+
+@pytest.mark.parametrize("lr", ["direct", "subtractive"])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,d,n_P,hd", [(2048, 3, 0, 32), (2048, 3, 16, 32), (4096, 2, 0, 64),
+                                        (8192, 3, 0, 128)])
+def test_forward_direct_and_subtractive(lr, dt, T, d, n_P, hd):
+    """The comparison schedules against the oracle's own (attention.py:333-362, 458-482)."""
+    spec = A.to_device(build_mask(T, d, chunk=128, n_P=n_P), DEV, want_direct=True)
+    Phi, Psi, Vb = _feats(2, T, hd, dt, seed=43, k_scale=0.5)
+    Pd, Sd, Wd = (x.to(DEV) for x in (Phi, Psi, Vb))
+    out = A.smat_attention(Pd, Sd, Wd, spec, long_range=lr)
+    torch.cuda.synchronize()
+    if dt == torch.float32:
+        ref = O.smat_attention(Phi.double(), Psi.double(), Vb.double(), spec, long_range=lr)
+        tol = 1e-5 if lr == "direct" else 1e-4      # subtractive cancels in the normaliser
+        _say(lr, T, d, n_P, hd, f"fp32 rel {_rel(out, ref):.2e}")
+        assert _rel(out, ref) < tol
+    else:
+        ref = O.smat_attention(Phi, Psi, Vb, spec, long_range=lr)
+        e = (out.double().cpu() - ref.double()).abs().max().item()
+        _say(lr, T, d, n_P, hd, f"bf16 |O - ref| {e:.2e}")
+        assert e < 2e-2
+    # the schedules agree with the pooled one
+    pooled = A.smat_attention(Pd, Sd, Wd, spec)
+    assert (out - pooled).abs().max().item() < (1e-3 if dt == torch.float32 else 3e-2)
+
+
+def test_decode_endpoint():
+    T = 1024
+    spec = build_mask(T, T.bit_length() - 1, chunk=8)
+    Phi, Psi, Vb = _feats(1, T, 32, torch.float32, seed=44)
+    Pd, Sd, Wd = (x.to(DEV) for x in (Phi, Psi, Vb))
+    full = A.smat_attention(Pd, Sd, Wd, spec)
+    dec = A.SmatDecoder(Sd[:, :spec.n], Wd[:, :spec.n], spec)
+    for t in range(spec.n, spec.n + 40):
+        o = dec.step(Pd[:, t], Sd[:, t], Wd[:, t])
+        assert (o - full[:, t]).abs().max().item() < 1e-4 * max(1.0, full[:, t].abs().max().item())
