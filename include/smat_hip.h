@@ -265,6 +265,38 @@ int smat_walsh(const float* F, float* U, int nb, int N, int64_t rp, void* stream
 int smat_incidence_complement(const float* F, float* U, int nb, int N0, int B, int64_t rp,
                               void* stream);
 
+/*
+ * Gram sums over token lists (CSR): G[i] = sum_{j in tokens[offs[i] .. offs[i+1])}
+ * psi_j^T vb_j, fp32 (nitems, r, p) contiguous; psi / vb are row matrices with
+ * row strides k_st / v_st (sequences flattened: token = sequence * T + t).
+ * The pool by cell of a content-addressed assignment, src/smat/assign.py:431-436.
+ */
+int smat_gram_lists(int dtype, const void* psi, const void* vb, const int32_t* tokens,
+                    const int64_t* offs, float* G, int nitems, int r, int p,
+                    int64_t k_st, int64_t v_st, void* stream);
+
+/*
+ * Read by type over row lists (CSR): Y[i] = phi[i] U[h] for every row i in
+ * rows[roffs[h] .. roffs[h+1]), h < ntypes; maxcnt bounds the list lengths.
+ * U: (ntypes, r, p) fp32, Y rows y_st apart.  The point / plane read of a
+ * content-addressed assignment, src/smat/assign.py:437-439, 471-472.
+ */
+int smat_query_lists(int dtype, const void* phi, const float* U, float* Y,
+                     const int32_t* rows, const int64_t* roffs, int ntypes, int maxcnt,
+                     int r, int p, int64_t q_st, int64_t y_st, void* stream);
+
+/*
+ * Content hash of token rows u (nb, L, dm; dtype of u): for head h and
+ * coordinate k < dim, z = (LN(u) . Wn[h,k]) gamma[h,k] + bias[h,k],
+ * s = clamp(q Phi_N(z), 0, q - 1e-4), cell = sum_k floor(s_k) q^(dim-1-k).
+ * Wn: (nh, dim, dm) unit rows, fp32.  Outputs s (nb*nh, L, dim) fp32 and
+ * cells (nb*nh, L) int64.  Replaces the hard path of ContentAssign._cells,
+ * src/smat/assign.py:246-295.
+ */
+int smat_cell_hash(int dtype, const void* u, const float* Wn, const float* gamma,
+                   const float* bias, float* s_out, int64_t* cells, int nb, int L, int dm,
+                   int nh, int dim, int q, int64_t u_sb, int64_t u_st, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,256 @@
+"""Content-addressed assignment on the GPU (the reference's src/smat/assign.py).
+
+``ContentAssign`` replaces the positional maps ``prof(j) = (j - n_P) mod N0``
+and ``type(i) = i mod B`` with a hash of token content and runs the whole
+long-range branch: pool the distant keys by cell, apply the geometry's
+cosets for the plane read, contract every recent query with the state of its
+type.  It returns the augmented long-range term ``(nb*h, T_R, p)`` that the
+causal branch adds before the single division -- where ``query_by_type``
+sits in the positional schedule.
+
+GPU work per call:
+
+* ``smat_cell_hash`` (HIP): LayerNorm, the unit-row projection, the normal
+  CDF and the floor, one wave per token row (assign.py:246-276);
+* a stable sort of tokens by cell (torch, index plumbing);
+* ``smat_gram_lists`` (HIP): the pool ``F_x = sum_{cell(j) = x} Psi_j^T Vb_j``
+  over each cell's token list (assign.py:431-436);
+* plane read: ``smat_incidence`` over the (direction, offset) cosets
+  (assign.py:442);
+* ``smat_query_lists`` (HIP): ``y_i = Phi_i U_type(i)`` over each type's row
+  list (assign.py:437-439, 471-472).
+
+Supported: ``mode`` point/plane (codim 1 or dim), ``src`` hidden/embed/id,
+``shift``, ``plant``, ``freeze``, the linear direction head, ``dir_override``,
+the hard mask (``anneal = 1``).  Parameters are created in the reference's
+order, so a module built after ``torch.manual_seed(s)`` holds the reference's
+values.  The forward is not differentiable here (the straight-through
+backward of the hash is not implemented); options outside the list raise
+``NotImplementedError`` at construction.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from .kernels.hip_fwd import _code, _rows3, call, stream_of
+
+__all__ = ["ContentAssign", "grouped_planes"]
+
+
+def grouped_planes(q: int, dim: int):
+    """(dirs, grouped): normalised directions of F_q^dim and, per (direction,
+    offset), the q^(dim-1) points of that affine hyperplane -- the reference's
+    enumeration (assign.py:45-60): lex-ordered points, leading nonzero = 1,
+    points of a hyperplane in increasing order."""
+    idx = np.arange(q ** dim, dtype=np.int64)
+    pts = np.stack([(idx // q ** (dim - 1 - k)) % q for k in range(dim)], axis=1)
+    nz = pts != 0
+    lead = nz.argmax(axis=1)
+    is_dir = nz.any(axis=1) & (pts[np.arange(q ** dim), lead] == 1)
+    dirs = pts[is_dir]
+    inner = (pts @ dirs.T) % q
+    order = np.argsort(inner, axis=0, kind="stable")
+    grouped = order.T.reshape(dirs.shape[0], q, q ** (dim - 1))
+    return dirs, grouped
+
+
+class ContentAssign(nn.Module):
+    """Hash tokens to profiles and queries to types; run the long-range branch.
+
+    Mirrors ``src/smat/assign.py:ContentAssign`` (constructor :136-243,
+    ``_cells`` :246-317, ``forward`` :352-406, ``_dense_read`` :431-472).
+    """
+
+    def __init__(self, n_heads, d_model, spec, mode="point", plant=True, src="hidden",
+                 freeze=False, shift=0, codim=None, vocab=None, conv_width=0,
+                 dir_head="linear", dir_hidden=512, dir_window=4, dir_soft=False):
+        super().__init__()
+        if conv_width > 1:
+            raise NotImplementedError("ContentAssign: conv_width > 1 (learned key convolution)")
+        if dir_head != "linear":
+            raise NotImplementedError(f"ContentAssign: dir_head={dir_head!r}; only the linear "
+                                      f"direction head")
+        self.codim = None if codim is None else int(codim)
+        if self.codim is not None:
+            assert 1 <= self.codim <= int(spec.dim), (self.codim, spec.dim)
+            if self.codim not in (1, int(spec.dim)):
+                raise NotImplementedError("ContentAssign: codimension between 1 and dim")
+            mode = "point" if self.codim == int(spec.dim) else "plane"
+        assert spec.kind == "geometric" and spec.dim >= 1
+        self.h = n_heads
+        self.q, self.dim, self.N0 = int(spec.q), int(spec.dim), int(spec.N0)
+        self.mode, self.plant = mode, plant
+        self.src, self.freeze, self.shift = src, freeze, int(shift)
+        self.conv_width = int(conv_width)
+        if src == "id":
+            assert vocab is not None, "the id hash needs the vocabulary size"
+            g = torch.Generator().manual_seed(1234)
+            self.register_buffer("id_cell",
+                                 torch.randint(0, int(spec.N0), (vocab, n_heads), generator=g))
+        if mode == "plane" and self.dim == 1:
+            self.mode = "point"
+        self.ln = nn.LayerNorm(d_model, elementwise_affine=False)
+        self.W = nn.Parameter(torch.randn(n_heads, self.dim, d_model), requires_grad=not freeze)
+        self.gamma = nn.Parameter(torch.ones(n_heads, self.dim), requires_grad=not freeze)
+        self.b = nn.Parameter(torch.zeros(n_heads, self.dim), requires_grad=not freeze)
+        if self.mode == "plane":
+            dirs, grouped = grouped_planes(self.q, self.dim)
+            self.D, self.n_cosets = int(grouped.shape[0]), int(grouped.shape[1])
+            self.dir_head = dir_head
+            self.dir_soft = bool(dir_soft)
+            # the reference draws this projection twice for the linear head
+            # (assign.py:201-203 and :237-238); the second draw is the one kept
+            self.Wd = nn.Parameter(torch.randn(n_heads, self.D, d_model) * d_model ** -0.5,
+                                   requires_grad=not freeze)
+            self.Wd = nn.Parameter(torch.randn(n_heads, self.D, d_model) * d_model ** -0.5,
+                                   requires_grad=not freeze)
+            M = np.zeros((self.D, self.n_cosets, self.N0), dtype=np.float32)
+            for e in range(self.D):
+                for o in range(self.n_cosets):
+                    M[e, o, grouped[e, o]] = 1.0
+            self.register_buffer("M", torch.from_numpy(M))
+            self.register_buffer("coset_of", torch.from_numpy(M.argmax(1)))
+            self.register_buffer("coset_pts", torch.from_numpy(
+                grouped.reshape(self.D * self.n_cosets, -1).astype(np.int32)))
+        cols = spec.planted_cols if spec.planted_cols is not None else np.zeros(0, dtype=np.int64)
+        self.register_buffer("plant_cols", torch.as_tensor(np.asarray(cols), dtype=torch.long))
+        self.register_buffer("plant_cells",
+                             torch.as_tensor([self.q ** (self.dim - l)
+                                              for l in range(1, self.dim + 1)], dtype=torch.long))
+        self.anneal = 1.0
+        self.last_soft_q = None
+        self.last_hard_k = None
+        self.probe = False
+        self.last = None
+        self.last_occ = None
+        self.last_dens = None
+        self.aux = None
+
+    # ------------------------------------------------------------------ hash
+    def _hash(self, u):
+        """(nb, L, d_model) -> cells (nb*h, L) int64 and s (nb*h, L, dim) = q Phi_N(z)."""
+        nb, L, dm = u.shape
+        uc, u_sb, u_st = _rows3(u)
+        Wn = (self.W / self.W.norm(dim=-1, keepdim=True).clamp_min(1e-6)).detach().float()
+        Wn = Wn.contiguous()
+        gam = self.gamma.detach().float().contiguous()
+        bia = self.b.detach().float().contiguous()
+        s = torch.empty(nb * self.h, L, self.dim, device=u.device, dtype=torch.float32)
+        cells = torch.empty(nb * self.h, L, device=u.device, dtype=torch.int64)
+        call("smat_cell_hash", _code(uc, "ContentAssign"), uc.data_ptr(), Wn.data_ptr(),
+             gam.data_ptr(), bia.data_ptr(), s.data_ptr(), cells.data_ptr(), nb, L, dm,
+             self.h, self.dim, self.q, u_sb, u_st, stream_of(uc))
+        return cells, s
+
+    def _cells(self, u, plant_at=False, tok_w=None):
+        """Hard cells of every token (nb*h, L) int64, as assign.py:_cells with
+        anneal = 1: the hash, the planted columns, and the load-balance term
+        (``aux``) from the soft bin occupancy."""
+        if self.anneal < 1.0:
+            raise NotImplementedError("ContentAssign: the soft read (anneal < 1)")
+        cells, s = self._hash(u)
+        B, L = cells.shape
+        lo = s.floor()
+        frac = s - lo
+        lo = lo.long()
+        hi = (lo + 1).clamp(max=self.q - 1)
+        soft_lo, soft_hi = 1.0 - frac, frac
+        if tok_w is not None:
+            tw = tok_w.reshape(B, L, 1).to(s.dtype)
+            soft_lo, soft_hi = soft_lo * tw, soft_hi * tw
+        occ = torch.zeros(B, self.dim, self.q, device=s.device, dtype=s.dtype)
+        occ = occ.scatter_add(-1, lo.transpose(1, 2), soft_lo.transpose(1, 2))
+        occ = occ.scatter_add(-1, hi.transpose(1, 2), soft_hi.transpose(1, 2))
+        occ = occ / occ.sum(-1, keepdim=True).clamp_min(1e-6)
+        self.aux = None if self.freeze else (occ * (occ.clamp_min(1e-9) * self.q).log()).sum(-1).mean()
+        if plant_at and self.plant and self.plant_cols.numel():
+            cols = self.plant_cols[self.plant_cols < L]
+            if cols.numel():
+                cells[:, cols.to(cells.device)] = self.plant_cells[: cols.numel()].to(cells.device)
+        return cells
+
+    def _cells_id(self, ids):
+        nb, L = ids.shape
+        return self.id_cell[ids].permute(0, 2, 1).reshape(nb * self.h, L)
+
+    # ------------------------------------------------------------- the branch
+    def forward(self, u, Phi, Psi, Vb, n, emb=None, key_src=None, key_w=None,
+                dir_override=None, ids=None):
+        """u: (nb, T, d_model) layer input; Phi, Psi: (nb*h, T, r); Vb: (nb*h, T, p);
+        n: landmark/recent boundary.  Returns fp32 (nb*h, T - n, p)."""
+        if torch.is_grad_enabled() and (
+                any(t is not None and t.requires_grad for t in (u, Phi, Psi, Vb, emb, key_src))
+                or any(prm.requires_grad for prm in self.parameters())):
+            raise NotImplementedError("ContentAssign: the backward is not implemented; call "
+                                      "under torch.no_grad()")
+        if self.src == "id":
+            assert ids is not None, "the id hash needs token ids"
+            ik = ids if not self.shift else torch.cat(
+                [ids.new_zeros(ids.shape[0], self.shift), ids[:, :-self.shift]], dim=1)
+            ck, cq = self._cells_id(ik[:, :n]), self._cells_id(ids[:, n:])
+            self.aux = None
+        else:
+            h = u if (self.src == "hidden" or emb is None) else emb
+            hk = h if key_src is None else key_src
+            if self.shift:
+                hk = torch.cat([h.new_zeros(h.shape[0], self.shift, h.shape[2]),
+                                h[:, :-self.shift]], dim=1)
+            ck = self._cells(hk[:, :n], plant_at=True, tok_w=key_w)
+            aux_k = self.aux
+            cq = self._cells(h[:, n:])
+            self.aux = None if self.freeze else aux_k + self.aux
+        self.last_hard_k = ck.detach()
+        return self._read(u, Phi, Psi, Vb, n, ck, cq, dir_override)
+
+    def _read(self, u, Phi, Psi, Vb, n, ck, cq, dir_override):
+        nbh, T, r = Phi.shape
+        p = Vb.shape[-1]
+        T_R = T - n
+        dev = Phi.device
+        N0 = self.N0
+        # ---- pool by cell: tokens of each (sequence, cell), in token order
+        key = (torch.arange(nbh, device=dev).unsqueeze(1) * N0 + ck).reshape(-1)
+        order = torch.argsort(key, stable=True)
+        seq = order // n
+        tokens = (seq * T + (order - seq * n)).to(torch.int32)
+        counts = torch.bincount(key, minlength=nbh * N0)
+        offs = torch.zeros(nbh * N0 + 1, device=dev, dtype=torch.int64)
+        offs[1:] = torch.cumsum(counts, 0)
+        Ps = Psi if Psi.stride(0) == T * Psi.stride(1) else Psi.contiguous()
+        Vs = Vb if Vb.stride(0) == T * Vb.stride(1) else Vb.contiguous()
+        F = torch.empty(nbh, N0, r, p, device=dev, dtype=torch.float32)
+        call("smat_gram_lists", _code(Ps, "ContentAssign"), Ps.data_ptr(), Vs.data_ptr(),
+             tokens.data_ptr(), offs.data_ptr(), F.data_ptr(), nbh * N0, r, p,
+             Ps.stride(1), Vs.stride(1), stream_of(Ps))
+        # ---- the read: a type per recent query
+        if self.mode == "point":
+            U, ntypes, typ = F, N0, cq
+        else:
+            nrows = self.D * self.n_cosets
+            U = torch.empty(nbh, nrows, r, p, device=dev, dtype=torch.float32)
+            pts = self.coset_pts.to(dev)
+            call("smat_incidence", F.data_ptr(), None, pts.data_ptr(), 0, None, pts.shape[1],
+                 U.data_ptr(), nbh, N0, nrows, r * p, stream_of(F))
+            if dir_override is not None:
+                e_star = dir_override.reshape(nbh, T_R).long()
+            else:
+                dl = torch.einsum("blm,hem->bhle", u[:, n:].float(), self.Wd.float())
+                e_star = dl.reshape(nbh, T_R, self.D).argmax(-1)
+            typ = e_star * self.n_cosets + self.coset_of.to(dev)[e_star, cq]
+            ntypes = nrows
+        key = (torch.arange(nbh, device=dev).unsqueeze(1) * ntypes + typ).reshape(-1)
+        order = torch.argsort(key, stable=True)
+        seq = order // T_R
+        rows = (seq * T + n + (order - seq * T_R)).to(torch.int32)
+        counts = torch.bincount(key, minlength=nbh * ntypes)
+        roffs = torch.zeros(nbh * ntypes + 1, device=dev, dtype=torch.int64)
+        roffs[1:] = torch.cumsum(counts, 0)
+        maxcnt = int(counts.max().item()) if counts.numel() else 0
+        Pr = Phi if Phi.stride(0) == T * Phi.stride(1) else Phi.contiguous()
+        Y = torch.empty(nbh, T, p, device=dev, dtype=torch.float32)
+        call("smat_query_lists", _code(Pr, "ContentAssign"), Pr.data_ptr(), U.data_ptr(),
+             Y.data_ptr(), rows.data_ptr(), roffs.data_ptr(), nbh * ntypes, maxcnt, r, p,
+             Pr.stride(1), Y.stride(1), stream_of(Pr))
+        return Y[:, n:]

@@ -329,6 +329,25 @@ int direct_dispatch(int dtype, const void* psi, const void* vb, const int32_t* c
                        (int64_t)B * rp, rp, 0, nullptr, stream, "smat_direct");
 }
 
+// Gram sums over token lists in CSR form: item i sums rows tokens[offs[i] ..
+// offs[i+1]) of the (rows, r) / (rows, p) matrices psi / vb -- the pool of a
+// content-addressed assignment, items (sequence, cell) over tokens sorted by
+// cell.  G: (nitems, r, p) contiguous.
+int gram_lists_dispatch(int dtype, const void* psi, const void* vb, const int32_t* tokens,
+                        const int64_t* offs, float* G, int nitems, int r, int p, int64_t k_st,
+                        int64_t v_st, hipStream_t stream) {
+  GramItems it{};
+  it.mode = 2;
+  it.n_P = 0;
+  it.cols = tokens;
+  it.offs = offs;
+  it.nsplit = 1;
+  it.per = 1 << 30;
+  const int64_t rp = (int64_t)r * p;
+  return gram_dispatch(dtype, psi, vb, G, nullptr, it, nitems, 1, r, p, 0, k_st, 0, v_st, 0, rp,
+                       0, nullptr, stream, "smat_gram_lists");
+}
+
 }  // namespace smat
 
 extern "C" int smat_chunk_states(int dtype, const void* psi, const void* vb, float* D, int nb,
@@ -383,4 +402,18 @@ extern "C" int smat_direct(int dtype, const void* psi, const void* vb, const int
   SMAT_REQUIRE(k_st >= r && v_st >= p, SMAT_EINVAL, "smat_direct: row stride too short");
   return direct_dispatch(dtype, psi, vb, cols, counts, kappa, U, nb, B, n_P, r, p, k_sb, k_st,
                          v_sb, v_st, (hipStream_t)stream);
+}
+
+extern "C" int smat_gram_lists(int dtype, const void* psi, const void* vb, const int32_t* tokens,
+                               const int64_t* offs, float* G, int nitems, int r, int p,
+                               int64_t k_st, int64_t v_st, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(psi && vb && tokens && offs && G, SMAT_EINVAL, "smat_gram_lists: null pointer");
+  SMAT_REQUIRE(nitems >= 0, SMAT_EINVAL, "smat_gram_lists: bad sizes");
+  SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 1 && p <= kMaxP, SMAT_EUNSUPPORTED,
+               "smat_gram_lists: r=%d p=%d beyond r<=%d, p<=%d", r, p, kMaxR, kMaxP);
+  SMAT_REQUIRE(k_st >= r && v_st >= p, SMAT_EINVAL, "smat_gram_lists: row stride too short");
+  return gram_lists_dispatch(dtype, psi, vb, tokens, offs, G, nitems, r, p, k_st, v_st,
+                             (hipStream_t)stream);
 }

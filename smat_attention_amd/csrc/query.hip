@@ -30,7 +30,8 @@ constexpr int kCTPerWave = 3;
 template <typename In>
 __global__ __launch_bounds__(qy::kThreads) void query_kernel(
     const In* __restrict__ phi, const float* __restrict__ U, float* __restrict__ Y, int T_R, int B,
-    int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st, int nrb, int vec_q) {
+    int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st, int nrb, int vec_q,
+    const int32_t* __restrict__ rows, const int64_t* __restrict__ roffs) {
   using namespace qy;
   typedef typename Traits<In>::frag Frag;
   const int h = blockIdx.x / nrb;
@@ -40,8 +41,10 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
   const int row16 = lane & 15, grp = lane >> 4;
   const int rk = (r + 31) >> 5;
   const int nct = (p + 15) >> 4;
-  // rows of type h: i = h + k*B, k < cnt
-  const int cnt = (h < T_R) ? (T_R - h + B - 1) / B : 0;
+  // rows of type h: i = h + k*B, k < cnt -- or, with a row table, the rows
+  // rows[roffs[h] .. roffs[h+1])
+  const int cnt = rows ? (int)(roffs[h + 1] - roffs[h]) : (h < T_R) ? (T_R - h + B - 1) / B : 0;
+  const int32_t* hrows = rows ? rows + roffs[h] : nullptr;
   const int k0 = rb * kRowsPerWG;
   if (k0 >= cnt) return;
   const int nmt = min(kMT, (cnt - k0 + 15) / 16);
@@ -64,7 +67,7 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
     for (int t = 0; t < kMT; ++t) {
       const int k = k0 + 16 * t + row16;
       const int nv = (t < nmt && k < cnt) ? min(8, r - a0) : 0;
-      const int64_t i = (int64_t)h + (int64_t)k * B;
+      const int64_t i = !(k < cnt) ? 0 : hrows ? (int64_t)hrows[k] : (int64_t)h + (int64_t)k * B;
       pa[t] = load8<In>(phib + i * q_st + a0, nv, vec_q);
     }
 #pragma unroll
@@ -116,7 +119,10 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const int k = k0 + 16 * t + 4 * grp + i4;
-        if (k < cnt && c < p) Yb[((int64_t)h + (int64_t)k * B) * y_st + c] = acc[t][j][i4];
+        if (k < cnt && c < p) {
+          const int64_t i = hrows ? (int64_t)hrows[k] : (int64_t)h + (int64_t)k * B;
+          Yb[i * y_st + c] = acc[t][j][i4];
+        }
       }
     }
   }
@@ -298,8 +304,27 @@ static int launch_query(const void* phi, const float* U, float* Y, int nb, int T
   }
   const int vq = rows_vec_ok(phi, q_sb, q_st, sizeof(In));
   hipLaunchKernelGGL(query_kernel<In>, dim3((unsigned)gx, (unsigned)nb), dim3(qy::kThreads), 0,
-                     stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb, q_st, y_sb, y_st, nrb, vq);
+                     stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb, q_st, y_sb, y_st, nrb, vq,
+                     nullptr, nullptr);
   return launch_status("smat_query");
+}
+
+template <typename In>
+static int launch_query_lists(const void* phi, const float* U, float* Y, const int32_t* rows,
+                              const int64_t* roffs, int ntypes, int maxcnt, int r, int p,
+                              int64_t q_st, int64_t y_st, hipStream_t stream) {
+  const int nrb = (maxcnt + qy::kRowsPerWG - 1) / qy::kRowsPerWG;
+  const int64_t gx = (int64_t)ntypes * nrb;
+  if (gx >= (1ll << 31)) {
+    set_error("smat_query_lists: problem too large");
+    return SMAT_EUNSUPPORTED;
+  }
+  if (gx == 0) return SMAT_OK;
+  const int vq = rows_vec_ok(phi, 0, q_st, sizeof(In));
+  hipLaunchKernelGGL(query_kernel<In>, dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0, stream,
+                     (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st, (int64_t)0, y_st,
+                     nrb, vq, rows, roffs);
+  return launch_status("smat_query_lists");
 }
 
 int query_dispatch(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R, int B,
@@ -346,4 +371,28 @@ extern "C" int smat_query(int dtype, const void* phi_rec, const float* U, float*
   SMAT_REQUIRE(q_st >= r && y_st >= p, SMAT_EINVAL, "smat_query: row stride too short");
   return query_dispatch(dtype, phi_rec, U, Y, nb, T_R, B, r, p, q_sb, q_st, y_sb, y_st,
                         (hipStream_t)stream);
+}
+
+extern "C" int smat_query_lists(int dtype, const void* phi, const float* U, float* Y,
+                                const int32_t* rows, const int64_t* roffs, int ntypes, int maxcnt,
+                                int r, int p, int64_t q_st, int64_t y_st, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(phi && U && Y && rows && roffs, SMAT_EINVAL, "smat_query_lists: null pointer");
+  SMAT_REQUIRE(ntypes >= 0 && maxcnt >= 0, SMAT_EINVAL, "smat_query_lists: bad sizes");
+  SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 1 && p <= kMaxP, SMAT_EUNSUPPORTED,
+               "smat_query_lists: r=%d p=%d beyond r<=%d, p<=%d", r, p, kMaxR, kMaxP);
+  SMAT_REQUIRE(q_st >= r && y_st >= p, SMAT_EINVAL, "smat_query_lists: row stride too short");
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case SMAT_BF16:
+      return launch_query_lists<bf16>(phi, U, Y, rows, roffs, ntypes, maxcnt, r, p, q_st, y_st, st);
+    case SMAT_F16:
+      return launch_query_lists<f16>(phi, U, Y, rows, roffs, ntypes, maxcnt, r, p, q_st, y_st, st);
+    case SMAT_F32:
+      return launch_query_lists<float>(phi, U, Y, rows, roffs, ntypes, maxcnt, r, p, q_st, y_st,
+                                       st);
+  }
+  set_error("smat_query_lists: unknown dtype %d", dtype);
+  return SMAT_EINVAL;
 }

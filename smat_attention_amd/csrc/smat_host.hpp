@@ -71,9 +71,11 @@ struct GramItems {
   int nsplit, per;
   // mode 2: item i sums the landmark columns cols[i*kappa .. i*kappa + counts[i])
   // (tokens n_P + col): the unpooled (direct) long-range sums of row types.
+  // With offs set (CSR), item i's columns are cols[offs[i] .. offs[i+1]).
   const int32_t* cols;
   const int32_t* counts;
   int kappa;
+  const int64_t* offs;
 };
 
 __device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& start,
@@ -94,7 +96,7 @@ __device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& s
   } else if (it.mode == 2) {
     start = it.n_P;
     stride = 1;
-    count = it.counts[i];
+    count = it.offs ? (int)(it.offs[i + 1] - it.offs[i]) : it.counts[i];
   } else {
     if (i < it.N0) {
       const int nX = it.n - it.n_P;
@@ -112,7 +114,8 @@ __device__ __forceinline__ void gram_item(const GramItems& it, int i, int64_t& s
 // Token of term `idx` of item `item` (start, stride from gram_item).
 __device__ __forceinline__ int64_t gram_token(const GramItems& it, int item, int64_t start,
                                               int64_t stride, int idx) {
-  if (it.mode == 2) return start + it.cols[(int64_t)item * it.kappa + idx];
+  if (it.mode == 2)
+    return start + it.cols[(it.offs ? it.offs[item] : (int64_t)item * it.kappa) + idx];
   return start + (int64_t)idx * stride;
 }
 

@@ -1,0 +1,85 @@
+#!/usr/bin/env python3
+"""Write the content-assignment fixtures that only the reference itself pins.
+
+The hash of ``ContentAssign._cells`` (src/smat/assign.py:246-317) is float
+arithmetic whose bins decide every token's cell, and the module's parameters
+come from the global RNG in constructor order (:136-243); no closed form fixes
+either.  This script imports the reference's own ``assign.py`` and
+``mask.py`` (in the build container), builds the module after a fixed seed,
+runs its forward on seeded inputs and stores inputs, parameters, cells and
+outputs as data:
+
+    assign_golden.npz   per case: u, Phi, Psi, Vb, W, gamma, b, [Wd], the key
+                        cells (last_hard_k), the query cells (cells_of), the
+                        load-balance term aux and the forward output y
+
+Run from the repository root (needs /root/reference, numpy and torch):
+
+    python tests/golden/make_assign_golden.py
+"""
+from __future__ import annotations
+
+import importlib.util
+import os
+import sys
+
+import numpy as np
+import torch
+
+REF = "/root/reference/src/smat"
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+# (name, T, d, mode, heads, d_model, nb): point and plane reads, d = 2 and 3
+CASES = [
+    ("T512_d3_point", 512, 3, "point", 2, 64, 2),
+    ("T512_d3_plane", 512, 3, "plane", 2, 64, 2),
+    ("T512_d2_point", 512, 2, "point", 2, 64, 2),
+]
+
+
+def _load(name, path):
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def main():
+    mask = _load("_ref_smat_mask", os.path.join(REF, "mask.py"))
+    assign = _load("_ref_smat_assign", os.path.join(REF, "assign.py"))
+    out = {}
+    for name, T, d, mode, h, dm, nb in CASES:
+        spec = mask.build_mask(T, d, chunk=64)
+        n, r = spec.n, 16
+        torch.manual_seed(1000)
+        m = assign.ContentAssign(h, dm, spec, mode=mode)
+        m.eval()
+        g = torch.Generator().manual_seed(2000)
+        u = torch.randn(nb, T, dm, generator=g)
+        Phi = torch.rand(nb * h, T, r, generator=g) + 0.5
+        Psi = torch.rand(nb * h, T, r, generator=g) * 0.1 + 0.05
+        Vb = torch.cat([torch.randn(nb * h, T, r, generator=g), torch.ones(nb * h, T, 1)], -1)
+        with torch.no_grad():
+            y = m(u, Phi, Psi, Vb, n)
+            cq = m.cells_of(u[:, n:]).permute(0, 2, 1).reshape(nb * h, T - n)
+        out[f"{name}/u"] = u.numpy()
+        out[f"{name}/Phi"] = Phi.numpy()
+        out[f"{name}/Psi"] = Psi.numpy()
+        out[f"{name}/Vb"] = Vb.numpy()
+        out[f"{name}/W"] = m.W.detach().numpy()
+        out[f"{name}/gamma"] = m.gamma.detach().numpy()
+        out[f"{name}/b"] = m.b.detach().numpy()
+        if mode == "plane":
+            out[f"{name}/Wd"] = m.Wd.detach().numpy()
+        out[f"{name}/ck"] = m.last_hard_k.numpy()
+        out[f"{name}/cq"] = cq.numpy()
+        out[f"{name}/aux"] = np.array(float(m.aux))
+        out[f"{name}/y"] = y.numpy()
+        out[f"{name}/meta"] = np.array([T, d, h, dm, nb, n, r, 1 if mode == "plane" else 0])
+    np.savez_compressed(os.path.join(HERE, "assign_golden.npz"), **out)
+    print("wrote", len(CASES), "cases")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,107 @@
+"""Content-addressed assignment (src/smat/assign.py): the oracle against the
+reference's own fixtures, the module's parameters, and (on the GPU) the HIP
+path against both."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import assign_ref as R
+from smat_attention_amd.mask import build_mask
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "assign_golden.npz")
+CASES = ["T512_d3_point", "T512_d3_plane", "T512_d2_point"]
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return np.load(GOLD)
+
+
+def _case(gold, name):
+    g = {k.split("/", 1)[1]: torch.from_numpy(gold[k]) for k in gold.files if k.startswith(name + "/")}
+    T, d, h, dm, nb, n, r, plane = [int(x) for x in g["meta"]]
+    return g, dict(T=T, d=d, h=h, dm=dm, nb=nb, n=n, r=r, mode="plane" if plane else "point")
+
+
+def _module(meta, device="cpu"):
+    from smat_attention_amd.assign import ContentAssign
+    spec = build_mask(meta["T"], meta["d"], chunk=64)
+    torch.manual_seed(1000)
+    m = ContentAssign(meta["h"], meta["dm"], spec, mode=meta["mode"])
+    return m.to(device), spec
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_oracle_reproduces_reference_fixtures(gold, name):
+    g, meta = _case(gold, name)
+    spec = build_mask(meta["T"], meta["d"], chunk=64)
+    n, h = meta["n"], meta["h"]
+    ck, sk = R.cells(g["u"][:, :n], g["W"], g["gamma"], g["b"], spec.q, spec.dim, h)
+    ck = R.plant(ck, torch.as_tensor(spec.planted_cols, dtype=torch.long),
+                 torch.tensor([spec.q ** (spec.dim - l) for l in range(1, spec.dim + 1)]))
+    cq, _ = R.cells(g["u"][:, n:], g["W"], g["gamma"], g["b"], spec.q, spec.dim, h)
+    assert torch.equal(ck, g["ck"]) and torch.equal(cq, g["cq"])
+    M = None
+    if meta["mode"] == "plane":
+        from smat_attention_amd.assign import grouped_planes
+        _, grouped = grouped_planes(spec.q, spec.dim)
+        M = torch.zeros(grouped.shape[0], grouped.shape[1], spec.N0)
+        for e in range(grouped.shape[0]):
+            for o in range(grouped.shape[1]):
+                M[e, o, grouped[e, o]] = 1.0
+    y = R.dense_read(g["Phi"], g["Psi"], g["Vb"], n, ck, cq, spec.N0, mode=meta["mode"], M=M,
+                     Wd=g.get("Wd"), u=g["u"], h=h)
+    rel = (y - g["y"]).abs().max() / g["y"].abs().max()
+    assert rel < 1e-5
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_module_parameters_match_reference_init(gold, name):
+    """Constructed after the same seed, the module holds the reference's values."""
+    g, meta = _case(gold, name)
+    m, _ = _module(meta)
+    assert torch.equal(m.W.detach(), g["W"])
+    assert torch.equal(m.gamma.detach(), g["gamma"]) and torch.equal(m.b.detach(), g["b"])
+    if meta["mode"] == "plane":
+        assert torch.equal(m.Wd.detach(), g["Wd"])
+
+
+def test_grouped_planes_are_the_hyperplanes():
+    """Every (direction, offset) row is the solution set of <a_e, x> = o."""
+    from smat_attention_amd.assign import grouped_planes
+    for q, dim in [(5, 2), (3, 3), (7, 1)]:
+        dirs, grouped = grouped_planes(q, dim)
+        idx = np.arange(q ** dim)
+        pts = np.stack([(idx // q ** (dim - 1 - k)) % q for k in range(dim)], axis=1)
+        assert grouped.shape == (dirs.shape[0], q, q ** (dim - 1))
+        for e in range(dirs.shape[0]):
+            for o in range(q):
+                sel = np.flatnonzero((pts @ dirs[e]) % q == o)
+                assert np.array_equal(np.sort(grouped[e, o]), sel)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", CASES)
+def test_content_assign_on_gpu(gold, name):
+    """HIP hash + sorted pool + list read against the reference's fixtures."""
+    g, meta = _case(gold, name)
+    dev = torch.device("cuda:0")
+    m, spec = _module(meta, dev)
+    n = meta["n"]
+    with torch.no_grad():
+        y = m(g["u"].to(dev), g["Phi"].to(dev), g["Psi"].to(dev), g["Vb"].to(dev), n)
+        ck = m.last_hard_k.cpu()
+        cq, s = m._hash(g["u"][:, n:].to(dev))
+    torch.cuda.synchronize()
+    # cells: identical except a token whose q*Phi(z) sits within float noise of a bin edge
+    _, sk_ref = R.cells(g["u"][:, :n], g["W"], g["gamma"], g["b"], spec.q, spec.dim, meta["h"])
+    near = ((sk_ref - sk_ref.round()).abs() < 1e-4).any(-1)
+    bad = (ck != g["ck"]) & ~near
+    assert int(bad.sum()) == 0
+    assert torch.equal(cq.cpu(), g["cq"]) or int((cq.cpu() != g["cq"]).sum()) <= 2
+    if int((ck != g["ck"]).sum()) == 0:
+        rel = (y.cpu() - g["y"]).abs().max() / g["y"].abs().max()
+        assert rel < 1e-5
+    assert abs(float(m.aux) - float(g["aux"])) < 1e-5
