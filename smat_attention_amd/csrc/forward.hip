@@ -162,6 +162,7 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     // With no profiled landmark columns (n == n_P) every U_h is the global
     // channel alone (or zero): the incidence runs with an empty row.
     const bool profiled = n > n_P;
+    const char* phi_rec = (const char*)phi + (int64_t)n * q_st * elem_bytes(dtype);
     rc = pool_dispatch(dtype, psi, vb, F, Fg, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st, part,
                        part_bytes, st);
     if (rc) return rc;
@@ -171,9 +172,6 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
       rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
                               profiled ? deg : 0, U, nb, N0, B, rp, st);
     if (rc) return rc;
-  }
-  if (T_R > 0) {
-    const char* phi_rec = (const char*)phi + (int64_t)n * q_st * elem_bytes(dtype);
     rc = query_dispatch(dtype, phi_rec, U, Y, nb, T_R, B, r, p, q_sb, q_st, (int64_t)T_R * yst,
                         yst, st);
     if (rc) return rc;

@@ -299,6 +299,289 @@ static int launch_plane(const float* F, const float* F_glob, const int* code, in
 }
 
 // ---------------------------------------------------------------------------
+// Wave-per-direction kernel (d = 3): persistent, one line group per wave
+// ---------------------------------------------------------------------------
+
+// ds_read_b128 serves a 32-lane half of a wave at the full rate when both of its
+// sixteen-lane rows read sixteen consecutive 16-byte units that start at the
+// same offset modulo 16 units; rows that start at different offsets take about
+// twice as long.  The plane kernel above hands its rows to different lines, so
+// most of its reads are of the slow kind.  Here a wave owns sixteen
+// consecutive lines b0 .. b0+15 of ONE direction m, and its four rows are the
+// four 16-byte planes of those lines (E = 16 floats): at step t every row reads
+// entries kCW*t + s_t + j, j = lane & 15, with one s_t = (b0 - m t) mod q for
+// the whole wave.  Columns are kCW = 56 entries apart (>= q + 15: the first 15
+// points of a column are stored again after its end, so the sixteen entries
+// never wrap).  Lane l of every row holds the offset of step c0 + l of the
+// current run of sixteen steps, and a step takes it with a DPP row broadcast
+// folded into the address add: one vector instruction besides the four sums.
+// Lines b >= q of the last group of a direction read in bounds and are not
+// stored.  Vertical lines (e = 0, the column x1 = b) read entry kCW*b + t + j
+// from lane j: lanes are kCW + 1 entries apart, an odd stride, so sixteen
+// distinct phases, and the steps are immediate offsets.
+//
+// The panel (4 planes x kCW*q entries, 147 KB at q = 41) leaves no room for a
+// second one, so the workgroup is persistent and prefetches the next item's
+// panel into registers while it sums the current one: HBM latency stays off
+// the critical path without a second LDS buffer.
+namespace iw {
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kE = 16;            // floats of r*p per item (four planes)
+constexpr int kPlanes = kE / 4;
+constexpr int kPF = 7;            // panel chunks each thread prefetches (N0 <= 1792)
+constexpr int kU = 8;             // steps issued together
+constexpr int kGroup = 16;        // lines per wave task
+constexpr int kCW = 56;           // entries per column: >= q + 15, even (see below)
+}  // namespace iw
+
+// Lane n of each sixteen-lane row of v, broadcast to the whole row (DPP row_newbcast).
+template <int N>
+__device__ __forceinline__ int row_bcast(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0x150 + N, 0xf, 0xf, false);
+}
+
+// Eight steps of a sloped line: step H + n reads the byte offset that lane H + n
+// of the row holds in otab.  The eight reads are issued together and waited for
+// once.
+template <int H>
+__device__ __forceinline__ void wave_steps8(float4& acc, const char* vb, int otab) {
+  float4 v[8];
+  v[0] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 0>(otab));
+  v[1] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 1>(otab));
+  v[2] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 2>(otab));
+  v[3] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 3>(otab));
+  v[4] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 4>(otab));
+  v[5] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 5>(otab));
+  v[6] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 6>(otab));
+  v[7] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 7>(otab));
+  __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0): one wait for the eight
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) add4(acc, v[u]);
+}
+
+// Sixteen steps of a sloped line with the reads pipelined: four are in flight
+// while the previous four are summed (same registers as wave_steps8).
+template <int H>
+__device__ __forceinline__ void wave_read4(float4* v, const char* vb, int otab) {
+  v[0] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 0>(otab));
+  v[1] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 1>(otab));
+  v[2] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 2>(otab));
+  v[3] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 3>(otab));
+}
+__device__ __forceinline__ void wave_add4(float4& acc, const float4* v) {
+  add4(acc, v[0]);
+  add4(acc, v[1]);
+  add4(acc, v[2]);
+  add4(acc, v[3]);
+}
+__device__ __forceinline__ void wave_steps16(float4& acc, const char* vb, int otab) {
+  float4 a[4], b[4];
+  wave_read4<0>(a, vb, otab);
+  wave_read4<4>(b, vb, otab);
+  __builtin_amdgcn_s_waitcnt(0xC47F);                // lgkmcnt(4): a has landed
+  __builtin_amdgcn_sched_barrier(0);
+  wave_add4(acc, a);
+  __builtin_amdgcn_sched_barrier(0);
+  wave_read4<8>(a, vb, otab);
+  __builtin_amdgcn_s_waitcnt(0xC47F);
+  __builtin_amdgcn_sched_barrier(0);
+  wave_add4(acc, b);
+  __builtin_amdgcn_sched_barrier(0);
+  wave_read4<12>(b, vb, otab);
+  __builtin_amdgcn_s_waitcnt(0xC47F);
+  __builtin_amdgcn_sched_barrier(0);
+  wave_add4(acc, a);
+  __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0)
+  __builtin_amdgcn_sched_barrier(0);
+  wave_add4(acc, b);
+}
+
+// The steps H .. cnt-1 (cnt - H < 8) of a partial block.
+template <int H>
+__device__ __forceinline__ void wave_steps_tail(float4& acc, const char* vb, int otab, int cnt) {
+#define SMAT_TAIL_STEP(n) \
+  if (H + n < cnt) add4(acc, *reinterpret_cast<const float4*>(vb + row_bcast<H + n>(otab)));
+  SMAT_TAIL_STEP(0) SMAT_TAIL_STEP(1) SMAT_TAIL_STEP(2) SMAT_TAIL_STEP(3)
+  SMAT_TAIL_STEP(4) SMAT_TAIL_STEP(5) SMAT_TAIL_STEP(6)
+#undef SMAT_TAIL_STEP
+}
+
+static int64_t wave_plane_entries(int q) {
+  return ((int64_t)iw::kCW * q + 15) / 16 * 16;
+}
+static int64_t wave_lds_bytes(int q) {
+  return iw::kPlanes * wave_plane_entries(q) * 16 + (((int64_t)q * (q + 1) * 2 + 15) & ~15);
+}
+
+template <bool HasG>
+__global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
+    const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
+    int q, float* __restrict__ U, int N0, int B, int64_t rp, int nslices, int64_t total,
+    int64_t per_xcd, int plane) {
+  using namespace iw;
+  extern __shared__ float4 smem[];
+  const int W = q + 15;
+  const int nlines = q * (q + 1);
+  short* line_type = reinterpret_cast<short*>(smem + (size_t)kPlanes * plane);
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wv = __builtin_amdgcn_readfirstlane(wave_id());
+
+  const int xcd = blockIdx.x % inc::kXCD;
+  const int64_t nk = gridDim.x / inc::kXCD;
+  const int64_t first = (int64_t)xcd * per_xcd + blockIdx.x / inc::kXCD;
+  const int64_t end = min<int64_t>(total, (int64_t)(xcd + 1) * per_xcd);
+  if (first >= end) return;
+
+  for (int c = tid; c < nlines; c += kThreads) line_type[c] = -1;
+  __syncthreads();
+  for (int h = tid; h < B; h += kThreads) {
+    const int c = code[h];
+    if (c >= 0 && c < nlines) line_type[c] = (short)h;
+  }
+
+  // Panel chunk u of this thread: point x = idx >> 2, plane k = idx & 3, stored
+  // at entry W*x1 + x0 of plane k and again every q entries up to W.
+  // Chunk u is point x = tid/4 + u*kThreads/4: its F offset is src0 + u*src_step
+  // (N0 * rp < 2^31, checked on the host); its LDS entry and the number of
+  // copies (entries x0, x0 + q, ... < W) are packed as entry | copies << 24.
+  const int kx = tid & 3;                            // the plane of every chunk of this thread
+  const int src0 = (tid >> 2) * (int)rp + 4 * kx;
+  const int src_step = (kThreads / 4) * (int)rp;
+  int dst[kPF];
+#pragma unroll
+  for (int u = 0; u < kPF; ++u) {
+    const int x = (tid + kThreads * u) >> 2;
+    const int x0 = x / q, x1 = x - x0 * q;
+    const int ncopy = x < N0 ? (W - x0 + q - 1) / q : 0;
+    dst[u] = (kx * plane + kCW * x1 + x0) | (ncopy << 24);
+  }
+  float4 pf[kPF];
+  auto prefetch = [&](int64_t item) {
+    const int64_t b = item / nslices;
+    const int64_t e0 = (item - b * nslices) * kE;
+    const float* Fb = F + b * (int64_t)N0 * rp + e0 + src0;
+    const bool in = e0 + 4 * kx < rp;
+#pragma unroll
+    for (int u = 0; u < kPF; ++u)
+      pf[u] = ((dst[u] >> 24) > 0 && in)
+                  ? *reinterpret_cast<const float4*>(Fb + (int64_t)u * src_step)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  prefetch(first);
+
+  const int j = lane & 15, kpl = lane >> 4;
+  const float inv_q = 1.0f / (float)q;
+  const int P = (q + kGroup - 1) / kGroup;           // groups per direction
+  const int G = (q + 1) * P;
+  const char* pbase = reinterpret_cast<const char*>(smem) + (size_t)kpl * plane * 16;
+
+  for (int64_t item = first; item < end; item += nk) {
+#pragma unroll
+    for (int u = 0; u < kPF; ++u) {
+      const int e = dst[u] & 0xffffff, nc = dst[u] >> 24;
+      for (int c = 0; c < nc; ++c) smem[e + c * q] = pf[u];
+    }
+    lds_barrier();                                   // panel (and line table) complete
+    const int64_t b = item / nslices;
+    const int64_t e0 = (item - b * nslices) * kE;
+    const bool live = e0 + 4 * kpl < rp;
+    float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (HasG && live) g = *reinterpret_cast<const float4*>(Fg + b * rp + e0 + 4 * kpl);
+    if (item + nk < end) prefetch(item + nk);        // lands while this item is summed
+    float* Ub = U + b * (int64_t)B * rp + e0 + 4 * kpl;
+
+    for (int grp = wv; grp < G; grp += kWaves) {
+      const int dir = grp / P;
+      const int b0 = (grp - dir * P) * kGroup;
+      const int bl = b0 + j;
+      const bool valid = bl < q;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      int lc;
+      if (dir < q) {
+        // Step t reads entry kCW*t + s_t + j, s_t = (b0 + (q - m) t) mod q.  Lane l
+        // of every row holds the byte offset of step c0 + l of the current run of
+        // sixteen steps; each step broadcasts its lane within the row (DPP) into
+        // the address add, so a step costs one vector add besides the sums.
+        const int m = dir;
+        lc = (m + 1) * q + bl;
+        const char* vb = pbase + 16 * j;
+        for (int c0 = 0; c0 < q; c0 += 16) {
+          const int t = c0 + j;
+          const int v = b0 + (q - m) * t;            // < 2^24: exact in float
+          int r = v - q * (int)((float)v * inv_q);
+          r += r < 0 ? q : 0;
+          r -= r >= q ? q : 0;
+          const int otab = 16 * (kCW * t + r);
+          if (c0 + 16 <= q) {
+            wave_steps16(acc, vb, otab);
+          } else if (c0 + 8 <= q) {
+            wave_steps8<0>(acc, vb, otab);
+            if (c0 + 8 < q) wave_steps_tail<8>(acc, vb, otab, q - c0);
+          } else {
+            wave_steps_tail<0>(acc, vb, otab, q - c0);
+          }
+        }
+      } else {
+        lc = bl;
+        const int col = valid ? bl : (bl >= kGroup ? bl - kGroup : 0);
+        const char* vb = pbase + 16 * (kCW * col + j);
+        int t = 0;
+        for (; t + kU <= q; t += kU) {
+          float4 v[kU];
+#pragma unroll
+          for (int u = 0; u < kU; ++u) v[u] = *reinterpret_cast<const float4*>(vb + 16 * (t + u));
+          __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0)
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < kU; ++u) add4(acc, v[u]);
+        }
+        for (; t < q; ++t) add4(acc, *reinterpret_cast<const float4*>(vb + 16 * t));
+      }
+      const int h = valid ? line_type[lc] : -1;
+      if (h >= 0 && live) {
+        if (HasG) add4(acc, g);
+        *reinterpret_cast<float4*>(Ub + (int64_t)h * rp) = acc;
+      }
+    }
+    lds_barrier();                                   // every wave is done with the panel
+  }
+}
+
+static bool wave_kernel_fits(int q, int N0, int64_t rp) {
+  return q + 15 <= iw::kCW && (int64_t)N0 * 4 <= (int64_t)iw::kPF * iw::kThreads &&
+         (int64_t)N0 * rp < (1ll << 31) &&
+         wave_lds_bytes(q) <= inc::kPlaneLdsBudget && q >= 2 && q * (q + 1) < 32768;
+}
+
+static int launch_wave(const float* F, const float* F_glob, const int* code, int q, float* U,
+                       int nb, int N0, int B, int64_t rp, hipStream_t stream) {
+  using namespace iw;
+  const int nslices = (int)((rp + kE - 1) / kE);
+  const int64_t total = (int64_t)nb * nslices;
+  int dev = 0, ncu = 256;
+  (void)hipGetDevice(&dev);
+  (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  const int64_t per_xcd = (total + inc::kXCD - 1) / inc::kXCD;
+  const int64_t per_xcd_wgs = std::max<int64_t>(1, std::min<int64_t>(ncu / inc::kXCD, per_xcd));
+  const unsigned grid = (unsigned)(per_xcd_wgs * inc::kXCD);
+  const int plane = (int)wave_plane_entries(q);
+  const size_t smem = (size_t)wave_lds_bytes(q);
+  static bool attr_set[2] = {false, false};
+  auto kern = F_glob ? incidence_wave_kernel<true> : incidence_wave_kernel<false>;
+  if (!attr_set[F_glob ? 1 : 0]) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              inc::kPlaneLdsBudget);
+    attr_set[F_glob ? 1 : 0] = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, q, U, N0,
+                     B, rp, nslices, total, per_xcd, plane);
+  return launch_status("smat_incidence_plane");
+}
+
+// ---------------------------------------------------------------------------
 // L2 kernel
 // ---------------------------------------------------------------------------
 
@@ -458,6 +741,15 @@ int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int
   return launch_status("smat_incidence");
 }
 
+static int plane_mode_env() {
+  static int mode = -1;
+  if (mode < 0) {
+    const char* s = getenv("SMAT_INCIDENCE_PLANE");
+    mode = (s && s[0] == 'o') ? 1 : 0;   // "old": the line-per-lane plane kernel
+  }
+  return mode;
+}
+
 int incidence_plane_dispatch(const float* F, const float* F_glob, const int* code, int q,
                              float* U, int nb, int N0, int B, int64_t rp, hipStream_t stream) {
   if (nb == 0 || B == 0 || rp == 0) return SMAT_OK;
@@ -468,6 +760,8 @@ int incidence_plane_dispatch(const float* F, const float* F_glob, const int* cod
               "(q=%d N0=%d rp=%lld)", q, N0, (long long)rp);
     return SMAT_EUNSUPPORTED;
   }
+  if (wave_kernel_fits(q, N0, rp) && plane_mode_env() == 0)
+    return launch_wave(F, F_glob, code, q, U, nb, N0, B, rp, stream);
   // Two workgroups per CU at E = 8 (one stages its panel while the other sums)
   // measured ahead of one at E = 16; wider panels fall back to one per CU.
   const int64_t entries = (int64_t)q * (q + 15);

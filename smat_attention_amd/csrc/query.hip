@@ -327,24 +327,28 @@ static int launch_query_lists(const void* phi, const float* U, float* Y, const i
   return launch_status("smat_query_lists");
 }
 
+static int launch_query_stream(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R, int B, int64_t q_sb, int64_t q_st,
+                               int64_t y_sb, int64_t y_st, hipStream_t stream) {
+  int dev = 0, ncu = 256;
+  (void)hipGetDevice(&dev);
+  (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  const int64_t nitems = (int64_t)nb * B;
+  const unsigned grid = (unsigned)std::min<int64_t>(nitems, (int64_t)ncu);
+  if (dtype == SMAT_BF16)
+    hipLaunchKernelGGL(query_stream_kernel<bf16>, dim3(grid), dim3(qs::kThreads), 0, stream,
+                       (const bf16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st);
+  else
+    hipLaunchKernelGGL(query_stream_kernel<f16>, dim3(grid), dim3(qs::kThreads), 0, stream,
+                       (const f16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st);
+  return launch_status("smat_query");
+}
+
 int query_dispatch(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R, int B,
                    int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
                    hipStream_t stream) {
   if (nb == 0 || T_R == 0 || B == 0) return SMAT_OK;
-  if (query_stream_ok(dtype, phi, U, Y, T_R, B, r, p, q_sb, q_st, y_sb, y_st)) {
-    int dev = 0, ncu = 256;
-    (void)hipGetDevice(&dev);
-    (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
-    const int64_t nitems = (int64_t)nb * B;
-    const unsigned grid = (unsigned)std::min<int64_t>(nitems, (int64_t)ncu);
-    if (dtype == SMAT_BF16)
-      hipLaunchKernelGGL(query_stream_kernel<bf16>, dim3(grid), dim3(qs::kThreads), 0, stream,
-                         (const bf16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st);
-    else
-      hipLaunchKernelGGL(query_stream_kernel<f16>, dim3(grid), dim3(qs::kThreads), 0, stream,
-                         (const f16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st);
-    return launch_status("smat_query");
-  }
+  if (query_stream_ok(dtype, phi, U, Y, T_R, B, r, p, q_sb, q_st, y_sb, y_st))
+    return launch_query_stream(dtype, phi, U, Y, nb, T_R, B, q_sb, q_st, y_sb, y_st, stream);
   switch (dtype) {
     case SMAT_BF16:
       return launch_query<bf16>(phi, U, Y, nb, T_R, B, r, p, q_sb, q_st, y_sb, y_st, stream);

@@ -119,17 +119,25 @@ def test_incidence(T, d):
     assert _rel(U2, ref) < 1e-6
 
 
-@pytest.mark.parametrize("T,n_P", [(2048, 0), (32768, 0), (131072, 0), (2048, 16)])
-def test_incidence_generated_lines(T, n_P):
-    _say("incidence, d=3 lines generated in-kernel", T, n_P)
-    spec = A.to_device(build_mask(T, 3, chunk=128, n_P=n_P), DEV)
+@pytest.mark.parametrize("T,n_P,rp,glob", [
+    (2048, 0, (32, 33), True), (32768, 0, (128, 129), True), (131072, 0, (128, 129), True),
+    (2048, 16, (32, 33), True), (131072, 0, (128, 129), False), (1024, 0, (8, 9), False),
+    (512, 0, (4, 7), True)])
+def test_incidence_generated_lines(T, n_P, rp, glob):
+    # r*p = 72 and 28 leave a partial last 16-float slice
+    _say("incidence, d=3 lines generated in-kernel", T, n_P, rp, glob)
+    spec = A.to_device(build_mask(T, 3, chunk=128 if T >= 2048 else 64, n_P=n_P), DEV)
     assert spec.plane_code_t is not None
     g = torch.Generator().manual_seed(8)
-    nb, r, p = (1, 128, 129) if T >= 32768 else (2, 32, 33)
+    r, p = rp
+    nb = 1 if T >= 32768 else 2
     F = torch.randn(nb, spec.N0, r, p, generator=g)
     Fg = torch.randn(nb, r, p, generator=g)
-    U = K.incidence_plane(F.to(DEV), spec.plane_code_t, spec.q, F_glob=Fg.to(DEV))
-    ref = O.apply_incidence(F.double(), spec) + Fg.double().unsqueeze(1)
+    U = K.incidence_plane(F.to(DEV), spec.plane_code_t, spec.q,
+                          F_glob=Fg.to(DEV) if glob else None)
+    ref = O.apply_incidence(F.double(), spec)
+    if glob:
+        ref = ref + Fg.double().unsqueeze(1)
     assert _rel(U, ref) < 1e-6
 
 
@@ -360,6 +368,23 @@ def test_forward_long_prefill_d3_bf16_T32768():
     assert _rel(sub, out[:2]) < 1e-6
     again = A.smat_attention(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), spec)
     assert torch.equal(again, out)       # and a repeated launch is bit-identical
+
+
+def test_forward_long_prefill_d3_bf16_T131072():
+    """The benchmark shape (B=1, H=8, head_dim=128, d=3, T=131072, bf16): head 0 vs
+    the oracle, and the fused call against the stage-by-stage path."""
+    _say("forward T=131072 d=3 nb=8 hd=128 bf16")
+    T = 131072
+    spec = build_mask(T, 3, chunk=128)
+    Phi, Psi, Vb = _feats(8, T, 128, torch.bfloat16, seed=0, k_scale=128 ** -0.5)
+    out = A.smat_attention(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), spec)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _check_forward(spec, Phi[:1], Psi[:1], Vb[:1], dt=torch.bfloat16, label="T=131072 d=3 head 0")
+    staged = A.smat_attention(Phi[:2].to(DEV), Psi[:2].to(DEV), Vb[:2].to(DEV), spec,
+                              return_parts=True)
+    staged = staged[0] if isinstance(staged, tuple) else staged
+    assert _rel(staged, out[:2]) < 1e-5      # one fused call == the stage-by-stage path
 
 
 def test_exact_non_influence():
