@@ -444,31 +444,33 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
 
   // Panel chunk u of this thread: point x = idx >> 2, plane k = idx & 3, stored
   // at entry W*x1 + x0 of plane k and again every q entries up to W.
-  // Chunk u is point x = tid/4 + u*kThreads/4: its F offset is src0 + u*src_step
-  // (N0 * rp < 2^31, checked on the host); its LDS entry and the number of
-  // copies (entries x0, x0 + q, ... < W) are packed as entry | copies << 24.
-  const int kx = tid & 3;                            // the plane of every chunk of this thread
-  const int src0 = (tid >> 2) * (int)rp + 4 * kx;
-  const int src_step = (kThreads / 4) * (int)rp;
-  int dst[kPF];
+  // Chunk u of this thread: plane kx = row of the lane, and slot
+  // ps = 16 * (wave + 16 u) + (lane & 15) in column-major point order
+  // (x1 = ps / q, x0 = ps mod q), so the sixteen lanes of a row write sixteen
+  // consecutive LDS entries of one plane.  Its F offset (N0 * rp < 2^31,
+  // checked on the host) is x*rp + 4*kx for the point x = x0*q + x1; its LDS
+  // entry and the number of copies (entries x0, x0 + q, ... < W) are packed as
+  // entry | copies << 24.
+  const int kx = (tid >> 4) & 3;
+  int dst[kPF], src[kPF];
 #pragma unroll
   for (int u = 0; u < kPF; ++u) {
-    const int x = (tid + kThreads * u) >> 2;
-    const int x0 = x / q, x1 = x - x0 * q;
-    const int ncopy = x < N0 ? (W - x0 + q - 1) / q : 0;
+    const int ps = 16 * ((tid >> 6) + kWaves * u) + (tid & 15);
+    const int x1 = ps / q, x0 = ps - x1 * q;
+    const int ncopy = ps < N0 ? (W - x0 + q - 1) / q : 0;
     dst[u] = (kx * plane + kCW * x1 + x0) | (ncopy << 24);
+    src[u] = (x0 * q + x1) * (int)rp + 4 * kx;
   }
   float4 pf[kPF];
   auto prefetch = [&](int64_t item) {
     const int64_t b = item / nslices;
     const int64_t e0 = (item - b * nslices) * kE;
-    const float* Fb = F + b * (int64_t)N0 * rp + e0 + src0;
+    const float* Fb = F + b * (int64_t)N0 * rp + e0;
     const bool in = e0 + 4 * kx < rp;
 #pragma unroll
     for (int u = 0; u < kPF; ++u)
-      pf[u] = ((dst[u] >> 24) > 0 && in)
-                  ? *reinterpret_cast<const float4*>(Fb + (int64_t)u * src_step)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
+      pf[u] = ((dst[u] >> 24) > 0 && in) ? *reinterpret_cast<const float4*>(Fb + src[u])
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
   };
   prefetch(first);
 
@@ -476,6 +478,8 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   const float inv_q = 1.0f / (float)q;
   const int P = (q + kGroup - 1) / kGroup;           // groups per direction
   const int G = (q + 1) * P;
+  const int dir0 = wv / P, part0 = wv - dir0 * P;
+  const int ddir = kWaves / P, dpart = kWaves - ddir * P;
   const char* pbase = reinterpret_cast<const char*>(smem) + (size_t)kpl * plane * 16;
 
   for (int64_t item = first; item < end; item += nk) {
@@ -493,9 +497,11 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     if (item + nk < end) prefetch(item + nk);        // lands while this item is summed
     float* Ub = U + b * (int64_t)B * rp + e0 + 4 * kpl;
 
+    // group grp = wv + kWaves*i is part `part` of direction `dir`; both are
+    // advanced without a division (kWaves = P*ddir + dpart)
+    int dir = dir0, part = part0;
     for (int grp = wv; grp < G; grp += kWaves) {
-      const int dir = grp / P;
-      const int b0 = (grp - dir * P) * kGroup;
+      const int b0 = part * kGroup;
       const int bl = b0 + j;
       const bool valid = bl < q;
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -508,13 +514,15 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
         const int m = dir;
         lc = (m + 1) * q + bl;
         const char* vb = pbase + 16 * j;
+        // lane j: s = s_{c0+j}, advanced by d16 = -16m mod q per run
+        const int v = b0 + (q - m) * j;              // < 2^24: exact in float
+        int sj = v - q * (int)((float)v * inv_q);
+        sj += sj < 0 ? q : 0;
+        sj -= sj >= q ? q : 0;
+        const unsigned d16 = (unsigned)((16 * (q - m)) % q);
+        int colpart = 16 * kCW * j;
         for (int c0 = 0; c0 < q; c0 += 16) {
-          const int t = c0 + j;
-          const int v = b0 + (q - m) * t;            // < 2^24: exact in float
-          int r = v - q * (int)((float)v * inv_q);
-          r += r < 0 ? q : 0;
-          r -= r >= q ? q : 0;
-          const int otab = 16 * (kCW * t + r);
+          const int otab = colpart + 16 * sj;
           if (c0 + 16 <= q) {
             wave_steps16(acc, vb, otab);
           } else if (c0 + 8 <= q) {
@@ -523,6 +531,9 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
           } else {
             wave_steps_tail<0>(acc, vb, otab, q - c0);
           }
+          const unsigned c = (unsigned)sj + d16;
+          sj = (int)min(c, c - (unsigned)q);
+          colpart += 16 * 16 * kCW;
         }
       } else {
         lc = bl;
@@ -544,6 +555,12 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
       if (h >= 0 && live) {
         if (HasG) add4(acc, g);
         *reinterpret_cast<float4*>(Ub + (int64_t)h * rp) = acc;
+      }
+      part += dpart;
+      dir += ddir;
+      if (part >= P) {
+        part -= P;
+        ++dir;
       }
     }
     lds_barrier();                                   // every wave is done with the panel
