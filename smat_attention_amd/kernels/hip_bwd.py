@@ -39,7 +39,10 @@ from ._lib import DTYPE_CODE, call, ptr, stream_of
 from . import hip_fwd as _hip
 
 __all__ = ["smat_attention_grad", "SmatAttentionFunction", "transposed_incidence",
-           "patch", "unpatch", "patched"]
+           "chunk_local", "pool", "incidence", "patch", "unpatch", "patched"]
+
+# the forward kernels as imported, before patch() swaps the module attributes
+_FWD = {"chunk_local": _hip.chunk_local, "pool": _hip.pool, "incidence": _hip.incidence}
 
 def _code(t):
     return DTYPE_CODE[t.dtype]
@@ -253,20 +256,180 @@ class SmatAttentionFunction(torch.autograd.Function):
                 dg.to(g.dtype) if need_dg else None, None, None)
 
 
-# The reference's patch()/unpatch() make its kernel path differentiable
-# (triton_bwd.py:334-346); without them backend="auto" silently drops the
-# kernels' gradients.  Here smat_attention is differentiable whenever an input
-# requires grad, so these only record the request, for callers that use them.
-_PATCHED = [False]
+# ---------------------------------------------------------------------------
+# The three kernels as autograd Functions (triton_bwd.py:154-316).  Products
+# run on smat_bgemm (fp32 MFMA, fp32 accumulation) from the stored inputs.
+# ---------------------------------------------------------------------------
+
+class _ChunkLocalFn(torch.autograd.Function):
+    """``out = Phi_c Sin + tril(Phi_c Psi_c^T) Vb_c`` per chunk (triton_bwd.py:154-197):
+    dPhi = dO Sin^T + tril(dO Vb^T) Psi,  dPsi = tril(dO Vb^T)^T Phi,
+    dVb = tril(Phi Psi^T)^T dO,  dSin = Phi^T dO."""
+
+    @staticmethod
+    def forward(ctx, Phi_c, Psi_c, Vb_c, Sin):
+        out = _FWD["chunk_local"](Phi_c, Psi_c, Vb_c, Sin)
+        ctx.save_for_backward(Phi_c, Psi_c, Vb_c, Sin)
+        return out
+
+    @staticmethod
+    def backward(ctx, dOut):
+        Phi_c, Psi_c, Vb_c, Sin = ctx.saved_tensors
+        nb, nc, C, R = Phi_c.shape
+        P = Vb_c.shape[-1]
+        dev = Phi_c.device
+        q, k, v = Phi_c.contiguous(), Psi_c.contiguous(), Vb_c.contiguous()
+        s_ = Sin.float().contiguous()
+        do = dOut.float().contiguous()
+        CR, CP, RP, CC = C * R, C * P, R * P, C * C
+        cr, cp_, cc, rp_ = (nc * CR, CR, R, 1), (nc * CP, CP, P, 1), (nc * CC, CC, C, 1), \
+            (nc * RP, RP, P, 1)
+        A = torch.empty(nb, nc, C, C, device=dev, dtype=torch.float32)
+        dA = torch.empty_like(A)
+        _bgemm(q, k, A, M=C, N=C, K=R, n1=nb, n2=nc, a=cr, b=(nc * CR, CR, 1, R), c=cc, mask=1)
+        _bgemm(do, v, dA, M=C, N=C, K=P, n1=nb, n2=nc, a=cp_, b=(nc * CP, CP, 1, P), c=cc,
+               mask=1)
+        dq = torch.empty(nb, nc, C, R, device=dev, dtype=torch.float32)
+        dk = torch.empty_like(dq)
+        dv = torch.empty(nb, nc, C, P, device=dev, dtype=torch.float32)
+        ds = torch.empty(nb, nc, R, P, device=dev, dtype=torch.float32)
+        _bgemm(do, s_, dq, M=C, N=R, K=P, n1=nb, n2=nc, a=cp_, b=(nc * RP, RP, 1, P), c=cr)
+        _bgemm(dA, k, dq, M=C, N=R, K=C, n1=nb, n2=nc, a=cc, b=cr, c=cr, beta=1)
+        _bgemm(dA, q, dk, M=C, N=R, K=C, n1=nb, n2=nc, a=(nc * CC, CC, 1, C), b=cr, c=cr)
+        _bgemm(A, do, dv, M=C, N=P, K=C, n1=nb, n2=nc, a=(nc * CC, CC, 1, C), b=cp_, c=cp_)
+        _bgemm(q, do, ds, M=R, N=P, K=C, n1=nb, n2=nc, a=(nc * CR, CR, 1, R), b=cp_, c=rp_)
+        return (dq.to(Phi_c.dtype), dk.to(Psi_c.dtype), dv.to(Vb_c.dtype), ds.to(Sin.dtype))
+
+
+class _PoolFn(torch.autograd.Function):
+    """``F_x = sum_j Psi_j^T Vb_j`` over landmark tokens j = n_P + x + s*N0
+    (triton_bwd.py:240-271): dPsi_j = dF_x Vb_j, dVb_j = dF_x^T Psi_j; tokens
+    outside [n_P, n) get zero gradient."""
+
+    @staticmethod
+    def forward(ctx, Psi, Vb, n_P, n, N0):
+        F = _FWD["pool"](Psi, Vb, n_P, n, N0)
+        ctx.save_for_backward(Psi, Vb)
+        ctx.dims = (n_P, n, N0)
+        return F
+
+    @staticmethod
+    def backward(ctx, dF):
+        Psi, Vb = ctx.saved_tensors
+        n_P, n, N0 = ctx.dims
+        nb, T, R = Psi.shape
+        P = Vb.shape[-1]
+        Ps, Vv = Psi.contiguous(), Vb.contiguous()
+        dFc = dF.float().contiguous()
+        dPsi = torch.zeros(nb, T, R, device=Psi.device, dtype=torch.float32)
+        dVb = torch.zeros(nb, T, P, device=Psi.device, dtype=torch.float32)
+        rp = R * P
+        gq, grem = divmod(n - n_P, N0)
+        for lo, hi, cnt in ((0, grem, gq + 1), (grem, N0, gq)):
+            if hi <= lo or cnt <= 0:
+                continue
+            tok0 = n_P + lo
+            _bgemm(Vv, dFc, dPsi, M=cnt, N=R, K=P, n1=nb, n2=hi - lo,
+                   a=(T * P, P, N0 * P, 1), b=(N0 * rp, rp, 1, P), c=(T * R, R, N0 * R, 1),
+                   a_off=tok0 * P, b_off=lo * rp, c_off=tok0 * R)
+            _bgemm(Ps, dFc, dVb, M=cnt, N=P, K=R, n1=nb, n2=hi - lo,
+                   a=(T * R, R, N0 * R, 1), b=(N0 * rp, rp, P, 1), c=(T * P, P, N0 * P, 1),
+                   a_off=tok0 * R, b_off=lo * rp, c_off=tok0 * P)
+        return dPsi.to(Psi.dtype), dVb.to(Vb.dtype), None, None, None
+
+
+_TRANSPOSE_CACHE = {}
+
+
+def _point_planes(plane_pts, N0):
+    """``(N0, D)`` table of the row types through each point (ascending), from
+    the ``(B, deg)`` table (triton_bwd.py:281-297); D must be the same for every
+    point."""
+    key = (plane_pts.data_ptr(), tuple(plane_pts.shape), N0)
+    hit = _TRANSPOSE_CACHE.get(key)
+    if hit is not None:
+        return hit
+    B, deg = plane_pts.shape
+    pts = plane_pts.reshape(-1).long()
+    rows = torch.arange(B, device=plane_pts.device).repeat_interleave(deg)
+    order = torch.argsort(pts * B + rows)
+    pts, rows = pts[order], rows[order]
+    counts = torch.bincount(pts, minlength=N0)
+    if int(counts.min()) != int(counts.max()):
+        raise ValueError("incidence transpose is not uniform; the table kernel needs a "
+                         "constant number of row types per point")
+    table = rows.reshape(N0, int(counts[0])).to(torch.int32).contiguous()
+    _TRANSPOSE_CACHE[key] = table
+    return table
+
+
+class _IncidenceFn(torch.autograd.Function):
+    """``U = C F`` (triton_bwd.py:300-316): dF = C^T dU, the same kernel over the
+    transposed table."""
+
+    @staticmethod
+    def forward(ctx, F, plane_pts, B):
+        U = _FWD["incidence"](F, plane_pts, B)
+        ctx.table = _point_planes(plane_pts, F.shape[1])
+        ctx.N0 = F.shape[1]
+        ctx.in_dtype = F.dtype
+        return U
+
+    @staticmethod
+    def backward(ctx, dU):
+        dF = _FWD["incidence"](dU.contiguous().float(), ctx.table, ctx.N0)
+        return dF.to(ctx.in_dtype), None, None
+
+
+def chunk_local(Phi_c, Psi_c, Vb_c, Sin):
+    """Differentiable :func:`hip_fwd.chunk_local` (triton_bwd.py:319-320)."""
+    return _ChunkLocalFn.apply(Phi_c, Psi_c, Vb_c, Sin)
+
+
+def pool(Psi, Vb, n_P, n, N0, *, F_glob=None):
+    """Differentiable :func:`hip_fwd.pool` (triton_bwd.py:323-324).  With
+    ``F_glob`` the global channel is filled as by the forward kernel; that
+    output buffer carries no gradient."""
+    if F_glob is not None:
+        if torch.is_grad_enabled() and (Psi.requires_grad or Vb.requires_grad):
+            raise NotImplementedError("pool: gradients through F_glob are not provided; use "
+                                      "smat_attention, whose backward covers the channel")
+        return _FWD["pool"](Psi, Vb, n_P, n, N0, F_glob=F_glob)
+    return _PoolFn.apply(Psi, Vb, n_P, n, N0)
+
+
+def incidence(F, plane_pts, B):
+    """Differentiable :func:`hip_fwd.incidence` (triton_bwd.py:327-328)."""
+    return _IncidenceFn.apply(F, plane_pts, B)
+
+
+# patch() swaps the differentiable wrappers into the kernel module that the
+# schedule dispatches through (and its reference-named alias), as
+# triton_bwd.py:334-346 does for its Triton table; unpatch() restores the
+# plain kernels.  smat_attention itself is differentiable either way: with an
+# input that requires grad it runs as one autograd node (SmatAttentionFunction).
+_ORIG = {}
+
+
+def _kernel_modules():
+    from . import triton_fwd as _alias
+    return (_hip, _alias)
 
 
 def patch():
-    _PATCHED[0] = True
+    if _ORIG:
+        return
+    for mod in _kernel_modules():
+        for name, fn in (("chunk_local", chunk_local), ("pool", pool), ("incidence", incidence)):
+            _ORIG[(mod.__name__, name)] = (mod, getattr(mod, name))
+            setattr(mod, name, fn)
 
 
 def unpatch():
-    _PATCHED[0] = False
+    for (mod_name, name), (mod, fn) in _ORIG.items():
+        setattr(mod, name, fn)
+    _ORIG.clear()
 
 
 def patched() -> bool:
-    return _PATCHED[0]
+    return bool(_ORIG)

@@ -71,3 +71,24 @@ def test_workspace_query_arithmetic():
     # d = 1 splits the single long progression: partial buffers appear
     assert _lib.query("smat_pool_workspace_bytes", 8, 0, 65536, 1, r, p) > 0
     assert _lib.query("smat_pool_workspace_bytes", 8, 0, 65536, 1681, r, p) == 0
+
+
+def test_patch_swaps_the_kernel_table():
+    """triton_bwd.patch()/unpatch() (triton_bwd.py:334-346): the differentiable
+    wrappers replace chunk_local/pool/incidence in the kernel module and its
+    reference-named alias, and are restored after."""
+    from smat_attention_amd.kernels import hip_bwd, hip_fwd, triton_bwd, triton_fwd
+    orig = (hip_fwd.chunk_local, hip_fwd.pool, hip_fwd.incidence)
+    triton_bwd.patch()
+    try:
+        assert hip_bwd.patched()
+        for mod in (hip_fwd, triton_fwd):
+            assert mod.chunk_local is hip_bwd.chunk_local
+            assert mod.pool is hip_bwd.pool
+            assert mod.incidence is hip_bwd.incidence
+        triton_bwd.patch()                     # idempotent
+    finally:
+        triton_bwd.unpatch()
+    assert not hip_bwd.patched()
+    assert (hip_fwd.chunk_local, hip_fwd.pool, hip_fwd.incidence) == orig
+    assert (triton_fwd.chunk_local, triton_fwd.pool, triton_fwd.incidence) == orig

@@ -115,3 +115,80 @@ def test_forward_unchanged_when_grad_is_recorded():
     tracked = A.smat_attention(*xs, spec)
     assert tracked.requires_grad
     assert (tracked.detach() - plain).abs().max().item() <= 1e-6 * plain.abs().max().item()
+
+
+# ---------------------------------------------------------------------------
+# The three kernels as autograd Functions, and patch() (triton_bwd.py:154-346)
+# ---------------------------------------------------------------------------
+
+def _fn_grads(fn, inputs, w):
+    xs = [t.detach().clone().requires_grad_(True) for t in inputs]
+    out = fn(*xs)
+    (out * w.to(out.dtype)).sum().backward()
+    return out.detach(), [x.grad.detach() for x in xs]
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_chunk_local_function_gradients(dt):
+    from smat_attention_amd.kernels import hip_bwd as Bw
+    _say("chunk_local autograd Function", dt)
+    g = torch.Generator().manual_seed(21)
+    nb, nc, C, r, p = 2, 3, 64, 32, 33
+    Phi = (torch.rand(nb, nc, C, r, generator=g) + 0.5).to(dt)
+    Psi = (torch.rand(nb, nc, C, r, generator=g) + 0.5).to(dt)
+    Vb = torch.randn(nb, nc, C, p, generator=g).to(dt)
+    Sin = torch.randn(nb, nc, r, p, generator=g)
+    w = torch.randn(nb, nc, C, p, generator=g)
+    _, got = _fn_grads(Bw.chunk_local, [t.to(DEV) for t in (Phi, Psi, Vb, Sin)], w.to(DEV))
+    _, ref = _fn_grads(lambda a, b, c, d: O.chunk_local(a, b, c, d, acc=torch.float64),
+                       [t.double() for t in (Phi, Psi, Vb, Sin)], w.double())
+    tol = 1e-5 if dt == torch.float32 else 2e-2
+    for name, a, b in zip(("dPhi", "dPsi", "dVb", "dSin"), got, ref):
+        assert a.dtype == (dt if name != "dSin" else torch.float32)
+        err = _rel(a.cpu(), b) if dt == torch.float32 else _nrel(a.cpu(), b)
+        assert err < tol, (name, err)
+
+
+@pytest.mark.parametrize("T,d,n_P", [(2048, 3, 0), (2048, 3, 16), (2000, 2, 0), (4096, 4, 0)])
+def test_pool_and_incidence_function_gradients(T, d, n_P):
+    from smat_attention_amd.kernels import hip_bwd as Bw
+    _say("pool / incidence autograd Functions", T, d, n_P)
+    spec = A.to_device(build_mask(T, d, chunk=128, n_P=n_P), DEV)
+    g = torch.Generator().manual_seed(22)
+    nb, r, p = 2, 32, 33
+    Psi = torch.rand(nb, T, r, generator=g) + 0.5
+    Vb = torch.randn(nb, T, p, generator=g)
+    wF = torch.randn(nb, spec.N0, r, p, generator=g)
+    _, got = _fn_grads(lambda a, b: Bw.pool(a, b, spec.n_P, spec.n, spec.N0),
+                       [Psi.to(DEV), Vb.to(DEV)], wF.to(DEV))
+    _, ref = _fn_grads(lambda a, b: O.pool_profiles(a, b, spec, acc_dtype=torch.float64),
+                       [Psi.double(), Vb.double()], wF.double())
+    for name, a, b in zip(("dPsi", "dVb"), got, ref):
+        assert _rel(a.cpu(), b) < 1e-5, (name, _rel(a.cpu(), b))
+    if not spec.uniform_deg:
+        return
+    F = torch.randn(nb, spec.N0, r, p, generator=g)
+    wU = torch.randn(nb, spec.B, r, p, generator=g)
+    _, got = _fn_grads(lambda f: Bw.incidence(f, spec.plane_pts_t, spec.B), [F.to(DEV)],
+                       wU.to(DEV))
+    _, ref = _fn_grads(lambda f: O.apply_incidence(f, spec), [F.double()], wU.double())
+    assert _rel(got[0].cpu(), ref[0]) < 1e-6
+
+
+def test_patch_makes_the_kernel_table_differentiable():
+    from smat_attention_amd.kernels import hip_bwd as Bw
+    from smat_attention_amd.kernels import hip_fwd as K
+    _say("patch()/unpatch() on the kernel table")
+    spec = A.to_device(build_mask(1024, 3, chunk=128), DEV)
+    Psi = (torch.rand(1, 1024, 16, device=DEV) + 0.5).requires_grad_(True)
+    Vb = torch.randn(1, 1024, 17, device=DEV).requires_grad_(True)
+    assert not K.pool(Psi, Vb, spec.n_P, spec.n, spec.N0).requires_grad
+    Bw.patch()
+    try:
+        F = K.pool(Psi, Vb, spec.n_P, spec.n, spec.N0)
+        assert F.requires_grad
+        F.sum().backward()
+        assert Psi.grad is not None and torch.isfinite(Psi.grad).all()
+    finally:
+        Bw.unpatch()
+    assert not K.pool(Psi, Vb, spec.n_P, spec.n, spec.N0).requires_grad
