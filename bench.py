@@ -177,6 +177,25 @@ def kernel_table(spec, Phi, Psi, Vb, reps):
     return rows
 
 
+def featurise_bench(nb, T, hd, reps):
+    """Time the feature map and value packing (attention.py:82-106: Phi, the
+    gated Psi and [V, 1] in one launch) on bf16 q, k, v and gate h ~ U[0.5, 1.5),
+    as the reference's bench draws them (bench_prefill.py:189-198); the
+    reference reports this as featurise_ms, outside the prefill time."""
+    import torch
+    from smat_attention_amd import attention as A
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cpu").manual_seed(1)
+    Q, K, V = (torch.randn(nb, T, hd, generator=gen).to(dev, torch.bfloat16) for _ in range(3))
+    h = (torch.rand(nb, T, generator=gen) + 0.5).to(dev, torch.bfloat16)
+    phi = A.make_phi(hd, hd, device=dev, dtype=torch.bfloat16, seed=0)
+    us = Events(torch).time(lambda: A.featurise(Q, K, V, phi, h=h), reps)
+    nbytes = nb * T * 2 * (3 * hd + 2 * hd + (hd + 1) + 1)
+    del Q, K, V, h
+    return {"us": round(us, 1), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes,
+            "config": f"nb={nb} T={T} d_qk=r=d_v={hd} bf16, elu+1 map, key gate"}
+
+
 def useful_flops(spec, nb, T, r, p, C=128):
     """Mask-density-scaled MFMA work of the schedule: causal intra-chunk QK^T and
     AV, Phi Sin, chunk summaries, pooling, type-major query (2 flops per MAC)."""
@@ -367,6 +386,8 @@ def main():
                  "compulsory_bytes": cb},
         "kernels_us": {k: round(v["us"], 1) for k, v in rows.items()},
     }
+    result["featurise"] = featurise_bench(nb, T, hd, args.kernel_reps)
+    log(f"[bench] featurise {result['featurise']}")
     if not args.no_decode:
         del Phi, Psi, Vb, ws, out
         torch.cuda.empty_cache()

@@ -266,6 +266,22 @@ int smat_incidence_complement(const float* F, float* U, int nb, int N0, int B, i
                               void* stream);
 
 /*
+ * Feature map and value packing, src/smat/attention.py:82-106:
+ * Phi = map(Q W^T), Psi = map(K W^T) * h, Vb = [V, 1] in the input dtype,
+ * map = elu(x) + 1 (kind 0) or relu(x) + 1e-3 (kind 1), with torch's rounding
+ * steps (product, map and gate each rounded to the dtype).  Q, K: (nb, T, d_qk)
+ * rows, W: (r, d_qk) contiguous, h: (nb, T) or NULL, V: (nb, T, d_v).
+ * Phi/Psi rows o_st apart, Vb rows vb_st > d_v apart (the pad is not written).
+ * k (with psi) and v (with vb) may be NULL to skip those outputs.
+ * d_qk <= 128, r <= 128.
+ */
+int smat_featurise(int dtype, const void* q, const void* k, const void* v, const void* W,
+                   const void* h, void* phi, void* psi, void* vb, int nb, int T, int d_qk,
+                   int r, int d_v, int kind, int64_t q_sb, int64_t q_st, int64_t k_sb,
+                   int64_t k_st, int64_t v_sb, int64_t v_st, int64_t h_sb, int64_t o_sb,
+                   int64_t o_st, int64_t vb_sb, int64_t vb_st, void* stream);
+
+/*
  * Gram sums over token lists (CSR): G[i] = sum_{j in tokens[offs[i] .. offs[i+1])}
  * psi_j^T vb_j, fp32 (nitems, r, p) contiguous; psi / vb are row matrices with
  * row strides k_st / v_st (sequences flattened: token = sequence * T + t).

@@ -82,8 +82,27 @@ def _acc(x: torch.Tensor, acc_dtype, who: str) -> torch.dtype:
 # feature map (attention.py:82-106)
 # ---------------------------------------------------------------------------
 
+class FeatureMap:
+    """The map ``x -> elu(x W^T) + 1`` (or ``relu(x W^T) + 1e-3``) that
+    :func:`make_phi` returns: callable like the reference's closure
+    (attention.py:82-96), with ``W`` and ``kind`` exposed so :func:`featurise`
+    can run it as one HIP launch.  GPU tensors go through the kernel; CPU
+    tensors through the same torch ops the reference uses."""
+
+    def __init__(self, W: torch.Tensor, kind: str):
+        self.W, self.kind = W, kind
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda:
+            return _hip.featurise(self.W, self.kind, x)[0]
+        y = x @ self.W.T
+        if self.kind == "elu1":
+            return torch.nn.functional.elu(y) + 1.0
+        return torch.nn.functional.relu(y) + 1e-3
+
+
 def make_phi(d_qk: int, r: int, *, kind: str = "elu1", device="cpu",
-             dtype=torch.float32, seed: int = 0) -> Callable:
+             dtype=torch.float32, seed: int = 0) -> FeatureMap:
     """A positive rank-``r`` feature map with ``W ~ randn(r, d_qk)/sqrt(d_qk)``.
 
     ``W`` comes from a seeded CPU generator in float64 and is then cast, as in
@@ -92,19 +111,23 @@ def make_phi(d_qk: int, r: int, *, kind: str = "elu1", device="cpu",
     gen = torch.Generator(device="cpu").manual_seed(seed)
     W = (torch.randn(r, d_qk, generator=gen, dtype=torch.float64)
          / np.sqrt(d_qk)).to(device=device, dtype=dtype)
-    if kind == "elu1":
-        return lambda x: torch.nn.functional.elu(x @ W.T) + 1.0
-    if kind == "relu":
-        return lambda x: torch.nn.functional.relu(x @ W.T) + 1e-3
-    raise ValueError(f"unknown feature map {kind!r}")
+    if kind not in ("elu1", "relu"):
+        raise ValueError(f"unknown feature map {kind!r}")
+    return FeatureMap(W, kind)
 
 
 def featurise(Q, K, V, phi, *, g=None, h=None):
     """``(Q, K, V) -> (Phi, Psi, Vb)`` with the key gate folded into ``Psi``.
 
-    ``Vb = [V, 1]`` is returned as a view whose rows start on 16-byte
-    boundaries (row stride rounded up to 8 elements).
+    With a :class:`FeatureMap` on GPU tensors this is one HIP launch (both
+    maps, the gate and ``[V, 1]``).  ``g`` is accepted and unused, as in the
+    reference (the output gate is applied by :func:`smat_attention`).  Any
+    other callable is the caller's own map and is called as given.  ``Vb`` is
+    returned as a view whose rows start on 16-byte boundaries (row stride
+    rounded up to 8 elements).
     """
+    if isinstance(phi, FeatureMap) and Q.is_cuda:
+        return _hip.featurise(phi.W, phi.kind, Q, K, V, h)
     Phi = phi(Q)
     Psi = phi(K)
     if h is not None:

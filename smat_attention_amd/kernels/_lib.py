@@ -66,6 +66,9 @@ SIGNATURES = {
                           _p, _i64, _p]),
     "smat_direct": (_i, [_i, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64,
                          _p]),
+    "smat_featurise": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,
+                            _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _p]),
     "smat_gram_lists": (_i, [_i, _p, _p, _p, _p, _p, _i, _i, _i, _i64, _i64, _p]),
     "smat_query_lists": (_i, [_i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _p]),
     "smat_cell_hash": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i64, _p]),

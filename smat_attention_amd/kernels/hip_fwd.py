@@ -100,6 +100,59 @@ def validate_table(plane_pts: torch.Tensor, N0: int) -> None:
 # the reference's five functions
 # ---------------------------------------------------------------------------
 
+_FEATURE_KINDS = {"elu1": 0, "relu": 1}
+
+
+def featurise(W, kind: str, Q, K=None, V=None, h=None):
+    """``Phi = map(Q W^T)``, ``Psi = map(K W^T) * h``, ``Vb = [V, 1]`` in one launch
+    (attention.py:82-106).  Returns ``(Phi, Psi, Vb)``, ``None`` for the parts
+    not asked for; ``Vb`` is a view of rows padded to 16 bytes."""
+    who = "featurise"
+    _on_gpu(who, Q, W, K, V, h)
+    for t in (W, K, V, h):
+        if t is not None and t.dtype != Q.dtype:
+            raise TypeError(f"{who}: all inputs must share Q's dtype {Q.dtype}, got {t.dtype}")
+    if kind not in _FEATURE_KINDS:
+        raise ValueError(f"{who}: unknown feature map {kind!r}")
+    code = _code(Q, who)
+    nb, T, dqk = Q.shape
+    r = W.shape[0]
+    if W.shape != (r, dqk):
+        raise ValueError(f"{who}: W is {tuple(W.shape)}, expected ({r}, {dqk})")
+    Wc = W.contiguous()
+    q, q_sb, q_st = _rows3(Q)
+    Phi = torch.empty(nb, T, r, device=Q.device, dtype=Q.dtype)
+    Psi = k = None
+    k_sb = k_st = 0
+    if K is not None:
+        if K.shape != Q.shape:
+            raise ValueError(f"{who}: K is {tuple(K.shape)}, Q is {tuple(Q.shape)}")
+        k, k_sb, k_st = _rows3(K)
+        Psi = torch.empty_like(Phi)
+    Vb = v = None
+    v_sb = v_st = vb_sb = vb_st = 0
+    d_v = 0
+    if V is not None:
+        if V.shape[:2] != Q.shape[:2]:
+            raise ValueError(f"{who}: V is {tuple(V.shape)}, Q is {tuple(Q.shape)}")
+        d_v = V.shape[-1]
+        v, v_sb, v_st = _rows3(V)
+        pad = -(-(d_v + 1) // 8) * 8
+        buf = torch.empty(nb, T, pad, device=V.device, dtype=V.dtype)
+        Vb = buf[..., :d_v + 1]
+        vb_sb, vb_st = buf.stride(0), buf.stride(1)
+    hc = None
+    if h is not None:
+        if K is None or h.shape != Q.shape[:2]:
+            raise ValueError(f"{who}: the key gate h must be ({nb}, {T}) and needs K")
+        hc = h.contiguous()
+    call("smat_featurise", code, q.data_ptr(), ptr(k), ptr(v), Wc.data_ptr(), ptr(hc),
+         Phi.data_ptr(), ptr(Psi), ptr(Vb), nb, T, dqk, r, d_v, _FEATURE_KINDS[kind],
+         q_sb, q_st, k_sb, k_st, v_sb, v_st, hc.stride(0) if hc is not None else 0,
+         Phi.stride(0), Phi.stride(1), vb_sb, vb_st, stream_of(Q))
+    return Phi, Psi, Vb
+
+
 def chunk_local(Phi_c, Psi_c, Vb_c, Sin):
     """``Phi_b Sin_b + (Phi_b Psi_b^T . L_C) Vb_b`` for every chunk, fused.
 

@@ -504,3 +504,53 @@ def test_decode_endpoint():
     for t in range(spec.n, spec.n + 40):
         o = dec.step(Pd[:, t], Sd[:, t], Wd[:, t])
         assert (o - full[:, t]).abs().max().item() < 1e-4 * max(1.0, full[:, t].abs().max().item())
+
+
+# ---------------------------------------------------------------------------
+# featurise (attention.py:82-106) on HIP
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("T,dqk,r,dv,kind,gate", [
+    (1000, 128, 128, 128, "elu1", True), (777, 64, 64, 64, "elu1", False),
+    (130, 32, 48, 7, "relu", True), (64, 40, 16, 33, "elu1", True)])
+def test_featurise(dt, T, dqk, r, dv, kind, gate):
+    """Phi/Psi/Vb of one HIP launch against the oracle's torch featurise on the
+    same inputs.  fp32: relative 1e-5.  16-bit: the product is accumulated in
+    another order than torch's, so a rounded product can land one step away
+    and elu carries that step on: at most 1e-4 of the outputs may differ by
+    more than 2 ulp of the value (2^-7 relative for bf16, 2^-10 for fp16), none
+    by more than 4 %.  A wrong rounding order or gate moves far more.  Vb is an
+    exact copy."""
+    _say("featurise", dt, T, dqk, r, dv, kind, gate)
+    g = torch.Generator().manual_seed(31)
+    nb = 3
+    Q = (torch.randn(nb, T, dqk, generator=g) * 0.5).to(dt)
+    K = (torch.randn(nb, T, dqk, generator=g) * 0.5).to(dt)
+    V = torch.randn(nb, T, dv, generator=g).to(dt)
+    h = (torch.rand(nb, T, generator=g) + 0.5).to(dt) if gate else None
+    phi_ref = O.make_phi(dqk, r, kind=kind, dtype=dt, seed=3)
+    ref = O.featurise(Q, K, V, phi_ref, h=h)
+    phi = A.make_phi(dqk, r, kind=kind, device=DEV, dtype=dt, seed=3)
+    got = A.featurise(Q.to(DEV), K.to(DEV), V.to(DEV), phi, h=None if h is None else h.to(DEV))
+    for name, a, b in zip(("Phi", "Psi"), got[:2], ref[:2]):
+        a = a.cpu().double()
+        b = b.double()
+        assert a.shape == b.shape
+        if dt == torch.float32:
+            assert _rel(a, b) < 1e-5, name
+        else:
+            ulp = 2.0 ** (-7 if dt == torch.bfloat16 else -10)
+            rel = (a - b).abs() / b.abs().clamp_min(1e-30)
+            assert (rel > ulp).double().mean().item() <= 1e-4, (name, rel.max().item())
+            assert rel.max().item() < 0.04, name
+    assert torch.equal(got[2].cpu(), ref[2])
+    # the map alone, called on a GPU tensor
+    assert torch.equal(phi(Q.to(DEV)), got[0])
+
+
+def test_featurise_rejects_mixed_dtypes():
+    phi = A.make_phi(32, 32, device=DEV, dtype=torch.float32)
+    Q = torch.randn(1, 16, 32, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        A.featurise(Q, Q, Q, phi)
