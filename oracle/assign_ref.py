@@ -65,3 +65,58 @@ def dense_read(Phi, Psi, Vb, n: int, ck, cq, N0: int, *, mode: str = "point", M=
     po = torch.einsum("bix,eox->bieo", Wq, Mf)
     wo = torch.nn.functional.one_hot(po.argmax(-1), Mf.shape[1]).to(acc)
     return torch.einsum("bie,bieo,bieop->bip", we, wo, Z)
+
+
+def hash_s(u, W, gamma, b, q: int, h: int):
+    """assign.py:251-256 with autograd: s = clamp(q Phi_N(LN(u) W^ gamma + b), 0, q - 1e-4),
+    (nb*h, L, dim)."""
+    nb, L, dm = u.shape
+    Wn = W / W.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+    ln = torch.nn.functional.layer_norm(u, (dm,))
+    z = torch.einsum("blm,hkm->bhlk", ln, Wn) * gamma[None, :, None, :] + b[None, :, None, :]
+    s = (torch.special.ndtr(z) * q).clamp(0.0, q - 1e-4)
+    return s.reshape(nb * h, L, W.shape[1])
+
+
+def ste_weights(s, q: int, N0: int):
+    """assign.py:257-266 and :290-295 at anneal = 1: the dense (B, L, N0) cell
+    weights, forward the one-hot of the all-low cell, backward the two-bin
+    interpolation of every coordinate."""
+    B, L, dim = s.shape
+    lo = s.floor()
+    frac = s - lo
+    lo = lo.long()
+    hi = (lo + 1).clamp(max=q - 1)
+    idx = torch.zeros(B, L, 1, dtype=torch.long)
+    w = torch.ones(B, L, 1, dtype=s.dtype)
+    for k in range(dim):
+        place = q ** (dim - 1 - k)
+        f = frac[..., k:k + 1]
+        e_lo = 1.0 + ((1.0 - f) - (1.0 - f).detach())
+        e_hi = f - f.detach()
+        idx = torch.cat([idx + lo[..., k:k + 1] * place, idx + hi[..., k:k + 1] * place], -1)
+        w = torch.cat([w * e_lo, w * e_hi], -1)
+    return torch.zeros(B, L, N0, dtype=s.dtype).scatter_add(-1, idx, w)
+
+
+def dense_point_ste(u, Phi, Psi, Vb, n: int, W, gamma, b, q: int, dim: int, h: int, N0: int,
+                    planted_cols=None, plant_cells=None):
+    """The point branch as assign.py:374-446 computes it on its dense path, with
+    autograd through Phi, Psi, Vb and the hash (u, W, gamma, b): planted key
+    columns get a fixed one-hot row (:305-317), F = Wk^T (Psi (x) Vb) (:436),
+    y_i = Phi_i (Wq F)_i (:439-441).  Returns (nb*h, T - n, p)."""
+    Wk = ste_weights(hash_s(u[:, :n], W, gamma, b, q, h), q, N0)
+    if planted_cols is not None and len(planted_cols):
+        cols = torch.as_tensor(planted_cols, dtype=torch.long)
+        cols = cols[cols < n]
+        one = torch.zeros(cols.numel(), N0, dtype=Wk.dtype)
+        one[torch.arange(cols.numel()), plant_cells[: cols.numel()]] = 1.0
+        Wk = Wk.clone()
+        Wk[:, cols] = one
+    Wq = ste_weights(hash_s(u[:, n:], W, gamma, b, q, h), q, N0)
+    B, _, r = Psi.shape
+    p = Vb.shape[-1]
+    PV = torch.einsum("bnr,bnp->bnrp", Psi[:, :n], Vb[:, :n]).reshape(B, n, r * p)
+    F = torch.bmm(Wk.transpose(1, 2), PV).view(B, N0, r, p)
+    Uq = torch.bmm(Wq, F.reshape(B, N0, r * p)).view(B, -1, r, p)
+    return torch.einsum("bir,birp->bip", Phi[:, n:], Uq)

@@ -24,9 +24,12 @@ Supported: ``mode`` point/plane (codim 1 or dim), ``src`` hidden/embed/id,
 ``shift``, ``plant``, ``freeze``, the linear direction head, ``dir_override``,
 the hard mask (``anneal = 1``).  Parameters are created in the reference's
 order, so a module built after ``torch.manual_seed(s)`` holds the reference's
-values.  The forward is not differentiable here (the straight-through
-backward of the hash is not implemented); options outside the list raise
-``NotImplementedError`` at construction.
+values.  Point mode trains: the hash runs under torch autograd and the
+pool, the read and their gradients run on the list kernels, with the
+straight-through gradient of the reference's dense path (see ``_PointRead``).
+The plane read is forward-only and raises ``NotImplementedError`` when a
+gradient is asked of it; options outside the list raise the same at
+construction.
 """
 from __future__ import annotations
 
@@ -183,8 +186,7 @@ class ContentAssign(nn.Module):
         if torch.is_grad_enabled() and (
                 any(t is not None and t.requires_grad for t in (u, Phi, Psi, Vb, emb, key_src))
                 or any(prm.requires_grad for prm in self.parameters())):
-            raise NotImplementedError("ContentAssign: the backward is not implemented; call "
-                                      "under torch.no_grad()")
+            return self._forward_train(u, Phi, Psi, Vb, n, emb, key_src, key_w, ids)
         if self.src == "id":
             assert ids is not None, "the id hash needs token ids"
             ik = ids if not self.shift else torch.cat(
@@ -203,6 +205,88 @@ class ContentAssign(nn.Module):
             self.aux = None if self.freeze else aux_k + self.aux
         self.last_hard_k = ck.detach()
         return self._read(u, Phi, Psi, Vb, n, ck, cq, dir_override)
+
+    # ------------------------------------------------------------ training
+    def _soft_hash(self, u):
+        """``s = clamp(q Phi_N(LN(u) W^ gamma + b), 0, q - 1e-4)`` with autograd, in
+        the reference's op order (assign.py:251-256): the hash of the training
+        path, whose floor gives the same cells as the HIP hash."""
+        nb, L, _ = u.shape
+        Wn = self.W / self.W.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+        z = torch.einsum("blm,hkm->bhlk", self.ln(u), Wn) * self.gamma[None, :, None, :] \
+            + self.b[None, :, None, :]
+        s = torch.special.ndtr(z)
+        s = (s * self.q).clamp(0.0, self.q - 1e-4)
+        return s.reshape(nb * self.h, L, self.dim)
+
+    def _ste_pairs(self, s, plant_at=False, tok_w=None):
+        """The 2^dim (cell, weight) pairs of every token at anneal = 1
+        (assign.py:257-270): forward weight 1 on the all-low cell and 0 on the
+        others, gradient through the interpolation weights.  Returns the chosen
+        cells (planted columns overwritten), idx (B, L, K), w (B, L, K) and the
+        load-balance term."""
+        B, L, _ = s.shape
+        lo = s.floor()
+        frac = s - lo
+        lo = lo.long()
+        hi = (lo + 1).clamp(max=self.q - 1)
+        idx = torch.zeros(B, L, 1, dtype=torch.long, device=s.device)
+        w = torch.ones(B, L, 1, device=s.device, dtype=s.dtype)
+        for k in range(self.dim):
+            place = self.q ** (self.dim - 1 - k)
+            f = frac[..., k:k + 1]
+            s_lo, s_hi = 1.0 - f, f
+            e_lo = 1.0 + (s_lo - s_lo.detach())
+            e_hi = s_hi - s_hi.detach()
+            idx = torch.cat([idx + lo[..., k:k + 1] * place, idx + hi[..., k:k + 1] * place], -1)
+            w = torch.cat([w * e_lo, w * e_hi], dim=-1)
+        soft_lo, soft_hi = 1.0 - frac, frac
+        if tok_w is not None:
+            tw = tok_w.reshape(B, L, 1).to(s.dtype)
+            soft_lo, soft_hi = soft_lo * tw, soft_hi * tw
+        occ = torch.zeros(B, self.dim, self.q, device=s.device, dtype=s.dtype)
+        occ = occ.scatter_add(-1, lo.transpose(1, 2), soft_lo.transpose(1, 2))
+        occ = occ.scatter_add(-1, hi.transpose(1, 2), soft_hi.transpose(1, 2))
+        occ = occ / occ.sum(-1, keepdim=True).clamp_min(1e-6)
+        aux = None if self.freeze else (occ * (occ.clamp_min(1e-9) * self.q).log()).sum(-1).mean()
+        cells = idx[..., 0].clone()
+        if plant_at and self.plant and self.plant_cols.numel():
+            cols = self.plant_cols[self.plant_cols < L].to(s.device)
+            if cols.numel():
+                # a fixed, input-independent profile: no gradient through its weights
+                cells[:, cols] = self.plant_cells[: cols.numel()].to(s.device)
+                w = w.clone()
+                w[:, cols] = w[:, cols].detach()
+        return cells, idx, w, aux
+
+    def _forward_train(self, u, Phi, Psi, Vb, n, emb, key_src, key_w, ids):
+        """The branch with gradients (point mode): the hash is torch autograd on
+        the 16 dim values per token, the pool, the read and all their gradients
+        are HIP (:class:`_PointRead`)."""
+        if self.mode != "point":
+            raise NotImplementedError("ContentAssign: gradients of the plane read are not "
+                                      "implemented; use mode='point' or torch.no_grad()")
+        if self.src == "id":
+            assert ids is not None, "the id hash needs token ids"
+            ik = ids if not self.shift else torch.cat(
+                [ids.new_zeros(ids.shape[0], self.shift), ids[:, :-self.shift]], dim=1)
+            ck, cq = self._cells_id(ik[:, :n]), self._cells_id(ids[:, n:])
+            idxk, idxq = ck.unsqueeze(-1), cq.unsqueeze(-1)
+            wk = torch.ones(idxk.shape, device=u.device)
+            wq = torch.ones(idxq.shape, device=u.device)
+            self.aux = None
+        else:
+            h = u if (self.src == "hidden" or emb is None) else emb
+            hk = h if key_src is None else key_src
+            if self.shift:
+                hk = torch.cat([h.new_zeros(h.shape[0], self.shift, h.shape[2]),
+                                h[:, :-self.shift]], dim=1)
+            ck, idxk, wk, aux_k = self._ste_pairs(self._soft_hash(hk[:, :n]), plant_at=True,
+                                                  tok_w=key_w)
+            cq, idxq, wq, aux_q = self._ste_pairs(self._soft_hash(h[:, n:]))
+            self.aux = None if self.freeze else aux_k + aux_q
+        self.last_hard_k = ck.detach()
+        return _PointRead.apply(Phi, Psi, Vb, wk, wq, idxk, idxq, ck, cq, n, self.N0)
 
     def _read(self, u, Phi, Psi, Vb, n, ck, cq, dir_override):
         nbh, T, r = Phi.shape
@@ -254,3 +338,114 @@ class ContentAssign(nn.Module):
              Y.data_ptr(), rows.data_ptr(), roffs.data_ptr(), nbh * ntypes, maxcnt, r, p,
              Pr.stride(1), Y.stride(1), stream_of(Pr))
         return Y[:, n:]
+
+
+# ---------------------------------------------------------------------------
+# List helpers and the point branch with its gradients (HIP)
+# ---------------------------------------------------------------------------
+
+def _lists(cls, ncls):
+    """CSR of the rows of each (sequence, class): cls (nb, L) int -> row indices
+    (int32, into the (nb*L) flattened rows, ascending within a class), offsets
+    (int64, nb*ncls + 1) and the longest list."""
+    nb, L = cls.shape
+    key = (torch.arange(nb, device=cls.device).unsqueeze(1) * ncls + cls).reshape(-1)
+    order = torch.argsort(key, stable=True)
+    counts = torch.bincount(key, minlength=nb * ncls)
+    offs = torch.zeros(nb * ncls + 1, device=cls.device, dtype=torch.int64)
+    offs[1:] = torch.cumsum(counts, 0)
+    maxcnt = int(counts.max().item()) if counts.numel() else 0
+    return order.to(torch.int32), offs, maxcnt
+
+
+def _gram_lists(A, B, cls, ncls):
+    """``G[b, x] = sum_{l: cls[b,l] = x} A[b,l]^T B[b,l]``: A (nb, L, r), B (nb, L, p),
+    same dtype, contiguous -> fp32 (nb, ncls, r, p) (smat_gram_lists)."""
+    nb, L, r = A.shape
+    p = B.shape[-1]
+    tok, offs, _ = _lists(cls, ncls)
+    G = torch.empty(nb, ncls, r, p, device=A.device, dtype=torch.float32)
+    call("smat_gram_lists", _code(A, "ContentAssign"), A.data_ptr(), B.data_ptr(),
+         tok.data_ptr(), offs.data_ptr(), G.data_ptr(), nb * ncls, r, p, A.stride(1),
+         B.stride(1), stream_of(A))
+    return G
+
+
+def _read_lists(X, U, cls):
+    """``Y[b, l] = X[b, l] U[b, cls[b, l]]``: X (nb, L, c) contiguous, U fp32
+    (nb, ncls, c, o) contiguous -> fp32 (nb, L, o) (smat_query_lists)."""
+    nb, L, c = X.shape
+    ncls, o = U.shape[1], U.shape[-1]
+    rows, roffs, maxcnt = _lists(cls, ncls)
+    Y = None
+    # the kernel contracts at most 128 columns; wider X (c = head_dim + 1) is
+    # read in column blocks whose partial products add up
+    for c0 in range(0, c, 128):
+        c1 = min(c, c0 + 128)
+        Xs = X if c1 - c0 == c else X[..., c0:c1].contiguous()
+        Us = U if c1 - c0 == c else U[:, :, c0:c1].contiguous()
+        Ys = torch.empty(nb, L, o, device=X.device, dtype=torch.float32)
+        call("smat_query_lists", _code(Xs, "ContentAssign"), Xs.data_ptr(), Us.data_ptr(),
+             Ys.data_ptr(), rows.data_ptr(), roffs.data_ptr(), nb * ncls, maxcnt, c1 - c0, o,
+             Xs.stride(1), Ys.stride(1), stream_of(Xs))
+        Y = Ys if Y is None else Y.add_(Ys)
+    return Y
+
+
+def _read_pairs(X, U, idx):
+    """``Z[b, l, k] = X[b, l] U[b, idx[b, l, k]]`` for every pair: (nb, L, K, o)."""
+    nb, L, c = X.shape
+    K = idx.shape[-1]
+    Xr = X.unsqueeze(2).expand(nb, L, K, c).reshape(nb, L * K, c).contiguous()
+    return _read_lists(Xr, U, idx.reshape(nb, L * K)).view(nb, L, K, -1)
+
+
+class _PointRead(torch.autograd.Function):
+    """The point read of the content-addressed branch with the dense path's
+    gradients (assign.py:431-446 under autograd): forward
+    ``F_x = sum_{ck_j = x} Psi_j^T Vb_j``, ``y_i = Phi_i F_{cq_i}`` over the
+    chosen cells; backward, with the pair weights w (forward one-hot):
+
+        dF_x   = sum_{cq_i = x} Phi_i^T dy_i          dPhi_i = F_{cq_i} dy_i
+        dPsi_j = dF_{ck_j} Vb_j                      dVb_j  = dF_{ck_j}^T Psi_j
+        dwq_ik = Phi_i . (F_{idxq_ik} dy_i)          dwk_jk = Psi_j . (dF_{idxk_jk} Vb_j)
+
+    Every product is a HIP list-Gram or list-read; the transposed tables are
+    copies.  Landmark rows of Phi and recent rows of Psi, Vb get zero."""
+
+    @staticmethod
+    def forward(ctx, Phi, Psi, Vb, wk, wq, idxk, idxq, ck, cq, n, N0):
+        nbh, T, r = Phi.shape
+        p = Vb.shape[-1]
+        if r > 128 or p > 144:
+            raise NotImplementedError("ContentAssign gradients: r <= 128, p <= 144")
+        Pk = Psi[:, :n].contiguous()
+        Vk = Vb[:, :n].contiguous()
+        Phr = Phi[:, n:].contiguous()
+        F = _gram_lists(Pk, Vk, ck, N0)
+        Y = _read_lists(Phr, F, cq)
+        ctx.save_for_backward(Phr, Pk, Vk, F, idxk, idxq, ck, cq)
+        ctx.meta = (n, N0, Phi.shape, Phi.dtype, Psi.dtype, Vb.dtype, wk.dtype, wq.dtype)
+        return Y
+
+    @staticmethod
+    def backward(ctx, dY):
+        Phr, Pk, Vk, F, idxk, idxq, ck, cq = ctx.saved_tensors
+        n, N0, shape, d_phi, d_psi, d_vb, d_wk, d_wq = ctx.meta
+        nbh, T, r = shape
+        p = Vk.shape[-1]
+        dY = dY.float().contiguous()
+        Ph32, P32, V32 = Phr.float(), Pk.float(), Vk.float()
+        dF = _gram_lists(Ph32, dY, cq, N0)
+        FT = F.transpose(-1, -2).contiguous()
+        dFT = dF.transpose(-1, -2).contiguous()
+        dPhi = torch.zeros(nbh, T, r, device=dY.device, dtype=torch.float32)
+        dPsi = torch.zeros(nbh, T, r, device=dY.device, dtype=torch.float32)
+        dVb = torch.zeros(nbh, T, p, device=dY.device, dtype=torch.float32)
+        dPhi[:, n:] = _read_lists(dY, FT, cq)
+        dPsi[:, :n] = _read_lists(V32, dFT, ck)
+        dVb[:, :n] = _read_lists(P32, dF, ck)
+        dwq = (_read_pairs(dY, FT, idxq) * Ph32.unsqueeze(2)).sum(-1)
+        dwk = (_read_pairs(V32, dFT, idxk) * P32.unsqueeze(2)).sum(-1)
+        return (dPhi.to(d_phi), dPsi.to(d_psi), dVb.to(d_vb), dwk.to(d_wk), dwq.to(d_wq),
+                None, None, None, None, None, None)

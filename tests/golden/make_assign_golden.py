@@ -11,7 +11,9 @@ outputs as data:
 
     assign_golden.npz   per case: u, Phi, Psi, Vb, W, gamma, b, [Wd], the key
                         cells (last_hard_k), the query cells (cells_of), the
-                        load-balance term aux and the forward output y
+                        load-balance term aux and the forward output y; point
+                        cases also R and the gradients of (y * R).sum(): du,
+                        dPhi, dPsi, dVb, dW, dgamma, db
 
 Run from the repository root (needs /root/reference, numpy and torch):
 
@@ -77,6 +79,19 @@ def main():
         out[f"{name}/aux"] = np.array(float(m.aux))
         out[f"{name}/y"] = y.numpy()
         out[f"{name}/meta"] = np.array([T, d, h, dm, nb, n, r, 1 if mode == "plane" else 0])
+        if mode == "point":
+            # gradients of (y * R).sum() through the module's straight-through path
+            R = torch.randn(y.shape, generator=torch.Generator().manual_seed(3000))
+            xs = [t.detach().clone().requires_grad_(True) for t in (u, Phi, Psi, Vb)]
+            m.zero_grad()
+            yg = m(xs[0], xs[1], xs[2], xs[3], n)
+            (yg * R).sum().backward()
+            out[f"{name}/R"] = R.numpy()
+            for key, t in zip(("du", "dPhi", "dPsi", "dVb"), xs):
+                out[f"{name}/{key}"] = t.grad.numpy()
+            out[f"{name}/dW"] = m.W.grad.numpy()
+            out[f"{name}/dgamma"] = m.gamma.grad.numpy()
+            out[f"{name}/db"] = m.b.grad.numpy()
     np.savez_compressed(os.path.join(HERE, "assign_golden.npz"), **out)
     print("wrote", len(CASES), "cases")
 
