@@ -1,10 +1,14 @@
-"""CPU restatement of the content-addressed assignment's forward (hard mask).
+"""CPU restatement of the content-addressed assignment.
 
 Test infrastructure (see ``oracle/__init__.py``).  Follows
 src/smat/assign.py: the hash of ``_cells`` (:246-276, the ``anneal = 1``
 branch :288-295), the planted key columns (:305-317), the dense read
 ``_dense_read`` (:431-472) with one-hot forward weights, for the point and
-plane (linear direction head) modes.  Pure torch on CPU tensors.
+plane (linear direction head) modes; with autograd, the straight-through
+weights of the dense point read (``dense_point_ste``) and the (cell, weight)
+pair branch of the soft phase and the ``sparse_ops`` path (``pairs_branch``:
+:257-313, :378-406, with the pool / read maps of
+src/smat_lm/smat_pool_ops.py:1-11 written densely).  Pure torch on CPU tensors.
 """
 from __future__ import annotations
 
@@ -120,3 +124,94 @@ def dense_point_ste(u, Phi, Psi, Vb, n: int, W, gamma, b, q: int, dim: int, h: i
     F = torch.bmm(Wk.transpose(1, 2), PV).view(B, N0, r, p)
     Uq = torch.bmm(Wq, F.reshape(B, N0, r * p)).view(B, -1, r, p)
     return torch.einsum("bir,birp->bip", Phi[:, n:], Uq)
+
+
+def soft_pairs(s, q: int, dim: int, anneal: float = 1.0, single: bool = False):
+    """assign.py:257-284: the 2^dim (cell, weight) pairs of every token, weight
+    ``(1 - a) s + a e`` per coordinate (``e`` the straight-through form of the
+    interpolation weight ``s``); with ``single`` and ``a >= 1`` the chosen cell
+    alone (``hard_k1``).  Returns idx, w of shape (B, L, K)."""
+    B, L, _ = s.shape
+    a = float(anneal)
+    lo = s.floor()
+    frac = s - lo
+    lo = lo.long()
+    hi = (lo + 1).clamp(max=q - 1)
+    if single and a >= 1.0:
+        idx = torch.zeros(B, L, 1, dtype=torch.long)
+        w = torch.ones(B, L, 1, dtype=s.dtype)
+        for k in range(dim):
+            f = frac[..., k:k + 1]
+            idx = idx + lo[..., k:k + 1] * q ** (dim - 1 - k)
+            w = w * (1.0 + ((1.0 - f) - (1.0 - f).detach()))
+        return idx, w
+    idx = torch.zeros(B, L, 1, dtype=torch.long)
+    w = torch.ones(B, L, 1, dtype=s.dtype)
+    for k in range(dim):
+        place = q ** (dim - 1 - k)
+        f = frac[..., k:k + 1]
+        s_lo, s_hi = 1.0 - f, f
+        e_lo = 1.0 + (s_lo - s_lo.detach())
+        e_hi = s_hi - s_hi.detach()
+        idx = torch.cat([idx + lo[..., k:k + 1] * place, idx + hi[..., k:k + 1] * place], -1)
+        w = torch.cat([w * ((1 - a) * s_lo + a * e_lo), w * ((1 - a) * s_hi + a * e_hi)], -1)
+    return idx, w
+
+
+def plant_pairs(idx, w, planted_cols, plant_cells):
+    """assign.py:305-313: planted key columns get their fixed cell, weight 1 on
+    the first pair and 0 on the others, no gradient."""
+    cols = torch.as_tensor(planted_cols, dtype=torch.long)
+    cols = cols[cols < idx.shape[1]]
+    if cols.numel() == 0:
+        return idx, w
+    idx, w = idx.clone(), w.clone()
+    idx[:, cols, :] = plant_cells[: cols.numel()].view(1, -1, 1)
+    w[:, cols, :] = 0.0
+    w[:, cols, 0] = 1.0
+    return idx, w
+
+
+def pairs_dense(idx, w, N0: int):
+    """(B, L, N0) cell weights: every pair's weight added to its cell
+    (assign.py:297 ``scatter_add``)."""
+    B, L, _ = idx.shape
+    return torch.zeros(B, L, N0, dtype=w.dtype).scatter_add(-1, idx, w)
+
+
+def pairs_branch(u, Phi, Psi, Vb, n: int, W, gamma, b, q: int, dim: int, h: int, N0: int, *,
+                 anneal: float = 1.0, single: bool = False, planted_cols=None,
+                 plant_cells=None, mode: str = "point", M=None, Wd=None, coset_of=None):
+    """The long-range term over (cell, weight) pairs with autograd: the dense
+    read with the soft cell weights (assign.py:431-442) and the ``sparse_ops``
+    path (:378-406) -- ``F = Wk^T (Psi (x) Vb)``, point ``y = Phi (Wq F)``;
+    plane: ``Fc = M F`` summed to the direction cosets, the direction the
+    argmax of ``softmax(u Wd)`` with the straight-through factor
+    ``1 + pmax - pmax.detach()``, each query pair read at (direction, coset of
+    its cell).  Returns (nb*h, T - n, p)."""
+    planted = planted_cols is not None and any(int(c) < n for c in planted_cols)
+    # a planted key side is planted into the full pairs (assign.py:306-310)
+    idxk, wk = soft_pairs(hash_s(u[:, :n], W, gamma, b, q, h), q, dim, anneal,
+                          single and not planted)
+    if planted:
+        idxk, wk = plant_pairs(idxk, wk, planted_cols, plant_cells)
+    idxq, wq = soft_pairs(hash_s(u[:, n:], W, gamma, b, q, h), q, dim, anneal, single)
+    Bs, _, r = Psi.shape
+    p = Vb.shape[-1]
+    PV = torch.einsum("bnr,bnp->bnrp", Psi[:, :n], Vb[:, :n]).reshape(Bs, n, r * p)
+    F = torch.bmm(pairs_dense(idxk, wk, N0).transpose(1, 2), PV).view(Bs, N0, r, p)
+    Phi_r = Phi[:, n:]
+    if mode == "point":
+        Uq = torch.bmm(pairs_dense(idxq, wq, N0), F.reshape(Bs, N0, r * p)).view(Bs, -1, r, p)
+        return torch.einsum("bir,birp->bip", Phi_r, Uq)
+    D, nc = M.shape[0], M.shape[1]
+    Fc = torch.einsum("eox,bxrp->beorp", M, F).reshape(Bs, D * nc, r * p)
+    T_R = Phi_r.shape[1]
+    dl = torch.einsum("blm,hem->bhle", u[:, n:], Wd).reshape(Bs, T_R, D)
+    pe = torch.softmax(dl, dim=-1)
+    e_star = pe.argmax(-1, keepdim=True)
+    pmax = pe.gather(-1, e_star)
+    ste = 1.0 + (pmax - pmax.detach())
+    rows = e_star * nc + coset_of[e_star.expand_as(idxq), idxq]
+    Uq = torch.bmm(pairs_dense(rows, wq, D * nc), Fc).view(Bs, T_R, r, p)
+    return torch.einsum("bir,birp->bip", Phi_r, Uq) * ste

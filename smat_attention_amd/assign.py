@@ -37,7 +37,8 @@ import numpy as np
 import torch
 import torch.nn as nn
 
-from .kernels.hip_fwd import _code, _rows3, call, stream_of
+from .kernels.hip_fwd import _code, _on_gpu, _rows3, call, stream_of
+from .pool_ops import _gram_lists, _read_lists, _read_pairs, pool_sorted, read_sorted
 
 __all__ = ["ContentAssign", "grouped_planes"]
 
@@ -183,6 +184,17 @@ class ContentAssign(nn.Module):
                 dir_override=None, ids=None):
         """u: (nb, T, d_model) layer input; Phi, Psi: (nb*h, T, r); Vb: (nb*h, T, p);
         n: landmark/recent boundary.  Returns fp32 (nb*h, T - n, p)."""
+        sparse = bool(getattr(self, "sparse_ops", False))
+        if self.mode == "plane" and not sparse and torch.is_grad_enabled() and (
+                any(t is not None and t.requires_grad for t in (u, Phi, Psi, Vb, emb, key_src))
+                or any(prm.requires_grad for prm in self.parameters())):
+            raise NotImplementedError("ContentAssign: gradients of the dense plane read are not "
+                                      "implemented; set sparse_ops, or use torch.no_grad()")
+        _on_gpu("ContentAssign", u, Phi, Psi, Vb, emb, key_src, key_w, ids)
+        if self.src != "id" and (self.anneal < 1.0 or getattr(self, "sparse_ops", False)):
+            # the id hash is one-hot whatever the anneal and always reads densely
+            # (assign.py:359-364)
+            return self._forward_pairs(u, Phi, Psi, Vb, n, emb, key_src, key_w, ids, dir_override)
         if torch.is_grad_enabled() and (
                 any(t is not None and t.requires_grad for t in (u, Phi, Psi, Vb, emb, key_src))
                 or any(prm.requires_grad for prm in self.parameters())):
@@ -219,13 +231,19 @@ class ContentAssign(nn.Module):
         s = (s * self.q).clamp(0.0, self.q - 1e-4)
         return s.reshape(nb * self.h, L, self.dim)
 
-    def _ste_pairs(self, s, plant_at=False, tok_w=None):
-        """The 2^dim (cell, weight) pairs of every token at anneal = 1
-        (assign.py:257-270): forward weight 1 on the all-low cell and 0 on the
-        others, gradient through the interpolation weights.  Returns the chosen
-        cells (planted columns overwritten), idx (B, L, K), w (B, L, K) and the
-        load-balance term."""
+    def _ste_pairs(self, s, plant_at=False, tok_w=None, single=False):
+        """The 2^dim (cell, weight) pairs of every token (assign.py:257-295):
+        weight ``(1 - a) s + a e`` per coordinate, with ``s`` the interpolation
+        weight and ``e`` its straight-through form (forward 1 on the low bin and
+        0 on the high one, the gradient of ``s``), ``a`` the anneal.  With
+        ``single`` and ``a >= 1`` only the chosen cell is kept, its weight the
+        product of the low bins' straight-through factors (the sparse path's
+        ``hard_k1``) -- except on a key side with planted columns, which the
+        reference plants into the full pairs.  Planted key columns get their
+        fixed cell with weight 1 and no gradient (:305-317).  Returns the chosen cells, idx (B, L, K),
+        w (B, L, K) and the load-balance term."""
         B, L, _ = s.shape
+        a = float(self.anneal)
         lo = s.floor()
         frac = s - lo
         lo = lo.long()
@@ -238,8 +256,22 @@ class ContentAssign(nn.Module):
             s_lo, s_hi = 1.0 - f, f
             e_lo = 1.0 + (s_lo - s_lo.detach())
             e_hi = s_hi - s_hi.detach()
+            w_lo, w_hi = (1 - a) * s_lo + a * e_lo, (1 - a) * s_hi + a * e_hi
             idx = torch.cat([idx + lo[..., k:k + 1] * place, idx + hi[..., k:k + 1] * place], -1)
-            w = torch.cat([w * e_lo, w * e_hi], dim=-1)
+            w = torch.cat([w * w_lo, w * w_hi], dim=-1)
+        cols = None
+        if plant_at and self.plant and self.plant_cols.numel():
+            cols = self.plant_cols[self.plant_cols < L].to(s.device)
+            cols = cols if cols.numel() else None
+        # the reference plants into a copy of the full pairs (assign.py:306-310),
+        # so a planted key side keeps all 2^dim pairs even where one would do
+        if single and cols is None and a >= 1.0 and getattr(self, "hard_k1", True):
+            idx = torch.zeros(B, L, 1, dtype=torch.long, device=s.device)
+            w = torch.ones(B, L, 1, device=s.device, dtype=s.dtype)
+            for k in range(self.dim):
+                f = frac[..., k:k + 1]
+                idx = idx + lo[..., k:k + 1] * self.q ** (self.dim - 1 - k)
+                w = w * (1.0 + ((1.0 - f) - (1.0 - f).detach()))
         soft_lo, soft_hi = 1.0 - frac, frac
         if tok_w is not None:
             tw = tok_w.reshape(B, L, 1).to(s.dtype)
@@ -250,14 +282,75 @@ class ContentAssign(nn.Module):
         occ = occ / occ.sum(-1, keepdim=True).clamp_min(1e-6)
         aux = None if self.freeze else (occ * (occ.clamp_min(1e-9) * self.q).log()).sum(-1).mean()
         cells = idx[..., 0].clone()
-        if plant_at and self.plant and self.plant_cols.numel():
-            cols = self.plant_cols[self.plant_cols < L].to(s.device)
-            if cols.numel():
-                # a fixed, input-independent profile: no gradient through its weights
-                cells[:, cols] = self.plant_cells[: cols.numel()].to(s.device)
-                w = w.clone()
-                w[:, cols] = w[:, cols].detach()
+        if cols is not None:
+            # a fixed, input-independent profile: no gradient through its weights
+            pc = self.plant_cells[: cols.numel()].to(s.device)
+            cells[:, cols] = pc
+            idx = idx.clone()
+            idx[:, cols, :] = pc.view(1, -1, 1)
+            w = w.clone()
+            w[:, cols, :] = 0.0
+            w[:, cols, 0] = 1.0
         return cells, idx, w, aux
+
+    def _pairs_of(self, u, n, emb, key_src, key_w, ids, single):
+        """Key and query pairs (assign.py:357-378) for the pair reads."""
+        if self.src == "id":
+            assert ids is not None, "the id hash needs token ids"
+            ik = ids if not self.shift else torch.cat(
+                [ids.new_zeros(ids.shape[0], self.shift), ids[:, :-self.shift]], dim=1)
+            ck, cq = self._cells_id(ik[:, :n]), self._cells_id(ids[:, n:])
+            self.aux = None
+            one = lambda c: torch.ones(c.shape + (1,), device=u.device)
+            return ck, ck.unsqueeze(-1), one(ck), cq, cq.unsqueeze(-1), one(cq)
+        h = u if (self.src == "hidden" or emb is None) else emb
+        hk = h if key_src is None else key_src
+        if self.shift:
+            hk = torch.cat([h.new_zeros(h.shape[0], self.shift, h.shape[2]),
+                            h[:, :-self.shift]], dim=1)
+        ck, idxk, wk, aux_k = self._ste_pairs(self._soft_hash(hk[:, :n]), plant_at=True,
+                                              tok_w=key_w, single=single)
+        cq, idxq, wq, aux_q = self._ste_pairs(self._soft_hash(h[:, n:]), single=single)
+        self.aux = None if self.freeze else aux_k + aux_q
+        return ck, idxk, wk, cq, idxq, wq
+
+    def _forward_pairs(self, u, Phi, Psi, Vb, n, emb, key_src, key_w, ids, dir_override):
+        """The branch over (cell, weight) pairs: the soft phase of the dense
+        read (anneal < 1, assign.py:431-442 with the soft cell weights) and the
+        ``sparse_ops`` path (:378-406).  Pool and read are
+        :func:`pool_sorted` / :func:`read_sorted` (HIP list kernels, with
+        gradients); the plane read aggregates F to the direction cosets with the
+        incidence kernel first."""
+        if getattr(self, "delta_updates", False):
+            raise NotImplementedError("ContentAssign: delta_updates (the delta-rule pool)")
+        sparse = bool(getattr(self, "sparse_ops", False))
+        if self.mode == "plane" and not sparse:
+            raise NotImplementedError("ContentAssign: the dense plane read at anneal < 1; "
+                                      "set sparse_ops for the coset read")
+        ck, idxk, wk, cq, idxq, wq = self._pairs_of(u, n, emb, key_src, key_w, ids, sparse)
+        self.last_hard_k = ck.detach()
+        P, V, Phi_r = Psi[:, :n], Vb[:, :n], Phi[:, n:]
+        dt = P.dtype
+        F = pool_sorted(P, V, idxk, wk.to(dt), self.N0)
+        if self.mode == "point":
+            return read_sorted(Phi_r, idxq, wq.to(dt), F)
+        from .kernels import hip_bwd
+        nrows = self.D * self.n_cosets
+        Fc = hip_bwd.incidence(F, self.coset_pts.to(F.device), nrows).to(F.dtype)
+        nbh, T_R = Phi_r.shape[0], Phi_r.shape[1]
+        if dir_override is not None:
+            e_star = dir_override.reshape(nbh, T_R, 1).long()
+            ste = torch.ones(nbh, T_R, 1, device=u.device)
+        else:
+            dl = torch.einsum("blm,hem->bhle", u[:, n:], self.Wd.to(u.dtype)).reshape(nbh, T_R,
+                                                                                     self.D)
+            pe = torch.softmax(dl.float(), dim=-1)
+            e_star = pe.argmax(-1, keepdim=True)
+            pmax = pe.gather(-1, e_star)
+            ste = 1.0 + (pmax - pmax.detach())
+        coset = self.coset_of.to(u.device)[e_star.expand_as(idxq), idxq]
+        y = read_sorted(Phi_r, e_star * self.n_cosets + coset, wq.to(dt), Fc)
+        return y * ste.to(y.dtype)
 
     def _forward_train(self, u, Phi, Psi, Vb, n, emb, key_src, key_w, ids):
         """The branch with gradients (point mode): the hash is torch autograd on
@@ -341,64 +434,8 @@ class ContentAssign(nn.Module):
 
 
 # ---------------------------------------------------------------------------
-# List helpers and the point branch with its gradients (HIP)
+# The hard point branch with its gradients (HIP)
 # ---------------------------------------------------------------------------
-
-def _lists(cls, ncls):
-    """CSR of the rows of each (sequence, class): cls (nb, L) int -> row indices
-    (int32, into the (nb*L) flattened rows, ascending within a class), offsets
-    (int64, nb*ncls + 1) and the longest list."""
-    nb, L = cls.shape
-    key = (torch.arange(nb, device=cls.device).unsqueeze(1) * ncls + cls).reshape(-1)
-    order = torch.argsort(key, stable=True)
-    counts = torch.bincount(key, minlength=nb * ncls)
-    offs = torch.zeros(nb * ncls + 1, device=cls.device, dtype=torch.int64)
-    offs[1:] = torch.cumsum(counts, 0)
-    maxcnt = int(counts.max().item()) if counts.numel() else 0
-    return order.to(torch.int32), offs, maxcnt
-
-
-def _gram_lists(A, B, cls, ncls):
-    """``G[b, x] = sum_{l: cls[b,l] = x} A[b,l]^T B[b,l]``: A (nb, L, r), B (nb, L, p),
-    same dtype, contiguous -> fp32 (nb, ncls, r, p) (smat_gram_lists)."""
-    nb, L, r = A.shape
-    p = B.shape[-1]
-    tok, offs, _ = _lists(cls, ncls)
-    G = torch.empty(nb, ncls, r, p, device=A.device, dtype=torch.float32)
-    call("smat_gram_lists", _code(A, "ContentAssign"), A.data_ptr(), B.data_ptr(),
-         tok.data_ptr(), offs.data_ptr(), G.data_ptr(), nb * ncls, r, p, A.stride(1),
-         B.stride(1), stream_of(A))
-    return G
-
-
-def _read_lists(X, U, cls):
-    """``Y[b, l] = X[b, l] U[b, cls[b, l]]``: X (nb, L, c) contiguous, U fp32
-    (nb, ncls, c, o) contiguous -> fp32 (nb, L, o) (smat_query_lists)."""
-    nb, L, c = X.shape
-    ncls, o = U.shape[1], U.shape[-1]
-    rows, roffs, maxcnt = _lists(cls, ncls)
-    Y = None
-    # the kernel contracts at most 128 columns; wider X (c = head_dim + 1) is
-    # read in column blocks whose partial products add up
-    for c0 in range(0, c, 128):
-        c1 = min(c, c0 + 128)
-        Xs = X if c1 - c0 == c else X[..., c0:c1].contiguous()
-        Us = U if c1 - c0 == c else U[:, :, c0:c1].contiguous()
-        Ys = torch.empty(nb, L, o, device=X.device, dtype=torch.float32)
-        call("smat_query_lists", _code(Xs, "ContentAssign"), Xs.data_ptr(), Us.data_ptr(),
-             Ys.data_ptr(), rows.data_ptr(), roffs.data_ptr(), nb * ncls, maxcnt, c1 - c0, o,
-             Xs.stride(1), Ys.stride(1), stream_of(Xs))
-        Y = Ys if Y is None else Y.add_(Ys)
-    return Y
-
-
-def _read_pairs(X, U, idx):
-    """``Z[b, l, k] = X[b, l] U[b, idx[b, l, k]]`` for every pair: (nb, L, K, o)."""
-    nb, L, c = X.shape
-    K = idx.shape[-1]
-    Xr = X.unsqueeze(2).expand(nb, L, K, c).reshape(nb, L * K, c).contiguous()
-    return _read_lists(Xr, U, idx.reshape(nb, L * K)).view(nb, L, K, -1)
-
 
 class _PointRead(torch.autograd.Function):
     """The point read of the content-addressed branch with the dense path's

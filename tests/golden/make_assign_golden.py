@@ -12,8 +12,9 @@ outputs as data:
     assign_golden.npz   per case: u, Phi, Psi, Vb, W, gamma, b, [Wd], the key
                         cells (last_hard_k), the query cells (cells_of), the
                         load-balance term aux and the forward output y; point
-                        cases also R and the gradients of (y * R).sum(): du,
-                        dPhi, dPsi, dVb, dW, dgamma, db
+                        and sparse_ops cases also R and the gradients of
+                        (y * R).sum(): du, dPhi, dPsi, dVb, dW, dgamma, db
+                        (and dWd for the plane read)
 
 Run from the repository root (needs /root/reference, numpy and torch):
 
@@ -29,13 +30,20 @@ import numpy as np
 import torch
 
 REF = "/root/reference/src/smat"
+REF_LM = "/root/reference/src/smat_lm"     # smat_pool_ops, imported by the sparse_ops path
 HERE = os.path.dirname(os.path.abspath(__file__))
 
-# (name, T, d, mode, heads, d_model, nb): point and plane reads, d = 2 and 3
+# (name, T, d, mode, heads, d_model, nb, anneal, sparse_ops): point and plane
+# reads, d = 2 and 3; the soft phase (anneal < 1) of the dense read and the
+# sparse_ops pair path (one chosen cell at anneal 1, all 2^dim pairs below)
 CASES = [
-    ("T512_d3_point", 512, 3, "point", 2, 64, 2),
-    ("T512_d3_plane", 512, 3, "plane", 2, 64, 2),
-    ("T512_d2_point", 512, 2, "point", 2, 64, 2),
+    ("T512_d3_point", 512, 3, "point", 2, 64, 2, 1.0, False),
+    ("T512_d3_plane", 512, 3, "plane", 2, 64, 2, 1.0, False),
+    ("T512_d2_point", 512, 2, "point", 2, 64, 2, 1.0, False),
+    ("T512_d3_point_soft", 512, 3, "point", 2, 64, 2, 0.5, False),
+    ("T512_d3_point_sparse", 512, 3, "point", 2, 64, 2, 1.0, True),
+    ("T512_d3_point_sparse_soft", 512, 3, "point", 2, 64, 2, 0.5, True),
+    ("T512_d3_plane_sparse", 512, 3, "plane", 2, 64, 2, 1.0, True),
 ]
 
 
@@ -48,15 +56,18 @@ def _load(name, path):
 
 
 def main():
+    sys.path.insert(0, REF_LM)
     mask = _load("_ref_smat_mask", os.path.join(REF, "mask.py"))
     assign = _load("_ref_smat_assign", os.path.join(REF, "assign.py"))
     out = {}
-    for name, T, d, mode, h, dm, nb in CASES:
+    for name, T, d, mode, h, dm, nb, anneal, sparse in CASES:
         spec = mask.build_mask(T, d, chunk=64)
         n, r = spec.n, 16
         torch.manual_seed(1000)
         m = assign.ContentAssign(h, dm, spec, mode=mode)
         m.eval()
+        m.anneal = anneal
+        m.sparse_ops = sparse
         g = torch.Generator().manual_seed(2000)
         u = torch.randn(nb, T, dm, generator=g)
         Phi = torch.rand(nb * h, T, r, generator=g) + 0.5
@@ -79,7 +90,8 @@ def main():
         out[f"{name}/aux"] = np.array(float(m.aux))
         out[f"{name}/y"] = y.numpy()
         out[f"{name}/meta"] = np.array([T, d, h, dm, nb, n, r, 1 if mode == "plane" else 0])
-        if mode == "point":
+        out[f"{name}/opts"] = np.array([anneal, 1.0 if sparse else 0.0])
+        if mode == "point" or sparse:
             # gradients of (y * R).sum() through the module's straight-through path
             R = torch.randn(y.shape, generator=torch.Generator().manual_seed(3000))
             xs = [t.detach().clone().requires_grad_(True) for t in (u, Phi, Psi, Vb)]
@@ -92,6 +104,8 @@ def main():
             out[f"{name}/dW"] = m.W.grad.numpy()
             out[f"{name}/dgamma"] = m.gamma.grad.numpy()
             out[f"{name}/db"] = m.b.grad.numpy()
+            if mode == "plane":
+                out[f"{name}/dWd"] = m.Wd.grad.numpy()
     np.savez_compressed(os.path.join(HERE, "assign_golden.npz"), **out)
     print("wrote", len(CASES), "cases")
 

@@ -11,7 +11,12 @@ from oracle import assign_ref as R
 from smat_attention_amd.mask import build_mask
 
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "assign_golden.npz")
-CASES = ["T512_d3_point", "T512_d3_plane", "T512_d2_point"]
+# hard dense reads (anneal 1) and the pair reads: the soft phase of the dense
+# read, the sparse_ops path at anneal 1 (one cell per token) and below (2^dim)
+HARD_CASES = ["T512_d3_point", "T512_d3_plane", "T512_d2_point"]
+PAIR_CASES = ["T512_d3_point_soft", "T512_d3_point_sparse", "T512_d3_point_sparse_soft",
+              "T512_d3_plane_sparse"]
+CASES = HARD_CASES + PAIR_CASES
 
 
 @pytest.fixture(scope="module")
@@ -22,7 +27,9 @@ def gold():
 def _case(gold, name):
     g = {k.split("/", 1)[1]: torch.from_numpy(gold[k]) for k in gold.files if k.startswith(name + "/")}
     T, d, h, dm, nb, n, r, plane = [int(x) for x in g["meta"]]
-    return g, dict(T=T, d=d, h=h, dm=dm, nb=nb, n=n, r=r, mode="plane" if plane else "point")
+    anneal, sparse = (float(x) for x in g["opts"]) if "opts" in g else (1.0, 0.0)
+    return g, dict(T=T, d=d, h=h, dm=dm, nb=nb, n=n, r=r, mode="plane" if plane else "point",
+                   anneal=anneal, sparse=bool(sparse))
 
 
 def _module(meta, device="cpu"):
@@ -30,10 +37,22 @@ def _module(meta, device="cpu"):
     spec = build_mask(meta["T"], meta["d"], chunk=64)
     torch.manual_seed(1000)
     m = ContentAssign(meta["h"], meta["dm"], spec, mode=meta["mode"])
+    m.anneal = meta["anneal"]
+    m.sparse_ops = meta["sparse"]
     return m.to(device), spec
 
 
-@pytest.mark.parametrize("name", CASES)
+def _plane_tables(spec):
+    from smat_attention_amd.assign import grouped_planes
+    _, grouped = grouped_planes(spec.q, spec.dim)
+    M = torch.zeros(grouped.shape[0], grouped.shape[1], spec.N0)
+    for e in range(grouped.shape[0]):
+        for o in range(grouped.shape[1]):
+            M[e, o, grouped[e, o]] = 1.0
+    return M, M.argmax(1)
+
+
+@pytest.mark.parametrize("name", HARD_CASES)
 def test_oracle_reproduces_reference_fixtures(gold, name):
     g, meta = _case(gold, name)
     spec = build_mask(meta["T"], meta["d"], chunk=64)
@@ -43,14 +62,7 @@ def test_oracle_reproduces_reference_fixtures(gold, name):
                  torch.tensor([spec.q ** (spec.dim - l) for l in range(1, spec.dim + 1)]))
     cq, _ = R.cells(g["u"][:, n:], g["W"], g["gamma"], g["b"], spec.q, spec.dim, h)
     assert torch.equal(ck, g["ck"]) and torch.equal(cq, g["cq"])
-    M = None
-    if meta["mode"] == "plane":
-        from smat_attention_amd.assign import grouped_planes
-        _, grouped = grouped_planes(spec.q, spec.dim)
-        M = torch.zeros(grouped.shape[0], grouped.shape[1], spec.N0)
-        for e in range(grouped.shape[0]):
-            for o in range(grouped.shape[1]):
-                M[e, o, grouped[e, o]] = 1.0
+    M = _plane_tables(spec)[0] if meta["mode"] == "plane" else None
     y = R.dense_read(g["Phi"], g["Psi"], g["Vb"], n, ck, cq, spec.N0, mode=meta["mode"], M=M,
                      Wd=g.get("Wd"), u=g["u"], h=h)
     rel = (y - g["y"]).abs().max() / g["y"].abs().max()
@@ -107,8 +119,12 @@ def test_content_assign_on_gpu(gold, name):
     assert abs(float(m.aux.detach()) - float(g["aux"])) < 1e-5
 
 
-GRAD_CASES = ["T512_d3_point", "T512_d2_point"]
+GRAD_CASES = ["T512_d3_point", "T512_d2_point"] + PAIR_CASES
 GRAD_KEYS = ("du", "dPhi", "dPsi", "dVb", "dW", "dgamma", "db")
+
+
+def _grad_keys(meta):
+    return GRAD_KEYS + (("dWd",) if meta["mode"] == "plane" else ())
 
 
 def _grads(fn, g, meta, params):
@@ -116,7 +132,7 @@ def _grads(fn, g, meta, params):
     y = fn(xs, params)
     (y * g["R"].to(y.dtype).to(y.device)).sum().backward()
     out = {"d" + k: xs[k].grad.detach().cpu() for k in ("u", "Phi", "Psi", "Vb")}
-    out.update({"d" + k: params[k].grad.detach().cpu() for k in ("W", "gamma", "b")})
+    out.update({"d" + k: params[k].grad.detach().cpu() for k in params})
     return y.detach().cpu(), out
 
 
@@ -124,7 +140,7 @@ def _grel(a, b):
     return ((a.double() - b.double()).abs().max() / b.double().abs().max().clamp_min(1e-30)).item()
 
 
-@pytest.mark.parametrize("name", GRAD_CASES)
+@pytest.mark.parametrize("name", ["T512_d3_point", "T512_d2_point"])
 def test_oracle_gradients_match_reference_fixtures(gold, name):
     """The oracle's dense straight-through restatement, under autograd, gives the
     reference module's gradients (fixtures of assign.py's own backward)."""
@@ -159,11 +175,15 @@ def test_content_assign_gradients_on_gpu(gold, name):
     def fn(xs, p_):
         return m(xs["u"], xs["Phi"], xs["Psi"], xs["Vb"], meta["n"])
     prm = {"W": m.W, "gamma": m.gamma, "b": m.b}
+    if meta["mode"] == "plane":
+        with torch.no_grad():
+            m.Wd.copy_(g["Wd"].to(dev))
+        prm["Wd"] = m.Wd
     y, gr = _grads(fn, gd, meta, prm)
     assert _grel(y, g["y"]) < 1e-5
     assert abs(float(m.aux.detach()) - float(g["aux"])) < 1e-5
     assert torch.equal(m.last_hard_k.cpu(), g["ck"].long())
-    for k in GRAD_KEYS:
+    for k in _grad_keys(meta):
         assert _grel(gr[k], g[k]) < 1e-4, (k, _grel(gr[k], g[k]))
 
 
@@ -177,6 +197,9 @@ def test_plane_mode_gradients_raise():
     Phi = torch.rand(2, 512, 8)
     Vb = torch.rand(2, 512, 9)
     with pytest.raises(NotImplementedError, match="plane"):
+        m(u, Phi, Phi, Vb, 256)
+    m.sparse_ops = True         # the coset read trains, on the GPU
+    with pytest.raises(ValueError, match="GPU"):
         m(u, Phi, Phi, Vb, 256)
 
 
@@ -218,3 +241,105 @@ def test_content_assign_gradients_head_dim_128():
     assert _grel(y1, y0) < 1e-5
     for k in GRAD_KEYS:
         assert _grel(g1[k], g0[k]) < 1e-4, (k, _grel(g1[k], g0[k]))
+
+
+@pytest.mark.parametrize("name", ["T512_d3_point", "T512_d2_point"] + PAIR_CASES)
+def test_oracle_pair_branch_matches_reference_fixtures(gold, name):
+    """The oracle's pair branch (soft weights, one-cell sparse pairs, coset
+    read) under CPU autograd gives the reference module's forward and
+    gradients, for every case the fixtures hold gradients of."""
+    g, meta = _case(gold, name)
+    spec = build_mask(meta["T"], meta["d"], chunk=64)
+    pc = torch.tensor([spec.q ** (spec.dim - l) for l in range(1, spec.dim + 1)])
+    keys = ("W", "gamma", "b") + (("Wd",) if meta["mode"] == "plane" else ())
+    prm = {k: g[k].clone().requires_grad_(True) for k in keys}
+    M, coset_of = _plane_tables(spec) if meta["mode"] == "plane" else (None, None)
+
+    def fn(xs, p_):
+        return R.pairs_branch(xs["u"], xs["Phi"], xs["Psi"], xs["Vb"], meta["n"], p_["W"],
+                              p_["gamma"], p_["b"], spec.q, spec.dim, meta["h"], spec.N0,
+                              anneal=meta["anneal"], single=meta["sparse"],
+                              planted_cols=spec.planted_cols, plant_cells=pc, mode=meta["mode"],
+                              M=M, Wd=p_.get("Wd"), coset_of=coset_of)
+    y, gr = _grads(fn, g, meta, prm)
+    assert _grel(y, g["y"]) < 1e-5
+    for k in _grad_keys(meta):
+        assert _grel(gr[k], g[k]) < 1e-4, (k, _grel(gr[k], g[k]))
+
+
+def test_oracle_pair_maps_brute_force():
+    """The dense form of the pair maps against explicit loops:
+    F[b, x] = sum_{j,k: idx = x} w Psi_j Vb_j^T, y_i = sum_k w Phi_i F[idx_ik],
+    duplicates within a token included."""
+    gen = torch.Generator().manual_seed(5)
+    Bs, L, m, K, N0, r, p = 2, 6, 5, 3, 4, 2, 3
+    Psi, Vb, Phi = (torch.randn(Bs, L, r, generator=gen), torch.randn(Bs, L, p, generator=gen),
+                    torch.randn(Bs, m, r, generator=gen))
+    idk = torch.randint(0, N0, (Bs, L, K), generator=gen)
+    idk[0, 0, 1] = idk[0, 0, 0]
+    idq = torch.randint(0, N0, (Bs, m, K), generator=gen)
+    wk, wq = torch.randn(Bs, L, K, generator=gen), torch.randn(Bs, m, K, generator=gen)
+    F = torch.bmm(R.pairs_dense(idk, wk, N0).transpose(1, 2),
+                  torch.einsum("bnr,bnp->bnrp", Psi, Vb).reshape(Bs, L, r * p)).view(Bs, N0, r, p)
+    y = torch.einsum("bir,birp->bip", Phi,
+                     torch.bmm(R.pairs_dense(idq, wq, N0), F.reshape(Bs, N0, r * p)).view(Bs, m, r, p))
+    Fl = torch.zeros(Bs, N0, r, p)
+    for b in range(Bs):
+        for j in range(L):
+            for k in range(K):
+                Fl[b, idk[b, j, k]] += wk[b, j, k] * torch.outer(Psi[b, j], Vb[b, j])
+    yl = torch.zeros(Bs, m, p)
+    for b in range(Bs):
+        for i in range(m):
+            for k in range(K):
+                yl[b, i] += wq[b, i, k] * (Phi[b, i] @ Fl[b, idq[b, i, k]])
+    assert torch.allclose(F, Fl, atol=1e-5) and torch.allclose(y, yl, atol=1e-5)
+
+
+def test_pool_ops_refuse_cpu_tensors_and_bad_cells():
+    from smat_attention_amd import pool_ops
+    Psi = torch.rand(1, 4, 2)
+    idx = torch.zeros(1, 4, 1, dtype=torch.long)
+    with pytest.raises(ValueError, match="GPU"):
+        pool_ops.pool_segmented(Psi, Psi, idx, torch.ones(1, 4, 1), 3)
+    with pytest.raises(ValueError, match="cell indices"):
+        pool_ops._check("pool_segmented", idx + 3, torch.ones(1, 4, 1), 3, 4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,r,p", [(1, 16, 17), (4, 16, 17), (8, 128, 129)])
+def test_pool_ops_match_dense_maps(K, r, p):
+    """pool_segmented / read_gather (HIP list kernels, fp32) and every gradient
+    against the dense maps under fp64 CPU autograd (the reference's own
+    exactness check, smat_pool_ops.py:94-117), repeated cells included."""
+    from smat_attention_amd import pool_ops
+    gen = torch.Generator().manual_seed(10 + K)
+    Bs, n, m, N0 = 3, 300, 200, 7
+    Psi, Vb, Phi = (torch.randn(Bs, n, r, generator=gen), torch.randn(Bs, n, p, generator=gen),
+                    torch.randn(Bs, m, r, generator=gen))
+    idk, idq = (torch.randint(0, N0, (Bs, n, K), generator=gen),
+                torch.randint(0, N0, (Bs, m, K), generator=gen))
+    wk, wq = torch.rand(Bs, n, K, generator=gen), torch.rand(Bs, m, K, generator=gen)
+    R_ = torch.randn(Bs, m, p, generator=gen)
+    ins = {"Psi": Psi, "Vb": Vb, "Phi": Phi, "wk": wk, "wq": wq}
+
+    def run(dev, dt, pool, read):
+        xs = {k: v.to(dev, dt).requires_grad_(True) for k, v in ins.items()}
+        F = pool(xs["Psi"], xs["Vb"], idk.to(dev), xs["wk"], N0)
+        y = read(xs["Phi"], idq.to(dev), xs["wq"], F)
+        (y * R_.to(dev, dt)).sum().backward()
+        return y.detach().cpu(), {k: v.grad.detach().cpu() for k, v in xs.items()}
+
+    def dpool(Ps, V, idx, w, N0_):
+        return torch.bmm(R.pairs_dense(idx, w, N0_).transpose(1, 2),
+                         torch.einsum("bnr,bnp->bnrp", Ps, V).reshape(Bs, n, r * p)).view(Bs, N0_, r, p)
+
+    def dread(Ph, idx, w, F):
+        U = torch.bmm(R.pairs_dense(idx, w, F.shape[1]), F.reshape(Bs, F.shape[1], r * p))
+        return torch.einsum("bir,birp->bip", Ph, U.view(Bs, m, r, p))
+    y0, g0 = run("cpu", torch.float64, dpool, dread)
+    y1, g1 = run(torch.device("cuda:0"), torch.float32, pool_ops.pool_segmented,
+                 pool_ops.read_gather)
+    assert _grel(y1, y0) < 1e-5
+    for k in g0:
+        assert _grel(g1[k], g0[k]) < 1e-5, (k, _grel(g1[k], g0[k]))
