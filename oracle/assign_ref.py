@@ -181,14 +181,19 @@ def pairs_dense(idx, w, N0: int):
 
 def pairs_branch(u, Phi, Psi, Vb, n: int, W, gamma, b, q: int, dim: int, h: int, N0: int, *,
                  anneal: float = 1.0, single: bool = False, planted_cols=None,
-                 plant_cells=None, mode: str = "point", M=None, Wd=None, coset_of=None):
+                 plant_cells=None, mode: str = "point", M=None, Wd=None, coset_of=None,
+                 dir_soft: bool = False):
     """The long-range term over (cell, weight) pairs with autograd: the dense
-    read with the soft cell weights (assign.py:431-442) and the ``sparse_ops``
-    path (:378-406) -- ``F = Wk^T (Psi (x) Vb)``, point ``y = Phi (Wq F)``;
-    plane: ``Fc = M F`` summed to the direction cosets, the direction the
-    argmax of ``softmax(u Wd)`` with the straight-through factor
-    ``1 + pmax - pmax.detach()``, each query pair read at (direction, coset of
-    its cell).  Returns (nb*h, T - n, p)."""
+    read with the cell weights of any anneal (assign.py:431-472) and, with
+    ``single``, the ``sparse_ops`` path (:378-406) -- ``F = Wk^T (Psi (x) Vb)``,
+    point ``y = Phi (Wq F)``.  Plane, sparse: ``Fc = M F`` summed to the
+    direction cosets, the direction the argmax of ``softmax(u Wd)`` with the
+    straight-through factor ``1 + pmax - pmax.detach()``, each query pair read
+    at (direction, coset of its cell).  Plane, dense: ``Z = Phi (M F)`` for
+    every (direction, offset), mixed by the direction weights ``we`` (the
+    straight-through one-hot of the softmax, or the softmax with
+    ``dir_soft``) and the straight-through one-hot ``wo`` of the coset
+    marginal ``Wq M``.  Returns (nb*h, T - n, p)."""
     planted = planted_cols is not None and any(int(c) < n for c in planted_cols)
     # a planted key side is planted into the full pairs (assign.py:306-310)
     idxk, wk = soft_pairs(hash_s(u[:, :n], W, gamma, b, q, h), q, dim, anneal,
@@ -205,10 +210,18 @@ def pairs_branch(u, Phi, Psi, Vb, n: int, W, gamma, b, q: int, dim: int, h: int,
         Uq = torch.bmm(pairs_dense(idxq, wq, N0), F.reshape(Bs, N0, r * p)).view(Bs, -1, r, p)
         return torch.einsum("bir,birp->bip", Phi_r, Uq)
     D, nc = M.shape[0], M.shape[1]
-    Fc = torch.einsum("eox,bxrp->beorp", M, F).reshape(Bs, D * nc, r * p)
     T_R = Phi_r.shape[1]
     dl = torch.einsum("blm,hem->bhle", u[:, n:], Wd).reshape(Bs, T_R, D)
     pe = torch.softmax(dl, dim=-1)
+    if not single:
+        U = torch.einsum("eox,bxrp->beorp", M, F)
+        Z = torch.einsum("bir,beorp->bieop", Phi_r, U)
+        we = pe if dir_soft else \
+            torch.zeros_like(pe).scatter_(-1, pe.argmax(-1, keepdim=True), 1.0) + (pe - pe.detach())
+        po = torch.einsum("bix,eox->bieo", pairs_dense(idxq, wq, N0), M)
+        wo = torch.zeros_like(po).scatter_(-1, po.argmax(-1, keepdim=True), 1.0) + (po - po.detach())
+        return torch.einsum("bie,bieo,bieop->bip", we, wo, Z)
+    Fc = torch.einsum("eox,bxrp->beorp", M, F).reshape(Bs, D * nc, r * p)
     e_star = pe.argmax(-1, keepdim=True)
     pmax = pe.gather(-1, e_star)
     ste = 1.0 + (pmax - pmax.detach())

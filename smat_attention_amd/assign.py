@@ -22,14 +22,15 @@ GPU work per call:
 
 Supported: ``mode`` point/plane (codim 1 or dim), ``src`` hidden/embed/id,
 ``shift``, ``plant``, ``freeze``, the linear direction head, ``dir_override``,
-the hard mask (``anneal = 1``).  Parameters are created in the reference's
+``dir_soft``, ``anneal`` in [0, 1], ``sparse_ops`` (with ``hard_k1``).  Parameters are created in the reference's
 order, so a module built after ``torch.manual_seed(s)`` holds the reference's
-values.  Point mode trains: the hash runs under torch autograd and the
-pool, the read and their gradients run on the list kernels, with the
-straight-through gradient of the reference's dense path (see ``_PointRead``).
-The plane read is forward-only and raises ``NotImplementedError`` when a
-gradient is asked of it; options outside the list raise the same at
-construction.
+values.  Both reads train, with the reference's gradients: the hash runs
+under torch autograd and the pool, the reads and their gradients run on the
+list and incidence kernels (see ``_forward_grad``), for the dense read at
+any ``anneal`` (the soft phase included), ``dir_soft`` and ``dir_override``,
+and for the ``sparse_ops`` pair path.  Options outside the list
+(``conv_width > 1``, other direction heads, ``delta_updates``) raise
+``NotImplementedError``.
 """
 from __future__ import annotations
 
@@ -38,7 +39,7 @@ import torch
 import torch.nn as nn
 
 from .kernels.hip_fwd import _code, _on_gpu, _rows3, call, stream_of
-from .pool_ops import _gram_lists, _read_lists, _read_pairs, pool_sorted, read_sorted
+from .pool_ops import _gram_lists, _read_lists, _read_pairs, _repeat, pool_sorted, read_sorted
 
 __all__ = ["ContentAssign", "grouped_planes"]
 
@@ -184,21 +185,17 @@ class ContentAssign(nn.Module):
                 dir_override=None, ids=None):
         """u: (nb, T, d_model) layer input; Phi, Psi: (nb*h, T, r); Vb: (nb*h, T, p);
         n: landmark/recent boundary.  Returns fp32 (nb*h, T - n, p)."""
-        sparse = bool(getattr(self, "sparse_ops", False))
-        if self.mode == "plane" and not sparse and torch.is_grad_enabled() and (
-                any(t is not None and t.requires_grad for t in (u, Phi, Psi, Vb, emb, key_src))
-                or any(prm.requires_grad for prm in self.parameters())):
-            raise NotImplementedError("ContentAssign: gradients of the dense plane read are not "
-                                      "implemented; set sparse_ops, or use torch.no_grad()")
+        if getattr(self, "delta_updates", False):
+            raise NotImplementedError("ContentAssign: delta_updates (the delta-rule pool)")
         _on_gpu("ContentAssign", u, Phi, Psi, Vb, emb, key_src, key_w, ids)
-        if self.src != "id" and (self.anneal < 1.0 or getattr(self, "sparse_ops", False)):
-            # the id hash is one-hot whatever the anneal and always reads densely
-            # (assign.py:359-364)
-            return self._forward_pairs(u, Phi, Psi, Vb, n, emb, key_src, key_w, ids, dir_override)
-        if torch.is_grad_enabled() and (
+        soft = self.src != "id" and (self.anneal < 1.0 or getattr(self, "sparse_ops", False))
+        # dir_soft mixes the directions in training mode, with or without grad
+        soft = soft or (self.mode == "plane" and getattr(self, "dir_soft", False) and self.training
+                        and dir_override is None and getattr(self, "dir_ovr", None) is None)
+        if soft or (torch.is_grad_enabled() and (
                 any(t is not None and t.requires_grad for t in (u, Phi, Psi, Vb, emb, key_src))
-                or any(prm.requires_grad for prm in self.parameters())):
-            return self._forward_train(u, Phi, Psi, Vb, n, emb, key_src, key_w, ids)
+                or any(prm.requires_grad for prm in self.parameters()))):
+            return self._forward_grad(u, Phi, Psi, Vb, n, emb, key_src, key_w, ids, dir_override)
         if self.src == "id":
             assert ids is not None, "the id hash needs token ids"
             ik = ids if not self.shift else torch.cat(
@@ -314,72 +311,79 @@ class ContentAssign(nn.Module):
         self.aux = None if self.freeze else aux_k + aux_q
         return ck, idxk, wk, cq, idxq, wq
 
-    def _forward_pairs(self, u, Phi, Psi, Vb, n, emb, key_src, key_w, ids, dir_override):
-        """The branch over (cell, weight) pairs: the soft phase of the dense
-        read (anneal < 1, assign.py:431-442 with the soft cell weights) and the
-        ``sparse_ops`` path (:378-406).  Pool and read are
-        :func:`pool_sorted` / :func:`read_sorted` (HIP list kernels, with
-        gradients); the plane read aggregates F to the direction cosets with the
-        incidence kernel first."""
+    def _forward_grad(self, u, Phi, Psi, Vb, n, emb, key_src, key_w, ids, dir_override):
+        """The branch with the gradients of the reference's autograd, over the
+        (cell, weight) pairs of every token.
+
+        * the dense read (assign.py:431-472): at ``anneal = 1`` the forward
+          weights are one-hot, so the pool and the point read run over the
+          chosen cells (:class:`_HardPool`, :class:`_HardRead`) and the pairs
+          only enter the weight gradients; below, the soft pool and read
+          (:func:`pool_sorted` / :func:`read_sorted`); the plane read sums F to
+          the direction cosets (incidence kernel) and reads the chosen
+          (direction, offset) of each query (:class:`_PlaneRead`);
+        * the ``sparse_ops`` path (:378-406): pool and read over the pairs,
+          the plane read with the straight-through factor on the direction.
+
+        The hash is torch autograd on the dim values per token; every pool,
+        read and their gradients are HIP list kernels.  Returns fp32."""
         if getattr(self, "delta_updates", False):
             raise NotImplementedError("ContentAssign: delta_updates (the delta-rule pool)")
-        sparse = bool(getattr(self, "sparse_ops", False))
-        if self.mode == "plane" and not sparse:
-            raise NotImplementedError("ContentAssign: the dense plane read at anneal < 1; "
-                                      "set sparse_ops for the coset read")
+        sparse = bool(getattr(self, "sparse_ops", False)) and self.src != "id"
         ck, idxk, wk, cq, idxq, wq = self._pairs_of(u, n, emb, key_src, key_w, ids, sparse)
         self.last_hard_k = ck.detach()
         P, V, Phi_r = Psi[:, :n], Vb[:, :n], Phi[:, n:]
         dt = P.dtype
-        F = pool_sorted(P, V, idxk, wk.to(dt), self.N0)
-        if self.mode == "point":
-            return read_sorted(Phi_r, idxq, wq.to(dt), F)
-        from .kernels import hip_bwd
-        nrows = self.D * self.n_cosets
-        Fc = hip_bwd.incidence(F, self.coset_pts.to(F.device), nrows).to(F.dtype)
+        dev = Phi.device
         nbh, T_R = Phi_r.shape[0], Phi_r.shape[1]
+        nrows = self.D * self.n_cosets if self.mode == "plane" else 0
+        if sparse:
+            F = pool_sorted(P, V, idxk, wk.to(dt), self.N0)
+            if self.mode == "point":
+                return read_sorted(Phi_r, idxq, wq.to(dt), F).float()
+            from .kernels import hip_bwd
+            Fc = hip_bwd.incidence(F, self.coset_pts.to(dev), nrows).to(F.dtype)
+            if dir_override is not None:
+                e_star = dir_override.reshape(nbh, T_R, 1).long()
+                ste = torch.ones(nbh, T_R, 1, device=dev)
+            else:
+                dl = torch.einsum("blm,hem->bhle", u[:, n:], self.Wd.to(u.dtype)).reshape(
+                    nbh, T_R, self.D)
+                pe = torch.softmax(dl.float(), dim=-1)
+                e_star = pe.argmax(-1, keepdim=True)
+                pmax = pe.gather(-1, e_star)
+                ste = 1.0 + (pmax - pmax.detach())
+            coset = self.coset_of.to(dev)[e_star.expand_as(idxq), idxq]
+            y = read_sorted(Phi_r, e_star * self.n_cosets + coset, wq.to(dt), Fc)
+            return (y * ste.to(y.dtype)).float()
+        hard = self.anneal >= 1.0 or self.src == "id"
+        if hard:
+            F = _HardPool.apply(P, V, wk, idxk, ck, self.N0)
+        else:
+            F = pool_sorted(P, V, idxk, wk.to(dt), self.N0).float()
+        if self.mode == "point":
+            if hard:
+                return _HardRead.apply(Phi_r, F, wq, idxq, cq)
+            return read_sorted(Phi_r, idxq, wq.to(dt), F.to(dt)).float()
+        from .kernels import hip_bwd
+        U = hip_bwd.incidence(F, self.coset_pts.to(dev), nrows)
+        if dir_override is None:
+            dir_override = getattr(self, "dir_ovr", None)
         if dir_override is not None:
-            e_star = dir_override.reshape(nbh, T_R, 1).long()
-            ste = torch.ones(nbh, T_R, 1, device=u.device)
+            # the direction is given, not learned (assign.py:461-462)
+            we = torch.zeros(nbh, T_R, self.D, device=dev).scatter_(
+                -1, dir_override.reshape(nbh, T_R, 1).long(), 1.0)
         else:
-            dl = torch.einsum("blm,hem->bhle", u[:, n:], self.Wd.to(u.dtype)).reshape(nbh, T_R,
-                                                                                     self.D)
-            pe = torch.softmax(dl.float(), dim=-1)
-            e_star = pe.argmax(-1, keepdim=True)
-            pmax = pe.gather(-1, e_star)
-            ste = 1.0 + (pmax - pmax.detach())
-        coset = self.coset_of.to(u.device)[e_star.expand_as(idxq), idxq]
-        y = read_sorted(Phi_r, e_star * self.n_cosets + coset, wq.to(dt), Fc)
-        return y * ste.to(y.dtype)
-
-    def _forward_train(self, u, Phi, Psi, Vb, n, emb, key_src, key_w, ids):
-        """The branch with gradients (point mode): the hash is torch autograd on
-        the 16 dim values per token, the pool, the read and all their gradients
-        are HIP (:class:`_PointRead`)."""
-        if self.mode != "point":
-            raise NotImplementedError("ContentAssign: gradients of the plane read are not "
-                                      "implemented; use mode='point' or torch.no_grad()")
-        if self.src == "id":
-            assert ids is not None, "the id hash needs token ids"
-            ik = ids if not self.shift else torch.cat(
-                [ids.new_zeros(ids.shape[0], self.shift), ids[:, :-self.shift]], dim=1)
-            ck, cq = self._cells_id(ik[:, :n]), self._cells_id(ids[:, n:])
-            idxk, idxq = ck.unsqueeze(-1), cq.unsqueeze(-1)
-            wk = torch.ones(idxk.shape, device=u.device)
-            wq = torch.ones(idxq.shape, device=u.device)
-            self.aux = None
-        else:
-            h = u if (self.src == "hidden" or emb is None) else emb
-            hk = h if key_src is None else key_src
-            if self.shift:
-                hk = torch.cat([h.new_zeros(h.shape[0], self.shift, h.shape[2]),
-                                h[:, :-self.shift]], dim=1)
-            ck, idxk, wk, aux_k = self._ste_pairs(self._soft_hash(hk[:, :n]), plant_at=True,
-                                                  tok_w=key_w)
-            cq, idxq, wq, aux_q = self._ste_pairs(self._soft_hash(h[:, n:]))
-            self.aux = None if self.freeze else aux_k + aux_q
-        self.last_hard_k = ck.detach()
-        return _PointRead.apply(Phi, Psi, Vb, wk, wq, idxk, idxq, ck, cq, n, self.N0)
+            dl = torch.einsum("blm,hem->bhle", u[:, n:], self.Wd).reshape(nbh, T_R, self.D)
+            self.last_dir_logits = dl
+            pe = torch.softmax(dl, dim=-1)
+            if getattr(self, "dir_soft", False) and self.training:
+                we = pe
+            else:
+                we = torch.zeros_like(pe).scatter_(-1, pe.argmax(-1, keepdim=True), 1.0) + \
+                    (pe - pe.detach())
+        return _PlaneRead.apply(Phi_r, U, we.float(), wq, idxq, self.coset_of.to(dev),
+                                self.n_cosets)
 
     def _read(self, u, Phi, Psi, Vb, n, ck, cq, dir_override):
         nbh, T, r = Phi.shape
@@ -437,52 +441,136 @@ class ContentAssign(nn.Module):
 # The hard point branch with its gradients (HIP)
 # ---------------------------------------------------------------------------
 
-class _PointRead(torch.autograd.Function):
-    """The point read of the content-addressed branch with the dense path's
-    gradients (assign.py:431-446 under autograd): forward
-    ``F_x = sum_{ck_j = x} Psi_j^T Vb_j``, ``y_i = Phi_i F_{cq_i}`` over the
-    chosen cells; backward, with the pair weights w (forward one-hot):
+def _one_hot_first(w):
+    """Whether the forward weights put 1 on each row's first pair and 0 elsewhere."""
+    return bool((w[..., 0] == 1).all()) and bool((w[..., 1:] == 0).all())
 
-        dF_x   = sum_{cq_i = x} Phi_i^T dy_i          dPhi_i = F_{cq_i} dy_i
-        dPsi_j = dF_{ck_j} Vb_j                      dVb_j  = dF_{ck_j}^T Psi_j
-        dwq_ik = Phi_i . (F_{idxq_ik} dy_i)          dwk_jk = Psi_j . (dF_{idxk_jk} Vb_j)
 
-    Every product is a HIP list-Gram or list-read; the transposed tables are
-    copies.  Landmark rows of Phi and recent rows of Psi, Vb get zero."""
+class _HardPool(torch.autograd.Function):
+    """The dense pool with one-hot forward weights (assign.py:431-436 at
+    ``anneal = 1``): ``F_x = sum_{ck_j = x} Psi_j^T Vb_j``; backward
+    ``dPsi_j = dF[ck_j] Vb_j``, ``dVb_j = dF[ck_j]^T Psi_j`` and, for every
+    pair, ``dw_jk = Psi_j . (dF[idx_jk] Vb_j)``.  fp32 F."""
 
     @staticmethod
-    def forward(ctx, Phi, Psi, Vb, wk, wq, idxk, idxq, ck, cq, n, N0):
-        nbh, T, r = Phi.shape
-        p = Vb.shape[-1]
+    def forward(ctx, P, V, wk, idxk, ck, N0):
+        r, p = P.shape[-1], V.shape[-1]
         if r > 128 or p > 144:
             raise NotImplementedError("ContentAssign gradients: r <= 128, p <= 144")
-        Pk = Psi[:, :n].contiguous()
-        Vk = Vb[:, :n].contiguous()
-        Phr = Phi[:, n:].contiguous()
+        Pk, Vk = P.contiguous(), V.contiguous()
         F = _gram_lists(Pk, Vk, ck, N0)
-        Y = _read_lists(Phr, F, cq)
-        ctx.save_for_backward(Phr, Pk, Vk, F, idxk, idxq, ck, cq)
-        ctx.meta = (n, N0, Phi.shape, Phi.dtype, Psi.dtype, Vb.dtype, wk.dtype, wq.dtype)
+        ctx.save_for_backward(Pk, Vk, idxk, ck)
+        ctx.dtypes = (P.dtype, V.dtype, wk.dtype)
+        return F
+
+    @staticmethod
+    def backward(ctx, dF):
+        Pk, Vk, idxk, ck = ctx.saved_tensors
+        dF = dF.float().contiguous()
+        dFT = dF.transpose(-1, -2).contiguous()
+        P32, V32 = Pk.float(), Vk.float()
+        dPsi = _read_lists(V32, dFT, ck)
+        dVb = _read_lists(P32, dF, ck)
+        dwk = (_read_pairs(V32, dFT, idxk) * P32.unsqueeze(2)).sum(-1)
+        dp, dv, dw = ctx.dtypes
+        return dPsi.to(dp), dVb.to(dv), dwk.to(dw), None, None, None
+
+
+class _HardRead(torch.autograd.Function):
+    """The dense point read with one-hot forward weights (assign.py:437-441 at
+    ``anneal = 1``): ``y_i = Phi_i F[cq_i]``; backward ``dPhi_i = F[cq_i] dy_i``,
+    ``dF_x = sum_{cq_i = x} Phi_i^T dy_i`` and ``dw_ik = Phi_i . (F[idx_ik] dy_i)``."""
+
+    @staticmethod
+    def forward(ctx, Phr, F, wq, idxq, cq):
+        Phr = Phr.contiguous()
+        Y = _read_lists(Phr, F.contiguous(), cq)
+        ctx.save_for_backward(Phr, F, idxq, cq)
+        ctx.dtypes = (Phr.dtype, wq.dtype)
         return Y
 
     @staticmethod
     def backward(ctx, dY):
-        Phr, Pk, Vk, F, idxk, idxq, ck, cq = ctx.saved_tensors
-        n, N0, shape, d_phi, d_psi, d_vb, d_wk, d_wq = ctx.meta
-        nbh, T, r = shape
-        p = Vk.shape[-1]
+        Phr, F, idxq, cq = ctx.saved_tensors
         dY = dY.float().contiguous()
-        Ph32, P32, V32 = Phr.float(), Pk.float(), Vk.float()
-        dF = _gram_lists(Ph32, dY, cq, N0)
+        Ph32 = Phr.float()
         FT = F.transpose(-1, -2).contiguous()
-        dFT = dF.transpose(-1, -2).contiguous()
-        dPhi = torch.zeros(nbh, T, r, device=dY.device, dtype=torch.float32)
-        dPsi = torch.zeros(nbh, T, r, device=dY.device, dtype=torch.float32)
-        dVb = torch.zeros(nbh, T, p, device=dY.device, dtype=torch.float32)
-        dPhi[:, n:] = _read_lists(dY, FT, cq)
-        dPsi[:, :n] = _read_lists(V32, dFT, ck)
-        dVb[:, :n] = _read_lists(P32, dF, ck)
+        dPhi = _read_lists(dY, FT, cq)
+        dF = _gram_lists(Ph32, dY, cq, F.shape[1])
         dwq = (_read_pairs(dY, FT, idxq) * Ph32.unsqueeze(2)).sum(-1)
-        dwk = (_read_pairs(V32, dFT, idxk) * P32.unsqueeze(2)).sum(-1)
-        return (dPhi.to(d_phi), dPsi.to(d_psi), dVb.to(d_vb), dwk.to(d_wk), dwq.to(d_wq),
-                None, None, None, None, None, None)
+        dp, dw = ctx.dtypes
+        return dPhi.to(dp), dF, dwq.to(dw), None, None
+
+
+def _offset_rows(idxq, wq, coset_of, nc):
+    """(B, T_R, D) row ``e*nc + o*`` of every direction: o* the argmax over
+    offsets of the query's coset marginal ``po[e, o] = sum_k wq_k [coset(e,
+    idx_k) = o]`` (assign.py:466)."""
+    D = coset_of.shape[0]
+    base = torch.arange(D, device=idxq.device) * nc
+    if _one_hot_first(wq):
+        return base + coset_of[:, idxq[..., 0]].permute(1, 2, 0)
+    B, T_R, _ = idxq.shape
+    rows = torch.empty(B, T_R, D, dtype=torch.long, device=idxq.device)
+    for e in range(D):
+        po = torch.zeros(B, T_R, nc, device=idxq.device, dtype=wq.dtype)
+        po.scatter_add_(-1, coset_of[e][idxq], wq)
+        rows[..., e] = e * nc + po.argmax(-1)
+    return rows
+
+
+class _PlaneRead(torch.autograd.Function):
+    """The dense plane read (assign.py:443-472) under the reference's autograd:
+    ``y_i = sum_{e,o} we[i,e] wo[i,e,o] Phi_i U[e,o]`` with ``wo`` the
+    straight-through one-hot of the coset marginal ``po = Wq M`` and ``we``
+    the direction weights (straight-through one-hot of the softmax, the softmax
+    itself, or a given direction).  Forward reads the chosen offset of each
+    direction that carries weight; backward::
+
+        dPhi_i  = sum_e we[i,e] U[e,o*] dy_i     dU[e,o*] += we[i,e] Phi_i^T dy_i
+        dwe[i,e] = Phi_i U[e,o*(i,e)] dy_i      (every direction)
+        dwq_ik  = sum_e we[i,e] Phi_i U[e, coset(e, idx_ik)] dy_i
+
+    (the last is ``dpo`` through ``M`` back to the query's pair weights).
+    U: fp32 (B, D*nc, r, p) from the incidence kernel over the cosets."""
+
+    @staticmethod
+    def forward(ctx, Phr, U, we, wq, idxq, coset_of, nc):
+        P32 = Phr.float().contiguous()
+        U = U.contiguous()
+        we_f, wq_f = we.detach(), wq.detach()
+        rows = _offset_rows(idxq, wq_f, coset_of, nc)
+        onehot = bool(((we_f == 0) | (we_f == 1)).all()) and bool((we_f.sum(-1) == 1).all())
+        if onehot:
+            e_star = we_f.argmax(-1, keepdim=True)
+            y = _read_lists(P32, U, rows.gather(-1, e_star).squeeze(-1))
+        else:
+            y = (_read_pairs(P32, U, rows) * we_f.unsqueeze(-1)).sum(2)
+        ctx.save_for_backward(P32, U, we_f, idxq, rows, coset_of)
+        ctx.meta = (onehot, nc, Phr.dtype, we.dtype, wq.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        P32, U, we_f, idxq, rows, coset_of = ctx.saved_tensors
+        onehot, nc, d_phi, d_we, d_wq = ctx.meta
+        B, T_R, D = we_f.shape
+        K = idxq.shape[-1]
+        dy = dy.float().contiguous()
+        UT = U.transpose(-1, -2).contiguous()
+        Gy = _read_pairs(dy, UT, rows)                        # (B, T_R, D, r)
+        dwe = (Gy * P32.unsqueeze(2)).sum(-1)
+        dPhi = (Gy * we_f.unsqueeze(-1)).sum(2)
+        if onehot:
+            e_star = we_f.argmax(-1, keepdim=True)
+            dU = _gram_lists(P32, dy, rows.gather(-1, e_star).squeeze(-1), D * nc)
+            rk = e_star * nc + coset_of[e_star.expand_as(idxq), idxq]
+            dwq = (_read_pairs(dy, UT, rk) * P32.unsqueeze(2)).sum(-1)
+        else:
+            A = (P32.unsqueeze(2) * we_f.unsqueeze(-1)).reshape(B, T_R * D, -1)
+            dU = _gram_lists(A, _repeat(dy, D), rows.reshape(B, T_R * D), D * nc)
+            e = torch.arange(D, device=idxq.device).view(1, 1, D, 1)
+            rk = (e * nc + coset_of[e.expand(B, T_R, D, K), idxq.unsqueeze(2).expand(B, T_R, D, K)])
+            Z = (_read_pairs(dy, UT, rk.reshape(B, T_R, D * K)) * P32.unsqueeze(2)).sum(-1)
+            dwq = (Z.view(B, T_R, D, K) * we_f.unsqueeze(-1)).sum(2)
+        return dPhi.to(d_phi), dU, dwe.to(d_we), dwq.to(d_wq), None, None, None

@@ -11,10 +11,12 @@ outputs as data:
 
     assign_golden.npz   per case: u, Phi, Psi, Vb, W, gamma, b, [Wd], the key
                         cells (last_hard_k), the query cells (cells_of), the
-                        load-balance term aux and the forward output y; point
-                        and sparse_ops cases also R and the gradients of
+                        load-balance term aux and the forward output y; every
+                        case also R and the gradients of
                         (y * R).sum(): du, dPhi, dPsi, dVb, dW, dgamma, db
-                        (and dWd for the plane read)
+                        (and dWd for the plane read); an input equal to an
+                        earlier case's is stored once, the later case holding
+                        ``<key>.base``, the first holder's name, in its place
 
 Run from the repository root (needs /root/reference, numpy and torch):
 
@@ -44,7 +46,11 @@ CASES = [
     ("T512_d3_point_sparse", 512, 3, "point", 2, 64, 2, 1.0, True),
     ("T512_d3_point_sparse_soft", 512, 3, "point", 2, 64, 2, 0.5, True),
     ("T512_d3_plane_sparse", 512, 3, "plane", 2, 64, 2, 1.0, True),
+    ("T512_d3_plane_soft", 512, 3, "plane", 2, 64, 2, 0.5, False),
+    ("T512_d3_plane_dirsoft", 512, 3, "plane", 2, 64, 2, 1.0, False),
 ]
+DIR_SOFT = {"T512_d3_plane_dirsoft"}      # dir_soft mixes the directions in training mode
+SHARED = ("u", "Phi", "Psi", "Vb", "W", "gamma", "b", "Wd", "R")
 
 
 def _load(name, path):
@@ -68,6 +74,9 @@ def main():
         m.eval()
         m.anneal = anneal
         m.sparse_ops = sparse
+        if name in DIR_SOFT:
+            m.dir_soft = True
+            m.train()
         g = torch.Generator().manual_seed(2000)
         u = torch.randn(nb, T, dm, generator=g)
         Phi = torch.rand(nb * h, T, r, generator=g) + 0.5
@@ -90,22 +99,37 @@ def main():
         out[f"{name}/aux"] = np.array(float(m.aux))
         out[f"{name}/y"] = y.numpy()
         out[f"{name}/meta"] = np.array([T, d, h, dm, nb, n, r, 1 if mode == "plane" else 0])
-        out[f"{name}/opts"] = np.array([anneal, 1.0 if sparse else 0.0])
-        if mode == "point" or sparse:
-            # gradients of (y * R).sum() through the module's straight-through path
-            R = torch.randn(y.shape, generator=torch.Generator().manual_seed(3000))
-            xs = [t.detach().clone().requires_grad_(True) for t in (u, Phi, Psi, Vb)]
-            m.zero_grad()
-            yg = m(xs[0], xs[1], xs[2], xs[3], n)
-            (yg * R).sum().backward()
-            out[f"{name}/R"] = R.numpy()
-            for key, t in zip(("du", "dPhi", "dPsi", "dVb"), xs):
-                out[f"{name}/{key}"] = t.grad.numpy()
-            out[f"{name}/dW"] = m.W.grad.numpy()
-            out[f"{name}/dgamma"] = m.gamma.grad.numpy()
-            out[f"{name}/db"] = m.b.grad.numpy()
-            if mode == "plane":
-                out[f"{name}/dWd"] = m.Wd.grad.numpy()
+        out[f"{name}/opts"] = np.array([anneal, 1.0 if sparse else 0.0,
+                                        1.0 if name in DIR_SOFT else 0.0])
+        # gradients of (y * R).sum() through the module's straight-through path
+        R = torch.randn(y.shape, generator=torch.Generator().manual_seed(3000))
+        xs = [t.detach().clone().requires_grad_(True) for t in (u, Phi, Psi, Vb)]
+        m.zero_grad()
+        yg = m(xs[0], xs[1], xs[2], xs[3], n)
+        (yg * R).sum().backward()
+        out[f"{name}/R"] = R.numpy()
+        for key, t in zip(("du", "dPhi", "dPsi", "dVb"), xs):
+            out[f"{name}/{key}"] = t.grad.numpy()
+        out[f"{name}/dW"] = m.W.grad.numpy()
+        out[f"{name}/dgamma"] = m.gamma.grad.numpy()
+        out[f"{name}/db"] = m.b.grad.numpy()
+        if mode == "plane":
+            out[f"{name}/dWd"] = m.Wd.grad.numpy()
+    # cases built from the same seeds share their inputs: keep each once and
+    # point later cases at the first holder (``<case>/<key>.base``)
+    first = {}
+    for name, *_ in CASES:
+        for key in SHARED:
+            k = f"{name}/{key}"
+            if k not in out:
+                continue
+            hit = next((b for b in first.get(key, []) if np.array_equal(out[f"{b}/{key}"], out[k])),
+                       None)
+            if hit is None:
+                first.setdefault(key, []).append(name)
+            else:
+                del out[k]
+                out[f"{name}/{key}.base"] = np.array(hit)
     np.savez_compressed(os.path.join(HERE, "assign_golden.npz"), **out)
     print("wrote", len(CASES), "cases")
 

@@ -15,7 +15,7 @@ GOLD = os.path.join(os.path.dirname(__file__), "golden", "assign_golden.npz")
 # read, the sparse_ops path at anneal 1 (one cell per token) and below (2^dim)
 HARD_CASES = ["T512_d3_point", "T512_d3_plane", "T512_d2_point"]
 PAIR_CASES = ["T512_d3_point_soft", "T512_d3_point_sparse", "T512_d3_point_sparse_soft",
-              "T512_d3_plane_sparse"]
+              "T512_d3_plane_sparse", "T512_d3_plane_soft", "T512_d3_plane_dirsoft"]
 CASES = HARD_CASES + PAIR_CASES
 
 
@@ -25,11 +25,19 @@ def gold():
 
 
 def _case(gold, name):
-    g = {k.split("/", 1)[1]: torch.from_numpy(gold[k]) for k in gold.files if k.startswith(name + "/")}
+    g = {}
+    for k in gold.files:
+        if k.startswith(name + "/"):
+            key = k.split("/", 1)[1]
+            if key.endswith(".base"):      # an input stored once, under an earlier case
+                key = key[:-5]
+                g[key] = torch.from_numpy(gold[f"{gold[k]}/{key}"])
+            else:
+                g[key] = torch.from_numpy(gold[k])
     T, d, h, dm, nb, n, r, plane = [int(x) for x in g["meta"]]
-    anneal, sparse = (float(x) for x in g["opts"]) if "opts" in g else (1.0, 0.0)
+    anneal, sparse, dir_soft = (float(x) for x in g["opts"])
     return g, dict(T=T, d=d, h=h, dm=dm, nb=nb, n=n, r=r, mode="plane" if plane else "point",
-                   anneal=anneal, sparse=bool(sparse))
+                   anneal=anneal, sparse=bool(sparse), dir_soft=bool(dir_soft))
 
 
 def _module(meta, device="cpu"):
@@ -39,6 +47,9 @@ def _module(meta, device="cpu"):
     m = ContentAssign(meta["h"], meta["dm"], spec, mode=meta["mode"])
     m.anneal = meta["anneal"]
     m.sparse_ops = meta["sparse"]
+    if meta["dir_soft"]:
+        m.dir_soft = True
+        m.train()
     return m.to(device), spec
 
 
@@ -119,7 +130,7 @@ def test_content_assign_on_gpu(gold, name):
     assert abs(float(m.aux.detach()) - float(g["aux"])) < 1e-5
 
 
-GRAD_CASES = ["T512_d3_point", "T512_d2_point"] + PAIR_CASES
+GRAD_CASES = ["T512_d3_point", "T512_d2_point", "T512_d3_plane"] + PAIR_CASES
 GRAD_KEYS = ("du", "dPhi", "dPsi", "dVb", "dW", "dgamma", "db")
 
 
@@ -187,19 +198,19 @@ def test_content_assign_gradients_on_gpu(gold, name):
         assert _grel(gr[k], g[k]) < 1e-4, (k, _grel(gr[k], g[k]))
 
 
-def test_plane_mode_gradients_raise():
-    """The plane read is forward-only: asking it for gradients raises before
-    any kernel runs."""
+def test_content_assign_refuses_cpu_tensors_and_unbuilt_options():
+    """The module runs on the GPU only and says so before any kernel; the
+    delta-rule pool (an option outside the port) raises."""
     from smat_attention_amd.assign import ContentAssign
     spec = build_mask(512, 3, chunk=64)
     m = ContentAssign(2, 32, spec, mode="plane")
     u = torch.randn(1, 512, 32)
     Phi = torch.rand(2, 512, 8)
     Vb = torch.rand(2, 512, 9)
-    with pytest.raises(NotImplementedError, match="plane"):
-        m(u, Phi, Phi, Vb, 256)
-    m.sparse_ops = True         # the coset read trains, on the GPU
     with pytest.raises(ValueError, match="GPU"):
+        m(u, Phi, Phi, Vb, 256)
+    m.delta_updates = True
+    with pytest.raises(NotImplementedError, match="delta"):
         m(u, Phi, Phi, Vb, 256)
 
 
@@ -243,7 +254,7 @@ def test_content_assign_gradients_head_dim_128():
         assert _grel(g1[k], g0[k]) < 1e-4, (k, _grel(g1[k], g0[k]))
 
 
-@pytest.mark.parametrize("name", ["T512_d3_point", "T512_d2_point"] + PAIR_CASES)
+@pytest.mark.parametrize("name", GRAD_CASES)
 def test_oracle_pair_branch_matches_reference_fixtures(gold, name):
     """The oracle's pair branch (soft weights, one-cell sparse pairs, coset
     read) under CPU autograd gives the reference module's forward and
@@ -260,7 +271,8 @@ def test_oracle_pair_branch_matches_reference_fixtures(gold, name):
                               p_["gamma"], p_["b"], spec.q, spec.dim, meta["h"], spec.N0,
                               anneal=meta["anneal"], single=meta["sparse"],
                               planted_cols=spec.planted_cols, plant_cells=pc, mode=meta["mode"],
-                              M=M, Wd=p_.get("Wd"), coset_of=coset_of)
+                              M=M, Wd=p_.get("Wd"), coset_of=coset_of,
+                              dir_soft=meta["dir_soft"])
     y, gr = _grads(fn, g, meta, prm)
     assert _grel(y, g["y"]) < 1e-5
     for k in _grad_keys(meta):
