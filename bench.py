@@ -15,9 +15,11 @@ between two device synchronisations.  Printed: one JSON line with the
 throughput (tokens/s = B*T / step time), the roofline of the dominant kernel
 (timed live with events on the stream the kernels run on), the CPU baseline
 (the oracle's restatement of the reference's torch path, on a bounded
-sample, timed on this host) and the cached-decode rate.
+sample, timed on this host), the cached-decode rate and, outside the step,
+the time of one content-hashed training step (forward and backward, B=8,
+H=12, head_dim 64, T=4096, bf16, d = 2 and 3).
 
-    python bench.py [--steps K] [--warmup W] [--T 131072] [--no-cpu] [--no-decode]
+    python bench.py [--steps K] [--warmup W] [--T 131072] [--no-cpu] [--no-decode] [--no-train]
 """
 from __future__ import annotations
 
@@ -78,6 +80,7 @@ def parse():
                     help="heads in the CPU baseline sample (of --heads)")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-train", action="store_true", help="skip the training-step timing")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -194,6 +197,43 @@ def featurise_bench(nb, T, hd, reps):
     del Q, K, V, h
     return {"us": round(us, 1), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes,
             "config": f"nb={nb} T={T} d_qk=r=d_v={hd} bf16, elu+1 map, key gate"}
+
+
+def train_step_bench(d, reps, B=8, H=12, hd=64, T=4096):
+    """One training step of the content-hashed layer, forward and backward, on
+    bf16 q, k, v ~ N(0, 1) (k scaled by 1/sqrt(hd)) and an fp32 hidden state
+    the hash reads (d_model = H*hd), upstream gradient ~ N(0, 1): the feature
+    map, the segmented causal scan plus the content-addressed long-range term
+    on the recent rows, the single division (model.py:300-311), then
+    backward to q, k, v, the hidden state and the hash parameters."""
+    import torch
+    from smat_attention_amd import attention as A
+    from smat_attention_amd.assign import ContentAssign
+    from smat_attention_amd.mask import build_mask
+    dev = torch.device("cuda:0")
+    spec = build_mask(T, d, chunk=128)
+    n = spec.n
+    gen = torch.Generator(device="cpu").manual_seed(2)
+    bf = torch.bfloat16
+    Q = torch.randn(B * H, T, hd, generator=gen).to(dev, bf).requires_grad_(True)
+    K = (torch.randn(B * H, T, hd, generator=gen) / hd ** 0.5).to(dev, bf).requires_grad_(True)
+    V = torch.randn(B * H, T, hd, generator=gen).to(dev, bf).requires_grad_(True)
+    X = torch.randn(B, T, H * hd, generator=gen).to(dev).requires_grad_(True)
+    dO = torch.randn(B * H, T, hd, generator=gen).to(dev, bf)
+    torch.manual_seed(7)
+    m = ContentAssign(H, H * hd, spec, mode="point").to(dev)
+    phi = A.make_phi(hd, hd, device=dev, dtype=bf, seed=0)
+
+    def step():
+        Phi, Psi, Vb = A.featurise(Q, K, V, phi)
+        Hs = A.segmented_causal_scan(Phi, Psi, Vb, n, 128)
+        Hs = torch.cat([Hs[:, :n], Hs[:, n:] + m(X, Phi, Psi, Vb, n)], dim=1)
+        o = Hs[..., :-1] / Hs[..., -1:].clamp_min(1e-6)
+        (o.to(bf) * dO).float().sum().backward()
+    us = Events(torch).time(step, reps)
+    return {"ms": round(us / 1e3, 3), "tokens_per_s": round(B * T / (us * 1e-6), 1),
+            "config": f"B={B} H={H} head_dim={hd} T={T} d={d} bf16, content-hashed point read, "
+                      f"fwd+bwd"}
 
 
 def useful_flops(spec, nb, T, r, p, C=128):
@@ -388,8 +428,16 @@ def main():
     }
     result["featurise"] = featurise_bench(nb, T, hd, args.kernel_reps)
     log(f"[bench] featurise {result['featurise']}")
+    if not args.no_train:
+        del ws, out
+        torch.cuda.empty_cache()
+        result["train_step"] = {f"d{d}": train_step_bench(d, max(3, args.kernel_reps // 2))
+                                for d in (2, 3)}
+        log(f"[bench] train step {result['train_step']}")
     if not args.no_decode:
-        del Phi, Psi, Vb, ws, out
+        del Phi, Psi, Vb
+        if args.no_train:
+            del ws, out
         torch.cuda.empty_cache()
         result["decode"] = decode_bench(args)
         log(f"[bench] decode {result['decode']}")

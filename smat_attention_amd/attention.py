@@ -82,6 +82,10 @@ def _acc(x: torch.Tensor, acc_dtype, who: str) -> torch.dtype:
 # feature map (attention.py:82-106)
 # ---------------------------------------------------------------------------
 
+def _wants_grad(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
 class FeatureMap:
     """The map ``x -> elu(x W^T) + 1`` (or ``relu(x W^T) + 1e-3``) that
     :func:`make_phi` returns: callable like the reference's closure
@@ -94,6 +98,9 @@ class FeatureMap:
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         if x.is_cuda:
+            if _wants_grad(x, self.W):
+                from .kernels.hip_bwd import FeaturiseFunction
+                return FeaturiseFunction.apply(self.W, self.kind, x, None, None, None)[0]
             return _hip.featurise(self.W, self.kind, x)[0]
         y = x @ self.W.T
         if self.kind == "elu1":
@@ -124,9 +131,14 @@ def featurise(Q, K, V, phi, *, g=None, h=None):
     reference (the output gate is applied by :func:`smat_attention`).  Any
     other callable is the caller's own map and is called as given.  ``Vb`` is
     returned as a view whose rows start on 16-byte boundaries (row stride
-    rounded up to 8 elements).
+    rounded up to 8 elements).  Gradients reach Q, K, V, h and W as in the
+    reference (an autograd node around the launch).
     """
     if isinstance(phi, FeatureMap) and Q.is_cuda:
+        if _wants_grad(Q, K, V, h, phi.W):
+            # the HIP launch forward, the map's derivative backward
+            from .kernels.hip_bwd import FeaturiseFunction
+            return FeaturiseFunction.apply(phi.W, phi.kind, Q, K, V, h)
         return _hip.featurise(phi.W, phi.kind, Q, K, V, h)
     Phi = phi(Q)
     Psi = phi(K)
@@ -281,11 +293,22 @@ def segmented_causal_scan(Phi, Psi, Vb, n: int, chunk: int = 128,
     who = "segmented_causal_scan"
     _backend(backend, who)
     _acc(Phi, acc_dtype, who)
-    nb, T, r = Phi.shape
-    p = Vb.shape[-1]
+    T = Phi.shape[1]
     C = min(chunk, T)
     if n % C:
         raise ValueError(f"segment boundary n={n} is not a multiple of chunk={C}")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (Phi, Psi, Vb)):
+        # the reference differentiates its torch path; here one autograd node
+        # with the HIP backward
+        from .kernels.hip_bwd import CausalScanFunction
+        return CausalScanFunction.apply(Phi, Psi, Vb, n, C,
+                                        lambda P, S, V: _causal_scan(P, S, V, n, C))
+    return _causal_scan(Phi, Psi, Vb, n, C)
+
+
+def _causal_scan(Phi, Psi, Vb, n: int, C: int):
+    nb, T, r = Phi.shape
+    p = Vb.shape[-1]
     if C <= 128:
         return _hip.causal_scan(Phi, Psi, Vb, n, C, write_H=True)
     # wide chunks: summaries, scan and chunk-local pass as separate kernels

@@ -98,46 +98,19 @@ def _incidence_rows(src, idx, indptr, n_out, nb, n_in, rp):
     return out
 
 
-def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=None,
-                        need_dg: bool = False):
-    """``(dPhi, dPsi, dVb, dg)`` of ``out = smat_attention(Phi, Psi, Vb, spec, g=g)``
-    given the forward's ``U`` (nb, B, r, p) and ``H`` (nb, T, p, long-range
-    term included), fp32 gradients."""
-    nb, T, r = Phi.shape
-    p = Vb.shape[-1]
-    C = min(chunk, T)
-    n, n_P, N0, B = spec.n, spec.n_P, spec.N0, spec.B
-    T_R = T - n
-    dev = Phi.device
-    nc = -(-T // C)
-    Tp = nc * C
-
-    # ---- normalise --------------------------------------------------------
-    dout = dout.float().contiguous()
-    H = H.float().contiguous()
-    dH = torch.zeros(nb, Tp, p, device=dev, dtype=torch.float32)      # rows >= T stay 0
-    dg = torch.empty(nb, T, device=dev, dtype=torch.float32) if need_dg else None
-    gc = g.float().contiguous() if g is not None else None
-    call("smat_normalise_backward", dout.data_ptr(), H.data_ptr(), ptr(gc), dH.data_ptr(),
-         ptr(dg), nb, T, p, dout.stride(0), dout.stride(1), H.stride(0), H.stride(1),
-         dH.stride(0), dH.stride(1), gc.stride(0) if gc is not None else 0, stream_of(dH))
-
-    # inputs padded to whole chunks (zeros contribute nothing)
-    def padded(x):
-        x = x.contiguous()
-        if Tp == T:
-            return x
-        out = torch.zeros(nb, Tp, x.shape[-1], device=dev, dtype=x.dtype)
-        out[:, :T] = x
-        return out
-
-    Ph, Ps, Vv = padded(Phi), padded(Psi), padded(Vb)
-
+def causal_scan_grad(Ph, Ps, Vv, dH, n: int, C: int):
+    """``(dPhi, dPsi, dVb)`` of the segmented causal scan ``H`` (attention.py:134-192)
+    given ``dH``: inputs padded to whole chunks of ``C`` rows, fp32 ``(nb, Tp, .)``
+    gradients (the rows past the input are zero-padding).  Chunk states and
+    their per-segment exclusive scan, the reverse scan of ``Phi_b^T dH_b``, and
+    the per-chunk products, all on smat_bgemm and the segment-scan kernels."""
+    nb, Tp, r = Ph.shape
+    p = Vv.shape[-1]
+    nc = Tp // C
+    dev = Ph.device
     dPhi = torch.empty(nb, Tp, r, device=dev, dtype=torch.float32)
     dPsi = torch.empty(nb, Tp, r, device=dev, dtype=torch.float32)
     dVb = torch.empty(nb, Tp, p, device=dev, dtype=torch.float32)
-
-    # ---- causal: states, reverse states, per-chunk products ---------------
     D = _hip.chunk_states(Ps, Vv, C)                    # (nb, nc, r, p)
     Sin = _hip.segment_scan(D, n // C)
     Dr = torch.empty(nb, nc, r, p, device=dev, dtype=torch.float32)
@@ -174,6 +147,46 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
     _bgemm(A, dH, dVb, M=C, N=p, K=C, n1=nb, n2=nc,
            a=(nc * CC, CC, 1, C), b=cp_, c=cp_, beta=1)
     del A, dA, Sin, Q, D
+
+    return dPhi, dPsi, dVb
+
+
+def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=None,
+                        need_dg: bool = False):
+    """``(dPhi, dPsi, dVb, dg)`` of ``out = smat_attention(Phi, Psi, Vb, spec, g=g)``
+    given the forward's ``U`` (nb, B, r, p) and ``H`` (nb, T, p, long-range
+    term included), fp32 gradients."""
+    nb, T, r = Phi.shape
+    p = Vb.shape[-1]
+    C = min(chunk, T)
+    n, n_P, N0, B = spec.n, spec.n_P, spec.N0, spec.B
+    T_R = T - n
+    dev = Phi.device
+    nc = -(-T // C)
+    Tp = nc * C
+
+    # ---- normalise --------------------------------------------------------
+    dout = dout.float().contiguous()
+    H = H.float().contiguous()
+    dH = torch.zeros(nb, Tp, p, device=dev, dtype=torch.float32)      # rows >= T stay 0
+    dg = torch.empty(nb, T, device=dev, dtype=torch.float32) if need_dg else None
+    gc = g.float().contiguous() if g is not None else None
+    call("smat_normalise_backward", dout.data_ptr(), H.data_ptr(), ptr(gc), dH.data_ptr(),
+         ptr(dg), nb, T, p, dout.stride(0), dout.stride(1), H.stride(0), H.stride(1),
+         dH.stride(0), dH.stride(1), gc.stride(0) if gc is not None else 0, stream_of(dH))
+
+    # inputs padded to whole chunks (zeros contribute nothing)
+    def padded(x):
+        x = x.contiguous()
+        if Tp == T:
+            return x
+        out = torch.zeros(nb, Tp, x.shape[-1], device=dev, dtype=x.dtype)
+        out[:, :T] = x
+        return out
+
+    Ph, Ps, Vv = padded(Phi), padded(Psi), padded(Vb)
+
+    dPhi, dPsi, dVb = causal_scan_grad(Ph, Ps, Vv, dH, n, C)
 
     # ---- long range --------------------------------------------------------
     if T_R > 0:
@@ -254,6 +267,97 @@ class SmatAttentionFunction(torch.autograd.Function):
                 dPsi.to(Psi.dtype) if ctx.needs_input_grad[1] else None,
                 dVb.to(Vb.dtype) if ctx.needs_input_grad[2] else None,
                 dg.to(g.dtype) if need_dg else None, None, None)
+
+
+class CausalScanFunction(torch.autograd.Function):
+    """``segmented_causal_scan`` with its HIP backward (:func:`causal_scan_grad`);
+    the reference differentiates its torch path (attention.py:134-192)."""
+
+    @staticmethod
+    def forward(ctx, Phi, Psi, Vb, n, C, run):
+        H = run(Phi.detach(), Psi.detach(), Vb.detach())
+        ctx.save_for_backward(Phi, Psi, Vb)
+        ctx.n, ctx.C = n, C
+        return H
+
+    @staticmethod
+    def backward(ctx, dH):
+        Phi, Psi, Vb = ctx.saved_tensors
+        nb, T, r = Phi.shape
+        C = ctx.C
+        Tp = -(-T // C) * C
+
+        def padded(x, dt=None):
+            x = x.contiguous() if dt is None else x.to(dt).contiguous()
+            if Tp == T:
+                return x
+            out = torch.zeros(nb, Tp, x.shape[-1], device=x.device, dtype=x.dtype)
+            out[:, :T] = x
+            return out
+        dPhi, dPsi, dVb = causal_scan_grad(padded(Phi), padded(Psi), padded(Vb),
+                                           padded(dH, torch.float32), ctx.n, C)
+        return (dPhi[:, :T].to(Phi.dtype), dPsi[:, :T].to(Psi.dtype), dVb[:, :T].to(Vb.dtype),
+                None, None, None)
+
+
+class FeaturiseFunction(torch.autograd.Function):
+    """``featurise`` / the feature map (attention.py:82-106) with gradients:
+    forward the HIP launch; backward, with ``y = x W^T`` and ``m`` the map,
+    ``dx = (dPhi * m'(y)) W``, ``dW = sum (dPhi * m'(y))^T x`` for the query
+    and gated key maps, ``dh = sum_r dPsi * m(y_k)`` and ``dV = dVb[..., :d_v]``.
+    ``m'`` is 1 above 0 and ``e^y`` (elu + 1) or 0 (relu) below; the products
+    are plain GEMMs in fp32."""
+
+    @staticmethod
+    def forward(ctx, W, kind, Q, K, V, h):
+        Phi, Psi, Vb = _hip.featurise(W.detach(), kind, Q.detach(),
+                                         None if K is None else K.detach(),
+                                         None if V is None else V.detach(),
+                                         None if h is None else h.detach())
+        ctx.save_for_backward(W, Q, K, h)
+        ctx.kind = kind
+        ctx.d_v = None if V is None else V.shape[-1]
+        ctx.v_dtype = None if V is None else V.dtype
+        return Phi, Psi, Vb
+
+    @staticmethod
+    def backward(ctx, dPhi, dPsi, dVb):
+        W, Q, K, h = ctx.saved_tensors
+        W32 = W.float()
+
+        def dmap(y):
+            pos = y > 0
+            if ctx.kind == "elu1":
+                return torch.where(pos, torch.ones_like(y), torch.exp(torch.clamp(y, max=0.0)))
+            return pos.to(y.dtype)
+
+        def fmap(y):
+            if ctx.kind == "elu1":
+                return torch.nn.functional.elu(y) + 1.0
+            return torch.nn.functional.relu(y) + 1e-3
+        dW = torch.zeros_like(W32) if ctx.needs_input_grad[0] else None
+        dQ = dK = dV = dh = None
+        if dPhi is not None:
+            x = Q.float()
+            y = x @ W32.T
+            gq = dPhi.float() * dmap(y)
+            dQ = (gq @ W32).to(Q.dtype)
+            if dW is not None:
+                dW += gq.reshape(-1, gq.shape[-1]).T @ x.reshape(-1, x.shape[-1])
+        if K is not None and dPsi is not None:
+            x = K.float()
+            y = x @ W32.T
+            gk = dPsi.float()
+            if h is not None:
+                dh = (gk * fmap(y)).sum(-1).to(h.dtype)
+                gk = gk * h.float().unsqueeze(-1)
+            gk = gk * dmap(y)
+            dK = (gk @ W32).to(K.dtype)
+            if dW is not None:
+                dW += gk.reshape(-1, gk.shape[-1]).T @ x.reshape(-1, x.shape[-1])
+        if ctx.d_v is not None and dVb is not None:
+            dV = dVb[..., :ctx.d_v].to(ctx.v_dtype)
+        return (dW.to(W.dtype) if dW is not None else None, None, dQ, dK, dV, dh)
 
 
 # ---------------------------------------------------------------------------

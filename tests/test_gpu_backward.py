@@ -192,3 +192,140 @@ def test_patch_makes_the_kernel_table_differentiable():
     finally:
         Bw.unpatch()
     assert not K.pool(Psi, Vb, spec.n_P, spec.n, spec.N0).requires_grad
+
+
+def _grel(a, b):
+    return ((a.double() - b.double()).abs().max() / b.double().abs().max().clamp_min(1e-30)).item()
+
+
+@pytest.mark.parametrize("kind", ["elu1", "relu"])
+def test_featurise_gradients(kind):
+    """featurise on the GPU (HIP forward, the map's derivative backward): every
+    gradient -- Q, K, V, the key gate h and W -- against fp64 autograd of the
+    oracle's torch map on the same values (the reference differentiates its
+    torch featurise, attention.py:82-106)."""
+    gen = torch.Generator().manual_seed(31)
+    nb, T, dqk, dv, r = 2, 300, 64, 64, 48
+    ins = {"Q": torch.randn(nb, T, dqk, generator=gen), "K": torch.randn(nb, T, dqk, generator=gen),
+           "V": torch.randn(nb, T, dv, generator=gen),
+           "h": torch.rand(nb, T, generator=gen) + 0.5,
+           "W": torch.randn(r, dqk, generator=gen) / dqk ** 0.5}
+    Rs = [torch.randn(nb, T, r, generator=gen), torch.randn(nb, T, r, generator=gen),
+          torch.randn(nb, T, dv + 1, generator=gen)]
+    _say("featurise grads", kind)
+
+    def run(dev, dt, feat):
+        xs = {k: v.to(dev, dt).requires_grad_(True) for k, v in ins.items()}
+        outs = feat(xs)
+        sum((o.float() * R_.to(dev)).sum() for o, R_ in zip(outs, Rs)).backward()
+        return [o.detach().cpu() for o in outs], {k: v.grad.detach().cpu() for k, v in xs.items()}
+
+    def ref(xs):
+        W = xs["W"]
+        m = (lambda x: torch.nn.functional.elu(x @ W.T) + 1.0) if kind == "elu1" else \
+            (lambda x: torch.nn.functional.relu(x @ W.T) + 1e-3)
+        return O.featurise(xs["Q"], xs["K"], xs["V"], m, h=xs["h"])
+
+    def hip(xs):
+        return A.featurise(xs["Q"], xs["K"], xs["V"], A.FeatureMap(xs["W"], kind), h=xs["h"])
+    o0, g0 = run("cpu", torch.float64, ref)
+    o1, g1 = run(DEV, torch.float32, hip)
+    for a, b in zip(o1, o0):
+        assert _grel(a, b) < 1e-5
+    for k in g0:
+        assert _grel(g1[k], g0[k]) < 1e-5, (k, _grel(g1[k], g0[k]))
+    # the map alone (make_phi's callable) is differentiable too
+    xq = ins["Q"].to(DEV).requires_grad_(True)
+    A.FeatureMap(ins["W"].to(DEV), kind)(xq).sum().backward()
+    assert xq.grad is not None and torch.isfinite(xq.grad).all()
+
+
+@pytest.mark.parametrize("T,n,C,r,p", [(1024, 512, 128, 16, 17), (1000, 512, 64, 32, 33),
+                                       (4096, 2048, 128, 64, 65), (2048, 1024, 256, 16, 17)])
+def test_segmented_causal_scan_gradients(T, n, C, r, p):
+    """segmented_causal_scan alone as an autograd node (HIP forward and
+    backward): dPhi, dPsi, dVb against fp64 autograd of the oracle's scan,
+    padded tails and a wide chunk included."""
+    gen = torch.Generator().manual_seed(T + C)
+    nb = 3
+    ins = [torch.rand(nb, T, r, generator=gen) + 0.1, torch.rand(nb, T, r, generator=gen) * 0.1,
+           torch.randn(nb, T, p, generator=gen)]
+    R_ = torch.randn(nb, T, p, generator=gen)
+    _say("scan grads", T, n, C, r, p)
+
+    def run(dev, dt, f):
+        xs = [t.to(dev, dt).requires_grad_(True) for t in ins]
+        H = f(*xs)
+        (H.float() * R_.to(dev)).sum().backward()
+        return H.detach().cpu(), [x.grad.detach().cpu() for x in xs]
+    h0, g0 = run("cpu", torch.float64, lambda a, b, c: O.segmented_causal_scan(a, b, c, n, C))
+    h1, g1 = run(DEV, torch.float32, lambda a, b, c: A.segmented_causal_scan(a, b, c, n, C))
+    assert _grel(h1, h0) < 1e-5
+    for a, b in zip(g1, g0):
+        assert _grel(a, b) < 1e-5
+
+
+@pytest.mark.parametrize("d", [2, 3])
+def test_training_step_content_hashed(d):
+    """The content-hashed training step at head_dim 64, T = 4096 (4 of the
+    configuration's 12 heads, so the fp64 oracle finishes in seconds): the
+    feature map, the segmented causal scan plus the content-addressed long-range
+    term added to the recent rows, the single division (the reference model's
+    layer, model.py:300-311); dQ, dK, dV and the hash input's gradient against
+    the same step in fp64 through the oracle, fp32 inputs."""
+    from oracle import assign_ref as RA
+    from smat_attention_amd.assign import ContentAssign
+    H_, T, hd = 4, 4096, 64
+    spec = build_mask(T, d, chunk=128)
+    n = spec.n
+    gen = torch.Generator().manual_seed(40 + d)
+    Q = torch.randn(1, H_, T, hd, generator=gen) * 0.5
+    K = torch.randn(1, H_, T, hd, generator=gen) / hd ** 0.5
+    V = torch.randn(1, H_, T, hd, generator=gen)
+    X = torch.randn(1, T, 96, generator=gen)                  # the layer input the hash reads
+    dO = torch.randn(H_, T, hd, generator=gen)
+    torch.manual_seed(7)
+    m = ContentAssign(H_, 96, spec, mode="point")
+    W = O.phi_weight(hd, hd, dtype=torch.float64, seed=0)
+    pc = torch.tensor([spec.q ** (spec.dim - l) for l in range(1, spec.dim + 1)])
+    _say("training step", d, spec.q, spec.N0)
+
+    def step_ref(q, k, v, x, prm):
+        phi = lambda z: torch.nn.functional.elu(z @ W.T) + 1.0
+        Phi, Psi, Vb = O.featurise(q.reshape(H_, T, hd), k.reshape(H_, T, hd),
+                                   v.reshape(H_, T, hd), phi)
+        Hs = O.segmented_causal_scan(Phi, Psi, Vb, n, 128)
+        Ylr = RA.pairs_branch(x, Phi, Psi, Vb, n, prm["W"], prm["gamma"], prm["b"], spec.q,
+                              spec.dim, H_, spec.N0, planted_cols=spec.planted_cols,
+                              plant_cells=pc)
+        Hs = torch.cat([Hs[:, :n], Hs[:, n:] + Ylr], dim=1)
+        return Hs[..., :-1] / Hs[..., -1:].clamp_min(1e-6)
+
+    def step_hip(q, k, v, x, prm):
+        phi = A.FeatureMap(W.to(DEV, torch.float32), "elu1")
+        Phi, Psi, Vb = A.featurise(q.reshape(H_, T, hd), k.reshape(H_, T, hd),
+                                   v.reshape(H_, T, hd), phi)
+        Hs = A.segmented_causal_scan(Phi, Psi, Vb, n, 128)
+        Ylr = m(x, Phi, Psi, Vb, n)
+        Hs = torch.cat([Hs[:, :n], Hs[:, n:] + Ylr], dim=1)
+        return Hs[..., :-1] / Hs[..., -1:].clamp_min(1e-6)
+
+    def run(dev, dt, step, prm):
+        xs = [t.to(dev, dt).requires_grad_(True) for t in (Q, K, V, X)]
+        o = step(*xs, prm)
+        (o * dO.to(dev, dt)).sum().backward()
+        return o.detach().cpu(), [t.grad.detach().cpu() for t in xs]
+    prm64 = {k: getattr(m, k).detach().double().requires_grad_(True) for k in ("W", "gamma", "b")}
+    o0, g0 = run("cpu", torch.float64, step_ref, prm64)
+    m.to(DEV)
+    o1, g1 = run(DEV, torch.float32, step_hip, None)
+    # the fp32 hash must give the fp64 cells for the comparison to mean anything
+    ck64, _ = RA.cells(X[:, :n].double(), prm64["W"].detach(), prm64["gamma"].detach(),
+                       prm64["b"].detach(), spec.q, spec.dim, H_)
+    ck64 = RA.plant(ck64, torch.as_tensor(spec.planted_cols, dtype=torch.long), pc)
+    assert torch.equal(m.last_hard_k.cpu(), ck64)
+    assert _grel(o1, o0) < 1e-5
+    for name, a, b in zip(("dQ", "dK", "dV", "dX"), g1, g0):
+        assert _grel(a, b) < 1e-5, (name, _grel(a, b))
+    for k, pr in prm64.items():
+        assert _grel(getattr(m, k).grad.cpu(), pr.grad) < 1e-4, k
