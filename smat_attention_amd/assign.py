@@ -39,7 +39,8 @@ import torch
 import torch.nn as nn
 
 from .kernels.hip_fwd import _code, _on_gpu, _rows3, call, stream_of
-from .pool_ops import _gram_lists, _read_lists, _read_pairs, _repeat, pool_sorted, read_sorted
+from .pool_ops import (_gram_lists, _lists, _read_lists, _read_pairs, _repeat, pool_sorted,
+                       read_sorted)
 
 __all__ = ["ContentAssign", "grouped_planes"]
 
@@ -450,7 +451,9 @@ class _HardPool(torch.autograd.Function):
     """The dense pool with one-hot forward weights (assign.py:431-436 at
     ``anneal = 1``): ``F_x = sum_{ck_j = x} Psi_j^T Vb_j``; backward
     ``dPsi_j = dF[ck_j] Vb_j``, ``dVb_j = dF[ck_j]^T Psi_j`` and, for every
-    pair, ``dw_jk = Psi_j . (dF[idx_jk] Vb_j)``.  fp32 F."""
+    pair, ``dw_jk = Psi_j . (dF[idx_jk] Vb_j)`` -- for the first pair (the
+    chosen cell, ``idx_j0 = ck_j``) that is ``Psi_j . dPsi_j``.  The cell
+    lists are sorted once per step.  fp32 F."""
 
     @staticmethod
     def forward(ctx, P, V, wk, idxk, ck, N0):
@@ -458,8 +461,10 @@ class _HardPool(torch.autograd.Function):
         if r > 128 or p > 144:
             raise NotImplementedError("ContentAssign gradients: r <= 128, p <= 144")
         Pk, Vk = P.contiguous(), V.contiguous()
-        F = _gram_lists(Pk, Vk, ck, N0)
+        lists = _lists(ck, N0)
+        F = _gram_lists(Pk, Vk, ck, N0, lists)
         ctx.save_for_backward(Pk, Vk, idxk, ck)
+        ctx.lists = lists
         ctx.dtypes = (P.dtype, V.dtype, wk.dtype)
         return F
 
@@ -469,23 +474,37 @@ class _HardPool(torch.autograd.Function):
         dF = dF.float().contiguous()
         dFT = dF.transpose(-1, -2).contiguous()
         P32, V32 = Pk.float(), Vk.float()
-        dPsi = _read_lists(V32, dFT, ck)
-        dVb = _read_lists(P32, dF, ck)
-        dwk = (_read_pairs(V32, dFT, idxk) * P32.unsqueeze(2)).sum(-1)
+        dPsi = _read_lists(V32, dFT, ck, ctx.lists)
+        dVb = _read_lists(P32, dF, ck, ctx.lists)
+        dwk = _pair_dw(P32, dPsi, V32, dFT, idxk)
         dp, dv, dw = ctx.dtypes
         return dPsi.to(dp), dVb.to(dv), dwk.to(dw), None, None, None
+
+
+def _pair_dw(X, G0, Y, UT, idx):
+    """``dw[b, l, k] = X_l . (U[idx_lk] Y_l)`` for every pair, given
+    ``G0 = U[idx_l0] Y_l`` of the first pair (already computed as a gradient):
+    the other pairs are one list read over the flattened (row, pair) lists."""
+    dw0 = (X * G0).sum(-1, keepdim=True)
+    if idx.shape[-1] == 1:
+        return dw0
+    rest = (_read_pairs(Y, UT, idx[..., 1:].contiguous()) * X.unsqueeze(2)).sum(-1)
+    return torch.cat([dw0, rest], -1)
 
 
 class _HardRead(torch.autograd.Function):
     """The dense point read with one-hot forward weights (assign.py:437-441 at
     ``anneal = 1``): ``y_i = Phi_i F[cq_i]``; backward ``dPhi_i = F[cq_i] dy_i``,
-    ``dF_x = sum_{cq_i = x} Phi_i^T dy_i`` and ``dw_ik = Phi_i . (F[idx_ik] dy_i)``."""
+    ``dF_x = sum_{cq_i = x} Phi_i^T dy_i`` and ``dw_ik = Phi_i . (F[idx_ik] dy_i)``
+    (``Phi_i . dPhi_i`` for the first pair)."""
 
     @staticmethod
     def forward(ctx, Phr, F, wq, idxq, cq):
         Phr = Phr.contiguous()
-        Y = _read_lists(Phr, F.contiguous(), cq)
+        lists = _lists(cq, F.shape[1])
+        Y = _read_lists(Phr, F.contiguous(), cq, lists)
         ctx.save_for_backward(Phr, F, idxq, cq)
+        ctx.lists = lists
         ctx.dtypes = (Phr.dtype, wq.dtype)
         return Y
 
@@ -495,9 +514,9 @@ class _HardRead(torch.autograd.Function):
         dY = dY.float().contiguous()
         Ph32 = Phr.float()
         FT = F.transpose(-1, -2).contiguous()
-        dPhi = _read_lists(dY, FT, cq)
-        dF = _gram_lists(Ph32, dY, cq, F.shape[1])
-        dwq = (_read_pairs(dY, FT, idxq) * Ph32.unsqueeze(2)).sum(-1)
+        dPhi = _read_lists(dY, FT, cq, ctx.lists)
+        dF = _gram_lists(Ph32, dY, cq, F.shape[1], ctx.lists)
+        dwq = _pair_dw(Ph32, dPhi, dY, FT, idxq)
         dp, dw = ctx.dtypes
         return dPhi.to(dp), dF, dwq.to(dw), None, None
 

@@ -13,10 +13,12 @@ namespace dc {
 constexpr int kThreads = 1024;
 constexpr int kCols = 144;                // p <= 144 columns, one thread column each
 constexpr int kParts = kThreads / kCols;  // 7 feature partitions (1008 threads busy)
+constexpr int kRows = (kMaxR + kParts - 1) / kParts;   // rows per thread, at most 19
 }  // namespace dc
 
 // One workgroup per sequence: thread (part, c) owns column c of the rows
-// a = part, part + 7, ...; it advances S there (S_out = S_in + psi vb^T) and
+// a = part, part + 7, ... (at most 19, all loaded up front); it advances S
+// there (S_out = S_in + psi vb^T) and
 // accumulates phi_a (S_out + U_h)[a][c].  The 7 partial sums of each column
 // meet in LDS, which also hands every column the normaliser o[p-1] -- one read
 // of S, U_h and one write of S per sequence, nothing recomputed.
@@ -35,6 +37,29 @@ __global__ __launch_bounds__(dc::kThreads) void decode_step_kernel(
   const int c = tid % kCols, part = tid / kCols;
   const int h = (int)(step % B);
 
+  const int64_t rp = (int64_t)r * p;
+  const float* Sb = S_in + b * rp;
+  float* Sob = S_out + b * rp;
+  const float* Ub = U + (b * B + h) * rp;
+  const bool mine = part < kParts && c < p;
+
+  // every row of this thread (at most kRows) is loaded before phi, psi and vb
+  // are staged: the state and the step's inputs are in flight together, one
+  // memory latency per step instead of two.  U_h is read with non-temporal
+  // loads (a type row comes back only B steps later); S is read again next
+  // step and may stay in the caches.
+  float sv[kRows], uv[kRows];
+  if (mine) {
+#pragma unroll
+    for (int u = 0; u < kRows; ++u) {
+      const int a = part + u * kParts;
+      if (a < r) {
+        const int64_t o = (int64_t)a * p + c;
+        sv[u] = Sb[o];
+        uv[u] = __builtin_nontemporal_load(Ub + o);
+      }
+    }
+  }
   if (tid < r) {
     sphi[tid] = to_f32(phi[b * q_sb + tid]);
     spsi[tid] = to_f32(psi[b * k_sb + tid]);
@@ -42,37 +67,17 @@ __global__ __launch_bounds__(dc::kThreads) void decode_step_kernel(
   if (tid < p) svb[tid] = to_f32(vb[b * v_sb + tid]);
   __syncthreads();
 
-  const int64_t rp = (int64_t)r * p;
-  const float* Sb = S_in + b * rp;
-  float* Sob = S_out + b * rp;
-  const float* Ub = U + (b * B + h) * rp;
-
   float acc = 0.f;
-  if (part < kParts && c < p) {
+  if (mine) {
     const float vc = svb[c];
-    int a = part;
-    // rows in groups of 4: eight loads issued before the first use
-    for (; a + 3 * kParts < r; a += 4 * kParts) {
-      float sv[4], uv[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t o = (int64_t)(a + u * kParts) * p + c;
-        sv[u] = Sb[o];
-        uv[u] = Ub[o];
+    for (int u = 0; u < kRows; ++u) {
+      const int a = part + u * kParts;
+      if (a < r) {
+        const float s = sv[u] + spsi[a] * vc;
+        Sob[(int64_t)a * p + c] = s;
+        acc += sphi[a] * (s + uv[u]);
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int au = a + u * kParts;
-        const float s = sv[u] + spsi[au] * vc;
-        Sob[(int64_t)au * p + c] = s;
-        acc += sphi[au] * (s + uv[u]);
-      }
-    }
-    for (; a < r; a += kParts) {
-      const int64_t o = (int64_t)a * p + c;
-      const float s = Sb[o] + spsi[a] * vc;
-      Sob[o] = s;
-      acc += sphi[a] * (s + Ub[o]);
     }
   }
   if (part < kParts) red[part][c] = acc;

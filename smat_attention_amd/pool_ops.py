@@ -50,12 +50,13 @@ def _lists(cls, ncls):
     return order.to(torch.int32), offs, maxcnt
 
 
-def _gram_lists(A, B, cls, ncls):
+def _gram_lists(A, B, cls, ncls, lists=None):
     """``G[b, x] = sum_{l: cls[b,l] = x} A[b,l]^T B[b,l]``: A (nb, L, r), B (nb, L, p),
-    same dtype, contiguous -> fp32 (nb, ncls, r, p) (smat_gram_lists)."""
+    same dtype, contiguous -> fp32 (nb, ncls, r, p) (smat_gram_lists).  ``lists``:
+    the CSR of ``cls`` when the caller already has it."""
     nb, L, r = A.shape
     p = B.shape[-1]
-    tok, offs, _ = _lists(cls, ncls)
+    tok, offs, _ = lists if lists is not None else _lists(cls, ncls)
     G = torch.empty(nb, ncls, r, p, device=A.device, dtype=torch.float32)
     call("smat_gram_lists", _code(A, "pool_ops"), A.data_ptr(), B.data_ptr(),
          tok.data_ptr(), offs.data_ptr(), G.data_ptr(), nb * ncls, r, p, A.stride(1),
@@ -63,12 +64,13 @@ def _gram_lists(A, B, cls, ncls):
     return G
 
 
-def _read_lists(X, U, cls):
+def _read_lists(X, U, cls, lists=None):
     """``Y[b, l] = X[b, l] U[b, cls[b, l]]``: X (nb, L, c) contiguous, U fp32
-    (nb, ncls, c, o) contiguous -> fp32 (nb, L, o) (smat_query_lists)."""
+    (nb, ncls, c, o) contiguous -> fp32 (nb, L, o) (smat_query_lists).  ``lists``:
+    the CSR of ``cls`` when the caller already has it."""
     nb, L, c = X.shape
     ncls, o = U.shape[1], U.shape[-1]
-    rows, roffs, maxcnt = _lists(cls, ncls)
+    rows, roffs, maxcnt = lists if lists is not None else _lists(cls, ncls)
     Y = None
     # the kernel contracts at most 128 columns; wider X (c = head_dim + 1) is
     # read in column blocks whose partial products add up
