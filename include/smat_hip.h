@@ -80,6 +80,30 @@ int smat_segment_scan(const float* D, float* Sin, int nb, int nc, int nc0, int64
                       void* stream);
 
 /*
+ * The decayed scan (S_t = a_t S_{t-1} + psi_t vb_t^T, y_t = Phi_t S_t, one
+ * reset at chunk nc0), in two entry points over chunks of C rows.
+ * Replaces decayed_segmented_scan, src/smat/model.py:41-82 (torch in the
+ * reference: :60-68 within chunks, :71-80 across them).
+ *
+ * smat_decay_scan: Sin[c] = the state entering chunk c,
+ *   S <- aC[c] S + D[c] after chunk c, S = 0 at c = nc0;
+ * D, Sin: (nb, nc, rp) fp32 contiguous (Sin may not alias D); aC: (nb, nc)
+ * fp32, the total decay exp(L_C) of each chunk.
+ *
+ * smat_chunk_local_decay: as smat_chunk_local with the within-chunk decay:
+ *   out_b[m] = exp(L_m) Phi_m Sin_b + sum_{n <= m} exp(L_m - L_n) (Phi_m . Psi_n) Vb_n
+ * L: (nbc, C) fp32 contiguous, L_m the running sum of the log-decays of chunk
+ * b up to row m.  The masked weights are never formed.
+ */
+int smat_decay_scan(const float* D, const float* aC, float* Sin, int nb, int nc, int nc0,
+                    int64_t rp, void* stream);
+int smat_chunk_local_decay(int dtype, const void* phi, const void* psi, const void* vb,
+                           const float* sin, const float* L, float* out, int64_t nbc, int C,
+                           int r, int p, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
+                           int64_t v_sb, int64_t v_st, int64_t s_sb, int64_t s_sr,
+                           int64_t o_sb, int64_t o_st, void* stream);
+
+/*
  * The causal pass fused: segmented chunked scan with one reset at n (chunk
  * C <= 128), then either (write_H = 1) H = [[L_n,0],[0,L_{T_R}]] Phi Psi^T Vb
  * into out (nb, T, p) fp32, or (write_H = 0) the normalised output

@@ -103,6 +103,58 @@ def segmented_causal_scan(Phi, Psi, Vb, n: int, chunk: int = 128, acc_dtype=None
     return out.reshape(nb, T + pad, p)[:, :T]
 
 
+def decayed_segmented_scan(Phi, Psi, Vb, logA, n: int, chunk: int = 128):
+    """model.py:41-82: the chunked decayed scan, fp32 in the reference (here the
+    inputs' dtype, so fp64 inputs give the fp64 restatement)."""
+    nb, T, r = Phi.shape
+    p = Vb.shape[-1]
+    C = min(chunk, T)
+    pad = (-T) % C
+    if pad:
+        Phi = torch.nn.functional.pad(Phi, (0, 0, 0, pad))
+        Psi = torch.nn.functional.pad(Psi, (0, 0, 0, pad))
+        Vb = torch.nn.functional.pad(Vb, (0, 0, 0, pad))
+        logA = torch.nn.functional.pad(logA, (0, pad))
+    nc = (T + pad) // C
+    nc0 = n // C
+    Phi_c, Psi_c = Phi.reshape(nb, nc, C, r), Psi.reshape(nb, nc, C, r)
+    Vb_c, la = Vb.reshape(nb, nc, C, p), logA.reshape(nb, nc, C)
+    L = torch.cumsum(la, dim=-1)
+    tri = torch.ones(C, C, dtype=torch.bool).tril()
+    diff = (L.unsqueeze(-1) - L.unsqueeze(-2)).masked_fill(~tri, float("-inf"))
+    A = (Phi_c @ Psi_c.transpose(-1, -2)) * torch.exp(diff)
+    out = A @ Vb_c
+    wj = torch.exp(L[..., -1:] - L)
+    D = (Psi_c * wj.unsqueeze(-1)).transpose(-1, -2) @ Vb_c
+    aC = torch.exp(L[..., -1])
+    S = torch.zeros(nb, r, p, dtype=Phi.dtype)
+    rows = []
+    for b in range(nc):
+        if b == nc0:
+            S = torch.zeros_like(S)
+        rows.append(out[:, b] + (Phi_c[:, b] * torch.exp(L[:, b]).unsqueeze(-1)) @ S)
+        S = aC[:, b].view(nb, 1, 1) * S + D[:, b]
+    return torch.stack(rows, 1).reshape(nb, nc * C, p)[:, :T]
+
+
+def decayed_scan_tokens(Phi, Psi, Vb, logA, n: int, chunk: int = 128):
+    """The recurrence itself, token by token (for small checks): S_t =
+    a_t S_{t-1} + psi_t vb_t^T, y_t = Phi_t S_t, the state cleared where chunk
+    n // chunk begins (model.py:75-76 resets at that chunk)."""
+    nb, T, r = Phi.shape
+    p = Vb.shape[-1]
+    C = min(chunk, T)
+    reset = (n // C) * C
+    S = torch.zeros(nb, r, p, dtype=Phi.dtype)
+    ys = []
+    for t in range(T):
+        if t == reset:
+            S = torch.zeros_like(S)
+        S = torch.exp(logA[:, t]).view(nb, 1, 1) * S + Psi[:, t].unsqueeze(-1) * Vb[:, t].unsqueeze(1)
+        ys.append(torch.einsum("br,brp->bp", Phi[:, t], S))
+    return torch.stack(ys, 1)
+
+
 # ---------------------------------------------------------------------------
 # long range (attention.py:199-330, torch branches)
 # ---------------------------------------------------------------------------

@@ -39,7 +39,7 @@ from .mask import MaskSpec
 
 __all__ = [
     "make_phi", "featurise", "to_device",
-    "segmented_causal_scan", "pool_profiles", "apply_incidence",
+    "segmented_causal_scan", "decayed_segmented_scan", "pool_profiles", "apply_incidence",
     "query_by_type", "zeta_transform", "walsh_incidence", "direct_long_range",
     "smat_attention", "dense_masked_kernel_attention", "SmatDecoder",
     "have_triton", "have_hip",
@@ -322,6 +322,53 @@ def _causal_scan(Phi, Psi, Vb, n: int, C: int):
         Vb = torch.nn.functional.pad(Vb, (0, 0, 0, pad))
     out = _hip.chunk_local(Phi.reshape(nb, nc, C, r), Psi.reshape(nb, nc, C, r),
                            Vb.reshape(nb, nc, C, p), Sin)
+    return out.reshape(nb, nc * C, p)[:, :T]
+
+
+def decayed_segmented_scan(Phi, Psi, Vb, logA, n: int, chunk: int = 128):
+    """The causal term with a selective decay (src/smat/model.py:41-82)::
+
+        S_t = a_t S_{t-1} + psi_t vb_t^T,   y_t = Phi_t S_t,   a_t = exp(logA_t)
+
+    with one reset at chunk ``n // chunk``, chunked, fp32, as the reference
+    computes it: the within-chunk weights ``exp(L_i - L_j)`` (``L`` the running
+    sum of ``logA`` inside a chunk, formed only for ``j <= i``), the chunk
+    summaries ``sum_j exp(L_C - L_j) psi_j vb_j^T`` and the states carried
+    across chunks with the total decay ``exp(L_C)``.  ``Phi, Psi (nb, T, r)``,
+    ``Vb (nb, T, p)``, ``logA (nb, T)`` -> fp32 ``(nb, T, p)``.
+
+    GPU work: the chunk summaries on the chunk-state kernel (over the
+    decay-weighted Psi), the state recurrence ``smat_decay_scan`` and the
+    within-chunk pass ``smat_chunk_local_decay``; the reference upcasts to
+    fp32 first, and so does this (the fp32 MFMA path).  Forward only: asking
+    for a gradient raises.
+    """
+    who = "decayed_segmented_scan"
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (Phi, Psi, Vb, logA)):
+        raise NotImplementedError(f"{who}: forward only; call under torch.no_grad()")
+    for t in (Phi, Psi, Vb, logA):
+        if not t.is_cuda:
+            raise ValueError(f"{who}: tensors must be on the GPU (got {t.device})")
+    nb, T, r = Phi.shape
+    p = Vb.shape[-1]
+    if logA.shape != (nb, T):
+        raise ValueError(f"{who}: logA is {tuple(logA.shape)}, expected {(nb, T)}")
+    C = min(chunk, T)
+    pad = (-T) % C
+    Ph, Ps, Vv, la = Phi.float(), Psi.float(), Vb.float(), logA.float()
+    if pad:
+        Ph = torch.nn.functional.pad(Ph, (0, 0, 0, pad))
+        Ps = torch.nn.functional.pad(Ps, (0, 0, 0, pad))
+        Vv = torch.nn.functional.pad(Vv, (0, 0, 0, pad))
+        la = torch.nn.functional.pad(la, (0, pad))
+    nc = (T + pad) // C
+    L = torch.cumsum(la.reshape(nb, nc, C), dim=-1)
+    wj = torch.exp(L[..., -1:] - L)                               # decay to the chunk end, <= 1
+    Psw = (Ps.reshape(nb, nc, C, r) * wj.unsqueeze(-1)).reshape(nb, nc * C, r)
+    D = _hip.chunk_states(Psw, Vv.contiguous(), C)
+    Sin = _hip.decay_scan(D, torch.exp(L[..., -1]), n // C)
+    out = _hip.chunk_local_decay(Ph.reshape(nb, nc, C, r), Ps.reshape(nb, nc, C, r),
+                                 Vv.reshape(nb, nc, C, p), Sin, L)
     return out.reshape(nb, nc * C, p)[:, :T]
 
 

@@ -18,6 +18,12 @@
 //     for 16-bit inputs (two MFMAs keep ~16 mantissa bits of the fp32 state);
 //     fp32 inputs use fp32 MFMA throughout;
 //   * Psi and Vb are staged in 64-token blocks, only up to the diagonal.
+//
+// With Decay (the decayed scan, src/smat/model.py:41-82) every row m of the
+// chunk also carries L_m, the running sum of the log-decays within its chunk:
+// the inter-chunk term of row m is scaled by exp(L_m) and the score of (m, n),
+// n <= m, by exp(L_m - L_n) after the causal mask -- the masked weights are
+// never formed, so no exp of a positive difference is taken.
 #include "smat_host.hpp"
 
 namespace smat {
@@ -46,12 +52,12 @@ constexpr int smem_bytes() {
 }
 }  // namespace cl
 
-template <typename In>
+template <typename In, bool Decay>
 __global__ __launch_bounds__(cl::kThreads, 2) void chunk_local_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
-    const float* __restrict__ sin, float* __restrict__ out, int C, int r, int p,
-    int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
-    int64_t s_sb, int64_t s_sr, int64_t o_sb, int64_t o_st, int vec_q, int vec_k) {
+    const float* __restrict__ sin, const float* __restrict__ L, float* __restrict__ out, int C,
+    int r, int p, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
+    int64_t v_st, int64_t s_sb, int64_t s_sr, int64_t o_sb, int64_t o_st, int vec_q, int vec_k) {
   using namespace cl;
   typedef typename Traits<In>::frag Frag;
   __shared__ __attribute__((aligned(16))) char smem[smem_bytes<In>()];
@@ -145,6 +151,20 @@ __global__ __launch_bounds__(cl::kThreads, 2) void chunk_local_kernel(
     __syncthreads();
   }
 
+  const float* Lb = Decay ? L + b * (int64_t)C : nullptr;
+  if constexpr (Decay) {
+    // row m of the inter-chunk term: exp(L_m) Phi_m Sin
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = mrow0[t] + 4 * grp + i;
+        const float e = m < C ? expf(Lb[m]) : 0.f;
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct) acc[t][ct][i] *= e;
+      }
+  }
+
   // ---- within-chunk term: tril(Phi Psi^T) Vb -----------------------------
   In* psiS = reinterpret_cast<In*>(smem);            // [kBN][kRPad]
   In* vbT = psiS + kBN * kRPad;                      // [kCols][kNPad]
@@ -193,6 +213,15 @@ __global__ __launch_bounds__(cl::kThreads, 2) void chunk_local_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             if (nt0 + 4 * grp + i > mr0 + row16) s[nt][i] = 0.f;
+          if constexpr (Decay) {
+            const int m = mr0 + row16;
+            const float Lm = m < C ? Lb[m] : 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int n = nt0 + 4 * grp + i;
+              if (n <= m && n < C) s[nt][i] *= expf(Lm - Lb[n]);
+            }
+          }
         }
         // A fragment of S: element j < 4 is n = nb0 + 4 grp + j, j >= 4 is
         // n = nb0 + 16 + 4 grp + (j - 4).
@@ -238,34 +267,35 @@ __global__ __launch_bounds__(cl::kThreads, 2) void chunk_local_kernel(
 
 template <typename In>
 static int launch_chunk_local(const void* phi, const void* psi, const void* vb, const float* sin,
-                              float* out, int64_t nbc, int C, int r, int p, int64_t q_sb,
-                              int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
-                              int64_t v_st, int64_t s_sb, int64_t s_sr, int64_t o_sb,
-                              int64_t o_st, hipStream_t stream) {
+                              const float* L, float* out, int64_t nbc, int C, int r, int p,
+                              int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
+                              int64_t v_sb, int64_t v_st, int64_t s_sb, int64_t s_sr,
+                              int64_t o_sb, int64_t o_st, hipStream_t stream) {
   const int eb = sizeof(In);
   const int vq = rows_vec_ok(phi, q_sb, q_st, eb);
   const int vk = rows_vec_ok(psi, k_sb, k_st, eb);
   dim3 grid((unsigned)nbc, (unsigned)((C + cl::kBM - 1) / cl::kBM));
-  hipLaunchKernelGGL(chunk_local_kernel<In>, grid, dim3(cl::kThreads), 0, stream,
-                     (const In*)phi, (const In*)psi, (const In*)vb, sin, out, C, r, p, q_sb, q_st,
-                     k_sb, k_st, v_sb, v_st, s_sb, s_sr, o_sb, o_st, vq, vk);
-  return launch_status("smat_chunk_local");
+  auto kern = L ? chunk_local_kernel<In, true> : chunk_local_kernel<In, false>;
+  hipLaunchKernelGGL(kern, grid, dim3(cl::kThreads), 0, stream, (const In*)phi, (const In*)psi,
+                     (const In*)vb, sin, L, out, C, r, p, q_sb, q_st, k_sb, k_st, v_sb, v_st, s_sb,
+                     s_sr, o_sb, o_st, vq, vk);
+  return launch_status(L ? "smat_chunk_local_decay" : "smat_chunk_local");
 }
 
 int chunk_local_dispatch(int dtype, const void* phi, const void* psi, const void* vb,
                          const float* sin, float* out, int64_t nbc, int C, int r, int p,
                          int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
                          int64_t v_st, int64_t s_sb, int64_t s_sr, int64_t o_sb, int64_t o_st,
-                         hipStream_t stream) {
+                         hipStream_t stream, const float* L) {
   switch (dtype) {
     case SMAT_BF16:
-      return launch_chunk_local<bf16>(phi, psi, vb, sin, out, nbc, C, r, p, q_sb, q_st, k_sb,
+      return launch_chunk_local<bf16>(phi, psi, vb, sin, L, out, nbc, C, r, p, q_sb, q_st, k_sb,
                                       k_st, v_sb, v_st, s_sb, s_sr, o_sb, o_st, stream);
     case SMAT_F16:
-      return launch_chunk_local<f16>(phi, psi, vb, sin, out, nbc, C, r, p, q_sb, q_st, k_sb,
+      return launch_chunk_local<f16>(phi, psi, vb, sin, L, out, nbc, C, r, p, q_sb, q_st, k_sb,
                                      k_st, v_sb, v_st, s_sb, s_sr, o_sb, o_st, stream);
     case SMAT_F32:
-      return launch_chunk_local<float>(phi, psi, vb, sin, out, nbc, C, r, p, q_sb, q_st, k_sb,
+      return launch_chunk_local<float>(phi, psi, vb, sin, L, out, nbc, C, r, p, q_sb, q_st, k_sb,
                                        k_st, v_sb, v_st, s_sb, s_sr, o_sb, o_st, stream);
   }
   set_error("smat_chunk_local: unknown dtype %d", dtype);
@@ -294,5 +324,28 @@ extern "C" int smat_chunk_local(int dtype, const void* phi, const void* psi, con
                "smat_chunk_local: a row stride is shorter than its row");
   if (nbc == 0) return SMAT_OK;
   return chunk_local_dispatch(dtype, phi, psi, vb, sin, out, nbc, C, r, p, q_sb, q_st, k_sb, k_st,
-                              v_sb, v_st, s_sb, s_sr, o_sb, o_st, (hipStream_t)stream);
+                              v_sb, v_st, s_sb, s_sr, o_sb, o_st, (hipStream_t)stream, nullptr);
+}
+
+extern "C" int smat_chunk_local_decay(int dtype, const void* phi, const void* psi, const void* vb,
+                                      const float* sin, const float* L, float* out, int64_t nbc,
+                                      int C, int r, int p, int64_t q_sb, int64_t q_st,
+                                      int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
+                                      int64_t s_sb, int64_t s_sr, int64_t o_sb, int64_t o_st,
+                                      void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(phi && psi && vb && sin && L && out, SMAT_EINVAL,
+               "smat_chunk_local_decay: null pointer");
+  SMAT_REQUIRE(nbc >= 0 && nbc < (1ll << 31), SMAT_EINVAL, "smat_chunk_local_decay: nbc=%lld",
+               (long long)nbc);
+  SMAT_REQUIRE(C >= 1 && C <= kMaxC, SMAT_EUNSUPPORTED,
+               "smat_chunk_local_decay: C=%d not in [1, %d]", C, kMaxC);
+  SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 1 && p <= kMaxP, SMAT_EUNSUPPORTED,
+               "smat_chunk_local_decay: r=%d p=%d beyond r<=%d, p<=%d", r, p, kMaxR, kMaxP);
+  SMAT_REQUIRE(q_st >= r && k_st >= r && v_st >= p && s_sr >= p && o_st >= p, SMAT_EINVAL,
+               "smat_chunk_local_decay: a row stride is shorter than its row");
+  if (nbc == 0) return SMAT_OK;
+  return chunk_local_dispatch(dtype, phi, psi, vb, sin, out, nbc, C, r, p, q_sb, q_st, k_sb, k_st,
+                              v_sb, v_st, s_sb, s_sr, o_sb, o_st, (hipStream_t)stream, L);
 }

@@ -41,7 +41,7 @@ int chunk_local_dispatch(int dtype, const void* phi, const void* psi, const void
                          const float* sin, float* out, int64_t nbc, int C, int r, int p,
                          int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
                          int64_t v_st, int64_t s_sb, int64_t s_sr, int64_t o_sb, int64_t o_st,
-                         hipStream_t stream);
+                         hipStream_t stream, const float* L = nullptr);
 int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int idx_is_64,
                        const int64_t* indptr, int deg, float* U, int nb, int N0, int B, int64_t rp,
                        hipStream_t stream);

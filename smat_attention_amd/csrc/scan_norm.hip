@@ -30,6 +30,26 @@ __global__ __launch_bounds__(256) void segment_scan_kernel(const float* __restri
   }
 }
 
+// The decayed recurrence over chunks (src/smat/model.py:71-80):
+//   Sin[c] = the state entering chunk c;  S <- aC[c] S + D[c];  S = 0 at c = nc0.
+__global__ __launch_bounds__(256) void decay_scan_kernel(const float* __restrict__ D,
+                                                         const float* __restrict__ aC,
+                                                         float* __restrict__ Sin, int nc, int nc0,
+                                                         int64_t rp) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (e >= rp) return;
+  const float* Db = D + b * nc * rp + e;
+  const float* ab = aC + b * nc;
+  float* Sb = Sin + b * nc * rp + e;
+  float run = 0.f;
+  for (int c = 0; c < nc; ++c) {
+    if (c == nc0) run = 0.f;
+    Sb[(int64_t)c * rp] = run;
+    run = ab[c] * run + Db[(int64_t)c * rp];
+  }
+}
+
 // The mirror image for the backward pass: Sout[c] = sum of D[c'] over the
 // later chunks c' > c of the same segment (the state flowing backwards).
 __global__ __launch_bounds__(256) void segment_scan_rev_kernel(const float* __restrict__ D,
@@ -130,6 +150,20 @@ int normalise_dispatch(const float* H, const float* Y, const float* g, float* ou
 }
 
 }  // namespace smat
+
+extern "C" int smat_decay_scan(const float* D, const float* aC, float* Sin, int nb, int nc,
+                               int nc0, int64_t rp, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(D && aC && Sin && D != Sin, SMAT_EINVAL, "smat_decay_scan: null or aliased D/Sin");
+  SMAT_REQUIRE(nb >= 0 && nb < 65536 && nc >= 0 && rp >= 0, SMAT_EINVAL,
+               "smat_decay_scan: bad sizes");
+  if (nb == 0 || nc == 0 || rp == 0) return SMAT_OK;
+  dim3 grid((unsigned)((rp + 255) / 256), (unsigned)nb);
+  hipLaunchKernelGGL(decay_scan_kernel, grid, dim3(256), 0, (hipStream_t)stream, D, aC, Sin, nc,
+                     nc0, rp);
+  return launch_status("smat_decay_scan");
+}
 
 extern "C" int smat_segment_scan(const float* D, float* Sin, int nb, int nc, int nc0, int64_t rp,
                                  void* stream) {

@@ -187,6 +187,7 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
     Ph, Ps, Vv = padded(Phi), padded(Psi), padded(Vb)
 
     dPhi, dPsi, dVb = causal_scan_grad(Ph, Ps, Vv, dH, n, C)
+    rp = r * p
 
     # ---- long range --------------------------------------------------------
     if T_R > 0:

@@ -177,6 +177,51 @@ def chunk_local(Phi_c, Psi_c, Vb_c, Sin):
     return out.reshape(nb, nc, C, P)
 
 
+def chunk_local_decay(Phi_c, Psi_c, Vb_c, Sin, L):
+    """``exp(L_m) Phi_m Sin_b + sum_{n <= m} exp(L_m - L_n) (Phi_m . Psi_n) Vb_n`` for
+    every chunk (the decayed scan's within-chunk pass, model.py:60-68, 77).
+
+    Shapes as :func:`chunk_local` plus ``L (nb, nc, C)`` fp32, the running sum
+    of the log-decays within each chunk -> fp32 ``(nb, nc, C, p)``.
+    """
+    who = "chunk_local_decay"
+    _on_gpu(who, Phi_c, Psi_c, Vb_c, Sin, L)
+    nb, nc, C, R = Phi_c.shape
+    P = Vb_c.shape[-1]
+    if Psi_c.dtype != Phi_c.dtype or Vb_c.dtype != Phi_c.dtype:
+        raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
+    if L.shape != (nb, nc, C):
+        raise ValueError(f"{who}: L is {tuple(L.shape)}, expected {(nb, nc, C)}")
+    code = _code(Phi_c, who)
+    q, q_sb, q_st = _rows3(Phi_c.reshape(nb * nc, C, R))
+    k, k_sb, k_st = _rows3(Psi_c.reshape(nb * nc, C, R))
+    v, v_sb, v_st = _rows3(Vb_c.reshape(nb * nc, C, P))
+    s, s_sb, s_sr = _rows3(_fp32_rows(Sin).reshape(nb * nc, R, P))
+    Lc = L.float().contiguous()
+    out = torch.empty(nb * nc, C, P, device=q.device, dtype=torch.float32)
+    call("smat_chunk_local_decay", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), s.data_ptr(),
+         Lc.data_ptr(), out.data_ptr(), nb * nc, C, R, P, q_sb, q_st, k_sb, k_st, v_sb, v_st,
+         s_sb, s_sr, out.stride(0), out.stride(1), stream_of(q))
+    return out.reshape(nb, nc, C, P)
+
+
+def decay_scan(D, aC, nc0: int):
+    """States entering each chunk of the decayed scan: ``S <- aC[c] S + D[c]``
+    with one reset at chunk ``nc0`` (model.py:71-80).  ``D (nb, nc, r, p)``,
+    ``aC (nb, nc)`` -> fp32 ``Sin (nb, nc, r, p)``."""
+    who = "decay_scan"
+    _on_gpu(who, D, aC)
+    nb, nc, R, P = D.shape
+    if aC.shape != (nb, nc):
+        raise ValueError(f"{who}: aC is {tuple(aC.shape)}, expected {(nb, nc)}")
+    Dc = D.contiguous().float()
+    ac = aC.contiguous().float()
+    Sin = torch.empty_like(Dc)
+    call("smat_decay_scan", Dc.data_ptr(), ac.data_ptr(), Sin.data_ptr(), nb, nc, nc0, R * P,
+         stream_of(Dc))
+    return Sin
+
+
 def incidence_plane(F, plane_code, q: int, *, F_glob=None):
     """``U_h = sum_{x in H_h} F_x`` for d = 3 with the lines generated from
     ``plane_code`` (int32 ``(B,)``, ``e*q + b``) instead of a point table."""

@@ -554,3 +554,38 @@ def test_featurise_rejects_mixed_dtypes():
     Q = torch.randn(1, 16, 32, device=DEV, dtype=torch.bfloat16)
     with pytest.raises(TypeError):
         A.featurise(Q, Q, Q, phi)
+
+
+
+# ---------------------------------------------------------------------------
+# the decayed scan (model.py:41-82)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,n,C,r,p,strength", [
+    (1024, 512, 128, 16, 17, 1 / 16), (1000, 500, 64, 32, 33, 1 / 16),
+    (4096, 2048, 128, 64, 65, 1 / 16), (512, 256, 128, 128, 129, 2.0), (300, 0, 128, 8, 9, 0.5)])
+def test_decayed_scan(dt, T, n, C, r, p, strength):
+    """decayed_segmented_scan on HIP against the fp64 oracle on the same values:
+    the model's decay logsigmoid(x)/16 and strong decays (weights down to
+    e^-250 inside a chunk), a reset inside a chunk, padded tails, head sizes 16
+    to 128.  The reference computes in fp32 from upcast inputs, so does this:
+    1e-5 relative for every input dtype."""
+    _say("decayed scan", dt, T, n, C, r, p, strength)
+    g = torch.Generator().manual_seed(T + C + r)
+    nb = 3
+    Phi = (torch.rand(nb, T, r, generator=g) + 0.1).to(dt)
+    Psi = (torch.rand(nb, T, r, generator=g) * 0.2).to(dt)
+    Vb = torch.cat([torch.randn(nb, T, p - 1, generator=g), torch.ones(nb, T, 1)], -1).to(dt)
+    logA = torch.nn.functional.logsigmoid(torch.randn(nb, T, generator=g)) * strength
+    with torch.no_grad():
+        got = A.decayed_segmented_scan(Phi.to(DEV), Psi.to(DEV), Vb.to(DEV), logA.to(DEV), n, C)
+    ref = O.decayed_segmented_scan(Phi.double(), Psi.double(), Vb.double(), logA.double(), n, C)
+    assert torch.isfinite(got).all()
+    assert _rel(got.cpu(), ref) < 1e-5
+
+
+def test_decayed_scan_refuses_gradients():
+    Phi = torch.rand(1, 16, 4, device=DEV, requires_grad=True)
+    with pytest.raises(NotImplementedError, match="forward only"):
+        A.decayed_segmented_scan(Phi, Phi, Phi, torch.zeros(1, 16, device=DEV), 8, 8)

@@ -285,3 +285,39 @@ def test_planted_mistakes_are_caught(monkeypatch):
     assert err() > 1e-3
     monkeypatch.setattr(S, "chunk_local", orig_cl)
     assert err() < 1e-10
+
+
+@pytest.mark.parametrize("T,n,C", [(48, 24, 8), (50, 20, 8), (37, 16, 16), (64, 0, 16)])
+def test_decayed_scan_is_the_recurrence(T, n, C):
+    """The chunked decayed scan (model.py:41-82) equals the recurrence run
+    token by token, padded tails and a reset inside a chunk (n % C != 0: the
+    reference clears the state where chunk n // C begins) included."""
+    g = torch.Generator().manual_seed(T + n + C)
+    nb, r, p = 2, 3, 4
+    Phi, Psi = torch.rand(nb, T, r, generator=g, dtype=torch.float64), \
+        torch.rand(nb, T, r, generator=g, dtype=torch.float64)
+    Vb = torch.randn(nb, T, p, generator=g, dtype=torch.float64)
+    logA = -torch.rand(nb, T, generator=g, dtype=torch.float64) * 2.0
+    a = S.decayed_segmented_scan(Phi, Psi, Vb, logA, n, C)
+    b = S.decayed_scan_tokens(Phi, Psi, Vb, logA, n, C)
+    assert (a - b).abs().max().item() < 1e-12
+
+
+def test_decayed_scan_without_decay_is_the_plain_scan():
+    """logA = 0: every a_t is 1 and the decayed scan is the segmented causal
+    scan.  And the recurrence check has teeth: a reset one chunk late, or a
+    decay applied at half strength (plausible slips), miss it by far."""
+    g = torch.Generator().manual_seed(3)
+    nb, T, r, p, n, C = 2, 64, 4, 5, 32, 16
+    Phi, Psi = torch.rand(nb, T, r, generator=g, dtype=torch.float64), \
+        torch.rand(nb, T, r, generator=g, dtype=torch.float64)
+    Vb = torch.randn(nb, T, p, generator=g, dtype=torch.float64)
+    zero = torch.zeros(nb, T, dtype=torch.float64)
+    assert (S.decayed_segmented_scan(Phi, Psi, Vb, zero, n, C)
+            - S.segmented_causal_scan(Phi, Psi, Vb, n, C)).abs().max().item() < 1e-12
+    logA = -torch.rand(nb, T, generator=g, dtype=torch.float64)
+    ref = S.decayed_scan_tokens(Phi, Psi, Vb, logA, n, C)
+    late = S.decayed_segmented_scan(Phi, Psi, Vb, logA, n + C, C)
+    half = S.decayed_segmented_scan(Phi, Psi, Vb, logA / 2, n, C)
+    assert (late - ref).abs().max().item() > 1e-3
+    assert (half - ref).abs().max().item() > 1e-3
