@@ -355,3 +355,59 @@ def test_pool_ops_match_dense_maps(K, r, p):
     assert _grel(y1, y0) < 1e-5
     for k in g0:
         assert _grel(g1[k], g0[k]) < 1e-5, (k, _grel(g1[k], g0[k]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,d", [(128, 2), (128, 3), (512, 2), (512, 3)])
+@pytest.mark.parametrize("mode", ["point", "plane"])
+def test_branch_is_masked_attention_under_its_own_hash(T, d, mode):
+    """The HIP branch equals dense masked kernel attention under the mask its
+    own hash induces (the reference's exactness check,
+    tests/test_content_addr.py:11-42): G[i, j] = 1 when key j's cell is query
+    i's cell (point), or lies on query i's chosen hyperplane (plane)."""
+    from smat_attention_amd.assign import ContentAssign
+    spec = build_mask(T, d, chunk=32)
+    n, m_ = spec.n, spec.T_R
+    nb, h, dh, r, p = 3, 2, 8, 5, 4
+    torch.manual_seed(0)
+    dev = torch.device("cuda:0")
+    ca = ContentAssign(h, dh, spec, mode=mode).to(dev)
+    B = nb * h
+    g = torch.Generator().manual_seed(T + d)
+    u = torch.randn(nb, T, dh, generator=g)
+    Phi, Psi = torch.rand(B, T, r, generator=g), torch.rand(B, T, r, generator=g)
+    Vb = torch.randn(B, T, p, generator=g)
+    with torch.no_grad():
+        got = ca(u.to(dev), Phi.to(dev), Psi.to(dev), Vb.to(dev), n).cpu().double()
+        kc = ca.last_hard_k.cpu()
+        qc, _ = ca._hash(u[:, n:].to(dev))
+        qc = qc.cpu()
+    if ca.mode == "point":
+        G = (qc.unsqueeze(2) == kc.unsqueeze(1)).double()
+    else:
+        dl = torch.einsum("blm,hem->bhle", u[:, n:], ca.Wd.detach().cpu())
+        e = dl.reshape(B, m_, ca.D).argmax(-1)
+        o = ca.coset_of.cpu()[e, qc]
+        Mi = ca.M.cpu().double()[e, o]
+        G = Mi.gather(2, kc.unsqueeze(1).expand(B, m_, n))
+    Sc = torch.einsum("bir,bjr->bij", Phi[:, n:].double(), Psi[:, :n].double())
+    ref = (Sc * G) @ Vb[:, :n].double()
+    assert G.mean().item() > 0, "the mask is empty: the check would be vacuous"
+    assert _grel(got, ref) < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["point", "plane"])
+def test_straight_through_gradient_reaches_the_hash(mode):
+    """A nonzero gradient reaches the hash projection W (the reference's
+    tests/test_content_addr.py:45-55), through the HIP training path."""
+    from smat_attention_amd.assign import ContentAssign
+    spec = build_mask(512, 3, chunk=32)
+    dev = torch.device("cuda:0")
+    torch.manual_seed(1)
+    ca = ContentAssign(2, 8, spec, mode=mode).to(dev)
+    g = torch.Generator().manual_seed(2)
+    u = torch.randn(3, 512, 8, generator=g).to(dev)
+    Phi, Psi = torch.rand(6, 512, 5, generator=g).to(dev), torch.rand(6, 512, 5, generator=g).to(dev)
+    ca(u, Phi, Psi, torch.randn(6, 512, 4, generator=g).to(dev), spec.n).sum().backward()
+    assert ca.W.grad.abs().max().item() > 0
