@@ -97,6 +97,16 @@ int smat_segment_scan(const float* D, float* Sin, int nb, int nc, int nc0, int64
  */
 int smat_decay_scan(const float* D, const float* aC, float* Sin, int nb, int nc, int nc0,
                     int64_t rp, void* stream);
+
+/*
+ * The gradient of smat_decay_scan, walking the chunks backwards: given dSin
+ * (the gradient of every state entering a chunk), dD[c] receives the gradient
+ * of the summary D[c]: g = 0; for c = nc-1 .. 0: gn = (c + 1 == nc0 ? 0 : g);
+ * dD[c] = gn; g = dSin[c] + aC[c] gn.  Shapes as smat_decay_scan.  Replaces
+ * torch autograd through src/smat/model.py:71-80.
+ */
+int smat_decay_scan_reverse(const float* dSin, const float* aC, float* dD, int nb, int nc,
+                            int nc0, int64_t rp, void* stream);
 int smat_chunk_local_decay(int dtype, const void* phi, const void* psi, const void* vb,
                            const float* sin, const float* L, float* out, int64_t nbc, int C,
                            int r, int p, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,

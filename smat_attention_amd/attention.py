@@ -340,20 +340,27 @@ def decayed_segmented_scan(Phi, Psi, Vb, logA, n: int, chunk: int = 128):
     GPU work: the chunk summaries on the chunk-state kernel (over the
     decay-weighted Psi), the state recurrence ``smat_decay_scan`` and the
     within-chunk pass ``smat_chunk_local_decay``; the reference upcasts to
-    fp32 first, and so does this (the fp32 MFMA path).  Forward only: asking
-    for a gradient raises.
+    fp32 first, and so does this (the fp32 MFMA path).  Gradients reach Phi,
+    Psi, Vb and logA (an autograd node whose backward runs on smat_bgemm and
+    ``smat_decay_scan_reverse``).
     """
     who = "decayed_segmented_scan"
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (Phi, Psi, Vb, logA)):
-        raise NotImplementedError(f"{who}: forward only; call under torch.no_grad()")
     for t in (Phi, Psi, Vb, logA):
         if not t.is_cuda:
             raise ValueError(f"{who}: tensors must be on the GPU (got {t.device})")
     nb, T, r = Phi.shape
-    p = Vb.shape[-1]
     if logA.shape != (nb, T):
         raise ValueError(f"{who}: logA is {tuple(logA.shape)}, expected {(nb, T)}")
     C = min(chunk, T)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (Phi, Psi, Vb, logA)):
+        from .kernels.hip_bwd import DecayedScanFunction
+        return DecayedScanFunction.apply(Phi, Psi, Vb, logA, n, C)
+    return _decayed_forward(*_decayed_inputs(Phi, Psi, Vb, logA, C), n, C)[0][:, :T]
+
+
+def _decayed_inputs(Phi, Psi, Vb, logA, C: int):
+    """fp32 copies padded to whole chunks (zero rows, zero log-decay)."""
+    T = Phi.shape[1]
     pad = (-T) % C
     Ph, Ps, Vv, la = Phi.float(), Psi.float(), Vb.float(), logA.float()
     if pad:
@@ -361,15 +368,23 @@ def decayed_segmented_scan(Phi, Psi, Vb, logA, n: int, chunk: int = 128):
         Ps = torch.nn.functional.pad(Ps, (0, 0, 0, pad))
         Vv = torch.nn.functional.pad(Vv, (0, 0, 0, pad))
         la = torch.nn.functional.pad(la, (0, pad))
-    nc = (T + pad) // C
+    return Ph.contiguous(), Ps.contiguous(), Vv.contiguous(), la.contiguous()
+
+
+def _decayed_forward(Ph, Ps, Vv, la, n: int, C: int):
+    """(out (nb, Tp, p), L (nb, nc, C), Sin (nb, nc, r, p)) of the decayed scan
+    over padded fp32 inputs."""
+    nb, Tp, r = Ph.shape
+    p = Vv.shape[-1]
+    nc = Tp // C
     L = torch.cumsum(la.reshape(nb, nc, C), dim=-1)
     wj = torch.exp(L[..., -1:] - L)                               # decay to the chunk end, <= 1
-    Psw = (Ps.reshape(nb, nc, C, r) * wj.unsqueeze(-1)).reshape(nb, nc * C, r)
-    D = _hip.chunk_states(Psw, Vv.contiguous(), C)
+    Psw = (Ps.reshape(nb, nc, C, r) * wj.unsqueeze(-1)).reshape(nb, Tp, r)
+    D = _hip.chunk_states(Psw, Vv, C)
     Sin = _hip.decay_scan(D, torch.exp(L[..., -1]), n // C)
     out = _hip.chunk_local_decay(Ph.reshape(nb, nc, C, r), Ps.reshape(nb, nc, C, r),
                                  Vv.reshape(nb, nc, C, p), Sin, L)
-    return out.reshape(nb, nc * C, p)[:, :T]
+    return out.reshape(nb, Tp, p), L, Sin
 
 
 def pool_profiles(Psi, Vb, spec: MaskSpec, acc_dtype=None, backend: str = "auto"):

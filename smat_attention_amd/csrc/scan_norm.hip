@@ -50,6 +50,28 @@ __global__ __launch_bounds__(256) void decay_scan_kernel(const float* __restrict
   }
 }
 
+// Its gradient, walking the chunks backwards (the reset at nc0 stops the flow):
+//   g = 0;  for c = nc-1 .. 0:  gn = (c + 1 == nc0) ? 0 : g;  dD[c] = gn;
+//                               g = dSin[c] + aC[c] gn
+// dD[c] is the gradient of the summary D[c] (that of the state after chunk c).
+__global__ __launch_bounds__(256) void decay_scan_rev_kernel(const float* __restrict__ dSin,
+                                                             const float* __restrict__ aC,
+                                                             float* __restrict__ dD, int nc,
+                                                             int nc0, int64_t rp) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (e >= rp) return;
+  const float* gb = dSin + b * nc * rp + e;
+  const float* ab = aC + b * nc;
+  float* db = dD + b * nc * rp + e;
+  float g = 0.f;
+  for (int c = nc - 1; c >= 0; --c) {
+    const float gn = (c + 1 == nc0) ? 0.f : g;
+    db[(int64_t)c * rp] = gn;
+    g = gb[(int64_t)c * rp] + ab[c] * gn;
+  }
+}
+
 // The mirror image for the backward pass: Sout[c] = sum of D[c'] over the
 // later chunks c' > c of the same segment (the state flowing backwards).
 __global__ __launch_bounds__(256) void segment_scan_rev_kernel(const float* __restrict__ D,
@@ -163,6 +185,21 @@ extern "C" int smat_decay_scan(const float* D, const float* aC, float* Sin, int 
   hipLaunchKernelGGL(decay_scan_kernel, grid, dim3(256), 0, (hipStream_t)stream, D, aC, Sin, nc,
                      nc0, rp);
   return launch_status("smat_decay_scan");
+}
+
+extern "C" int smat_decay_scan_reverse(const float* dSin, const float* aC, float* dD, int nb,
+                                       int nc, int nc0, int64_t rp, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(dSin && aC && dD && dSin != dD, SMAT_EINVAL,
+               "smat_decay_scan_reverse: null or aliased dSin/dD");
+  SMAT_REQUIRE(nb >= 0 && nb < 65536 && nc >= 0 && rp >= 0, SMAT_EINVAL,
+               "smat_decay_scan_reverse: bad sizes");
+  if (nb == 0 || nc == 0 || rp == 0) return SMAT_OK;
+  dim3 grid((unsigned)((rp + 255) / 256), (unsigned)nb);
+  hipLaunchKernelGGL(decay_scan_rev_kernel, grid, dim3(256), 0, (hipStream_t)stream, dSin, aC,
+                     dD, nc, nc0, rp);
+  return launch_status("smat_decay_scan_reverse");
 }
 
 extern "C" int smat_segment_scan(const float* D, float* Sin, int nb, int nc, int nc0, int64_t rp,

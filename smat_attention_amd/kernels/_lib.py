@@ -43,6 +43,7 @@ SIGNATURES = {
     "smat_chunk_states": (_i, [_i, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64, _p]),
     "smat_segment_scan": (_i, [_p, _p, _i, _i, _i, _i64, _p]),
     "smat_decay_scan": (_i, [_p, _p, _p, _i, _i, _i, _i64, _p]),
+    "smat_decay_scan_reverse": (_i, [_p, _p, _p, _i, _i, _i, _i64, _p]),
     "smat_chunk_local_decay": (_i, [_i, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _i,
                                     _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                     _p]),

@@ -38,7 +38,8 @@ from . import _lib
 from ._lib import DTYPE_CODE, call, ptr, stream_of
 from . import hip_fwd as _hip
 
-__all__ = ["smat_attention_grad", "SmatAttentionFunction", "transposed_incidence",
+__all__ = ["smat_attention_grad", "SmatAttentionFunction", "DecayedScanFunction",
+           "transposed_incidence",
            "chunk_local", "pool", "incidence", "patch", "unpatch", "patched"]
 
 # the forward kernels as imported, before patch() swaps the module attributes
@@ -299,6 +300,108 @@ class CausalScanFunction(torch.autograd.Function):
                                            padded(dH, torch.float32), ctx.n, C)
         return (dPhi[:, :T].to(Phi.dtype), dPsi[:, :T].to(Psi.dtype), dVb[:, :T].to(Vb.dtype),
                 None, None, None)
+
+
+class DecayedScanFunction(torch.autograd.Function):
+    """``decayed_segmented_scan`` (model.py:41-82) with its backward on HIP.
+
+    Per chunk, with ``A = Phi Psi^T``, ``W_ij = exp(L_i - L_j)`` (j <= i),
+    ``e_i = exp(L_i)``, ``w_j = exp(L_C - L_j)``, the state ``Sin`` entering
+    the chunk and ``dO`` the output gradient::
+
+        dPhi  = e (dO Sin^T) + (dO Vb^T . W) Psi
+        dPsi  = (dO Vb^T . W)^T Phi + w (Vb dD^T)
+        dVb   = (A . W)^T dO + w (Psi dD)
+        dSin  = Phi^T (e dO);   dD by the reverse recurrence (smat_decay_scan_reverse)
+        dL_i  = rowsum_i(P) - colsum_i(P) + e_i (Phi_i Sin) . dO_i - w_i (Psi_i dD) . Vb_i
+        dL_C += sum_j w_j (Psi_j dD) . Vb_j + exp(L_C) <dD, Sin>,   P = A . W . (dO Vb^T)
+
+    and ``dlogA`` the reverse running sum of ``dL`` inside each chunk.  The
+    products run on smat_bgemm (fp32 MFMA), the (C, C) weightings and row
+    scales on torch elementwise kernels."""
+
+    @staticmethod
+    def forward(ctx, Phi, Psi, Vb, logA, n, C):
+        from .. import attention as A
+        Ph, Ps, Vv, la = A._decayed_inputs(Phi.detach(), Psi.detach(), Vb.detach(),
+                                           logA.detach(), C)
+        out, L, Sin = A._decayed_forward(Ph, Ps, Vv, la, n, C)
+        ctx.save_for_backward(Ph, Ps, Vv, L, Sin)
+        ctx.meta = (n, C, Phi.shape[1], Phi.dtype, Psi.dtype, Vb.dtype, logA.dtype)
+        return out[:, :Phi.shape[1]]
+
+    @staticmethod
+    def backward(ctx, dout):
+        Ph, Ps, Vv, L, Sin = ctx.saved_tensors
+        n, C, T, d_phi, d_psi, d_vb, d_la = ctx.meta
+        nb, Tp, r = Ph.shape
+        p = Vv.shape[-1]
+        nc = Tp // C
+        dev = Ph.device
+        rp, CC = r * p, C * C
+        dO = torch.zeros(nb, Tp, p, device=dev, dtype=torch.float32)
+        dO[:, :T] = dout.float()
+        cr, cp_ = (Tp * r, C * r, r, 1), (Tp * p, C * p, p, 1)
+        cc_ = (nc * CC, CC, C, 1)
+        e = torch.exp(L)                                            # (nb, nc, C)
+        w = torch.exp(L[..., -1:] - L)
+        tri = torch.ones(C, C, device=dev, dtype=torch.bool).tril()
+        Wd = torch.exp((L.unsqueeze(-1) - L.unsqueeze(-2)).masked_fill(~tri, float("-inf")))
+        A = torch.empty(nb, nc, C, C, device=dev, dtype=torch.float32)
+        dA = torch.empty_like(A)
+        _bgemm(Ph, Ps, A, M=C, N=C, K=r, n1=nb, n2=nc,
+               a=(Tp * r, C * r, r, 1), b=(Tp * r, C * r, 1, r), c=cc_, mask=1)
+        _bgemm(dO, Vv, dA, M=C, N=C, K=p, n1=nb, n2=nc,
+               a=(Tp * p, C * p, p, 1), b=(Tp * p, C * p, 1, p), c=cc_, mask=1)
+        AW = A * Wd
+        dAW = dA * Wd
+        P = AW * dA
+        dL = P.sum(-1) - P.sum(-2)
+        del A, dA, P, Wd
+        # dPhi = e (dO Sin^T) + dAW Psi
+        dPhi = torch.empty(nb, Tp, r, device=dev, dtype=torch.float32)
+        _bgemm(dO, Sin, dPhi, M=C, N=r, K=p, n1=nb, n2=nc,
+               a=cp_, b=(nc * rp, rp, 1, p), c=cr)
+        dPhi.view(nb, nc, C, r).mul_(e.unsqueeze(-1))
+        _bgemm(dAW, Ps, dPhi, M=C, N=r, K=C, n1=nb, n2=nc, a=cc_, b=cr, c=cr, beta=1)
+        # dSin = Phi^T (e dO), then the reverse recurrence
+        dOe = (dO.view(nb, nc, C, p) * e.unsqueeze(-1)).reshape(nb, Tp, p)
+        dSin = torch.empty(nb, nc, r, p, device=dev, dtype=torch.float32)
+        _bgemm(Ph, dOe, dSin, M=r, N=p, K=C, n1=nb, n2=nc,
+               a=(Tp * r, C * r, 1, r), b=cp_, c=(nc * rp, rp, p, 1))
+        del dOe
+        aC = e[..., -1].contiguous()
+        dD = torch.empty_like(dSin)
+        call("smat_decay_scan_reverse", dSin.data_ptr(), aC.data_ptr(), dD.data_ptr(), nb, nc,
+             n // C, rp, stream_of(dD))
+        del dSin
+        # dPsi = dAW^T Phi + w (Vb dD^T)
+        dPsi = torch.empty(nb, Tp, r, device=dev, dtype=torch.float32)
+        _bgemm(dAW, Ph, dPsi, M=C, N=r, K=C, n1=nb, n2=nc,
+               a=(nc * CC, CC, 1, C), b=cr, c=cr)
+        X = torch.empty(nb, Tp, r, device=dev, dtype=torch.float32)
+        _bgemm(Vv, dD, X, M=C, N=r, K=p, n1=nb, n2=nc, a=cp_, b=(nc * rp, rp, 1, p), c=cr)
+        dPsi.view(nb, nc, C, r).add_(X.view(nb, nc, C, r) * w.unsqueeze(-1))
+        del X, dAW
+        # dVb = AW^T dO + w (Psi dD); the summaries' weights' gradient from the same product
+        dVb = torch.empty(nb, Tp, p, device=dev, dtype=torch.float32)
+        _bgemm(AW, dO, dVb, M=C, N=p, K=C, n1=nb, n2=nc,
+               a=(nc * CC, CC, 1, C), b=cp_, c=cp_)
+        del AW
+        Y = torch.empty(nb, Tp, p, device=dev, dtype=torch.float32)
+        _bgemm(Ps, dD, Y, M=C, N=p, K=r, n1=nb, n2=nc, a=cr, b=(nc * rp, rp, p, 1), c=cp_)
+        Yc = Y.view(nb, nc, C, p)
+        dVb.view(nb, nc, C, p).add_(Yc * w.unsqueeze(-1))
+        wdw = w * (Yc * Vv.view(nb, nc, C, p)).sum(-1)               # w_j (Psi_j dD) . Vb_j
+        dL -= wdw
+        dL[..., -1] += wdw.sum(-1) + aC * (dD * Sin).sum((-2, -1))
+        # the inter-chunk term's row scale: e_i (Phi_i Sin) . dO_i
+        _bgemm(Ph, Sin, Y, M=C, N=p, K=r, n1=nb, n2=nc, a=cr, b=(nc * rp, rp, p, 1), c=cp_)
+        dL += e * (Yc * dO.view(nb, nc, C, p)).sum(-1)
+        del Y, Yc, dD
+        dla = torch.flip(torch.cumsum(torch.flip(dL, [-1]), -1), [-1]).reshape(nb, Tp)
+        return (dPhi[:, :T].to(d_phi), dPsi[:, :T].to(d_psi), dVb[:, :T].to(d_vb),
+                dla[:, :T].to(d_la), None, None)
 
 
 class FeaturiseFunction(torch.autograd.Function):
