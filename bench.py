@@ -205,7 +205,8 @@ def train_step_bench(d, reps, B=8, H=12, hd=64, T=4096):
     the hash reads (d_model = H*hd), upstream gradient ~ N(0, 1): the feature
     map, the segmented causal scan plus the content-addressed long-range term
     on the recent rows, the single division (model.py:300-311), then
-    backward to q, k, v, the hidden state and the hash parameters."""
+    backward to q, k, v, the hidden state and the hash parameters; and the same
+    step with positional assignment (smat_attention, forward and backward)."""
     import torch
     from smat_attention_amd import attention as A
     from smat_attention_amd.assign import ContentAssign
@@ -231,9 +232,19 @@ def train_step_bench(d, reps, B=8, H=12, hd=64, T=4096):
         o = Hs[..., :-1] / Hs[..., -1:].clamp_min(1e-6)
         (o.to(bf) * dO).float().sum().backward()
     us = Events(torch).time(step, reps)
-    return {"ms": round(us / 1e3, 3), "tokens_per_s": round(B * T / (us * 1e-6), 1),
-            "config": f"B={B} H={H} head_dim={hd} T={T} d={d} bf16, content-hashed point read, "
-                      f"fwd+bwd"}
+    res = {"ms": round(us / 1e3, 3), "tokens_per_s": round(B * T / (us * 1e-6), 1),
+           "config": f"B={B} H={H} head_dim={hd} T={T} d={d} bf16, content-hashed point read, "
+                     f"fwd+bwd"}
+    # the positional schedule on the same tensors: smat_attention forward and backward
+    spec_t = A.to_device(spec, dev)
+
+    def step_pos():
+        Phi, Psi, Vb = A.featurise(Q, K, V, phi)
+        o = A.smat_attention(Phi, Psi, Vb, spec_t)
+        (o.to(bf) * dO).float().sum().backward()
+    us = Events(torch).time(step_pos, reps)
+    res["positional_ms"] = round(us / 1e3, 3)
+    return res
 
 
 def useful_flops(spec, nb, T, r, p, C=128):
