@@ -387,6 +387,30 @@ def test_forward_long_prefill_d3_bf16_T131072():
     assert _rel(staged, out[:2]) < 1e-5      # one fused call == the stage-by-stage path
 
 
+def test_forward_long_prefill_d3_bf16_T524288():
+    """The largest long-prefill shape (T = 524288, d = 3: q = 67, N0 = 4489, B = 4556,
+    the line-per-lane incidence kernel), one head, bf16: finite; the fused call
+    equals the stage-by-stage path; and the pooled long-range term equals the
+    direct one (each row type summing its landmark outer products without
+    pooling or incidence) -- two independent paths at full size, where the
+    fp64 oracle would take minutes."""
+    _say("forward T=524288 d=3 nb=1 hd=128 bf16")
+    T = 524288
+    spec = build_mask(T, 3, chunk=128)
+    assert (spec.q, spec.N0, spec.B) == (67, 4489, 4556)
+    Phi, Psi, Vb = _feats(1, T, 128, torch.bfloat16, seed=5, k_scale=128 ** -0.5)
+    Pd, Sd, Wd = Phi.to(DEV), Psi.to(DEV), Vb.to(DEV)
+    out = A.smat_attention(Pd, Sd, Wd, spec)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    staged = A.smat_attention(Pd, Sd, Wd, spec, return_parts=True)
+    staged = staged[0] if isinstance(staged, tuple) else staged
+    assert _rel(staged, out) < 1e-5
+    spec_d = A.to_device(spec, DEV, want_direct=True)
+    direct = A.smat_attention(Pd, Sd, Wd, spec_d, long_range="direct")
+    assert _rel(direct, out) < 1e-5
+
+
 def test_exact_non_influence():
     """A landmark payload outside a recent row's mask leaves that row bit-identical
     (the reference's test_smat.py:292-324, on the GPU path)."""
