@@ -27,28 +27,32 @@ namespace smat {
 namespace sf {
 constexpr int kThreads = 256;
 constexpr int kC = 128;                  // rows per chunk handled (chunk <= 128)
-constexpr int kRK = 4;                   // r <= 128
-constexpr int kNCT = 9;                  // p <= 144
-constexpr int kCols = kNCT * 16;
-constexpr int kRPad = kRK * 32 + 8;      // row length of r-indexed LDS rows
+
+// Tile shape: RK k-blocks of 32 features (r <= 32 RK) and NCT column tiles of
+// 16 (p <= 16 NCT).  The wide shape (4, 9) covers r <= 128, p <= 144; the
+// narrow one (2, 5) covers r <= 64, p <= 80 with half the registers and under
+// half the LDS, so two workgroups share a CU.
+template <int RK> constexpr int rpad() { return RK * 32 + 8; }   // r-indexed LDS rows
 
 // tokens per staged block: 64 for 16-bit inputs, 32 for fp32 (LDS budget)
 template <typename In> constexpr int bn() { return sizeof(In) == 4 ? 32 : 64; }
 template <typename In> constexpr int npad() { return bn<In>() + 8; }
 
-template <typename In>
+template <typename In, int RK, int NCT>
 constexpr int state_bytes() {
-  return Traits<In>::split ? 2 * kCols * kRPad * (int)sizeof(In) : kCols * kRPad * 4;
+  return Traits<In>::split ? 2 * NCT * 16 * rpad<RK>() * (int)sizeof(In)
+                           : NCT * 16 * rpad<RK>() * 4;
 }
-template <typename In>
+template <typename In, int RK, int NCT>
 constexpr int block_bytes() {
-  // psiS [bn][kRPad], psiT [128][npad], vbT [kCols][npad]
-  return (bn<In>() * kRPad + 128 * npad<In>() + kCols * npad<In>()) * (int)sizeof(In);
+  // psiS [bn][rpad], psiT [32 RK][npad], vbT [16 NCT][npad]
+  return (bn<In>() * rpad<RK>() + RK * 32 * npad<In>() + NCT * 16 * npad<In>()) *
+         (int)sizeof(In);
 }
 }  // namespace sf
 
-template <typename In, bool VEC>
-__global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
+template <typename In, bool VEC, int kRK, int kNCT>
+__global__ __launch_bounds__(sf::kThreads, kRK <= 2 ? 2 : 1) void scan_fused_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
     const float* __restrict__ Sg, const float* __restrict__ Y, const float* __restrict__ gate,
     float* __restrict__ out, ScanArgs a) {
@@ -56,13 +60,18 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
   typedef typename Traits<In>::frag Frag;
   constexpr int kBN = bn<In>();
   constexpr int kNPad = npad<In>();
-  __shared__ __attribute__((aligned(16))) char smem[state_bytes<In>() + block_bytes<In>()];
+  constexpr int kRPad = rpad<kRK>();
+  constexpr int kCols = kNCT * 16;
+  constexpr int kTW = kRK / 2;          // 16-row tiles of S per wave: wave w owns tiles kTW w + t
+  static_assert(kRK % 2 == 0, "four waves split 2 kRK row tiles of S");
+  __shared__ __attribute__((aligned(16))) char smem[state_bytes<In, kRK, kNCT>() +
+                                                    block_bytes<In, kRK, kNCT>()];
   In* sT_hi = reinterpret_cast<In*>(smem);                 // S^T [c][a] (hi, or fp32 whole)
   In* sT_lo = sT_hi + kCols * kRPad;
   float* sT32 = reinterpret_cast<float*>(smem);
-  In* psiS = reinterpret_cast<In*>(smem + state_bytes<In>());   // [kBN][kRPad]
-  In* psiT = psiS + kBN * kRPad;                                 // [128][kNPad]
-  In* vbT = psiT + 128 * kNPad;                                  // [kCols][kNPad]
+  In* psiS = reinterpret_cast<In*>(smem + state_bytes<In, kRK, kNCT>());   // [kBN][kRPad]
+  In* psiT = psiS + kBN * kRPad;                                 // [32 kRK][kNPad]
+  In* vbT = psiT + kRK * 32 * kNPad;                             // [kCols][kNPad]
 
   const int grp = blockIdx.x;
   const int64_t b = blockIdx.y;
@@ -93,16 +102,18 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
   const int ncols = nct * 16;
   const int tpsi = (kBN / 8) * kgroups;
   const int ttot = tpsi + (kBN / 8) * (ncols / 8);
+  // tiles per thread: the most the shape can stage, (kBN/8)(4 kRK + 2 kNCT)
+  constexpr int kTiles = ((kBN / 8) * (4 * kRK + 2 * kNCT) + kThreads - 1) / kThreads;
   struct Pf {
-    Tile8<In> tl[2];
-    int tt[2], c0[2];
-    bool psi[2], live[2];
+    Tile8<In> tl[kTiles];
+    int tt[kTiles], c0[kTiles];
+    bool psi[kTiles], live[kTiles];
   } pf;
   auto stage_issue = [&](Pf& f, int chk, int nb0) {
     const int64_t tk0 = (int64_t)chk * C;
     const int cv = (int)min((int64_t)C, (int64_t)a.T - tk0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kTiles; ++j) {
       const int tile = threadIdx.x + j * kThreads;
       f.live[j] = tile < ttot;
       if (!f.live[j]) continue;
@@ -134,7 +145,7 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
   };
   auto stage_commit = [&](Pf& f, In* dS, In* dT, In* dV) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kTiles; ++j) {
       if (!f.live[j]) continue;
       if constexpr (VEC) tile8_finish<In>(f.tl[j]);
       if (f.psi[j]) {
@@ -148,12 +159,12 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
   if (c0 < c1) stage_issue(pf, c0, 0);
 
   // ---- incoming state: this wave's rows of S in accumulators, S^T in LDS ----
-  f32x4 accS[2][kNCT];
+  f32x4 accS[kTW][kNCT];
   {
     const float* Sb = Sg + ((int64_t)b * gridDim.x + grp) * (int64_t)r * p;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int rt = 2 * w + t;
+    for (int t = 0; t < kTW; ++t) {
+      const int rt = kTW * w + t;
 #pragma unroll
       for (int ct = 0; ct < kNCT; ++ct) {
         const int c = ct * 16 + row16;
@@ -181,8 +192,8 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
     // four consecutive rows of one column, one 8-byte (fp32: 16-byte) store.
     lds_barrier();        // previous chunk's readers of sT are done
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int rt = 2 * w + t;
+    for (int t = 0; t < kTW; ++t) {
+      const int rt = kTW * w + t;
 #pragma unroll
       for (int ct = 0; ct < kNCT; ++ct) {
         const int off = (ct * 16 + row16) * kRPad + rt * 16 + 4 * g4;
@@ -215,26 +226,31 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
         phiA[t][kb] = load8v<In, VEC>(phib + (t0 + m) * a.q_st + k0, phib + t0 * a.q_st, nv);
       }
     }
-    // ---- this chunk's long-range rows (recent rows only), loaded now so the
-    // latency overlaps the products; branch-free from a clamped address ----
+    // ---- this chunk's long-range rows (recent rows only), branch-free from a
+    // clamped address.  The wide shape loads them now so the latency overlaps
+    // the products; the narrow one, two workgroups to a CU, loads them just
+    // before they are added and keeps the registers for the products ----
     float yv[2][kNCT][4];
+    auto load_y = [&]() {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 2; ++t) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = mrow[t] + 4 * g4 + i;
-        const int64_t row = t0 + m;
-        const bool rec = m < Cv && !a.write_H && Y != nullptr && row >= a.n;
-        const float* yrow = rec ? Y + b * a.y_sb + (row - a.n) * a.y_st : Y;
+        for (int i = 0; i < 4; ++i) {
+          const int m = mrow[t] + 4 * g4 + i;
+          const int64_t row = t0 + m;
+          const bool rec = m < Cv && !a.write_H && Y != nullptr && row >= a.n;
+          const float* yrow = rec ? Y + b * a.y_sb + (row - a.n) * a.y_st : Y;
 #pragma unroll
-        for (int ct = 0; ct < kNCT; ++ct) {
-          const int c = ct * 16 + row16;
-          const bool ok = rec && c < p;
-          const float v = (Y != nullptr) ? yrow[ok ? c : 0] : 0.f;
-          yv[t][ct][i] = ok ? v : 0.f;
+          for (int ct = 0; ct < kNCT; ++ct) {
+            const int c = ct * 16 + row16;
+            const bool ok = rec && c < p;
+            const float v = (Y != nullptr) ? yrow[ok ? c : 0] : 0.f;
+            yv[t][ct][i] = ok ? v : 0.f;
+          }
         }
       }
-    }
+    };
+    if constexpr (kRK > 2) load_y();
     lds_barrier();        // sT complete
 
     // ---- inter-chunk term: Phi S ----
@@ -333,8 +349,8 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
       for (int kk = 0; kk < kBN / 32; ++kk) {
         if (n0 + 32 * kk >= Cv) continue;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int rt = 2 * w + t;
+        for (int t = 0; t < kTW; ++t) {
+          const int rt = kTW * w + t;
           if (rt >= nrt) continue;
           const Frag av = *reinterpret_cast<const Frag*>(psiT + (rt * 16 + row16) * kNPad +
                                                          32 * kk + 8 * g4);
@@ -350,6 +366,7 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
     }
 
     // ---- normalise and store the chunk's rows ----
+    if constexpr (kRK <= 2) load_y();
     const int pn = p - 1;                         // the normaliser column
     const int ctn = pn >> 4, ln = pn & 15;
 #pragma unroll
@@ -394,21 +411,30 @@ __global__ __launch_bounds__(sf::kThreads, 1) void scan_fused_kernel(
   }
 }
 
-template <typename In>
-static int launch_scan_fused(const void* phi, const void* psi, const void* vb, const float* Sg,
-                             const float* Y, const float* gate, float* out, int nb, int ng,
-                             const ScanArgs& a, hipStream_t stream) {
+template <typename In, int RK, int NCT>
+static int launch_scan_fused_shape(const void* phi, const void* psi, const void* vb,
+                                   const float* Sg, const float* Y, const float* gate, float* out,
+                                   int nb, int ng, const ScanArgs& a, hipStream_t stream) {
   const int eb = sizeof(In);
   const bool vec = rows_vec_ok(phi, a.q_sb, a.q_st, eb) && rows_vec_ok(psi, a.k_sb, a.k_st, eb) &&
                    rows_vec_ok(vb, a.v_sb, a.v_st, eb);
   dim3 grid((unsigned)ng, (unsigned)nb);
   if (vec)
-    hipLaunchKernelGGL((scan_fused_kernel<In, true>), grid, dim3(sf::kThreads), 0, stream,
-                       (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a);
+    hipLaunchKernelGGL((scan_fused_kernel<In, true, RK, NCT>), grid, dim3(sf::kThreads), 0,
+                       stream, (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a);
   else
-    hipLaunchKernelGGL((scan_fused_kernel<In, false>), grid, dim3(sf::kThreads), 0, stream,
-                       (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a);
+    hipLaunchKernelGGL((scan_fused_kernel<In, false, RK, NCT>), grid, dim3(sf::kThreads), 0,
+                       stream, (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a);
   return launch_status("smat_causal_scan");
+}
+
+template <typename In>
+static int launch_scan_fused(const void* phi, const void* psi, const void* vb, const float* Sg,
+                             const float* Y, const float* gate, float* out, int nb, int ng,
+                             const ScanArgs& a, hipStream_t stream) {
+  if (a.r <= 64 && a.p <= 80)
+    return launch_scan_fused_shape<In, 2, 5>(phi, psi, vb, Sg, Y, gate, out, nb, ng, a, stream);
+  return launch_scan_fused_shape<In, 4, 9>(phi, psi, vb, Sg, Y, gate, out, nb, ng, a, stream);
 }
 
 int chunk_states_dispatch(int dtype, const void* psi, const void* vb, float* D, int nb, int T,

@@ -215,7 +215,8 @@ def test_chunk_states_and_segment_scan(dt):
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("T,n,C,hd", [(2048, 1024, 128, 64), (2048 + 77, 1024, 128, 32),
                                       (4096, 2048, 64, 32), (1000, 0, 128, 32),
-                                      (8192, 4096, 128, 128), (300, 256, 128, 16)])
+                                      (8192, 4096, 128, 128), (300, 256, 128, 16),
+                                      (2048 + 40, 1024, 64, 48)])
 def test_causal_scan_fused(dt, T, n, C, hd):
     _say("causal scan fused", dt, T, n, C, hd)
     Phi, Psi, Vb = _feats(2, T, hd, dt, seed=9)
