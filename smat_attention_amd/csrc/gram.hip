@@ -20,21 +20,30 @@ namespace smat {
 
 namespace gr {
 constexpr int kThreads = 256;
-constexpr int kBT = 32;                 // tokens per staged block (one MFMA k-block)
-constexpr int kTPad = kBT + 8;          // LDS row length (tokens) of the transposed tiles
-constexpr int kRows = 128;              // r <= 128
-constexpr int kCols = 144;              // p <= 144
-constexpr int kNCT = kCols / 16;
+constexpr int kBT = 32;                 // token granularity of split-K runs
+
+// Tile shape: wave w owns the 16-row tiles kTW w .. kTW w + kTW - 1 of G and
+// the first 16 kNCT columns.  Wide (2, 9): r <= 128, p <= 144; narrow (1, 5):
+// r <= 64, p <= 80, a quarter of the accumulators and under half the LDS.
+// Tokens per staged block: 64 for 16-bit inputs, 32 for fp32.
+template <typename In> constexpr int bt() { return sizeof(In) == 4 ? 32 : 64; }
 }  // namespace gr
 
-// How item i of batch b maps to a token progression.
-template <typename In, bool VEC>
-__global__ __launch_bounds__(gr::kThreads) void gram_kernel(
+// G = sum Psi_t^T Vb_t over one progression.  Each block of tokens is staged
+// in LDS transposed (Psi^T[a][t], Vb^T[c][t]) from 8 x 8 tiles; the next
+// block's tiles are loaded into registers while the current block is
+// multiplied, so one memory latency per block overlaps the MFMAs.
+template <typename In, bool VEC, int kTW, int kNCT>
+__global__ __launch_bounds__(gr::kThreads, kTW == 1 ? 4 : 2) void gram_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, float* __restrict__ G,
     float* __restrict__ G_last, GramItems it, int r, int p, int64_t k_sb, int64_t k_st,
     int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si, int64_t gl_sb) {
   using namespace gr;
   typedef typename Traits<In>::frag Frag;
+  constexpr int kB = bt<In>();
+  constexpr int kTPad = kB + 8;           // LDS row length (tokens) of the transposed tiles
+  constexpr int kRows = 64 * kTW;
+  constexpr int kCols = 16 * kNCT;
   __shared__ __attribute__((aligned(16))) In psiT[kRows * kTPad];
   __shared__ __attribute__((aligned(16))) In vbT[kCols * kTPad];
 
@@ -59,55 +68,82 @@ __global__ __launch_bounds__(gr::kThreads) void gram_kernel(
   const In* psib = psi + b * k_sb;
   const In* vbb = vb + b * v_sb;
 
-  f32x4 acc[2][kNCT];
+  f32x4 acc[kTW][kNCT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < kTW; ++t)
 #pragma unroll
     for (int ct = 0; ct < kNCT; ++ct) acc[t][ct] = zero4();
 
+  // staging: tiles [0, tpsi) are Psi's, the rest Vb's; a thread owns tiles
+  // tid + j kThreads, at most kTiles of them
   const int nrows = nrt * 16, ncols = nct * 16;
-  for (int s0 = 0; s0 < count; s0 += kBT) {
-    // stage Psi^T[a][tt] and Vb^T[c][tt] for tokens s0 + tt, 8 x 8 tiles
-    {
-      const int tpsi = (kBT / 8) * (nrows / 8);
-      const int tvb = (kBT / 8) * (ncols / 8);
-      for (int tile = threadIdx.x; tile < tpsi + tvb; tile += kThreads) {
-        const bool is_psi = tile < tpsi;
-        const int tix = is_psi ? tile : tile - tpsi;
-        const int per_row = is_psi ? nrows / 8 : ncols / 8;
-        const int tt = (tix / per_row) * 8, c0 = (tix % per_row) * 8;
-        const In* rowp[8];
+  const int tpsi = (kB / 8) * (nrows / 8);
+  const int ttot = tpsi + (kB / 8) * (ncols / 8);
+  constexpr int kTiles = ((kB / 8) * (kRows / 8 + kCols / 8) + kThreads - 1) / kThreads;
+  struct Pf {
+    Tile8<In> tl[kTiles];
+    int tt[kTiles], c0[kTiles];
+    bool psi[kTiles], live[kTiles];
+  } pf;
+  auto stage_issue = [&](int s0) {
+    const int64_t tok0 = gram_token(it, item, start, stride, s0);    // valid: s0 < count
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int sidx = s0 + tt + u;
-          const int64_t tok = sidx < count ? gram_token(it, item, start, stride, sidx) : 0;
-          rowp[u] = sidx < count ? (is_psi ? psib + tok * k_st : vbb + tok * v_st) : nullptr;
-        }
-        Tile8<In> tl;
-        const int64_t tok0 = gram_token(it, item, start, stride, s0);    // valid: s0 < count
-        if (is_psi) {
-          tile8_load<In, VEC>(tl, rowp, psib + tok0 * k_st, c0, r);
-          tile8_store_T<In>(tl, psiT, kTPad, c0, tt);
-        } else {
-          tile8_load<In, VEC>(tl, rowp, vbb + tok0 * v_st, c0, p);
-          tile8_store_T<In>(tl, vbT, kTPad, c0, tt);
+    for (int j = 0; j < kTiles; ++j) {
+      const int tile = threadIdx.x + j * kThreads;
+      pf.live[j] = tile < ttot;
+      if (!pf.live[j]) continue;
+      const bool is_psi = tile < tpsi;
+      const int tix = is_psi ? tile : tile - tpsi;
+      const int per_row = is_psi ? nrows / 8 : ncols / 8;
+      pf.psi[j] = is_psi;
+      pf.tt[j] = (tix / per_row) * 8;
+      pf.c0[j] = (tix % per_row) * 8;
+      const In* rowp[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int sidx = s0 + pf.tt[j] + u;
+        const int64_t tok = sidx < count ? gram_token(it, item, start, stride, sidx) : 0;
+        rowp[u] = sidx < count ? (is_psi ? psib + tok * k_st : vbb + tok * v_st) : nullptr;
+      }
+      const In* safe = is_psi ? psib + tok0 * k_st : vbb + tok0 * v_st;
+      if constexpr (VEC)
+        tile8_issue<In>(pf.tl[j], rowp, safe, pf.c0[j], is_psi ? r : p);
+      else
+        tile8_load<In, false>(pf.tl[j], rowp, safe, pf.c0[j], is_psi ? r : p);
+    }
+  };
+  auto stage_commit = [&]() {
+#pragma unroll
+    for (int j = 0; j < kTiles; ++j) {
+      if (!pf.live[j]) continue;
+      if constexpr (VEC) tile8_finish<In>(pf.tl[j]);
+      tile8_store_T<In>(pf.tl[j], pf.psi[j] ? psiT : vbT, kTPad, pf.c0[j], pf.tt[j]);
+    }
+  };
+
+  if (count > 0) stage_issue(0);
+  for (int s0 = 0; s0 < count; s0 += kB) {
+    if (s0 > 0) lds_barrier();       // the previous block's readers are done
+    stage_commit();
+    lds_barrier();
+    if (s0 + kB < count) stage_issue(s0 + kB);
+#pragma unroll
+    for (int ks = 0; ks < kB / 32; ++ks) {
+#pragma unroll
+      for (int t = 0; t < kTW; ++t) {
+        const int rt = kTW * w + t;
+        if (rt >= nrt) continue;
+        const Frag a =
+            *reinterpret_cast<const Frag*>(psiT + (rt * 16 + row16) * kTPad + 32 * ks + 8 * grp);
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct) {
+          if (ct >= nct) continue;
+          const Frag bf = *reinterpret_cast<const Frag*>(vbT + (ct * 16 + row16) * kTPad +
+                                                         32 * ks + 8 * grp);
+          acc[t][ct] = mma(acc[t][ct], a, bf);
         }
       }
     }
-    lds_barrier();
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int rt = 2 * w + t;
-      if (rt >= nrt) continue;
-      const Frag a = *reinterpret_cast<const Frag*>(psiT + (rt * 16 + row16) * kTPad + 8 * grp);
-#pragma unroll
-      for (int ct = 0; ct < kNCT; ++ct) {
-        if (ct >= nct) continue;
-        const Frag bf = *reinterpret_cast<const Frag*>(vbT + (ct * 16 + row16) * kTPad + 8 * grp);
-        acc[t][ct] = mma(acc[t][ct], a, bf);
-      }
-    }
-    lds_barrier();
   }
 
   // nsplit > 1: G is the partial buffer (nb, nitems, nsplit, r, p) and G_last
@@ -119,8 +155,8 @@ __global__ __launch_bounds__(gr::kThreads) void gram_kernel(
   else
     Gb = (G_last != nullptr && item == nitems - 1) ? G_last + b * gl_sb : G + b * g_sb + item * g_si;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int rt = 2 * w + t;
+  for (int t = 0; t < kTW; ++t) {
+    const int rt = kTW * w + t;
     if (rt >= nrt) continue;
 #pragma unroll
     for (int ct = 0; ct < kNCT; ++ct) {
@@ -153,8 +189,8 @@ __global__ __launch_bounds__(256) void gram_reduce_kernel(const float* __restric
   dst[e] = acc;
 }
 
-template <typename In>
-static int launch_gram(const void* psi, const void* vb, float* G, float* G_last,
+template <typename In, int TW, int NCT>
+static int launch_gram_shape(const void* psi, const void* vb, float* G, float* G_last,
                        const GramItems& it, int nitems, int nb, int r, int p, int64_t k_sb,
                        int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
                        int64_t gl_sb, float* partials, hipStream_t stream, const char* who) {
@@ -167,11 +203,11 @@ static int launch_gram(const void* psi, const void* vb, float* G, float* G_last,
   }
   if (it.nsplit > 1) {
     if (vk && vv)
-      hipLaunchKernelGGL((gram_kernel<In, true>), dim3((unsigned)gx, (unsigned)nb),
+      hipLaunchKernelGGL((gram_kernel<In, true, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
                          dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, partials,
                          nullptr, it, r, p, k_sb, k_st, v_sb, v_st, 0, 0, 0);
     else
-      hipLaunchKernelGGL((gram_kernel<In, false>), dim3((unsigned)gx, (unsigned)nb),
+      hipLaunchKernelGGL((gram_kernel<In, false, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
                          dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, partials,
                          nullptr, it, r, p, k_sb, k_st, v_sb, v_st, 0, 0, 0);
     int st = launch_status(who);
@@ -183,14 +219,26 @@ static int launch_gram(const void* psi, const void* vb, float* G, float* G_last,
     return launch_status(who);
   }
   if (vk && vv)
-    hipLaunchKernelGGL((gram_kernel<In, true>), dim3((unsigned)gx, (unsigned)nb),
+    hipLaunchKernelGGL((gram_kernel<In, true, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, G, G_last,
                        it, r, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb);
   else
-    hipLaunchKernelGGL((gram_kernel<In, false>), dim3((unsigned)gx, (unsigned)nb),
+    hipLaunchKernelGGL((gram_kernel<In, false, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, G, G_last,
                        it, r, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb);
   return launch_status(who);
+}
+
+template <typename In>
+static int launch_gram(const void* psi, const void* vb, float* G, float* G_last,
+                       const GramItems& it, int nitems, int nb, int r, int p, int64_t k_sb,
+                       int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                       int64_t gl_sb, float* partials, hipStream_t stream, const char* who) {
+  if (r <= 64 && p <= 80)
+    return launch_gram_shape<In, 1, 5>(psi, vb, G, G_last, it, nitems, nb, r, p, k_sb, k_st, v_sb,
+                                       v_st, g_sb, g_si, gl_sb, partials, stream, who);
+  return launch_gram_shape<In, 2, 9>(psi, vb, G, G_last, it, nitems, nb, r, p, k_sb, k_st, v_sb,
+                                     v_st, g_sb, g_si, gl_sb, partials, stream, who);
 }
 
 // Choose the split of the longest progression so that a launch has enough
