@@ -11,88 +11,110 @@ namespace smat {
 
 namespace dc {
 constexpr int kThreads = 1024;
-constexpr int kCols = 144;                // p <= 144 columns, one thread column each
-constexpr int kParts = kThreads / kCols;  // 7 feature partitions (1008 threads busy)
-constexpr int kRows = (kMaxR + kParts - 1) / kParts;   // rows per thread, at most 19
 }  // namespace dc
 
-// One workgroup per sequence: thread (part, c) owns column c of the rows
-// a = part, part + 7, ... (at most 19, all loaded up front); it advances S
-// there (S_out = S_in + psi vb^T) and
-// accumulates phi_a (S_out + U_h)[a][c].  The 7 partial sums of each column
-// meet in LDS, which also hands every column the normaliser o[p-1] -- one read
-// of S, U_h and one write of S per sequence, nothing recomputed.
-template <typename In>
+// One sequence is split by value columns over nsplit workgroups (blockIdx.y):
+// workgroup s owns columns [s cw, s cw + cw) of the p - 1 value columns, cw =
+// ceil((p - 1) / nsplit), and also the normaliser column p - 1, which every
+// workgroup needs for its division (only s = 0 writes it back).  Within a
+// workgroup, thread (part, cl) owns local column cl of the rows a = part,
+// part + kParts, ... (at most kRows, all loaded up front); it advances S there
+// (S_out = S_in + psi vb^T) and accumulates phi_a (S_out + U_h)[a][c].  The
+// kParts partial sums of each column meet in LDS, which also hands every
+// column the normaliser -- S and U_h are read once and S written once, the
+// normaliser column aside.
+template <typename In, int kCols>
 __global__ __launch_bounds__(dc::kThreads) void decode_step_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
     const float* __restrict__ S_in, float* __restrict__ S_out, const float* __restrict__ U,
     float* __restrict__ out, float* __restrict__ o_full, int B, int r, int p, int64_t step,
     int64_t q_sb, int64_t k_sb, int64_t v_sb) {
   using namespace dc;
-  __shared__ float sphi[kMaxR], spsi[kMaxR], svb[kMaxP];
+  constexpr int kParts = kThreads / kCols;                 // feature partitions
+  constexpr int kRows = (kMaxR + kParts - 1) / kParts;     // rows per thread
+  __shared__ float sphi[kThreads], spsi[kThreads], svb[kThreads];   // one slot per thread
   __shared__ float red[kParts][kCols];
 
   const int64_t b = blockIdx.x;
+  const int sp = blockIdx.y, nsplit = gridDim.y;
   const int tid = threadIdx.x;
-  const int c = tid % kCols, part = tid / kCols;
+  const int cl = tid % kCols, part = tid / kCols;
   const int h = (int)(step % B);
+  const int cw = (p - 1 + nsplit - 1) / nsplit;            // value columns per workgroup
+  const int cbeg = sp * cw;
+  const int ncw = max(0, min(p - 1, cbeg + cw) - cbeg);    // this one's (ncw < kCols)
+  const int c = cl < ncw ? cbeg + cl : p - 1;              // cl = ncw: the normaliser
+  const bool mine = part < kParts && cl <= ncw;
+  const bool writes = cl < ncw || sp == 0;                 // S and o_full of column c
 
   const int64_t rp = (int64_t)r * p;
   const float* Sb = S_in + b * rp;
   float* Sob = S_out + b * rp;
   const float* Ub = U + (b * B + h) * rp;
-  const bool mine = part < kParts && c < p;
 
-  // every row of this thread (at most kRows) is loaded before phi, psi and vb
-  // are staged: the state and the step's inputs are in flight together, one
-  // memory latency per step instead of two.  U_h is read with non-temporal
-  // loads (a type row comes back only B steps later); S is read again next
-  // step and may stay in the caches.
+  // Loads, in issue order: this step's phi, psi and vb entry, then every row
+  // of this thread (at most kRows of S and of U_h).  All are unconditional
+  // (clamped indices), so each thread has a fixed count in flight, and loads
+  // retire in order: the barrier that publishes phi, psi and vb waits for the
+  // first three only, and each row below waits for its own pair while the
+  // rest stream in -- the stores of S' start as the first rows land.  U_h is
+  // read with non-temporal loads (a type row comes back only B steps later);
+  // S is read again next step and may stay in the caches.
+  const float fphi = to_f32(phi[b * q_sb + min(tid, r - 1)]);
+  const float fpsi = to_f32(psi[b * k_sb + min(tid, r - 1)]);
+  const float fvb = to_f32(vb[b * v_sb + min(tid, p - 1)]);
+  __builtin_amdgcn_sched_barrier(0);   // ... issued before the rows
   float sv[kRows], uv[kRows];
-  if (mine) {
 #pragma unroll
-    for (int u = 0; u < kRows; ++u) {
-      const int a = part + u * kParts;
-      if (a < r) {
-        const int64_t o = (int64_t)a * p + c;
-        sv[u] = Sb[o];
-        uv[u] = __builtin_nontemporal_load(Ub + o);
-      }
-    }
+  for (int u = 0; u < kRows; ++u) {
+    const int64_t o = (int64_t)min(part + u * kParts, r - 1) * p + c;    // c < p always
+    sv[u] = Sb[o];
+    uv[u] = __builtin_nontemporal_load(Ub + o);
   }
-  if (tid < r) {
-    sphi[tid] = to_f32(phi[b * q_sb + tid]);
-    spsi[tid] = to_f32(psi[b * k_sb + tid]);
-  }
-  if (tid < p) svb[tid] = to_f32(vb[b * v_sb + tid]);
+  __builtin_amdgcn_sched_barrier(0);   // the rows are issued before the barrier below
+  // unconditional stores: a branch here would let the compiler sink the
+  // three loads below the rows (entries past r and p are never read)
+  sphi[tid] = fphi;
+  spsi[tid] = fpsi;
+  svb[tid] = fvb;
   __syncthreads();
 
+  // branch-free but for the store, so the row loads stay ahead of the
+  // barrier (a branch around their uses would let the compiler sink them)
   float acc = 0.f;
-  if (mine) {
-    const float vc = svb[c];
+  const float vc = svb[c];
 #pragma unroll
-    for (int u = 0; u < kRows; ++u) {
-      const int a = part + u * kParts;
-      if (a < r) {
-        const float s = sv[u] + spsi[a] * vc;
-        Sob[(int64_t)a * p + c] = s;
-        acc += sphi[a] * (s + uv[u]);
-      }
-    }
+  for (int u = 0; u < kRows; ++u) {
+    const int a = part + u * kParts;
+    const int ac = min(a, r - 1);
+    const bool ok = mine && a < r;
+    const float s = sv[u] + spsi[ac] * vc;
+    if (ok && writes) Sob[(int64_t)a * p + c] = s;
+    acc += ok ? sphi[ac] * (s + uv[u]) : 0.f;
   }
-  if (part < kParts) red[part][c] = acc;
+  if (part < kParts) red[part][cl] = acc;
   __syncthreads();
 
-  if (tid < p) {
+  if (tid <= ncw) {
     float o = 0.f, den = 0.f;
 #pragma unroll
     for (int i = 0; i < kParts; ++i) {
       o += red[i][tid];
-      den += red[i][p - 1];
+      den += red[i][ncw];
     }
-    if (o_full) o_full[b * p + tid] = o;
-    if (tid < p - 1) out[b * (p - 1) + tid] = o / den;
+    const int cc = tid < ncw ? cbeg + tid : p - 1;
+    if (o_full && (tid < ncw || sp == 0)) o_full[b * p + cc] = o;
+    if (tid < ncw) out[b * (p - 1) + cc] = o / den;
   }
+}
+
+// Column split: the fewest workgroups per sequence (1, 2 or 4) that give at
+// least 256 workgroups, one per CU, so a small batch still streams S and U_h
+// through every CU.
+static int decode_split(int nb) {
+  int ns = 1;
+  while (ns < 4 && (int64_t)nb * ns < 256) ns <<= 1;
+  return ns;
 }
 
 template <typename In>
@@ -100,9 +122,22 @@ static int launch_decode(const void* phi, const void* psi, const void* vb, const
                          float* S_out, const float* U, float* out, float* o_full, int nb, int B,
                          int r, int p, int64_t step, int64_t q_sb, int64_t k_sb, int64_t v_sb,
                          hipStream_t stream) {
-  hipLaunchKernelGGL(decode_step_kernel<In>, dim3((unsigned)nb), dim3(dc::kThreads), 0, stream,
-                     (const In*)phi, (const In*)psi, (const In*)vb, S_in, S_out, U, out, o_full,
-                     B, r, p, step, q_sb, k_sb, v_sb);
+  const int ns = decode_split(nb);
+  const dim3 grid((unsigned)nb, (unsigned)ns);
+  // local columns: ceil((p - 1) / ns) value columns and the normaliser, with
+  // p <= 144: at most 144, 73 and 37
+  if (ns == 1)
+    hipLaunchKernelGGL((decode_step_kernel<In, 144>), grid, dim3(dc::kThreads), 0, stream,
+                       (const In*)phi, (const In*)psi, (const In*)vb, S_in, S_out, U, out, o_full,
+                       B, r, p, step, q_sb, k_sb, v_sb);
+  else if (ns == 2)
+    hipLaunchKernelGGL((decode_step_kernel<In, 80>), grid, dim3(dc::kThreads), 0, stream,
+                       (const In*)phi, (const In*)psi, (const In*)vb, S_in, S_out, U, out, o_full,
+                       B, r, p, step, q_sb, k_sb, v_sb);
+  else
+    hipLaunchKernelGGL((decode_step_kernel<In, 48>), grid, dim3(dc::kThreads), 0, stream,
+                       (const In*)phi, (const In*)psi, (const In*)vb, S_in, S_out, U, out, o_full,
+                       B, r, p, step, q_sb, k_sb, v_sb);
   return launch_status("smat_decode_step");
 }
 

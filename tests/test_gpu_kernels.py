@@ -466,6 +466,24 @@ def test_decode_matches_prefill(dt, T, d):
     assert dec.cache_words() == 3 * (spec.B + 1) * 32 * 33
 
 
+@pytest.mark.parametrize("nb,hd", [(256, 128), (128, 128), (128, 47), (64, 2), (3, 128)])
+def test_decode_column_split(nb, hd):
+    """The step kernel splits a sequence's value columns over 1, 2 or 4
+    workgroups by batch size (256, 128 and 64 sequences here, with odd and
+    tiny column counts): every split reproduces the prefill's rows."""
+    _say("decode split", nb, hd)
+    T = 1024
+    spec = build_mask(T, 3, chunk=128)
+    Phi, Psi, Vb = _feats(nb, T, hd, torch.float32, seed=15)
+    Pd, Sd, Wd = (x.to(DEV) for x in (Phi, Psi, Vb))
+    pre = A.smat_attention(Pd, Sd, Wd, spec)
+    n = spec.n
+    dec = A.SmatDecoder(Sd[:, :n], Wd[:, :n], spec)
+    for i in range(24):
+        o = dec.step(Pd[:, n + i], Sd[:, n + i], Wd[:, n + i])
+        assert _rel(o, pre[:, n + i]) < 1e-5, i
+
+
 # ---------------------------------------------------------------------------
 # the other schedules: endpoint (zeta + Walsh), direct, subtractive
 # ---------------------------------------------------------------------------
