@@ -504,8 +504,13 @@ __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* ps
   }
 }
 
-template <typename In>
-__global__ __launch_bounds__(ss::kThreads, 2) void gram_stream_kernel(
+// ONE: every item of the launch has at most kStep terms (the profile pool at
+// long T: (n - n_P) / N0 tokens a profile), so one buffer suffices.  Its
+// 35 KB of LDS let three workgroups share a CU instead of two, which is what
+// a launch of one-step items -- a load latency, a few MFMAs and a 66 KB
+// store each -- is limited by.
+template <typename In, bool ONE>
+__global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, float* __restrict__ G,
     float* __restrict__ G_last, GramItems it, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
     int64_t v_st, int64_t g_sb, int64_t g_si, int64_t gl_sb) {
@@ -513,8 +518,8 @@ __global__ __launch_bounds__(ss::kThreads, 2) void gram_stream_kernel(
   typedef typename Traits<In>::frag Frag;
   __shared__ __attribute__((aligned(16))) uint4 psi0[kTileChunks];
   __shared__ __attribute__((aligned(16))) uint4 vb0[kVbTileChunks];
-  __shared__ __attribute__((aligned(16))) uint4 psi1[kTileChunks];
-  __shared__ __attribute__((aligned(16))) uint4 vb1[kVbTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 psi1[ONE ? 1 : kTileChunks];
+  __shared__ __attribute__((aligned(16))) uint4 vb1[ONE ? 1 : kVbTileChunks];
 
   const int item = blockIdx.x;
   const int64_t b = blockIdx.y;
@@ -541,7 +546,7 @@ __global__ __launch_bounds__(ss::kThreads, 2) void gram_stream_kernel(
     int lane = lane_id();
     asm volatile("" : "+v"(lane));
     const int g = lane >> 4;
-    if (s + 1 < nsteps) {
+    if (!ONE && s + 1 < nsteps) {
       issue_gram<In>(BUF ? psi0 : psi1, BUF ? vb0 : vb1, psib, vbb, it, item, start, stride,
                      (s + 1) * kStep, count, k_st, v_st, w, lane);
       if (w < 2)
@@ -574,9 +579,13 @@ __global__ __launch_bounds__(ss::kThreads, 2) void gram_stream_kernel(
     }
     lds_barrier();     // this buffer is free for the DMA issued next step
   };
-  for (int s = 0; s < nsteps; s += 2) {
-    step(std::integral_constant<int, 0>{}, s);
-    if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+  if constexpr (ONE) {
+    if (nsteps > 0) step(std::integral_constant<int, 0>{}, 0);     // nsteps <= 1
+  } else {
+    for (int s = 0; s < nsteps; s += 2) {
+      step(std::integral_constant<int, 0>{}, s);
+      if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+    }
   }
 
   const int lane = lane_id();
@@ -609,14 +618,33 @@ int gram_stream_launch(int dtype, const void* psi, const void* vb, float* G, flo
                        int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
                        int64_t gl_sb, hipStream_t stream, const char* who) {
   dim3 grid((unsigned)nitems, (unsigned)nb);
-  if (dtype == SMAT_BF16)
-    hipLaunchKernelGGL(gram_stream_kernel<bf16>, grid, dim3(ss::kThreads), 0, stream,
-                       (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
-                       v_st, g_sb, g_si, gl_sb);
-  else
-    hipLaunchKernelGGL(gram_stream_kernel<f16>, grid, dim3(ss::kThreads), 0, stream,
-                       (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
-                       v_st, g_sb, g_si, gl_sb);
+  // the longest item: a profile has ceil((n - n_P) / N0) terms, the global
+  // channel (item N0, when launched) n_P
+  bool one = false;
+  if (it.mode == 1) {
+    int64_t maxc = it.N0 > 0 ? ((int64_t)it.n - it.n_P + it.N0 - 1) / it.N0 : 0;
+    if (nitems > it.N0) maxc = maxc > it.n_P ? maxc : it.n_P;
+    one = maxc <= ss::kStep;
+  }
+  if (dtype == SMAT_BF16) {
+    if (one)
+      hipLaunchKernelGGL((gram_stream_kernel<bf16, true>), grid, dim3(ss::kThreads), 0, stream,
+                         (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
+                         v_st, g_sb, g_si, gl_sb);
+    else
+      hipLaunchKernelGGL((gram_stream_kernel<bf16, false>), grid, dim3(ss::kThreads), 0, stream,
+                         (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
+                         v_st, g_sb, g_si, gl_sb);
+  } else {
+    if (one)
+      hipLaunchKernelGGL((gram_stream_kernel<f16, true>), grid, dim3(ss::kThreads), 0, stream,
+                         (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
+                         v_st, g_sb, g_si, gl_sb);
+    else
+      hipLaunchKernelGGL((gram_stream_kernel<f16, false>), grid, dim3(ss::kThreads), 0, stream,
+                         (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
+                         v_st, g_sb, g_si, gl_sb);
+  }
   return launch_status(who);
 }
 
