@@ -137,39 +137,58 @@ __device__ __forceinline__ typename Traits<In>::frag vb_tr(const uint4* tile, in
   return join<In>(h2[0], h2[1]);
 }
 
-// Issue the DMA of one step's Phi, Psi and Vb rows [ts, ts + 64) into one
-// buffer.  Load I of the 50 goes to wave I % 8: waves 0 and 1 issue seven,
-// the others six.  Each load moves 64 x 16 bytes to 1 KB of consecutive LDS;
-// which global chunk a lane fetches implements the swizzle.
+// The DMA of one step's Phi, Psi and Vb rows [ts, ts + 64) into one buffer.
+// Load I of the 50 goes to wave I % 8 as its slot u = I / 8: slots 0-1 are
+// Phi's loads 0-15, slots 2-3 Psi's, slots 4-6 Vb's 18 (waves 0 and 1 issue
+// seven, the others six).  Each load moves 64 x 16 bytes to 1 KB of
+// consecutive LDS; which global chunk a lane fetches implements the swizzle.
+// That choice does not depend on the step, so a lane's byte offset from the
+// step's first row is computed once per slot (dma_offsets); a step adds it
+// to the wave-uniform row base of the slot's tensor.
+struct DmaOffsets {
+  uint32_t off[7];
+};
+
+template <typename In>
+__device__ __forceinline__ void dma_offsets(DmaOffsets& d, const ScanArgs& a, int w, int lane) {
+#pragma unroll
+  for (int u = 0; u < 7; ++u) {
+    const int I = w + 8 * u;
+    int64_t e = 0;                                   // element offset from row ts
+    if (u < 4) {
+      const int li = I & 15;
+      const int row = 4 * li + (lane >> 4);
+      const int k = (lane & 15) ^ swz16(row);
+      e = (int64_t)row * (u < 2 ? a.q_st : a.k_st) + 8 * k;
+    } else if (I < ss::kLoads) {
+      const int L = 64 * (I - 2 * ss::kPhiLoads) + lane;
+      const int row = L / ss::kVbChunks;
+      const int k = L - row * ss::kVbChunks;
+      // chunks past the row (columns >= row stride) carry no data the
+      // kernel keeps; read the row's first chunk instead of the next row
+      const int col = 8 * k + 8 <= a.v_st ? 8 * k : 0;
+      e = (int64_t)row * a.v_st + col;
+    }
+    d.off[u] = (uint32_t)(e * (int64_t)sizeof(In));
+  }
+}
+
 template <typename In>
 __device__ __forceinline__ void issue_step(uint4* dphi, uint4* dpsi, uint4* dvb, const In* phib,
                                            const In* psib, const In* vbb, int64_t ts,
-                                           const ScanArgs& a, int w, int lane) {
+                                           const ScanArgs& a, int w, const DmaOffsets& d) {
+  const char* bphi = reinterpret_cast<const char*>(phib + ts * a.q_st);
+  const char* bpsi = reinterpret_cast<const char*>(psib + ts * a.k_st);
+  const char* bvb = reinterpret_cast<const char*>(vbb + ts * a.v_st);
 #pragma unroll
   for (int u = 0; u < 7; ++u) {
     const int I = w + 8 * u;
     if (I < ss::kLoads) {
-      const In* src;
-      uint4* dst;
-      if (I < 2 * ss::kPhiLoads) {
-        const bool is_phi = I < ss::kPhiLoads;
-        const int li = is_phi ? I : I - ss::kPhiLoads;
-        const int row = 4 * li + (lane >> 4);
-        const int k = (lane & 15) ^ swz16(row);
-        src = (is_phi ? phib + (ts + row) * a.q_st : psib + (ts + row) * a.k_st) + 8 * k;
-        dst = (is_phi ? dphi : dpsi) + 64 * li;
-      } else {
-        const int li = I - 2 * ss::kPhiLoads;
-        const int L = 64 * li + lane;
-        const int row = L / ss::kVbChunks;
-        const int k = L - row * ss::kVbChunks;
-        // chunks past the row (columns >= row stride) carry no data the
-        // kernel keeps; read the row's first chunk instead of the next row
-        const int col = 8 * k + 8 <= a.v_st ? 8 * k : 0;
-        src = vbb + (ts + row) * a.v_st + col;
-        dst = dvb + 64 * li;
-      }
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
+      const char* base = u < 2 ? bphi : u < 4 ? bpsi : bvb;
+      uint4* dst = u < 2 ? dphi + 64 * I
+                 : u < 4 ? dpsi + 64 * (I - ss::kPhiLoads)
+                         : dvb + 64 * (I - 2 * ss::kPhiLoads);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + d.off[u]),
                                        (SMAT_LDS void*)(SMAT_LDS char*)(dst), 16, 0, 0);
     }
   }
@@ -183,16 +202,36 @@ struct YRegs {
 
 // Twelve loads, always issued (dummy in-bounds addresses when a term is
 // absent), so the compiler's waits on them count a fixed number of loads.
-__device__ __forceinline__ void issue_y(YRegs& R, const float* Yb, const float* gb,
-                                       const float* dummy, int64_t ts, const ScanArgs& a, int w,
-                                       int lane) {
+// Per-lane byte offsets of the step's Y and output rows from row ts (the
+// lane's rows 16 tt + lane % 16 at columns 16 w + 4 g), computed once; a step
+// adds them to wave-uniform row bases.  y8 is the normaliser column's offset
+// from the lane's Y chunk.
+struct RowOffsets {
+  uint32_t y[4], o[4];
+  int y8;
+};
+
+__device__ __forceinline__ void row_offsets(RowOffsets& R, const ScanArgs& a, int w, int lane) {
   const int r16 = lane & 15, g = lane >> 4;
-  const bool rec = Yb != nullptr && ts >= a.n;
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
-    const float* yrow = rec ? Yb + (ts - a.n + 16 * tt + r16) * a.y_st : dummy;
-    R.y[tt] = *reinterpret_cast<const float4*>(rec ? yrow + 16 * w + 4 * g : dummy);
-    R.y8[tt] = rec ? yrow[a.p - 1] : 0.f;
+    R.y[tt] = (uint32_t)(((int64_t)(16 * tt + r16) * a.y_st + 16 * w + 4 * g) * 4);
+    R.o[tt] = (uint32_t)(((int64_t)(16 * tt + r16) * a.o_st + 16 * w + 4 * g) * 4);
+  }
+  R.y8 = (a.p - 1 - 16 * w - 4 * g) * 4;
+}
+
+__device__ __forceinline__ void issue_y(YRegs& R, const float* Yb, const float* gb,
+                                       const float* dummy, int64_t ts, const ScanArgs& a,
+                                       const RowOffsets& ro, int lane) {
+  const int r16 = lane & 15;
+  const bool rec = Yb != nullptr && ts >= a.n;
+  const char* yb = rec ? reinterpret_cast<const char*>(Yb + (ts - a.n) * a.y_st) : nullptr;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const char* yc = rec ? yb + ro.y[tt] : reinterpret_cast<const char*>(dummy);
+    R.y[tt] = *reinterpret_cast<const float4*>(yc);
+    R.y8[tt] = rec ? *reinterpret_cast<const float*>(yc + ro.y8) : 0.f;
     R.gv[tt] = gb ? gb[ts + 16 * tt + r16] : 1.f;
   }
 }
@@ -253,7 +292,11 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   float* outb = out + b * a.o_sb;
   const float* Sb = Sg + ((int64_t)b * gridDim.x + grp) * (int64_t)128 * a.p;
 
-  if (nsteps > 0) issue_step<In>(phi0, psi0, vb0, phib, psib, vbb, tk0, a, w, lane);
+  DmaOffsets dmo;
+  dma_offsets<In>(dmo, a, w, lane);
+  RowOffsets rof;
+  row_offsets(rof, a, w, lane);
+  if (nsteps > 0) issue_step<In>(phi0, psi0, vb0, phib, psib, vbb, tk0, a, w, dmo);
 
   // incoming state: S[a][16w + lane%16] for all a, and the normaliser column
   // block S[a][128 + lane%16] for this wave's rows a in [16w, 16w + 16)
@@ -290,7 +333,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     const int r16 = lane & 15, g = lane >> 4;
     if (s + 1 < nsteps) {
       issue_step<In>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib, vbb,
-                     ts + kStep, a, w, lane);
+                     ts + kStep, a, w, dmo);
       if (w < 2)
         wait_vmcnt<7>();
       else
@@ -300,7 +343,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     }
     lds_barrier();      // every wave's DMA of this step has landed
     YRegs yr;
-    issue_y(yr, Yb, gb, Sb, ts, a, w, lane);
+    issue_y(yr, Yb, gb, Sb, ts, a, rof, lane);
 
     // (a) this wave's share of the causal score tiles A^T = Psi Phi^T
     //     entries 0..9: (ut, tt) with ut <= tt; 10, 11: zero tiles (1,0), (3,2)
@@ -447,7 +490,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
       o.y *= inv;
       o.z *= inv;
       o.w *= inv;
-      *reinterpret_cast<float4*>(outb + (ts + t) * a.o_st + 16 * w + 4 * g) = o;
+      *reinterpret_cast<float4*>(reinterpret_cast<char*>(outb + ts * a.o_st) + rof.o[tt]) = o;
     }
   };
 
@@ -659,6 +702,11 @@ bool scan_stream_ok(int dtype, const void* phi, const void* psi, const void* vb,
     return false;
   if (!rows_vec_ok(out, a.o_sb, a.o_st, 4)) return false;
   if (Y && !rows_vec_ok(Y, a.y_sb, a.y_st, 4)) return false;
+  // per-lane row offsets are 32-bit bytes over 64 rows
+  constexpr int64_t kMaxSt = 1 << 20;
+  if (a.q_st >= kMaxSt || a.k_st >= kMaxSt || a.v_st >= kMaxSt || a.o_st >= kMaxSt ||
+      a.y_st >= kMaxSt)
+    return false;
   const char* env = getenv("SMAT_SCAN");
   if (env && env[0] == 'f') return false;        // SMAT_SCAN=fused: the general kernel
   return true;
