@@ -329,3 +329,41 @@ def test_training_step_content_hashed(d):
         assert _grel(a, b) < 1e-5, (name, _grel(a, b))
     for k, pr in prm64.items():
         assert _grel(getattr(m, k).grad.cpu(), pr.grad) < 1e-4, k
+
+
+# ---------------------------------------------------------------------------
+# smat_bgemm itself: every product of the backward runs on it
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ta,tb", [(torch.float32, torch.float32), (torch.bfloat16, torch.float32),
+                                   (torch.float32, torch.bfloat16), (torch.bfloat16, torch.bfloat16),
+                                   (torch.float16, torch.float32)])
+@pytest.mark.parametrize("a_t,b_t", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("mask,beta", [(0, 0), (1, 0), (2, 1), (0, 1)])
+def test_bgemm_layouts_masks_and_accumulation(ta, tb, a_t, b_t, mask, beta):
+    """C[i] (+)= A[i] B[i] over a two-level batch, with each operand stored
+    row-major or transposed (swapped strides), ragged M, N, K, the two causal
+    masks and beta, against the fp64 product of the same values."""
+    from smat_attention_amd.kernels.hip_bwd import _bgemm
+    n1, n2, M, N, K = 2, 3, 70, 65, 45
+    g = torch.Generator().manual_seed(60)
+    A64 = torch.randn(n1, n2, M, K, generator=g, dtype=torch.float64)
+    B64 = torch.randn(n1, n2, K, N, generator=g, dtype=torch.float64)
+    C0 = torch.randn(n1, n2, M, N, generator=g, dtype=torch.float64)
+    Aq, Bq = A64.to(ta), B64.to(tb)                  # the values the kernel sees
+    # stored layouts: A as (.., M, K) or (.., K, M); B as (.., K, N) or (.., N, K)
+    As = (Aq.transpose(-1, -2) if a_t else Aq).contiguous().to(DEV)
+    Bs = (Bq.transpose(-1, -2) if b_t else Bq).contiguous().to(DEV)
+    a = (n2 * M * K, M * K, 1, M) if a_t else (n2 * M * K, M * K, K, 1)
+    b = (n2 * K * N, K * N, 1, K) if b_t else (n2 * K * N, K * N, N, 1)
+    C = C0.float().to(DEV)
+    _bgemm(As, Bs, C, M=M, N=N, K=K, n1=n1, n2=n2, a=a, b=b,
+           c=(n2 * M * N, M * N, N, 1), beta=beta, mask=mask)
+    ref = Aq.double() @ Bq.double()
+    if mask == 1:
+        ref = torch.tril(ref)
+    elif mask == 2:
+        ref = torch.triu(ref)
+    if beta:
+        ref = ref + C0.float().double()
+    assert (C.double().cpu() - ref).abs().max().item() < 1e-5 * ref.abs().max().item()

@@ -168,10 +168,13 @@ def test_query(dt, T, d, r, p):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("T,d,n_P", [(4096, 3, 0), (8192, 2, 0), (2048, 3, 16), (32768, 3, 0)])
+@pytest.mark.parametrize("T,d,n_P", [(4096, 3, 0), (8192, 2, 0), (2048, 3, 16), (32768, 3, 0),
+                                     (32768, 2, 0), (32768, 2, 16)])
 def test_pool_streaming_head_dim_128(dt, T, d, n_P, monkeypatch):
     """The DMA-streamed Gram kernel (16-bit, r = 128, p = 129) on the profile
-    pool, incl. the global channel, against fp64 and the general kernel."""
+    pool, incl. the global channel, against fp64 and the general kernel.
+    Profiles of at most 64 tokens take its single-buffer form; d = 2 at
+    T = 32768 (about 125 tokens a profile) the double-buffered one."""
     _say("pool streaming", dt, T, d, n_P)
     spec = build_mask(T, d, chunk=128, n_P=n_P)
     nb = 4
@@ -212,7 +215,7 @@ def test_chunk_states_and_segment_scan(dt):
     assert torch.count_nonzero(Sin[:, n // C]).item() == 0
 
 
-@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T,n,C,hd", [(2048, 1024, 128, 64), (2048 + 77, 1024, 128, 32),
                                       (4096, 2048, 64, 32), (1000, 0, 128, 32),
                                       (8192, 4096, 128, 128), (300, 256, 128, 16),
