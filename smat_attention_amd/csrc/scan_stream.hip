@@ -559,8 +559,10 @@ __global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
     int64_t v_st, int64_t g_sb, int64_t g_si, int64_t gl_sb) {
   using namespace ss;
   typedef typename Traits<In>::frag Frag;
-  __shared__ __attribute__((aligned(16))) uint4 psi0[kTileChunks];
-  __shared__ __attribute__((aligned(16))) uint4 vb0[kVbTileChunks];
+  // psi0 and vb0 are one array: after the last step it stages the output
+  __shared__ __attribute__((aligned(16))) uint4 stage0[kTileChunks + kVbTileChunks];
+  uint4* psi0 = stage0;
+  uint4* vb0 = stage0 + kTileChunks;
   __shared__ __attribute__((aligned(16))) uint4 psi1[ONE ? 1 : kTileChunks];
   __shared__ __attribute__((aligned(16))) uint4 vb1[ONE ? 1 : kVbTileChunks];
 
@@ -633,6 +635,31 @@ __global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
 
   const int lane = lane_id();
   const int r16 = lane & 15, g = lane >> 4;
+  if (p == 129 && (reinterpret_cast<uintptr_t>(Gout) & 15) == 0) {
+    // The r x p result is one contiguous block.  Stage it 64 rows (33 KB) at
+    // a time in the idle tile buffer and store each half as consecutive
+    // 16-byte stores: whole cache lines, instead of 64-byte runs of
+    // 516-byte rows.
+    float* st = reinterpret_cast<float*>(stage0);
+    constexpr int kHalf = 64 * 129;                  // floats
+    for (int h = 0; h < 2; ++h) {
+      lds_barrier();                                 // the tile buffer is free
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          st[(16 * q4 + 4 * g + i) * 129 + 16 * w + r16] = accS[4 * h + q4][i];
+      if ((w >> 2) == h && r16 == 0) {               // column 128: rows 16 w + 4 g + i
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[(16 * (w & 3) + 4 * g + i) * 129 + 128] = accS8[i];
+      }
+      lds_barrier();
+      const float4* src = reinterpret_cast<const float4*>(st);
+      float4* dst = reinterpret_cast<float4*>(Gout + h * kHalf);
+      for (int e = threadIdx.x; e < kHalf / 4; e += kThreads) dst[e] = src[e];
+    }
+    return;
+  }
 #pragma unroll
   for (int at = 0; at < 8; ++at)
 #pragma unroll
