@@ -22,8 +22,21 @@ __global__ __launch_bounds__(256) void segment_scan_kernel(const float* __restri
   const int c_hi = seg == 0 ? nc0 : nc;
   const float* Db = D + b * nc * rp + e;
   float* Sb = Sin + b * nc * rp + e;
+  // eight loads in flight per thread, then their eight running sums (same
+  // order of additions as one at a time)
   float run = 0.f;
-  for (int c = c_lo; c < c_hi; ++c) {
+  int c = c_lo;
+  for (; c + 8 <= c_hi; c += 8) {
+    float d[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) d[u] = Db[(int64_t)(c + u) * rp];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      Sb[(int64_t)(c + u) * rp] = run;
+      run += d[u];
+    }
+  }
+  for (; c < c_hi; ++c) {
     const float d = Db[(int64_t)c * rp];
     Sb[(int64_t)c * rp] = run;
     run += d;
