@@ -639,7 +639,9 @@ __global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
     // The r x p result is one contiguous block.  Stage it 64 rows (33 KB) at
     // a time in the idle tile buffer and store each half as consecutive
     // 16-byte stores: whole cache lines, instead of 64-byte runs of
-    // 516-byte rows.
+    // 516-byte rows.  Non-temporal: the table (888 MB for the long-prefill
+    // pool) is far larger than the last-level cache and is read back only by
+    // the next kernel.
     float* st = reinterpret_cast<float*>(stage0);
     constexpr int kHalf = 64 * 129;                  // floats
     for (int h = 0; h < 2; ++h) {
@@ -656,7 +658,13 @@ __global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
       lds_barrier();
       const float4* src = reinterpret_cast<const float4*>(st);
       float4* dst = reinterpret_cast<float4*>(Gout + h * kHalf);
-      for (int e = threadIdx.x; e < kHalf / 4; e += kThreads) dst[e] = src[e];
+      for (int e = threadIdx.x; e < kHalf / 4; e += kThreads) {
+        const float4 v = src[e];
+        __builtin_nontemporal_store(v.x, &dst[e].x);
+        __builtin_nontemporal_store(v.y, &dst[e].y);
+        __builtin_nontemporal_store(v.z, &dst[e].z);
+        __builtin_nontemporal_store(v.w, &dst[e].w);
+      }
     }
     return;
   }
