@@ -232,6 +232,9 @@ int smat_bgemm(int dtype_a, int dtype_b, const void* A, const void* B, float* C,
  * a geometric mask: pool -> incidence (+ global channel) -> query ->
  * chunk states -> segmented scan -> chunk-local pass -> normalise.
  * idx/indptr/deg describe C as for smat_incidence; B, N0, n, n_P from the spec.
+ * idx may be NULL when C is the identity (deg = 1, B = N0, row h = [h]: every
+ * d = 2 geometric mask) and n_P = 0: the query then reads F as U and the
+ * incidence pass is skipped (U = F exactly, as the gather would give).
  * plane_code/q, when plane_code is not NULL, select smat_incidence_plane's
  * generated lines instead of the table (d = 3 masks).
  * out: (nb, T, p-1) fp32 with row stride o_st; g optional.  H_out, if not

@@ -180,6 +180,9 @@ def to_device(spec: MaskSpec, device, *, want_direct: bool = False) -> MaskSpec:
     spec.plane_code_t = torch.from_numpy(codes).to(device) if codes is not None else None
     for t in (spec.C_indices_t, spec.C_indices_i32_t, spec.C_indices_par_t):
         t._smat_checked_N0 = spec.N0
+    # C = I (every d = 2 geometric mask: row h is [h]): U = F exactly
+    spec.incidence_identity = bool(spec.uniform_deg == 1 and spec.B == spec.N0
+                                   and np.array_equal(ind, np.arange(spec.N0)))
     if spec.uniform_deg:
         spec.plane_pts_t = spec.C_indices_t.view(spec.B, spec.uniform_deg)
         spec.plane_pts_t._smat_checked_N0 = spec.N0
@@ -540,6 +543,8 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
     if plain and timer is None and not return_parts:
         idx, indptr, deg = _incidence_args(spec)
         pc = spec.plane_code_t if _plane_ok(spec, r * Vb.shape[-1]) else None
+        if getattr(spec, "incidence_identity", False) and spec.n_P == 0:
+            idx, pc = None, None                     # the query reads F as U
         return _hip.forward(Phi, Psi, Vb, idx, deg, n=n, n_P=spec.n_P, N0=spec.N0, B=spec.B,
                             chunk=C, indptr=indptr, plane_code=pc, field_q=spec.q, g=g,
                             workspace=workspace)

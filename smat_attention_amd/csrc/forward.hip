@@ -122,8 +122,10 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
                             int64_t workspace_bytes, void* stream) {
   using namespace smat;
   clear_error();
-  SMAT_REQUIRE(phi && psi && vb && idx && out && workspace, SMAT_EINVAL,
-               "smat_forward: null pointer");
+  SMAT_REQUIRE(phi && psi && vb && out && workspace, SMAT_EINVAL, "smat_forward: null pointer");
+  SMAT_REQUIRE(idx || (deg == 1 && B == N0 && n_P == 0), SMAT_EINVAL,
+               "smat_forward: idx may be NULL only for the identity incidence (deg=1, B=N0, "
+               "n_P=0; got deg=%d B=%d N0=%d n_P=%d)", deg, B, N0, n_P);
   SMAT_REQUIRE(dtype == SMAT_BF16 || dtype == SMAT_F16 || dtype == SMAT_F32, SMAT_EINVAL,
                "smat_forward: unknown dtype %d", dtype);
   SMAT_REQUIRE(nb >= 1 && T >= 1 && C >= 1 && C <= kMaxC, SMAT_EINVAL,
@@ -166,13 +168,16 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     rc = pool_dispatch(dtype, psi, vb, F, Fg, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st, part,
                        part_bytes, st);
     if (rc) return rc;
-    if (plane_code && profiled)
+    const float* Uq = U;
+    if (!idx)                                        // identity incidence: U = F
+      Uq = F;
+    else if (plane_code && profiled)
       rc = incidence_plane_dispatch(F, Fg, plane_code, q, U, nb, N0, B, rp, st);
     else
       rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
                               profiled ? deg : 0, U, nb, N0, B, rp, st);
     if (rc) return rc;
-    rc = query_dispatch(dtype, phi_rec, U, Y, nb, T_R, B, r, p, q_sb, q_st, (int64_t)T_R * yst,
+    rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, q_sb, q_st, (int64_t)T_R * yst,
                         yst, st);
     if (rc) return rc;
   }

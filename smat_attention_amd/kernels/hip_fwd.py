@@ -456,7 +456,9 @@ def forward_workspace_bytes(nb, T, n, N0, B, n_P, C, r, p) -> int:
 def forward(Phi, Psi, Vb, idx, deg: int, *, n: int, n_P: int, N0: int, B: int, chunk: int,
             indptr=None, plane_code=None, field_q: int = 0, g=None, out=None, H_out=None,
             workspace=None):
-    """The whole forward schedule in one call; returns fp32 ``(nb, T, p-1)``."""
+    """The whole forward schedule in one call; returns fp32 ``(nb, T, p-1)``.
+    ``idx=None`` (with ``deg=1``, ``B=N0``, ``n_P=0``) declares the incidence the
+    identity: the query reads the pooled table directly."""
     who = "forward"
     _on_gpu(who, Phi, Psi, Vb, idx, indptr, g, out, H_out)
     nb, T, R = Phi.shape
@@ -479,8 +481,9 @@ def forward(Phi, Psi, Vb, idx, deg: int, *, n: int, n_P: int, N0: int, B: int, c
     base = workspace.data_ptr()
     aligned = (base + 255) & ~255
     avail = workspace.numel() - (aligned - base)
-    call("smat_forward", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), idx.data_ptr(),
-         int(idx.dtype == torch.int64), ptr(indptr), deg, ptr(plane_code), field_q,
+    call("smat_forward", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), ptr(idx),
+         int(idx is not None and idx.dtype == torch.int64), ptr(indptr), deg, ptr(plane_code),
+         field_q,
          out.data_ptr(), ptr(H_out), ptr(gc),
          nb, T, n, n_P, N0, B, chunk, R, P, q_sb, q_st, k_sb, k_st, v_sb, v_st,
          out.stride(0), out.stride(1), gc.stride(0) if gc is not None else 0,

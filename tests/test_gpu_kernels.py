@@ -657,3 +657,27 @@ def test_decayed_scan_gradients(T, n, C, r, p, strength):
     assert _rel(y1, y0) < 1e-5
     for name, a, b in zip(("dPhi", "dPsi", "dVb", "dlogA"), g1, g0):
         assert _rel(a, b) < 1e-5, (name, _rel(a, b))
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_forward_identity_incidence_skips_the_gather(dt):
+    """At d = 2 the incidence is the identity (row h = [h]): the one-call
+    forward queries F directly, bit-identical to running the gather."""
+    _say("identity incidence", dt)
+    spec = A.to_device(build_mask(4096, 2, chunk=128), DEV)
+    assert spec.incidence_identity and spec.n_P == 0
+    Phi, Psi, Vb = _feats(2, 4096, 64, dt, seed=50)
+    Pd, Sd, Wd = (x.to(DEV) for x in (Phi, Psi, Vb))
+    fast = A.smat_attention(Pd, Sd, Wd, spec)
+    spec.incidence_identity = False
+    try:
+        slow = A.smat_attention(Pd, Sd, Wd, spec)
+    finally:
+        spec.incidence_identity = True
+    assert torch.equal(fast, slow)
+    # d = 3 keeps the gather, and the C ABI refuses a NULL table for it
+    spec3 = A.to_device(build_mask(4096, 3, chunk=128), DEV)
+    assert not spec3.incidence_identity
+    with pytest.raises(Exception, match="identity incidence"):
+        K.forward(Pd, Sd, Wd, None, spec3.uniform_deg, n=spec3.n, n_P=0, N0=spec3.N0,
+                  B=spec3.B, chunk=128)
