@@ -424,6 +424,8 @@ def _incidence(F, spec: MaskSpec, F_glob):
     """``C F`` (+ the global channel) through the fastest kernel the mask allows."""
     nb, N0, r, p = F.shape
     Ff = F.contiguous().float()
+    if getattr(spec, "incidence_identity", False) and F_glob is None:
+        return Ff                                    # C = I: U = F exactly
     U = torch.empty(nb, spec.B, r, p, device=F.device, dtype=torch.float32)
     profiled = spec.n > spec.n_P
     if profiled and getattr(spec, "plane_code_t", None) is not None and _plane_ok(spec, r * p):

@@ -218,8 +218,11 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
             if not full and rem < B:
                 dU[:, rem:] = 0
         # dF = C^T dU (and the global channel's sum over all types)
-        t_ptr, t_idx = transposed_incidence(spec, dev)
-        dF = _incidence_rows(dU, t_idx, t_ptr, N0, nb, B, rp)
+        if getattr(spec, "incidence_identity", False):
+            dF = dU.view(nb, N0, rp)                 # C = I: C^T dU = dU
+        else:
+            t_ptr, t_idx = transposed_incidence(spec, dev)
+            dF = _incidence_rows(dU, t_idx, t_ptr, N0, nb, B, rp)
         nX = n - n_P
         gq, grem = divmod(nX, N0)
         Nrp = N0 * rp

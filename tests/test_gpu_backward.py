@@ -62,7 +62,8 @@ def _nrel(a, b):
     return ((a - b).norm() / b.norm().clamp_min(1e-300)).item()
 
 
-@pytest.mark.parametrize("T,d,n_P,hd,gate", [(1024, 2, 0, 32, False), (2048, 3, 0, 32, True),
+@pytest.mark.parametrize("T,d,n_P,hd,gate", [(1024, 2, 0, 32, False), (1024, 2, 16, 32, True),
+                                             (2048, 3, 0, 32, True),
                                              (2048, 3, 16, 32, False), (2000, 3, 0, 16, False),
                                              (1024, 1, 0, 32, False), (4096, 4, 0, 16, True),
                                              (2048, 3, 0, 64, False)])
