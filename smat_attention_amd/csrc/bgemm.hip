@@ -11,16 +11,19 @@
 // fp16 or fp32; they are widened to fp32 when staged, and the products run on
 // v_mfma_f32_16x16x4_f32, so results are fp32 products summed in fp32.
 //
-// Tiling: a 256-thread workgroup computes a 64 x 64 block of C; wave w owns the
-// 32 x 32 quarter (w >> 1, w & 1) as 2 x 2 MFMA tiles.  K advances 32 at a
-// time through LDS (A as [m][k], B as [n][k]).
+// Tiling: a 256-thread workgroup computes a 64 x kBN block of C.  kBN = 64:
+// wave w owns the 32 x 32 quarter (w >> 1, w & 1) as 2 x 2 MFMA tiles.
+// kBN = 80, for N just past a multiple of 64 (p = 65, 129: value columns plus
+// the ones column): wave w owns rows 16w .. 16w + 15 across five column tiles,
+// so N = 65 takes one block instead of two.  K advances 32 at a time through
+// LDS (A as [m][k], B as [n][k]).
 #include "smat_host.hpp"
 
 namespace smat {
 
 namespace bg {
 constexpr int kThreads = 256;
-constexpr int kBM = 64, kBN = 64, kBK = 32;
+constexpr int kBM = 64, kBK = 32;
 constexpr int kPad = kBK + 4;        // LDS row length (floats)
 }  // namespace bg
 
@@ -32,11 +35,15 @@ struct GemmArgs {
   int beta, mask;           // mask: 0 none, 1 keep m >= n, 2 keep m <= n
 };
 
-template <typename TA, typename TB>
+template <typename TA, typename TB, int kBN>
 __global__ __launch_bounds__(bg::kThreads) void bgemm_kernel(const TA* __restrict__ A,
                                                              const TB* __restrict__ B,
                                                              float* __restrict__ Cm, GemmArgs g) {
   using namespace bg;
+  static_assert(kBN == 64 || kBN == 80, "column block of 64 or 80");
+  constexpr int kWC = kBN == 64 ? 2 : 1;            // waves across the columns
+  constexpr int kTM = kBN == 64 ? 2 : 1;            // 16-row MFMA tiles per wave
+  constexpr int kTN = kBN == 64 ? 2 : 5;            // 16-column MFMA tiles per wave
   __shared__ __attribute__((aligned(16))) float sA[kBM * kPad];
   __shared__ __attribute__((aligned(16))) float sB[kBN * kPad];
 
@@ -48,7 +55,7 @@ __global__ __launch_bounds__(bg::kThreads) void bgemm_kernel(const TA* __restric
   const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
   const int lane = lane_id(), w = wave_id();
   const int row16 = lane & 15, grp = lane >> 4;
-  const int wm = (w >> 1) * 32, wn = (w & 1) * 32;
+  const int wm = (w / kWC) * 16 * kTM, wn = (w % kWC) * 16 * kTN;
 
   // a masked block contributes nothing: skip its products (the store still
   // writes zeros where beta = 0)
@@ -56,11 +63,11 @@ __global__ __launch_bounds__(bg::kThreads) void bgemm_kernel(const TA* __restric
   if (g.mask == 1 && n0 > m0 + kBM - 1) skip = true;
   if (g.mask == 2 && m0 > n0 + kBN - 1) skip = true;
 
-  f32x4 acc[2][2];
+  f32x4 acc[kTM][kTN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kTM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = zero4();
+    for (int j = 0; j < kTN; ++j) acc[i][j] = zero4();
 
   if (!skip) {
     for (int k0 = 0; k0 < g.K; k0 += kBK) {
@@ -78,13 +85,13 @@ __global__ __launch_bounds__(bg::kThreads) void bgemm_kernel(const TA* __restric
       }
       __syncthreads();
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < kTM; ++i) {
         f32x8 a;
         const float* ap = sA + (wm + 16 * i + row16) * kPad + 8 * grp;
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[e] = ap[e];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < kTN; ++j) {
           f32x8 bv;
           const float* bp = sB + (wn + 16 * j + row16) * kPad + 8 * grp;
 #pragma unroll
@@ -97,9 +104,9 @@ __global__ __launch_bounds__(bg::kThreads) void bgemm_kernel(const TA* __restric
   }
 
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kTM; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kTN; ++j) {
       const int n = n0 + wn + 16 * j + row16;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -118,10 +125,17 @@ __global__ __launch_bounds__(bg::kThreads) void bgemm_kernel(const TA* __restric
 template <typename TA, typename TB>
 static int launch_bgemm(const void* A, const void* B, float* C, int n1, const GemmArgs& g,
                         hipStream_t stream) {
-  dim3 grid((unsigned)((g.N + bg::kBN - 1) / bg::kBN), (unsigned)((g.M + bg::kBM - 1) / bg::kBM),
+  // the column block that pads N least (ties: 64)
+  const int64_t pad64 = (int64_t)(g.N + 63) / 64 * 64, pad80 = (int64_t)(g.N + 79) / 80 * 80;
+  const int bn = pad80 < pad64 ? 80 : 64;
+  dim3 grid((unsigned)((g.N + bn - 1) / bn), (unsigned)((g.M + bg::kBM - 1) / bg::kBM),
             (unsigned)(n1 * g.n2));
-  hipLaunchKernelGGL((bgemm_kernel<TA, TB>), grid, dim3(bg::kThreads), 0, stream, (const TA*)A,
-                     (const TB*)B, C, g);
+  if (bn == 80)
+    hipLaunchKernelGGL((bgemm_kernel<TA, TB, 80>), grid, dim3(bg::kThreads), 0, stream,
+                       (const TA*)A, (const TB*)B, C, g);
+  else
+    hipLaunchKernelGGL((bgemm_kernel<TA, TB, 64>), grid, dim3(bg::kThreads), 0, stream,
+                       (const TA*)A, (const TB*)B, C, g);
   return launch_status("smat_bgemm");
 }
 

@@ -341,12 +341,14 @@ def test_training_step_content_hashed(d):
                                    (torch.float16, torch.float32)])
 @pytest.mark.parametrize("a_t,b_t", [(False, False), (True, False), (False, True), (True, True)])
 @pytest.mark.parametrize("mask,beta", [(0, 0), (1, 0), (2, 1), (0, 1)])
-def test_bgemm_layouts_masks_and_accumulation(ta, tb, a_t, b_t, mask, beta):
+@pytest.mark.parametrize("M,N,K", [(70, 65, 45), (64, 129, 70)])
+def test_bgemm_layouts_masks_and_accumulation(ta, tb, a_t, b_t, mask, beta, M, N, K):
     """C[i] (+)= A[i] B[i] over a two-level batch, with each operand stored
     row-major or transposed (swapped strides), ragged M, N, K, the two causal
-    masks and beta, against the fp64 product of the same values."""
+    masks and beta, against the fp64 product of the same values.  N = 65 and
+    129 take the 80-column block, N = 64 products elsewhere the 64-column one."""
     from smat_attention_amd.kernels.hip_bwd import _bgemm
-    n1, n2, M, N, K = 2, 3, 70, 65, 45
+    n1, n2 = 2, 3
     g = torch.Generator().manual_seed(60)
     A64 = torch.randn(n1, n2, M, K, generator=g, dtype=torch.float64)
     B64 = torch.randn(n1, n2, K, N, generator=g, dtype=torch.float64)
