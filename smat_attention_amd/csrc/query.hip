@@ -22,18 +22,21 @@ namespace qy {
 constexpr int kThreads = 256;
 constexpr int kRowsPerWG = 64;
 constexpr int kMT = kRowsPerWG / 16;
-constexpr int kRK = 4;       // r <= 128
-constexpr int kNCT = 9;      // p <= 144
-constexpr int kCTPerWave = 3;
 }  // namespace qy
 
-template <typename In>
+// Tile shape: kRK k-blocks of 32 features and kNCT column tiles of 16, split
+// over the four waves (wave w: tiles w, w + 4, ...).  Wide (4, 9): r <= 128,
+// p <= 144.  Narrow (2, 5): r <= 64, p <= 80, half the accumulators and
+// fragments, for head_dim 64; (3, 5) for contractions over head_dim + 1
+// columns (r <= 96).
+template <typename In, int kRK, int kNCT>
 __global__ __launch_bounds__(qy::kThreads) void query_kernel(
     const In* __restrict__ phi, const float* __restrict__ U, float* __restrict__ Y, int T_R, int B,
     int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st, int nrb, int vec_q,
     const int32_t* __restrict__ rows, const int64_t* __restrict__ roffs) {
   using namespace qy;
   typedef typename Traits<In>::frag Frag;
+  constexpr int kCTPerWave = (kNCT + 3) / 4;
   const int h = blockIdx.x / nrb;
   const int rb = blockIdx.x - h * nrb;
   const int64_t b = blockIdx.y;
@@ -303,9 +306,18 @@ static int launch_query(const void* phi, const float* U, float* Y, int nb, int T
     return SMAT_EUNSUPPORTED;
   }
   const int vq = rows_vec_ok(phi, q_sb, q_st, sizeof(In));
-  hipLaunchKernelGGL(query_kernel<In>, dim3((unsigned)gx, (unsigned)nb), dim3(qy::kThreads), 0,
-                     stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb, q_st, y_sb, y_st, nrb, vq,
-                     nullptr, nullptr);
+  if (r <= 64 && p <= 80)
+    hipLaunchKernelGGL((query_kernel<In, 2, 5>), dim3((unsigned)gx, (unsigned)nb),
+                       dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
+                       q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
+  else if (r <= 96 && p <= 80)
+    hipLaunchKernelGGL((query_kernel<In, 3, 5>), dim3((unsigned)gx, (unsigned)nb),
+                       dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
+                       q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
+  else
+    hipLaunchKernelGGL((query_kernel<In, 4, 9>), dim3((unsigned)gx, (unsigned)nb),
+                       dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
+                       q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   return launch_status("smat_query");
 }
 
@@ -321,9 +333,18 @@ static int launch_query_lists(const void* phi, const float* U, float* Y, const i
   }
   if (gx == 0) return SMAT_OK;
   const int vq = rows_vec_ok(phi, 0, q_st, sizeof(In));
-  hipLaunchKernelGGL(query_kernel<In>, dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0, stream,
-                     (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st, (int64_t)0, y_st,
-                     nrb, vq, rows, roffs);
+  if (r <= 64 && p <= 80)
+    hipLaunchKernelGGL((query_kernel<In, 2, 5>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
+                       stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
+                       (int64_t)0, y_st, nrb, vq, rows, roffs);
+  else if (r <= 96 && p <= 80)
+    hipLaunchKernelGGL((query_kernel<In, 3, 5>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
+                       stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
+                       (int64_t)0, y_st, nrb, vq, rows, roffs);
+  else
+    hipLaunchKernelGGL((query_kernel<In, 4, 9>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
+                       stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
+                       (int64_t)0, y_st, nrb, vq, rows, roffs);
   return launch_status("smat_query_lists");
 }
 

@@ -153,7 +153,8 @@ def test_incidence_ragged_endpoint_csr():
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("T,d,r,p", [(4096, 3, 32, 33), (8192, 2, 64, 65), (4096, 1, 128, 129),
+@pytest.mark.parametrize("T,d,r,p", [(4096, 3, 32, 33), (8192, 2, 64, 65), (4096, 3, 80, 65),
+                                     (4096, 3, 96, 80), (4096, 1, 128, 129),
                                      (32768, 3, 128, 129), (131072, 3, 128, 129)])
 def test_query(dt, T, d, r, p):
     _say("query", dt, T, d, r, p)
