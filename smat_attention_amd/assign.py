@@ -39,8 +39,8 @@ import torch
 import torch.nn as nn
 
 from .kernels.hip_fwd import _code, _on_gpu, _rows3, call, stream_of
-from .pool_ops import (_gram_lists, _lists, _read_lists, _read_pairs, _repeat, pool_sorted,
-                       read_sorted)
+from .pool_ops import (_f32_rows, _gram_lists, _lists, _read_lists, _read_pairs, _repeat,
+                       pool_sorted, read_sorted)
 
 __all__ = ["ContentAssign", "grouped_planes"]
 
@@ -473,7 +473,7 @@ class _HardPool(torch.autograd.Function):
         Pk, Vk, idxk, ck = ctx.saved_tensors
         dF = dF.float().contiguous()
         dFT = dF.transpose(-1, -2).contiguous()
-        P32, V32 = Pk.float(), Vk.float()
+        P32, V32 = Pk.float(), _f32_rows(Vk)         # Vb rows of p floats, 16-byte aligned
         dPsi = _read_lists(V32, dFT, ck, ctx.lists)
         dVb = _read_lists(P32, dF, ck, ctx.lists)
         dwk = _pair_dw(P32, dPsi, V32, dFT, idxk)
@@ -511,7 +511,7 @@ class _HardRead(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dY):
         Phr, F, idxq, cq = ctx.saved_tensors
-        dY = dY.float().contiguous()
+        dY = _f32_rows(dY)                            # rows of p floats, 16-byte aligned
         Ph32 = Phr.float()
         FT = F.transpose(-1, -2).contiguous()
         dPhi = _read_lists(dY, FT, cq, ctx.lists)

@@ -86,6 +86,19 @@ def _read_lists(X, U, cls, lists=None):
     return Y
 
 
+def _f32_rows(x):
+    """fp32 copy of ``x`` (nb, L, c) whose rows start 16-byte aligned: a view of
+    rows padded to a multiple of 4 floats (the pad is never read), so the list
+    kernels load X with 16-byte loads."""
+    c = x.shape[-1]
+    cp = -(-c // 4) * 4
+    if cp == c:
+        return x.float().contiguous()
+    buf = torch.empty(*x.shape[:-1], cp, device=x.device, dtype=torch.float32)
+    buf[..., :c] = x
+    return buf[..., :c]
+
+
 def _read_pairs(X, U, idx):
     """``Z[b, l, k] = X[b, l] U[b, idx[b, l, k]]`` for every pair: (nb, L, K, o)."""
     nb, L, c = X.shape
