@@ -70,20 +70,41 @@ __global__ __launch_bounds__(bg::kThreads) void bgemm_kernel(const TA* __restric
     for (int j = 0; j < kTN; ++j) acc[i][j] = zero4();
 
   if (!skip) {
-    for (int k0 = 0; k0 < g.K; k0 += kBK) {
-      for (int idx = threadIdx.x; idx < kBM * kBK; idx += kThreads) {
+    // the next K step's elements are loaded into registers while the current
+    // step is multiplied (element idx = tid + e kThreads of each tile)
+    constexpr int kPA = kBM * kBK / kThreads, kPB = kBN * kBK / kThreads;   // 8; 8 or 10
+    float ra[kPA], rb[kPB];
+    auto load = [&](int k0) {
+#pragma unroll
+      for (int e = 0; e < kPA; ++e) {
+        const int idx = threadIdx.x + e * kThreads;
         const int mm = idx / kBK, kk = idx - mm * kBK;
         const int m = m0 + mm, k = k0 + kk;
-        sA[mm * kPad + kk] =
-            (m < g.M && k < g.K) ? to_f32(Ab[(int64_t)m * g.am + (int64_t)k * g.ak]) : 0.f;
+        ra[e] = (m < g.M && k < g.K) ? to_f32(Ab[(int64_t)m * g.am + (int64_t)k * g.ak]) : 0.f;
       }
-      for (int idx = threadIdx.x; idx < kBN * kBK; idx += kThreads) {
+#pragma unroll
+      for (int e = 0; e < kPB; ++e) {
+        const int idx = threadIdx.x + e * kThreads;
         const int nn = idx / kBK, kk = idx - nn * kBK;
         const int n = n0 + nn, k = k0 + kk;
-        sB[nn * kPad + kk] =
-            (n < g.N && k < g.K) ? to_f32(Bb[(int64_t)k * g.bk + (int64_t)n * g.bn]) : 0.f;
+        rb[e] = (n < g.N && k < g.K) ? to_f32(Bb[(int64_t)k * g.bk + (int64_t)n * g.bn]) : 0.f;
+      }
+    };
+    load(0);
+    for (int k0 = 0; k0 < g.K; k0 += kBK) {
+      if (k0 > 0) __syncthreads();       // the previous step's readers are done
+#pragma unroll
+      for (int e = 0; e < kPA; ++e) {
+        const int idx = threadIdx.x + e * kThreads;
+        sA[(idx / kBK) * kPad + idx % kBK] = ra[e];
+      }
+#pragma unroll
+      for (int e = 0; e < kPB; ++e) {
+        const int idx = threadIdx.x + e * kThreads;
+        sB[(idx / kBK) * kPad + idx % kBK] = rb[e];
       }
       __syncthreads();
+      if (k0 + kBK < g.K) load(k0 + kBK);
 #pragma unroll
       for (int i = 0; i < kTM; ++i) {
         f32x8 a;
@@ -99,7 +120,6 @@ __global__ __launch_bounds__(bg::kThreads) void bgemm_kernel(const TA* __restric
           acc[i][j] = mma(acc[i][j], a, bv);
         }
       }
-      __syncthreads();
     }
   }
 
