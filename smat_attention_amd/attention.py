@@ -660,7 +660,17 @@ class SmatDecoder:
         dev = Psi_prefix.device
         _staged(spec, dev)
         F_glob = torch.empty(nb, r, p, device=dev, dtype=torch.float32) if spec.n_P else None
-        F = _hip.pool(Psi_prefix, Vb_prefix, spec.n_P, spec.n, spec.N0, F_glob=F_glob)
+        Vp = Vb_prefix
+        if (Vp.dtype in (torch.bfloat16, torch.float16) and Vp.dim() == 3
+                and (Vp.stride(-1) != 1 or Vp.stride(1) % 8 or Vp.stride(0) % 8)):
+            # 16-byte aligned rows (a view of rows padded to 8 elements) let the
+            # pool use its vector-load kernels; one copy of the prefix pays for
+            # itself several times over at long T
+            pad = -(-p // 8) * 8
+            buf = torch.empty(*Vp.shape[:-1], pad, device=Vp.device, dtype=Vp.dtype)
+            buf[..., :p] = Vp
+            Vp = buf[..., :p]
+        F = _hip.pool(Psi_prefix, Vp, spec.n_P, spec.n, spec.N0, F_glob=F_glob)
         if spec.kind == "endpoint" and incidence_backend in ("auto", "walsh"):
             self.U = walsh_incidence(F)
         else:
