@@ -61,6 +61,14 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
 #pragma unroll
     for (int j = 0; j < kCTPerWave; ++j) acc[t][j] = zero4();
 
+  // this lane's row of each 16-row tile, looked up once (a list entry or
+  // h + kB); the stores below take their rows from these lanes by shuffle
+  int64_t ri[kMT];
+#pragma unroll
+  for (int t = 0; t < kMT; ++t) {
+    const int k = k0 + 16 * t + row16;
+    ri[t] = !(k < cnt) ? 0 : hrows ? (int64_t)hrows[k] : (int64_t)h + (int64_t)k * B;
+  }
 #pragma unroll
   for (int kb = 0; kb < kRK; ++kb) {
     if (kb >= rk) continue;
@@ -70,8 +78,7 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
     for (int t = 0; t < kMT; ++t) {
       const int k = k0 + 16 * t + row16;
       const int nv = (t < nmt && k < cnt) ? min(8, r - a0) : 0;
-      const int64_t i = !(k < cnt) ? 0 : hrows ? (int64_t)hrows[k] : (int64_t)h + (int64_t)k * B;
-      pa[t] = load8<In>(phib + i * q_st + a0, nv, vec_q);
+      pa[t] = load8<In>(phib + ri[t] * q_st + a0, nv, vec_q);
     }
 #pragma unroll
     for (int j = 0; j < kCTPerWave; ++j) {
@@ -114,6 +121,15 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
 #pragma unroll
   for (int t = 0; t < kMT; ++t) {
     if (t >= nmt) continue;
+    // row of output element i4: tile row 4 grp + i4, held by lane 4 grp + i4
+    int64_t ro[4];
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int src = 4 * grp + i4;
+      const int lo = __shfl((int)(ri[t] & 0xffffffff), src, 64);
+      const int hi = __shfl((int)(ri[t] >> 32), src, 64);
+      ro[i4] = ((int64_t)hi << 32) | (uint32_t)lo;
+    }
 #pragma unroll
     for (int j = 0; j < kCTPerWave; ++j) {
       const int ct = w + 4 * j;
@@ -122,10 +138,7 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const int k = k0 + 16 * t + 4 * grp + i4;
-        if (k < cnt && c < p) {
-          const int64_t i = hrows ? (int64_t)hrows[k] : (int64_t)h + (int64_t)k * B;
-          Yb[i * y_st + c] = acc[t][j][i4];
-        }
+        if (k < cnt && c < p) Yb[ro[i4] * y_st + c] = acc[t][j][i4];
       }
     }
   }
