@@ -46,6 +46,30 @@ const char* smat_last_error(void);
 const char* smat_version(void);
 
 /*
+ * Test hook with no counterpart in the reference: select, process-wide, the
+ * general kernel that a specialised one replaced, so that tests can compare
+ * the two on the same inputs.  value 1 selects the general kernel, 0 (the
+ * default) the specialised one; returns the previous value, or SMAT_EINVAL.
+ *   SMAT_VARIANT_SCAN             general fused causal scan instead of the
+ *                                 head_dim-128 streaming scan
+ *   SMAT_VARIANT_GRAM             general Gram kernel instead of the
+ *                                 head_dim-128 streaming pool / prepass
+ *   SMAT_VARIANT_QUERY            general query kernel instead of the
+ *                                 head_dim-128 streaming query
+ *   SMAT_VARIANT_INCIDENCE        L2 gather kernel instead of the LDS panel
+ *   SMAT_VARIANT_INCIDENCE_PLANE  line-per-lane generated-line kernel instead
+ *                                 of the wave-per-direction one
+ * Not for production use: a call changes the kernels of every later call.
+ */
+#define SMAT_VARIANT_SCAN 0
+#define SMAT_VARIANT_GRAM 1
+#define SMAT_VARIANT_QUERY 2
+#define SMAT_VARIANT_INCIDENCE 3
+#define SMAT_VARIANT_INCIDENCE_PLANE 4
+#define SMAT_NUM_VARIANTS 5
+int smat_set_variant(int which, int value);
+
+/*
  * Fused within-chunk pass, one output block per chunk:
  *   out_b = Phi_b Sin_b + (tril(Phi_b Psi_b^T)) Vb_b
  * Phi_b, Psi_b: (C, r) of dtype; Vb_b: (C, p) of dtype; Sin_b: (r, p) fp32;

@@ -11,6 +11,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "smat_host.hpp"
 
 namespace smat {
@@ -25,6 +27,14 @@ void set_error(const char* fmt, ...) {
 }
 
 void clear_error() { g_err[0] = 0; }
+
+static std::atomic<int> g_variant[SMAT_NUM_VARIANTS];
+
+int variant(int which) {
+  return (which >= 0 && which < SMAT_NUM_VARIANTS)
+             ? g_variant[which].load(std::memory_order_relaxed)
+             : 0;
+}
 
 // defined in the other translation units
 int pool_dispatch(int dtype, const void* psi, const void* vb, float* F, float* F_glob, int nb,
@@ -103,6 +113,16 @@ static FwdLayout fwd_layout(int nb, int T, int n, int N0, int B, int n_P, int C,
 extern "C" const char* smat_last_error(void) { return smat::g_err; }
 
 extern "C" const char* smat_version(void) { return "0.1 gfx950"; }
+
+extern "C" int smat_set_variant(int which, int value) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(which >= 0 && which < SMAT_NUM_VARIANTS, SMAT_EINVAL,
+               "smat_set_variant: unknown variant selector %d", which);
+  SMAT_REQUIRE(value == 0 || value == 1, SMAT_EINVAL,
+               "smat_set_variant: value must be 0 or 1, got %d", value);
+  return g_variant[which].exchange(value);
+}
 
 extern "C" int64_t smat_forward_workspace_bytes(int nb, int T, int n, int N0, int B, int n_P,
                                                 int C, int r, int p) {

@@ -195,8 +195,8 @@ static int launch_gram_shape(const void* psi, const void* vb, float* G, float* G
                        int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
                        int64_t gl_sb, float* partials, hipStream_t stream, const char* who) {
   const int64_t gx = (int64_t)nitems * it.nsplit;
-  const int vk = rows_vec_ok(psi, k_sb, k_st, sizeof(In));
-  const int vv = rows_vec_ok(vb, v_sb, v_st, sizeof(In));
+  const int vk = rows_vec8_ok(psi, k_sb, k_st);
+  const int vv = rows_vec8_ok(vb, v_sb, v_st);
   if (gx >= (1ll << 31) || nb >= 65536) {
     set_error("%s: problem too large", who);
     return SMAT_EUNSUPPORTED;

@@ -711,15 +711,6 @@ static int launch_lds_deg(const float* F, const float* F_glob, const void* idx,
   return launch_lds<Idx, E, 80>(F, F_glob, idx, indptr, deg, U, nb, N0, B, rp, stream);
 }
 
-static int incidence_mode_env() {
-  static int mode = -1;
-  if (mode < 0) {
-    const char* s = getenv("SMAT_INCIDENCE");
-    mode = (s && s[0] == 'l' && s[1] == '2') ? 1 : 0;   // "l2": force the L2 kernel
-  }
-  return mode;
-}
-
 int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int idx_is_64,
                        const int64_t* indptr, int deg, float* U, int nb, int N0, int B, int64_t rp,
                        hipStream_t stream) {
@@ -728,7 +719,7 @@ int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int
   const bool aligned = (rp % 4 == 0) && aligned16(F) && aligned16(U) &&
                        (!F_glob || aligned16(F_glob));
   const int E = lds_slice_width(N0);
-  if (aligned && E > 0 && incidence_mode_env() == 0) {
+  if (aligned && E > 0 && variant(SMAT_VARIANT_INCIDENCE) == 0) {
 #define SMAT_LDS(IDX)                                                                       \
   (E == 16 ? launch_lds_deg<IDX, 16>(F, F_glob, idx, indptr, deg, U, nb, N0, B, rp, stream) \
    : E == 8 ? launch_lds_deg<IDX, 8>(F, F_glob, idx, indptr, deg, U, nb, N0, B, rp, stream) \
@@ -758,15 +749,6 @@ int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int
   return launch_status("smat_incidence");
 }
 
-static int plane_mode_env() {
-  static int mode = -1;
-  if (mode < 0) {
-    const char* s = getenv("SMAT_INCIDENCE_PLANE");
-    mode = (s && s[0] == 'o') ? 1 : 0;   // "old": the line-per-lane plane kernel
-  }
-  return mode;
-}
-
 int incidence_plane_dispatch(const float* F, const float* F_glob, const int* code, int q,
                              float* U, int nb, int N0, int B, int64_t rp, hipStream_t stream) {
   if (nb == 0 || B == 0 || rp == 0) return SMAT_OK;
@@ -777,7 +759,7 @@ int incidence_plane_dispatch(const float* F, const float* F_glob, const int* cod
               "(q=%d N0=%d rp=%lld)", q, N0, (long long)rp);
     return SMAT_EUNSUPPORTED;
   }
-  if (wave_kernel_fits(q, N0, rp) && plane_mode_env() == 0)
+  if (wave_kernel_fits(q, N0, rp) && variant(SMAT_VARIANT_INCIDENCE_PLANE) == 0)
     return launch_wave(F, F_glob, code, q, U, nb, N0, B, rp, stream);
   // Two workgroups per CU at E = 8 (one stages its panel while the other sums)
   // measured ahead of one at E = 16; wider panels fall back to one per CU.

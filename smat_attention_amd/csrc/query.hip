@@ -303,8 +303,7 @@ static bool query_stream_ok(int dtype, const void* phi, const float* U, const fl
   if ((T_R + B - 1) / B > 16 * qs::kMT) return false;        // <= 48 rows per type
   if (!rows_vec_ok(phi, q_sb, q_st, 2) || !aligned16(U) || !rows_vec_ok(Y, y_sb, y_st, 4))
     return false;
-  const char* env = getenv("SMAT_QUERY");
-  return !(env && env[0] == 'o');                             // SMAT_QUERY=old
+  return variant(SMAT_VARIANT_QUERY) == 0;
 }
 
 template <typename In>

@@ -415,9 +415,8 @@ template <typename In, int RK, int NCT>
 static int launch_scan_fused_shape(const void* phi, const void* psi, const void* vb,
                                    const float* Sg, const float* Y, const float* gate, float* out,
                                    int nb, int ng, const ScanArgs& a, hipStream_t stream) {
-  const int eb = sizeof(In);
-  const bool vec = rows_vec_ok(phi, a.q_sb, a.q_st, eb) && rows_vec_ok(psi, a.k_sb, a.k_st, eb) &&
-                   rows_vec_ok(vb, a.v_sb, a.v_st, eb);
+  const bool vec = rows_vec8_ok(phi, a.q_sb, a.q_st) && rows_vec8_ok(psi, a.k_sb, a.k_st) &&
+                   rows_vec8_ok(vb, a.v_sb, a.v_st);
   dim3 grid((unsigned)ng, (unsigned)nb);
   if (vec)
     hipLaunchKernelGGL((scan_fused_kernel<In, true, RK, NCT>), grid, dim3(sf::kThreads), 0,

@@ -686,9 +686,7 @@ bool gram_stream_ok(int dtype, const void* psi, const void* vb, int r, int p, in
   if ((int64_t)nitems * nb < 256) return false;        // few, long items: the split-K kernel
   if (!rows_vec_ok(psi, k_sb, k_st, 2) || !rows_vec_ok(vb, v_sb, v_st, 2) || v_st < 136)
     return false;
-  const char* env = getenv("SMAT_GRAM");
-  if (env && env[0] == 'o') return false;              // SMAT_GRAM=old: the general kernel
-  return true;
+  return variant(SMAT_VARIANT_GRAM) == 0;
 }
 
 int gram_stream_launch(int dtype, const void* psi, const void* vb, float* G, float* G_last,
@@ -742,9 +740,7 @@ bool scan_stream_ok(int dtype, const void* phi, const void* psi, const void* vb,
   if (a.q_st >= kMaxSt || a.k_st >= kMaxSt || a.v_st >= kMaxSt || a.o_st >= kMaxSt ||
       a.y_st >= kMaxSt)
     return false;
-  const char* env = getenv("SMAT_SCAN");
-  if (env && env[0] == 'f') return false;        // SMAT_SCAN=fused: the general kernel
-  return true;
+  return variant(SMAT_VARIANT_SCAN) == 0;
 }
 
 int scan_stream_launch(int dtype, const void* phi, const void* psi, const void* vb,

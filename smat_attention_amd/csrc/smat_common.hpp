@@ -153,12 +153,14 @@ __device__ __forceinline__ void tile8_finish(Tile8<In>& tl) {
 // the row start of token t (nullptr: a padding token, loaded as zeros).
 // Columns >= ncols load as zeros.
 //
-// VEC (rows 16-byte aligned, row stride a multiple of 16 bytes): branch-free.
+// VEC (rows 16-byte aligned, row stride a multiple of 8 elements): branch-free.
 // Every row is read with one 16-byte (fp32: 32-byte) load -- a padding row,
 // or a tile starting at or past column ncols, from `safe` (the start of any
 // valid row of the same matrix) -- and the padding rows and columns are then
 // zeroed with selects.  A live read covers [c0, c0+8) with c0 < ncols and c0 a
-// multiple of 8, so it ends at or before round_up(ncols, 8) <= the row stride:
+// multiple of 8, so it ends at or before round_up(ncols, 8), which is at most
+// the row stride because VEC is taken only for strides that are multiples of 8
+// elements (rows_vec8_ok; for fp32 a stride of 4 mod 8 floats would not do):
 // no read leaves its row, hence none leaves the allocation.  Branches around loads make the
 // compiler wait for every outstanding load where they join, which would
 // serialise the staging; this form keeps all eight loads in flight.

@@ -15,6 +15,11 @@ namespace smat {
 void set_error(const char* fmt, ...);
 void clear_error();
 
+// Kernel variant selected for `which` (SMAT_VARIANT_*, smat_set_variant);
+// 0 is the default kernel.  Set only by the explicit test hook, never from
+// the environment.
+int variant(int which);
+
 // Checked at every entry point before any launch.
 #define SMAT_REQUIRE(cond, code, ...)            \
   do {                                           \
@@ -40,6 +45,18 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 inline bool rows_vec_ok(const void* p, int64_t sb, int64_t ld, int elem_bytes) {
   const int64_t per16 = 16 / elem_bytes;
   return aligned16(p) && (ld % per16 == 0) && (sb % per16 == 0);
+}
+
+// True when the 8-element tile loaders (tile8_load / tile8_issue / load8v with
+// VEC) may read rows starting at p: rows 16-byte aligned and row and batch
+// strides multiples of 8 elements.  Those loaders read a row's last group
+// [c0, c0 + 8) whole, up to round_up(ncols, 8), which stays inside the row's
+// stride only when the stride is a multiple of 8 elements.  For 16-bit
+// elements this is rows_vec_ok; fp32 rows need 32-byte strides (a row of 36
+// floats would let the group at column 32 read 4 floats into the next row,
+// and past the allocation on the last row).
+inline bool rows_vec8_ok(const void* p, int64_t sb, int64_t ld) {
+  return aligned16(p) && (ld % 8 == 0) && (sb % 8 == 0);
 }
 
 inline int elem_bytes(int dtype) { return dtype == SMAT_F32 ? 4 : 2; }

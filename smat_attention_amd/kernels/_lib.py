@@ -7,6 +7,7 @@ entry point raises :class:`HipKernelError` carrying the library's message.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -38,6 +39,7 @@ _i, _i64, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
 SIGNATURES = {
     "smat_last_error": (ctypes.c_char_p, []),
     "smat_version": (ctypes.c_char_p, []),
+    "smat_set_variant": (_i, [_i, _i]),
     "smat_chunk_local": (_i, [_i, _p, _p, _p, _p, _p, _i64, _i, _i, _i,
                               _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "smat_chunk_states": (_i, [_i, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64, _p]),
@@ -133,6 +135,26 @@ def query(name: str, *args) -> int:
 
 def version() -> str:
     return load().smat_version().decode()
+
+
+VARIANTS = {"scan": 0, "gram": 1, "query": 2, "incidence": 3, "incidence_plane": 4}
+
+
+@contextlib.contextmanager
+def general_kernel(name: str):
+    """Within the block, run the general kernel that the specialised one named
+    ``name`` (a key of :data:`VARIANTS`) replaced (``smat_set_variant``), then
+    restore the previous choice.  A test hook: it switches every call made
+    meanwhile, on every thread."""
+    which = VARIANTS[name]
+    lib = load()
+    prev = lib.smat_set_variant(which, 1)
+    if prev < 0:
+        raise HipKernelError("smat_set_variant", prev, lib.smat_last_error().decode())
+    try:
+        yield
+    finally:
+        lib.smat_set_variant(which, prev)
 
 
 def stream_of(t: torch.Tensor) -> int:

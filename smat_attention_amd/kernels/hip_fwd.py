@@ -66,6 +66,23 @@ def _on_gpu(who: str, *ts):
             raise ValueError(f"{who}: tensors must be on the GPU (got {t.device})")
 
 
+def _shape(who: str, name: str, t: torch.Tensor, want) -> None:
+    """Raise ValueError unless ``t.shape`` equals ``want`` (``None`` entries match
+    any size).  The kernels trust these sizes: a short buffer would be read past
+    its end."""
+    got = tuple(t.shape)
+    if len(got) != len(want) or any(w is not None and g != w for g, w in zip(got, want)):
+        shown = tuple("*" if w is None else w for w in want)
+        raise ValueError(f"{who}: {name} has shape {got}, expected {shown}")
+
+
+def _same_dtype(who: str, ref: torch.Tensor, **ts) -> None:
+    for name, t in ts.items():
+        if t is not None and t.dtype != ref.dtype:
+            raise TypeError(f"{who}: {name} is {t.dtype}, expected {ref.dtype} like the "
+                            f"other feature inputs")
+
+
 def _rows3(t: torch.Tensor):
     """``t`` as a (batch, rows, cols) tensor with unit column stride, plus its
     batch and row strides in elements.  Copies only when no such view exists."""
@@ -163,8 +180,10 @@ def chunk_local(Phi_c, Psi_c, Vb_c, Sin):
     _on_gpu(who, Phi_c, Psi_c, Vb_c, Sin)
     nb, nc, C, R = Phi_c.shape
     P = Vb_c.shape[-1]
-    if Psi_c.dtype != Phi_c.dtype or Vb_c.dtype != Phi_c.dtype:
-        raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
+    _same_dtype(who, Phi_c, Psi_c=Psi_c, Vb_c=Vb_c)
+    _shape(who, "Psi_c", Psi_c, (nb, nc, C, R))
+    _shape(who, "Vb_c", Vb_c, (nb, nc, C, P))
+    _shape(who, "Sin", Sin, (nb, nc, R, P))
     code = _code(Phi_c, who)
     q, q_sb, q_st = _rows3(Phi_c.reshape(nb * nc, C, R))
     k, k_sb, k_st = _rows3(Psi_c.reshape(nb * nc, C, R))
@@ -188,8 +207,10 @@ def chunk_local_decay(Phi_c, Psi_c, Vb_c, Sin, L):
     _on_gpu(who, Phi_c, Psi_c, Vb_c, Sin, L)
     nb, nc, C, R = Phi_c.shape
     P = Vb_c.shape[-1]
-    if Psi_c.dtype != Phi_c.dtype or Vb_c.dtype != Phi_c.dtype:
-        raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
+    _same_dtype(who, Phi_c, Psi_c=Psi_c, Vb_c=Vb_c)
+    _shape(who, "Psi_c", Psi_c, (nb, nc, C, R))
+    _shape(who, "Vb_c", Vb_c, (nb, nc, C, P))
+    _shape(who, "Sin", Sin, (nb, nc, R, P))
     if L.shape != (nb, nc, C):
         raise ValueError(f"{who}: L is {tuple(L.shape)}, expected {(nb, nc, C)}")
     code = _code(Phi_c, who)
@@ -228,6 +249,12 @@ def incidence_plane(F, plane_code, q: int, *, F_glob=None):
     who = "incidence_plane"
     _on_gpu(who, F, plane_code, F_glob)
     nb, N0, R, P = F.shape
+    if plane_code.dim() != 1 or plane_code.dtype != torch.int32:
+        raise ValueError(f"{who}: plane_code must be int32 (B,)")
+    if q * q != N0:
+        raise ValueError(f"{who}: N0={N0} is not q^2 for q={q}")
+    if F_glob is not None:
+        _shape(who, "F_glob", F_glob, (nb, R, P))
     B = plane_code.shape[0]
     Ff = F.contiguous().float()
     U = torch.empty(nb, B, R, P, device=F.device, dtype=torch.float32)
@@ -276,8 +303,8 @@ def pool(Psi, Vb, n_P: int, n: int, N0: int, *, F_glob: Optional[torch.Tensor] =
     _on_gpu(who, Psi, Vb)
     nb, T, R = Psi.shape
     P = Vb.shape[-1]
-    if Vb.dtype != Psi.dtype:
-        raise TypeError(f"{who}: Psi and Vb must share a dtype")
+    _same_dtype(who, Psi, Vb=Vb)
+    _shape(who, "Vb", Vb, (nb, T, P))
     if not (0 <= n_P <= n <= T):
         raise ValueError(f"{who}: need 0 <= n_P <= n <= T, got n_P={n_P} n={n} T={T}")
     code = _code(Psi, who)
@@ -304,6 +331,8 @@ def chunk_states(Psi, Vb, C: int):
     _on_gpu(who, Psi, Vb)
     nb, T, R = Psi.shape
     P = Vb.shape[-1]
+    _same_dtype(who, Psi, Vb=Vb)
+    _shape(who, "Vb", Vb, (nb, T, P))
     code = _code(Psi, who)
     k, k_sb, k_st = _rows3(Psi)
     v, v_sb, v_st = _rows3(Vb)
@@ -323,8 +352,17 @@ def causal_scan(Phi, Psi, Vb, n: int, chunk: int, *, Y=None, g=None, write_H: bo
     _on_gpu(who, Phi, Psi, Vb, Y, g, out)
     nb, T, R = Phi.shape
     P = Vb.shape[-1]
-    if Psi.dtype != Phi.dtype or Vb.dtype != Phi.dtype:
-        raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
+    _same_dtype(who, Phi, Psi=Psi, Vb=Vb)
+    _shape(who, "Psi", Psi, (nb, T, R))
+    _shape(who, "Vb", Vb, (nb, T, P))
+    if Y is not None:
+        _shape(who, "Y", Y, (nb, T - n, P))
+    if g is not None:
+        _shape(who, "g", g, (nb, T))
+    if out is not None and (out.shape != (nb, T, P if write_H else P - 1)
+                            or out.dtype != torch.float32 or out.stride(-1) != 1):
+        raise ValueError(f"{who}: out must be fp32 {(nb, T, P if write_H else P - 1)} with "
+                         f"unit column stride")
     code = _code(Phi, who)
     q, q_sb, q_st = _rows3(Phi)
     k, k_sb, k_st = _rows3(Psi)
@@ -356,7 +394,10 @@ def direct(Psi, Vb, cols, counts, n_P: int):
         raise TypeError(f"{who}: cols and counts must be int32")
     nb, T, R = Psi.shape
     P = Vb.shape[-1]
+    _same_dtype(who, Psi, Vb=Vb)
+    _shape(who, "Vb", Vb, (nb, T, P))
     B, kappa = cols.shape
+    _shape(who, "counts", counts, (B,))
     code = _code(Psi, who)
     k, k_sb, k_st = _rows3(Psi)
     v, v_sb, v_st = _rows3(Vb)
@@ -424,6 +465,9 @@ def query(Phi_rec, U):
     _on_gpu(who, Phi_rec, U)
     nb, T_R, R = Phi_rec.shape
     B, P = U.shape[1], U.shape[-1]
+    _shape(who, "U", U, (nb, B, R, P))
+    if B < 1:
+        raise ValueError(f"{who}: U has no row types")
     code = _code(Phi_rec, who)
     q, q_sb, q_st = _rows3(Phi_rec)
     Uc = U.contiguous().float()
@@ -438,6 +482,10 @@ def normalise(H, n: int, Y=None, g=None):
     who = "normalise"
     _on_gpu(who, H, Y, g)
     nb, T, P = H.shape
+    if Y is not None:
+        _shape(who, "Y", Y, (nb, T - n, P))
+    if g is not None:
+        _shape(who, "g", g, (nb, T))
     Hc = _fp32_rows(H)
     Yc = _fp32_rows(Y) if Y is not None else None
     gc = g.float().contiguous() if g is not None else None
@@ -463,20 +511,32 @@ def forward(Phi, Psi, Vb, idx, deg: int, *, n: int, n_P: int, N0: int, B: int, c
     _on_gpu(who, Phi, Psi, Vb, idx, indptr, g, out, H_out)
     nb, T, R = Phi.shape
     P = Vb.shape[-1]
-    if Psi.dtype != Phi.dtype or Vb.dtype != Phi.dtype:
-        raise TypeError(f"{who}: Phi, Psi and Vb must share a dtype")
+    _same_dtype(who, Phi, Psi=Psi, Vb=Vb)
+    _shape(who, "Psi", Psi, (nb, T, R))
+    _shape(who, "Vb", Vb, (nb, T, P))
+    if g is not None:
+        _shape(who, "g", g, (nb, T))
     code = _code(Phi, who)
     q, q_sb, q_st = _rows3(Phi)
     k, k_sb, k_st = _rows3(Psi)
     v, v_sb, v_st = _rows3(Vb)
     if out is None:
         out = torch.empty(nb, T, P - 1, device=Phi.device, dtype=torch.float32)
+    elif out.shape != (nb, T, P - 1) or out.dtype != torch.float32 or out.stride(-1) != 1:
+        raise ValueError(f"{who}: out must be fp32 {(nb, T, P - 1)} with unit column stride")
     if H_out is not None and (H_out.shape != (nb, T, P) or not H_out.is_contiguous()
                               or H_out.dtype != torch.float32):
         raise ValueError(f"{who}: H_out must be contiguous fp32 ({nb}, {T}, {P})")
     gc = g.float().contiguous() if g is not None else None
     need = forward_workspace_bytes(nb, T, n, N0, B, n_P, chunk, R, P)
-    if workspace is None or workspace.numel() < need:
+
+    def _room(ws):
+        # bytes left in ``ws`` once its base is rounded up to 256
+        if ws is None or ws.device != Phi.device or ws.dtype != torch.uint8:
+            return -1
+        return ws.numel() - (((ws.data_ptr() + 255) & ~255) - ws.data_ptr())
+
+    if _room(workspace) < need:
         workspace = torch.empty(need + 256, device=Phi.device, dtype=torch.uint8)
     base = workspace.data_ptr()
     aligned = (base + 255) & ~255
@@ -496,8 +556,23 @@ def decode_step(Phi_t, Psi_t, Vb_t, S_in, S_out, U, step: int, *, out=None, o_fu
     who = "decode_step"
     _on_gpu(who, Phi_t, Psi_t, Vb_t, S_in, S_out, U)
     nb, R = Phi_t.shape
-    P = Vb_t.shape[-1]
-    B = U.shape[1]
+    _shape(who, "U", U, (nb, None, R, None))
+    B, P = U.shape[1], U.shape[3]
+    _shape(who, "Psi_t", Psi_t, (nb, R))
+    _shape(who, "Vb_t", Vb_t, (nb, P))
+    _shape(who, "S_in", S_in, (nb, R, P))
+    _shape(who, "S_out", S_out, (nb, R, P))
+    _shape(who, "U", U, (nb, B, R, P))
+    if B < 1:
+        raise ValueError(f"{who}: U has no row types")
+    if S_in.data_ptr() == S_out.data_ptr():
+        raise ValueError(f"{who}: S_in and S_out must be distinct buffers")
+    if not (Psi_t.dtype == Vb_t.dtype == Phi_t.dtype):
+        # the reference takes each input to the accumulation dtype (fp32,
+        # attention.py:522-528); mixed inputs do the same here, exactly
+        for t in (Phi_t, Psi_t, Vb_t):
+            _code(t, who)
+        Phi_t, Psi_t, Vb_t = Phi_t.float(), Psi_t.float(), Vb_t.float()
     code = _code(Phi_t, who)
     for t in (Phi_t, Psi_t, Vb_t):
         if t.stride(-1) != 1:
@@ -507,6 +582,11 @@ def decode_step(Phi_t, Psi_t, Vb_t, S_in, S_out, U, step: int, *, out=None, o_fu
             raise ValueError(f"{who}: S and U must be contiguous fp32")
     if out is None:
         out = torch.empty(nb, P - 1, device=Phi_t.device, dtype=torch.float32)
+    elif out.shape != (nb, P - 1) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError(f"{who}: out must be contiguous fp32 {(nb, P - 1)}")
+    if o_full is not None and (o_full.shape != (nb, P) or o_full.dtype != torch.float32
+                               or not o_full.is_contiguous()):
+        raise ValueError(f"{who}: o_full must be contiguous fp32 {(nb, P)}")
     call("smat_decode_step", code, Phi_t.data_ptr(), Psi_t.data_ptr(), Vb_t.data_ptr(),
          S_in.data_ptr(), S_out.data_ptr(), U.data_ptr(), out.data_ptr(), ptr(o_full), nb, B, R,
          P, int(step), Phi_t.stride(0), Psi_t.stride(0), Vb_t.stride(0), stream_of(U))

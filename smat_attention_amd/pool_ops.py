@@ -87,11 +87,12 @@ def _read_lists(X, U, cls, lists=None):
 
 
 def _f32_rows(x):
-    """fp32 copy of ``x`` (nb, L, c) whose rows start 16-byte aligned: a view of
-    rows padded to a multiple of 4 floats (the pad is never read), so the list
-    kernels load X with 16-byte loads."""
+    """fp32 copy of ``x`` (nb, L, c) whose rows start 32-byte aligned: a view of
+    rows padded to a multiple of 8 floats (the pad is read, never used), so the
+    list kernels load X in whole 8-float groups: the last group of a row ends
+    at the padded row length, inside the row's own stride."""
     c = x.shape[-1]
-    cp = -(-c // 4) * 4
+    cp = -(-c // 8) * 8
     if cp == c:
         return x.float().contiguous()
     buf = torch.empty(*x.shape[:-1], cp, device=x.device, dtype=torch.float32)

@@ -18,6 +18,7 @@ import torch
 import oracle.schedule as O
 from smat_attention_amd import attention as A
 from smat_attention_amd.kernels import hip_fwd as K
+from smat_attention_amd.kernels._lib import general_kernel
 from smat_attention_amd.mask import build_mask
 
 pytestmark = pytest.mark.gpu
@@ -171,7 +172,7 @@ def test_query(dt, T, d, r, p):
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T,d,n_P", [(4096, 3, 0), (8192, 2, 0), (2048, 3, 16), (32768, 3, 0),
                                      (32768, 2, 0), (32768, 2, 16)])
-def test_pool_streaming_head_dim_128(dt, T, d, n_P, monkeypatch):
+def test_pool_streaming_head_dim_128(dt, T, d, n_P):
     """The DMA-streamed Gram kernel (16-bit, r = 128, p = 129) on the profile
     pool, incl. the global channel, against fp64 and the general kernel.
     Profiles of at most 64 tokens take its single-buffer form; d = 2 at
@@ -185,10 +186,9 @@ def test_pool_streaming_head_dim_128(dt, T, d, n_P, monkeypatch):
     Sd, Vd = Psi.to(DEV), Vp.to(DEV)[..., :129]
     Fg = torch.empty(nb, 128, 129, device=DEV) if n_P else None
     F = K.pool(Sd, Vd, spec.n_P, spec.n, spec.N0, F_glob=Fg)
-    monkeypatch.setenv("SMAT_GRAM", "old")
     Fg_old = torch.empty(nb, 128, 129, device=DEV) if n_P else None
-    F_old = K.pool(Sd, Vd, spec.n_P, spec.n, spec.N0, F_glob=Fg_old)
-    monkeypatch.delenv("SMAT_GRAM")
+    with general_kernel("gram"):
+        F_old = K.pool(Sd, Vd, spec.n_P, spec.n, spec.N0, F_glob=Fg_old)
     ref = O.pool_profiles(Psi.double(), Vb.double(), spec)
     assert _rel(F, ref) < 1e-5 and _rel(F_old, ref) < 1e-5
     if n_P:
@@ -246,7 +246,7 @@ def test_causal_scan_fused(dt, T, n, C, hd):
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T,n,C", [(4096, 2048, 128), (8192, 0, 128), (4096, 4096, 128),
                                    (4096, 1024, 64), (2048 + 64, 1024, 128), (16384, 8192, 128)])
-def test_causal_scan_streaming(dt, T, n, C, monkeypatch):
+def test_causal_scan_streaming(dt, T, n, C):
     """The head_dim-128 streaming kernel (16-bit inputs, p = 129, 64-token
     steps through LDS) against the oracle's reference path, and against the
     general fused kernel on the same inputs."""
@@ -267,9 +267,8 @@ def test_causal_scan_streaming(dt, T, n, C, monkeypatch):
     Yd = Yp.to(DEV)[..., :P] if T > n else None
     gd = gate.to(DEV)
     out = K.causal_scan(Pd, Sd, Vd, n, C, Y=Yd, g=gd)
-    monkeypatch.setenv("SMAT_SCAN", "fused")
-    old = K.causal_scan(Pd, Sd, Vd, n, C, Y=Yd, g=gd)
-    monkeypatch.delenv("SMAT_SCAN")
+    with general_kernel("scan"):
+        old = K.causal_scan(Pd, Sd, Vd, n, C, Y=Yd, g=gd)
     torch.cuda.synchronize()
     ref = O.segmented_causal_scan(Phi, Psi, Vb, n, chunk=C).double()
     if T > n:

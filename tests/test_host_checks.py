@@ -1,0 +1,160 @@
+"""Host-side argument checks of the kernel wrappers and of the C ABI, CPU only.
+
+The kernels trust the sizes and dtypes they are given (a short buffer would be
+read past its end), so every wrapper validates them before it calls into the
+library.  These tests run the wrappers on CPU tensors with the device check
+switched off and the library call replaced by a recorder: a bad argument must
+raise before anything is launched.
+"""
+import pytest
+import torch
+
+from smat_attention_amd.kernels import _lib
+from smat_attention_amd.kernels import hip_fwd as K
+
+
+@pytest.fixture
+def no_device(monkeypatch):
+    """Skip the GPU-residency check and record library calls instead of making them."""
+    calls = []
+    monkeypatch.setattr(K, "_on_gpu", lambda who, *ts: None)
+    monkeypatch.setattr(K, "call", lambda name, *args: calls.append((name, args)) or 0)
+    monkeypatch.setattr(K, "stream_of", lambda t: 0)
+    return calls
+
+
+def _decode_args(nb=4, r=8, p=9, B=3, dt=torch.float32):
+    return dict(Phi_t=torch.rand(nb, r, dtype=dt), Psi_t=torch.rand(nb, r, dtype=dt),
+                Vb_t=torch.rand(nb, p, dtype=dt), S_in=torch.zeros(nb, r, p),
+                S_out=torch.zeros(nb, r, p), U=torch.zeros(nb, B, r, p), step=0)
+
+
+def test_decode_step_checks_shapes(no_device):
+    a = _decode_args()
+    K.decode_step(**a)
+    assert no_device and no_device[-1][0] == "smat_decode_step"
+    for name, bad in (("Psi_t", torch.rand(4, 7)), ("Vb_t", torch.rand(4, 10)),
+                      ("S_in", torch.zeros(4, 8, 8)), ("U", torch.zeros(3, 3, 8, 9)),
+                      ("S_out", torch.zeros(4, 9, 9))):
+        b = dict(a, **{name: bad})
+        with pytest.raises(ValueError, match=name):
+            K.decode_step(**b)
+    with pytest.raises(ValueError, match="distinct"):
+        K.decode_step(**dict(a, S_out=a["S_in"]))
+
+
+def test_decode_step_mixed_dtypes_compute_in_fp32(no_device):
+    """Mixed feature dtypes are taken to fp32 as the reference takes every input
+    to its accumulation dtype; the kernel is then told fp32 and reads fp32 rows."""
+    a = _decode_args()
+    a["Psi_t"] = a["Psi_t"].bfloat16()
+    a["Vb_t"] = a["Vb_t"].half()
+    K.decode_step(**a)
+    name, args = no_device[-1]
+    assert name == "smat_decode_step" and args[0] == _lib.SMAT_F32
+
+
+def test_wrappers_reject_mismatched_dtypes_and_shapes(no_device):
+    Psi = torch.rand(2, 256, 8, dtype=torch.bfloat16)
+    Vb = torch.rand(2, 256, 9, dtype=torch.bfloat16)
+    with pytest.raises(TypeError, match="Vb"):
+        K.chunk_states(Psi, Vb.float(), 128)
+    with pytest.raises(ValueError, match="Vb"):
+        K.chunk_states(Psi, Vb[:, :128], 128)
+    with pytest.raises(TypeError, match="Vb"):
+        K.pool(Psi, Vb.half(), 0, 128, 4)
+    K.chunk_states(Psi, Vb, 128)
+    # the query's U must match Phi_rec's batch and rank
+    Phi = torch.rand(2, 100, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="U"):
+        K.query(Phi, torch.zeros(2, 5, 7, 9))
+    with pytest.raises(ValueError, match="U"):
+        K.query(Phi, torch.zeros(3, 5, 8, 9))
+    K.query(Phi, torch.zeros(2, 5, 8, 9))
+    with pytest.raises(ValueError, match="Y"):
+        K.causal_scan(Phi, Phi, torch.rand(2, 100, 9, dtype=torch.bfloat16), 64, 64,
+                      Y=torch.zeros(2, 30, 9))
+    with pytest.raises(ValueError, match="Sin"):
+        K.chunk_local(torch.rand(1, 2, 64, 8), torch.rand(1, 2, 64, 8), torch.rand(1, 2, 64, 9),
+                      torch.zeros(1, 2, 8, 8))
+
+
+def test_forward_reuses_an_unaligned_workspace_only_if_it_fits(no_device, monkeypatch):
+    """A workspace of exactly the queried size whose base is not 256-byte aligned
+    has less room after alignment: forward() allocates instead of passing a
+    short region to the library."""
+    need = 4096
+    monkeypatch.setattr(K, "forward_workspace_bytes", lambda *a: need)
+    Phi = torch.rand(1, 256, 8, dtype=torch.bfloat16)
+    Vb = torch.rand(1, 256, 9, dtype=torch.bfloat16)
+    big = torch.empty(need + 512, dtype=torch.uint8)
+    off = (-big.data_ptr()) % 256 + 16            # a base 16 bytes past a 256-byte boundary
+    exact = big[off:off + need]
+    assert exact.data_ptr() % 256 == 16
+    K.forward(Phi, Phi, Vb, None, 1, n=128, n_P=0, N0=4, B=4, chunk=128, workspace=exact)
+    args = no_device[-1][1]
+    base, avail = args[-3], args[-2]
+    assert avail >= need and base % 256 == 0
+    assert not (exact.data_ptr() <= base < exact.data_ptr() + need)   # a fresh buffer
+    roomy = big[off:]
+    K.forward(Phi, Phi, Vb, None, 1, n=128, n_P=0, N0=4, B=4, chunk=128, workspace=roomy)
+    base, avail = no_device[-1][1][-3], no_device[-1][1][-2]
+    assert roomy.data_ptr() <= base < roomy.data_ptr() + roomy.numel() and avail >= need
+
+
+def test_variant_hook_is_explicit_and_restored():
+    """Kernel variants are chosen through smat_set_variant only (no environment
+    variable is read); the context manager restores the previous choice."""
+    lib = _lib.load()
+    assert lib.smat_set_variant(0, 0) == 0
+    with _lib.general_kernel("scan"):
+        assert lib.smat_set_variant(0, 1) == 1
+    assert lib.smat_set_variant(0, 0) == 0
+    assert lib.smat_set_variant(99, 1) == -1          # SMAT_EINVAL
+    assert lib.smat_set_variant(1, 7) == -1
+    assert lib.smat_set_variant(1, 0) == 0            # a good call clears the message
+    assert lib.smat_last_error() == b""
+
+
+# ---------------------------------------------------------------------------
+# the bound of the 8-element tile loaders (smat_common.hpp tile8_load)
+# ---------------------------------------------------------------------------
+
+def _tile8_reads(ncols, stride, elem, rows):
+    """Byte ranges a VEC tile loader reads for a matrix of ``rows`` rows: every
+    8-element group starting at a multiple of 8 below ``ncols`` is read whole
+    (one 8*elem-byte load at row * stride + c0)."""
+    for row in range(rows):
+        for c0 in range(0, ncols, 8):
+            start = (row * stride + c0) * elem
+            yield start, start + 8 * elem
+
+
+def _vec8_ok(stride, batch_stride):
+    """The dispatch predicate the kernels use (rows_vec8_ok, 16-byte aligned base)."""
+    return stride % 8 == 0 and batch_stride % 8 == 0
+
+
+@pytest.mark.parametrize("elem", [2, 4])
+@pytest.mark.parametrize("ncols", [33, 65, 129, 64, 128, 17])
+def test_vector_tile_reads_stay_in_the_allocation(elem, ncols):
+    """Every stride the list operands and feature rows use (packed, padded to 4
+    and to 8 elements): when the dispatch takes the vector path, no read ends
+    past rows * stride elements, the extent of the matrix."""
+    rows = 5
+    for stride in sorted({ncols, -(-ncols // 4) * 4, -(-ncols // 8) * 8}):
+        if _vec8_ok(stride, stride * rows):
+            extent = rows * stride * elem
+            assert max(end for _, end in _tile8_reads(ncols, stride, elem, rows)) <= extent
+
+
+@pytest.mark.parametrize("ncols,stride", [(33, 36), (65, 68), (129, 132)])
+def test_fp32_rows_padded_to_4_floats_take_the_element_path(ncols, stride):
+    """fp32 rows padded to 4 floats are 16-byte aligned, which the former
+    predicate (16-byte groups) accepted, yet the last 8-float group of the
+    last row reads 16 bytes past the matrix.  The 8-element predicate turns
+    them away."""
+    rows = 5
+    over = max(end for _, end in _tile8_reads(ncols, stride, 4, rows)) - rows * stride * 4
+    assert over == 16
+    assert stride % 4 == 0 and not _vec8_ok(stride, stride * rows)
