@@ -214,6 +214,13 @@ def plane_line_codes(spec: MaskSpec) -> Optional[np.ndarray]:
         return None
     q, B = spec.q, spec.B
     rows = np.sort(np.asarray(spec.C_indices, dtype=np.int64).reshape(B, q), axis=1)
+    ids = getattr(spec, "plane_ids", None)
+    if ids is not None and len(ids) == B:
+        # build_mask recorded each row's line: regenerate and compare below
+        e, b = np.divmod(np.asarray(ids, dtype=np.int64), q)
+        vertical = e == 0
+        return _checked_codes(q, rows, e, b, vertical)
+    # a spec from elsewhere: recover each line from two of its points
     x0, x1 = rows // q, rows % q
     vertical = np.all(x1 == x1[:, :1], axis=1)          # e = 0: constant x1
     # e >= 1: x0 + m x1 = b with m from two points of the row (x1 distinct there)
@@ -224,15 +231,18 @@ def plane_line_codes(spec: MaskSpec) -> Optional[np.ndarray]:
     b = (x0[:, 0] + m * x1[:, 0]) % q
     e = np.where(vertical, 0, m + 1)
     b = np.where(vertical, x1[:, 0], b)
-    code = (e * q + b).astype(np.int64)
-    # regenerate every line and compare with the table
+    return _checked_codes(q, rows, e, b, vertical)
+
+
+def _checked_codes(q, rows, e, b, vertical):
+    """``e*q + b`` as int32 if every generated line equals its (sorted) row of C."""
     t = np.arange(q, dtype=np.int64)[None, :]
     gen_vert = t * q + b[:, None]
     gen_sl = ((b[:, None] - (e[:, None] - 1) * t) % q) * q + t
     gen = np.sort(np.where(vertical[:, None], gen_vert, gen_sl), axis=1)
     if not np.array_equal(gen, rows):
         return None
-    return code.astype(np.int32)
+    return (e * q + b).astype(np.int32)
 
 
 def parity_interleaved_table(spec: MaskSpec) -> np.ndarray:

@@ -274,3 +274,99 @@ def test_plane_line_codes_absent_for_other_masks():
     from smat_attention_amd.attention import plane_line_codes
     assert plane_line_codes(build_mask(4096, 2, chunk=128)) is None
     assert plane_line_codes(build_mask(8192, 4, chunk=128)) is None
+
+
+# --------------------------------------------------------------------------
+# the audit's own checks catch planted mistakes; witness and cost model
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T,d", [(4096, 3), (16384, 4)])
+def test_audit_catches_a_moved_point(T, d):
+    """Each row must satisfy its hyperplane's equation: moving one point of one
+    row (a plausible off-by-one in the table) fails ``rows_on_hyperplanes``
+    and ``exact`` even though degrees and counts are unchanged."""
+    s = build_mask(T, d, chunk=128)
+    a = incidence_audit(s)
+    assert a["rows_on_hyperplanes"] and a["exact"] and a["planted_identity"]
+    rows = s.C_indices.reshape(s.B, -1).copy()
+    h = s.B // 2
+    row = set(int(x) for x in rows[h])
+    outsider = next(x for x in range(s.N0) if x not in row)
+    rows[h, -1] = outsider
+    rows[h] = np.sort(rows[h])
+    bad = build_mask(T, d, chunk=128)
+    bad.C_indices = rows.reshape(-1)
+    b = incidence_audit(bad)
+    assert not b["rows_on_hyperplanes"] and not b["exact"]
+
+
+def test_audit_catches_a_wrong_planted_order():
+    s = build_mask(4096, 3, chunk=128)
+    rows = s.C_indices.reshape(s.B, -1).copy()
+    rows[[0, 1]] = rows[[1, 0]]                  # swap the first two row types
+    s.C_indices = rows.reshape(-1)
+    s.plane_ids = s.plane_ids[[1, 0] + list(range(2, s.B))]
+    a = incidence_audit(s)
+    assert a["rows_on_hyperplanes"] and not a["planted_identity"] and not a["exact"]
+
+
+@pytest.mark.parametrize("T", [512, 1024, 1000])
+def test_endpoint_audit_and_witness(T):
+    """Endpoint masks: the Walsh rows, and the witness at T = 2^m where the
+    recent block holds exactly B rows (the first recent column suffices)."""
+    s = build_mask(T, T.bit_length() - 1, chunk=8)
+    a = incidence_audit(s)
+    assert s.kind == "endpoint" and a["walsh_rows"] and a["exact"]
+    cols, ok, rows = shatter_witness(s)
+    assert ok and len(cols) == s.d
+    M = materialise(s, np.int8)
+    for pat, found in rows.items():
+        kind, i = found
+        r = i if kind == "zeta" else s.n + i
+        assert [bool(M[r, c]) for c in cols] == [bool((pat >> j) & 1) for j in range(len(cols))]
+
+
+@pytest.mark.parametrize("T,d", [(2048, 3), (4096, 4), (2048, 2)])
+def test_geometric_witness_rows_realise_their_patterns(T, d):
+    s = build_mask(T, d, chunk=64)
+    cols, ok, rows = shatter_witness(s)
+    assert ok
+    M = materialise(s, np.int8)
+    for (R, bit), i in rows.items():
+        got = [bool(M[s.n + i, c]) for c in cols]
+        assert got == [bool((R >> l) & 1) for l in range(s.dim)] + [bool(bit)]
+
+
+def test_cost_model_counts():
+    """Useful MFMA work of the long prefill at T = 131072, d = 3, r = p - 1 = 128:
+    1.386e11 FLOP over 8 heads; the incidence's adds are nnz(C) r p; the
+    endpoint nnz counts row 0 whole and every other Walsh row half."""
+    e = estimate_cost(131072, 3, 128, 128)
+    assert abs(8 * e["mfma_flops"] - 1.3865e11) / 1.3865e11 < 1e-3
+    assert e["incidence_adds"] == 70602 * 128 * 129
+    assert e["macs"] == sum(e[k] for k in ("macs_intra", "macs_states", "macs_pool",
+                                           "macs_query"))
+    s = build_mask(1024, 10, chunk=64)
+    assert estimate_cost(1024, 10, 8, 8)["I_prof"] == s.I_prof
+    assert estimate_cost(4096, 3, 8, 8)["I_prof"] == build_mask(4096, 3, chunk=128).I_prof
+
+
+def test_plane_ids_name_the_row_types():
+    """plane_ids[h] = e*q + b of row type h: the planted ones first."""
+    s = build_mask(131072, 3, chunk=128)
+    assert s.plane_ids.shape == (s.B,)
+    assert len(np.unique(s.plane_ids)) == s.B
+    rest = s.plane_ids[s.n_planted:]
+    assert np.all(np.diff(rest) > 0)
+
+
+@pytest.mark.parametrize("T", [4096, 131072])
+def test_line_codes_recorded_equal_recovered(T):
+    """The line codes taken from build_mask's plane_ids equal those recovered
+    from the rows alone (the path a mask built elsewhere takes)."""
+    from smat_attention_amd.attention import plane_line_codes
+    spec = build_mask(T, 3, chunk=128)
+    recorded = plane_line_codes(spec)
+    spec.plane_ids = None
+    recovered = plane_line_codes(spec)
+    assert recorded is not None and np.array_equal(recorded, recovered)
