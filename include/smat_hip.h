@@ -157,6 +157,28 @@ int smat_causal_scan(int dtype, const void* phi, const void* psi, const void* vb
                      void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * smat_causal_scan without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  It has no counterpart in the reference.  Arguments and
+ * results as smat_causal_scan; its scratch is a fixed array of
+ * smat_causal_scan_noalloc_max_bytes() = 64 MiB per GPU, held by the library
+ * from its load until the process ends.  When the default grouping of chunks
+ * would need more, it sums longer groups of chunks (fewer summaries; the same
+ * result up to fp32 rounding), and returns SMAT_EUNSUPPORTED when even one
+ * group per segment does not fit (4 * nb * r * p * 4 bytes: nb up to 254
+ * sequences at r = 128, p = 129).  It calls no hipMalloc or hipFree.  All
+ * calls on one GPU share that GPU's array: calls that overlap there (other
+ * streams, other host threads) race.
+ */
+int64_t smat_causal_scan_noalloc_max_bytes(void);
+int smat_causal_scan_noalloc(int dtype, const void* phi, const void* psi, const void* vb,
+                             const float* Y, const float* g, float* out, int nb, int T, int n,
+                             int C, int r, int p, int64_t q_sb, int64_t q_st, int64_t k_sb,
+                             int64_t k_st, int64_t v_sb, int64_t v_st, int64_t y_sb,
+                             int64_t y_st, int64_t o_sb, int64_t o_st, int64_t g_sb,
+                             int write_H, void* stream);
+
+/*
  * Profile pooling  F_x = sum_{j in [n_P, n), (j - n_P) mod N0 = x} Psi_j^T Vb_j
  * (fp32, F: (nb, N0, r, p) contiguous).  If F_glob is not NULL and n_P > 0 it
  * also receives the global-channel term sum_{j < n_P} Psi_j^T Vb_j, (nb, r, p).

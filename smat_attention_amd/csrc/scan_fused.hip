@@ -20,6 +20,8 @@
 // hi/lo 16-bit parts for 16-bit inputs, as the B operand of the next chunk's
 // Phi S.  Psi and Vb are staged once per 64-token block and feed both the
 // intra-chunk product and the update.
+#include <mutex>
+
 #include "smat_host.hpp"
 
 namespace smat {
@@ -456,6 +458,12 @@ static int scan_group_chunks(int nb, int nc) {
   return K;
 }
 
+int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb, const float* Y,
+                    const float* gate, float* out, int nb, int T, int n, int C, int K, int r,
+                    int p, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                    int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
+                    int64_t g_sb, int write_H, void* ws, hipStream_t stream);
+
 int64_t causal_scan_workspace_bytes(int nb, int T, int C, int r, int p) {
   const int nc = (T + C - 1) / C;
   const int K = scan_group_chunks(nb, nc);
@@ -478,8 +486,22 @@ int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void
               (long long)ws_bytes);
     return SMAT_EINVAL;
   }
+  return causal_scan_run(dtype, phi, psi, vb, Y, gate, out, nb, T, n, C, K, r, p, q_sb, q_st,
+                         k_sb, k_st, v_sb, v_st, y_sb, y_st, o_sb, o_st, g_sb, write_H, ws,
+                         stream);
+}
+
+// The causal pass with groups of K chunks; ws holds 2 * al256(nb * ng * r * p
+// floats) bytes (ng = ceil(nc / K) + 1): the group summaries, then their scan.
+int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb, const float* Y,
+                    const float* gate, float* out, int nb, int T, int n, int C, int K, int r,
+                    int p, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                    int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
+                    int64_t g_sb, int write_H, void* ws, hipStream_t stream) {
+  const int nc = (T + C - 1) / C;
+  const int ng_max = (nc + K - 1) / K + 1;
   float* G = (float*)ws;
-  float* Sg = (float*)((char*)ws + need / 2);
+  float* Sg = (float*)((char*)ws + (((int64_t)nb * ng_max * r * p * 4 + 255) & ~(int64_t)255));
   int ng = 0, ng0 = 0;
   int rc = chunk_states_dispatch(dtype, psi, vb, G, nb, T, C, K, n, r, p, k_sb, k_st, v_sb, v_st,
                                  nullptr, 0, stream, &ng, &ng0);
@@ -522,7 +544,107 @@ int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void
   return SMAT_EINVAL;
 }
 
+// ---------------------------------------------------------------------------
+// The allocation-free variant: scratch in a fixed device array.
+//
+// `scratch` holds the group summaries and their segmented scan that the
+// workspace of smat_causal_scan holds otherwise.  The name is a host-side
+// stand-in, not a device address: host code uses the address that
+// hipGetSymbolAddress returns for the current device (each GPU holds its own
+// copy of the array), looked up once per device on the first call there.
+// Every element the kernels read from it is written earlier in the same call
+// (all group summaries, then their scan), so nothing needs clearing; calls
+// that overlap on one GPU (different streams) share the array and race.
+// ---------------------------------------------------------------------------
+
+constexpr int64_t kNoAllocScratchBytes = 64ll << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("smat_causal_scan_noalloc: no current device (%s, device %d)",
+              hipGetErrorString(e), dev);
+    return SMAT_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("smat_causal_scan_noalloc: hipGetSymbolAddress failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return SMAT_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SMAT_OK;
+}
+
+// Scratch bytes for group size K (as causal_scan_workspace_bytes at its K).
+static int64_t scan_scratch_bytes(int nb, int nc, int K, int r, int p) {
+  const int ng = (nc + K - 1) / K + 1;
+  return 2 * (((int64_t)nb * ng * r * p * 4 + 255) & ~(int64_t)255);
+}
+
+// The group size of the allocating entry point when its scratch fits the
+// array, else the least power-of-two multiple of it that fits (larger groups,
+// fewer summaries; 0 when not even one group per segment fits).
+static int noalloc_group_chunks(int nb, int nc, int r, int p) {
+  int K = scan_group_chunks(nb, nc);
+  while (scan_scratch_bytes(nb, nc, K, r, p) > kNoAllocScratchBytes) {
+    if (K >= nc) return 0;
+    K *= 2;
+  }
+  return K;
+}
+
 }  // namespace smat
+
+extern "C" int64_t smat_causal_scan_noalloc_max_bytes(void) {
+  return smat::kNoAllocScratchBytes;
+}
+
+extern "C" int smat_causal_scan_noalloc(int dtype, const void* phi, const void* psi,
+                                        const void* vb, const float* Y, const float* gate,
+                                        float* out, int nb, int T, int n, int C, int r, int p,
+                                        int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
+                                        int64_t v_sb, int64_t v_st, int64_t y_sb, int64_t y_st,
+                                        int64_t o_sb, int64_t o_st, int64_t g_sb, int write_H,
+                                        void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(phi && psi && vb && out, SMAT_EINVAL, "smat_causal_scan_noalloc: null pointer");
+  SMAT_REQUIRE(nb >= 0 && T >= 0 && C >= 1 && C <= sf::kC, SMAT_EUNSUPPORTED,
+               "smat_causal_scan_noalloc: chunk C=%d not in [1, %d]", C, sf::kC);
+  SMAT_REQUIRE(n >= 0 && n <= T && n % C == 0, SMAT_EINVAL,
+               "smat_causal_scan_noalloc: n=%d must be a multiple of C=%d in [0, T]", n, C);
+  SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 2 && p <= kMaxP, SMAT_EUNSUPPORTED,
+               "smat_causal_scan_noalloc: r=%d p=%d beyond r<=%d, 2<=p<=%d", r, p, kMaxR,
+               kMaxP);
+  SMAT_REQUIRE(q_st >= r && k_st >= r && v_st >= p && o_st >= (write_H ? p : p - 1),
+               SMAT_EINVAL, "smat_causal_scan_noalloc: a row stride is shorter than its row");
+  if (nb == 0 || T == 0) return SMAT_OK;
+  const int nc = (T + C - 1) / C;
+  const int K = noalloc_group_chunks(nb, nc, r, p);
+  SMAT_REQUIRE(K > 0, SMAT_EUNSUPPORTED,
+               "smat_causal_scan_noalloc: nb=%d sequences of r=%d x p=%d states need more "
+               "than the %lld-byte scratch array even with one group per segment; use "
+               "smat_causal_scan with a workspace",
+               nb, r, p, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  int rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  return causal_scan_run(dtype, phi, psi, vb, Y, gate, out, nb, T, n, C, K, r, p, q_sb, q_st,
+                         k_sb, k_st, v_sb, v_st, y_sb, y_st, o_sb, o_st, g_sb, write_H, ws,
+                         (hipStream_t)stream);
+}
 
 extern "C" int64_t smat_causal_scan_workspace_bytes(int nb, int T, int C, int r, int p) {
   if (nb <= 0 || T <= 0 || C <= 0 || r <= 0 || p <= 0) return 0;

@@ -53,6 +53,10 @@ SIGNATURES = {
     "smat_causal_scan": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,
                               _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                               _i, _p, _i64, _p]),
+    "smat_causal_scan_noalloc_max_bytes": (_i64, []),
+    "smat_causal_scan_noalloc": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,
+                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                      _i64, _i64, _i, _p]),
     "smat_segment_scan_reverse": (_i, [_p, _p, _i, _i, _i, _i64, _p]),
     "smat_normalise_backward": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i64, _i64, _i64, _i64,
                                      _i64, _i64, _i64, _p]),
