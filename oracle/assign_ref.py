@@ -104,12 +104,21 @@ def ste_weights(s, q: int, N0: int):
 
 
 def dense_point_ste(u, Phi, Psi, Vb, n: int, W, gamma, b, q: int, dim: int, h: int, N0: int,
-                    planted_cols=None, plant_cells=None):
+                    planted_cols=None, plant_cells=None, s_shift=None):
     """The point branch as assign.py:374-446 computes it on its dense path, with
     autograd through Phi, Psi, Vb and the hash (u, W, gamma, b): planted key
     columns get a fixed one-hot row (:305-317), F = Wk^T (Psi (x) Vb) (:436),
-    y_i = Phi_i (Wq F)_i (:439-441).  Returns (nb*h, T - n, p)."""
-    Wk = ste_weights(hash_s(u[:, :n], W, gamma, b, q, h), q, N0)
+    y_i = Phi_i (Wq F)_i (:439-441).  Returns (nb*h, T - n, p).
+
+    ``s_shift`` (optional, (nb*h, T, dim), no gradient) is added to the hash
+    values before the cells are taken: a check uses it to move a value that
+    lies within rounding of a bin edge into the bin another implementation
+    chose; the gradient does not depend on it (the weights' derivative depends
+    on the bin, not on the position inside it)."""
+    s_all = hash_s(u, W, gamma, b, q, h)
+    if s_shift is not None:
+        s_all = s_all + s_shift.detach()
+    Wk = ste_weights(s_all[:, :n], q, N0)
     if planted_cols is not None and len(planted_cols):
         cols = torch.as_tensor(planted_cols, dtype=torch.long)
         cols = cols[cols < n]
@@ -117,7 +126,7 @@ def dense_point_ste(u, Phi, Psi, Vb, n: int, W, gamma, b, q: int, dim: int, h: i
         one[torch.arange(cols.numel()), plant_cells[: cols.numel()]] = 1.0
         Wk = Wk.clone()
         Wk[:, cols] = one
-    Wq = ste_weights(hash_s(u[:, n:], W, gamma, b, q, h), q, N0)
+    Wq = ste_weights(s_all[:, n:], q, N0)
     B, _, r = Psi.shape
     p = Vb.shape[-1]
     PV = torch.einsum("bnr,bnp->bnrp", Psi[:, :n], Vb[:, :n]).reshape(B, n, r * p)

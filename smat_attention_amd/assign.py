@@ -128,6 +128,7 @@ class ContentAssign(nn.Module):
         self.anneal = 1.0
         self.last_soft_q = None
         self.last_hard_k = None
+        self.last_hard_q = None
         self.probe = False
         self.last = None
         self.last_occ = None
@@ -214,6 +215,7 @@ class ContentAssign(nn.Module):
             cq = self._cells(h[:, n:])
             self.aux = None if self.freeze else aux_k + self.aux
         self.last_hard_k = ck.detach()
+        self.last_hard_q = cq.detach()
         return self._read(u, Phi, Psi, Vb, n, ck, cq, dir_override)
 
     # ------------------------------------------------------------ training
@@ -333,6 +335,7 @@ class ContentAssign(nn.Module):
         sparse = bool(getattr(self, "sparse_ops", False)) and self.src != "id"
         ck, idxk, wk, cq, idxq, wq = self._pairs_of(u, n, emb, key_src, key_w, ids, sparse)
         self.last_hard_k = ck.detach()
+        self.last_hard_q = cq.detach()
         P, V, Phi_r = Psi[:, :n], Vb[:, :n], Phi[:, n:]
         dt = P.dtype
         dev = Phi.device

@@ -695,6 +695,25 @@ class SmatDecoder:
     def S(self) -> torch.Tensor:
         return self._S[self._cur]
 
+    def advance(self, Psi_block, Vb_block) -> None:
+        """Take the next ``L`` recent tokens into the running state at once:
+        ``S += sum_t psi_t vb_t^T`` over the block (one Gram launch) and the
+        step counter moves by ``L``, as ``L`` calls of :meth:`step` would leave
+        them.  For resuming decode after a chunked prefill of those tokens
+        (the reference steps through them one by one, attention.py:522-528).
+        ``Psi_block (nb, L, r)``, ``Vb_block (nb, L, p)``."""
+        who = "SmatDecoder.advance"
+        nb, L, r = Psi_block.shape
+        if (nb, r) != (self.nb, self.r) or Vb_block.shape != (nb, L, self.p):
+            raise ValueError(f"{who}: blocks must be ({self.nb}, L, {self.r}) and "
+                             f"({self.nb}, L, {self.p}), got {tuple(Psi_block.shape)} and "
+                             f"{tuple(Vb_block.shape)}")
+        if L == 0:
+            return
+        G = _hip.pool(Psi_block, Vb_block, 0, L, 1)            # one profile: the whole block
+        self._S[self._cur].add_(G[:, 0])
+        self.i += L
+
     def step(self, Phi_t, Psi_t, Vb_t, *, out=None):
         """One token.  ``Phi_t, Psi_t: (nb, r)``, ``Vb_t: (nb, p)``; returns fp32 ``(nb, p-1)``."""
         S_in, S_out = self._S[self._cur], self._S[1 - self._cur]

@@ -332,6 +332,112 @@ def test_training_step_content_hashed(d):
         assert _grel(getattr(m, k).grad.cpu(), pr.grad) < 1e-4, k
 
 
+def _device_bins(s64, cells, q, dim, margin):
+    """Shift that moves each fp64 hash value into the bin the device chose.
+
+    ``s64 (B, L, dim)`` are the oracle's hash values and ``cells (B, L)`` the
+    device's cells on the same inputs.  Where they disagree, every coordinate
+    whose bin differs must lie within ``margin`` of the edge between the two
+    bins (device rounding, not a different hash); the shift puts it just
+    inside the device's bin.  Returns (shift, number of coordinates moved)."""
+    digits = torch.stack([(cells // q ** (dim - 1 - k)) % q for k in range(dim)], -1)
+    lo = s64.floor().long()
+    moved = digits != lo
+    if moved.any():
+        edge = torch.where(digits > lo, digits, digits + 1).double()
+        assert (s64[moved] - edge[moved]).abs().max().item() < margin, \
+            "a cell differs from the oracle away from a bin edge"
+        assert ((digits - lo).abs()[moved] == 1).all()
+    target = torch.where(digits > lo, digits.double() + 1e-9, digits.double() + 1 - 1e-9)
+    shift = torch.where(moved, target - s64, torch.zeros_like(s64))
+    return shift, int(moved.sum())
+
+
+@pytest.mark.parametrize("d", [2, 3])
+def test_training_step_content_hashed_bf16_full_shape(d):
+    """The training configuration itself: B=8, H=12, head_dim 64, T=4096, bf16
+    q, k, v ~ N(0, 1) (k scaled 1/sqrt(64)), the content hash reading k (u = k
+    viewed as (B, T, 768), hashed from its fp32 values as the reference's layer
+    hashes x.float(), model.py:265, 313), dO ~ N(0, 1); forward and backward on
+    the GPU.  Batch element 0 -- all 12 heads, since each head's hash reads every
+    head's k -- against fp64 autograd through the oracle on the same bf16 values:
+
+    * cells equal the oracle's except within 1e-4 of a bin edge (fp32 vs fp64
+      rounding of the hash); there the oracle is given the device's bin, which
+      changes no gradient formula (the straight-through weights' derivative
+      depends on the bin only);
+    * O within 2e-2 absolute (the bf16 bar);
+    * dQ, dK (through the features and the hash), dV within 2e-2
+      norm-relative, the reference's bar for its kernel gradients
+      (tests/test_triton_bwd.py:24-64).  dQ is the loosest: it carries the
+      bf16 rounding of the feature map's product; the reference's own torch
+      path in bf16 (the oracle run on bf16 tensors) is 1.7e-2 from fp64 in dQ
+      at this shape (positional, d = 2, 2 heads), this path about 1.5e-2."""
+    from oracle import assign_ref as RA
+    from smat_attention_amd.assign import ContentAssign
+    B, H, hd, T = 8, 12, 64, 4096
+    spec = build_mask(T, d, chunk=128)
+    n, q, dim = spec.n, spec.q, spec.dim
+    _say("training step bf16 full shape", d, q, spec.N0)
+    gen = torch.Generator().manual_seed(50 + d)
+    bf = torch.bfloat16
+    Q = torch.randn(B * H, T, hd, generator=gen).to(bf)
+    K = (torch.randn(B * H, T, hd, generator=gen) / hd ** 0.5).to(bf)
+    V = torch.randn(B * H, T, hd, generator=gen).to(bf)
+    dO = torch.randn(B * H, T, hd, generator=gen)
+    torch.manual_seed(7)
+    m = ContentAssign(H, H * hd, spec, mode="point")
+    pc = torch.tensor([q ** (dim - l) for l in range(1, dim + 1)])
+
+    def as_u(k, nb):
+        return k.reshape(nb, H, T, hd).transpose(1, 2).reshape(nb, T, H * hd)
+
+    # ---- the GPU step over the whole batch
+    prm = {k: getattr(m, k).detach().double() for k in ("W", "gamma", "b")}
+    m.to(DEV)
+    phi = A.make_phi(hd, hd, device=DEV, dtype=bf, seed=0)
+    xs = [t.to(DEV).requires_grad_(True) for t in (Q, K, V)]
+    Phi, Psi, Vb = A.featurise(*xs, phi)
+    Hs = A.segmented_causal_scan(Phi, Psi, Vb, n, 128)
+    Ylr = m(as_u(xs[1], B).float(), Phi, Psi, Vb, n)
+    Hs = torch.cat([Hs[:, :n], Hs[:, n:] + Ylr], dim=1)
+    o = Hs[..., :-1] / Hs[..., -1:].clamp_min(1e-6)
+    (o * dO.to(DEV)).sum().backward()
+    o1 = o.detach()[:H].cpu()
+    g1 = [x.grad[:H].cpu() for x in xs]
+    ck1, cq1 = m.last_hard_k[:H].cpu(), m.last_hard_q[:H].cpu()
+
+    # ---- batch element 0 in fp64 through the oracle, on the same bf16 values
+    W64 = phi.W.double().cpu()
+    f64 = lambda z: torch.nn.functional.elu(z @ W64.T) + 1.0
+    x0 = [t[:H].double().requires_grad_(True) for t in (Q, K, V)]
+    u0 = as_u(x0[1], 1)
+    s64 = RA.hash_s(u0.detach(), prm["W"], prm["gamma"], prm["b"], q, H)
+    cells64 = torch.zeros(H, T, dtype=torch.long)
+    for k in range(dim):
+        cells64 += s64[..., k].floor().long() * q ** (dim - 1 - k)
+    cols = torch.as_tensor(spec.planted_cols, dtype=torch.long)
+    assert torch.equal(RA.plant(cells64[:, :n], cols, pc)[:, cols], ck1[:, cols])
+    dev_cells = torch.cat([ck1, cq1], 1)
+    dev_cells[:, cols] = cells64[:, cols]           # planted keys carry no hash bin
+    shift, moved = _device_bins(s64, dev_cells, q, dim, margin=1e-4)
+    _say(f"  coordinates at a bin edge given the device's bin: {moved} of {s64.numel()}")
+    Phi0, Psi0, Vb0 = O.featurise(*x0, f64)
+    Hs0 = O.segmented_causal_scan(Phi0, Psi0, Vb0, n, 128)
+    Y0 = RA.dense_point_ste(u0, Phi0, Psi0, Vb0, n, prm["W"], prm["gamma"], prm["b"], q, dim,
+                            H, spec.N0, planted_cols=spec.planted_cols, plant_cells=pc,
+                            s_shift=shift)
+    Hs0 = torch.cat([Hs0[:, :n], Hs0[:, n:] + Y0], dim=1)
+    o0 = Hs0[..., :-1] / Hs0[..., -1:].clamp_min(1e-6)
+    (o0 * dO[:H].double()).sum().backward()
+    e_o = (o1.double() - o0.detach()).abs().max().item()
+    errs = {nm: _nrel(a, b.grad) for nm, a, b in zip(("dQ", "dK", "dV"), g1, x0)}
+    _say(f"  O {e_o:.2e} (abs); " + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+    assert e_o < 2e-2
+    for nm, e in errs.items():
+        assert e < 2e-2, (nm, e)
+
+
 # ---------------------------------------------------------------------------
 # smat_bgemm itself: every product of the backward runs on it
 # ---------------------------------------------------------------------------

@@ -415,6 +415,50 @@ def test_forward_long_prefill_d3_bf16_T524288():
     assert _rel(direct, out) < 1e-5
 
 
+@pytest.mark.parametrize("T,heads", [(32768, 2), (131072, 1)])
+def test_forward_dense_control_d1_bf16(T, heads):
+    """The d = 1 control of the long prefill (B=1, H=8, head_dim=128, bf16, k
+    scaled 1/sqrt(128)): M^(1) = L_T, one profile (N0 = 1: the split-K pool)
+    and one row type (the query reads one U for all T/2 recent rows).  The
+    first heads against the oracle; all heads against the plain causal linear
+    attention on the GPU (one unbroken scan, no pool, incidence or query)."""
+    _say(f"forward T={T} d=1 nb=8 hd=128 bf16")
+    spec = build_mask(T, 1, chunk=128)
+    assert (spec.N0, spec.B, spec.n) == (1, 1, T // 2)
+    Phi, Psi, Vb = _feats(8, T, 128, torch.bfloat16, seed=0, k_scale=128 ** -0.5)
+    Pd, Sd, Wd = Phi.to(DEV), Psi.to(DEV), Vb.to(DEV)
+    out = A.smat_attention(Pd, Sd, Wd, spec)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _check_forward(spec, Phi[:heads], Psi[:heads], Vb[:heads], dt=torch.bfloat16,
+                   label=f"T={T} d=1 heads 0-{heads - 1}")
+    H = A.segmented_causal_scan(Pd, Sd, Wd, 0, 128)
+    plain = H[..., :-1] / H[..., -1:]
+    e = _rel(out, plain)
+    _say(f"  d=1 vs plain causal: rel {e:.2e}")
+    assert e < 1e-4
+
+
+def test_forward_dense_control_d1_bf16_T524288():
+    """d = 1 at T = 524288 (one head, bf16): the fused call equals the staged
+    path and equals plain causal linear attention (an unbroken scan) --
+    properties that hold at full size, where the fp64 oracle would take minutes."""
+    _say("forward T=524288 d=1 nb=1 hd=128 bf16")
+    T = 524288
+    spec = build_mask(T, 1, chunk=128)
+    Phi, Psi, Vb = _feats(1, T, 128, torch.bfloat16, seed=6, k_scale=128 ** -0.5)
+    Pd, Sd, Wd = Phi.to(DEV), Psi.to(DEV), Vb.to(DEV)
+    out = A.smat_attention(Pd, Sd, Wd, spec)
+    staged = A.smat_attention(Pd, Sd, Wd, spec, return_parts=True)[0]
+    H = A.segmented_causal_scan(Pd, Sd, Wd, 0, 128)
+    plain = H[..., :-1] / H[..., -1:]
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    e_s, e_p = _rel(staged, out), _rel(out, plain)
+    _say(f"  staged {e_s:.2e}  plain causal {e_p:.2e}")
+    assert e_s < 1e-5 and e_p < 1e-4
+
+
 def test_exact_non_influence():
     """A landmark payload outside a recent row's mask leaves that row bit-identical
     (the reference's test_smat.py:292-324, on the GPU path)."""
@@ -467,6 +511,78 @@ def test_decode_matches_prefill(dt, T, d):
     else:
         assert (got.double() - ref64).abs().max().item() < 2e-2
     assert dec.cache_words() == 3 * (spec.B + 1) * 32 * 33
+
+
+def test_decode_after_prefill_4096_steps():
+    """The cached-decode configuration: B=16, H=8 (nb = 128), head_dim 128, d = 3,
+    a 65536-token context, then 4096 steps, bf16 q, k, v ~ N(0, 1) (k scaled
+    1/sqrt(128)) from a seeded generator.  The mask is built for the whole
+    69632 tokens (q = 37, B = 1406, n = 34816), so every decoded row lies in
+    it.  The decoder's U comes from the landmark block, the prefilled recent
+    tokens [n, 65536) enter its state in one advance(), then 4096 steps.
+    Every decoded row of every sequence is checked against the same row of
+    one fused prefill over all 69632 tokens (2e-2 absolute: the prefill rounds
+    the in-chunk scores to bf16 as the reference does, the decoder does not),
+    and sequences 0-1 against the fp64 oracle's decoder on the same values
+    (1e-5 relative: the decoder computes in fp32 from the bf16 values)."""
+    nb, hd, T_pre, steps = 128, 128, 65536, 4096
+    T = T_pre + steps
+    _say(f"decode nb={nb} hd={hd} prefill {T_pre} + {steps} steps bf16")
+    spec = build_mask(T, 3, chunk=128)
+    assert (spec.q, spec.B, spec.n) == (37, 1406, 34816)
+    n = spec.n
+    g = torch.Generator(device=DEV).manual_seed(0)
+    bf = torch.bfloat16
+    Q = torch.randn(nb, T, hd, device=DEV, generator=g).to(bf)
+    Kk = (torch.randn(nb, T, hd, device=DEV, generator=g) * hd ** -0.5).to(bf)
+    V = torch.randn(nb, T, hd, device=DEV, generator=g).to(bf)
+    phi = A.make_phi(hd, hd, device=DEV, dtype=bf, seed=0)
+    Phi, Psi, Vb = A.featurise(Q, Kk, V, phi)
+    del Q, Kk, V
+    pre = A.smat_attention(Phi, Psi, Vb, spec)[:, T_pre:]
+    dec = A.SmatDecoder(Psi[:, :n], Vb[:, :n], spec)
+    dec.advance(Psi[:, n:T_pre], Vb[:, n:T_pre])
+    assert dec.i == T_pre - n
+    got = torch.empty(steps, nb, hd, device=DEV)
+    for i in range(steps):
+        t = T_pre + i
+        dec.step(Phi[:, t], Psi[:, t], Vb[:, t], out=got[i])
+    torch.cuda.synchronize()
+    got = got.transpose(0, 1)
+    assert torch.isfinite(got).all()
+    e_pre = (got - pre).abs().max().item()
+    # sequences 0-1 in fp64: U from the landmark block, the prefilled recent
+    # block summed into S, then the oracle's steps
+    P2, S2, V2 = (x[:2].double().cpu() for x in (Phi, Psi, Vb))
+    ref = O.SmatDecoder(S2[:, :n], V2[:, :n], spec)
+    ref.S = S2[:, n:T_pre].transpose(-1, -2) @ V2[:, n:T_pre]
+    ref.i = T_pre - n
+    want = torch.stack([ref.step(P2[:, T_pre + i], S2[:, T_pre + i], V2[:, T_pre + i])
+                        for i in range(steps)], 1)
+    e64 = _rel(got[:2], want)
+    _say(f"  vs prefill rows {e_pre:.2e} (abs); seqs 0-1 vs fp64 {e64:.2e} (rel)")
+    assert e_pre < 2e-2 and e64 < 1e-5
+
+
+def test_decode_advance_equals_steps():
+    """advance() over a block leaves the state and the step counter exactly
+    where stepping through the block token by token does (fp32, small)."""
+    _say("decode advance vs steps")
+    T, d = 4096, 3
+    spec = build_mask(T, d, chunk=128)
+    Phi, Psi, Vb = _feats(3, T, 32, torch.float32, seed=15)
+    Pd, Sd, Wd = (x.to(DEV) for x in (Phi, Psi, Vb))
+    n, L = spec.n, 300
+    a = A.SmatDecoder(Sd[:, :n], Wd[:, :n], spec)
+    b = A.SmatDecoder(Sd[:, :n], Wd[:, :n], spec)
+    a.advance(Sd[:, n:n + L], Wd[:, n:n + L])
+    for t in range(n, n + L):
+        b.step(Pd[:, t], Sd[:, t], Wd[:, t])
+    assert a.i == b.i == L
+    assert _rel(a.S, b.S) < 1e-6
+    oa = torch.stack([a.step(Pd[:, t], Sd[:, t], Wd[:, t]) for t in range(n + L, n + L + 50)], 1)
+    ob = torch.stack([b.step(Pd[:, t], Sd[:, t], Wd[:, t]) for t in range(n + L, n + L + 50)], 1)
+    assert _rel(oa, ob) < 1e-5
 
 
 @pytest.mark.parametrize("nb,hd", [(256, 128), (128, 128), (128, 47), (64, 2), (3, 128)])
