@@ -17,9 +17,12 @@ throughput (tokens/s = B*T / step time), the roofline of the dominant kernel
 (the oracle's restatement of the reference's torch path, on a bounded
 sample, timed on this host), the cached-decode rate and, outside the step,
 the time of one content-hashed training step (forward and backward, B=8,
-H=12, head_dim 64, T=4096, bf16, d = 2 and 3).
+H=12, head_dim 64, T=4096, bf16, d = 2 and 3), the long prefill at every
+T in {32768, 131072, 524288} with d = 3 and the d = 1 control, and cached
+decode over 4096 steps after a 65536-token context (B=16, H=8).
 
-    python bench.py [--steps K] [--warmup W] [--T 131072] [--no-cpu] [--no-decode] [--no-train]
+    python bench.py [--steps K] [--warmup W] [--T 131072] [--no-cpu] [--no-decode]
+                    [--no-train] [--no-rows]
 """
 from __future__ import annotations
 
@@ -81,7 +84,10 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the training-step timing")
-    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--decode-steps", type=int, default=4096)
+    ap.add_argument("--no-rows", action="store_true",
+                    help="skip the per-T / d = 1 prefill rows")
+    ap.add_argument("--row-steps", type=int, default=10)
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first copy a 1 GiB fp32 buffer 3 times: the known-size kernel "
@@ -116,6 +122,71 @@ def to_gpu_padded(Phi, Psi, Vb, dev):
     buf = torch.zeros(*Vb.shape[:-1], pad, device=dev, dtype=Vb.dtype)
     buf[..., :p] = Vb.to(dev)
     return Phi.to(dev), Psi.to(dev), buf[..., :p]
+
+
+def gpu_inputs(nb, T, hd, seed):
+    """Seeded draw on the GPU, featurised by the HIP feature map in bf16:
+    q, k, v ~ N(0, 1), k scaled by 1/sqrt(hd); Vb rows padded to 16 bytes."""
+    import torch
+    from smat_attention_amd import attention as A
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    bf = torch.bfloat16
+    Q = torch.randn(nb, T, hd, device=dev, generator=g).to(bf)
+    K = (torch.randn(nb, T, hd, device=dev, generator=g) * hd ** -0.5).to(bf)
+    V = torch.randn(nb, T, hd, device=dev, generator=g).to(bf)
+    return A.featurise(Q, K, V, A.make_phi(hd, hd, device=dev, dtype=bf, seed=0))
+
+
+def time_forward(spec, Phi, Psi, Vb, steps, warmup):
+    """ms per forward (one library call, inputs resident), host clock between
+    two device synchronisations."""
+    import torch
+    from smat_attention_amd import attention as A
+    nb, T, r = Phi.shape
+    ws = torch.empty(A._hip.forward_workspace_bytes(nb, T, spec.n, spec.N0, spec.B, spec.n_P,
+                                                    128, r, Vb.shape[-1]) + 256,
+                     device=Phi.device, dtype=torch.uint8)
+    for _ in range(warmup):
+        A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    assert torch.isfinite(out).all()
+    return ms
+
+
+def prefill_rows(args):
+    """The long prefill at T in {32768, 131072, 524288}, d = 3 and the d = 1
+    control (B=1, H=8, head_dim 128, bf16): ms, tokens/s, the fraction of the
+    dense-bf16 MFMA peak on useful FLOPs, and the fraction of the schedule's
+    roofline max(t_MFMA, t_HBM) on its compulsory bytes."""
+    import torch
+    from smat_attention_amd import attention as A
+    from smat_attention_amd.mask import build_mask, estimate_cost
+    nb, hd = args.heads, args.head_dim
+    rows = {}
+    for T in (32768, 131072, 524288):
+        Phi, Psi, Vb = gpu_inputs(nb, T, hd, seed=T)
+        for d in (3, 1):
+            spec = A.to_device(build_mask(T, d, chunk=128), Phi.device)
+            ms = time_forward(spec, Phi, Psi, Vb, args.row_steps, 2)
+            est = estimate_cost(T, d, hd, hd, chunk=128)
+            flops = nb * est["mfma_flops"]
+            cbytes = nb * (est["inputs_bf16"] + est["output_fp32"])
+            t_roof = max(flops / (BF16_PEAK_TFLOPS * 1e12), cbytes / (HBM_PEAK_GBS * 1e9))
+            rows[f"T{T}_d{d}"] = {
+                "ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                "mfma_frac_of_bf16_peak": round(flops / (ms * 1e-3) / (BF16_PEAK_TFLOPS * 1e12), 4),
+                "schedule_roofline_frac": round(t_roof / (ms * 1e-3), 4),
+                "q": spec.q, "B_types": spec.B, "nnz_C": spec.I_prof}
+            log(f"[bench] prefill T={T} d={d}: {ms:.3f} ms, {T / ms / 1e3:.2f} M tok/s")
+        del Phi, Psi, Vb
+        torch.cuda.empty_cache()
+    return rows
 
 
 class Events:
@@ -259,95 +330,174 @@ def compulsory_bytes(nb, T, r, p, eb_in=2, eb_out=4):
     return nb * (T * (2 * r + p) * eb_in + T * (p - 1) * eb_out)
 
 
+def host_cpu_info():
+    """CPU model, logical CPUs and physical cores visible to this process."""
+    aff = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else []
+    model, cores, cur = "", set(), {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f.read().splitlines() + [""]:
+                if not line.strip():
+                    if cur and (not aff or int(cur.get("processor", -1)) in aff):
+                        cores.add((cur.get("physical id", "0"), cur.get("core id",
+                                                                     cur.get("processor"))))
+                        model = model or cur.get("model name", "")
+                    cur = {}
+                    continue
+                k, _, v = line.partition(":")
+                cur[k.strip()] = v.strip()
+    except OSError:
+        pass
+    return {"cpu_model": model, "host_cpus": os.cpu_count(),
+            "logical_cpus_visible": len(aff) or os.cpu_count(),
+            "physical_cores_visible": len(cores) or None}
+
+
+def _median_time(fn, runs=3):
+    fn()                                            # one warm-up
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
 def cpu_baseline(args, spec, Phi, Psi, Vb):
-    """The oracle's restatement of the reference's torch path, timed on the host:
-    median of 3 runs after one warm-up, on ``cpu_heads`` of the heads."""
+    """The oracle's restatement of the reference's torch path, timed on this
+    host on bounded samples of each workload (median of 3 runs after one
+    warm-up, as the reference's harness times, analysis/bench_prefill.py:81-102):
+
+    * the long prefill at T = 131072 and T = 32768 (the first 32768 tokens of
+      the same draw), d = 3 and d = 1, on ``cpu_heads`` of the heads, scaled to
+      all heads (heads are independent);
+    * cached decode: 8 of the 128 sequences, U from the 34816-token landmark
+      block and the state of the rest of the 65536-token context (not timed),
+      then 64 steps timed, scaled to 128 sequences;
+    * the CPU plumbing configuration in full (nb = 4, T = 1024, d = 2, fp32).
+    """
     import torch
     import oracle.schedule as O
-    threads = max(1, min(args.cpu_threads, os.cpu_count() or 1))
+    from smat_attention_amd.mask import build_mask
+    info = host_cpu_info()
+    threads = max(1, min(args.cpu_threads, info["physical_cores_visible"]
+                         or info["logical_cpus_visible"] or 1))
     torch.set_num_threads(threads)
-    h = args.cpu_heads
-    P, S, W = Phi[:h].contiguous(), Psi[:h].contiguous(), Vb[:h].contiguous()
-    O.smat_attention(P, S, W, spec)
-    ts = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        O.smat_attention(P, S, W, spec)
-        ts.append(time.perf_counter() - t0)
-    t = statistics.median(ts)
-    t_full = t * (Phi.shape[0] / h)              # heads are independent
-    return {"value": round(args.T / t_full, 1), "unit": "tokens/s", "cores": threads,
+    nb, h = Phi.shape[0], args.cpu_heads
+    rows = {}
+    for T in dict.fromkeys((args.T, 32768)):
+        P, S, W = (x[:h, :T].contiguous() for x in (Phi, Psi, Vb))
+        for d in (3, 1):
+            sp = spec if (T, d) == (args.T, args.d) else build_mask(T, d, chunk=128)
+            t = _median_time(lambda: O.smat_attention(P, S, W, sp))
+            t_all = t * nb / h
+            rows[f"T{T}_d{d}"] = {"tokens_per_s": round(T / t_all, 1),
+                                  "s_per_sample": round(t, 3)}
+            log(f"[bench] cpu T={T} d={d}: {t:.3f} s for {h} heads")
+    # decode: 8 sequences, 64 steps
+    ns, hd = 8, args.head_dim
+    dspec = build_mask(65536 + 4096, 3, chunk=128)
+    n = dspec.n
+    g = torch.Generator().manual_seed(3)
+    feat = lambda *sh: (torch.nn.functional.elu(torch.randn(*sh, generator=g)) + 1
+                        ).to(torch.bfloat16)
+    vb = lambda *sh: torch.cat([torch.randn(*sh, hd, generator=g), torch.ones(*sh, 1)],
+                               -1).to(torch.bfloat16)
+    dec = O.SmatDecoder(feat(ns, n, hd), vb(ns, n), dspec)
+    Pr, Vr = feat(ns, 65536 - n, hd), vb(ns, 65536 - n)
+    dec.S = Pr.float().transpose(-1, -2) @ Vr.float()
+    dec.i = 65536 - n
+    steps = 64
+    ph, ps, vv = feat(steps, ns, hd), feat(steps, ns, hd), vb(steps, ns)
+
+    def run_steps():
+        for i in range(steps):
+            dec.step(ph[i], ps[i], vv[i])
+    t = _median_time(run_steps)
+    rows["decode"] = {"us_per_step": round(t / steps * 1e6 * 128 / ns, 1),
+                      "sample": f"{ns} of 128 sequences, {steps} steps, scaled x{128 // ns}"}
+    log(f"[bench] cpu decode: {rows['decode']}")
+    # CPU plumbing configuration in full
+    sp1 = build_mask(1024, 2, chunk=128)
+    Q1, K1, V1 = O.seeded_qkv(4, 1024, 64, 64, seed=0)
+    P1, S1, W1 = O.featurise(Q1, K1, V1, O.make_phi(64, 64, seed=0))
+    t = _median_time(lambda: O.smat_attention(P1, S1, W1, sp1))
+    rows["plumbing_T1024_d2_fp32"] = {"ms": round(t * 1e3, 2),
+                                      "tokens_per_s": round(4 * 1024 / t, 1)}
+    main_row = rows[f"T{args.T}_d{args.d}"]
+    return {"value": main_row["tokens_per_s"], "unit": "tokens/s", "cores": threads,
             "kind": "port",
-            "sample": (f"{h} of {Phi.shape[0]} heads at T={args.T}, d={args.d}, bf16 inputs "
-                       f"(reference torch path restated, oracle/schedule.py); median of 3 "
-                       f"after 1 warm-up = {t:.3f} s, scaled x{Phi.shape[0] // h} to all heads"),
-            "host_cpus": os.cpu_count()}
+            "sample": (f"{h} of {nb} heads at T={args.T}, d={args.d}, bf16 inputs (reference "
+                       f"torch path restated, oracle/schedule.py); median of 3 after 1 "
+                       f"warm-up = {main_row['s_per_sample']} s, scaled x{nb // h} to all heads"),
+            **info, "threads": threads, "rows": rows}
 
 
 def decode_bench(args):
-    """Cached decode at B=16, H=8 (nb=128), head_dim 128, d=3, T=65536 prefill."""
+    """Cached decode at B=16, H=8 (nb = 128), head_dim 128, d = 3: a 65536-token
+    context, then ``decode_steps`` (4096) steps, bf16 q, k, v ~ N(0, 1) drawn on
+    the GPU and featurised there.  The mask covers all 69632 tokens (q = 37,
+    B = 1406, n = 34816).  U is built from the landmark block and the
+    context's recent tokens enter the state in one advance(); every step has
+    its own inputs.  The steps are captured once into a HIP graph and replayed
+    (no host launch cost between steps); the same steps launched eagerly are
+    timed on a second decoder."""
     import torch
     from smat_attention_amd import attention as A
     from smat_attention_amd.mask import build_mask
     dev = torch.device("cuda:0")
     nb, hd, T_pre = 128, 128, 65536
     T_total = T_pre + 4096
-    spec = build_mask(T_total, 3, chunk=128)
-    r, p = hd, hd + 1
-    gen = torch.Generator(device="cpu").manual_seed(0)
-    # the landmark block is what U is built from; recent-step inputs are fresh
-    n = spec.n
-    Psi = (torch.nn.functional.elu(torch.randn(nb, n, r, generator=gen) * 0.3) + 1
-           ).to(torch.bfloat16).to(dev)
-    Vb = torch.cat([torch.randn(nb, n, hd, generator=gen), torch.ones(nb, n, 1)], -1
-                   ).to(torch.bfloat16).to(dev)
-    dec = A.SmatDecoder(Psi, Vb, spec)
-    del Psi, Vb
-    steps = args.decode_steps
-    ph = (torch.nn.functional.elu(torch.randn(steps, nb, r, generator=gen)) + 1
-          ).to(torch.bfloat16).to(dev)
-    ps = (torch.nn.functional.elu(torch.randn(steps, nb, r, generator=gen)) + 1
-          ).to(torch.bfloat16).to(dev)
-    vb = torch.cat([torch.randn(steps, nb, hd, generator=gen), torch.ones(steps, nb, 1)], -1
-                   ).to(torch.bfloat16).to(dev)
-    out = torch.empty(nb, p - 1, device=dev)
-    for i in range(8):
-        dec.step(ph[i], ps[i], vb[i], out=out)
-    torch.cuda.synchronize()
+    steps = min(args.decode_steps, 4096)
+    steps -= steps % 2           # an even count returns the state to its first buffer
+    spec = A.to_device(build_mask(T_total, 3, chunk=128), dev)
+    r, p, n = hd, hd + 1, spec.n
+    Phi, Psi, Vb = gpu_inputs(nb, T_total, hd, seed=7)
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = torch.empty(nb, p - 1, device=dev)
+
+    def decoder():
+        dec = A.SmatDecoder(Psi[:, :n], Vb[:, :n], spec)
+        dec.advance(Psi[:, n:T_pre], Vb[:, n:T_pre])
+        return dec
+
+    dec = decoder()
+    eager = min(steps, 512)
+    for i in range(8):
+        dec.step(Phi[:, T_pre + i], Psi[:, T_pre + i], Vb[:, T_pre + i], out=out)
+    torch.cuda.synchronize()
     e0.record(s)
-    for i in range(steps):
-        dec.step(ph[i], ps[i], vb[i], out=out)
+    for i in range(eager):
+        dec.step(Phi[:, T_pre + i], Psi[:, T_pre + i], Vb[:, T_pre + i], out=out)
     e1.record(s)
     e1.synchronize()
-    us_eager = e0.elapsed_time(e1) / steps * 1e3
-    # the same steps captured once into a HIP graph and replayed: no host
-    # launch cost between steps (an even step count returns the double-buffered
-    # state to the buffer it started in)
-    gsteps = steps - (steps % 2)
+    us_eager = e0.elapsed_time(e1) / eager * 1e3
+    del dec
+    dec = decoder()
     graph = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
     cap.wait_stream(s)
     with torch.cuda.stream(cap):
         with torch.cuda.graph(graph, stream=cap):
-            for i in range(gsteps):
-                dec.step(ph[i], ps[i], vb[i], out=out)
+            for i in range(steps):
+                dec.step(Phi[:, T_pre + i], Psi[:, T_pre + i], Vb[:, T_pre + i], out=out)
     s.wait_stream(cap)
-    graph.replay()
+    graph.replay()                  # the 4096 decode steps after the context
     torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
     e0.record(s)
-    graph.replay()
+    graph.replay()                  # the same work again (state carries on), timed
     e1.record(s)
     e1.synchronize()
-    us = e0.elapsed_time(e1) / gsteps * 1e3
+    us = e0.elapsed_time(e1) / steps * 1e3
     # per step and sequence: U[type] read, S read, S write (r*p fp32 each), plus io
     step_bytes = nb * (3 * r * p * 4 + (2 * r + p) * 2 + (p - 1) * 4)
     return {"us_per_step": round(us, 2), "GBs": round(step_bytes / (us * 1e-6) / 1e9, 1),
             "frac_hbm": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "us_per_step_eager": round(us_eager, 2),
-            "config": f"nb=128 (B=16,H=8), r=128, p=129, d=3, prefill {T_pre}, "
-                      f"B_types={spec.B}, {gsteps} steps replayed from one HIP graph",
+            "config": f"nb=128 (B=16,H=8), r=128, p=129, d=3, context {T_pre} then {steps} "
+                      f"steps, B_types={spec.B}, replayed from one HIP graph",
             "bytes_per_step": step_bytes, "U_cache_GB": round(dec.U.numel() * 4 / 1e9, 2)}
 
 
@@ -437,19 +587,21 @@ def main():
                  "compulsory_bytes": cb},
         "kernels_us": {k: round(v["us"], 1) for k, v in rows.items()},
     }
+    if dom == "incidence":
+        # priced against HBM, but limited on chip: fp32 vector adds and LDS reads
+        result["roofline"]["limited_by"] = "VALU issue and LDS reads (rocprofv3 counters)"
     result["featurise"] = featurise_bench(nb, T, hd, args.kernel_reps)
     log(f"[bench] featurise {result['featurise']}")
+    del ws, out, Phi, Psi, Vb
+    torch.cuda.empty_cache()
+    if not args.no_rows:
+        result["prefill_rows"] = prefill_rows(args)
     if not args.no_train:
-        del ws, out
-        torch.cuda.empty_cache()
         result["train_step"] = {f"d{d}": train_step_bench(d, max(3, args.kernel_reps // 2))
                                 for d in (2, 3)}
         log(f"[bench] train step {result['train_step']}")
+    torch.cuda.empty_cache()
     if not args.no_decode:
-        del Phi, Psi, Vb
-        if args.no_train:
-            del ws, out
-        torch.cuda.empty_cache()
         result["decode"] = decode_bench(args)
         log(f"[bench] decode {result['decode']}")
     if not args.no_cpu:
