@@ -88,6 +88,8 @@ def parse():
     ap.add_argument("--no-rows", action="store_true",
                     help="skip the per-T / d = 1 prefill rows")
     ap.add_argument("--row-steps", type=int, default=10)
+    ap.add_argument("--clock-warmup", type=float, default=1.0,
+                    help="seconds of untimed forward calls before the warm-up steps")
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first copy a 1 GiB fp32 buffer 3 times: the known-size kernel "
@@ -173,7 +175,7 @@ def prefill_rows(args):
         Phi, Psi, Vb = gpu_inputs(nb, T, hd, seed=T)
         for d in (3, 1):
             spec = A.to_device(build_mask(T, d, chunk=128), Phi.device)
-            ms = time_forward(spec, Phi, Psi, Vb, args.row_steps, 2)
+            ms = time_forward(spec, Phi, Psi, Vb, args.row_steps, 5)
             est = estimate_cost(T, d, hd, hd, chunk=128)
             flops = nb * est["mfma_flops"]
             cbytes = nb * (est["inputs_bf16"] + est["output_fp32"])
@@ -535,10 +537,16 @@ def main():
                                                     128, r, p) + 256,
                      device=dev, dtype=torch.uint8)
     out = None
+    # bring the GPU's clocks up to their steady state before anything is timed:
+    # about a second of forward calls (untimed), then the W warm-up steps
+    t_warm = time.perf_counter()
+    while time.perf_counter() - t_warm < args.clock_warmup:
+        A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         out = A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
     torch.cuda.synchronize()
-    log(f"[bench] warmup done ({args.warmup} steps)")
+    log(f"[bench] warmup done ({args.clock_warmup:.1f} s of clock warm-up, {args.warmup} steps)")
     t0 = time.perf_counter()
     for _ in range(args.steps):
         out = A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
