@@ -39,6 +39,7 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+VALU_F32_ADD_PEAK_T = 39.32    # fp32 vector adds, 10^12/s: 1024 SIMDs x 16 lanes x 2.4 GHz
 
 # HBM bytes per launch of a stage on a workload, measured with two rocprofv3
 # counter passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --copy-probe` and scaled by
@@ -47,7 +48,7 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 # holds the sha256 prefix of the kernel source it was measured on, and is reported
 # only while that source is unchanged.
 MEASURED_TRAFFIC = {
-    ("incidence", 131072, 3, 8, 128): ("csrc/incidence.hip", "1f89781205bf2f16", 1_799_420_718),
+    ("incidence", 131072, 3, 8, 128): ("csrc/incidence.hip", "38ef05f6a93ab9df", 1_799_270_400),
 }
 
 
@@ -214,40 +215,58 @@ class Events:
 
 def kernel_table(spec, Phi, Psi, Vb, reps):
     """Average duration and algorithmic traffic/work of each stage of the fused
-    forward, timed with events on torch's current stream (the kernels' stream):
-    pool, incidence, type-major query, and the fused causal pass (chunk-group
-    Gram prepass + group scan + the scan kernel that also adds Y, normalises
-    and writes the output)."""
+    forward: pool, incidence, type-major query, and the fused causal pass
+    (chunk-group Gram prepass + group scan + the scan kernel that also adds Y,
+    normalises and writes the output).  The stages run in the forward's order,
+    each bracketed by events on torch's current stream (the kernels' stream),
+    so every stage meets the caches as the forward leaves them (F just written
+    by the pool, U just written by the incidence)."""
     import torch
     from smat_attention_amd import attention as A
     from smat_attention_amd.kernels import hip_fwd as K
-    ev = Events(torch)
     nb, T, r = Phi.shape
     p = Vb.shape[-1]
     n, C, N0, B, T_R = spec.n, 128, spec.N0, spec.B, spec.T_R
     eb = Phi.element_size()
     rp4 = r * p * 4
-    F = K.pool(Psi, Vb, spec.n_P, n, N0)
-    inc = lambda: A.apply_incidence(F, spec)
-    U = inc()
-    qry = lambda: K.query(Phi[:, n:], U)
-    Y = qry()
     out = torch.empty(nb, T, p - 1, device=Phi.device)
-    rows = {}
+    names = ("pool", "incidence", "query", "causal_scan")
+    s = torch.cuda.current_stream()
+
+    def one(ev):
+        ev[0].record(s)
+        F = K.pool(Psi, Vb, spec.n_P, n, N0)
+        ev[1].record(s)
+        U = A.apply_incidence(F, spec)
+        ev[2].record(s)
+        Y = K.query(Phi[:, n:], U)
+        ev[3].record(s)
+        K.causal_scan(Phi, Psi, Vb, n, C, Y=Y, out=out)
+        ev[4].record(s)
+
+    mk = lambda: [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+    one(mk())                                     # allocations settle
+    torch.cuda.synchronize()
+    evs = [mk() for _ in range(reps)]
+    for ev in evs:
+        one(ev)
+    torch.cuda.synchronize()
+    us = {k: statistics.fmean(ev[i].elapsed_time(ev[i + 1]) * 1e3 for ev in evs)
+          for i, k in enumerate(names)}
     # algorithmic bytes: each operand read once and each result written once
-    rows["pool"] = dict(us=ev.time(lambda: K.pool(Psi, Vb, spec.n_P, n, N0), reps),
-                        bytes=nb * ((n - spec.n_P) * (r + p) * eb + N0 * rp4),
-                        flops=2 * nb * (n - spec.n_P) * r * p)
-    rows["incidence"] = dict(us=ev.time(inc, reps),
-                             bytes=nb * (N0 + B) * rp4, flops=nb * spec.I_prof * r * p)
-    rows["query"] = dict(us=ev.time(qry, reps),
-                         bytes=nb * (B * rp4 + T_R * r * eb + T_R * p * 4),
-                         flops=2 * nb * T_R * r * p)
-    rows["causal_scan"] = dict(
-        us=ev.time(lambda: K.causal_scan(Phi, Psi, Vb, n, C, Y=Y, out=out), reps),
-        bytes=nb * (T * (2 * r + p) * eb + T_R * p * 4 + T * (p - 1) * 4),
-        flops=2 * nb * (T * (C + 1) / 2 * (r + p) + 2 * T * r * p))
-    for k, v in rows.items():
+    rows = {
+        "pool": dict(us=us["pool"], bytes=nb * ((n - spec.n_P) * (r + p) * eb + N0 * rp4),
+                     flops=2 * nb * (n - spec.n_P) * r * p),
+        "incidence": dict(us=us["incidence"], bytes=nb * (N0 + B) * rp4,
+                          flops=nb * spec.I_prof * r * p),
+        "query": dict(us=us["query"], bytes=nb * (B * rp4 + T_R * r * eb + T_R * p * 4),
+                      flops=2 * nb * T_R * r * p),
+        "causal_scan": dict(
+            us=us["causal_scan"],
+            bytes=nb * (T * (2 * r + p) * eb + T_R * p * 4 + T * (p - 1) * 4),
+            flops=2 * nb * (T * (C + 1) / 2 * (r + p) + 2 * T * r * p)),
+    }
+    for v in rows.values():
         v["GBs"] = v["bytes"] / (v["us"] * 1e-6) / 1e9
         v["TFLOPs"] = v["flops"] / (v["us"] * 1e-6) / 1e12
     return rows
@@ -598,6 +617,14 @@ def main():
     if dom == "incidence":
         # priced against HBM, but limited on chip: fp32 vector adds and LDS reads
         result["roofline"]["limited_by"] = "VALU issue and LDS reads (rocprofv3 counters)"
+        # the same launch against the vector ALUs' fp32 add rate: 256 CUs x 4 SIMDs
+        # x 16 lanes per clock at 2.4 GHz (one wave64 add per SIMD per 4 clocks)
+        adds = drow["flops"]
+        result["roofline"]["valu"] = {
+            "adds_per_launch": int(adds),
+            "achieved_Tadd_s": round(adds / (drow["us"] * 1e-6) / 1e12, 2),
+            "peak_Tadd_s": VALU_F32_ADD_PEAK_T,
+            "frac": round(adds / (drow["us"] * 1e-6) / 1e12 / VALU_F32_ADD_PEAK_T, 4)}
     result["featurise"] = featurise_bench(nb, T, hd, args.kernel_reps)
     log(f"[bench] featurise {result['featurise']}")
     del ws, out, Phi, Psi, Vb
