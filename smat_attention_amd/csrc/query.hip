@@ -242,6 +242,12 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
     const int h = (int)(item - b * B);
     const int cnt = (T_R - h + B - 1) / B;
     const int c = 16 * w + r16;
+    // Lane group g takes the k-slots of feature group pg of each 32: 0, 2, 1, 3
+    // for g = 0..3.  A 4-byte LDS read is served 32 lanes at a time, and U_h
+    // rows 16 apart (rows of 129 floats) fall on disjoint banks where rows 8
+    // apart overlap.  U_h^T and Phi^T agree on the order, so the product is
+    // unchanged.
+    const int pg = (g >> 1) | ((g & 1) << 1);
     f32x4 acc[kMT];
 #pragma unroll
     for (int t = 0; t < kMT; ++t) acc[t] = zero4();
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
       Frag ah, al;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float uv = c < kP ? us[(32 * kb + 8 * g + e) * kP + c] : 0.f;
+        const float uv = c < kP ? us[(32 * kb + 8 * pg + e) * kP + c] : 0.f;
         In hh, ll;
         split2<In>(uv, hh, ll);
         ah[e] = hh;
@@ -259,7 +265,7 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
 #pragma unroll
       for (int t = 0; t < kMT; ++t) {
         const int row = 16 * t + r16;
-        const Frag pb = *reinterpret_cast<const Frag*>(ps + row * 16 + ((4 * kb + g) ^ (row & 15)));
+        const Frag pb = *reinterpret_cast<const Frag*>(ps + row * 16 + ((4 * kb + pg) ^ (row & 15)));
         acc[t] = mma(acc[t], ah, pb);
         acc[t] = mma(acc[t], al, pb);
       }

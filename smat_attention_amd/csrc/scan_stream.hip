@@ -29,13 +29,21 @@
 //     lane i receives element (i & 3) of the 8 bytes addressed by lane
 //     4j + (i >> 2) as its element j.
 //
-// LDS layout.  Phi and Psi tiles are 64 rows of 256 bytes (sixteen 16-byte
-// chunks); chunk k of row t is stored at slot k ^ swz16(t), which spreads
-// both the sixteen rows of a row-wise fragment read and the four rows x 32
-// bytes of a transposing read over distinct bank groups.  Vb tiles are 64
-// rows of 288 bytes (18 chunks, columns 0..143), unswizzled: consecutive rows
-// are 32 bytes apart in bank space already.  The score share is 64 rows of
-// 128 bytes with chunk k of row t at k ^ swz8(t).
+// LDS layout.  The LDS has 64 banks of 4 bytes.  A 16-byte read is served
+// in four phases of 16 lanes: lanes 32h + 4j .. 32h + 4j + 3 go in phase
+// (h, parity of j) for j = 0..7.  An 8-byte read, transposing or not, is
+// served in two phases of 32 consecutive lanes.  A phase is conflict-free
+// when its lanes' bytes fall in distinct banks (lanes reading the same
+// address share the access).  Phi, Psi and Vb columns 0..127 are tiles of
+// 64 rows of 256 bytes (sixteen 16-byte chunks); chunk k of row t is stored
+// at slot k ^ swz16(t).  That one XOR satisfies all three reads of a tile: a
+// row-wise 16-byte fragment read (16 rows, chunk 4 kk + lane/16), a
+// row-wise 8-byte read (16 rows x 2 halves), and a transposing read (8 rows
+// x 2 chunks x 2 halves).  Vb columns 128..135 (the normaliser column and
+// padding) are a separate tile of 64 rows of 16 bytes.  The score share is
+// 64 rows of 128 bytes with chunk k of row t at k ^ swz8(t).  The normaliser
+// partials are 64 rows of 32 bytes whose two halves swap in rows 8..15 of
+// every 16, so a phase's 16 rows cover the 256 bytes of the banks once.
 #include <stdlib.h>
 
 #include <type_traits>
@@ -47,20 +55,26 @@ namespace smat {
 namespace ss {
 constexpr int kThreads = 512;
 constexpr int kStep = 64;                      // tokens per step
-constexpr int kRowChunks = 16;                 // 16-byte chunks per Phi/Psi row
-constexpr int kVbChunks = 18;                  // per Vb row in LDS (144 columns)
+constexpr int kRowChunks = 16;                 // 16-byte chunks per Phi/Psi/Vb row
 constexpr int kTileChunks = kStep * kRowChunks;    // 1024
-constexpr int kVbTileChunks = kStep * kVbChunks;   // 1152
+constexpr int kVbTileChunks = kTileChunks + kStep; // + columns 128..135, one chunk a row
 constexpr int kPhiLoads = kTileChunks / 64;        // wave-wide DMA loads per tile: 16
-constexpr int kVbLoads = kVbTileChunks / 64;       // 18
-constexpr int kLoads = 2 * kPhiLoads + kVbLoads;   // 50 per step, over eight waves
+constexpr int kVbLoads = kVbTileChunks / 64;       // 17
+constexpr int kLoads = 2 * kPhiLoads + kVbLoads;   // 49 per step, over eight waves
 }  // namespace ss
 
 #define SMAT_LDS __attribute__((address_space(3)))
 typedef short short4v __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ int swz16(int t) { return ((t & 7) << 1) | ((t >> 3) & 1); }
+__device__ __forceinline__ int swz16(int t) {
+  return (((t & 7) << 1) | ((t >> 3) & 1)) ^ (t & 8);
+}
 __device__ __forceinline__ int swz8(int t) { return (t >> 1) & 7; }
+// Float index of wave w's normaliser partial of row t: 8 floats a row, the two
+// 4-float halves swapped in rows 8..15 of every 16.
+__device__ __forceinline__ int norm_slot(int t, int w) {
+  return t * 8 + 4 * ((w >> 2) ^ ((t >> 3) & 1)) + (w & 3);
+}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -121,26 +135,30 @@ __device__ __forceinline__ typename Traits<In>::frag psi_tr(const uint4* tile, i
 
 // Fragment of Vb along tokens (column 16*ct + lane%16, k-slots = tokens
 // 32*ks + 8*grp + j): the B operand of the state update and the A operand
-// (Vb^T) of the within-step product.
+// (Vb^T) of the within-step product.  Column tiles 0..7 are read like Psi's;
+// tile 8 (columns 128..143) comes from the 16-byte rows of columns 128..135,
+// and its lanes 8..15 repeat columns 128..135 in place of 136..143, which
+// no caller keeps.
 template <typename In>
 __device__ __forceinline__ typename Traits<In>::frag vb_tr(const uint4* tile, int ct, int ks,
                                                            int lane) {
+  if (ct < 8) return psi_tr<In>(tile, ct, ks, lane);
   const int r16 = lane & 15, g = lane >> 4;
   typename Traits<In>::half_frag h2[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int row = 32 * ks + 8 * g + 4 * h + (r16 >> 2);
-    const char* p = reinterpret_cast<const char*>(tile) + row * (ss::kVbChunks * 16) +
-                    (16 * ct + 4 * (r16 & 3)) * 2;
+    const char* p = reinterpret_cast<const char*>(tile + ss::kTileChunks + row) + 8 * (r16 & 1);
     h2[h] = tr_read<In>(p);
   }
   return join<In>(h2[0], h2[1]);
 }
 
 // The DMA of one step's Phi, Psi and Vb rows [ts, ts + 64) into one buffer.
-// Load I of the 50 goes to wave I % 8 as its slot u = I / 8: slots 0-1 are
-// Phi's loads 0-15, slots 2-3 Psi's, slots 4-6 Vb's 18 (waves 0 and 1 issue
-// seven, the others six).  Each load moves 64 x 16 bytes to 1 KB of
+// Load I of the 49 goes to wave I % 8 as its slot u = I / 8: slots 0-1 are
+// Phi's loads 0-15, slots 2-3 Psi's, slots 4-5 Vb's columns 0..127, and slot
+// 6 (wave 0 only) Vb's columns 128..135, lane = row (wave 0 issues seven
+// loads, the others six).  Each load moves 64 x 16 bytes to 1 KB of
 // consecutive LDS; which global chunk a lane fetches implements the swizzle.
 // That choice does not depend on the step, so a lane's byte offset from the
 // step's first row is computed once per slot (dma_offsets); a step adds it
@@ -155,19 +173,13 @@ __device__ __forceinline__ void dma_offsets(DmaOffsets& d, const ScanArgs& a, in
   for (int u = 0; u < 7; ++u) {
     const int I = w + 8 * u;
     int64_t e = 0;                                   // element offset from row ts
-    if (u < 4) {
+    if (u < 6) {
       const int li = I & 15;
       const int row = 4 * li + (lane >> 4);
       const int k = (lane & 15) ^ swz16(row);
-      e = (int64_t)row * (u < 2 ? a.q_st : a.k_st) + 8 * k;
+      e = (int64_t)row * (u < 2 ? a.q_st : u < 4 ? a.k_st : a.v_st) + 8 * k;
     } else if (I < ss::kLoads) {
-      const int L = 64 * (I - 2 * ss::kPhiLoads) + lane;
-      const int row = L / ss::kVbChunks;
-      const int k = L - row * ss::kVbChunks;
-      // chunks past the row (columns >= row stride) carry no data the
-      // kernel keeps; read the row's first chunk instead of the next row
-      const int col = 8 * k + 8 <= a.v_st ? 8 * k : 0;
-      e = (int64_t)row * a.v_st + col;
+      e = (int64_t)lane * a.v_st + 128;              // columns 128..135 of row = lane
     }
     d.off[u] = (uint32_t)(e * (int64_t)sizeof(In));
   }
@@ -260,7 +272,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   __shared__ __attribute__((aligned(16))) uint4 psi1[kTileChunks];
   __shared__ __attribute__((aligned(16))) uint4 vb1[kVbTileChunks];
   __shared__ __attribute__((aligned(16))) uint4 share[kStep * 8];
-  // normaliser partials: normp[t][w] = wave w's share of H[t][p-1]
+  // normaliser partials: wave w's share of H[t][p-1] at normp[norm_slot(t, w)]
   __shared__ __attribute__((aligned(16))) float normp[kStep * 8];
 
   const int grp = blockIdx.x;
@@ -334,7 +346,8 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     if (s + 1 < nsteps) {
       issue_step<In>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib, vbb,
                      ts + kStep, a, w, dmo);
-      if (w < 2)
+      static_assert(kLoads / 8 == 6 && kLoads % 8 == 1, "seven loads on wave 0, six on the rest");
+      if (w == 0)
         wait_vmcnt<7>();
       else
         wait_vmcnt<6>();
@@ -385,6 +398,22 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     f32x4 accO[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) accO[tt] = zero4();
+    // Row t = 16 tt + r16 of the Phi tile, one opaque base per tt.  Rows t and
+    // t + 16 sit at the same swizzle 4096 bytes apart; seen as such, their two
+    // 8-byte reads are fused into one ds_read2st64_b64, which the LDS serves at
+    // half the rate of two ds_read_b64 and with this pattern's lanes in
+    // conflict.  With opaque bases every read stays a ds_read_b64.
+    const char* prow[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      uint32_t off = (uint32_t)(16 * tt + r16) * (ss::kRowChunks * 16);
+      asm volatile("" : "+v"(off));
+      prow[tt] = reinterpret_cast<const char*>(tphi) + off;
+    }
+    const int sw = swz16(r16);
+    auto phi_half = [&](int tt, int k) {
+      return *reinterpret_cast<const Half*>(prow[tt] + ((k ^ sw) * 16 + 8 * (g & 1)));
+    };
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       Frag shi, slo;
@@ -400,9 +429,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
       }
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
-        const int t = 16 * tt + r16;
-        const Frag bf = join<In>(row_half<In>(tphi, t, 4 * kk + (g >> 1), g & 1),
-                                 row_half<In>(tphi, t, 4 * kk + 2 + (g >> 1), g & 1));
+        const Frag bf = join<In>(phi_half(tt, 4 * kk + (g >> 1)), phi_half(tt, 4 * kk + 2 + (g >> 1)));
         accO[tt] = mma(accO[tt], shi, bf);
         accO[tt] = mma(accO[tt], slo, bf);
       }
@@ -420,14 +447,14 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const int t = 16 * tt + r16;
-        const Half bf = row_half<In>(tphi, t, 2 * w + (g >> 1), g & 1);
+        const Half bf = phi_half(tt, 2 * w + (g >> 1));
         f32x4 pn = mma16(zero4(), s8hi, bf);
         pn = mma16(pn, s8lo, bf);
         if (g == (cn >> 2)) {
           if (tt == w)
             own = pn[cn & 3];
           else
-            normp[t * 8 + w] = pn[cn & 3];
+            normp[norm_slot(t, w)] = pn[cn & 3];
         }
       }
     }
@@ -461,7 +488,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
           if (tt == w) p8 = mma(p8, vb8[ks], bf);
         }
       }
-      if (tt == w && g == (cn >> 2)) normp[t * 8 + w] = own + p8[cn & 3];
+      if (tt == w && g == (cn >> 2)) normp[norm_slot(t, w)] = own + p8[cn & 3];
     }
     lds_barrier();
 
@@ -470,8 +497,8 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const int t = 16 * tt + r16;
-      const float4 n0 = *reinterpret_cast<const float4*>(normp + t * 8);
-      const float4 n1 = *reinterpret_cast<const float4*>(normp + t * 8 + 4);
+      const float4 n0 = *reinterpret_cast<const float4*>(normp + norm_slot(t, 0));
+      const float4 n1 = *reinterpret_cast<const float4*>(normp + norm_slot(t, 4));
       float den = ((n0.x + n0.y) + (n0.z + n0.w)) + ((n1.x + n1.y) + (n1.z + n1.w));
       float4 o;
       o.x = accO[tt][0];
@@ -510,15 +537,15 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 // the Vb fragment, so they add nothing.
 // ---------------------------------------------------------------------------
 
-// Issue one step's DMA: Psi (16 loads) and Vb (18) for rows
-// tok(row) = start + stride * (base + row), row < 64; waves 0, 1 issue five
+// Issue one step's DMA: Psi (16 loads) and Vb (17) for rows
+// tok(row) = start + stride * (base + row), row < 64; wave 0 issues five
 // loads, the others four.
 template <typename In>
 __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* psib,
                                            const In* vbb, const GramItems& it, int item,
                                            int64_t start, int64_t stride, int base, int count,
                                            int64_t k_st, int64_t v_st, int w, int lane) {
-  constexpr int kL = ss::kPhiLoads + ss::kVbLoads;     // 34
+  constexpr int kL = ss::kPhiLoads + ss::kVbLoads;     // 33
 #pragma unroll
   for (int u = 0; u < 5; ++u) {
     const int I = w + 8 * u;
@@ -532,11 +559,10 @@ __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* ps
         src = psib + tok * k_st + 8 * k;
         dst = dpsi + 64 * I;
       } else {
+        // Vb columns 0..127 swizzled like Psi, then columns 128..135, lane = row
         const int li = I - ss::kPhiLoads;
-        const int L = 64 * li + lane;
-        const int row = L / ss::kVbChunks;
-        const int k = L - row * ss::kVbChunks;
-        const int col = 8 * k + 8 <= v_st ? 8 * k : 0;
+        const int row = li < ss::kPhiLoads ? 4 * li + (lane >> 4) : lane;
+        const int col = li < ss::kPhiLoads ? 8 * ((lane & 15) ^ swz16(row)) : 128;
         const int64_t tok = gram_token(it, item, start, stride, base + row < count ? base + row : 0);
         src = vbb + tok * v_st + col;
         dst = dvb + 64 * li;
@@ -561,6 +587,7 @@ __global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
   typedef typename Traits<In>::frag Frag;
   // psi0 and vb0 are one array: after the last step it stages the output
   __shared__ __attribute__((aligned(16))) uint4 stage0[kTileChunks + kVbTileChunks];
+  static_assert((kTileChunks + kVbTileChunks) * 16 >= 64 * 129 * 4, "stage holds 64 rows of G");
   uint4* psi0 = stage0;
   uint4* vb0 = stage0 + kTileChunks;
   __shared__ __attribute__((aligned(16))) uint4 psi1[ONE ? 1 : kTileChunks];
@@ -594,7 +621,8 @@ __global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
     if (!ONE && s + 1 < nsteps) {
       issue_gram<In>(BUF ? psi0 : psi1, BUF ? vb0 : vb1, psib, vbb, it, item, start, stride,
                      (s + 1) * kStep, count, k_st, v_st, w, lane);
-      if (w < 2)
+      static_assert(kPhiLoads + kVbLoads == 33, "five loads on wave 0, four on the rest");
+      if (w == 0)
         wait_vmcnt<5>();
       else
         wait_vmcnt<4>();
