@@ -274,6 +274,27 @@ int smat_bgemm(int dtype_a, int dtype_b, const void* A, const void* B, float* C,
                int64_t cn, int beta, int mask, void* stream);
 
 /*
+ * Fused backward of the intra-chunk causal scan, one workgroup per
+ * (sequence, chunk) with the C x C scores A = tril(Phi Psi^T) and
+ * dA = tril(dH Vb^T) kept on chip:
+ *   dPhi = dA Psi + dH Sin^T,  dPsi = dA^T Phi + Vb Q^T,  dVb = A^T dH + Psi Q
+ * for 16-bit Phi, Psi, Vb (nb x nc*C rows; dtype SMAT_BF16 or SMAT_F16), fp32
+ * dH (nb x nc*C x p), the chunk-entry states Sin and the reverse-scan states Q
+ * (both nb x nc x r x p, contiguous).  Writes fp32 dPhi, dPsi (row stride
+ * d_st) and dVb (row stride e_st); every row of the nc chunks is written.
+ * Serves r = 64, p = 65, C = 128 with 16-byte aligned rows of Phi, Psi, dPhi
+ * and dPsi (SMAT_EUNSUPPORTED otherwise).  The products of
+ * src/smat/kernels/triton_bwd.py:49-147 (_cl_bwd_dphi_kernel and
+ * _cl_bwd_dpsi_dvb_kernel) with the chunk states of attention.py:134-192.
+ */
+int smat_chunk_backward(int dtype, const void* phi, const void* psi, const void* vb,
+                        const float* dH, const float* Sin, const float* Q, float* dPhi,
+                        float* dPsi, float* dVb, int nb, int nc, int r, int p, int C,
+                        int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                        int64_t v_st, int64_t h_sb, int64_t h_st, int64_t d_sb, int64_t d_st,
+                        int64_t e_sb, int64_t e_st, void* stream);
+
+/*
  * Whole forward schedule of smat_attention (src/smat/attention.py:391-455) for
  * a geometric mask: pool -> incidence (+ global channel) -> query ->
  * chunk states -> segmented scan -> chunk-local pass -> normalise.

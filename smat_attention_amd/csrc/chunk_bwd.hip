@@ -1,0 +1,535 @@
+// Fused backward of the intra-chunk causal scan for 16-bit inputs at
+// r = 64 features and p = 65 value columns (head_dim 64 plus the ones column),
+// chunks of C = 128 tokens -- the training shape.  Per chunk, with the
+// chunk's incoming state Sin (r x p) and the state Q flowing backwards from
+// the later chunks of its segment (r x p, the exclusive reverse scan of
+// Phi^T dH):
+//
+//   A  = tril(Phi Psi^T),   dA = tril(dH Vb^T)               (C x C, on chip)
+//   dPhi = dA Psi + dH Sin^T
+//   dPsi = dA^T Phi + Vb Q^T
+//   dVb  = A^T dH + Psi Q
+//
+// (the gradient of src/smat/attention.py:134-192 inside one chunk; the
+// reference fuses the same products in src/smat/kernels/triton_bwd.py:49-147
+// as a row-parallel dPhi kernel and a column-parallel dPsi/dVb kernel.)
+//
+// One workgroup of eight waves per (sequence, chunk).  The chunk's Phi, Psi,
+// Vb, dH, Sin and Q are staged in LDS once.  Wave w then does two passes:
+//
+//   * row pass, row tile i = w (tokens 16w .. 16w+15): for every column tile
+//     s <= i it forms the 16 x 16 block of dA^T = Vb dH^T in MFMA
+//     accumulators and feeds it, split hi/lo, straight back in as the B
+//     operand of dPhi^T = Psi^T dA^T (+ Sin dH^T);
+//   * column pass, column tile j = w: for every row tile t >= j it forms the
+//     blocks of dA = dH Vb^T and A = Phi Psi^T the same way and feeds them to
+//     dPsi^T = Phi^T dA (+ Q Vb^T) and dVb^T = dH^T A (+ Q^T Psi^T).
+//
+// The row pass of wave w visits w + 1 tiles and the column pass 8 - w, so
+// every wave does the same work.  The outputs are formed transposed so that
+// each lane ends with four consecutive columns of one token row.
+//
+// k-slot order.  A 16 x 16 accumulator tile gives lane (n, g) rows 4g .. 4g+3;
+// two tiles give it {4g + e, 16 + 4g + e}.  The MFMA contracts over any order
+// of its 32 k-slots as long as both operands use it, so a pair of
+// accumulator tiles is a B operand as it stands, and the matching A operand
+// is read from LDS along those tokens: the gfx950 transposing read
+// ds_read_b64_tr_b16 returns four consecutive token rows of one column per
+// lane.
+//
+// Precision: Phi, Psi and Vb are exact in the MFMA's 16-bit inputs; every
+// fp32 operand (dH, Sin, Q, A, dA) goes in as hi + lo (about 2^-17
+// relative), and a product of two fp32 operands takes hi.hi + hi.lo + lo.hi.
+// Value column 64 (the ones column) is the K = 16 tail of the contractions
+// over p and a fifth output column tile of dVb.
+//
+// LDS: Phi, Psi and Vb columns 0..63 as 128 rows of 128 bytes, 16-byte chunk
+// k of row t at k ^ (t & 6), which keeps both the row-wise 16-byte reads and
+// the transposing reads free of bank conflicts; Vb column 64 on its own; dH,
+// Sin and Q as fp32 rows of 68 floats (column reads by sixteen lanes of rows
+// 4 or 8 apart fall on disjoint banks).
+#include "smat_host.hpp"
+
+namespace smat {
+
+namespace cb {
+constexpr int kC = 128;          // tokens per chunk
+constexpr int kR = 64;           // features
+constexpr int kP = 65;           // value columns incl. the ones column
+constexpr int kThreads = 512;
+constexpr int kS = 68;           // fp32 LDS row stride (floats)
+constexpr int kRowChunks = 8;    // 16-byte chunks per 16-bit row of 64
+}  // namespace cb
+
+__device__ __forceinline__ f32x4 mma_k16(f32x4 c, bf16x4 a, bf16x4 b) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a),
+                                                   __builtin_bit_cast(s4, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma_k16(f32x4 c, f16x4 a, f16x4 b) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// 16-byte chunk slot of (row, chunk) in a 128-row x 128-byte tile.
+__device__ __forceinline__ int cb_slot(int row, int k) { return row * cb::kRowChunks + (k ^ (row & 6)); }
+
+template <typename In>
+__device__ __forceinline__ typename Traits<In>::half_frag cb_tr(const uint4* tile, int row, int k,
+                                                                int half) {
+  typedef short short4v __attribute__((ext_vector_type(4)));
+  const char* p = reinterpret_cast<const char*>(tile + cb_slot(row, k)) + 8 * half;
+  short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4v*)(__attribute__((address_space(3))) char*)(p));
+  return __builtin_bit_cast(typename Traits<In>::half_frag, v);
+}
+
+// The A operand along tokens of a transposed 16-bit tile (Phi^T or Psi^T):
+// lane (m = 16 ct + lane % 16, g) gets, as k-slot 4h + e, column m of token
+// row 16 tile[h] + 4g + e.  Lane 4e + q of each sixteen addresses row
+// 16 tile[h] + 4g + e, columns 16 ct + 4q .. +3.
+template <typename In>
+__device__ __forceinline__ typename Traits<In>::frag cb_tr_pair(const uint4* tile, int t0, int t1,
+                                                               int ct, int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  const int k = 2 * ct + ((r16 & 3) >> 1), half = r16 & 1;
+  const auto a = cb_tr<In>(tile, 16 * t0 + 4 * g + (r16 >> 2), k, half);
+  const auto b = cb_tr<In>(tile, 16 * t1 + 4 * g + (r16 >> 2), k, half);
+  typename Traits<In>::frag f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[e] = a[e];
+    f[4 + e] = b[e];
+  }
+  return f;
+}
+
+// Row-wise operand of a 16-bit tile: lane (row 16 tile + lane % 16, g) gets
+// columns 32 kc + 8g .. +7.
+template <typename In>
+__device__ __forceinline__ typename Traits<In>::frag cb_row(const uint4* tile, int tile_row, int kc,
+                                                           int lane) {
+  return *reinterpret_cast<const typename Traits<In>::frag*>(
+      tile + cb_slot(16 * tile_row + (lane & 15), 4 * kc + (lane >> 4)));
+}
+
+// Row-wise operand of an fp32 LDS tile (rows of kS floats), split hi/lo:
+// lane (row, g) gets columns 32 kc + 8g .. +7.
+template <typename In>
+__device__ __forceinline__ void cb_row32(const float* t, int row, int kc, int g,
+                                         typename Traits<In>::frag& hi,
+                                         typename Traits<In>::frag& lo) {
+  const float4 a = *reinterpret_cast<const float4*>(t + row * cb::kS + 32 * kc + 8 * g);
+  const float4 b = *reinterpret_cast<const float4*>(t + row * cb::kS + 32 * kc + 8 * g + 4);
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    In h, l;
+    split2<In>(v[e], h, l);
+    hi[e] = h;
+    lo[e] = l;
+  }
+}
+
+// The K = 16 tail over value columns 64..79 of an fp32 LDS tile: only column
+// 64 exists, k-slot 0 of lane group 0.
+template <typename In>
+__device__ __forceinline__ void cb_tail32(const float* t, int row, int g,
+                                          typename Traits<In>::half_frag& hi,
+                                          typename Traits<In>::half_frag& lo) {
+  const float v = g == 0 ? t[row * cb::kS + 64] : 0.f;
+  In h, l;
+  split2<In>(v, h, l);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = from_f32<In>(0.f);
+    lo[e] = from_f32<In>(0.f);
+  }
+  hi[0] = h;
+  lo[0] = l;
+}
+
+// hi/lo 16-bit B operand from two accumulator tiles (k-slot 4h + e <- tile h, entry e).
+template <typename In>
+__device__ __forceinline__ void cb_split_pair(const f32x4& a, const f32x4& b,
+                                              typename Traits<In>::frag& hi,
+                                              typename Traits<In>::frag& lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    In h, l;
+    split2<In>(a[e], h, l);
+    hi[e] = h;
+    lo[e] = l;
+    split2<In>(b[e], h, l);
+    hi[4 + e] = h;
+    lo[4 + e] = l;
+  }
+}
+
+struct ChunkBwdArgs {
+  int nc;                       // chunks per sequence
+  int64_t q_sb, q_st, k_sb, k_st, v_sb, v_st;   // Phi, Psi, Vb (elements)
+  int64_t h_sb, h_st;           // dH (floats)
+  int64_t d_sb, d_st;           // dPhi and dPsi (floats)
+  int64_t e_sb, e_st;           // dVb (floats)
+};
+
+template <typename In>
+__global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
+    const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
+    const float* __restrict__ dH, const float* __restrict__ Sin, const float* __restrict__ Qs,
+    float* __restrict__ dPhi, float* __restrict__ dPsi, float* __restrict__ dVb, ChunkBwdArgs a) {
+  using namespace cb;
+  typedef typename Traits<In>::frag Frag;
+  typedef typename Traits<In>::half_frag Half;
+  __shared__ __attribute__((aligned(16))) uint4 sPhi[kC * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sPsi[kC * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sVb[kC * kRowChunks];
+  __shared__ __attribute__((aligned(16))) float sdH[kC * kS];
+  __shared__ __attribute__((aligned(16))) float sSin[kR * kS];
+  __shared__ __attribute__((aligned(16))) float sQ[kR * kS];
+  __shared__ In sVb64[kC];
+
+  const int c = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int64_t t0 = (int64_t)c * kC;
+  const In* phib = phi + b * a.q_sb + t0 * a.q_st;
+  const In* psib = psi + b * a.k_sb + t0 * a.k_st;
+  const In* vbb = vb + b * a.v_sb + t0 * a.v_st;
+  const float* dHb = dH + b * a.h_sb + t0 * a.h_st;
+  const int64_t st_off = ((int64_t)b * a.nc + c) * (kR * kP);
+  const float* Sinb = Sin + st_off;
+  const float* Qb = Qs + st_off;
+
+  // ---- stage the chunk in LDS -------------------------------------------
+  // Phi and Psi rows (64 elements, 16-byte aligned rows: checked on the host)
+  uint4 rphi[2], rpsi[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int e = tid + kThreads * u;              // chunk of 8 elements, < 1024
+    const int row = e >> 3, k = e & 7;
+    rphi[u] = *reinterpret_cast<const uint4*>(phib + row * a.q_st + 8 * k);
+    rpsi[u] = *reinterpret_cast<const uint4*>(psib + row * a.k_st + 8 * k);
+  }
+  // Vb (65 elements a row, any stride), dH (65 floats a row), Sin and Q
+  // (64 x 65 floats, contiguous): element-wise, consecutive threads on
+  // consecutive elements
+  constexpr int kVbN = kC * kP;                     // 8320
+  constexpr int kVbIt = (kVbN + kThreads - 1) / kThreads;   // 17
+  constexpr int kSN = kR * kP;                      // 4160
+  constexpr int kSIt = (kSN + kThreads - 1) / kThreads;     // 9
+  In rvb[kVbIt];
+  float rdh[kVbIt], rsin[kSIt], rq[kSIt];
+#pragma unroll
+  for (int u = 0; u < kVbIt; ++u) {
+    const int e = tid + kThreads * u;
+    const int ee = e < kVbN ? e : 0;
+    const int row = ee / kP, col = ee - row * kP;
+    rvb[u] = vbb[row * a.v_st + col];
+    rdh[u] = dHb[row * a.h_st + col];
+  }
+#pragma unroll
+  for (int u = 0; u < kSIt; ++u) {
+    const int e = tid + kThreads * u;
+    const int ee = e < kSN ? e : 0;
+    rsin[u] = Sinb[ee];
+    rq[u] = Qb[ee];
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int e = tid + kThreads * u;
+    const int row = e >> 3, k = e & 7;
+    sPhi[cb_slot(row, k)] = rphi[u];
+    sPsi[cb_slot(row, k)] = rpsi[u];
+  }
+#pragma unroll
+  for (int u = 0; u < kVbIt; ++u) {
+    const int e = tid + kThreads * u;
+    if (e < kVbN) {
+      const int row = e / kP, col = e - row * kP;
+      if (col < 64)
+        reinterpret_cast<In*>(sVb + cb_slot(row, col >> 3))[col & 7] = rvb[u];
+      else
+        sVb64[row] = rvb[u];
+      sdH[row * kS + col] = rdh[u];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kSIt; ++u) {
+    const int e = tid + kThreads * u;
+    if (e < kSN) {
+      const int row = e / kP, col = e - row * kP;
+      sSin[row * kS + col] = rsin[u];
+      sQ[row * kS + col] = rq[u];
+    }
+  }
+  __syncthreads();
+
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int lane = lane_id();
+  const int r16 = lane & 15, g = lane >> 4;
+  const Half hzero = {};
+
+  // ---- row pass: dPhi rows of tile i = w ----------------------------------
+  {
+    const int i = w;
+    const int trow = 16 * i + r16;
+    Frag dh_hi[2], dh_lo[2];
+    Half dht_hi, dht_lo;
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) cb_row32<In>(sdH, trow, kc, g, dh_hi[kc], dh_lo[kc]);
+    cb_tail32<In>(sdH, trow, g, dht_hi, dht_lo);
+
+    f32x4 acc[4];
+    // dPhi^T += Sin dH^T: A = Sin rows a (k = value column), B = dH^T
+#pragma unroll
+    for (int at = 0; at < 4; ++at) {
+      f32x4 s = zero4();
+      const int arow = 16 * at + r16;
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        Frag hi, lo;
+        cb_row32<In>(sSin, arow, kc, g, hi, lo);
+        s = mma(s, hi, dh_hi[kc]);
+        s = mma(s, hi, dh_lo[kc]);
+        s = mma(s, lo, dh_hi[kc]);
+      }
+      Half thi, tlo;
+      cb_tail32<In>(sSin, arow, g, thi, tlo);
+      s = mma_k16(s, thi, dht_hi);
+      s = mma_k16(s, thi, dht_lo);
+      s = mma_k16(s, tlo, dht_hi);
+      acc[at] = s;
+    }
+    // dPhi^T += Psi^T dA^T over column tiles s <= i, two at a time
+    for (int sp = 0; 2 * sp <= i; ++sp) {
+      f32x4 dat[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int st = 2 * sp + h;
+        f32x4 d = zero4();
+        if (st <= i) {
+          // dA^T[s][t] = sum_c Vb[s][c] dH[t][c]: A = Vb rows s, B = dH^T
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc) {
+            const Frag vf = cb_row<In>(sVb, st, kc, lane);
+            d = mma(d, vf, dh_hi[kc]);
+            d = mma(d, vf, dh_lo[kc]);
+          }
+          Half vt = hzero;
+          if (g == 0) vt[0] = sVb64[16 * st + r16];
+          d = mma_k16(d, vt, dht_hi);
+          d = mma_k16(d, vt, dht_lo);
+          if (st == i) {
+            // lane (t = r16, g) holds s = 16 st + 4g + e: keep s <= t
+#pragma unroll
+            for (int e = 0; e < 4; ++e) d[e] = 4 * g + e <= r16 ? d[e] : 0.f;
+          }
+        }
+        dat[h] = d;
+      }
+      Frag bh, bl;
+      cb_split_pair<In>(dat[0], dat[1], bh, bl);
+      const int st1 = 2 * sp + 1 < 8 ? 2 * sp + 1 : 2 * sp;
+#pragma unroll
+      for (int at = 0; at < 4; ++at) {
+        const Frag pa = cb_tr_pair<In>(sPsi, 2 * sp, st1, at, lane);
+        acc[at] = mma(acc[at], pa, bh);
+        acc[at] = mma(acc[at], pa, bl);
+      }
+    }
+    // lane (t, g) holds dPhi[t][16 at + 4g + e]
+    float* out = dPhi + b * a.d_sb + (t0 + trow) * a.d_st;
+#pragma unroll
+    for (int at = 0; at < 4; ++at)
+      *reinterpret_cast<float4*>(out + 16 * at + 4 * g) =
+          make_float4(acc[at][0], acc[at][1], acc[at][2], acc[at][3]);
+  }
+
+  // ---- column pass: dPsi and dVb rows of tile j = w -----------------------
+  {
+    const int j = w;
+    const int srow = 16 * j + r16;
+    Frag vf[2], pf[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      vf[kc] = cb_row<In>(sVb, j, kc, lane);
+      pf[kc] = cb_row<In>(sPsi, j, kc, lane);
+    }
+    Half vt = hzero;
+    if (g == 0) vt[0] = sVb64[srow];
+
+    f32x4 accq[4], accv[5];
+    // dPsi^T += Q Vb^T: A = Q rows a, B = Vb^T
+#pragma unroll
+    for (int at = 0; at < 4; ++at) {
+      f32x4 s = zero4();
+      const int arow = 16 * at + r16;
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        Frag hi, lo;
+        cb_row32<In>(sQ, arow, kc, g, hi, lo);
+        s = mma(s, hi, vf[kc]);
+        s = mma(s, lo, vf[kc]);
+      }
+      Half thi, tlo;
+      cb_tail32<In>(sQ, arow, g, thi, tlo);
+      s = mma_k16(s, thi, vt);
+      s = mma_k16(s, tlo, vt);
+      accq[at] = s;
+    }
+    // dVb^T += Q^T Psi^T: A = Q^T (rows = value column c, k = feature a)
+#pragma unroll
+    for (int ct = 0; ct < 5; ++ct) {
+      f32x4 s = zero4();
+      const int col = 16 * ct + r16;
+      const bool okc = col < kP;
+      const int cc = okc ? col : 0;                  // columns past p read column 0, then zero
+#pragma unroll
+      for (int ka = 0; ka < 2; ++ka) {
+        Frag hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float v = okc ? sQ[(32 * ka + 8 * g + e) * kS + cc] : 0.f;
+          In h, l;
+          split2<In>(v, h, l);
+          hi[e] = h;
+          lo[e] = l;
+        }
+        s = mma(s, hi, pf[ka]);
+        s = mma(s, lo, pf[ka]);
+      }
+      accv[ct] = s;
+    }
+    // over row tiles t >= j, two at a time
+    for (int tp = 0; j + 2 * tp < 8; ++tp) {
+      const int tt0 = j + 2 * tp;
+      const int tt1 = tt0 + 1 < 8 ? tt0 + 1 : tt0;
+      const bool has1 = tt0 + 1 < 8;
+      f32x4 da[2], aa[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int tt = h ? tt1 : tt0;
+        f32x4 d = zero4(), s = zero4();
+        if (h == 0 || has1) {
+          const int trow = 16 * tt + r16;
+          // dA[t][s] = sum_c dH[t][c] Vb[s][c]: A = dH rows t, B = Vb^T
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc) {
+            Frag hi, lo;
+            cb_row32<In>(sdH, trow, kc, g, hi, lo);
+            d = mma(d, hi, vf[kc]);
+            d = mma(d, lo, vf[kc]);
+            // A[t][s] = sum_a Phi[t][a] Psi[s][a]
+            s = mma(s, cb_row<In>(sPhi, tt, kc, lane), pf[kc]);
+          }
+          Half thi, tlo;
+          cb_tail32<In>(sdH, trow, g, thi, tlo);
+          d = mma_k16(d, thi, vt);
+          d = mma_k16(d, tlo, vt);
+          if (tt == j) {
+            // lane (s = r16, g) holds t = 16 tt + 4g + e: keep t >= s
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const bool keep = 4 * g + e >= r16;
+              d[e] = keep ? d[e] : 0.f;
+              s[e] = keep ? s[e] : 0.f;
+            }
+          }
+        }
+        da[h] = d;
+        aa[h] = s;
+      }
+      Frag dah, dal, aah, aal;
+      cb_split_pair<In>(da[0], da[1], dah, dal);
+      cb_split_pair<In>(aa[0], aa[1], aah, aal);
+      // dPsi^T += Phi^T dA
+#pragma unroll
+      for (int at = 0; at < 4; ++at) {
+        const Frag pa = cb_tr_pair<In>(sPhi, tt0, tt1, at, lane);
+        accq[at] = mma(accq[at], pa, dah);
+        accq[at] = mma(accq[at], pa, dal);
+      }
+      // dVb^T += dH^T A: A operand = dH^T (rows = value column c, k = token t)
+#pragma unroll
+      for (int ct = 0; ct < 5; ++ct) {
+        const int col = 16 * ct + r16;
+        const bool okc = col < kP;
+        const int cc = okc ? col : 0;
+        Frag hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int tt = e < 4 ? tt0 : tt1;
+          const bool ok = okc && (e < 4 || has1);
+          const float v = ok ? sdH[(16 * tt + 4 * g + (e & 3)) * kS + cc] : 0.f;
+          In h, l;
+          split2<In>(v, h, l);
+          hi[e] = h;
+          lo[e] = l;
+        }
+        accv[ct] = mma(accv[ct], hi, aah);
+        accv[ct] = mma(accv[ct], hi, aal);
+        accv[ct] = mma(accv[ct], lo, aah);
+      }
+    }
+    // lane (s, g) holds dPsi[s][16 at + 4g + e] and dVb[s][16 ct + 4g + e]
+    float* op = dPsi + b * a.d_sb + (t0 + srow) * a.d_st;
+#pragma unroll
+    for (int at = 0; at < 4; ++at)
+      *reinterpret_cast<float4*>(op + 16 * at + 4 * g) =
+          make_float4(accq[at][0], accq[at][1], accq[at][2], accq[at][3]);
+    float* ov = dVb + b * a.e_sb + (t0 + srow) * a.e_st;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[16 * ct + 4 * g + e] = accv[ct][e];
+    if (g == 0) ov[64] = accv[4][0];
+  }
+}
+
+bool chunk_bwd_ok(int dtype, const void* phi, const void* psi, int r, int p, int C,
+                  int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t d_sb,
+                  int64_t d_st, const void* dphi, const void* dpsi) {
+  if (dtype != SMAT_BF16 && dtype != SMAT_F16) return false;
+  if (r != cb::kR || p != cb::kP || C != cb::kC) return false;
+  return rows_vec_ok(phi, q_sb, q_st, 2) && rows_vec_ok(psi, k_sb, k_st, 2) &&
+         rows_vec_ok(dphi, d_sb, d_st, 4) && rows_vec_ok(dpsi, d_sb, d_st, 4);
+}
+
+}  // namespace smat
+
+extern "C" int smat_chunk_backward(int dtype, const void* phi, const void* psi, const void* vb,
+                                   const float* dH, const float* Sin, const float* Q, float* dPhi,
+                                   float* dPsi, float* dVb, int nb, int nc, int r, int p, int C,
+                                   int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
+                                   int64_t v_sb, int64_t v_st, int64_t h_sb, int64_t h_st,
+                                   int64_t d_sb, int64_t d_st, int64_t e_sb, int64_t e_st,
+                                   void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(phi && psi && vb && dH && Sin && Q && dPhi && dPsi && dVb, SMAT_EINVAL,
+               "smat_chunk_backward: null pointer");
+  SMAT_REQUIRE(nb >= 0 && nc >= 0, SMAT_EINVAL, "smat_chunk_backward: bad sizes");
+  SMAT_REQUIRE(nc < 65536 * 32 && nb < 65536, SMAT_EUNSUPPORTED,
+               "smat_chunk_backward: grid %d x %d too large", nc, nb);
+  SMAT_REQUIRE(chunk_bwd_ok(dtype, phi, psi, r, p, C, q_sb, q_st, k_sb, k_st, d_sb, d_st, dPhi,
+                            dPsi),
+               SMAT_EUNSUPPORTED,
+               "smat_chunk_backward: needs 16-bit inputs, r=64, p=65, C=128 and 16-byte "
+               "aligned rows of Phi, Psi, dPhi and dPsi (got dtype=%d r=%d p=%d C=%d)",
+               dtype, r, p, C);
+  SMAT_REQUIRE(v_st >= p && h_st >= p && e_st >= p && d_st >= r, SMAT_EINVAL,
+               "smat_chunk_backward: row stride too short");
+  if (nb == 0 || nc == 0) return SMAT_OK;
+  ChunkBwdArgs a{nc, q_sb, q_st, k_sb, k_st, v_sb, v_st, h_sb, h_st, d_sb, d_st, e_sb, e_st};
+  const dim3 grid((unsigned)nc, (unsigned)nb);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == SMAT_BF16)
+    hipLaunchKernelGGL(chunk_bwd_kernel<bf16>, grid, dim3(cb::kThreads), 0, st,
+                       (const bf16*)phi, (const bf16*)psi, (const bf16*)vb, dH, Sin, Q, dPhi,
+                       dPsi, dVb, a);
+  else
+    hipLaunchKernelGGL(chunk_bwd_kernel<f16>, grid, dim3(cb::kThreads), 0, st, (const f16*)phi,
+                       (const f16*)psi, (const f16*)vb, dH, Sin, Q, dPhi, dPsi, dVb, a);
+  return launch_status("smat_chunk_backward");
+}

@@ -99,6 +99,22 @@ def _incidence_rows(src, idx, indptr, n_out, nb, n_in, rp):
     return out
 
 
+# The fused chunk backward (smat_chunk_backward) serves 16-bit inputs at
+# r = 64, p = 65, C = 128; tests switch it off to compare it with the chain of
+# smat_bgemm products it replaces.
+FUSED_CHUNK_BACKWARD = True
+
+
+def fused_chunk_backward_ok(Ph, Ps, Vv, C: int) -> bool:
+    return (FUSED_CHUNK_BACKWARD and Ph.dtype in (torch.bfloat16, torch.float16)
+            and Ps.dtype == Ph.dtype and Vv.dtype == Ph.dtype and C == 128
+            and Ph.shape[-1] == 64 and Ps.shape[-1] == 64 and Vv.shape[-1] == 65
+            and Ph.stride(-1) == 1 and Ps.stride(-1) == 1 and Vv.stride(-1) == 1
+            and Ph.stride(1) % 8 == 0 and Ps.stride(1) % 8 == 0
+            and Ph.stride(0) % 8 == 0 and Ps.stride(0) % 8 == 0
+            and Ph.data_ptr() % 16 == 0 and Ps.data_ptr() % 16 == 0)
+
+
 def causal_scan_grad(Ph, Ps, Vv, dH, n: int, C: int):
     """``(dPhi, dPsi, dVb)`` of the segmented causal scan ``H`` (attention.py:134-192)
     given ``dH``: inputs padded to whole chunks of ``C`` rows, fp32 ``(nb, Tp, .)``
@@ -123,6 +139,14 @@ def causal_scan_grad(Ph, Ps, Vv, dH, n: int, C: int):
     call("smat_segment_scan_reverse", Dr.data_ptr(), Q.data_ptr(), nb, nc, n // C, rp,
          stream_of(Q))
     del Dr
+    if fused_chunk_backward_ok(Ph, Ps, Vv, C):
+        # A and dA stay on chip: one launch for the six products below
+        call("smat_chunk_backward", _code(Ph), Ph.data_ptr(), Ps.data_ptr(), Vv.data_ptr(),
+             dH.data_ptr(), Sin.data_ptr(), Q.data_ptr(), dPhi.data_ptr(), dPsi.data_ptr(),
+             dVb.data_ptr(), nb, nc, r, p, C, Ph.stride(0), Ph.stride(1), Ps.stride(0),
+             Ps.stride(1), Vv.stride(0), Vv.stride(1), dH.stride(0), dH.stride(1),
+             dPhi.stride(0), dPhi.stride(1), dVb.stride(0), dVb.stride(1), stream_of(dPhi))
+        return dPhi, dPsi, dVb
     A = torch.empty(nb, nc, C, C, device=dev, dtype=torch.float32)
     dA = torch.empty_like(A)
     CC = C * C

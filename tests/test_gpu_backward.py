@@ -266,6 +266,45 @@ def test_segmented_causal_scan_gradients(T, n, C, r, p):
         assert _grel(a, b) < 1e-5
 
 
+@pytest.mark.parametrize("T,n", [(4096, 2048), (1000, 384), (1024, 1024), (2048, 0)])
+def test_fused_chunk_backward(T, n):
+    """smat_chunk_backward (bf16 inputs, r = 64, p = 65, C = 128: the training
+    shape) against the chain of smat_bgemm products it replaces, and both
+    against fp64 autograd of the oracle's scan on the same bf16 values: fp32
+    gradients, padded tail chunk and both segment splits included."""
+    from smat_attention_amd.kernels import hip_bwd as HB
+    C, r, p, nb = 128, 64, 65, 3
+    Tp = -(-T // C) * C
+    gen = torch.Generator().manual_seed(T + n)
+    bf = torch.bfloat16
+
+    def rows(width, make):
+        x = torch.zeros(nb, Tp, width)
+        x[:, :T] = make((nb, T, width))
+        return x
+    Ph = rows(r, lambda s: torch.rand(s, generator=gen) + 0.1).to(bf)
+    Ps = rows(r, lambda s: torch.rand(s, generator=gen) * 0.1).to(bf)
+    Vv = rows(p, lambda s: torch.randn(s, generator=gen)).to(bf)
+    dH = rows(p, lambda s: torch.randn(s, generator=gen))
+    _say("fused chunk backward", T, n)
+    args = [x.to(DEV) for x in (Ph, Ps, Vv, dH)]
+    assert HB.fused_chunk_backward_ok(*args[:3], C)
+    got = [x.cpu() for x in HB.causal_scan_grad(*args, n, C)]
+    try:
+        HB.FUSED_CHUNK_BACKWARD = False
+        ref = [x.cpu() for x in HB.causal_scan_grad(*args, n, C)]
+    finally:
+        HB.FUSED_CHUNK_BACKWARD = True
+    xs = [x[:, :T].double().requires_grad_(True) for x in (Ph, Ps, Vv)]
+    H = O.segmented_causal_scan(*xs, n, C)
+    (H * dH[:, :T].double()).sum().backward()
+    for name, a, b, x in zip(("dPhi", "dPsi", "dVb"), got, ref, xs):
+        e_chain, e_64 = _grel(a, b), _grel(a[:, :T], x.grad)
+        _say(f"  {name}: vs bgemm {e_chain:.2e}, vs fp64 {e_64:.2e}")
+        assert e_chain < 1e-4 and e_64 < 1e-4, name
+        assert torch.isfinite(a).all()
+
+
 @pytest.mark.parametrize("d", [2, 3])
 def test_training_step_content_hashed(d):
     """The content-hashed training step at head_dim 64, T = 4096 (4 of the
