@@ -295,6 +295,39 @@ int smat_chunk_backward(int dtype, const void* phi, const void* psi, const void*
                         int64_t e_sb, int64_t e_st, void* stream);
 
 /*
+ * Backward of the long-range branch (attention.py:196-330) at r = 64, p = 65
+ * for 16-bit inputs (dtype SMAT_BF16 or SMAT_F16; SMAT_EUNSUPPORTED
+ * otherwise); dY is dH on the recent rows, fp32.
+ *
+ * smat_lr_dphi: dPhi[n + h + k*B] += dH[n + h + k*B] U_h^T for every row type
+ * h < B and k with h + k*B < T_R; U fp32 (nb x B x r x p, 16-byte aligned
+ * matrices), dPhi fp32 rows 16-byte aligned.  The query's gradient, which
+ * the reference takes from torch autograd of attention.py:287-330.
+ *
+ * smat_lr_dfeat: dF[x] = sum over t in tok[tptr[x] .. tptr[x+1]) of
+ * Phi_t^T dH_t (r x p fp32, dF contiguous nb x nitems x r x p).  With
+ * the list of point x holding the recent rows of every row type whose
+ * hyperplane contains x, this is C^T dU with dU_h the query's parameter
+ * gradient: the reference's dU (torch) and incidence backward
+ * (src/smat/kernels/triton_bwd.py:262-276) in one pass.
+ *
+ * smat_pool_backward: for every profile x < N0 and its tokens
+ * j = n_P + x + s*N0 < n, dPsi_j += Vb_j dF_x^T and dVb_j += Psi_j dF_x; when
+ * n_P > 0, item N0 (dF row N0, the global channel) does tokens 0 .. n_P-1.
+ * dF_x is read once for both (src/smat/kernels/triton_bwd.py:203-237).
+ */
+int smat_lr_dphi(int dtype, const float* dH, const float* U, float* dPhi, int nb, int T_R, int B,
+                 int n, int r, int p, int64_t h_sb, int64_t h_st, int64_t u_sb, int64_t d_sb,
+                 int64_t d_st, void* stream);
+int smat_lr_dfeat(int dtype, const void* phi, const float* dH, const int32_t* tptr,
+                  const int32_t* tok, float* dF, int nb, int nitems, int r, int p, int64_t q_sb,
+                  int64_t q_st, int64_t h_sb, int64_t h_st, int64_t f_sb, void* stream);
+int smat_pool_backward(int dtype, const void* psi, const void* vb, const float* dF, float* dPsi,
+                       float* dVb, int nb, int N0, int n, int n_P, int r, int p, int64_t k_sb,
+                       int64_t k_st, int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb,
+                       int64_t d_st, int64_t e_sb, int64_t e_st, void* stream);
+
+/*
  * Whole forward schedule of smat_attention (src/smat/attention.py:391-455) for
  * a geometric mask: pool -> incidence (+ global channel) -> query ->
  * chunk states -> segmented scan -> chunk-local pass -> normalise.

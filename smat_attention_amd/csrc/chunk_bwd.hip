@@ -48,122 +48,9 @@
 // the transposing reads free of bank conflicts; Vb column 64 on its own; dH,
 // Sin and Q as fp32 rows of 68 floats (column reads by sixteen lanes of rows
 // 4 or 8 apart fall on disjoint banks).
-#include "smat_host.hpp"
+#include "bwd_common.hpp"
 
 namespace smat {
-
-namespace cb {
-constexpr int kC = 128;          // tokens per chunk
-constexpr int kR = 64;           // features
-constexpr int kP = 65;           // value columns incl. the ones column
-constexpr int kThreads = 512;
-constexpr int kS = 68;           // fp32 LDS row stride (floats)
-constexpr int kRowChunks = 8;    // 16-byte chunks per 16-bit row of 64
-}  // namespace cb
-
-__device__ __forceinline__ f32x4 mma_k16(f32x4 c, bf16x4 a, bf16x4 b) {
-  typedef short s4 __attribute__((ext_vector_type(4)));
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a),
-                                                   __builtin_bit_cast(s4, b), c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x4 mma_k16(f32x4 c, f16x4 a, f16x4 b) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-}
-
-// 16-byte chunk slot of (row, chunk) in a 128-row x 128-byte tile.
-__device__ __forceinline__ int cb_slot(int row, int k) { return row * cb::kRowChunks + (k ^ (row & 6)); }
-
-template <typename In>
-__device__ __forceinline__ typename Traits<In>::half_frag cb_tr(const uint4* tile, int row, int k,
-                                                                int half) {
-  typedef short short4v __attribute__((ext_vector_type(4)));
-  const char* p = reinterpret_cast<const char*>(tile + cb_slot(row, k)) + 8 * half;
-  short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) short4v*)(__attribute__((address_space(3))) char*)(p));
-  return __builtin_bit_cast(typename Traits<In>::half_frag, v);
-}
-
-// The A operand along tokens of a transposed 16-bit tile (Phi^T or Psi^T):
-// lane (m = 16 ct + lane % 16, g) gets, as k-slot 4h + e, column m of token
-// row 16 tile[h] + 4g + e.  Lane 4e + q of each sixteen addresses row
-// 16 tile[h] + 4g + e, columns 16 ct + 4q .. +3.
-template <typename In>
-__device__ __forceinline__ typename Traits<In>::frag cb_tr_pair(const uint4* tile, int t0, int t1,
-                                                               int ct, int lane) {
-  const int r16 = lane & 15, g = lane >> 4;
-  const int k = 2 * ct + ((r16 & 3) >> 1), half = r16 & 1;
-  const auto a = cb_tr<In>(tile, 16 * t0 + 4 * g + (r16 >> 2), k, half);
-  const auto b = cb_tr<In>(tile, 16 * t1 + 4 * g + (r16 >> 2), k, half);
-  typename Traits<In>::frag f;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    f[e] = a[e];
-    f[4 + e] = b[e];
-  }
-  return f;
-}
-
-// Row-wise operand of a 16-bit tile: lane (row 16 tile + lane % 16, g) gets
-// columns 32 kc + 8g .. +7.
-template <typename In>
-__device__ __forceinline__ typename Traits<In>::frag cb_row(const uint4* tile, int tile_row, int kc,
-                                                           int lane) {
-  return *reinterpret_cast<const typename Traits<In>::frag*>(
-      tile + cb_slot(16 * tile_row + (lane & 15), 4 * kc + (lane >> 4)));
-}
-
-// Row-wise operand of an fp32 LDS tile (rows of kS floats), split hi/lo:
-// lane (row, g) gets columns 32 kc + 8g .. +7.
-template <typename In>
-__device__ __forceinline__ void cb_row32(const float* t, int row, int kc, int g,
-                                         typename Traits<In>::frag& hi,
-                                         typename Traits<In>::frag& lo) {
-  const float4 a = *reinterpret_cast<const float4*>(t + row * cb::kS + 32 * kc + 8 * g);
-  const float4 b = *reinterpret_cast<const float4*>(t + row * cb::kS + 32 * kc + 8 * g + 4);
-  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    In h, l;
-    split2<In>(v[e], h, l);
-    hi[e] = h;
-    lo[e] = l;
-  }
-}
-
-// The K = 16 tail over value columns 64..79 of an fp32 LDS tile: only column
-// 64 exists, k-slot 0 of lane group 0.
-template <typename In>
-__device__ __forceinline__ void cb_tail32(const float* t, int row, int g,
-                                          typename Traits<In>::half_frag& hi,
-                                          typename Traits<In>::half_frag& lo) {
-  const float v = g == 0 ? t[row * cb::kS + 64] : 0.f;
-  In h, l;
-  split2<In>(v, h, l);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    hi[e] = from_f32<In>(0.f);
-    lo[e] = from_f32<In>(0.f);
-  }
-  hi[0] = h;
-  lo[0] = l;
-}
-
-// hi/lo 16-bit B operand from two accumulator tiles (k-slot 4h + e <- tile h, entry e).
-template <typename In>
-__device__ __forceinline__ void cb_split_pair(const f32x4& a, const f32x4& b,
-                                              typename Traits<In>::frag& hi,
-                                              typename Traits<In>::frag& lo) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    In h, l;
-    split2<In>(a[e], h, l);
-    hi[e] = h;
-    lo[e] = l;
-    split2<In>(b[e], h, l);
-    hi[4 + e] = h;
-    lo[4 + e] = l;
-  }
-}
 
 struct ChunkBwdArgs {
   int nc;                       // chunks per sequence

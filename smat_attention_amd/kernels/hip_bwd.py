@@ -91,6 +91,55 @@ def transposed_incidence(spec, device):
     return t_ptr, t_idx
 
 
+def recent_token_lists(spec, device):
+    """CSR ``(tptr, tok)`` (int32) of the recent rows feeding each pooled item's
+    gradient: for point x < N0, the rows n + h + k*B < T of every row type h
+    whose hyperplane contains x (the transposed incidence, each line's rows in
+    order); when n_P > 0, item N0 (the global channel) lists every recent row.
+    Cached on the spec."""
+    key = ("_smat_RT", str(device))
+    hit = getattr(spec, "_smat_RT", None)
+    if hit is not None and hit[0] == key:
+        return hit[1], hit[2]
+    n, T_R, B, N0 = spec.n, spec.T_R, spec.B, spec.N0
+    ptr_ = np.asarray(spec.C_indptr, dtype=np.int64)
+    ind = np.asarray(spec.C_indices, dtype=np.int64)
+    lines = np.repeat(np.arange(B, dtype=np.int64), np.diff(ptr_))
+    order = np.lexsort((lines, ind))
+    pts, lines = ind[order], lines[order]
+    h = np.arange(B, dtype=np.int64)
+    cnt = np.where(h < T_R, (T_R - h + B - 1) // B, 0)
+    per = cnt[lines]
+    parts = [n + hh + B * np.arange(c, dtype=np.int64) for hh, c in zip(lines.tolist(), per.tolist())]
+    counts = np.bincount(pts, weights=per, minlength=N0).astype(np.int64)
+    if spec.n_P:
+        parts.append(np.arange(n, n + T_R, dtype=np.int64))
+        counts = np.concatenate([counts, [T_R]])
+    tok = np.concatenate(parts) if parts else np.zeros(0, np.int64)
+    tptr = np.concatenate([[0], np.cumsum(counts)])
+    assert tptr[-1] == len(tok) < 2 ** 31
+    out = (torch.from_numpy(tptr.astype(np.int32)).to(device),
+           torch.from_numpy(tok.astype(np.int32)).to(device))
+    spec._smat_RT = (key,) + out
+    return out
+
+
+# The long-range backward kernels (smat_lr_dphi, smat_lr_dfeat,
+# smat_pool_backward) serve 16-bit inputs at r = 64, p = 65; tests switch them
+# off to compare with the smat_bgemm products they replace.
+FUSED_LONG_RANGE_BACKWARD = True
+
+
+def long_range_backward_ok(Ph, Ps, Vv) -> bool:
+    return (FUSED_LONG_RANGE_BACKWARD and Ph.dtype in (torch.bfloat16, torch.float16)
+            and Ps.dtype == Ph.dtype and Vv.dtype == Ph.dtype
+            and Ph.shape[-1] == 64 and Ps.shape[-1] == 64 and Vv.shape[-1] == 65
+            and Ph.stride(-1) == 1 and Ps.stride(-1) == 1 and Vv.stride(-1) == 1
+            and Ph.stride(1) % 8 == 0 and Ps.stride(1) % 8 == 0
+            and Ph.stride(0) % 8 == 0 and Ps.stride(0) % 8 == 0
+            and Ph.data_ptr() % 16 == 0 and Ps.data_ptr() % 16 == 0)
+
+
 def _incidence_rows(src, idx, indptr, n_out, nb, n_in, rp):
     """out[b, y] = sum_{t in row y} src[b, idx[t]] over (n_in)-row fp32 panels."""
     out = torch.empty(nb, n_out, rp, device=src.device, dtype=torch.float32)
@@ -215,7 +264,25 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
     rp = r * p
 
     # ---- long range --------------------------------------------------------
-    if T_R > 0:
+    if T_R > 0 and long_range_backward_ok(Ph, Ps, Vv):
+        # three streaming launches: the query's dPhi, dF = C^T dU straight
+        # from the token lists (dU never stored), the pool backward
+        st = stream_of(dPhi)
+        Uc = U.float().contiguous()
+        code = _code(Ph)
+        call("smat_lr_dphi", code, dH.data_ptr(), Uc.data_ptr(), dPhi.data_ptr(), nb, T_R, B, n,
+             r, p, dH.stride(0), dH.stride(1), Uc.stride(0), dPhi.stride(0), dPhi.stride(1), st)
+        tptr, tok = recent_token_lists(spec, dev)
+        nitems = N0 + (1 if n_P else 0)
+        dF = torch.empty(nb, nitems, r, p, device=dev, dtype=torch.float32)
+        call("smat_lr_dfeat", code, Ph.data_ptr(), dH.data_ptr(), tptr.data_ptr(),
+             tok.data_ptr(), dF.data_ptr(), nb, nitems, r, p, Ph.stride(0), Ph.stride(1),
+             dH.stride(0), dH.stride(1), dF.stride(0), st)
+        call("smat_pool_backward", code, Ps.data_ptr(), Vv.data_ptr(), dF.data_ptr(),
+             dPsi.data_ptr(), dVb.data_ptr(), nb, N0, n, n_P, r, p, Ps.stride(0), Ps.stride(1),
+             Vv.stride(0), Vv.stride(1), dF.stride(0), dPsi.stride(0), dPsi.stride(1),
+             dVb.stride(0), dVb.stride(1), st)
+    elif T_R > 0:
         Uc = U.float().contiguous()
         dU = torch.empty(nb, B, r, p, device=dev, dtype=torch.float32)
         full, rem = divmod(T_R, B)

@@ -305,6 +305,48 @@ def test_fused_chunk_backward(T, n):
         assert torch.isfinite(a).all()
 
 
+@pytest.mark.parametrize("T,d,n_P,gate", [(4096, 3, 0, False), (4096, 2, 0, False),
+                                          (2048, 3, 16, True), (3000, 3, 0, False)])
+def test_fused_attention_backward(T, d, n_P, gate):
+    """The whole gradient of smat_attention with bf16 inputs at head_dim 64 --
+    the fused chunk backward and the long-range kernels (smat_lr_dphi,
+    smat_lr_dfeat, smat_pool_backward) -- against the smat_bgemm products they
+    replace (max-relative < 1e-4: the kernels' hi/lo products), and against
+    fp64 autograd of the oracle on the same bf16 values at the bf16 bar
+    (norm-relative < 2e-2: the forward rounds the within-chunk scores to the
+    input dtype, as the reference does, and the fp64 oracle does not).  fp32
+    gradients, before the cast to the input dtype."""
+    from smat_attention_amd.kernels import hip_bwd as HB
+    spec = build_mask(T, d, chunk=128, n_P=n_P)
+    nb = 2
+    Phi, Psi, Vb = (x.to(torch.bfloat16) for x in _feats(nb, T, 64, seed=5, k_scale=0.125))
+    gen = torch.Generator().manual_seed(6)
+    w = torch.randn(nb, T, 64, generator=gen)
+    g = torch.rand(nb, T, generator=gen) + 0.5 if gate else None
+    _say("fused attention backward", T, d, n_P, gate)
+    xs = [x.to(DEV) for x in (Phi, Psi, Vb)]
+    gd = g.to(DEV) if g is not None else None
+    assert HB.long_range_backward_ok(*xs) and HB.fused_chunk_backward_ok(*xs, 128)
+    out, parts = A.smat_attention(*xs, spec, g=gd, return_parts=True, _no_grad_fn=True)
+    dout = w.to(DEV)
+
+    def grads():
+        return [y.cpu() for y in HB.smat_attention_grad(*xs, spec, parts["U"], parts["H"], dout,
+                                                        g=gd)[:3]]
+    got = grads()
+    try:
+        HB.FUSED_LONG_RANGE_BACKWARD = HB.FUSED_CHUNK_BACKWARD = False
+        ref = grads()
+    finally:
+        HB.FUSED_LONG_RANGE_BACKWARD = HB.FUSED_CHUNK_BACKWARD = True
+    _, r64 = _grads_ref(spec, Phi, Psi, Vb, w, g)
+    for name, a, b, c in zip(("dPhi", "dPsi", "dVb"), got, ref, r64):
+        e_chain, e_64 = _grel(a, b), _nrel(a, c)
+        _say(f"  {name}: vs bgemm {e_chain:.2e}, vs fp64 (norm) {e_64:.2e}")
+        assert torch.isfinite(a).all()
+        assert e_chain < 1e-4 and e_64 < 2e-2, name
+
+
 @pytest.mark.parametrize("d", [2, 3])
 def test_training_step_content_hashed(d):
     """The content-hashed training step at head_dim 64, T = 4096 (4 of the
