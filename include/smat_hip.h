@@ -328,6 +328,38 @@ int smat_pool_backward(int dtype, const void* psi, const void* vb, const float* 
                        int64_t d_st, int64_t e_sb, int64_t e_st, void* stream);
 
 /*
+ * Gradients of ContentAssign's hard point read and pool (src/smat/assign.py:
+ * 431-441 at anneal = 1, whose forward weights are the one-hot of pair 0) at
+ * r = 64, p = 65 for 16-bit Phi/Psi/Vb (SMAT_EUNSUPPORTED otherwise).  ent
+ * lists, for every (sequence b, cell x), the entries e = token*K + pair of
+ * sequence b whose pair points at x: ent[eoffs[b*N0 + x] .. eoffs[b*N0+x+1]),
+ * every (token, pair) once.
+ *
+ * smat_cell_read_backward: for y_i = Phi_i F[cell_i0] and upstream dY (fp32,
+ * rows of stride y_st): dPhi_i = F[x] dY_i (pair 0), dw[i*K + k] =
+ * Phi_i . (F[x] dY_i) for every entry, dF[x] = sum over pair-0 entries of
+ * Phi_i^T dY_i.  Writes every row of dPhi, dw and dF (fp32).
+ *
+ * smat_cell_pool_backward: for F[x] = sum_{cell_j0 = x} Psi_j^T Vb_j and dF:
+ * dPsi_j = Vb_j dF[x]^T and dVb_j = Psi_j dF[x] (pair 0), dw[j*K + k] =
+ * Psi_j . (Vb_j dF[x]^T) for every entry (fp32).
+ *
+ * The reference's autograd of the dense read and pool; its fused pool
+ * backward is src/smat/kernels/triton_bwd.py:203-237.
+ */
+int smat_cell_read_backward(int dtype, const void* phr, const float* dY, const float* F,
+                            const int32_t* ent, const int64_t* eoffs, float* dPhi, float* dF,
+                            float* dw, int nb, int N0, int K, int r, int p, int64_t q_sb,
+                            int64_t q_st, int64_t y_sb, int64_t y_st, int64_t f_sb,
+                            int64_t d_sb, int64_t d_st, int64_t w_sb, void* stream);
+int smat_cell_pool_backward(int dtype, const void* psi, const void* vb, const float* dF,
+                            const int32_t* ent, const int64_t* eoffs, float* dPsi, float* dVb,
+                            float* dw, int nb, int N0, int K, int r, int p, int64_t k_sb,
+                            int64_t k_st, int64_t v_sb, int64_t v_st, int64_t f_sb,
+                            int64_t d_sb, int64_t d_st, int64_t e_sb, int64_t e_st,
+                            int64_t w_sb, void* stream);
+
+/*
  * Whole forward schedule of smat_attention (src/smat/attention.py:391-455) for
  * a geometric mask: pool -> incidence (+ global channel) -> query ->
  * chunk states -> segmented scan -> chunk-local pass -> normalise.

@@ -445,6 +445,35 @@ class ContentAssign(nn.Module):
 # The hard point branch with its gradients (HIP)
 # ---------------------------------------------------------------------------
 
+# The fused backward kernels of the hard read and pool (smat_cell_read_backward,
+# smat_cell_pool_backward) serve 16-bit inputs at r = 64, p = 65; tests switch
+# them off to compare with the list reads they replace.
+FUSED_CELL_BACKWARD = True
+
+
+def _cell_backward_ok(X, Y, r_ok=64, p_ok=65):
+    return (FUSED_CELL_BACKWARD and X.dtype in (torch.bfloat16, torch.float16)
+            and X.shape[-1] == r_ok and (Y is None or (Y.dtype == X.dtype
+                                                       and Y.shape[-1] == p_ok))
+            and X.stride(-1) == 1 and X.stride(1) % 8 == 0 and X.stride(0) % 8 == 0
+            and X.data_ptr() % 16 == 0)
+
+
+def _entry_lists(idx, N0):
+    """CSR of the (token, pair) entries of every (sequence, cell): idx (nb, L, K)
+    -> entry ids token*K + pair (int32, ascending within a cell) and offsets
+    (int64, nb*N0 + 1)."""
+    nb, L, K = idx.shape
+    key = (torch.arange(nb, device=idx.device).unsqueeze(1) * N0
+           + idx.reshape(nb, L * K)).reshape(-1)
+    order = torch.argsort(key, stable=True)
+    ent = (order % (L * K)).to(torch.int32)
+    counts = torch.bincount(key, minlength=nb * N0)
+    eoffs = torch.zeros(nb * N0 + 1, device=idx.device, dtype=torch.int64)
+    eoffs[1:] = torch.cumsum(counts, 0)
+    return ent, eoffs
+
+
 def _one_hot_first(w):
     """Whether the forward weights put 1 on each row's first pair and 0 elsewhere."""
     return bool((w[..., 0] == 1).all()) and bool((w[..., 1:] == 0).all())
@@ -475,12 +504,26 @@ class _HardPool(torch.autograd.Function):
     def backward(ctx, dF):
         Pk, Vk, idxk, ck = ctx.saved_tensors
         dF = dF.float().contiguous()
+        dp, dv, dw = ctx.dtypes
+        if _cell_backward_ok(Pk, Vk):
+            # one launch per (sequence, cell): dPsi, dVb and every pair's dw
+            nb, L, r = Pk.shape
+            p, N0, K = Vk.shape[-1], dF.shape[1], idxk.shape[-1]
+            ent, eoffs = _entry_lists(idxk, N0)
+            dPsi = torch.empty(nb, L, r, device=Pk.device, dtype=torch.float32)
+            dVb = torch.empty(nb, L, p, device=Pk.device, dtype=torch.float32)
+            dwk = torch.empty(nb, L, K, device=Pk.device, dtype=torch.float32)
+            call("smat_cell_pool_backward", _code(Pk, "ContentAssign"), Pk.data_ptr(),
+                 Vk.data_ptr(), dF.data_ptr(), ent.data_ptr(), eoffs.data_ptr(), dPsi.data_ptr(),
+                 dVb.data_ptr(), dwk.data_ptr(), nb, N0, K, r, p, Pk.stride(0), Pk.stride(1),
+                 Vk.stride(0), Vk.stride(1), dF.stride(0), dPsi.stride(0), dPsi.stride(1),
+                 dVb.stride(0), dVb.stride(1), dwk.stride(0), stream_of(dF))
+            return dPsi.to(dp), dVb.to(dv), dwk.to(dw), None, None, None
         dFT = dF.transpose(-1, -2).contiguous()
         P32, V32 = Pk.float(), _f32_rows(Vk)         # Vb rows of p floats, 16-byte aligned
         dPsi = _read_lists(V32, dFT, ck, ctx.lists)
         dVb = _read_lists(P32, dF, ck, ctx.lists)
         dwk = _pair_dw(P32, dPsi, V32, dFT, idxk)
-        dp, dv, dw = ctx.dtypes
         return dPsi.to(dp), dVb.to(dv), dwk.to(dw), None, None, None
 
 
@@ -514,13 +557,30 @@ class _HardRead(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dY):
         Phr, F, idxq, cq = ctx.saved_tensors
+        dp, dw = ctx.dtypes
+        if _cell_backward_ok(Phr, None) and F.shape[-1] == 65 and F.shape[-2] == 64:
+            # one launch per (sequence, cell): dPhi, dF and every pair's dw
+            dYc = dY.float()
+            dYc = dYc if dYc.stride(-1) == 1 else dYc.contiguous()
+            Fc = F.float().contiguous()
+            nb, L, r = Phr.shape
+            N0, p, K = Fc.shape[1], Fc.shape[-1], idxq.shape[-1]
+            ent, eoffs = _entry_lists(idxq, N0)
+            dPhi = torch.empty(nb, L, r, device=Phr.device, dtype=torch.float32)
+            dF = torch.empty(nb, N0, r, p, device=Phr.device, dtype=torch.float32)
+            dwq = torch.empty(nb, L, K, device=Phr.device, dtype=torch.float32)
+            call("smat_cell_read_backward", _code(Phr, "ContentAssign"), Phr.data_ptr(),
+                 dYc.data_ptr(), Fc.data_ptr(), ent.data_ptr(), eoffs.data_ptr(),
+                 dPhi.data_ptr(), dF.data_ptr(), dwq.data_ptr(), nb, N0, K, r, p, Phr.stride(0),
+                 Phr.stride(1), dYc.stride(0), dYc.stride(1), Fc.stride(0), dPhi.stride(0),
+                 dPhi.stride(1), dwq.stride(0), stream_of(Fc))
+            return dPhi.to(dp), dF, dwq.to(dw), None, None
         dY = _f32_rows(dY)                            # rows of p floats, 16-byte aligned
         Ph32 = Phr.float()
         FT = F.transpose(-1, -2).contiguous()
         dPhi = _read_lists(dY, FT, cq, ctx.lists)
         dF = _gram_lists(Ph32, dY, cq, F.shape[1], ctx.lists)
         dwq = _pair_dw(Ph32, dPhi, dY, FT, idxq)
-        dp, dw = ctx.dtypes
         return dPhi.to(dp), dF, dwq.to(dw), None, None
 
 

@@ -1,0 +1,381 @@
+// Gradients of the content-addressed point read and pool at the training
+// shape (16-bit Phi, Psi, Vb; r = 64, p = 65; fp32 tables), for the hard
+// forward of ContentAssign (assign.py:431-441 at anneal = 1): every token j
+// carries K (cell, weight) pairs whose forward weights are the one-hot of
+// its chosen cell (pair 0), and whose weights still take gradients.
+//
+//   read   y_i = Phi_i F[c_i]  ->  v = F[x] dy_i for every pair (i, k) with
+//          cell x:  dPhi_i = v (pair 0),  dw_ik = Phi_i . v,
+//          dF[x] = sum over pair-0 entries of Phi_i^T dy_i
+//   pool   F[x] = sum_{c_j = x} Psi_j^T Vb_j  ->  v = dF[x] Vb_j:
+//          dPsi_j = v, dVb_j = Psi_j dF[x] (pair 0),  dw_jk = Psi_j . v
+//
+// One workgroup of four waves per (sequence, cell), over the CSR list of the
+// (token, pair) entries that point at the cell; the cell's r x p table is
+// staged in LDS once.  The products against the table run on fp32 MFMA
+// (v_mfma_f32_16x16x4_f32; frag element j holds k = 4j + g): their sums over
+// value columns cancel the normaliser column against the values, which a
+// hi/lo 16-bit split would not resolve.  dF, a sum over tokens per column,
+// runs on 16-bit MFMA with dy split hi/lo, like the pool.
+#include "bwd_common.hpp"
+
+namespace smat {
+
+namespace cw {
+constexpr int kThreads = 256;
+constexpr int kRP = cb::kR * cb::kP;      // 4160
+constexpr int kStep = 32;                 // entries a step (read backward)
+}  // namespace cw
+
+__device__ __forceinline__ void cw_stage_rp(float* s, const float* src) {
+  using namespace cb;
+  for (int f = threadIdx.x; f < cw::kRP / 4; f += cw::kThreads) {
+    const float4 v = reinterpret_cast<const float4*>(src)[f];
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = 4 * f + q;
+      const int row = e / kP, col = e - row * kP;
+      s[row * kS + col] = vv[q];
+    }
+  }
+}
+
+// Sum over the four 16-lane groups of a wave (lanes r16, r16 + 16, +32, +48).
+__device__ __forceinline__ float cw_sum_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Read backward.  Per step, 32 entries are gathered into LDS: the token's Phi
+// row (swizzled 128-byte rows), its dy row (rows of kS floats), the token and
+// pair.  Wave w forms feature tile w of v^T = F dy^T for two 16-entry tiles
+// (A = F rows, loaded once; B = dy rows), stores dPhi for pair-0 entries and
+// reduces Phi . v over the lane groups and, through LDS, the waves.  The dF
+// Gram over the step's pair-0 entries follows (A = Phi^T by transposing
+// reads, B = dy columns split hi/lo, zero for other pairs): wave w owns value
+// column tile w, wave 0 also tile 4 (column 64).
+// ---------------------------------------------------------------------------
+template <typename In>
+__global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
+    const In* __restrict__ phr, const float* __restrict__ dY, const float* __restrict__ F,
+    const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, float* __restrict__ dPhi,
+    float* __restrict__ dF, float* __restrict__ dw, int N0, int K, int64_t q_sb, int64_t q_st,
+    int64_t y_sb, int64_t y_st, int64_t f_sb, int64_t d_sb, int64_t d_st, int64_t w_sb) {
+  using namespace cb;
+  typedef typename Traits<In>::frag Frag;
+  typedef typename Traits<In>::half_frag Half;
+  __shared__ __attribute__((aligned(16))) float sF[kR * kS];
+  __shared__ __attribute__((aligned(16))) uint4 sPh[cw::kStep * kRowChunks];
+  __shared__ __attribute__((aligned(16))) float sY[cw::kStep * kS];
+  __shared__ float sDot[4][cw::kStep];
+  __shared__ int sTok[cw::kStep], sPair[cw::kStep];
+
+  const int x = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int64_t beg = eoffs[b * N0 + x], end = eoffs[b * N0 + x + 1];
+  cw_stage_rp(sF, F + b * f_sb + (int64_t)x * cw::kRP);
+  __syncthreads();
+
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int lane = lane_id(), r16 = lane & 15, g = lane >> 4;
+  f32x8 fa[2];
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) fa[kc][j] = sF[(16 * w + r16) * kS + 32 * kc + 4 * j + g];
+  const float fat = g == 0 ? sF[(16 * w + r16) * kS + 64] : 0.f;
+
+  const In* phb = phr + b * q_sb;
+  const float* dYb = dY + b * y_sb;
+  float* dPb = dPhi + b * d_sb;
+  float* dwb = dw + b * w_sb;
+  f32x4 acc[4], acc4[4];
+#pragma unroll
+  for (int at = 0; at < 4; ++at) {
+    acc[at] = zero4();
+    acc4[at] = zero4();
+  }
+  constexpr int kYN = cw::kStep * kP;                          // 2080
+  constexpr int kYIt = (kYN + cw::kThreads - 1) / cw::kThreads;   // 9
+  for (int64_t s0 = beg; s0 < end; s0 += cw::kStep) {
+    const int ts = tid >> 3, kk = tid & 7;
+    const bool okt = s0 + ts < end;
+    const int e = ent[okt ? s0 + ts : beg];
+    const int tok = e / K;
+    uint4 pv = *reinterpret_cast<const uint4*>(phb + (int64_t)tok * q_st + 8 * kk);
+    if (!okt) pv = make_uint4(0, 0, 0, 0);
+    float yv[kYIt];
+#pragma unroll
+    for (int u = 0; u < kYIt; ++u) {
+      const int q = tid + cw::kThreads * u;
+      const int qq = q < kYN ? q : 0;
+      const int slot = qq / kP, col = qq - slot * kP;
+      const bool ok = q < kYN && s0 + slot < end;
+      const int ty = ent[ok ? s0 + slot : beg] / K;
+      yv[u] = ok ? dYb[(int64_t)ty * y_st + col] : 0.f;
+    }
+    if (s0 > beg) __syncthreads();                   // the last step's readers are done
+    sPh[cb_slot(ts, kk)] = pv;
+    if (kk == 0) {
+      sTok[ts] = okt ? tok : -1;
+      sPair[ts] = e - tok * K;
+    }
+#pragma unroll
+    for (int u = 0; u < kYIt; ++u) {
+      const int q = tid + cw::kThreads * u;
+      if (q < kYN) {
+        const int slot = q / kP, col = q - slot * kP;
+        sY[slot * kS + col] = yv[u];
+      }
+    }
+    __syncthreads();
+
+    // v = F dy for the two 16-entry tiles; dPhi (pair 0) and Phi . v
+#pragma unroll
+    for (int et = 0; et < 2; ++et) {
+      const int es = 16 * et + r16;
+      f32x4 v = zero4();
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        f32x8 yb;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) yb[j] = sY[es * kS + 32 * kc + 4 * j + g];
+        v = mma(v, fa[kc], yb);
+      }
+      v = __builtin_amdgcn_mfma_f32_16x16x4f32(fat, g == 0 ? sY[es * kS + 64] : 0.f, v, 0, 0, 0);
+      // lane (es, g) holds v[16w + 4g + i]; Phi of the entry at the same columns
+      const Half ph = *reinterpret_cast<const Half*>(
+          reinterpret_cast<const char*>(sPh + cb_slot(es, 2 * w + (g >> 1))) + 8 * (g & 1));
+      float pd = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pd += to_f32(ph[i]) * v[i];
+      pd = cw_sum_groups(pd);
+      if (g == 0) sDot[w][es] = pd;
+      const int t = sTok[es];
+      if (t >= 0 && sPair[es] == 0)
+        *reinterpret_cast<float4*>(dPb + (int64_t)t * d_st + 16 * w + 4 * g) =
+            make_float4(v[0], v[1], v[2], v[3]);
+    }
+
+    // dF += Phi^T dy over the pair-0 entries of the step
+    auto bfrag = [&](int ct, Frag& hi, Frag& lo) {
+      const int col = 16 * ct + r16;
+      const bool okc = col < kP;
+      const int cc = okc ? col : 0;
+#pragma unroll
+      for (int e8 = 0; e8 < 8; ++e8) {
+        const int es = 8 * g + e8;
+        const bool use = okc && sTok[es] >= 0 && sPair[es] == 0;
+        const float v = use ? sY[es * kS + cc] : 0.f;
+        In hh, ll;
+        split2<In>(v, hh, ll);
+        hi[e8] = hh;
+        lo[e8] = ll;
+      }
+    };
+    Frag bh, bl, b4h, b4l;
+    bfrag(w, bh, bl);
+    if (w == 0) bfrag(4, b4h, b4l);
+#pragma unroll
+    for (int at = 0; at < 4; ++at) {
+      const int k = 2 * at + ((r16 & 3) >> 1), half = r16 & 1;
+      const Half lo4 = cb_tr<In>(sPh, 8 * g + (r16 >> 2), k, half);
+      const Half hi4 = cb_tr<In>(sPh, 8 * g + 4 + (r16 >> 2), k, half);
+      Frag pa;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pa[i] = lo4[i];
+        pa[4 + i] = hi4[i];
+      }
+      acc[at] = mma(acc[at], pa, bh);
+      acc[at] = mma(acc[at], pa, bl);
+      if (w == 0) {
+        acc4[at] = mma(acc4[at], pa, b4h);
+        acc4[at] = mma(acc4[at], pa, b4l);
+      }
+    }
+    __syncthreads();                                 // sDot complete
+    if (tid < cw::kStep && sTok[tid] >= 0)
+      dwb[(int64_t)sTok[tid] * K + sPair[tid]] =
+          (sDot[0][tid] + sDot[1][tid]) + (sDot[2][tid] + sDot[3][tid]);
+  }
+  // lane (c = 16w + r16, g) holds dF[16 at + 4g + i][c]
+  float* out = dF + b * f_sb + (int64_t)x * cw::kRP;
+#pragma unroll
+  for (int at = 0; at < 4; ++at)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[(16 * at + 4 * g + i) * kP + 16 * w + r16] = acc[at][i];
+  if (w == 0 && r16 == 0) {
+#pragma unroll
+    for (int at = 0; at < 4; ++at)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[(16 * at + 4 * g + i) * kP + 64] = acc4[at][i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pool backward.  dF[x] staged once; per 16 entries, wave w forms feature
+// tile w of v^T = dF Vb^T (A = dF rows) and value-column tile w of
+// dVb^T = dF^T Psi^T (A = dF columns; wave 0 also column 64), B from the
+// entries' own Vb and Psi rows in global memory.  Stores dPsi and dVb for
+// pair-0 entries and Psi . v for every entry.
+// ---------------------------------------------------------------------------
+template <typename In>
+__global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
+    const In* __restrict__ psi, const In* __restrict__ vb, const float* __restrict__ dF,
+    const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, float* __restrict__ dPsi,
+    float* __restrict__ dVb, float* __restrict__ dw, int N0, int K, int64_t k_sb, int64_t k_st,
+    int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st, int64_t e_sb,
+    int64_t e_st, int64_t w_sb) {
+  using namespace cb;
+  __shared__ __attribute__((aligned(16))) float sF[kR * kS];
+  __shared__ float sDot[4][16];
+  const int x = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int64_t beg = eoffs[b * N0 + x], end = eoffs[b * N0 + x + 1];
+  if (beg == end) return;                            // uniform over the workgroup
+  cw_stage_rp(sF, dF + b * f_sb + (int64_t)x * cw::kRP);
+  __syncthreads();
+
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int lane = lane_id(), r16 = lane & 15, g = lane >> 4;
+  // A operands: dF rows a = 16w + r16 (for v) and dF columns c = 16w + r16
+  // (for dVb; wave 0 also c = 64 + r16, of which only 64 exists)
+  f32x8 fr[2], fc[2], fc4[2];
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      fr[kc][j] = sF[(16 * w + r16) * kS + 32 * kc + 4 * j + g];
+      fc[kc][j] = sF[(32 * kc + 4 * j + g) * kS + 16 * w + r16];
+      fc4[kc][j] = r16 == 0 ? sF[(32 * kc + 4 * j + g) * kS + 64] : 0.f;
+    }
+  const float frt = g == 0 ? sF[(16 * w + r16) * kS + 64] : 0.f;
+
+  const In* psib = psi + b * k_sb;
+  const In* vbb = vb + b * v_sb;
+  float* dPb = dPsi + b * d_sb;
+  float* dVbb = dVb + b * e_sb;
+  float* dwb = dw + b * w_sb;
+  for (int64_t s0 = beg; s0 < end; s0 += 16) {
+    const bool ok = s0 + r16 < end;
+    const int e = ent[ok ? s0 + r16 : beg];
+    const int tok = e / K, pair = e - tok * K;
+    const In* vrow = vbb + (int64_t)tok * v_st;
+    const In* prow = psib + (int64_t)tok * k_st;
+    f32x8 vbf[2], psf[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        vbf[kc][j] = ok ? to_f32(vrow[32 * kc + 4 * j + g]) : 0.f;
+        psf[kc][j] = ok ? to_f32(prow[32 * kc + 4 * j + g]) : 0.f;
+      }
+    const float vbt = ok && g == 0 ? to_f32(vrow[64]) : 0.f;
+    // v^T tile w: lane (entry r16, g) holds v[16w + 4g + i]
+    f32x4 v = zero4(), dv = zero4(), dv4 = zero4();
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      v = mma(v, fr[kc], vbf[kc]);
+      dv = mma(dv, fc[kc], psf[kc]);
+      if (w == 0) dv4 = mma(dv4, fc4[kc], psf[kc]);
+    }
+    v = __builtin_amdgcn_mfma_f32_16x16x4f32(frt, vbt, v, 0, 0, 0);
+    float pd = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pd += (ok ? to_f32(prow[16 * w + 4 * g + i]) : 0.f) * v[i];
+    pd = cw_sum_groups(pd);
+    if (g == 0) sDot[w][r16] = pd;
+    if (ok && pair == 0) {
+      *reinterpret_cast<float4*>(dPb + (int64_t)tok * d_st + 16 * w + 4 * g) =
+          make_float4(v[0], v[1], v[2], v[3]);
+      float* ov = dVbb + (int64_t)tok * e_st + 16 * w + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ov[i] = dv[i];
+      if (w == 0 && g == 0) dVbb[(int64_t)tok * e_st + 64] = dv4[0];
+    }
+    __syncthreads();
+    if (tid < 16 && s0 + tid < end) {
+      const int e2 = ent[s0 + tid];
+      dwb[e2] = (sDot[0][tid] + sDot[1][tid]) + (sDot[2][tid] + sDot[3][tid]);
+    }
+    __syncthreads();                                 // sDot is rewritten next step
+  }
+}
+
+static bool cw_ok(int dtype, int r, int p, int K) {
+  return (dtype == SMAT_BF16 || dtype == SMAT_F16) && r == cb::kR && p == cb::kP && K >= 1;
+}
+
+}  // namespace smat
+
+extern "C" int smat_cell_read_backward(int dtype, const void* phr, const float* dY,
+                                       const float* F, const int32_t* ent, const int64_t* eoffs,
+                                       float* dPhi, float* dF, float* dw, int nb, int N0, int K,
+                                       int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                                       int64_t y_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
+                                       int64_t w_sb, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(phr && dY && F && ent && eoffs && dPhi && dF && dw, SMAT_EINVAL,
+               "smat_cell_read_backward: null pointer");
+  SMAT_REQUIRE(nb >= 0 && N0 >= 1, SMAT_EINVAL, "smat_cell_read_backward: bad sizes");
+  SMAT_REQUIRE(cw_ok(dtype, r, p, K), SMAT_EUNSUPPORTED,
+               "smat_cell_read_backward: needs dtype bf16/f16, r=64, p=65 (got %d, %d, %d)",
+               dtype, r, p);
+  SMAT_REQUIRE(rows_vec_ok(phr, q_sb, q_st, 2) && rows_vec_ok(dPhi, d_sb, d_st, 4) &&
+                   aligned16(F) && f_sb % 4 == 0 && y_st >= p && f_sb >= (int64_t)N0 * r * p,
+               SMAT_EINVAL, "smat_cell_read_backward: Phi, dPhi and F must be 16-byte aligned");
+  SMAT_REQUIRE(N0 < 65536 * 32 && nb < 65536, SMAT_EUNSUPPORTED,
+               "smat_cell_read_backward: grid too large");
+  if (nb == 0) return SMAT_OK;
+  const dim3 grid((unsigned)N0, (unsigned)nb);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == SMAT_BF16)
+    hipLaunchKernelGGL(cell_read_bwd_kernel<bf16>, grid, dim3(cw::kThreads), 0, st,
+                       (const bf16*)phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, q_sb, q_st, y_sb,
+                       y_st, f_sb, d_sb, d_st, w_sb);
+  else
+    hipLaunchKernelGGL(cell_read_bwd_kernel<f16>, grid, dim3(cw::kThreads), 0, st,
+                       (const f16*)phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, q_sb, q_st, y_sb,
+                       y_st, f_sb, d_sb, d_st, w_sb);
+  return launch_status("smat_cell_read_backward");
+}
+
+extern "C" int smat_cell_pool_backward(int dtype, const void* psi, const void* vb,
+                                       const float* dF, const int32_t* ent, const int64_t* eoffs,
+                                       float* dPsi, float* dVb, float* dw, int nb, int N0, int K,
+                                       int r, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                                       int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
+                                       int64_t e_sb, int64_t e_st, int64_t w_sb, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(psi && vb && dF && ent && eoffs && dPsi && dVb && dw, SMAT_EINVAL,
+               "smat_cell_pool_backward: null pointer");
+  SMAT_REQUIRE(nb >= 0 && N0 >= 1, SMAT_EINVAL, "smat_cell_pool_backward: bad sizes");
+  SMAT_REQUIRE(cw_ok(dtype, r, p, K), SMAT_EUNSUPPORTED,
+               "smat_cell_pool_backward: needs dtype bf16/f16, r=64, p=65 (got %d, %d, %d)",
+               dtype, r, p);
+  SMAT_REQUIRE(rows_vec_ok(dPsi, d_sb, d_st, 4) && aligned16(dF) && f_sb % 4 == 0 &&
+                   k_st >= r && v_st >= p && e_st >= p && f_sb >= (int64_t)N0 * r * p,
+               SMAT_EINVAL, "smat_cell_pool_backward: dPsi and dF must be 16-byte aligned");
+  SMAT_REQUIRE(N0 < 65536 * 32 && nb < 65536, SMAT_EUNSUPPORTED,
+               "smat_cell_pool_backward: grid too large");
+  if (nb == 0) return SMAT_OK;
+  const dim3 grid((unsigned)N0, (unsigned)nb);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == SMAT_BF16)
+    hipLaunchKernelGGL(cell_pool_bwd_kernel<bf16>, grid, dim3(cw::kThreads), 0, st,
+                       (const bf16*)psi, (const bf16*)vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K,
+                       k_sb, k_st, v_sb, v_st, f_sb, d_sb, d_st, e_sb, e_st, w_sb);
+  else
+    hipLaunchKernelGGL(cell_pool_bwd_kernel<f16>, grid, dim3(cw::kThreads), 0, st,
+                       (const f16*)psi, (const f16*)vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K,
+                       k_sb, k_st, v_sb, v_st, f_sb, d_sb, d_st, e_sb, e_st, w_sb);
+  return launch_status("smat_cell_pool_backward");
+}

@@ -348,6 +348,49 @@ def test_fused_attention_backward(T, d, n_P, gate):
 
 
 @pytest.mark.parametrize("d", [2, 3])
+def test_fused_cell_backward(d):
+    """ContentAssign's hard point read and pool at head_dim 64, bf16: the fused
+    backward kernels (smat_cell_read_backward, smat_cell_pool_backward) against
+    the list reads and pair sums they replace, same forward.  The hash
+    parameters' gradients (through every pair's weight gradient) within 1e-4;
+    dQ, dK, dV, cast to bf16 by autograd, within 2e-3 norm-relative."""
+    from smat_attention_amd import assign as AS
+    B, H, hd, T = 2, 4, 64, 2048
+    spec = build_mask(T, d, chunk=128)
+    n = spec.n
+    gen = torch.Generator().manual_seed(70 + d)
+    bf = torch.bfloat16
+    Q = torch.randn(B * H, T, hd, generator=gen).to(bf)
+    K = (torch.randn(B * H, T, hd, generator=gen) / hd ** 0.5).to(bf)
+    V = torch.randn(B * H, T, hd, generator=gen).to(bf)
+    dY = torch.randn(B * H, T - n, hd + 1, generator=gen).to(DEV)
+    torch.manual_seed(7)
+    m = AS.ContentAssign(H, H * hd, spec, mode="point").to(DEV)
+    phi = A.make_phi(hd, hd, device=DEV, dtype=bf, seed=0)
+    _say("fused cell backward", d, spec.N0)
+
+    def run(fused):
+        AS.FUSED_CELL_BACKWARD = fused
+        try:
+            xs = [t.to(DEV).requires_grad_(True) for t in (Q, K, V)]
+            Phi, Psi, Vb = A.featurise(*xs, phi)
+            u = xs[1].reshape(B, H, T, hd).transpose(1, 2).reshape(B, T, H * hd).float()
+            m.zero_grad()
+            Y = m(u, Phi, Psi, Vb, n)
+            (Y * dY).sum().backward()
+            return ([x.grad.float().cpu() for x in xs]
+                    + [getattr(m, k).grad.detach().cpu() for k in ("W", "gamma", "b")])
+        finally:
+            AS.FUSED_CELL_BACKWARD = True
+    g1, g0 = run(True), run(False)
+    for name, a, b in zip(("dQ", "dK", "dV", "dW", "dgamma", "db"), g1, g0):
+        e = _nrel(a, b) if name in ("dQ", "dK", "dV") else _grel(a, b)
+        _say(f"  {name}: {e:.2e}")
+        assert torch.isfinite(a).all()
+        assert e < (2e-3 if name in ("dQ", "dK", "dV") else 1e-4), name
+
+
+@pytest.mark.parametrize("d", [2, 3])
 def test_training_step_content_hashed(d):
     """The content-hashed training step at head_dim 64, T = 4096 (4 of the
     configuration's 12 heads, so the fp64 oracle finishes in seconds): the
