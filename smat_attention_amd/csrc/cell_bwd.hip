@@ -48,15 +48,49 @@ __device__ __forceinline__ float cw_sum_groups(float v) {
   return v;
 }
 
+// One step's gather: 32 entries, eight threads per entry (slot = tid / 8,
+// sub = tid % 8).  A thread loads its entry's id once, then a 16-byte piece of
+// the 64-wide 16-bit row (columns 8 sub .. +7) and every eighth element of the
+// 65-wide row (columns sub + 8u).  Loads land in registers and the kernel
+// writes them to LDS at the top of the step.  Issuing the next step's gather
+// before the current step's products overlaps its two dependent latencies
+// (entry id, then rows) with them.  The per-entry token, pair and dot
+// partials are read after the step's last barrier, so they alternate
+// between two buffers by step parity while the next step's rows are written.
+template <typename In, typename Row65>
+struct CwGather {
+  static constexpr int kU = 9;                 // ceil(65 / 8)
+  int tok, pair;
+  bool ok;
+  uint4 r64;
+  Row65 r65[kU];
+  __device__ __forceinline__ void load(const int32_t* ent, int64_t s0, int64_t beg, int64_t end,
+                                       int K, const In* rows64, int64_t st64, const Row65* rows65,
+                                       int64_t st65, int tid) {
+    const int slot = tid >> 3, sub = tid & 7;
+    ok = s0 + slot < end;
+    const int e = ent[ok ? s0 + slot : beg];
+    tok = e / K;
+    pair = e - tok * K;
+    r64 = *reinterpret_cast<const uint4*>(rows64 + (int64_t)tok * st64 + 8 * sub);
+    const Row65* r = rows65 + (int64_t)tok * st65;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int col = sub + 8 * u;
+      r65[u] = r[col < cb::kP ? col : 0];
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
-// Read backward.  Per step, 32 entries are gathered into LDS: the token's Phi
-// row (swizzled 128-byte rows), its dy row (rows of kS floats), the token and
-// pair.  Wave w forms feature tile w of v^T = F dy^T for two 16-entry tiles
-// (A = F rows, loaded once; B = dy rows), stores dPhi for pair-0 entries and
-// reduces Phi . v over the lane groups and, through LDS, the waves.  The dF
-// Gram over the step's pair-0 entries follows (A = Phi^T by transposing
-// reads, B = dy columns split hi/lo, zero for other pairs): wave w owns value
-// column tile w, wave 0 also tile 4 (column 64).
+// Read backward.  Per step of 32 entries: the entries' Phi rows (LDS,
+// swizzled 128-byte rows) and dy rows (fp32 rows of kS), token and pair.
+// Wave w forms feature tile w of v^T = F dy^T for two 16-entry tiles (A = F
+// rows, loaded once; B = dy rows), stores dPhi for pair-0 entries and reduces
+// Phi . v over the lane groups and, through LDS, the waves.  The dF Gram over
+// the step's pair-0 entries follows (A = Phi^T by transposing reads, B = dy
+// columns split hi/lo, zero for other pairs): wave w owns value-column tile
+// w, wave 0 also tile 4 (column 64).
 // ---------------------------------------------------------------------------
 template <typename In>
 __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
@@ -70,13 +104,17 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
   __shared__ __attribute__((aligned(16))) float sF[kR * kS];
   __shared__ __attribute__((aligned(16))) uint4 sPh[cw::kStep * kRowChunks];
   __shared__ __attribute__((aligned(16))) float sY[cw::kStep * kS];
-  __shared__ float sDot[4][cw::kStep];
-  __shared__ int sTok[cw::kStep], sPair[cw::kStep];
+  __shared__ float sDotB[2][4][cw::kStep];
+  __shared__ int sTokB[2][cw::kStep], sPairB[2][cw::kStep];
 
   const int x = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x;
   const int64_t beg = eoffs[b * N0 + x], end = eoffs[b * N0 + x + 1];
+  const In* phb = phr + b * q_sb;
+  const float* dYb = dY + b * y_sb;
+  CwGather<In, float> ga;
+  if (beg < end) ga.load(ent, beg, beg, end, K, phb, q_st, dYb, y_st, tid);
   cw_stage_rp(sF, F + b * f_sb + (int64_t)x * cw::kRP);
   __syncthreads();
 
@@ -89,8 +127,6 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
     for (int j = 0; j < 8; ++j) fa[kc][j] = sF[(16 * w + r16) * kS + 32 * kc + 4 * j + g];
   const float fat = g == 0 ? sF[(16 * w + r16) * kS + 64] : 0.f;
 
-  const In* phb = phr + b * q_sb;
-  const float* dYb = dY + b * y_sb;
   float* dPb = dPhi + b * d_sb;
   float* dwb = dw + b * w_sb;
   f32x4 acc[4], acc4[4];
@@ -99,40 +135,26 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
     acc[at] = zero4();
     acc4[at] = zero4();
   }
-  constexpr int kYN = cw::kStep * kP;                          // 2080
-  constexpr int kYIt = (kYN + cw::kThreads - 1) / cw::kThreads;   // 9
   for (int64_t s0 = beg; s0 < end; s0 += cw::kStep) {
-    const int ts = tid >> 3, kk = tid & 7;
-    const bool okt = s0 + ts < end;
-    const int e = ent[okt ? s0 + ts : beg];
-    const int tok = e / K;
-    uint4 pv = *reinterpret_cast<const uint4*>(phb + (int64_t)tok * q_st + 8 * kk);
-    if (!okt) pv = make_uint4(0, 0, 0, 0);
-    float yv[kYIt];
+    const int par = (int)(((s0 - beg) / cw::kStep) & 1);
+    float (*sDot)[cw::kStep] = sDotB[par];
+    int* sTok = sTokB[par];
+    int* sPair = sPairB[par];
+    {
+      const int slot = tid >> 3, sub = tid & 7;
+      sPh[cb_slot(slot, sub)] = ga.ok ? ga.r64 : make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int u = 0; u < kYIt; ++u) {
-      const int q = tid + cw::kThreads * u;
-      const int qq = q < kYN ? q : 0;
-      const int slot = qq / kP, col = qq - slot * kP;
-      const bool ok = q < kYN && s0 + slot < end;
-      const int ty = ent[ok ? s0 + slot : beg] / K;
-      yv[u] = ok ? dYb[(int64_t)ty * y_st + col] : 0.f;
-    }
-    if (s0 > beg) __syncthreads();                   // the last step's readers are done
-    sPh[cb_slot(ts, kk)] = pv;
-    if (kk == 0) {
-      sTok[ts] = okt ? tok : -1;
-      sPair[ts] = e - tok * K;
-    }
-#pragma unroll
-    for (int u = 0; u < kYIt; ++u) {
-      const int q = tid + cw::kThreads * u;
-      if (q < kYN) {
-        const int slot = q / kP, col = q - slot * kP;
-        sY[slot * kS + col] = yv[u];
+      for (int u = 0; u < CwGather<In, float>::kU; ++u) {
+        const int col = sub + 8 * u;
+        if (col < kP) sY[slot * kS + col] = ga.ok ? ga.r65[u] : 0.f;
+      }
+      if (sub == 0) {
+        sTok[slot] = ga.ok ? ga.tok : -1;
+        sPair[slot] = ga.pair;
       }
     }
     __syncthreads();
+    if (s0 + cw::kStep < end) ga.load(ent, s0 + cw::kStep, beg, end, K, phb, q_st, dYb, y_st, tid);
 
     // v = F dy for the two 16-entry tiles; dPhi (pair 0) and Phi . v
 #pragma unroll
@@ -177,9 +199,8 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
         lo[e8] = ll;
       }
     };
-    Frag bh, bl, b4h, b4l;
+    Frag bh, bl;
     bfrag(w, bh, bl);
-    if (w == 0) bfrag(4, b4h, b4l);
 #pragma unroll
     for (int at = 0; at < 4; ++at) {
       const int k = 2 * at + ((r16 & 3) >> 1), half = r16 & 1;
@@ -194,11 +215,13 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
       acc[at] = mma(acc[at], pa, bh);
       acc[at] = mma(acc[at], pa, bl);
       if (w == 0) {
+        Frag b4h, b4l;
+        bfrag(4, b4h, b4l);
         acc4[at] = mma(acc4[at], pa, b4h);
         acc4[at] = mma(acc4[at], pa, b4l);
       }
     }
-    __syncthreads();                                 // sDot complete
+    __syncthreads();                                 // sDot complete; LDS free for the next step
     if (tid < cw::kStep && sTok[tid] >= 0)
       dwb[(int64_t)sTok[tid] * K + sPair[tid]] =
           (sDot[0][tid] + sDot[1][tid]) + (sDot[2][tid] + sDot[3][tid]);
@@ -218,11 +241,11 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Pool backward.  dF[x] staged once; per 16 entries, wave w forms feature
-// tile w of v^T = dF Vb^T (A = dF rows) and value-column tile w of
-// dVb^T = dF^T Psi^T (A = dF columns; wave 0 also column 64), B from the
-// entries' own Vb and Psi rows in global memory.  Stores dPsi and dVb for
-// pair-0 entries and Psi . v for every entry.
+// Pool backward.  dF[x] staged once; per step of 32 entries, their Psi and Vb
+// rows are staged as fp32 rows of kS (LDS).  Wave w forms feature tile w of
+// v^T = dF Vb^T (A = dF rows) and value-column tile w of dVb^T = dF^T Psi^T
+// (A = dF columns; wave 0 also column 64) for two 16-entry tiles, stores dPsi
+// and dVb for pair-0 entries and Psi . v for every entry.
 // ---------------------------------------------------------------------------
 template <typename In>
 __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
@@ -233,12 +256,19 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
     int64_t e_st, int64_t w_sb) {
   using namespace cb;
   __shared__ __attribute__((aligned(16))) float sF[kR * kS];
-  __shared__ float sDot[4][16];
+  __shared__ __attribute__((aligned(16))) float sP[cw::kStep * kS];
+  __shared__ __attribute__((aligned(16))) float sV[cw::kStep * kS];
+  __shared__ float sDotB[2][4][cw::kStep];
+  __shared__ int sTokB[2][cw::kStep], sPairB[2][cw::kStep];
   const int x = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x;
   const int64_t beg = eoffs[b * N0 + x], end = eoffs[b * N0 + x + 1];
   if (beg == end) return;                            // uniform over the workgroup
+  const In* psib = psi + b * k_sb;
+  const In* vbb = vb + b * v_sb;
+  CwGather<In, In> ga;
+  ga.load(ent, beg, beg, end, K, psib, k_st, vbb, v_st, tid);
   cw_stage_rp(sF, dF + b * f_sb + (int64_t)x * cw::kRP);
   __syncthreads();
 
@@ -246,65 +276,92 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
   const int lane = lane_id(), r16 = lane & 15, g = lane >> 4;
   // A operands: dF rows a = 16w + r16 (for v) and dF columns c = 16w + r16
   // (for dVb; wave 0 also c = 64 + r16, of which only 64 exists)
-  f32x8 fr[2], fc[2], fc4[2];
+  f32x8 fr[2], fc[2];
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       fr[kc][j] = sF[(16 * w + r16) * kS + 32 * kc + 4 * j + g];
       fc[kc][j] = sF[(32 * kc + 4 * j + g) * kS + 16 * w + r16];
-      fc4[kc][j] = r16 == 0 ? sF[(32 * kc + 4 * j + g) * kS + 64] : 0.f;
     }
   const float frt = g == 0 ? sF[(16 * w + r16) * kS + 64] : 0.f;
 
-  const In* psib = psi + b * k_sb;
-  const In* vbb = vb + b * v_sb;
   float* dPb = dPsi + b * d_sb;
   float* dVbb = dVb + b * e_sb;
   float* dwb = dw + b * w_sb;
-  for (int64_t s0 = beg; s0 < end; s0 += 16) {
-    const bool ok = s0 + r16 < end;
-    const int e = ent[ok ? s0 + r16 : beg];
-    const int tok = e / K, pair = e - tok * K;
-    const In* vrow = vbb + (int64_t)tok * v_st;
-    const In* prow = psib + (int64_t)tok * k_st;
-    f32x8 vbf[2], psf[2];
+  for (int64_t s0 = beg; s0 < end; s0 += cw::kStep) {
+    const int par = (int)(((s0 - beg) / cw::kStep) & 1);
+    float (*sDot)[cw::kStep] = sDotB[par];
+    int* sTok = sTokB[par];
+    int* sPair = sPairB[par];
+    {
+      const int slot = tid >> 3, sub = tid & 7;
+      const typename Traits<In>::frag pv = __builtin_bit_cast(typename Traits<In>::frag, ga.r64);
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
+      for (int i = 0; i < 8; ++i) sP[slot * kS + 8 * sub + i] = ga.ok ? to_f32(pv[i]) : 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        vbf[kc][j] = ok ? to_f32(vrow[32 * kc + 4 * j + g]) : 0.f;
-        psf[kc][j] = ok ? to_f32(prow[32 * kc + 4 * j + g]) : 0.f;
+      for (int u = 0; u < CwGather<In, In>::kU; ++u) {
+        const int col = sub + 8 * u;
+        if (col < kP) sV[slot * kS + col] = ga.ok ? to_f32(ga.r65[u]) : 0.f;
       }
-    const float vbt = ok && g == 0 ? to_f32(vrow[64]) : 0.f;
-    // v^T tile w: lane (entry r16, g) holds v[16w + 4g + i]
-    f32x4 v = zero4(), dv = zero4(), dv4 = zero4();
-#pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
-      v = mma(v, fr[kc], vbf[kc]);
-      dv = mma(dv, fc[kc], psf[kc]);
-      if (w == 0) dv4 = mma(dv4, fc4[kc], psf[kc]);
-    }
-    v = __builtin_amdgcn_mfma_f32_16x16x4f32(frt, vbt, v, 0, 0, 0);
-    float pd = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pd += (ok ? to_f32(prow[16 * w + 4 * g + i]) : 0.f) * v[i];
-    pd = cw_sum_groups(pd);
-    if (g == 0) sDot[w][r16] = pd;
-    if (ok && pair == 0) {
-      *reinterpret_cast<float4*>(dPb + (int64_t)tok * d_st + 16 * w + 4 * g) =
-          make_float4(v[0], v[1], v[2], v[3]);
-      float* ov = dVbb + (int64_t)tok * e_st + 16 * w + 4 * g;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ov[i] = dv[i];
-      if (w == 0 && g == 0) dVbb[(int64_t)tok * e_st + 64] = dv4[0];
+      if (sub == 0) {
+        sTok[slot] = ga.ok ? ga.tok : -1;
+        sPair[slot] = ga.pair;
+      }
     }
     __syncthreads();
-    if (tid < 16 && s0 + tid < end) {
-      const int e2 = ent[s0 + tid];
-      dwb[e2] = (sDot[0][tid] + sDot[1][tid]) + (sDot[2][tid] + sDot[3][tid]);
+    if (s0 + cw::kStep < end) ga.load(ent, s0 + cw::kStep, beg, end, K, psib, k_st, vbb, v_st, tid);
+
+#pragma unroll
+    for (int et = 0; et < 2; ++et) {
+      const int es = 16 * et + r16;
+      f32x4 v = zero4(), dv = zero4();
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        f32x8 vbf, psf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          vbf[j] = sV[es * kS + 32 * kc + 4 * j + g];
+          psf[j] = sP[es * kS + 32 * kc + 4 * j + g];
+        }
+        v = mma(v, fr[kc], vbf);
+        dv = mma(dv, fc[kc], psf);
+      }
+      v = __builtin_amdgcn_mfma_f32_16x16x4f32(frt, g == 0 ? sV[es * kS + 64] : 0.f, v, 0, 0, 0);
+      // lane (es, g): v[16w + 4g + i] (dPsi), dv[16w + 4g + i] (dVb columns)
+      float pd = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pd += sP[es * kS + 16 * w + 4 * g + i] * v[i];
+      pd = cw_sum_groups(pd);
+      if (g == 0) sDot[w][es] = pd;
+      const int t = sTok[es];
+      if (t >= 0 && sPair[es] == 0) {
+        *reinterpret_cast<float4*>(dPb + (int64_t)t * d_st + 16 * w + 4 * g) =
+            make_float4(v[0], v[1], v[2], v[3]);
+        float* ov = dVbb + (int64_t)t * e_st + 16 * w + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov[i] = dv[i];
+      }
+      if (w == 0) {
+        // column 64 of dVb: sum_a dF[a][64] Psi[a] (lane group 0, slot 0)
+        f32x4 d4 = zero4();
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+          f32x8 a4, psf;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            a4[j] = r16 == 0 ? sF[(32 * kc + 4 * j + g) * kS + 64] : 0.f;
+            psf[j] = sP[es * kS + 32 * kc + 4 * j + g];
+          }
+          d4 = mma(d4, a4, psf);
+        }
+        if (g == 0 && t >= 0 && sPair[es] == 0) dVbb[(int64_t)t * e_st + 64] = d4[0];
+      }
     }
-    __syncthreads();                                 // sDot is rewritten next step
+    __syncthreads();                                 // sDot complete; LDS free for the next step
+    if (tid < cw::kStep && sTok[tid] >= 0)
+      dwb[(int64_t)sTok[tid] * K + sPair[tid]] =
+          (sDot[0][tid] + sDot[1][tid]) + (sDot[2][tid] + sDot[3][tid]);
   }
 }
 
