@@ -126,4 +126,61 @@ __device__ __forceinline__ void cb_split_pair(const f32x4& a, const f32x4& b,
   }
 }
 
+// Stage one contiguous r x p fp32 matrix (16-byte aligned) in LDS rows of kS,
+// all threads of the workgroup.
+__device__ __forceinline__ void cb_stage_rp(float* s, const float* src) {
+  using namespace cb;
+  for (int f = threadIdx.x; f < (cb::kR * cb::kP) / 4; f += (int)blockDim.x) {
+    const float4 v = reinterpret_cast<const float4*>(src)[f];
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = 4 * f + q;
+      const int row = e / kP, col = e - row * kP;
+      s[row * kS + col] = vv[q];
+    }
+  }
+}
+
+// Sum over the four 16-lane groups of a wave (lanes r16, r16 + 16, +32, +48).
+__device__ __forceinline__ float cb_sum_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// One step's gather: 32 entries, eight threads per entry (slot = tid / 8,
+// sub = tid % 8).  A thread loads its entry's id once, then a 16-byte piece of
+// the 64-wide 16-bit row (columns 8 sub .. +7) and every eighth element of the
+// 65-wide row (columns sub + 8u).  Loads land in registers and the kernel
+// writes them to LDS at the top of the step.  Issuing the next step's gather
+// before the current step's products overlaps its two dependent latencies
+// (entry id, then rows) with them.  The per-entry token, pair and dot
+// partials are read after the step's last barrier, so they alternate
+// between two buffers by step parity while the next step's rows are written.
+template <typename In, typename Row65>
+struct CbGather {
+  static constexpr int kU = 9;                 // ceil(65 / 8)
+  int tok, pair;
+  bool ok;
+  uint4 r64;
+  Row65 r65[kU];
+  __device__ __forceinline__ void load(const int32_t* ent, int64_t s0, int64_t beg, int64_t end,
+                                       int K, const In* rows64, int64_t st64, const Row65* rows65,
+                                       int64_t st65, int tid) {
+    const int slot = tid >> 3, sub = tid & 7;
+    ok = s0 + slot < end;
+    const int e = ent[ok ? s0 + slot : beg];
+    tok = e / K;
+    pair = e - tok * K;
+    r64 = *reinterpret_cast<const uint4*>(rows64 + (int64_t)tok * st64 + 8 * sub);
+    const Row65* r = rows65 + (int64_t)tok * st65;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int col = sub + 8 * u;
+      r65[u] = r[col < cb::kP ? col : 0];
+    }
+  }
+};
+
 }  // namespace smat

@@ -27,61 +27,6 @@ constexpr int kRP = cb::kR * cb::kP;      // 4160
 constexpr int kStep = 32;                 // entries a step (read backward)
 }  // namespace cw
 
-__device__ __forceinline__ void cw_stage_rp(float* s, const float* src) {
-  using namespace cb;
-  for (int f = threadIdx.x; f < cw::kRP / 4; f += cw::kThreads) {
-    const float4 v = reinterpret_cast<const float4*>(src)[f];
-    const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = 4 * f + q;
-      const int row = e / kP, col = e - row * kP;
-      s[row * kS + col] = vv[q];
-    }
-  }
-}
-
-// Sum over the four 16-lane groups of a wave (lanes r16, r16 + 16, +32, +48).
-__device__ __forceinline__ float cw_sum_groups(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
-}
-
-// One step's gather: 32 entries, eight threads per entry (slot = tid / 8,
-// sub = tid % 8).  A thread loads its entry's id once, then a 16-byte piece of
-// the 64-wide 16-bit row (columns 8 sub .. +7) and every eighth element of the
-// 65-wide row (columns sub + 8u).  Loads land in registers and the kernel
-// writes them to LDS at the top of the step.  Issuing the next step's gather
-// before the current step's products overlaps its two dependent latencies
-// (entry id, then rows) with them.  The per-entry token, pair and dot
-// partials are read after the step's last barrier, so they alternate
-// between two buffers by step parity while the next step's rows are written.
-template <typename In, typename Row65>
-struct CwGather {
-  static constexpr int kU = 9;                 // ceil(65 / 8)
-  int tok, pair;
-  bool ok;
-  uint4 r64;
-  Row65 r65[kU];
-  __device__ __forceinline__ void load(const int32_t* ent, int64_t s0, int64_t beg, int64_t end,
-                                       int K, const In* rows64, int64_t st64, const Row65* rows65,
-                                       int64_t st65, int tid) {
-    const int slot = tid >> 3, sub = tid & 7;
-    ok = s0 + slot < end;
-    const int e = ent[ok ? s0 + slot : beg];
-    tok = e / K;
-    pair = e - tok * K;
-    r64 = *reinterpret_cast<const uint4*>(rows64 + (int64_t)tok * st64 + 8 * sub);
-    const Row65* r = rows65 + (int64_t)tok * st65;
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int col = sub + 8 * u;
-      r65[u] = r[col < cb::kP ? col : 0];
-    }
-  }
-};
-
 // ---------------------------------------------------------------------------
 // Read backward.  Per step of 32 entries: the entries' Phi rows (LDS,
 // swizzled 128-byte rows) and dy rows (fp32 rows of kS), token and pair.
@@ -113,9 +58,9 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
   const int64_t beg = eoffs[b * N0 + x], end = eoffs[b * N0 + x + 1];
   const In* phb = phr + b * q_sb;
   const float* dYb = dY + b * y_sb;
-  CwGather<In, float> ga;
+  CbGather<In, float> ga;
   if (beg < end) ga.load(ent, beg, beg, end, K, phb, q_st, dYb, y_st, tid);
-  cw_stage_rp(sF, F + b * f_sb + (int64_t)x * cw::kRP);
+  cb_stage_rp(sF, F + b * f_sb + (int64_t)x * cw::kRP);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
@@ -144,7 +89,7 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
       const int slot = tid >> 3, sub = tid & 7;
       sPh[cb_slot(slot, sub)] = ga.ok ? ga.r64 : make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int u = 0; u < CwGather<In, float>::kU; ++u) {
+      for (int u = 0; u < CbGather<In, float>::kU; ++u) {
         const int col = sub + 8 * u;
         if (col < kP) sY[slot * kS + col] = ga.ok ? ga.r65[u] : 0.f;
       }
@@ -175,7 +120,7 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
       float pd = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) pd += to_f32(ph[i]) * v[i];
-      pd = cw_sum_groups(pd);
+      pd = cb_sum_groups(pd);
       if (g == 0) sDot[w][es] = pd;
       const int t = sTok[es];
       if (t >= 0 && sPair[es] == 0)
@@ -267,9 +212,9 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
   if (beg == end) return;                            // uniform over the workgroup
   const In* psib = psi + b * k_sb;
   const In* vbb = vb + b * v_sb;
-  CwGather<In, In> ga;
+  CbGather<In, In> ga;
   ga.load(ent, beg, beg, end, K, psib, k_st, vbb, v_st, tid);
-  cw_stage_rp(sF, dF + b * f_sb + (int64_t)x * cw::kRP);
+  cb_stage_rp(sF, dF + b * f_sb + (int64_t)x * cw::kRP);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
@@ -300,7 +245,7 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
 #pragma unroll
       for (int i = 0; i < 8; ++i) sP[slot * kS + 8 * sub + i] = ga.ok ? to_f32(pv[i]) : 0.f;
 #pragma unroll
-      for (int u = 0; u < CwGather<In, In>::kU; ++u) {
+      for (int u = 0; u < CbGather<In, In>::kU; ++u) {
         const int col = sub + 8 * u;
         if (col < kP) sV[slot * kS + col] = ga.ok ? to_f32(ga.r65[u]) : 0.f;
       }
@@ -332,7 +277,7 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
       float pd = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) pd += sP[es * kS + 16 * w + 4 * g + i] * v[i];
-      pd = cw_sum_groups(pd);
+      pd = cb_sum_groups(pd);
       if (g == 0) sDot[w][es] = pd;
       const int t = sTok[es];
       if (t >= 0 && sPair[es] == 0) {

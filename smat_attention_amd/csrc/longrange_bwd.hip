@@ -29,21 +29,6 @@ constexpr int kRP = cb::kR * cb::kP;   // 4160 floats per r x p matrix
 constexpr int kStep = 32;           // tokens per K step of the list gram
 }  // namespace lr
 
-// Stage one contiguous r x p fp32 matrix (16-byte aligned) in LDS rows of kS.
-__device__ __forceinline__ void lr_stage_rp(float* s, const float* src) {
-  using namespace cb;
-  for (int f = threadIdx.x; f < lr::kRP / 4; f += lr::kThreads) {
-    const float4 v = reinterpret_cast<const float4*>(src)[f];
-    const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = 4 * f + q;
-      const int row = e / kP, col = e - row * kP;
-      s[row * kS + col] = vv[q];
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // dPhi[n + h + kB] += dY[n + h + kB] U_h^T, one workgroup per (h, sequence).
 // Wave w forms feature tile w of the transposed product, dPhi^T = U_h dY^T:
@@ -67,7 +52,7 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dphi_kernel(
   const int64_t b = blockIdx.y;
   const int cnt = h < T_R ? (T_R - h + B - 1) / B : 0;
   if (cnt == 0) return;                              // uniform over the workgroup
-  lr_stage_rp(sU, U + b * u_sb + (int64_t)h * lr::kRP);
+  cb_stage_rp(sU, U + b * u_sb + (int64_t)h * lr::kRP);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
@@ -112,10 +97,11 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dphi_kernel(
 // ---------------------------------------------------------------------------
 // dF[x] = sum over the token list of item x of Phi_t^T dY_t, one workgroup
 // per (item, sequence): 32 tokens a step are gathered into LDS (Phi rows
-// swizzled, dY rows of kS floats), then D[a][c] += Phi^T dY with A = Phi^T by
-// transposing reads (k-slot 8g + e = token slot) and B = dY columns split
-// hi/lo.  Wave w owns value-column tile w for all four feature tiles; wave 0
-// also tile 4 (column 64).
+// swizzled, dY rows of kS floats; eight threads a token, the next step's
+// gather in flight during the products), then D[a][c] += Phi^T dY with
+// A = Phi^T by transposing reads (k-slot 8g + e = token slot) and B = dY
+// columns split hi/lo.  Wave w owns value-column tile w for all four feature
+// tiles; wave 0 also tile 4 (column 64).
 // ---------------------------------------------------------------------------
 template <typename In>
 __global__ __launch_bounds__(lr::kThreads) void lr_dfeat_kernel(
@@ -130,7 +116,7 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dfeat_kernel(
   const int x = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x;
-  const int beg = tptr[x], end = tptr[x + 1];
+  const int64_t beg = tptr[x], end = tptr[x + 1];
   const In* phib = phi + b * q_sb;
   const float* dHb = dH + b * h_sb;
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
@@ -142,39 +128,23 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dfeat_kernel(
     acc[at] = zero4();
     acc4[at] = zero4();
   }
-  constexpr int kYN = lr::kStep * kP;                        // 2080 floats a step
-  constexpr int kYIt = (kYN + lr::kThreads - 1) / lr::kThreads;   // 9
-  for (int s0 = beg; s0 < end; s0 += lr::kStep) {
-    // gather: Phi chunk (token slot tid / 8, chunk tid % 8), dY elements
-    const int ts = tid >> 3, kk = tid & 7;
-    const bool okt = s0 + ts < end;
-    const int64_t t = tok[okt ? s0 + ts : beg];
-    uint4 pv = *reinterpret_cast<const uint4*>(phib + t * q_st + 8 * kk);
-    if (!okt) pv = make_uint4(0, 0, 0, 0);
-    float yv[kYIt];
-#pragma unroll
-    for (int u = 0; u < kYIt; ++u) {
-      const int e = tid + lr::kThreads * u;
-      const int ee = e < kYN ? e : 0;
-      const int slot = ee / kP, col = ee - slot * kP;
-      const bool ok = e < kYN && s0 + slot < end;
-      const int64_t ty = tok[ok ? s0 + slot : beg];
-      yv[u] = ok ? dHb[ty * h_st + col] : 0.f;
-    }
+  CbGather<In, float> ga;
+  if (beg < end) ga.load(tok, beg, beg, end, 1, phib, q_st, dHb, h_st, tid);
+  for (int64_t s0 = beg; s0 < end; s0 += lr::kStep) {
     if (s0 > beg) __syncthreads();                   // the last step's readers are done
-    sPh[cb_slot(ts, kk)] = pv;
+    {
+      const int slot = tid >> 3, sub = tid & 7;
+      sPh[cb_slot(slot, sub)] = ga.ok ? ga.r64 : make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int u = 0; u < kYIt; ++u) {
-      const int e = tid + lr::kThreads * u;
-      if (e < kYN) {
-        const int slot = e / kP, col = e - slot * kP;
-        sY[slot * kS + col] = yv[u];
+      for (int u = 0; u < CbGather<In, float>::kU; ++u) {
+        const int col = sub + 8 * u;
+        if (col < kP) sY[slot * kS + col] = ga.ok ? ga.r65[u] : 0.f;
       }
     }
     __syncthreads();
+    if (s0 + lr::kStep < end) ga.load(tok, s0 + lr::kStep, beg, end, 1, phib, q_st, dHb, h_st, tid);
 
-    // B = dY (k = token slot 8g + e, n = column c), for column tile w and,
-    // on wave 0, tile 4
+    // B = dY (k = token slot 8g + e, n = column c)
     auto bfrag = [&](int ct, Frag& hi, Frag& lo) {
       const int col = 16 * ct + r16;
       const bool okc = col < kP;
@@ -188,9 +158,8 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dfeat_kernel(
         lo[e] = ll;
       }
     };
-    Frag bh, bl, b4h, b4l;
+    Frag bh, bl;
     bfrag(w, bh, bl);
-    if (w == 0) bfrag(4, b4h, b4l);
 #pragma unroll
     for (int at = 0; at < 4; ++at) {
       // A = Phi^T: lane (a = 16 at + r16, g), k-slot 4h + e = token slot
@@ -208,6 +177,8 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dfeat_kernel(
       acc[at] = mma(acc[at], pa, bh);
       acc[at] = mma(acc[at], pa, bl);
       if (w == 0) {
+        Frag b4h, b4l;
+        bfrag(4, b4h, b4l);
         acc4[at] = mma(acc4[at], pa, b4h);
         acc4[at] = mma(acc4[at], pa, b4l);
       }
@@ -253,7 +224,7 @@ __global__ __launch_bounds__(lr::kThreads) void lr_pool_bwd_kernel(
   const int nX = n - n_P;
   const int cnt = x < N0 ? (x < nX ? (nX - x + N0 - 1) / N0 : 0) : n_P;
   if (cnt == 0) return;                              // uniform over the workgroup
-  lr_stage_rp(sF, dF + b * f_sb + (int64_t)x * lr::kRP);
+  cb_stage_rp(sF, dF + b * f_sb + (int64_t)x * lr::kRP);
   __syncthreads();
 
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
