@@ -85,6 +85,9 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the training-step timing")
+    ap.add_argument("--train-only", action="store_true",
+                    help="time the training steps alone (for profiling): no prefill, decode, "
+                         "CPU baseline or JSON line")
     ap.add_argument("--decode-steps", type=int, default=4096)
     ap.add_argument("--no-rows", action="store_true",
                     help="skip the per-T / d = 1 prefill rows")
@@ -545,6 +548,10 @@ def main():
         torch.cuda.synchronize()
         del x, y
         log("[bench] copy probe: 3 x 1 GiB device copies")
+    if args.train_only:
+        for d in (2, 3):
+            log(f"[bench] train step d={d}: {train_step_bench(d, max(3, args.kernel_reps // 2))}")
+        return
     nb, T, hd = args.heads, args.T, args.head_dim
     r, p = hd, hd + 1
     spec = build_mask(T, args.d, chunk=128)
