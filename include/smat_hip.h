@@ -347,6 +347,24 @@ int smat_pool_backward(int dtype, const void* psi, const void* vb, const float* 
  * The reference's autograd of the dense read and pool; its fused pool
  * backward is src/smat/kernels/triton_bwd.py:203-237.
  */
+/*
+ * Backward of one feature map (attention.py:82-106) at d_qk = r = 64 for
+ * 16-bit inputs (SMAT_EUNSUPPORTED otherwise): with y = x W^T (fp32) and G the
+ * upstream gradient of the map's output,
+ *   g = G * m'(y) * h,  dx = g W (in x's dtype),  dW = sum g^T x (fp32),
+ *   dh = sum_f G * m(y) (in h's dtype, when h is not NULL),
+ * m = elu + 1 (kind 0) or relu + 1e-3 (kind 1).  dWp is scratch for
+ * smat_featurise_backward_parts(nb, T) partial 64 x 64 fp32 sums; dW
+ * receives their total (beta = 1 adds it to dW).  The torch autograd of the
+ * reference's featurise, one launch and a reduction.
+ */
+int64_t smat_featurise_backward_parts(int nb, int T);
+int smat_featurise_backward(int dtype, const void* x, const void* G, const void* W, const void* h,
+                            void* dx, float* dWp, float* dW, void* dh, int nb, int T, int d_qk,
+                            int r, int kind, int beta, int64_t x_sb, int64_t x_st, int64_t g_sb,
+                            int64_t g_st, int64_t h_sb, int64_t o_sb, int64_t o_st,
+                            int64_t dh_sb, void* stream);
+
 int smat_cell_read_backward(int dtype, const void* phr, const float* dY, const float* F,
                             const int32_t* ent, const int64_t* eoffs, float* dPhi, float* dF,
                             float* dw, int nb, int N0, int K, int r, int p, int64_t q_sb,

@@ -76,6 +76,9 @@ SIGNATURES = {
     "smat_cell_pool_backward": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,
                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _i64, _p]),
+    "smat_featurise_backward_parts": (_i64, [_i, _i]),
+    "smat_featurise_backward": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,
+                                     _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "smat_pool_workspace_bytes": (_i64, [_i, _i, _i, _i, _i, _i]),
     "smat_pool": (_i, [_i, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,
                        _i64, _i64, _i64, _i64, _p, _i64, _p]),

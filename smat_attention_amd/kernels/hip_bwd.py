@@ -521,6 +521,8 @@ class FeaturiseFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dPhi, dPsi, dVb):
         W, Q, K, h = ctx.saved_tensors
+        if fused_featurise_backward_ok(W, Q, K, h, dPhi, dPsi):
+            return _featurise_backward_fused(ctx, W, Q, K, h, dPhi, dPsi, dVb)
         W32 = W.float()
 
         def dmap(y):
@@ -556,6 +558,65 @@ class FeaturiseFunction(torch.autograd.Function):
         if ctx.d_v is not None and dVb is not None:
             dV = dVb[..., :ctx.d_v].to(ctx.v_dtype)
         return (dW.to(W.dtype) if dW is not None else None, None, dQ, dK, dV, dh)
+
+
+# The fused feature-map backward (smat_featurise_backward) serves 16-bit
+# inputs at d_qk = r = 64; tests switch it off to compare with the torch
+# products it replaces.
+FUSED_FEATURISE_BACKWARD = True
+
+
+def _rows_ok(t):
+    return (t.stride(-1) == 1 and t.stride(1) % 8 == 0 and t.stride(0) % 8 == 0
+            and t.data_ptr() % 16 == 0)
+
+
+def fused_featurise_backward_ok(W, Q, K, h, dPhi, dPsi) -> bool:
+    if not FUSED_FEATURISE_BACKWARD or Q.dtype not in (torch.bfloat16, torch.float16):
+        return False
+    if W.shape != (64, 64) or Q.shape[-1] != 64 or W.dtype != Q.dtype:
+        return False
+    for t in (K, dPhi, dPsi):
+        if t is not None and (t.dtype != Q.dtype or t.shape[-1] != 64 or not _rows_ok(t)):
+            return False
+    return _rows_ok(Q) and (h is None or h.dtype == Q.dtype)
+
+
+def _featurise_backward_fused(ctx, W, Q, K, h, dPhi, dPsi, dVb):
+    """FeaturiseFunction's backward on smat_featurise_backward: one launch per
+    map (recomputed y, the map's derivative, the gate, dx and the partial dW
+    sums) and a reduction of dW."""
+    dev = Q.device
+    nb, T, _ = Q.shape
+    Wc = W.contiguous()
+    code = _code(Q)
+    kind = 0 if ctx.kind == "elu1" else 1
+    parts = max(1, int(_lib.query("smat_featurise_backward_parts", nb, T)))
+    dWp = torch.empty(parts, 64, 64, device=dev, dtype=torch.float32)
+    dW32 = torch.zeros(64, 64, device=dev, dtype=torch.float32)
+    beta = 0
+    dQ = dK = dV = dh = None
+    st = stream_of(Q)
+    for X, G, hh, want in ((Q, dPhi, None, True), (K, dPsi, h, K is not None)):
+        if not want or G is None:
+            continue
+        dX = torch.empty(nb, T, 64, device=dev, dtype=X.dtype)
+        dhh = torch.empty(nb, T, device=dev, dtype=hh.dtype) if hh is not None else None
+        hc = hh.contiguous() if hh is not None else None
+        call("smat_featurise_backward", code, X.data_ptr(), G.data_ptr(), Wc.data_ptr(),
+             ptr(hc), dX.data_ptr(), dWp.data_ptr(), dW32.data_ptr(), ptr(dhh), nb, T, 64, 64,
+             kind, beta, X.stride(0), X.stride(1), G.stride(0), G.stride(1),
+             hc.stride(0) if hc is not None else 0, dX.stride(0), dX.stride(1),
+             dhh.stride(0) if dhh is not None else 0, st)
+        beta = 1
+        if X is Q:
+            dQ = dX
+        else:
+            dK, dh = dX, dhh
+    if ctx.d_v is not None and dVb is not None:
+        dV = dVb[..., :ctx.d_v].to(ctx.v_dtype)
+    dW = dW32.to(W.dtype) if ctx.needs_input_grad[0] else None
+    return (dW, None, dQ, dK, dV, dh)
 
 
 # ---------------------------------------------------------------------------

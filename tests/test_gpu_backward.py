@@ -390,6 +390,46 @@ def test_fused_cell_backward(d):
         assert e < (2e-3 if name in ("dQ", "dK", "dV") else 1e-4), name
 
 
+@pytest.mark.parametrize("kind,gate,T", [("elu1", True, 1000), ("relu", True, 2048),
+                                         ("elu1", False, 4096)])
+def test_fused_featurise_backward(kind, gate, T):
+    """The feature map's backward at head_dim 64, bf16 (smat_featurise_backward)
+    against the torch products it replaces, same forward and upstream
+    gradients: dQ, dK, dh (bf16) within 2e-3 norm-relative, dW (bf16) within
+    2e-3, dV equal; a tail tile (T = 1000) and both maps."""
+    from smat_attention_amd.kernels import hip_bwd as HB
+    nb, hd = 6, 64
+    gen = torch.Generator().manual_seed(80 + T)
+    bf = torch.bfloat16
+    Q, K, V = (torch.randn(nb, T, hd, generator=gen).to(bf) for _ in range(3))
+    h = (torch.rand(nb, T, generator=gen) + 0.5).to(bf) if gate else None
+    dPhi, dPsi = (torch.randn(nb, T, hd, generator=gen).to(bf) for _ in range(2))
+    dVb = torch.randn(nb, T, hd + 1, generator=gen).to(bf)
+    _say("fused featurise backward", kind, gate, T)
+
+    def run(fused):
+        HB.FUSED_FEATURISE_BACKWARD = fused
+        try:
+            phi = A.make_phi(hd, hd, kind=kind, device=DEV, dtype=bf, seed=3)
+            phi.W.requires_grad_(True)
+            xs = [t.to(DEV).requires_grad_(True) for t in (Q, K, V)]
+            hd_ = h.to(DEV).requires_grad_(True) if h is not None else None
+            Phi, Psi, Vb = A.featurise(*xs, phi, h=hd_)
+            torch.autograd.backward([Phi, Psi, Vb], [dPhi.to(DEV), dPsi.to(DEV), dVb.to(DEV)])
+            out = [x.grad.float().cpu() for x in xs] + [phi.W.grad.float().cpu()]
+            if hd_ is not None:
+                out.append(hd_.grad.float().cpu())
+            return out
+        finally:
+            HB.FUSED_FEATURISE_BACKWARD = True
+    g1, g0 = run(True), run(False)
+    for name, a, b in zip(("dQ", "dK", "dV", "dW", "dh"), g1, g0):
+        e = _nrel(a, b)
+        _say(f"  {name}: {e:.2e}")
+        assert torch.isfinite(a).all()
+        assert e < 2e-3, name
+
+
 @pytest.mark.parametrize("d", [2, 3])
 def test_training_step_content_hashed(d):
     """The content-hashed training step at head_dim 64, T = 4096 (4 of the
