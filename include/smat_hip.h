@@ -500,6 +500,34 @@ int smat_cell_hash(int dtype, const void* u, const float* Wn, const float* gamma
                    const float* bias, float* s_out, int64_t* cells, int nb, int L, int dm,
                    int nh, int dim, int q, int64_t u_sb, int64_t u_st, void* stream);
 
+/*
+ * The (cell, weight) pairs of the training path at anneal = 1, from the
+ * projections z (nb, L, nh*dim) fp32, z = (LN(u) . Wn) gamma + bias: s
+ * (nb*nh, L, dim) as smat_cell_hash, the chosen cells (nb*nh, L), the 2^dim
+ * pair cells idx (nb*nh, L, 2^dim) (pair p takes the high bin
+ * min(floor(s_k) + 1, q - 1) in coordinate k when bit k of p is set) and the
+ * soft bin occupancy occ (nb*nh, dim, q): 1 - frac at the low bin plus frac at
+ * the high bin, summed over the L tokens.  plant (L,) int64 or null: a cell
+ * >= 0 replaces every pair of that token (the planted key columns).
+ * dim <= 8, dim*q <= 4096, nh*dim <= 64.  Replaces the pair construction and
+ * the occupancy of src/smat/assign.py:257-317 (anneal = 1, no token weights).
+ */
+int smat_hash_pairs(const float* z, const int64_t* plant, float* s_out, int64_t* cells,
+                    int64_t* idx, float* occ, int nb, int L, int nh, int dim, int q,
+                    void* stream);
+
+/*
+ * Gradient of z (nb, L, nh*dim) fp32 from the gradients of the pairs' weights
+ * dw (nb*nh, L, 2^dim) and of the occupancy docc (nb*nh, dim, q), either null,
+ * through the straight-through weights of src/smat/assign.py:262-295 at
+ * anneal = 1 (forward one-hot on pair 0) and the clamped normal CDF:
+ * dz_k = q phi(z_k) [in range] (dw[2^k] - dw[0] + docc[k][hi_k] - docc[k][lo_k]);
+ * planted tokens (plant >= 0) take no dw term.  s_fwd is smat_hash_pairs' s.
+ */
+int smat_hash_pairs_backward(const float* z, const float* s_fwd, const int64_t* plant,
+                             const float* dw, const float* docc, float* dz, int nb, int L,
+                             int nh, int dim, int q, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -308,11 +308,53 @@ class ContentAssign(nn.Module):
         if self.shift:
             hk = torch.cat([h.new_zeros(h.shape[0], self.shift, h.shape[2]),
                             h[:, :-self.shift]], dim=1)
-        ck, idxk, wk, aux_k = self._ste_pairs(self._soft_hash(hk[:, :n]), plant_at=True,
-                                              tok_w=key_w, single=single)
-        cq, idxq, wq, aux_q = self._ste_pairs(self._soft_hash(h[:, n:]), single=single)
+        if self._fused_pairs_ok(h, key_w, single):
+            ck, idxk, wk, aux_k = self._hash_pairs(hk[:, :n], plant_at=True)
+            cq, idxq, wq, aux_q = self._hash_pairs(h[:, n:])
+        else:
+            ck, idxk, wk, aux_k = self._ste_pairs(self._soft_hash(hk[:, :n]), plant_at=True,
+                                                  tok_w=key_w, single=single)
+            cq, idxq, wq, aux_q = self._ste_pairs(self._soft_hash(h[:, n:]), single=single)
         self.aux = None if self.freeze else aux_k + aux_q
         return ck, idxk, wk, cq, idxq, wq
+
+    def _fused_pairs_ok(self, h, key_w, single):
+        return (FUSED_HASH_PAIRS and self.anneal >= 1.0 and key_w is None and not single
+                and h.dtype == torch.float32 and self.dim <= 8 and self.dim * self.q <= 4096
+                and self.h * self.dim <= 64)
+
+    def _plant_map(self, L, device):
+        """(L,) int64: the planted cell of each key column, -1 elsewhere."""
+        key = (L, str(device))
+        cache = getattr(self, "_plant_maps", None)
+        if cache is None:
+            cache = self._plant_maps = {}
+        if key not in cache:
+            pm = torch.full((L,), -1, dtype=torch.int64)
+            if self.plant and self.plant_cols.numel():
+                cols = self.plant_cols[self.plant_cols < L].cpu()
+                pm[cols] = self.plant_cells[: cols.numel()].cpu()
+            cache[key] = pm.to(device)
+        return cache[key]
+
+    def _hash_pairs(self, hu, plant_at=False):
+        """``_ste_pairs(_soft_hash(hu))`` at ``anneal = 1`` with no token
+        weights, in three autograd steps: the projections z (LayerNorm and the
+        unit rows as in :meth:`_soft_hash`, torch), then the pairs, the
+        straight-through weights and the occupancy (``smat_hash_pairs``, with
+        ``smat_hash_pairs_backward`` for the gradient of z), then the
+        load-balance term from the occupancy (torch)."""
+        nb, L, dm = hu.shape
+        Wn = self.W / self.W.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+        hd = self.h * self.dim
+        xh = self.ln(hu).reshape(nb * L, dm)
+        z = (xh @ Wn.reshape(hd, dm).t()) * self.gamma.reshape(hd) + self.b.reshape(hd)
+        plant = self._plant_map(L, hu.device) if (plant_at and self.plant) else None
+        cells, idx, w, occ = _HashPairs.apply(z.reshape(nb, L, hd), self.h, self.dim, self.q,
+                                              plant)
+        occ = occ / occ.sum(-1, keepdim=True).clamp_min(1e-6)
+        aux = None if self.freeze else (occ * (occ.clamp_min(1e-9) * self.q).log()).sum(-1).mean()
+        return cells, idx, w, aux
 
     def _forward_grad(self, u, Phi, Psi, Vb, n, emb, key_src, key_w, ids, dir_override):
         """The branch with the gradients of the reference's autograd, over the
@@ -472,6 +514,58 @@ def _entry_lists(idx, N0):
     eoffs = torch.zeros(nb * N0 + 1, device=idx.device, dtype=torch.int64)
     eoffs[1:] = torch.cumsum(counts, 0)
     return ent, eoffs
+
+
+# The pairs of the training path from one kernel (smat_hash_pairs) and its
+# backward; tests switch it off to compare with the torch straight-through path.
+FUSED_HASH_PAIRS = True
+
+
+class _HashPairs(torch.autograd.Function):
+    """z (nb, L, h*dim) -> cells (nb*h, L), idx (nb*h, L, 2^dim), the one-hot
+    forward weights w (nb*h, L, 2^dim) and the soft occupancy (nb*h, dim, q):
+    the straight-through pairs of assign.py:257-317 at ``anneal = 1``.  The
+    gradients of w and of the occupancy come back to z through
+    ``smat_hash_pairs_backward``."""
+
+    @staticmethod
+    def forward(ctx, z, nh, dim, q, plant):
+        nb, L, _ = z.shape
+        B, K = nb * nh, 1 << dim
+        z = z.contiguous()
+        s = torch.empty(B, L, dim, device=z.device, dtype=torch.float32)
+        cells = torch.empty(B, L, device=z.device, dtype=torch.int64)
+        idx = torch.empty(B, L, K, device=z.device, dtype=torch.int64)
+        occ = torch.empty(B, dim, q, device=z.device, dtype=torch.float32)
+        if L:
+            call("smat_hash_pairs", z.data_ptr(), None if plant is None else plant.data_ptr(),
+                 s.data_ptr(), cells.data_ptr(), idx.data_ptr(), occ.data_ptr(), nb, L, nh, dim,
+                 q, stream_of(z))
+        else:
+            occ.zero_()
+        w = torch.zeros(B, L, K, device=z.device, dtype=torch.float32)
+        w[..., 0] = 1.0
+        ctx.save_for_backward(z, s)
+        ctx.plant, ctx.shape = plant, (nb, L, nh, dim, q)
+        ctx.mark_non_differentiable(cells, idx)
+        ctx.set_materialize_grads(False)
+        return cells, idx, w, occ
+
+    @staticmethod
+    def backward(ctx, dcells, didx, dw, docc):
+        z, s = ctx.saved_tensors
+        nb, L, nh, dim, q = ctx.shape
+        if (dw is None and docc is None) or not L:
+            return None, None, None, None, None
+        dw = None if dw is None else dw.float().contiguous()
+        docc = None if docc is None else docc.float().contiguous()
+        dz = torch.empty_like(z)
+        plant = ctx.plant
+        call("smat_hash_pairs_backward", z.data_ptr(), s.data_ptr(),
+             None if plant is None else plant.data_ptr(),
+             None if dw is None else dw.data_ptr(), None if docc is None else docc.data_ptr(),
+             dz.data_ptr(), nb, L, nh, dim, q, stream_of(z))
+        return dz, None, None, None, None
 
 
 def _one_hot_first(w):

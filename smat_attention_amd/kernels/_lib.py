@@ -100,6 +100,8 @@ SIGNATURES = {
     "smat_gram_lists": (_i, [_i, _p, _p, _p, _p, _p, _i, _i, _i, _i64, _i64, _p]),
     "smat_query_lists": (_i, [_i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _p]),
     "smat_cell_hash": (_i, [_i, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i64, _p]),
+    "smat_hash_pairs": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p]),
+    "smat_hash_pairs_backward": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p]),
     "smat_zeta": (_i, [_p, _p, _i, _i, _i64, _p]),
     "smat_walsh": (_i, [_p, _p, _i, _i, _i64, _p]),
     "smat_incidence_complement": (_i, [_p, _p, _i, _i, _i, _i64, _p]),

@@ -390,6 +390,51 @@ def test_fused_cell_backward(d):
         assert e < (2e-3 if name in ("dQ", "dK", "dV") else 1e-4), name
 
 
+@pytest.mark.parametrize("d,plant,nb,L,dm", [(2, False, 2, 300, 96), (2, True, 2, 517, 96),
+                                             (3, True, 1, 1000, 768), (3, False, 3, 64, 160),
+                                             (4, True, 2, 256, 96), (5, True, 1, 700, 64)])
+def test_fused_hash_pairs(d, plant, nb, L, dm):
+    """The training path's pairs from smat_hash_pairs and its backward against
+    the torch straight-through construction they replace (``_soft_hash`` then
+    ``_ste_pairs``, the reference's op order, assign.py:246-317) on the same
+    module and fp32 input: cells, pair cells and forward weights equal, the
+    load-balance term within 1e-6, and the gradients of u, W, gamma and b for
+    a random upstream gradient of every pair weight plus 3 x the load-balance
+    term within 1e-5 of the largest entry.  Hash dimension d - 1 = 1..4 (2 to
+    16 pairs per token), planted key columns included."""
+    from smat_attention_amd.assign import ContentAssign
+    H = 3
+    spec = build_mask(4096, d, chunk=128)
+    gen = torch.Generator().manual_seed(90 + d)
+    u0 = torch.randn(nb, L, dm, generator=gen)
+    G = torch.randn(nb * H, L, 1 << spec.dim, generator=gen).to(DEV)
+    torch.manual_seed(11 + d)
+    m = ContentAssign(H, dm, spec, mode="point").to(DEV)
+    with torch.no_grad():
+        m.gamma.mul_(1.5)
+        m.b.normal_(0.0, 0.3)
+    _say("fused hash pairs", d, plant, nb, L, dm, spec.q)
+
+    def run(fused):
+        m.zero_grad()
+        u = u0.to(DEV).requires_grad_(True)
+        if fused:
+            cells, idx, w, aux = m._hash_pairs(u, plant_at=plant)
+        else:
+            cells, idx, w, aux = m._ste_pairs(m._soft_hash(u), plant_at=plant)
+        ((w * G).sum() + 3.0 * aux).backward()
+        return (cells.cpu(), idx.cpu(), w.detach().cpu(), aux.item(),
+                [u.grad.cpu()] + [getattr(m, k).grad.detach().cpu() for k in ("W", "gamma", "b")])
+    c1, i1, w1, a1, g1 = run(True)
+    c0, i0, w0, a0, g0 = run(False)
+    assert torch.equal(c1, c0) and torch.equal(i1, i0) and torch.equal(w1, w0)
+    assert abs(a1 - a0) < 1e-6 * max(1.0, abs(a0)), (a1, a0)
+    for name, a, b in zip(("du", "dW", "dgamma", "db"), g1, g0):
+        e = _grel(a, b)
+        _say(f"  {name}: {e:.2e}")
+        assert torch.isfinite(a).all() and e < 1e-5, name
+
+
 @pytest.mark.parametrize("kind,gate,T", [("elu1", True, 1000), ("relu", True, 2048),
                                          ("elu1", False, 4096)])
 def test_fused_featurise_backward(kind, gate, T):
