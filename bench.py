@@ -323,8 +323,7 @@ def train_step_bench(d, reps, B=8, H=12, hd=64, T=4096):
     def step():
         Phi, Psi, Vb = A.featurise(Q, K, V, phi)
         Hs = A.segmented_causal_scan(Phi, Psi, Vb, n, 128)
-        Hs = torch.cat([Hs[:, :n], Hs[:, n:] + m(X, Phi, Psi, Vb, n)], dim=1)
-        o = Hs[..., :-1] / Hs[..., -1:].clamp_min(1e-6)
+        o = A.combine_normalise(Hs, m(X, Phi, Psi, Vb, n), n)      # cat + clamped division
         (o.to(bf) * dO).float().sum().backward()
     us = Events(torch).time(step, reps)
     res = {"ms": round(us / 1e3, 3), "tokens_per_s": round(B * T / (us * 1e-6), 1),

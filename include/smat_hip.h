@@ -258,6 +258,29 @@ int smat_normalise_backward(const float* dout, const float* H, const float* g, f
                             int64_t g_sb, void* stream);
 
 /*
+ * The layer's combine and division with the normaliser floored at eps:
+ * N = H + [0; Y] (Y's rows added from row n on; Y (nb, T-n, p) may be NULL),
+ * out[t, c] = N[t, c] / max(N[t, p-1], eps) for c < p-1.  H (nb, T, p), out
+ * (nb, T, p-1), fp32, each with its own (batch, row) strides.  Replaces
+ * torch.cat([H[:, :n], H[:, n:] + Ylr]) and H[..., :-1] / H[..., -1:].clamp_min(eps)
+ * of src/smat/model.py:296-300 (eps = 1e-6 there).
+ */
+int smat_combine_normalise(const float* H, const float* Y, float* out, int nb, int T, int n,
+                           int p, float eps, int64_t h_sb, int64_t h_st, int64_t y_sb,
+                           int64_t y_st, int64_t o_sb, int64_t o_st, void* stream);
+
+/*
+ * Backward of smat_combine_normalise: dN[t, c] = dout[t, c] / den (c < p-1),
+ * dN[t, p-1] = -sum_c dN[t, c] N[t, c] / den, or 0 where N[t, p-1] < eps (the
+ * floor passes no gradient), den = max(N[t, p-1], eps).  dN (nb, T, p) is the
+ * gradient of H, and its rows from n on are the gradient of Y.
+ */
+int smat_combine_normalise_backward(const float* dout, const float* H, const float* Y, float* dH,
+                                    int nb, int T, int n, int p, float eps, int64_t o_sb,
+                                    int64_t o_st, int64_t h_sb, int64_t h_st, int64_t y_sb,
+                                    int64_t y_st, int64_t d_sb, int64_t d_st, void* stream);
+
+/*
  * Strided batched GEMM on fp32 MFMA (backward pass building block):
  *   C[i] = A[i] . B[i]  (beta = 0)  or  C[i] += A[i] . B[i]  (beta = 1),
  * A[i]: M x K, B[i]: K x N, C[i]: M x N fp32, for i = (i1, i2) in
@@ -480,7 +503,9 @@ int smat_gram_lists(int dtype, const void* psi, const void* vb, const int32_t* t
 
 /*
  * Read by type over row lists (CSR): Y[i] = phi[i] U[h] for every row i in
- * rows[roffs[h] .. roffs[h+1]), h < ntypes; maxcnt bounds the list lengths.
+ * rows[roffs[h] .. roffs[h+1]), h < ntypes.  maxcnt sizes the grid (about the
+ * longest list; any value >= 0 is correct: longer lists are walked by the
+ * same workgroups), so a caller need not read the list lengths back.
  * U: (ntypes, r, p) fp32, Y rows y_st apart.  The point / plane read of a
  * content-addressed assignment, src/smat/assign.py:437-439, 471-472.
  */

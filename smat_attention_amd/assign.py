@@ -39,8 +39,8 @@ import torch
 import torch.nn as nn
 
 from .kernels.hip_fwd import _code, _on_gpu, _rows3, call, stream_of
-from .pool_ops import (_f32_rows, _gram_lists, _lists, _read_lists, _read_pairs, _repeat,
-                       pool_sorted, read_sorted)
+from .pool_ops import (_csr, _f32_rows, _gram_lists, _list_hint, _lists, _read_lists, _read_pairs,
+                       _repeat, pool_sorted, read_sorted)
 
 __all__ = ["ContentAssign", "grouped_planes"]
 
@@ -439,12 +439,9 @@ class ContentAssign(nn.Module):
         N0 = self.N0
         # ---- pool by cell: tokens of each (sequence, cell), in token order
         key = (torch.arange(nbh, device=dev).unsqueeze(1) * N0 + ck).reshape(-1)
-        order = torch.argsort(key, stable=True)
+        order, offs = _csr(key, nbh * N0)
         seq = order // n
         tokens = (seq * T + (order - seq * n)).to(torch.int32)
-        counts = torch.bincount(key, minlength=nbh * N0)
-        offs = torch.zeros(nbh * N0 + 1, device=dev, dtype=torch.int64)
-        offs[1:] = torch.cumsum(counts, 0)
         Ps = Psi if Psi.stride(0) == T * Psi.stride(1) else Psi.contiguous()
         Vs = Vb if Vb.stride(0) == T * Vb.stride(1) else Vb.contiguous()
         F = torch.empty(nbh, N0, r, p, device=dev, dtype=torch.float32)
@@ -468,13 +465,10 @@ class ContentAssign(nn.Module):
             typ = e_star * self.n_cosets + self.coset_of.to(dev)[e_star, cq]
             ntypes = nrows
         key = (torch.arange(nbh, device=dev).unsqueeze(1) * ntypes + typ).reshape(-1)
-        order = torch.argsort(key, stable=True)
+        order, roffs = _csr(key, nbh * ntypes)
         seq = order // T_R
         rows = (seq * T + n + (order - seq * T_R)).to(torch.int32)
-        counts = torch.bincount(key, minlength=nbh * ntypes)
-        roffs = torch.zeros(nbh * ntypes + 1, device=dev, dtype=torch.int64)
-        roffs[1:] = torch.cumsum(counts, 0)
-        maxcnt = int(counts.max().item()) if counts.numel() else 0
+        maxcnt = _list_hint(T_R, ntypes)
         Pr = Phi if Phi.stride(0) == T * Phi.stride(1) else Phi.contiguous()
         Y = torch.empty(nbh, T, p, device=dev, dtype=torch.float32)
         call("smat_query_lists", _code(Pr, "ContentAssign"), Pr.data_ptr(), U.data_ptr(),
@@ -508,12 +502,8 @@ def _entry_lists(idx, N0):
     nb, L, K = idx.shape
     key = (torch.arange(nb, device=idx.device).unsqueeze(1) * N0
            + idx.reshape(nb, L * K)).reshape(-1)
-    order = torch.argsort(key, stable=True)
-    ent = (order % (L * K)).to(torch.int32)
-    counts = torch.bincount(key, minlength=nb * N0)
-    eoffs = torch.zeros(nb * N0 + 1, device=idx.device, dtype=torch.int64)
-    eoffs[1:] = torch.cumsum(counts, 0)
-    return ent, eoffs
+    order, eoffs = _csr(key, nb * N0)
+    return (order % (L * K)).to(torch.int32), eoffs
 
 
 # The pairs of the training path from one kernel (smat_hash_pairs) and its

@@ -39,7 +39,8 @@ from .mask import MaskSpec
 
 __all__ = [
     "make_phi", "featurise", "to_device",
-    "segmented_causal_scan", "decayed_segmented_scan", "pool_profiles", "apply_incidence",
+    "segmented_causal_scan", "decayed_segmented_scan", "combine_normalise", "pool_profiles",
+    "apply_incidence",
     "query_by_type", "zeta_transform", "walsh_incidence", "direct_long_range",
     "smat_attention", "dense_masked_kernel_attention", "SmatDecoder",
     "have_triton", "have_hip",
@@ -317,6 +318,26 @@ def segmented_causal_scan(Phi, Psi, Vb, n: int, chunk: int = 128,
         return CausalScanFunction.apply(Phi, Psi, Vb, n, C,
                                         lambda P, S, V: _causal_scan(P, S, V, n, C))
     return _causal_scan(Phi, Psi, Vb, n, C)
+
+
+def combine_normalise(H, Y, n: int, eps: float = 1e-6):
+    """The layer's last step over the causal term ``H`` (nb, T, p) and the
+    long-range term ``Y`` (nb, T - n, p) of the recent rows, in one kernel each
+    way: ``N = cat([H[:, :n], H[:, n:] + Y], 1)``, then
+    ``N[..., :-1] / N[..., -1:].clamp_min(eps)`` (model.py:296-300, 311-316).
+    ``Y`` may be None (no long-range rows).  Returns fp32 (nb, T, p - 1);
+    differentiable in H and Y."""
+    who = "combine_normalise"
+    _hip._on_gpu(who, H, Y)
+    nb, T, P = H.shape
+    if not 0 <= n <= T or P < 2:
+        raise ValueError(f"{who}: need 0 <= n <= T and p >= 2 (n={n}, T={T}, p={P})")
+    if Y is not None and tuple(Y.shape) != (nb, T - n, P):
+        raise ValueError(f"{who}: Y must be {(nb, T - n, P)}, got {tuple(Y.shape)}")
+    if eps < 0:
+        raise ValueError(f"{who}: eps must be >= 0")
+    from .kernels.hip_bwd import CombineNormaliseFunction
+    return CombineNormaliseFunction.apply(H, Y, n, eps)
 
 
 def _causal_scan(Phi, Psi, Vb, n: int, C: int):

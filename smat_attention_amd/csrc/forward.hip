@@ -62,7 +62,8 @@ int query_dispatch(int dtype, const void* phi, const float* U, float* Y, int nb,
                    hipStream_t stream);
 int normalise_dispatch(const float* H, const float* Y, const float* g, float* out, int nb, int T,
                        int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb, int64_t y_st,
-                       int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream);
+                       int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream,
+                       float eps);
 
 int64_t causal_scan_workspace_bytes(int nb, int T, int C, int r, int p);
 int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void* vb,
@@ -255,5 +256,5 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     }
   }
   return normalise_dispatch(H, T_R > 0 ? Y : nullptr, g, out, nb, T, n, p, h_sb, p,
-                            (int64_t)T_R * yst, yst, o_sb, o_st, g_sb, st);
+                            (int64_t)T_R * yst, yst, o_sb, o_st, g_sb, st, -1.f);
 }

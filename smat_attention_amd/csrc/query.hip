@@ -48,97 +48,100 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
   // rows[roffs[h] .. roffs[h+1])
   const int cnt = rows ? (int)(roffs[h + 1] - roffs[h]) : (h < T_R) ? (T_R - h + B - 1) / B : 0;
   const int32_t* hrows = rows ? rows + roffs[h] : nullptr;
-  const int k0 = rb * kRowsPerWG;
-  if (k0 >= cnt) return;
-  const int nmt = min(kMT, (cnt - k0 + 15) / 16);
+  // row blocks rb, rb + nrb, ...: a list longer than the grid was sized for
+  // is still covered
+  for (int rbi = rb; rbi * kRowsPerWG < cnt; rbi += nrb) {
+    const int k0 = rbi * kRowsPerWG;
+    const int nmt = min(kMT, (cnt - k0 + 15) / 16);
 
-  const In* phib = phi + b * q_sb;
-  const float* Uh = U + (b * B + h) * (int64_t)r * p;
+    const In* phib = phi + b * q_sb;
+    const float* Uh = U + (b * B + h) * (int64_t)r * p;
 
-  f32x4 acc[kMT][kCTPerWave];
+    f32x4 acc[kMT][kCTPerWave];
 #pragma unroll
-  for (int t = 0; t < kMT; ++t)
+    for (int t = 0; t < kMT; ++t)
 #pragma unroll
-    for (int j = 0; j < kCTPerWave; ++j) acc[t][j] = zero4();
+      for (int j = 0; j < kCTPerWave; ++j) acc[t][j] = zero4();
 
-  // this lane's row of each 16-row tile, looked up once (a list entry or
-  // h + kB); the stores below take their rows from these lanes by shuffle
-  int64_t ri[kMT];
-#pragma unroll
-  for (int t = 0; t < kMT; ++t) {
-    const int k = k0 + 16 * t + row16;
-    ri[t] = !(k < cnt) ? 0 : hrows ? (int64_t)hrows[k] : (int64_t)h + (int64_t)k * B;
-  }
-#pragma unroll
-  for (int kb = 0; kb < kRK; ++kb) {
-    if (kb >= rk) continue;
-    const int a0 = 32 * kb + 8 * grp;
-    Frag pa[kMT];
+    // this lane's row of each 16-row tile, looked up once (a list entry or
+    // h + kB); the stores below take their rows from these lanes by shuffle
+    int64_t ri[kMT];
 #pragma unroll
     for (int t = 0; t < kMT; ++t) {
       const int k = k0 + 16 * t + row16;
-      const int nv = (t < nmt && k < cnt) ? min(8, r - a0) : 0;
-      pa[t] = load8<In>(phib + ri[t] * q_st + a0, nv, vec_q);
+      ri[t] = !(k < cnt) ? 0 : hrows ? (int64_t)hrows[k] : (int64_t)h + (int64_t)k * B;
     }
 #pragma unroll
-    for (int j = 0; j < kCTPerWave; ++j) {
-      const int ct = w + 4 * j;
-      if (ct >= nct) continue;
-      const int c = ct * 16 + row16;
-      float u[8];
+    for (int kb = 0; kb < kRK; ++kb) {
+      if (kb >= rk) continue;
+      const int a0 = 32 * kb + 8 * grp;
+      Frag pa[kMT];
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        u[e] = (c < p && a0 + e < r) ? Uh[(int64_t)(a0 + e) * p + c] : 0.f;
-      if constexpr (Traits<In>::split) {
-        Frag bh, bl;
+      for (int t = 0; t < kMT; ++t) {
+        const int k = k0 + 16 * t + row16;
+        const int nv = (t < nmt && k < cnt) ? min(8, r - a0) : 0;
+        pa[t] = load8<In>(phib + ri[t] * q_st + a0, nv, vec_q);
+      }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          In hh, ll;
-          split2<In>(u[e], hh, ll);
-          bh[e] = hh;
-          bl[e] = ll;
-        }
+      for (int j = 0; j < kCTPerWave; ++j) {
+        const int ct = w + 4 * j;
+        if (ct >= nct) continue;
+        const int c = ct * 16 + row16;
+        float u[8];
 #pragma unroll
-        for (int t = 0; t < kMT; ++t) {
-          if (t >= nmt) continue;
-          acc[t][j] = mma(acc[t][j], pa[t], bh);
-          acc[t][j] = mma(acc[t][j], pa[t], bl);
-        }
-      } else {
-        Frag bf;
+        for (int e = 0; e < 8; ++e)
+          u[e] = (c < p && a0 + e < r) ? Uh[(int64_t)(a0 + e) * p + c] : 0.f;
+        if constexpr (Traits<In>::split) {
+          Frag bh, bl;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) bf[e] = u[e];
+          for (int e = 0; e < 8; ++e) {
+            In hh, ll;
+            split2<In>(u[e], hh, ll);
+            bh[e] = hh;
+            bl[e] = ll;
+          }
 #pragma unroll
-        for (int t = 0; t < kMT; ++t) {
-          if (t >= nmt) continue;
-          acc[t][j] = mma(acc[t][j], pa[t], bf);
+          for (int t = 0; t < kMT; ++t) {
+            if (t >= nmt) continue;
+            acc[t][j] = mma(acc[t][j], pa[t], bh);
+            acc[t][j] = mma(acc[t][j], pa[t], bl);
+          }
+        } else {
+          Frag bf;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) bf[e] = u[e];
+#pragma unroll
+          for (int t = 0; t < kMT; ++t) {
+            if (t >= nmt) continue;
+            acc[t][j] = mma(acc[t][j], pa[t], bf);
+          }
         }
       }
     }
-  }
 
-  float* Yb = Y + b * y_sb;
+    float* Yb = Y + b * y_sb;
 #pragma unroll
-  for (int t = 0; t < kMT; ++t) {
-    if (t >= nmt) continue;
-    // row of output element i4: tile row 4 grp + i4, held by lane 4 grp + i4
-    int64_t ro[4];
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const int src = 4 * grp + i4;
-      const int lo = __shfl((int)(ri[t] & 0xffffffff), src, 64);
-      const int hi = __shfl((int)(ri[t] >> 32), src, 64);
-      ro[i4] = ((int64_t)hi << 32) | (uint32_t)lo;
-    }
-#pragma unroll
-    for (int j = 0; j < kCTPerWave; ++j) {
-      const int ct = w + 4 * j;
-      if (ct >= nct) continue;
-      const int c = ct * 16 + row16;
+    for (int t = 0; t < kMT; ++t) {
+      if (t >= nmt) continue;
+      // row of output element i4: tile row 4 grp + i4, held by lane 4 grp + i4
+      int64_t ro[4];
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
-        const int k = k0 + 16 * t + 4 * grp + i4;
-        if (k < cnt && c < p) Yb[ro[i4] * y_st + c] = acc[t][j][i4];
+        const int src = 4 * grp + i4;
+        const int lo = __shfl((int)(ri[t] & 0xffffffff), src, 64);
+        const int hi = __shfl((int)(ri[t] >> 32), src, 64);
+        ro[i4] = ((int64_t)hi << 32) | (uint32_t)lo;
+      }
+#pragma unroll
+      for (int j = 0; j < kCTPerWave; ++j) {
+        const int ct = w + 4 * j;
+        if (ct >= nct) continue;
+        const int c = ct * 16 + row16;
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int k = k0 + 16 * t + 4 * grp + i4;
+          if (k < cnt && c < p) Yb[ro[i4] * y_st + c] = acc[t][j][i4];
+        }
       }
     }
   }
@@ -343,7 +346,8 @@ template <typename In>
 static int launch_query_lists(const void* phi, const float* U, float* Y, const int32_t* rows,
                               const int64_t* roffs, int ntypes, int maxcnt, int r, int p,
                               int64_t q_st, int64_t y_st, hipStream_t stream) {
-  const int nrb = (maxcnt + qy::kRowsPerWG - 1) / qy::kRowsPerWG;
+  // maxcnt only sizes the grid: a workgroup walks row blocks rb, rb + nrb, ...
+  const int nrb = std::max(1, (maxcnt + qy::kRowsPerWG - 1) / qy::kRowsPerWG);
   const int64_t gx = (int64_t)ntypes * nrb;
   if (gx >= (1ll << 31)) {
     set_error("smat_query_lists: problem too large");

@@ -106,26 +106,34 @@ __global__ __launch_bounds__(256) void segment_scan_rev_kernel(const float* __re
   }
 }
 
-// Backward of out = H[:, :p-1] / H[:, p-1] * g, one wave per row:
-//   dH_c = dout_c g / den (c < p-1),  dH_{p-1} = -sum_c dH_c H_c / den,
-//   dg = sum_c dout_c H_c / den.
+// Backward of out = N[:, :p-1] / den * g, one wave per row, where
+// N = H + [0; Y] (the Y rows added from row n on; Y may be null) and den is
+// N[:, p-1], floored at eps when kFloor (the layer's clamp_min):
+//   dN_c = dout_c g / den (c < p-1),
+//   dN_{p-1} = -sum_c dN_c N_c / den (0 where the floor is active),
+//   dg = sum_c dout_c N_c / den.
+// dN is the gradient of H and, from row n on, of Y as well.
+template <bool kFloor>
 __global__ __launch_bounds__(256) void normalise_bwd_kernel(
-    const float* __restrict__ dout, const float* __restrict__ H, const float* __restrict__ g,
-    float* __restrict__ dH, float* __restrict__ dg, int T, int p, int64_t o_sb, int64_t o_st,
-    int64_t h_sb, int64_t h_st, int64_t d_sb, int64_t d_st, int64_t g_sb) {
+    const float* __restrict__ dout, const float* __restrict__ H, const float* __restrict__ Y,
+    const float* __restrict__ g, float* __restrict__ dH, float* __restrict__ dg, int T, int n,
+    int p, float eps, int64_t o_sb, int64_t o_st, int64_t h_sb, int64_t h_st, int64_t y_sb,
+    int64_t y_st, int64_t d_sb, int64_t d_st, int64_t g_sb) {
   const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
   const int64_t b = blockIdx.y;
   const int lane = lane_id();
   if (row >= T) return;
   const float* h = H + b * h_sb + row * h_st;
+  const float* y = (Y != nullptr && row >= n) ? Y + b * y_sb + (row - n) * y_st : nullptr;
   const float* d = dout + b * o_sb + row * o_st;
   float* dh = dH + b * d_sb + row * d_st;
-  const float den = h[p - 1];
+  const float den_raw = y ? h[p - 1] + y[p - 1] : h[p - 1];
+  const float den = kFloor ? fmaxf(den_raw, eps) : den_raw;
   const float inv = 1.f / den;
   const float gate = g ? g[b * g_sb + row] : 1.f;
   float sh = 0.f, sg = 0.f;
   for (int c = lane; c < p - 1; c += 64) {
-    const float o = h[c] * inv;
+    const float o = (y ? h[c] + y[c] : h[c]) * inv;
     const float dc = d[c] * gate * inv;
     dh[c] = dc;
     sh += dc * o;
@@ -136,7 +144,7 @@ __global__ __launch_bounds__(256) void normalise_bwd_kernel(
     sg += __shfl_down(sg, off, 64);
   }
   if (lane == 0) {
-    dh[p - 1] = -sh;
+    dh[p - 1] = (kFloor && !(den_raw >= eps)) ? 0.f : -sh;
     if (dg) dg[b * T + row] = sg;
   }
 }
@@ -150,11 +158,13 @@ int segment_scan_dispatch(const float* D, float* Sin, int nb, int nc, int nc0, i
   return launch_status("smat_segment_scan");
 }
 
-// One wave per output row: the normaliser is read once, every column divided.
+// One wave per output row: the normaliser is read once, every column divided;
+// with kFloor (eps >= 0 at dispatch) the normaliser is floored at eps first.
+template <bool kFloor>
 __global__ __launch_bounds__(256) void normalise_kernel(
     const float* __restrict__ H, const float* __restrict__ Y, const float* __restrict__ g,
-    float* __restrict__ out, int T, int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb,
-    int64_t y_st, int64_t o_sb, int64_t o_st, int64_t g_sb) {
+    float* __restrict__ out, int T, int n, int p, float eps, int64_t h_sb, int64_t h_st,
+    int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st, int64_t g_sb) {
   const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
   const int64_t b = blockIdx.y;
   const int lane = lane_id();
@@ -163,6 +173,7 @@ __global__ __launch_bounds__(256) void normalise_kernel(
   const float* y = (Y != nullptr && row >= n) ? Y + b * y_sb + (row - n) * y_st : nullptr;
   float den = h[p - 1];
   if (y) den += y[p - 1];
+  if (kFloor) den = fmaxf(den, eps);
   const float gate = g ? g[b * g_sb + row] : 1.f;
   float* o = out + b * o_sb + row * o_st;
   for (int c = lane; c < p - 1; c += 64) {
@@ -176,12 +187,33 @@ __global__ __launch_bounds__(256) void normalise_kernel(
 
 int normalise_dispatch(const float* H, const float* Y, const float* g, float* out, int nb, int T,
                        int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb, int64_t y_st,
-                       int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream) {
+                       int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream,
+                       float eps) {
   if (nb == 0 || T == 0) return SMAT_OK;
   dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
-  hipLaunchKernelGGL(normalise_kernel, grid, dim3(256), 0, stream, H, Y, g, out, T, n, p, h_sb,
-                     h_st, y_sb, y_st, o_sb, o_st, g_sb);
+  if (eps >= 0.f)
+    hipLaunchKernelGGL(normalise_kernel<true>, grid, dim3(256), 0, stream, H, Y, g, out, T, n, p,
+                       eps, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb);
+  else
+    hipLaunchKernelGGL(normalise_kernel<false>, grid, dim3(256), 0, stream, H, Y, g, out, T, n, p,
+                       0.f, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb);
   return launch_status("smat_normalise");
+}
+
+int normalise_bwd_dispatch(const float* dout, const float* H, const float* Y, const float* g,
+                           float* dH, float* dg, int nb, int T, int n, int p, float eps,
+                           int64_t o_sb, int64_t o_st, int64_t h_sb, int64_t h_st, int64_t y_sb,
+                           int64_t y_st, int64_t d_sb, int64_t d_st, int64_t g_sb,
+                           hipStream_t stream) {
+  if (nb == 0 || T == 0) return SMAT_OK;
+  dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
+  if (eps >= 0.f)
+    hipLaunchKernelGGL(normalise_bwd_kernel<true>, grid, dim3(256), 0, stream, dout, H, Y, g, dH,
+                       dg, T, n, p, eps, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st, g_sb);
+  else
+    hipLaunchKernelGGL(normalise_bwd_kernel<false>, grid, dim3(256), 0, stream, dout, H, Y, g, dH,
+                       dg, T, n, p, 0.f, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st, g_sb);
+  return launch_status("smat_normalise_backward");
 }
 
 }  // namespace smat
@@ -236,7 +268,7 @@ extern "C" int smat_normalise(const float* H, const float* Y, const float* g, fl
                "smat_normalise: bad sizes (T=%d n=%d p=%d)", T, n, p);
   SMAT_REQUIRE(h_st >= p && o_st >= p - 1, SMAT_EINVAL, "smat_normalise: row stride too short");
   return normalise_dispatch(H, Y, g, out, nb, T, n, p, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb,
-                            (hipStream_t)stream);
+                            (hipStream_t)stream, -1.f);
 }
 
 extern "C" int smat_segment_scan_reverse(const float* D, float* Sout, int nb, int nc, int nc0,
@@ -263,9 +295,36 @@ extern "C" int smat_normalise_backward(const float* dout, const float* H, const 
   SMAT_REQUIRE(dout && H && dH, SMAT_EINVAL, "smat_normalise_backward: null pointer");
   SMAT_REQUIRE(nb >= 0 && T >= 0 && p >= 2 && h_st >= p && d_st >= p && o_st >= p - 1,
                SMAT_EINVAL, "smat_normalise_backward: bad sizes");
-  if (nb == 0 || T == 0) return SMAT_OK;
-  dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
-  hipLaunchKernelGGL(normalise_bwd_kernel, grid, dim3(256), 0, (hipStream_t)stream, dout, H, g, dH,
-                     dg, T, p, o_sb, o_st, h_sb, h_st, d_sb, d_st, g_sb);
-  return launch_status("smat_normalise_backward");
+  return normalise_bwd_dispatch(dout, H, nullptr, g, dH, dg, nb, T, 0, p, -1.f, o_sb, o_st, h_sb,
+                                h_st, 0, 0, d_sb, d_st, g_sb, (hipStream_t)stream);
+}
+
+extern "C" int smat_combine_normalise(const float* H, const float* Y, float* out, int nb, int T,
+                                      int n, int p, float eps, int64_t h_sb, int64_t h_st,
+                                      int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
+                                      void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(H && out, SMAT_EINVAL, "smat_combine_normalise: null pointer");
+  SMAT_REQUIRE(nb >= 0 && T >= 0 && n >= 0 && n <= T && p >= 2 && eps >= 0.f, SMAT_EINVAL,
+               "smat_combine_normalise: bad sizes (T=%d n=%d p=%d) or eps < 0", T, n, p);
+  SMAT_REQUIRE(h_st >= p && o_st >= p - 1 && (!Y || y_st >= p), SMAT_EINVAL,
+               "smat_combine_normalise: row stride too short");
+  return normalise_dispatch(H, Y, nullptr, out, nb, T, n, p, h_sb, h_st, y_sb, y_st, o_sb, o_st, 0,
+                            (hipStream_t)stream, eps);
+}
+
+extern "C" int smat_combine_normalise_backward(const float* dout, const float* H, const float* Y,
+                                               float* dH, int nb, int T, int n, int p, float eps,
+                                               int64_t o_sb, int64_t o_st, int64_t h_sb,
+                                               int64_t h_st, int64_t y_sb, int64_t y_st,
+                                               int64_t d_sb, int64_t d_st, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(dout && H && dH, SMAT_EINVAL, "smat_combine_normalise_backward: null pointer");
+  SMAT_REQUIRE(nb >= 0 && T >= 0 && n >= 0 && n <= T && p >= 2 && eps >= 0.f && h_st >= p &&
+                   d_st >= p && o_st >= p - 1 && (!Y || y_st >= p),
+               SMAT_EINVAL, "smat_combine_normalise_backward: bad sizes");
+  return normalise_bwd_dispatch(dout, H, Y, nullptr, dH, nullptr, nb, T, n, p, eps, o_sb, o_st,
+                                h_sb, h_st, y_sb, y_st, d_sb, d_st, 0, (hipStream_t)stream);
 }

@@ -33,7 +33,7 @@ class HipKernelError(RuntimeError):
         self.func, self.code = func, code
 
 
-_i, _i64, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+_i, _i64, _p, _f = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
 
 # name -> (restype, argtypes); must match include/smat_hip.h
 SIGNATURES = {
@@ -60,6 +60,10 @@ SIGNATURES = {
     "smat_segment_scan_reverse": (_i, [_p, _p, _i, _i, _i, _i64, _p]),
     "smat_normalise_backward": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i64, _i64, _i64, _i64,
                                      _i64, _i64, _i64, _p]),
+    "smat_combine_normalise": (_i, [_p, _p, _p, _i, _i, _i, _i, _f, _i64, _i64, _i64, _i64,
+                                    _i64, _i64, _p]),
+    "smat_combine_normalise_backward": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _f, _i64, _i64,
+                                             _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "smat_bgemm": (_i, [_i, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64,
                         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _p]),
     "smat_chunk_backward": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,

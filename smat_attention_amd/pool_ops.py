@@ -36,18 +36,31 @@ __all__ = ["pool_segmented", "read_gather", "pool_sorted", "read_sorted"]
 # List helpers
 # ---------------------------------------------------------------------------
 
+def _csr(key, nkeys):
+    """Stable order of ``key`` (int64, values in [0, nkeys)) and the offsets
+    (int64, nkeys + 1) of each key's run in that order: a sort and a binary
+    search on the device, nothing read back to the host (a count by
+    ``bincount`` reads the largest key back, which stalls the host until the
+    device has caught up)."""
+    ks, order = torch.sort(key, stable=True)
+    offs = torch.searchsorted(ks, torch.arange(nkeys + 1, device=key.device, dtype=key.dtype))
+    return order, offs
+
+
+def _list_hint(n, ncls):
+    """Grid size hint of ``smat_query_lists``: twice the mean list length of n
+    rows over ncls classes (longer lists are covered by the same workgroups)."""
+    return 2 * -(-n // max(ncls, 1))
+
+
 def _lists(cls, ncls):
     """CSR of the rows of each (sequence, class): cls (nb, L) int -> row indices
     (int32, into the (nb*L) flattened rows, ascending within a class), offsets
-    (int64, nb*ncls + 1) and the longest list."""
+    (int64, nb*ncls + 1) and the list-length hint of the query kernel."""
     nb, L = cls.shape
     key = (torch.arange(nb, device=cls.device).unsqueeze(1) * ncls + cls).reshape(-1)
-    order = torch.argsort(key, stable=True)
-    counts = torch.bincount(key, minlength=nb * ncls)
-    offs = torch.zeros(nb * ncls + 1, device=cls.device, dtype=torch.int64)
-    offs[1:] = torch.cumsum(counts, 0)
-    maxcnt = int(counts.max().item()) if counts.numel() else 0
-    return order.to(torch.int32), offs, maxcnt
+    order, offs = _csr(key, nb * ncls)
+    return order.to(torch.int32), offs, _list_hint(L, ncls)
 
 
 def _gram_lists(A, B, cls, ncls, lists=None):

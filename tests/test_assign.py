@@ -318,6 +318,46 @@ def test_pool_ops_refuse_cpu_tensors_and_bad_cells():
         pool_ops._check("pool_segmented", idx + 3, torch.ones(1, 4, 1), 3, 4)
 
 
+def test_csr_offsets_match_counts():
+    """The device CSR builder (a stable sort and a binary search, no read-back)
+    against bincount and a stable argsort, empty keys and an empty input
+    included."""
+    from smat_attention_amd.pool_ops import _csr
+    gen = torch.Generator().manual_seed(3)
+    for n, nkeys in ((1000, 37), (5, 40), (0, 4), (300, 1)):
+        key = torch.randint(0, nkeys, (n,), generator=gen)
+        if n:
+            key[key == nkeys // 2] = 0                  # some keys with no entries
+        order, offs = _csr(key, nkeys)
+        counts = torch.bincount(key, minlength=nkeys)
+        assert torch.equal(offs[1:] - offs[:-1], counts) and offs[0] == 0 and offs[-1] == n
+        assert torch.equal(order, torch.argsort(key, stable=True))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hint", [0, 1, 64, None])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_list_read_covers_lists_longer_than_the_grid(hint, dt):
+    """smat_query_lists sized by a hint below the longest list (80 % of the
+    rows in one class, up to 560 rows against a 64-row workgroup): every row is
+    still read, y_l = X_l U[cls_l] against the fp64 product (1e-5 for fp32, the
+    bf16 inputs' own values for bf16)."""
+    from smat_attention_amd import pool_ops
+    gen = torch.Generator().manual_seed(17)
+    nb, L, ncls, r, p = 2, 700, 5, 64, 65
+    cls = torch.where(torch.rand(nb, L, generator=gen) < 0.8, 0,
+                      torch.randint(1, ncls, (nb, L), generator=gen))
+    X = torch.randn(nb, L, r, generator=gen).to(dt)
+    U = torch.randn(nb, ncls, r, p, generator=gen)
+    dev = torch.device("cuda:0")
+    rows, offs, h = pool_ops._lists(cls.to(dev), ncls)
+    Y = pool_ops._read_lists(X.to(dev), U.to(dev), cls.to(dev),
+                             (rows, offs, h if hint is None else hint))
+    Ug = U.double()[torch.arange(nb).unsqueeze(1), cls]
+    ref = (X.double().unsqueeze(-1) * Ug).sum(-2)
+    assert _grel(Y.cpu(), ref) < (1e-5 if dt == torch.float32 else 1e-4)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("K,r,p", [(1, 16, 17), (4, 16, 17), (8, 128, 129)])
 def test_pool_ops_match_dense_maps(K, r, p):

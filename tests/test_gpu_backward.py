@@ -390,6 +390,46 @@ def test_fused_cell_backward(d):
         assert e < (2e-3 if name in ("dQ", "dK", "dV") else 1e-4), name
 
 
+@pytest.mark.parametrize("T,n,p,with_y", [(300, 128, 65, True), (256, 0, 65, True),
+                                           (256, 256, 129, False), (1000, 512, 17, True)])
+def test_combine_normalise(T, n, p, with_y):
+    """combine_normalise (smat_combine_normalise and its backward) against the
+    reference layer's torch ops in fp64 -- ``cat([H[:, :n], H[:, n:] + Y])``
+    then ``N[..., :-1] / N[..., -1:].clamp_min(1e-6)`` (model.py:296-300) --
+    output and the gradients of H and Y within 1e-6 of the largest entry.  A
+    tenth of the rows have a normaliser below the floor (down to 0), where the
+    floor divides and passes no gradient to the normaliser."""
+    gen = torch.Generator().manual_seed(T + n + p)
+    nb = 3
+    H = torch.randn(nb, T, p, generator=gen)
+    H[..., -1] = H[..., -1].abs() + 0.5
+    Y = torch.randn(nb, T - n, p, generator=gen) * 0.3 if with_y else None
+    if Y is not None:
+        Y[..., -1] = Y[..., -1].abs()
+    small = torch.rand(nb, T, generator=gen) < 0.1
+    H[..., -1] = torch.where(small, torch.rand(nb, T, generator=gen) * 1e-6, H[..., -1])
+    if Y is not None:
+        Y[..., -1] = torch.where(small[:, n:], torch.zeros(()), Y[..., -1])
+    dO = torch.randn(nb, T, p - 1, generator=gen)
+
+    def ref(h, y):
+        N = h if y is None else torch.cat([h[:, :n], h[:, n:] + y], dim=1)
+        return N[..., :-1] / N[..., -1:].clamp_min(1e-6)
+
+    xs0 = [t.double().requires_grad_(True) for t in (H, Y) if t is not None]
+    o0 = ref(*(xs0 if with_y else xs0 + [None]))
+    (o0 * dO.double()).sum().backward()
+    xs1 = [t.to(DEV).requires_grad_(True) for t in (H, Y) if t is not None]
+    o1 = A.combine_normalise(xs1[0], xs1[1] if with_y else None, n)
+    (o1 * dO.to(DEV)).sum().backward()
+    assert o1.dtype == torch.float32 and o1.shape == (nb, T, p - 1)
+    assert _grel(o1.detach().cpu(), o0.detach()) < 1e-6
+    for name, a, b in zip(("dH", "dY"), xs1, xs0):
+        e = _grel(a.grad.cpu(), b.grad)
+        _say(f"  {name}: {e:.2e}")
+        assert e < 1e-6, name
+
+
 @pytest.mark.parametrize("d,plant,nb,L,dm", [(2, False, 2, 300, 96), (2, True, 2, 517, 96),
                                              (3, True, 1, 1000, 768), (3, False, 3, 64, 160),
                                              (4, True, 2, 256, 96), (5, True, 1, 700, 64)])
