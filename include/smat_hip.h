@@ -514,6 +514,22 @@ int smat_query_lists(int dtype, const void* phi, const float* U, float* Y,
                      int r, int p, int64_t q_st, int64_t y_st, void* stream);
 
 /*
+ * Class lists (CSR) of every sequence by a counting sort: keys (nb, L) int64 in
+ * [0, ncls) -> order (nb*L) int32, the items of sequence 0's class 0, class 1,
+ * ..., then sequence 1's, each list in item order (the stable sort of
+ * b*ncls + key); an item is b*L + l (global_index) or l.  offs (nb*ncls + 1)
+ * int64: list (b, c) is order[offs[b*ncls + c] .. offs[b*ncls + c + 1]).
+ * workspace: smat_csr_workspace_bytes(nb, L, ncls) bytes.  ncls <= 8192,
+ * nb*L < 2^31; keys outside [0, ncls) are clamped into it.  Nothing is read
+ * back to the host.  Replaces the torch.argsort / bincount grouping of the
+ * cell and type lists, src/smat/assign.py:431-439 and
+ * src/smat/kernels/smat_pool_ops.py:158-182.
+ */
+int64_t smat_csr_workspace_bytes(int nb, int L, int ncls);
+int smat_csr_lists(const int64_t* keys, int32_t* order, int64_t* offs, void* workspace, int nb,
+                   int L, int ncls, int global_index, void* stream);
+
+/*
  * Content hash of token rows u (nb, L, dm; dtype of u): for head h and
  * coordinate k < dim, z = (LN(u) . Wn[h,k]) gamma[h,k] + bias[h,k],
  * s = clamp(q Phi_N(z), 0, q - 1e-4), cell = sum_k floor(s_k) q^(dim-1-k).

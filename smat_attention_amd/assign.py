@@ -39,8 +39,8 @@ import torch
 import torch.nn as nn
 
 from .kernels.hip_fwd import _code, _on_gpu, _rows3, call, stream_of
-from .pool_ops import (_csr, _f32_rows, _gram_lists, _list_hint, _lists, _read_lists, _read_pairs,
-                       _repeat, pool_sorted, read_sorted)
+from .pool_ops import (_class_lists, _f32_rows, _gram_lists, _list_hint, _lists, _read_lists,
+                       _read_pairs, _repeat, pool_sorted, read_sorted)
 
 __all__ = ["ContentAssign", "grouped_planes"]
 
@@ -309,8 +309,14 @@ class ContentAssign(nn.Module):
             hk = torch.cat([h.new_zeros(h.shape[0], self.shift, h.shape[2]),
                             h[:, :-self.shift]], dim=1)
         if self._fused_pairs_ok(h, key_w, single):
-            ck, idxk, wk, aux_k = self._hash_pairs(hk[:, :n], plant_at=True)
-            cq, idxq, wq, aux_q = self._hash_pairs(h[:, n:])
+            if hk is h:
+                # one LayerNorm and projection over the whole hidden state
+                z = self._hash_z(h)
+                ck, idxk, wk, aux_k = self._pairs_from_z(z[:, :n], plant_at=True)
+                cq, idxq, wq, aux_q = self._pairs_from_z(z[:, n:])
+            else:
+                ck, idxk, wk, aux_k = self._pairs_from_z(self._hash_z(hk[:, :n]), plant_at=True)
+                cq, idxq, wq, aux_q = self._pairs_from_z(self._hash_z(h[:, n:]))
         else:
             ck, idxk, wk, aux_k = self._ste_pairs(self._soft_hash(hk[:, :n]), plant_at=True,
                                                   tok_w=key_w, single=single)
@@ -339,19 +345,27 @@ class ContentAssign(nn.Module):
 
     def _hash_pairs(self, hu, plant_at=False):
         """``_ste_pairs(_soft_hash(hu))`` at ``anneal = 1`` with no token
-        weights, in three autograd steps: the projections z (LayerNorm and the
-        unit rows as in :meth:`_soft_hash`, torch), then the pairs, the
-        straight-through weights and the occupancy (``smat_hash_pairs``, with
-        ``smat_hash_pairs_backward`` for the gradient of z), then the
-        load-balance term from the occupancy (torch)."""
+        weights, in three autograd steps: the projections z (:meth:`_hash_z`),
+        then the pairs, the straight-through weights and the occupancy
+        (``smat_hash_pairs``, with ``smat_hash_pairs_backward`` for the gradient
+        of z), then the load-balance term from the occupancy (torch)."""
+        return self._pairs_from_z(self._hash_z(hu), plant_at)
+
+    def _hash_z(self, hu):
+        """z = LN(hu) . Wn gamma + b, (nb, L, h*dim), as :meth:`_soft_hash`
+        before the CDF; the product's weight gradient is split over the
+        tokens (:class:`_Project`)."""
         nb, L, dm = hu.shape
         Wn = self.W / self.W.norm(dim=-1, keepdim=True).clamp_min(1e-6)
         hd = self.h * self.dim
         xh = self.ln(hu).reshape(nb * L, dm)
-        z = (xh @ Wn.reshape(hd, dm).t()) * self.gamma.reshape(hd) + self.b.reshape(hd)
-        plant = self._plant_map(L, hu.device) if (plant_at and self.plant) else None
-        cells, idx, w, occ = _HashPairs.apply(z.reshape(nb, L, hd), self.h, self.dim, self.q,
-                                              plant)
+        z = _Project.apply(xh, Wn.reshape(hd, dm)) * self.gamma.reshape(hd) + self.b.reshape(hd)
+        return z.reshape(nb, L, hd)
+
+    def _pairs_from_z(self, z, plant_at=False):
+        nb, L, _ = z.shape
+        plant = self._plant_map(L, z.device) if (plant_at and self.plant) else None
+        cells, idx, w, occ = _HashPairs.apply(z, self.h, self.dim, self.q, plant)
         occ = occ / occ.sum(-1, keepdim=True).clamp_min(1e-6)
         aux = None if self.freeze else (occ * (occ.clamp_min(1e-9) * self.q).log()).sum(-1).mean()
         return cells, idx, w, aux
@@ -438,8 +452,8 @@ class ContentAssign(nn.Module):
         dev = Phi.device
         N0 = self.N0
         # ---- pool by cell: tokens of each (sequence, cell), in token order
-        key = (torch.arange(nbh, device=dev).unsqueeze(1) * N0 + ck).reshape(-1)
-        order, offs = _csr(key, nbh * N0)
+        order, offs = _class_lists(ck, N0)
+        order = order.long()
         seq = order // n
         tokens = (seq * T + (order - seq * n)).to(torch.int32)
         Ps = Psi if Psi.stride(0) == T * Psi.stride(1) else Psi.contiguous()
@@ -464,8 +478,8 @@ class ContentAssign(nn.Module):
                 e_star = dl.reshape(nbh, T_R, self.D).argmax(-1)
             typ = e_star * self.n_cosets + self.coset_of.to(dev)[e_star, cq]
             ntypes = nrows
-        key = (torch.arange(nbh, device=dev).unsqueeze(1) * ntypes + typ).reshape(-1)
-        order, roffs = _csr(key, nbh * ntypes)
+        order, roffs = _class_lists(typ, ntypes)
+        order = order.long()
         seq = order // T_R
         rows = (seq * T + n + (order - seq * T_R)).to(torch.int32)
         maxcnt = _list_hint(T_R, ntypes)
@@ -500,15 +514,41 @@ def _entry_lists(idx, N0):
     -> entry ids token*K + pair (int32, ascending within a cell) and offsets
     (int64, nb*N0 + 1)."""
     nb, L, K = idx.shape
-    key = (torch.arange(nb, device=idx.device).unsqueeze(1) * N0
-           + idx.reshape(nb, L * K)).reshape(-1)
-    order, eoffs = _csr(key, nb * N0)
-    return (order % (L * K)).to(torch.int32), eoffs
+    return _class_lists(idx.reshape(nb, L * K), N0, global_index=False)
 
 
 # The pairs of the training path from one kernel (smat_hash_pairs) and its
 # backward; tests switch it off to compare with the torch straight-through path.
 FUSED_HASH_PAIRS = True
+
+
+class _Project(torch.autograd.Function):
+    """``x @ W^T`` for many token rows x (R, dm) and few output rows W (k, dm).
+    The weight gradient ``dy^T x`` has a long contraction (R) and a small
+    output (k x dm); it is taken as a batched product over 16-32 slices of the
+    rows and a sum of the slices, which spreads it over many workgroups."""
+
+    @staticmethod
+    def forward(ctx, x, W):
+        ctx.save_for_backward(x, W)
+        return x @ W.t()
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, W = ctx.saved_tensors
+        dx = dy @ W if ctx.needs_input_grad[0] else None
+        dW = None
+        if ctx.needs_input_grad[1]:
+            R, k = dy.shape
+            S = 32
+            while S > 1 and (R % S or R // S < 256):
+                S //= 2
+            if S > 1:
+                dyT = dy.reshape(S, R // S, k).transpose(1, 2).contiguous()
+                dW = torch.bmm(dyT, x.reshape(S, R // S, x.shape[1]).contiguous()).sum(0)
+            else:
+                dW = dy.t().contiguous() @ x
+        return dx, dW
 
 
 class _HashPairs(torch.autograd.Function):

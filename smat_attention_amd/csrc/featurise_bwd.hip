@@ -179,14 +179,33 @@ __global__ __launch_bounds__(fb::kThreads) void featurise_bwd_kernel(
 }
 
 // dW[i] = (sum over parts of dWp[part][i]) (+ dW[i] when accumulating), fp32.
-__global__ __launch_bounds__(256) void featurise_dw_reduce_kernel(const float* __restrict__ dWp,
-                                                                  float* __restrict__ dW,
-                                                                  int nparts, int n, int beta) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
+// A workgroup owns 64 consecutive i (one coalesced 256-byte run per part);
+// its 16 waves take parts w, w + 16, ... with four independent loads in
+// flight, and the 16 partial sums meet in LDS, in a fixed order.
+__global__ __launch_bounds__(1024) void featurise_dw_reduce_kernel(const float* __restrict__ dWp,
+                                                                   float* __restrict__ dW,
+                                                                   int nparts, int n, int beta) {
+  __shared__ float red[16][64];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 64 + lane;
   float s = 0.f;
-  for (int p = 0; p < nparts; ++p) s += dWp[(int64_t)p * n + i];
-  dW[i] = beta ? dW[i] + s : s;
+  if (i < n) {
+    int p = w;
+    for (; p + 48 < nparts; p += 64) {
+      const float a = dWp[(int64_t)p * n + i], b = dWp[(int64_t)(p + 16) * n + i];
+      const float c = dWp[(int64_t)(p + 32) * n + i], d = dWp[(int64_t)(p + 48) * n + i];
+      s += (a + b) + (c + d);
+    }
+    for (; p < nparts; p += 16) s += dWp[(int64_t)p * n + i];
+  }
+  red[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && i < n) {
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t += red[k][lane];
+    dW[i] = beta ? dW[i] + t : t;
+  }
 }
 
 }  // namespace smat
@@ -237,7 +256,7 @@ extern "C" int smat_featurise_backward(int dtype, const void* x, const void* G, 
     if (rc != SMAT_OK) return rc;
   }
   const int n = fb::kD * fb::kD;
-  hipLaunchKernelGGL(featurise_dw_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, st, dWp, dW,
+  hipLaunchKernelGGL(featurise_dw_reduce_kernel, dim3((n + 63) / 64), dim3(1024), 0, st, dWp, dW,
                      (int)parts, n, beta);
   return launch_status("smat_featurise_backward");
 }

@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import torch
 
+from .kernels import _lib
 from .kernels.hip_fwd import _code, _on_gpu, call, stream_of
 
 __all__ = ["pool_segmented", "read_gather", "pool_sorted", "read_sorted"]
@@ -47,6 +48,35 @@ def _csr(key, nkeys):
     return order, offs
 
 
+_CSR_MAX_CLASSES = 8192
+
+
+def _class_lists(keys, ncls, global_index=True):
+    """Lists of every (sequence, class): keys (nb, L) in [0, ncls) -> order
+    (nb*L,) int32, the items of sequence 0's class 0, class 1, ..., then
+    sequence 1's, each list in item order (the stable sort of ``b*ncls + key``);
+    an item is ``b*L + l`` (``global_index``) or ``l``.  offs (nb*ncls + 1,)
+    int64.  A counting sort on the device (``smat_csr_lists``), nothing read
+    back to the host."""
+    nb, L = keys.shape
+    dev = keys.device
+    if ncls > _CSR_MAX_CLASSES:
+        flat = (torch.arange(nb, device=dev).unsqueeze(1) * ncls + keys).reshape(-1)
+        order, offs = _csr(flat, nb * ncls)
+        if not global_index:
+            order = order % max(L, 1)
+        return order.to(torch.int32), offs
+    k = keys if (keys.dtype == torch.int64 and keys.is_contiguous()) else \
+        keys.to(torch.int64).contiguous()
+    order = torch.empty(nb * L, device=dev, dtype=torch.int32)
+    offs = torch.empty(nb * ncls + 1, device=dev, dtype=torch.int64)
+    ws = torch.empty(max(1, _lib.query("smat_csr_workspace_bytes", nb, L, ncls)), device=dev,
+                     dtype=torch.uint8)
+    call("smat_csr_lists", k.data_ptr(), order.data_ptr(), offs.data_ptr(), ws.data_ptr(), nb, L,
+         ncls, int(global_index), stream_of(k))
+    return order, offs
+
+
 def _list_hint(n, ncls):
     """Grid size hint of ``smat_query_lists``: twice the mean list length of n
     rows over ncls classes (longer lists are covered by the same workgroups)."""
@@ -58,9 +88,8 @@ def _lists(cls, ncls):
     (int32, into the (nb*L) flattened rows, ascending within a class), offsets
     (int64, nb*ncls + 1) and the list-length hint of the query kernel."""
     nb, L = cls.shape
-    key = (torch.arange(nb, device=cls.device).unsqueeze(1) * ncls + cls).reshape(-1)
-    order, offs = _csr(key, nb * ncls)
-    return order.to(torch.int32), offs, _list_hint(L, ncls)
+    order, offs = _class_lists(cls, ncls)
+    return order, offs, _list_hint(L, ncls)
 
 
 def _gram_lists(A, B, cls, ncls, lists=None):

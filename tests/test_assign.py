@@ -335,6 +335,34 @@ def test_csr_offsets_match_counts():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("nb,L,ncls", [(3, 300, 7), (2, 5000, 169), (1, 2048, 1), (4, 64, 300),
+                                       (2, 0, 5), (96, 8192, 169), (1, 4100, 8192)])
+def test_class_lists_match_stable_sort(nb, L, ncls):
+    """smat_csr_lists (the counting sort behind every cell and type list)
+    against torch's stable argsort and bincount of ``b*ncls + key`` on the CPU:
+    the same order (as global and as in-sequence item ids) and offsets.  Ragged
+    tiles (L not a multiple of 2048), one class, empty classes, empty
+    sequences and the largest class count included."""
+    from smat_attention_amd.pool_ops import _class_lists
+    gen = torch.Generator().manual_seed(nb * 7 + L + ncls)
+    keys = torch.randint(0, ncls, (nb, L), generator=gen)
+    if L and ncls > 2:
+        keys[keys == ncls // 2] = 0                     # an empty class in every sequence
+    flat = (torch.arange(nb).unsqueeze(1) * ncls + keys).reshape(-1)
+    ref = torch.argsort(flat, stable=True)
+    cnt = torch.bincount(flat, minlength=nb * ncls)
+    dev = torch.device("cuda:0")
+    for glob in (True, False):
+        order, offs = _class_lists(keys.to(dev), ncls, global_index=glob)
+        assert order.dtype == torch.int32 and offs.dtype == torch.int64
+        want = ref if glob else ref % max(L, 1)
+        assert torch.equal(order.cpu().long(), want)
+        offs = offs.cpu()
+        assert offs[0] == 0 and offs[-1] == nb * L
+        assert torch.equal(offs[1:] - offs[:-1], cnt)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("hint", [0, 1, 64, None])
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 def test_list_read_covers_lists_longer_than_the_grid(hint, dt):

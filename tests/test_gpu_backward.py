@@ -475,6 +475,47 @@ def test_fused_hash_pairs(d, plant, nb, L, dm):
         assert torch.isfinite(a).all() and e < 1e-5, name
 
 
+@pytest.mark.parametrize("d,T,n", [(3, 1024, 512), (2, 700, 256), (4, 512, 384)])
+def test_fused_pairs_whole_state(d, T, n):
+    """Both sides' pairs from one LayerNorm and projection over the whole
+    hidden state (keys: rows before n, planted; queries: the rest) against the
+    torch straight-through path on each side's slice: cells, pair cells and
+    weights equal, and the gradients of u, W, gamma and b for random upstream
+    gradients of every pair weight plus 3 x the load-balance term within 1e-5
+    of the largest entry."""
+    from smat_attention_amd import assign as AS
+    H, dm, nb = 3, 128, 2
+    spec = build_mask(4096, d, chunk=128)
+    gen = torch.Generator().manual_seed(300 + d)
+    u0 = torch.randn(nb, T, dm, generator=gen)
+    K = 1 << spec.dim
+    Gk = torch.randn(nb * H, n, K, generator=gen).to(DEV)
+    Gq = torch.randn(nb * H, T - n, K, generator=gen).to(DEV)
+    torch.manual_seed(5)
+    m = AS.ContentAssign(H, dm, spec, mode="point").to(DEV)
+    _say("fused pairs over the whole state", d, T, n)
+
+    def run(fused):
+        AS.FUSED_HASH_PAIRS = fused
+        try:
+            m.zero_grad()
+            u = u0.to(DEV).requires_grad_(True)
+            ck, ik, wk, cq, iq, wq = m._pairs_of(u, n, None, None, None, None, False)
+            ((wk * Gk).sum() + (wq * Gq).sum() + 3.0 * m.aux).backward()
+            return ([t.cpu() for t in (ck, ik, wk.detach(), cq, iq, wq.detach())],
+                    [u.grad.cpu()] + [getattr(m, k).grad.detach().cpu() for k in ("W", "gamma", "b")])
+        finally:
+            AS.FUSED_HASH_PAIRS = True
+    f1, g1 = run(True)
+    f0, g0 = run(False)
+    for a, b in zip(f1, f0):
+        assert torch.equal(a, b)
+    for name, a, b in zip(("du", "dW", "dgamma", "db"), g1, g0):
+        e = _grel(a, b)
+        _say(f"  {name}: {e:.2e}")
+        assert torch.isfinite(a).all() and e < 1e-5, name
+
+
 @pytest.mark.parametrize("kind,gate,T", [("elu1", True, 1000), ("relu", True, 2048),
                                          ("elu1", False, 4096)])
 def test_fused_featurise_backward(kind, gate, T):
