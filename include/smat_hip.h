@@ -260,25 +260,29 @@ int smat_normalise_backward(const float* dout, const float* H, const float* g, f
 /*
  * The layer's combine and division with the normaliser floored at eps:
  * N = H + [0; Y] (Y's rows added from row n on; Y (nb, T-n, p) may be NULL),
- * out[t, c] = N[t, c] / max(N[t, p-1], eps) for c < p-1.  H (nb, T, p), out
- * (nb, T, p-1), fp32, each with its own (batch, row) strides.  Replaces
- * torch.cat([H[:, :n], H[:, n:] + Ylr]) and H[..., :-1] / H[..., -1:].clamp_min(eps)
- * of src/smat/model.py:296-300 (eps = 1e-6 there).
+ * out[t, c] = N[t, c] / max(N[t, p-1], eps) for c < p-1.  H, Y fp32 (nb, T, p);
+ * out (nb, T, p-1) of out_dtype (SMAT_F32, SMAT_BF16 or SMAT_F16: the fp32
+ * quotient rounded to nearest even), each with its own (batch, row) strides.
+ * Replaces torch.cat([H[:, :n], H[:, n:] + Ylr]), H[..., :-1] /
+ * H[..., -1:].clamp_min(eps) and the cast .to(x.dtype) of src/smat/model.py:296-300
+ * and :317 (eps = 1e-6 there).
  */
-int smat_combine_normalise(const float* H, const float* Y, float* out, int nb, int T, int n,
-                           int p, float eps, int64_t h_sb, int64_t h_st, int64_t y_sb,
-                           int64_t y_st, int64_t o_sb, int64_t o_st, void* stream);
+int smat_combine_normalise(int out_dtype, const float* H, const float* Y, void* out, int nb,
+                           int T, int n, int p, float eps, int64_t h_sb, int64_t h_st,
+                           int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st, void* stream);
 
 /*
  * Backward of smat_combine_normalise: dN[t, c] = dout[t, c] / den (c < p-1),
  * dN[t, p-1] = -sum_c dN[t, c] N[t, c] / den, or 0 where N[t, p-1] < eps (the
  * floor passes no gradient), den = max(N[t, p-1], eps).  dN (nb, T, p) is the
- * gradient of H, and its rows from n on are the gradient of Y.
+ * gradient of H, and its rows from n on are the gradient of Y.  dout of
+ * dout_dtype (SMAT_F32, SMAT_BF16 or SMAT_F16), widened to fp32.
  */
-int smat_combine_normalise_backward(const float* dout, const float* H, const float* Y, float* dH,
-                                    int nb, int T, int n, int p, float eps, int64_t o_sb,
-                                    int64_t o_st, int64_t h_sb, int64_t h_st, int64_t y_sb,
-                                    int64_t y_st, int64_t d_sb, int64_t d_st, void* stream);
+int smat_combine_normalise_backward(int dout_dtype, const void* dout, const float* H,
+                                    const float* Y, float* dH, int nb, int T, int n, int p,
+                                    float eps, int64_t o_sb, int64_t o_st, int64_t h_sb,
+                                    int64_t h_st, int64_t y_sb, int64_t y_st, int64_t d_sb,
+                                    int64_t d_st, void* stream);
 
 /*
  * Strided batched GEMM on fp32 MFMA (backward pass building block):

@@ -320,13 +320,15 @@ def segmented_causal_scan(Phi, Psi, Vb, n: int, chunk: int = 128,
     return _causal_scan(Phi, Psi, Vb, n, C)
 
 
-def combine_normalise(H, Y, n: int, eps: float = 1e-6):
+def combine_normalise(H, Y, n: int, eps: float = 1e-6, out_dtype=torch.float32):
     """The layer's last step over the causal term ``H`` (nb, T, p) and the
     long-range term ``Y`` (nb, T - n, p) of the recent rows, in one kernel each
     way: ``N = cat([H[:, :n], H[:, n:] + Y], 1)``, then
-    ``N[..., :-1] / N[..., -1:].clamp_min(eps)`` (model.py:296-300, 311-316).
-    ``Y`` may be None (no long-range rows).  Returns fp32 (nb, T, p - 1);
-    differentiable in H and Y."""
+    ``N[..., :-1] / N[..., -1:].clamp_min(eps)`` (model.py:296-300, 311-316),
+    computed in fp32 and stored as ``out_dtype`` (fp32, or the layer's
+    ``.to(x.dtype)`` cast of model.py:317 folded in: bf16 / fp16, rounded to
+    nearest even).  ``Y`` may be None (no long-range rows).  Returns
+    (nb, T, p - 1); differentiable in H and Y."""
     who = "combine_normalise"
     _hip._on_gpu(who, H, Y)
     nb, T, P = H.shape
@@ -336,8 +338,10 @@ def combine_normalise(H, Y, n: int, eps: float = 1e-6):
         raise ValueError(f"{who}: Y must be {(nb, T - n, P)}, got {tuple(Y.shape)}")
     if eps < 0:
         raise ValueError(f"{who}: eps must be >= 0")
+    if out_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError(f"{who}: out_dtype must be float32, bfloat16 or float16")
     from .kernels.hip_bwd import CombineNormaliseFunction
-    return CombineNormaliseFunction.apply(H, Y, n, eps)
+    return CombineNormaliseFunction.apply(H, Y, n, eps, out_dtype)
 
 
 def _causal_scan(Phi, Psi, Vb, n: int, C: int):

@@ -14,6 +14,27 @@
 namespace smat {
 
 namespace cb {
+
+// The (item, sequence) of this workgroup of a (nitems, nseq) grid, with all the
+// items of a sequence on one XCD: workgroups are dispatched to the 8 XCDs
+// round-robin by linear id, so XCD x takes sequences x, x + 8, ... in turn
+// and the rows its items share (a token in several cells' or points' lists)
+// are re-read from that XCD's L2 instead of from HBM.  Sequences past the
+// last multiple of 8 keep the plain mapping.
+__device__ __forceinline__ void xcd_item_seq(int& item, int64_t& seq) {
+  const int64_t nitems = gridDim.x, nseq = gridDim.y;
+  const int64_t lin = (int64_t)blockIdx.y * nitems + blockIdx.x;
+  const int64_t full = (nseq / 8) * 8 * nitems;
+  if (lin < full) {
+    const int64_t k = lin >> 3;
+    seq = (lin & 7) + 8 * (k / nitems);
+    item = (int)(k % nitems);
+  } else {
+    seq = lin / nitems;
+    item = (int)(lin % nitems);
+  }
+}
+
 constexpr int kC = 128;          // tokens per chunk
 constexpr int kR = 64;           // features
 constexpr int kP = 65;           // value columns incl. the ones column

@@ -52,8 +52,9 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
   __shared__ float sDotB[2][4][cw::kStep];
   __shared__ int sTokB[2][cw::kStep], sPairB[2][cw::kStep];
 
-  const int x = blockIdx.x;
-  const int64_t b = blockIdx.y;
+  int x;
+  int64_t b;
+  xcd_item_seq(x, b);
   const int tid = threadIdx.x;
   const int64_t beg = eoffs[b * N0 + x], end = eoffs[b * N0 + x + 1];
   const In* phb = phr + b * q_sb;
@@ -205,8 +206,9 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
   __shared__ __attribute__((aligned(16))) float sV[cw::kStep * kS];
   __shared__ float sDotB[2][4][cw::kStep];
   __shared__ int sTokB[2][cw::kStep], sPairB[2][cw::kStep];
-  const int x = blockIdx.x;
-  const int64_t b = blockIdx.y;
+  int x;
+  int64_t b;
+  xcd_item_seq(x, b);
   const int tid = threadIdx.x;
   const int64_t beg = eoffs[b * N0 + x], end = eoffs[b * N0 + x + 1];
   if (beg == end) return;                            // uniform over the workgroup

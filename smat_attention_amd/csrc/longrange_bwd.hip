@@ -113,8 +113,9 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dfeat_kernel(
   typedef typename Traits<In>::half_frag Half;
   __shared__ __attribute__((aligned(16))) uint4 sPh[lr::kStep * kRowChunks];
   __shared__ __attribute__((aligned(16))) float sY[lr::kStep * kS];
-  const int x = blockIdx.x;
-  const int64_t b = blockIdx.y;
+  int x;
+  int64_t b;
+  xcd_item_seq(x, b);
   const int tid = threadIdx.x;
   const int64_t beg = tptr[x], end = tptr[x + 1];
   const In* phib = phi + b * q_sb;
@@ -217,8 +218,9 @@ __global__ __launch_bounds__(lr::kThreads) void lr_pool_bwd_kernel(
   typedef typename Traits<In>::frag Frag;
   typedef typename Traits<In>::half_frag Half;
   __shared__ __attribute__((aligned(16))) float sF[kR * kS];
-  const int x = blockIdx.x;
-  const int64_t b = blockIdx.y;
+  int x;
+  int64_t b;
+  xcd_item_seq(x, b);
   const int64_t start = x < N0 ? (int64_t)n_P + x : 0;
   const int64_t stride = x < N0 ? N0 : 1;
   const int nX = n - n_P;

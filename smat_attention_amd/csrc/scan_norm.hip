@@ -113,9 +113,9 @@ __global__ __launch_bounds__(256) void segment_scan_rev_kernel(const float* __re
 //   dN_{p-1} = -sum_c dN_c N_c / den (0 where the floor is active),
 //   dg = sum_c dout_c N_c / den.
 // dN is the gradient of H and, from row n on, of Y as well.
-template <bool kFloor>
+template <bool kFloor, typename Din>
 __global__ __launch_bounds__(256) void normalise_bwd_kernel(
-    const float* __restrict__ dout, const float* __restrict__ H, const float* __restrict__ Y,
+    const Din* __restrict__ dout, const float* __restrict__ H, const float* __restrict__ Y,
     const float* __restrict__ g, float* __restrict__ dH, float* __restrict__ dg, int T, int n,
     int p, float eps, int64_t o_sb, int64_t o_st, int64_t h_sb, int64_t h_st, int64_t y_sb,
     int64_t y_st, int64_t d_sb, int64_t d_st, int64_t g_sb) {
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(256) void normalise_bwd_kernel(
   if (row >= T) return;
   const float* h = H + b * h_sb + row * h_st;
   const float* y = (Y != nullptr && row >= n) ? Y + b * y_sb + (row - n) * y_st : nullptr;
-  const float* d = dout + b * o_sb + row * o_st;
+  const Din* d = dout + b * o_sb + row * o_st;
   float* dh = dH + b * d_sb + row * d_st;
   const float den_raw = y ? h[p - 1] + y[p - 1] : h[p - 1];
   const float den = kFloor ? fmaxf(den_raw, eps) : den_raw;
@@ -134,10 +134,11 @@ __global__ __launch_bounds__(256) void normalise_bwd_kernel(
   float sh = 0.f, sg = 0.f;
   for (int c = lane; c < p - 1; c += 64) {
     const float o = (y ? h[c] + y[c] : h[c]) * inv;
-    const float dc = d[c] * gate * inv;
+    const float dv = to_f32(d[c]);
+    const float dc = dv * gate * inv;
     dh[c] = dc;
     sh += dc * o;
-    sg += d[c] * o;
+    sg += dv * o;
   }
   for (int off = 32; off > 0; off >>= 1) {
     sh += __shfl_down(sh, off, 64);
@@ -160,10 +161,10 @@ int segment_scan_dispatch(const float* D, float* Sin, int nb, int nc, int nc0, i
 
 // One wave per output row: the normaliser is read once, every column divided;
 // with kFloor (eps >= 0 at dispatch) the normaliser is floored at eps first.
-template <bool kFloor>
+template <bool kFloor, typename Out>
 __global__ __launch_bounds__(256) void normalise_kernel(
     const float* __restrict__ H, const float* __restrict__ Y, const float* __restrict__ g,
-    float* __restrict__ out, int T, int n, int p, float eps, int64_t h_sb, int64_t h_st,
+    Out* __restrict__ out, int T, int n, int p, float eps, int64_t h_sb, int64_t h_st,
     int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st, int64_t g_sb) {
   const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
   const int64_t b = blockIdx.y;
@@ -175,44 +176,56 @@ __global__ __launch_bounds__(256) void normalise_kernel(
   if (y) den += y[p - 1];
   if (kFloor) den = fmaxf(den, eps);
   const float gate = g ? g[b * g_sb + row] : 1.f;
-  float* o = out + b * o_sb + row * o_st;
+  Out* o = out + b * o_sb + row * o_st;
   for (int c = lane; c < p - 1; c += 64) {
     float num = h[c];
     if (y) num += y[c];
     float v = num / den;
     if (g) v *= gate;
-    o[c] = v;
+    o[c] = from_f32<Out>(v);
   }
+}
+
+template <typename Out>
+static int launch_normalise(const float* H, const float* Y, const float* g, Out* out, int nb, int T,
+                            int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb, int64_t y_st,
+                            int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream,
+                            float eps) {
+  if (nb == 0 || T == 0) return SMAT_OK;
+  dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
+  if (eps >= 0.f)
+    hipLaunchKernelGGL((normalise_kernel<true, Out>), grid, dim3(256), 0, stream, H, Y, g, out, T,
+                       n, p, eps, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb);
+  else
+    hipLaunchKernelGGL((normalise_kernel<false, Out>), grid, dim3(256), 0, stream, H, Y, g, out, T,
+                       n, p, 0.f, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb);
+  return launch_status("smat_normalise");
 }
 
 int normalise_dispatch(const float* H, const float* Y, const float* g, float* out, int nb, int T,
                        int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb, int64_t y_st,
                        int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream,
                        float eps) {
-  if (nb == 0 || T == 0) return SMAT_OK;
-  dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
-  if (eps >= 0.f)
-    hipLaunchKernelGGL(normalise_kernel<true>, grid, dim3(256), 0, stream, H, Y, g, out, T, n, p,
-                       eps, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb);
-  else
-    hipLaunchKernelGGL(normalise_kernel<false>, grid, dim3(256), 0, stream, H, Y, g, out, T, n, p,
-                       0.f, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb);
-  return launch_status("smat_normalise");
+  return launch_normalise<float>(H, Y, g, out, nb, T, n, p, h_sb, h_st, y_sb, y_st, o_sb, o_st,
+                                 g_sb, stream, eps);
 }
 
-int normalise_bwd_dispatch(const float* dout, const float* H, const float* Y, const float* g,
-                           float* dH, float* dg, int nb, int T, int n, int p, float eps,
-                           int64_t o_sb, int64_t o_st, int64_t h_sb, int64_t h_st, int64_t y_sb,
-                           int64_t y_st, int64_t d_sb, int64_t d_st, int64_t g_sb,
-                           hipStream_t stream) {
+template <typename Din>
+static int launch_normalise_bwd(const Din* dout, const float* H, const float* Y, const float* g,
+                                float* dH, float* dg, int nb, int T, int n, int p, float eps,
+                                int64_t o_sb, int64_t o_st, int64_t h_sb, int64_t h_st,
+                                int64_t y_sb, int64_t y_st, int64_t d_sb, int64_t d_st,
+                                int64_t g_sb, hipStream_t stream) {
   if (nb == 0 || T == 0) return SMAT_OK;
   dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
   if (eps >= 0.f)
-    hipLaunchKernelGGL(normalise_bwd_kernel<true>, grid, dim3(256), 0, stream, dout, H, Y, g, dH,
-                       dg, T, n, p, eps, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st, g_sb);
+    hipLaunchKernelGGL((normalise_bwd_kernel<true, Din>), grid, dim3(256), 0, stream, dout, H, Y,
+                       g, dH, dg, T, n, p, eps, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st,
+                       g_sb);
   else
-    hipLaunchKernelGGL(normalise_bwd_kernel<false>, grid, dim3(256), 0, stream, dout, H, Y, g, dH,
-                       dg, T, n, p, 0.f, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st, g_sb);
+    hipLaunchKernelGGL((normalise_bwd_kernel<false, Din>), grid, dim3(256), 0, stream, dout, H, Y,
+                       g, dH, dg, T, n, p, 0.f, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st,
+                       g_sb);
   return launch_status("smat_normalise_backward");
 }
 
@@ -295,14 +308,14 @@ extern "C" int smat_normalise_backward(const float* dout, const float* H, const 
   SMAT_REQUIRE(dout && H && dH, SMAT_EINVAL, "smat_normalise_backward: null pointer");
   SMAT_REQUIRE(nb >= 0 && T >= 0 && p >= 2 && h_st >= p && d_st >= p && o_st >= p - 1,
                SMAT_EINVAL, "smat_normalise_backward: bad sizes");
-  return normalise_bwd_dispatch(dout, H, nullptr, g, dH, dg, nb, T, 0, p, -1.f, o_sb, o_st, h_sb,
-                                h_st, 0, 0, d_sb, d_st, g_sb, (hipStream_t)stream);
+  return launch_normalise_bwd<float>(dout, H, nullptr, g, dH, dg, nb, T, 0, p, -1.f, o_sb, o_st,
+                                     h_sb, h_st, 0, 0, d_sb, d_st, g_sb, (hipStream_t)stream);
 }
 
-extern "C" int smat_combine_normalise(const float* H, const float* Y, float* out, int nb, int T,
-                                      int n, int p, float eps, int64_t h_sb, int64_t h_st,
-                                      int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
-                                      void* stream) {
+extern "C" int smat_combine_normalise(int out_dtype, const float* H, const float* Y, void* out,
+                                      int nb, int T, int n, int p, float eps, int64_t h_sb,
+                                      int64_t h_st, int64_t y_sb, int64_t y_st, int64_t o_sb,
+                                      int64_t o_st, void* stream) {
   using namespace smat;
   clear_error();
   SMAT_REQUIRE(H && out, SMAT_EINVAL, "smat_combine_normalise: null pointer");
@@ -310,21 +323,47 @@ extern "C" int smat_combine_normalise(const float* H, const float* Y, float* out
                "smat_combine_normalise: bad sizes (T=%d n=%d p=%d) or eps < 0", T, n, p);
   SMAT_REQUIRE(h_st >= p && o_st >= p - 1 && (!Y || y_st >= p), SMAT_EINVAL,
                "smat_combine_normalise: row stride too short");
-  return normalise_dispatch(H, Y, nullptr, out, nb, T, n, p, h_sb, h_st, y_sb, y_st, o_sb, o_st, 0,
-                            (hipStream_t)stream, eps);
+  hipStream_t st = (hipStream_t)stream;
+  switch (out_dtype) {
+    case SMAT_F32:
+      return launch_normalise<float>(H, Y, nullptr, (float*)out, nb, T, n, p, h_sb, h_st, y_sb,
+                                     y_st, o_sb, o_st, 0, st, eps);
+    case SMAT_BF16:
+      return launch_normalise<bf16>(H, Y, nullptr, (bf16*)out, nb, T, n, p, h_sb, h_st, y_sb, y_st,
+                                    o_sb, o_st, 0, st, eps);
+    case SMAT_F16:
+      return launch_normalise<f16>(H, Y, nullptr, (f16*)out, nb, T, n, p, h_sb, h_st, y_sb, y_st,
+                                   o_sb, o_st, 0, st, eps);
+  }
+  set_error("smat_combine_normalise: unknown dtype %d", out_dtype);
+  return SMAT_EINVAL;
 }
 
-extern "C" int smat_combine_normalise_backward(const float* dout, const float* H, const float* Y,
-                                               float* dH, int nb, int T, int n, int p, float eps,
-                                               int64_t o_sb, int64_t o_st, int64_t h_sb,
-                                               int64_t h_st, int64_t y_sb, int64_t y_st,
-                                               int64_t d_sb, int64_t d_st, void* stream) {
+extern "C" int smat_combine_normalise_backward(int dout_dtype, const void* dout, const float* H,
+                                               const float* Y, float* dH, int nb, int T, int n,
+                                               int p, float eps, int64_t o_sb, int64_t o_st,
+                                               int64_t h_sb, int64_t h_st, int64_t y_sb,
+                                               int64_t y_st, int64_t d_sb, int64_t d_st,
+                                               void* stream) {
   using namespace smat;
   clear_error();
   SMAT_REQUIRE(dout && H && dH, SMAT_EINVAL, "smat_combine_normalise_backward: null pointer");
   SMAT_REQUIRE(nb >= 0 && T >= 0 && n >= 0 && n <= T && p >= 2 && eps >= 0.f && h_st >= p &&
                    d_st >= p && o_st >= p - 1 && (!Y || y_st >= p),
                SMAT_EINVAL, "smat_combine_normalise_backward: bad sizes");
-  return normalise_bwd_dispatch(dout, H, Y, nullptr, dH, nullptr, nb, T, n, p, eps, o_sb, o_st,
-                                h_sb, h_st, y_sb, y_st, d_sb, d_st, 0, (hipStream_t)stream);
+  hipStream_t st = (hipStream_t)stream;
+  switch (dout_dtype) {
+    case SMAT_F32:
+      return launch_normalise_bwd<float>((const float*)dout, H, Y, nullptr, dH, nullptr, nb, T, n,
+                                         p, eps, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st, 0,
+                                         st);
+    case SMAT_BF16:
+      return launch_normalise_bwd<bf16>((const bf16*)dout, H, Y, nullptr, dH, nullptr, nb, T, n, p,
+                                        eps, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st, 0, st);
+    case SMAT_F16:
+      return launch_normalise_bwd<f16>((const f16*)dout, H, Y, nullptr, dH, nullptr, nb, T, n, p,
+                                       eps, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st, 0, st);
+  }
+  set_error("smat_combine_normalise_backward: unknown dtype %d", dout_dtype);
+  return SMAT_EINVAL;
 }

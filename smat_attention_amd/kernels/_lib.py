@@ -60,9 +60,9 @@ SIGNATURES = {
     "smat_segment_scan_reverse": (_i, [_p, _p, _i, _i, _i, _i64, _p]),
     "smat_normalise_backward": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i64, _i64, _i64, _i64,
                                      _i64, _i64, _i64, _p]),
-    "smat_combine_normalise": (_i, [_p, _p, _p, _i, _i, _i, _i, _f, _i64, _i64, _i64, _i64,
+    "smat_combine_normalise": (_i, [_i, _p, _p, _p, _i, _i, _i, _i, _f, _i64, _i64, _i64, _i64,
                                     _i64, _i64, _p]),
-    "smat_combine_normalise_backward": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _f, _i64, _i64,
+    "smat_combine_normalise_backward": (_i, [_i, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i64, _i64,
                                              _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "smat_bgemm": (_i, [_i, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64,
                         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _p]),

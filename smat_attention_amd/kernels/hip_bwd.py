@@ -805,14 +805,15 @@ class CombineNormaliseFunction(torch.autograd.Function):
     backward, whose dN is H's gradient and, from row n on, Y's."""
 
     @staticmethod
-    def forward(ctx, H, Y, n, eps):
+    def forward(ctx, H, Y, n, eps, out_dtype=torch.float32):
         Hc = _hip._fp32_rows(H)
         Yc = _hip._fp32_rows(Y) if Y is not None else None
         nb, T, P = Hc.shape
-        out = torch.empty(nb, T, P - 1, device=Hc.device, dtype=torch.float32)
-        call("smat_combine_normalise", Hc.data_ptr(), ptr(Yc), out.data_ptr(), nb, T, n, P,
-             float(eps), Hc.stride(0), Hc.stride(1), Yc.stride(0) if Yc is not None else 0,
-             Yc.stride(1) if Yc is not None else 0, out.stride(0), out.stride(1), stream_of(Hc))
+        out = torch.empty(nb, T, P - 1, device=Hc.device, dtype=out_dtype)
+        call("smat_combine_normalise", DTYPE_CODE[out_dtype], Hc.data_ptr(), ptr(Yc),
+             out.data_ptr(), nb, T, n, P, float(eps), Hc.stride(0), Hc.stride(1),
+             Yc.stride(0) if Yc is not None else 0, Yc.stride(1) if Yc is not None else 0,
+             out.stride(0), out.stride(1), stream_of(Hc))
         ctx.save_for_backward(Hc, Yc)
         ctx.n, ctx.eps = n, float(eps)
         ctx.dtypes = (H.dtype, None if Y is None else Y.dtype)
@@ -823,13 +824,14 @@ class CombineNormaliseFunction(torch.autograd.Function):
         Hc, Yc = ctx.saved_tensors
         n = ctx.n
         nb, T, P = Hc.shape
-        d = _hip._fp32_rows(dout)
+        d = dout if dout.dtype in DTYPE_CODE else dout.float()
+        d = d if d.stride(-1) == 1 else d.contiguous()
         dN = torch.empty(nb, T, P, device=Hc.device, dtype=torch.float32)
-        call("smat_combine_normalise_backward", d.data_ptr(), Hc.data_ptr(), ptr(Yc),
-             dN.data_ptr(), nb, T, n, P, ctx.eps, d.stride(0), d.stride(1), Hc.stride(0),
-             Hc.stride(1), Yc.stride(0) if Yc is not None else 0,
+        call("smat_combine_normalise_backward", DTYPE_CODE[d.dtype], d.data_ptr(), Hc.data_ptr(),
+             ptr(Yc), dN.data_ptr(), nb, T, n, P, ctx.eps, d.stride(0), d.stride(1),
+             Hc.stride(0), Hc.stride(1), Yc.stride(0) if Yc is not None else 0,
              Yc.stride(1) if Yc is not None else 0, dN.stride(0), dN.stride(1), stream_of(d))
         dH = dN.to(ctx.dtypes[0]) if ctx.needs_input_grad[0] else None
         dY = dN[:, n:].to(ctx.dtypes[1]) if (Yc is not None and ctx.needs_input_grad[1]) else None
-        return dH, dY, None, None
+        return dH, dY, None, None, None
 

@@ -390,15 +390,23 @@ def test_fused_cell_backward(d):
         assert e < (2e-3 if name in ("dQ", "dK", "dV") else 1e-4), name
 
 
-@pytest.mark.parametrize("T,n,p,with_y", [(300, 128, 65, True), (256, 0, 65, True),
-                                           (256, 256, 129, False), (1000, 512, 17, True)])
-def test_combine_normalise(T, n, p, with_y):
+@pytest.mark.parametrize("T,n,p,with_y,odt", [(300, 128, 65, True, torch.float32),
+                                               (256, 0, 65, True, torch.float32),
+                                               (256, 256, 129, False, torch.float32),
+                                               (1000, 512, 17, True, torch.float32),
+                                               (1000, 512, 65, True, torch.bfloat16),
+                                               (300, 100, 65, True, torch.float16)])
+def test_combine_normalise(T, n, p, with_y, odt):
     """combine_normalise (smat_combine_normalise and its backward) against the
     reference layer's torch ops in fp64 -- ``cat([H[:, :n], H[:, n:] + Y])``
     then ``N[..., :-1] / N[..., -1:].clamp_min(1e-6)`` (model.py:296-300) --
     output and the gradients of H and Y within 1e-6 of the largest entry.  A
     tenth of the rows have a normaliser below the floor (down to 0), where the
-    floor divides and passes no gradient to the normaliser."""
+    floor divides and passes no gradient to the normaliser.  With a 16-bit
+    output (the layer's cast folded in) every output is the fp64 value
+    rounded once (within half an ulp, plus 1e-6), and the gradients are those
+    of the upstream gradient as the cast's backward delivers it (rounded to the
+    output dtype)."""
     gen = torch.Generator().manual_seed(T + n + p)
     nb = 3
     H = torch.randn(nb, T, p, generator=gen)
@@ -406,7 +414,8 @@ def test_combine_normalise(T, n, p, with_y):
     Y = torch.randn(nb, T - n, p, generator=gen) * 0.3 if with_y else None
     if Y is not None:
         Y[..., -1] = Y[..., -1].abs()
-    small = torch.rand(nb, T, generator=gen) < 0.1
+    # rows under the floor (their quotients reach 1e6: not for a float16 output)
+    small = torch.rand(nb, T, generator=gen) < (0.1 if odt != torch.float16 else 0.0)
     H[..., -1] = torch.where(small, torch.rand(nb, T, generator=gen) * 1e-6, H[..., -1])
     if Y is not None:
         Y[..., -1] = torch.where(small[:, n:], torch.zeros(()), Y[..., -1])
@@ -416,14 +425,20 @@ def test_combine_normalise(T, n, p, with_y):
         N = h if y is None else torch.cat([h[:, :n], h[:, n:] + y], dim=1)
         return N[..., :-1] / N[..., -1:].clamp_min(1e-6)
 
+    dOe = dO.to(odt).double()                        # what reaches the division's backward
     xs0 = [t.double().requires_grad_(True) for t in (H, Y) if t is not None]
     o0 = ref(*(xs0 if with_y else xs0 + [None]))
-    (o0 * dO.double()).sum().backward()
+    (o0 * dOe).sum().backward()
     xs1 = [t.to(DEV).requires_grad_(True) for t in (H, Y) if t is not None]
-    o1 = A.combine_normalise(xs1[0], xs1[1] if with_y else None, n)
-    (o1 * dO.to(DEV)).sum().backward()
-    assert o1.dtype == torch.float32 and o1.shape == (nb, T, p - 1)
-    assert _grel(o1.detach().cpu(), o0.detach()) < 1e-6
+    o1 = A.combine_normalise(xs1[0], xs1[1] if with_y else None, n, out_dtype=odt)
+    (o1.float() * dO.to(DEV)).sum().backward()
+    assert o1.dtype == odt and o1.shape == (nb, T, p - 1)
+    if odt == torch.float32:
+        assert _grel(o1.detach().cpu(), o0.detach()) < 1e-6
+    else:
+        half_ulp = 2.0 ** -8 if odt == torch.bfloat16 else 2.0 ** -11
+        err = (o1.detach().cpu().double() - o0.detach()).abs()
+        assert (err <= o0.detach().abs() * half_ulp * (1 + 1e-5) + 1e-6).all()
     for name, a, b in zip(("dH", "dY"), xs1, xs0):
         e = _grel(a.grad.cpu(), b.grad)
         _say(f"  {name}: {e:.2e}")
