@@ -518,6 +518,32 @@ int smat_query_lists(int dtype, const void* phi, const float* U, float* Y,
                      int r, int p, int64_t q_st, int64_t y_st, void* stream);
 
 /*
+ * smat_forward from Q, K, V with the feature map inside the kernels:
+ * Phi = map(Q W^T), Psi = h * map(K W^T), Vb = [V, 1] (map: kind 0 elu + 1,
+ * kind 1 relu + 1e-3, torch's rounding steps; h (nb, T) the optional key gate,
+ * h_sb its batch stride) are formed in LDS by the pool, the query, the
+ * prepass and the scan from the Q, K, V tiles they stream, so Phi, Psi and Vb
+ * never reach memory (when a row type has more than 48 recent rows, the
+ * recent rows' Phi alone is featurised into the workspace for the general
+ * query).  W (128 x 128, features x d_qk) in the input dtype.  The other
+ * arguments are smat_forward's (no H_out); the workspace is
+ * smat_forward_fused_workspace_bytes(nb, T, n, N0, B, n_P, C) bytes.  Serves
+ * 16-bit inputs with d_qk = d_v = r = 128, T, n and C multiples of 64
+ * (C <= 128) and 16-byte aligned rows; otherwise returns SMAT_EUNSUPPORTED.
+ * Replaces featurise (src/smat/attention.py:82-106) followed by smat_attention
+ * (:391-455): the fused featurisation that src/smat/kernels/triton_fwd.py
+ * leaves to a separate torch pass.
+ */
+int64_t smat_forward_fused_workspace_bytes(int nb, int T, int n, int N0, int B, int n_P, int C);
+int smat_forward_fused(int dtype, const void* q, const void* k, const void* v, const void* W,
+                       const void* h, int kind, const void* idx, int idx_is_64,
+                       const int64_t* indptr, int deg, const int* plane_code, int field_q,
+                       float* out, const float* g, int nb, int T, int n, int n_P, int N0, int B,
+                       int C, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
+                       int64_t v_sb, int64_t v_st, int64_t h_sb, int64_t o_sb, int64_t o_st,
+                       int64_t g_sb, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Class lists (CSR) of every sequence by a counting sort: keys (nb, L) int64 in
  * [0, ncls) -> order (nb*L) int32, the items of sequence 0's class 0, class 1,
  * ..., then sequence 1's, each list in item order (the stable sort of

@@ -42,7 +42,7 @@ __all__ = [
     "segmented_causal_scan", "decayed_segmented_scan", "combine_normalise", "pool_profiles",
     "apply_incidence",
     "query_by_type", "zeta_transform", "walsh_incidence", "direct_long_range",
-    "smat_attention", "dense_masked_kernel_attention", "SmatDecoder",
+    "smat_attention", "smat_attention_fused", "dense_masked_kernel_attention", "SmatDecoder",
     "have_triton", "have_hip",
 ]
 
@@ -630,6 +630,62 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
         parts.update(U=U, Y_lr=Y_lr, H=Hfull)
         return out, parts
     return out
+
+
+def _fused_ok(Q, K, V, phi, spec, C, h) -> bool:
+    """Whether :func:`smat_attention_fused` runs the fused kernels for these inputs."""
+    if not (isinstance(phi, FeatureMap) and Q.is_cuda
+            and Q.dtype in (torch.bfloat16, torch.float16)):
+        return False
+    if spec.kind == "endpoint" or tuple(phi.W.shape) != (128, 128) or phi.W.dtype != Q.dtype:
+        return False
+    nb, T, dqk = Q.shape
+    if dqk != 128 or K.shape != Q.shape or V.shape != Q.shape or K.dtype != Q.dtype \
+            or V.dtype != Q.dtype or (h is not None and h.dtype != Q.dtype):
+        return False
+    if C not in (64, 128) or T % 64 or spec.n % C:
+        return False
+    for t in (Q, K, V):
+        if t.stride(-1) != 1 or t.stride(1) % 8 or t.stride(0) % 8 or t.data_ptr() % 16:
+            return False
+    return phi.W.is_contiguous() and phi.W.data_ptr() % 16 == 0
+
+
+def smat_attention_fused(Q, K, V, phi, spec: MaskSpec, *, g=None, h=None, chunk: int = 128,
+                         workspace: Optional[torch.Tensor] = None):
+    """``smat_attention(*featurise(Q, K, V, phi, h=h), spec, g=g)`` with the
+    feature map computed inside the schedule's kernels (the reference's
+    featurise, attention.py:82-106, then Algorithm 1, :391-455).
+
+    For 16-bit inputs at d_qk = d_v = r = 128 (the streaming shape: T, n and the
+    chunk multiples of 64) the pool, the
+    query, the prepass and the scan form ``Phi = map(Q W^T)``, ``Psi = h
+    map(K W^T)`` and ``Vb = [V, 1]`` in LDS from the Q, K, V tiles they stream
+    (``smat_forward_fused``), bitwise the features :func:`featurise` writes,
+    so the output equals the unfused path's while Phi, Psi and Vb never reach
+    memory (where a row type has more than 48 recent rows, the recent rows'
+    Phi alone is featurised for the general query kernel).  Other inputs, and
+    inputs that require grad, run :func:`featurise` then :func:`smat_attention`.
+    Returns fp32 (nb, T, d_v).
+    """
+    who = "smat_attention_fused"
+    _hip._on_gpu(who, Q, K, V, g, h)
+    T = Q.shape[1]
+    if T != spec.T:
+        raise ValueError(f"{who}: T={T} but the mask was built for T={spec.T}")
+    C = min(chunk, T)
+    if _wants_grad(Q, K, V, g, h, phi.W if isinstance(phi, FeatureMap) else None) \
+            or not _fused_ok(Q, K, V, phi, spec, C, h):
+        Phi, Psi, Vb = featurise(Q, K, V, phi, h=h)
+        return smat_attention(Phi, Psi, Vb, spec, chunk=chunk, g=g, workspace=workspace)
+    _staged(spec, Q.device)
+    idx, indptr, deg = _incidence_args(spec)
+    pc = spec.plane_code_t if _plane_ok(spec, 128 * 129) else None
+    if getattr(spec, "incidence_identity", False) and spec.n_P == 0:
+        idx, pc = None, None                         # the query reads F as U
+    return _hip.forward_fused(phi.W, phi.kind, Q, K, V, h, idx, deg, n=spec.n, n_P=spec.n_P,
+                              N0=spec.N0, B=spec.B, chunk=C, indptr=indptr, plane_code=pc,
+                              field_q=spec.q, g=g, workspace=workspace)
 
 
 def _subtractive(Phi, Psi, Vb, spec, C, g, tm, return_parts, incidence_backend):

@@ -1,0 +1,115 @@
+// The feature map of src/smat/attention.py:82-106 as a device-side stage, shared
+// by the stand-alone featurise kernel and the consumers that compute their
+// features in place (scan, Gram sums, query):
+//
+//   Phi = map(Q W^T),  Psi = map(K W^T) * h,  Vb = [V, 1]
+//   map = elu(.) + 1   (kind 0)   or   relu(.) + 1e-3   (kind 1)
+//
+// in the input dtype with torch's rounding steps: the product rounded to the
+// dtype, elu rounded, + 1 rounded, the gate product rounded (fp32 math in
+// between, as torch does for 16-bit tensors).
+#pragma once
+
+#include "smat_common.hpp"
+
+namespace smat {
+
+template <typename In>
+__device__ __forceinline__ float feature_map(float acc, int kind) {
+  const float v = to_f32(from_f32<In>(acc));                 // torch's matmul output
+  if (kind == 0) {
+    const float e = to_f32(from_f32<In>(v > 0.f ? v : expm1f(v)));
+    return to_f32(from_f32<In>(e + 1.0f));
+  }
+  return to_f32(from_f32<In>(fmaxf(v, 0.f) + 1e-3f));
+}
+
+// The feature map handed to a consumer kernel: W (128 x 128, features x d_qk,
+// row-major, 16-byte aligned rows), the optional key gate h (nb, T) and kind.
+struct FeatArgs {
+  const void* W;
+  const void* h;
+  int64_t h_sb;
+  int kind;
+};
+
+// Features [16 wf, 16 wf + 16) of W as MFMA A fragments over d_qk = 128: k-block
+// kb holds k-slots 32 kb + 8 (lane / 16) + j, j < 8.  A per-wave constant.
+template <typename In>
+__device__ __forceinline__ void feat_w_load(typename Traits<In>::frag (&wa)[4], const In* W, int wf,
+                                            int lane) {
+  const int r16 = lane & 15, g = lane >> 4;
+  const In* row = W + (int64_t)(16 * wf + r16) * 128;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+    wa[kb] = *reinterpret_cast<const typename Traits<In>::frag*>(row + 32 * kb + 8 * g);
+}
+
+// In place over NRT 16-row tiles starting at row tile rt0 of an LDS tile of
+// 256-byte rows whose 16-byte chunk k of row t sits at slot k ^ swz(t): read
+// the rows' 128 input values (X = Q or K), form this wave's features
+// C = W[16 wf .. +16] X^T on MFMA (lane (t, g) ends with features 16 wf + 4 g
+// .. +3 of row t), wait for every wave's reads (barrier), then overwrite the
+// row's feature chunk with map(C) (times gate[rt] for the lane's row of tile
+// rt0 + rt when use_gate).
+// Every wave of the workgroup calls it (the barrier); inactive waves only
+// meet the barrier.  The caller places a barrier before the feature rows are
+// read.  The MFMA sequence is the stand-alone kernel's (k-blocks 0..3 in
+// order), so the features are bitwise the same.
+template <typename In, int NRT, typename Swz>
+__device__ __forceinline__ void feat_rows(uint4* tile, int rt0, bool active,
+                                          const typename Traits<In>::frag (&wa)[4], int wf,
+                                          int kind, bool use_gate, const float (&gate)[NRT],
+                                          int lane, Swz swz) {
+  typedef typename Traits<In>::frag Frag;
+  typedef typename Traits<In>::half_frag Half;
+  const int r16 = lane & 15, g = lane >> 4;
+  f32x4 acc[NRT];
+  if (active) {
+    Frag bx[NRT][4];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      const int t = 16 * (rt0 + rt) + r16;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        bx[rt][kb] = *reinterpret_cast<const Frag*>(tile + t * 16 + ((4 * kb + g) ^ swz(t)));
+    }
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      acc[rt] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) acc[rt] = mma(acc[rt], wa[kb], bx[rt][kb]);
+    }
+  }
+  lds_barrier();                                     // every wave has read its rows
+  if (active) {
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      const int t = 16 * (rt0 + rt) + r16;
+      Half hv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float y = feature_map<In>(acc[rt][i], kind);
+        if (use_gate) y = to_f32(from_f32<In>(y * gate[rt]));
+        hv[i] = from_f32<In>(y);
+      }
+      char* p = reinterpret_cast<char*>(tile + t * 16 + ((2 * wf + (g >> 1)) ^ swz(t)));
+      *reinterpret_cast<Half*>(p + 8 * (g & 1)) = hv;
+    }
+  }
+}
+
+// Columns 128..135 of [V, 1] for 64 rows (one 16-byte chunk a row): the ones
+// column, then zeros.
+template <typename In>
+__device__ __forceinline__ void feat_ones_tile(uint4* chunks, int tid, int nthreads) {
+  typedef typename Traits<In>::frag Frag;
+  for (int t = tid; t < 64; t += nthreads) {
+    Frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = from_f32<In>(j == 0 ? 1.f : 0.f);
+    *reinterpret_cast<Frag*>(chunks + t) = f;
+  }
+}
+
+}  // namespace smat

@@ -17,6 +17,7 @@
 // sequence.
 #include <math.h>
 
+#include "feat_map.hpp"
 #include "smat_host.hpp"
 
 namespace smat {
@@ -27,16 +28,6 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kMaxDqk = 128;       // d_qk
 constexpr int kMaxRank = 128;      // feature rank
 }  // namespace ft
-
-template <typename In>
-__device__ __forceinline__ float feature_map(float acc, int kind) {
-  const float v = to_f32(from_f32<In>(acc));                 // torch's matmul output
-  if (kind == 0) {
-    const float e = to_f32(from_f32<In>(v > 0.f ? v : expm1f(v)));
-    return to_f32(from_f32<In>(e + 1.0f));
-  }
-  return to_f32(from_f32<In>(fmaxf(v, 0.f) + 1e-3f));
-}
 
 template <typename In>
 __global__ __launch_bounds__(ft::kThreads) void featurise_kernel(

@@ -13,6 +13,7 @@
 
 #include <atomic>
 
+#include "feat_map.hpp"
 #include "smat_host.hpp"
 
 namespace smat {
@@ -65,6 +66,20 @@ int normalise_dispatch(const float* H, const float* Y, const float* g, float* ou
                        int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream,
                        float eps);
 
+int gram_stream_launch_feat(int dtype, const void* k, const void* v, float* G, float* G_last,
+                            const GramItems& it, int nitems, int nb, int64_t k_sb, int64_t k_st,
+                            int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                            int64_t gl_sb, const FeatArgs& fa, hipStream_t stream,
+                            const char* who);
+int query_stream_launch_feat(int dtype, const void* q, const float* U, float* Y, int nb, int T_R,
+                             int B, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
+                             const FeatArgs& fa, hipStream_t stream);
+int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v, const float* Y,
+                         const float* gate, float* out, int nb, int T, int n, int C,
+                         int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                         int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
+                         int64_t g_sb, const FeatArgs& fa, void* ws, int64_t ws_bytes,
+                         hipStream_t stream);
 int64_t causal_scan_workspace_bytes(int nb, int T, int C, int r, int p);
 int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void* vb,
                          const float* Y, const float* gate, float* out, int nb, int T, int n,
@@ -257,4 +272,134 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
   }
   return normalise_dispatch(H, T_R > 0 ? Y : nullptr, g, out, nb, T, n, p, h_sb, p,
                             (int64_t)T_R * yst, yst, o_sb, o_st, g_sb, st, -1.f);
+}
+
+extern "C" int smat_featurise(int dtype, const void* q, const void* k, const void* v,
+                              const void* W, const void* h, void* phi, void* psi, void* vb,
+                              int nb, int T, int d_qk, int r, int d_v, int kind, int64_t q_sb,
+                              int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                              int64_t v_st, int64_t h_sb, int64_t o_sb, int64_t o_st,
+                              int64_t vb_sb, int64_t vb_st, void* stream);
+
+namespace smat {
+// More recent rows a row type than the streaming query's 48: the recent rows'
+// Phi is featurised into the workspace and read by the general query kernel.
+static bool fused_query_staged(int T, int n, int B) {
+  return T > n && (T - n + B - 1) / B > 48;
+}
+static int64_t fused_workspace_bytes(int nb, int T, int n, int N0, int B, int n_P, int C) {
+  const FwdLayout L = fwd_layout(nb, T, n, N0, B, n_P, C, 128, 129, false);
+  return L.total + (fused_query_staged(T, n, B) ? al256((int64_t)nb * (T - n) * 128 * 2) : 0);
+}
+}  // namespace smat
+
+extern "C" int64_t smat_forward_fused_workspace_bytes(int nb, int T, int n, int N0, int B,
+                                                      int n_P, int C) {
+  if (nb <= 0 || T <= 0 || C <= 0 || N0 <= 0 || B <= 0 || n < 0 || n > T) return 0;
+  return smat::fused_workspace_bytes(nb, T, n, N0, B, n_P, C);
+}
+
+// The forward of smat_forward computed from Q, K, V: the feature map
+// Phi = map(Q W^T), Psi = h map(K W^T), Vb = [V, 1] (src/smat/attention.py:82-106)
+// runs inside the pool, the query, the prepass and the scan, on tiles already
+// in LDS, so Phi, Psi and Vb are never written to memory -- except, when a
+// row type has more than 48 recent rows (beyond the streaming query), the
+// recent rows' Phi, which is featurised into the workspace for the general
+// query kernel.  Serves the head-dim-128 streaming shape: 16-bit inputs,
+// d_qk = d_v = r = 128 (p = 129), T, n and the chunk multiples of 64
+// (chunk <= 128), 16-byte aligned rows; anything else returns
+// SMAT_EUNSUPPORTED (the caller featurises, then calls smat_forward).
+extern "C" int smat_forward_fused(int dtype, const void* q, const void* k, const void* v,
+                                  const void* W, const void* h, int kind, const void* idx,
+                                  int idx_is_64, const int64_t* indptr, int deg,
+                                  const int* plane_code, int field_q, float* out, const float* g,
+                                  int nb, int T, int n, int n_P, int N0, int B, int C,
+                                  int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
+                                  int64_t v_sb, int64_t v_st, int64_t h_sb, int64_t o_sb,
+                                  int64_t o_st, int64_t g_sb, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  using namespace smat;
+  clear_error();
+  constexpr int r = 128, p = 129;
+  SMAT_REQUIRE(q && k && v && W && out && workspace, SMAT_EINVAL,
+               "smat_forward_fused: null pointer");
+  SMAT_REQUIRE(idx || (deg == 1 && B == N0 && n_P == 0), SMAT_EINVAL,
+               "smat_forward_fused: idx may be NULL only for the identity incidence");
+  SMAT_REQUIRE(kind == 0 || kind == 1, SMAT_EINVAL, "smat_forward_fused: kind must be 0 or 1");
+  SMAT_REQUIRE(nb >= 1 && T >= 1 && n >= 0 && n <= T && n_P >= 0 && n_P <= n && N0 >= 1 &&
+                   B >= 1,
+               SMAT_EINVAL, "smat_forward_fused: bad sizes (nb=%d T=%d n=%d n_P=%d N0=%d B=%d)",
+               nb, T, n, n_P, N0, B);
+  const int T_R = T - n;
+  constexpr int64_t kMaxSt = 1 << 20;
+  SMAT_REQUIRE(dtype == SMAT_BF16 || dtype == SMAT_F16, SMAT_EUNSUPPORTED,
+               "smat_forward_fused: 16-bit inputs only");
+  SMAT_REQUIRE(C >= 64 && C <= 128 && C % 64 == 0 && T % 64 == 0 && n % C == 0,
+               SMAT_EUNSUPPORTED,
+               "smat_forward_fused: T, n and the chunk (64 or 128) must be multiples of 64");
+  SMAT_REQUIRE(q_st >= 128 && k_st >= 128 && v_st >= 128 && o_st >= 128 && q_st < kMaxSt &&
+                   k_st < kMaxSt && v_st < kMaxSt && o_st < kMaxSt,
+               SMAT_EUNSUPPORTED, "smat_forward_fused: row strides must be in [128, 2^20)");
+  SMAT_REQUIRE(rows_vec_ok(q, q_sb, q_st, 2) && rows_vec_ok(k, k_sb, k_st, 2) &&
+                   rows_vec_ok(v, v_sb, v_st, 2) && rows_vec_ok(out, o_sb, o_st, 4) &&
+                   aligned16(W),
+               SMAT_EUNSUPPORTED, "smat_forward_fused: rows and W must be 16-byte aligned");
+  SMAT_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, SMAT_EINVAL,
+               "smat_forward_fused: workspace must be 256-byte aligned");
+  const FwdLayout L = fwd_layout(nb, T, n, N0, B, n_P, C, r, p, false);
+  const int64_t need = fused_workspace_bytes(nb, T, n, N0, B, n_P, C);
+  SMAT_REQUIRE(workspace_bytes >= need, SMAT_EINVAL,
+               "smat_forward_fused: workspace of %lld bytes needed, %lld given",
+               (long long)need, (long long)workspace_bytes);
+
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  float* F = (float*)(ws + L.F);
+  float* Fg = n_P > 0 ? (float*)(ws + L.Fg) : nullptr;
+  float* U = (float*)(ws + L.U);
+  float* Y = (float*)(ws + L.Y);
+  const int64_t rp = (int64_t)r * p;
+  const int64_t yst = y_stride(p);
+  const FeatArgs fa{W, h, h_sb, kind};
+  int rc;
+
+  if (T_R > 0) {
+    const bool profiled = n > n_P;
+    GramItems it{};
+    it.mode = 1;
+    it.n_P = n_P;
+    it.n = n;
+    it.N0 = N0;
+    it.nsplit = 1;
+    it.per = 1 << 30;
+    rc = gram_stream_launch_feat(dtype, k, v, F, Fg, it, N0 + (Fg ? 1 : 0), nb, k_sb, k_st, v_sb,
+                                 v_st, (int64_t)N0 * rp, rp, rp, fa, st, "smat_forward_fused");
+    if (rc) return rc;
+    const float* Uq = U;
+    if (!idx)
+      Uq = F;
+    else if (plane_code && profiled)
+      rc = incidence_plane_dispatch(F, Fg, plane_code, field_q, U, nb, N0, B, rp, st);
+    else
+      rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
+                              profiled ? deg : 0, U, nb, N0, B, rp, st);
+    if (rc) return rc;
+    const char* q_rec = (const char*)q + (int64_t)n * q_st * 2;
+    if (fused_query_staged(T, n, B)) {
+      void* phi_rec = ws + L.total;                  // (nb, T_R, 128), rows of 128
+      rc = smat_featurise(dtype, q_rec, nullptr, nullptr, W, nullptr, phi_rec, nullptr, nullptr,
+                          nb, T_R, 128, 128, 0, kind, q_sb, q_st, 0, 0, 0, 0, 0,
+                          (int64_t)T_R * 128, 128, 0, 0, stream);
+      if (rc) return rc;
+      rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, (int64_t)T_R * 128, 128,
+                          (int64_t)T_R * yst, yst, st);
+    } else {
+      rc = query_stream_launch_feat(dtype, q_rec, Uq, Y, nb, T_R, B, q_sb, q_st,
+                                    (int64_t)T_R * yst, yst, fa, st);
+    }
+    if (rc) return rc;
+  }
+  return causal_scan_run_feat(dtype, q, k, v, T_R > 0 ? Y : nullptr, g, out, nb, T, n, C, q_sb,
+                              q_st, k_sb, k_st, v_sb, v_st, (int64_t)T_R * yst, yst, o_sb, o_st,
+                              g_sb, fa, ws + L.scan, L.part - L.scan, st);
 }

@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "feat_map.hpp"
 #include "smat_host.hpp"
 
 namespace smat {
@@ -207,10 +208,14 @@ __device__ __forceinline__ void query_issue(float* ubuf, uint4* pbuf, const floa
   }
 }
 
-template <typename In>
+// FEAT: phi holds Q rows; each item's <= 48 Phi rows are formed in place from
+// the DMA'd Q rows (feat_rows: waves 0..7 one feature tile each, W in
+// registers; wave 8 meets the barriers).
+template <typename In, bool FEAT>
 __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
     const In* __restrict__ phi, const float* __restrict__ U, float* __restrict__ Y, int T_R,
-    int B, int64_t nitems, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st) {
+    int B, int64_t nitems, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
+    FeatArgs fa) {
   using namespace qs;
   typedef typename Traits<In>::frag Frag;
   __shared__ __attribute__((aligned(16))) float u0[kUFloats];
@@ -221,6 +226,10 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
   const int64_t G = gridDim.x;
   int64_t item = blockIdx.x;
   if (item < nitems) query_issue<In>(u0, p0, U, phi, item, T_R, B, q_sb, q_st, w, lane_id());
+  Frag wa[4];
+  if constexpr (FEAT) {
+    if (w < 8) feat_w_load<In>(wa, (const In*)fa.W, w, lane_id());
+  }
 
   auto step = [&](auto BUFC) {
     constexpr int BUF = decltype(BUFC)::value;
@@ -240,6 +249,12 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     lds_barrier();
+    if constexpr (FEAT) {
+      const float none[kMT] = {};
+      feat_rows<In, kMT>(BUF ? p1 : p0, 0, w < 8, wa, w, fa.kind, false, none, lane,
+                         [](int t) { return t & 15; });
+      lds_barrier();    // the item's Phi rows are complete
+    }
 
     const int64_t b = item / B;
     const int h = (int)(item - b * B);
@@ -370,20 +385,38 @@ static int launch_query_lists(const void* phi, const float* U, float* Y, const i
   return launch_status("smat_query_lists");
 }
 
-static int launch_query_stream(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R, int B, int64_t q_sb, int64_t q_st,
-                               int64_t y_sb, int64_t y_st, hipStream_t stream) {
+template <bool FEAT>
+static int query_stream_go(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R,
+                           int B, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
+                           const FeatArgs& fa, hipStream_t stream) {
   int dev = 0, ncu = 256;
   (void)hipGetDevice(&dev);
   (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
   const int64_t nitems = (int64_t)nb * B;
   const unsigned grid = (unsigned)std::min<int64_t>(nitems, (int64_t)ncu);
   if (dtype == SMAT_BF16)
-    hipLaunchKernelGGL(query_stream_kernel<bf16>, dim3(grid), dim3(qs::kThreads), 0, stream,
-                       (const bf16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st);
+    hipLaunchKernelGGL((query_stream_kernel<bf16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
+                       stream, (const bf16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st, fa);
   else
-    hipLaunchKernelGGL(query_stream_kernel<f16>, dim3(grid), dim3(qs::kThreads), 0, stream,
-                       (const f16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st);
+    hipLaunchKernelGGL((query_stream_kernel<f16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
+                       stream, (const f16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st, fa);
   return launch_status("smat_query");
+}
+
+static int launch_query_stream(int dtype, const void* phi, const float* U, float* Y, int nb,
+                               int T_R, int B, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                               int64_t y_st, hipStream_t stream) {
+  return query_stream_go<false>(dtype, phi, U, Y, nb, T_R, B, q_sb, q_st, y_sb, y_st, FeatArgs{},
+                                stream);
+}
+
+// The streaming query with the feature map in place: q holds Q rows of the
+// recent block (d_qk = 128), U fp32 (nb, B, 128, 129), at most 48 rows a type.
+int query_stream_launch_feat(int dtype, const void* q, const float* U, float* Y, int nb, int T_R,
+                             int B, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
+                             const FeatArgs& fa, hipStream_t stream) {
+  if (nb == 0 || T_R == 0 || B == 0) return SMAT_OK;
+  return query_stream_go<true>(dtype, q, U, Y, nb, T_R, B, q_sb, q_st, y_sb, y_st, fa, stream);
 }
 
 int query_dispatch(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R, int B,

@@ -22,6 +22,7 @@
 // intra-chunk product and the update.
 #include <mutex>
 
+#include "feat_map.hpp"
 #include "smat_host.hpp"
 
 namespace smat {
@@ -449,6 +450,15 @@ bool scan_stream_ok(int dtype, const void* phi, const void* psi, const void* vb,
 int scan_stream_launch(int dtype, const void* phi, const void* psi, const void* vb,
                        const float* Sg, const float* Y, const float* gate, float* out, int nb,
                        int ng, const ScanArgs& a, hipStream_t stream);
+int scan_stream_launch_feat(int dtype, const void* q, const void* k, const void* v,
+                            const float* Sg, const float* Y, const float* gate, float* out,
+                            int nb, int ng, const ScanArgs& a, const FeatArgs& fa,
+                            hipStream_t stream);
+int gram_stream_launch_feat(int dtype, const void* k, const void* v, float* G, float* G_last,
+                            const GramItems& it, int nitems, int nb, int64_t k_sb, int64_t k_st,
+                            int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                            int64_t gl_sb, const FeatArgs& fa, hipStream_t stream,
+                            const char* who);
 
 // Group size: enough workgroups to fill the GPU (one per CU at a time), and
 // no more than needed so the prepass stays small.
@@ -542,6 +552,71 @@ int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb,
   }
   set_error("smat_causal_scan: unknown dtype %d", dtype);
   return SMAT_EINVAL;
+}
+
+// The streaming causal pass with the feature map computed inside the kernels:
+// q, k, v are the Q, K, V rows (r = d_qk = d_v = 128); the prepass Gram sums
+// and the scan form Psi (and Phi) tiles in LDS from the DMA'd K (and Q) rows,
+// and Vb = [V, 1] from V.  Same workspace as causal_scan_dispatch.
+int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v, const float* Y,
+                         const float* gate, float* out, int nb, int T, int n, int C,
+                         int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
+                         int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
+                         int64_t g_sb, const FeatArgs& fa, void* ws, int64_t ws_bytes,
+                         hipStream_t stream) {
+  if (nb == 0 || T == 0) return SMAT_OK;
+  constexpr int r = 128, p = 129;
+  const int64_t rp = (int64_t)r * p;
+  const int nc = (T + C - 1) / C;
+  const int K = scan_group_chunks(nb, nc);
+  const int64_t need = causal_scan_workspace_bytes(nb, T, C, r, p);
+  if (ws_bytes < need) {
+    set_error("smat_forward_fused: causal-pass workspace of %lld bytes needed, %lld given",
+              (long long)need, (long long)ws_bytes);
+    return SMAT_EINVAL;
+  }
+  const int ng_max = (nc + K - 1) / K + 1;
+  float* G = (float*)ws;
+  float* Sg = (float*)((char*)ws + (((int64_t)nb * ng_max * rp * 4 + 255) & ~(int64_t)255));
+  GramItems it{};
+  it.mode = 0;
+  it.T = T;
+  it.C = C;
+  it.K = K;
+  it.nc = nc;
+  it.nc0 = n / C;
+  it.ng0 = (it.nc0 + K - 1) / K;
+  it.nsplit = 1;
+  it.per = K * C;
+  const int ng = it.ng0 + (nc - it.nc0 + K - 1) / K;
+  int rc = gram_stream_launch_feat(dtype, k, v, G, nullptr, it, ng, nb, k_sb, k_st, v_sb, v_st,
+                                   (int64_t)ng * rp, rp, 0, fa, stream, "smat_forward_fused");
+  if (rc) return rc;
+  rc = segment_scan_dispatch(G, Sg, nb, ng, it.ng0, rp, stream);
+  if (rc) return rc;
+  ScanArgs a{};
+  a.T = T;
+  a.n = n;
+  a.C = C;
+  a.K = K;
+  a.nc = nc;
+  a.nc0 = n / C;
+  a.ng0 = it.ng0;
+  a.r = r;
+  a.p = p;
+  a.q_sb = q_sb;
+  a.q_st = q_st;
+  a.k_sb = k_sb;
+  a.k_st = k_st;
+  a.v_sb = v_sb;
+  a.v_st = v_st;
+  a.y_sb = y_sb;
+  a.y_st = y_st;
+  a.o_sb = o_sb;
+  a.o_st = o_st;
+  a.g_sb = g_sb;
+  a.write_H = 0;
+  return scan_stream_launch_feat(dtype, q, k, v, Sg, Y, gate, out, nb, ng, a, fa, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -48,6 +48,7 @@
 
 #include <type_traits>
 
+#include "feat_map.hpp"
 #include "smat_host.hpp"
 
 namespace smat {
@@ -185,7 +186,9 @@ __device__ __forceinline__ void dma_offsets(DmaOffsets& d, const ScanArgs& a, in
   }
 }
 
-template <typename In>
+// FEAT: the rows are Q, K and V (the feature map runs in LDS afterwards), and
+// the ninth Vb tile is the constant [1, 0, ...] written once: six loads a wave.
+template <typename In, bool FEAT>
 __device__ __forceinline__ void issue_step(uint4* dphi, uint4* dpsi, uint4* dvb, const In* phib,
                                            const In* psib, const In* vbb, int64_t ts,
                                            const ScanArgs& a, int w, const DmaOffsets& d) {
@@ -193,7 +196,7 @@ __device__ __forceinline__ void issue_step(uint4* dphi, uint4* dpsi, uint4* dvb,
   const char* bpsi = reinterpret_cast<const char*>(psib + ts * a.k_st);
   const char* bvb = reinterpret_cast<const char*>(vbb + ts * a.v_st);
 #pragma unroll
-  for (int u = 0; u < 7; ++u) {
+  for (int u = 0; u < (FEAT ? 6 : 7); ++u) {
     const int I = w + 8 * u;
     if (I < ss::kLoads) {
       const char* base = u < 2 ? bphi : u < 4 ? bpsi : bvb;
@@ -257,11 +260,14 @@ __device__ __forceinline__ f32x4 mma16(f32x4 c, f16x4 a, f16x4 b) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
-template <typename In>
+// FEAT: phi, psi and vb are Q, K and V rows (v_st may be 128); each step's
+// Phi and Psi tiles are formed in place from the DMA'd Q and K tiles
+// (feat_rows, W in registers), the key gate applied to Psi.
+template <typename In, bool FEAT>
 __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
     const float* __restrict__ Sg, const float* __restrict__ Y, const float* __restrict__ gate,
-    float* __restrict__ out, ScanArgs a) {
+    float* __restrict__ out, ScanArgs a, FeatArgs fa) {
   using namespace ss;
   typedef typename Traits<In>::frag Frag;
   typedef typename Traits<In>::half_frag Half;
@@ -308,7 +314,15 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   dma_offsets<In>(dmo, a, w, lane);
   RowOffsets rof;
   row_offsets(rof, a, w, lane);
-  if (nsteps > 0) issue_step<In>(phi0, psi0, vb0, phib, psib, vbb, tk0, a, w, dmo);
+  if (nsteps > 0) issue_step<In, FEAT>(phi0, psi0, vb0, phib, psib, vbb, tk0, a, w, dmo);
+  Frag wa[4];
+  const In* hb = nullptr;
+  if constexpr (FEAT) {
+    feat_w_load<In>(wa, (const In*)fa.W, w, lane);
+    feat_ones_tile<In>(vb0 + kTileChunks, threadIdx.x, kThreads);
+    feat_ones_tile<In>(vb1 + kTileChunks, threadIdx.x, kThreads);
+    hb = fa.h ? (const In*)fa.h + b * fa.h_sb : nullptr;
+  }
 
   // incoming state: S[a][16w + lane%16] for all a, and the normaliser column
   // block S[a][128 + lane%16] for this wave's rows a in [16w, 16w + 16)
@@ -343,11 +357,17 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     int lane = lane_id();
     asm volatile("" : "+v"(lane));
     const int r16 = lane & 15, g = lane >> 4;
+    float hv[4];                      // FEAT: the key gate of the lane's four rows
+    if constexpr (FEAT) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) hv[tt] = hb ? to_f32(hb[ts + 16 * tt + r16]) : 1.f;
+    }
     if (s + 1 < nsteps) {
-      issue_step<In>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib, vbb,
-                     ts + kStep, a, w, dmo);
+      issue_step<In, FEAT>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib,
+                           vbb, ts + kStep, a, w, dmo);
       static_assert(kLoads / 8 == 6 && kLoads % 8 == 1, "seven loads on wave 0, six on the rest");
-      if (w == 0)
+      // the gate loads (issued first) are older than this step's six DMA loads
+      if (!FEAT && w == 0)
         wait_vmcnt<7>();
       else
         wait_vmcnt<6>();
@@ -355,6 +375,14 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
       wait_vmcnt<0>();
     }
     lds_barrier();      // every wave's DMA of this step has landed
+    if constexpr (FEAT) {
+      uint4* fphi = BUF ? phi1 : phi0;
+      uint4* fpsi = BUF ? psi1 : psi0;
+      const auto sw = [](int t) { return swz16(t); };
+      feat_rows<In, 4>(fphi, 0, true, wa, w, fa.kind, false, hv, lane, sw);
+      feat_rows<In, 4>(fpsi, 0, true, wa, w, fa.kind, hb != nullptr, hv, lane, sw);
+      lds_barrier();    // the step's Phi and Psi tiles are complete
+    }
     YRegs yr;
     issue_y(yr, Yb, gb, Sb, ts, a, rof, lane);
 
@@ -540,12 +568,13 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 // Issue one step's DMA: Psi (16 loads) and Vb (17) for rows
 // tok(row) = start + stride * (base + row), row < 64; wave 0 issues five
 // loads, the others four.
-template <typename In>
+// FEAT: K and V rows; the ninth Vb tile is constant, so 32 loads, four a wave.
+template <typename In, bool FEAT>
 __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* psib,
                                            const In* vbb, const GramItems& it, int item,
                                            int64_t start, int64_t stride, int base, int count,
                                            int64_t k_st, int64_t v_st, int w, int lane) {
-  constexpr int kL = ss::kPhiLoads + ss::kVbLoads;     // 33
+  constexpr int kL = ss::kPhiLoads + ss::kVbLoads - (FEAT ? 1 : 0);     // 33 or 32
 #pragma unroll
   for (int u = 0; u < 5; ++u) {
     const int I = w + 8 * u;
@@ -578,11 +607,14 @@ __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* ps
 // 35 KB of LDS let three workgroups share a CU instead of two, which is what
 // a launch of one-step items -- a load latency, a few MFMAs and a 66 KB
 // store each -- is limited by.
-template <typename In, bool ONE>
-__global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
+// FEAT: psi and vb are K and V rows; each step's Psi tile is formed in place
+// from the DMA'd K tile (feat_rows, W in registers, two halves of 32 rows),
+// times the key gate.
+template <typename In, bool ONE, bool FEAT>
+__global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_stream_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, float* __restrict__ G,
     float* __restrict__ G_last, GramItems it, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
-    int64_t v_st, int64_t g_sb, int64_t g_si, int64_t gl_sb) {
+    int64_t v_st, int64_t g_sb, int64_t g_si, int64_t gl_sb, FeatArgs fa) {
   using namespace ss;
   typedef typename Traits<In>::frag Frag;
   // psi0 and vb0 are one array: after the last step it stages the output
@@ -608,8 +640,16 @@ __global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
 #pragma unroll
   for (int at = 0; at < 8; ++at) accS[at] = zero4();
   if (nsteps > 0)
-    issue_gram<In>(psi0, vb0, psib, vbb, it, item, start, stride, 0, count, k_st, v_st, w,
-                   lane_id());
+    issue_gram<In, FEAT>(psi0, vb0, psib, vbb, it, item, start, stride, 0, count, k_st, v_st, w,
+                         lane_id());
+  Frag wa[4];
+  const In* hb = nullptr;
+  if constexpr (FEAT) {
+    feat_w_load<In>(wa, (const In*)fa.W, w, lane_id());
+    feat_ones_tile<In>(vb0 + kTileChunks, threadIdx.x, kThreads);
+    if (!ONE) feat_ones_tile<In>(vb1 + kTileChunks, threadIdx.x, kThreads);
+    hb = fa.h ? (const In*)fa.h + b * fa.h_sb : nullptr;
+  }
 
   auto step = [&](auto BUFC, int s) {
     constexpr int BUF = decltype(BUFC)::value;
@@ -618,11 +658,21 @@ __global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
     int lane = lane_id();
     asm volatile("" : "+v"(lane));
     const int g = lane >> 4;
+    float hv[4];                      // FEAT: the key gate of the lane's four rows
+    if constexpr (FEAT) {
+      const int r16 = lane & 15;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int row = s * kStep + 16 * tt + r16;
+        hv[tt] = hb ? to_f32(hb[gram_token(it, item, start, stride, row < count ? row : 0)]) : 1.f;
+      }
+    }
     if (!ONE && s + 1 < nsteps) {
-      issue_gram<In>(BUF ? psi0 : psi1, BUF ? vb0 : vb1, psib, vbb, it, item, start, stride,
-                     (s + 1) * kStep, count, k_st, v_st, w, lane);
+      issue_gram<In, FEAT>(BUF ? psi0 : psi1, BUF ? vb0 : vb1, psib, vbb, it, item, start, stride,
+                           (s + 1) * kStep, count, k_st, v_st, w, lane);
       static_assert(kPhiLoads + kVbLoads == 33, "five loads on wave 0, four on the rest");
-      if (w == 0)
+      // the gate loads (issued first) are older than this step's DMA loads
+      if (!FEAT && w == 0)
         wait_vmcnt<5>();
       else
         wait_vmcnt<4>();
@@ -630,6 +680,14 @@ __global__ __launch_bounds__(ss::kThreads, ONE ? 3 : 2) void gram_stream_kernel(
       wait_vmcnt<0>();
     }
     lds_barrier();
+    if constexpr (FEAT) {
+      uint4* fpsi = BUF ? psi1 : psi0;
+      const auto sw = [](int t) { return swz16(t); };
+      const float h01[2] = {hv[0], hv[1]}, h23[2] = {hv[2], hv[3]};
+      feat_rows<In, 2>(fpsi, 0, true, wa, w, fa.kind, hb != nullptr, h01, lane, sw);
+      feat_rows<In, 2>(fpsi, 2, true, wa, w, fa.kind, hb != nullptr, h23, lane, sw);
+      lds_barrier();    // the step's Psi tile is complete
+    }
     const int nvalid = count - s * kStep;        // rows of this step holding tokens
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -717,10 +775,12 @@ bool gram_stream_ok(int dtype, const void* psi, const void* vb, int r, int p, in
   return variant(SMAT_VARIANT_GRAM) == 0;
 }
 
-int gram_stream_launch(int dtype, const void* psi, const void* vb, float* G, float* G_last,
-                       const GramItems& it, int nitems, int nb, int p, int64_t k_sb,
-                       int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
-                       int64_t gl_sb, hipStream_t stream, const char* who) {
+template <bool FEAT>
+static int gram_stream_go(int dtype, const void* psi, const void* vb, float* G, float* G_last,
+                          const GramItems& it, int nitems, int nb, int p, int64_t k_sb,
+                          int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                          int64_t gl_sb, const FeatArgs& fa, hipStream_t stream,
+                          const char* who) {
   dim3 grid((unsigned)nitems, (unsigned)nb);
   // the longest item: a profile has ceil((n - n_P) / N0) terms, the global
   // channel (item N0, when launched) n_P
@@ -732,24 +792,44 @@ int gram_stream_launch(int dtype, const void* psi, const void* vb, float* G, flo
   }
   if (dtype == SMAT_BF16) {
     if (one)
-      hipLaunchKernelGGL((gram_stream_kernel<bf16, true>), grid, dim3(ss::kThreads), 0, stream,
-                         (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
-                         v_st, g_sb, g_si, gl_sb);
+      hipLaunchKernelGGL((gram_stream_kernel<bf16, true, FEAT>), grid, dim3(ss::kThreads), 0,
+                         stream, (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st,
+                         v_sb, v_st, g_sb, g_si, gl_sb, fa);
     else
-      hipLaunchKernelGGL((gram_stream_kernel<bf16, false>), grid, dim3(ss::kThreads), 0, stream,
-                         (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
-                         v_st, g_sb, g_si, gl_sb);
+      hipLaunchKernelGGL((gram_stream_kernel<bf16, false, FEAT>), grid, dim3(ss::kThreads), 0,
+                         stream, (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st,
+                         v_sb, v_st, g_sb, g_si, gl_sb, fa);
   } else {
     if (one)
-      hipLaunchKernelGGL((gram_stream_kernel<f16, true>), grid, dim3(ss::kThreads), 0, stream,
-                         (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
-                         v_st, g_sb, g_si, gl_sb);
+      hipLaunchKernelGGL((gram_stream_kernel<f16, true, FEAT>), grid, dim3(ss::kThreads), 0,
+                         stream, (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st,
+                         v_sb, v_st, g_sb, g_si, gl_sb, fa);
     else
-      hipLaunchKernelGGL((gram_stream_kernel<f16, false>), grid, dim3(ss::kThreads), 0, stream,
-                         (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st, v_sb,
-                         v_st, g_sb, g_si, gl_sb);
+      hipLaunchKernelGGL((gram_stream_kernel<f16, false, FEAT>), grid, dim3(ss::kThreads), 0,
+                         stream, (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st,
+                         v_sb, v_st, g_sb, g_si, gl_sb, fa);
   }
   return launch_status(who);
+}
+
+int gram_stream_launch(int dtype, const void* psi, const void* vb, float* G, float* G_last,
+                       const GramItems& it, int nitems, int nb, int p, int64_t k_sb,
+                       int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                       int64_t gl_sb, hipStream_t stream, const char* who) {
+  return gram_stream_go<false>(dtype, psi, vb, G, G_last, it, nitems, nb, p, k_sb, k_st, v_sb,
+                               v_st, g_sb, g_si, gl_sb, FeatArgs{}, stream, who);
+}
+
+// The Gram sums with the feature map in place: k, v are K and V rows
+// (d_qk = d_v = 128, 16-byte aligned rows); any item count (no split-K).
+int gram_stream_launch_feat(int dtype, const void* k, const void* v, float* G, float* G_last,
+                            const GramItems& it, int nitems, int nb, int64_t k_sb, int64_t k_st,
+                            int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
+                            int64_t gl_sb, const FeatArgs& fa, hipStream_t stream,
+                            const char* who) {
+  if (nitems == 0 || nb == 0) return SMAT_OK;
+  return gram_stream_go<true>(dtype, k, v, G, G_last, it, nitems, nb, 129, k_sb, k_st, v_sb, v_st,
+                              g_sb, g_si, gl_sb, fa, stream, who);
 }
 
 // The shapes this kernel serves; everything else runs scan_fused_kernel.
@@ -771,17 +851,35 @@ bool scan_stream_ok(int dtype, const void* phi, const void* psi, const void* vb,
   return variant(SMAT_VARIANT_SCAN) == 0;
 }
 
+template <bool FEAT>
+static int scan_stream_go(int dtype, const void* phi, const void* psi, const void* vb,
+                          const float* Sg, const float* Y, const float* gate, float* out, int nb,
+                          int ng, const ScanArgs& a, const FeatArgs& fa, hipStream_t stream) {
+  dim3 grid((unsigned)ng, (unsigned)nb);
+  if (dtype == SMAT_BF16)
+    hipLaunchKernelGGL((scan_stream_kernel<bf16, FEAT>), grid, dim3(ss::kThreads), 0, stream,
+                       (const bf16*)phi, (const bf16*)psi, (const bf16*)vb, Sg, Y, gate, out, a,
+                       fa);
+  else
+    hipLaunchKernelGGL((scan_stream_kernel<f16, FEAT>), grid, dim3(ss::kThreads), 0, stream,
+                       (const f16*)phi, (const f16*)psi, (const f16*)vb, Sg, Y, gate, out, a, fa);
+  return launch_status("smat_causal_scan");
+}
+
 int scan_stream_launch(int dtype, const void* phi, const void* psi, const void* vb,
                        const float* Sg, const float* Y, const float* gate, float* out, int nb,
                        int ng, const ScanArgs& a, hipStream_t stream) {
-  dim3 grid((unsigned)ng, (unsigned)nb);
-  if (dtype == SMAT_BF16)
-    hipLaunchKernelGGL(scan_stream_kernel<bf16>, grid, dim3(ss::kThreads), 0, stream,
-                       (const bf16*)phi, (const bf16*)psi, (const bf16*)vb, Sg, Y, gate, out, a);
-  else
-    hipLaunchKernelGGL(scan_stream_kernel<f16>, grid, dim3(ss::kThreads), 0, stream,
-                       (const f16*)phi, (const f16*)psi, (const f16*)vb, Sg, Y, gate, out, a);
-  return launch_status("smat_causal_scan");
+  return scan_stream_go<false>(dtype, phi, psi, vb, Sg, Y, gate, out, nb, ng, a, FeatArgs{},
+                               stream);
+}
+
+// The streaming causal pass with the feature map in place: phi, psi, vb are
+// Q, K, V rows (the shapes scan_stream_ok accepts, with V rows of 128).
+int scan_stream_launch_feat(int dtype, const void* q, const void* k, const void* v,
+                            const float* Sg, const float* Y, const float* gate, float* out,
+                            int nb, int ng, const ScanArgs& a, const FeatArgs& fa,
+                            hipStream_t stream) {
+  return scan_stream_go<true>(dtype, q, k, v, Sg, Y, gate, out, nb, ng, a, fa, stream);
 }
 
 }  // namespace smat

@@ -81,6 +81,10 @@ SIGNATURES = {
                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _i64, _p]),
     "smat_featurise_backward_parts": (_i64, [_i, _i]),
+    "smat_forward_fused": (_i, [_i, _p, _p, _p, _p, _p, _i, _p, _i, _p, _i, _p, _i, _p, _p,
+                                _i, _i, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64, _i64,
+                                _i64, _i64, _i64, _i64, _i64, _p, _i64, _p]),
+    "smat_forward_fused_workspace_bytes": (_i64, [_i, _i, _i, _i, _i, _i, _i]),
     "smat_csr_workspace_bytes": (_i64, [_i, _i, _i]),
     "smat_csr_lists": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "smat_featurise_backward": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,

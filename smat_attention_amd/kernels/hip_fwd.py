@@ -551,6 +551,52 @@ def forward(Phi, Psi, Vb, idx, deg: int, *, n: int, n_P: int, N0: int, B: int, c
     return out
 
 
+def forward_fused(W, kind: str, Q, K, V, h, idx, deg: int, *, n: int, n_P: int, N0: int, B: int,
+                  chunk: int, indptr=None, plane_code=None, field_q: int = 0, g=None,
+                  workspace=None):
+    """:func:`forward` from Q, K, V with the feature map inside the kernels
+    (``smat_forward_fused``): Phi, Psi and Vb are formed in LDS by the
+    consumers and never stored.  Returns fp32 ``(nb, T, d_v)``."""
+    who = "forward_fused"
+    _on_gpu(who, Q, K, V, W, h, idx, indptr, g)
+    nb, T, dqk = Q.shape
+    for t in (K, V, W, h):
+        if t is not None and t.dtype != Q.dtype:
+            raise TypeError(f"{who}: all inputs must share Q's dtype {Q.dtype}, got {t.dtype}")
+    if kind not in _FEATURE_KINDS:
+        raise ValueError(f"{who}: unknown feature map {kind!r}")
+    _shape(who, "K", K, (nb, T, dqk))
+    d_v = V.shape[-1]
+    _shape(who, "V", V, (nb, T, d_v))
+    if h is not None:
+        _shape(who, "h", h, (nb, T))
+    if g is not None:
+        _shape(who, "g", g, (nb, T))
+    code = _code(Q, who)
+    q, q_sb, q_st = _rows3(Q)
+    k, k_sb, k_st = _rows3(K)
+    v, v_sb, v_st = _rows3(V)
+    Wc = W.contiguous()
+    hc = h.contiguous() if h is not None else None
+    gc = g.float().contiguous() if g is not None else None
+    r, p = W.shape[0], d_v + 1
+    out = torch.empty(nb, T, d_v, device=Q.device, dtype=torch.float32)
+    need = _lib.query("smat_forward_fused_workspace_bytes", nb, T, n, N0, B, n_P, chunk)
+    if (workspace is None or workspace.device != Q.device or workspace.dtype != torch.uint8
+            or workspace.numel() < need + 256):
+        workspace = torch.empty(need + 256, device=Q.device, dtype=torch.uint8)
+    base = workspace.data_ptr()
+    aligned = (base + 255) & ~255
+    avail = workspace.numel() - (aligned - base)
+    call("smat_forward_fused", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), Wc.data_ptr(),
+         ptr(hc), _FEATURE_KINDS[kind], ptr(idx),
+         int(idx is not None and idx.dtype == torch.int64), ptr(indptr), deg, ptr(plane_code),
+         field_q, out.data_ptr(), ptr(gc), nb, T, n, n_P, N0, B, chunk, q_sb, q_st, k_sb, k_st,
+         v_sb, v_st, hc.stride(0) if hc is not None else 0, out.stride(0), out.stride(1),
+         gc.stride(0) if gc is not None else 0, aligned, avail, stream_of(q))
+    return out
+
+
 def decode_step(Phi_t, Psi_t, Vb_t, S_in, S_out, U, step: int, *, out=None, o_full=None):
     """One decode step for a batch; returns fp32 ``(nb, p-1)`` and writes ``S_out``."""
     who = "decode_step"
