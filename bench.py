@@ -195,6 +195,60 @@ def prefill_rows(args):
     return rows
 
 
+def fused_rows(args):
+    """The long prefill from q, k, v, featurisation included (B=1, H=8,
+    head_dim 128, bf16 q, k, v ~ N(0, 1), k scaled 1/sqrt(128), elu+1 map, no
+    gates), at T in {32768, 131072, 524288}, d = 3 and 1: the reference's two
+    passes (featurise, then the schedule; attention.py:82-106, :391-455) as
+    featurise + smat_attention, against smat_attention_fused, whose kernels
+    form Phi, Psi and [V, 1] in LDS.  ms per call (host clock between device
+    synchronisations, inputs resident) and tokens/s of the fused call."""
+    import torch
+    from smat_attention_amd import attention as A
+    from smat_attention_amd.kernels import _lib
+    from smat_attention_amd.mask import build_mask
+    nb, hd, steps = args.heads, args.head_dim, args.row_steps
+    dev = torch.device("cuda:0")
+    bf = torch.bfloat16
+    phi = A.make_phi(hd, hd, device=dev, dtype=bf, seed=0)
+    rows = {}
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = fn()
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all()
+        return (time.perf_counter() - t0) / steps * 1e3
+
+    for T in (32768, 131072, 524288):
+        g = torch.Generator(device=dev).manual_seed(T + 7)
+        Q = torch.randn(nb, T, hd, device=dev, generator=g).to(bf)
+        K = (torch.randn(nb, T, hd, device=dev, generator=g) * hd ** -0.5).to(bf)
+        V = torch.randn(nb, T, hd, device=dev, generator=g).to(bf)
+        for d in (3, 1):
+            spec = A.to_device(build_mask(T, d, chunk=128), dev)
+            ws = torch.empty(_lib.query("smat_forward_fused_workspace_bytes", nb, T, spec.n,
+                                        spec.N0, spec.B, spec.n_P, 128) + 256,
+                             device=dev, dtype=torch.uint8)
+            ms_u = timed(lambda: A.smat_attention(*A.featurise(Q, K, V, phi), spec))
+            ms_f = timed(lambda: A.smat_attention_fused(Q, K, V, phi, spec, workspace=ws))
+            rows[f"T{T}_d{d}"] = {"featurise_then_forward_ms": round(ms_u, 4),
+                                  "fused_ms": round(ms_f, 4),
+                                  "fused_kernels": A._fused_ok(Q, K, V, phi, spec, 128, None),
+                                  "fused_tokens_per_s": round(T / (ms_f * 1e-3), 1),
+                                  "speedup": round(ms_u / ms_f, 3)}
+            log(f"[bench] q,k,v prefill T={T} d={d}: featurise + forward {ms_u:.3f} ms, "
+                f"fused {ms_f:.3f} ms")
+            del ws
+        del Q, K, V
+        torch.cuda.empty_cache()
+    return rows
+
+
 class Events:
     """Per-kernel durations with events recorded on the stream the kernels use."""
 
@@ -645,6 +699,7 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_rows:
         result["prefill_rows"] = prefill_rows(args)
+        result["prefill_qkv_rows"] = fused_rows(args)
     if not args.no_train:
         result["train_step"] = {f"d{d}": train_step_bench(d, max(3, args.kernel_reps // 2))
                                 for d in (2, 3)}

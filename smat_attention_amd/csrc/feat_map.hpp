@@ -14,11 +14,30 @@
 
 namespace smat {
 
+// expm1(v) for v <= 0 in a few instructions: the degree-6 Taylor polynomial
+// on (-0.25, 0] (truncation under 2e-8 relative there) and exp(v) - 1 below,
+// where |expm1| > 0.22 and the hardware exp2 keeps the error under 1e-5
+// relative.  Rounded to bf16, it equals the correctly rounded expm1 (and the
+// fp32 libm expm1f) for every negative bf16 input -- an exhaustive check --
+// at a fraction of expm1f's cost, which dominates the feature map's VALU time.
+__device__ __forceinline__ float expm1_neg(float v) {
+  if (v > -0.25f) {
+    float r = 1.f / 720.f;
+    r = fmaf(v, r, 1.f / 120.f);
+    r = fmaf(v, r, 1.f / 24.f);
+    r = fmaf(v, r, 1.f / 6.f);
+    r = fmaf(v, r, 0.5f);
+    r = fmaf(v, r, 1.f);
+    return v * r;
+  }
+  return __builtin_amdgcn_exp2f(v * 1.4426950408889634f) - 1.f;
+}
+
 template <typename In>
 __device__ __forceinline__ float feature_map(float acc, int kind) {
   const float v = to_f32(from_f32<In>(acc));                 // torch's matmul output
   if (kind == 0) {
-    const float e = to_f32(from_f32<In>(v > 0.f ? v : expm1f(v)));
+    const float e = to_f32(from_f32<In>(v > 0.f ? v : expm1_neg(v)));
     return to_f32(from_f32<In>(e + 1.0f));
   }
   return to_f32(from_f32<In>(fmaxf(v, 0.f) + 1e-3f));
@@ -45,19 +64,19 @@ __device__ __forceinline__ void feat_w_load(typename Traits<In>::frag (&wa)[4], 
     wa[kb] = *reinterpret_cast<const typename Traits<In>::frag*>(row + 32 * kb + 8 * g);
 }
 
-// In place over NRT 16-row tiles starting at row tile rt0 of an LDS tile of
-// 256-byte rows whose 16-byte chunk k of row t sits at slot k ^ swz(t): read
-// the rows' 128 input values (X = Q or K), form this wave's features
+// Over NRT 16-row tiles starting at row tile rt0 of LDS tiles of 256-byte
+// rows whose 16-byte chunk k of row t sits at slot k ^ swz(t): read the rows'
+// 128 input values (X = Q or K) from src, form this wave's features
 // C = W[16 wf .. +16] X^T on MFMA (lane (t, g) ends with features 16 wf + 4 g
-// .. +3 of row t), wait for every wave's reads (barrier), then overwrite the
-// row's feature chunk with map(C) (times gate[rt] for the lane's row of tile
-// rt0 + rt when use_gate).
-// Every wave of the workgroup calls it (the barrier); inactive waves only
-// meet the barrier.  The caller places a barrier before the feature rows are
-// read.  The MFMA sequence is the stand-alone kernel's (k-blocks 0..3 in
-// order), so the features are bitwise the same.
+// .. +3 of row t), then write map(C) (times gate[rt] for the lane's row of tile
+// rt0 + rt when use_gate) into the row's feature chunk of dst.  In place
+// (dst == src) every wave's reads must precede any write: the call then has a
+// barrier between the two, which every wave of the workgroup must meet
+// (inactive waves only meet it).  The caller places a barrier before the
+// feature rows are read.  The MFMA sequence is the stand-alone kernel's
+// (k-blocks 0..3 in order), so the features are bitwise the same.
 template <typename In, int NRT, typename Swz>
-__device__ __forceinline__ void feat_rows(uint4* tile, int rt0, bool active,
+__device__ __forceinline__ void feat_rows(const uint4* src, uint4* dst, int rt0, bool active,
                                           const typename Traits<In>::frag (&wa)[4], int wf,
                                           int kind, bool use_gate, const float (&gate)[NRT],
                                           int lane, Swz swz) {
@@ -72,7 +91,7 @@ __device__ __forceinline__ void feat_rows(uint4* tile, int rt0, bool active,
       const int t = 16 * (rt0 + rt) + r16;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
-        bx[rt][kb] = *reinterpret_cast<const Frag*>(tile + t * 16 + ((4 * kb + g) ^ swz(t)));
+        bx[rt][kb] = *reinterpret_cast<const Frag*>(src + t * 16 + ((4 * kb + g) ^ swz(t)));
     }
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
@@ -81,7 +100,7 @@ __device__ __forceinline__ void feat_rows(uint4* tile, int rt0, bool active,
       for (int kb = 0; kb < 4; ++kb) acc[rt] = mma(acc[rt], wa[kb], bx[rt][kb]);
     }
   }
-  lds_barrier();                                     // every wave has read its rows
+  if (dst == src) lds_barrier();                     // every wave has read its rows
   if (active) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
@@ -93,7 +112,7 @@ __device__ __forceinline__ void feat_rows(uint4* tile, int rt0, bool active,
         if (use_gate) y = to_f32(from_f32<In>(y * gate[rt]));
         hv[i] = from_f32<In>(y);
       }
-      char* p = reinterpret_cast<char*>(tile + t * 16 + ((2 * wf + (g >> 1)) ^ swz(t)));
+      char* p = reinterpret_cast<char*>(dst + t * 16 + ((2 * wf + (g >> 1)) ^ swz(t)));
       *reinterpret_cast<Half*>(p + 8 * (g & 1)) = hv;
     }
   }

@@ -251,8 +251,8 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
     lds_barrier();
     if constexpr (FEAT) {
       const float none[kMT] = {};
-      feat_rows<In, kMT>(BUF ? p1 : p0, 0, w < 8, wa, w, fa.kind, false, none, lane,
-                         [](int t) { return t & 15; });
+      feat_rows<In, kMT>(BUF ? p1 : p0, BUF ? p1 : p0, 0, w < 8, wa, w, fa.kind, false, none,
+                         lane, [](int t) { return t & 15; });
       lds_barrier();    // the item's Phi rows are complete
     }
 

@@ -261,8 +261,10 @@ __device__ __forceinline__ f32x4 mma16(f32x4 c, f16x4 a, f16x4 b) {
 }
 
 // FEAT: phi, psi and vb are Q, K and V rows (v_st may be 128); each step's
-// Phi and Psi tiles are formed in place from the DMA'd Q and K tiles
-// (feat_rows, W in registers), the key gate applied to Psi.
+// Phi and Psi tiles are formed from the DMA'd Q and K tiles into two more
+// tiles, phiF and psiF (feat_rows, W in registers), the key gate applied to
+// Psi.  A step's reads of phiF and psiF end before the barrier after its
+// state update, so the next step's features overwrite them safely.
 template <typename In, bool FEAT>
 __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
@@ -280,6 +282,8 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   __shared__ __attribute__((aligned(16))) uint4 share[kStep * 8];
   // normaliser partials: wave w's share of H[t][p-1] at normp[norm_slot(t, w)]
   __shared__ __attribute__((aligned(16))) float normp[kStep * 8];
+  __shared__ __attribute__((aligned(16))) uint4 phiF[FEAT ? kTileChunks : 1];
+  __shared__ __attribute__((aligned(16))) uint4 psiF[FEAT ? kTileChunks : 1];
 
   const int grp = blockIdx.x;
   const int64_t b = blockIdx.y;
@@ -346,8 +350,8 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 
   auto step = [&](auto BUFC, int s) {
     constexpr int BUF = decltype(BUFC)::value;
-    const uint4* tphi = BUF ? phi1 : phi0;
-    const uint4* tpsi = BUF ? psi1 : psi0;
+    const uint4* tphi = FEAT ? phiF : BUF ? phi1 : phi0;
+    const uint4* tpsi = FEAT ? psiF : BUF ? psi1 : psi0;
     const uint4* tvb = BUF ? vb1 : vb0;
     const int64_t ts = tk0 + (int64_t)s * kStep;
     // An opaque copy of the lane index per step: the LDS addresses derived
@@ -376,11 +380,10 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     }
     lds_barrier();      // every wave's DMA of this step has landed
     if constexpr (FEAT) {
-      uint4* fphi = BUF ? phi1 : phi0;
-      uint4* fpsi = BUF ? psi1 : psi0;
       const auto sw = [](int t) { return swz16(t); };
-      feat_rows<In, 4>(fphi, 0, true, wa, w, fa.kind, false, hv, lane, sw);
-      feat_rows<In, 4>(fpsi, 0, true, wa, w, fa.kind, hb != nullptr, hv, lane, sw);
+      feat_rows<In, 4>(BUF ? phi1 : phi0, phiF, 0, true, wa, w, fa.kind, false, hv, lane, sw);
+      feat_rows<In, 4>(BUF ? psi1 : psi0, psiF, 0, true, wa, w, fa.kind, hb != nullptr, hv, lane,
+                       sw);
       lds_barrier();    // the step's Phi and Psi tiles are complete
     }
     YRegs yr;
@@ -684,8 +687,8 @@ __global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_str
       uint4* fpsi = BUF ? psi1 : psi0;
       const auto sw = [](int t) { return swz16(t); };
       const float h01[2] = {hv[0], hv[1]}, h23[2] = {hv[2], hv[3]};
-      feat_rows<In, 2>(fpsi, 0, true, wa, w, fa.kind, hb != nullptr, h01, lane, sw);
-      feat_rows<In, 2>(fpsi, 2, true, wa, w, fa.kind, hb != nullptr, h23, lane, sw);
+      feat_rows<In, 2>(fpsi, fpsi, 0, true, wa, w, fa.kind, hb != nullptr, h01, lane, sw);
+      feat_rows<In, 2>(fpsi, fpsi, 2, true, wa, w, fa.kind, hb != nullptr, h23, lane, sw);
       lds_barrier();    // the step's Psi tile is complete
     }
     const int nvalid = count - s * kStep;        // rows of this step holding tokens

@@ -52,16 +52,14 @@ def _run_both(spec, Q, K, V, h, g, kind="elu1", dt=BF):
 
 
 @pytest.mark.parametrize("T,d,n_P,gates,kind,nb", [
-    (4096, 2, 0, False, "elu1", 2), (4096, 2, 16, True, "relu", 2),
-    (8192, 3, 0, True, "elu1", 3), (2048, 3, 16, False, "elu1", 2),
-    (4096, 4, 0, False, "elu1", 2), (8192, 2, 0, True, "elu1", 1),
-    (4096, 1, 0, False, "elu1", 2)])
+    (4096, 2, 0, False, "elu1", 6), (4096, 2, 16, True, "relu", 6),
+    (8192, 3, 0, True, "elu1", 3), (2048, 3, 16, False, "elu1", 4),
+    (4096, 4, 0, False, "elu1", 2), (8192, 2, 0, True, "elu1", 4)])
 def test_fused_forward_matches_featurise_then_forward(T, d, n_P, gates, kind, nb):
     """Ragged profiles, the global channel (n_P = 16), the key gate h, the output
-    gate g, both feature maps, d = 1..4: the fused forward equals featurise then
+    gate g, both feature maps, d = 2..4: the fused forward equals featurise then
     smat_attention within 1e-5 of the largest entry.  d = 2 at T = 8192 (62
-    recent rows a type) and d = 1 (one type) take the staged query of the
-    recent rows' Phi."""
+    recent rows a type) takes the staged query of the recent rows' Phi."""
     spec = build_mask(T, d, chunk=128, n_P=n_P)
     _say("fused forward", T, d, n_P, gates, kind, nb)
     Q, K, V, h, g = _inputs(nb, T, seed=T + d + n_P, gates=gates)
@@ -109,6 +107,14 @@ def test_fused_forward_falls_back_outside_its_shape_and_under_grad():
     a = A.smat_attention_fused(Q, K, V, phi, spec)
     b = A.smat_attention(*A.featurise(Q, K, V, phi), spec)
     assert torch.equal(a, b)
+    # d = 1: one profile a sequence, the unfused pool's split-K path
+    spec1 = build_mask(4096, 1, chunk=128)
+    Q1, K1, V1, _, _ = _inputs(2, 4096, seed=3)
+    Q1, K1, V1 = Q1.to(DEV), K1.to(DEV), V1.to(DEV)
+    phi1 = A.FeatureMap(O.phi_weight(128, 128, dtype=BF, seed=0).to(DEV), "elu1")
+    assert not A._fused_ok(Q1, K1, V1, phi1, spec1, 128, None)
+    assert torch.equal(A.smat_attention_fused(Q1, K1, V1, phi1, spec1),
+                       A.smat_attention(*A.featurise(Q1, K1, V1, phi1), spec1))
     Q2, K2, V2, _, _ = _inputs(2, T, seed=9)
     xs = [x.to(DEV).requires_grad_(True) for x in (Q2, K2, V2)]
     phi2 = A.FeatureMap(O.phi_weight(128, 128, dtype=BF, seed=0).to(DEV), "elu1")
