@@ -568,14 +568,14 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
     wants_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (Phi, Psi, Vb, g))
     if wants_grad and not _no_grad_fn:
-        if not plain:
-            raise NotImplementedError(f"{who}: gradients are implemented for the pooled "
-                                      f"schedule of a geometric mask")
         if return_parts or timer is not None:
             raise NotImplementedError(f"{who}: return_parts/timer are forward-only; call "
                                       f"under torch.no_grad() or on detached inputs")
+        if endpoint:
+            from .kernels.hip_bwd import EndpointAttentionFunction
+            return EndpointAttentionFunction.apply(Phi, Psi, Vb, g, spec, C, long_range)
         from .kernels.hip_bwd import SmatAttentionFunction
-        return SmatAttentionFunction.apply(Phi, Psi, Vb, g, spec, C)
+        return SmatAttentionFunction.apply(Phi, Psi, Vb, g, spec, C, long_range)
 
     if plain and timer is None and not return_parts:
         idx, indptr, deg = _incidence_args(spec)

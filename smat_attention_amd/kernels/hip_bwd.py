@@ -225,6 +225,64 @@ def causal_scan_grad(Ph, Ps, Vv, dH, n: int, C: int):
     return dPhi, dPsi, dVb
 
 
+def _type_read_grad(Ph, dH, Uc, dPhi, Tp: int, row0: int, nrows: int, B: int):
+    """The type-major read's backward (query_by_type, attention.py:310-330): rows
+    ``row0 + h + k*B`` (k*B + h < nrows) read table ``U[h]``.  Accumulates
+    ``dPhi[row] += dH[row] U[h]^T`` and returns ``dU[h] = sum Phi[row]^T dH[row]``,
+    fp32 (nb, B, r, p).  Ph, dH, dPhi are (nb, Tp, .) rows; on smat_bgemm."""
+    nb, _, r = Ph.shape
+    p = dH.shape[-1]
+    rp = r * p
+    Brp = B * rp
+    dU = torch.empty(nb, B, r, p, device=Ph.device, dtype=torch.float32)
+    full, rem = divmod(nrows, B)
+    # rows of type h: row0 + h + k*B; first `full` rounds for every type, then
+    # one more row for types h < rem
+    if full:
+        _bgemm(dH, Uc, dPhi, M=full, N=r, K=p, n1=nb, n2=B,
+               a=(Tp * p, p, B * p, 1), b=(Brp, rp, 1, p), c=(Tp * r, r, B * r, 1),
+               beta=1, a_off=row0 * p, c_off=row0 * r)
+        _bgemm(Ph, dH, dU, M=r, N=p, K=full, n1=nb, n2=B,
+               a=(Tp * r, r, 1, B * r), b=(Tp * p, p, B * p, 1), c=(Brp, rp, p, 1),
+               a_off=row0 * r, b_off=row0 * p)
+    else:
+        dU.zero_()
+    if rem:
+        t0 = row0 + full * B
+        _bgemm(dH, Uc, dPhi, M=1, N=r, K=p, n1=nb, n2=rem,
+               a=(Tp * p, p, 0, 1), b=(Brp, rp, 1, p), c=(Tp * r, r, 0, 1),
+               beta=1, a_off=t0 * p, c_off=t0 * r)
+        _bgemm(Ph, dH, dU, M=r, N=p, K=1, n1=nb, n2=rem,
+               a=(Tp * r, r, 1, 0), b=(Tp * p, p, 0, 1), c=(Brp, rp, p, 1),
+               beta=1 if full else 0, a_off=t0 * r, b_off=t0 * p)
+        if not full and rem < B:
+            dU[:, rem:] = 0
+    return dU
+
+
+def _profile_pool_grad(Ps, Vv, dF, dPsi, dVb, Tp: int, n_P: int, n: int, N0: int):
+    """The profile pool's backward (pool_profiles, attention.py:199-236): token
+    ``n_P + x + s*N0 < n`` adds ``Psi^T Vb`` to profile x, so
+    ``dPsi[tok] += dF[x] Vb[tok]`` and ``dVb[tok] += dF[x]^T Psi[tok]``; on
+    smat_bgemm.  dF is (nb, N0, r*p) fp32."""
+    nb, _, r = Ps.shape
+    p = Vv.shape[-1]
+    rp = r * p
+    Nrp = N0 * rp
+    gq, grem = divmod(n - n_P, N0)
+    # pool backward over profile x's tokens n_P + x + s*N0
+    for lo, hi, cnt in ((0, grem, gq + 1), (grem, N0, gq)):
+        if hi <= lo or cnt <= 0:
+            continue
+        tok0 = n_P + lo
+        _bgemm(Vv, dF, dPsi, M=cnt, N=r, K=p, n1=nb, n2=hi - lo,
+               a=(Tp * p, p, N0 * p, 1), b=(Nrp, rp, 1, p), c=(Tp * r, r, N0 * r, 1),
+               beta=1, a_off=tok0 * p, b_off=lo * rp, c_off=tok0 * r)
+        _bgemm(Ps, dF, dVb, M=cnt, N=p, K=r, n1=nb, n2=hi - lo,
+               a=(Tp * r, r, N0 * r, 1), b=(Nrp, rp, p, 1), c=(Tp * p, p, N0 * p, 1),
+               beta=1, a_off=tok0 * r, b_off=lo * rp, c_off=tok0 * p)
+
+
 def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=None,
                         need_dg: bool = False):
     """``(dPhi, dPsi, dVb, dg)`` of ``out = smat_attention(Phi, Psi, Vb, spec, g=g)``
@@ -284,50 +342,14 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
              dVb.stride(0), dVb.stride(1), st)
     elif T_R > 0:
         Uc = U.float().contiguous()
-        dU = torch.empty(nb, B, r, p, device=dev, dtype=torch.float32)
-        full, rem = divmod(T_R, B)
-        Brp = B * rp
-        # rows of type h: n + h + k*B; first `full` rounds for every type, then
-        # one more row for types h < rem
-        if full:
-            _bgemm(dH, Uc, dPhi, M=full, N=r, K=p, n1=nb, n2=B,
-                   a=(Tp * p, p, B * p, 1), b=(Brp, rp, 1, p), c=(Tp * r, r, B * r, 1),
-                   beta=1, a_off=n * p, c_off=n * r)
-            _bgemm(Ph, dH, dU, M=r, N=p, K=full, n1=nb, n2=B,
-                   a=(Tp * r, r, 1, B * r), b=(Tp * p, p, B * p, 1), c=(Brp, rp, p, 1),
-                   a_off=n * r, b_off=n * p)
-        else:
-            dU.zero_()
-        if rem:
-            t0 = n + full * B
-            _bgemm(dH, Uc, dPhi, M=1, N=r, K=p, n1=nb, n2=rem,
-                   a=(Tp * p, p, 0, 1), b=(Brp, rp, 1, p), c=(Tp * r, r, 0, 1),
-                   beta=1, a_off=t0 * p, c_off=t0 * r)
-            _bgemm(Ph, dH, dU, M=r, N=p, K=1, n1=nb, n2=rem,
-                   a=(Tp * r, r, 1, 0), b=(Tp * p, p, 0, 1), c=(Brp, rp, p, 1),
-                   beta=1 if full else 0, a_off=t0 * r, b_off=t0 * p)
-            if not full and rem < B:
-                dU[:, rem:] = 0
+        dU = _type_read_grad(Ph, dH, Uc, dPhi, Tp, n, T_R, B)
         # dF = C^T dU (and the global channel's sum over all types)
         if getattr(spec, "incidence_identity", False):
             dF = dU.view(nb, N0, rp)                 # C = I: C^T dU = dU
         else:
             t_ptr, t_idx = transposed_incidence(spec, dev)
             dF = _incidence_rows(dU, t_idx, t_ptr, N0, nb, B, rp)
-        nX = n - n_P
-        gq, grem = divmod(nX, N0)
-        Nrp = N0 * rp
-        # pool backward over profile x's tokens n_P + x + s*N0
-        for lo, hi, cnt in ((0, grem, gq + 1), (grem, N0, gq)):
-            if hi <= lo or cnt <= 0:
-                continue
-            tok0 = n_P + lo
-            _bgemm(Vv, dF, dPsi, M=cnt, N=r, K=p, n1=nb, n2=hi - lo,
-                   a=(Tp * p, p, N0 * p, 1), b=(Nrp, rp, 1, p), c=(Tp * r, r, N0 * r, 1),
-                   beta=1, a_off=tok0 * p, b_off=lo * rp, c_off=tok0 * r)
-            _bgemm(Ps, dF, dVb, M=cnt, N=p, K=r, n1=nb, n2=hi - lo,
-                   a=(Tp * r, r, N0 * r, 1), b=(Nrp, rp, p, 1), c=(Tp * p, p, N0 * p, 1),
-                   beta=1, a_off=tok0 * r, b_off=lo * rp, c_off=tok0 * p)
+        _profile_pool_grad(Ps, Vv, dF, dPsi, dVb, Tp, n_P, n, N0)
         if n_P:
             allrows = torch.arange(B, device=dev, dtype=torch.int32)
             allrows._smat_checked_N0 = B
@@ -341,14 +363,22 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
 
 
 class SmatAttentionFunction(torch.autograd.Function):
-    """``smat_attention`` (pooled schedule, geometric mask) with its HIP backward."""
+    """``smat_attention`` on a geometric mask with its HIP backward.  The
+    direct and subtractive long-range schedules compute the same function as
+    the pooled one (the masked attention of attention.py:391-482), so their
+    gradient is the pooled schedule's: the forward runs the requested
+    schedule, the backward the pooled one on the pooled schedule's tables."""
 
     @staticmethod
-    def forward(ctx, Phi, Psi, Vb, g, spec, chunk):
+    def forward(ctx, Phi, Psi, Vb, g, spec, chunk, long_range="pooled"):
         from .. import attention as A
-        out, parts = A.smat_attention(Phi.detach(), Psi.detach(), Vb.detach(), spec,
-                                      chunk=chunk, g=None if g is None else g.detach(),
+        args = (Phi.detach(), Psi.detach(), Vb.detach(), spec)
+        gd = None if g is None else g.detach()
+        out, parts = A.smat_attention(*args, chunk=chunk, g=gd, long_range=long_range,
                                       return_parts=True, _no_grad_fn=True)
+        if "U" not in parts:                 # subtractive: the pooled tables for the backward
+            _, parts = A.smat_attention(*args, chunk=chunk, g=gd, return_parts=True,
+                                        _no_grad_fn=True)
         ctx.save_for_backward(Phi, Psi, Vb, g, parts["U"], parts["H"])
         ctx.spec, ctx.chunk = spec, chunk
         return out
@@ -362,7 +392,89 @@ class SmatAttentionFunction(torch.autograd.Function):
         return (dPhi.to(Phi.dtype) if ctx.needs_input_grad[0] else None,
                 dPsi.to(Psi.dtype) if ctx.needs_input_grad[1] else None,
                 dVb.to(Vb.dtype) if ctx.needs_input_grad[2] else None,
-                dg.to(g.dtype) if need_dg else None, None, None)
+                dg.to(g.dtype) if need_dg else None, None, None, None)
+
+
+class EndpointAttentionFunction(torch.autograd.Function):
+    """``smat_attention`` on the endpoint mask (attention.py:430-441) with its
+    gradient: every landmark token is its own profile and every recent row
+    its own type (n = N0 = B = 2^k, n_P = 0).  Forward: landmark row t reads
+    ``Z_t = sum_{x subset of t} Psi_x^T Vb_x`` (zeta), recent rows run the
+    causal scan restarted at n plus the long-range read of ``U = C F`` with
+    ``C[h, a] = 1{popcount(h & a) even}``.  Backward: the normalisation's,
+    the restarted scan's (causal_scan_grad), the two type reads'
+    (``_type_read_grad``: rows n + i read U, landmark rows read Z), then
+    ``dF = C dU`` (C is symmetric: the Walsh kernel) plus the superset sums of
+    dZ (zeta conjugated by the index complement, ``x -> N0 - 1 - x``), then
+    the pool's (``_profile_pool_grad``).  The direct and subtractive long
+    range are the same function, so they share this backward."""
+
+    @staticmethod
+    def forward(ctx, Phi, Psi, Vb, g, spec, chunk, long_range="pooled"):
+        from .. import attention as A
+        if spec.n_P or not (spec.n == spec.N0 == spec.B):
+            raise NotImplementedError("smat_attention: endpoint gradients need n = N0 = B and "
+                                      "n_P = 0")
+        args = (Phi.detach(), Psi.detach(), Vb.detach(), spec)
+        gd = None if g is None else g.detach()
+        out, parts = A.smat_attention(*args, chunk=chunk, g=gd, long_range=long_range,
+                                      return_parts=True, _no_grad_fn=True)
+        if "U" not in parts:
+            _, parts = A.smat_attention(*args, chunk=chunk, g=gd, return_parts=True,
+                                        _no_grad_fn=True)
+        ctx.save_for_backward(Phi, Psi, Vb, g, parts["U"], parts["H"])
+        ctx.spec, ctx.chunk = spec, chunk
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        Phi, Psi, Vb, g, U, H = ctx.saved_tensors
+        spec, C = ctx.spec, ctx.chunk
+        nb, T, r = Phi.shape
+        p = Vb.shape[-1]
+        n, N0 = spec.n, spec.N0
+        T_R = T - n
+        dev = Phi.device
+        need_dg = g is not None and ctx.needs_input_grad[3]
+        # ---- normalise
+        dout = dout.float().contiguous()
+        Hc = H.float().contiguous()
+        dH = torch.empty(nb, T, p, device=dev, dtype=torch.float32)
+        dg = torch.empty(nb, T, device=dev, dtype=torch.float32) if need_dg else None
+        gc = g.float().contiguous() if g is not None else None
+        call("smat_normalise_backward", dout.data_ptr(), Hc.data_ptr(), ptr(gc), dH.data_ptr(),
+             ptr(dg), nb, T, p, dout.stride(0), dout.stride(1), Hc.stride(0), Hc.stride(1),
+             dH.stride(0), dH.stride(1), gc.stride(0) if gc is not None else 0, stream_of(dH))
+        Ph, Ps, Vv = Phi.contiguous(), Psi.contiguous(), Vb.contiguous()
+        dPhi = torch.zeros(nb, T, r, device=dev, dtype=torch.float32)
+        dPsi = torch.zeros(nb, T, r, device=dev, dtype=torch.float32)
+        dVb = torch.zeros(nb, T, p, device=dev, dtype=torch.float32)
+        # ---- the recent block's causal scan, restarted at n (rows padded to whole chunks)
+        if T_R:
+            Tr = -(-T_R // C) * C
+
+            def padded(x):
+                out = torch.zeros(nb, Tr, x.shape[-1], device=dev, dtype=x.dtype)
+                out[:, :T_R] = x[:, n:]
+                return out
+            gP, gS, gV = causal_scan_grad(padded(Ph), padded(Ps), padded(Vv), padded(dH), 0, C)
+            dPhi[:, n:] = gP[:, :T_R]
+            dPsi[:, n:] = gS[:, :T_R]
+            dVb[:, n:] = gV[:, :T_R]
+        # ---- the two type reads: recent rows read U, landmark rows read Z
+        dF = torch.zeros(nb, N0, r, p, device=dev, dtype=torch.float32)
+        if T_R:
+            dU = _type_read_grad(Ph, dH, U.float().contiguous(), dPhi, T, n, T_R, spec.B)
+            dF += _hip.walsh(dU)                                  # C^T dU = C dU
+        if n:
+            Z = _hip.zeta(_hip.pool(Ps, Vv, 0, n, N0))
+            dZ = _type_read_grad(Ph, dH, Z, dPhi, T, 0, n, N0)
+            dF += _hip.zeta(dZ.flip(1).contiguous()).flip(1)    # superset sums
+            _profile_pool_grad(Ps, Vv, dF.view(nb, N0, r * p), dPsi, dVb, T, 0, n, N0)
+        return (dPhi.to(Phi.dtype) if ctx.needs_input_grad[0] else None,
+                dPsi.to(Psi.dtype) if ctx.needs_input_grad[1] else None,
+                dVb.to(Vb.dtype) if ctx.needs_input_grad[2] else None,
+                dg.to(g.dtype) if need_dg else None, None, None, None)
 
 
 class CausalScanFunction(torch.autograd.Function):

@@ -390,6 +390,47 @@ def test_fused_cell_backward(d):
         assert e < (2e-3 if name in ("dQ", "dK", "dV") else 1e-4), name
 
 
+@pytest.mark.parametrize("lr,T,d,n_P,gate", [
+    ("direct", 2048, 3, 0, False), ("direct", 2048, 3, 16, True),
+    ("subtractive", 2048, 3, 0, False), ("subtractive", 4096, 2, 16, True),
+    ("endpoint", 256, 0, 0, False), ("endpoint", 300, 0, 0, True), ("endpoint", 1024, 0, 0, False)])
+def test_schedule_gradients(lr, T, d, n_P, gate):
+    """Gradients through the direct and subtractive long-range schedules and
+    the endpoint mask (zeta landmark block, Walsh incidence), fp32, against
+    fp64 autograd through the oracle's own schedule (attention.py:333-384,
+    430-441, 458-482): dPhi, dPsi, dVb (and dg) within 1e-5 of the largest
+    entry (1e-4 for the subtractive schedule, whose forward cancels in the
+    normaliser)."""
+    nb, hd = 2, 32
+    if lr == "endpoint":
+        spec, C, lrs = build_mask(T, T.bit_length() - 1, chunk=8), 8, "pooled"
+        assert spec.kind == "endpoint"
+    else:
+        spec, C, lrs = build_mask(T, d, chunk=128, n_P=n_P), 128, lr
+    spec_d = A.to_device(spec, DEV, want_direct=lr == "direct")
+    _say("schedule gradients", lr, T, d, n_P, gate)
+    Phi, Psi, Vb = _feats(nb, T, hd, seed=60 + T)
+    gen = torch.Generator().manual_seed(61)
+    w = torch.randn(nb, T, hd, generator=gen)
+    g = (torch.rand(nb, T, generator=gen) + 0.5) if gate else None
+    xs = [t.to(DEV).requires_grad_(True) for t in (Phi, Psi, Vb)]
+    gd = g.to(DEV).requires_grad_(True) if g is not None else None
+    out = A.smat_attention(*xs, spec_d, chunk=C, g=gd, long_range=lrs)
+    (out * w.to(DEV)).sum().backward()
+    got = [x.grad.cpu() for x in xs] + ([gd.grad.cpu()] if gd is not None else [])
+    ys = [t.double().requires_grad_(True) for t in (Phi, Psi, Vb)]
+    g64 = g.double().requires_grad_(True) if g is not None else None
+    ref = O.smat_attention(*ys, spec, chunk=C, g=g64, long_range=lrs)
+    (ref * w.double()).sum().backward()
+    want = [y.grad for y in ys] + ([g64.grad] if g64 is not None else [])
+    assert _rel(out.detach().cpu(), ref.detach()) < (1e-4 if lr == "subtractive" else 1e-5)
+    tol = 1e-4 if lr == "subtractive" else 1e-5
+    for name, a, b in zip(("dPhi", "dPsi", "dVb", "dg"), got, want):
+        e = _rel(a, b)
+        _say(f"  {name}: {e:.2e}")
+        assert torch.isfinite(a).all() and e < tol, name
+
+
 @pytest.mark.parametrize("T,n,p,with_y,odt", [(300, 128, 65, True, torch.float32),
                                                (256, 0, 65, True, torch.float32),
                                                (256, 256, 129, False, torch.float32),
