@@ -88,6 +88,10 @@ def parse():
     ap.add_argument("--train-only", action="store_true",
                     help="time the training steps alone (for profiling): no prefill, decode, "
                          "CPU baseline or JSON line")
+    ap.add_argument("--qkv-only", action="store_true",
+                    help="time the path from q, k, v alone at --T / --d (for profiling): "
+                         "featurise + smat_attention, then smat_attention_fused, "
+                         "--kernel-reps calls each; no JSON line")
     ap.add_argument("--decode-steps", type=int, default=4096)
     ap.add_argument("--no-rows", action="store_true",
                     help="skip the per-T / d = 1 prefill rows")
@@ -247,6 +251,36 @@ def fused_rows(args):
         del Q, K, V
         torch.cuda.empty_cache()
     return rows
+
+
+def qkv_bench(args):
+    """The path from q, k, v at one (T, d): featurise + smat_attention, then
+    smat_attention_fused, ``--kernel-reps`` calls each after 3 warm-up calls,
+    bracketed by device synchronisations (inputs as in :func:`fused_rows`)."""
+    import torch
+    from smat_attention_amd import attention as A
+    from smat_attention_amd.mask import build_mask
+    nb, hd, T, reps = args.heads, args.head_dim, args.T, args.kernel_reps
+    dev = torch.device("cuda:0")
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(T + 7)
+    Q = torch.randn(nb, T, hd, device=dev, generator=g).to(bf)
+    K = (torch.randn(nb, T, hd, device=dev, generator=g) * hd ** -0.5).to(bf)
+    V = torch.randn(nb, T, hd, device=dev, generator=g).to(bf)
+    phi = A.make_phi(hd, hd, device=dev, dtype=bf, seed=0)
+    spec = A.to_device(build_mask(T, args.d, chunk=128), dev)
+    for name, fn in (("featurise + smat_attention",
+                      lambda: A.smat_attention(*A.featurise(Q, K, V, phi), spec)),
+                     ("smat_attention_fused", lambda: A.smat_attention_fused(Q, K, V, phi, spec))):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        log(f"[bench] q,k,v T={T} d={args.d} {name}: "
+            f"{(time.perf_counter() - t0) / reps * 1e3:.3f} ms")
 
 
 class Events:
@@ -612,6 +646,9 @@ def main():
     if args.train_only:
         for d in (2, 3):
             log(f"[bench] train step d={d}: {train_step_bench(d, max(3, args.kernel_reps // 2))}")
+        return
+    if args.qkv_only:
+        qkv_bench(args)
         return
     nb, T, hd = args.heads, args.T, args.head_dim
     r, p = hd, hd + 1

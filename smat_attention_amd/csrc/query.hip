@@ -30,7 +30,7 @@ constexpr int kMT = kRowsPerWG / 16;
 // p <= 144.  Narrow (2, 5): r <= 64, p <= 80, half the accumulators and
 // fragments, for head_dim 64; (3, 5) for contractions over head_dim + 1
 // columns (r <= 96).
-template <typename In, int kRK, int kNCT>
+template <typename In, int kRK, int kNCT, bool kLoop>
 __global__ __launch_bounds__(qy::kThreads) void query_kernel(
     const In* __restrict__ phi, const float* __restrict__ U, float* __restrict__ Y, int T_R, int B,
     int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st, int nrb, int vec_q,
@@ -42,21 +42,28 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
   const int rb = blockIdx.x - h * nrb;
   const int64_t b = blockIdx.y;
   const int lane = lane_id(), w = wave_id();
-  const int row16 = lane & 15, grp = lane >> 4;
+  const int row16_ = lane & 15, grp_ = lane >> 4;
   const int rk = (r + 31) >> 5;
   const int nct = (p + 15) >> 4;
   // rows of type h: i = h + k*B, k < cnt -- or, with a row table, the rows
   // rows[roffs[h] .. roffs[h+1])
   const int cnt = rows ? (int)(roffs[h + 1] - roffs[h]) : (h < T_R) ? (T_R - h + B - 1) / B : 0;
   const int32_t* hrows = rows ? rows + roffs[h] : nullptr;
-  // row blocks rb, rb + nrb, ...: a list longer than the grid was sized for
-  // is still covered
+  // Row block rb alone (kLoop false: the grid covers every block), or row
+  // blocks rb, rb + nrb, ... (kLoop true: a list longer than the grid was
+  // sized for is still covered)
   for (int rbi = rb; rbi * kRowsPerWG < cnt; rbi += nrb) {
     const int k0 = rbi * kRowsPerWG;
     const int nmt = min(kMT, (cnt - k0 + 15) / 16);
 
     const In* phib = phi + b * q_sb;
     const float* Uh = U + (b * B + h) * (int64_t)r * p;
+    // U's loads, their offsets and predicates do not depend on the row block.
+    // In the walk they are computed from opaque copies, so they stay inside it
+    // instead of being hoisted into registers for a second pass that only
+    // over-long lists take (63 VGPRs at r = 64 instead of 128).
+    int pu = p, ru = r, row16 = row16_, grp = grp_;
+    if constexpr (kLoop) asm volatile("" : "+s"(Uh), "+s"(pu), "+s"(ru), "+v"(row16), "+v"(grp));
 
     f32x4 acc[kMT][kCTPerWave];
 #pragma unroll
@@ -91,7 +98,7 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
         float u[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          u[e] = (c < p && a0 + e < r) ? Uh[(int64_t)(a0 + e) * p + c] : 0.f;
+          u[e] = (c < pu && a0 + e < ru) ? Uh[(int64_t)(a0 + e) * pu + c] : 0.f;
         if constexpr (Traits<In>::split) {
           Frag bh, bl;
 #pragma unroll
@@ -145,6 +152,7 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
         }
       }
     }
+    if constexpr (!kLoop) break;
   }
 }
 
@@ -343,15 +351,15 @@ static int launch_query(const void* phi, const float* U, float* Y, int nb, int T
   }
   const int vq = rows_vec_ok(phi, q_sb, q_st, sizeof(In));
   if (r <= 64 && p <= 80)
-    hipLaunchKernelGGL((query_kernel<In, 2, 5>), dim3((unsigned)gx, (unsigned)nb),
+    hipLaunchKernelGGL((query_kernel<In, 2, 5, false>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
                        q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   else if (r <= 96 && p <= 80)
-    hipLaunchKernelGGL((query_kernel<In, 3, 5>), dim3((unsigned)gx, (unsigned)nb),
+    hipLaunchKernelGGL((query_kernel<In, 3, 5, false>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
                        q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   else
-    hipLaunchKernelGGL((query_kernel<In, 4, 9>), dim3((unsigned)gx, (unsigned)nb),
+    hipLaunchKernelGGL((query_kernel<In, 4, 9, false>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
                        q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   return launch_status("smat_query");
@@ -371,15 +379,15 @@ static int launch_query_lists(const void* phi, const float* U, float* Y, const i
   if (gx == 0) return SMAT_OK;
   const int vq = rows_vec_ok(phi, 0, q_st, sizeof(In));
   if (r <= 64 && p <= 80)
-    hipLaunchKernelGGL((query_kernel<In, 2, 5>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
+    hipLaunchKernelGGL((query_kernel<In, 2, 5, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
                        stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
                        (int64_t)0, y_st, nrb, vq, rows, roffs);
   else if (r <= 96 && p <= 80)
-    hipLaunchKernelGGL((query_kernel<In, 3, 5>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
+    hipLaunchKernelGGL((query_kernel<In, 3, 5, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
                        stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
                        (int64_t)0, y_st, nrb, vq, rows, roffs);
   else
-    hipLaunchKernelGGL((query_kernel<In, 4, 9>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
+    hipLaunchKernelGGL((query_kernel<In, 4, 9, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
                        stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
                        (int64_t)0, y_st, nrb, vq, rows, roffs);
   return launch_status("smat_query_lists");
