@@ -82,6 +82,22 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Global loads the compiler does not track: their values may be used only
+// after a wait_vmcnt that covers them and an opaque redefinition (asm "+v"),
+// so no compiler-placed wait -- which would be vmcnt(0) with DMA loads and
+// stores pending beside them -- drains the DMA issued after them.  "memory"
+// keeps them in program order with the DMA, which the counts rely on.
+__device__ __forceinline__ f32x4 load4_untracked(const void* p) {
+  f32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=&v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ float load1_untracked(const void* p) {
+  float v;
+  asm volatile("global_load_dword %0, %1, off" : "=&v"(v) : "v"(p) : "memory");
+  return v;
+}
+
 // 8 bytes of a swizzled 256-byte row (t, chunk k, half h).
 template <typename In>
 __device__ __forceinline__ typename Traits<In>::half_frag row_half(const uint4* tile, int t, int k,
@@ -265,7 +281,7 @@ __device__ __forceinline__ f32x4 mma16(f32x4 c, f16x4 a, f16x4 b) {
 // tiles, phiF and psiF (feat_rows, W in registers), the key gate applied to
 // Psi.  A step's reads of phiF and psiF end before the barrier after its
 // state update, so the next step's features overwrite them safely.
-template <typename In, bool FEAT>
+template <typename In, bool FEAT, int NBUF, bool TERMS>
 __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
     const float* __restrict__ Sg, const float* __restrict__ Y, const float* __restrict__ gate,
@@ -279,6 +295,15 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   __shared__ __attribute__((aligned(16))) uint4 phi1[kTileChunks];
   __shared__ __attribute__((aligned(16))) uint4 psi1[kTileChunks];
   __shared__ __attribute__((aligned(16))) uint4 vb1[kVbTileChunks];
+  // NBUF = 3 (no feature map): a third buffer (160 768 bytes of LDS in all)
+  // keeps the rows of steps s + 1 and s + 2 in flight while step s computes.
+  // Y and the gate are then loaded untracked and waited for by count.
+  // TERMS = false compiles Y and the gate out (launches with neither): their
+  // pointers and flags would otherwise spill scalar registers every step.
+  static_assert(NBUF == 2 || (NBUF == 3 && !FEAT), "three buffers only without the feature map");
+  __shared__ __attribute__((aligned(16))) uint4 phi2[NBUF == 3 ? kTileChunks : 1];
+  __shared__ __attribute__((aligned(16))) uint4 psi2[NBUF == 3 ? kTileChunks : 1];
+  __shared__ __attribute__((aligned(16))) uint4 vb2[NBUF == 3 ? kVbTileChunks : 1];
   __shared__ __attribute__((aligned(16))) uint4 share[kStep * 8];
   // normaliser partials: wave w's share of H[t][p-1] at normp[norm_slot(t, w)]
   __shared__ __attribute__((aligned(16))) float normp[kStep * 8];
@@ -291,6 +316,9 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   // scalar branch.  (Under a vector condition the compiler masks EXEC around
   // an MFMA without branching past it, and MFMAs execute regardless of EXEC.)
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  // Eight waves: the DMA's loads 0..47 are then unconditional, and the
+  // compiler's count of loads issued after the Y loads is exact.
+  __builtin_assume(w >= 0 && w < 8);
   const int lane = lane_id();
   const int r16 = lane & 15, g = lane >> 4;
 
@@ -309,8 +337,8 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   const In* phib = phi + b * a.q_sb;
   const In* psib = psi + b * a.k_sb;
   const In* vbb = vb + b * a.v_sb;
-  const float* Yb = Y ? Y + b * a.y_sb : nullptr;
-  const float* gb = gate ? gate + b * a.g_sb : nullptr;
+  const float* Yb = (TERMS && Y) ? Y + b * a.y_sb : nullptr;
+  const float* gb = (TERMS && gate) ? gate + b * a.g_sb : nullptr;
   float* outb = out + b * a.o_sb;
   const float* Sb = Sg + ((int64_t)b * gridDim.x + grp) * (int64_t)128 * a.p;
 
@@ -342,6 +370,8 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     const float v8 = Sb[(int64_t)(16 * w + 4 * g + i) * a.p + (c8 < a.p ? c8 : 0)];
     accS8[i] = c8 < a.p ? v8 : 0.f;
   }
+  if (NBUF == 3 && nsteps > 1)
+    issue_step<In, FEAT>(phi1, psi1, vb1, phib, psib, vbb, tk0 + kStep, a, w, dmo);
   // Consume the state loads here, so that no wait for them (which would also
   // wait for the step DMA issued after them) is placed inside the loop.
 #pragma unroll
@@ -350,9 +380,9 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 
   auto step = [&](auto BUFC, int s) {
     constexpr int BUF = decltype(BUFC)::value;
-    const uint4* tphi = FEAT ? phiF : BUF ? phi1 : phi0;
-    const uint4* tpsi = FEAT ? psiF : BUF ? psi1 : psi0;
-    const uint4* tvb = BUF ? vb1 : vb0;
+    const uint4* tphi = FEAT ? phiF : BUF == 2 ? phi2 : BUF ? phi1 : phi0;
+    const uint4* tpsi = FEAT ? psiF : BUF == 2 ? psi2 : BUF ? psi1 : psi0;
+    const uint4* tvb = BUF == 2 ? vb2 : BUF ? vb1 : vb0;
     const int64_t ts = tk0 + (int64_t)s * kStep;
     // An opaque copy of the lane index per step: the LDS addresses derived
     // from it are recomputed inside the step instead of being hoisted out of
@@ -366,10 +396,22 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) hv[tt] = hb ? to_f32(hb[ts + 16 * tt + r16]) : 1.f;
     }
-    if (s + 1 < nsteps) {
+    static_assert(kLoads / 8 == 6 && kLoads % 8 == 1, "seven loads on wave 0, six on the rest");
+    if constexpr (NBUF == 3) {
+      // Issued after this step's DMA: the previous step's output stores and the
+      // next step's DMA, seven loads on wave 0 and six on the rest.  Loads
+      // complete in order, so waiting down to that many lands this step's rows.
+      if (s + 1 < nsteps) {
+        if (w == 0)
+          wait_vmcnt<7>();
+        else
+          wait_vmcnt<6>();
+      } else {
+        wait_vmcnt<0>();
+      }
+    } else if (s + 1 < nsteps) {
       issue_step<In, FEAT>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib,
                            vbb, ts + kStep, a, w, dmo);
-      static_assert(kLoads / 8 == 6 && kLoads % 8 == 1, "seven loads on wave 0, six on the rest");
       // the gate loads (issued first) are older than this step's six DMA loads
       if (!FEAT && w == 0)
         wait_vmcnt<7>();
@@ -387,7 +429,26 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
       lds_barrier();    // the step's Phi and Psi tiles are complete
     }
     YRegs yr;
-    issue_y(yr, Yb, gb, Sb, ts, a, rof, lane);
+    if constexpr (NBUF == 2) issue_y(yr, Yb, gb, Sb, ts, a, rof, lane);
+    // Three buffers: the step's Y rows and gates, untracked; the only vector
+    // memory issued after them before (e) is the DMA of step s + 2.
+    const bool rec = Yb != nullptr && ts >= a.n;
+    f32x4 ya[4];
+    float y8a[4], ga[4];
+    if constexpr (NBUF == 3) {
+      if (rec) {
+        const char* yb = reinterpret_cast<const char*>(Yb + (ts - a.n) * a.y_st);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          ya[tt] = load4_untracked(yb + rof.y[tt]);
+          y8a[tt] = load1_untracked(yb + rof.y[tt] + rof.y8);
+        }
+      }
+      if (gb) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) ga[tt] = load1_untracked(gb + ts + 16 * tt + r16);
+      }
+    }
 
     // (a) this wave's share of the causal score tiles A^T = Psi Phi^T
     //     entries 0..9: (ut, tt) with ut <= tt; 10, 11: zero tiles (1,0), (3,2)
@@ -422,6 +483,17 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
         char* p = reinterpret_cast<char*>(share + t * 8 + (k ^ swz8(t))) + 8 * (g & 1);
         *reinterpret_cast<Half*>(p) = hv;
       }
+    }
+
+    // Three buffers: step s + 2's rows go to the buffer step s - 1 used, free
+    // since that step's last barrier.  Issued after the score reads: before
+    // them, the compiler waits for the whole DMA in one of the three steps.
+    if constexpr (NBUF == 3) {
+      constexpr int NB = (BUF + 2) % 3;
+      if (s + 2 < nsteps)
+        issue_step<In, FEAT>(NB == 2 ? phi2 : NB ? phi1 : phi0, NB == 2 ? psi2 : NB ? psi1 : psi0,
+                             NB == 2 ? vb2 : NB ? vb1 : vb0, phib, psib, vbb, ts + 2 * kStep, a,
+                             w, dmo);
     }
 
     // (b) O^T = S^T Phi^T with the state before this step; the normaliser
@@ -524,7 +596,22 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     lds_barrier();
 
     // (e) long-range term, normalise, store four columns per lane per row tile
-    const bool rec = Yb != nullptr && ts >= a.n;
+    if constexpr (NBUF == 3) {
+      if (rec || gb) {
+        // everything issued after the Y and gate loads: step s + 2's DMA
+        if (s + 2 < nsteps) {
+          if (w == 0)
+            wait_vmcnt<7>();
+          else
+            wait_vmcnt<6>();
+        } else {
+          wait_vmcnt<0>();
+        }
+        asm volatile("" : "+v"(ya[0]), "+v"(ya[1]), "+v"(ya[2]), "+v"(ya[3]), "+v"(y8a[0]),
+                     "+v"(y8a[1]), "+v"(y8a[2]), "+v"(y8a[3]));
+        asm volatile("" : "+v"(ga[0]), "+v"(ga[1]), "+v"(ga[2]), "+v"(ga[3]));
+      }
+    }
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const int t = 16 * tt + r16;
@@ -537,13 +624,22 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
       o.z = accO[tt][2];
       o.w = accO[tt][3];
       if (rec) {
-        den += yr.y8[tt];
-        o.x += yr.y[tt].x;
-        o.y += yr.y[tt].y;
-        o.z += yr.y[tt].z;
-        o.w += yr.y[tt].w;
+        if constexpr (NBUF == 3) {
+          den += y8a[tt];
+          o.x += ya[tt][0];
+          o.y += ya[tt][1];
+          o.z += ya[tt][2];
+          o.w += ya[tt][3];
+        } else {
+          den += yr.y8[tt];
+          o.x += yr.y[tt].x;
+          o.y += yr.y[tt].y;
+          o.z += yr.y[tt].z;
+          o.w += yr.y[tt].w;
+        }
       }
-      const float inv = yr.gv[tt] / den;
+      const float num = NBUF == 3 ? (gb ? ga[tt] : 1.f) : yr.gv[tt];   // the gate (1 without)
+      const float inv = num / den;
       o.x *= inv;
       o.y *= inv;
       o.z *= inv;
@@ -552,9 +648,17 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     }
   };
 
-  for (int s = 0; s < nsteps; s += 2) {
-    step(std::integral_constant<int, 0>{}, s);
-    if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+  if constexpr (NBUF == 3) {
+    for (int s = 0; s < nsteps; s += 3) {
+      step(std::integral_constant<int, 0>{}, s);
+      if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+      if (s + 2 < nsteps) step(std::integral_constant<int, 2>{}, s + 2);
+    }
+  } else {
+    for (int s = 0; s < nsteps; s += 2) {
+      step(std::integral_constant<int, 0>{}, s);
+      if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+    }
   }
 }
 
@@ -854,18 +958,34 @@ bool scan_stream_ok(int dtype, const void* phi, const void* psi, const void* vb,
   return variant(SMAT_VARIANT_SCAN) == 0;
 }
 
+template <typename In, bool FEAT>
+static void scan_stream_kernel_launch(const void* phi, const void* psi, const void* vb,
+                                      const float* Sg, const float* Y, const float* gate,
+                                      float* out, dim3 grid, const ScanArgs& a, const FeatArgs& fa,
+                                      hipStream_t stream) {
+  const In* q = (const In*)phi;
+  const In* k = (const In*)psi;
+  const In* v = (const In*)vb;
+  if constexpr (FEAT)
+    hipLaunchKernelGGL((scan_stream_kernel<In, true, 2, true>), grid, dim3(ss::kThreads), 0,
+                       stream, q, k, v, Sg, Y, gate, out, a, fa);
+  else if (Y || gate)
+    hipLaunchKernelGGL((scan_stream_kernel<In, false, 3, true>), grid, dim3(ss::kThreads), 0,
+                       stream, q, k, v, Sg, Y, gate, out, a, fa);
+  else
+    hipLaunchKernelGGL((scan_stream_kernel<In, false, 3, false>), grid, dim3(ss::kThreads), 0,
+                       stream, q, k, v, Sg, Y, gate, out, a, fa);
+}
+
 template <bool FEAT>
 static int scan_stream_go(int dtype, const void* phi, const void* psi, const void* vb,
                           const float* Sg, const float* Y, const float* gate, float* out, int nb,
                           int ng, const ScanArgs& a, const FeatArgs& fa, hipStream_t stream) {
   dim3 grid((unsigned)ng, (unsigned)nb);
   if (dtype == SMAT_BF16)
-    hipLaunchKernelGGL((scan_stream_kernel<bf16, FEAT>), grid, dim3(ss::kThreads), 0, stream,
-                       (const bf16*)phi, (const bf16*)psi, (const bf16*)vb, Sg, Y, gate, out, a,
-                       fa);
+    scan_stream_kernel_launch<bf16, FEAT>(phi, psi, vb, Sg, Y, gate, out, grid, a, fa, stream);
   else
-    hipLaunchKernelGGL((scan_stream_kernel<f16, FEAT>), grid, dim3(ss::kThreads), 0, stream,
-                       (const f16*)phi, (const f16*)psi, (const f16*)vb, Sg, Y, gate, out, a, fa);
+    scan_stream_kernel_launch<f16, FEAT>(phi, psi, vb, Sg, Y, gate, out, grid, a, fa, stream);
   return launch_status("smat_causal_scan");
 }
 
