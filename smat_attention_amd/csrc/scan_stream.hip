@@ -676,7 +676,19 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 // tok(row) = start + stride * (base + row), row < 64; wave 0 issues five
 // loads, the others four.
 // FEAT: K and V rows; the ninth Vb tile is constant, so 32 loads, four a wave.
-template <typename In, bool FEAT>
+// Token of term idx: LIST (mode 2) reads it from the item's column list; the
+// other modes compute it, with no index loads whose waits (vmcnt(0), placed by
+// the compiler at every join after them) would drain the DMA in flight.
+template <bool LIST>
+__device__ __forceinline__ int64_t gram_token_of(const GramItems& it, int item, int64_t start,
+                                                 int64_t stride, int idx) {
+  if constexpr (LIST)
+    return gram_token(it, item, start, stride, idx);
+  else
+    return start + (int64_t)idx * stride;
+}
+
+template <typename In, bool FEAT, bool LIST>
 __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* psib,
                                            const In* vbb, const GramItems& it, int item,
                                            int64_t start, int64_t stride, int base, int count,
@@ -691,7 +703,8 @@ __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* ps
       if (I < ss::kPhiLoads) {
         const int row = 4 * I + (lane >> 4);
         const int k = (lane & 15) ^ swz16(row);
-        const int64_t tok = gram_token(it, item, start, stride, base + row < count ? base + row : 0);
+        const int64_t tok =
+            gram_token_of<LIST>(it, item, start, stride, base + row < count ? base + row : 0);
         src = psib + tok * k_st + 8 * k;
         dst = dpsi + 64 * I;
       } else {
@@ -699,7 +712,8 @@ __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* ps
         const int li = I - ss::kPhiLoads;
         const int row = li < ss::kPhiLoads ? 4 * li + (lane >> 4) : lane;
         const int col = li < ss::kPhiLoads ? 8 * ((lane & 15) ^ swz16(row)) : 128;
-        const int64_t tok = gram_token(it, item, start, stride, base + row < count ? base + row : 0);
+        const int64_t tok =
+            gram_token_of<LIST>(it, item, start, stride, base + row < count ? base + row : 0);
         src = vbb + tok * v_st + col;
         dst = dvb + 64 * li;
       }
@@ -717,7 +731,7 @@ __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* ps
 // FEAT: psi and vb are K and V rows; each step's Psi tile is formed in place
 // from the DMA'd K tile (feat_rows, W in registers, two halves of 32 rows),
 // times the key gate.
-template <typename In, bool ONE, bool FEAT>
+template <typename In, bool ONE, bool FEAT, bool LIST>
 __global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_stream_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, float* __restrict__ G,
     float* __restrict__ G_last, GramItems it, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
@@ -735,6 +749,7 @@ __global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_str
   const int item = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  __builtin_assume(w >= 0 && w < 8);                 // eight waves
   int64_t start, stride;
   int count;
   gram_item(it, item, start, stride, count);
@@ -747,7 +762,7 @@ __global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_str
 #pragma unroll
   for (int at = 0; at < 8; ++at) accS[at] = zero4();
   if (nsteps > 0)
-    issue_gram<In, FEAT>(psi0, vb0, psib, vbb, it, item, start, stride, 0, count, k_st, v_st, w,
+    issue_gram<In, FEAT, LIST>(psi0, vb0, psib, vbb, it, item, start, stride, 0, count, k_st, v_st, w,
                          lane_id());
   Frag wa[4];
   const In* hb = nullptr;
@@ -771,11 +786,12 @@ __global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_str
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const int row = s * kStep + 16 * tt + r16;
-        hv[tt] = hb ? to_f32(hb[gram_token(it, item, start, stride, row < count ? row : 0)]) : 1.f;
+        hv[tt] = hb ? to_f32(hb[gram_token_of<LIST>(it, item, start, stride, row < count ? row : 0)])
+                    : 1.f;
       }
     }
     if (!ONE && s + 1 < nsteps) {
-      issue_gram<In, FEAT>(BUF ? psi0 : psi1, BUF ? vb0 : vb1, psib, vbb, it, item, start, stride,
+      issue_gram<In, FEAT, LIST>(BUF ? psi0 : psi1, BUF ? vb0 : vb1, psib, vbb, it, item, start, stride,
                            (s + 1) * kStep, count, k_st, v_st, w, lane);
       static_assert(kPhiLoads + kVbLoads == 33, "five loads on wave 0, four on the rest");
       // the gate loads (issued first) are older than this step's DMA loads
@@ -882,6 +898,32 @@ bool gram_stream_ok(int dtype, const void* psi, const void* vb, int r, int p, in
   return variant(SMAT_VARIANT_GRAM) == 0;
 }
 
+template <typename In, bool FEAT>
+static void gram_stream_kernel_launch(const void* psi, const void* vb, float* G, float* G_last,
+                                      const GramItems& it, dim3 grid, bool one, int p,
+                                      int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
+                                      int64_t g_sb, int64_t g_si, int64_t gl_sb,
+                                      const FeatArgs& fa, hipStream_t stream) {
+  const In* k = (const In*)psi;
+  const In* v = (const In*)vb;
+  const dim3 blk(ss::kThreads);
+  // the feature map runs for profiles and chunk groups only: no list form
+  if (!FEAT && it.mode == 2) {
+    if (one)
+      hipLaunchKernelGGL((gram_stream_kernel<In, true, false, true>), grid, blk, 0, stream, k, v,
+                         G, G_last, it, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb, fa);
+    else
+      hipLaunchKernelGGL((gram_stream_kernel<In, false, false, true>), grid, blk, 0, stream, k, v,
+                         G, G_last, it, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb, fa);
+  } else if (one) {
+    hipLaunchKernelGGL((gram_stream_kernel<In, true, FEAT, false>), grid, blk, 0, stream, k, v, G,
+                       G_last, it, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb, fa);
+  } else {
+    hipLaunchKernelGGL((gram_stream_kernel<In, false, FEAT, false>), grid, blk, 0, stream, k, v,
+                       G, G_last, it, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb, fa);
+  }
+}
+
 template <bool FEAT>
 static int gram_stream_go(int dtype, const void* psi, const void* vb, float* G, float* G_last,
                           const GramItems& it, int nitems, int nb, int p, int64_t k_sb,
@@ -897,25 +939,12 @@ static int gram_stream_go(int dtype, const void* psi, const void* vb, float* G, 
     if (nitems > it.N0) maxc = maxc > it.n_P ? maxc : it.n_P;
     one = maxc <= ss::kStep;
   }
-  if (dtype == SMAT_BF16) {
-    if (one)
-      hipLaunchKernelGGL((gram_stream_kernel<bf16, true, FEAT>), grid, dim3(ss::kThreads), 0,
-                         stream, (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st,
-                         v_sb, v_st, g_sb, g_si, gl_sb, fa);
-    else
-      hipLaunchKernelGGL((gram_stream_kernel<bf16, false, FEAT>), grid, dim3(ss::kThreads), 0,
-                         stream, (const bf16*)psi, (const bf16*)vb, G, G_last, it, p, k_sb, k_st,
-                         v_sb, v_st, g_sb, g_si, gl_sb, fa);
-  } else {
-    if (one)
-      hipLaunchKernelGGL((gram_stream_kernel<f16, true, FEAT>), grid, dim3(ss::kThreads), 0,
-                         stream, (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st,
-                         v_sb, v_st, g_sb, g_si, gl_sb, fa);
-    else
-      hipLaunchKernelGGL((gram_stream_kernel<f16, false, FEAT>), grid, dim3(ss::kThreads), 0,
-                         stream, (const f16*)psi, (const f16*)vb, G, G_last, it, p, k_sb, k_st,
-                         v_sb, v_st, g_sb, g_si, gl_sb, fa);
-  }
+  if (dtype == SMAT_BF16)
+    gram_stream_kernel_launch<bf16, FEAT>(psi, vb, G, G_last, it, grid, one, p, k_sb, k_st, v_sb,
+                                          v_st, g_sb, g_si, gl_sb, fa, stream);
+  else
+    gram_stream_kernel_launch<f16, FEAT>(psi, vb, G, G_last, it, grid, one, p, k_sb, k_st, v_sb,
+                                         v_st, g_sb, g_si, gl_sb, fa, stream);
   return launch_status(who);
 }
 
@@ -935,6 +964,10 @@ int gram_stream_launch_feat(int dtype, const void* k, const void* v, float* G, f
                             int64_t gl_sb, const FeatArgs& fa, hipStream_t stream,
                             const char* who) {
   if (nitems == 0 || nb == 0) return SMAT_OK;
+  if (it.mode == 2) {                  // compiled for profiles and chunk groups only
+    set_error("%s: the feature map is not fused into list Gram sums", who);
+    return SMAT_EUNSUPPORTED;
+  }
   return gram_stream_go<true>(dtype, k, v, G, G_last, it, nitems, nb, 129, k_sb, k_st, v_sb, v_st,
                               g_sb, g_si, gl_sb, fa, stream, who);
 }
