@@ -299,40 +299,52 @@ static int launch_plane(const float* F, const float* F_glob, const int* code, in
 }
 
 // ---------------------------------------------------------------------------
-// Wave-per-direction kernel (d = 3): persistent, one line group per wave
+// Line-group kernel (d = 3): persistent, two line groups per wave
 // ---------------------------------------------------------------------------
 
-// ds_read_b128 serves a 32-lane half of a wave at the full rate when both of its
-// sixteen-lane rows read sixteen consecutive 16-byte units that start at the
-// same offset modulo 16 units; rows that start at different offsets take about
-// twice as long.  The plane kernel above hands its rows to different lines, so
-// most of its reads are of the slow kind.  Here a wave owns sixteen
-// consecutive lines b0 .. b0+15 of ONE direction m, and its four rows are the
-// four 16-byte planes of those lines (E = 16 floats): at step t every row reads
-// entries kCW*t + s_t + j, j = lane & 15, with one s_t = (b0 - m t) mod q for
-// the whole wave.  Columns are kCW = 56 entries apart (>= q + 15: the first 15
-// points of a column are stored again after its end, so the sixteen entries
-// never wrap).  Lane l of every row holds the offset of step c0 + l of the
-// current run of sixteen steps, and a step takes it with a DPP row broadcast
-// folded into the address add: one vector instruction besides the four sums.
-// Lines b >= q of the last group of a direction read in bounds and are not
-// stored.  Vertical lines (e = 0, the column x1 = b) read entry kCW*b + t + j
-// from lane j: lanes are kCW + 1 entries apart, an odd stride, so sixteen
-// distinct phases, and the steps are immediate offsets.
+// An item is one sequence's N0 x 16 slice of F (floats [e0, e0 + 16) of every
+// r*p row).  It sits in LDS as four planes of 16-byte entries (floats
+// [e0 + 4k, e0 + 4k + 4) in plane k), column by column: entry kCW*x1 + i of a
+// plane holds point (i mod q, x1) for i < q + 15, so the first 15 points of a
+// column appear again after its end and no run of sixteen consecutive entries
+// wraps.  The planes are kPlane entries apart, a multiple of sixteen, so the
+// same entry of two planes sits at the same bank phase.
 //
-// The panel (4 planes x kCW*q entries, 147 KB at q = 41) leaves no room for a
-// second one, so the workgroup is persistent and prefetches the next item's
-// panel into registers while it sums the current one: HBM latency stays off
-// the critical path without a second LDS buffer.
+// A sixteen-lane row owns sixteen consecutive lines b0 .. b0+15 of one
+// direction (a group) and one plane pair: rows 0 and 1 of a wave take group A
+// with planes (0, 1) and (2, 3), rows 2 and 3 group B, so the two rows of each
+// 32-lane half read the same entries of two planes -- the pattern ds_read_b128
+// serves at its full rate.  Lane j of a row reads, at step t,
+//   sloped line (m, b), points (b - m t mod q, t):  entry kCW*t + s_t + j,
+//       s_t = (b0 - m t) mod q, one value per row: sixteen consecutive entries,
+//       256 contiguous bytes, every bank once;
+//   vertical line b (the column x1 = b):  entry kCW*b + j + t, the column
+//       summed from a lane-dependent start; lanes kCW + 1 entries apart, an
+//       odd stride, so sixteen distinct 16-byte phases.
+// Either address is a lane part plus a row part.  Lane l of each row holds the
+// row part of step 16*run + l in ot[run], and a step broadcasts it within the
+// row (DPP) into the address add: one vector instruction, then two 16-byte
+// reads (the second plane of the pair is an immediate offset of the first) and
+// eight adds.  Steps are issued two at a time with three pairs in flight.
+// Lanes past q in a direction's last group read in bounds and store nothing.
+//
+// The panel (4 x kPlane entries, 147 KB) leaves no room for a second one, so
+// the workgroup is persistent and prefetches the next item's panel into
+// registers while it sums the current one.  Nothing in the summing loop may
+// wait on the vector memory counter, which counts those loads too: the kernel
+// fits 128 VGPRs without spilling (a spill reload waits for every load issued
+// before it), the chunk map is recomputed per item rather than kept live.
 namespace iw {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kE = 16;            // floats of r*p per item (four planes)
 constexpr int kPlanes = kE / 4;
 constexpr int kPF = 7;            // panel chunks each thread prefetches (N0 <= 1792)
-constexpr int kU = 8;             // steps issued together
-constexpr int kGroup = 16;        // lines per wave task
-constexpr int kCW = 56;           // entries per column: >= q + 15, even (see below)
+constexpr int kGroup = 16;        // lines per row
+constexpr int kCW = 56;           // entries per column: >= q + 15
+constexpr int kQMax = kCW - 15;   // largest q the layout holds
+constexpr int kPlane = (kCW * kQMax + 15) / 16 * 16;   // 2304 entries
+constexpr int kPlaneBytes = kPlane * 16;               // 36864: fits the 16-bit offset
 }  // namespace iw
 
 // Lane n of each sixteen-lane row of v, broadcast to the whole row (DPP row_newbcast).
@@ -341,90 +353,125 @@ __device__ __forceinline__ int row_bcast(int v) {
   return __builtin_amdgcn_update_dpp(0, v, 0x150 + N, 0xf, 0xf, false);
 }
 
-// Eight steps of a sloped line: step H + n reads the byte offset that lane H + n
-// of the row holds in otab.  The eight reads are issued together and waited for
-// once.
-template <int H>
-__device__ __forceinline__ void wave_steps8(float4& acc, const char* vb, int otab) {
-  float4 v[8];
-  v[0] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 0>(otab));
-  v[1] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 1>(otab));
-  v[2] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 2>(otab));
-  v[3] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 3>(otab));
-  v[4] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 4>(otab));
-  v[5] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 5>(otab));
-  v[6] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 6>(otab));
-  v[7] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 7>(otab));
-  __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0): one wait for the eight
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) add4(acc, v[u]);
+// x = (x_lo, y_lo), y = (x_hi, y_hi) over the 32-lane halves of the wave
+// (v_permlane32_swap).
+__device__ __forceinline__ void swap_halves(float& x, float& y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false,
+                                                  false);
+  x = __uint_as_float(r[0]);
+  y = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap_halves(int& x, int& y) {
+  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)y, false, false);
+  x = (int)r[0];
+  y = (int)r[1];
 }
 
-// Sixteen steps of a sloped line with the reads pipelined: four are in flight
-// while the previous four are summed (same registers as wave_steps8).
-template <int H>
-__device__ __forceinline__ void wave_read4(float4* v, const char* vb, int otab) {
-  v[0] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 0>(otab));
-  v[1] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 1>(otab));
-  v[2] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 2>(otab));
-  v[3] = *reinterpret_cast<const float4*>(vb + row_bcast<H + 3>(otab));
-}
-__device__ __forceinline__ void wave_add4(float4& acc, const float4* v) {
-  add4(acc, v[0]);
-  add4(acc, v[1]);
-  add4(acc, v[2]);
-  add4(acc, v[3]);
-}
-__device__ __forceinline__ void wave_steps16(float4& acc, const char* vb, int otab) {
-  float4 a[4], b[4];
-  wave_read4<0>(a, vb, otab);
-  wave_read4<4>(b, vb, otab);
-  __builtin_amdgcn_s_waitcnt(0xC47F);                // lgkmcnt(4): a has landed
-  __builtin_amdgcn_sched_barrier(0);
-  wave_add4(acc, a);
-  __builtin_amdgcn_sched_barrier(0);
-  wave_read4<8>(a, vb, otab);
-  __builtin_amdgcn_s_waitcnt(0xC47F);
-  __builtin_amdgcn_sched_barrier(0);
-  wave_add4(acc, b);
-  __builtin_amdgcn_sched_barrier(0);
-  wave_read4<12>(b, vb, otab);
-  __builtin_amdgcn_s_waitcnt(0xC47F);
-  __builtin_amdgcn_sched_barrier(0);
-  wave_add4(acc, a);
-  __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0)
-  __builtin_amdgcn_sched_barrier(0);
-  wave_add4(acc, b);
+// Step N: both planes of the pair at the lane part plus the row part of step N.
+template <int N>
+__device__ __forceinline__ void lg_issue(float4* v, const char* vb, const int* ot) {
+  const char* a = vb + row_bcast<N % 16>(ot[N / 16]);
+  v[0] = *reinterpret_cast<const float4*>(a);
+  v[1] = *reinterpret_cast<const float4*>(a + iw::kPlaneBytes);
 }
 
-// The steps H .. cnt-1 (cnt - H < 8) of a partial block.
-template <int H>
-__device__ __forceinline__ void wave_steps_tail(float4& acc, const char* vb, int otab, int cnt) {
-#define SMAT_TAIL_STEP(n) \
-  if (H + n < cnt) add4(acc, *reinterpret_cast<const float4*>(vb + row_bcast<H + n>(otab)));
-  SMAT_TAIL_STEP(0) SMAT_TAIL_STEP(1) SMAT_TAIL_STEP(2) SMAT_TAIL_STEP(3)
-  SMAT_TAIL_STEP(4) SMAT_TAIL_STEP(5) SMAT_TAIL_STEP(6)
-#undef SMAT_TAIL_STEP
+// Pair K of steps (2K, 2K + 1), into buffer K mod 3.
+template <int Q, int K>
+__device__ __forceinline__ void lg_issue_pair(float4 (&buf)[3][4], const char* vb, const int* ot) {
+  if constexpr (2 * K < Q) lg_issue<2 * K>(&buf[K % 3][0], vb, ot);
+  if constexpr (2 * K + 1 < Q) lg_issue<2 * K + 1>(&buf[K % 3][2], vb, ot);
 }
 
-static int64_t wave_plane_entries(int q) {
-  return ((int64_t)iw::kCW * q + 15) / 16 * 16;
+// The sums so far are materialised here and no memory access moves across:
+// without it the compiler sinks every add below every read, and the Q pairs of
+// reads in flight spill.
+__device__ __forceinline__ void lg_fence(float4& a0, float4& a1) {
+  asm volatile("" : "+v"(a0.x), "+v"(a0.y), "+v"(a0.z), "+v"(a0.w), "+v"(a1.x), "+v"(a1.y),
+               "+v"(a1.z), "+v"(a1.w)::"memory");
 }
+
+// Sum pair K (the compiler waits for its reads only), then issue pair K + 3
+// into the registers it frees; steps are summed in order 0 .. Q-1.
+template <int Q, int K>
+__device__ __forceinline__ void lg_pipe(float4& a0, float4& a1, float4 (&buf)[3][4],
+                                        const char* vb, const int* ot) {
+  if constexpr (2 * K < Q) {
+    if constexpr (K == 0) {
+      a0 = buf[0][0];
+      a1 = buf[0][1];
+    } else {
+      add4(a0, buf[K % 3][0]);
+      add4(a1, buf[K % 3][1]);
+    }
+    if constexpr (2 * K + 1 < Q) {
+      add4(a0, buf[K % 3][2]);
+      add4(a1, buf[K % 3][3]);
+    }
+    lg_fence(a0, a1);
+    __builtin_amdgcn_sched_barrier(0);
+    lg_issue_pair<Q, K + 3>(buf, vb, ot);
+    __builtin_amdgcn_sched_barrier(0);
+    lg_pipe<Q, K + 1>(a0, a1, buf, vb, ot);
+  }
+}
+
+// a0, a1 = the sums of a line's Q points in the two planes of the pair.
+template <int Q>
+__device__ __forceinline__ void lg_line_sums(float4& a0, float4& a1, const char* vb,
+                                             const int* ot) {
+  float4 buf[3][4];
+  lg_issue_pair<Q, 0>(buf, vb, ot);
+  lg_issue_pair<Q, 1>(buf, vb, ot);
+  lg_issue_pair<Q, 2>(buf, vb, ot);
+  __builtin_amdgcn_sched_barrier(0);
+  lg_pipe<Q, 0>(a0, a1, buf, vb, ot);
+}
+
+// Panel chunk u of thread tid: plane kx = (tid >> 4) & 3 and slot
+// ps = 16 * (wave + 16 u) + (tid & 15) in column-major point order
+// (x1 = ps / q, x0 = ps mod q), so the sixteen lanes of a row write sixteen
+// consecutive entries of one plane.  Its F offset in bytes (4 N0 rp < 2^32,
+// checked on the host) is 4 (x*rp + 4*kx) for the point x = x0*q + x1; its LDS
+// entry is kx*kPlane + kCW*x1 + x0, with copies at + q, + 2q, ... below W.
+template <int Q>
+struct LgChunk {
+  int entry, ncopy;
+  uint32_t src;
+  __device__ __forceinline__ LgChunk(int tid, int u, int64_t rp) {
+    constexpr int W = Q + 15;
+    const int kx = (tid >> 4) & 3;
+    const int ps = 16 * ((tid >> 6) + iw::kWaves * u) + (tid & 15);
+    const int x1 = ps / Q, x0 = ps - x1 * Q;
+    ncopy = ps < Q * Q ? (W - x0 + Q - 1) / Q : 0;
+    entry = kx * iw::kPlane + iw::kCW * x1 + x0;
+    src = 4u * ((uint32_t)(x0 * Q + x1) * (uint32_t)rp + 4u * kx);
+  }
+};
+
+static bool wave_kernel_fits(int q, int N0, int64_t rp) {
+  return q >= 2 && q <= iw::kQMax && N0 == q * q &&
+         (int64_t)N0 * iw::kPlanes <= (int64_t)iw::kPF * iw::kThreads &&
+         (int64_t)N0 * rp < (1ll << 30);
+}
+
 static int64_t wave_lds_bytes(int q) {
-  return iw::kPlanes * wave_plane_entries(q) * 16 + (((int64_t)q * (q + 1) * 2 + 15) & ~15);
+  return (int64_t)iw::kPlanes * iw::kPlane * 16 + (((int64_t)q * (q + 1) * 2 + 15) & ~15);
 }
 
-template <bool HasG>
+template <int Q, bool HasG>
 __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
-    int q, float* __restrict__ U, int N0, int B, int64_t rp, int nslices, int64_t total,
-    int64_t per_xcd, int plane) {
+    float* __restrict__ U, int B, int64_t rp, int nslices, int64_t total, int64_t per_xcd) {
   using namespace iw;
+  constexpr int q = Q;
+  constexpr int N0 = Q * Q;
+  constexpr int nlines = Q * (Q + 1);
+  constexpr int P = (Q + kGroup - 1) / kGroup;       // groups per direction
+  constexpr int G = (Q + 1) * P;                     // groups per item
+  constexpr int NT = (G + 1) / 2;                    // wave tasks (two groups) per item
+  constexpr int NR = (Q + 15) / 16;                  // runs of sixteen steps
   extern __shared__ float4 smem[];
-  const int W = q + 15;
-  const int nlines = q * (q + 1);
-  short* line_type = reinterpret_cast<short*>(smem + (size_t)kPlanes * plane);
+  short* line_type = reinterpret_cast<short*>(smem + (size_t)kPlanes * kPlane);
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wv = __builtin_amdgcn_readfirstlane(wave_id());
@@ -442,139 +489,117 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     if (c >= 0 && c < nlines) line_type[c] = (short)h;
   }
 
-  // Panel chunk u of this thread: point x = idx >> 2, plane k = idx & 3, stored
-  // at entry W*x1 + x0 of plane k and again every q entries up to W.
-  // Chunk u of this thread: plane kx = row of the lane, and slot
-  // ps = 16 * (wave + 16 u) + (lane & 15) in column-major point order
-  // (x1 = ps / q, x0 = ps mod q), so the sixteen lanes of a row write sixteen
-  // consecutive LDS entries of one plane.  Its F offset (N0 * rp < 2^31,
-  // checked on the host) is x*rp + 4*kx for the point x = x0*q + x1; its LDS
-  // entry and the number of copies (entries x0, x0 + q, ... < W) are packed as
-  // entry | copies << 24.
-  const int kx = (tid >> 4) & 3;
-  int dst[kPF], src[kPF];
-#pragma unroll
-  for (int u = 0; u < kPF; ++u) {
-    const int ps = 16 * ((tid >> 6) + kWaves * u) + (tid & 15);
-    const int x1 = ps / q, x0 = ps - x1 * q;
-    const int ncopy = ps < N0 ? (W - x0 + q - 1) / q : 0;
-    dst[u] = (kx * plane + kCW * x1 + x0) | (ncopy << 24);
-    src[u] = (x0 * q + x1) * (int)rp + 4 * kx;
-  }
   float4 pf[kPF];
+  // The chunk map is recomputed here on every call (tid passes through an
+  // empty asm so it is not hoisted out of the item loop and kept live).
+  // Sequences are taken last first: the pool writes F in sequence order, so
+  // the last sequences' rows are the ones still held by the memory-side cache.
+  const int64_t nbm1 = total / nslices - 1;
   auto prefetch = [&](int64_t item) {
-    const int64_t b = item / nslices;
-    const int64_t e0 = (item - b * nslices) * kE;
-    const float* Fb = F + b * (int64_t)N0 * rp + e0;
-    const bool in = e0 + 4 * kx < rp;
+    int t = tid;
+    asm volatile("" : "+v"(t));
+    const int64_t bi = item / nslices;
+    const int64_t b = nbm1 - bi;
+    const int64_t e0 = (item - bi * nslices) * kE;
+    const char* Fb = reinterpret_cast<const char*>(F + b * (int64_t)N0 * rp + e0);
+    const bool in = e0 + 4 * ((t >> 4) & 3) < rp;
 #pragma unroll
-    for (int u = 0; u < kPF; ++u)
-      pf[u] = ((dst[u] >> 24) > 0 && in) ? *reinterpret_cast<const float4*>(Fb + src[u])
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < kPF; ++u) {
+      const LgChunk<Q> ch(t, u, rp);
+      pf[u] = (ch.ncopy > 0 && in) ? *reinterpret_cast<const float4*>(Fb + ch.src)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   };
   prefetch(first);
 
-  const int j = lane & 15, kpl = lane >> 4;
+  // Row roles: group A or B of the wave's task, plane pair (0, 1) or (2, 3).
+  const int j = lane & 15;
+  const int gsel = lane >> 5;
+  const int pp = (lane >> 4) & 1;
+  const int splane = (pp << 1) | gsel;               // plane this lane stores (after swap_halves)
+  const char* pbase = reinterpret_cast<const char*>(smem) + (size_t)(2 * pp) * kPlaneBytes;
   const float inv_q = 1.0f / (float)q;
-  const int P = (q + kGroup - 1) / kGroup;           // groups per direction
-  const int G = (q + 1) * P;
-  const int dir0 = wv / P, part0 = wv - dir0 * P;
-  const int ddir = kWaves / P, dpart = kWaves - ddir * P;
-  const char* pbase = reinterpret_cast<const char*>(smem) + (size_t)kpl * plane * 16;
 
   for (int64_t item = first; item < end; item += nk) {
+    {
+      int t = tid;
+      asm volatile("" : "+v"(t));
 #pragma unroll
-    for (int u = 0; u < kPF; ++u) {
-      const int e = dst[u] & 0xffffff, nc = dst[u] >> 24;
-      for (int c = 0; c < nc; ++c) smem[e + c * q] = pf[u];
+      for (int u = 0; u < kPF; ++u) {
+        const LgChunk<Q> ch(t, u, rp);
+        for (int c = 0; c < ch.ncopy; ++c) smem[ch.entry + c * q] = pf[u];
+      }
     }
     lds_barrier();                                   // panel (and line table) complete
-    const int64_t b = item / nslices;
-    const int64_t e0 = (item - b * nslices) * kE;
-    const bool live = e0 + 4 * kpl < rp;
-    float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (HasG && live) g = *reinterpret_cast<const float4*>(Fg + b * rp + e0 + 4 * kpl);
+    const int64_t bi = item / nslices;
+    const int64_t b = nbm1 - bi;
+    const int64_t e0 = (item - bi * nslices) * kE;
     if (item + nk < end) prefetch(item + nk);        // lands while this item is summed
-    float* Ub = U + b * (int64_t)B * rp + e0 + 4 * kpl;
+    const bool live = e0 + 4 * splane < rp;          // rp % 4 == 0: whole planes
+    float* Ub = U + b * (int64_t)B * rp + e0 + 4 * splane;
 
-    // group grp = wv + kWaves*i is part `part` of direction `dir`; both are
-    // advanced without a division (kWaves = P*ddir + dpart)
-    int dir = dir0, part = part0;
-    for (int grp = wv; grp < G; grp += kWaves) {
-      const int b0 = part * kGroup;
-      const int bl = b0 + j;
-      const bool valid = bl < q;
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      int lc;
-      if (dir < q) {
-        // Step t reads entry kCW*t + s_t + j, s_t = (b0 + (q - m) t) mod q.  Lane l
-        // of every row holds the byte offset of step c0 + l of the current run of
-        // sixteen steps; each step broadcasts its lane within the row (DPP) into
-        // the address add, so a step costs one vector add besides the sums.
-        const int m = dir;
-        lc = (m + 1) * q + bl;
-        const char* vb = pbase + 16 * j;
-        // lane j: s = s_{c0+j}, advanced by d16 = -16m mod q per run
-        const int v = b0 + (q - m) * j;              // < 2^24: exact in float
-        int sj = v - q * (int)((float)v * inv_q);
-        sj += sj < 0 ? q : 0;
-        sj -= sj >= q ? q : 0;
-        const unsigned d16 = (unsigned)((16 * (q - m)) % q);
-        int colpart = 16 * kCW * j;
-        for (int c0 = 0; c0 < q; c0 += 16) {
-          const int otab = colpart + 16 * sj;
-          if (c0 + 16 <= q) {
-            wave_steps16(acc, vb, otab);
-          } else if (c0 + 8 <= q) {
-            wave_steps8<0>(acc, vb, otab);
-            if (c0 + 8 < q) wave_steps_tail<8>(acc, vb, otab, q - c0);
-          } else {
-            wave_steps_tail<0>(acc, vb, otab, q - c0);
-          }
-          const unsigned c = (unsigned)sj + d16;
-          sj = (int)min(c, c - (unsigned)q);
-          colpart += 16 * 16 * kCW;
+    for (int task = wv; task < NT; task += kWaves) {
+      const int grp = 2 * task + gsel;
+      const int dir = grp / P, part = grp - dir * P;
+      const int bl = part * kGroup + j;
+      const bool sloped = dir < q;
+      const bool valid = grp < G && bl < q;
+      // sloped: lane part 16 j; row part of step t = 16 (kCW t + s_t),
+      //   s_t = (b0 - m t) mod q, taken by lane l for t = 16 run + l.
+      // vertical (and the dead group of an odd G): lane part 16 (kCW col + j),
+      //   row part of step t = 16 t.
+      const int col = valid ? bl : (bl >= kGroup ? bl - kGroup : 0);
+      const char* vb = pbase + 16 * (sloped ? j : kCW * col + j);
+      int ot[NR];
+      {
+        const int m = sloped ? dir : 0;
+        const int v = part * kGroup + (q - m) * j;   // s_j for run 0 (small: exact in float)
+        int s = v - q * (int)((float)v * inv_q);
+        s += s < 0 ? q : 0;
+        s -= s >= q ? q : 0;
+        int d16 = (16 * (q - m)) % q;                // s advances by this per run
+        if (!sloped) {
+          s = 0;
+          d16 = 0;
         }
-      } else {
-        lc = bl;
-        const int col = valid ? bl : (bl >= kGroup ? bl - kGroup : 0);
-        const char* vb = pbase + 16 * (kCW * col + j);
-        int t = 0;
-        for (; t + kU <= q; t += kU) {
-          float4 v[kU];
+        const int cmul = sloped ? kCW : 1;
 #pragma unroll
-          for (int u = 0; u < kU; ++u) v[u] = *reinterpret_cast<const float4*>(vb + 16 * (t + u));
-          __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0)
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int u = 0; u < kU; ++u) add4(acc, v[u]);
+        for (int r = 0; r < NR; ++r) {
+          ot[r] = 16 * (cmul * (16 * r + j) + s);
+          const unsigned c = (unsigned)(s + d16);
+          s = (int)min(c, c - (unsigned)q);
         }
-        for (; t < q; ++t) add4(acc, *reinterpret_cast<const float4*>(vb + 16 * t));
       }
-      const int h = valid ? line_type[lc] : -1;
-      if (h >= 0 && live) {
-        if (HasG) add4(acc, g);
-        *reinterpret_cast<float4*>(Ub + (int64_t)h * rp) = acc;
-      }
-      part += dpart;
-      dir += ddir;
-      if (part >= P) {
-        part -= P;
-        ++dir;
+      float4 a0, a1;
+      lg_line_sums<Q>(a0, a1, vb, ot);
+      const int lc = sloped ? (dir + 1) * q + bl : bl;
+      int hA = valid ? line_type[lc] : -1, hB = hA;
+      // Rows 0-3 hold planes (0, 1) and (2, 3) of group A, then of group B, in
+      // (a0, a1).  One exchange of 32-lane halves leaves group A's four planes in
+      // a0 and group B's in a1 (rows 0-3: planes 0, 2, 1, 3), so each store
+      // writes a line's 64 bytes from four lanes of one instruction.
+      swap_halves(a0.x, a1.x);
+      swap_halves(a0.y, a1.y);
+      swap_halves(a0.z, a1.z);
+      swap_halves(a0.w, a1.w);
+      swap_halves(hA, hB);
+      if (live) {
+        if (HasG) {
+          const float4 g = *reinterpret_cast<const float4*>(Fg + b * rp + e0 + 4 * splane);
+          add4(a0, g);
+          add4(a1, g);
+        }
+        if (hA >= 0) *reinterpret_cast<float4*>(Ub + (int64_t)hA * rp) = a0;
+        if (hB >= 0) *reinterpret_cast<float4*>(Ub + (int64_t)hB * rp) = a1;
       }
     }
     lds_barrier();                                   // every wave is done with the panel
   }
 }
 
-static bool wave_kernel_fits(int q, int N0, int64_t rp) {
-  return q + 15 <= iw::kCW && (int64_t)N0 * 4 <= (int64_t)iw::kPF * iw::kThreads &&
-         (int64_t)N0 * rp < (1ll << 31) &&
-         wave_lds_bytes(q) <= inc::kPlaneLdsBudget && q >= 2 && q * (q + 1) < 32768;
-}
-
-static int launch_wave(const float* F, const float* F_glob, const int* code, int q, float* U,
-                       int nb, int N0, int B, int64_t rp, hipStream_t stream) {
+template <int Q>
+static int launch_wave_q(const float* F, const float* F_glob, const int* code, float* U, int nb,
+                         int B, int64_t rp, hipStream_t stream) {
   using namespace iw;
   const int nslices = (int)((rp + kE - 1) / kE);
   const int64_t total = (int64_t)nb * nslices;
@@ -584,20 +609,46 @@ static int launch_wave(const float* F, const float* F_glob, const int* code, int
   const int64_t per_xcd = (total + inc::kXCD - 1) / inc::kXCD;
   const int64_t per_xcd_wgs = std::max<int64_t>(1, std::min<int64_t>(ncu / inc::kXCD, per_xcd));
   const unsigned grid = (unsigned)(per_xcd_wgs * inc::kXCD);
-  const int plane = (int)wave_plane_entries(q);
-  const size_t smem = (size_t)wave_lds_bytes(q);
+  const size_t smem = (size_t)wave_lds_bytes(Q);
   static bool attr_set[2] = {false, false};
-  auto kern = F_glob ? incidence_wave_kernel<true> : incidence_wave_kernel<false>;
+  auto kern = F_glob ? incidence_wave_kernel<Q, true> : incidence_wave_kernel<Q, false>;
   if (!attr_set[F_glob ? 1 : 0]) {
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                               inc::kPlaneLdsBudget);
     attr_set[F_glob ? 1 : 0] = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, q, U, N0,
-                     B, rp, nslices, total, per_xcd, plane);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp,
+                     nslices, total, per_xcd);
   return launch_status("smat_incidence_plane");
 }
 
+// The line-group kernel is compiled for the prime field sizes it holds
+// (q <= 41); returns SMAT_EUNSUPPORTED for any other q.
+static int launch_wave(const float* F, const float* F_glob, const int* code, int q, float* U,
+                       int nb, int N0, int B, int64_t rp, hipStream_t stream) {
+  (void)N0;
+  switch (q) {
+#define SMAT_WAVE_Q(QV) \
+  case QV:              \
+    return launch_wave_q<QV>(F, F_glob, code, U, nb, B, rp, stream);
+    SMAT_WAVE_Q(2) SMAT_WAVE_Q(3) SMAT_WAVE_Q(5) SMAT_WAVE_Q(7) SMAT_WAVE_Q(11)
+    SMAT_WAVE_Q(13) SMAT_WAVE_Q(17) SMAT_WAVE_Q(19) SMAT_WAVE_Q(23) SMAT_WAVE_Q(29)
+    SMAT_WAVE_Q(31) SMAT_WAVE_Q(37) SMAT_WAVE_Q(41)
+#undef SMAT_WAVE_Q
+    default:
+      return SMAT_EUNSUPPORTED;
+  }
+}
+
+static bool wave_kernel_has_q(int q) {
+  switch (q) {
+    case 2: case 3: case 5: case 7: case 11: case 13: case 17: case 19: case 23: case 29:
+    case 31: case 37: case 41:
+      return true;
+    default:
+      return false;
+  }
+}
 // ---------------------------------------------------------------------------
 // L2 kernel
 // ---------------------------------------------------------------------------
@@ -759,7 +810,8 @@ int incidence_plane_dispatch(const float* F, const float* F_glob, const int* cod
               "(q=%d N0=%d rp=%lld)", q, N0, (long long)rp);
     return SMAT_EUNSUPPORTED;
   }
-  if (wave_kernel_fits(q, N0, rp) && variant(SMAT_VARIANT_INCIDENCE_PLANE) == 0)
+  if (wave_kernel_fits(q, N0, rp) && wave_kernel_has_q(q) &&
+      variant(SMAT_VARIANT_INCIDENCE_PLANE) == 0)
     return launch_wave(F, F_glob, code, q, U, nb, N0, B, rp, stream);
   // Two workgroups per CU at E = 8 (one stages its panel while the other sums)
   // measured ahead of one at E = 16; wider panels fall back to one per CU.

@@ -158,3 +158,131 @@ def test_fp32_rows_padded_to_4_floats_take_the_element_path(ncols, stride):
     over = max(end for _, end in _tile8_reads(ncols, stride, 4, rows)) - rows * stride * 4
     assert over == 16
     assert stride % 4 == 0 and not _vec8_ok(stride, stride * rows)
+
+
+# ---------------------------------------------------------------------------
+# the line-group incidence kernel's LDS addresses (incidence.hip, d = 3)
+# ---------------------------------------------------------------------------
+
+_KCW, _KPLANE, _KPF, _KTHREADS, _KPLANES = 56, 2304, 7, 1024, 4
+_WAVE_Q = (2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37, 41)
+
+
+def _wave_staging(q):
+    """Entries the staging writes, {entry index: point}, from the chunk map
+    (LgChunk: plane kx = (tid >> 4) & 3, slot ps = 16 (wave + 16 u) + (tid & 15),
+    x1 = ps // q, x0 = ps % q, copies at x0, x0 + q, ... < q + 15), and the
+    largest byte offset a prefetch read ends at, per unit of rp."""
+    W, N0 = q + 15, q * q
+    panel = {}
+    for tid in range(_KTHREADS):
+        kx = (tid >> 4) & 3
+        for u in range(_KPF):
+            ps = 16 * ((tid >> 6) + 16 * u) + (tid & 15)
+            if ps >= N0:
+                continue
+            x1, x0 = divmod(ps, q)
+            ncopy = (W - x0 + q - 1) // q
+            for c in range(ncopy):
+                e = kx * _KPLANE + _KCW * x1 + x0 + c * q
+                assert e not in panel
+                panel[e] = x0 * q + x1
+    return panel
+
+
+def _wave_reads(q):
+    """Yield (group, lane j, plane, step, entry) for every read the kernel makes,
+    with its address arithmetic: rows 0, 1 of a wave task take group 2 task with
+    plane pairs (0, 1), (2, 3) and rows 2, 3 group 2 task + 1; a row's lane l
+    computes ot[run] for step 16 run + l, and step t takes lane t % 16's value
+    of its own row."""
+    P = (q + 15) // 16
+    G = (q + 1) * P
+    NT = (G + 1) // 2
+    NR = (q + 15) // 16
+    for task in range(NT):
+        for gsel in range(2):
+            grp = 2 * task + gsel
+            dirn, part = divmod(grp, P)
+            sloped = dirn < q
+            m = dirn if sloped else 0
+            ot = {}
+            for l in range(16):
+                s = (part * 16 + (q - m) * l) % q if sloped else 0
+                d16 = (16 * (q - m)) % q if sloped else 0
+                cmul = _KCW if sloped else 1
+                for r in range(NR):
+                    ot[r, l] = 16 * (cmul * (16 * r + l) + s)
+                    c = (s + d16) % (1 << 32)
+                    s = min(c, (c - q) % (1 << 32))
+            for pp in range(2):
+                for j in range(16):
+                    bl = part * 16 + j
+                    valid = grp < G and bl < q
+                    col = bl if valid else (bl - 16 if bl >= 16 else 0)
+                    vb = 16 * (2 * pp * _KPLANE) + 16 * (j if sloped else _KCW * col + j)
+                    for t in range(q):
+                        addr = vb + ot[t // 16, t % 16]
+                        assert addr % 16 == 0
+                        for half in range(2):
+                            yield (grp, j, 2 * pp + half, pp, t,
+                                   (addr + half * 16 * _KPLANE) // 16)
+
+
+@pytest.mark.parametrize("q", _WAVE_Q)
+def test_line_group_incidence_reads_each_line_once_in_bounds(q):
+    """Emulates the line-group kernel for every field size it is compiled for:
+    every read lands on a staged entry inside the four planes (the line table
+    starts at 4 kPlane entries), and each stored line reads exactly its q points
+    once per plane -- the sloped line (m, b) the points (b - m t mod q, t), the
+    vertical line b the column x1 = b."""
+    panel = _wave_staging(q)
+    assert max(panel) < _KPLANES * _KPLANE
+    P = (q + 15) // 16
+    G = (q + 1) * P
+    got = {}
+    for grp, j, plane, pp, t, e in _wave_reads(q):
+        assert 0 <= e < _KPLANES * _KPLANE and e in panel
+        assert e // _KPLANE == plane
+        got.setdefault((grp, j, plane), []).append(panel[e])
+    for grp in range(G):
+        dirn, part = divmod(grp, P)
+        for j in range(16):
+            b = part * 16 + j
+            if b >= q:
+                continue
+            if dirn < q:
+                want = sorted(((b - dirn * t) % q) * q + t for t in range(q))
+            else:
+                want = sorted(x0 * q + b for x0 in range(q))
+            for plane in range(_KPLANES):
+                assert sorted(got[grp, j, plane]) == want
+
+
+@pytest.mark.parametrize("q", [29, 37, 41])
+def test_line_group_incidence_rows_read_one_bank_phase_each(q):
+    """At every step the sixteen lanes of a row read sixteen distinct 16-byte
+    phases (entry mod 16): consecutive entries for sloped lines, an odd stride
+    for vertical ones; and the two rows of a 32-lane half (the plane pairs of one
+    group) read at the same phases, the pattern ds_read_b128 serves at full rate."""
+    rows = {}
+    for grp, j, plane, pp, t, e in _wave_reads(q):
+        rows.setdefault((grp, plane - 2 * pp, pp, t), {})[j] = e
+    for (grp, half, pp, t), lanes in rows.items():
+        assert sorted(e % 16 for e in lanes.values()) == list(range(16))
+        other = rows[grp, half, 1 - pp, t]
+        assert all((lanes[j] - other[j]) % 16 == 0 for j in range(16))
+
+
+def test_line_group_incidence_half_exchange_stores_whole_lines():
+    """After the exchange of 32-lane halves (v_permlane32_swap of (a0, a1) and of
+    the line index) the first register holds group A's planes in rows 0-3 and
+    the second group B's, each row at the plane it stores (splane = 0, 2, 1, 3):
+    a line's four planes leave in one store instruction."""
+    a0 = [("A", 0), ("A", 2), ("B", 0), ("B", 2)]        # (group, plane) by row
+    a1 = [("A", 1), ("A", 3), ("B", 1), ("B", 3)]
+    x = a0[:2] + a1[:2]                                  # (x_lo, y_lo)
+    y = a0[2:] + a1[2:]                                  # (x_hi, y_hi)
+    splane = [((row & 1) << 1) | (row >> 1) for row in range(4)]
+    assert [p for _, p in x] == splane and [p for _, p in y] == splane
+    assert {g for g, _ in x} == {"A"} and {g for g, _ in y} == {"B"}
