@@ -427,31 +427,79 @@ __device__ __forceinline__ void lg_line_sums(float4& a0, float4& a1, const char*
   lg_pipe<Q, 0>(a0, a1, buf, vb, ot);
 }
 
+// x / Q and x mod Q for x below Max by a 24-bit multiply and a shift: M and S
+// are the smallest pair with floor(x M / 2^S) = floor(x / Q) over that range
+// (x M stays below 2^24, so v_mul_u32_u24 forms it).
+template <int Q, int Max>
+struct LgDiv {
+  static constexpr bool exact(unsigned M, int S) {
+    for (unsigned x = 0; x < (unsigned)Max; ++x)
+      if ((x * M) >> S != x / Q) return false;
+    return true;
+  }
+  static constexpr int shift() {
+    int S = 1;
+    while (!exact(((1u << S) + Q - 1) / Q, S)) ++S;
+    return S;
+  }
+  static constexpr int S = shift();
+  static constexpr unsigned M = ((1u << S) + Q - 1) / Q;
+  static_assert((unsigned long long)Max * M < (1ull << 24), "24-bit product");
+  __device__ __forceinline__ static unsigned div(unsigned x) { return __umul24(x, M) >> S; }
+  __device__ __forceinline__ static unsigned mod(unsigned x) { return x - Q * div(x); }
+};
+// b0 + (Q - m) j of a group's lane: below 16 P + 16 Q.
+template <int Q>
+using LgMod = LgDiv<Q, 16 * ((Q + 15) / 16) + 16 * Q>;
+
+// One group of the item: sixteen consecutive lines b0 .. b0+15 of direction
+// dir (dir < Q sloped with slope m = dir, dir = Q vertical; groups past the
+// last are dead and store nothing).  Lane j's row part at step t is built from
+// s_t = (s0 + qm t) mod Q with s0 = b0 for a sloped group (s_t = b0 - m t) and
+// s0 = qm = 0 for a vertical one; s advances by d16 over sixteen steps.  lcb + j
+// is lane j's line code (e*q + b).
+template <int Q>
+struct LgGroup {
+  static constexpr int P = (Q + 15) / 16;
+  static constexpr int G = (Q + 1) * P;
+  int b0, s0, qm, d16, lcb, nvalid, sloped;
+  __device__ __forceinline__ explicit LgGroup(int g) {
+    const int dir = g / P;
+    b0 = (g - dir * P) * 16;
+    sloped = dir < Q;
+    s0 = sloped ? b0 : 0;
+    qm = sloped ? Q - dir : 0;
+    d16 = (16 * qm) % Q;
+    lcb = sloped ? (dir + 1) * Q + b0 : b0;
+    nvalid = g < G ? min(16, Q - b0) : 0;
+  }
+  // Hide how the (scalar) fields were derived, so a per-lane choice between
+  // two groups selects the values instead of recomputing them per lane.
+  __device__ __forceinline__ void opaque() {
+    b0 = __builtin_amdgcn_readfirstlane(b0);
+    s0 = __builtin_amdgcn_readfirstlane(s0);
+    qm = __builtin_amdgcn_readfirstlane(qm);
+    d16 = __builtin_amdgcn_readfirstlane(d16);
+    lcb = __builtin_amdgcn_readfirstlane(lcb);
+    nvalid = __builtin_amdgcn_readfirstlane(nvalid);
+    sloped = __builtin_amdgcn_readfirstlane(sloped);
+  }
+};
+
 // Panel chunk u of thread tid: plane kx = (tid >> 4) & 3 and slot
 // ps = 16 * (wave + 16 u) + (tid & 15) in column-major point order
 // (x1 = ps / q, x0 = ps mod q), so the sixteen lanes of a row write sixteen
 // consecutive entries of one plane.  Its F offset in bytes (4 N0 rp < 2^32,
 // checked on the host) is 4 (x*rp + 4*kx) for the point x = x0*q + x1; its LDS
-// entry is kx*kPlane + kCW*x1 + x0, with copies at + q, + 2q, ... below W.
+// entry is kx*kPlane + kCW*x1 + x0, with copies at + q, + 2q, ... below q + 15.
 template <int Q>
-struct LgChunk {
-  int entry, ncopy;
-  uint32_t src;
-  __device__ __forceinline__ LgChunk(int tid, int u, int64_t rp) {
-    constexpr int W = Q + 15;
-    const int kx = (tid >> 4) & 3;
-    const int ps = 16 * ((tid >> 6) + iw::kWaves * u) + (tid & 15);
-    const int x1 = ps / Q, x0 = ps - x1 * Q;
-    ncopy = ps < Q * Q ? (W - x0 + Q - 1) / Q : 0;
-    entry = kx * iw::kPlane + iw::kCW * x1 + x0;
-    src = 4u * ((uint32_t)(x0 * Q + x1) * (uint32_t)rp + 4u * kx);
-  }
-};
+using LgSlot = LgDiv<Q, 16 * iw::kWaves * iw::kPF>;
 
-static bool wave_kernel_fits(int q, int N0, int64_t rp) {
+// Byte offsets into one sequence's F panel rows and U type rows are 32-bit.
+static bool wave_kernel_fits(int q, int N0, int B, int64_t rp) {
   return q >= 2 && q <= iw::kQMax && N0 == q * q &&
          (int64_t)N0 * iw::kPlanes <= (int64_t)iw::kPF * iw::kThreads &&
-         (int64_t)N0 * rp < (1ll << 30);
+         (int64_t)N0 * rp < (1ll << 30) && (int64_t)B * rp < (1ll << 30);
 }
 
 static int64_t wave_lds_bytes(int q) {
@@ -489,27 +537,33 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     if (c >= 0 && c < nlines) line_type[c] = (short)h;
   }
 
-  float4 pf[kPF];
-  // The chunk map is recomputed here on every call (tid passes through an
-  // empty asm so it is not hoisted out of the item loop and kept live).
   // Sequences are taken last first: the pool writes F in sequence order, so
   // the last sequences' rows are the ones still held by the memory-side cache.
   const int64_t nbm1 = total / nslices - 1;
-  auto prefetch = [&](int64_t item) {
-    int t = tid;
-    asm volatile("" : "+v"(t));
-    const int64_t bi = item / nslices;
-    const int64_t b = nbm1 - bi;
-    const int64_t e0 = (item - bi * nslices) * kE;
-    const char* Fb = reinterpret_cast<const char*>(F + b * (int64_t)N0 * rp + e0);
-    const bool in = e0 + 4 * ((t >> 4) & 3) < rp;
-#pragma unroll
-    for (int u = 0; u < kPF; ++u) {
-      const LgChunk<Q> ch(t, u, rp);
-      pf[u] = (ch.ncopy > 0 && in) ? *reinterpret_cast<const float4*>(Fb + ch.src)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+  // The chunk map of this thread (LgSlot) is recomputed on every item rather
+  // than kept live: ps0 passes through an empty asm so it is not hoisted.
+  const uint32_t ps0 = 16u * (uint32_t)(tid >> 6) + (uint32_t)(tid & 15);
+  const int kx = (tid >> 4) & 3;
+  const uint32_t rp4 = (uint32_t)rp * 4u;
+  float4 pf[kPF];
+  uint32_t src[kPF];
+  auto chunk_src = [&](uint32_t ps) {
+    const uint32_t x1 = LgSlot<Q>::div(ps), x0 = ps - Q * x1;
+    return __umul24(x0 * Q + x1, rp4) + 16u * kx;   // 4 (x rp + 4 kx)
   };
+  auto prefetch = [&](int64_t item) {
+    const int64_t bi = item / nslices;
+    const int64_t e0 = (item - bi * nslices) * kE;
+    const char* Fb = reinterpret_cast<const char*>(F + (nbm1 - bi) * (int64_t)N0 * rp + e0);
+    const bool in = e0 + 4 * kx < rp;
+#pragma unroll
+    for (int u = 0; u < kPF; ++u)
+      pf[u] = (ps0 + 256u * u < (uint32_t)N0 && in)
+                  ? *reinterpret_cast<const float4*>(Fb + src[u])
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+#pragma unroll
+  for (int u = 0; u < kPF; ++u) src[u] = chunk_src(ps0 + 256u * u);
   prefetch(first);
 
   // Row roles: group A or B of the wave's task, plane pair (0, 1) or (2, 3).
@@ -518,16 +572,24 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   const int pp = (lane >> 4) & 1;
   const int splane = (pp << 1) | gsel;               // plane this lane stores (after swap_halves)
   const char* pbase = reinterpret_cast<const char*>(smem) + (size_t)(2 * pp) * kPlaneBytes;
-  const float inv_q = 1.0f / (float)q;
+  const int lane16 = 16 * j, laneCW16 = 16 * kCW * j;
+  const uint32_t splane16 = 16u * splane;
 
   for (int64_t item = first; item < end; item += nk) {
     {
-      int t = tid;
-      asm volatile("" : "+v"(t));
+      uint32_t p0 = ps0;
+      asm volatile("" : "+v"(p0));
 #pragma unroll
       for (int u = 0; u < kPF; ++u) {
-        const LgChunk<Q> ch(t, u, rp);
-        for (int c = 0; c < ch.ncopy; ++c) smem[ch.entry + c * q] = pf[u];
+        const uint32_t ps = p0 + 256u * u;
+        const uint32_t x1 = LgSlot<Q>::div(ps), x0 = ps - Q * x1;
+        if (ps < (uint32_t)N0) {
+          float4* e = smem + (kx * kPlane + kCW * x1 + x0);
+#pragma unroll
+          for (int c = 0; c < (Q + 15 + Q - 1) / Q; ++c)
+            if (x0 + c * Q < (uint32_t)(Q + 15)) e[c * Q] = pf[u];
+        }
+        src[u] = __umul24(x0 * Q + x1, rp4) + 16u * kx;
       }
     }
     lds_barrier();                                   // panel (and line table) complete
@@ -536,44 +598,46 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     const int64_t e0 = (item - bi * nslices) * kE;
     if (item + nk < end) prefetch(item + nk);        // lands while this item is summed
     const bool live = e0 + 4 * splane < rp;          // rp % 4 == 0: whole planes
-    float* Ub = U + b * (int64_t)B * rp + e0 + 4 * splane;
+    // The U rows of this item start at Ubase; a lane stores at byte
+    // h * 4 rp + 16 splane of its type row h (below 2^32: checked on the host).
+    const char* Ubase = reinterpret_cast<const char*>(U + b * (int64_t)B * rp + e0);
 
     for (int task = wv; task < NT; task += kWaves) {
-      const int grp = 2 * task + gsel;
-      const int dir = grp / P, part = grp - dir * P;
-      const int bl = part * kGroup + j;
-      const bool sloped = dir < q;
-      const bool valid = grp < G && bl < q;
+      // The task's groups 2 task (rows 0-1) and 2 task + 1 (rows 2-3) are
+      // worked out on the scalar unit; each lane then takes its own.
+      LgGroup<Q> gA(2 * task), gB(2 * task + 1);
+      gA.opaque();                                   // select the values, not their
+      gB.opaque();                                   // derivation, per lane
+      const int b0 = gsel ? gB.b0 : gA.b0;
+      const int s0 = gsel ? gB.s0 : gA.s0;
+      const int qm = gsel ? gB.qm : gA.qm;
+      const int d16 = gsel ? gB.d16 : gA.d16;
+      const int lcb = gsel ? gB.lcb : gA.lcb;
+      const int nvalid = gsel ? gB.nvalid : gA.nvalid;
+      const bool sloped = (gsel ? gB.sloped : gA.sloped) != 0;
+      const bool valid = j < nvalid;
       // sloped: lane part 16 j; row part of step t = 16 (kCW t + s_t),
-      //   s_t = (b0 - m t) mod q, taken by lane l for t = 16 run + l.
-      // vertical (and the dead group of an odd G): lane part 16 (kCW col + j),
-      //   row part of step t = 16 t.
+      //   s_t = (b0 - m t) mod q = (b0 + qm t) mod q, taken by lane l for
+      //   t = 16 run + l.
+      // vertical (and the dead group of an odd G, s0 = qm = 0): lane part
+      //   16 (kCW col + j), row part of step t = 16 t, col clamped into the
+      //   columns for lanes past q.
+      const int bl = b0 + j;
       const int col = valid ? bl : (bl >= kGroup ? bl - kGroup : 0);
-      const char* vb = pbase + 16 * (sloped ? j : kCW * col + j);
+      const char* vb = pbase + lane16 + (sloped ? 0 : (int)__umul24(16 * kCW, col));
       int ot[NR];
       {
-        const int m = sloped ? dir : 0;
-        const int v = part * kGroup + (q - m) * j;   // s_j for run 0 (small: exact in float)
-        int s = v - q * (int)((float)v * inv_q);
-        s += s < 0 ? q : 0;
-        s -= s >= q ? q : 0;
-        int d16 = (16 * (q - m)) % q;                // s advances by this per run
-        if (!sloped) {
-          s = 0;
-          d16 = 0;
-        }
-        const int cmul = sloped ? kCW : 1;
+        int s = (int)LgMod<Q>::mod((unsigned)s0 + __umul24(qm, j));
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-          ot[r] = 16 * (cmul * (16 * r + j) + s);
+          ot[r] = (sloped ? 256 * kCW * r + laneCW16 : 256 * r + lane16) + 16 * s;
           const unsigned c = (unsigned)(s + d16);
           s = (int)min(c, c - (unsigned)q);
         }
       }
       float4 a0, a1;
       lg_line_sums<Q>(a0, a1, vb, ot);
-      const int lc = sloped ? (dir + 1) * q + bl : bl;
-      int hA = valid ? line_type[lc] : -1, hB = hA;
+      int hA = valid ? line_type[min(lcb + j, nlines - 1)] : -1, hB = hA;
       // Rows 0-3 hold planes (0, 1) and (2, 3) of group A, then of group B, in
       // (a0, a1).  One exchange of 32-lane halves leaves group A's four planes in
       // a0 and group B's in a1 (rows 0-3: planes 0, 2, 1, 3), so each store
@@ -589,8 +653,10 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
           add4(a0, g);
           add4(a1, g);
         }
-        if (hA >= 0) *reinterpret_cast<float4*>(Ub + (int64_t)hA * rp) = a0;
-        if (hB >= 0) *reinterpret_cast<float4*>(Ub + (int64_t)hB * rp) = a1;
+        if (hA >= 0)
+          *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + ((uint32_t)hA * rp4 + splane16)) = a0;
+        if (hB >= 0)
+          *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + ((uint32_t)hB * rp4 + splane16)) = a1;
       }
     }
     lds_barrier();                                   // every wave is done with the panel
@@ -810,7 +876,7 @@ int incidence_plane_dispatch(const float* F, const float* F_glob, const int* cod
               "(q=%d N0=%d rp=%lld)", q, N0, (long long)rp);
     return SMAT_EUNSUPPORTED;
   }
-  if (wave_kernel_fits(q, N0, rp) && wave_kernel_has_q(q) &&
+  if (wave_kernel_fits(q, N0, B, rp) && wave_kernel_has_q(q) &&
       variant(SMAT_VARIANT_INCIDENCE_PLANE) == 0)
     return launch_wave(F, F_glob, code, q, U, nb, N0, B, rp, stream);
   // Two workgroups per CU at E = 8 (one stages its panel while the other sums)

@@ -163,110 +163,147 @@ def test_fp32_rows_padded_to_4_floats_take_the_element_path(ncols, stride):
 # ---------------------------------------------------------------------------
 # the line-group incidence kernel's LDS addresses (incidence.hip, d = 3)
 # ---------------------------------------------------------------------------
+# The functions below restate the kernel's own integer arithmetic step by step
+# (LgDiv, LgSlot, LgGroup, the row parts ot[] and the lane parts vb), so a
+# change to that arithmetic must be mirrored here to keep the checks honest.
 
-_KCW, _KPLANE, _KPF, _KTHREADS, _KPLANES = 56, 2304, 7, 1024, 4
+_KCW, _KPLANE, _KPF, _KTHREADS, _KPLANES, _KWAVES = 56, 2304, 7, 1024, 4, 16
 _WAVE_Q = (2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37, 41)
+_U32 = 1 << 32
+
+
+def _lgdiv(q, xmax):
+    """(M, S) of LgDiv<q, xmax>: the smallest S with M = ceil(2^S / q) exact on
+    [0, xmax), and x M below 2^24 there."""
+    S = 1
+    while True:
+        M = ((1 << S) + q - 1) // q
+        if all((x * M) >> S == x // q for x in range(xmax)):
+            assert xmax * M < (1 << 24)
+            return M, S
+        S += 1
 
 
 def _wave_staging(q):
-    """Entries the staging writes, {entry index: point}, from the chunk map
-    (LgChunk: plane kx = (tid >> 4) & 3, slot ps = 16 (wave + 16 u) + (tid & 15),
-    x1 = ps // q, x0 = ps % q, copies at x0, x0 + q, ... < q + 15), and the
-    largest byte offset a prefetch read ends at, per unit of rp."""
-    W, N0 = q + 15, q * q
+    """Entries the staging writes, {entry index: point}: slot
+    ps = 16 (wave + 16 u) + (tid & 15) of plane kx = (tid >> 4) & 3, x1 = ps / q
+    by LgSlot's multiply-shift, copies at x0 + c q below q + 15; and every F
+    byte offset a prefetch reads, in units of 16 bytes at rp = 4."""
+    N0 = q * q
+    M, S = _lgdiv(q, 16 * _KWAVES * _KPF)
     panel = {}
     for tid in range(_KTHREADS):
         kx = (tid >> 4) & 3
         for u in range(_KPF):
             ps = 16 * ((tid >> 6) + 16 * u) + (tid & 15)
+            x1 = (ps * M) >> S
+            x0 = ps - q * x1
             if ps >= N0:
                 continue
-            x1, x0 = divmod(ps, q)
-            ncopy = (W - x0 + q - 1) // q
-            for c in range(ncopy):
-                e = kx * _KPLANE + _KCW * x1 + x0 + c * q
-                assert e not in panel
-                panel[e] = x0 * q + x1
+            assert (x1, x0) == divmod(ps, q)
+            for c in range((q + 15 + q - 1) // q):
+                if x0 + c * q < q + 15:
+                    e = kx * _KPLANE + _KCW * x1 + x0 + c * q
+                    assert e not in panel
+                    panel[e] = x0 * q + x1
     return panel
 
 
+def _group(q, g):
+    """LgGroup<q>(g): (b0, s0, qm, d16, lcb, nvalid, sloped)."""
+    P = (q + 15) // 16
+    G = (q + 1) * P
+    d = g // P
+    b0 = (g - d * P) * 16
+    sloped = d < q
+    s0 = b0 if sloped else 0
+    qm = q - d if sloped else 0
+    return b0, s0, qm, (16 * qm) % q, ((d + 1) * q + b0) if sloped else b0, \
+        (min(16, q - b0) if g < G else 0), sloped
+
+
 def _wave_reads(q):
-    """Yield (group, lane j, plane, step, entry) for every read the kernel makes,
-    with its address arithmetic: rows 0, 1 of a wave task take group 2 task with
-    plane pairs (0, 1), (2, 3) and rows 2, 3 group 2 task + 1; a row's lane l
-    computes ot[run] for step 16 run + l, and step t takes lane t % 16's value
+    """Yield (group, lane j, plane, pp, step, entry, line code) for every read the
+    kernel makes, by its own arithmetic: rows 0, 1 of a wave task take group
+    2 task (plane pairs (0, 1), (2, 3)), rows 2, 3 group 2 task + 1; a row's lane
+    l computes ot[run] for step 16 run + l, and step t takes lane t % 16's value
     of its own row."""
     P = (q + 15) // 16
     G = (q + 1) * P
     NT = (G + 1) // 2
     NR = (q + 15) // 16
+    M, S = _lgdiv(q, 16 * P + 16 * q)
     for task in range(NT):
         for gsel in range(2):
             grp = 2 * task + gsel
-            dirn, part = divmod(grp, P)
-            sloped = dirn < q
-            m = dirn if sloped else 0
+            b0, s0, qm, d16, lcb, nvalid, sloped = _group(q, grp)
             ot = {}
             for l in range(16):
-                s = (part * 16 + (q - m) * l) % q if sloped else 0
-                d16 = (16 * (q - m)) % q if sloped else 0
-                cmul = _KCW if sloped else 1
+                x = s0 + qm * l
+                s = x - q * ((x * M) >> S)
+                assert s == x % q
                 for r in range(NR):
-                    ot[r, l] = 16 * (cmul * (16 * r + l) + s)
-                    c = (s + d16) % (1 << 32)
-                    s = min(c, (c - q) % (1 << 32))
+                    ot[r, l] = (256 * _KCW * r + 16 * _KCW * l if sloped else 256 * r + 16 * l) \
+                        + 16 * s
+                    c = (s + d16) % _U32
+                    s = min(c, (c - q) % _U32)
             for pp in range(2):
                 for j in range(16):
-                    bl = part * 16 + j
-                    valid = grp < G and bl < q
+                    valid = j < nvalid
+                    bl = b0 + j
                     col = bl if valid else (bl - 16 if bl >= 16 else 0)
-                    vb = 16 * (2 * pp * _KPLANE) + 16 * (j if sloped else _KCW * col + j)
+                    vb = 16 * 2 * pp * _KPLANE + 16 * j + (0 if sloped else 16 * _KCW * col)
+                    lc = min(lcb + j, q * (q + 1) - 1)
                     for t in range(q):
                         addr = vb + ot[t // 16, t % 16]
                         assert addr % 16 == 0
                         for half in range(2):
                             yield (grp, j, 2 * pp + half, pp, t,
-                                   (addr + half * 16 * _KPLANE) // 16)
+                                   (addr + half * 16 * _KPLANE) // 16, lc if valid else None)
 
 
 @pytest.mark.parametrize("q", _WAVE_Q)
 def test_line_group_incidence_reads_each_line_once_in_bounds(q):
     """Emulates the line-group kernel for every field size it is compiled for:
     every read lands on a staged entry inside the four planes (the line table
-    starts at 4 kPlane entries), and each stored line reads exactly its q points
+    starts at 4 kPlane entries), each stored line reads exactly its q points
     once per plane -- the sloped line (m, b) the points (b - m t mod q, t), the
-    vertical line b the column x1 = b."""
+    vertical line b the column x1 = b -- and stores under its own line code."""
     panel = _wave_staging(q)
     assert max(panel) < _KPLANES * _KPLANE
     P = (q + 15) // 16
     G = (q + 1) * P
-    got = {}
-    for grp, j, plane, pp, t, e in _wave_reads(q):
+    got, codes = {}, {}
+    for grp, j, plane, pp, t, e, lc in _wave_reads(q):
         assert 0 <= e < _KPLANES * _KPLANE and e in panel
         assert e // _KPLANE == plane
         got.setdefault((grp, j, plane), []).append(panel[e])
+        codes[grp, j] = lc
     for grp in range(G):
         dirn, part = divmod(grp, P)
         for j in range(16):
             b = part * 16 + j
             if b >= q:
+                assert codes[grp, j] is None
                 continue
             if dirn < q:
                 want = sorted(((b - dirn * t) % q) * q + t for t in range(q))
+                assert codes[grp, j] == (dirn + 1) * q + b      # e = m + 1
             else:
                 want = sorted(x0 * q + b for x0 in range(q))
+                assert codes[grp, j] == b                       # e = 0
             for plane in range(_KPLANES):
                 assert sorted(got[grp, j, plane]) == want
 
 
-@pytest.mark.parametrize("q", [29, 37, 41])
+@pytest.mark.parametrize("q", [17, 29, 37, 41])
 def test_line_group_incidence_rows_read_one_bank_phase_each(q):
     """At every step the sixteen lanes of a row read sixteen distinct 16-byte
     phases (entry mod 16): consecutive entries for sloped lines, an odd stride
     for vertical ones; and the two rows of a 32-lane half (the plane pairs of one
     group) read at the same phases, the pattern ds_read_b128 serves at full rate."""
     rows = {}
-    for grp, j, plane, pp, t, e in _wave_reads(q):
+    for grp, j, plane, pp, t, e, lc in _wave_reads(q):
         rows.setdefault((grp, plane - 2 * pp, pp, t), {})[j] = e
     for (grp, half, pp, t), lanes in rows.items():
         assert sorted(e % 16 for e in lanes.values()) == list(range(16))
