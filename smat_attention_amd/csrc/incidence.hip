@@ -537,9 +537,6 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     if (c >= 0 && c < nlines) line_type[c] = (short)h;
   }
 
-  // Sequences are taken last first: the pool writes F in sequence order, so
-  // the last sequences' rows are the ones still held by the memory-side cache.
-  const int64_t nbm1 = total / nslices - 1;
   // The chunk map of this thread (LgSlot) is recomputed on every item rather
   // than kept live: ps0 passes through an empty asm so it is not hoisted.
   const uint32_t ps0 = 16u * (uint32_t)(tid >> 6) + (uint32_t)(tid & 15);
@@ -554,7 +551,7 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   auto prefetch = [&](int64_t item) {
     const int64_t bi = item / nslices;
     const int64_t e0 = (item - bi * nslices) * kE;
-    const char* Fb = reinterpret_cast<const char*>(F + (nbm1 - bi) * (int64_t)N0 * rp + e0);
+    const char* Fb = reinterpret_cast<const char*>(F + bi * (int64_t)N0 * rp + e0);
     const bool in = e0 + 4 * kx < rp;
 #pragma unroll
     for (int u = 0; u < kPF; ++u)
@@ -593,9 +590,8 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
       }
     }
     lds_barrier();                                   // panel (and line table) complete
-    const int64_t bi = item / nslices;
-    const int64_t b = nbm1 - bi;
-    const int64_t e0 = (item - bi * nslices) * kE;
+    const int64_t b = item / nslices;
+    const int64_t e0 = (item - b * nslices) * kE;
     if (item + nk < end) prefetch(item + nk);        // lands while this item is summed
     const bool live = e0 + 4 * splane < rp;          // rp % 4 == 0: whole planes
     // The U rows of this item start at Ubase; a lane stores at byte
