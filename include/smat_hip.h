@@ -58,7 +58,7 @@ const char* smat_version(void);
  *                                 head_dim-128 streaming query
  *   SMAT_VARIANT_INCIDENCE        L2 gather kernel instead of the LDS panel
  *   SMAT_VARIANT_INCIDENCE_PLANE  line-per-lane generated-line kernel instead
- *                                 of the wave-per-direction one
+ *                                 of the line-group one
  * Not for production use: a call changes the kernels of every later call.
  */
 #define SMAT_VARIANT_SCAN 0
