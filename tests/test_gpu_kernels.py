@@ -142,6 +142,29 @@ def test_incidence_generated_lines(T, n_P, rp, glob):
     assert _rel(U, ref) < 1e-6
 
 
+@pytest.mark.parametrize("T,chunk,q", [(64, 32, 5), (256, 32, 7), (768, 32, 11), (3072, 32, 13),
+                                     (6144, 32, 17), (12288, 32, 19), (16384, 32, 23),
+                                     (24576, 32, 29), (49152, 32, 31), (65536, 32, 37),
+                                     (131072, 32, 41)])
+@pytest.mark.parametrize("glob", [False, True])
+def test_incidence_line_groups_every_field(T, chunk, q, glob):
+    """The line-group kernel is compiled once per prime q: each instantiation the
+    masks reach against the fp64 oracle, at r*p = 20 (one whole and one partial
+    16-float slice), with and without the global channel."""
+    _say("incidence line groups", T, chunk, q, glob)
+    spec = A.to_device(build_mask(T, 3, chunk=chunk), DEV)
+    assert spec.q == q and spec.plane_code_t is not None
+    g = torch.Generator().manual_seed(q)
+    F = torch.randn(2, spec.N0, 4, 5, generator=g)
+    Fg = torch.randn(2, 4, 5, generator=g)
+    U = K.incidence_plane(F.to(DEV), spec.plane_code_t, spec.q,
+                          F_glob=Fg.to(DEV) if glob else None)
+    ref = O.apply_incidence(F.double(), spec)
+    if glob:
+        ref = ref + Fg.double().unsqueeze(1)
+    assert _rel(U, ref) < 1e-6
+
+
 def test_incidence_ragged_endpoint_csr():
     _say("incidence ragged (endpoint mask, CSR)")
     spec = A.to_device(build_mask(256, 8, chunk=8), DEV)
