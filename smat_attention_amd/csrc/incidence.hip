@@ -427,9 +427,9 @@ __device__ __forceinline__ void lg_line_sums(float4& a0, float4& a1, const char*
   lg_pipe<Q, 0>(a0, a1, buf, vb, ot);
 }
 
-// x / Q and x mod Q for x below Max by a 24-bit multiply and a shift: M and S
-// are the smallest pair with floor(x M / 2^S) = floor(x / Q) over that range
-// (x M stays below 2^24, so v_mul_u32_u24 forms it).
+// x / Q and x mod Q for x below Max by a multiply and a shift: M and S are the
+// smallest pair with floor(x M / 2^S) = floor(x / Q) over that range (where
+// x M stays below 2^24, v_mul_u32_u24 forms it; otherwise a 32-bit multiply).
 template <int Q, int Max>
 struct LgDiv {
   static constexpr bool exact(unsigned M, int S) {
@@ -444,8 +444,11 @@ struct LgDiv {
   }
   static constexpr int S = shift();
   static constexpr unsigned M = ((1u << S) + Q - 1) / Q;
-  static_assert((unsigned long long)Max * M < (1ull << 24), "24-bit product");
-  __device__ __forceinline__ static unsigned div(unsigned x) { return __umul24(x, M) >> S; }
+  static constexpr bool k24 = (unsigned long long)Max * M < (1ull << 24);
+  static_assert((unsigned long long)Max * M < (1ull << 32), "32-bit product");
+  __device__ __forceinline__ static unsigned div(unsigned x) {
+    return (k24 ? __umul24(x, M) : x * M) >> S;
+  }
   __device__ __forceinline__ static unsigned mod(unsigned x) { return x - Q * div(x); }
 };
 // b0 + (Q - m) j of a group's lane: below 16 P + 16 Q.
@@ -711,6 +714,261 @@ static bool wave_kernel_has_q(int q) {
       return false;
   }
 }
+
+// ---------------------------------------------------------------------------
+// Row-group kernel (d = 3, larger q): one line group per row, one plane a lane
+// ---------------------------------------------------------------------------
+
+// For 43 <= q <= 83 four 16-byte planes of the N0 points no longer fit in LDS
+// beside their column copies, so an item is one sequence's N0 x 4-float slice
+// of F: one plane, stored as in the line-group kernel (entry kCW*x1 + i holds
+// point (i mod q, x1) for i < q + 15, kCW = q + 15 rounded up to even).  Each
+// sixteen-lane row of a wave owns its own group of sixteen consecutive lines
+// of one direction and reads, at step t, the same entries as a line-group row
+// (sloped: kCW*t + s_t + j; vertical: kCW*b + j + t), one 16-byte read and
+// four adds a step after the DPP-broadcast address add.  The four rows of a
+// wave are four groups at different bank phases, which ds_read_b128 serves at
+// about half its full rate; the line-per-lane plane kernel it replaces also
+// paid three more vector instructions a step for each lane's own wrap.
+namespace ir {
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kE = 4;             // floats of r*p per item (one plane)
+constexpr int kPF = 7;            // panel chunks each thread prefetches (N0 <= 7168)
+constexpr int kQMin = 43, kQMax = 83;
+template <int Q>
+struct Shape {
+  static constexpr int kCW = (Q + 15 + 1) / 2 * 2;              // even: vertical stride odd
+  static constexpr int kEntries = (kCW * Q + 15) / 16 * 16;
+  static constexpr int kLdsBytes = kEntries * 16 + ((Q * (Q + 1) * 2 + 15) / 16) * 16;
+  static_assert(kLdsBytes <= 160 * 1024, "panel and line table fit the LDS");
+};
+}  // namespace ir
+
+// Step N: one plane at the lane part plus the row part of step N.
+template <int N>
+__device__ __forceinline__ void lr_issue(float4& v, const char* vb, const int* ot) {
+  v = *reinterpret_cast<const float4*>(vb + row_bcast<N % 16>(ot[N / 16]));
+}
+
+// Batch K of steps 4K .. 4K+3, into buffer K mod 3.
+template <int Q, int K>
+__device__ __forceinline__ void lr_issue_batch(float4 (&buf)[3][4], const char* vb, const int* ot) {
+  if constexpr (4 * K < Q) lr_issue<4 * K>(buf[K % 3][0], vb, ot);
+  if constexpr (4 * K + 1 < Q) lr_issue<4 * K + 1>(buf[K % 3][1], vb, ot);
+  if constexpr (4 * K + 2 < Q) lr_issue<4 * K + 2>(buf[K % 3][2], vb, ot);
+  if constexpr (4 * K + 3 < Q) lr_issue<4 * K + 3>(buf[K % 3][3], vb, ot);
+}
+
+__device__ __forceinline__ void lr_fence(float4& a) {
+  asm volatile("" : "+v"(a.x), "+v"(a.y), "+v"(a.z), "+v"(a.w)::"memory");
+}
+
+// Sum batch K (steps in order 0 .. Q-1), then issue batch K + 3 into its registers.
+template <int Q, int K>
+__device__ __forceinline__ void lr_pipe(float4& a, float4 (&buf)[3][4], const char* vb,
+                                        const int* ot) {
+  if constexpr (4 * K < Q) {
+    if constexpr (K == 0)
+      a = buf[0][0];
+    else
+      add4(a, buf[K % 3][0]);
+    if constexpr (4 * K + 1 < Q) add4(a, buf[K % 3][1]);
+    if constexpr (4 * K + 2 < Q) add4(a, buf[K % 3][2]);
+    if constexpr (4 * K + 3 < Q) add4(a, buf[K % 3][3]);
+    lr_fence(a);
+    __builtin_amdgcn_sched_barrier(0);
+    lr_issue_batch<Q, K + 3>(buf, vb, ot);
+    __builtin_amdgcn_sched_barrier(0);
+    lr_pipe<Q, K + 1>(a, buf, vb, ot);
+  }
+}
+
+template <int Q>
+__device__ __forceinline__ float4 lr_line_sum(const char* vb, const int* ot) {
+  float4 buf[3][4];
+  float4 a;
+  lr_issue_batch<Q, 0>(buf, vb, ot);
+  lr_issue_batch<Q, 1>(buf, vb, ot);
+  lr_issue_batch<Q, 2>(buf, vb, ot);
+  __builtin_amdgcn_sched_barrier(0);
+  lr_pipe<Q, 0>(a, buf, vb, ot);
+  return a;
+}
+
+// Slot ps of the panel: ps = 64 * (wave + 16 u) + lane, x1 = ps / q, x0 = ps mod q.
+template <int Q>
+using LrSlot = LgDiv<Q, 64 * ir::kWaves * ir::kPF>;
+
+static bool row_kernel_fits(int q, int N0, int B, int64_t rp) {
+  return q >= ir::kQMin && q <= ir::kQMax && N0 == q * q &&
+         (int64_t)N0 <= (int64_t)ir::kPF * ir::kThreads && (int64_t)N0 * rp < (1ll << 30) &&
+         (int64_t)B * rp < (1ll << 30);
+}
+
+template <int Q, bool HasG>
+__global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
+    const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
+    float* __restrict__ U, int B, int64_t rp, int nslices, int64_t total, int64_t per_xcd) {
+  using namespace ir;
+  typedef Shape<Q> Sh;
+  constexpr int q = Q;
+  constexpr int N0 = Q * Q;
+  constexpr int kCW = Sh::kCW;
+  constexpr int nlines = Q * (Q + 1);
+  constexpr int P = (Q + 15) / 16;                   // groups per direction
+  constexpr int G = (Q + 1) * P;                     // groups per item
+  constexpr int NT = (G + 3) / 4;                    // wave tasks (four groups) per item
+  constexpr int NR = (Q + 15) / 16;                  // runs of sixteen steps
+  extern __shared__ float4 smem[];
+  short* line_type = reinterpret_cast<short*>(smem + Sh::kEntries);
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wv = __builtin_amdgcn_readfirstlane(wave_id());
+
+  const int xcd = blockIdx.x % inc::kXCD;
+  const int64_t nk = gridDim.x / inc::kXCD;
+  const int64_t first = (int64_t)xcd * per_xcd + blockIdx.x / inc::kXCD;
+  const int64_t end = min<int64_t>(total, (int64_t)(xcd + 1) * per_xcd);
+  if (first >= end) return;
+
+  for (int c = tid; c < nlines; c += kThreads) line_type[c] = -1;
+  __syncthreads();
+  for (int h = tid; h < B; h += kThreads) {
+    const int c = code[h];
+    if (c >= 0 && c < nlines) line_type[c] = (short)h;
+  }
+
+  // Chunk u of this thread: slot ps0 + 1024 u, 16 bytes of one point; the map
+  // is recomputed per item (ps0 passes through an empty asm).
+  const uint32_t ps0 = (uint32_t)tid;
+  const uint32_t rp4 = (uint32_t)rp * 4u;
+  float4 pf[kPF];
+  uint32_t src[kPF];
+  auto prefetch = [&](int64_t item) {
+    const int64_t b = item / nslices;
+    const int64_t e0 = (item - b * nslices) * kE;
+    const char* Fb = reinterpret_cast<const char*>(F + b * (int64_t)N0 * rp + e0);
+#pragma unroll
+    for (int u = 0; u < kPF; ++u)
+      pf[u] = ps0 + 1024u * u < (uint32_t)N0 ? *reinterpret_cast<const float4*>(Fb + src[u])
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+#pragma unroll
+  for (int u = 0; u < kPF; ++u) {
+    const uint32_t ps = ps0 + 1024u * u;
+    const uint32_t x1 = LrSlot<Q>::div(ps), x0 = ps - Q * x1;
+    src[u] = __umul24(x0 * Q + x1, rp4);             // 4 x rp, x = x0*q + x1
+  }
+  prefetch(first);
+
+  const int j = lane & 15;
+  const int row = lane >> 4;                         // group of the wave's task
+  const int lane16 = 16 * j, laneCW16 = 16 * kCW * j;
+  const char* pbase = reinterpret_cast<const char*>(smem);
+
+  for (int64_t item = first; item < end; item += nk) {
+    {
+      uint32_t p0 = ps0;
+      asm volatile("" : "+v"(p0));
+#pragma unroll
+      for (int u = 0; u < kPF; ++u) {
+        const uint32_t ps = p0 + 1024u * u;
+        const uint32_t x1 = LrSlot<Q>::div(ps), x0 = ps - Q * x1;
+        if (ps < (uint32_t)N0) {
+          float4* e = smem + (kCW * x1 + x0);
+#pragma unroll
+          for (int c = 0; c < (Q + 15 + Q - 1) / Q; ++c)
+            if (x0 + c * Q < (uint32_t)(Q + 15)) e[c * Q] = pf[u];
+        }
+        src[u] = __umul24(x0 * Q + x1, rp4);
+      }
+    }
+    lds_barrier();                                   // panel (and line table) complete
+    const int64_t b = item / nslices;
+    const int64_t e0 = (item - b * nslices) * kE;
+    if (item + nk < end) prefetch(item + nk);        // lands while this item is summed
+    const bool live = e0 < rp;                       // rp % 4 == 0: whole planes
+    const char* Ubase = reinterpret_cast<const char*>(U + b * (int64_t)B * rp + e0);
+    float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (HasG && live) g = *reinterpret_cast<const float4*>(Fg + b * rp + e0);
+
+    for (int task = wv; task < NT; task += kWaves) {
+      const LgGroup<Q> gr(4 * task + row);           // the lane's own group (per row)
+      const bool valid = j < gr.nvalid;
+      const int bl = gr.b0 + j;
+      const int col = valid ? bl : (bl >= 16 ? bl - 16 : 0);
+      const char* vb = pbase + lane16 + (gr.sloped ? 0 : (int)__umul24(16 * kCW, col));
+      int ot[NR];
+      {
+        int s = (int)LgMod<Q>::mod((unsigned)gr.s0 + __umul24(gr.qm, j));
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          ot[r] = (gr.sloped ? 256 * kCW * r + laneCW16 : 256 * r + lane16) + 16 * s;
+          const unsigned c = (unsigned)(s + gr.d16);
+          s = (int)min(c, c - (unsigned)q);
+        }
+      }
+      float4 a = lr_line_sum<Q>(vb, ot);
+      const int h = valid ? line_type[min(gr.lcb + j, nlines - 1)] : -1;
+      if (live && h >= 0) {
+        if (HasG) add4(a, g);
+        *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + (uint32_t)h * rp4) = a;
+      }
+    }
+    lds_barrier();                                   // every wave is done with the panel
+  }
+}
+
+template <int Q>
+static int launch_row_q(const float* F, const float* F_glob, const int* code, float* U, int nb,
+                        int B, int64_t rp, hipStream_t stream) {
+  using namespace ir;
+  const int nslices = (int)((rp + kE - 1) / kE);
+  const int64_t total = (int64_t)nb * nslices;
+  int dev = 0, ncu = 256;
+  (void)hipGetDevice(&dev);
+  (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  const int64_t per_xcd = (total + inc::kXCD - 1) / inc::kXCD;
+  const int64_t per_xcd_wgs = std::max<int64_t>(1, std::min<int64_t>(ncu / inc::kXCD, per_xcd));
+  const unsigned grid = (unsigned)(per_xcd_wgs * inc::kXCD);
+  const size_t smem = (size_t)Shape<Q>::kLdsBytes;
+  static bool attr_set[2] = {false, false};
+  auto kern = F_glob ? incidence_row_kernel<Q, true> : incidence_row_kernel<Q, false>;
+  if (!attr_set[F_glob ? 1 : 0]) {
+    (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)smem);
+    attr_set[F_glob ? 1 : 0] = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp,
+                     nslices, total, per_xcd);
+  return launch_status("smat_incidence_plane");
+}
+
+// The row-group kernel is compiled for the primes 43 .. 83; returns
+// SMAT_EUNSUPPORTED for any other q.
+static int launch_row(const float* F, const float* F_glob, const int* code, int q, float* U,
+                      int nb, int B, int64_t rp, hipStream_t stream) {
+  switch (q) {
+#define SMAT_ROW_Q(QV) \
+  case QV:             \
+    return launch_row_q<QV>(F, F_glob, code, U, nb, B, rp, stream);
+    SMAT_ROW_Q(43) SMAT_ROW_Q(47) SMAT_ROW_Q(53) SMAT_ROW_Q(59) SMAT_ROW_Q(61) SMAT_ROW_Q(67)
+    SMAT_ROW_Q(71) SMAT_ROW_Q(73) SMAT_ROW_Q(79) SMAT_ROW_Q(83)
+#undef SMAT_ROW_Q
+    default:
+      return SMAT_EUNSUPPORTED;
+  }
+}
+
+static bool row_kernel_has_q(int q) {
+  switch (q) {
+    case 43: case 47: case 53: case 59: case 61: case 67: case 71: case 73: case 79: case 83:
+      return true;
+    default:
+      return false;
+  }
+}
 // ---------------------------------------------------------------------------
 // L2 kernel
 // ---------------------------------------------------------------------------
@@ -875,6 +1133,9 @@ int incidence_plane_dispatch(const float* F, const float* F_glob, const int* cod
   if (wave_kernel_fits(q, N0, B, rp) && wave_kernel_has_q(q) &&
       variant(SMAT_VARIANT_INCIDENCE_PLANE) == 0)
     return launch_wave(F, F_glob, code, q, U, nb, N0, B, rp, stream);
+  if (row_kernel_fits(q, N0, B, rp) && row_kernel_has_q(q) &&
+      variant(SMAT_VARIANT_INCIDENCE_PLANE) == 0)
+    return launch_row(F, F_glob, code, q, U, nb, B, rp, stream);
   // Two workgroups per CU at E = 8 (one stages its panel while the other sums)
   // measured ahead of one at E = 16; wider panels fall back to one per CU.
   const int64_t entries = (int64_t)q * (q + 15);

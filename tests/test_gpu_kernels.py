@@ -165,6 +165,47 @@ def test_incidence_line_groups_every_field(T, chunk, q, glob):
     assert _rel(U, ref) < 1e-6
 
 
+@pytest.mark.parametrize("T,chunk,q", [(139264, 32, 43), (163840, 32, 47), (229376, 32, 53),
+                                     (327680, 32, 59), (425984, 32, 61), (458752, 32, 67),
+                                     (655360, 32, 71), (720896, 32, 73), (786432, 32, 79),
+                                     (1048576, 32, 83)])
+@pytest.mark.parametrize("glob", [False, True])
+def test_incidence_row_groups_every_field(T, chunk, q, glob):
+    """The row-group kernel (one plane an item, a line group per sixteen-lane
+    row) takes the primes 43 .. 83: each instantiation against the fp64 oracle at
+    r*p = 20 (five planes), with and without the global channel."""
+    _say("incidence row groups", T, chunk, q, glob)
+    spec = A.to_device(build_mask(T, 3, chunk=chunk), DEV)
+    assert spec.q == q and spec.plane_code_t is not None
+    g = torch.Generator().manual_seed(q)
+    F = torch.randn(3, spec.N0, 4, 5, generator=g)
+    Fg = torch.randn(3, 4, 5, generator=g)
+    U = K.incidence_plane(F.to(DEV), spec.plane_code_t, spec.q,
+                          F_glob=Fg.to(DEV) if glob else None)
+    ref = O.apply_incidence(F.double(), spec)
+    if glob:
+        ref = ref + Fg.double().unsqueeze(1)
+    assert _rel(U, ref) < 1e-6
+
+
+@pytest.mark.parametrize("T,q,glob", [(139264, 43, True), (458752, 67, False)])
+def test_incidence_row_groups_many_items(T, q, glob):
+    """r*p = 1056 over two sequences: 528 one-plane items, several a workgroup,
+    so the register prefetch of the next item is exercised."""
+    _say("incidence row groups, several items a workgroup", T, q, glob)
+    spec = A.to_device(build_mask(T, 3, chunk=32), DEV)
+    assert spec.q == q
+    g = torch.Generator().manual_seed(T)
+    F = torch.randn(2, spec.N0, 32, 33, generator=g)
+    Fg = torch.randn(2, 32, 33, generator=g)
+    U = K.incidence_plane(F.to(DEV), spec.plane_code_t, spec.q,
+                          F_glob=Fg.to(DEV) if glob else None)
+    ref = O.apply_incidence(F.double(), spec)
+    if glob:
+        ref = ref + Fg.double().unsqueeze(1)
+    assert _rel(U, ref) < 1e-6
+
+
 def test_incidence_ragged_endpoint_csr():
     _say("incidence ragged (endpoint mask, CSR)")
     spec = A.to_device(build_mask(256, 8, chunk=8), DEV)

@@ -174,12 +174,12 @@ _U32 = 1 << 32
 
 def _lgdiv(q, xmax):
     """(M, S) of LgDiv<q, xmax>: the smallest S with M = ceil(2^S / q) exact on
-    [0, xmax), and x M below 2^24 there."""
+    [0, xmax), and x M below 2^32 there (the 24-bit multiply where below 2^24)."""
     S = 1
     while True:
         M = ((1 << S) + q - 1) // q
         if all((x * M) >> S == x // q for x in range(xmax)):
-            assert xmax * M < (1 << 24)
+            assert xmax * M < _U32
             return M, S
         S += 1
 
@@ -323,3 +323,111 @@ def test_line_group_incidence_half_exchange_stores_whole_lines():
     splane = [((row & 1) << 1) | (row >> 1) for row in range(4)]
     assert [p for _, p in x] == splane and [p for _, p in y] == splane
     assert {g for g, _ in x} == {"A"} and {g for g, _ in y} == {"B"}
+
+
+# ---------------------------------------------------------------------------
+# the row-group incidence kernel's LDS addresses (incidence.hip, d = 3, q > 41)
+# ---------------------------------------------------------------------------
+# Restates ir::Shape, LrSlot and the task loop of incidence_row_kernel: one
+# plane an item, each row of a wave its own group (group 4 task + row).
+
+_ROW_Q = (43, 47, 53, 59, 61, 67, 71, 73, 79, 83)
+
+
+def _row_shape(q):
+    """(kCW, kEntries, kLdsBytes) of ir::Shape<q>."""
+    cw = (q + 15 + 1) // 2 * 2
+    entries = (cw * q + 15) // 16 * 16
+    return cw, entries, entries * 16 + ((q * (q + 1) * 2 + 15) // 16) * 16
+
+
+def _row_staging(q):
+    """{entry: point} the staging writes: slot ps = tid + 1024 u, x1 = ps / q by
+    LrSlot's multiply-shift, copies at x0 + c q below q + 15."""
+    cw, _, _ = _row_shape(q)
+    M, S = _lgdiv(q, 64 * _KWAVES * _KPF)
+    panel = {}
+    for tid in range(_KTHREADS):
+        for u in range(_KPF):
+            ps = tid + 1024 * u
+            x1 = ((ps * M) % _U32) >> S
+            x0 = ps - q * x1
+            if ps >= q * q:
+                continue
+            assert (x1, x0) == divmod(ps, q)
+            for c in range((q + 15 + q - 1) // q):
+                if x0 + c * q < q + 15:
+                    e = cw * x1 + x0 + c * q
+                    assert e not in panel
+                    panel[e] = x0 * q + x1
+    return panel
+
+
+def _row_reads(q):
+    """Yield (group, lane j, step, entry, line code) for every read of the
+    row-group kernel: row k of wave task n takes group 4 n + k."""
+    cw, _, _ = _row_shape(q)
+    P = (q + 15) // 16
+    G = (q + 1) * P
+    NT = (G + 3) // 4
+    NR = (q + 15) // 16
+    M, S = _lgdiv(q, 16 * P + 16 * q)
+    for task in range(NT):
+        for row in range(4):
+            grp = 4 * task + row
+            b0, s0, qm, d16, lcb, nvalid, sloped = _group(q, grp)
+            ot = {}
+            for l in range(16):
+                x = s0 + qm * l
+                s = x - q * ((x * M) >> S)
+                assert s == x % q
+                for r in range(NR):
+                    ot[r, l] = (256 * cw * r + 16 * cw * l if sloped else 256 * r + 16 * l) \
+                        + 16 * s
+                    c = (s + d16) % _U32
+                    s = min(c, (c - q) % _U32)
+            for j in range(16):
+                valid = j < nvalid
+                bl = b0 + j
+                col = bl if valid else (bl - 16 if bl >= 16 else 0)
+                vb = 16 * j + (0 if sloped else 16 * cw * col)
+                lc = min(lcb + j, q * (q + 1) - 1)
+                for t in range(q):
+                    addr = vb + ot[t // 16, t % 16]
+                    assert addr % 16 == 0
+                    yield grp, j, t, addr // 16, (lc if valid else None)
+
+
+@pytest.mark.parametrize("q", _ROW_Q)
+def test_row_group_incidence_reads_each_line_once_in_bounds(q):
+    """Emulates the row-group kernel for every field size it is compiled for:
+    the panel and line table fit the 160 KB LDS, every read lands on a staged
+    entry below the line table, each stored line reads exactly its q points once
+    and stores under its own line code."""
+    cw, entries, lds = _row_shape(q)
+    assert lds <= 160 * 1024 and q * q <= _KPF * _KTHREADS
+    panel = _row_staging(q)
+    assert len(panel) == q * (q + 15) and max(panel) < entries
+    P = (q + 15) // 16
+    G = (q + 1) * P
+    got, codes, phases = {}, {}, {}
+    for grp, j, t, e, lc in _row_reads(q):
+        assert 0 <= e < entries and e in panel
+        got.setdefault((grp, j), []).append(panel[e])
+        codes[grp, j] = lc
+        phases.setdefault((grp, t), set()).add(e % 16)
+    assert all(len(v) == 16 for v in phases.values())   # one bank phase a lane
+    for grp in range(G):
+        dirn, part = divmod(grp, P)
+        for j in range(16):
+            b = part * 16 + j
+            if b >= q:
+                assert codes[grp, j] is None
+                continue
+            if dirn < q:
+                want = sorted(((b - dirn * t) % q) * q + t for t in range(q))
+                assert codes[grp, j] == (dirn + 1) * q + b
+            else:
+                want = sorted(x0 * q + b for x0 in range(q))
+                assert codes[grp, j] == b
+            assert sorted(got[grp, j]) == want
