@@ -19,6 +19,13 @@
 //   L2; each lane keeps 8 loads in flight.
 //
 // Both sum a hyperplane's points in the order of the table they are given.
+//
+// For d = 3 (N0 = q^2, hyperplanes are the q(q+1) lines of the plane over F_q)
+// the lines are generated from their codes and no point table is read:
+// incidence_wave_kernel (prime q <= 41: four 16-byte planes an item, a line
+//   group per pair of sixteen-lane rows, two planes a lane),
+// incidence_row_kernel (prime 43 <= q <= 83: one plane an item, a line group
+//   per row), and incidence_plane_kernel (any other q: a line per lane).
 #include <stdlib.h>
 
 #include <algorithm>
@@ -727,9 +734,9 @@ static bool wave_kernel_has_q(int q) {
 // of one direction and reads, at step t, the same entries as a line-group row
 // (sloped: kCW*t + s_t + j; vertical: kCW*b + j + t), one 16-byte read and
 // four adds a step after the DPP-broadcast address add.  The four rows of a
-// wave are four groups at different bank phases, which ds_read_b128 serves at
-// about half its full rate; the line-per-lane plane kernel it replaces also
-// paid three more vector instructions a step for each lane's own wrap.
+// wave are four consecutive groups: the two rows of a half-wave read the same
+// bank phase except at a step whose offsets wrap past q (ds_read_b128 serves
+// rows at different phases at about half its full rate).
 namespace ir {
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
