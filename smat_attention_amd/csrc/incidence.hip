@@ -582,6 +582,58 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   const int lane16 = 16 * j, laneCW16 = 16 * kCW * j;
   const uint32_t splane16 = 16u * splane;
 
+  // The lane state of each of the wave's tasks is the same for every item, so
+  // it is worked out once: tasks wv, wv + 16, ... (kTasks at most); for each,
+  // the lane part of the read address, the row parts ot[] of the q steps, and
+  // the byte offsets in an item's U rows of the two lines this lane stores
+  // after the half exchange (kNoLine: none).
+  constexpr int kTasks = (NT + kWaves - 1) / kWaves;
+  constexpr uint32_t kNoLine = ~0u;
+  int tvb[kTasks], tot[kTasks][NR];
+  uint32_t tsA[kTasks], tsB[kTasks];
+  lds_barrier();                                     // line table complete
+#pragma unroll
+  for (int k = 0; k < kTasks; ++k) {
+    const int task = wv + kWaves * k;                // past NT: dead, never summed
+    // The task's groups 2 task (rows 0-1) and 2 task + 1 (rows 2-3) are
+    // worked out on the scalar unit; each lane then takes its own.
+    LgGroup<Q> gA(2 * task), gB(2 * task + 1);
+    gA.opaque();                                     // select the values, not their
+    gB.opaque();                                     // derivation, per lane
+    const int b0 = gsel ? gB.b0 : gA.b0;
+    const int s0 = gsel ? gB.s0 : gA.s0;
+    const int qm = gsel ? gB.qm : gA.qm;
+    const int d16 = gsel ? gB.d16 : gA.d16;
+    const int lcb = gsel ? gB.lcb : gA.lcb;
+    const int nvalid = gsel ? gB.nvalid : gA.nvalid;
+    const bool sloped = (gsel ? gB.sloped : gA.sloped) != 0;
+    const bool valid = j < nvalid;
+    // sloped: lane part 16 j; row part of step t = 16 (kCW t + s_t),
+    //   s_t = (b0 - m t) mod q = (b0 + qm t) mod q, taken by lane l for
+    //   t = 16 run + l.
+    // vertical (and the dead group of an odd G, s0 = qm = 0): lane part
+    //   16 (kCW col + j), row part of step t = 16 t, col clamped into the
+    //   columns for lanes past q.
+    const int bl = b0 + j;
+    const int col = valid ? bl : (bl >= kGroup ? bl - kGroup : 0);
+    tvb[k] = lane16 + (sloped ? 0 : (int)__umul24(16 * kCW, col));
+    {
+      int s = (int)LgMod<Q>::mod((unsigned)s0 + __umul24(qm, j));
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        tot[k][r] = (sloped ? 256 * kCW * r + laneCW16 : 256 * r + lane16) + 16 * s;
+        const unsigned c = (unsigned)(s + d16);
+        s = (int)min(c, c - (unsigned)q);
+      }
+    }
+    int hA = valid ? line_type[min(lcb + j, nlines - 1)] : -1, hB = hA;
+    swap_halves(hA, hB);                             // the lines stored after the exchange
+    // a lane stores at byte h * 4 rp + 16 splane of its type row h (below 2^32:
+    // checked on the host)
+    tsA[k] = hA >= 0 ? (uint32_t)hA * rp4 + splane16 : kNoLine;
+    tsB[k] = hB >= 0 ? (uint32_t)hB * rp4 + splane16 : kNoLine;
+  }
+
   for (int64_t item = first; item < end; item += nk) {
     {
       uint32_t p0 = ps0;
@@ -608,42 +660,11 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     // h * 4 rp + 16 splane of its type row h (below 2^32: checked on the host).
     const char* Ubase = reinterpret_cast<const char*>(U + b * (int64_t)B * rp + e0);
 
-    for (int task = wv; task < NT; task += kWaves) {
-      // The task's groups 2 task (rows 0-1) and 2 task + 1 (rows 2-3) are
-      // worked out on the scalar unit; each lane then takes its own.
-      LgGroup<Q> gA(2 * task), gB(2 * task + 1);
-      gA.opaque();                                   // select the values, not their
-      gB.opaque();                                   // derivation, per lane
-      const int b0 = gsel ? gB.b0 : gA.b0;
-      const int s0 = gsel ? gB.s0 : gA.s0;
-      const int qm = gsel ? gB.qm : gA.qm;
-      const int d16 = gsel ? gB.d16 : gA.d16;
-      const int lcb = gsel ? gB.lcb : gA.lcb;
-      const int nvalid = gsel ? gB.nvalid : gA.nvalid;
-      const bool sloped = (gsel ? gB.sloped : gA.sloped) != 0;
-      const bool valid = j < nvalid;
-      // sloped: lane part 16 j; row part of step t = 16 (kCW t + s_t),
-      //   s_t = (b0 - m t) mod q = (b0 + qm t) mod q, taken by lane l for
-      //   t = 16 run + l.
-      // vertical (and the dead group of an odd G, s0 = qm = 0): lane part
-      //   16 (kCW col + j), row part of step t = 16 t, col clamped into the
-      //   columns for lanes past q.
-      const int bl = b0 + j;
-      const int col = valid ? bl : (bl >= kGroup ? bl - kGroup : 0);
-      const char* vb = pbase + lane16 + (sloped ? 0 : (int)__umul24(16 * kCW, col));
-      int ot[NR];
-      {
-        int s = (int)LgMod<Q>::mod((unsigned)s0 + __umul24(qm, j));
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          ot[r] = (sloped ? 256 * kCW * r + laneCW16 : 256 * r + lane16) + 16 * s;
-          const unsigned c = (unsigned)(s + d16);
-          s = (int)min(c, c - (unsigned)q);
-        }
-      }
+    for (int k = 0; k < kTasks; ++k) {
+      if (wv + kWaves * k >= NT) continue;
       float4 a0, a1;
-      lg_line_sums<Q>(a0, a1, vb, ot);
-      int hA = valid ? line_type[min(lcb + j, nlines - 1)] : -1, hB = hA;
+      lg_line_sums<Q>(a0, a1, pbase + tvb[k], tot[k]);
       // Rows 0-3 hold planes (0, 1) and (2, 3) of group A, then of group B, in
       // (a0, a1).  One exchange of 32-lane halves leaves group A's four planes in
       // a0 and group B's in a1 (rows 0-3: planes 0, 2, 1, 3), so each store
@@ -652,17 +673,14 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
       swap_halves(a0.y, a1.y);
       swap_halves(a0.z, a1.z);
       swap_halves(a0.w, a1.w);
-      swap_halves(hA, hB);
       if (live) {
         if (HasG) {
           const float4 g = *reinterpret_cast<const float4*>(Fg + b * rp + e0 + 4 * splane);
           add4(a0, g);
           add4(a1, g);
         }
-        if (hA >= 0)
-          *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + ((uint32_t)hA * rp4 + splane16)) = a0;
-        if (hB >= 0)
-          *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + ((uint32_t)hB * rp4 + splane16)) = a1;
+        if (tsA[k] != kNoLine) *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + tsA[k]) = a0;
+        if (tsB[k] != kNoLine) *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + tsB[k]) = a1;
       }
     }
     lds_barrier();                                   // every wave is done with the panel
