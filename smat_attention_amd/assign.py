@@ -496,13 +496,15 @@ class ContentAssign(nn.Module):
 # ---------------------------------------------------------------------------
 
 # The fused backward kernels of the hard read and pool (smat_cell_read_backward,
-# smat_cell_pool_backward) serve 16-bit inputs at r = 64, p = 65; tests switch
-# them off to compare with the list reads they replace.
+# smat_cell_pool_backward) serve bf16 inputs at r = 64, p = 65; tests switch
+# them off to compare with the list reads they replace.  They split fp32
+# operands (F, dF, dY) into bf16 hi/lo pairs, which keeps fp32's exponent
+# range; fp16 inputs take the list reads, which widen every operand to fp32.
 FUSED_CELL_BACKWARD = True
 
 
 def _cell_backward_ok(X, Y, r_ok=64, p_ok=65):
-    return (FUSED_CELL_BACKWARD and X.dtype in (torch.bfloat16, torch.float16)
+    return (FUSED_CELL_BACKWARD and X.dtype == torch.bfloat16
             and X.shape[-1] == r_ok and (Y is None or (Y.dtype == X.dtype
                                                        and Y.shape[-1] == p_ok))
             and X.stride(-1) == 1 and X.stride(1) % 8 == 0 and X.stride(0) % 8 == 0

@@ -91,22 +91,19 @@ class FeatureMap:
     """The map ``x -> elu(x W^T) + 1`` (or ``relu(x W^T) + 1e-3``) that
     :func:`make_phi` returns: callable like the reference's closure
     (attention.py:82-96), with ``W`` and ``kind`` exposed so :func:`featurise`
-    can run it as one HIP launch.  GPU tensors go through the kernel; CPU
-    tensors through the same torch ops the reference uses."""
+    can run it as one HIP launch.  GPU tensors only: there is no host path."""
 
     def __init__(self, W: torch.Tensor, kind: str):
         self.W, self.kind = W, kind
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
-        if x.is_cuda:
-            if _wants_grad(x, self.W):
-                from .kernels.hip_bwd import FeaturiseFunction
-                return FeaturiseFunction.apply(self.W, self.kind, x, None, None, None)[0]
-            return _hip.featurise(self.W, self.kind, x)[0]
-        y = x @ self.W.T
-        if self.kind == "elu1":
-            return torch.nn.functional.elu(y) + 1.0
-        return torch.nn.functional.relu(y) + 1e-3
+        if not x.is_cuda:
+            raise TypeError("FeatureMap runs on the GPU only (the HIP featurise kernel); "
+                            f"got a {x.device} tensor")
+        if _wants_grad(x, self.W):
+            from .kernels.hip_bwd import FeaturiseFunction
+            return FeaturiseFunction.apply(self.W, self.kind, x, None, None, None)[0]
+        return _hip.featurise(self.W, self.kind, x)[0]
 
 
 def make_phi(d_qk: int, r: int, *, kind: str = "elu1", device="cpu",
@@ -135,7 +132,10 @@ def featurise(Q, K, V, phi, *, g=None, h=None):
     rounded up to 8 elements).  Gradients reach Q, K, V, h and W as in the
     reference (an autograd node around the launch).
     """
-    if isinstance(phi, FeatureMap) and Q.is_cuda:
+    if isinstance(phi, FeatureMap):
+        if not Q.is_cuda:
+            raise TypeError("featurise with a FeatureMap runs on the GPU only (the HIP "
+                            f"featurise kernel); got {Q.device} tensors")
         if _wants_grad(Q, K, V, h, phi.W):
             # the HIP launch forward, the map's derivative backward
             from .kernels.hip_bwd import FeaturiseFunction

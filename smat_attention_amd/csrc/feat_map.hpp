@@ -10,6 +10,8 @@
 // between, as torch does for 16-bit tensors).
 #pragma once
 
+#include <type_traits>
+
 #include "smat_common.hpp"
 
 namespace smat {
@@ -33,11 +35,21 @@ __device__ __forceinline__ float expm1_neg(float v) {
   return __builtin_amdgcn_exp2f(v * 1.4426950408889634f) - 1.f;
 }
 
+// expm1 of a non-positive argument for input type In: the short form where the
+// result is rounded to bf16 (where it is exact after rounding, above), libm's
+// expm1f for fp16 (whose 11-bit significand the short form's 1e-5 error could
+// round differently) and for fp32 (where nothing rounds afterwards).
+template <typename In>
+__device__ __forceinline__ float expm1_nonpos(float v) {
+  if constexpr (std::is_same<In, bf16>::value) return expm1_neg(v);
+  else return expm1f(v);
+}
+
 template <typename In>
 __device__ __forceinline__ float feature_map(float acc, int kind) {
   const float v = to_f32(from_f32<In>(acc));                 // torch's matmul output
   if (kind == 0) {
-    const float e = to_f32(from_f32<In>(v > 0.f ? v : expm1_neg(v)));
+    const float e = to_f32(from_f32<In>(v > 0.f ? v : expm1_nonpos<In>(v)));
     return to_f32(from_f32<In>(e + 1.0f));
   }
   return to_f32(from_f32<In>(fmaxf(v, 0.f) + 1e-3f));

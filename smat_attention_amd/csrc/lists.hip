@@ -30,6 +30,11 @@ __device__ __forceinline__ int clamp_key(int64_t k, int ncls) {
   return k < 0 ? 0 : (k >= ncls ? ncls - 1 : (int)k);
 }
 
+// offs[0] = 0 for an empty batch (nb = 0: one offset, no lists).
+__global__ __launch_bounds__(64) void csr_empty_kernel(int64_t* __restrict__ offs) {
+  if (threadIdx.x == 0) offs[0] = 0;
+}
+
 // counts[(b * ntiles + t) * ncls + c] = items of tile t of sequence b with key c.
 __global__ __launch_bounds__(cs::kThreads) void csr_count_kernel(const int64_t* __restrict__ keys,
                                                                  int* __restrict__ counts, int L,
@@ -153,7 +158,12 @@ extern "C" int smat_csr_lists(const int64_t* keys, int32_t* order, int64_t* offs
                SMAT_EUNSUPPORTED, "smat_csr_lists: need 1 <= ncls <= %d and nb*L < 2^31",
                cs::kMaxCls);
   hipStream_t st = (hipStream_t)stream;
-  if (nb == 0) return SMAT_OK;
+  if (nb == 0) {
+    // no lists: the single offset is 0 (a kernel, not a memset, so a captured
+    // graph replays it as a kernel node)
+    hipLaunchKernelGGL(csr_empty_kernel, dim3(1), dim3(64), 0, st, offs);
+    return launch_status("smat_csr_lists");
+  }
   // L = 0: no tiles; the scan alone writes the (all-zero) offsets
   const int ntiles = (L + cs::kTile - 1) / cs::kTile;
   int nbits = 0;

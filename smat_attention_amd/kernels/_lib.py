@@ -15,7 +15,9 @@ import threading
 import torch
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.environ.get("SMAT_HIP_LIB", os.path.join(_PKG, "libsmat_hip.so"))
+# The package's own build output, and nothing else: no environment variable
+# can point the product at another library.
+LIB_PATH = os.path.join(_PKG, "libsmat_hip.so")
 
 SMAT_BF16, SMAT_F16, SMAT_F32 = 0, 1, 2
 DTYPE_CODE = {torch.bfloat16: SMAT_BF16, torch.float16: SMAT_F16, torch.float32: SMAT_F32}

@@ -125,13 +125,16 @@ def recent_token_lists(spec, device):
 
 
 # The long-range backward kernels (smat_lr_dphi, smat_lr_dfeat,
-# smat_pool_backward) serve 16-bit inputs at r = 64, p = 65; tests switch them
-# off to compare with the smat_bgemm products they replace.
+# smat_pool_backward) serve bf16 inputs at r = 64, p = 65; tests switch them
+# off to compare with the smat_bgemm products they replace.  They split fp32
+# operands (dH ~ dout / den, U, dF) into bf16 hi/lo pairs, which keeps fp32's
+# exponent range; fp16 pairs would overflow above 65504 and lose the lo
+# correction below 6e-5, so fp16 inputs take the fp32 smat_bgemm products.
 FUSED_LONG_RANGE_BACKWARD = True
 
 
 def long_range_backward_ok(Ph, Ps, Vv) -> bool:
-    return (FUSED_LONG_RANGE_BACKWARD and Ph.dtype in (torch.bfloat16, torch.float16)
+    return (FUSED_LONG_RANGE_BACKWARD and Ph.dtype == torch.bfloat16
             and Ps.dtype == Ph.dtype and Vv.dtype == Ph.dtype
             and Ph.shape[-1] == 64 and Ps.shape[-1] == 64 and Vv.shape[-1] == 65
             and Ph.stride(-1) == 1 and Ps.stride(-1) == 1 and Vv.stride(-1) == 1
@@ -148,14 +151,15 @@ def _incidence_rows(src, idx, indptr, n_out, nb, n_in, rp):
     return out
 
 
-# The fused chunk backward (smat_chunk_backward) serves 16-bit inputs at
-# r = 64, p = 65, C = 128; tests switch it off to compare it with the chain of
+# The fused chunk backward (smat_chunk_backward) serves bf16 inputs at
+# r = 64, p = 65, C = 128 (its hi/lo operand split needs bf16's exponent
+# range, as above); tests switch it off to compare it with the chain of
 # smat_bgemm products it replaces.
 FUSED_CHUNK_BACKWARD = True
 
 
 def fused_chunk_backward_ok(Ph, Ps, Vv, C: int) -> bool:
-    return (FUSED_CHUNK_BACKWARD and Ph.dtype in (torch.bfloat16, torch.float16)
+    return (FUSED_CHUNK_BACKWARD and Ph.dtype == torch.bfloat16
             and Ps.dtype == Ph.dtype and Vv.dtype == Ph.dtype and C == 128
             and Ph.shape[-1] == 64 and Ps.shape[-1] == 64 and Vv.shape[-1] == 65
             and Ph.stride(-1) == 1 and Ps.stride(-1) == 1 and Vv.stride(-1) == 1

@@ -336,7 +336,8 @@ def test_csr_offsets_match_counts():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("nb,L,ncls", [(3, 300, 7), (2, 5000, 169), (1, 2048, 1), (4, 64, 300),
-                                       (2, 0, 5), (96, 8192, 169), (1, 4100, 8192)])
+                                       (2, 0, 5), (96, 8192, 169), (1, 4100, 8192),
+                                       (0, 100, 5)])
 def test_class_lists_match_stable_sort(nb, L, ncls):
     """smat_csr_lists (the counting sort behind every cell and type list)
     against torch's stable argsort and bincount of ``b*ncls + key`` on the CPU:
@@ -360,6 +361,12 @@ def test_class_lists_match_stable_sort(nb, L, ncls):
         offs = offs.cpu()
         assert offs[0] == 0 and offs[-1] == nb * L
         assert torch.equal(offs[1:] - offs[:-1], cnt)
+    if nb == 0:
+        # the one offset of an empty batch is written, not left as it was
+        from smat_attention_amd.kernels._lib import call, stream_of
+        offs = torch.full((1,), 7, device=dev, dtype=torch.int64)
+        call("smat_csr_lists", None, None, offs.data_ptr(), None, 0, L, ncls, 1, stream_of(offs))
+        assert offs.item() == 0
 
 
 @pytest.mark.gpu

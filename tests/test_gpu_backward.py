@@ -107,6 +107,43 @@ def test_backward_training_shape_bf16(d):
         assert _nrel(a[:h], b) < 2e-2, name
 
 
+@pytest.mark.parametrize("d,n_P,gate", [(2, 0, False), (2, 16, True), (3, 0, False),
+                                          (3, 16, True)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_backward_head_dim_128(dt, d, n_P, gate):
+    """The whole schedule's gradient at head_dim 128 (r = 128, p = 129: a width
+    the reference's fused backward refuses, triton_bwd.py:166-167), T = 4096,
+    d = 2 and 3, with and without the global channel and the output gate.
+    fp32: dPhi, dPsi, dVb and dg within 1e-5 (max-relative) of fp64 autograd
+    through the oracle on the same values.  bf16: within the 16-bit bar
+    (norm-relative 2e-2) of the reference's torch path's autograd in bf16 on
+    the same inputs, and of fp64 autograd on those values."""
+    T, hd, nb = 4096, 128, 2
+    _say("backward head_dim 128", dt, T, d, n_P, gate)
+    spec = build_mask(T, d, chunk=128, n_P=n_P)
+    Phi, Psi, Vb = (x.to(dt) for x in _feats(nb, T, hd, seed=31, k_scale=hd ** -0.5))
+    gen = torch.Generator().manual_seed(32)
+    w = torch.randn(nb, T, hd, generator=gen)
+    g = (torch.rand(nb, T, generator=gen) + 0.5) if gate else None
+    out, gs = _grads_gpu(spec, Phi, Psi, Vb, w, g)
+    names = ("dPhi", "dPsi", "dVb", "dg")
+    ref64, r64 = _grads_ref(spec, Phi, Psi, Vb, w, g)
+    if dt == torch.float32:
+        assert _rel(out, ref64) < 1e-5
+        for name, a, b in zip(names, gs, r64):
+            e = _rel(a, b)
+            _say(f"  {name}: rel vs fp64 {e:.2e}")
+            assert e < 1e-5, name
+        return
+    assert all(torch.isfinite(x).all() for x in gs)
+    refbf, rbf = _grads_ref(spec, Phi, Psi, Vb, w, g, dtype=torch.bfloat16)
+    assert (out.double() - refbf.double()).abs().max().item() < 2e-2
+    for name, a, b, c in zip(names, gs, rbf, r64):
+        e, e64 = _nrel(a, b), _nrel(a, c)
+        _say(f"  {name}: norm-rel vs bf16 torch path {e:.2e}, vs fp64 {e64:.2e}")
+        assert e < 2e-2 and e64 < 2e-2, name
+
+
 def test_forward_unchanged_when_grad_is_recorded():
     _say("forward with and without autograd")
     spec = build_mask(2048, 3, chunk=128)
@@ -388,6 +425,73 @@ def test_fused_cell_backward(d):
         _say(f"  {name}: {e:.2e}")
         assert torch.isfinite(a).all()
         assert e < (2e-3 if name in ("dQ", "dK", "dV") else 1e-4), name
+
+
+def test_fp16_attention_backward_takes_fp32_products():
+    """fp16 inputs at the training shape's head_dim 64 take the fp32 smat_bgemm
+    products, not the fused kernels (whose bf16 hi/lo operand split needs fp32's
+    exponent range).  With normalisers of 1e4-1e5 (T = 4096, elu + 1 features),
+    where dH = dout / den is below fp16's normal range, the gradients stay
+    finite and within the 16-bit bar (norm-relative 2e-2) of fp64 autograd on
+    the same fp16 values."""
+    from smat_attention_amd.kernels import hip_bwd as HB
+    T, d, nb = 4096, 3, 2
+    spec = build_mask(T, d, chunk=128)
+    Phi, Psi, Vb = (x.to(torch.float16) for x in _feats(nb, T, 64, seed=8, k_scale=0.125))
+    xs = [x.to(DEV) for x in (Phi, Psi, Vb)]
+    assert not HB.long_range_backward_ok(*xs) and not HB.fused_chunk_backward_ok(*xs, 128)
+    w = torch.randn(nb, T, 64, generator=torch.Generator().manual_seed(9))
+    _say("fp16 attention backward", T, d)
+    out, parts = A.smat_attention(*xs, spec, return_parts=True)
+    den = parts["H"][..., -1].float()
+    _say(f"  normaliser range {den.min().item():.3g} .. {den.max().item():.3g}")
+    assert den.max().item() > 1e4
+    out, gs = _grads_gpu(spec, Phi, Psi, Vb, w)
+    _, r64 = _grads_ref(spec, Phi, Psi, Vb, w)
+    for name, a, b in zip(("dPhi", "dPsi", "dVb"), gs, r64):
+        e = _nrel(a, b)
+        _say(f"  {name}: norm-rel vs fp64 {e:.2e}")
+        assert torch.isfinite(a).all() and e < 2e-2, name
+
+
+def test_fp16_cell_backward_matches_fp32_inputs():
+    """ContentAssign's hard point read and pool with fp16 Q, K, V at head_dim 64
+    take the list reads (fp32 operands), not the fused bf16 cell kernels.  The
+    hash sees the same u either way, so the cells are those of the fp32 run on
+    the same values; dQ, dK, dV and the hash parameters' gradients within
+    norm-relative 2e-2 of that run."""
+    from smat_attention_amd import assign as AS
+    B, H, hd, T, d = 2, 4, 64, 2048, 3
+    spec = build_mask(T, d, chunk=128)
+    n = spec.n
+    gen = torch.Generator().manual_seed(81)
+    h16 = torch.float16
+    Q = torch.randn(B * H, T, hd, generator=gen).to(h16)
+    K = (torch.randn(B * H, T, hd, generator=gen) / hd ** 0.5).to(h16)
+    V = torch.randn(B * H, T, hd, generator=gen).to(h16)
+    # dY scaled so dK, whose hash term grows as 1/std of the small keys, stays
+    # inside fp16's range (it reaches 3e4 at unit dY)
+    dY = (torch.randn(B * H, T - n, hd + 1, generator=gen) / 128).to(DEV)
+    torch.manual_seed(7)
+    m = AS.ContentAssign(H, H * hd, spec, mode="point").to(DEV)
+    _say("fp16 cell backward", d, spec.N0)
+
+    def run(dt):
+        phi = A.make_phi(hd, hd, device=DEV, dtype=dt, seed=0)
+        xs = [t.to(DEV, dt).requires_grad_(True) for t in (Q, K, V)]
+        assert dt != h16 or not AS._cell_backward_ok(xs[0], None)
+        Phi, Psi, Vb = A.featurise(*xs, phi)
+        u = xs[1].reshape(B, H, T, hd).transpose(1, 2).reshape(B, T, H * hd).float()
+        m.zero_grad()
+        Y = m(u, Phi, Psi, Vb, n)
+        (Y * dY).sum().backward()
+        return ([x.grad.float().cpu() for x in xs]
+                + [getattr(m, k).grad.detach().cpu() for k in ("W", "gamma", "b")])
+    g16, g32 = run(h16), run(torch.float32)
+    for name, a, b in zip(("dQ", "dK", "dV", "dW", "dgamma", "db"), g16, g32):
+        e = _nrel(a, b)
+        _say(f"  {name}: {e:.2e}")
+        assert torch.isfinite(a).all() and e < 2e-2, name
 
 
 @pytest.mark.parametrize("lr,T,d,n_P,gate", [

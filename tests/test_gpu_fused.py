@@ -70,6 +70,30 @@ def test_fused_forward_matches_featurise_then_forward(T, d, n_P, gates, kind, nb
     assert torch.isfinite(fused).all() and e < 1e-5
 
 
+@pytest.mark.parametrize("T,d,n_P,gates", [(4096, 3, 0, True), (4096, 2, 16, False)])
+def test_fused_forward_fp16(T, d, n_P, gates):
+    """fp16 q, k, v: the fused kernels' fp16 instantiations (pool, query,
+    prepass, scan, with libm's expm1f in the map) equal featurise +
+    smat_attention within 1e-5 of the largest entry, and head 0 meets the
+    16-bit bar (2e-2 absolute on O) against the oracle's featurise and
+    schedule on the same fp16 values."""
+    F16 = torch.float16
+    spec = build_mask(T, d, chunk=128, n_P=n_P)
+    _say("fused forward fp16", T, d, n_P, gates)
+    # six sequences: the fused pool needs 256 (sequence, profile) items (N0 = 47 at d = 2)
+    Q, K, V, h, g = _inputs(6, T, seed=T + d + 7, dt=F16, gates=gates)
+    fused, unfused = _run_both(spec, Q, K, V, h, g, dt=F16)
+    e = _rel(fused, unfused)
+    W = O.phi_weight(128, 128, dtype=F16, seed=0)
+    phi_cpu = lambda x: torch.nn.functional.elu(x.float() @ W.float().T).to(F16) + 1.0
+    ref = O.smat_attention(*O.featurise(Q[:1], K[:1], V[:1], phi_cpu,
+                                        h=None if h is None else h[:1]),
+                           spec, g=None if g is None else g[:1])
+    e_o = (fused[:1].double().cpu() - ref.double()).abs().max().item()
+    _say(f"  vs unfused {e:.2e}; head 0 vs the torch path on fp16: O {e_o:.2e}")
+    assert torch.isfinite(fused).all() and e < 1e-5 and e_o < 2e-2
+
+
 def test_fused_forward_long_prefill_T32768():
     """The long-prefill configuration at T = 32768 (B=1, H=8, head_dim 128, d=3,
     bf16 q, k, v ~ N(0, 1), k scaled 1/sqrt(128)): all 8 heads against the
@@ -91,6 +115,38 @@ def test_fused_forward_long_prefill_T32768():
     phi = A.FeatureMap(W.to(DEV), "elu1")
     again = A.smat_attention_fused(Q.to(DEV), K.to(DEV), V.to(DEV), phi, spec)
     assert torch.equal(again, fused)
+
+
+def test_fused_forward_long_prefill_T131072():
+    """The benchmark shape (B=1, H=8, head_dim 128, d=3, T=131072, bf16 q, k, v
+    ~ N(0, 1), k scaled 1/sqrt(128); q = 41, the line-group incidence): all 8
+    heads of smat_attention_fused against featurise + smat_attention (1e-5 of
+    the largest entry); head 0 against the oracle's featurise and schedule on
+    the same bf16 values (the reference's torch path: 2e-2 absolute on O, and
+    1e-3 on the log-normaliser, read from the unfused HIP call's parts)."""
+    T = 131072
+    spec = build_mask(T, 3, chunk=128)
+    assert (spec.q, spec.N0, spec.B) == (41, 1681, 1722)
+    _say("fused forward T=131072 d=3 nb=8 hd=128 bf16")
+    Q, K, V, _, _ = _inputs(8, T, seed=0)
+    fused, unfused = _run_both(spec, Q, K, V, None, None)
+    e = _rel(fused, unfused)
+    _say(f"  all heads vs featurise + smat_attention: {e:.2e}")
+    assert torch.isfinite(fused).all() and e < 1e-5
+    del unfused
+    W = O.phi_weight(128, 128, dtype=BF, seed=0)
+    phi_cpu = lambda x: torch.nn.functional.elu(x @ W.T) + 1.0
+    feats = O.featurise(Q[:1], K[:1], V[:1], phi_cpu)
+    ref, rparts = O.smat_attention(*feats, spec, return_parts=True)
+    phi = A.FeatureMap(W.to(DEV), "elu1")
+    Pd, Sd, Wd = A.featurise(Q[:1].to(DEV), K[:1].to(DEV), V[:1].to(DEV), phi)
+    _, parts = A.smat_attention(Pd, Sd, Wd, spec, return_parts=True)
+    lse = torch.log(parts["H"][..., -1].double().cpu())
+    lse_ref = torch.log(rparts["H"][..., -1].double())
+    e_o = (fused[:1].double().cpu() - ref.double()).abs().max().item()
+    e_l = (lse - lse_ref).abs().max().item()
+    _say(f"  head 0 vs the torch path on bf16: O {e_o:.2e}, lse {e_l:.2e}")
+    assert e_o < 2e-2 and e_l < 1e-3
 
 
 def test_fused_forward_falls_back_outside_its_shape_and_under_grad():

@@ -457,11 +457,12 @@ def test_forward_long_prefill_d3_bf16_T131072():
 
 def test_forward_long_prefill_d3_bf16_T524288():
     """The largest long-prefill shape (T = 524288, d = 3: q = 67, N0 = 4489, B = 4556,
-    the line-per-lane incidence kernel), one head, bf16: finite; the fused call
-    equals the stage-by-stage path; and the pooled long-range term equals the
-    direct one (each row type summing its landmark outer products without
-    pooling or incidence) -- two independent paths at full size, where the
-    fp64 oracle would take minutes."""
+    the row-group incidence kernel), one head, bf16: against the oracle (the
+    reference's torch path on the same bf16 values: 2e-2 on O, 1e-3 on the
+    log-normaliser; and the fp64 schedule), the fused call equals the
+    stage-by-stage path, and the pooled long-range term equals the direct one
+    (each row type summing its landmark outer products without pooling or
+    incidence)."""
     _say("forward T=524288 d=3 nb=1 hd=128 bf16")
     T = 524288
     spec = build_mask(T, 3, chunk=128)
@@ -477,6 +478,8 @@ def test_forward_long_prefill_d3_bf16_T524288():
     spec_d = A.to_device(spec, DEV, want_direct=True)
     direct = A.smat_attention(Pd, Sd, Wd, spec_d, long_range="direct")
     assert _rel(direct, out) < 1e-5
+    del direct, staged
+    _check_forward(spec, Phi, Psi, Vb, dt=torch.bfloat16, label="T=524288 d=3 head 0")
 
 
 @pytest.mark.parametrize("T,heads", [(32768, 2), (131072, 1)])
@@ -504,9 +507,10 @@ def test_forward_dense_control_d1_bf16(T, heads):
 
 
 def test_forward_dense_control_d1_bf16_T524288():
-    """d = 1 at T = 524288 (one head, bf16): the fused call equals the staged
-    path and equals plain causal linear attention (an unbroken scan) --
-    properties that hold at full size, where the fp64 oracle would take minutes."""
+    """d = 1 at T = 524288 (one head, bf16): against the oracle (the reference's
+    torch path on the same bf16 values, 2e-2 on O and 1e-3 on the
+    log-normaliser, and the fp64 schedule); the fused call equals the staged
+    path and equals plain causal linear attention (an unbroken scan)."""
     _say("forward T=524288 d=1 nb=1 hd=128 bf16")
     T = 524288
     spec = build_mask(T, 1, chunk=128)
@@ -521,6 +525,8 @@ def test_forward_dense_control_d1_bf16_T524288():
     e_s, e_p = _rel(staged, out), _rel(out, plain)
     _say(f"  staged {e_s:.2e}  plain causal {e_p:.2e}")
     assert e_s < 1e-5 and e_p < 1e-4
+    del staged, H, plain
+    _check_forward(spec, Phi, Psi, Vb, dt=torch.bfloat16, label="T=524288 d=1 head 0")
 
 
 def test_exact_non_influence():
@@ -773,6 +779,38 @@ def test_featurise(dt, T, dqk, r, dv, kind, gate):
     assert torch.equal(got[2].cpu(), ref[2])
     # the map alone, called on a GPU tensor
     assert torch.equal(phi(Q.to(DEV)), got[0])
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_feature_map_every_negative_16_bit_input(dt):
+    """The elu + 1 map on every finite non-positive 16-bit input, through the
+    featurise launch with W = I (so the product is the input itself), against
+    expm1 in fp64 rounded to the dtype, then + 1 rounded (torch's rounding
+    steps).  bf16 runs the short expm1 form and must be bit-exact on all 32 641
+    inputs; fp16 runs libm's expm1f (about 1 ulp of fp32), which may land one
+    fp16 step off where the exact value sits within that ulp of a rounding
+    boundary: at most 1e-3 of the inputs, by one step."""
+    _say("feature map exhaustive", dt)
+    itype = torch.int16
+    bits = torch.arange(-32768, 32768, dtype=torch.int32).to(itype)
+    vals = bits.view(dt).float()
+    vals = vals[torch.isfinite(vals) & (vals <= 0)]
+    n = vals.numel()
+    rows = (n + 127) // 128
+    Q = torch.zeros(rows * 128)
+    Q[:n] = vals
+    Q = Q.reshape(1, rows, 128).to(dt)
+    phi = A.FeatureMap(torch.eye(128, device=DEV, dtype=dt), "elu1")
+    got = A.featurise(Q.to(DEV), Q.to(DEV), Q.to(DEV), phi)[0].cpu().reshape(-1)[:n]
+    v64 = vals.double()
+    e = torch.expm1(v64).to(dt)
+    want = (e.double() + 1.0).to(dt)
+    if dt == torch.bfloat16:
+        bad = (got.view(itype) != want.view(itype)).sum().item()
+        assert bad == 0, f"{bad} of {n} bf16 inputs differ"
+    else:
+        step = (got.view(itype).int() - want.view(itype).int()).abs()
+        assert step.max().item() <= 1 and (step > 0).double().mean().item() <= 1e-3
 
 
 def test_featurise_rejects_mixed_dtypes():
