@@ -62,6 +62,12 @@ def grouped_planes(q: int, dim: int):
     return dirs, grouped
 
 
+def _straight_through(value: float, surrogate):
+    """A tensor whose forward value is ``value`` everywhere and whose gradient
+    is that of ``surrogate``: value + (surrogate - surrogate.detach())."""
+    return value + (surrogate - surrogate.detach())
+
+
 class ContentAssign(nn.Module):
     """Hash tokens to profiles and queries to types; run the long-range branch.
 
@@ -158,20 +164,8 @@ class ContentAssign(nn.Module):
         if self.anneal < 1.0:
             raise NotImplementedError("ContentAssign: the soft read (anneal < 1)")
         cells, s = self._hash(u)
-        B, L = cells.shape
-        lo = s.floor()
-        frac = s - lo
-        lo = lo.long()
-        hi = (lo + 1).clamp(max=self.q - 1)
-        soft_lo, soft_hi = 1.0 - frac, frac
-        if tok_w is not None:
-            tw = tok_w.reshape(B, L, 1).to(s.dtype)
-            soft_lo, soft_hi = soft_lo * tw, soft_hi * tw
-        occ = torch.zeros(B, self.dim, self.q, device=s.device, dtype=s.dtype)
-        occ = occ.scatter_add(-1, lo.transpose(1, 2), soft_lo.transpose(1, 2))
-        occ = occ.scatter_add(-1, hi.transpose(1, 2), soft_hi.transpose(1, 2))
-        occ = occ / occ.sum(-1, keepdim=True).clamp_min(1e-6)
-        self.aux = None if self.freeze else (occ * (occ.clamp_min(1e-9) * self.q).log()).sum(-1).mean()
+        L = cells.shape[1]
+        self.aux = None if self.freeze else self._balance(s, tok_w)
         if plant_at and self.plant and self.plant_cols.numel():
             cols = self.plant_cols[self.plant_cols < L]
             if cols.numel():
@@ -231,66 +225,86 @@ class ContentAssign(nn.Module):
         s = (s * self.q).clamp(0.0, self.q - 1e-4)
         return s.reshape(nb * self.h, L, self.dim)
 
+    def _balance(self, s, tok_w=None):
+        """Load-balance term of the hash (the reference's ``aux``,
+        assign.py:290-298): a token whose coordinate k sits at s = j + f puts
+        mass 1 - f on bin j and f on bin min(j + 1, q - 1), times its gate
+        weight ``tok_w``.  Per (sequence, coordinate) the masses over the q bins,
+        divided by their total (floored at 1e-6), form the occupancy o, and the
+        term is KL(o || uniform) = sum_j o_j log(q max(o_j, 1e-9)), averaged
+        over sequences and coordinates.  One index_add over both endpoints of
+        every token."""
+        B, L, dim = s.shape
+        q = self.q
+        j = s.detach().floor()
+        f = s - j                                    # carries the gradient of s
+        ends = torch.stack([j, (j + 1).clamp(max=q - 1)], -1).long()     # (B, L, dim, 2)
+        mass = torch.stack([1.0 - f, f], -1)
+        if tok_w is not None:
+            mass = mass * tok_w.reshape(B, L, 1, 1).to(s.dtype)
+        slot = torch.arange(B * dim, device=s.device).view(B, 1, dim, 1) * q + ends
+        occ = torch.zeros(B * dim * q, device=s.device, dtype=s.dtype)
+        occ = occ.index_add(0, slot.reshape(-1), mass.reshape(-1)).view(B, dim, q)
+        occ = occ / occ.sum(-1, keepdim=True).clamp_min(1e-6)
+        return (occ * torch.log(q * occ.clamp_min(1e-9))).sum(-1).mean()
+
     def _ste_pairs(self, s, plant_at=False, tok_w=None, single=False):
-        """The 2^dim (cell, weight) pairs of every token (assign.py:257-295):
-        weight ``(1 - a) s + a e`` per coordinate, with ``s`` the interpolation
-        weight and ``e`` its straight-through form (forward 1 on the low bin and
-        0 on the high one, the gradient of ``s``), ``a`` the anneal.  With
-        ``single`` and ``a >= 1`` only the chosen cell is kept, its weight the
-        product of the low bins' straight-through factors (the sparse path's
-        ``hard_k1``) -- except on a key side with planted columns, which the
-        reference plants into the full pairs.  Planted key columns get their
-        fixed cell with weight 1 and no gradient (:305-317).  Returns the chosen cells, idx (B, L, K),
-        w (B, L, K) and the load-balance term."""
-        B, L, _ = s.shape
-        a = float(self.anneal)
-        lo = s.floor()
-        frac = s - lo
-        lo = lo.long()
-        hi = (lo + 1).clamp(max=self.q - 1)
-        idx = torch.zeros(B, L, 1, dtype=torch.long, device=s.device)
-        w = torch.ones(B, L, 1, device=s.device, dtype=s.dtype)
-        for k in range(self.dim):
-            place = self.q ** (self.dim - 1 - k)
-            f = frac[..., k:k + 1]
-            s_lo, s_hi = 1.0 - f, f
-            e_lo = 1.0 + (s_lo - s_lo.detach())
-            e_hi = s_hi - s_hi.detach()
-            w_lo, w_hi = (1 - a) * s_lo + a * e_lo, (1 - a) * s_hi + a * e_hi
-            idx = torch.cat([idx + lo[..., k:k + 1] * place, idx + hi[..., k:k + 1] * place], -1)
-            w = torch.cat([w * w_lo, w * w_hi], dim=-1)
+        """The 2^dim (cell, weight) pairs of every token (assign.py:257-295).
+
+        Coordinate k of s = j_k + f_k interpolates between its low bin j_k and
+        its high bin min(j_k + 1, q - 1).  Pair m takes the high bin in the
+        coordinates whose bit is set in m (bit k for coordinate k; pair 0 is the
+        chosen cell), cell = sum_k bin_k q^(dim-1-k), and weight
+        prod_k c_k with c_k = (1 - a) (1 - f_k) + a lo_k on a low bin and
+        (1 - a) f_k + a hi_k on a high one, a the anneal.  lo_k and hi_k are
+        straight-through factors: forward 1 and 0, gradients those of 1 - f_k
+        and f_k.  With ``single`` and a >= 1 only pair 0 is kept, weight
+        prod_k lo_k (the sparse path's ``hard_k1``) -- except on a key side with
+        planted columns, which keeps all pairs as the reference does.
+        Planted key columns read their fixed cell at weight 1 on pair 0 and 0
+        elsewhere, with no gradient (:305-317).  Returns the chosen cells,
+        idx (B, L, K), w (B, L, K) and the load-balance term."""
+        B, L, dim = s.shape
+        q, a = self.q, float(self.anneal)
+        j = s.detach().floor()
+        f = s - j
+        lo_bin = j.long()
+        hi_bin = (lo_bin + 1).clamp(max=q - 1)
+        st_lo = _straight_through(1.0, 1.0 - f)
+        st_hi = _straight_through(0.0, f)
+        c_lo = (1 - a) * (1.0 - f) + a * st_lo
+        c_hi = (1 - a) * f + a * st_hi
         cols = None
         if plant_at and self.plant and self.plant_cols.numel():
             cols = self.plant_cols[self.plant_cols < L].to(s.device)
             cols = cols if cols.numel() else None
-        # the reference plants into a copy of the full pairs (assign.py:306-310),
-        # so a planted key side keeps all 2^dim pairs even where one would do
-        if single and cols is None and a >= 1.0 and getattr(self, "hard_k1", True):
-            idx = torch.zeros(B, L, 1, dtype=torch.long, device=s.device)
-            w = torch.ones(B, L, 1, device=s.device, dtype=s.dtype)
-            for k in range(self.dim):
-                f = frac[..., k:k + 1]
-                idx = idx + lo[..., k:k + 1] * self.q ** (self.dim - 1 - k)
-                w = w * (1.0 + ((1.0 - f) - (1.0 - f).detach()))
-        soft_lo, soft_hi = 1.0 - frac, frac
-        if tok_w is not None:
-            tw = tok_w.reshape(B, L, 1).to(s.dtype)
-            soft_lo, soft_hi = soft_lo * tw, soft_hi * tw
-        occ = torch.zeros(B, self.dim, self.q, device=s.device, dtype=s.dtype)
-        occ = occ.scatter_add(-1, lo.transpose(1, 2), soft_lo.transpose(1, 2))
-        occ = occ.scatter_add(-1, hi.transpose(1, 2), soft_hi.transpose(1, 2))
-        occ = occ / occ.sum(-1, keepdim=True).clamp_min(1e-6)
-        aux = None if self.freeze else (occ * (occ.clamp_min(1e-9) * self.q).log()).sum(-1).mean()
+        place = [q ** (dim - 1 - k) for k in range(dim)]
+        hard = single and cols is None and a >= 1.0 and getattr(self, "hard_k1", True)
+        idx_l, w_l = [], []
+        for m in ([0] if hard else range(1 << dim)):
+            cell, wt = 0, None
+            for k in range(dim):
+                high = (m >> k) & 1
+                cell = cell + (hi_bin if high else lo_bin)[..., k] * place[k]
+                ck = st_lo[..., k] if hard else (c_hi if high else c_lo)[..., k]
+                wt = ck if wt is None else wt * ck
+            idx_l.append(cell)
+            w_l.append(wt)
+        idx = torch.stack(idx_l, -1)
+        w = torch.stack(w_l, -1)
+        aux = None if self.freeze else self._balance(s, tok_w)
         cells = idx[..., 0].clone()
         if cols is not None:
-            # a fixed, input-independent profile: no gradient through its weights
             pc = self.plant_cells[: cols.numel()].to(s.device)
             cells[:, cols] = pc
-            idx = idx.clone()
-            idx[:, cols, :] = pc.view(1, -1, 1)
-            w = w.clone()
-            w[:, cols, :] = 0.0
-            w[:, cols, 0] = 1.0
+            planted = torch.zeros(L, dtype=torch.bool, device=s.device)
+            planted[cols] = True
+            cell_of = torch.zeros(L, dtype=idx.dtype, device=s.device)
+            cell_of[cols] = pc
+            first = torch.zeros(idx.shape[-1], dtype=w.dtype, device=s.device)
+            first[0] = 1.0
+            idx = torch.where(planted.view(1, L, 1), cell_of.view(1, L, 1), idx)
+            w = torch.where(planted.view(1, L, 1), first.view(1, 1, -1), w)
         return cells, idx, w, aux
 
     def _pairs_of(self, u, n, emb, key_src, key_w, ids, single):

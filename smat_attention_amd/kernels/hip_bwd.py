@@ -817,47 +817,44 @@ class _PoolFn(torch.autograd.Function):
         return dPsi.to(Psi.dtype), dVb.to(Vb.dtype), None, None, None
 
 
-_TRANSPOSE_CACHE = {}
+def _adjoint_lists(plane_pts, N0: int):
+    """C^T of a ``(B, deg)`` point table as CSR lists, built on the device.
 
-
-def _point_planes(plane_pts, N0):
-    """``(N0, D)`` table of the row types through each point (ascending), from
-    the ``(B, deg)`` table (triton_bwd.py:281-297); D must be the same for every
-    point."""
-    key = (plane_pts.data_ptr(), tuple(plane_pts.shape), N0)
-    hit = _TRANSPOSE_CACHE.get(key)
-    if hit is not None:
-        return hit
+    The table's B*deg entries, read as one sequence of keys (the points), go
+    through the counting sort behind every list of this package
+    (``smat_csr_lists``): entries grouped by point, each group in table order,
+    so entry ``e`` of point x names row type ``e // deg`` and the row types of
+    a point come out ascending.  Nothing is read back to the host, nothing is
+    cached, and points on any number of hyperplanes (ragged C^T) are allowed.
+    Returns ``(rows int32 (B*deg,), offsets int64 (N0 + 1,))``."""
+    from ..pool_ops import _class_lists
     B, deg = plane_pts.shape
-    pts = plane_pts.reshape(-1).long()
-    rows = torch.arange(B, device=plane_pts.device).repeat_interleave(deg)
-    order = torch.argsort(pts * B + rows)
-    pts, rows = pts[order], rows[order]
-    counts = torch.bincount(pts, minlength=N0)
-    if int(counts.min()) != int(counts.max()):
-        raise ValueError("incidence transpose is not uniform; the table kernel needs a "
-                         "constant number of row types per point")
-    table = rows.reshape(N0, int(counts[0])).to(torch.int32).contiguous()
-    _TRANSPOSE_CACHE[key] = table
-    return table
+    order, offs = _class_lists(plane_pts.reshape(1, B * deg), N0, global_index=False)
+    return torch.div(order, deg, rounding_mode="floor").to(torch.int32), offs
 
 
 class _IncidenceFn(torch.autograd.Function):
-    """``U = C F`` (triton_bwd.py:300-316): dF = C^T dU, the same kernel over the
-    transposed table."""
+    """The incidence ``U = C F`` as an autograd node (the reference's is
+    triton_bwd.py:300-316).  The map is linear with adjoint C^T, so
+    ``dF_x = sum of dU_h over the row types h through x``: the CSR form of
+    the incidence kernel over C^T's lists, made from the same table in the
+    forward."""
 
     @staticmethod
     def forward(ctx, F, plane_pts, B):
         U = _FWD["incidence"](F, plane_pts, B)
-        ctx.table = _point_planes(plane_pts, F.shape[1])
-        ctx.N0 = F.shape[1]
-        ctx.in_dtype = F.dtype
+        rows, offs = _adjoint_lists(plane_pts, F.shape[1])
+        ctx.save_for_backward(rows, offs)
+        ctx.f_dtype = F.dtype
         return U
 
     @staticmethod
     def backward(ctx, dU):
-        dF = _FWD["incidence"](dU.contiguous().float(), ctx.table, ctx.N0)
-        return dF.to(ctx.in_dtype), None, None
+        rows, offs = ctx.saved_tensors
+        nb, B, R, P = dU.shape
+        N0 = offs.numel() - 1
+        dF = _incidence_rows(dU.float().contiguous(), rows, offs, N0, nb, B, R * P)
+        return dF.view(nb, N0, R, P).to(ctx.f_dtype), None, None
 
 
 def chunk_local(Phi_c, Psi_c, Vb_c, Sin):

@@ -91,6 +91,45 @@ def test_module_parameters_match_reference_init(gold, name):
         assert torch.equal(m.Wd.detach(), g["Wd"])
 
 
+@pytest.mark.parametrize("name", CASES)
+def test_pairs_and_balance_term_on_the_host(gold, name):
+    """The module's straight-through pairs and load-balance term, run on host
+    tensors of the hash that the reference module saw (the oracle's hash_s
+    of the fixture's inputs and parameters): pairs equal to the oracle's
+    (assign.py:257-317 restated; cells exact, weights and their gradients
+    through s within 1e-6) at anneal 1 and 0.5, all pairs and the single
+    chosen cell, planted key columns included; the balance term of both sides
+    equal to the reference module's ``aux`` within 1e-5."""
+    g, meta = _case(gold, name)
+    m, spec = _module(meta)
+    n, h = meta["n"], meta["h"]
+    gen = torch.Generator().manual_seed(5)
+    aux = 0.0
+    for u, plant in ((g["u"][:, :n], True), (g["u"][:, n:], False)):
+        s0 = R.hash_s(u, g["W"], g["gamma"], g["b"], spec.q, h).detach()
+        cols = torch.as_tensor(spec.planted_cols, dtype=torch.long)
+        planted = plant and bool((cols < s0.shape[1]).any())
+        for anneal in (1.0, 0.5):
+            for single in (False, True):
+                m.anneal = anneal
+                s = s0.clone().requires_grad_(True)
+                cells, idx, w, a = m._ste_pairs(s, plant_at=plant, single=single)
+                sr = s0.clone().requires_grad_(True)
+                idx_r, w_r = R.soft_pairs(sr, spec.q, spec.dim, anneal,
+                                          single=single and not planted)
+                if plant:
+                    idx_r, w_r = R.plant_pairs(idx_r, w_r, spec.planted_cols, m.plant_cells)
+                assert torch.equal(idx, idx_r) and torch.equal(cells, idx_r[..., 0])
+                assert (w - w_r).abs().max().item() < 1e-6
+                wt = torch.randn(w.shape, generator=gen, dtype=w.dtype)
+                (w * wt).sum().backward()
+                (w_r * wt).sum().backward()
+                assert (s.grad - sr.grad).abs().max().item() < 1e-6
+        aux = aux + float(m._balance(s0))
+    if "aux" in g:
+        assert abs(aux - float(g["aux"])) < 1e-5
+
+
 def test_grouped_planes_are_the_hyperplanes():
     """Every (direction, offset) row is the solution set of <a_e, x> = o."""
     from smat_attention_amd.assign import grouped_planes
