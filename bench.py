@@ -118,9 +118,9 @@ def make_inputs(nb, T, hd, dtype, seed=0):
     Q = torch.randn(nb, T, hd, generator=gen)
     K = torch.randn(nb, T, hd, generator=gen) * hd ** -0.5
     V = torch.randn(nb, T, hd, generator=gen)
-    phi = make_phi(hd, hd, dtype=torch.float32, seed=0)
-    Phi = phi(Q).to(dtype)
-    Psi = phi(K).to(dtype)
+    W = make_phi(hd, hd, dtype=torch.float32, seed=0).W
+    Phi = (torch.nn.functional.elu(Q @ W.T) + 1).to(dtype)
+    Psi = (torch.nn.functional.elu(K @ W.T) + 1).to(dtype)
     Vb = torch.cat([V, torch.ones(nb, T, 1)], dim=-1).to(dtype)
     return Phi, Psi, Vb
 
@@ -305,46 +305,20 @@ class Events:
         return e0.elapsed_time(e1) / reps * 1e3      # microseconds per launch
 
 
-def kernel_table(spec, Phi, Psi, Vb, reps):
-    """Average duration and algorithmic traffic/work of each stage of the fused
-    forward: pool, incidence, type-major query, and the fused causal pass
-    (chunk-group Gram prepass + group scan + the scan kernel that also adds Y,
-    normalises and writes the output).  The stages run in the forward's order,
-    each bracketed by events on torch's current stream (the kernels' stream),
-    so every stage meets the caches as the forward leaves them (F just written
-    by the pool, U just written by the incidence)."""
-    import torch
-    from smat_attention_amd import attention as A
-    from smat_attention_amd.kernels import hip_fwd as K
+def kernel_table(spec, Phi, Psi, us):
+    """Algorithmic traffic/work of each stage of the one-call forward, priced
+    at ``us``, the stage durations measured in the timed steps: each stage's
+    last kernel launch binds an event to its end (smat_set_stage_events) --
+    the pool, the incidence, the type-major query and the causal pass (the
+    chunk-group Gram prepass, the group scan and the scan kernel that also adds
+    Y, normalises and writes the output) -- so a stage is the time from the
+    previous stage's end to its own (its kernels and the dispatch gap before
+    them)."""
     nb, T, r = Phi.shape
-    p = Vb.shape[-1]
+    p = r + 1
     n, C, N0, B, T_R = spec.n, 128, spec.N0, spec.B, spec.T_R
     eb = Phi.element_size()
     rp4 = r * p * 4
-    out = torch.empty(nb, T, p - 1, device=Phi.device)
-    names = ("pool", "incidence", "query", "causal_scan")
-    s = torch.cuda.current_stream()
-
-    def one(ev):
-        ev[0].record(s)
-        F = K.pool(Psi, Vb, spec.n_P, n, N0)
-        ev[1].record(s)
-        U = A.apply_incidence(F, spec)
-        ev[2].record(s)
-        Y = K.query(Phi[:, n:], U)
-        ev[3].record(s)
-        K.causal_scan(Phi, Psi, Vb, n, C, Y=Y, out=out)
-        ev[4].record(s)
-
-    mk = lambda: [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
-    one(mk())                                     # allocations settle
-    torch.cuda.synchronize()
-    evs = [mk() for _ in range(reps)]
-    for ev in evs:
-        one(ev)
-    torch.cuda.synchronize()
-    us = {k: statistics.fmean(ev[i].elapsed_time(ev[i + 1]) * 1e3 for ev in evs)
-          for i, k in enumerate(names)}
     # algorithmic bytes: each operand read once and each result written once
     rows = {
         "pool": dict(us=us["pool"], bytes=nb * ((n - spec.n_P) * (r + p) * eb + N0 * rp4),
@@ -662,27 +636,47 @@ def main():
                                                     128, r, p) + 256,
                      device=dev, dtype=torch.uint8)
     out = None
-    # bring the GPU's clocks up to their steady state before anything is timed:
-    # about a second of forward calls (untimed), then the W warm-up steps
+    # bring the GPU's clocks and power to the steady state of back-to-back
+    # forwards before anything is timed: about a second of them (untimed, in
+    # bursts of 16 between synchronisations), then the W warm-up steps.  A
+    # forward followed by an idle host gap runs at another power state, and the
+    # first back-to-back forwards after it run up to 20 % slower for ~10 steps.
     t_warm = time.perf_counter()
     while time.perf_counter() - t_warm < args.clock_warmup:
-        A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
+        for _ in range(16):
+            A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
         torch.cuda.synchronize()
     for _ in range(args.warmup):
         out = A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
     torch.cuda.synchronize()
     log(f"[bench] warmup done ({args.clock_warmup:.1f} s of clock warm-up, {args.warmup} steps)")
+    # every timed step binds one event per stage to the end of that stage's
+    # last kernel (smat_set_stage_events); step k's pool runs from step k-1's
+    # last event (the first from one recorded before the loop)
+    from smat_attention_amd.kernels import _lib
+    stages = _lib.STAGES
+    cur = torch.cuda.current_stream()
+    first = torch.cuda.Event(enable_timing=True)
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in stages] for _ in range(args.steps)]
+    for e in [first] + [e for m in marks for e in m]:
+        e.record(cur)                            # create the handles before timing
+    torch.cuda.synchronize()
+    first.record(cur)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        out = A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
+    for m in marks:
+        with _lib.stage_events(m):
+            out = A.smat_attention(Phi, Psi, Vb, spec, workspace=ws)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms = dt / args.steps * 1e3
     tokens_per_s = T / (ms * 1e-3)                # B*T tokens per step, B = 1
     log(f"[bench] {args.steps} steps: {ms:.3f} ms/step, {tokens_per_s / 1e6:.2f} M tokens/s")
     assert torch.isfinite(out).all()
-
-    rows = kernel_table(spec, Phi, Psi, Vb, args.kernel_reps)
+    ends = [first] + [m[-1] for m in marks]
+    stage_us = {k: statistics.fmean((marks[j][i - 1] if i else ends[j]).elapsed_time(marks[j][i])
+                                    for j in range(args.steps)) * 1e3
+                for i, k in enumerate(stages)}
+    rows = kernel_table(spec, Phi, Psi, stage_us)
     for k, v in rows.items():
         log(f"[bench] {k:13s} {v['us']:9.1f} us  {v['GBs']:7.0f} GB/s  {v['TFLOPs']:6.1f} TF/s")
     # the roofline is one kernel's: causal_scan is three launches (the prepass,
@@ -714,13 +708,22 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dom,
                      "achieved": round(drow["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(drow["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": ("rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this "
+                                        "workload (profiles/), scaled by a 1 GiB copy; "
+                                        "reported only while the kernel source's sha256 "
+                                        "matches the one measured, not measured in this run"),
                      "us_per_launch": round(drow["us"], 2),
+                     "timing": "in the timed steps: from the end of the previous stage's "
+                               "kernel to the end of this one, events bound by the launches "
+                               "inside the one-call forward (smat_set_stage_events), mean "
+                               "over the steps",
                      "algorithmic_bytes_per_launch": int(drow["bytes"])},
         "mfma": {"useful_flops": uf, "achieved_TFLOPs": round(uf / (ms * 1e-3) / 1e12, 2),
                  "frac_of_bf16_peak": round(uf / (ms * 1e-3) / (BF16_PEAK_TFLOPS * 1e12), 4),
                  "schedule_roofline_frac": round(max(t_mfma, t_hbm) / (ms * 1e-3), 4),
                  "compulsory_bytes": cb},
         "kernels_us": {k: round(v["us"], 1) for k, v in rows.items()},
+        "stages_sum_ms": round(sum(v["us"] for v in rows.values()) / 1e3, 4),
     }
     if dom == "incidence":
         # priced against HBM, but limited on chip: fp32 vector adds and LDS reads

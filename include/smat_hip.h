@@ -420,6 +420,22 @@ int smat_cell_pool_backward(int dtype, const void* psi, const void* vb, const fl
  */
 int64_t smat_forward_workspace_bytes(int nb, int T, int n, int N0, int B, int n_P,
                                      int C, int r, int p);
+
+/*
+ * Stage marks of smat_forward and smat_forward_fused, for the calling thread.
+ * Stage s is 0 the pool, 1 the incidence, 2 the query, 3 the causal pass; with
+ * n hipEvent_t handles set, each later call binds events[s] to the end of
+ * stage s's last kernel through the launch itself (hipExtLaunchKernelGGL's
+ * stop event: no marker packet between kernels), so the time from events[s-1]
+ * to events[s] is stage s as the one-call forward runs it, kernels plus the
+ * dispatch gaps between them (stage 0: from an event the caller records
+ * before the call).  The device-side counterpart of the timer argument of
+ * smat_attention (src/smat/attention.py:391-455, whose phases lr_pool,
+ * lr_incidence, lr_query and scan + normalise these stages are).  Stages a
+ * call does not run (no recent rows) record nothing.  n = 0 clears them; at
+ * most 8.  The caller keeps the events alive while they are set.
+ */
+int smat_set_stage_events(void* const* events, int n);
 int smat_forward(int dtype, const void* phi, const void* psi, const void* vb,
                  const void* idx, int idx_is_64, const int64_t* indptr, int deg,
                  const int* plane_code, int q,

@@ -143,7 +143,7 @@ static int butterfly_dispatch(const float* X, float* Y, int nb, int N, int64_t r
     auto kern = butterfly_lds_kernel<QQ>;                                                      \
     (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,   \
                               bfy::kLdsBudget);                                                \
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(bfy::kThreads), smem, stream, X, Y, N, \
+    smat::launch(kern, dim3((unsigned)grid), dim3(bfy::kThreads), smem, stream, X, Y, N, \
                        logN, rp, nslices, mode);                                               \
   }
     if (Q == 4) SMAT_BFY(4) else if (Q == 2) SMAT_BFY(2) else SMAT_BFY(1)
@@ -161,16 +161,16 @@ static int butterfly_dispatch(const float* X, float* Y, int nb, int N, int64_t r
   const int64_t rp4 = rp / 4;
   const int64_t npairs = (int64_t)nb * (N / 2) * rp4;
   for (int j = 0; j < logN; ++j) {
-    hipLaunchKernelGGL(butterfly_pass_kernel, dim3((unsigned)((npairs + 255) / 256)), dim3(256), 0,
+    smat::launch(butterfly_pass_kernel, dim3((unsigned)((npairs + 255) / 256)), dim3(256), 0,
                        stream, Y, N, j, rp4, npairs, mode);
   }
   if (mode == 1) {
     const int64_t t1 = (int64_t)nb * (N - 1) * rp4;
     if (t1 > 0)
-      hipLaunchKernelGGL(walsh_finish_kernel, dim3((unsigned)((t1 + 255) / 256)), dim3(256), 0,
+      smat::launch(walsh_finish_kernel, dim3((unsigned)((t1 + 255) / 256)), dim3(256), 0,
                          stream, Y, N, rp4, t1, 0);
     const int64_t t0 = (int64_t)nb * rp4;
-    hipLaunchKernelGGL(walsh_finish_kernel, dim3((unsigned)((t0 + 255) / 256)), dim3(256), 0,
+    smat::launch(walsh_finish_kernel, dim3((unsigned)((t0 + 255) / 256)), dim3(256), 0,
                        stream, Y, N, rp4, t0, 1);
   }
   return launch_status(who);
@@ -235,7 +235,7 @@ extern "C" int smat_incidence_complement(const float* F, float* U, int nb, int N
   const int64_t rp4 = rp / 4;
   const int64_t total = (int64_t)nb * rp4;
   if (total == 0 || B == 0) return SMAT_OK;
-  hipLaunchKernelGGL(complement_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+  smat::launch(complement_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, F, U, N0, B, rp4, total);
   return launch_status("smat_incidence_complement");
 }

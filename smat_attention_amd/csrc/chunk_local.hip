@@ -276,7 +276,7 @@ static int launch_chunk_local(const void* phi, const void* psi, const void* vb, 
   const int vk = rows_vec_ok(psi, k_sb, k_st, eb);
   dim3 grid((unsigned)nbc, (unsigned)((C + cl::kBM - 1) / cl::kBM));
   auto kern = L ? chunk_local_kernel<In, true> : chunk_local_kernel<In, false>;
-  hipLaunchKernelGGL(kern, grid, dim3(cl::kThreads), 0, stream, (const In*)phi, (const In*)psi,
+  smat::launch(kern, grid, dim3(cl::kThreads), 0, stream, (const In*)phi, (const In*)psi,
                      (const In*)vb, sin, L, out, C, r, p, q_sb, q_st, k_sb, k_st, v_sb, v_st, s_sb,
                      s_sr, o_sb, o_st, vq, vk);
   return launch_status(L ? "smat_chunk_local_decay" : "smat_chunk_local");

@@ -202,7 +202,7 @@ extern "C" int smat_featurise(int dtype, const void* q, const void* k, const voi
   const void* kk = have_k ? k : nullptr;
   const void* vv = have_v ? v : nullptr;
 #define SMAT_FT(T_)                                                                            \
-  hipLaunchKernelGGL(featurise_kernel<T_>, dim3(grid), dim3(ft::kThreads), 0, st, (const T_*)q, \
+  smat::launch(featurise_kernel<T_>, dim3(grid), dim3(ft::kThreads), 0, st, (const T_*)q, \
                      (const T_*)kk, (const T_*)vv, (const T_*)W, (const T_*)h, (T_*)phi, (T_*)psi, \
                      (T_*)vb, nb, T, d_qk, r, d_v, kind, q_sb, q_st, k_sb, k_st, v_sb, v_st,     \
                      h_sb, o_sb, o_st, vb_sb, vb_st, ntiles, vec)

@@ -126,7 +126,42 @@ static FwdLayout fwd_layout(int nb, int T, int n, int N0, int B, int n_P, int C,
 
 }  // namespace smat
 
+// Stage marks of the one-call forwards (smat_set_stage_events): for stage s
+// (0 pool, 1 incidence, 2 query, 3 causal pass) events[s], bound by the
+// stage's kernel launches to the end of its last kernel (smat::launch), for
+// the calling thread.
+namespace smat {
+
+constexpr int kMaxStageMarks = 8;
+static thread_local hipEvent_t g_marks[kMaxStageMarks];
+static thread_local int g_nmarks = 0;
+static thread_local int g_stage = -1;          // the marked stage running now, or -1
+
+void stage_launch_events(hipEvent_t* start, hipEvent_t* stop) {
+  *start = nullptr;
+  *stop = (g_stage >= 0 && g_stage < g_nmarks) ? g_marks[g_stage] : nullptr;
+}
+
+// Marks the kernels launched during its lifetime as stage `s`.
+struct StageScope {
+  explicit StageScope(int s) { g_stage = s; }
+  ~StageScope() { g_stage = -1; }
+};
+
+}  // namespace smat
+
 extern "C" const char* smat_last_error(void) { return smat::g_err; }
+
+extern "C" int smat_set_stage_events(void* const* events, int n) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(n >= 0 && n <= kMaxStageMarks && (n == 0 || events), SMAT_EINVAL,
+               "smat_set_stage_events: need 0 <= n <= %d events", kMaxStageMarks);
+  for (int i = 0; i < kMaxStageMarks; ++i) g_marks[i] = i < n ? (hipEvent_t)events[i] : nullptr;
+  g_nmarks = n;
+  g_stage = -1;
+  return SMAT_OK;
+}
 
 extern "C" const char* smat_version(void) { return "0.1 gfx950"; }
 
@@ -201,24 +236,34 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     // channel alone (or zero): the incidence runs with an empty row.
     const bool profiled = n > n_P;
     const char* phi_rec = (const char*)phi + (int64_t)n * q_st * elem_bytes(dtype);
-    rc = pool_dispatch(dtype, psi, vb, F, Fg, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st, part,
-                       part_bytes, st);
+    {
+      StageScope stage(0);
+      rc = pool_dispatch(dtype, psi, vb, F, Fg, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st,
+                         part, part_bytes, st);
+    }
     if (rc) return rc;
     const float* Uq = U;
-    if (!idx)                                        // identity incidence: U = F
-      Uq = F;
-    else if (plane_code && profiled)
-      rc = incidence_plane_dispatch(F, Fg, plane_code, q, U, nb, N0, B, rp, st);
-    else
-      rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
-                              profiled ? deg : 0, U, nb, N0, B, rp, st);
+    {
+      StageScope stage(1);
+      if (!idx)                                      // identity incidence: U = F
+        Uq = F;
+      else if (plane_code && profiled)
+        rc = incidence_plane_dispatch(F, Fg, plane_code, q, U, nb, N0, B, rp, st);
+      else
+        rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
+                                profiled ? deg : 0, U, nb, N0, B, rp, st);
+    }
     if (rc) return rc;
-    rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, q_sb, q_st, (int64_t)T_R * yst,
-                        yst, st);
+    {
+      StageScope stage(2);
+      rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, q_sb, q_st,
+                          (int64_t)T_R * yst, yst, st);
+    }
     if (rc) return rc;
   }
 
   // ---- causal pass ------------------------------------------------------
+  StageScope stage(3);
   if (L.fused) {
     // one kernel: segmented scan, + Y on recent rows, normalise, gate
     return causal_scan_dispatch(dtype, phi, psi, vb, T_R > 0 ? Y : nullptr, g, out, nb, T, n, C,
@@ -372,33 +417,44 @@ extern "C" int smat_forward_fused(int dtype, const void* q, const void* k, const
     it.N0 = N0;
     it.nsplit = 1;
     it.per = 1 << 30;
-    rc = gram_stream_launch_feat(dtype, k, v, F, Fg, it, N0 + (Fg ? 1 : 0), nb, k_sb, k_st, v_sb,
-                                 v_st, (int64_t)N0 * rp, rp, rp, fa, st, "smat_forward_fused");
+    {
+      StageScope stage(0);
+      rc = gram_stream_launch_feat(dtype, k, v, F, Fg, it, N0 + (Fg ? 1 : 0), nb, k_sb, k_st,
+                                   v_sb, v_st, (int64_t)N0 * rp, rp, rp, fa, st,
+                                   "smat_forward_fused");
+    }
     if (rc) return rc;
     const float* Uq = U;
-    if (!idx)
-      Uq = F;
-    else if (plane_code && profiled)
-      rc = incidence_plane_dispatch(F, Fg, plane_code, field_q, U, nb, N0, B, rp, st);
-    else
-      rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
-                              profiled ? deg : 0, U, nb, N0, B, rp, st);
+    {
+      StageScope stage(1);
+      if (!idx)
+        Uq = F;
+      else if (plane_code && profiled)
+        rc = incidence_plane_dispatch(F, Fg, plane_code, field_q, U, nb, N0, B, rp, st);
+      else
+        rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
+                                profiled ? deg : 0, U, nb, N0, B, rp, st);
+    }
     if (rc) return rc;
     const char* q_rec = (const char*)q + (int64_t)n * q_st * 2;
-    if (fused_query_staged(T, n, B)) {
-      void* phi_rec = ws + L.total;                  // (nb, T_R, 128), rows of 128
-      rc = smat_featurise(dtype, q_rec, nullptr, nullptr, W, nullptr, phi_rec, nullptr, nullptr,
-                          nb, T_R, 128, 128, 0, kind, q_sb, q_st, 0, 0, 0, 0, 0,
-                          (int64_t)T_R * 128, 128, 0, 0, stream);
-      if (rc) return rc;
-      rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, (int64_t)T_R * 128, 128,
-                          (int64_t)T_R * yst, yst, st);
-    } else {
-      rc = query_stream_launch_feat(dtype, q_rec, Uq, Y, nb, T_R, B, q_sb, q_st,
-                                    (int64_t)T_R * yst, yst, fa, st);
+    {
+      StageScope stage(2);
+      if (fused_query_staged(T, n, B)) {
+        void* phi_rec = ws + L.total;                // (nb, T_R, 128), rows of 128
+        rc = smat_featurise(dtype, q_rec, nullptr, nullptr, W, nullptr, phi_rec, nullptr,
+                            nullptr, nb, T_R, 128, 128, 0, kind, q_sb, q_st, 0, 0, 0, 0, 0,
+                            (int64_t)T_R * 128, 128, 0, 0, stream);
+        if (rc == SMAT_OK)
+          rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, (int64_t)T_R * 128, 128,
+                              (int64_t)T_R * yst, yst, st);
+      } else {
+        rc = query_stream_launch_feat(dtype, q_rec, Uq, Y, nb, T_R, B, q_sb, q_st,
+                                      (int64_t)T_R * yst, yst, fa, st);
+      }
     }
     if (rc) return rc;
   }
+  StageScope stage(3);
   return causal_scan_run_feat(dtype, q, k, v, T_R > 0 ? Y : nullptr, g, out, nb, T, n, C, q_sb,
                               q_st, k_sb, k_st, v_sb, v_st, (int64_t)T_R * yst, yst, o_sb, o_st,
                               g_sb, fa, ws + L.scan, L.part - L.scan, st);

@@ -203,27 +203,27 @@ static int launch_gram_shape(const void* psi, const void* vb, float* G, float* G
   }
   if (it.nsplit > 1) {
     if (vk && vv)
-      hipLaunchKernelGGL((gram_kernel<In, true, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
+      smat::launch((gram_kernel<In, true, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
                          dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, partials,
                          nullptr, it, r, p, k_sb, k_st, v_sb, v_st, 0, 0, 0);
     else
-      hipLaunchKernelGGL((gram_kernel<In, false, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
+      smat::launch((gram_kernel<In, false, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
                          dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, partials,
                          nullptr, it, r, p, k_sb, k_st, v_sb, v_st, 0, 0, 0);
     int st = launch_status(who);
     if (st != SMAT_OK) return st;
     const int64_t rp = (int64_t)r * p;
-    hipLaunchKernelGGL(gram_reduce_kernel, dim3((unsigned)((rp + 255) / 256), nitems, nb),
+    smat::launch(gram_reduce_kernel, dim3((unsigned)((rp + 255) / 256), nitems, nb),
                        dim3(256), 0, stream, partials, G, G_last, nitems, it.nsplit, rp, g_sb,
                        g_si, gl_sb);
     return launch_status(who);
   }
   if (vk && vv)
-    hipLaunchKernelGGL((gram_kernel<In, true, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
+    smat::launch((gram_kernel<In, true, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, G, G_last,
                        it, r, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb);
   else
-    hipLaunchKernelGGL((gram_kernel<In, false, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
+    smat::launch((gram_kernel<In, false, TW, NCT>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(gr::kThreads), 0, stream, (const In*)psi, (const In*)vb, G, G_last,
                        it, r, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb);
   return launch_status(who);

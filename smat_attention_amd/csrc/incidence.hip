@@ -300,7 +300,7 @@ static int launch_plane(const float* F, const float* F_glob, const int* code, in
                               kPlaneLdsBudget);
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(1024), smem, stream, F, F_glob, code, q,
+  smat::launch(kern, dim3((unsigned)grid), dim3(1024), smem, stream, F, F_glob, code, q,
                      U, N0, B, rp, nslices, total, per_xcd);
   return launch_status("smat_incidence_plane");
 }
@@ -707,7 +707,7 @@ static int launch_wave_q(const float* F, const float* F_glob, const int* code, f
                               inc::kPlaneLdsBudget);
     attr_set[F_glob ? 1 : 0] = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp,
+  smat::launch(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp,
                      nslices, total, per_xcd);
   return launch_status("smat_incidence_plane");
 }
@@ -965,7 +965,7 @@ static int launch_row_q(const float* F, const float* F_glob, const int* code, fl
                               (int)smem);
     attr_set[F_glob ? 1 : 0] = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp,
+  smat::launch(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp,
                      nslices, total, per_xcd);
   return launch_status("smat_incidence_plane");
 }
@@ -1091,7 +1091,7 @@ static int launch_lds(const float* F, const float* F_glob, const void* idx, cons
                         inc::kLdsBudget);
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), smem, stream, F, F_glob,
+  smat::launch(kern, dim3((unsigned)grid), dim3(kThreads), smem, stream, F, F_glob,
                      (const Idx*)idx, indptr, deg, U, N0, B, rp, nslices, total, per_xcd);
   return launch_status("smat_incidence");
 }
@@ -1133,7 +1133,7 @@ int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int
     return SMAT_EUNSUPPORTED;
   }
 #define SMAT_INC_LAUNCH(IDX, VEC)                                                              \
-  hipLaunchKernelGGL((incidence_l2_kernel<IDX, VEC>), dim3((unsigned)grid), dim3(kThreads), 0, \
+  smat::launch((incidence_l2_kernel<IDX, VEC>), dim3((unsigned)grid), dim3(kThreads), 0, \
                      stream, F, F_glob, (const IDX*)idx, indptr, deg, U, N0, B, rp, nslices,   \
                      nhg, total, per_xcd)
   if (idx_is_64) {

@@ -351,15 +351,15 @@ static int launch_query(const void* phi, const float* U, float* Y, int nb, int T
   }
   const int vq = rows_vec_ok(phi, q_sb, q_st, sizeof(In));
   if (r <= 64 && p <= 80)
-    hipLaunchKernelGGL((query_kernel<In, 2, 5, false>), dim3((unsigned)gx, (unsigned)nb),
+    smat::launch((query_kernel<In, 2, 5, false>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
                        q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   else if (r <= 96 && p <= 80)
-    hipLaunchKernelGGL((query_kernel<In, 3, 5, false>), dim3((unsigned)gx, (unsigned)nb),
+    smat::launch((query_kernel<In, 3, 5, false>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
                        q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   else
-    hipLaunchKernelGGL((query_kernel<In, 4, 9, false>), dim3((unsigned)gx, (unsigned)nb),
+    smat::launch((query_kernel<In, 4, 9, false>), dim3((unsigned)gx, (unsigned)nb),
                        dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
                        q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   return launch_status("smat_query");
@@ -379,15 +379,15 @@ static int launch_query_lists(const void* phi, const float* U, float* Y, const i
   if (gx == 0) return SMAT_OK;
   const int vq = rows_vec_ok(phi, 0, q_st, sizeof(In));
   if (r <= 64 && p <= 80)
-    hipLaunchKernelGGL((query_kernel<In, 2, 5, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
+    smat::launch((query_kernel<In, 2, 5, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
                        stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
                        (int64_t)0, y_st, nrb, vq, rows, roffs);
   else if (r <= 96 && p <= 80)
-    hipLaunchKernelGGL((query_kernel<In, 3, 5, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
+    smat::launch((query_kernel<In, 3, 5, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
                        stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
                        (int64_t)0, y_st, nrb, vq, rows, roffs);
   else
-    hipLaunchKernelGGL((query_kernel<In, 4, 9, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
+    smat::launch((query_kernel<In, 4, 9, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
                        stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
                        (int64_t)0, y_st, nrb, vq, rows, roffs);
   return launch_status("smat_query_lists");
@@ -403,10 +403,10 @@ static int query_stream_go(int dtype, const void* phi, const float* U, float* Y,
   const int64_t nitems = (int64_t)nb * B;
   const unsigned grid = (unsigned)std::min<int64_t>(nitems, (int64_t)ncu);
   if (dtype == SMAT_BF16)
-    hipLaunchKernelGGL((query_stream_kernel<bf16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
+    smat::launch((query_stream_kernel<bf16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
                        stream, (const bf16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st, fa);
   else
-    hipLaunchKernelGGL((query_stream_kernel<f16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
+    smat::launch((query_stream_kernel<f16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
                        stream, (const f16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st, fa);
   return launch_status("smat_query");
 }

@@ -422,10 +422,10 @@ static int launch_scan_fused_shape(const void* phi, const void* psi, const void*
                    rows_vec8_ok(vb, a.v_sb, a.v_st);
   dim3 grid((unsigned)ng, (unsigned)nb);
   if (vec)
-    hipLaunchKernelGGL((scan_fused_kernel<In, true, RK, NCT>), grid, dim3(sf::kThreads), 0,
+    smat::launch((scan_fused_kernel<In, true, RK, NCT>), grid, dim3(sf::kThreads), 0,
                        stream, (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a);
   else
-    hipLaunchKernelGGL((scan_fused_kernel<In, false, RK, NCT>), grid, dim3(sf::kThreads), 0,
+    smat::launch((scan_fused_kernel<In, false, RK, NCT>), grid, dim3(sf::kThreads), 0,
                        stream, (const In*)phi, (const In*)psi, (const In*)vb, Sg, Y, gate, out, a);
   return launch_status("smat_causal_scan");
 }

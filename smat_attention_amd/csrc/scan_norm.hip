@@ -155,7 +155,7 @@ int segment_scan_dispatch(const float* D, float* Sin, int nb, int nc, int nc0, i
   if (nb == 0 || nc == 0 || rp == 0) return SMAT_OK;
   // nc0 == 0 or nc0 == nc: one segment.  Segment 1 is [nc0, nc).
   dim3 grid((unsigned)((rp + 255) / 256), (unsigned)nb, 2);
-  hipLaunchKernelGGL(segment_scan_kernel, grid, dim3(256), 0, stream, D, Sin, nc, nc0, rp);
+  smat::launch(segment_scan_kernel, grid, dim3(256), 0, stream, D, Sin, nc, nc0, rp);
   return launch_status("smat_segment_scan");
 }
 
@@ -194,10 +194,10 @@ static int launch_normalise(const float* H, const float* Y, const float* g, Out*
   if (nb == 0 || T == 0) return SMAT_OK;
   dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
   if (eps >= 0.f)
-    hipLaunchKernelGGL((normalise_kernel<true, Out>), grid, dim3(256), 0, stream, H, Y, g, out, T,
+    smat::launch((normalise_kernel<true, Out>), grid, dim3(256), 0, stream, H, Y, g, out, T,
                        n, p, eps, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb);
   else
-    hipLaunchKernelGGL((normalise_kernel<false, Out>), grid, dim3(256), 0, stream, H, Y, g, out, T,
+    smat::launch((normalise_kernel<false, Out>), grid, dim3(256), 0, stream, H, Y, g, out, T,
                        n, p, 0.f, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb);
   return launch_status("smat_normalise");
 }
@@ -219,11 +219,11 @@ static int launch_normalise_bwd(const Din* dout, const float* H, const float* Y,
   if (nb == 0 || T == 0) return SMAT_OK;
   dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
   if (eps >= 0.f)
-    hipLaunchKernelGGL((normalise_bwd_kernel<true, Din>), grid, dim3(256), 0, stream, dout, H, Y,
+    smat::launch((normalise_bwd_kernel<true, Din>), grid, dim3(256), 0, stream, dout, H, Y,
                        g, dH, dg, T, n, p, eps, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st,
                        g_sb);
   else
-    hipLaunchKernelGGL((normalise_bwd_kernel<false, Din>), grid, dim3(256), 0, stream, dout, H, Y,
+    smat::launch((normalise_bwd_kernel<false, Din>), grid, dim3(256), 0, stream, dout, H, Y,
                        g, dH, dg, T, n, p, 0.f, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st,
                        g_sb);
   return launch_status("smat_normalise_backward");
@@ -240,7 +240,7 @@ extern "C" int smat_decay_scan(const float* D, const float* aC, float* Sin, int 
                "smat_decay_scan: bad sizes");
   if (nb == 0 || nc == 0 || rp == 0) return SMAT_OK;
   dim3 grid((unsigned)((rp + 255) / 256), (unsigned)nb);
-  hipLaunchKernelGGL(decay_scan_kernel, grid, dim3(256), 0, (hipStream_t)stream, D, aC, Sin, nc,
+  smat::launch(decay_scan_kernel, grid, dim3(256), 0, (hipStream_t)stream, D, aC, Sin, nc,
                      nc0, rp);
   return launch_status("smat_decay_scan");
 }
@@ -255,7 +255,7 @@ extern "C" int smat_decay_scan_reverse(const float* dSin, const float* aC, float
                "smat_decay_scan_reverse: bad sizes");
   if (nb == 0 || nc == 0 || rp == 0) return SMAT_OK;
   dim3 grid((unsigned)((rp + 255) / 256), (unsigned)nb);
-  hipLaunchKernelGGL(decay_scan_rev_kernel, grid, dim3(256), 0, (hipStream_t)stream, dSin, aC,
+  smat::launch(decay_scan_rev_kernel, grid, dim3(256), 0, (hipStream_t)stream, dSin, aC,
                      dD, nc, nc0, rp);
   return launch_status("smat_decay_scan_reverse");
 }
@@ -294,7 +294,7 @@ extern "C" int smat_segment_scan_reverse(const float* D, float* Sout, int nb, in
                "smat_segment_scan_reverse: need 0 <= nc0 <= nc (nc=%d nc0=%d)", nc, nc0);
   if (nb == 0 || nc == 0 || rp == 0) return SMAT_OK;
   dim3 grid((unsigned)((rp + 255) / 256), (unsigned)nb, 2);
-  hipLaunchKernelGGL(segment_scan_rev_kernel, grid, dim3(256), 0, (hipStream_t)stream, D, Sout, nc,
+  smat::launch(segment_scan_rev_kernel, grid, dim3(256), 0, (hipStream_t)stream, D, Sout, nc,
                      nc0, rp);
   return launch_status("smat_segment_scan_reverse");
 }

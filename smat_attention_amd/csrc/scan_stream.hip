@@ -910,16 +910,16 @@ static void gram_stream_kernel_launch(const void* psi, const void* vb, float* G,
   // the feature map runs for profiles and chunk groups only: no list form
   if (!FEAT && it.mode == 2) {
     if (one)
-      hipLaunchKernelGGL((gram_stream_kernel<In, true, false, true>), grid, blk, 0, stream, k, v,
+      smat::launch((gram_stream_kernel<In, true, false, true>), grid, blk, 0, stream, k, v,
                          G, G_last, it, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb, fa);
     else
-      hipLaunchKernelGGL((gram_stream_kernel<In, false, false, true>), grid, blk, 0, stream, k, v,
+      smat::launch((gram_stream_kernel<In, false, false, true>), grid, blk, 0, stream, k, v,
                          G, G_last, it, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb, fa);
   } else if (one) {
-    hipLaunchKernelGGL((gram_stream_kernel<In, true, FEAT, false>), grid, blk, 0, stream, k, v, G,
+    smat::launch((gram_stream_kernel<In, true, FEAT, false>), grid, blk, 0, stream, k, v, G,
                        G_last, it, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb, fa);
   } else {
-    hipLaunchKernelGGL((gram_stream_kernel<In, false, FEAT, false>), grid, blk, 0, stream, k, v,
+    smat::launch((gram_stream_kernel<In, false, FEAT, false>), grid, blk, 0, stream, k, v,
                        G, G_last, it, p, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb, fa);
   }
 }
@@ -1000,13 +1000,13 @@ static void scan_stream_kernel_launch(const void* phi, const void* psi, const vo
   const In* k = (const In*)psi;
   const In* v = (const In*)vb;
   if constexpr (FEAT)
-    hipLaunchKernelGGL((scan_stream_kernel<In, true, 2, true>), grid, dim3(ss::kThreads), 0,
+    smat::launch((scan_stream_kernel<In, true, 2, true>), grid, dim3(ss::kThreads), 0,
                        stream, q, k, v, Sg, Y, gate, out, a, fa);
   else if (Y || gate)
-    hipLaunchKernelGGL((scan_stream_kernel<In, false, 3, true>), grid, dim3(ss::kThreads), 0,
+    smat::launch((scan_stream_kernel<In, false, 3, true>), grid, dim3(ss::kThreads), 0,
                        stream, q, k, v, Sg, Y, gate, out, a, fa);
   else
-    hipLaunchKernelGGL((scan_stream_kernel<In, false, 3, false>), grid, dim3(ss::kThreads), 0,
+    smat::launch((scan_stream_kernel<In, false, 3, false>), grid, dim3(ss::kThreads), 0,
                        stream, q, k, v, Sg, Y, gate, out, a, fa);
 }
 

@@ -2,6 +2,7 @@
 // per-thread error message, and dtype dispatch.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -28,6 +29,23 @@ int variant(int which);
       return (code);                             \
     }                                            \
   } while (0)
+
+// Stage marks of the one-call forwards (smat_set_stage_events): the events a
+// launch made now binds to its kernel's start and end, or nulls when no marked
+// stage is active on this thread.  Every launch of a marked stage binds the
+// stage's event to its end (the stage's last launch wins); no start events.
+void stage_launch_events(hipEvent_t* start, hipEvent_t* stop);
+
+// Every kernel launch of the forward's kernels goes through here: with stage
+// events active, hipExtLaunchKernelGGL has the launch itself record them, so a
+// stage is timed as its kernels run, with no marker between them.
+template <typename... Formals, typename... Actuals>
+inline void launch(void (*kern)(Formals...), dim3 grid, dim3 block, uint32_t shmem,
+                   hipStream_t st, Actuals... args) {
+  hipEvent_t a = nullptr, b = nullptr;
+  stage_launch_events(&a, &b);
+  hipExtLaunchKernelGGL(kern, grid, block, shmem, st, a, b, 0u, args...);
+}
 
 inline int launch_status(const char* who) {
   hipError_t e = hipGetLastError();

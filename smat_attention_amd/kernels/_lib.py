@@ -42,6 +42,7 @@ SIGNATURES = {
     "smat_last_error": (ctypes.c_char_p, []),
     "smat_version": (ctypes.c_char_p, []),
     "smat_set_variant": (_i, [_i, _i]),
+    "smat_set_stage_events": (_i, [_p, _i]),
     "smat_chunk_local": (_i, [_i, _p, _p, _p, _p, _p, _i64, _i, _i, _i,
                               _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "smat_chunk_states": (_i, [_i, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64, _p]),
@@ -190,6 +191,30 @@ def general_kernel(name: str):
         yield
     finally:
         lib.smat_set_variant(which, prev)
+
+
+STAGES = ("pool", "incidence", "query", "causal_scan")
+
+
+@contextlib.contextmanager
+def stage_events(events):
+    """Within the block, every one-call forward (``smat_forward``,
+    ``smat_forward_fused``) made on this thread binds ``events[i]`` (a
+    ``torch.cuda.Event`` with timing, one per stage of :data:`STAGES`) to the
+    end of stage i's last kernel, through the launch itself
+    (``smat_set_stage_events``).  With an event recorded just before the call,
+    consecutive events bracket each stage as the call ran it."""
+    handles = []
+    for e in events:
+        if not e.cuda_event:
+            e.record()                     # the handle exists once recorded
+        handles.append(e.cuda_event)
+    arr = (ctypes.c_void_p * len(handles))(*handles)
+    call("smat_set_stage_events", arr, len(handles))
+    try:
+        yield
+    finally:
+        call("smat_set_stage_events", None, 0)
 
 
 def stream_of(t: torch.Tensor) -> int:

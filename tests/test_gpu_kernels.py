@@ -899,3 +899,37 @@ def test_forward_identity_incidence_skips_the_gather(dt):
     with pytest.raises(Exception, match="identity incidence"):
         K.forward(Pd, Sd, Wd, None, spec3.uniform_deg, n=spec3.n, n_P=0, N0=spec3.N0,
                   B=spec3.B, chunk=128)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_stage_events_time_the_one_call_forward(fused):
+    """smat_set_stage_events: in a one-call forward (plain and fused, T = 8192,
+    d = 3, head_dim 128) each stage's last launch binds its event to its end:
+    the events come in stage order after one recorded before the call, and the
+    output equals a call without events; cleared, later calls leave the
+    events as they were."""
+    from smat_attention_amd.kernels import _lib
+    _say("stage events", fused)
+    T = 8192
+    spec = build_mask(T, 3, chunk=128)
+    gen = torch.Generator().manual_seed(12)
+    bf = torch.bfloat16
+    Q, K, V = (torch.randn(2, T, 128, generator=gen).to(DEV, bf) for _ in range(3))
+    phi = A.FeatureMap(O.phi_weight(128, 128, dtype=bf, seed=0).to(DEV), "elu1")
+    Phi, Psi, Vb = A.featurise(Q, K, V, phi)
+    run = (lambda: A.smat_attention_fused(Q, K, V, phi, spec)) if fused else \
+        (lambda: A.smat_attention(Phi, Psi, Vb, spec))
+    plain = run()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    with _lib.stage_events(ev[1:]):
+        ev[0].record()
+        got = run()
+    torch.cuda.synchronize()
+    assert torch.equal(got, plain)
+    stage = [ev[i].elapsed_time(ev[i + 1]) for i in range(4)]
+    _say("  stages (ms)", [round(x, 4) for x in stage])
+    assert all(x > 0 for x in stage)
+    stamp = ev[0].elapsed_time(ev[4])
+    run()
+    torch.cuda.synchronize()
+    assert ev[0].elapsed_time(ev[4]) == stamp
