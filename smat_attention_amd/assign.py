@@ -20,16 +20,22 @@ GPU work per call:
 * ``smat_query_lists`` (HIP): ``y_i = Phi_i U_type(i)`` over each type's row
   list (assign.py:437-439, 471-472).
 
-Supported: ``mode`` point/plane (codim 1 or dim), ``src`` hidden/embed/id,
-``shift``, ``plant``, ``freeze``, the linear direction head, ``dir_override``,
-``dir_soft``, ``anneal`` in [0, 1], ``sparse_ops`` (with ``hard_k1``).  Parameters are created in the reference's
-order, so a module built after ``torch.manual_seed(s)`` holds the reference's
-values.  Both reads train, with the reference's gradients: the hash runs
-under torch autograd and the pool, the reads and their gradients run on the
-list and incidence kernels (see ``_forward_grad``), for the dense read at
-any ``anneal`` (the soft phase included), ``dir_soft`` and ``dir_override``,
-and for the ``sparse_ops`` pair path.  Options outside the list
-(``conv_width > 1``, other direction heads, ``delta_updates``) raise
+Supported: ``mode`` point/plane and any codimension 1 .. dim (``codim``: the
+read sums the coset of a codimension-c subspace through the query's cell),
+``src`` hidden/embed/id, ``shift``, ``plant``, ``freeze``, the key convolution
+``kconv`` of ``conv_width > 1`` (created for the caller, as the reference
+does), the ``linear``, ``mlp``, ``delta`` and ``fixed`` direction heads,
+``dir_override``, ``dir_soft``, ``anneal`` in [0, 1], ``sparse_ops`` (with
+``hard_k1``), and the analysis methods ``cells_of``, ``oracle_dir``,
+``agreement`` and ``key_agreement``.  Parameters are created in the
+reference's order, so a module built after ``torch.manual_seed(s)`` holds the
+reference's values.  Both reads train, with the reference's gradients: the
+hash runs under torch autograd and the pool, the reads and their gradients run
+on the list and incidence kernels (see ``_forward_grad``), for the dense read
+at any ``anneal`` (the soft phase included), ``dir_soft`` and
+``dir_override``, and for the ``sparse_ops`` pair path.  ``delta_updates``
+(the reference pools by the gated delta rule of the FLA library,
+``chunk_gated_delta_rule``, src/smat_lm/smat_delta_pool.py) raises
 ``NotImplementedError``.
 """
 from __future__ import annotations
@@ -42,7 +48,7 @@ from .kernels.hip_fwd import _code, _on_gpu, _rows3, call, stream_of
 from .pool_ops import (_class_lists, _f32_rows, _gram_lists, _list_hint, _lists, _read_lists,
                        _read_pairs, _repeat, pool_sorted, read_sorted)
 
-__all__ = ["ContentAssign", "grouped_planes"]
+__all__ = ["ContentAssign", "grouped_planes", "grouped_flats"]
 
 
 def grouped_planes(q: int, dim: int):
@@ -62,6 +68,38 @@ def grouped_planes(q: int, dim: int):
     return dirs, grouped
 
 
+def grouped_flats(q: int, dim: int, codim: int):
+    """(D_c, q^codim, q^(dim-codim)) point indices: every partition of F_q^dim
+    into the cosets of a codimension-``codim`` subspace, the reference's
+    enumeration (assign.py:63-90).  A full-rank codim x dim matrix A over F_q
+    maps point x to the coset A x; the matrices are taken in lexicographic
+    order of their entries (row-major), a partition is kept the first time a
+    matrix induces it, and its cosets are numbered by their smallest point,
+    each listing its points in increasing order.  codim = 1 gives the
+    hyperplane partitions of :func:`grouped_planes` (in another order)."""
+    N0 = q ** dim
+    pts = np.stack([(np.arange(N0) // q ** (dim - 1 - k)) % q for k in range(dim)], 1)
+    n_cos, deg = q ** codim, q ** (dim - codim)
+    weights = q ** np.arange(codim)
+    digits = np.arange(codim * dim)
+    seen, parts = set(), []
+    for code in range(q ** (codim * dim)):
+        A = ((code // q ** (codim * dim - 1 - digits)) % q).reshape(codim, dim)
+        key = ((pts @ A.T) % q) @ weights            # the coset of each point, as a number
+        _, first, inverse = np.unique(key, return_index=True, return_inverse=True)
+        if len(first) != n_cos:
+            continue                                 # A is not of full rank
+        rank = np.empty(n_cos, dtype=np.int64)
+        rank[np.argsort(first)] = np.arange(n_cos)   # cosets by their smallest point
+        label = rank[inverse.reshape(-1)]
+        sig = label.tobytes()
+        if sig in seen:
+            continue
+        seen.add(sig)
+        parts.append(np.argsort(label, kind="stable").reshape(n_cos, deg))
+    return np.stack(parts)
+
+
 def _straight_through(value: float, surrogate):
     """A tensor whose forward value is ``value`` everywhere and whose gradient
     is that of ``surrogate``: value + (surrogate - surrogate.detach())."""
@@ -79,16 +117,11 @@ class ContentAssign(nn.Module):
                  freeze=False, shift=0, codim=None, vocab=None, conv_width=0,
                  dir_head="linear", dir_hidden=512, dir_window=4, dir_soft=False):
         super().__init__()
-        if conv_width > 1:
-            raise NotImplementedError("ContentAssign: conv_width > 1 (learned key convolution)")
-        if dir_head != "linear":
-            raise NotImplementedError(f"ContentAssign: dir_head={dir_head!r}; only the linear "
-                                      f"direction head")
+        if dir_head not in ("linear", "mlp", "delta", "fixed"):
+            raise ValueError(f"ContentAssign: unknown dir_head {dir_head!r}")
         self.codim = None if codim is None else int(codim)
         if self.codim is not None:
             assert 1 <= self.codim <= int(spec.dim), (self.codim, spec.dim)
-            if self.codim not in (1, int(spec.dim)):
-                raise NotImplementedError("ContentAssign: codimension between 1 and dim")
             mode = "point" if self.codim == int(spec.dim) else "plane"
         assert spec.kind == "geometric" and spec.dim >= 1
         self.h = n_heads
@@ -96,6 +129,14 @@ class ContentAssign(nn.Module):
         self.mode, self.plant = mode, plant
         self.src, self.freeze, self.shift = src, freeze, int(shift)
         self.conv_width = int(conv_width)
+        if self.conv_width > 1:
+            # the key-side hash input's depthwise causal convolution, uniform over
+            # its lags at the start; the caller applies it (key_src), as in the
+            # reference, which creates it here (so its draw precedes W's)
+            self.kconv = nn.Conv1d(d_model, d_model, self.conv_width, groups=d_model, bias=False)
+            with torch.no_grad():
+                self.kconv.weight.fill_(1.0 / self.conv_width)
+            self.kconv.weight.requires_grad_(not freeze)
         if src == "id":
             assert vocab is not None, "the id hash needs the vocabulary size"
             g = torch.Generator().manual_seed(1234)
@@ -108,16 +149,47 @@ class ContentAssign(nn.Module):
         self.gamma = nn.Parameter(torch.ones(n_heads, self.dim), requires_grad=not freeze)
         self.b = nn.Parameter(torch.zeros(n_heads, self.dim), requires_grad=not freeze)
         if self.mode == "plane":
-            dirs, grouped = grouped_planes(self.q, self.dim)
+            if self.codim in (None, 1):
+                grouped = grouped_planes(self.q, self.dim)[1]
+            else:
+                grouped = grouped_flats(self.q, self.dim, self.codim)
             self.D, self.n_cosets = int(grouped.shape[0]), int(grouped.shape[1])
-            self.dir_head = dir_head
+            self.dir_head = dir_head if self.codim in (None, 1) else "linear"
             self.dir_soft = bool(dir_soft)
-            # the reference draws this projection twice for the linear head
-            # (assign.py:201-203 and :237-238); the second draw is the one kept
+            # the linear projection of the direction logits; the sparse read
+            # scores directions with it whatever the head (assign.py:201-203)
             self.Wd = nn.Parameter(torch.randn(n_heads, self.D, d_model) * d_model ** -0.5,
                                    requires_grad=not freeze)
-            self.Wd = nn.Parameter(torch.randn(n_heads, self.D, d_model) * d_model ** -0.5,
-                                   requires_grad=not freeze)
+            if self.dir_head in ("delta", "fixed"):
+                # logits summed over the previous dir_window tokens' cells:
+                # Wdelta[head, lag, cell difference, direction] (assign.py:204-233)
+                self.win = int(dir_window)
+                pts = np.stack([(np.arange(self.N0) // self.q ** (self.dim - 1 - j)) % self.q
+                                for j in range(self.dim)], 1)
+                place = self.q ** np.arange(self.dim - 1, -1, -1)
+                diff = ((pts[:, None, :] - pts[None, :, :]) % self.q) @ place
+                self.register_buffer("diff_tab", torch.as_tensor(diff, dtype=torch.long))
+                self.Wdelta = nn.Parameter(torch.zeros(n_heads, self.win, self.N0, self.D),
+                                           requires_grad=not freeze)
+                nn.init.normal_(self.Wdelta, std=0.02)
+                if self.dir_head == "fixed":
+                    # 1 where direction e annihilates the difference: a fixed map
+                    dirs = grouped_planes(self.q, self.dim)[0]
+                    ind = torch.as_tensor((pts @ dirs.T) % self.q == 0, dtype=torch.float32)
+                    with torch.no_grad():
+                        self.Wdelta.copy_(ind.expand(n_heads, self.win, self.N0, self.D))
+                    self.Wdelta.requires_grad_(False)
+            elif self.dir_head == "mlp":
+                self.Wd1 = nn.Parameter(torch.randn(n_heads, dir_hidden, d_model) * d_model ** -0.5,
+                                        requires_grad=not freeze)
+                self.bd1 = nn.Parameter(torch.zeros(n_heads, dir_hidden), requires_grad=not freeze)
+                self.Wd = nn.Parameter(torch.randn(n_heads, self.D, dir_hidden)
+                                       * dir_hidden ** -0.5, requires_grad=not freeze)
+            else:
+                # the reference draws the linear projection a second time
+                # (assign.py:236-238); the second draw is the one kept
+                self.Wd = nn.Parameter(torch.randn(n_heads, self.D, d_model) * d_model ** -0.5,
+                                       requires_grad=not freeze)
             M = np.zeros((self.D, self.n_cosets, self.N0), dtype=np.float32)
             for e in range(self.D):
                 for o in range(self.n_cosets):
@@ -132,7 +204,7 @@ class ContentAssign(nn.Module):
                              torch.as_tensor([self.q ** (self.dim - l)
                                               for l in range(1, self.dim + 1)], dtype=torch.long))
         self.anneal = 1.0
-        self.last_soft_q = None
+        self._soft_src = {"q": None, "k": None}
         self.last_hard_k = None
         self.last_hard_q = None
         self.probe = False
@@ -176,6 +248,148 @@ class ContentAssign(nn.Module):
         nb, L = ids.shape
         return self.id_cell[ids].permute(0, 2, 1).reshape(nb * self.h, L)
 
+    # --------------------------------------------------------- soft cells
+    def _soft_cells(self, side):
+        """The dense soft cell distribution (B, L, N0) of the last forward's
+        query (``side`` "q") or key ("k", before planting) tokens: each token
+        spreads over the 2^dim cells around its hash with the interpolation
+        weights prod_k (1 - f_k or f_k), no straight-through part (the
+        reference's ``_soft``, assign.py:266, 291).  Recomputed from the
+        recorded hash input, so it carries gradients to the hash parameters
+        (and the input) when grad mode is on; for the id hash the one-hot of
+        the table cell."""
+        rec = self._soft_src.get(side)
+        if rec is None:
+            return None
+        kind, t = rec
+        if kind == "cells":
+            return torch.nn.functional.one_hot(t, self.N0).float()
+        s = self._soft_hash(t)
+        B, L, dim = s.shape
+        q = self.q
+        j = s.detach().floor()
+        f = s - j
+        lo, hi = j.long(), (j.long() + 1).clamp(max=q - 1)
+        out = torch.zeros(B, L, self.N0, device=s.device, dtype=s.dtype)
+        for m in range(1 << dim):
+            cell, wt = 0, None
+            for k in range(dim):
+                high = (m >> k) & 1
+                cell = cell + (hi if high else lo)[..., k] * q ** (dim - 1 - k)
+                ck = f[..., k] if high else 1.0 - f[..., k]
+                wt = ck if wt is None else wt * ck
+            out = out.scatter_add(-1, cell.unsqueeze(-1), wt.unsqueeze(-1))
+        return out
+
+    @property
+    def last_soft_q(self):
+        """Soft cell distribution (nb*h, T_R, N0) of the last forward's recent
+        queries (the reference's ``last_soft_q``); None after a sparse_ops
+        forward, as there."""
+        return self._soft_cells("q")
+
+    @last_soft_q.setter
+    def last_soft_q(self, value):
+        self._soft_src["q"] = None if value is None else ("cells", value.argmax(-1))
+
+    @property
+    def last_soft_k(self):
+        """Soft cell distribution (nb*h, n, N0) of the last forward's distant
+        keys, before planting.  The reference reads this attribute in
+        ``key_agreement`` but never assigns it (so its method raises); here the
+        forward records it like the query side."""
+        return self._soft_cells("k")
+
+    @last_soft_k.setter
+    def last_soft_k(self, value):
+        self._soft_src["k"] = None if value is None else ("cells", value.argmax(-1))
+
+    # ------------------------------------------------------------ analysis
+    def cells_of(self, v):
+        """``(..., d_model) -> (..., h)`` cell index of every head, for one
+        hidden state at a time (assign.py:319-328): the hash of the forward,
+        evaluated in the reference's op order (torch, on v's device)."""
+        Wn = self.W / self.W.norm(dim=-1, keepdim=True).clamp_min(1e-6)
+        z = torch.einsum("...m,hkm->...hk", self.ln(v), Wn) * self.gamma + self.b
+        dig = (torch.special.ndtr(z) * self.q).clamp(0.0, self.q - 1e-4).floor().long()
+        place = torch.tensor([self.q ** (self.dim - 1 - k) for k in range(self.dim)],
+                             device=v.device)
+        return (dig * place).sum(-1)
+
+    def oracle_dir(self, cells):
+        """cells (B, L, k) -> (B, L): the first direction along which all k cells
+        share their offset (the hyperplane of that direction through them), 0 if
+        none does (assign.py:330-344)."""
+        dirs = grouped_planes(self.q, self.dim)[0]
+        pts = np.stack([(np.arange(self.N0) // self.q ** (self.dim - 1 - j)) % self.q
+                        for j in range(self.dim)], 1)
+        offset = torch.as_tensor((pts @ dirs.T) % self.q, device=cells.device)   # (N0, D)
+        per = offset[cells]                                                      # (B, L, k, D)
+        common = (per == per[..., :1, :]).all(-2)                                # (B, L, D)
+        first = common.int().argmax(-1)
+        return torch.where(common.any(-1), first, torch.zeros_like(first))
+
+    def _route_loss(self, soft, src, target_cells, valid):
+        """-(mean over valid pairs) of log p(target cell): the cell distribution
+        ``soft`` (B, m, N0) of token ``src`` at the cell ``target_cells`` (B, P)
+        (the negative log-likelihood of the routing, floored at 1e-9); pairs are
+        (nb, P), repeated over the h heads of each sequence."""
+        nb = src.shape[0]
+        rep = soft.shape[0] // nb
+        i = src.repeat_interleave(rep, 0).clamp_min(0)
+        tgt = target_cells.clamp_min(0)
+        v = valid.repeat_interleave(rep, 0).to(soft.dtype)
+        p = soft.gather(1, i.unsqueeze(-1).expand(-1, -1, self.N0))
+        lp = p.gather(-1, tgt.unsqueeze(-1)).squeeze(-1).clamp_min(1e-9).log()
+        return -(lp * v).sum() / v.sum().clamp_min(1.0)
+
+    def agreement(self, pairs, valid):
+        """Routing term of the query side (assign.py:499-515): pairs (nb, P, 2)
+        of (recent query i, distant position j) and valid (nb, P); the query's
+        soft cell distribution should put its mass on the hard cell of the
+        distant key j.  None before a forward that records them."""
+        soft = self.last_soft_q
+        if soft is None or self.last_hard_k is None:
+            return None
+        rep = soft.shape[0] // pairs.shape[0]
+        j = pairs[..., 1].repeat_interleave(rep, 0).clamp_min(0)
+        return self._route_loss(soft, pairs[..., 0], self.last_hard_k.gather(1, j), valid)
+
+    def key_agreement(self, pay_pos, key_cells, valid):
+        """Routing term of the key side (assign.py:476-497): a payload at
+        distant position pay_pos (nb, P) should be filed under key_cells
+        (nb, P, detached targets); valid (nb, P)."""
+        soft = self.last_soft_k
+        if soft is None:
+            return None
+        rep = soft.shape[0] // pay_pos.shape[0]
+        return self._route_loss(soft, pay_pos, key_cells.repeat_interleave(rep, 0), valid)
+
+    def _dir_logits(self, u, n, ids=None):
+        """Direction logits (nb*h, T_R, D) of the recent queries for the dense
+        plane read (assign.py:445-458): linear in the layer input, a one-layer
+        gelu network (``mlp``), or (``delta`` / ``fixed``) the sum over the
+        previous ``dir_window`` tokens of Wdelta[head, lag, cell difference],
+        cells from the id table."""
+        T_R = u.shape[1] - n
+        head = getattr(self, "dir_head", "linear")
+        if head in ("delta", "fixed"):
+            assert ids is not None, "the delta direction head needs token ids"
+            nb = ids.shape[0]
+            cq = self.id_cell[ids[:, n:]]                                  # (nb, T_R, h)
+            hsel = torch.arange(self.h, device=ids.device)[None, None, :]
+            dl = 0.0
+            for lag in range(1, self.win + 1):
+                cs = self.id_cell[ids[:, n - lag:ids.shape[1] - lag]]
+                dl = dl + self.Wdelta[:, lag - 1][hsel, self.diff_tab[cs, cq]]
+            return dl.permute(0, 2, 1, 3).reshape(nb * self.h, T_R, self.D)
+        if head == "mlp":
+            hid = torch.einsum("blm,hkm->bhlk", u[:, n:], self.Wd1) + self.bd1[None, :, None, :]
+            dl = torch.einsum("bhlk,hek->bhle", torch.nn.functional.gelu(hid), self.Wd)
+        else:
+            dl = torch.einsum("blm,hem->bhle", u[:, n:], self.Wd)
+        return dl.reshape(u.shape[0] * self.h, T_R, self.D)
+
     # ------------------------------------------------------------- the branch
     def forward(self, u, Phi, Psi, Vb, n, emb=None, key_src=None, key_w=None,
                 dir_override=None, ids=None):
@@ -197,6 +411,7 @@ class ContentAssign(nn.Module):
             ik = ids if not self.shift else torch.cat(
                 [ids.new_zeros(ids.shape[0], self.shift), ids[:, :-self.shift]], dim=1)
             ck, cq = self._cells_id(ik[:, :n]), self._cells_id(ids[:, n:])
+            self._soft_src = {"q": ("cells", cq), "k": ("cells", ck)}
             self.aux = None
         else:
             h = u if (self.src == "hidden" or emb is None) else emb
@@ -207,10 +422,11 @@ class ContentAssign(nn.Module):
             ck = self._cells(hk[:, :n], plant_at=True, tok_w=key_w)
             aux_k = self.aux
             cq = self._cells(h[:, n:])
+            self._soft_src = {"q": ("hash", h[:, n:]), "k": ("hash", hk[:, :n])}
             self.aux = None if self.freeze else aux_k + self.aux
         self.last_hard_k = ck.detach()
         self.last_hard_q = cq.detach()
-        return self._read(u, Phi, Psi, Vb, n, ck, cq, dir_override)
+        return self._read(u, Phi, Psi, Vb, n, ck, cq, dir_override, ids)
 
     # ------------------------------------------------------------ training
     def _soft_hash(self, u):
@@ -314,6 +530,7 @@ class ContentAssign(nn.Module):
             ik = ids if not self.shift else torch.cat(
                 [ids.new_zeros(ids.shape[0], self.shift), ids[:, :-self.shift]], dim=1)
             ck, cq = self._cells_id(ik[:, :n]), self._cells_id(ids[:, n:])
+            self._soft_src = {"q": ("cells", cq), "k": ("cells", ck)}
             self.aux = None
             one = lambda c: torch.ones(c.shape + (1,), device=u.device)
             return ck, ck.unsqueeze(-1), one(ck), cq, cq.unsqueeze(-1), one(cq)
@@ -336,6 +553,9 @@ class ContentAssign(nn.Module):
                                                   tok_w=key_w, single=single)
             cq, idxq, wq, aux_q = self._ste_pairs(self._soft_hash(h[:, n:]), single=single)
         self.aux = None if self.freeze else aux_k + aux_q
+        # the sparse read forms no dense soft distribution (assign.py:289-291)
+        self._soft_src = ({"q": None, "k": None} if single else
+                          {"q": ("hash", h[:, n:]), "k": ("hash", hk[:, :n])})
         return ck, idxk, wk, cq, idxq, wq
 
     def _fused_pairs_ok(self, h, key_w, single):
@@ -448,7 +668,7 @@ class ContentAssign(nn.Module):
             we = torch.zeros(nbh, T_R, self.D, device=dev).scatter_(
                 -1, dir_override.reshape(nbh, T_R, 1).long(), 1.0)
         else:
-            dl = torch.einsum("blm,hem->bhle", u[:, n:], self.Wd).reshape(nbh, T_R, self.D)
+            dl = self._dir_logits(u, n, ids)
             self.last_dir_logits = dl
             pe = torch.softmax(dl, dim=-1)
             if getattr(self, "dir_soft", False) and self.training:
@@ -459,7 +679,7 @@ class ContentAssign(nn.Module):
         return _PlaneRead.apply(Phi_r, U, we.float(), wq, idxq, self.coset_of.to(dev),
                                 self.n_cosets)
 
-    def _read(self, u, Phi, Psi, Vb, n, ck, cq, dir_override):
+    def _read(self, u, Phi, Psi, Vb, n, ck, cq, dir_override, ids=None):
         nbh, T, r = Phi.shape
         p = Vb.shape[-1]
         T_R = T - n
@@ -485,11 +705,14 @@ class ContentAssign(nn.Module):
             pts = self.coset_pts.to(dev)
             call("smat_incidence", F.data_ptr(), None, pts.data_ptr(), 0, None, pts.shape[1],
                  U.data_ptr(), nbh, N0, nrows, r * p, stream_of(F))
+            if dir_override is None:
+                dir_override = getattr(self, "dir_ovr", None)
             if dir_override is not None:
                 e_star = dir_override.reshape(nbh, T_R).long()
             else:
-                dl = torch.einsum("blm,hem->bhle", u[:, n:].float(), self.Wd.float())
-                e_star = dl.reshape(nbh, T_R, self.D).argmax(-1)
+                dl = self._dir_logits(u, n, ids)
+                self.last_dir_logits = dl
+                e_star = dl.argmax(-1)
             typ = e_star * self.n_cosets + self.coset_of.to(dev)[e_star, cq]
             ntypes = nrows
         order, roffs = _class_lists(typ, ntypes)

@@ -251,6 +251,8 @@ def test_content_assign_refuses_cpu_tensors_and_unbuilt_options():
     m.delta_updates = True
     with pytest.raises(NotImplementedError, match="delta"):
         m(u, Phi, Phi, Vb, 256)
+    with pytest.raises(ValueError, match="dir_head"):
+        ContentAssign(2, 32, spec, mode="plane", dir_head="attention")
 
 
 @pytest.mark.gpu
@@ -525,3 +527,177 @@ def test_straight_through_gradient_reaches_the_hash(mode):
     Phi, Psi = torch.rand(6, 512, 5, generator=g).to(dev), torch.rand(6, 512, 5, generator=g).to(dev)
     ca(u, Phi, Psi, torch.randn(6, 512, 4, generator=g).to(dev), spec.n).sum().backward()
     assert ca.W.grad.abs().max().item() > 0
+
+
+# ---------------------------------------------------------------------------
+# options beyond the point / plane reads: key convolution, direction heads,
+# codimension, analysis methods (tests/golden/make_assign_golden_ext.py)
+# ---------------------------------------------------------------------------
+
+GOLD_EXT = os.path.join(os.path.dirname(__file__), "golden", "assign_golden_ext.npz")
+EXT_CASES = {
+    "T512_d3_point_conv4": (512, 3, dict(mode="point", conv_width=4)),
+    "T512_d3_plane_mlp": (512, 3, dict(mode="plane", dir_head="mlp", dir_hidden=32)),
+    "T512_d3_plane_delta": (512, 3, dict(mode="plane", src="id", vocab=64, dir_head="delta",
+                                         dir_window=4)),
+    "T512_d3_plane_fixed": (512, 3, dict(mode="plane", src="id", vocab=64, dir_head="fixed",
+                                         dir_window=3)),
+    "T512_d4_codim2": (512, 4, dict(codim=2)),
+    "T512_d4_codim3": (512, 4, dict(codim=3)),
+}
+EXT_H, EXT_DM = 2, 32
+
+
+@pytest.fixture(scope="module")
+def gold_ext():
+    return np.load(GOLD_EXT)
+
+
+def _ext(gold_ext, name):
+    return {k.split("/", 1)[1]: torch.from_numpy(gold_ext[k]) for k in gold_ext.files
+            if k.startswith(name + "/")}
+
+
+def _ext_module(name, device="cpu"):
+    from smat_attention_amd.assign import ContentAssign
+    T, d, opts = EXT_CASES[name]
+    spec = build_mask(T, d, chunk=64)
+    torch.manual_seed(1000)
+    m = ContentAssign(EXT_H, EXT_DM, spec, **opts)
+    m.eval()
+    return m.to(device), spec
+
+
+@pytest.mark.parametrize("name", sorted(EXT_CASES))
+def test_option_parameters_match_reference_init(gold_ext, name):
+    """Built after the same seed, every parameter and table the option adds
+    (the key convolution, the mlp head's layers, Wdelta and the fixed
+    indicator, the id table, the coset matrix M of a codimension-2 read over
+    F_5^3) equals the reference module's."""
+    g = _ext(gold_ext, name)
+    m, _ = _ext_module(name)
+    params = dict(m.named_parameters())
+    params.update(dict(m.named_buffers()))
+    want = {k[len("param."):]: v for k, v in g.items() if k.startswith("param.")}
+    assert set(want) <= set(params), set(want) - set(params)
+    for k, v in want.items():
+        assert torch.equal(params[k].detach().to(v.dtype), v), k
+
+
+def test_grouped_flats_are_coset_partitions():
+    """Every partition of grouped_flats(5, 3, 2) is the set of cosets of a
+    1-dimensional subspace of F_5^3 (the line through 0 in the direction of the
+    difference of two points of a coset): 31 distinct partitions, one per
+    line through the origin, of 25 cosets of 5 points each; codim 1 gives the
+    hyperplane partitions of grouped_planes."""
+    from smat_attention_amd.assign import grouped_flats, grouped_planes
+    q, dim = 5, 3
+    g = grouped_flats(q, dim, 2)
+    assert g.shape == (31, 25, 5)
+    pts = np.stack([(np.arange(q ** dim) // q ** (dim - 1 - k)) % q for k in range(dim)], 1)
+    seen = set()
+    for part in g:
+        assert sorted(part.reshape(-1).tolist()) == list(range(q ** dim))
+        d0 = (pts[part[0, 1]] - pts[part[0, 0]]) % q
+        for coset in part:
+            diffs = (pts[coset] - pts[coset[0]]) % q
+            # every point of the coset is the first plus a multiple of d0
+            assert all(any(np.array_equal(x, (t * d0) % q) for t in range(q)) for x in diffs)
+        seen.add(frozenset(frozenset(c.tolist()) for c in part))
+    assert len(seen) == 31
+    hp = {frozenset(frozenset(c.tolist()) for c in part) for part in grouped_planes(q, dim)[1]}
+    assert {frozenset(frozenset(c.tolist()) for c in part)
+            for part in grouped_flats(q, dim, 1)} == hp
+
+
+def test_cells_of_and_oracle_dir_match_reference(gold_ext):
+    """cells_of (the hash of one hidden state per head) and oracle_dir (the
+    first direction whose offsets agree over a set of cells) equal the
+    reference module's on the fixture's inputs, for sets of 1, 2 and 3 cells."""
+    from smat_attention_amd.assign import ContentAssign
+    g = _ext(gold_ext, "T512_d3_analysis")
+    spec = build_mask(512, 3, chunk=64)
+    torch.manual_seed(1000)
+    m = ContentAssign(EXT_H, EXT_DM, spec, mode="plane")
+    assert torch.equal(m.cells_of(g["cells_v"]), g["cells_of"])
+    for k in (1, 2, 3):
+        assert torch.equal(m.oracle_dir(g[f"oracle_cells{k}"]), g[f"oracle_dir{k}"]), k
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(EXT_CASES))
+def test_options_forward_and_gradients_on_gpu(gold_ext, name):
+    """The hard read with each option on the GPU against the reference
+    module's output (1e-5 relative) and the gradients of (y * R).sum() with
+    respect to Phi, Psi, Vb, the layer input and every trained parameter
+    (1e-4 relative): the mlp and delta direction heads (the fixed head's
+    frozen indicator), the codimension-2 coset read and the point read of
+    codimension dim, and a module with the key convolution."""
+    dev = torch.device("cuda:0")
+    g = _ext(gold_ext, name)
+    gin = _ext(gold_ext, "inputs")
+    m, spec = _ext_module(name, dev)
+    n = spec.n
+    kw = {"ids": g["ids"].to(dev)} if "ids" in g else {}
+    xs = [gin[k].to(dev) for k in ("u", "Phi", "Psi", "Vb")]
+    with torch.no_grad():
+        y = m(*xs, n, **kw).cpu()
+    rel = lambda a, b: ((a.double() - b.double()).abs().max() / b.abs().max()).item()
+    assert rel(y, g["y"]) < 1e-5
+    xs = [x.clone().requires_grad_(True) for x in xs]
+    m.zero_grad()
+    yg = m(*xs, n, **kw)
+    assert rel(yg.detach().cpu(), g["y"]) < 1e-5
+    (yg * g["R"].to(dev)).sum().backward()
+    for key, x in zip(("u", "Phi", "Psi", "Vb"), xs):
+        if f"grad.{key}" in g:
+            assert rel(x.grad.cpu(), g[f"grad.{key}"]) < 1e-4, key
+    params = dict(m.named_parameters())
+    for k, v in g.items():
+        if k.startswith("grad.") and k[5:] in params:
+            assert rel(params[k[5:]].grad.cpu(), v) < 1e-4, k
+
+
+@pytest.mark.gpu
+def test_agreement_terms_on_gpu(gold_ext):
+    """agreement (the query side's routing term) after a forward of the d = 3
+    plane read: value within 1e-5 and its gradients to W, gamma and b within
+    1e-4 of the reference module's.  key_agreement reads the key side's soft
+    distribution, which the reference never records: with the recent half of
+    the layer input equal to the distant half, the two sides' distributions
+    are equal, and key_agreement at payload positions J filed under their
+    hard cells equals agreement over the pairs (J, J)."""
+    from smat_attention_amd.assign import ContentAssign
+    dev = torch.device("cuda:0")
+    g = _ext(gold_ext, "T512_d3_analysis")
+    gin = _ext(gold_ext, "inputs")
+    spec = build_mask(512, 3, chunk=64)
+    n = spec.n
+    torch.manual_seed(1000)
+    m = ContentAssign(EXT_H, EXT_DM, spec, mode="plane").to(dev)
+    m.eval()
+    xs = [gin[k].to(dev) for k in ("u", "Phi", "Psi", "Vb")]
+    m(*xs, n)
+    assert torch.equal(m.last_hard_k.cpu(), g["hard_k"])
+    a = m.agreement(g["pairs"].to(dev), g["valid"].to(dev))
+    assert abs(a.item() - g["agreement"].item()) < 1e-5 * max(1.0, abs(g["agreement"].item()))
+    a.backward()
+    for k in ("W", "gamma", "b"):
+        want = g[f"grad.{k}"]
+        got = getattr(m, k).grad.cpu()
+        assert ((got - want).abs().max() / want.abs().max()).item() < 1e-4, k
+    # the key side, pinned through the query side
+    torch.manual_seed(5)
+    m1 = ContentAssign(1, EXT_DM, spec, mode="plane").to(dev)
+    m1.eval()
+    u = xs[0][:, :n].repeat(1, 2, 1)                       # recent half == distant half
+    Phi, Psi, Vb = (x[:1] for x in xs[1:])
+    with torch.no_grad():
+        m1(u, Phi, Psi, Vb, n)
+        assert torch.equal(m1.last_soft_k, m1.last_soft_q)
+        J = torch.randint(0, n, (1, 9), generator=torch.Generator().manual_seed(6)).to(dev)
+        valid = torch.ones(1, 9, dtype=torch.bool, device=dev)
+        C = m1.last_hard_k.gather(1, J)
+        ka = m1.key_agreement(J, C, valid)
+        qa = m1.agreement(torch.stack([J, J], -1), valid)
+    assert torch.isfinite(ka) and ka.item() == qa.item()
