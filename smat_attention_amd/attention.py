@@ -569,8 +569,14 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
         t is not None and t.requires_grad for t in (Phi, Psi, Vb, g))
     if wants_grad and not _no_grad_fn:
         if return_parts or timer is not None:
-            raise NotImplementedError(f"{who}: return_parts/timer are forward-only; call "
-                                      f"under torch.no_grad() or on detached inputs")
+            if not plain or spec.plane_pts_t is None:
+                raise NotImplementedError(
+                    f"{who}: return_parts/timer under autograd are provided for the pooled "
+                    f"schedule of a geometric mask; the {long_range} schedule"
+                    f"{' of the endpoint mask' if endpoint else ''} records them under "
+                    f"torch.no_grad() or on detached inputs")
+            return _staged_with_grad(Phi, Psi, Vb, spec, C, g,
+                                     timer or (lambda name: nullcontext()), return_parts)
         if endpoint:
             from .kernels.hip_bwd import EndpointAttentionFunction
             return EndpointAttentionFunction.apply(Phi, Psi, Vb, g, spec, C, long_range)
@@ -630,6 +636,35 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
         parts.update(U=U, Y_lr=Y_lr, H=Hfull)
         return out, parts
     return out
+
+
+def _staged_with_grad(Phi, Psi, Vb, spec, C, g, tm, return_parts):
+    """The pooled schedule phase by phase, each phase an autograd node on the
+    HIP kernels, for a differentiable call that asks for its parts or times its
+    phases (the reference's torch path does both under autograd,
+    attention.py:391-455): the pool (and the global channel's rank-one term,
+    a pool of the first n_P tokens into one profile), the incidence, the
+    type-major query, the segmented causal scan and the division.  The parts
+    are part of the graph, as the reference's are."""
+    from .kernels import hip_bwd as HB
+    n, n_P, N0, B = spec.n, spec.n_P, spec.N0, spec.B
+    with tm("lr_pool"):
+        F = HB.pool(Psi, Vb, n_P, n, N0)
+        F_glob = HB.pool(Psi, Vb, 0, n_P, 1)[:, 0] if n_P else None
+    with tm("lr_incidence"):
+        U = HB.incidence(F, spec.plane_pts_t, B)
+        if F_glob is not None:
+            U = U + F_glob.unsqueeze(1)
+    with tm("lr_query"):
+        Y_lr = HB.QueryFunction.apply(Phi[:, n:], U) if Phi.shape[1] > n else None
+    with tm("scan"):
+        H = segmented_causal_scan(Phi, Psi, Vb, n=n, chunk=C)
+    with tm("normalise"):
+        out = HB.NormaliseFunction.apply(H, Y_lr, g, n)
+    if not return_parts:
+        return out
+    Hfull = H if Y_lr is None else torch.cat([H[:, :n], H[:, n:] + Y_lr], dim=1)
+    return out, {"U": U, "Y_lr": Y_lr, "H": Hfull}
 
 
 def _fused_ok(Q, K, V, phi, spec, C, h) -> bool:

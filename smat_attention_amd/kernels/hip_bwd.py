@@ -911,6 +911,63 @@ def patched() -> bool:
     return bool(_ORIG)
 
 
+class QueryFunction(torch.autograd.Function):
+    """The type-major read ``Y[i] = Phi_rec[i] U[i mod B]`` (query_by_type,
+    attention.py:310-330) as an autograd node: :func:`hip_fwd.query` forward;
+    backward ``dPhi_rec[i] = dY[i] U^T`` and ``dU[h] = sum Phi_rec[i]^T dY[i]``
+    over the rows of type h (:func:`_type_read_grad`, on smat_bgemm)."""
+
+    @staticmethod
+    def forward(ctx, Phi_rec, U):
+        ctx.save_for_backward(Phi_rec, U)
+        return _hip.query(Phi_rec, U)
+
+    @staticmethod
+    def backward(ctx, dY):
+        Phi_rec, U = ctx.saved_tensors
+        nb, T_R, r = Phi_rec.shape
+        B = U.shape[1]
+        Ph = Phi_rec.contiguous()
+        dYc = dY.float().contiguous()
+        dPhi = torch.zeros(nb, T_R, r, device=Ph.device, dtype=torch.float32)
+        dU = _type_read_grad(Ph, dYc, U.float().contiguous(), dPhi, T_R, 0, T_R, B)
+        return dPhi.to(Phi_rec.dtype), dU.to(U.dtype)
+
+
+class NormaliseFunction(torch.autograd.Function):
+    """``N = cat([H[:, :n], H[:, n:] + Y])``, ``out = (N[..., :-1] / N[..., -1:]) g``
+    (attention.py:446-453, the division without a floor) as an autograd node:
+    :func:`hip_fwd.normalise` forward, ``smat_normalise_backward`` backward
+    (dN, whose rows from n on are Y's gradient, and dg)."""
+
+    @staticmethod
+    def forward(ctx, H, Y, g, n):
+        ctx.save_for_backward(H, Y, g)
+        ctx.n = n
+        return _hip.normalise(H, n, Y, g)
+
+    @staticmethod
+    def backward(ctx, dout):
+        H, Y, g = ctx.saved_tensors
+        n = ctx.n
+        N = H.float().contiguous()
+        if Y is not None:
+            N = N.clone()
+            N[:, n:] += Y.float()
+        nb, T, p = N.shape
+        d = dout.float().contiguous()
+        dN = torch.empty(nb, T, p, device=N.device, dtype=torch.float32)
+        need_dg = g is not None and ctx.needs_input_grad[2]
+        dg = torch.empty(nb, T, device=N.device, dtype=torch.float32) if need_dg else None
+        gc = g.float().contiguous() if g is not None else None
+        call("smat_normalise_backward", d.data_ptr(), N.data_ptr(), ptr(gc), dN.data_ptr(),
+             ptr(dg), nb, T, p, d.stride(0), d.stride(1), N.stride(0), N.stride(1),
+             dN.stride(0), dN.stride(1), gc.stride(0) if gc is not None else 0, stream_of(dN))
+        dH = dN.to(H.dtype) if ctx.needs_input_grad[0] else None
+        dY = dN[:, n:].to(Y.dtype) if (Y is not None and ctx.needs_input_grad[1]) else None
+        return dH, dY, (dg.to(g.dtype) if need_dg else None), None
+
+
 class CombineNormaliseFunction(torch.autograd.Function):
     """``N = cat([H[:, :n], H[:, n:] + Y])``, ``out = N[..., :-1] /
     N[..., -1:].clamp_min(eps)`` (model.py:296-300) as one autograd node:

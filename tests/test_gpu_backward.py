@@ -144,6 +144,59 @@ def test_backward_head_dim_128(dt, d, n_P, gate):
         assert e < 2e-2 and e64 < 2e-2, name
 
 
+@pytest.mark.parametrize("T,d,n_P,gate", [(2048, 3, 0, False), (2048, 3, 16, True),
+                                          (1024, 2, 0, True)])
+def test_parts_and_timer_under_autograd(T, d, n_P, gate):
+    """return_parts and timer on a differentiable call (the reference's torch
+    path gives both under autograd, attention.py:391-455): the phases run as
+    autograd nodes on the HIP kernels, the timer sees lr_pool, lr_incidence,
+    lr_query, scan and normalise, the output equals the one-node call's, and the
+    gradients of a loss over the output and the parts U and H match fp64
+    autograd through the oracle's parts (fp32, 1e-5)."""
+    _say("parts and timer under autograd", T, d, n_P, gate)
+    spec = build_mask(T, d, chunk=128, n_P=n_P)
+    Phi, Psi, Vb = _feats(2, T, 32, seed=41)
+    gen = torch.Generator().manual_seed(42)
+    w = torch.randn(2, T, 32, generator=gen)
+    wH = torch.randn(2, T, 33, generator=gen)
+    wU = torch.randn(2, spec.B, 32, 33, generator=gen)
+    g = torch.rand(2, T, generator=gen) + 0.5 if gate else None
+    seen = []
+
+    class Timer:
+        def __init__(self, name):
+            seen.append(name)
+
+        def __enter__(self):
+            return self
+
+        def __exit__(self, *a):
+            return False
+
+    def loss(out, parts, dt):
+        return ((out * w.to(out.device, dt)).sum() + (parts["H"] * wH.to(out.device, dt)).sum()
+                + (parts["U"] * wU.to(out.device, dt)).sum())
+
+    xs = [t.to(DEV).requires_grad_(True) for t in (Phi, Psi, Vb)]
+    gd = g.to(DEV).requires_grad_(True) if gate else None
+    out, parts = A.smat_attention(*xs, spec, g=gd, return_parts=True, timer=Timer)
+    assert seen == ["lr_pool", "lr_incidence", "lr_query", "scan", "normalise"]
+    assert out.requires_grad and parts["H"].requires_grad and parts["U"].requires_grad
+    one = A.smat_attention(*xs, spec, g=gd)
+    assert _rel(out.detach().cpu(), one.detach().cpu()) < 1e-6
+    loss(out, parts, torch.float32).backward()
+    got = [x.grad.cpu() for x in xs] + ([gd.grad.cpu()] if gate else [])
+    rs = [t.double().requires_grad_(True) for t in (Phi, Psi, Vb)]
+    rg = g.double().requires_grad_(True) if gate else None
+    ro, rparts = O.smat_attention(*rs, spec, g=rg, acc_dtype=torch.float64, return_parts=True)
+    loss(ro, rparts, torch.float64).backward()
+    want = [x.grad for x in rs] + ([rg.grad] if gate else [])
+    for name, a, b in zip(("dPhi", "dPsi", "dVb", "dg"), got, want):
+        e = _rel(a, b)
+        _say(f"  {name}: rel vs fp64 {e:.2e}")
+        assert e < 1e-5, name
+
+
 def test_forward_unchanged_when_grad_is_recorded():
     _say("forward with and without autograd")
     spec = build_mask(2048, 3, chunk=128)
