@@ -519,17 +519,10 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     };
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      Frag shi, slo;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        In h0, l0, h1, l1;
-        split2<In>(accS[2 * kk][i], h0, l0);
-        split2<In>(accS[2 * kk + 1][i], h1, l1);
-        shi[i] = h0;
-        slo[i] = l0;
-        shi[4 + i] = h1;
-        slo[4 + i] = l1;
-      }
+      Half h0, l0, h1, l1;
+      split4<In>(accS[2 * kk], h0, l0);
+      split4<In>(accS[2 * kk + 1], h1, l1);
+      const Frag shi = join<In>(h0, h1), slo = join<In>(l0, l1);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const Frag bf = join<In>(phi_half(tt, 4 * kk + (g >> 1)), phi_half(tt, 4 * kk + 2 + (g >> 1)));
@@ -540,13 +533,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     float own = 0.f;                       // wave w < 4: its row tile's value, finished in (d)
     {
       Half s8hi, s8lo;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        In h0, l0;
-        split2<In>(accS8[i], h0, l0);
-        s8hi[i] = h0;
-        s8lo[i] = l0;
-      }
+      split4<In>(accS8, s8hi, s8lo);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const int t = 16 * tt + r16;
@@ -639,7 +626,9 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
         }
       }
       const float num = NBUF == 3 ? (gb ? ga[tt] : 1.f) : yr.gv[tt];   // the gate (1 without)
-      const float inv = num / den;
+      // the reciprocal (1 ulp) in place of the IEEE division's ten-instruction
+      // sequence; the product below rounds once more either way
+      const float inv = num * __builtin_amdgcn_rcpf(den);
       o.x *= inv;
       o.y *= inv;
       o.z *= inv;

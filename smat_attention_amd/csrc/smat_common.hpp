@@ -79,6 +79,38 @@ __device__ __forceinline__ void split2(float x, In& hi, In& lo) {
   lo = from_f32<In>(x - to_f32(hi));
 }
 
+// split2 of four values into half fragments.  For bf16 each pair of values
+// takes one conversion for both hi parts (v_cvt_pk_bf16_f32) and reads them
+// back as fp32 by shifting; the results are split2's, value by value.
+template <typename In>
+__device__ __forceinline__ void split4(const f32x4& x, typename Traits<In>::half_frag& hi,
+                                       typename Traits<In>::half_frag& lo) {
+  if constexpr (__is_same(In, bf16)) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const f32x2 v = {x[2 * q], x[2 * q + 1]};
+      const bf16x2 h = __builtin_convertvector(v, bf16x2);
+      const unsigned u = __builtin_bit_cast(unsigned, h);
+      const f32x2 back = {__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u)};
+      const bf16x2 l = __builtin_convertvector(v - back, bf16x2);
+      hi[2 * q] = h[0];
+      hi[2 * q + 1] = h[1];
+      lo[2 * q] = l[0];
+      lo[2 * q + 1] = l[1];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      In h, l;
+      split2<In>(x[i], h, l);
+      hi[i] = h;
+      lo[i] = l;
+    }
+  }
+}
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
