@@ -307,19 +307,29 @@ int smat_bgemm(int dtype_a, int dtype_b, const void* A, const void* B, float* C,
  *   dPhi = dA Psi + dH Sin^T,  dPsi = dA^T Phi + Vb Q^T,  dVb = A^T dH + Psi Q
  * for 16-bit Phi, Psi, Vb (nb x nc*C rows; dtype SMAT_BF16 or SMAT_F16), fp32
  * dH (nb x nc*C x p), the chunk-entry states Sin and the reverse-scan states Q
- * (both nb x nc x r x p, contiguous).  Writes fp32 dPhi, dPsi (row stride
- * d_st) and dVb (row stride e_st); every row of the nc chunks is written.
- * Serves r = 64, p = 65, C = 128 with 16-byte aligned rows of Phi, Psi, dPhi
- * and dPsi (SMAT_EUNSUPPORTED otherwise).  The products of
+ * (both nb x nc x r x p, contiguous).  Writes dPhi, dPsi (row stride d_st)
+ * and dVb (row stride e_st), strides in elements of out_dtype: SMAT_F32, or
+ * dtype itself for gradients rounded to nearest even in the inputs' type;
+ * every row of the nc chunks is written.  Serves r = 64, p = 65, C = 128 with
+ * 16-byte aligned rows of Phi, Psi, dPhi and dPsi (SMAT_EUNSUPPORTED
+ * otherwise).  Optional fp32 terms (NULL: none) are added before the store,
+ * rows addressed by absolute index: add_phi (rows ap_st apart, sequences
+ * ap_sb) on dPhi rows [add_split, add_end), add_psi (ak_*) and add_vb (av_*)
+ * on dPsi and dVb rows [0, add_split) -- the long-range branch's gradients
+ * (smat_lr_dphi, smat_pool_backward with accumulate = 0), so that the sum
+ * is rounded once.  The products of
  * src/smat/kernels/triton_bwd.py:49-147 (_cl_bwd_dphi_kernel and
  * _cl_bwd_dpsi_dvb_kernel) with the chunk states of attention.py:134-192.
  */
-int smat_chunk_backward(int dtype, const void* phi, const void* psi, const void* vb,
-                        const float* dH, const float* Sin, const float* Q, float* dPhi,
-                        float* dPsi, float* dVb, int nb, int nc, int r, int p, int C,
+int smat_chunk_backward(int dtype, int out_dtype, const void* phi, const void* psi,
+                        const void* vb, const float* dH, const float* Sin, const float* Q,
+                        void* dPhi, void* dPsi, void* dVb, int nb, int nc, int r, int p, int C,
                         int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
                         int64_t v_st, int64_t h_sb, int64_t h_st, int64_t d_sb, int64_t d_st,
-                        int64_t e_sb, int64_t e_st, void* stream);
+                        int64_t e_sb, int64_t e_st, const float* add_phi, const float* add_psi,
+                        const float* add_vb, int64_t ap_sb, int64_t ap_st, int64_t ak_sb,
+                        int64_t ak_st, int64_t av_sb, int64_t av_st, int64_t add_split,
+                        int64_t add_end, void* stream);
 
 /*
  * Backward of the long-range branch (attention.py:196-330) at r = 64, p = 65
@@ -342,17 +352,22 @@ int smat_chunk_backward(int dtype, const void* phi, const void* psi, const void*
  * j = n_P + x + s*N0 < n, dPsi_j += Vb_j dF_x^T and dVb_j += Psi_j dF_x; when
  * n_P > 0, item N0 (dF row N0, the global channel) does tokens 0 .. n_P-1.
  * dF_x is read once for both (src/smat/kernels/triton_bwd.py:203-237).
+ *
+ * accumulate = 1 adds into dPhi / dPsi / dVb as written above; 0 stores the
+ * term itself (every recent row has one row type and every landmark row one
+ * profile or the global channel, so each of those rows is written once and
+ * the others are left as they are).
  */
 int smat_lr_dphi(int dtype, const float* dH, const float* U, float* dPhi, int nb, int T_R, int B,
                  int n, int r, int p, int64_t h_sb, int64_t h_st, int64_t u_sb, int64_t d_sb,
-                 int64_t d_st, void* stream);
+                 int64_t d_st, int accumulate, void* stream);
 int smat_lr_dfeat(int dtype, const void* phi, const float* dH, const int32_t* tptr,
                   const int32_t* tok, float* dF, int nb, int nitems, int r, int p, int64_t q_sb,
                   int64_t q_st, int64_t h_sb, int64_t h_st, int64_t f_sb, void* stream);
 int smat_pool_backward(int dtype, const void* psi, const void* vb, const float* dF, float* dPsi,
                        float* dVb, int nb, int N0, int n, int n_P, int r, int p, int64_t k_sb,
                        int64_t k_st, int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb,
-                       int64_t d_st, int64_t e_sb, int64_t e_st, void* stream);
+                       int64_t d_st, int64_t e_sb, int64_t e_st, int accumulate, void* stream);
 
 /*
  * Gradients of ContentAssign's hard point read and pool (src/smat/assign.py:
@@ -365,11 +380,16 @@ int smat_pool_backward(int dtype, const void* psi, const void* vb, const float* 
  * smat_cell_read_backward: for y_i = Phi_i F[cell_i0] and upstream dY (fp32,
  * rows of stride y_st): dPhi_i = F[x] dY_i (pair 0), dw[i*K + k] =
  * Phi_i . (F[x] dY_i) for every entry, dF[x] = sum over pair-0 entries of
- * Phi_i^T dY_i.  Writes every row of dPhi, dw and dF (fp32).
+ * Phi_i^T dY_i.  Writes the dPhi row of every token with a pair-0 entry,
+ * every dw and every dF (fp32).
  *
  * smat_cell_pool_backward: for F[x] = sum_{cell_j0 = x} Psi_j^T Vb_j and dF:
  * dPsi_j = Vb_j dF[x]^T and dVb_j = Psi_j dF[x] (pair 0), dw[j*K + k] =
  * Psi_j . (Vb_j dF[x]^T) for every entry (fp32).
+ *
+ * Both: dPhi, dPsi and dVb of out_dtype (SMAT_F32, or dtype for gradients
+ * rounded to nearest even in the inputs' type; strides in its elements), with
+ * batch and row strides of their own, so they may be rows of larger tensors.
  *
  * The reference's autograd of the dense read and pool; its fused pool
  * backward is src/smat/kernels/triton_bwd.py:203-237.
@@ -392,14 +412,14 @@ int smat_featurise_backward(int dtype, const void* x, const void* G, const void*
                             int64_t g_st, int64_t h_sb, int64_t o_sb, int64_t o_st,
                             int64_t dh_sb, void* stream);
 
-int smat_cell_read_backward(int dtype, const void* phr, const float* dY, const float* F,
-                            const int32_t* ent, const int64_t* eoffs, float* dPhi, float* dF,
-                            float* dw, int nb, int N0, int K, int r, int p, int64_t q_sb,
+int smat_cell_read_backward(int dtype, int out_dtype, const void* phr, const float* dY,
+                            const float* F, const int32_t* ent, const int64_t* eoffs, void* dPhi,
+                            float* dF, float* dw, int nb, int N0, int K, int r, int p, int64_t q_sb,
                             int64_t q_st, int64_t y_sb, int64_t y_st, int64_t f_sb,
                             int64_t d_sb, int64_t d_st, int64_t w_sb, void* stream);
-int smat_cell_pool_backward(int dtype, const void* psi, const void* vb, const float* dF,
-                            const int32_t* ent, const int64_t* eoffs, float* dPsi, float* dVb,
-                            float* dw, int nb, int N0, int K, int r, int p, int64_t k_sb,
+int smat_cell_pool_backward(int dtype, int out_dtype, const void* psi, const void* vb,
+                            const float* dF, const int32_t* ent, const int64_t* eoffs, void* dPsi,
+                            void* dVb, float* dw, int nb, int N0, int K, int r, int p, int64_t k_sb,
                             int64_t k_st, int64_t v_sb, int64_t v_st, int64_t f_sb,
                             int64_t d_sb, int64_t d_st, int64_t e_sb, int64_t e_st,
                             int64_t w_sb, void* stream);
@@ -563,7 +583,9 @@ int smat_forward_fused(int dtype, const void* q, const void* k, const void* v, c
  * Class lists (CSR) of every sequence by a counting sort: keys (nb, L) int64 in
  * [0, ncls) -> order (nb*L) int32, the items of sequence 0's class 0, class 1,
  * ..., then sequence 1's, each list in item order (the stable sort of
- * b*ncls + key); an item is b*L + l (global_index) or l.  offs (nb*ncls + 1)
+ * b*ncls + key); an item is b*seq_rows + row0 + l (global_index: the row of a
+ * rows [row0, row0 + L) slice of sequences seq_rows rows long; seq_rows = L,
+ * row0 = 0 numbers the items b*L + l) or l.  offs (nb*ncls + 1)
  * int64: list (b, c) is order[offs[b*ncls + c] .. offs[b*ncls + c + 1]).
  * workspace: smat_csr_workspace_bytes(nb, L, ncls) bytes.  ncls <= 8192,
  * nb*L < 2^31; keys outside [0, ncls) are clamped into it.  Nothing is read
@@ -573,7 +595,8 @@ int smat_forward_fused(int dtype, const void* q, const void* k, const void* v, c
  */
 int64_t smat_csr_workspace_bytes(int nb, int L, int ncls);
 int smat_csr_lists(const int64_t* keys, int32_t* order, int64_t* offs, void* workspace, int nb,
-                   int L, int ncls, int global_index, void* stream);
+                   int L, int ncls, int global_index, int64_t seq_rows, int64_t row0,
+                   void* stream);
 
 /*
  * Content hash of token rows u (nb, L, dm; dtype of u): for head h and

@@ -652,12 +652,12 @@ class ContentAssign(nn.Module):
             return (y * ste.to(y.dtype)).float()
         hard = self.anneal >= 1.0 or self.src == "id"
         if hard:
-            F = _HardPool.apply(P, V, wk, idxk, ck, self.N0)
+            F = _HardPool.apply(Psi, Vb, wk, idxk, ck, self.N0)
         else:
             F = pool_sorted(P, V, idxk, wk.to(dt), self.N0).float()
         if self.mode == "point":
             if hard:
-                return _HardRead.apply(Phi_r, F, wq, idxq, cq)
+                return _HardRead.apply(Phi, F, wq, idxq, cq)
             return read_sorted(Phi_r, idxq, wq.to(dt), F.to(dt)).float()
         from .kernels import hip_bwd
         U = hip_bwd.incidence(F, self.coset_pts.to(dev), nrows)
@@ -842,52 +842,87 @@ def _one_hot_first(w):
     return bool((w[..., 0] == 1).all()) and bool((w[..., 1:] == 0).all())
 
 
+def _whole_rows(*xs):
+    """Whether every (nb, T, .) tensor stores each sequence's T rows one after
+    another (batch stride = T * row stride), so that flat row ids ``b*T + t``
+    address them from the first element."""
+    return all(x.stride(-1) == 1 and x.stride(0) == x.shape[1] * x.stride(1) for x in xs)
+
+
+def _grad_rows(x, lo, hi, dtype):
+    """A gradient for ``x`` (nb, T, c) whose rows ``[lo, hi)`` a kernel writes:
+    the rows outside are zero.  Rows of c elements, 16-byte aligned."""
+    g = torch.empty(x.shape, device=x.device, dtype=dtype)
+    if lo > 0:
+        g[:, :lo].zero_()
+    if hi < x.shape[1]:
+        g[:, hi:].zero_()
+    return g
+
+
+def _slice_grad(x, g, lo):
+    """(nb, T, c) gradient of ``x`` from the gradient ``g`` of rows ``[lo, lo + L)``."""
+    out = torch.zeros(x.shape, device=x.device, dtype=x.dtype)
+    out[:, lo:lo + g.shape[1]] = g
+    return out
+
+
 class _HardPool(torch.autograd.Function):
     """The dense pool with one-hot forward weights (assign.py:431-436 at
-    ``anneal = 1``): ``F_x = sum_{ck_j = x} Psi_j^T Vb_j``; backward
-    ``dPsi_j = dF[ck_j] Vb_j``, ``dVb_j = dF[ck_j]^T Psi_j`` and, for every
-    pair, ``dw_jk = Psi_j . (dF[idx_jk] Vb_j)`` -- for the first pair (the
-    chosen cell, ``idx_j0 = ck_j``) that is ``Psi_j . dPsi_j``.  The cell
-    lists are sorted once per step.  fp32 F."""
+    ``anneal = 1``): ``F_x = sum_{ck_j = x} Psi_j^T Vb_j`` over the first ``n``
+    rows of Psi and Vb (``n = ck.shape[1]``); backward ``dPsi_j = dF[ck_j]
+    Vb_j``, ``dVb_j = dF[ck_j]^T Psi_j`` and, for every pair, ``dw_jk = Psi_j .
+    (dF[idx_jk] Vb_j)`` -- for the first pair (the chosen cell, ``idx_j0 =
+    ck_j``) that is ``Psi_j . dPsi_j``.  Psi and Vb are the layer's whole
+    (nb, T, .) tensors: the kernels read the key rows in place, and the
+    gradients are whole tensors of Psi's and Vb's dtypes with zero rows from
+    ``n`` on, so no slice is copied either way.  fp32 F."""
 
     @staticmethod
-    def forward(ctx, P, V, wk, idxk, ck, N0):
-        r, p = P.shape[-1], V.shape[-1]
+    def forward(ctx, Psi, Vb, wk, idxk, ck, N0):
+        r, p = Psi.shape[-1], Vb.shape[-1]
         if r > 128 or p > 144:
             raise NotImplementedError("ContentAssign gradients: r <= 128, p <= 144")
-        Pk, Vk = P.contiguous(), V.contiguous()
-        lists = _lists(ck, N0)
-        F = _gram_lists(Pk, Vk, ck, N0, lists)
-        ctx.save_for_backward(Pk, Vk, idxk, ck)
-        ctx.lists = lists
-        ctx.dtypes = (P.dtype, V.dtype, wk.dtype)
+        n = ck.shape[1]
+        if _whole_rows(Psi, Vb):
+            lists = _lists(ck, N0, seq_rows=Psi.shape[1])
+            F = _gram_lists(Psi, Vb, ck, N0, lists)
+        else:
+            F = _gram_lists(Psi[:, :n].contiguous(), Vb[:, :n].contiguous(), ck, N0)
+        ctx.save_for_backward(Psi, Vb, idxk, ck)
+        ctx.n = n
+        ctx.w_dtype = wk.dtype
         return F
 
     @staticmethod
     def backward(ctx, dF):
-        Pk, Vk, idxk, ck = ctx.saved_tensors
+        Psi, Vb, idxk, ck = ctx.saved_tensors
+        n = ctx.n
         dF = dF.float().contiguous()
-        dp, dv, dw = ctx.dtypes
-        if _cell_backward_ok(Pk, Vk):
-            # one launch per (sequence, cell): dPsi, dVb and every pair's dw
-            nb, L, r = Pk.shape
-            p, N0, K = Vk.shape[-1], dF.shape[1], idxk.shape[-1]
+        if _cell_backward_ok(Psi, Vb):
+            # one launch per (sequence, cell): dPsi, dVb and every pair's dw,
+            # rounded to the inputs' type as they are stored
+            nb, _, r = Psi.shape
+            p, N0, K = Vb.shape[-1], dF.shape[1], idxk.shape[-1]
             ent, eoffs = _entry_lists(idxk, N0)
-            dPsi = torch.empty(nb, L, r, device=Pk.device, dtype=torch.float32)
-            dVb = torch.empty(nb, L, p, device=Pk.device, dtype=torch.float32)
-            dwk = torch.empty(nb, L, K, device=Pk.device, dtype=torch.float32)
-            call("smat_cell_pool_backward", _code(Pk, "ContentAssign"), Pk.data_ptr(),
-                 Vk.data_ptr(), dF.data_ptr(), ent.data_ptr(), eoffs.data_ptr(), dPsi.data_ptr(),
-                 dVb.data_ptr(), dwk.data_ptr(), nb, N0, K, r, p, Pk.stride(0), Pk.stride(1),
-                 Vk.stride(0), Vk.stride(1), dF.stride(0), dPsi.stride(0), dPsi.stride(1),
-                 dVb.stride(0), dVb.stride(1), dwk.stride(0), stream_of(dF))
-            return dPsi.to(dp), dVb.to(dv), dwk.to(dw), None, None, None
+            dPsi = _grad_rows(Psi, 0, n, Psi.dtype)
+            dVb = _grad_rows(Vb, 0, n, Vb.dtype)
+            dwk = torch.empty(nb, n, K, device=Psi.device, dtype=torch.float32)
+            call("smat_cell_pool_backward", _code(Psi, "ContentAssign"), _code(dPsi, "ContentAssign"),
+                 Psi.data_ptr(), Vb.data_ptr(), dF.data_ptr(), ent.data_ptr(), eoffs.data_ptr(),
+                 dPsi.data_ptr(), dVb.data_ptr(), dwk.data_ptr(), nb, N0, K, r, p, Psi.stride(0),
+                 Psi.stride(1), Vb.stride(0), Vb.stride(1), dF.stride(0), dPsi.stride(0),
+                 dPsi.stride(1), dVb.stride(0), dVb.stride(1), dwk.stride(0), stream_of(dF))
+            return dPsi, dVb, dwk.to(ctx.w_dtype), None, None, None
+        Pk, Vk = Psi[:, :n].contiguous(), Vb[:, :n].contiguous()
+        lists = _lists(ck, dF.shape[1])
         dFT = dF.transpose(-1, -2).contiguous()
         P32, V32 = Pk.float(), _f32_rows(Vk)         # Vb rows of p floats, 16-byte aligned
-        dPsi = _read_lists(V32, dFT, ck, ctx.lists)
-        dVb = _read_lists(P32, dF, ck, ctx.lists)
+        dPsi = _read_lists(V32, dFT, ck, lists)
+        dVb = _read_lists(P32, dF, ck, lists)
         dwk = _pair_dw(P32, dPsi, V32, dFT, idxk)
-        return dPsi.to(dp), dVb.to(dv), dwk.to(dw), None, None, None
+        return (_slice_grad(Psi, dPsi, 0), _slice_grad(Vb, dVb, 0), dwk.to(ctx.w_dtype), None,
+                None, None)
 
 
 def _pair_dw(X, G0, Y, UT, idx):
@@ -903,48 +938,69 @@ def _pair_dw(X, G0, Y, UT, idx):
 
 class _HardRead(torch.autograd.Function):
     """The dense point read with one-hot forward weights (assign.py:437-441 at
-    ``anneal = 1``): ``y_i = Phi_i F[cq_i]``; backward ``dPhi_i = F[cq_i] dy_i``,
-    ``dF_x = sum_{cq_i = x} Phi_i^T dy_i`` and ``dw_ik = Phi_i . (F[idx_ik] dy_i)``
-    (``Phi_i . dPhi_i`` for the first pair)."""
+    ``anneal = 1``): ``y_i = Phi_i F[cq_i]`` for the last ``T_R = cq.shape[1]``
+    rows of Phi; backward ``dPhi_i = F[cq_i] dy_i``, ``dF_x = sum_{cq_i = x}
+    Phi_i^T dy_i`` and ``dw_ik = Phi_i . (F[idx_ik] dy_i)`` (``Phi_i . dPhi_i``
+    for the first pair).  Phi is the layer's whole (nb, T, r) tensor, read in
+    place; its gradient is a whole tensor of Phi's dtype, zero before the
+    recent rows.  y: fp32 (nb, T_R, p), rows of sequences T rows apart (a view
+    of a (nb, T, p) buffer whose first T_R rows of each sequence it holds)."""
 
     @staticmethod
-    def forward(ctx, Phr, F, wq, idxq, cq):
-        Phr = Phr.contiguous()
-        lists = _lists(cq, F.shape[1])
-        Y = _read_lists(Phr, F.contiguous(), cq, lists)
-        ctx.save_for_backward(Phr, F, idxq, cq)
-        ctx.lists = lists
-        ctx.dtypes = (Phr.dtype, wq.dtype)
+    def forward(ctx, Phi, F, wq, idxq, cq):
+        nb, T, r = Phi.shape
+        T_R = cq.shape[1]
+        n = T - T_R
+        N0, p = F.shape[1], F.shape[-1]
+        Fc = F.contiguous()
+        if _whole_rows(Phi) and r <= 128:
+            # row ids b*T + l address Phi from row n and the output from row 0
+            rows, roffs, hint = _lists(cq, N0, seq_rows=T)
+            Yw = torch.empty(nb, T, p, device=Phi.device, dtype=torch.float32)
+            Xr = Phi[:, n:]
+            call("smat_query_lists", _code(Xr, "ContentAssign"), Xr.data_ptr(), Fc.data_ptr(),
+                 Yw.data_ptr(), rows.data_ptr(), roffs.data_ptr(), nb * N0, hint, r, p,
+                 Xr.stride(1), Yw.stride(1), stream_of(Xr))
+            Y = Yw[:, :T_R]
+        else:
+            Y = _read_lists(Phi[:, n:].contiguous(), Fc, cq)
+        ctx.save_for_backward(Phi, F, idxq, cq)
+        ctx.w_dtype = wq.dtype
         return Y
 
     @staticmethod
     def backward(ctx, dY):
-        Phr, F, idxq, cq = ctx.saved_tensors
-        dp, dw = ctx.dtypes
+        Phi, F, idxq, cq = ctx.saved_tensors
+        nb, T, r = Phi.shape
+        T_R = cq.shape[1]
+        n = T - T_R
+        Phr = Phi[:, n:]
         if _cell_backward_ok(Phr, None) and F.shape[-1] == 65 and F.shape[-2] == 64:
             # one launch per (sequence, cell): dPhi, dF and every pair's dw
             dYc = dY.float()
             dYc = dYc if dYc.stride(-1) == 1 else dYc.contiguous()
             Fc = F.float().contiguous()
-            nb, L, r = Phr.shape
             N0, p, K = Fc.shape[1], Fc.shape[-1], idxq.shape[-1]
             ent, eoffs = _entry_lists(idxq, N0)
-            dPhi = torch.empty(nb, L, r, device=Phr.device, dtype=torch.float32)
-            dF = torch.empty(nb, N0, r, p, device=Phr.device, dtype=torch.float32)
-            dwq = torch.empty(nb, L, K, device=Phr.device, dtype=torch.float32)
-            call("smat_cell_read_backward", _code(Phr, "ContentAssign"), Phr.data_ptr(),
-                 dYc.data_ptr(), Fc.data_ptr(), ent.data_ptr(), eoffs.data_ptr(),
-                 dPhi.data_ptr(), dF.data_ptr(), dwq.data_ptr(), nb, N0, K, r, p, Phr.stride(0),
-                 Phr.stride(1), dYc.stride(0), dYc.stride(1), Fc.stride(0), dPhi.stride(0),
-                 dPhi.stride(1), dwq.stride(0), stream_of(Fc))
-            return dPhi.to(dp), dF, dwq.to(dw), None, None
+            dPhi = _grad_rows(Phi, n, T, Phi.dtype)
+            dPr = dPhi[:, n:]
+            dF = torch.empty(nb, N0, r, p, device=Phi.device, dtype=torch.float32)
+            dwq = torch.empty(nb, T_R, K, device=Phi.device, dtype=torch.float32)
+            call("smat_cell_read_backward", _code(Phr, "ContentAssign"),
+                 _code(dPr, "ContentAssign"), Phr.data_ptr(), dYc.data_ptr(), Fc.data_ptr(),
+                 ent.data_ptr(), eoffs.data_ptr(), dPr.data_ptr(), dF.data_ptr(), dwq.data_ptr(),
+                 nb, N0, K, r, p, Phr.stride(0), Phr.stride(1), dYc.stride(0), dYc.stride(1),
+                 Fc.stride(0), dPr.stride(0), dPr.stride(1), dwq.stride(0), stream_of(Fc))
+            return dPhi, dF, dwq.to(ctx.w_dtype), None, None
+        Phr = Phr.contiguous()
+        lists = _lists(cq, F.shape[1])
         dY = _f32_rows(dY)                            # rows of p floats, 16-byte aligned
         Ph32 = Phr.float()
         FT = F.transpose(-1, -2).contiguous()
-        dPhi = _read_lists(dY, FT, cq, ctx.lists)
-        dF = _gram_lists(Ph32, dY, cq, F.shape[1], ctx.lists)
+        dPhi = _read_lists(dY, FT, cq, lists)
+        dF = _gram_lists(Ph32, dY, cq, F.shape[1], lists)
         dwq = _pair_dw(Ph32, dPhi, dY, FT, idxq)
-        return dPhi.to(dp), dF, dwq.to(dw), None, None
+        return _slice_grad(Phi, dPhi, n), dF, dwq.to(ctx.w_dtype), None, None
 
 
 def _offset_rows(idxq, wq, coset_of, nc):

@@ -628,13 +628,16 @@ def smat_attention(Phi, Psi, Vb, spec: MaskSpec, *, chunk: int = 128, g=None,
     else:
         with tm("scan"):
             H = segmented_causal_scan(Phi, Psi, Vb, n=n, chunk=C)
+    if return_parts:
+        # H is this call's own buffer: the long-range term goes into it in
+        # place, and the parts' H is the sum the division reads
+        with tm("normalise"):
+            H[:, n:] += Y_lr
+            out = _hip.normalise(H, n, None, g)
+        parts.update(U=U, Y_lr=Y_lr, H=H)
+        return out, parts
     with tm("normalise"):
         out = _hip.normalise(H, n, Y_lr, g)
-    if return_parts:
-        Hfull = H.clone()
-        Hfull[:, n:] += Y_lr
-        parts.update(U=U, Y_lr=Y_lr, H=Hfull)
-        return out, parts
     return out
 
 

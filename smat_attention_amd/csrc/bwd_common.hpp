@@ -163,6 +163,26 @@ __device__ __forceinline__ void cb_stage_rp(float* s, const float* src) {
   }
 }
 
+// Gradient rows leave as fp32 or rounded (to nearest even) to the inputs'
+// 16-bit type.  Four consecutive values: one 16-byte store of floats, or one
+// 8-byte store of 16-bit values (rows 16-byte aligned, the group at a column
+// that is a multiple of 4).
+__device__ __forceinline__ void store_grad4(float* p, const f32x4& v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <typename Out>
+__device__ __forceinline__ void store_grad4(Out* p, const f32x4& v) {
+  typename Traits<Out>::half_frag h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h[i] = from_f32<Out>(v[i]);
+  *reinterpret_cast<typename Traits<Out>::half_frag*>(p) = h;
+}
+// The code of a gradient output type, as the host entry points take it.
+template <typename Out> constexpr int out_code();
+template <> constexpr int out_code<float>() { return SMAT_F32; }
+template <> constexpr int out_code<bf16>() { return SMAT_BF16; }
+template <> constexpr int out_code<f16>() { return SMAT_F16; }
+
 // Sum over the four 16-lane groups of a wave (lanes r16, r16 + 16, +32, +48).
 __device__ __forceinline__ float cb_sum_groups(float v) {
   v += __shfl_xor(v, 16);

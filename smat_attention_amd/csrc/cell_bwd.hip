@@ -37,10 +37,10 @@ constexpr int kStep = 32;                 // entries a step (read backward)
 // columns split hi/lo, zero for other pairs): wave w owns value-column tile
 // w, wave 0 also tile 4 (column 64).
 // ---------------------------------------------------------------------------
-template <typename In>
+template <typename In, typename Out>
 __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
     const In* __restrict__ phr, const float* __restrict__ dY, const float* __restrict__ F,
-    const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, float* __restrict__ dPhi,
+    const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, Out* __restrict__ dPhi,
     float* __restrict__ dF, float* __restrict__ dw, int N0, int K, int64_t q_sb, int64_t q_st,
     int64_t y_sb, int64_t y_st, int64_t f_sb, int64_t d_sb, int64_t d_st, int64_t w_sb) {
   using namespace cb;
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
     for (int j = 0; j < 8; ++j) fa[kc][j] = sF[(16 * w + r16) * kS + 32 * kc + 4 * j + g];
   const float fat = g == 0 ? sF[(16 * w + r16) * kS + 64] : 0.f;
 
-  float* dPb = dPhi + b * d_sb;
+  Out* dPb = dPhi + b * d_sb;
   float* dwb = dw + b * w_sb;
   f32x4 acc[4], acc4[4];
 #pragma unroll
@@ -124,9 +124,7 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
       pd = cb_sum_groups(pd);
       if (g == 0) sDot[w][es] = pd;
       const int t = sTok[es];
-      if (t >= 0 && sPair[es] == 0)
-        *reinterpret_cast<float4*>(dPb + (int64_t)t * d_st + 16 * w + 4 * g) =
-            make_float4(v[0], v[1], v[2], v[3]);
+      if (t >= 0 && sPair[es] == 0) store_grad4(dPb + (int64_t)t * d_st + 16 * w + 4 * g, v);
     }
 
     // dF += Phi^T dy over the pair-0 entries of the step
@@ -193,11 +191,11 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
 // (A = dF columns; wave 0 also column 64) for two 16-entry tiles, stores dPsi
 // and dVb for pair-0 entries and Psi . v for every entry.
 // ---------------------------------------------------------------------------
-template <typename In>
+template <typename In, typename Out>
 __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, const float* __restrict__ dF,
-    const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, float* __restrict__ dPsi,
-    float* __restrict__ dVb, float* __restrict__ dw, int N0, int K, int64_t k_sb, int64_t k_st,
+    const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, Out* __restrict__ dPsi,
+    Out* __restrict__ dVb, float* __restrict__ dw, int N0, int K, int64_t k_sb, int64_t k_st,
     int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st, int64_t e_sb,
     int64_t e_st, int64_t w_sb) {
   using namespace cb;
@@ -233,8 +231,8 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
     }
   const float frt = g == 0 ? sF[(16 * w + r16) * kS + 64] : 0.f;
 
-  float* dPb = dPsi + b * d_sb;
-  float* dVbb = dVb + b * e_sb;
+  Out* dPb = dPsi + b * d_sb;
+  Out* dVbb = dVb + b * e_sb;
   float* dwb = dw + b * w_sb;
   for (int64_t s0 = beg; s0 < end; s0 += cw::kStep) {
     const int par = (int)(((s0 - beg) / cw::kStep) & 1);
@@ -283,11 +281,10 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
       if (g == 0) sDot[w][es] = pd;
       const int t = sTok[es];
       if (t >= 0 && sPair[es] == 0) {
-        *reinterpret_cast<float4*>(dPb + (int64_t)t * d_st + 16 * w + 4 * g) =
-            make_float4(v[0], v[1], v[2], v[3]);
-        float* ov = dVbb + (int64_t)t * e_st + 16 * w + 4 * g;
+        store_grad4(dPb + (int64_t)t * d_st + 16 * w + 4 * g, v);
+        Out* ov = dVbb + (int64_t)t * e_st + 16 * w + 4 * g;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ov[i] = dv[i];
+        for (int i = 0; i < 4; ++i) ov[i] = from_f32<Out>(dv[i]);
       }
       if (w == 0) {
         // column 64 of dVb: sum_a dF[a][64] Psi[a] (lane group 0, slot 0)
@@ -302,7 +299,7 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
           }
           d4 = mma(d4, a4, psf);
         }
-        if (g == 0 && t >= 0 && sPair[es] == 0) dVbb[(int64_t)t * e_st + 64] = d4[0];
+        if (g == 0 && t >= 0 && sPair[es] == 0) dVbb[(int64_t)t * e_st + 64] = from_f32<Out>(d4[0]);
       }
     }
     __syncthreads();                                 // sDot complete; LDS free for the next step
@@ -312,15 +309,39 @@ __global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
   }
 }
 
-static bool cw_ok(int dtype, int r, int p, int K) {
-  return (dtype == SMAT_BF16 || dtype == SMAT_F16) && r == cb::kR && p == cb::kP && K >= 1;
+static bool cw_ok(int dtype, int out_dtype, int r, int p, int K) {
+  return (dtype == SMAT_BF16 || dtype == SMAT_F16) &&
+         (out_dtype == SMAT_F32 || out_dtype == dtype) && r == cb::kR && p == cb::kP && K >= 1;
+}
+
+template <typename In, typename Out>
+static void cell_read_launch(dim3 grid, hipStream_t st, const void* phr, const float* dY,
+                             const float* F, const int32_t* ent, const int64_t* eoffs, void* dPhi,
+                             float* dF, float* dw, int N0, int K, int64_t q_sb, int64_t q_st,
+                             int64_t y_sb, int64_t y_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
+                             int64_t w_sb) {
+  hipLaunchKernelGGL((cell_read_bwd_kernel<In, Out>), grid, dim3(cw::kThreads), 0, st,
+                     (const In*)phr, dY, F, ent, eoffs, (Out*)dPhi, dF, dw, N0, K, q_sb, q_st,
+                     y_sb, y_st, f_sb, d_sb, d_st, w_sb);
+}
+
+template <typename In, typename Out>
+static void cell_pool_launch(dim3 grid, hipStream_t st, const void* psi, const void* vb,
+                             const float* dF, const int32_t* ent, const int64_t* eoffs, void* dPsi,
+                             void* dVb, float* dw, int N0, int K, int64_t k_sb, int64_t k_st,
+                             int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
+                             int64_t e_sb, int64_t e_st, int64_t w_sb) {
+  hipLaunchKernelGGL((cell_pool_bwd_kernel<In, Out>), grid, dim3(cw::kThreads), 0, st,
+                     (const In*)psi, (const In*)vb, dF, ent, eoffs, (Out*)dPsi, (Out*)dVb, dw, N0,
+                     K, k_sb, k_st, v_sb, v_st, f_sb, d_sb, d_st, e_sb, e_st, w_sb);
 }
 
 }  // namespace smat
 
-extern "C" int smat_cell_read_backward(int dtype, const void* phr, const float* dY,
-                                       const float* F, const int32_t* ent, const int64_t* eoffs,
-                                       float* dPhi, float* dF, float* dw, int nb, int N0, int K,
+extern "C" int smat_cell_read_backward(int dtype, int out_dtype, const void* phr,
+                                       const float* dY, const float* F, const int32_t* ent,
+                                       const int64_t* eoffs, void* dPhi, float* dF, float* dw,
+                                       int nb, int N0, int K,
                                        int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb,
                                        int64_t y_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
                                        int64_t w_sb, void* stream) {
@@ -329,10 +350,12 @@ extern "C" int smat_cell_read_backward(int dtype, const void* phr, const float* 
   SMAT_REQUIRE(phr && dY && F && ent && eoffs && dPhi && dF && dw, SMAT_EINVAL,
                "smat_cell_read_backward: null pointer");
   SMAT_REQUIRE(nb >= 0 && N0 >= 1, SMAT_EINVAL, "smat_cell_read_backward: bad sizes");
-  SMAT_REQUIRE(cw_ok(dtype, r, p, K), SMAT_EUNSUPPORTED,
-               "smat_cell_read_backward: needs dtype bf16/f16, r=64, p=65 (got %d, %d, %d)",
-               dtype, r, p);
-  SMAT_REQUIRE(rows_vec_ok(phr, q_sb, q_st, 2) && rows_vec_ok(dPhi, d_sb, d_st, 4) &&
+  SMAT_REQUIRE(cw_ok(dtype, out_dtype, r, p, K), SMAT_EUNSUPPORTED,
+               "smat_cell_read_backward: needs dtype bf16/f16, out_dtype fp32 or dtype, r=64, "
+               "p=65 (got %d, %d, %d, %d)",
+               dtype, out_dtype, r, p);
+  SMAT_REQUIRE(rows_vec_ok(phr, q_sb, q_st, 2) &&
+                   rows_vec_ok(dPhi, d_sb, d_st, elem_bytes(out_dtype)) &&
                    aligned16(F) && f_sb % 4 == 0 && y_st >= p && f_sb >= (int64_t)N0 * r * p,
                SMAT_EINVAL, "smat_cell_read_backward: Phi, dPhi and F must be 16-byte aligned");
   SMAT_REQUIRE(N0 < 65536 * 32 && nb < 65536, SMAT_EUNSUPPORTED,
@@ -340,20 +363,22 @@ extern "C" int smat_cell_read_backward(int dtype, const void* phr, const float* 
   if (nb == 0) return SMAT_OK;
   const dim3 grid((unsigned)N0, (unsigned)nb);
   hipStream_t st = (hipStream_t)stream;
+  const bool f32 = out_dtype == SMAT_F32;
   if (dtype == SMAT_BF16)
-    hipLaunchKernelGGL(cell_read_bwd_kernel<bf16>, grid, dim3(cw::kThreads), 0, st,
-                       (const bf16*)phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, q_sb, q_st, y_sb,
-                       y_st, f_sb, d_sb, d_st, w_sb);
+    (f32 ? cell_read_launch<bf16, float> : cell_read_launch<bf16, bf16>)(
+        grid, st, phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, q_sb, q_st, y_sb, y_st, f_sb, d_sb,
+        d_st, w_sb);
   else
-    hipLaunchKernelGGL(cell_read_bwd_kernel<f16>, grid, dim3(cw::kThreads), 0, st,
-                       (const f16*)phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, q_sb, q_st, y_sb,
-                       y_st, f_sb, d_sb, d_st, w_sb);
+    (f32 ? cell_read_launch<f16, float> : cell_read_launch<f16, f16>)(
+        grid, st, phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, q_sb, q_st, y_sb, y_st, f_sb, d_sb,
+        d_st, w_sb);
   return launch_status("smat_cell_read_backward");
 }
 
-extern "C" int smat_cell_pool_backward(int dtype, const void* psi, const void* vb,
-                                       const float* dF, const int32_t* ent, const int64_t* eoffs,
-                                       float* dPsi, float* dVb, float* dw, int nb, int N0, int K,
+extern "C" int smat_cell_pool_backward(int dtype, int out_dtype, const void* psi,
+                                       const void* vb, const float* dF, const int32_t* ent,
+                                       const int64_t* eoffs, void* dPsi, void* dVb, float* dw,
+                                       int nb, int N0, int K,
                                        int r, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
                                        int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
                                        int64_t e_sb, int64_t e_st, int64_t w_sb, void* stream) {
@@ -362,10 +387,12 @@ extern "C" int smat_cell_pool_backward(int dtype, const void* psi, const void* v
   SMAT_REQUIRE(psi && vb && dF && ent && eoffs && dPsi && dVb && dw, SMAT_EINVAL,
                "smat_cell_pool_backward: null pointer");
   SMAT_REQUIRE(nb >= 0 && N0 >= 1, SMAT_EINVAL, "smat_cell_pool_backward: bad sizes");
-  SMAT_REQUIRE(cw_ok(dtype, r, p, K), SMAT_EUNSUPPORTED,
-               "smat_cell_pool_backward: needs dtype bf16/f16, r=64, p=65 (got %d, %d, %d)",
-               dtype, r, p);
-  SMAT_REQUIRE(rows_vec_ok(dPsi, d_sb, d_st, 4) && aligned16(dF) && f_sb % 4 == 0 &&
+  SMAT_REQUIRE(cw_ok(dtype, out_dtype, r, p, K), SMAT_EUNSUPPORTED,
+               "smat_cell_pool_backward: needs dtype bf16/f16, out_dtype fp32 or dtype, r=64, "
+               "p=65 (got %d, %d, %d, %d)",
+               dtype, out_dtype, r, p);
+  SMAT_REQUIRE(rows_vec_ok(dPsi, d_sb, d_st, elem_bytes(out_dtype)) && aligned16(dF) &&
+                   f_sb % 4 == 0 &&
                    k_st >= r && v_st >= p && e_st >= p && f_sb >= (int64_t)N0 * r * p,
                SMAT_EINVAL, "smat_cell_pool_backward: dPsi and dF must be 16-byte aligned");
   SMAT_REQUIRE(N0 < 65536 * 32 && nb < 65536, SMAT_EUNSUPPORTED,
@@ -373,13 +400,14 @@ extern "C" int smat_cell_pool_backward(int dtype, const void* psi, const void* v
   if (nb == 0) return SMAT_OK;
   const dim3 grid((unsigned)N0, (unsigned)nb);
   hipStream_t st = (hipStream_t)stream;
+  const bool f32 = out_dtype == SMAT_F32;
   if (dtype == SMAT_BF16)
-    hipLaunchKernelGGL(cell_pool_bwd_kernel<bf16>, grid, dim3(cw::kThreads), 0, st,
-                       (const bf16*)psi, (const bf16*)vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K,
-                       k_sb, k_st, v_sb, v_st, f_sb, d_sb, d_st, e_sb, e_st, w_sb);
+    (f32 ? cell_pool_launch<bf16, float> : cell_pool_launch<bf16, bf16>)(
+        grid, st, psi, vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K, k_sb, k_st, v_sb, v_st, f_sb,
+        d_sb, d_st, e_sb, e_st, w_sb);
   else
-    hipLaunchKernelGGL(cell_pool_bwd_kernel<f16>, grid, dim3(cw::kThreads), 0, st,
-                       (const f16*)psi, (const f16*)vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K,
-                       k_sb, k_st, v_sb, v_st, f_sb, d_sb, d_st, e_sb, e_st, w_sb);
+    (f32 ? cell_pool_launch<f16, float> : cell_pool_launch<f16, f16>)(
+        grid, st, psi, vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K, k_sb, k_st, v_sb, v_st, f_sb,
+        d_sb, d_st, e_sb, e_st, w_sb);
   return launch_status("smat_cell_pool_backward");
 }

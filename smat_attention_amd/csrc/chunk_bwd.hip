@@ -56,15 +56,23 @@ struct ChunkBwdArgs {
   int nc;                       // chunks per sequence
   int64_t q_sb, q_st, k_sb, k_st, v_sb, v_st;   // Phi, Psi, Vb (elements)
   int64_t h_sb, h_st;           // dH (floats)
-  int64_t d_sb, d_st;           // dPhi and dPsi (floats)
-  int64_t e_sb, e_st;           // dVb (floats)
+  int64_t d_sb, d_st;           // dPhi and dPsi (elements of Out)
+  int64_t e_sb, e_st;           // dVb (elements of Out)
+  // optional fp32 terms added before the store (NULL: none): add_phi on rows
+  // [add_split, add_end) of dPhi, add_psi and add_vb on rows [0, add_split)
+  // of dPsi and dVb; rows are addressed by their absolute index
+  const float* add_phi;
+  const float* add_psi;
+  const float* add_vb;
+  int64_t ap_sb, ap_st, ak_sb, ak_st, av_sb, av_st;
+  int64_t add_split, add_end;
 };
 
-template <typename In>
+template <typename In, typename Out>
 __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
     const float* __restrict__ dH, const float* __restrict__ Sin, const float* __restrict__ Qs,
-    float* __restrict__ dPhi, float* __restrict__ dPsi, float* __restrict__ dVb, ChunkBwdArgs a) {
+    Out* __restrict__ dPhi, Out* __restrict__ dPsi, Out* __restrict__ dVb, ChunkBwdArgs a) {
   using namespace cb;
   typedef typename Traits<In>::frag Frag;
   typedef typename Traits<In>::half_frag Half;
@@ -226,11 +234,21 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
       }
     }
     // lane (t, g) holds dPhi[t][16 at + 4g + e]
-    float* out = dPhi + b * a.d_sb + (t0 + trow) * a.d_st;
+    const int64_t row = t0 + trow;
+    if (a.add_phi != nullptr && row >= a.add_split && row < a.add_end) {
+      const float* ad = a.add_phi + b * a.ap_sb + row * a.ap_st + 4 * g;
 #pragma unroll
-    for (int at = 0; at < 4; ++at)
-      *reinterpret_cast<float4*>(out + 16 * at + 4 * g) =
-          make_float4(acc[at][0], acc[at][1], acc[at][2], acc[at][3]);
+      for (int at = 0; at < 4; ++at) {
+        const float4 v = *reinterpret_cast<const float4*>(ad + 16 * at);
+        acc[at][0] += v.x;
+        acc[at][1] += v.y;
+        acc[at][2] += v.z;
+        acc[at][3] += v.w;
+      }
+    }
+    Out* out = dPhi + b * a.d_sb + row * a.d_st;
+#pragma unroll
+    for (int at = 0; at < 4; ++at) store_grad4(out + 16 * at + 4 * g, acc[at]);
   }
 
   // ---- column pass: dPsi and dVb rows of tile j = w -----------------------
@@ -360,38 +378,71 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
       }
     }
     // lane (s, g) holds dPsi[s][16 at + 4g + e] and dVb[s][16 ct + 4g + e]
-    float* op = dPsi + b * a.d_sb + (t0 + srow) * a.d_st;
+    const int64_t row = t0 + srow;
+    if (a.add_psi != nullptr && row < a.add_split) {
+      const float* ad = a.add_psi + b * a.ak_sb + row * a.ak_st + 4 * g;
 #pragma unroll
-    for (int at = 0; at < 4; ++at)
-      *reinterpret_cast<float4*>(op + 16 * at + 4 * g) =
-          make_float4(accq[at][0], accq[at][1], accq[at][2], accq[at][3]);
-    float* ov = dVb + b * a.e_sb + (t0 + srow) * a.e_st;
+      for (int at = 0; at < 4; ++at) {
+        const float4 v = *reinterpret_cast<const float4*>(ad + 16 * at);
+        accq[at][0] += v.x;
+        accq[at][1] += v.y;
+        accq[at][2] += v.z;
+        accq[at][3] += v.w;
+      }
+    }
+    if (a.add_vb != nullptr && row < a.add_split) {
+      const float* ad = a.add_vb + b * a.av_sb + row * a.av_st;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) accv[ct][e] += ad[16 * ct + 4 * g + e];
+      if (g == 0) accv[4][0] += ad[64];
+    }
+    Out* op = dPsi + b * a.d_sb + row * a.d_st;
+#pragma unroll
+    for (int at = 0; at < 4; ++at) store_grad4(op + 16 * at + 4 * g, accq[at]);
+    Out* ov = dVb + b * a.e_sb + row * a.e_st;
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ov[16 * ct + 4 * g + e] = accv[ct][e];
-    if (g == 0) ov[64] = accv[4][0];
+      for (int e = 0; e < 4; ++e) ov[16 * ct + 4 * g + e] = from_f32<Out>(accv[ct][e]);
+    if (g == 0) ov[64] = from_f32<Out>(accv[4][0]);
   }
 }
 
-bool chunk_bwd_ok(int dtype, const void* phi, const void* psi, int r, int p, int C,
-                  int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t d_sb,
+bool chunk_bwd_ok(int dtype, int out_dtype, const void* phi, const void* psi, int r, int p,
+                  int C, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t d_sb,
                   int64_t d_st, const void* dphi, const void* dpsi) {
   if (dtype != SMAT_BF16 && dtype != SMAT_F16) return false;
+  if (out_dtype != SMAT_F32 && out_dtype != dtype) return false;
   if (r != cb::kR || p != cb::kP || C != cb::kC) return false;
+  const int ob = elem_bytes(out_dtype);
   return rows_vec_ok(phi, q_sb, q_st, 2) && rows_vec_ok(psi, k_sb, k_st, 2) &&
-         rows_vec_ok(dphi, d_sb, d_st, 4) && rows_vec_ok(dpsi, d_sb, d_st, 4);
+         rows_vec_ok(dphi, d_sb, d_st, ob) && rows_vec_ok(dpsi, d_sb, d_st, ob);
+}
+
+template <typename In, typename Out>
+static void chunk_bwd_launch(const void* phi, const void* psi, const void* vb, const float* dH,
+                             const float* Sin, const float* Q, void* dPhi, void* dPsi, void* dVb,
+                             const ChunkBwdArgs& a, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((chunk_bwd_kernel<In, Out>), grid, dim3(cb::kThreads), 0, st,
+                     (const In*)phi, (const In*)psi, (const In*)vb, dH, Sin, Q, (Out*)dPhi,
+                     (Out*)dPsi, (Out*)dVb, a);
 }
 
 }  // namespace smat
 
-extern "C" int smat_chunk_backward(int dtype, const void* phi, const void* psi, const void* vb,
-                                   const float* dH, const float* Sin, const float* Q, float* dPhi,
-                                   float* dPsi, float* dVb, int nb, int nc, int r, int p, int C,
+extern "C" int smat_chunk_backward(int dtype, int out_dtype, const void* phi, const void* psi,
+                                   const void* vb, const float* dH, const float* Sin,
+                                   const float* Q, void* dPhi, void* dPsi, void* dVb, int nb,
+                                   int nc, int r, int p, int C,
                                    int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st,
                                    int64_t v_sb, int64_t v_st, int64_t h_sb, int64_t h_st,
                                    int64_t d_sb, int64_t d_st, int64_t e_sb, int64_t e_st,
-                                   void* stream) {
+                                   const float* add_phi, const float* add_psi,
+                                   const float* add_vb, int64_t ap_sb, int64_t ap_st,
+                                   int64_t ak_sb, int64_t ak_st, int64_t av_sb, int64_t av_st,
+                                   int64_t add_split, int64_t add_end, void* stream) {
   using namespace smat;
   clear_error();
   SMAT_REQUIRE(phi && psi && vb && dH && Sin && Q && dPhi && dPsi && dVb, SMAT_EINVAL,
@@ -399,24 +450,34 @@ extern "C" int smat_chunk_backward(int dtype, const void* phi, const void* psi, 
   SMAT_REQUIRE(nb >= 0 && nc >= 0, SMAT_EINVAL, "smat_chunk_backward: bad sizes");
   SMAT_REQUIRE(nc < 65536 * 32 && nb < 65536, SMAT_EUNSUPPORTED,
                "smat_chunk_backward: grid %d x %d too large", nc, nb);
-  SMAT_REQUIRE(chunk_bwd_ok(dtype, phi, psi, r, p, C, q_sb, q_st, k_sb, k_st, d_sb, d_st, dPhi,
-                            dPsi),
+  SMAT_REQUIRE(chunk_bwd_ok(dtype, out_dtype, phi, psi, r, p, C, q_sb, q_st, k_sb, k_st, d_sb,
+                            d_st, dPhi, dPsi),
                SMAT_EUNSUPPORTED,
-               "smat_chunk_backward: needs 16-bit inputs, r=64, p=65, C=128 and 16-byte "
-               "aligned rows of Phi, Psi, dPhi and dPsi (got dtype=%d r=%d p=%d C=%d)",
-               dtype, r, p, C);
+               "smat_chunk_backward: needs 16-bit inputs, fp32 or input-typed gradients, r=64, "
+               "p=65, C=128 and 16-byte aligned rows of Phi, Psi, dPhi and dPsi (got dtype=%d "
+               "out_dtype=%d r=%d p=%d C=%d)",
+               dtype, out_dtype, r, p, C);
   SMAT_REQUIRE(v_st >= p && h_st >= p && e_st >= p && d_st >= r, SMAT_EINVAL,
                "smat_chunk_backward: row stride too short");
+  SMAT_REQUIRE(0 <= add_split && add_split <= add_end && add_end <= (int64_t)nc * C &&
+                   (!add_phi || (rows_vec_ok(add_phi, ap_sb, ap_st, 4) && ap_st >= r)) &&
+                   (!add_psi || (rows_vec_ok(add_psi, ak_sb, ak_st, 4) && ak_st >= r)) &&
+                   (!add_vb || av_st >= p),
+               SMAT_EINVAL,
+               "smat_chunk_backward: added terms need 0 <= add_split <= add_end <= nc*C, "
+               "16-byte aligned rows for Phi and Psi and full rows");
   if (nb == 0 || nc == 0) return SMAT_OK;
-  ChunkBwdArgs a{nc, q_sb, q_st, k_sb, k_st, v_sb, v_st, h_sb, h_st, d_sb, d_st, e_sb, e_st};
+  ChunkBwdArgs a{nc,      q_sb,    q_st,    k_sb,  k_st,  v_sb,  v_st,      h_sb,   h_st,
+                 d_sb,    d_st,    e_sb,    e_st,  add_phi, add_psi, add_vb, ap_sb, ap_st,
+                 ak_sb,   ak_st,   av_sb,   av_st, add_split, add_end};
   const dim3 grid((unsigned)nc, (unsigned)nb);
   hipStream_t st = (hipStream_t)stream;
+  const bool f32 = out_dtype == SMAT_F32;
   if (dtype == SMAT_BF16)
-    hipLaunchKernelGGL(chunk_bwd_kernel<bf16>, grid, dim3(cb::kThreads), 0, st,
-                       (const bf16*)phi, (const bf16*)psi, (const bf16*)vb, dH, Sin, Q, dPhi,
-                       dPsi, dVb, a);
+    (f32 ? chunk_bwd_launch<bf16, float> : chunk_bwd_launch<bf16, bf16>)(
+        phi, psi, vb, dH, Sin, Q, dPhi, dPsi, dVb, a, grid, st);
   else
-    hipLaunchKernelGGL(chunk_bwd_kernel<f16>, grid, dim3(cb::kThreads), 0, st, (const f16*)phi,
-                       (const f16*)psi, (const f16*)vb, dH, Sin, Q, dPhi, dPsi, dVb, a);
+    (f32 ? chunk_bwd_launch<f16, float> : chunk_bwd_launch<f16, f16>)(
+        phi, psi, vb, dH, Sin, Q, dPhi, dPsi, dVb, a, grid, st);
   return launch_status("smat_chunk_backward");
 }

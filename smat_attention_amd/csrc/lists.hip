@@ -103,12 +103,14 @@ __global__ __launch_bounds__(cs::kThreads) void csr_scan_kernel(int* __restrict_
   if (b == nb - 1 && threadIdx.x == 0) offs[(int64_t)nb * ncls] = (int64_t)nb * L;
 }
 
-// One wave per tile: order[b L + base(c) + rank] = item (b L + i with glob,
-// else i), items taken in order 64 at a time; bases are relative to b L.
+// One wave per tile: order[b L + base(c) + rank] = item (b seq_rows + row0 + i
+// with glob, else i), items taken in order 64 at a time; bases are relative
+// to b L.
 __global__ __launch_bounds__(64) void csr_place_kernel(const int64_t* __restrict__ keys,
                                                        const int* __restrict__ bases,
                                                        int32_t* __restrict__ order, int L,
-                                                       int ncls, int ntiles, int nbits, int glob) {
+                                                       int ncls, int ntiles, int nbits, int glob,
+                                                       int64_t seq_rows, int64_t row0) {
   extern __shared__ int next[];                      // ncls ints
   const int t = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x;
@@ -131,7 +133,7 @@ __global__ __launch_bounds__(64) void csr_place_kernel(const int64_t* __restrict
     const int pos = valid ? next[key] + __popcll(match & below) : 0;
     __syncthreads();                                 // all reads of next[] before the update
     if (valid) {
-      order[(int64_t)b * L + pos] = glob ? (int32_t)((int64_t)b * L + i) : (int32_t)i;
+      order[(int64_t)b * L + pos] = glob ? (int32_t)((int64_t)b * seq_rows + row0 + i) : (int32_t)i;
       // the highest lane of each key group advances that key's cursor
       if ((match >> lane) == 1ull) next[key] += __popcll(match);
     }
@@ -148,11 +150,18 @@ extern "C" int64_t smat_csr_workspace_bytes(int nb, int L, int ncls) {
 }
 
 extern "C" int smat_csr_lists(const int64_t* keys, int32_t* order, int64_t* offs, void* workspace,
-                              int nb, int L, int ncls, int global_index, void* stream) {
+                              int nb, int L, int ncls, int global_index, int64_t seq_rows,
+                              int64_t row0, void* stream) {
   using namespace smat;
   clear_error();
   SMAT_REQUIRE(offs && (nb == 0 || L == 0 || (keys && order && workspace)), SMAT_EINVAL,
                "smat_csr_lists: null pointer");
+  SMAT_REQUIRE(!global_index || (seq_rows >= L && row0 >= 0 && row0 <= seq_rows - L &&
+                                   (int64_t)nb * seq_rows < (1ll << 31)),
+               SMAT_EINVAL,
+               "smat_csr_lists: global items need L <= seq_rows, 0 <= row0 <= seq_rows - L and "
+               "nb*seq_rows < 2^31 (L=%d seq_rows=%lld row0=%lld)", L, (long long)seq_rows,
+               (long long)row0);
   SMAT_REQUIRE(nb >= 0 && L >= 0 && ncls >= 1 && ncls <= cs::kMaxCls &&
                    (int64_t)nb * L < (1ll << 31),
                SMAT_EUNSUPPORTED, "smat_csr_lists: need 1 <= ncls <= %d and nb*L < 2^31",
@@ -177,6 +186,6 @@ extern "C" int smat_csr_lists(const int64_t* keys, int32_t* order, int64_t* offs
                      ncls, ntiles);
   if (ntiles)
     hipLaunchKernelGGL(csr_place_kernel, dim3(ntiles, nb), dim3(64), lds, st, keys, counts, order,
-                       L, ncls, ntiles, nbits, global_index);
+                       L, ncls, ntiles, nbits, global_index, seq_rows, row0);
   return launch_status("smat_csr_lists");
 }

@@ -45,7 +45,7 @@ template <typename In>
 __global__ __launch_bounds__(lr::kThreads) void lr_dphi_kernel(
     const float* __restrict__ dH, const float* __restrict__ U, float* __restrict__ dPhi,
     int T_R, int B, int n, int64_t h_sb, int64_t h_st, int64_t u_sb, int64_t d_sb,
-    int64_t d_st) {
+    int64_t d_st, int accumulate) {
   using namespace cb;
   __shared__ __attribute__((aligned(16))) float sU[kR * kS];
   const int h = blockIdx.x;
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dphi_kernel(
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ut, yt, acc, 0, 0, 0);
     if (ok) {
       float4* o = reinterpret_cast<float4*>(dPb + row * d_st + 16 * w + 4 * g);
-      float4 cur = *o;
+      float4 cur = accumulate ? *o : make_float4(0.f, 0.f, 0.f, 0.f);
       cur.x += acc[0];
       cur.y += acc[1];
       cur.z += acc[2];
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(lr::kThreads) void lr_pool_bwd_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, const float* __restrict__ dF,
     float* __restrict__ dPsi, float* __restrict__ dVb, int N0, int n, int n_P, int64_t k_sb,
     int64_t k_st, int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
-    int64_t e_sb, int64_t e_st) {
+    int64_t e_sb, int64_t e_st, int accumulate) {
   using namespace cb;
   typedef typename Traits<In>::frag Frag;
   typedef typename Traits<In>::half_frag Half;
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(lr::kThreads) void lr_pool_bwd_kernel(
     if (ok) {
       // lane (j, g): dPsi[j][16w + 4g + e], dVb[j][16w + 4g + e] (and dVb[j][64])
       float4* o = reinterpret_cast<float4*>(dPb + j * d_st + 16 * w + 4 * g);
-      float4 cur = *o;
+      float4 cur = accumulate ? *o : make_float4(0.f, 0.f, 0.f, 0.f);
       cur.x += ap[0];
       cur.y += ap[1];
       cur.z += ap[2];
@@ -308,8 +308,8 @@ __global__ __launch_bounds__(lr::kThreads) void lr_pool_bwd_kernel(
       *o = cur;
       float* ov = dVbb + j * e_st + 16 * w + 4 * g;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ov[e] += av[e];
-      if (w == 0 && g == 0) dVbb[j * e_st + 64] += av4[0];
+      for (int e = 0; e < 4; ++e) ov[e] = (accumulate ? ov[e] : 0.f) + av[e];
+      if (w == 0 && g == 0) dVbb[j * e_st + 64] = (accumulate ? dVbb[j * e_st + 64] : 0.f) + av4[0];
     }
   }
 }
@@ -322,7 +322,8 @@ static bool lr_shape_ok(int dtype, int r, int p) {
 
 extern "C" int smat_lr_dphi(int dtype, const float* dH, const float* U, float* dPhi, int nb,
                             int T_R, int B, int n, int r, int p, int64_t h_sb, int64_t h_st,
-                            int64_t u_sb, int64_t d_sb, int64_t d_st, void* stream) {
+                            int64_t u_sb, int64_t d_sb, int64_t d_st, int accumulate,
+                            void* stream) {
   using namespace smat;
   clear_error();
   SMAT_REQUIRE(dH && U && dPhi, SMAT_EINVAL, "smat_lr_dphi: null pointer");
@@ -338,10 +339,10 @@ extern "C" int smat_lr_dphi(int dtype, const float* dH, const float* U, float* d
   hipStream_t st = (hipStream_t)stream;
   if (dtype == SMAT_BF16)
     hipLaunchKernelGGL(lr_dphi_kernel<bf16>, grid, dim3(lr::kThreads), 0, st, dH, U, dPhi, T_R, B,
-                       n, h_sb, h_st, u_sb, d_sb, d_st);
+                       n, h_sb, h_st, u_sb, d_sb, d_st, accumulate);
   else
     hipLaunchKernelGGL(lr_dphi_kernel<f16>, grid, dim3(lr::kThreads), 0, st, dH, U, dPhi, T_R, B,
-                       n, h_sb, h_st, u_sb, d_sb, d_st);
+                       n, h_sb, h_st, u_sb, d_sb, d_st, accumulate);
   return launch_status("smat_lr_dphi");
 }
 
@@ -375,7 +376,7 @@ extern "C" int smat_pool_backward(int dtype, const void* psi, const void* vb, co
                                   float* dPsi, float* dVb, int nb, int N0, int n, int n_P, int r,
                                   int p, int64_t k_sb, int64_t k_st, int64_t v_sb, int64_t v_st,
                                   int64_t f_sb, int64_t d_sb, int64_t d_st, int64_t e_sb,
-                                  int64_t e_st, void* stream) {
+                                  int64_t e_st, int accumulate, void* stream) {
   using namespace smat;
   clear_error();
   SMAT_REQUIRE(psi && vb && dF && dPsi && dVb, SMAT_EINVAL, "smat_pool_backward: null pointer");
@@ -396,10 +397,10 @@ extern "C" int smat_pool_backward(int dtype, const void* psi, const void* vb, co
   if (dtype == SMAT_BF16)
     hipLaunchKernelGGL(lr_pool_bwd_kernel<bf16>, grid, dim3(lr::kThreads), 0, st,
                        (const bf16*)psi, (const bf16*)vb, dF, dPsi, dVb, N0, n, n_P, k_sb, k_st,
-                       v_sb, v_st, f_sb, d_sb, d_st, e_sb, e_st);
+                       v_sb, v_st, f_sb, d_sb, d_st, e_sb, e_st, accumulate);
   else
     hipLaunchKernelGGL(lr_pool_bwd_kernel<f16>, grid, dim3(lr::kThreads), 0, st, (const f16*)psi,
                        (const f16*)vb, dF, dPsi, dVb, N0, n, n_P, k_sb, k_st, v_sb, v_st, f_sb,
-                       d_sb, d_st, e_sb, e_st);
+                       d_sb, d_st, e_sb, e_st, accumulate);
   return launch_status("smat_pool_backward");
 }

@@ -69,18 +69,19 @@ SIGNATURES = {
                                              _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "smat_bgemm": (_i, [_i, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64,
                         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i, _i, _p]),
-    "smat_chunk_backward": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,
+    "smat_chunk_backward": (_i, [_i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,
                                  _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                 _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _i64, _p]),
     "smat_lr_dphi": (_i, [_i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64,
-                          _i64, _p]),
+                          _i64, _i, _p]),
     "smat_lr_dfeat": (_i, [_i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _i64,
                            _i64, _p]),
     "smat_pool_backward": (_i, [_i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i64,
-                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
-    "smat_cell_read_backward": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,
+                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p]),
+    "smat_cell_read_backward": (_i, [_i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,
                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
-    "smat_cell_pool_backward": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,
+    "smat_cell_pool_backward": (_i, [_i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,
                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _i64, _p]),
     "smat_featurise_backward_parts": (_i64, [_i, _i]),
@@ -89,7 +90,7 @@ SIGNATURES = {
                                 _i64, _i64, _i64, _i64, _i64, _p, _i64, _p]),
     "smat_forward_fused_workspace_bytes": (_i64, [_i, _i, _i, _i, _i, _i, _i]),
     "smat_csr_workspace_bytes": (_i64, [_i, _i, _i]),
-    "smat_csr_lists": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "smat_csr_lists": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _p]),
     "smat_featurise_backward": (_i, [_i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,
                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "smat_pool_workspace_bytes": (_i64, [_i, _i, _i, _i, _i, _i]),

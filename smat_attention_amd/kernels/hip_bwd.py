@@ -168,38 +168,58 @@ def fused_chunk_backward_ok(Ph, Ps, Vv, C: int) -> bool:
             and Ph.data_ptr() % 16 == 0 and Ps.data_ptr() % 16 == 0)
 
 
-def causal_scan_grad(Ph, Ps, Vv, dH, n: int, C: int):
+def causal_scan_grad(Ph, Ps, Vv, dH, n: int, C: int, out_dtype=None, add=None):
     """``(dPhi, dPsi, dVb)`` of the segmented causal scan ``H`` (attention.py:134-192)
-    given ``dH``: inputs padded to whole chunks of ``C`` rows, fp32 ``(nb, Tp, .)``
-    gradients (the rows past the input are zero-padding).  Chunk states and
-    their per-segment exclusive scan, the reverse scan of ``Phi_b^T dH_b``, and
-    the per-chunk products, all on smat_bgemm and the segment-scan kernels."""
+    given ``dH``: inputs padded to whole chunks of ``C`` rows, ``(nb, Tp, .)``
+    gradients (the rows past the input are zero-padding), fp32 -- or, with
+    ``out_dtype`` the inputs' 16-bit type and the fused chunk backward serving
+    the shape, rounded to that type by the kernel that forms them.  ``add``
+    (fused chunk backward only): ``(aPhi, aPsi, aVb, split, end)``, fp32 terms
+    the kernel adds before the store -- aPhi's rows [split, end) to dPhi,
+    aPsi's and aVb's rows [0, split) to dPsi and dVb (absolute row indices;
+    aPsi / aVb may be None).  Chunk states and their per-segment exclusive
+    scan, the reverse scan of ``Phi_b^T dH_b``, and the per-chunk products, all
+    on smat_bgemm and the segment-scan kernels."""
     nb, Tp, r = Ph.shape
     p = Vv.shape[-1]
     nc = Tp // C
     dev = Ph.device
-    dPhi = torch.empty(nb, Tp, r, device=dev, dtype=torch.float32)
-    dPsi = torch.empty(nb, Tp, r, device=dev, dtype=torch.float32)
-    dVb = torch.empty(nb, Tp, p, device=dev, dtype=torch.float32)
+    fused = fused_chunk_backward_ok(Ph, Ps, Vv, C)
+    if add is not None and not fused:
+        raise ValueError("causal_scan_grad: added terms need the fused chunk backward")
+    gdt = out_dtype if (fused and out_dtype == Ph.dtype) else torch.float32
+    dPhi = torch.empty(nb, Tp, r, device=dev, dtype=gdt)
+    dPsi = torch.empty(nb, Tp, r, device=dev, dtype=gdt)
+    dVb = torch.empty(nb, Tp, p, device=dev, dtype=gdt)
     D = _hip.chunk_states(Ps, Vv, C)                    # (nb, nc, r, p)
     Sin = _hip.segment_scan(D, n // C)
     Dr = torch.empty(nb, nc, r, p, device=dev, dtype=torch.float32)
     rp = r * p
-    # Dr_b = Phi_b^T dH_b
+    # Dr_b = Phi_b^T dH_b (rows of Phi and dH at their own strides)
+    qb, qt = Ph.stride(0), Ph.stride(1)
+    hb, ht = dH.stride(0), dH.stride(1)
     _bgemm(Ph, dH, Dr, M=r, N=p, K=C, n1=nb, n2=nc,
-           a=(Tp * r, C * r, 1, r), b=(Tp * p, C * p, p, 1), c=(nc * rp, rp, p, 1))
+           a=(qb, C * qt, 1, qt), b=(hb, C * ht, ht, 1), c=(nc * rp, rp, p, 1))
     Q = torch.empty_like(Dr)
     call("smat_segment_scan_reverse", Dr.data_ptr(), Q.data_ptr(), nb, nc, n // C, rp,
          stream_of(Q))
     del Dr
-    if fused_chunk_backward_ok(Ph, Ps, Vv, C):
+    if fused:
         # A and dA stay on chip: one launch for the six products below
-        call("smat_chunk_backward", _code(Ph), Ph.data_ptr(), Ps.data_ptr(), Vv.data_ptr(),
-             dH.data_ptr(), Sin.data_ptr(), Q.data_ptr(), dPhi.data_ptr(), dPsi.data_ptr(),
-             dVb.data_ptr(), nb, nc, r, p, C, Ph.stride(0), Ph.stride(1), Ps.stride(0),
-             Ps.stride(1), Vv.stride(0), Vv.stride(1), dH.stride(0), dH.stride(1),
-             dPhi.stride(0), dPhi.stride(1), dVb.stride(0), dVb.stride(1), stream_of(dPhi))
+        aP, aS, aV, split, end = add if add is not None else (None, None, None, 0, 0)
+
+        def sb(x, i):
+            return x.stride(i) if x is not None else 0
+        call("smat_chunk_backward", _code(Ph), _code(dPhi), Ph.data_ptr(), Ps.data_ptr(),
+             Vv.data_ptr(), dH.data_ptr(), Sin.data_ptr(), Q.data_ptr(), dPhi.data_ptr(),
+             dPsi.data_ptr(), dVb.data_ptr(), nb, nc, r, p, C, Ph.stride(0), Ph.stride(1),
+             Ps.stride(0), Ps.stride(1), Vv.stride(0), Vv.stride(1), dH.stride(0), dH.stride(1),
+             dPhi.stride(0), dPhi.stride(1), dVb.stride(0), dVb.stride(1), ptr(aP), ptr(aS),
+             ptr(aV), sb(aP, 0), sb(aP, 1), sb(aS, 0), sb(aS, 1), sb(aV, 0), sb(aV, 1), split, end,
+             stream_of(dPhi))
         return dPhi, dPsi, dVb
+    # the products below address Phi, Psi, Vb and dH as contiguous rows
+    Ph, Ps, Vv, dH = (x.contiguous() for x in (Ph, Ps, Vv, dH))
     A = torch.empty(nb, nc, C, C, device=dev, dtype=torch.float32)
     dA = torch.empty_like(A)
     CC = C * C
@@ -288,10 +308,12 @@ def _profile_pool_grad(Ps, Vv, dF, dPsi, dVb, Tp: int, n_P: int, n: int, N0: int
 
 
 def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=None,
-                        need_dg: bool = False):
+                        need_dg: bool = False, out_dtype=None):
     """``(dPhi, dPsi, dVb, dg)`` of ``out = smat_attention(Phi, Psi, Vb, spec, g=g)``
     given the forward's ``U`` (nb, B, r, p) and ``H`` (nb, T, p, long-range
-    term included), fp32 gradients."""
+    term included), fp32 gradients -- or, with ``out_dtype`` the inputs'
+    16-bit type where the fused kernels serve the shape, gradients rounded to
+    that type once, by the kernel that adds the last term (dg stays fp32)."""
     nb, T, r = Phi.shape
     p = Vb.shape[-1]
     C = min(chunk, T)
@@ -304,16 +326,19 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
     # ---- normalise --------------------------------------------------------
     dout = dout.float().contiguous()
     H = H.float().contiguous()
-    dH = torch.zeros(nb, Tp, p, device=dev, dtype=torch.float32)      # rows >= T stay 0
+    dH = torch.empty(nb, Tp, p, device=dev, dtype=torch.float32)
+    if Tp > T:
+        dH[:, T:].zero_()                                              # padding rows
     dg = torch.empty(nb, T, device=dev, dtype=torch.float32) if need_dg else None
     gc = g.float().contiguous() if g is not None else None
     call("smat_normalise_backward", dout.data_ptr(), H.data_ptr(), ptr(gc), dH.data_ptr(),
          ptr(dg), nb, T, p, dout.stride(0), dout.stride(1), H.stride(0), H.stride(1),
          dH.stride(0), dH.stride(1), gc.stride(0) if gc is not None else 0, stream_of(dH))
 
-    # inputs padded to whole chunks (zeros contribute nothing)
+    # inputs padded to whole chunks (zeros contribute nothing); rows of unit
+    # column stride are used where they lie
     def padded(x):
-        x = x.contiguous()
+        x = x if x.stride(-1) == 1 else x.contiguous()
         if Tp == T:
             return x
         out = torch.zeros(nb, Tp, x.shape[-1], device=dev, dtype=x.dtype)
@@ -321,9 +346,40 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
         return out
 
     Ph, Ps, Vv = padded(Phi), padded(Psi), padded(Vb)
+    rp = r * p
+
+    if (T_R > 0 and long_range_backward_ok(Ph, Ps, Vv) and fused_chunk_backward_ok(Ph, Ps, Vv, C)
+            and out_dtype == Ph.dtype):
+        # the long-range terms first, stored as fp32 rows (each row has one
+        # row type, each landmark row one profile): the chunk backward adds
+        # them to the causal terms and rounds each sum once
+        st = stream_of(dH)
+        Uc = U.float().contiguous()
+        code = _code(Ph)
+        aPhi = torch.empty(nb, T, r, device=dev, dtype=torch.float32)     # rows [n, T)
+        call("smat_lr_dphi", code, dH.data_ptr(), Uc.data_ptr(), aPhi.data_ptr(), nb, T_R, B, n,
+             r, p, dH.stride(0), dH.stride(1), Uc.stride(0), aPhi.stride(0), aPhi.stride(1), 0,
+             st)
+        aPsi = aVb = None
+        if n > 0:
+            tptr, tok = recent_token_lists(spec, dev)
+            nitems = N0 + (1 if n_P else 0)
+            dF = torch.empty(nb, nitems, r, p, device=dev, dtype=torch.float32)
+            call("smat_lr_dfeat", code, Ph.data_ptr(), dH.data_ptr(), tptr.data_ptr(),
+                 tok.data_ptr(), dF.data_ptr(), nb, nitems, r, p, Ph.stride(0), Ph.stride(1),
+                 dH.stride(0), dH.stride(1), dF.stride(0), st)
+            aPsi = torch.empty(nb, n, r, device=dev, dtype=torch.float32)
+            aVb = torch.empty(nb, n, p, device=dev, dtype=torch.float32)
+            call("smat_pool_backward", code, Ps.data_ptr(), Vv.data_ptr(), dF.data_ptr(),
+                 aPsi.data_ptr(), aVb.data_ptr(), nb, N0, n, n_P, r, p, Ps.stride(0),
+                 Ps.stride(1), Vv.stride(0), Vv.stride(1), dF.stride(0), aPsi.stride(0),
+                 aPsi.stride(1), aVb.stride(0), aVb.stride(1), 0, st)
+            del dF
+        dPhi, dPsi, dVb = causal_scan_grad(Ph, Ps, Vv, dH, n, C, out_dtype=out_dtype,
+                                           add=(aPhi, aPsi, aVb, n, T))
+        return dPhi[:, :T], dPsi[:, :T], dVb[:, :T], dg
 
     dPhi, dPsi, dVb = causal_scan_grad(Ph, Ps, Vv, dH, n, C)
-    rp = r * p
 
     # ---- long range --------------------------------------------------------
     if T_R > 0 and long_range_backward_ok(Ph, Ps, Vv):
@@ -333,7 +389,8 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
         Uc = U.float().contiguous()
         code = _code(Ph)
         call("smat_lr_dphi", code, dH.data_ptr(), Uc.data_ptr(), dPhi.data_ptr(), nb, T_R, B, n,
-             r, p, dH.stride(0), dH.stride(1), Uc.stride(0), dPhi.stride(0), dPhi.stride(1), st)
+             r, p, dH.stride(0), dH.stride(1), Uc.stride(0), dPhi.stride(0), dPhi.stride(1), 1,
+             st)
         tptr, tok = recent_token_lists(spec, dev)
         nitems = N0 + (1 if n_P else 0)
         dF = torch.empty(nb, nitems, r, p, device=dev, dtype=torch.float32)
@@ -343,7 +400,7 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
         call("smat_pool_backward", code, Ps.data_ptr(), Vv.data_ptr(), dF.data_ptr(),
              dPsi.data_ptr(), dVb.data_ptr(), nb, N0, n, n_P, r, p, Ps.stride(0), Ps.stride(1),
              Vv.stride(0), Vv.stride(1), dF.stride(0), dPsi.stride(0), dPsi.stride(1),
-             dVb.stride(0), dVb.stride(1), st)
+             dVb.stride(0), dVb.stride(1), 1, st)
     elif T_R > 0:
         Uc = U.float().contiguous()
         dU = _type_read_grad(Ph, dH, Uc, dPhi, Tp, n, T_R, B)
@@ -392,7 +449,8 @@ class SmatAttentionFunction(torch.autograd.Function):
         Phi, Psi, Vb, g, U, H = ctx.saved_tensors
         need_dg = g is not None and ctx.needs_input_grad[3]
         dPhi, dPsi, dVb, dg = smat_attention_grad(Phi, Psi, Vb, ctx.spec, U, H, dout,
-                                                  chunk=ctx.chunk, g=g, need_dg=need_dg)
+                                                  chunk=ctx.chunk, g=g, need_dg=need_dg,
+                                                  out_dtype=Phi.dtype)
         return (dPhi.to(Phi.dtype) if ctx.needs_input_grad[0] else None,
                 dPsi.to(Psi.dtype) if ctx.needs_input_grad[1] else None,
                 dVb.to(Vb.dtype) if ctx.needs_input_grad[2] else None,
@@ -500,14 +558,16 @@ class CausalScanFunction(torch.autograd.Function):
         Tp = -(-T // C) * C
 
         def padded(x, dt=None):
-            x = x.contiguous() if dt is None else x.to(dt).contiguous()
+            x = x if dt is None else x.to(dt)
+            x = x if x.stride(-1) == 1 else x.contiguous()
             if Tp == T:
                 return x
             out = torch.zeros(nb, Tp, x.shape[-1], device=x.device, dtype=x.dtype)
             out[:, :T] = x
             return out
         dPhi, dPsi, dVb = causal_scan_grad(padded(Phi), padded(Psi), padded(Vb),
-                                           padded(dH, torch.float32), ctx.n, C)
+                                           padded(dH, torch.float32), ctx.n, C,
+                                           out_dtype=Phi.dtype)
         return (dPhi[:, :T].to(Phi.dtype), dPsi[:, :T].to(Psi.dtype), dVb[:, :T].to(Vb.dtype),
                 None, None, None)
 

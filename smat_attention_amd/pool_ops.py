@@ -51,20 +51,25 @@ def _csr(key, nkeys):
 _CSR_MAX_CLASSES = 8192
 
 
-def _class_lists(keys, ncls, global_index=True):
+def _class_lists(keys, ncls, global_index=True, seq_rows=None, row0=0):
     """Lists of every (sequence, class): keys (nb, L) in [0, ncls) -> order
     (nb*L,) int32, the items of sequence 0's class 0, class 1, ..., then
     sequence 1's, each list in item order (the stable sort of ``b*ncls + key``);
-    an item is ``b*L + l`` (``global_index``) or ``l``.  offs (nb*ncls + 1,)
+    an item is ``b*seq_rows + row0 + l`` (``global_index``: the row of the item
+    in a tensor of sequences ``seq_rows`` rows long, whose rows ``[row0, row0 +
+    L)`` the keys label; by default ``b*L + l``) or ``l``.  offs (nb*ncls + 1,)
     int64.  A counting sort on the device (``smat_csr_lists``), nothing read
     back to the host."""
     nb, L = keys.shape
     dev = keys.device
+    seq_rows = L if seq_rows is None else int(seq_rows)
     if ncls > _CSR_MAX_CLASSES:
         flat = (torch.arange(nb, device=dev).unsqueeze(1) * ncls + keys).reshape(-1)
         order, offs = _csr(flat, nb * ncls)
         if not global_index:
             order = order % max(L, 1)
+        elif seq_rows != L or row0:
+            order = order + (order // max(L, 1)) * (seq_rows - L) + row0
         return order.to(torch.int32), offs
     k = keys if (keys.dtype == torch.int64 and keys.is_contiguous()) else \
         keys.to(torch.int64).contiguous()
@@ -73,7 +78,7 @@ def _class_lists(keys, ncls, global_index=True):
     ws = torch.empty(max(1, _lib.query("smat_csr_workspace_bytes", nb, L, ncls)), device=dev,
                      dtype=torch.uint8)
     call("smat_csr_lists", k.data_ptr(), order.data_ptr(), offs.data_ptr(), ws.data_ptr(), nb, L,
-         ncls, int(global_index), stream_of(k))
+         ncls, int(global_index), seq_rows, int(row0), stream_of(k))
     return order, offs
 
 
@@ -83,12 +88,14 @@ def _list_hint(n, ncls):
     return 2 * -(-n // max(ncls, 1))
 
 
-def _lists(cls, ncls):
+def _lists(cls, ncls, seq_rows=None, row0=0):
     """CSR of the rows of each (sequence, class): cls (nb, L) int -> row indices
-    (int32, into the (nb*L) flattened rows, ascending within a class), offsets
-    (int64, nb*ncls + 1) and the list-length hint of the query kernel."""
+    (int32, into the flattened rows of sequences ``seq_rows`` rows long whose
+    rows ``[row0, row0 + L)`` cls labels -- by default the (nb*L) rows --
+    ascending within a class), offsets (int64, nb*ncls + 1) and the
+    list-length hint of the query kernel."""
     nb, L = cls.shape
-    order, offs = _class_lists(cls, ncls)
+    order, offs = _class_lists(cls, ncls, seq_rows=seq_rows, row0=row0)
     return order, offs, _list_hint(L, ncls)
 
 

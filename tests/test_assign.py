@@ -406,7 +406,8 @@ def test_class_lists_match_stable_sort(nb, L, ncls):
         # the one offset of an empty batch is written, not left as it was
         from smat_attention_amd.kernels._lib import call, stream_of
         offs = torch.full((1,), 7, device=dev, dtype=torch.int64)
-        call("smat_csr_lists", None, None, offs.data_ptr(), None, 0, L, ncls, 1, stream_of(offs))
+        call("smat_csr_lists", None, None, offs.data_ptr(), None, 0, L, ncls, 1, L, 0,
+             stream_of(offs))
         assert offs.item() == 0
 
 

@@ -393,6 +393,11 @@ def test_fused_chunk_backward(T, n):
         _say(f"  {name}: vs bgemm {e_chain:.2e}, vs fp64 {e_64:.2e}")
         assert e_chain < 1e-4 and e_64 < 1e-4, name
         assert torch.isfinite(a).all()
+    # gradients stored in bf16 by the kernel: the fp32 ones rounded to nearest
+    # even, bit for bit (the same accumulators, only the store differs)
+    g16 = [x.cpu() for x in HB.causal_scan_grad(*args, n, C, out_dtype=bf)]
+    for name, a, b in zip(("dPhi", "dPsi", "dVb"), g16, got):
+        assert a.dtype == bf and torch.equal(a, b.to(bf)), name
 
 
 @pytest.mark.parametrize("T,d,n_P,gate", [(4096, 3, 0, False), (4096, 2, 0, False),
@@ -435,6 +440,12 @@ def test_fused_attention_backward(T, d, n_P, gate):
         _say(f"  {name}: vs bgemm {e_chain:.2e}, vs fp64 (norm) {e_64:.2e}")
         assert torch.isfinite(a).all()
         assert e_chain < 1e-4 and e_64 < 2e-2, name
+    # gradients in bf16: the long-range terms stored first and added by the
+    # chunk backward form the same fp32 sums as the fp32 path, rounded once
+    g16 = [y.cpu() for y in HB.smat_attention_grad(*xs, spec, parts["U"], parts["H"], dout,
+                                                   g=gd, out_dtype=torch.bfloat16)[:3]]
+    for name, a, b in zip(("dPhi", "dPsi", "dVb"), g16, got):
+        assert a.dtype == torch.bfloat16 and torch.equal(a, b.to(torch.bfloat16)), name
 
 
 @pytest.mark.parametrize("d", [2, 3])
@@ -478,6 +489,60 @@ def test_fused_cell_backward(d):
         _say(f"  {name}: {e:.2e}")
         assert torch.isfinite(a).all()
         assert e < (2e-3 if name in ("dQ", "dK", "dV") else 1e-4), name
+
+
+def test_cell_backward_16bit_outputs_are_rounded_fp32():
+    """smat_cell_read_backward and smat_cell_pool_backward with out_dtype bf16
+    store the fp32 results rounded to nearest even, bit for bit, into rows of
+    larger tensors (the key rows [0, n) and query rows [n, T) of (nb, T, .)
+    gradients) and write every row a pair-0 entry names: the buffers start as
+    NaN, and the rows outside are left untouched."""
+    from smat_attention_amd import assign as AS
+    from smat_attention_amd.kernels.hip_fwd import call, stream_of
+    nb, T, n, N0, K, r, p = 3, 1500, 700, 37, 4, 64, 65
+    gen = torch.Generator().manual_seed(91)
+    bf = torch.bfloat16
+    X = (torch.rand(nb, T, r, generator=gen) + 0.1).to(bf).to(DEV)      # Phi / Psi
+    Vb = torch.randn(nb, T, p, generator=gen).to(bf).to(DEV)
+    dY = torch.randn(nb, T - n, p, generator=gen).to(DEV)
+    F = torch.randn(nb, N0, r, p, generator=gen).to(DEV)
+    idx = torch.randint(0, N0, (nb, T - n, K), generator=gen).to(DEV)
+    idk = torch.randint(0, N0, (nb, n, K), generator=gen).to(DEV)
+
+    def read(out_dt):
+        ent, eoffs = AS._entry_lists(idx, N0)
+        dX = torch.full((nb, T, r), float("nan"), device=DEV, dtype=out_dt)
+        dF = torch.empty(nb, N0, r, p, device=DEV)
+        dw = torch.empty(nb, T - n, K, device=DEV)
+        Xr, dXr = X[:, n:], dX[:, n:]
+        call("smat_cell_read_backward", 0, AS._code(dXr, "t"), Xr.data_ptr(), dY.data_ptr(),
+             F.data_ptr(), ent.data_ptr(), eoffs.data_ptr(), dXr.data_ptr(), dF.data_ptr(),
+             dw.data_ptr(), nb, N0, K, r, p, Xr.stride(0), Xr.stride(1), dY.stride(0),
+             dY.stride(1), F.stride(0), dXr.stride(0), dXr.stride(1), dw.stride(0),
+             stream_of(F))
+        return dX.cpu(), dF.cpu(), dw.cpu()
+
+    def pool(out_dt):
+        ent, eoffs = AS._entry_lists(idk, N0)
+        dX = torch.full((nb, T, r), float("nan"), device=DEV, dtype=out_dt)
+        dV = torch.full((nb, T, p), float("nan"), device=DEV, dtype=out_dt)
+        dw = torch.empty(nb, n, K, device=DEV)
+        call("smat_cell_pool_backward", 0, AS._code(dX, "t"), X.data_ptr(), Vb.data_ptr(),
+             F.data_ptr(), ent.data_ptr(), eoffs.data_ptr(), dX.data_ptr(), dV.data_ptr(),
+             dw.data_ptr(), nb, N0, K, r, p, X.stride(0), X.stride(1), Vb.stride(0),
+             Vb.stride(1), F.stride(0), dX.stride(0), dX.stride(1), dV.stride(0), dV.stride(1),
+             dw.stride(0), stream_of(F))
+        return dX.cpu(), dV.cpu(), dw.cpu()
+    _say("cell backward 16-bit outputs", nb, T, n, N0, K)
+    (a32, f32, w32), (a16, f16_, w16) = read(torch.float32), read(bf)
+    assert torch.isfinite(a32[:, n:]).all() and torch.isnan(a32[:, :n]).all()
+    assert torch.equal(a16[:, n:], a32[:, n:].to(bf)) and torch.isnan(a16[:, :n].float()).all()
+    assert torch.equal(f16_, f32) and torch.equal(w16, w32)
+    (p32, v32, w32), (p16, v16, w16) = pool(torch.float32), pool(bf)
+    for a, b in ((p16, p32), (v16, v32)):
+        assert torch.isfinite(b[:, :n]).all() and torch.isnan(b[:, n:]).all()
+        assert torch.equal(a[:, :n], b[:, :n].to(bf)) and torch.isnan(a[:, n:].float()).all()
+    assert torch.equal(w16, w32)
 
 
 def test_fp16_attention_backward_takes_fp32_products():
