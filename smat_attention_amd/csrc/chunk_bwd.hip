@@ -54,6 +54,7 @@ namespace smat {
 
 struct ChunkBwdArgs {
   int nc;                       // chunks per sequence
+  int vec_dh, vec_vb;           // dH / Vb staged in 16-byte loads (see the kernel)
   int64_t q_sb, q_st, k_sb, k_st, v_sb, v_st;   // Phi, Psi, Vb (elements)
   int64_t h_sb, h_st;           // dH (floats)
   int64_t d_sb, d_st;           // dPhi and dPsi (elements of Out)
@@ -79,10 +80,16 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
   __shared__ __attribute__((aligned(16))) uint4 sPhi[kC * kRowChunks];
   __shared__ __attribute__((aligned(16))) uint4 sPsi[kC * kRowChunks];
   __shared__ __attribute__((aligned(16))) uint4 sVb[kC * kRowChunks];
-  __shared__ __attribute__((aligned(16))) float sdH[kC * kS];
-  __shared__ __attribute__((aligned(16))) float sSin[kR * kS];
-  __shared__ __attribute__((aligned(16))) float sQ[kR * kS];
-  __shared__ In sVb64[kC];
+  // the fp32 operands split once into 16-bit hi and lo tiles, laid out as the
+  // 16-bit ones (columns 0..63 swizzled, column 64 on its own)
+  __shared__ __attribute__((aligned(16))) uint4 sdHh[kC * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sdHl[kC * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sSinh[kR * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sSinl[kR * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sQh[kR * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sQl[kR * kRowChunks];
+  __shared__ In sVb64[kC], sdH64h[kC], sdH64l[kC];
+  __shared__ In sSin64h[kR], sSin64l[kR], sQ64h[kR], sQ64l[kR];
 
   const int c = blockIdx.x;
   const int64_t b = blockIdx.y;
@@ -97,7 +104,22 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
   const float* Qb = Qs + st_off;
 
   // ---- stage the chunk in LDS -------------------------------------------
-  // Phi and Psi rows (64 elements, 16-byte aligned rows: checked on the host)
+  // Phi and Psi rows: 64 elements, 16-byte aligned (checked on the host).
+  // Sin and Q (64 x 65 floats, contiguous) as float4s.  dH as float4s of the
+  // chunk's contiguous block when its rows are 65 floats apart (vec_dh); Vb
+  // as nine 16-byte pieces a row (columns 0..71: 64 to the swizzled rows,
+  // column 64 from the ninth) when its rows are 16-byte aligned and at least
+  // 72 elements apart (vec_vb); otherwise element-wise, consecutive threads
+  // on consecutive elements.  All loads are issued before the first LDS
+  // write.
+  constexpr int kVbN = kC * kP;                     // 8320
+  constexpr int kVbIt = (kVbN + kThreads - 1) / kThreads;   // 17
+  constexpr int kS4 = kR * kP / 4;                  // 1040 float4s of Sin / Q
+  constexpr int kS4It = (kS4 + kThreads - 1) / kThreads;    // 3
+  constexpr int kH4 = kVbN / 4;                     // 2080 float4s of dH
+  constexpr int kH4It = (kH4 + kThreads - 1) / kThreads;    // 5
+  constexpr int kV16 = kC * 9;                      // 1152 16-byte pieces of Vb
+  constexpr int kV16It = (kV16 + kThreads - 1) / kThreads;  // 3
   uint4 rphi[2], rpsi[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
@@ -106,29 +128,103 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
     rphi[u] = *reinterpret_cast<const uint4*>(phib + row * a.q_st + 8 * k);
     rpsi[u] = *reinterpret_cast<const uint4*>(psib + row * a.k_st + 8 * k);
   }
-  // Vb (65 elements a row, any stride), dH (65 floats a row), Sin and Q
-  // (64 x 65 floats, contiguous): element-wise, consecutive threads on
-  // consecutive elements
-  constexpr int kVbN = kC * kP;                     // 8320
-  constexpr int kVbIt = (kVbN + kThreads - 1) / kThreads;   // 17
-  constexpr int kSN = kR * kP;                      // 4160
-  constexpr int kSIt = (kSN + kThreads - 1) / kThreads;     // 9
-  In rvb[kVbIt];
-  float rdh[kVbIt], rsin[kSIt], rq[kSIt];
+  float4 rsin[kS4It], rq[kS4It];
 #pragma unroll
-  for (int u = 0; u < kVbIt; ++u) {
-    const int e = tid + kThreads * u;
-    const int ee = e < kVbN ? e : 0;
-    const int row = ee / kP, col = ee - row * kP;
-    rvb[u] = vbb[row * a.v_st + col];
-    rdh[u] = dHb[row * a.h_st + col];
+  for (int u = 0; u < kS4It; ++u) {
+    const int e4 = tid + kThreads * u;
+    const int ee = e4 < kS4 ? e4 : 0;
+    rsin[u] = reinterpret_cast<const float4*>(Sinb)[ee];
+    rq[u] = reinterpret_cast<const float4*>(Qb)[ee];
   }
+  // element e of a row-major block of rows of kP floats, split hi/lo, to its
+  // place in a pair of 16-bit tiles (and their column-64 arrays)
+  auto put = [](uint4* th, uint4* tl, In* h64, In* l64, int e, In h, In l) {
+    const int row = e / kP, col = e - row * kP;
+    if (col < 64) {
+      reinterpret_cast<In*>(th + cb_slot(row, col >> 3))[col & 7] = h;
+      reinterpret_cast<In*>(tl + cb_slot(row, col >> 3))[col & 7] = l;
+    } else {
+      h64[row] = h;
+      l64[row] = l;
+    }
+  };
+  auto put4 = [&](uint4* th, uint4* tl, In* h64, In* l64, int e, const float4& v) {
+    Half h, l;
+    split4<In>(f32x4{v.x, v.y, v.z, v.w}, h, l);
 #pragma unroll
-  for (int u = 0; u < kSIt; ++u) {
-    const int e = tid + kThreads * u;
-    const int ee = e < kSN ? e : 0;
-    rsin[u] = Sinb[ee];
-    rq[u] = Qb[ee];
+    for (int q = 0; q < 4; ++q) put(th, tl, h64, l64, e + q, h[q], l[q]);
+  };
+  if (a.vec_dh) {
+    float4 rdh[kH4It];
+#pragma unroll
+    for (int u = 0; u < kH4It; ++u) {
+      const int e4 = tid + kThreads * u;
+      rdh[u] = reinterpret_cast<const float4*>(dHb)[e4 < kH4 ? e4 : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < kH4It; ++u) {
+      const int e4 = tid + kThreads * u;
+      if (e4 < kH4) put4(sdHh, sdHl, sdH64h, sdH64l, 4 * e4, rdh[u]);
+    }
+  } else {
+    float rdh[kVbIt];
+#pragma unroll
+    for (int u = 0; u < kVbIt; ++u) {
+      const int e = tid + kThreads * u;
+      const int ee = e < kVbN ? e : 0;
+      const int row = ee / kP, col = ee - row * kP;
+      rdh[u] = dHb[row * a.h_st + col];
+    }
+#pragma unroll
+    for (int u = 0; u < kVbIt; ++u) {
+      const int e = tid + kThreads * u;
+      if (e < kVbN) {
+        In h, l;
+        split2<In>(rdh[u], h, l);
+        put(sdHh, sdHl, sdH64h, sdH64l, e, h, l);
+      }
+    }
+  }
+  if (a.vec_vb) {
+    uint4 rvb[kV16It];
+#pragma unroll
+    for (int u = 0; u < kV16It; ++u) {
+      const int q = tid + kThreads * u;
+      const int qq = q < kV16 ? q : 0;
+      const int row = qq / 9, k = qq - 9 * row;
+      rvb[u] = *reinterpret_cast<const uint4*>(vbb + row * a.v_st + 8 * k);
+    }
+#pragma unroll
+    for (int u = 0; u < kV16It; ++u) {
+      const int q = tid + kThreads * u;
+      if (q < kV16) {
+        const int row = q / 9, k = q - 9 * row;
+        if (k < 8)
+          sVb[cb_slot(row, k)] = rvb[u];
+        else
+          sVb64[row] = __builtin_bit_cast(Frag, rvb[u])[0];
+      }
+    }
+  } else {
+    In rvb[kVbIt];
+#pragma unroll
+    for (int u = 0; u < kVbIt; ++u) {
+      const int e = tid + kThreads * u;
+      const int ee = e < kVbN ? e : 0;
+      const int row = ee / kP, col = ee - row * kP;
+      rvb[u] = vbb[row * a.v_st + col];
+    }
+#pragma unroll
+    for (int u = 0; u < kVbIt; ++u) {
+      const int e = tid + kThreads * u;
+      if (e < kVbN) {
+        const int row = e / kP, col = e - row * kP;
+        if (col < 64)
+          reinterpret_cast<In*>(sVb + cb_slot(row, col >> 3))[col & 7] = rvb[u];
+        else
+          sVb64[row] = rvb[u];
+      }
+    }
   }
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
@@ -138,24 +234,11 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
     sPsi[cb_slot(row, k)] = rpsi[u];
   }
 #pragma unroll
-  for (int u = 0; u < kVbIt; ++u) {
-    const int e = tid + kThreads * u;
-    if (e < kVbN) {
-      const int row = e / kP, col = e - row * kP;
-      if (col < 64)
-        reinterpret_cast<In*>(sVb + cb_slot(row, col >> 3))[col & 7] = rvb[u];
-      else
-        sVb64[row] = rvb[u];
-      sdH[row * kS + col] = rdh[u];
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kSIt; ++u) {
-    const int e = tid + kThreads * u;
-    if (e < kSN) {
-      const int row = e / kP, col = e - row * kP;
-      sSin[row * kS + col] = rsin[u];
-      sQ[row * kS + col] = rq[u];
+  for (int u = 0; u < kS4It; ++u) {
+    const int e4 = tid + kThreads * u;
+    if (e4 < kS4) {
+      put4(sSinh, sSinl, sSin64h, sSin64l, 4 * e4, rsin[u]);
+      put4(sQh, sQl, sQ64h, sQ64l, 4 * e4, rq[u]);
     }
   }
   __syncthreads();
@@ -164,6 +247,30 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
   const int lane = lane_id();
   const int r16 = lane & 15, g = lane >> 4;
   const Half hzero = {};
+  // the K = 16 tail over value columns 64..79: column 64 in k-slot 0 of lane
+  // group 0
+  auto tail16 = [&](const In* h64, const In* l64, int row, Half& hi, Half& lo) {
+    hi = hzero;
+    lo = hzero;
+    if (g == 0) {
+      hi[0] = h64[row];
+      lo[0] = l64[row];
+    }
+  };
+  // A operand down 8 consecutive rows row0 + 8g .. +7 of a 16-bit tile: lane
+  // (m = 16 ct + lane % 16, g), k-slot e <- column m of row row0 + 8g + e
+  auto col8 = [&](const uint4* tile, int row0, int ct) {
+    const int k = 2 * ct + ((r16 & 3) >> 1), half = r16 & 1;
+    const Half lo4 = cb_tr<In>(tile, row0 + 8 * g + (r16 >> 2), k, half);
+    const Half hi4 = cb_tr<In>(tile, row0 + 8 * g + 4 + (r16 >> 2), k, half);
+    Frag f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = lo4[e];
+      f[4 + e] = hi4[e];
+    }
+    return f;
+  };
 
   // ---- row pass: dPhi rows of tile i = w ----------------------------------
   {
@@ -172,8 +279,11 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
     Frag dh_hi[2], dh_lo[2];
     Half dht_hi, dht_lo;
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) cb_row32<In>(sdH, trow, kc, g, dh_hi[kc], dh_lo[kc]);
-    cb_tail32<In>(sdH, trow, g, dht_hi, dht_lo);
+    for (int kc = 0; kc < 2; ++kc) {
+      dh_hi[kc] = cb_row<In>(sdHh, i, kc, lane);
+      dh_lo[kc] = cb_row<In>(sdHl, i, kc, lane);
+    }
+    tail16(sdH64h, sdH64l, trow, dht_hi, dht_lo);
 
     f32x4 acc[4];
     // dPhi^T += Sin dH^T: A = Sin rows a (k = value column), B = dH^T
@@ -183,14 +293,14 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
       const int arow = 16 * at + r16;
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
-        Frag hi, lo;
-        cb_row32<In>(sSin, arow, kc, g, hi, lo);
+        const Frag hi = cb_row<In>(sSinh, at, kc, lane);
+        const Frag lo = cb_row<In>(sSinl, at, kc, lane);
         s = mma(s, hi, dh_hi[kc]);
         s = mma(s, hi, dh_lo[kc]);
         s = mma(s, lo, dh_hi[kc]);
       }
       Half thi, tlo;
-      cb_tail32<In>(sSin, arow, g, thi, tlo);
+      tail16(sSin64h, sSin64l, arow, thi, tlo);
       s = mma_k16(s, thi, dht_hi);
       s = mma_k16(s, thi, dht_lo);
       s = mma_k16(s, tlo, dht_hi);
@@ -272,13 +382,11 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
       const int arow = 16 * at + r16;
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
-        Frag hi, lo;
-        cb_row32<In>(sQ, arow, kc, g, hi, lo);
-        s = mma(s, hi, vf[kc]);
-        s = mma(s, lo, vf[kc]);
+        s = mma(s, cb_row<In>(sQh, at, kc, lane), vf[kc]);
+        s = mma(s, cb_row<In>(sQl, at, kc, lane), vf[kc]);
       }
       Half thi, tlo;
-      cb_tail32<In>(sQ, arow, g, thi, tlo);
+      tail16(sQ64h, sQ64l, arow, thi, tlo);
       s = mma_k16(s, thi, vt);
       s = mma_k16(s, tlo, vt);
       accq[at] = s;
@@ -287,19 +395,20 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
 #pragma unroll
     for (int ct = 0; ct < 5; ++ct) {
       f32x4 s = zero4();
-      const int col = 16 * ct + r16;
-      const bool okc = col < kP;
-      const int cc = okc ? col : 0;                  // columns past p read column 0, then zero
+      const bool okc = 16 * ct + r16 < kP;
 #pragma unroll
       for (int ka = 0; ka < 2; ++ka) {
+        // A = Q^T: lane (c, g), k-slot e <- Q[32 ka + 8g + e][c]
         Frag hi, lo;
+        if (ct < 4) {
+          hi = col8(sQh, 32 * ka, ct);
+          lo = col8(sQl, 32 * ka, ct);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float v = okc ? sQ[(32 * ka + 8 * g + e) * kS + cc] : 0.f;
-          In h, l;
-          split2<In>(v, h, l);
-          hi[e] = h;
-          lo[e] = l;
+          for (int e = 0; e < 8; ++e) {
+            hi[e] = okc ? sQ64h[32 * ka + 8 * g + e] : from_f32<In>(0.f);
+            lo[e] = okc ? sQ64l[32 * ka + 8 * g + e] : from_f32<In>(0.f);
+          }
         }
         s = mma(s, hi, pf[ka]);
         s = mma(s, lo, pf[ka]);
@@ -321,15 +430,13 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
           // dA[t][s] = sum_c dH[t][c] Vb[s][c]: A = dH rows t, B = Vb^T
 #pragma unroll
           for (int kc = 0; kc < 2; ++kc) {
-            Frag hi, lo;
-            cb_row32<In>(sdH, trow, kc, g, hi, lo);
-            d = mma(d, hi, vf[kc]);
-            d = mma(d, lo, vf[kc]);
+            d = mma(d, cb_row<In>(sdHh, tt, kc, lane), vf[kc]);
+            d = mma(d, cb_row<In>(sdHl, tt, kc, lane), vf[kc]);
             // A[t][s] = sum_a Phi[t][a] Psi[s][a]
             s = mma(s, cb_row<In>(sPhi, tt, kc, lane), pf[kc]);
           }
           Half thi, tlo;
-          cb_tail32<In>(sdH, trow, g, thi, tlo);
+          tail16(sdH64h, sdH64l, trow, thi, tlo);
           d = mma_k16(d, thi, vt);
           d = mma_k16(d, tlo, vt);
           if (tt == j) {
@@ -358,19 +465,26 @@ __global__ __launch_bounds__(cb::kThreads, 1) void chunk_bwd_kernel(
       // dVb^T += dH^T A: A operand = dH^T (rows = value column c, k = token t)
 #pragma unroll
       for (int ct = 0; ct < 5; ++ct) {
-        const int col = 16 * ct + r16;
-        const bool okc = col < kP;
-        const int cc = okc ? col : 0;
+        // A = dH^T: lane (c, g), k-slot 4h + e <- dH[16 tile[h] + 4g + e][c]
         Frag hi, lo;
+        if (ct < 4) {
+          hi = cb_tr_pair<In>(sdHh, tt0, tt1, ct, lane);
+          lo = cb_tr_pair<In>(sdHl, tt0, tt1, ct, lane);
+        } else {
+          const bool okc = r16 == 0;                 // column 64
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int tt = e < 4 ? tt0 : tt1;
-          const bool ok = okc && (e < 4 || has1);
-          const float v = ok ? sdH[(16 * tt + 4 * g + (e & 3)) * kS + cc] : 0.f;
-          In h, l;
-          split2<In>(v, h, l);
-          hi[e] = h;
-          lo[e] = l;
+          for (int e = 0; e < 8; ++e) {
+            const int trr = 16 * (e < 4 ? tt0 : tt1) + 4 * g + (e & 3);
+            hi[e] = okc ? sdH64h[trr] : from_f32<In>(0.f);
+            lo[e] = okc ? sdH64l[trr] : from_f32<In>(0.f);
+          }
+        }
+        if (!has1) {
+#pragma unroll
+          for (int e = 4; e < 8; ++e) {
+            hi[e] = from_f32<In>(0.f);
+            lo[e] = from_f32<In>(0.f);
+          }
         }
         accv[ct] = mma(accv[ct], hi, aah);
         accv[ct] = mma(accv[ct], hi, aal);
@@ -467,9 +581,15 @@ extern "C" int smat_chunk_backward(int dtype, int out_dtype, const void* phi, co
                "smat_chunk_backward: added terms need 0 <= add_split <= add_end <= nc*C, "
                "16-byte aligned rows for Phi and Psi and full rows");
   if (nb == 0 || nc == 0) return SMAT_OK;
-  ChunkBwdArgs a{nc,      q_sb,    q_st,    k_sb,  k_st,  v_sb,  v_st,      h_sb,   h_st,
-                 d_sb,    d_st,    e_sb,    e_st,  add_phi, add_psi, add_vb, ap_sb, ap_st,
-                 ak_sb,   ak_st,   av_sb,   av_st, add_split, add_end};
+  SMAT_REQUIRE(aligned16(Sin) && aligned16(Q), SMAT_EINVAL,
+               "smat_chunk_backward: Sin and Q must be 16-byte aligned");
+  // dH: the chunk's 128 rows of 65 floats are one 16-byte aligned block
+  const int vec_dh = h_st == p && h_sb % 4 == 0 && aligned16(dH);
+  // Vb: nine 16-byte pieces a row stay inside the row's stride
+  const int vec_vb = v_st >= 72 && v_st % 8 == 0 && v_sb % 8 == 0 && aligned16(vb);
+  ChunkBwdArgs a{nc,    vec_dh, vec_vb, q_sb,  q_st,    k_sb,    k_st,   v_sb,  v_st,
+                 h_sb,  h_st,   d_sb,   d_st,  e_sb,    e_st,    add_phi, add_psi, add_vb,
+                 ap_sb, ap_st,  ak_sb,  ak_st, av_sb,   av_st,   add_split, add_end};
   const dim3 grid((unsigned)nc, (unsigned)nb);
   hipStream_t st = (hipStream_t)stream;
   const bool f32 = out_dtype == SMAT_F32;

@@ -106,9 +106,17 @@ __global__ __launch_bounds__(256) void segment_scan_rev_kernel(const float* __re
   }
 }
 
-// Backward of out = N[:, :p-1] / den * g, one wave per row, where
-// N = H + [0; Y] (the Y rows added from row n on; Y may be null) and den is
-// N[:, p-1], floored at eps when kFloor (the layer's clamp_min):
+// Rows of the normalisation: sixteen lanes a row, four rows a wave, sixteen
+// a workgroup; lane l of a row's group takes columns l, l + 16, ... (each
+// load coalesced over the group).
+namespace nrm {
+constexpr int kLanes = 16;
+constexpr int kRows = 256 / kLanes;
+}  // namespace nrm
+
+// Backward of out = N[:, :p-1] / den * g, where N = H + [0; Y] (the Y rows
+// added from row n on; Y may be null) and den is N[:, p-1], floored at eps
+// when kFloor (the layer's clamp_min):
 //   dN_c = dout_c g / den (c < p-1),
 //   dN_{p-1} = -sum_c dN_c N_c / den (0 where the floor is active),
 //   dg = sum_c dout_c N_c / den.
@@ -119,10 +127,10 @@ __global__ __launch_bounds__(256) void normalise_bwd_kernel(
     const float* __restrict__ g, float* __restrict__ dH, float* __restrict__ dg, int T, int n,
     int p, float eps, int64_t o_sb, int64_t o_st, int64_t h_sb, int64_t h_st, int64_t y_sb,
     int64_t y_st, int64_t d_sb, int64_t d_st, int64_t g_sb) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  const int64_t row = (int64_t)blockIdx.x * nrm::kRows + (threadIdx.x >> 4);
   const int64_t b = blockIdx.y;
-  const int lane = lane_id();
-  if (row >= T) return;
+  const int l = threadIdx.x & (nrm::kLanes - 1);
+  if (row >= T) return;                              // whole 16-lane groups
   const float* h = H + b * h_sb + row * h_st;
   const float* y = (Y != nullptr && row >= n) ? Y + b * y_sb + (row - n) * y_st : nullptr;
   const Din* d = dout + b * o_sb + row * o_st;
@@ -132,7 +140,8 @@ __global__ __launch_bounds__(256) void normalise_bwd_kernel(
   const float inv = 1.f / den;
   const float gate = g ? g[b * g_sb + row] : 1.f;
   float sh = 0.f, sg = 0.f;
-  for (int c = lane; c < p - 1; c += 64) {
+#pragma unroll 4
+  for (int c = l; c < p - 1; c += nrm::kLanes) {
     const float o = (y ? h[c] + y[c] : h[c]) * inv;
     const float dv = to_f32(d[c]);
     const float dc = dv * gate * inv;
@@ -140,11 +149,12 @@ __global__ __launch_bounds__(256) void normalise_bwd_kernel(
     sh += dc * o;
     sg += dv * o;
   }
-  for (int off = 32; off > 0; off >>= 1) {
-    sh += __shfl_down(sh, off, 64);
-    sg += __shfl_down(sg, off, 64);
+#pragma unroll
+  for (int off = nrm::kLanes / 2; off > 0; off >>= 1) {
+    sh += __shfl_xor(sh, off, nrm::kLanes);
+    sg += __shfl_xor(sg, off, nrm::kLanes);
   }
-  if (lane == 0) {
+  if (l == 0) {
     dh[p - 1] = (kFloor && !(den_raw >= eps)) ? 0.f : -sh;
     if (dg) dg[b * T + row] = sg;
   }
@@ -159,16 +169,17 @@ int segment_scan_dispatch(const float* D, float* Sin, int nb, int nc, int nc0, i
   return launch_status("smat_segment_scan");
 }
 
-// One wave per output row: the normaliser is read once, every column divided;
-// with kFloor (eps >= 0 at dispatch) the normaliser is floored at eps first.
+// Sixteen lanes per output row: the normaliser is read once, every column
+// divided; with kFloor (eps >= 0 at dispatch) the normaliser is floored at
+// eps first.
 template <bool kFloor, typename Out>
 __global__ __launch_bounds__(256) void normalise_kernel(
     const float* __restrict__ H, const float* __restrict__ Y, const float* __restrict__ g,
     Out* __restrict__ out, int T, int n, int p, float eps, int64_t h_sb, int64_t h_st,
     int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st, int64_t g_sb) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  const int64_t row = (int64_t)blockIdx.x * nrm::kRows + (threadIdx.x >> 4);
   const int64_t b = blockIdx.y;
-  const int lane = lane_id();
+  const int lane = threadIdx.x & (nrm::kLanes - 1);
   if (row >= T) return;
   const float* h = H + b * h_sb + row * h_st;
   const float* y = (Y != nullptr && row >= n) ? Y + b * y_sb + (row - n) * y_st : nullptr;
@@ -177,7 +188,8 @@ __global__ __launch_bounds__(256) void normalise_kernel(
   if (kFloor) den = fmaxf(den, eps);
   const float gate = g ? g[b * g_sb + row] : 1.f;
   Out* o = out + b * o_sb + row * o_st;
-  for (int c = lane; c < p - 1; c += 64) {
+#pragma unroll 4
+  for (int c = lane; c < p - 1; c += nrm::kLanes) {
     float num = h[c];
     if (y) num += y[c];
     float v = num / den;
@@ -192,7 +204,7 @@ static int launch_normalise(const float* H, const float* Y, const float* g, Out*
                             int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream,
                             float eps) {
   if (nb == 0 || T == 0) return SMAT_OK;
-  dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
+  dim3 grid((unsigned)((T + nrm::kRows - 1) / nrm::kRows), (unsigned)nb);
   if (eps >= 0.f)
     smat::launch((normalise_kernel<true, Out>), grid, dim3(256), 0, stream, H, Y, g, out, T,
                        n, p, eps, h_sb, h_st, y_sb, y_st, o_sb, o_st, g_sb);
@@ -217,7 +229,7 @@ static int launch_normalise_bwd(const Din* dout, const float* H, const float* Y,
                                 int64_t y_sb, int64_t y_st, int64_t d_sb, int64_t d_st,
                                 int64_t g_sb, hipStream_t stream) {
   if (nb == 0 || T == 0) return SMAT_OK;
-  dim3 grid((unsigned)((T + 3) / 4), (unsigned)nb);
+  dim3 grid((unsigned)((T + nrm::kRows - 1) / nrm::kRows), (unsigned)nb);
   if (eps >= 0.f)
     smat::launch((normalise_bwd_kernel<true, Din>), grid, dim3(256), 0, stream, dout, H, Y,
                        g, dH, dg, T, n, p, eps, o_sb, o_st, h_sb, h_st, y_sb, y_st, d_sb, d_st,
