@@ -332,6 +332,20 @@ int smat_chunk_backward(int dtype, int out_dtype, const void* phi, const void* p
                         int64_t add_end, void* stream);
 
 /*
+ * The per-chunk state gradient of the causal scan, Dr_c = Phi_c^T dH_c for
+ * every (sequence, chunk): fp32 (nb x nc x r x p, contiguous, 16-byte
+ * aligned), the input of the reverse scan (smat_segment_scan_reverse) that
+ * gives smat_chunk_backward its Q.  16-bit Phi (rows 16-byte aligned), fp32
+ * dH (nb x nc*C rows, row stride h_st >= p); products on 16-bit MFMA with dH
+ * split hi/lo.  Serves r = 64, p = 65, C = 128 (SMAT_EUNSUPPORTED
+ * otherwise).  Part of the gradient of src/smat/attention.py:134-192 (the
+ * reference takes it from torch autograd).
+ */
+int smat_chunk_dstates(int dtype, const void* phi, const float* dH, float* Dr, int nb, int nc,
+                       int r, int p, int C, int64_t q_sb, int64_t q_st, int64_t h_sb,
+                       int64_t h_st, void* stream);
+
+/*
  * Backward of the long-range branch (attention.py:196-330) at r = 64, p = 65
  * for 16-bit inputs (dtype SMAT_BF16 or SMAT_F16; SMAT_EUNSUPPORTED
  * otherwise); dY is dH on the recent rows, fp32.

@@ -544,6 +544,142 @@ static void chunk_bwd_launch(const void* phi, const void* psi, const void* vb, c
                      (Out*)dPsi, (Out*)dVb, a);
 }
 
+// ---------------------------------------------------------------------------
+// The per-chunk state gradient Dr_c = Phi_c^T dH_c (r x p fp32, one matrix per
+// (sequence, chunk); the input of the reverse scan that gives Q), one
+// workgroup of four waves per item.  Phi's chunk is staged as 16-bit rows
+// (swizzled), dH's split into 16-bit hi/lo tiles as in chunk_bwd_kernel.
+// Wave w forms rows 16w .. 16w+15 of Dr (features) across five value-column
+// tiles: A = Phi^T and B = dH, both read down the chunk's tokens with the
+// transposing reads, 32 tokens a product; lane (c, g) ends with
+// Dr[16w + 4g + e][c].
+// ---------------------------------------------------------------------------
+namespace cds {
+constexpr int kThreads = 256;
+}  // namespace cds
+
+template <typename In>
+__global__ __launch_bounds__(cds::kThreads) void chunk_dstate_kernel(
+    const In* __restrict__ phi, const float* __restrict__ dH, float* __restrict__ Dr, int nc,
+    int vec_dh, int64_t q_sb, int64_t q_st, int64_t h_sb, int64_t h_st) {
+  using namespace cb;
+  typedef typename Traits<In>::frag Frag;
+  typedef typename Traits<In>::half_frag Half;
+  __shared__ __attribute__((aligned(16))) uint4 sPhi[kC * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sdHh[kC * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sdHl[kC * kRowChunks];
+  __shared__ In sdH64h[kC], sdH64l[kC];
+
+  const int c = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int64_t t0 = (int64_t)c * kC;
+  const In* phib = phi + b * q_sb + t0 * q_st;
+  const float* dHb = dH + b * h_sb + t0 * h_st;
+  constexpr int kN = kC * kP;                       // 8320 dH values
+  constexpr int kPhiIt = kC * kRowChunks / cds::kThreads;   // 4
+  constexpr int kH4 = kN / 4;                       // 2080 float4s
+  constexpr int kH4It = (kH4 + cds::kThreads - 1) / cds::kThreads;   // 9
+  constexpr int kHIt = (kN + cds::kThreads - 1) / cds::kThreads;     // 33
+
+  auto put = [&](int e, In h, In l) {
+    const int row = e / kP, col = e - row * kP;
+    if (col < 64) {
+      reinterpret_cast<In*>(sdHh + cb_slot(row, col >> 3))[col & 7] = h;
+      reinterpret_cast<In*>(sdHl + cb_slot(row, col >> 3))[col & 7] = l;
+    } else {
+      sdH64h[row] = h;
+      sdH64l[row] = l;
+    }
+  };
+  // Phi's rows straight to LDS (issued after dH's loads, which stay in flight)
+  auto put_phi = [&]() {
+#pragma unroll
+    for (int u = 0; u < kPhiIt; ++u) {
+      const int e = tid + cds::kThreads * u;
+      sPhi[cb_slot(e >> 3, e & 7)] =
+          *reinterpret_cast<const uint4*>(phib + (e >> 3) * q_st + 8 * (e & 7));
+    }
+  };
+  if (vec_dh) {
+    float4 rdh[kH4It];
+#pragma unroll
+    for (int u = 0; u < kH4It; ++u) {
+      const int e4 = tid + cds::kThreads * u;
+      rdh[u] = reinterpret_cast<const float4*>(dHb)[e4 < kH4 ? e4 : 0];
+    }
+    put_phi();
+#pragma unroll
+    for (int u = 0; u < kH4It; ++u) {
+      const int e4 = tid + cds::kThreads * u;
+      if (e4 < kH4) {
+        Half h, l;
+        split4<In>(f32x4{rdh[u].x, rdh[u].y, rdh[u].z, rdh[u].w}, h, l);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) put(4 * e4 + q, h[q], l[q]);
+      }
+    }
+  } else {
+    put_phi();
+    for (int u = 0; u < kHIt; ++u) {
+      const int e = tid + cds::kThreads * u;
+      if (e < kN) {
+        const int row = e / kP, col = e - row * kP;
+        In h, l;
+        split2<In>(dHb[row * h_st + col], h, l);
+        put(e, h, l);
+      }
+    }
+  }
+  __syncthreads();
+
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int lane = lane_id(), r16 = lane & 15, g = lane >> 4;
+  // lane (m = 16 ct + lane % 16, g), k-slot e <- column m of row row0 + 8g + e
+  auto col8 = [&](const uint4* tile, int row0, int ct) {
+    const int k = 2 * ct + ((r16 & 3) >> 1), half = r16 & 1;
+    const Half lo4 = cb_tr<In>(tile, row0 + 8 * g + (r16 >> 2), k, half);
+    const Half hi4 = cb_tr<In>(tile, row0 + 8 * g + 4 + (r16 >> 2), k, half);
+    Frag f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = lo4[e];
+      f[4 + e] = hi4[e];
+    }
+    return f;
+  };
+  f32x4 acc[5];
+#pragma unroll
+  for (int ct = 0; ct < 5; ++ct) acc[ct] = zero4();
+#pragma unroll
+  for (int ks = 0; ks < kC / 32; ++ks) {
+    const Frag pa = col8(sPhi, 32 * ks, w);          // Phi^T rows 16w + r16
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      acc[ct] = mma(acc[ct], pa, col8(sdHh, 32 * ks, ct));
+      acc[ct] = mma(acc[ct], pa, col8(sdHl, 32 * ks, ct));
+    }
+    Frag bh, bl;                                     // column 64: lane r16 = 0
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int t = 32 * ks + 8 * g + e;
+      bh[e] = r16 == 0 ? sdH64h[t] : from_f32<In>(0.f);
+      bl[e] = r16 == 0 ? sdH64l[t] : from_f32<In>(0.f);
+    }
+    acc[4] = mma(acc[4], pa, bh);
+    acc[4] = mma(acc[4], pa, bl);
+  }
+  float* out = Dr + ((int64_t)b * nc + c) * (kR * kP);
+#pragma unroll
+  for (int ct = 0; ct < 5; ++ct) {
+    const int col = 16 * ct + r16;
+    if (col < kP) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[(16 * w + 4 * g + e) * kP + col] = acc[ct][e];
+    }
+  }
+}
+
 }  // namespace smat
 
 extern "C" int smat_chunk_backward(int dtype, int out_dtype, const void* phi, const void* psi,
@@ -600,4 +736,32 @@ extern "C" int smat_chunk_backward(int dtype, int out_dtype, const void* phi, co
     (f32 ? chunk_bwd_launch<f16, float> : chunk_bwd_launch<f16, f16>)(
         phi, psi, vb, dH, Sin, Q, dPhi, dPsi, dVb, a, grid, st);
   return launch_status("smat_chunk_backward");
+}
+
+extern "C" int smat_chunk_dstates(int dtype, const void* phi, const float* dH, float* Dr, int nb,
+                                  int nc, int r, int p, int C, int64_t q_sb, int64_t q_st,
+                                  int64_t h_sb, int64_t h_st, void* stream) {
+  using namespace smat;
+  clear_error();
+  SMAT_REQUIRE(phi && dH && Dr, SMAT_EINVAL, "smat_chunk_dstates: null pointer");
+  SMAT_REQUIRE(nb >= 0 && nc >= 0, SMAT_EINVAL, "smat_chunk_dstates: bad sizes");
+  SMAT_REQUIRE(nc < 65536 * 32 && nb < 65536, SMAT_EUNSUPPORTED,
+               "smat_chunk_dstates: grid %d x %d too large", nc, nb);
+  SMAT_REQUIRE((dtype == SMAT_BF16 || dtype == SMAT_F16) && r == cb::kR && p == cb::kP &&
+                   C == cb::kC && rows_vec_ok(phi, q_sb, q_st, 2) && h_st >= p && aligned16(Dr),
+               SMAT_EUNSUPPORTED,
+               "smat_chunk_dstates: needs 16-bit Phi with 16-byte aligned rows, r=64, p=65, "
+               "C=128 (got dtype=%d r=%d p=%d C=%d)",
+               dtype, r, p, C);
+  if (nb == 0 || nc == 0) return SMAT_OK;
+  const int vec_dh = h_st == p && h_sb % 4 == 0 && aligned16(dH);
+  const dim3 grid((unsigned)nc, (unsigned)nb);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == SMAT_BF16)
+    hipLaunchKernelGGL(chunk_dstate_kernel<bf16>, grid, dim3(cds::kThreads), 0, st,
+                       (const bf16*)phi, dH, Dr, nc, vec_dh, q_sb, q_st, h_sb, h_st);
+  else
+    hipLaunchKernelGGL(chunk_dstate_kernel<f16>, grid, dim3(cds::kThreads), 0, st,
+                       (const f16*)phi, dH, Dr, nc, vec_dh, q_sb, q_st, h_sb, h_st);
+  return launch_status("smat_chunk_dstates");
 }

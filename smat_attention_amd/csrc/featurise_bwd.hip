@@ -7,8 +7,8 @@
 // with m(y) = elu(y) + 1, m'(y) = 1 (y > 0) or e^y (kind 0), or m(y) =
 // relu(y) + 1e-3, m'(y) = [y > 0] (kind 1); G is the upstream gradient of the
 // map's output (dPhi, or dPsi before the gate).  Persistent workgroups of four
-// waves stage W once and walk 64-token tiles of one sequence: x, G (and h)
-// through LDS.  Wave w:
+// waves stage W once and walk 64-token tiles: x, G (and h) through LDS, the
+// next tile's rows in flight while the current tile is multiplied.  Wave w:
 //
 //   * forms y^T for its 16 tokens (A = W rows, B = x rows; lane (t, g) holds
 //     features 4g + i of each feature tile), applies m' and the gate, and
@@ -65,26 +65,44 @@ __global__ __launch_bounds__(fb::kThreads) void featurise_bwd_kernel(
     return kind == 0 ? (y > 0.f ? y : expm1f(y)) + 1.f : fmaxf(y, 0.f) + 1e-3f;
   };
 
+  // x and G rows of a tile (16-byte chunks; rows past T are zero) and the
+  // gate: the next tile's are loaded into registers while the current one
+  // is multiplied, and written to LDS at the top of the next iteration
+  constexpr int kChunks = fb::kTile * kRowChunks / fb::kThreads;    // 2 a thread
+  uint4 px[kChunks], pg[kChunks];
+  float ph = 1.f;
+  auto issue = [&](int64_t tile) {
+    const int64_t b = tile / tiles_per_seq;
+    const int t0 = (int)(tile - b * tiles_per_seq) * fb::kTile;
+#pragma unroll
+    for (int u = 0; u < kChunks; ++u) {
+      const int i = tid + fb::kThreads * u;
+      const int row = i >> 3, k = i & 7;
+      const bool ok = t0 + row < T;
+      const int64_t t = ok ? t0 + row : t0;
+      px[u] = *reinterpret_cast<const uint4*>(x + b * x_sb + t * x_st + 8 * k);
+      pg[u] = *reinterpret_cast<const uint4*>(G + b * g_sb + t * g_st + 8 * k);
+      if (!ok) px[u] = pg[u] = make_uint4(0, 0, 0, 0);
+    }
+    if (tid < fb::kTile) {
+      const bool ok = t0 + tid < T;
+      ph = h && ok ? to_f32(h[b * h_sb + t0 + tid]) : 1.f;
+    }
+  };
+  if ((int64_t)blockIdx.x < ntiles) issue(blockIdx.x);
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int64_t b = tile / tiles_per_seq;
     const int t0 = (int)(tile - b * tiles_per_seq) * fb::kTile;
     __syncthreads();                                 // W staged / the last tile's readers done
-    // stage x and G rows (16-byte chunks; rows past T are zero) and the gate
-    for (int i = tid; i < fb::kTile * kRowChunks; i += fb::kThreads) {
-      const int row = i >> 3, k = i & 7;
-      const bool ok = t0 + row < T;
-      const int64_t t = ok ? t0 + row : t0;
-      uint4 xv = *reinterpret_cast<const uint4*>(x + b * x_sb + t * x_st + 8 * k);
-      uint4 gv = *reinterpret_cast<const uint4*>(G + b * g_sb + t * g_st + 8 * k);
-      if (!ok) xv = gv = make_uint4(0, 0, 0, 0);
-      sX[cb_slot(row, k)] = xv;
-      sG[cb_slot(row, k)] = gv;
+#pragma unroll
+    for (int u = 0; u < kChunks; ++u) {
+      const int i = tid + fb::kThreads * u;
+      sX[cb_slot(i >> 3, i & 7)] = px[u];
+      sG[cb_slot(i >> 3, i & 7)] = pg[u];
     }
-    if (tid < fb::kTile) {
-      const bool ok = t0 + tid < T;
-      sH[tid] = h && ok ? to_f32(h[b * h_sb + t0 + tid]) : 1.f;
-    }
+    if (tid < fb::kTile) sH[tid] = ph;
     __syncthreads();
+    if (tile + gridDim.x < ntiles) issue(tile + gridDim.x);
 
     // ---- dx and dh for tokens 16w .. 16w+15 of the tile -------------------
     {
@@ -214,7 +232,15 @@ extern "C" int64_t smat_featurise_backward_parts(int nb, int T) {
   using namespace smat;
   if (nb <= 0 || T <= 0) return 0;
   const int64_t ntiles = (int64_t)nb * ((T + fb::kTile - 1) / fb::kTile);
-  return ntiles < 1024 ? ntiles : 1024;
+  // as many workgroups as the device holds at once (each walks its tiles)
+  int dev = 0, ncu = 256, per_cu = 0;
+  (void)hipGetDevice(&dev);
+  (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, featurise_bwd_kernel<bf16>,
+                                                   fb::kThreads, 0) != hipSuccess || per_cu < 1)
+    per_cu = 2;
+  const int64_t cap = (int64_t)ncu * per_cu;
+  return ntiles < cap ? ntiles : cap;
 }
 
 extern "C" int smat_featurise_backward(int dtype, const void* x, const void* G, const void* W,

@@ -73,6 +73,8 @@ SIGNATURES = {
                                  _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _i64, _p]),
+    "smat_chunk_dstates": (_i, [_i, _p, _p, _p, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64,
+                                _p]),
     "smat_lr_dphi": (_i, [_i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i64, _i64, _i64,
                           _i64, _i, _p]),
     "smat_lr_dfeat": (_i, [_i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _i64, _i64,

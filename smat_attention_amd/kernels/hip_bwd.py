@@ -198,8 +198,12 @@ def causal_scan_grad(Ph, Ps, Vv, dH, n: int, C: int, out_dtype=None, add=None):
     # Dr_b = Phi_b^T dH_b (rows of Phi and dH at their own strides)
     qb, qt = Ph.stride(0), Ph.stride(1)
     hb, ht = dH.stride(0), dH.stride(1)
-    _bgemm(Ph, dH, Dr, M=r, N=p, K=C, n1=nb, n2=nc,
-           a=(qb, C * qt, 1, qt), b=(hb, C * ht, ht, 1), c=(nc * rp, rp, p, 1))
+    if fused:
+        call("smat_chunk_dstates", _code(Ph), Ph.data_ptr(), dH.data_ptr(), Dr.data_ptr(), nb,
+             nc, r, p, C, qb, qt, hb, ht, stream_of(Dr))
+    else:
+        _bgemm(Ph, dH, Dr, M=r, N=p, K=C, n1=nb, n2=nc,
+               a=(qb, C * qt, 1, qt), b=(hb, C * ht, ht, 1), c=(nc * rp, rp, p, 1))
     Q = torch.empty_like(Dr)
     call("smat_segment_scan_reverse", Dr.data_ptr(), Q.data_ptr(), nb, nc, n // C, rp,
          stream_of(Q))

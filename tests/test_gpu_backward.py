@@ -400,6 +400,28 @@ def test_fused_chunk_backward(T, n):
         assert a.dtype == bf and torch.equal(a, b.to(bf)), name
 
 
+@pytest.mark.parametrize("vb_pad", [False, True])
+def test_chunk_state_gradients(vb_pad):
+    """smat_chunk_dstates: Dr_c = Phi_c^T dH_c for every (sequence, chunk), bf16
+    Phi and fp32 dH (contiguous rows of 65 floats, or rows 72 apart), against
+    fp64 products of the same values: within 2e-5 of each matrix's largest
+    entry (dH enters split hi/lo, about 2^-17 relative)."""
+    from smat_attention_amd.kernels.hip_fwd import call, stream_of
+    nb, nc, r, p, C = 3, 5, 64, 65, 128
+    gen = torch.Generator().manual_seed(93)
+    Ph = (torch.rand(nb, nc * C, r, generator=gen) + 0.1).to(torch.bfloat16)
+    dH = torch.randn(nb, nc * C, 72 if vb_pad else p, generator=gen)[..., :p]
+    Phd, dHd = Ph.to(DEV), dH.to(DEV)
+    Dr = torch.empty(nb, nc, r, p, device=DEV)
+    call("smat_chunk_dstates", 0, Phd.data_ptr(), dHd.data_ptr(), Dr.data_ptr(), nb, nc, r, p, C,
+         Phd.stride(0), Phd.stride(1), dHd.stride(0), dHd.stride(1), stream_of(Dr))
+    ref = torch.einsum("bcta,bctv->bcav", Ph.double().reshape(nb, nc, C, r),
+                       dH.double().reshape(nb, nc, C, p))
+    err = ((Dr.cpu().double() - ref).abs().amax((-1, -2)) / ref.abs().amax((-1, -2))).max()
+    _say("chunk state gradients", vb_pad, f"{float(err):.2e}")
+    assert float(err) < 2e-5
+
+
 @pytest.mark.parametrize("T,d,n_P,gate", [(4096, 3, 0, False), (4096, 2, 0, False),
                                           (2048, 3, 16, True), (3000, 3, 0, False)])
 def test_fused_attention_backward(T, d, n_P, gate):
