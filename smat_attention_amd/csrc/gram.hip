@@ -14,7 +14,7 @@
 // operands need 8 consecutive TOKENS per lane, so each 32-token block of Psi
 // and Vb is staged in LDS transposed (Psi^T[a][t], Vb^T[c][t]); wave w owns
 // the 16-row tiles 2w and 2w+1 of G and every column tile.
-#include "smat_host.hpp"
+#include "bwd_common.hpp"
 
 namespace smat {
 
@@ -260,6 +260,156 @@ static int64_t plan_split(GramItems& it, int nitems, int nb, int max_count, int 
   return nsplit > 1 ? (int64_t)nb * nitems * nsplit * r * p * 4 : 0;
 }
 
+
+// Gram sums at r = 64, p = 65 for 16-bit inputs (the training shape), any
+// progression or token list of GramItems: item i of sequence b sums its
+// terms kB at a time (128 for chunk summaries, 32 for the short profiles and
+// cell lists, whose workgroups then take a quarter of the LDS; the last
+// block is staged in whole 32-row groups, rows past the end zero).  One workgroup of four waves per item: Psi's rows to LDS as
+// 16-bit rows (swizzled), Vb's columns 0..63 the same and column 64 on its
+// own; wave w forms rows 16w .. 16w+15 of G (features) across five
+// value-column tiles, A = Psi^T and B = Vb read down the tokens with the
+// transposing reads, 32 tokens a product (both operands exact in 16 bits).
+// Item nitems-1 goes to G_last when that is given.
+namespace cg {
+constexpr int kThreads = 256;
+}  // namespace cg
+
+template <typename In, int kB>
+__global__ __launch_bounds__(cg::kThreads) void gram64_kernel(
+    const In* __restrict__ psi, const In* __restrict__ vb, float* __restrict__ G,
+    float* __restrict__ G_last, GramItems it, int vec_v, int64_t k_sb, int64_t k_st,
+    int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si, int64_t gl_sb) {
+  using namespace cb;
+  typedef typename Traits<In>::frag Frag;
+  typedef typename Traits<In>::half_frag Half;
+  __shared__ __attribute__((aligned(16))) uint4 sPsi[kB * kRowChunks];
+  __shared__ __attribute__((aligned(16))) uint4 sVb[kB * kRowChunks];
+  __shared__ In sVb64[kB];
+
+  const int item = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int tid = threadIdx.x;
+  int64_t start, stride;
+  int count;
+  gram_item(it, item, start, stride, count);
+  const In* psib = psi + b * k_sb;
+  const In* vbb = vb + b * v_sb;
+  const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  const int lane = lane_id(), r16 = lane & 15, g = lane >> 4;
+  // lane (m = 16 ct + lane % 16, g), k-slot e <- column m of row row0 + 8g + e
+  auto col8 = [&](const uint4* tile, int row0, int ct) {
+    const int k = 2 * ct + ((r16 & 3) >> 1), half = r16 & 1;
+    const Half lo4 = cb_tr<In>(tile, row0 + 8 * g + (r16 >> 2), k, half);
+    const Half hi4 = cb_tr<In>(tile, row0 + 8 * g + 4 + (r16 >> 2), k, half);
+    Frag f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = lo4[e];
+      f[4 + e] = hi4[e];
+    }
+    return f;
+  };
+  f32x4 acc[5];
+#pragma unroll
+  for (int ct = 0; ct < 5; ++ct) acc[ct] = zero4();
+  const uint4 z4 = make_uint4(0, 0, 0, 0);
+  for (int s0 = 0; s0 < count; s0 += kB) {
+    const int nv = min(kB, count - s0);              // valid rows of the block
+    const int n32 = (nv + 31) & ~31;                 // rows staged (whole 32-row groups)
+    if (s0 > 0) __syncthreads();                     // the last block's readers are done
+    // Psi: n32 rows x 8 chunks
+    for (int e = tid; e < n32 * kRowChunks; e += cg::kThreads) {
+      const int row = e >> 3, k = e & 7;
+      const int64_t t = gram_token(it, item, start, stride, s0 + (row < nv ? row : 0));
+      uint4 v = *reinterpret_cast<const uint4*>(psib + t * k_st + 8 * k);
+      if (row >= nv) v = z4;
+      sPsi[cb_slot(row, k)] = v;
+    }
+    if (vec_v) {
+      // Vb: nine 16-byte pieces a row (columns 0..71)
+      for (int e = tid; e < n32 * 9; e += cg::kThreads) {
+        const int row = e / 9, k = e - 9 * row;
+        const int64_t t = gram_token(it, item, start, stride, s0 + (row < nv ? row : 0));
+        uint4 v = *reinterpret_cast<const uint4*>(vbb + t * v_st + 8 * k);
+        if (row >= nv) v = z4;
+        if (k < 8)
+          sVb[cb_slot(row, k)] = v;
+        else
+          sVb64[row] = __builtin_bit_cast(Frag, v)[0];
+      }
+    } else {
+      for (int e = tid; e < n32 * kP; e += cg::kThreads) {
+        const int row = e / kP, col = e - row * kP;
+        const int64_t t = gram_token(it, item, start, stride, s0 + (row < nv ? row : 0));
+        const In v = row < nv ? vbb[t * v_st + col] : from_f32<In>(0.f);
+        if (col < 64)
+          reinterpret_cast<In*>(sVb + cb_slot(row, col >> 3))[col & 7] = v;
+        else
+          sVb64[row] = v;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kB / 32; ++ks) {
+      if (32 * ks >= nv) break;                      // uniform: the staged rows end at n32
+      const Frag pa = col8(sPsi, 32 * ks, w);        // Psi^T rows 16w + r16
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) acc[ct] = mma(acc[ct], pa, col8(sVb, 32 * ks, ct));
+      Frag bv;                                       // column 64: lane r16 = 0
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        bv[e] = r16 == 0 ? sVb64[32 * ks + 8 * g + e] : from_f32<In>(0.f);
+      acc[4] = mma(acc[4], pa, bv);
+    }
+  }
+  float* out = (G_last != nullptr && item == (int)gridDim.x - 1) ? G_last + b * gl_sb
+                                                                 : G + b * g_sb + item * g_si;
+#pragma unroll
+  for (int ct = 0; ct < 5; ++ct) {
+    const int col = 16 * ct + r16;
+    if (col < kP) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[(16 * w + 4 * g + e) * kP + col] = acc[ct][e];
+    }
+  }
+}
+
+// The r = 64, p = 65 fast path: 16-bit inputs, Psi rows 16-byte aligned, and
+// enough items to fill the device without split-K.
+static bool gram64_ok(int dtype, const void* psi, int r, int p, int64_t k_sb, int64_t k_st,
+                      int nitems, int nb) {
+  return (dtype == SMAT_BF16 || dtype == SMAT_F16) && r == cb::kR && p == cb::kP &&
+         rows_vec_ok(psi, k_sb, k_st, 2) && (int64_t)nitems * nb >= 512 && nb < 65536 &&
+         variant(SMAT_VARIANT_GRAM) == 0;
+}
+
+static int gram64_launch(int dtype, const void* psi, const void* vb, float* G, float* G_last,
+                         const GramItems& it, int nitems, int nb, int64_t k_sb, int64_t k_st,
+                         int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si, int64_t gl_sb,
+                         hipStream_t stream, const char* who) {
+  // nine 16-byte pieces a row stay inside the row's stride
+  const int vec_v = v_st >= 72 && v_st % 8 == 0 && v_sb % 8 == 0 && aligned16(vb);
+  const dim3 grid((unsigned)nitems, (unsigned)nb);
+  const bool wide = it.mode == 0;                    // chunk summaries: 128 or more terms
+#define SMAT_G64(T_, B_)                                                                     \
+  smat::launch(gram64_kernel<T_, B_>, grid, dim3(cg::kThreads), 0, stream, (const T_*)psi, \
+               (const T_*)vb, G, G_last, it, vec_v, k_sb, k_st, v_sb, v_st, g_sb, g_si, gl_sb)
+  if (dtype == SMAT_BF16) {
+    if (wide)
+      SMAT_G64(bf16, 128);
+    else
+      SMAT_G64(bf16, 32);
+  } else {
+    if (wide)
+      SMAT_G64(f16, 128);
+    else
+      SMAT_G64(f16, 32);
+  }
+#undef SMAT_G64
+  return launch_status(who);
+}
+
 bool gram_stream_ok(int dtype, const void* psi, const void* vb, int r, int p, int64_t k_sb,
                     int64_t k_st, int64_t v_sb, int64_t v_st, const GramItems& it, int nitems,
                     int nb);
@@ -273,6 +423,9 @@ int gram_dispatch(int dtype, const void* psi, const void* vb, float* G, float* G
                   int64_t k_st, int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
                   int64_t gl_sb, float* partials, hipStream_t stream, const char* who) {
   if (nitems == 0 || nb == 0) return SMAT_OK;
+  if (gram64_ok(dtype, psi, r, p, k_sb, k_st, nitems, nb))
+    return gram64_launch(dtype, psi, vb, G, G_last, it, nitems, nb, k_sb, k_st, v_sb, v_st, g_sb,
+                         g_si, gl_sb, stream, who);
   if (gram_stream_ok(dtype, psi, vb, r, p, k_sb, k_st, v_sb, v_st, it, nitems, nb))
     return gram_stream_launch(dtype, psi, vb, G, G_last, it, nitems, nb, p, k_sb, k_st, v_sb, v_st,
                               g_sb, g_si, gl_sb, stream, who);

@@ -260,6 +260,33 @@ def test_pool_streaming_head_dim_128(dt, T, d, n_P):
         assert _rel(Fg, gref) < 1e-5
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,d,n_P", [(8192, 3, 0), (8192, 3, 16), (4096, 2, 0)])
+def test_pool_head_dim_64_many_profiles(dt, T, d, n_P):
+    """The 16-bit r = 64, p = 65 Gram kernel (taken when a launch has at least
+    512 items) on the profile pool, incl. the global channel's last-item
+    buffer, Vb rows 72 apart as featurise lays them out: against fp64 and
+    against the general kernel on the same inputs."""
+    _say("pool head_dim 64", dt, T, d, n_P)
+    spec = build_mask(T, d, chunk=128, n_P=n_P)
+    nb = 16
+    Phi, Psi, Vb = _feats(nb, T, 64, dt, seed=37)
+    Vp = torch.zeros(nb, T, 72, dtype=dt)
+    Vp[..., :65] = Vb
+    Sd, Vd = Psi.to(DEV), Vp.to(DEV)[..., :65]
+    assert nb * spec.N0 >= 512
+    Fg = torch.empty(nb, 64, 65, device=DEV) if n_P else None
+    F = K.pool(Sd, Vd, spec.n_P, spec.n, spec.N0, F_glob=Fg)
+    Fg_old = torch.empty(nb, 64, 65, device=DEV) if n_P else None
+    with general_kernel("gram"):
+        F_old = K.pool(Sd, Vd, spec.n_P, spec.n, spec.N0, F_glob=Fg_old)
+    ref = O.pool_profiles(Psi.double(), Vb.double(), spec)
+    assert _rel(F, ref) < 1e-5 and _rel(F_old, ref) < 1e-5
+    if n_P:
+        gref = Psi[:, :n_P].double().transpose(-1, -2) @ Vb[:, :n_P].double()
+        assert _rel(Fg, gref) < 1e-5 and _rel(Fg_old, gref) < 1e-5
+
+
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 def test_chunk_states_and_segment_scan(dt):
     _say("chunk_states + segment_scan", dt)
@@ -278,6 +305,35 @@ def test_chunk_states_and_segment_scan(dt):
     # the reset: the first chunk of each segment sees a zero state, exactly
     assert torch.count_nonzero(Sin[:, 0]).item() == 0
     assert torch.count_nonzero(Sin[:, n // C]).item() == 0
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("vb_pad", [False, True])
+def test_chunk_states_many_sequences(dt, vb_pad):
+    """The 16-bit r = 64, p = 65 chunk-summary kernel (taken when a launch has
+    at least 512 items): 64 sequences, a ragged last chunk, Vb rows 65 or 72
+    apart, against fp64 sums of the same values; and the causal pass that
+    uses it for its group summaries (two chunks a group at this size, split
+    at n) against the oracle's scan."""
+    _say("chunk_states many sequences", dt, vb_pad)
+    nb, T, C, r, p, n = 64, 3000, 128, 64, 65, 1024
+    Phi, Psi, Vb = _feats(nb, T, 64, dt, seed=17)
+    Vd = Vb.to(DEV)
+    if vb_pad:
+        Vp = torch.zeros(nb, T, 72, dtype=dt, device=DEV)
+        Vp[..., :p] = Vd
+        Vd = Vp[..., :p]
+    D = K.chunk_states(Psi.to(DEV), Vd, C)
+    pad = (-T) % C
+    nc = (T + pad) // C
+    Psi_p = torch.nn.functional.pad(Psi.double(), (0, 0, 0, pad))
+    Vb_p = torch.nn.functional.pad(Vb.double(), (0, 0, 0, pad))
+    Dref = torch.einsum("bcta,bctv->bcav", Psi_p.reshape(nb, nc, C, r),
+                        Vb_p.reshape(nb, nc, C, p))
+    assert _rel(D, Dref) < 1e-5
+    H = K.causal_scan(Phi.to(DEV), Psi.to(DEV), Vd, n, C, write_H=True)
+    ref = O.segmented_causal_scan(Phi[:4], Psi[:4], Vb[:4], n, chunk=C)
+    assert _rel(H[:4], ref) < 1e-2
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
