@@ -360,13 +360,14 @@ def featurise_bench(nb, T, hd, reps):
 def train_step_bench(d, reps, B=8, H=12, hd=64, T=4096):
     """One training step of the content-hashed layer, forward and backward, on
     bf16 q, k, v ~ N(0, 1) (k scaled by 1/sqrt(hd)) and an fp32 hidden state
-    the hash reads (d_model = H*hd), upstream gradient ~ N(0, 1): the feature
-    map, the segmented causal scan plus the content-addressed long-range term
-    on the recent rows, the single division and the cast to bf16
-    (model.py:296-300, 317), then backward to q, k, v, the hidden state and
+    the hash reads (d_model = H*hd), upstream gradient dO ~ N(0, 1): the
+    feature map, the segmented causal scan plus the content-addressed
+    long-range term on the recent rows, the single division and the cast to
+    bf16 (model.py:296-300, 317), then backward from dO (``o.backward(dO)``:
+    the gradient the next layer hands back) to q, k, v, the hidden state and
     the hash parameters, their gradients cleared first as zero_grad
     (set_to_none) does; and the same step with positional assignment
-    (smat_attention, forward and backward)."""
+    (smat_attention, the cast to bf16, forward and backward)."""
     import torch
     from smat_attention_amd import attention as A
     from smat_attention_amd.assign import ContentAssign
@@ -393,7 +394,7 @@ def train_step_bench(d, reps, B=8, H=12, hd=64, T=4096):
         Hs = A.segmented_causal_scan(Phi, Psi, Vb, n, 128)
         # cat + clamped division + the cast to the model dtype
         o = A.combine_normalise(Hs, m(X, Phi, Psi, Vb, n), n, out_dtype=bf)
-        (o * dO).float().sum().backward()
+        o.backward(dO)
     us = Events(torch).time(step, reps)
     res = {"ms": round(us / 1e3, 3), "tokens_per_s": round(B * T / (us * 1e-6), 1),
            "config": f"B={B} H={H} head_dim={hd} T={T} d={d} bf16, content-hashed point read, "
@@ -405,8 +406,8 @@ def train_step_bench(d, reps, B=8, H=12, hd=64, T=4096):
         for t in (Q, K, V):
             t.grad = None
         Phi, Psi, Vb = A.featurise(Q, K, V, phi)
-        o = A.smat_attention(Phi, Psi, Vb, spec_t)
-        (o.to(bf) * dO).float().sum().backward()
+        o = A.smat_attention(Phi, Psi, Vb, spec_t).to(bf)
+        o.backward(dO)
     us = Events(torch).time(step_pos, reps)
     res["positional_ms"] = round(us / 1e3, 3)
     return res
