@@ -6,7 +6,7 @@
 // (src/smat/assign.py:431-439, src/smat/kernels/smat_pool_ops.py:158-182).
 //
 // Three launches, none of which reads anything back to the host:
-//   1. count: a histogram of each tile of kTile items (LDS atomics);
+//   1. count: a histogram of each tile of items (LDS atomics);
 //   2. scan:  per sequence, the class totals' exclusive scan gives the list
 //             offsets, and a running sum over tiles each tile's base per class;
 //   3. place: one wave per tile walks its items 64 at a time in order; a
@@ -21,10 +21,22 @@
 namespace smat {
 
 namespace cs {
-constexpr int kTile = 2048;       // items per tile
+constexpr int kMinTile = 512;     // items per tile, while the tile counts stay small
 constexpr int kMaxCls = 8192;     // classes per sequence (LDS table of ints)
 constexpr int kThreads = 256;
+constexpr int64_t kCountBudget = 1 << 22;   // tile counts per sequence (ints)
 }  // namespace cs
+
+// Items per tile: 512, doubled while a sequence's tile counts (tiles x
+// classes) exceed 4 Mi ints.  Shorter tiles make more, shorter placement
+// chains (one wave walks a tile 64 items at a time); the counts bound the
+// workspace and the scan's walk over tiles.
+static int csr_tile(int L, int ncls) {
+  int tile = cs::kMinTile;
+  while (tile < (1 << 20) && (int64_t)((L + tile - 1) / tile) * ncls > cs::kCountBudget)
+    tile *= 2;
+  return tile;
+}
 
 __device__ __forceinline__ int clamp_key(int64_t k, int ncls) {
   return k < 0 ? 0 : (k >= ncls ? ncls - 1 : (int)k);
@@ -38,13 +50,13 @@ __global__ __launch_bounds__(64) void csr_empty_kernel(int64_t* __restrict__ off
 // counts[(b * ntiles + t) * ncls + c] = items of tile t of sequence b with key c.
 __global__ __launch_bounds__(cs::kThreads) void csr_count_kernel(const int64_t* __restrict__ keys,
                                                                  int* __restrict__ counts, int L,
-                                                                 int ncls, int ntiles) {
+                                                                 int ncls, int ntiles, int tile) {
   extern __shared__ int hist[];                      // ncls ints
   const int t = blockIdx.x, b = blockIdx.y;
   for (int c = threadIdx.x; c < ncls; c += cs::kThreads) hist[c] = 0;
   __syncthreads();
   const int64_t* kb = keys + (int64_t)b * L;
-  const int i0 = t * cs::kTile, i1 = min(L, i0 + cs::kTile);
+  const int i0 = t * tile, i1 = min(L, i0 + tile);
   for (int i = i0 + threadIdx.x; i < i1; i += cs::kThreads)
     atomicAdd(&hist[clamp_key(kb[i], ncls)], 1);
   __syncthreads();
@@ -109,8 +121,8 @@ __global__ __launch_bounds__(cs::kThreads) void csr_scan_kernel(int* __restrict_
 __global__ __launch_bounds__(64) void csr_place_kernel(const int64_t* __restrict__ keys,
                                                        const int* __restrict__ bases,
                                                        int32_t* __restrict__ order, int L,
-                                                       int ncls, int ntiles, int nbits, int glob,
-                                                       int64_t seq_rows, int64_t row0) {
+                                                       int ncls, int ntiles, int tile, int nbits,
+                                                       int glob, int64_t seq_rows, int64_t row0) {
   extern __shared__ int next[];                      // ncls ints
   const int t = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x;
@@ -118,7 +130,7 @@ __global__ __launch_bounds__(64) void csr_place_kernel(const int64_t* __restrict
   for (int c = lane; c < ncls; c += 64) next[c] = bb[c];
   __syncthreads();
   const int64_t* kb = keys + (int64_t)b * L;
-  const int i0 = t * cs::kTile, i1 = min(L, i0 + cs::kTile);
+  const int i0 = t * tile, i1 = min(L, i0 + tile);
   const uint64_t below = (1ull << lane) - 1ull;
   for (int g = i0; g < i1; g += 64) {
     const int i = g + lane;
@@ -145,7 +157,8 @@ __global__ __launch_bounds__(64) void csr_place_kernel(const int64_t* __restrict
 
 extern "C" int64_t smat_csr_workspace_bytes(int nb, int L, int ncls) {
   if (nb <= 0 || L <= 0 || ncls <= 0) return 0;
-  const int64_t ntiles = (L + smat::cs::kTile - 1) / smat::cs::kTile;
+  const int tile = smat::csr_tile(L, ncls);
+  const int64_t ntiles = (L + tile - 1) / tile;
   return (int64_t)nb * ntiles * ncls * (int64_t)sizeof(int);
 }
 
@@ -174,18 +187,19 @@ extern "C" int smat_csr_lists(const int64_t* keys, int32_t* order, int64_t* offs
     return launch_status("smat_csr_lists");
   }
   // L = 0: no tiles; the scan alone writes the (all-zero) offsets
-  const int ntiles = (L + cs::kTile - 1) / cs::kTile;
+  const int tile = csr_tile(L, ncls);
+  const int ntiles = (L + tile - 1) / tile;
   int nbits = 0;
   while ((1 << nbits) < ncls) ++nbits;
   int* counts = (int*)workspace;
   const size_t lds = (size_t)ncls * sizeof(int);
   if (ntiles)
     hipLaunchKernelGGL(csr_count_kernel, dim3(ntiles, nb), dim3(cs::kThreads), lds, st, keys,
-                       counts, L, ncls, ntiles);
+                       counts, L, ncls, ntiles, tile);
   hipLaunchKernelGGL(csr_scan_kernel, dim3(nb), dim3(cs::kThreads), 0, st, counts, offs, nb, L,
                      ncls, ntiles);
   if (ntiles)
     hipLaunchKernelGGL(csr_place_kernel, dim3(ntiles, nb), dim3(64), lds, st, keys, counts, order,
-                       L, ncls, ntiles, nbits, global_index, seq_rows, row0);
+                       L, ncls, ntiles, tile, nbits, global_index, seq_rows, row0);
   return launch_status("smat_csr_lists");
 }
