@@ -378,13 +378,15 @@ def test_csr_offsets_match_counts():
 @pytest.mark.gpu
 @pytest.mark.parametrize("nb,L,ncls", [(3, 300, 7), (2, 5000, 169), (1, 2048, 1), (4, 64, 300),
                                        (2, 0, 5), (96, 8192, 169), (1, 4100, 8192),
-                                       (0, 100, 5)])
+                                       (0, 100, 5), (1, 600_000, 8192)])
 def test_class_lists_match_stable_sort(nb, L, ncls):
     """smat_csr_lists (the counting sort behind every cell and type list)
     against torch's stable argsort and bincount of ``b*ncls + key`` on the CPU:
-    the same order (as global and as in-sequence item ids) and offsets.  Ragged
-    tiles (L not a multiple of 2048), one class, empty classes, empty
-    sequences and the largest class count included."""
+    the same order (as global, as in-sequence and as rows of longer sequences
+    from a row offset) and offsets.  Ragged tiles (L not a multiple of the
+    512-item tile), one class, empty classes, empty sequences, the largest
+    class count and a sequence long enough that the tile doubles (600 000
+    items, 8192 classes: 2048-item tiles) included."""
     from smat_attention_amd.pool_ops import _class_lists
     gen = torch.Generator().manual_seed(nb * 7 + L + ncls)
     keys = torch.randint(0, ncls, (nb, L), generator=gen)
@@ -402,6 +404,12 @@ def test_class_lists_match_stable_sort(nb, L, ncls):
         offs = offs.cpu()
         assert offs[0] == 0 and offs[-1] == nb * L
         assert torch.equal(offs[1:] - offs[:-1], cnt)
+    if L:
+        # rows [11, 11 + L) of sequences L + 37 rows long: item b*(L+37) + 11 + l
+        order, offs = _class_lists(keys.to(dev), ncls, seq_rows=L + 37, row0=11)
+        want = (ref // L) * (L + 37) + 11 + ref % L
+        assert torch.equal(order.cpu().long(), want)
+        assert torch.equal(offs.cpu()[1:] - offs.cpu()[:-1], cnt)
     if nb == 0:
         # the one offset of an empty batch is written, not left as it was
         from smat_attention_amd.kernels._lib import call, stream_of

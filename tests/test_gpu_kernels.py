@@ -782,6 +782,26 @@ def test_forward_direct_and_subtractive(lr, dt, T, d, n_P, hd):
     assert (out - pooled).abs().max().item() < (1e-3 if dt == torch.float32 else 3e-2)
 
 
+def test_direct_head_dim_64_many_items():
+    """The direct schedule's unpooled sums (Gram items over landmark column
+    lists) at r = 64, p = 65, bf16, 16 sequences -- 2912 items, so the 16-bit
+    r = 64 Gram kernel runs -- against the general Gram kernel on the same
+    inputs and against the oracle on two sequences."""
+    T, d, nb = 4096, 3, 16
+    spec = A.to_device(build_mask(T, d, chunk=128), DEV, want_direct=True)
+    assert nb * spec.B >= 512
+    Phi, Psi, Vb = _feats(nb, T, 64, torch.bfloat16, seed=47, k_scale=0.5)
+    Pd, Sd, Wd = (x.to(DEV) for x in (Phi, Psi, Vb))
+    _say("direct head_dim 64", T, d, nb)
+    out = A.smat_attention(Pd, Sd, Wd, spec, long_range="direct")
+    with general_kernel("gram"):
+        old = A.smat_attention(Pd, Sd, Wd, spec, long_range="direct")
+    torch.cuda.synchronize()
+    assert _rel(out, old) < 1e-5
+    ref = O.smat_attention(Phi[:2], Psi[:2], Vb[:2], spec, long_range="direct")
+    assert (out[:2].double().cpu() - ref.double()).abs().max().item() < 2e-2
+
+
 def test_decode_endpoint():
     T = 1024
     spec = build_mask(T, T.bit_length() - 1, chunk=8)
