@@ -12,7 +12,10 @@
 //
 // One workgroup of four waves per (sequence, cell), over the CSR list of the
 // (token, pair) entries that point at the cell; the cell's r x p table is
-// staged in LDS once.  The products against the table run on fp32 MFMA
+// staged in LDS once.  Four workgroups share a CU (registers capped at 128
+// a lane): their waves spend most of their time waiting on the gathers, and
+// a fourth workgroup hides more of it (the read kernel ran 430 us at three,
+// 367 us at four at C4 d = 3).  The products against the table run on fp32 MFMA
 // (v_mfma_f32_16x16x4_f32; frag element j holds k = 4j + g): their sums over
 // value columns cancel the normaliser column against the values, which a
 // hi/lo 16-bit split would not resolve.  dF, a sum over tokens per column,
@@ -38,7 +41,7 @@ constexpr int kStep = 32;                 // entries a step (read backward)
 // w, wave 0 also tile 4 (column 64).
 // ---------------------------------------------------------------------------
 template <typename In, typename Out>
-__global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
+__global__ __launch_bounds__(cw::kThreads, 4) void cell_read_bwd_kernel(
     const In* __restrict__ phr, const float* __restrict__ dY, const float* __restrict__ F,
     const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, Out* __restrict__ dPhi,
     float* __restrict__ dF, float* __restrict__ dw, int N0, int K, int64_t q_sb, int64_t q_st,
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(cw::kThreads) void cell_read_bwd_kernel(
 // and dVb for pair-0 entries and Psi . v for every entry.
 // ---------------------------------------------------------------------------
 template <typename In, typename Out>
-__global__ __launch_bounds__(cw::kThreads) void cell_pool_bwd_kernel(
+__global__ __launch_bounds__(cw::kThreads, 4) void cell_pool_bwd_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, const float* __restrict__ dF,
     const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, Out* __restrict__ dPsi,
     Out* __restrict__ dVb, float* __restrict__ dw, int N0, int K, int64_t k_sb, int64_t k_st,

@@ -13,7 +13,10 @@
 //                       per profile x, dF_x read once for both
 //
 // Each launch streams one r x p fp32 matrix per item (U_h, dF_x) against the
-// few token rows of that item -- bandwidth kernels.  The products run on bf16
+// few token rows of that item -- bandwidth kernels whose waves mostly wait
+// on their loads: the list gram and the pool backward cap their registers
+// so five workgroups share a CU (a few spilled values; 245 -> 232 and
+// 171 -> 163 us at C4 d = 3).  The products run on bf16
 // MFMA with fp32 operands split hi/lo, except the query's dPhi (fp32 MFMA, see
 // there).  The reference differentiates
 // the query and incidence with torch and fuses the pool backward in
@@ -104,7 +107,7 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dphi_kernel(
 // tiles; wave 0 also tile 4 (column 64).
 // ---------------------------------------------------------------------------
 template <typename In>
-__global__ __launch_bounds__(lr::kThreads) void lr_dfeat_kernel(
+__global__ __launch_bounds__(lr::kThreads, 5) void lr_dfeat_kernel(
     const In* __restrict__ phi, const float* __restrict__ dH, const int32_t* __restrict__ tptr,
     const int32_t* __restrict__ tok, float* __restrict__ dF, int64_t q_sb, int64_t q_st,
     int64_t h_sb, int64_t h_st, int64_t f_sb) {
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(lr::kThreads) void lr_dfeat_kernel(
 // (wave 0 also column tile 4) for the tokens, 16 at a time, and adds them in.
 // ---------------------------------------------------------------------------
 template <typename In>
-__global__ __launch_bounds__(lr::kThreads) void lr_pool_bwd_kernel(
+__global__ __launch_bounds__(lr::kThreads, 5) void lr_pool_bwd_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, const float* __restrict__ dF,
     float* __restrict__ dPsi, float* __restrict__ dVb, int N0, int n, int n_P, int64_t k_sb,
     int64_t k_st, int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
