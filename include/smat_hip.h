@@ -387,9 +387,10 @@ int smat_pool_backward(int dtype, const void* psi, const void* vb, const float* 
  * Gradients of ContentAssign's hard point read and pool (src/smat/assign.py:
  * 431-441 at anneal = 1, whose forward weights are the one-hot of pair 0) at
  * r = 64, p = 65 for 16-bit Phi/Psi/Vb (SMAT_EUNSUPPORTED otherwise).  ent
- * lists, for every (sequence b, cell x), the entries e = token*K + pair of
- * sequence b whose pair points at x: ent[eoffs[b*N0 + x] .. eoffs[b*N0+x+1]),
- * every (token, pair) once.
+ * lists, for every (sequence b, cell x), the entries e = pair*L + token of
+ * sequence b (L tokens, K pairs each) whose pair points at x, in ascending
+ * order (so a cell's pair-0 entries come first):
+ * ent[eoffs[b*N0 + x] .. eoffs[b*N0+x+1]), every (token, pair) once.
  *
  * smat_cell_read_backward: for y_i = Phi_i F[cell_i0] and upstream dY (fp32,
  * rows of stride y_st): dPhi_i = F[x] dY_i (pair 0), dw[i*K + k] =
@@ -428,12 +429,14 @@ int smat_featurise_backward(int dtype, const void* x, const void* G, const void*
 
 int smat_cell_read_backward(int dtype, int out_dtype, const void* phr, const float* dY,
                             const float* F, const int32_t* ent, const int64_t* eoffs, void* dPhi,
-                            float* dF, float* dw, int nb, int N0, int K, int r, int p, int64_t q_sb,
+                            float* dF, float* dw, int nb, int N0, int K, int L, int r, int p,
+                            int64_t q_sb,
                             int64_t q_st, int64_t y_sb, int64_t y_st, int64_t f_sb,
                             int64_t d_sb, int64_t d_st, int64_t w_sb, void* stream);
 int smat_cell_pool_backward(int dtype, int out_dtype, const void* psi, const void* vb,
                             const float* dF, const int32_t* ent, const int64_t* eoffs, void* dPsi,
-                            void* dVb, float* dw, int nb, int N0, int K, int r, int p, int64_t k_sb,
+                            void* dVb, float* dw, int nb, int N0, int K, int L, int r, int p,
+                            int64_t k_sb,
                             int64_t k_st, int64_t v_sb, int64_t v_st, int64_t f_sb,
                             int64_t d_sb, int64_t d_st, int64_t e_sb, int64_t e_st,
                             int64_t w_sb, void* stream);

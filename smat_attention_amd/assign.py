@@ -750,10 +750,10 @@ def _cell_backward_ok(X, Y, r_ok=64, p_ok=65):
 
 def _entry_lists(idx, N0):
     """CSR of the (token, pair) entries of every (sequence, cell): idx (nb, L, K)
-    -> entry ids token*K + pair (int32, ascending within a cell) and offsets
-    (int64, nb*N0 + 1)."""
+    -> entry ids pair*L + token (int32, ascending within a cell, so a cell's
+    pair-0 entries come first) and offsets (int64, nb*N0 + 1)."""
     nb, L, K = idx.shape
-    return _class_lists(idx.reshape(nb, L * K), N0, global_index=False)
+    return _class_lists(idx.transpose(1, 2).reshape(nb, K * L), N0, global_index=False)
 
 
 # The pairs of the training path from one kernel (smat_hash_pairs) and its
@@ -910,7 +910,7 @@ class _HardPool(torch.autograd.Function):
             dwk = torch.empty(nb, n, K, device=Psi.device, dtype=torch.float32)
             call("smat_cell_pool_backward", _code(Psi, "ContentAssign"), _code(dPsi, "ContentAssign"),
                  Psi.data_ptr(), Vb.data_ptr(), dF.data_ptr(), ent.data_ptr(), eoffs.data_ptr(),
-                 dPsi.data_ptr(), dVb.data_ptr(), dwk.data_ptr(), nb, N0, K, r, p, Psi.stride(0),
+                 dPsi.data_ptr(), dVb.data_ptr(), dwk.data_ptr(), nb, N0, K, n, r, p, Psi.stride(0),
                  Psi.stride(1), Vb.stride(0), Vb.stride(1), dF.stride(0), dPsi.stride(0),
                  dPsi.stride(1), dVb.stride(0), dVb.stride(1), dwk.stride(0), stream_of(dF))
             return dPsi, dVb, dwk.to(ctx.w_dtype), None, None, None
@@ -989,7 +989,7 @@ class _HardRead(torch.autograd.Function):
             call("smat_cell_read_backward", _code(Phr, "ContentAssign"),
                  _code(dPr, "ContentAssign"), Phr.data_ptr(), dYc.data_ptr(), Fc.data_ptr(),
                  ent.data_ptr(), eoffs.data_ptr(), dPr.data_ptr(), dF.data_ptr(), dwq.data_ptr(),
-                 nb, N0, K, r, p, Phr.stride(0), Phr.stride(1), dYc.stride(0), dYc.stride(1),
+                 nb, N0, K, T_R, r, p, Phr.stride(0), Phr.stride(1), dYc.stride(0), dYc.stride(1),
                  Fc.stride(0), dPr.stride(0), dPr.stride(1), dwq.stride(0), stream_of(Fc))
             return dPhi, dF, dwq.to(ctx.w_dtype), None, None
         Phr = Phr.contiguous()

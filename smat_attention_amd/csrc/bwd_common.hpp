@@ -206,14 +206,16 @@ struct CbGather {
   bool ok;
   uint4 r64;
   Row65 r65[kU];
+  // Entry ids are pair-major, pair * L + token (L tokens a sequence), so each
+  // cell's list holds its pair-0 entries first.
   __device__ __forceinline__ void load(const int32_t* ent, int64_t s0, int64_t beg, int64_t end,
-                                       int K, const In* rows64, int64_t st64, const Row65* rows65,
+                                       int L, const In* rows64, int64_t st64, const Row65* rows65,
                                        int64_t st65, int tid) {
     const int slot = tid >> 3, sub = tid & 7;
     ok = s0 + slot < end;
     const int e = ent[ok ? s0 + slot : beg];
-    tok = e / K;
-    pair = e - tok * K;
+    pair = (int)((unsigned)e / (unsigned)L);
+    tok = e - pair * L;
     r64 = *reinterpret_cast<const uint4*>(rows64 + (int64_t)tok * st64 + 8 * sub);
     const Row65* r = rows65 + (int64_t)tok * st65;
 #pragma unroll

@@ -11,7 +11,10 @@
 //          dPsi_j = v, dVb_j = Psi_j dF[x] (pair 0),  dw_jk = Psi_j . v
 //
 // One workgroup of four waves per (sequence, cell), over the CSR list of the
-// (token, pair) entries that point at the cell; the cell's r x p table is
+// (token, pair) entries that point at the cell, numbered pair * L + token so
+// that the pair-0 entries come first: a step of entries with no pair-0 entry
+// skips the work only pair-0 entries need (the read's dF Gram, the pool's
+// dVb products), seven eighths of the steps at 2^3 pairs a token; the cell's r x p table is
 // staged in LDS once.  Four workgroups share a CU (registers capped at 128
 // a lane): their waves spend most of their time waiting on the gathers, and
 // a fourth workgroup hides more of it (the read kernel ran 430 us at three,
@@ -44,8 +47,9 @@ template <typename In, typename Out>
 __global__ __launch_bounds__(cw::kThreads, 4) void cell_read_bwd_kernel(
     const In* __restrict__ phr, const float* __restrict__ dY, const float* __restrict__ F,
     const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, Out* __restrict__ dPhi,
-    float* __restrict__ dF, float* __restrict__ dw, int N0, int K, int64_t q_sb, int64_t q_st,
-    int64_t y_sb, int64_t y_st, int64_t f_sb, int64_t d_sb, int64_t d_st, int64_t w_sb) {
+    float* __restrict__ dF, float* __restrict__ dw, int N0, int K, int L, int64_t q_sb,
+    int64_t q_st, int64_t y_sb, int64_t y_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
+    int64_t w_sb) {
   using namespace cb;
   typedef typename Traits<In>::frag Frag;
   typedef typename Traits<In>::half_frag Half;
@@ -63,7 +67,7 @@ __global__ __launch_bounds__(cw::kThreads, 4) void cell_read_bwd_kernel(
   const In* phb = phr + b * q_sb;
   const float* dYb = dY + b * y_sb;
   CbGather<In, float> ga;
-  if (beg < end) ga.load(ent, beg, beg, end, K, phb, q_st, dYb, y_st, tid);
+  if (beg < end) ga.load(ent, beg, beg, end, L, phb, q_st, dYb, y_st, tid);
   cb_stage_rp(sF, F + b * f_sb + (int64_t)x * cw::kRP);
   __syncthreads();
 
@@ -103,7 +107,8 @@ __global__ __launch_bounds__(cw::kThreads, 4) void cell_read_bwd_kernel(
       }
     }
     __syncthreads();
-    if (s0 + cw::kStep < end) ga.load(ent, s0 + cw::kStep, beg, end, K, phb, q_st, dYb, y_st, tid);
+    if (s0 + cw::kStep < end) ga.load(ent, s0 + cw::kStep, beg, end, L, phb, q_st, dYb, y_st, tid);
+    const bool has0 = sPair[0] == 0;                 // uniform: entry 0 of the step is valid
 
     // v = F dy for the two 16-entry tiles; dPhi (pair 0) and Phi . v
 #pragma unroll
@@ -146,26 +151,28 @@ __global__ __launch_bounds__(cw::kThreads, 4) void cell_read_bwd_kernel(
         lo[e8] = ll;
       }
     };
-    Frag bh, bl;
-    bfrag(w, bh, bl);
+    if (has0) {                                      // steps past the pair-0 entries add nothing
+      Frag bh, bl;
+      bfrag(w, bh, bl);
 #pragma unroll
-    for (int at = 0; at < 4; ++at) {
-      const int k = 2 * at + ((r16 & 3) >> 1), half = r16 & 1;
-      const Half lo4 = cb_tr<In>(sPh, 8 * g + (r16 >> 2), k, half);
-      const Half hi4 = cb_tr<In>(sPh, 8 * g + 4 + (r16 >> 2), k, half);
-      Frag pa;
+      for (int at = 0; at < 4; ++at) {
+        const int k = 2 * at + ((r16 & 3) >> 1), half = r16 & 1;
+        const Half lo4 = cb_tr<In>(sPh, 8 * g + (r16 >> 2), k, half);
+        const Half hi4 = cb_tr<In>(sPh, 8 * g + 4 + (r16 >> 2), k, half);
+        Frag pa;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pa[i] = lo4[i];
-        pa[4 + i] = hi4[i];
-      }
-      acc[at] = mma(acc[at], pa, bh);
-      acc[at] = mma(acc[at], pa, bl);
-      if (w == 0) {
-        Frag b4h, b4l;
-        bfrag(4, b4h, b4l);
-        acc4[at] = mma(acc4[at], pa, b4h);
-        acc4[at] = mma(acc4[at], pa, b4l);
+        for (int i = 0; i < 4; ++i) {
+          pa[i] = lo4[i];
+          pa[4 + i] = hi4[i];
+        }
+        acc[at] = mma(acc[at], pa, bh);
+        acc[at] = mma(acc[at], pa, bl);
+        if (w == 0) {
+          Frag b4h, b4l;
+          bfrag(4, b4h, b4l);
+          acc4[at] = mma(acc4[at], pa, b4h);
+          acc4[at] = mma(acc4[at], pa, b4l);
+        }
       }
     }
     __syncthreads();                                 // sDot complete; LDS free for the next step
@@ -198,9 +205,9 @@ template <typename In, typename Out>
 __global__ __launch_bounds__(cw::kThreads, 4) void cell_pool_bwd_kernel(
     const In* __restrict__ psi, const In* __restrict__ vb, const float* __restrict__ dF,
     const int32_t* __restrict__ ent, const int64_t* __restrict__ eoffs, Out* __restrict__ dPsi,
-    Out* __restrict__ dVb, float* __restrict__ dw, int N0, int K, int64_t k_sb, int64_t k_st,
-    int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st, int64_t e_sb,
-    int64_t e_st, int64_t w_sb) {
+    Out* __restrict__ dVb, float* __restrict__ dw, int N0, int K, int L, int64_t k_sb,
+    int64_t k_st, int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
+    int64_t e_sb, int64_t e_st, int64_t w_sb) {
   using namespace cb;
   __shared__ __attribute__((aligned(16))) float sF[kR * kS];
   __shared__ __attribute__((aligned(16))) float sP[cw::kStep * kS];
@@ -216,7 +223,7 @@ __global__ __launch_bounds__(cw::kThreads, 4) void cell_pool_bwd_kernel(
   const In* psib = psi + b * k_sb;
   const In* vbb = vb + b * v_sb;
   CbGather<In, In> ga;
-  ga.load(ent, beg, beg, end, K, psib, k_st, vbb, v_st, tid);
+  ga.load(ent, beg, beg, end, L, psib, k_st, vbb, v_st, tid);
   cb_stage_rp(sF, dF + b * f_sb + (int64_t)x * cw::kRP);
   __syncthreads();
 
@@ -258,7 +265,8 @@ __global__ __launch_bounds__(cw::kThreads, 4) void cell_pool_bwd_kernel(
       }
     }
     __syncthreads();
-    if (s0 + cw::kStep < end) ga.load(ent, s0 + cw::kStep, beg, end, K, psib, k_st, vbb, v_st, tid);
+    if (s0 + cw::kStep < end) ga.load(ent, s0 + cw::kStep, beg, end, L, psib, k_st, vbb, v_st, tid);
+    const bool has0 = sPair[0] == 0;                 // uniform: entry 0 of the step is valid
 
 #pragma unroll
     for (int et = 0; et < 2; ++et) {
@@ -273,7 +281,7 @@ __global__ __launch_bounds__(cw::kThreads, 4) void cell_pool_bwd_kernel(
           psf[j] = sP[es * kS + 32 * kc + 4 * j + g];
         }
         v = mma(v, fr[kc], vbf);
-        dv = mma(dv, fc[kc], psf);
+        if (has0) dv = mma(dv, fc[kc], psf);         // dVb: pair-0 entries only
       }
       v = __builtin_amdgcn_mfma_f32_16x16x4f32(frt, g == 0 ? sV[es * kS + 64] : 0.f, v, 0, 0, 0);
       // lane (es, g): v[16w + 4g + i] (dPsi), dv[16w + 4g + i] (dVb columns)
@@ -289,7 +297,7 @@ __global__ __launch_bounds__(cw::kThreads, 4) void cell_pool_bwd_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) ov[i] = from_f32<Out>(dv[i]);
       }
-      if (w == 0) {
+      if (w == 0 && has0) {
         // column 64 of dVb: sum_a dF[a][64] Psi[a] (lane group 0, slot 0)
         f32x4 d4 = zero4();
 #pragma unroll
@@ -320,23 +328,23 @@ static bool cw_ok(int dtype, int out_dtype, int r, int p, int K) {
 template <typename In, typename Out>
 static void cell_read_launch(dim3 grid, hipStream_t st, const void* phr, const float* dY,
                              const float* F, const int32_t* ent, const int64_t* eoffs, void* dPhi,
-                             float* dF, float* dw, int N0, int K, int64_t q_sb, int64_t q_st,
+                             float* dF, float* dw, int N0, int K, int L, int64_t q_sb, int64_t q_st,
                              int64_t y_sb, int64_t y_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
                              int64_t w_sb) {
   hipLaunchKernelGGL((cell_read_bwd_kernel<In, Out>), grid, dim3(cw::kThreads), 0, st,
-                     (const In*)phr, dY, F, ent, eoffs, (Out*)dPhi, dF, dw, N0, K, q_sb, q_st,
+                     (const In*)phr, dY, F, ent, eoffs, (Out*)dPhi, dF, dw, N0, K, L, q_sb, q_st,
                      y_sb, y_st, f_sb, d_sb, d_st, w_sb);
 }
 
 template <typename In, typename Out>
 static void cell_pool_launch(dim3 grid, hipStream_t st, const void* psi, const void* vb,
                              const float* dF, const int32_t* ent, const int64_t* eoffs, void* dPsi,
-                             void* dVb, float* dw, int N0, int K, int64_t k_sb, int64_t k_st,
+                             void* dVb, float* dw, int N0, int K, int L, int64_t k_sb, int64_t k_st,
                              int64_t v_sb, int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
                              int64_t e_sb, int64_t e_st, int64_t w_sb) {
   hipLaunchKernelGGL((cell_pool_bwd_kernel<In, Out>), grid, dim3(cw::kThreads), 0, st,
                      (const In*)psi, (const In*)vb, dF, ent, eoffs, (Out*)dPsi, (Out*)dVb, dw, N0,
-                     K, k_sb, k_st, v_sb, v_st, f_sb, d_sb, d_st, e_sb, e_st, w_sb);
+                     K, L, k_sb, k_st, v_sb, v_st, f_sb, d_sb, d_st, e_sb, e_st, w_sb);
 }
 
 }  // namespace smat
@@ -344,7 +352,7 @@ static void cell_pool_launch(dim3 grid, hipStream_t st, const void* psi, const v
 extern "C" int smat_cell_read_backward(int dtype, int out_dtype, const void* phr,
                                        const float* dY, const float* F, const int32_t* ent,
                                        const int64_t* eoffs, void* dPhi, float* dF, float* dw,
-                                       int nb, int N0, int K,
+                                       int nb, int N0, int K, int L,
                                        int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb,
                                        int64_t y_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
                                        int64_t w_sb, void* stream) {
@@ -352,7 +360,8 @@ extern "C" int smat_cell_read_backward(int dtype, int out_dtype, const void* phr
   clear_error();
   SMAT_REQUIRE(phr && dY && F && ent && eoffs && dPhi && dF && dw, SMAT_EINVAL,
                "smat_cell_read_backward: null pointer");
-  SMAT_REQUIRE(nb >= 0 && N0 >= 1, SMAT_EINVAL, "smat_cell_read_backward: bad sizes");
+  SMAT_REQUIRE(nb >= 0 && N0 >= 1 && L >= 1 && (int64_t)K * L < (1ll << 31), SMAT_EINVAL,
+               "smat_cell_read_backward: bad sizes");
   SMAT_REQUIRE(cw_ok(dtype, out_dtype, r, p, K), SMAT_EUNSUPPORTED,
                "smat_cell_read_backward: needs dtype bf16/f16, out_dtype fp32 or dtype, r=64, "
                "p=65 (got %d, %d, %d, %d)",
@@ -369,19 +378,19 @@ extern "C" int smat_cell_read_backward(int dtype, int out_dtype, const void* phr
   const bool f32 = out_dtype == SMAT_F32;
   if (dtype == SMAT_BF16)
     (f32 ? cell_read_launch<bf16, float> : cell_read_launch<bf16, bf16>)(
-        grid, st, phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, q_sb, q_st, y_sb, y_st, f_sb, d_sb,
-        d_st, w_sb);
+        grid, st, phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, L, q_sb, q_st, y_sb, y_st, f_sb,
+        d_sb, d_st, w_sb);
   else
     (f32 ? cell_read_launch<f16, float> : cell_read_launch<f16, f16>)(
-        grid, st, phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, q_sb, q_st, y_sb, y_st, f_sb, d_sb,
-        d_st, w_sb);
+        grid, st, phr, dY, F, ent, eoffs, dPhi, dF, dw, N0, K, L, q_sb, q_st, y_sb, y_st, f_sb,
+        d_sb, d_st, w_sb);
   return launch_status("smat_cell_read_backward");
 }
 
 extern "C" int smat_cell_pool_backward(int dtype, int out_dtype, const void* psi,
                                        const void* vb, const float* dF, const int32_t* ent,
                                        const int64_t* eoffs, void* dPsi, void* dVb, float* dw,
-                                       int nb, int N0, int K,
+                                       int nb, int N0, int K, int L,
                                        int r, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
                                        int64_t v_st, int64_t f_sb, int64_t d_sb, int64_t d_st,
                                        int64_t e_sb, int64_t e_st, int64_t w_sb, void* stream) {
@@ -389,7 +398,8 @@ extern "C" int smat_cell_pool_backward(int dtype, int out_dtype, const void* psi
   clear_error();
   SMAT_REQUIRE(psi && vb && dF && ent && eoffs && dPsi && dVb && dw, SMAT_EINVAL,
                "smat_cell_pool_backward: null pointer");
-  SMAT_REQUIRE(nb >= 0 && N0 >= 1, SMAT_EINVAL, "smat_cell_pool_backward: bad sizes");
+  SMAT_REQUIRE(nb >= 0 && N0 >= 1 && L >= 1 && (int64_t)K * L < (1ll << 31), SMAT_EINVAL,
+               "smat_cell_pool_backward: bad sizes");
   SMAT_REQUIRE(cw_ok(dtype, out_dtype, r, p, K), SMAT_EUNSUPPORTED,
                "smat_cell_pool_backward: needs dtype bf16/f16, out_dtype fp32 or dtype, r=64, "
                "p=65 (got %d, %d, %d, %d)",
@@ -406,11 +416,11 @@ extern "C" int smat_cell_pool_backward(int dtype, int out_dtype, const void* psi
   const bool f32 = out_dtype == SMAT_F32;
   if (dtype == SMAT_BF16)
     (f32 ? cell_pool_launch<bf16, float> : cell_pool_launch<bf16, bf16>)(
-        grid, st, psi, vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K, k_sb, k_st, v_sb, v_st, f_sb,
+        grid, st, psi, vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K, L, k_sb, k_st, v_sb, v_st, f_sb,
         d_sb, d_st, e_sb, e_st, w_sb);
   else
     (f32 ? cell_pool_launch<f16, float> : cell_pool_launch<f16, f16>)(
-        grid, st, psi, vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K, k_sb, k_st, v_sb, v_st, f_sb,
+        grid, st, psi, vb, dF, ent, eoffs, dPsi, dVb, dw, N0, K, L, k_sb, k_st, v_sb, v_st, f_sb,
         d_sb, d_st, e_sb, e_st, w_sb);
   return launch_status("smat_cell_pool_backward");
 }

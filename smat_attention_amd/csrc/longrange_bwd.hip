@@ -133,7 +133,9 @@ __global__ __launch_bounds__(lr::kThreads, 5) void lr_dfeat_kernel(
     acc4[at] = zero4();
   }
   CbGather<In, float> ga;
-  if (beg < end) ga.load(tok, beg, beg, end, 1, phib, q_st, dHb, h_st, tid);
+  // plain token ids: an L above every id decodes each as (pair 0, token id)
+  constexpr int kNoPair = 0x7fffffff;
+  if (beg < end) ga.load(tok, beg, beg, end, kNoPair, phib, q_st, dHb, h_st, tid);
   for (int64_t s0 = beg; s0 < end; s0 += lr::kStep) {
     if (s0 > beg) __syncthreads();                   // the last step's readers are done
     {
@@ -146,7 +148,8 @@ __global__ __launch_bounds__(lr::kThreads, 5) void lr_dfeat_kernel(
       }
     }
     __syncthreads();
-    if (s0 + lr::kStep < end) ga.load(tok, s0 + lr::kStep, beg, end, 1, phib, q_st, dHb, h_st, tid);
+    if (s0 + lr::kStep < end)
+      ga.load(tok, s0 + lr::kStep, beg, end, kNoPair, phib, q_st, dHb, h_st, tid);
 
     // B = dY (k = token slot 8g + e, n = column c)
     auto bfrag = [&](int ct, Frag& hi, Frag& lo) {

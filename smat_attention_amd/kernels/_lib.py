@@ -81,9 +81,9 @@ SIGNATURES = {
                            _i64, _p]),
     "smat_pool_backward": (_i, [_i, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i64, _i64,
                                 _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p]),
-    "smat_cell_read_backward": (_i, [_i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,
+    "smat_cell_read_backward": (_i, [_i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,
                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
-    "smat_cell_pool_backward": (_i, [_i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i,
+    "smat_cell_pool_backward": (_i, [_i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i,
                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _i64, _p]),
     "smat_featurise_backward_parts": (_i64, [_i, _i]),

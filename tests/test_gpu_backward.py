@@ -539,7 +539,7 @@ def test_cell_backward_16bit_outputs_are_rounded_fp32():
         Xr, dXr = X[:, n:], dX[:, n:]
         call("smat_cell_read_backward", 0, AS._code(dXr, "t"), Xr.data_ptr(), dY.data_ptr(),
              F.data_ptr(), ent.data_ptr(), eoffs.data_ptr(), dXr.data_ptr(), dF.data_ptr(),
-             dw.data_ptr(), nb, N0, K, r, p, Xr.stride(0), Xr.stride(1), dY.stride(0),
+             dw.data_ptr(), nb, N0, K, T - n, r, p, Xr.stride(0), Xr.stride(1), dY.stride(0),
              dY.stride(1), F.stride(0), dXr.stride(0), dXr.stride(1), dw.stride(0),
              stream_of(F))
         return dX.cpu(), dF.cpu(), dw.cpu()
@@ -551,7 +551,7 @@ def test_cell_backward_16bit_outputs_are_rounded_fp32():
         dw = torch.empty(nb, n, K, device=DEV)
         call("smat_cell_pool_backward", 0, AS._code(dX, "t"), X.data_ptr(), Vb.data_ptr(),
              F.data_ptr(), ent.data_ptr(), eoffs.data_ptr(), dX.data_ptr(), dV.data_ptr(),
-             dw.data_ptr(), nb, N0, K, r, p, X.stride(0), X.stride(1), Vb.stride(0),
+             dw.data_ptr(), nb, N0, K, n, r, p, X.stride(0), X.stride(1), Vb.stride(0),
              Vb.stride(1), F.stride(0), dX.stride(0), dX.stride(1), dV.stride(0), dV.stride(1),
              dw.stride(0), stream_of(F))
         return dX.cpu(), dV.cpu(), dw.cpu()
