@@ -40,7 +40,8 @@ int variant(int which) {
 // defined in the other translation units
 int pool_dispatch(int dtype, const void* psi, const void* vb, float* F, float* F_glob, int nb,
                   int n_P, int n, int N0, int r, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
-                  int64_t v_st, float* partials, int64_t partial_bytes, hipStream_t stream);
+                  int64_t v_st, float* partials, int64_t partial_bytes, hipStream_t stream,
+                  int64_t f_ld);
 int64_t pool_workspace_bytes(int nb, int n_P, int n, int N0, int r, int p, bool glob);
 int chunk_states_dispatch(int dtype, const void* psi, const void* vb, float* D, int nb, int T,
                           int C, int K, int n, int r, int p, int64_t k_sb, int64_t k_st,
@@ -57,10 +58,13 @@ int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int
                        const int64_t* indptr, int deg, float* U, int nb, int N0, int B, int64_t rp,
                        hipStream_t stream);
 int incidence_plane_dispatch(const float* F, const float* F_glob, const int* code, int q,
-                             float* U, int nb, int N0, int B, int64_t rp, hipStream_t stream);
+                             float* U, int nb, int N0, int B, int64_t rp, int64_t ld,
+                             hipStream_t stream);
+int64_t incidence_spread_ld(int64_t rp);
+int64_t incidence_plane_ld(int q, int N0, int B, int64_t rp);
 int query_dispatch(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R, int B,
-                   int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
-                   hipStream_t stream);
+                   int r, int p, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                   int64_t y_st, hipStream_t stream);
 int normalise_dispatch(const float* H, const float* Y, const float* g, float* out, int nb, int T,
                        int n, int p, int64_t h_sb, int64_t h_st, int64_t y_sb, int64_t y_st,
                        int64_t o_sb, int64_t o_st, int64_t g_sb, hipStream_t stream,
@@ -72,8 +76,8 @@ int gram_stream_launch_feat(int dtype, const void* k, const void* v, float* G, f
                             int64_t gl_sb, const FeatArgs& fa, hipStream_t stream,
                             const char* who);
 int query_stream_launch_feat(int dtype, const void* q, const float* U, float* Y, int nb, int T_R,
-                             int B, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
-                             const FeatArgs& fa, hipStream_t stream);
+                             int B, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                             int64_t y_st, const FeatArgs& fa, hipStream_t stream);
 int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v, const float* Y,
                          const float* gate, float* out, int nb, int T, int n, int C,
                          int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
@@ -108,9 +112,12 @@ static FwdLayout fwd_layout(int nb, int T, int n, int N0, int B, int n_P, int C,
   const int T_R = T - n;
   L.fused = (C <= 128) && !want_H;
   int64_t off = 0;
-  L.F = off;   off += al256((int64_t)nb * N0 * rp * 4);
+  // F and U rows are sized for the spread row stride, which the forward
+  // takes when the line-group or row-group incidence runs (rp otherwise).
+  const int64_t ld = incidence_spread_ld(rp);
+  L.F = off;   off += al256((int64_t)nb * N0 * ld * 4);
   L.Fg = off;  off += n_P > 0 ? al256((int64_t)nb * rp * 4) : 0;
-  L.U = off;   off += al256((int64_t)nb * B * rp * 4);
+  L.U = off;   off += al256((int64_t)nb * B * ld * 4);
   L.Y = off;   off += al256((int64_t)nb * T_R * y_stride(p) * 4);
   if (L.fused) {
     L.scan = off; off += al256(causal_scan_workspace_bytes(nb, T, C, r, p));
@@ -236,10 +243,12 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     // channel alone (or zero): the incidence runs with an empty row.
     const bool profiled = n > n_P;
     const char* phi_rec = (const char*)phi + (int64_t)n * q_st * elem_bytes(dtype);
+    // row stride of F and U
+    const int64_t ld = idx && plane_code && profiled ? incidence_plane_ld(q, N0, B, rp) : rp;
     {
       StageScope stage(0);
       rc = pool_dispatch(dtype, psi, vb, F, Fg, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st,
-                         part, part_bytes, st);
+                         part, part_bytes, st, ld);
     }
     if (rc) return rc;
     const float* Uq = U;
@@ -248,7 +257,7 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
       if (!idx)                                      // identity incidence: U = F
         Uq = F;
       else if (plane_code && profiled)
-        rc = incidence_plane_dispatch(F, Fg, plane_code, q, U, nb, N0, B, rp, st);
+        rc = incidence_plane_dispatch(F, Fg, plane_code, q, U, nb, N0, B, rp, ld, st);
       else
         rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
                                 profiled ? deg : 0, U, nb, N0, B, rp, st);
@@ -256,7 +265,7 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     if (rc) return rc;
     {
       StageScope stage(2);
-      rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, q_sb, q_st,
+      rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, ld, q_sb, q_st,
                           (int64_t)T_R * yst, yst, st);
     }
     if (rc) return rc;
@@ -410,6 +419,9 @@ extern "C" int smat_forward_fused(int dtype, const void* q, const void* k, const
 
   if (T_R > 0) {
     const bool profiled = n > n_P;
+    // row stride of F and U
+    const int64_t ld =
+        idx && plane_code && profiled ? incidence_plane_ld(field_q, N0, B, rp) : rp;
     GramItems it{};
     it.mode = 1;
     it.n_P = n_P;
@@ -420,7 +432,7 @@ extern "C" int smat_forward_fused(int dtype, const void* q, const void* k, const
     {
       StageScope stage(0);
       rc = gram_stream_launch_feat(dtype, k, v, F, Fg, it, N0 + (Fg ? 1 : 0), nb, k_sb, k_st,
-                                   v_sb, v_st, (int64_t)N0 * rp, rp, rp, fa, st,
+                                   v_sb, v_st, (int64_t)N0 * ld, ld, rp, fa, st,
                                    "smat_forward_fused");
     }
     if (rc) return rc;
@@ -430,7 +442,7 @@ extern "C" int smat_forward_fused(int dtype, const void* q, const void* k, const
       if (!idx)
         Uq = F;
       else if (plane_code && profiled)
-        rc = incidence_plane_dispatch(F, Fg, plane_code, field_q, U, nb, N0, B, rp, st);
+        rc = incidence_plane_dispatch(F, Fg, plane_code, field_q, U, nb, N0, B, rp, ld, st);
       else
         rc = incidence_dispatch(F, Fg, idx, idx_is_64, profiled ? indptr : nullptr,
                                 profiled ? deg : 0, U, nb, N0, B, rp, st);
@@ -445,10 +457,10 @@ extern "C" int smat_forward_fused(int dtype, const void* q, const void* k, const
                             nullptr, nb, T_R, 128, 128, 0, kind, q_sb, q_st, 0, 0, 0, 0, 0,
                             (int64_t)T_R * 128, 128, 0, 0, stream);
         if (rc == SMAT_OK)
-          rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, (int64_t)T_R * 128, 128,
-                              (int64_t)T_R * yst, yst, st);
+          rc = query_dispatch(dtype, phi_rec, Uq, Y, nb, T_R, B, r, p, ld, (int64_t)T_R * 128,
+                              128, (int64_t)T_R * yst, yst, st);
       } else {
-        rc = query_stream_launch_feat(dtype, q_rec, Uq, Y, nb, T_R, B, q_sb, q_st,
+        rc = query_stream_launch_feat(dtype, q_rec, Uq, Y, nb, T_R, B, ld, q_sb, q_st,
                                       (int64_t)T_R * yst, yst, fa, st);
       }
     }

@@ -494,9 +494,11 @@ int64_t pool_workspace_bytes(int nb, int n_P, int n, int N0, int r, int p, bool 
   return need;
 }
 
+// F: (nb, N0) rows of r * p floats, f_ld floats apart.
 int pool_dispatch(int dtype, const void* psi, const void* vb, float* F, float* F_glob, int nb,
                   int n_P, int n, int N0, int r, int p, int64_t k_sb, int64_t k_st, int64_t v_sb,
-                  int64_t v_st, float* partials, int64_t partial_bytes, hipStream_t stream) {
+                  int64_t v_st, float* partials, int64_t partial_bytes, hipStream_t stream,
+                  int64_t f_ld) {
   const bool glob = (F_glob != nullptr && n_P > 0);
   int64_t need = 0;
   GramItems it = pool_items(n_P, n, N0, glob, nb, r, p, &need);
@@ -507,7 +509,7 @@ int pool_dispatch(int dtype, const void* psi, const void* vb, float* F, float* F
   }
   const int64_t rp = (int64_t)r * p;
   return gram_dispatch(dtype, psi, vb, F, glob ? F_glob : nullptr, it, N0 + (glob ? 1 : 0), nb, r,
-                       p, k_sb, k_st, v_sb, v_st, (int64_t)N0 * rp, rp, rp, partials, stream,
+                       p, k_sb, k_st, v_sb, v_st, (int64_t)N0 * f_ld, f_ld, rp, partials, stream,
                        "smat_pool");
 }
 
@@ -586,7 +588,8 @@ extern "C" int smat_pool(int dtype, const void* psi, const void* vb, float* F, f
   SMAT_REQUIRE(workspace == nullptr || aligned16(workspace), SMAT_EINVAL,
                "smat_pool: workspace must be 16-byte aligned");
   return pool_dispatch(dtype, psi, vb, F, F_glob, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st,
-                       (float*)workspace, workspace ? workspace_bytes : 0, (hipStream_t)stream);
+                       (float*)workspace, workspace ? workspace_bytes : 0, (hipStream_t)stream,
+                       (int64_t)r * p);
 }
 
 extern "C" int smat_direct(int dtype, const void* psi, const void* vb, const int32_t* cols,

@@ -374,51 +374,66 @@ __device__ __forceinline__ void swap_halves(int& x, int& y) {
   y = (int)r[1];
 }
 
+// Where the row parts of the steps live.  Step t's row part is held by lane
+// t mod V of run t / V (of every sixteen-lane row), and a step broadcasts it
+// from there.  A direction's last group has only kTail live lines; its other
+// lanes are switched off while the lines are summed (no reads, no adds), so
+// the broadcasting lanes must be live ones: V = kTail where that costs at most
+// two more runs than V = 16 (the registers of the task state), else 16 and
+// the spare lanes run with the others (their sums are never stored).
+template <int Q>
+struct LgRuns {
+  static constexpr int kTail = Q % 16 ? Q % 16 : 16;
+  static constexpr bool kMask = (Q + kTail - 1) / kTail <= (Q + 15) / 16 + 2;
+  static constexpr int V = kMask ? kTail : 16;
+  static constexpr int NR = (Q + V - 1) / V;
+  // steps in flight: one fewer where the extra runs need the registers
+  static constexpr int D = NR > (Q + 15) / 16 ? 4 : Q >= 37 ? 5 : 6;
+};
+
 // Step N: both planes of the pair at the lane part plus the row part of step N.
-template <int N>
+template <int N, int V>
 __device__ __forceinline__ void lg_issue(float4* v, const char* vb, const int* ot) {
-  const char* a = vb + row_bcast<N % 16>(ot[N / 16]);
+  const char* a = vb + row_bcast<N % V>(ot[N / V]);
   v[0] = *reinterpret_cast<const float4*>(a);
   v[1] = *reinterpret_cast<const float4*>(a + iw::kPlaneBytes);
 }
 
-// Pair K of steps (2K, 2K + 1), into buffer K mod 3.
-template <int Q, int K>
-__device__ __forceinline__ void lg_issue_pair(float4 (&buf)[3][4], const char* vb, const int* ot) {
-  if constexpr (2 * K < Q) lg_issue<2 * K>(&buf[K % 3][0], vb, ot);
-  if constexpr (2 * K + 1 < Q) lg_issue<2 * K + 1>(&buf[K % 3][2], vb, ot);
-}
-
 // The sums so far are materialised here and no memory access moves across:
-// without it the compiler sinks every add below every read, and the Q pairs of
+// without it the compiler sinks every add below every read, and the Q steps of
 // reads in flight spill.
 __device__ __forceinline__ void lg_fence(float4& a0, float4& a1) {
   asm volatile("" : "+v"(a0.x), "+v"(a0.y), "+v"(a0.z), "+v"(a0.w), "+v"(a1.x), "+v"(a1.y),
                "+v"(a1.z), "+v"(a1.w)::"memory");
 }
 
-// Sum pair K (the compiler waits for its reads only), then issue pair K + 3
-// into the registers it frees; steps are summed in order 0 .. Q-1.
-template <int Q, int K>
-__device__ __forceinline__ void lg_pipe(float4& a0, float4& a1, float4 (&buf)[3][4],
+// Sum step N (the compiler waits for its reads only), then issue step N + D
+// into the registers it frees; steps are summed in order 0 .. Q-1 with D
+// steps' reads in flight.
+template <int Q, int D, int N>
+__device__ __forceinline__ void lg_pipe(float4& a0, float4& a1, float4 (&buf)[D][2],
                                         const char* vb, const int* ot) {
-  if constexpr (2 * K < Q) {
-    if constexpr (K == 0) {
+  if constexpr (N < Q) {
+    if constexpr (N == 0) {
       a0 = buf[0][0];
       a1 = buf[0][1];
     } else {
-      add4(a0, buf[K % 3][0]);
-      add4(a1, buf[K % 3][1]);
-    }
-    if constexpr (2 * K + 1 < Q) {
-      add4(a0, buf[K % 3][2]);
-      add4(a1, buf[K % 3][3]);
+      add4(a0, buf[N % D][0]);
+      add4(a1, buf[N % D][1]);
     }
     lg_fence(a0, a1);
     __builtin_amdgcn_sched_barrier(0);
-    lg_issue_pair<Q, K + 3>(buf, vb, ot);
+    if constexpr (N + D < Q) lg_issue<N + D, LgRuns<Q>::V>(buf[N % D], vb, ot);
     __builtin_amdgcn_sched_barrier(0);
-    lg_pipe<Q, K + 1>(a0, a1, buf, vb, ot);
+    lg_pipe<Q, D, N + 1>(a0, a1, buf, vb, ot);
+  }
+}
+
+template <int Q, int D, int N>
+__device__ __forceinline__ void lg_prologue(float4 (&buf)[D][2], const char* vb, const int* ot) {
+  if constexpr (N < D && N < Q) {
+    lg_issue<N, LgRuns<Q>::V>(buf[N], vb, ot);
+    lg_prologue<Q, D, N + 1>(buf, vb, ot);
   }
 }
 
@@ -426,12 +441,11 @@ __device__ __forceinline__ void lg_pipe(float4& a0, float4& a1, float4 (&buf)[3]
 template <int Q>
 __device__ __forceinline__ void lg_line_sums(float4& a0, float4& a1, const char* vb,
                                              const int* ot) {
-  float4 buf[3][4];
-  lg_issue_pair<Q, 0>(buf, vb, ot);
-  lg_issue_pair<Q, 1>(buf, vb, ot);
-  lg_issue_pair<Q, 2>(buf, vb, ot);
+  constexpr int D = LgRuns<Q>::D;
+  float4 buf[D][2];
+  lg_prologue<Q, D, 0>(buf, vb, ot);
   __builtin_amdgcn_sched_barrier(0);
-  lg_pipe<Q, 0>(a0, a1, buf, vb, ot);
+  lg_pipe<Q, D, 0>(a0, a1, buf, vb, ot);
 }
 
 // x / Q and x mod Q for x below Max by a multiply and a shift: M and S are the
@@ -472,7 +486,7 @@ template <int Q>
 struct LgGroup {
   static constexpr int P = (Q + 15) / 16;
   static constexpr int G = (Q + 1) * P;
-  int b0, s0, qm, d16, lcb, nvalid, sloped;
+  int b0, s0, qm, d16, dV, lcb, nvalid, sloped;
   __device__ __forceinline__ explicit LgGroup(int g) {
     const int dir = g / P;
     b0 = (g - dir * P) * 16;
@@ -480,6 +494,7 @@ struct LgGroup {
     s0 = sloped ? b0 : 0;
     qm = sloped ? Q - dir : 0;
     d16 = (16 * qm) % Q;
+    dV = (LgRuns<Q>::V * qm) % Q;
     lcb = sloped ? (dir + 1) * Q + b0 : b0;
     nvalid = g < G ? min(16, Q - b0) : 0;
   }
@@ -490,6 +505,7 @@ struct LgGroup {
     s0 = __builtin_amdgcn_readfirstlane(s0);
     qm = __builtin_amdgcn_readfirstlane(qm);
     d16 = __builtin_amdgcn_readfirstlane(d16);
+    dV = __builtin_amdgcn_readfirstlane(dV);
     lcb = __builtin_amdgcn_readfirstlane(lcb);
     nvalid = __builtin_amdgcn_readfirstlane(nvalid);
     sloped = __builtin_amdgcn_readfirstlane(sloped);
@@ -505,11 +521,13 @@ struct LgGroup {
 template <int Q>
 using LgSlot = LgDiv<Q, 16 * iw::kWaves * iw::kPF>;
 
-// Byte offsets into one sequence's F panel rows and U type rows are 32-bit.
-static bool wave_kernel_fits(int q, int N0, int B, int64_t rp) {
+// Byte offsets into one sequence's F panel rows and U type rows are 32-bit;
+// ld is their row stride in floats.
+static bool wave_kernel_fits(int q, int N0, int B, int64_t ld) {
   return q >= 2 && q <= iw::kQMax && N0 == q * q &&
          (int64_t)N0 * iw::kPlanes <= (int64_t)iw::kPF * iw::kThreads &&
-         (int64_t)N0 * rp < (1ll << 30) && (int64_t)B * rp < (1ll << 30);
+         (int64_t)N0 * ld < (1ll << 30) && (int64_t)B * ld < (1ll << 30) && ld < (1ll << 22) &&
+         B < 0xffff;
 }
 
 static int64_t wave_lds_bytes(int q) {
@@ -519,7 +537,7 @@ static int64_t wave_lds_bytes(int q) {
 template <int Q, bool HasG>
 __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
-    float* __restrict__ U, int B, int64_t rp, int nslices, int64_t total, int64_t per_xcd) {
+    float* __restrict__ U, int B, int64_t rp, int64_t ld, int nslices, int64_t total, int64_t per_xcd) {
   using namespace iw;
   constexpr int q = Q;
   constexpr int N0 = Q * Q;
@@ -527,7 +545,8 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   constexpr int P = (Q + kGroup - 1) / kGroup;       // groups per direction
   constexpr int G = (Q + 1) * P;                     // groups per item
   constexpr int NT = (G + 1) / 2;                    // wave tasks (two groups) per item
-  constexpr int NR = (Q + 15) / 16;                  // runs of sixteen steps
+  constexpr int V = LgRuns<Q>::V;                    // steps per run of row parts
+  constexpr int NR = LgRuns<Q>::NR;                  // runs
   extern __shared__ float4 smem[];
   short* line_type = reinterpret_cast<short*>(smem + (size_t)kPlanes * kPlane);
   const int tid = threadIdx.x;
@@ -551,17 +570,17 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   // than kept live: ps0 passes through an empty asm so it is not hoisted.
   const uint32_t ps0 = 16u * (uint32_t)(tid >> 6) + (uint32_t)(tid & 15);
   const int kx = (tid >> 4) & 3;
-  const uint32_t rp4 = (uint32_t)rp * 4u;
+  const uint32_t ld4 = (uint32_t)ld * 4u;   // bytes from one F or U row to the next
   float4 pf[kPF];
   uint32_t src[kPF];
   auto chunk_src = [&](uint32_t ps) {
     const uint32_t x1 = LgSlot<Q>::div(ps), x0 = ps - Q * x1;
-    return __umul24(x0 * Q + x1, rp4) + 16u * kx;   // 4 (x rp + 4 kx)
+    return __umul24(x0 * Q + x1, ld4) + 16u * kx;   // 4 (x ld + 4 kx)
   };
   auto prefetch = [&](int64_t item) {
     const int64_t bi = item / nslices;
     const int64_t e0 = (item - bi * nslices) * kE;
-    const char* Fb = reinterpret_cast<const char*>(F + bi * (int64_t)N0 * rp + e0);
+    const char* Fb = reinterpret_cast<const char*>(F + bi * (int64_t)N0 * ld + e0);
     const bool in = e0 + 4 * kx < rp;
 #pragma unroll
     for (int u = 0; u < kPF; ++u)
@@ -585,12 +604,13 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   // The lane state of each of the wave's tasks is the same for every item, so
   // it is worked out once: tasks wv, wv + 16, ... (kTasks at most); for each,
   // the lane part of the read address, the row parts ot[] of the q steps, and
-  // the byte offsets in an item's U rows of the two lines this lane stores
-  // after the half exchange (kNoLine: none).
+  // the type rows of the two lines this lane stores after the half exchange,
+  // 16 bits each (kNoLine: none).
   constexpr int kTasks = (NT + kWaves - 1) / kWaves;
-  constexpr uint32_t kNoLine = ~0u;
+  constexpr uint32_t kNoLine = 0xffffu;
   int tvb[kTasks], tot[kTasks][NR];
-  uint32_t tsA[kTasks], tsB[kTasks];
+  uint32_t tsAB[kTasks];
+  bool tlive[kTasks];                                // the lane sums a line of its group
   lds_barrier();                                     // line table complete
 #pragma unroll
   for (int k = 0; k < kTasks; ++k) {
@@ -603,14 +623,15 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     const int b0 = gsel ? gB.b0 : gA.b0;
     const int s0 = gsel ? gB.s0 : gA.s0;
     const int qm = gsel ? gB.qm : gA.qm;
-    const int d16 = gsel ? gB.d16 : gA.d16;
+    const int dV = gsel ? gB.dV : gA.dV;
     const int lcb = gsel ? gB.lcb : gA.lcb;
     const int nvalid = gsel ? gB.nvalid : gA.nvalid;
     const bool sloped = (gsel ? gB.sloped : gA.sloped) != 0;
     const bool valid = j < nvalid;
+    tlive[k] = valid || !LgRuns<Q>::kMask;
     // sloped: lane part 16 j; row part of step t = 16 (kCW t + s_t),
     //   s_t = (b0 - m t) mod q = (b0 + qm t) mod q, taken by lane l for
-    //   t = 16 run + l.
+    //   t = V run + l (lanes l >= V hold values no step reads).
     // vertical (and the dead group of an odd G, s0 = qm = 0): lane part
     //   16 (kCW col + j), row part of step t = 16 t, col clamped into the
     //   columns for lanes past q.
@@ -621,17 +642,14 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
       int s = (int)LgMod<Q>::mod((unsigned)s0 + __umul24(qm, j));
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        tot[k][r] = (sloped ? 256 * kCW * r + laneCW16 : 256 * r + lane16) + 16 * s;
-        const unsigned c = (unsigned)(s + d16);
+        tot[k][r] = (sloped ? 16 * kCW * V * r + laneCW16 : 16 * V * r + lane16) + 16 * s;
+        const unsigned c = (unsigned)(s + dV);
         s = (int)min(c, c - (unsigned)q);
       }
     }
     int hA = valid ? line_type[min(lcb + j, nlines - 1)] : -1, hB = hA;
     swap_halves(hA, hB);                             // the lines stored after the exchange
-    // a lane stores at byte h * 4 rp + 16 splane of its type row h (below 2^32:
-    // checked on the host)
-    tsA[k] = hA >= 0 ? (uint32_t)hA * rp4 + splane16 : kNoLine;
-    tsB[k] = hB >= 0 ? (uint32_t)hB * rp4 + splane16 : kNoLine;
+    tsAB[k] = (hA >= 0 ? (uint32_t)hA : kNoLine) | ((hB >= 0 ? (uint32_t)hB : kNoLine) << 16);
   }
 
   for (int64_t item = first; item < end; item += nk) {
@@ -648,7 +666,7 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
           for (int c = 0; c < (Q + 15 + Q - 1) / Q; ++c)
             if (x0 + c * Q < (uint32_t)(Q + 15)) e[c * Q] = pf[u];
         }
-        src[u] = __umul24(x0 * Q + x1, rp4) + 16u * kx;
+        src[u] = __umul24(x0 * Q + x1, ld4) + 16u * kx;
       }
     }
     lds_barrier();                                   // panel (and line table) complete
@@ -657,14 +675,16 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     if (item + nk < end) prefetch(item + nk);        // lands while this item is summed
     const bool live = e0 + 4 * splane < rp;          // rp % 4 == 0: whole planes
     // The U rows of this item start at Ubase; a lane stores at byte
-    // h * 4 rp + 16 splane of its type row h (below 2^32: checked on the host).
-    const char* Ubase = reinterpret_cast<const char*>(U + b * (int64_t)B * rp + e0);
+    // h * 4 ld + 16 splane of its type row h (below 2^32: checked on the host).
+    const char* Ubase = reinterpret_cast<const char*>(U + b * (int64_t)B * ld + e0);
 
 #pragma unroll
     for (int k = 0; k < kTasks; ++k) {
       if (wv + kWaves * k >= NT) continue;
       float4 a0, a1;
-      lg_line_sums<Q>(a0, a1, pbase + tvb[k], tot[k]);
+      // The lanes past a last group's lines are off while it is summed; the
+      // lanes the steps broadcast from (l < V) are live in every group.
+      if (tlive[k]) lg_line_sums<Q>(a0, a1, pbase + tvb[k], tot[k]);
       // Rows 0-3 hold planes (0, 1) and (2, 3) of group A, then of group B, in
       // (a0, a1).  One exchange of 32-lane halves leaves group A's four planes in
       // a0 and group B's in a1 (rows 0-3: planes 0, 2, 1, 3), so each store
@@ -679,8 +699,12 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
           add4(a0, g);
           add4(a1, g);
         }
-        if (tsA[k] != kNoLine) *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + tsA[k]) = a0;
-        if (tsB[k] != kNoLine) *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + tsB[k]) = a1;
+        // a lane stores at byte h * 4 ld + 16 splane of its type row h (below
+        // 2^32: checked on the host; h < 2^16 and 4 ld < 2^24)
+        const uint32_t hA = tsAB[k] & 0xffffu, hB = tsAB[k] >> 16;
+        char* Uw = const_cast<char*>(Ubase);
+        if (hA != kNoLine) *reinterpret_cast<float4*>(Uw + __umul24(hA, ld4) + splane16) = a0;
+        if (hB != kNoLine) *reinterpret_cast<float4*>(Uw + __umul24(hB, ld4) + splane16) = a1;
       }
     }
     lds_barrier();                                   // every wave is done with the panel
@@ -689,7 +713,7 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
 
 template <int Q>
 static int launch_wave_q(const float* F, const float* F_glob, const int* code, float* U, int nb,
-                         int B, int64_t rp, hipStream_t stream) {
+                         int B, int64_t rp, int64_t ld, hipStream_t stream) {
   using namespace iw;
   const int nslices = (int)((rp + kE - 1) / kE);
   const int64_t total = (int64_t)nb * nslices;
@@ -707,7 +731,7 @@ static int launch_wave_q(const float* F, const float* F_glob, const int* code, f
                               inc::kPlaneLdsBudget);
     attr_set[F_glob ? 1 : 0] = true;
   }
-  smat::launch(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp,
+  smat::launch(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp, ld,
                      nslices, total, per_xcd);
   return launch_status("smat_incidence_plane");
 }
@@ -715,12 +739,12 @@ static int launch_wave_q(const float* F, const float* F_glob, const int* code, f
 // The line-group kernel is compiled for the prime field sizes it holds
 // (q <= 41); returns SMAT_EUNSUPPORTED for any other q.
 static int launch_wave(const float* F, const float* F_glob, const int* code, int q, float* U,
-                       int nb, int N0, int B, int64_t rp, hipStream_t stream) {
+                       int nb, int N0, int B, int64_t rp, int64_t ld, hipStream_t stream) {
   (void)N0;
   switch (q) {
 #define SMAT_WAVE_Q(QV) \
   case QV:              \
-    return launch_wave_q<QV>(F, F_glob, code, U, nb, B, rp, stream);
+    return launch_wave_q<QV>(F, F_glob, code, U, nb, B, rp, ld, stream);
     SMAT_WAVE_Q(2) SMAT_WAVE_Q(3) SMAT_WAVE_Q(5) SMAT_WAVE_Q(7) SMAT_WAVE_Q(11)
     SMAT_WAVE_Q(13) SMAT_WAVE_Q(17) SMAT_WAVE_Q(19) SMAT_WAVE_Q(23) SMAT_WAVE_Q(29)
     SMAT_WAVE_Q(31) SMAT_WAVE_Q(37) SMAT_WAVE_Q(41)
@@ -825,16 +849,16 @@ __device__ __forceinline__ float4 lr_line_sum(const char* vb, const int* ot) {
 template <int Q>
 using LrSlot = LgDiv<Q, 64 * ir::kWaves * ir::kPF>;
 
-static bool row_kernel_fits(int q, int N0, int B, int64_t rp) {
+static bool row_kernel_fits(int q, int N0, int B, int64_t ld) {
   return q >= ir::kQMin && q <= ir::kQMax && N0 == q * q &&
-         (int64_t)N0 <= (int64_t)ir::kPF * ir::kThreads && (int64_t)N0 * rp < (1ll << 30) &&
-         (int64_t)B * rp < (1ll << 30);
+         (int64_t)N0 <= (int64_t)ir::kPF * ir::kThreads && (int64_t)N0 * ld < (1ll << 30) &&
+         (int64_t)B * ld < (1ll << 30);
 }
 
 template <int Q, bool HasG>
 __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
     const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
-    float* __restrict__ U, int B, int64_t rp, int nslices, int64_t total, int64_t per_xcd) {
+    float* __restrict__ U, int B, int64_t rp, int64_t ld, int nslices, int64_t total, int64_t per_xcd) {
   using namespace ir;
   typedef Shape<Q> Sh;
   constexpr int q = Q;
@@ -867,13 +891,13 @@ __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
   // Chunk u of this thread: slot ps0 + 1024 u, 16 bytes of one point; the map
   // is recomputed per item (ps0 passes through an empty asm).
   const uint32_t ps0 = (uint32_t)tid;
-  const uint32_t rp4 = (uint32_t)rp * 4u;
+  const uint32_t ld4 = (uint32_t)ld * 4u;   // bytes from one F or U row to the next
   float4 pf[kPF];
   uint32_t src[kPF];
   auto prefetch = [&](int64_t item) {
     const int64_t b = item / nslices;
     const int64_t e0 = (item - b * nslices) * kE;
-    const char* Fb = reinterpret_cast<const char*>(F + b * (int64_t)N0 * rp + e0);
+    const char* Fb = reinterpret_cast<const char*>(F + b * (int64_t)N0 * ld + e0);
 #pragma unroll
     for (int u = 0; u < kPF; ++u)
       pf[u] = ps0 + 1024u * u < (uint32_t)N0 ? *reinterpret_cast<const float4*>(Fb + src[u])
@@ -883,7 +907,7 @@ __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
   for (int u = 0; u < kPF; ++u) {
     const uint32_t ps = ps0 + 1024u * u;
     const uint32_t x1 = LrSlot<Q>::div(ps), x0 = ps - Q * x1;
-    src[u] = __umul24(x0 * Q + x1, rp4);             // 4 x rp, x = x0*q + x1
+    src[u] = __umul24(x0 * Q + x1, ld4);             // 4 x ld, x = x0*q + x1
   }
   prefetch(first);
 
@@ -906,7 +930,7 @@ __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
           for (int c = 0; c < (Q + 15 + Q - 1) / Q; ++c)
             if (x0 + c * Q < (uint32_t)(Q + 15)) e[c * Q] = pf[u];
         }
-        src[u] = __umul24(x0 * Q + x1, rp4);
+        src[u] = __umul24(x0 * Q + x1, ld4);
       }
     }
     lds_barrier();                                   // panel (and line table) complete
@@ -914,7 +938,7 @@ __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
     const int64_t e0 = (item - b * nslices) * kE;
     if (item + nk < end) prefetch(item + nk);        // lands while this item is summed
     const bool live = e0 < rp;                       // rp % 4 == 0: whole planes
-    const char* Ubase = reinterpret_cast<const char*>(U + b * (int64_t)B * rp + e0);
+    const char* Ubase = reinterpret_cast<const char*>(U + b * (int64_t)B * ld + e0);
     float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
     if (HasG && live) g = *reinterpret_cast<const float4*>(Fg + b * rp + e0);
 
@@ -938,7 +962,7 @@ __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
       const int h = valid ? line_type[min(gr.lcb + j, nlines - 1)] : -1;
       if (live && h >= 0) {
         if (HasG) add4(a, g);
-        *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + (uint32_t)h * rp4) = a;
+        *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + (uint32_t)h * ld4) = a;
       }
     }
     lds_barrier();                                   // every wave is done with the panel
@@ -947,7 +971,7 @@ __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
 
 template <int Q>
 static int launch_row_q(const float* F, const float* F_glob, const int* code, float* U, int nb,
-                        int B, int64_t rp, hipStream_t stream) {
+                        int B, int64_t rp, int64_t ld, hipStream_t stream) {
   using namespace ir;
   const int nslices = (int)((rp + kE - 1) / kE);
   const int64_t total = (int64_t)nb * nslices;
@@ -965,7 +989,7 @@ static int launch_row_q(const float* F, const float* F_glob, const int* code, fl
                               (int)smem);
     attr_set[F_glob ? 1 : 0] = true;
   }
-  smat::launch(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp,
+  smat::launch(kern, dim3(grid), dim3(kThreads), smem, stream, F, F_glob, code, U, B, rp, ld,
                      nslices, total, per_xcd);
   return launch_status("smat_incidence_plane");
 }
@@ -973,11 +997,11 @@ static int launch_row_q(const float* F, const float* F_glob, const int* code, fl
 // The row-group kernel is compiled for the primes 43 .. 83; returns
 // SMAT_EUNSUPPORTED for any other q.
 static int launch_row(const float* F, const float* F_glob, const int* code, int q, float* U,
-                      int nb, int B, int64_t rp, hipStream_t stream) {
+                      int nb, int B, int64_t rp, int64_t ld, hipStream_t stream) {
   switch (q) {
 #define SMAT_ROW_Q(QV) \
   case QV:             \
-    return launch_row_q<QV>(F, F_glob, code, U, nb, B, rp, stream);
+    return launch_row_q<QV>(F, F_glob, code, U, nb, B, rp, ld, stream);
     SMAT_ROW_Q(43) SMAT_ROW_Q(47) SMAT_ROW_Q(53) SMAT_ROW_Q(59) SMAT_ROW_Q(61) SMAT_ROW_Q(67)
     SMAT_ROW_Q(71) SMAT_ROW_Q(73) SMAT_ROW_Q(79) SMAT_ROW_Q(83)
 #undef SMAT_ROW_Q
@@ -1145,22 +1169,55 @@ int incidence_dispatch(const float* F, const float* F_glob, const void* idx, int
   return launch_status("smat_incidence");
 }
 
+// F and U rows of rp floats laid out ld floats apart with ld / 16 odd.  The
+// line-group and row-group kernels move each row in 64-byte pieces, and the
+// spacing of the pieces sets the rate HBM serves them at: at 8 sequences,
+// q = 41, the kernel takes 606-618 us with ld = rp = 16512 (1032 x 16), 545-560
+// us with ld = 16528, 16560, 16592, 16624 and 636-641 us with ld a multiple of
+// 128 floats (MI355X, measured).
+int64_t incidence_spread_ld(int64_t rp) {
+  int64_t ld = (rp + 15) / 16 * 16;
+  if ((ld / 16) % 2 == 0) ld += 16;
+  return ld;
+}
+
+static bool plane_groups_run(int q, int N0, int B, int64_t ld) {
+  if (variant(SMAT_VARIANT_INCIDENCE_PLANE) != 0) return false;
+  return (wave_kernel_fits(q, N0, B, ld) && wave_kernel_has_q(q)) ||
+         (row_kernel_fits(q, N0, B, ld) && row_kernel_has_q(q));
+}
+
+// The row stride a one-call forward lays F and U out with: the spread stride
+// when the line-group or row-group kernel runs the incidence, else rp.
+int64_t incidence_plane_ld(int q, int N0, int B, int64_t rp) {
+  const int64_t ld = incidence_spread_ld(rp);
+  return rp % 4 == 0 && plane_groups_run(q, N0, B, ld) ? ld : rp;
+}
+
+// F: (nb, N0) rows and U: (nb, B) rows of rp floats, ld floats apart; ld may
+// exceed rp only where the line-group or row-group kernel runs.
 int incidence_plane_dispatch(const float* F, const float* F_glob, const int* code, int q,
-                             float* U, int nb, int N0, int B, int64_t rp, hipStream_t stream) {
+                             float* U, int nb, int N0, int B, int64_t rp, int64_t ld,
+                             hipStream_t stream) {
   if (nb == 0 || B == 0 || rp == 0) return SMAT_OK;
-  const bool aligned = (rp % 4 == 0) && aligned16(F) && aligned16(U) &&
+  const bool aligned = (rp % 4 == 0) && (ld % 4 == 0) && aligned16(F) && aligned16(U) &&
                        (!F_glob || aligned16(F_glob));
-  if (!aligned || (int64_t)q * q != N0 || q > 181) {
-    set_error("smat_incidence_plane: needs rp %% 4 == 0, aligned tables and N0 = q^2 "
-              "(q=%d N0=%d rp=%lld)", q, N0, (long long)rp);
+  if (!aligned || (int64_t)q * q != N0 || q > 181 || ld < rp) {
+    set_error("smat_incidence_plane: needs rp %% 4 == 0, ld >= rp, aligned tables and N0 = q^2 "
+              "(q=%d N0=%d rp=%lld ld=%lld)", q, N0, (long long)rp, (long long)ld);
     return SMAT_EUNSUPPORTED;
   }
-  if (wave_kernel_fits(q, N0, B, rp) && wave_kernel_has_q(q) &&
+  if (wave_kernel_fits(q, N0, B, ld) && wave_kernel_has_q(q) &&
       variant(SMAT_VARIANT_INCIDENCE_PLANE) == 0)
-    return launch_wave(F, F_glob, code, q, U, nb, N0, B, rp, stream);
-  if (row_kernel_fits(q, N0, B, rp) && row_kernel_has_q(q) &&
+    return launch_wave(F, F_glob, code, q, U, nb, N0, B, rp, ld, stream);
+  if (row_kernel_fits(q, N0, B, ld) && row_kernel_has_q(q) &&
       variant(SMAT_VARIANT_INCIDENCE_PLANE) == 0)
-    return launch_row(F, F_glob, code, q, U, nb, B, rp, stream);
+    return launch_row(F, F_glob, code, q, U, nb, B, rp, ld, stream);
+  if (ld != rp) {
+    set_error("smat_incidence_plane: row stride %lld != %lld needs the line-group or row-group "
+              "kernel (q=%d)", (long long)ld, (long long)rp, q);
+    return SMAT_EUNSUPPORTED;
+  }
   // Two workgroups per CU at E = 8 (one stages its panel while the other sums)
   // measured ahead of one at E = 16; wider panels fall back to one per CU.
   const int64_t entries = (int64_t)q * (q + 15);
@@ -1198,5 +1255,6 @@ extern "C" int smat_incidence_plane(const float* F, const float* F_glob, const i
   SMAT_REQUIRE(F && code && U, SMAT_EINVAL, "smat_incidence_plane: null pointer");
   SMAT_REQUIRE(nb >= 0 && q >= 2 && B >= 0 && rp >= 0, SMAT_EINVAL,
                "smat_incidence_plane: bad sizes");
-  return incidence_plane_dispatch(F, F_glob, code, q, U, nb, N0, B, rp, (hipStream_t)stream);
+  return incidence_plane_dispatch(F, F_glob, code, q, U, nb, N0, B, rp, rp,
+                                  (hipStream_t)stream);
 }

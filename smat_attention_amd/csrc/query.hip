@@ -33,8 +33,8 @@ constexpr int kMT = kRowsPerWG / 16;
 template <typename In, int kRK, int kNCT, bool kLoop>
 __global__ __launch_bounds__(qy::kThreads) void query_kernel(
     const In* __restrict__ phi, const float* __restrict__ U, float* __restrict__ Y, int T_R, int B,
-    int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st, int nrb, int vec_q,
-    const int32_t* __restrict__ rows, const int64_t* __restrict__ roffs) {
+    int r, int p, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st, int nrb,
+    int vec_q, const int32_t* __restrict__ rows, const int64_t* __restrict__ roffs) {
   using namespace qy;
   typedef typename Traits<In>::frag Frag;
   constexpr int kCTPerWave = (kNCT + 3) / 4;
@@ -57,7 +57,7 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
     const int nmt = min(kMT, (cnt - k0 + 15) / 16);
 
     const In* phib = phi + b * q_sb;
-    const float* Uh = U + (b * B + h) * (int64_t)r * p;
+    const float* Uh = U + (b * B + h) * u_ld;
     // U's loads, their offsets and predicates do not depend on the row block.
     // In the walk they are computed from opaque copies, so they stay inside it
     // instead of being hoisted into registers for a second pass that only
@@ -184,12 +184,13 @@ constexpr int kUFloats = kULoads * 256;                   // 16640 (LDS image in
 template <typename In>
 __device__ __forceinline__ void query_issue(float* ubuf, uint4* pbuf, const float* U,
                                             const In* phi, int64_t item, int T_R, int B,
-                                            int64_t q_sb, int64_t q_st, int w, int lane) {
+                                            int64_t u_ld, int64_t q_sb, int64_t q_st, int w,
+                                            int lane) {
   using namespace qs;
   const int64_t b = item / B;
   const int h = (int)(item - b * B);
   const int cnt = (T_R - h + B - 1) / B;
-  const float* Uh = U + item * (int64_t)(kR * kP);
+  const float* Uh = U + item * u_ld;
   const In* phib = phi + b * q_sb;
 #pragma unroll
   for (int u = 0; u < (kLoads + kWaves - 1) / kWaves; ++u) {
@@ -222,7 +223,7 @@ __device__ __forceinline__ void query_issue(float* ubuf, uint4* pbuf, const floa
 template <typename In, bool FEAT>
 __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
     const In* __restrict__ phi, const float* __restrict__ U, float* __restrict__ Y, int T_R,
-    int B, int64_t nitems, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
+    int B, int64_t nitems, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
     FeatArgs fa) {
   using namespace qs;
   typedef typename Traits<In>::frag Frag;
@@ -233,7 +234,8 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
   const int64_t G = gridDim.x;
   int64_t item = blockIdx.x;
-  if (item < nitems) query_issue<In>(u0, p0, U, phi, item, T_R, B, q_sb, q_st, w, lane_id());
+  if (item < nitems)
+    query_issue<In>(u0, p0, U, phi, item, T_R, B, u_ld, q_sb, q_st, w, lane_id());
   Frag wa[4];
   if constexpr (FEAT) {
     if (w < 8) feat_w_load<In>(wa, (const In*)fa.W, w, lane_id());
@@ -248,7 +250,8 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
     const int r16 = lane & 15, g = lane >> 4;
     const int64_t next = item + G;
     if (next < nitems) {
-      query_issue<In>(BUF ? u0 : u1, BUF ? p0 : p1, U, phi, next, T_R, B, q_sb, q_st, w, lane);
+      query_issue<In>(BUF ? u0 : u1, BUF ? p0 : p1, U, phi, next, T_R, B, u_ld, q_sb, q_st, w,
+                      lane);
       if (w < kLoads % kWaves)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads / kWaves + 1) : "memory");
       else
@@ -324,8 +327,8 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
 
 template <typename In>
 static int launch_query(const void* phi, const float* U, float* Y, int nb, int T_R, int B, int r,
-                        int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
-                        hipStream_t stream);
+                        int p, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                        int64_t y_st, hipStream_t stream);
 
 static bool query_stream_ok(int dtype, const void* phi, const float* U, const float* Y, int T_R,
                             int B, int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb,
@@ -340,8 +343,8 @@ static bool query_stream_ok(int dtype, const void* phi, const float* U, const fl
 
 template <typename In>
 static int launch_query(const void* phi, const float* U, float* Y, int nb, int T_R, int B, int r,
-                        int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
-                        hipStream_t stream) {
+                        int p, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                        int64_t y_st, hipStream_t stream) {
   const int maxcnt = (T_R + B - 1) / B;
   const int nrb = (maxcnt + qy::kRowsPerWG - 1) / qy::kRowsPerWG;
   const int64_t gx = (int64_t)B * nrb;
@@ -352,16 +355,16 @@ static int launch_query(const void* phi, const float* U, float* Y, int nb, int T
   const int vq = rows_vec_ok(phi, q_sb, q_st, sizeof(In));
   if (r <= 64 && p <= 80)
     smat::launch((query_kernel<In, 2, 5, false>), dim3((unsigned)gx, (unsigned)nb),
-                       dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
-                       q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
+                       dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, u_ld,
+                       q_sb, q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   else if (r <= 96 && p <= 80)
     smat::launch((query_kernel<In, 3, 5, false>), dim3((unsigned)gx, (unsigned)nb),
-                       dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
-                       q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
+                       dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, u_ld,
+                       q_sb, q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   else
     smat::launch((query_kernel<In, 4, 9, false>), dim3((unsigned)gx, (unsigned)nb),
-                       dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, q_sb,
-                       q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
+                       dim3(qy::kThreads), 0, stream, (const In*)phi, U, Y, T_R, B, r, p, u_ld,
+                       q_sb, q_st, y_sb, y_st, nrb, vq, nullptr, nullptr);
   return launch_status("smat_query");
 }
 
@@ -380,23 +383,23 @@ static int launch_query_lists(const void* phi, const float* U, float* Y, const i
   const int vq = rows_vec_ok(phi, 0, q_st, sizeof(In));
   if (r <= 64 && p <= 80)
     smat::launch((query_kernel<In, 2, 5, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
-                       stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
-                       (int64_t)0, y_st, nrb, vq, rows, roffs);
+                       stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)r * p,
+                       (int64_t)0, q_st, (int64_t)0, y_st, nrb, vq, rows, roffs);
   else if (r <= 96 && p <= 80)
     smat::launch((query_kernel<In, 3, 5, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
-                       stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
-                       (int64_t)0, y_st, nrb, vq, rows, roffs);
+                       stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)r * p,
+                       (int64_t)0, q_st, (int64_t)0, y_st, nrb, vq, rows, roffs);
   else
     smat::launch((query_kernel<In, 4, 9, true>), dim3((unsigned)gx, 1u), dim3(qy::kThreads), 0,
-                       stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)0, q_st,
-                       (int64_t)0, y_st, nrb, vq, rows, roffs);
+                       stream, (const In*)phi, U, Y, 0, ntypes, r, p, (int64_t)r * p,
+                       (int64_t)0, q_st, (int64_t)0, y_st, nrb, vq, rows, roffs);
   return launch_status("smat_query_lists");
 }
 
 template <bool FEAT>
 static int query_stream_go(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R,
-                           int B, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
-                           const FeatArgs& fa, hipStream_t stream) {
+                           int B, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                           int64_t y_st, const FeatArgs& fa, hipStream_t stream) {
   int dev = 0, ncu = 256;
   (void)hipGetDevice(&dev);
   (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
@@ -404,42 +407,51 @@ static int query_stream_go(int dtype, const void* phi, const float* U, float* Y,
   const unsigned grid = (unsigned)std::min<int64_t>(nitems, (int64_t)ncu);
   if (dtype == SMAT_BF16)
     smat::launch((query_stream_kernel<bf16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
-                       stream, (const bf16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st, fa);
+                       stream, (const bf16*)phi, U, Y, T_R, B, nitems, u_ld, q_sb, q_st, y_sb,
+                       y_st, fa);
   else
     smat::launch((query_stream_kernel<f16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
-                       stream, (const f16*)phi, U, Y, T_R, B, nitems, q_sb, q_st, y_sb, y_st, fa);
+                       stream, (const f16*)phi, U, Y, T_R, B, nitems, u_ld, q_sb, q_st, y_sb,
+                       y_st, fa);
   return launch_status("smat_query");
 }
 
 static int launch_query_stream(int dtype, const void* phi, const float* U, float* Y, int nb,
-                               int T_R, int B, int64_t q_sb, int64_t q_st, int64_t y_sb,
-                               int64_t y_st, hipStream_t stream) {
-  return query_stream_go<false>(dtype, phi, U, Y, nb, T_R, B, q_sb, q_st, y_sb, y_st, FeatArgs{},
-                                stream);
+                               int T_R, int B, int64_t u_ld, int64_t q_sb, int64_t q_st,
+                               int64_t y_sb, int64_t y_st, hipStream_t stream) {
+  return query_stream_go<false>(dtype, phi, U, Y, nb, T_R, B, u_ld, q_sb, q_st, y_sb, y_st,
+                                FeatArgs{}, stream);
 }
 
 // The streaming query with the feature map in place: q holds Q rows of the
-// recent block (d_qk = 128), U fp32 (nb, B, 128, 129), at most 48 rows a type.
+// recent block (d_qk = 128), U fp32 (nb, B) rows of 128 x 129 floats, u_ld
+// floats apart, at most 48 rows a type.
 int query_stream_launch_feat(int dtype, const void* q, const float* U, float* Y, int nb, int T_R,
-                             int B, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
-                             const FeatArgs& fa, hipStream_t stream) {
+                             int B, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                             int64_t y_st, const FeatArgs& fa, hipStream_t stream) {
   if (nb == 0 || T_R == 0 || B == 0) return SMAT_OK;
-  return query_stream_go<true>(dtype, q, U, Y, nb, T_R, B, q_sb, q_st, y_sb, y_st, fa, stream);
+  return query_stream_go<true>(dtype, q, U, Y, nb, T_R, B, u_ld, q_sb, q_st, y_sb, y_st, fa,
+                               stream);
 }
 
+// U: (nb, B) rows of r * p floats, u_ld floats apart (u_ld % 4 == 0 for the
+// streaming kernel's 16-byte copies).
 int query_dispatch(int dtype, const void* phi, const float* U, float* Y, int nb, int T_R, int B,
-                   int r, int p, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
-                   hipStream_t stream) {
+                   int r, int p, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb,
+                   int64_t y_st, hipStream_t stream) {
   if (nb == 0 || T_R == 0 || B == 0) return SMAT_OK;
-  if (query_stream_ok(dtype, phi, U, Y, T_R, B, r, p, q_sb, q_st, y_sb, y_st))
-    return launch_query_stream(dtype, phi, U, Y, nb, T_R, B, q_sb, q_st, y_sb, y_st, stream);
+  if (u_ld % 4 == 0 && query_stream_ok(dtype, phi, U, Y, T_R, B, r, p, q_sb, q_st, y_sb, y_st))
+    return launch_query_stream(dtype, phi, U, Y, nb, T_R, B, u_ld, q_sb, q_st, y_sb, y_st,
+                               stream);
   switch (dtype) {
     case SMAT_BF16:
-      return launch_query<bf16>(phi, U, Y, nb, T_R, B, r, p, q_sb, q_st, y_sb, y_st, stream);
+      return launch_query<bf16>(phi, U, Y, nb, T_R, B, r, p, u_ld, q_sb, q_st, y_sb, y_st,
+                                stream);
     case SMAT_F16:
-      return launch_query<f16>(phi, U, Y, nb, T_R, B, r, p, q_sb, q_st, y_sb, y_st, stream);
+      return launch_query<f16>(phi, U, Y, nb, T_R, B, r, p, u_ld, q_sb, q_st, y_sb, y_st, stream);
     case SMAT_F32:
-      return launch_query<float>(phi, U, Y, nb, T_R, B, r, p, q_sb, q_st, y_sb, y_st, stream);
+      return launch_query<float>(phi, U, Y, nb, T_R, B, r, p, u_ld, q_sb, q_st, y_sb, y_st,
+                                 stream);
   }
   set_error("smat_query: unknown dtype %d", dtype);
   return SMAT_EINVAL;
@@ -457,8 +469,8 @@ extern "C" int smat_query(int dtype, const void* phi_rec, const float* U, float*
   SMAT_REQUIRE(r >= 1 && r <= kMaxR && p >= 1 && p <= kMaxP, SMAT_EUNSUPPORTED,
                "smat_query: r=%d p=%d beyond r<=%d, p<=%d", r, p, kMaxR, kMaxP);
   SMAT_REQUIRE(q_st >= r && y_st >= p, SMAT_EINVAL, "smat_query: row stride too short");
-  return query_dispatch(dtype, phi_rec, U, Y, nb, T_R, B, r, p, q_sb, q_st, y_sb, y_st,
-                        (hipStream_t)stream);
+  return query_dispatch(dtype, phi_rec, U, Y, nb, T_R, B, r, p, (int64_t)r * p, q_sb, q_st, y_sb,
+                        y_st, (hipStream_t)stream);
 }
 
 extern "C" int smat_query_lists(int dtype, const void* phi, const float* U, float* Y,
