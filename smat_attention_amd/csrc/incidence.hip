@@ -374,66 +374,51 @@ __device__ __forceinline__ void swap_halves(int& x, int& y) {
   y = (int)r[1];
 }
 
-// Where the row parts of the steps live.  Step t's row part is held by lane
-// t mod V of run t / V (of every sixteen-lane row), and a step broadcasts it
-// from there.  A direction's last group has only kTail live lines; its other
-// lanes are switched off while the lines are summed (no reads, no adds), so
-// the broadcasting lanes must be live ones: V = kTail where that costs at most
-// two more runs than V = 16 (the registers of the task state), else 16 and
-// the spare lanes run with the others (their sums are never stored).
-template <int Q>
-struct LgRuns {
-  static constexpr int kTail = Q % 16 ? Q % 16 : 16;
-  static constexpr bool kMask = (Q + kTail - 1) / kTail <= (Q + 15) / 16 + 2;
-  static constexpr int V = kMask ? kTail : 16;
-  static constexpr int NR = (Q + V - 1) / V;
-  // steps in flight: one fewer where the extra runs need the registers
-  static constexpr int D = NR > (Q + 15) / 16 ? 4 : Q >= 37 ? 5 : 6;
-};
-
 // Step N: both planes of the pair at the lane part plus the row part of step N.
-template <int N, int V>
+template <int N>
 __device__ __forceinline__ void lg_issue(float4* v, const char* vb, const int* ot) {
-  const char* a = vb + row_bcast<N % V>(ot[N / V]);
+  const char* a = vb + row_bcast<N % 16>(ot[N / 16]);
   v[0] = *reinterpret_cast<const float4*>(a);
   v[1] = *reinterpret_cast<const float4*>(a + iw::kPlaneBytes);
 }
 
+// Pair K of steps (2K, 2K + 1), into buffer K mod 3.
+template <int Q, int K>
+__device__ __forceinline__ void lg_issue_pair(float4 (&buf)[3][4], const char* vb, const int* ot) {
+  if constexpr (2 * K < Q) lg_issue<2 * K>(&buf[K % 3][0], vb, ot);
+  if constexpr (2 * K + 1 < Q) lg_issue<2 * K + 1>(&buf[K % 3][2], vb, ot);
+}
+
 // The sums so far are materialised here and no memory access moves across:
-// without it the compiler sinks every add below every read, and the Q steps of
+// without it the compiler sinks every add below every read, and the Q pairs of
 // reads in flight spill.
 __device__ __forceinline__ void lg_fence(float4& a0, float4& a1) {
   asm volatile("" : "+v"(a0.x), "+v"(a0.y), "+v"(a0.z), "+v"(a0.w), "+v"(a1.x), "+v"(a1.y),
                "+v"(a1.z), "+v"(a1.w)::"memory");
 }
 
-// Sum step N (the compiler waits for its reads only), then issue step N + D
-// into the registers it frees; steps are summed in order 0 .. Q-1 with D
-// steps' reads in flight.
-template <int Q, int D, int N>
-__device__ __forceinline__ void lg_pipe(float4& a0, float4& a1, float4 (&buf)[D][2],
+// Sum pair K (the compiler waits for its reads only), then issue pair K + 3
+// into the registers it frees; steps are summed in order 0 .. Q-1.
+template <int Q, int K>
+__device__ __forceinline__ void lg_pipe(float4& a0, float4& a1, float4 (&buf)[3][4],
                                         const char* vb, const int* ot) {
-  if constexpr (N < Q) {
-    if constexpr (N == 0) {
+  if constexpr (2 * K < Q) {
+    if constexpr (K == 0) {
       a0 = buf[0][0];
       a1 = buf[0][1];
     } else {
-      add4(a0, buf[N % D][0]);
-      add4(a1, buf[N % D][1]);
+      add4(a0, buf[K % 3][0]);
+      add4(a1, buf[K % 3][1]);
+    }
+    if constexpr (2 * K + 1 < Q) {
+      add4(a0, buf[K % 3][2]);
+      add4(a1, buf[K % 3][3]);
     }
     lg_fence(a0, a1);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (N + D < Q) lg_issue<N + D, LgRuns<Q>::V>(buf[N % D], vb, ot);
+    lg_issue_pair<Q, K + 3>(buf, vb, ot);
     __builtin_amdgcn_sched_barrier(0);
-    lg_pipe<Q, D, N + 1>(a0, a1, buf, vb, ot);
-  }
-}
-
-template <int Q, int D, int N>
-__device__ __forceinline__ void lg_prologue(float4 (&buf)[D][2], const char* vb, const int* ot) {
-  if constexpr (N < D && N < Q) {
-    lg_issue<N, LgRuns<Q>::V>(buf[N], vb, ot);
-    lg_prologue<Q, D, N + 1>(buf, vb, ot);
+    lg_pipe<Q, K + 1>(a0, a1, buf, vb, ot);
   }
 }
 
@@ -441,11 +426,12 @@ __device__ __forceinline__ void lg_prologue(float4 (&buf)[D][2], const char* vb,
 template <int Q>
 __device__ __forceinline__ void lg_line_sums(float4& a0, float4& a1, const char* vb,
                                              const int* ot) {
-  constexpr int D = LgRuns<Q>::D;
-  float4 buf[D][2];
-  lg_prologue<Q, D, 0>(buf, vb, ot);
+  float4 buf[3][4];
+  lg_issue_pair<Q, 0>(buf, vb, ot);
+  lg_issue_pair<Q, 1>(buf, vb, ot);
+  lg_issue_pair<Q, 2>(buf, vb, ot);
   __builtin_amdgcn_sched_barrier(0);
-  lg_pipe<Q, D, 0>(a0, a1, buf, vb, ot);
+  lg_pipe<Q, 0>(a0, a1, buf, vb, ot);
 }
 
 // x / Q and x mod Q for x below Max by a multiply and a shift: M and S are the
@@ -486,7 +472,7 @@ template <int Q>
 struct LgGroup {
   static constexpr int P = (Q + 15) / 16;
   static constexpr int G = (Q + 1) * P;
-  int b0, s0, qm, d16, dV, lcb, nvalid, sloped;
+  int b0, s0, qm, d16, lcb, nvalid, sloped;
   __device__ __forceinline__ explicit LgGroup(int g) {
     const int dir = g / P;
     b0 = (g - dir * P) * 16;
@@ -494,7 +480,6 @@ struct LgGroup {
     s0 = sloped ? b0 : 0;
     qm = sloped ? Q - dir : 0;
     d16 = (16 * qm) % Q;
-    dV = (LgRuns<Q>::V * qm) % Q;
     lcb = sloped ? (dir + 1) * Q + b0 : b0;
     nvalid = g < G ? min(16, Q - b0) : 0;
   }
@@ -505,7 +490,6 @@ struct LgGroup {
     s0 = __builtin_amdgcn_readfirstlane(s0);
     qm = __builtin_amdgcn_readfirstlane(qm);
     d16 = __builtin_amdgcn_readfirstlane(d16);
-    dV = __builtin_amdgcn_readfirstlane(dV);
     lcb = __builtin_amdgcn_readfirstlane(lcb);
     nvalid = __builtin_amdgcn_readfirstlane(nvalid);
     sloped = __builtin_amdgcn_readfirstlane(sloped);
@@ -526,8 +510,7 @@ using LgSlot = LgDiv<Q, 16 * iw::kWaves * iw::kPF>;
 static bool wave_kernel_fits(int q, int N0, int B, int64_t ld) {
   return q >= 2 && q <= iw::kQMax && N0 == q * q &&
          (int64_t)N0 * iw::kPlanes <= (int64_t)iw::kPF * iw::kThreads &&
-         (int64_t)N0 * ld < (1ll << 30) && (int64_t)B * ld < (1ll << 30) && ld < (1ll << 22) &&
-         B < 0xffff;
+         (int64_t)N0 * ld < (1ll << 30) && (int64_t)B * ld < (1ll << 30);
 }
 
 static int64_t wave_lds_bytes(int q) {
@@ -537,7 +520,8 @@ static int64_t wave_lds_bytes(int q) {
 template <int Q, bool HasG>
 __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
-    float* __restrict__ U, int B, int64_t rp, int64_t ld, int nslices, int64_t total, int64_t per_xcd) {
+    float* __restrict__ U, int B, int64_t rp, int64_t ld, int nslices, int64_t total,
+    int64_t per_xcd) {
   using namespace iw;
   constexpr int q = Q;
   constexpr int N0 = Q * Q;
@@ -545,8 +529,7 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   constexpr int P = (Q + kGroup - 1) / kGroup;       // groups per direction
   constexpr int G = (Q + 1) * P;                     // groups per item
   constexpr int NT = (G + 1) / 2;                    // wave tasks (two groups) per item
-  constexpr int V = LgRuns<Q>::V;                    // steps per run of row parts
-  constexpr int NR = LgRuns<Q>::NR;                  // runs
+  constexpr int NR = (Q + 15) / 16;                  // runs of sixteen steps
   extern __shared__ float4 smem[];
   short* line_type = reinterpret_cast<short*>(smem + (size_t)kPlanes * kPlane);
   const int tid = threadIdx.x;
@@ -604,13 +587,12 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   // The lane state of each of the wave's tasks is the same for every item, so
   // it is worked out once: tasks wv, wv + 16, ... (kTasks at most); for each,
   // the lane part of the read address, the row parts ot[] of the q steps, and
-  // the type rows of the two lines this lane stores after the half exchange,
-  // 16 bits each (kNoLine: none).
+  // the byte offsets in an item's U rows of the two lines this lane stores
+  // after the half exchange (kNoLine: none).
   constexpr int kTasks = (NT + kWaves - 1) / kWaves;
-  constexpr uint32_t kNoLine = 0xffffu;
+  constexpr uint32_t kNoLine = ~0u;
   int tvb[kTasks], tot[kTasks][NR];
-  uint32_t tsAB[kTasks];
-  bool tlive[kTasks];                                // the lane sums a line of its group
+  uint32_t tsA[kTasks], tsB[kTasks];
   lds_barrier();                                     // line table complete
 #pragma unroll
   for (int k = 0; k < kTasks; ++k) {
@@ -623,15 +605,14 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     const int b0 = gsel ? gB.b0 : gA.b0;
     const int s0 = gsel ? gB.s0 : gA.s0;
     const int qm = gsel ? gB.qm : gA.qm;
-    const int dV = gsel ? gB.dV : gA.dV;
+    const int d16 = gsel ? gB.d16 : gA.d16;
     const int lcb = gsel ? gB.lcb : gA.lcb;
     const int nvalid = gsel ? gB.nvalid : gA.nvalid;
     const bool sloped = (gsel ? gB.sloped : gA.sloped) != 0;
     const bool valid = j < nvalid;
-    tlive[k] = valid || !LgRuns<Q>::kMask;
     // sloped: lane part 16 j; row part of step t = 16 (kCW t + s_t),
     //   s_t = (b0 - m t) mod q = (b0 + qm t) mod q, taken by lane l for
-    //   t = V run + l (lanes l >= V hold values no step reads).
+    //   t = 16 run + l.
     // vertical (and the dead group of an odd G, s0 = qm = 0): lane part
     //   16 (kCW col + j), row part of step t = 16 t, col clamped into the
     //   columns for lanes past q.
@@ -642,14 +623,17 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
       int s = (int)LgMod<Q>::mod((unsigned)s0 + __umul24(qm, j));
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        tot[k][r] = (sloped ? 16 * kCW * V * r + laneCW16 : 16 * V * r + lane16) + 16 * s;
-        const unsigned c = (unsigned)(s + dV);
+        tot[k][r] = (sloped ? 256 * kCW * r + laneCW16 : 256 * r + lane16) + 16 * s;
+        const unsigned c = (unsigned)(s + d16);
         s = (int)min(c, c - (unsigned)q);
       }
     }
     int hA = valid ? line_type[min(lcb + j, nlines - 1)] : -1, hB = hA;
     swap_halves(hA, hB);                             // the lines stored after the exchange
-    tsAB[k] = (hA >= 0 ? (uint32_t)hA : kNoLine) | ((hB >= 0 ? (uint32_t)hB : kNoLine) << 16);
+    // a lane stores at byte h * 4 ld + 16 splane of its type row h (below 2^32:
+    // checked on the host)
+    tsA[k] = hA >= 0 ? (uint32_t)hA * ld4 + splane16 : kNoLine;
+    tsB[k] = hB >= 0 ? (uint32_t)hB * ld4 + splane16 : kNoLine;
   }
 
   for (int64_t item = first; item < end; item += nk) {
@@ -682,9 +666,7 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     for (int k = 0; k < kTasks; ++k) {
       if (wv + kWaves * k >= NT) continue;
       float4 a0, a1;
-      // The lanes past a last group's lines are off while it is summed; the
-      // lanes the steps broadcast from (l < V) are live in every group.
-      if (tlive[k]) lg_line_sums<Q>(a0, a1, pbase + tvb[k], tot[k]);
+      lg_line_sums<Q>(a0, a1, pbase + tvb[k], tot[k]);
       // Rows 0-3 hold planes (0, 1) and (2, 3) of group A, then of group B, in
       // (a0, a1).  One exchange of 32-lane halves leaves group A's four planes in
       // a0 and group B's in a1 (rows 0-3: planes 0, 2, 1, 3), so each store
@@ -699,12 +681,8 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
           add4(a0, g);
           add4(a1, g);
         }
-        // a lane stores at byte h * 4 ld + 16 splane of its type row h (below
-        // 2^32: checked on the host; h < 2^16 and 4 ld < 2^24)
-        const uint32_t hA = tsAB[k] & 0xffffu, hB = tsAB[k] >> 16;
-        char* Uw = const_cast<char*>(Ubase);
-        if (hA != kNoLine) *reinterpret_cast<float4*>(Uw + __umul24(hA, ld4) + splane16) = a0;
-        if (hB != kNoLine) *reinterpret_cast<float4*>(Uw + __umul24(hB, ld4) + splane16) = a1;
+        if (tsA[k] != kNoLine) *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + tsA[k]) = a0;
+        if (tsB[k] != kNoLine) *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + tsB[k]) = a1;
       }
     }
     lds_barrier();                                   // every wave is done with the panel
@@ -858,7 +836,8 @@ static bool row_kernel_fits(int q, int N0, int B, int64_t ld) {
 template <int Q, bool HasG>
 __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
     const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
-    float* __restrict__ U, int B, int64_t rp, int64_t ld, int nslices, int64_t total, int64_t per_xcd) {
+    float* __restrict__ U, int B, int64_t rp, int64_t ld, int nslices, int64_t total,
+    int64_t per_xcd) {
   using namespace ir;
   typedef Shape<Q> Sh;
   constexpr int q = Q;

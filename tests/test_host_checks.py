@@ -209,19 +209,8 @@ def _wave_staging(q):
     return panel
 
 
-def _runs(q):
-    """LgRuns<q>: (mask, V, NR) -- step t's row part is lane t % V of run t // V;
-    a last group's spare lanes are off (mask) when that costs at most two runs
-    more than V = 16."""
-    tail = q % 16 or 16
-    mask = (q + tail - 1) // tail <= (q + 15) // 16 + 2
-    V = tail if mask else 16
-    return mask, V, (q + V - 1) // V
-
-
-def _group(q, g, V=16):
-    """LgGroup<q>(g): (b0, s0, qm, (V qm) mod q, lcb, nvalid, sloped); the
-    line-group kernel steps s by V qm (dV), the row-group kernel by 16 qm (d16)."""
+def _group(q, g):
+    """LgGroup<q>(g): (b0, s0, qm, d16, lcb, nvalid, sloped)."""
     P = (q + 15) // 16
     G = (q + 1) * P
     d = g // P
@@ -229,7 +218,7 @@ def _group(q, g, V=16):
     sloped = d < q
     s0 = b0 if sloped else 0
     qm = q - d if sloped else 0
-    return b0, s0, qm, (V * qm) % q, ((d + 1) * q + b0) if sloped else b0, \
+    return b0, s0, qm, (16 * qm) % q, ((d + 1) * q + b0) if sloped else b0, \
         (min(16, q - b0) if g < G else 0), sloped
 
 
@@ -237,41 +226,36 @@ def _wave_reads(q):
     """Yield (group, lane j, plane, pp, step, entry, line code) for every read the
     kernel makes, by its own arithmetic: rows 0, 1 of a wave task take group
     2 task (plane pairs (0, 1), (2, 3)), rows 2, 3 group 2 task + 1; a row's lane
-    l computes ot[run] for step V run + l, and step t takes lane t % V's value
-    of its own row.  Lanes switched off (past a last group's lines, when the
-    kernel masks them) read nothing, and no live lane takes a row part from a
-    lane that is off."""
+    l computes ot[run] for step 16 run + l, and step t takes lane t % 16's value
+    of its own row."""
     P = (q + 15) // 16
     G = (q + 1) * P
     NT = (G + 1) // 2
-    mask, V, NR = _runs(q)
+    NR = (q + 15) // 16
     M, S = _lgdiv(q, 16 * P + 16 * q)
     for task in range(NT):
         for gsel in range(2):
             grp = 2 * task + gsel
-            b0, s0, qm, dV, lcb, nvalid, sloped = _group(q, grp, V)
+            b0, s0, qm, d16, lcb, nvalid, sloped = _group(q, grp)
             ot = {}
             for l in range(16):
                 x = s0 + qm * l
                 s = x - q * ((x * M) >> S)
                 assert s == x % q
                 for r in range(NR):
-                    ot[r, l] = (16 * _KCW * V * r + 16 * _KCW * l if sloped
-                                else 16 * V * r + 16 * l) + 16 * s
-                    c = (s + dV) % _U32
+                    ot[r, l] = (256 * _KCW * r + 16 * _KCW * l if sloped else 256 * r + 16 * l) \
+                        + 16 * s
+                    c = (s + d16) % _U32
                     s = min(c, (c - q) % _U32)
             for pp in range(2):
                 for j in range(16):
                     valid = j < nvalid
-                    if mask and not valid:
-                        continue                 # off while the group is summed
                     bl = b0 + j
                     col = bl if valid else (bl - 16 if bl >= 16 else 0)
                     vb = 16 * 2 * pp * _KPLANE + 16 * j + (0 if sloped else 16 * _KCW * col)
                     lc = min(lcb + j, q * (q + 1) - 1)
                     for t in range(q):
-                        assert not mask or t % V < nvalid   # the broadcasting lane is live
-                        addr = vb + ot[t // V, t % V]
+                        addr = vb + ot[t // 16, t % 16]
                         assert addr % 16 == 0
                         for half in range(2):
                             yield (grp, j, 2 * pp + half, pp, t,
@@ -300,7 +284,7 @@ def test_line_group_incidence_reads_each_line_once_in_bounds(q):
         for j in range(16):
             b = part * 16 + j
             if b >= q:
-                assert codes.get((grp, j)) is None
+                assert codes[grp, j] is None
                 continue
             if dirn < q:
                 want = sorted(((b - dirn * t) % q) * q + t for t in range(q))
@@ -322,12 +306,9 @@ def test_line_group_incidence_rows_read_one_bank_phase_each(q):
     for grp, j, plane, pp, t, e, lc in _wave_reads(q):
         rows.setdefault((grp, plane - 2 * pp, pp, t), {})[j] = e
     for (grp, half, pp, t), lanes in rows.items():
-        phases = [e % 16 for e in lanes.values()]
-        assert len(set(phases)) == len(phases)
-        assert len(lanes) == 16 or (len(lanes) == q % 16 and _runs(q)[0])
+        assert sorted(e % 16 for e in lanes.values()) == list(range(16))
         other = rows[grp, half, 1 - pp, t]
-        assert lanes.keys() == other.keys()
-        assert all((lanes[j] - other[j]) % 16 == 0 for j in lanes)
+        assert all((lanes[j] - other[j]) % 16 == 0 for j in range(16))
 
 
 def test_line_group_incidence_half_exchange_stores_whole_lines():
