@@ -451,12 +451,12 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     }
 
     // (a) this wave's share of the causal score tiles A^T = Psi Phi^T
-    //     entries 0..9: (ut, tt) with ut <= tt; 10, 11: zero tiles (1,0), (3,2)
-#pragma unroll
-    for (int rep = 0; rep < 2; ++rep) {
-      const int e = w + 8 * rep;
-      if (e < 12) {
-        int ut, tt;
+    //     entries 0..9: (ut, tt) with ut <= tt; 10, 11: zero tiles (1,0), (3,2).
+    //     Wave w takes entry w and, for w < 4, entry w + 8: waves 0, 1 two
+    //     products, whose fragments are all read first and whose MFMA chains
+    //     interleave; waves 2, 3 a product and a zero tile.
+    {
+      auto entry = [](int e, int& ut, int& tt) {
         if (e < 10) {
           tt = e < 1 ? 0 : e < 3 ? 1 : e < 6 ? 2 : 3;
           ut = e - (tt * (tt + 1)) / 2;
@@ -464,14 +464,10 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
           ut = e == 10 ? 1 : 3;
           tt = e == 10 ? 0 : 2;
         }
-        f32x4 acc = zero4();
-        if (e < 10) {
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk)
-            acc = mma(acc, row_chunk<In>(tpsi, 16 * ut + r16, 4 * kk + g),
-                      row_chunk<In>(tphi, 16 * tt + r16, 4 * kk + g));
-        }
-        // acc[i] = A^T[t' = 16ut + 4g + i][t = 16tt + r16] = A[t][t']
+      };
+      // acc[i] = A^T[t' = 16ut + 4g + i][t = 16tt + r16] = A[t][t'], masked,
+      // rounded to the input type and stored to the share
+      auto put = [&](const f32x4& acc, int ut, int tt) {
         Half hv;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -482,7 +478,37 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
         const int k = 2 * ut + (g >> 1);
         char* p = reinterpret_cast<char*>(share + t * 8 + (k ^ swz8(t))) + 8 * (g & 1);
         *reinterpret_cast<Half*>(p) = hv;
+      };
+      int ut0, tt0, ut1, tt1;
+      entry(w, ut0, tt0);
+      entry(w + 8, ut1, tt1);
+      Frag fa0[4], fb0[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        fa0[kk] = row_chunk<In>(tpsi, 16 * ut0 + r16, 4 * kk + g);
+        fb0[kk] = row_chunk<In>(tphi, 16 * tt0 + r16, 4 * kk + g);
       }
+      f32x4 acc0 = zero4();
+      if (w < 2) {
+        Frag fa1[4], fb1[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          fa1[kk] = row_chunk<In>(tpsi, 16 * ut1 + r16, 4 * kk + g);
+          fb1[kk] = row_chunk<In>(tphi, 16 * tt1 + r16, 4 * kk + g);
+        }
+        f32x4 acc1 = zero4();
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          acc0 = mma(acc0, fa0[kk], fb0[kk]);
+          acc1 = mma(acc1, fa1[kk], fb1[kk]);
+        }
+        put(acc1, ut1, tt1);
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) acc0 = mma(acc0, fa0[kk], fb0[kk]);
+        if (w < 4) put(zero4(), ut1, tt1);
+      }
+      put(acc0, ut0, tt0);
     }
 
     // Three buffers: step s + 2's rows go to the buffer step s - 1 used, free
@@ -517,68 +543,93 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     auto phi_half = [&](int tt, int k) {
       return *reinterpret_cast<const Half*>(prow[tt] + ((k ^ sw) * 16 + 8 * (g & 1)));
     };
+    // The Phi fragments of k-block kk + 1 are read while block kk's state is
+    // split and multiplied, and the hi parts of the four row tiles go before
+    // the lo parts, so no MFMA waits on the one before it.
+    Frag bfs[2][4];
+    auto read_bf = [&](Frag(&dst)[4], int kk) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+        dst[tt] = join<In>(phi_half(tt, 4 * kk + (g >> 1)), phi_half(tt, 4 * kk + 2 + (g >> 1)));
+    };
+    read_bf(bfs[0], 0);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
+      if (kk + 1 < 4) read_bf(bfs[(kk + 1) & 1], kk + 1);
       Half h0, l0, h1, l1;
       split4<In>(accS[2 * kk], h0, l0);
       split4<In>(accS[2 * kk + 1], h1, l1);
       const Frag shi = join<In>(h0, h1), slo = join<In>(l0, l1);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const Frag bf = join<In>(phi_half(tt, 4 * kk + (g >> 1)), phi_half(tt, 4 * kk + 2 + (g >> 1)));
-        accO[tt] = mma(accO[tt], shi, bf);
-        accO[tt] = mma(accO[tt], slo, bf);
-      }
+      for (int tt = 0; tt < 4; ++tt) accO[tt] = mma(accO[tt], shi, bfs[kk & 1][tt]);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) accO[tt] = mma(accO[tt], slo, bfs[kk & 1][tt]);
     }
     float own = 0.f;                       // wave w < 4: its row tile's value, finished in (d)
     {
-      Half s8hi, s8lo;
-      split4<In>(accS8, s8hi, s8lo);
+      Half s8hi, s8lo, bfn[4];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const int t = 16 * tt + r16;
-        const Half bf = phi_half(tt, 2 * w + (g >> 1));
-        f32x4 pn = mma16(zero4(), s8hi, bf);
-        pn = mma16(pn, s8lo, bf);
-        if (g == (cn >> 2)) {
+      for (int tt = 0; tt < 4; ++tt) bfn[tt] = phi_half(tt, 2 * w + (g >> 1));
+      split4<In>(accS8, s8hi, s8lo);
+      f32x4 pn[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) pn[tt] = mma16(zero4(), s8hi, bfn[tt]);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) pn[tt] = mma16(pn[tt], s8lo, bfn[tt]);
+      if (g == (cn >> 2)) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
           if (tt == w)
-            own = pn[cn & 3];
+            own = pn[tt][cn & 3];
           else
-            normp[norm_slot(t, w)] = pn[cn & 3];
+            normp[norm_slot(16 * tt + r16, w)] = pn[tt][cn & 3];
         }
       }
     }
 
     // (c) S += Psi^T Vb over the step's 64 tokens
-    Frag vbw[2], vb8[2];
+    // The ninth tile's rows of this wave take the Psi fragment of row tile w
+    // once more, outside the loop: a branch on at == w inside it would split
+    // the loop into blocks the compiler cannot move a read across.
+    // The sixteen (ks, at) products run in order with the Psi fragments of the
+    // next two read ahead (sched barriers keep the compiler from sinking the
+    // reads to their MFMAs).
+    Frag vbw[2], vb8[2], pa[3];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       vbw[ks] = vb_tr<In>(tvb, w, ks, lane);
       vb8[ks] = vb_tr<In>(tvb, 8, ks, lane);
-#pragma unroll
-      for (int at = 0; at < 8; ++at) {
-        const Frag pa = psi_tr<In>(tpsi, at, ks, lane);
-        accS[at] = mma(accS[at], pa, vbw[ks]);
-        if (at == w) accS8 = mma(accS8, pa, vb8[ks]);
-      }
     }
+    pa[0] = psi_tr<In>(tpsi, 0, 0, lane);
+    pa[1] = psi_tr<In>(tpsi, 1, 0, lane);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + 2 < 16) pa[(i + 2) % 3] = psi_tr<In>(tpsi, (i + 2) & 7, (i + 2) >> 3, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      accS[i & 7] = mma(accS[i & 7], pa[i % 3], vbw[i >> 3]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) accS8 = mma(accS8, psi_tr<In>(tpsi, w, ks, lane), vb8[ks]);
     lds_barrier();       // the score share is complete
 
     // (d) O^T += Vb^T A^T within the step; waves 0..3 add the row sums of A
     //     (the ones column) to their row tile's normaliser
+    auto share_bf = [&](int t, int ks) {
+      return *reinterpret_cast<const Frag*>(share + t * 8 + ((4 * ks + g) ^ swz8(t)));
+    };
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const int t = 16 * tt + r16;
-      f32x4 p8 = zero4();
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (ks <= (tt >> 1)) {
-          const Frag bf = *reinterpret_cast<const Frag*>(share + t * 8 + ((4 * ks + g) ^ swz8(t)));
-          accO[tt] = mma(accO[tt], vbw[ks], bf);
-          if (tt == w) p8 = mma(p8, vb8[ks], bf);
-        }
-      }
-      if (tt == w && g == (cn >> 2)) normp[norm_slot(t, w)] = own + p8[cn & 3];
+      for (int ks = 0; ks < 2; ++ks)
+        if (ks <= (tt >> 1)) accO[tt] = mma(accO[tt], vbw[ks], share_bf(t, ks));
+    }
+    if (w < 4) {        // row tile w's normaliser: the row sums of its score tiles
+      const int t = 16 * w + r16;
+      f32x4 p8 = mma(zero4(), vb8[0], share_bf(t, 0));
+      if (w >= 2) p8 = mma(p8, vb8[1], share_bf(t, 1));
+      if (g == (cn >> 2)) normp[norm_slot(t, w)] = own + p8[cn & 3];
     }
     lds_barrier();
 
