@@ -618,12 +618,16 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     auto share_bf = [&](int t, int ks) {
       return *reinterpret_cast<const Frag*>(share + t * 8 + ((4 * ks + g) ^ swz8(t)));
     };
+    {
+      Frag sh[4][2];    // the six causal score fragments, read before their MFMAs
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int t = 16 * tt + r16;
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int ks = 0; ks <= (tt >> 1); ++ks) sh[tt][ks] = share_bf(16 * tt + r16, ks);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        if (ks <= (tt >> 1)) accO[tt] = mma(accO[tt], vbw[ks], share_bf(t, ks));
+#pragma unroll
+        for (int tt = 2 * ks; tt < 4; ++tt) accO[tt] = mma(accO[tt], vbw[ks], sh[tt][ks]);
     }
     if (w < 4) {        // row tile w's normaliser: the row sums of its score tiles
       const int t = 16 * w + r16;
