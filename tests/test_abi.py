@@ -66,7 +66,13 @@ def test_workspace_query_arithmetic():
     rp4 = r * p * 4
     nc = T // C
     y_st = (p + 3) // 4 * 4          # the long-range term's rows are padded to 16 bytes
-    expect_min = nb * (N0 + B + 2 * nc) * rp4 + nb * (T - n) * y_st * 4 + nb * T * p * 4
+    # F and U rows are sized for the stride the line-group incidence takes: the
+    # first odd multiple of 16 floats at or above r * p (16528 here)
+    ld = (r * p + 15) // 16 * 16
+    ld += 16 if (ld // 16) % 2 == 0 else 0
+    assert ld == 16528
+    expect_min = (nb * (N0 + B) * ld * 4 + nb * 2 * nc * rp4 + nb * (T - n) * y_st * 4
+                  + nb * T * p * 4)
     assert expect_min <= ws <= expect_min + 16 * 256
     # d = 1 splits the single long progression: partial buffers appear
     assert _lib.query("smat_pool_workspace_bytes", 8, 0, 65536, 1, r, p) > 0
