@@ -575,10 +575,12 @@ int smat_query_lists(int dtype, const void* phi, const float* U, float* Y,
  * Phi = map(Q W^T), Psi = h * map(K W^T), Vb = [V, 1] (map: kind 0 elu + 1,
  * kind 1 relu + 1e-3, torch's rounding steps; h (nb, T) the optional key gate,
  * h_sb its batch stride) are formed in LDS by the pool, the query, the
- * prepass and the scan from the Q, K, V tiles they stream, so Phi, Psi and Vb
+ * prepass and the scan from the Q, K, V tiles they stream, so Phi and Vb
  * never reach memory (when a row type has more than 48 recent rows, the
  * recent rows' Phi alone is featurised into the workspace for the general
- * query).  W (128 x 128, features x d_qk) in the input dtype.  The other
+ * query); the causal pass's prepass stores the Psi rows it forms to the
+ * workspace and the scan reads them.  W (128 x 128, features x d_qk) in the
+ * input dtype.  The other
  * arguments are smat_forward's (no H_out); the workspace is
  * smat_forward_fused_workspace_bytes(nb, T, n, N0, B, n_P, C) bytes.  Serves
  * 16-bit inputs with d_qk = d_v = r = 128, T, n and C multiples of 64

@@ -62,6 +62,10 @@ struct FeatArgs {
   const void* h;
   int64_t h_sb;
   int kind;
+  // Where a Gram prepass that forms Psi also stores it, rows of 128 at row
+  // stride 128 and sequence stride psi_sb (none when null).
+  void* psi_out = nullptr;
+  int64_t psi_sb = 0;
 };
 
 // Features [16 wf, 16 wf + 16) of W as MFMA A fragments over d_qk = 128: k-block

@@ -83,7 +83,7 @@ int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v,
                          int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
                          int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
                          int64_t g_sb, const FeatArgs& fa, void* ws, int64_t ws_bytes,
-                         hipStream_t stream);
+                         void* psi_buf, hipStream_t stream);
 int64_t causal_scan_workspace_bytes(int nb, int T, int C, int r, int p);
 int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void* vb,
                          const float* Y, const float* gate, float* out, int nb, int T, int n,
@@ -341,9 +341,14 @@ namespace smat {
 static bool fused_query_staged(int T, int n, int B) {
   return T > n && (T - n + B - 1) / B > 48;
 }
+// Beyond the forward's layout: the staged recent Phi rows (if any), then the
+// Psi rows the prepass forms and the scan reads (nb x T rows of 128).
+static int64_t fused_phi_bytes(int nb, int T, int n, int B) {
+  return fused_query_staged(T, n, B) ? al256((int64_t)nb * (T - n) * 128 * 2) : 0;
+}
 static int64_t fused_workspace_bytes(int nb, int T, int n, int N0, int B, int n_P, int C) {
   const FwdLayout L = fwd_layout(nb, T, n, N0, B, n_P, C, 128, 129, false);
-  return L.total + (fused_query_staged(T, n, B) ? al256((int64_t)nb * (T - n) * 128 * 2) : 0);
+  return L.total + fused_phi_bytes(nb, T, n, B) + al256((int64_t)nb * T * 128 * 2);
 }
 }  // namespace smat
 
@@ -356,10 +361,11 @@ extern "C" int64_t smat_forward_fused_workspace_bytes(int nb, int T, int n, int 
 // The forward of smat_forward computed from Q, K, V: the feature map
 // Phi = map(Q W^T), Psi = h map(K W^T), Vb = [V, 1] (src/smat/attention.py:82-106)
 // runs inside the pool, the query, the prepass and the scan, on tiles already
-// in LDS, so Phi, Psi and Vb are never written to memory -- except, when a
-// row type has more than 48 recent rows (beyond the streaming query), the
-// recent rows' Phi, which is featurised into the workspace for the general
-// query kernel.  Serves the head-dim-128 streaming shape: 16-bit inputs,
+// in LDS, so Phi and Vb are never written to memory -- except, when a row
+// type has more than 48 recent rows (beyond the streaming query), the recent
+// rows' Phi, which is featurised into the workspace for the general query
+// kernel.  Psi is formed once, by the causal pass's prepass, which stores it
+// to the workspace for the scan.  Serves the head-dim-128 streaming shape: 16-bit inputs,
 // d_qk = d_v = r = 128 (p = 129), T, n and the chunk multiples of 64
 // (chunk <= 128), 16-byte aligned rows; anything else returns
 // SMAT_EUNSUPPORTED (the caller featurises, then calls smat_forward).
@@ -467,7 +473,8 @@ extern "C" int smat_forward_fused(int dtype, const void* q, const void* k, const
     if (rc) return rc;
   }
   StageScope stage(3);
+  void* psi_rows = ws + L.total + fused_phi_bytes(nb, T, n, B);
   return causal_scan_run_feat(dtype, q, k, v, T_R > 0 ? Y : nullptr, g, out, nb, T, n, C, q_sb,
                               q_st, k_sb, k_st, v_sb, v_st, (int64_t)T_R * yst, yst, o_sb, o_st,
-                              g_sb, fa, ws + L.scan, L.part - L.scan, st);
+                              g_sb, fa, ws + L.scan, L.part - L.scan, psi_rows, st);
 }

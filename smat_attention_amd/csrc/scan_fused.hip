@@ -453,7 +453,7 @@ int scan_stream_launch(int dtype, const void* phi, const void* psi, const void* 
 int scan_stream_launch_feat(int dtype, const void* q, const void* k, const void* v,
                             const float* Sg, const float* Y, const float* gate, float* out,
                             int nb, int ng, const ScanArgs& a, const FeatArgs& fa,
-                            hipStream_t stream);
+                            bool psi_formed, hipStream_t stream);
 int gram_stream_launch_feat(int dtype, const void* k, const void* v, float* G, float* G_last,
                             const GramItems& it, int nitems, int nb, int64_t k_sb, int64_t k_st,
                             int64_t v_sb, int64_t v_st, int64_t g_sb, int64_t g_si,
@@ -557,13 +557,15 @@ int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb,
 // The streaming causal pass with the feature map computed inside the kernels:
 // q, k, v are the Q, K, V rows (r = d_qk = d_v = 128); the prepass Gram sums
 // and the scan form Psi (and Phi) tiles in LDS from the DMA'd K (and Q) rows,
-// and Vb = [V, 1] from V.  Same workspace as causal_scan_dispatch.
+// and Vb = [V, 1] from V.  Same workspace as causal_scan_dispatch.  With
+// psi_buf (nb x T rows of 128, 16-bit) the prepass also stores the Psi tiles
+// it forms there and the scan reads them, forming only Phi.
 int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v, const float* Y,
                          const float* gate, float* out, int nb, int T, int n, int C,
                          int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
                          int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
                          int64_t g_sb, const FeatArgs& fa, void* ws, int64_t ws_bytes,
-                         hipStream_t stream) {
+                         void* psi_buf, hipStream_t stream) {
   if (nb == 0 || T == 0) return SMAT_OK;
   constexpr int r = 128, p = 129;
   const int64_t rp = (int64_t)r * p;
@@ -589,8 +591,11 @@ int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v,
   it.nsplit = 1;
   it.per = K * C;
   const int ng = it.ng0 + (nc - it.nc0 + K - 1) / K;
+  FeatArgs fp = fa;
+  fp.psi_out = psi_buf;
+  fp.psi_sb = (int64_t)T * 128;
   int rc = gram_stream_launch_feat(dtype, k, v, G, nullptr, it, ng, nb, k_sb, k_st, v_sb, v_st,
-                                   (int64_t)ng * rp, rp, 0, fa, stream, "smat_forward_fused");
+                                   (int64_t)ng * rp, rp, 0, fp, stream, "smat_forward_fused");
   if (rc) return rc;
   rc = segment_scan_dispatch(G, Sg, nb, ng, it.ng0, rp, stream);
   if (rc) return rc;
@@ -606,8 +611,8 @@ int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v,
   a.p = p;
   a.q_sb = q_sb;
   a.q_st = q_st;
-  a.k_sb = k_sb;
-  a.k_st = k_st;
+  a.k_sb = psi_buf ? fp.psi_sb : k_sb;
+  a.k_st = psi_buf ? 128 : k_st;
   a.v_sb = v_sb;
   a.v_st = v_st;
   a.y_sb = y_sb;
@@ -616,7 +621,8 @@ int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v,
   a.o_st = o_st;
   a.g_sb = g_sb;
   a.write_H = 0;
-  return scan_stream_launch_feat(dtype, q, k, v, Sg, Y, gate, out, nb, ng, a, fa, stream);
+  return scan_stream_launch_feat(dtype, q, psi_buf ? psi_buf : k, v, Sg, Y, gate, out, nb, ng, a,
+                                 fa, psi_buf != nullptr, stream);
 }
 
 // ---------------------------------------------------------------------------

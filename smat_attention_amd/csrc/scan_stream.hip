@@ -276,12 +276,13 @@ __device__ __forceinline__ f32x4 mma16(f32x4 c, f16x4 a, f16x4 b) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
-// FEAT: phi, psi and vb are Q, K and V rows (v_st may be 128); each step's
-// Phi and Psi tiles are formed from the DMA'd Q and K tiles into two more
-// tiles, phiF and psiF (feat_rows, W in registers), the key gate applied to
-// Psi.  A step's reads of phiF and psiF end before the barrier after its
+// FEAT = 1: phi, psi and vb are Q, K and V rows (v_st may be 128); each
+// step's Phi and Psi tiles are formed from the DMA'd Q and K tiles into two
+// more tiles, phiF and psiF (feat_rows, W in registers), the key gate applied
+// to Psi.  A step's reads of phiF and psiF end before the barrier after its
 // state update, so the next step's features overwrite them safely.
-template <typename In, bool FEAT, int NBUF, bool TERMS>
+// FEAT = 2: psi holds Psi rows already (gate applied), only Phi is formed.
+template <typename In, int FEAT, int NBUF, bool TERMS>
 __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
     const float* __restrict__ Sg, const float* __restrict__ Y, const float* __restrict__ gate,
@@ -308,7 +309,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   // normaliser partials: wave w's share of H[t][p-1] at normp[norm_slot(t, w)]
   __shared__ __attribute__((aligned(16))) float normp[kStep * 8];
   __shared__ __attribute__((aligned(16))) uint4 phiF[FEAT ? kTileChunks : 1];
-  __shared__ __attribute__((aligned(16))) uint4 psiF[FEAT ? kTileChunks : 1];
+  __shared__ __attribute__((aligned(16))) uint4 psiF[FEAT == 1 ? kTileChunks : 1];
 
   // Groups run last sequence first, last group first: the prepass just read
   // the same Psi and Vb rows in the opposite order, so the first groups here
@@ -350,14 +351,14 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   dma_offsets<In>(dmo, a, w, lane);
   RowOffsets rof;
   row_offsets(rof, a, w, lane);
-  if (nsteps > 0) issue_step<In, FEAT>(phi0, psi0, vb0, phib, psib, vbb, tk0, a, w, dmo);
+  if (nsteps > 0) issue_step<In, FEAT != 0>(phi0, psi0, vb0, phib, psib, vbb, tk0, a, w, dmo);
   Frag wa[4];
   const In* hb = nullptr;
   if constexpr (FEAT) {
     feat_w_load<In>(wa, (const In*)fa.W, w, lane);
     feat_ones_tile<In>(vb0 + kTileChunks, threadIdx.x, kThreads);
     feat_ones_tile<In>(vb1 + kTileChunks, threadIdx.x, kThreads);
-    hb = fa.h ? (const In*)fa.h + b * fa.h_sb : nullptr;
+    if (FEAT == 1) hb = fa.h ? (const In*)fa.h + b * fa.h_sb : nullptr;
   }
 
   // incoming state: S[a][16w + lane%16] for all a, and the normaliser column
@@ -375,7 +376,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     accS8[i] = c8 < a.p ? v8 : 0.f;
   }
   if (NBUF == 3 && nsteps > 1)
-    issue_step<In, FEAT>(phi1, psi1, vb1, phib, psib, vbb, tk0 + kStep, a, w, dmo);
+    issue_step<In, FEAT != 0>(phi1, psi1, vb1, phib, psib, vbb, tk0 + kStep, a, w, dmo);
   // Consume the state loads here, so that no wait for them (which would also
   // wait for the step DMA issued after them) is placed inside the loop.
 #pragma unroll
@@ -385,7 +386,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   auto step = [&](auto BUFC, int s) {
     constexpr int BUF = decltype(BUFC)::value;
     const uint4* tphi = FEAT ? phiF : BUF == 2 ? phi2 : BUF ? phi1 : phi0;
-    const uint4* tpsi = FEAT ? psiF : BUF == 2 ? psi2 : BUF ? psi1 : psi0;
+    const uint4* tpsi = FEAT == 1 ? psiF : BUF == 2 ? psi2 : BUF ? psi1 : psi0;
     const uint4* tvb = BUF == 2 ? vb2 : BUF ? vb1 : vb0;
     const int64_t ts = tk0 + (int64_t)s * kStep;
     // An opaque copy of the lane index per step: the LDS addresses derived
@@ -395,8 +396,8 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     int lane = lane_id();
     asm volatile("" : "+v"(lane));
     const int r16 = lane & 15, g = lane >> 4;
-    float hv[4];                      // FEAT: the key gate of the lane's four rows
-    if constexpr (FEAT) {
+    float hv[4] = {1.f, 1.f, 1.f, 1.f};    // FEAT = 1: the key gate of the lane's four rows
+    if constexpr (FEAT == 1) {
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) hv[tt] = hb ? to_f32(hb[ts + 16 * tt + r16]) : 1.f;
     }
@@ -414,7 +415,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
         wait_vmcnt<0>();
       }
     } else if (s + 1 < nsteps) {
-      issue_step<In, FEAT>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib,
+      issue_step<In, FEAT != 0>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib,
                            vbb, ts + kStep, a, w, dmo);
       // the gate loads (issued first) are older than this step's six DMA loads
       if (!FEAT && w == 0)
@@ -428,9 +429,10 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     if constexpr (FEAT) {
       const auto sw = [](int t) { return swz16(t); };
       feat_rows<In, 4>(BUF ? phi1 : phi0, phiF, 0, true, wa, w, fa.kind, false, hv, lane, sw);
-      feat_rows<In, 4>(BUF ? psi1 : psi0, psiF, 0, true, wa, w, fa.kind, hb != nullptr, hv, lane,
-                       sw);
-      lds_barrier();    // the step's Phi and Psi tiles are complete
+      if constexpr (FEAT == 1)
+        feat_rows<In, 4>(BUF ? psi1 : psi0, psiF, 0, true, wa, w, fa.kind, hb != nullptr, hv, lane,
+                         sw);
+      lds_barrier();    // the step's Phi (and Psi) tiles are complete
     }
     YRegs yr;
     if constexpr (NBUF == 2) issue_y(yr, Yb, gb, Sb, ts, a, rof, lane);
@@ -521,7 +523,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     if constexpr (NBUF == 3) {
       constexpr int NB = (BUF + 2) % 3;
       if (s + 2 < nsteps)
-        issue_step<In, FEAT>(NB == 2 ? phi2 : NB ? phi1 : phi0, NB == 2 ? psi2 : NB ? psi1 : psi0,
+        issue_step<In, FEAT != 0>(NB == 2 ? phi2 : NB ? phi1 : phi0, NB == 2 ? psi2 : NB ? psi1 : psi0,
                              NB == 2 ? vb2 : NB ? vb1 : vb0, phib, psib, vbb, ts + 2 * kStep, a,
                              w, dmo);
     }
@@ -867,6 +869,18 @@ __global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_str
       feat_rows<In, 2>(fpsi, fpsi, 0, true, wa, w, fa.kind, hb != nullptr, h01, lane, sw);
       feat_rows<In, 2>(fpsi, fpsi, 2, true, wa, w, fa.kind, hb != nullptr, h23, lane, sw);
       lds_barrier();    // the step's Psi tile is complete
+      if (fa.psi_out != nullptr) {
+        // the tile's rows to psi_out: thread (t, c) of 64 rows x 8 pairs of
+        // 16-byte chunks, un-swizzled, for the rows that hold tokens
+        const int t = threadIdx.x >> 3, c = 2 * (threadIdx.x & 7);
+        const int row = s * kStep + t;
+        if (row < count) {
+          const int64_t tok = gram_token_of<LIST>(it, item, start, stride, row);
+          uint4* dst = reinterpret_cast<uint4*>((In*)fa.psi_out + b * fa.psi_sb + tok * 128);
+          dst[c] = fpsi[t * kRowChunks + (c ^ swz16(t))];
+          dst[c + 1] = fpsi[t * kRowChunks + ((c + 1) ^ swz16(t))];
+        }
+      }
     }
     const int nvalid = count - s * kStep;        // rows of this step holding tokens
 #pragma unroll
@@ -1048,7 +1062,7 @@ bool scan_stream_ok(int dtype, const void* phi, const void* psi, const void* vb,
   return variant(SMAT_VARIANT_SCAN) == 0;
 }
 
-template <typename In, bool FEAT>
+template <typename In, int FEAT>
 static void scan_stream_kernel_launch(const void* phi, const void* psi, const void* vb,
                                       const float* Sg, const float* Y, const float* gate,
                                       float* out, dim3 grid, const ScanArgs& a, const FeatArgs& fa,
@@ -1056,18 +1070,18 @@ static void scan_stream_kernel_launch(const void* phi, const void* psi, const vo
   const In* q = (const In*)phi;
   const In* k = (const In*)psi;
   const In* v = (const In*)vb;
-  if constexpr (FEAT)
-    smat::launch((scan_stream_kernel<In, true, 2, true>), grid, dim3(ss::kThreads), 0,
+  if constexpr (FEAT != 0)
+    smat::launch((scan_stream_kernel<In, FEAT, 2, true>), grid, dim3(ss::kThreads), 0,
                        stream, q, k, v, Sg, Y, gate, out, a, fa);
   else if (Y || gate)
-    smat::launch((scan_stream_kernel<In, false, 3, true>), grid, dim3(ss::kThreads), 0,
+    smat::launch((scan_stream_kernel<In, 0, 3, true>), grid, dim3(ss::kThreads), 0,
                        stream, q, k, v, Sg, Y, gate, out, a, fa);
   else
-    smat::launch((scan_stream_kernel<In, false, 3, false>), grid, dim3(ss::kThreads), 0,
+    smat::launch((scan_stream_kernel<In, 0, 3, false>), grid, dim3(ss::kThreads), 0,
                        stream, q, k, v, Sg, Y, gate, out, a, fa);
 }
 
-template <bool FEAT>
+template <int FEAT>
 static int scan_stream_go(int dtype, const void* phi, const void* psi, const void* vb,
                           const float* Sg, const float* Y, const float* gate, float* out, int nb,
                           int ng, const ScanArgs& a, const FeatArgs& fa, hipStream_t stream) {
@@ -1082,17 +1096,19 @@ static int scan_stream_go(int dtype, const void* phi, const void* psi, const voi
 int scan_stream_launch(int dtype, const void* phi, const void* psi, const void* vb,
                        const float* Sg, const float* Y, const float* gate, float* out, int nb,
                        int ng, const ScanArgs& a, hipStream_t stream) {
-  return scan_stream_go<false>(dtype, phi, psi, vb, Sg, Y, gate, out, nb, ng, a, FeatArgs{},
-                               stream);
+  return scan_stream_go<0>(dtype, phi, psi, vb, Sg, Y, gate, out, nb, ng, a, FeatArgs{},
+                           stream);
 }
 
-// The streaming causal pass with the feature map in place: phi, psi, vb are
-// Q, K, V rows (the shapes scan_stream_ok accepts, with V rows of 128).
+// The streaming causal pass with the feature map in place: q and v are Q
+// and V rows (the shapes scan_stream_ok accepts, with V rows of 128); k is
+// K rows, or the Psi rows (key gate applied) when psi_formed.
 int scan_stream_launch_feat(int dtype, const void* q, const void* k, const void* v,
                             const float* Sg, const float* Y, const float* gate, float* out,
                             int nb, int ng, const ScanArgs& a, const FeatArgs& fa,
-                            hipStream_t stream) {
-  return scan_stream_go<true>(dtype, q, k, v, Sg, Y, gate, out, nb, ng, a, fa, stream);
+                            bool psi_formed, hipStream_t stream) {
+  if (psi_formed) return scan_stream_go<2>(dtype, q, k, v, Sg, Y, gate, out, nb, ng, a, fa, stream);
+  return scan_stream_go<1>(dtype, q, k, v, Sg, Y, gate, out, nb, ng, a, fa, stream);
 }
 
 }  // namespace smat
