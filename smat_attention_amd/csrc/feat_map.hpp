@@ -22,17 +22,19 @@ namespace smat {
 // relative.  Rounded to bf16, it equals the correctly rounded expm1 (and the
 // fp32 libm expm1f) for every negative bf16 input -- an exhaustive check --
 // at a fraction of expm1f's cost, which dominates the feature map's VALU time.
+// Both forms are computed and one selected: no divergent branch, so the
+// feature map's instructions interleave with the MFMAs around them.  (For
+// v > 0 the exp2 form may be inf; callers select v there.)
 __device__ __forceinline__ float expm1_neg(float v) {
-  if (v > -0.25f) {
-    float r = 1.f / 720.f;
-    r = fmaf(v, r, 1.f / 120.f);
-    r = fmaf(v, r, 1.f / 24.f);
-    r = fmaf(v, r, 1.f / 6.f);
-    r = fmaf(v, r, 0.5f);
-    r = fmaf(v, r, 1.f);
-    return v * r;
-  }
-  return __builtin_amdgcn_exp2f(v * 1.4426950408889634f) - 1.f;
+  float r = 1.f / 720.f;
+  r = fmaf(v, r, 1.f / 120.f);
+  r = fmaf(v, r, 1.f / 24.f);
+  r = fmaf(v, r, 1.f / 6.f);
+  r = fmaf(v, r, 0.5f);
+  r = fmaf(v, r, 1.f);
+  const float near = v * r;
+  const float far = __builtin_amdgcn_exp2f(v * 1.4426950408889634f) - 1.f;
+  return v > -0.25f ? near : far;
 }
 
 // expm1 of a non-positive argument for input type In: the short form where the
@@ -45,14 +47,25 @@ __device__ __forceinline__ float expm1_nonpos(float v) {
   else return expm1f(v);
 }
 
-template <typename In>
-__device__ __forceinline__ float feature_map(float acc, int kind) {
+template <typename In, int KIND>
+__device__ __forceinline__ float feature_map_k(float acc) {
   const float v = to_f32(from_f32<In>(acc));                 // torch's matmul output
-  if (kind == 0) {
-    const float e = to_f32(from_f32<In>(v > 0.f ? v : expm1_nonpos<In>(v)));
+  if constexpr (KIND == 0) {
+    float e;
+    if constexpr (std::is_same<In, bf16>::value) {
+      const float m = expm1_neg(v);                            // computed for every lane
+      e = to_f32(from_f32<In>(v > 0.f ? v : m));
+    } else {
+      e = to_f32(from_f32<In>(v > 0.f ? v : expm1_nonpos<In>(v)));
+    }
     return to_f32(from_f32<In>(e + 1.0f));
   }
   return to_f32(from_f32<In>(fmaxf(v, 0.f) + 1e-3f));
+}
+
+template <typename In>
+__device__ __forceinline__ float feature_map(float acc, int kind) {
+  return kind == 0 ? feature_map_k<In, 0>(acc) : feature_map_k<In, 1>(acc);
 }
 
 // The feature map handed to a consumer kernel: W (128 x 128, features x d_qk,
@@ -117,20 +130,28 @@ __device__ __forceinline__ void feat_rows(const uint4* src, uint4* dst, int rt0,
     }
   }
   if (dst == src) lds_barrier();                     // every wave has read its rows
-  if (active) {
+  // one branch on the (uniform) kind around all of the rows' values
+  auto put = [&](auto KC) {
+    constexpr int KIND = decltype(KC)::value;
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
       const int t = 16 * (rt0 + rt) + r16;
       Half hv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float y = feature_map<In>(acc[rt][i], kind);
+        float y = feature_map_k<In, KIND>(acc[rt][i]);
         if (use_gate) y = to_f32(from_f32<In>(y * gate[rt]));
         hv[i] = from_f32<In>(y);
       }
       char* p = reinterpret_cast<char*>(dst + t * 16 + ((2 * wf + (g >> 1)) ^ swz(t)));
       *reinterpret_cast<Half*>(p + 8 * (g & 1)) = hv;
     }
+  };
+  if (active) {
+    if (kind == 0)
+      put(std::integral_constant<int, 0>{});
+    else
+      put(std::integral_constant<int, 1>{});
   }
 }
 

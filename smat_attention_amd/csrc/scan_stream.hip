@@ -281,7 +281,8 @@ __device__ __forceinline__ f32x4 mma16(f32x4 c, f16x4 a, f16x4 b) {
 // more tiles, phiF and psiF (feat_rows, W in registers), the key gate applied
 // to Psi.  A step's reads of phiF and psiF end before the barrier after its
 // state update, so the next step's features overwrite them safely.
-// FEAT = 2: psi holds Psi rows already (gate applied), only Phi is formed.
+// FEAT = 2: psi holds Psi rows already (gate applied), only Phi is formed,
+// in place over the DMA'd Q tile, with three row buffers.
 template <typename In, int FEAT, int NBUF, bool TERMS>
 __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     const In* __restrict__ phi, const In* __restrict__ psi, const In* __restrict__ vb,
@@ -296,19 +297,20 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   __shared__ __attribute__((aligned(16))) uint4 phi1[kTileChunks];
   __shared__ __attribute__((aligned(16))) uint4 psi1[kTileChunks];
   __shared__ __attribute__((aligned(16))) uint4 vb1[kVbTileChunks];
-  // NBUF = 3 (no feature map): a third buffer (160 768 bytes of LDS in all)
-  // keeps the rows of steps s + 1 and s + 2 in flight while step s computes.
+  // NBUF = 3 (no Psi formed here): a third buffer (160 768 bytes of LDS in
+  // all) keeps the rows of steps s + 1 and s + 2 in flight while step s
+  // computes.
   // Y and the gate are then loaded untracked and waited for by count.
   // TERMS = false compiles Y and the gate out (launches with neither): their
   // pointers and flags would otherwise spill scalar registers every step.
-  static_assert(NBUF == 2 || (NBUF == 3 && !FEAT), "three buffers only without the feature map");
+  static_assert(NBUF == 2 || (NBUF == 3 && FEAT != 1), "three buffers only without Psi formed here");
   __shared__ __attribute__((aligned(16))) uint4 phi2[NBUF == 3 ? kTileChunks : 1];
   __shared__ __attribute__((aligned(16))) uint4 psi2[NBUF == 3 ? kTileChunks : 1];
   __shared__ __attribute__((aligned(16))) uint4 vb2[NBUF == 3 ? kVbTileChunks : 1];
   __shared__ __attribute__((aligned(16))) uint4 share[kStep * 8];
   // normaliser partials: wave w's share of H[t][p-1] at normp[norm_slot(t, w)]
   __shared__ __attribute__((aligned(16))) float normp[kStep * 8];
-  __shared__ __attribute__((aligned(16))) uint4 phiF[FEAT ? kTileChunks : 1];
+  __shared__ __attribute__((aligned(16))) uint4 phiF[FEAT && NBUF == 2 ? kTileChunks : 1];
   __shared__ __attribute__((aligned(16))) uint4 psiF[FEAT == 1 ? kTileChunks : 1];
 
   // Groups run last sequence first, last group first: the prepass just read
@@ -358,6 +360,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     feat_w_load<In>(wa, (const In*)fa.W, w, lane);
     feat_ones_tile<In>(vb0 + kTileChunks, threadIdx.x, kThreads);
     feat_ones_tile<In>(vb1 + kTileChunks, threadIdx.x, kThreads);
+    if (NBUF == 3) feat_ones_tile<In>(vb2 + kTileChunks, threadIdx.x, kThreads);
     if (FEAT == 1) hb = fa.h ? (const In*)fa.h + b * fa.h_sb : nullptr;
   }
 
@@ -382,10 +385,14 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 #pragma unroll
   for (int at = 0; at < 8; ++at) asm volatile("" : "+v"(accS[at]));
   asm volatile("" : "+v"(accS8));
+  if constexpr (FEAT) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(wa[kb]));
+  }
 
   auto step = [&](auto BUFC, int s) {
     constexpr int BUF = decltype(BUFC)::value;
-    const uint4* tphi = FEAT ? phiF : BUF == 2 ? phi2 : BUF ? phi1 : phi0;
+    const uint4* tphi = FEAT && NBUF == 2 ? phiF : BUF == 2 ? phi2 : BUF ? phi1 : phi0;
     const uint4* tpsi = FEAT == 1 ? psiF : BUF == 2 ? psi2 : BUF ? psi1 : psi0;
     const uint4* tvb = BUF == 2 ? vb2 : BUF ? vb1 : vb0;
     const int64_t ts = tk0 + (int64_t)s * kStep;
@@ -404,10 +411,11 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     static_assert(kLoads / 8 == 6 && kLoads % 8 == 1, "seven loads on wave 0, six on the rest");
     if constexpr (NBUF == 3) {
       // Issued after this step's DMA: the previous step's output stores and the
-      // next step's DMA, seven loads on wave 0 and six on the rest.  Loads
-      // complete in order, so waiting down to that many lands this step's rows.
+      // next step's DMA, seven loads on wave 0 and six on the rest (six on every
+      // wave with the feature map).  Loads complete in order, so waiting down
+      // to that many lands this step's rows.
       if (s + 1 < nsteps) {
-        if (w == 0)
+        if (!FEAT && w == 0)
           wait_vmcnt<7>();
         else
           wait_vmcnt<6>();
@@ -426,7 +434,13 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
       wait_vmcnt<0>();
     }
     lds_barrier();      // every wave's DMA of this step has landed
-    if constexpr (FEAT) {
+    if constexpr (FEAT && NBUF == 3) {
+      // in place: feat_rows reads every wave's rows, then waits, then writes
+      const auto sw = [](int t) { return swz16(t); };
+      uint4* tq = BUF == 2 ? phi2 : BUF ? phi1 : phi0;
+      feat_rows<In, 4>(tq, tq, 0, true, wa, w, fa.kind, false, hv, lane, sw);
+      lds_barrier();    // the step's Phi tile is complete
+    } else if constexpr (FEAT) {
       const auto sw = [](int t) { return swz16(t); };
       feat_rows<In, 4>(BUF ? phi1 : phi0, phiF, 0, true, wa, w, fa.kind, false, hv, lane, sw);
       if constexpr (FEAT == 1)
@@ -648,7 +662,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
       if (rec || gb) {
         // everything issued after the Y and gate loads: step s + 2's DMA
         if (s + 2 < nsteps) {
-          if (w == 0)
+          if (!FEAT && w == 0)
             wait_vmcnt<7>();
           else
             wait_vmcnt<6>();
@@ -1071,8 +1085,8 @@ static void scan_stream_kernel_launch(const void* phi, const void* psi, const vo
   const In* k = (const In*)psi;
   const In* v = (const In*)vb;
   if constexpr (FEAT != 0)
-    smat::launch((scan_stream_kernel<In, FEAT, 2, true>), grid, dim3(ss::kThreads), 0,
-                       stream, q, k, v, Sg, Y, gate, out, a, fa);
+    smat::launch((scan_stream_kernel<In, FEAT, FEAT == 2 ? 3 : 2, true>), grid,
+                 dim3(ss::kThreads), 0, stream, q, k, v, Sg, Y, gate, out, a, fa);
   else if (Y || gate)
     smat::launch((scan_stream_kernel<In, 0, 3, true>), grid, dim3(ss::kThreads), 0,
                        stream, q, k, v, Sg, Y, gate, out, a, fa);
