@@ -97,6 +97,42 @@ __device__ __forceinline__ float load1_untracked(const void* p) {
   asm volatile("global_load_dword %0, %1, off" : "=&v"(v) : "v"(p) : "memory");
   return v;
 }
+// A 16-bit element, zero-extended into a 32-bit register, untracked likewise.
+__device__ __forceinline__ uint32_t load_u16_untracked(const void* p) {
+  uint32_t v;
+  asm volatile("global_load_ushort %0, %1, off" : "=&v"(v) : "v"(p) : "memory");
+  return v;
+}
+
+// One HBM -> LDS copy of 16 bytes a lane (global_load_lds_dwordx4: lane i
+// writes bytes [16 i, 16 i + 16) from dst, a wave-uniform LDS address).
+// UNTRACKED issues it from inline assembly, so the compiler does not know that
+// an LDS write is in flight.  Tracked, every LDS read it cannot tell apart from
+// the copy's target -- the transposing reads among them -- gets a compiler
+// wait of vmcnt(0) in front, which drains the next step's copy right after it
+// is issued and leaves nothing to overlap with the step's compute.  Untracked,
+// the kernels' own vmcnt waits (loads complete in order) and barriers are what
+// order each read after the copy it reads; loads the compiler does track must
+// then not be pending across such a copy, or their compiler waits (counting
+// only tracked loads) drain it as well.
+template <bool UNTRACKED>
+__device__ __forceinline__ void lds_dma16(const void* src, uint4* dst) {
+  if constexpr (UNTRACKED) {
+    const uint32_t m0 =
+        __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(SMAT_LDS char*)(dst));
+    // m0 (the LDS address) is saved and restored around the copy: the
+    // compiler reserves it and may keep a value of its own there
+    uint32_t keep;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(keep)
+        : "v"(src), "s"(m0)
+        : "memory");
+  } else {
+    __builtin_amdgcn_global_load_lds(src, (SMAT_LDS void*)(SMAT_LDS char*)(dst), 16, 0, 0);
+  }
+}
 
 // 8 bytes of a swizzled 256-byte row (t, chunk k, half h).
 template <typename In>
@@ -204,7 +240,7 @@ __device__ __forceinline__ void dma_offsets(DmaOffsets& d, const ScanArgs& a, in
 
 // FEAT: the rows are Q, K and V (the feature map runs in LDS afterwards), and
 // the ninth Vb tile is the constant [1, 0, ...] written once: six loads a wave.
-template <typename In, bool FEAT>
+template <typename In, bool FEAT, bool UNTRACKED>
 __device__ __forceinline__ void issue_step(uint4* dphi, uint4* dpsi, uint4* dvb, const In* phib,
                                            const In* psib, const In* vbb, int64_t ts,
                                            const ScanArgs& a, int w, const DmaOffsets& d) {
@@ -219,8 +255,7 @@ __device__ __forceinline__ void issue_step(uint4* dphi, uint4* dpsi, uint4* dvb,
       uint4* dst = u < 2 ? dphi + 64 * I
                  : u < 4 ? dpsi + 64 * (I - ss::kPhiLoads)
                          : dvb + 64 * (I - 2 * ss::kPhiLoads);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base + d.off[u]),
-                                       (SMAT_LDS void*)(SMAT_LDS char*)(dst), 16, 0, 0);
+      lds_dma16<UNTRACKED>(reinterpret_cast<const void*>(base + d.off[u]), dst);
     }
   }
 }
@@ -353,7 +388,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
   dma_offsets<In>(dmo, a, w, lane);
   RowOffsets rof;
   row_offsets(rof, a, w, lane);
-  if (nsteps > 0) issue_step<In, FEAT != 0>(phi0, psi0, vb0, phib, psib, vbb, tk0, a, w, dmo);
+  if (nsteps > 0) issue_step<In, FEAT != 0, NBUF == 3>(phi0, psi0, vb0, phib, psib, vbb, tk0, a, w, dmo);
   Frag wa[4];
   const In* hb = nullptr;
   if constexpr (FEAT) {
@@ -378,10 +413,10 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     const float v8 = Sb[(int64_t)(16 * w + 4 * g + i) * a.p + (c8 < a.p ? c8 : 0)];
     accS8[i] = c8 < a.p ? v8 : 0.f;
   }
-  if (NBUF == 3 && nsteps > 1)
-    issue_step<In, FEAT != 0>(phi1, psi1, vb1, phib, psib, vbb, tk0 + kStep, a, w, dmo);
-  // Consume the state loads here, so that no wait for them (which would also
-  // wait for the step DMA issued after them) is placed inside the loop.
+  // Consume the state (and W) loads here, so that no wait for them is placed
+  // inside the loop.  With three buffers the copies are untracked and the
+  // compiler's wait here is vmcnt(0), which lands step 0's rows too; step
+  // 1's copy goes out after it.
 #pragma unroll
   for (int at = 0; at < 8; ++at) asm volatile("" : "+v"(accS[at]));
   asm volatile("" : "+v"(accS8));
@@ -389,6 +424,8 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(wa[kb]));
   }
+  if (NBUF == 3 && nsteps > 1)
+    issue_step<In, FEAT != 0, true>(phi1, psi1, vb1, phib, psib, vbb, tk0 + kStep, a, w, dmo);
 
   auto step = [&](auto BUFC, int s) {
     constexpr int BUF = decltype(BUFC)::value;
@@ -423,7 +460,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
         wait_vmcnt<0>();
       }
     } else if (s + 1 < nsteps) {
-      issue_step<In, FEAT != 0>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib,
+      issue_step<In, FEAT != 0, NBUF == 3>(BUF ? phi0 : phi1, BUF ? psi0 : psi1, BUF ? vb0 : vb1, phib, psib,
                            vbb, ts + kStep, a, w, dmo);
       // the gate loads (issued first) are older than this step's six DMA loads
       if (!FEAT && w == 0)
@@ -537,7 +574,7 @@ __global__ __launch_bounds__(ss::kThreads, 1) void scan_stream_kernel(
     if constexpr (NBUF == 3) {
       constexpr int NB = (BUF + 2) % 3;
       if (s + 2 < nsteps)
-        issue_step<In, FEAT != 0>(NB == 2 ? phi2 : NB ? phi1 : phi0, NB == 2 ? psi2 : NB ? psi1 : psi0,
+        issue_step<In, FEAT != 0, NBUF == 3>(NB == 2 ? phi2 : NB ? phi1 : phi0, NB == 2 ? psi2 : NB ? psi1 : psi0,
                              NB == 2 ? vb2 : NB ? vb1 : vb0, phib, psib, vbb, ts + 2 * kStep, a,
                              w, dmo);
     }
@@ -781,8 +818,9 @@ __device__ __forceinline__ void issue_gram(uint4* dpsi, uint4* dvb, const In* ps
         src = vbb + tok * v_st + col;
         dst = dvb + 64 * li;
       }
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                       (SMAT_LDS void*)(SMAT_LDS char*)(dst), 16, 0, 0);
+      // untracked except with the list's token loads, whose own compiler
+      // waits drain the copies anyway
+      lds_dma16<!LIST>(reinterpret_cast<const void*>(src), dst);
     }
   }
 }
@@ -844,6 +882,10 @@ __global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_str
     feat_ones_tile<In>(vb0 + kTileChunks, threadIdx.x, kThreads);
     if (!ONE) feat_ones_tile<In>(vb1 + kTileChunks, threadIdx.x, kThreads);
     hb = fa.h ? (const In*)fa.h + b * fa.h_sb : nullptr;
+    // consumed here (the compiler's wait also lands step 0's rows), so no
+    // wait for W sits inside the loop
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(wa[kb]));
   }
 
   auto step = [&](auto BUFC, int s) {
@@ -853,14 +895,18 @@ __global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_str
     int lane = lane_id();
     asm volatile("" : "+v"(lane));
     const int g = lane >> 4;
-    float hv[4];                      // FEAT: the key gate of the lane's four rows
+    // FEAT: the key gate of the lane's four rows, loaded untracked before the
+    // next step's copy and consumed after the wait that covers it
+    uint32_t hraw[4] = {0, 0, 0, 0};
     if constexpr (FEAT) {
       const int r16 = lane & 15;
+      if (hb) {
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const int row = s * kStep + 16 * tt + r16;
-        hv[tt] = hb ? to_f32(hb[gram_token_of<LIST>(it, item, start, stride, row < count ? row : 0)])
-                    : 1.f;
+        for (int tt = 0; tt < 4; ++tt) {
+          const int row = s * kStep + 16 * tt + r16;
+          hraw[tt] = load_u16_untracked(
+              hb + gram_token_of<LIST>(it, item, start, stride, row < count ? row : 0));
+        }
       }
     }
     if (!ONE && s + 1 < nsteps) {
@@ -877,6 +923,12 @@ __global__ __launch_bounds__(ss::kThreads, (ONE && !FEAT) ? 3 : 2) void gram_str
     }
     lds_barrier();
     if constexpr (FEAT) {
+      float hv[4] = {1.f, 1.f, 1.f, 1.f};
+      if (hb) {
+        asm volatile("" : "+v"(hraw[0]), "+v"(hraw[1]), "+v"(hraw[2]), "+v"(hraw[3]));
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) hv[tt] = to_f32(__builtin_bit_cast(In, (uint16_t)hraw[tt]));
+      }
       uint4* fpsi = BUF ? psi1 : psi0;
       const auto sw = [](int t) { return swz16(t); };
       const float h01[2] = {hv[0], hv[1]}, h23[2] = {hv[2], hv[3]};
