@@ -77,11 +77,6 @@ __device__ __forceinline__ int norm_slot(int t, int w) {
   return t * 8 + 4 * ((w >> 2) ^ ((t >> 3) & 1)) + (w & 3);
 }
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 // Global loads the compiler does not track: their values may be used only
 // after a wait_vmcnt that covers them and an opaque redefinition (asm "+v"),
 // so no compiler-placed wait -- which would be vmcnt(0) with DMA loads and
@@ -102,36 +97,6 @@ __device__ __forceinline__ uint32_t load_u16_untracked(const void* p) {
   uint32_t v;
   asm volatile("global_load_ushort %0, %1, off" : "=&v"(v) : "v"(p) : "memory");
   return v;
-}
-
-// One HBM -> LDS copy of 16 bytes a lane (global_load_lds_dwordx4: lane i
-// writes bytes [16 i, 16 i + 16) from dst, a wave-uniform LDS address).
-// UNTRACKED issues it from inline assembly, so the compiler does not know that
-// an LDS write is in flight.  Tracked, every LDS read it cannot tell apart from
-// the copy's target -- the transposing reads among them -- gets a compiler
-// wait of vmcnt(0) in front, which drains the next step's copy right after it
-// is issued and leaves nothing to overlap with the step's compute.  Untracked,
-// the kernels' own vmcnt waits (loads complete in order) and barriers are what
-// order each read after the copy it reads; loads the compiler does track must
-// then not be pending across such a copy, or their compiler waits (counting
-// only tracked loads) drain it as well.
-template <bool UNTRACKED>
-__device__ __forceinline__ void lds_dma16(const void* src, uint4* dst) {
-  if constexpr (UNTRACKED) {
-    const uint32_t m0 =
-        __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(SMAT_LDS char*)(dst));
-    // m0 (the LDS address) is saved and restored around the copy: the
-    // compiler reserves it and may keep a value of its own there
-    uint32_t keep;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(keep)
-        : "v"(src), "s"(m0)
-        : "memory");
-  } else {
-    __builtin_amdgcn_global_load_lds(src, (SMAT_LDS void*)(SMAT_LDS char*)(dst), 16, 0, 0);
-  }
 }
 
 // 8 bytes of a swizzled 256-byte row (t, chunk k, half h).

@@ -279,4 +279,41 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Wait until at most N vector memory operations of the wave are outstanding
+// (loads and stores complete in the order they were issued).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One HBM -> LDS copy of 16 bytes a lane (global_load_lds_dwordx4: lane i
+// writes bytes [16 i, 16 i + 16) from dst, a wave-uniform LDS address).
+// UNTRACKED issues it from inline assembly, so the compiler does not know that
+// an LDS write is in flight.  Tracked, every LDS read it cannot tell apart from
+// the copy's target -- the transposing reads among them -- gets a compiler
+// wait of vmcnt(0) in front, which drains the copies issued ahead and leaves
+// nothing to overlap with the compute.  Untracked, the kernel's own vmcnt
+// waits and barriers are what order each read after the copy it reads; loads
+// the compiler does track must then not be pending across such a copy, or
+// their compiler waits (counting only tracked loads) drain it as well.  m0
+// (the LDS address) is saved and restored around the copy: the compiler
+// reserves it and may keep a value of its own there.
+template <bool UNTRACKED>
+__device__ __forceinline__ void lds_dma16(const void* src, void* dst) {
+  typedef __attribute__((address_space(3))) char lds_char;
+  if constexpr (UNTRACKED) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_char*)(dst));
+    uint32_t keep;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(keep)
+        : "v"(src), "s"(m0)
+        : "memory");
+  } else {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_char*)(dst),
+                                     16, 0, 0);
+  }
+}
+
 }  // namespace smat
