@@ -576,7 +576,7 @@ int smat_query_lists(int dtype, const void* phi, const float* U, float* Y,
  * kind 1 relu + 1e-3, torch's rounding steps; h (nb, T) the optional key gate,
  * h_sb its batch stride) are formed in LDS by the pool, the query, the
  * prepass and the scan from the Q, K, V tiles they stream, so Phi and Vb
- * never reach memory (when a row type has more than 48 recent rows, the
+ * never reach memory (when a row type has more than 64 recent rows, the
  * recent rows' Phi alone is featurised into the workspace for the general
  * query); the causal pass's prepass stores the Psi rows it forms to the
  * workspace and the scan reads them.  W (128 x 128, features x d_qk) in the

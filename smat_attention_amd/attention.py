@@ -706,7 +706,7 @@ def smat_attention_fused(Q, K, V, phi, spec: MaskSpec, *, g=None, h=None, chunk:
     map(K W^T)`` and ``Vb = [V, 1]`` in LDS from the Q, K, V tiles they stream
     (``smat_forward_fused``), bitwise the features :func:`featurise` writes,
     so the output equals the unfused path's while Phi, Psi and Vb never reach
-    memory (where a row type has more than 48 recent rows, the recent rows'
+    memory (where a row type has more than 64 recent rows, the recent rows'
     Phi alone is featurised for the general query kernel).  Other inputs --
     other widths and dtypes, fewer than 256 (sequence, profile) pools (d = 1)
     -- and inputs that require grad run :func:`featurise` then

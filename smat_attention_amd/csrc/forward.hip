@@ -336,10 +336,10 @@ extern "C" int smat_featurise(int dtype, const void* q, const void* k, const voi
                               int64_t vb_sb, int64_t vb_st, void* stream);
 
 namespace smat {
-// More recent rows a row type than the streaming query's 48: the recent rows'
+// More recent rows a row type than the streaming query's 64: the recent rows'
 // Phi is featurised into the workspace and read by the general query kernel.
 static bool fused_query_staged(int T, int n, int B) {
-  return T > n && (T - n + B - 1) / B > 48;
+  return T > n && (T - n + B - 1) / B > 64;
 }
 // Beyond the forward's layout: the staged recent Phi rows (if any), then the
 // Psi rows the prepass forms and the scan reads (nb x T rows of 128).
@@ -362,7 +362,7 @@ extern "C" int64_t smat_forward_fused_workspace_bytes(int nb, int T, int n, int 
 // Phi = map(Q W^T), Psi = h map(K W^T), Vb = [V, 1] (src/smat/attention.py:82-106)
 // runs inside the pool, the query, the prepass and the scan, on tiles already
 // in LDS, so Phi and Vb are never written to memory -- except, when a row
-// type has more than 48 recent rows (beyond the streaming query), the recent
+// type has more than 64 recent rows (beyond the streaming query), the recent
 // rows' Phi, which is featurised into the workspace for the general query
 // kernel.  Psi is formed once, by the causal pass's prepass, which stores it
 // to the workspace for the scan.  Serves the head-dim-128 streaming shape: 16-bit inputs,

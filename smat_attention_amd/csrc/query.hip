@@ -158,118 +158,181 @@ __global__ __launch_bounds__(qy::kThreads) void query_kernel(
 
 // ---------------------------------------------------------------------------
 // Head-dim-128 variant (16-bit inputs, r = 128, p = 129): persistent
-// workgroups of nine waves walk the (sequence, row type) items.  Each item's
-// U_h (66 KB fp32) and its <= 48 Phi rows (12 KB) are copied HBM -> LDS with
-// global_load_lds_dwordx4, double-buffered: the next item streams in while
-// the current one is multiplied.  The product is taken transposed,
-// Y^T = U_h^T Phi^T: wave w owns column tile w, its A operand is U_h^T read
-// from LDS and split hi/lo, its B operand the Phi rows (row chunks swizzled by
-// row so sixteen rows read without bank conflicts), and each lane ends with
-// four consecutive columns of one row -- 16-byte stores into Y rows padded to
-// 4 floats.
+// workgroups of nine waves walk the (sequence, row type) items, MT 16-row
+// tiles an item (MT = 3: up to 48 rows a type, MT = 4: up to 64).  The product
+// is taken transposed, Y^T = U_h^T Phi^T: wave w owns column tile w, its A
+// operand is U_h^T read from LDS and split hi/lo, its B operand the Phi rows
+// (row chunks swizzled by row so sixteen rows read without bank conflicts),
+// and each lane ends with four consecutive columns of one row -- 16-byte
+// stores into Y rows padded to 4 floats.
+//
+// U_h (66 KB fp32) is copied HBM -> LDS with global_load_lds_dwordx4 in
+// slices of one k-block (32 rows, 16.5 KB) through a ring of slots, the
+// copies of the next slices in flight while one slice is multiplied; an
+// item's Phi rows (12 or 16 KB) go to one of three buffers, copied just
+// before the item's first slice.  Seven slots (six slices, 1.5 items, ahead)
+// beside the three 12 KB Phi buffers; six beside 16 KB ones.  At MT = 3 this
+// runs as fast as two whole-item buffers did (at about 90 % of a device copy's
+// rate), and it leaves room for the fourth row tile, which two whole-item
+// buffers do not (165 KB).
 // ---------------------------------------------------------------------------
 
 namespace qs {
 constexpr int kWaves = 9;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kR = 128, kP = 129;
-constexpr int kUChunks = kR * kP / 4;                     // 16-byte chunks of U_h: 4128
-constexpr int kULoads = (kUChunks + 63) / 64;             // wave-wide DMA loads: 65
-constexpr int kMT = 3;                                    // row tiles: <= 48 rows per type
-constexpr int kPhiLoads = 16 * kMT * 16 / 64;             // 48 rows x 16 chunks: 12
-constexpr int kLoads = kULoads + kPhiLoads;               // 77 per item
-constexpr int kUFloats = kULoads * 256;                   // 16640 (LDS image incl. tail)
+constexpr int kKB = 4;                                    // slices (k-blocks) per item
+constexpr int kSliceChunks = 32 * kP / 4;                 // 16-byte chunks of a slice: 1032
+constexpr int kSliceLoads = (kSliceChunks + 63) / 64;     // wave-wide copies: 17
+constexpr int kSlotFloats = kSliceLoads * 256;            // 4352 (the tail included)
+constexpr int kPhiBufs = 3;
+template <int MT>
+struct Shape {
+  static constexpr int kPhiLoads = 16 * MT * 16 / 64;     // MT x 16 rows x 16 chunks: 12 or 16
+  static constexpr int kPhiChunks = kPhiLoads * 64;
+  static constexpr int kSlots = MT == 3 ? 7 : 6;
+  static constexpr int kAhead = kSlots - 1;               // slices issued ahead
+  static constexpr int kLds = kSlots * kSlotFloats * 4 + kPhiBufs * kPhiChunks * 16;
+  static_assert(kLds <= 160 * 1024, "LDS");
+  // copies wave w issues for a slice and for a Phi block (copies w and w + 9)
+  static constexpr int slice_loads(int w) { return w + kWaves < kSliceLoads ? 2 : 1; }
+  static constexpr int phi_loads(int w) { return w + kWaves < kPhiLoads ? 2 : 1; }
+  static_assert(kSliceLoads <= 2 * kWaves && kPhiLoads <= 2 * kWaves, "two copies a wave");
+  // Phi blocks among slices j + 1 .. j + kAhead - 1 when slice j is k-block kb
+  static constexpr int phi_after(int kb) {
+    int z = 0;
+    for (int k = kb + 1; k < kb + kAhead; ++k) z += k % kKB == 0;
+    return z;
+  }
+  // The slice copies before j + kAhead - 1 and one Phi block each item: with
+  // kAhead slots ahead, item i + kAhead / kKB + 1's Phi copy goes out once
+  // item i's last use of its buffer is past a barrier.
+  static_assert((kAhead + kKB - 1) / kKB + 1 <= kPhiBufs, "Phi buffers in use at once");
+};
 }  // namespace qs
 
-template <typename In>
-__device__ __forceinline__ void query_issue(float* ubuf, uint4* pbuf, const float* U,
-                                            const In* phi, int64_t item, int T_R, int B,
+// The copies of k-block kb of item into a ring slot, preceded, for the first
+// k-block, by the item's Phi rows into pbuf: older than the slice's copies,
+// they have landed whenever the slice has.  Untracked (the waits are the
+// kernel's own); lanes past the slice re-read its first chunk, rows past the
+// type's count its first row.
+template <typename In, int MT>
+__device__ __forceinline__ void query_issue(float* slot, uint4* pbuf, const float* U,
+                                            const In* phi, int64_t item, int kb, int T_R, int B,
                                             int64_t u_ld, int64_t q_sb, int64_t q_st, int w,
                                             int lane) {
   using namespace qs;
-  const int64_t b = item / B;
-  const int h = (int)(item - b * B);
-  const int cnt = (T_R - h + B - 1) / B;
-  const float* Uh = U + item * u_ld;
-  const In* phib = phi + b * q_sb;
+  if (kb == 0) {
+    const int64_t b = item / B;
+    const int h = (int)(item - b * B);
+    const int cnt = (T_R - h + B - 1) / B;
+    const In* phib = phi + b * q_sb;
 #pragma unroll
-  for (int u = 0; u < (kLoads + kWaves - 1) / kWaves; ++u) {
-    const int I = w + kWaves * u;
-    if (I < kLoads) {
-      const void* src;
-      void* dst;
-      if (I < kULoads) {
-        const int c = 64 * I + lane;
-        src = Uh + 4 * (c < kUChunks ? c : 0);
-        dst = ubuf + 256 * I;
-      } else {
-        const int li = I - kULoads;
-        const int row = 4 * li + (lane >> 4);
+    for (int u = 0; u < 2; ++u) {
+      const int I = w + kWaves * u;
+      if (I < Shape<MT>::kPhiLoads) {
+        const int row = 4 * I + (lane >> 4);
         const int k = (lane & 15) ^ (row & 15);
         const int rr = row < cnt ? row : 0;
-        src = phib + ((int64_t)h + (int64_t)rr * B) * q_st + 8 * k;
-        dst = pbuf + 64 * li;
+        lds_dma16<true>(phib + ((int64_t)h + (int64_t)rr * B) * q_st + 8 * k, pbuf + 64 * I);
       }
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(
-                                                __attribute__((address_space(3))) char*)(dst),
-                                       16, 0, 0);
+    }
+  }
+  const float* Us = U + item * u_ld + (int64_t)kb * (32 * kP);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int I = w + kWaves * u;
+    if (I < kSliceLoads) {
+      const int c = 64 * I + lane;
+      lds_dma16<true>(Us + 4 * (c < kSliceChunks ? c : 0), slot + 256 * I);
     }
   }
 }
 
-// FEAT: phi holds Q rows; each item's <= 48 Phi rows are formed in place from
-// the DMA'd Q rows (feat_rows: waves 0..7 one feature tile each, W in
-// registers; wave 8 meets the barriers).
-template <typename In, bool FEAT>
+// Before slice j (k-block KB) is read: the copies issued after its own are
+// those of slices j + 1 .. j + kAhead - 1 and the Phi block of each first
+// slice among them, so waiting down to their number lands slice j and its Phi
+// block.  Three classes of waves issue different numbers of copies.
+template <int MT, int KB>
+__device__ __forceinline__ void query_wait(int w) {
+  using S = qs::Shape<MT>;
+  constexpr int kAfter = S::kAhead - 1;
+  constexpr int z = S::phi_after(KB);
+  constexpr int kP2 = S::kPhiLoads - qs::kWaves;          // waves with two Phi copies
+  static_assert(S::slice_loads(kP2 - 1) == 2 && S::slice_loads(7) == 2 &&
+                    S::slice_loads(8) == 1 && S::phi_loads(kP2) == 1 && kP2 <= 8,
+                "the three wave classes");
+  if (w < kP2)
+    wait_vmcnt<kAfter * 2 + z * 2>();
+  else if (w < 8)
+    wait_vmcnt<kAfter * 2 + z * 1>();
+  else
+    wait_vmcnt<kAfter * 1 + z * 1>();
+}
+
+// FEAT: phi holds Q rows; each item's Phi rows are formed in place from the
+// copied Q rows (feat_rows: waves 0..7 one feature tile each, W in registers;
+// wave 8 meets the barriers).
+template <typename In, bool FEAT, int MT>
 __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
     const In* __restrict__ phi, const float* __restrict__ U, float* __restrict__ Y, int T_R,
     int B, int64_t nitems, int64_t u_ld, int64_t q_sb, int64_t q_st, int64_t y_sb, int64_t y_st,
     FeatArgs fa) {
   using namespace qs;
+  using S = Shape<MT>;
   typedef typename Traits<In>::frag Frag;
-  __shared__ __attribute__((aligned(16))) float u0[kUFloats];
-  __shared__ __attribute__((aligned(16))) float u1[kUFloats];
-  __shared__ __attribute__((aligned(16))) uint4 p0[kPhiLoads * 64];
-  __shared__ __attribute__((aligned(16))) uint4 p1[kPhiLoads * 64];
+  __shared__ __attribute__((aligned(16))) float ring[S::kSlots * kSlotFloats];
+  __shared__ __attribute__((aligned(16))) uint4 pbufs[kPhiBufs * S::kPhiChunks];
   const int w = __builtin_amdgcn_readfirstlane(wave_id());
+  __builtin_assume(w >= 0 && w < kWaves);
   const int64_t G = gridDim.x;
-  int64_t item = blockIdx.x;
-  if (item < nitems)
-    query_issue<In>(u0, p0, U, phi, item, T_R, B, u_ld, q_sb, q_st, w, lane_id());
+  const int64_t item0 = blockIdx.x;
+  const int nmine = item0 < nitems ? (int)((nitems - 1 - item0) / G + 1) : 0;
+  const int nsl = kKB * nmine;                        // slices this workgroup walks
   Frag wa[4];
   if constexpr (FEAT) {
-    if (w < 8) feat_w_load<In>(wa, (const In*)fa.W, w, lane_id());
+    if (w < 8) {
+      feat_w_load<In>(wa, (const In*)fa.W, w, lane_id());
+      // landed here, before any copy: no compiler wait for W inside the loop
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+v"(wa[kb]));
+    }
   }
+  for (int j = 0; j < S::kAhead && j < nsl; ++j)
+    query_issue<In, MT>(ring + j * kSlotFloats, pbufs + ((j / kKB) % kPhiBufs) * S::kPhiChunks,
+                        U, phi, item0 + (int64_t)(j / kKB) * G, j % kKB, T_R, B, u_ld, q_sb,
+                        q_st, w, lane_id());
 
-  auto step = [&](auto BUFC) {
-    constexpr int BUF = decltype(BUFC)::value;
-    const float* us = BUF ? u1 : u0;
-    const uint4* ps = BUF ? p1 : p0;
+  f32x4 acc[MT];
+  int slot = 0;                                       // j mod kSlots
+  int pbi = 0;                                        // (j / kKB) mod kPhiBufs
+  auto step = [&](auto KBC, int j, int64_t item) {
+    constexpr int KB = decltype(KBC)::value;
     int lane = lane_id();
     asm volatile("" : "+v"(lane));
     const int r16 = lane & 15, g = lane >> 4;
-    const int64_t next = item + G;
-    if (next < nitems) {
-      query_issue<In>(BUF ? u0 : u1, BUF ? p0 : p1, U, phi, next, T_R, B, u_ld, q_sb, q_st, w,
-                      lane);
-      if (w < kLoads % kWaves)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads / kWaves + 1) : "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLoads / kWaves) : "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (j + S::kAhead - 1 < nsl)
+      query_wait<MT, KB>(w);
+    else
+      wait_vmcnt<0>();
+    lds_barrier();      // slice j (and its Phi block) is in LDS; slice j - 1's slot is free
+    if (j + S::kAhead < nsl) {
+      // slice j + kAhead: k-block (KB + kAhead) % 4 of the item that many ahead
+      constexpr int kbn = (KB + S::kAhead) % kKB;
+      constexpr int ahead = (KB + S::kAhead) / kKB;
+      const int sn = slot == 0 ? S::kSlots - 1 : slot - 1;
+      const int pn = (pbi + ahead) % kPhiBufs;
+      query_issue<In, MT>(ring + sn * kSlotFloats, pbufs + pn * S::kPhiChunks, U, phi,
+                          item + (int64_t)ahead * G, kbn, T_R, B, u_ld, q_sb, q_st, w, lane);
     }
-    lds_barrier();
-    if constexpr (FEAT) {
-      const float none[kMT] = {};
-      feat_rows<In, kMT>(BUF ? p1 : p0, BUF ? p1 : p0, 0, w < 8, wa, w, fa.kind, false, none,
-                         lane, [](int t) { return t & 15; });
+    uint4* ps = pbufs + pbi * S::kPhiChunks;
+    if constexpr (FEAT && KB == 0) {
+      const float none[MT] = {};
+      feat_rows<In, MT>(ps, ps, 0, w < 8, wa, w, fa.kind, false, none, lane,
+                        [](int t) { return t & 15; });
       lds_barrier();    // the item's Phi rows are complete
     }
-
-    const int64_t b = item / B;
-    const int h = (int)(item - b * B);
-    const int cnt = (T_R - h + B - 1) / B;
+    const float* us = ring + slot * kSlotFloats;
     const int c = 16 * w + r16;
     // Lane group g takes the k-slots of feature group pg of each 32: 0, 2, 1, 3
     // for g = 0..3.  A 4-byte LDS read is served 32 lanes at a time, and U_h
@@ -277,51 +340,57 @@ __global__ __launch_bounds__(qs::kThreads, 1) void query_stream_kernel(
     // apart overlap.  U_h^T and Phi^T agree on the order, so the product is
     // unchanged.
     const int pg = (g >> 1) | ((g & 1) << 1);
-    f32x4 acc[kMT];
+    if constexpr (KB == 0) {
 #pragma unroll
-    for (int t = 0; t < kMT; ++t) acc[t] = zero4();
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      Frag ah, al;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float uv = c < kP ? us[(32 * kb + 8 * pg + e) * kP + c] : 0.f;
-        In hh, ll;
-        split2<In>(uv, hh, ll);
-        ah[e] = hh;
-        al[e] = ll;
-      }
-#pragma unroll
-      for (int t = 0; t < kMT; ++t) {
-        const int row = 16 * t + r16;
-        const Frag pb = *reinterpret_cast<const Frag*>(ps + row * 16 + ((4 * kb + pg) ^ (row & 15)));
-        acc[t] = mma(acc[t], ah, pb);
-        acc[t] = mma(acc[t], al, pb);
-      }
+      for (int t = 0; t < MT; ++t) acc[t] = zero4();
     }
-    float* Yb = Y + b * y_sb;
-    const int c0 = 16 * w + 4 * g;
+    Frag ah, al;
 #pragma unroll
-    for (int t = 0; t < kMT; ++t) {
-      const int k = 16 * t + r16;
-      if (k < cnt) {
-        float* yrow = Yb + ((int64_t)h + (int64_t)k * B) * y_st;
-        if (c0 + 3 < kP) {
-          *reinterpret_cast<float4*>(yrow + c0) = make_float4(acc[t][0], acc[t][1], acc[t][2],
-                                                              acc[t][3]);
-        } else {
+    for (int e = 0; e < 8; ++e) {
+      const float uv = c < kP ? us[(8 * pg + e) * kP + c] : 0.f;
+      In hh, ll;
+      split2<In>(uv, hh, ll);
+      ah[e] = hh;
+      al[e] = ll;
+    }
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (c0 + i < kP) yrow[c0 + i] = acc[t][i];
+    for (int t = 0; t < MT; ++t) {
+      const int row = 16 * t + r16;
+      const Frag pb = *reinterpret_cast<const Frag*>(ps + row * 16 + ((4 * KB + pg) ^ (row & 15)));
+      acc[t] = mma(acc[t], ah, pb);
+      acc[t] = mma(acc[t], al, pb);
+    }
+    if constexpr (KB == kKB - 1) {
+      const int64_t b = item / B;
+      const int h = (int)(item - b * B);
+      const int cnt = (T_R - h + B - 1) / B;
+      float* Yb = Y + b * y_sb;
+      const int c0 = 16 * w + 4 * g;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int k = 16 * t + r16;
+        if (k < cnt) {
+          float* yrow = Yb + ((int64_t)h + (int64_t)k * B) * y_st;
+          if (c0 + 3 < kP) {
+            *reinterpret_cast<float4*>(yrow + c0) =
+                make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (c0 + i < kP) yrow[c0 + i] = acc[t][i];
+          }
         }
       }
+      pbi = pbi == kPhiBufs - 1 ? 0 : pbi + 1;
     }
-    lds_barrier();     // this buffer is free for the DMA issued next step
-    item = next;
+    slot = slot == S::kSlots - 1 ? 0 : slot + 1;
   };
-  while (item < nitems) {
-    step(std::integral_constant<int, 0>{});
-    if (item < nitems) step(std::integral_constant<int, 1>{});
+  for (int j = 0; j < nsl; j += kKB) {
+    const int64_t item = item0 + (int64_t)(j / kKB) * G;
+    step(std::integral_constant<int, 0>{}, j, item);
+    step(std::integral_constant<int, 1>{}, j + 1, item);
+    step(std::integral_constant<int, 2>{}, j + 2, item);
+    step(std::integral_constant<int, 3>{}, j + 3, item);
   }
 }
 
@@ -335,7 +404,7 @@ static bool query_stream_ok(int dtype, const void* phi, const float* U, const fl
                             int64_t y_st) {
   if (dtype != SMAT_BF16 && dtype != SMAT_F16) return false;
   if (r != qs::kR || p != qs::kP) return false;
-  if ((T_R + B - 1) / B > 16 * qs::kMT) return false;        // <= 48 rows per type
+  if ((T_R + B - 1) / B > 64) return false;                 // <= 64 rows per type
   if (!rows_vec_ok(phi, q_sb, q_st, 2) || !aligned16(U) || !rows_vec_ok(Y, y_sb, y_st, 4))
     return false;
   return variant(SMAT_VARIANT_QUERY) == 0;
@@ -405,14 +474,27 @@ static int query_stream_go(int dtype, const void* phi, const float* U, float* Y,
   (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
   const int64_t nitems = (int64_t)nb * B;
   const unsigned grid = (unsigned)std::min<int64_t>(nitems, (int64_t)ncu);
-  if (dtype == SMAT_BF16)
-    smat::launch((query_stream_kernel<bf16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
-                       stream, (const bf16*)phi, U, Y, T_R, B, nitems, u_ld, q_sb, q_st, y_sb,
-                       y_st, fa);
-  else
-    smat::launch((query_stream_kernel<f16, FEAT>), dim3(grid), dim3(qs::kThreads), 0,
-                       stream, (const f16*)phi, U, Y, T_R, B, nitems, u_ld, q_sb, q_st, y_sb,
-                       y_st, fa);
+  // three row tiles up to 48 rows a type, four up to 64
+  const bool four = (T_R + B - 1) / B > 48;
+  if (dtype == SMAT_BF16) {
+    if (four)
+      smat::launch((query_stream_kernel<bf16, FEAT, 4>), dim3(grid), dim3(qs::kThreads), 0,
+                   stream, (const bf16*)phi, U, Y, T_R, B, nitems, u_ld, q_sb, q_st, y_sb, y_st,
+                   fa);
+    else
+      smat::launch((query_stream_kernel<bf16, FEAT, 3>), dim3(grid), dim3(qs::kThreads), 0,
+                   stream, (const bf16*)phi, U, Y, T_R, B, nitems, u_ld, q_sb, q_st, y_sb, y_st,
+                   fa);
+  } else {
+    if (four)
+      smat::launch((query_stream_kernel<f16, FEAT, 4>), dim3(grid), dim3(qs::kThreads), 0,
+                   stream, (const f16*)phi, U, Y, T_R, B, nitems, u_ld, q_sb, q_st, y_sb, y_st,
+                   fa);
+    else
+      smat::launch((query_stream_kernel<f16, FEAT, 3>), dim3(grid), dim3(qs::kThreads), 0,
+                   stream, (const f16*)phi, U, Y, T_R, B, nitems, u_ld, q_sb, q_st, y_sb, y_st,
+                   fa);
+  }
   return launch_status("smat_query");
 }
 

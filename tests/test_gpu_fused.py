@@ -149,6 +149,21 @@ def test_fused_forward_long_prefill_T131072():
     assert e_o < 2e-2 and e_l < 1e-3
 
 
+def test_fused_forward_long_prefill_T524288():
+    """T = 524288, d = 3 (q = 67, the row-group incidence; 57-58 recent rows a
+    row type, the streaming query's four-tile form), one head: the fused call
+    against featurise + smat_attention (1e-5 of the largest entry)."""
+    T = 524288
+    spec = build_mask(T, 3, chunk=128)
+    assert (spec.q, spec.N0, spec.B) == (67, 4489, 4556)
+    _say("fused forward T=524288 d=3 nb=1 hd=128 bf16")
+    Q, K, V, _, _ = _inputs(1, T, seed=2)
+    fused, unfused = _run_both(spec, Q, K, V, None, None)
+    e = _rel(fused, unfused)
+    _say(f"  vs featurise + smat_attention: {e:.2e}")
+    assert torch.isfinite(fused).all() and e < 1e-5
+
+
 def test_fused_forward_falls_back_outside_its_shape_and_under_grad():
     """head_dim 64 (the d=2 single-GPU configuration's width) is not a fused
     shape: smat_attention_fused runs featurise then smat_attention, bitwise the

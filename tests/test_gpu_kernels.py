@@ -234,6 +234,25 @@ def test_query(dt, T, d, r, p):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T_R", [(300, 300 * 48), (300, 300 * 48 + 1), (300, 300 * 64),
+                                   (257, 257 * 57 + 130), (1, 40)])
+def test_query_streaming_rows_per_type(dt, B, T_R):
+    """The streaming query (16-bit Phi, r = 128, p = 129) at the edges of its
+    two tile counts: three 16-row tiles up to 48 rows a type, four up to 64
+    (49 rows for the first type only, 57-58 as at T = 524288, d = 3), and a
+    single type; against fp64 (U enters as hi + lo 16-bit parts)."""
+    from types import SimpleNamespace
+    _say("query streaming rows per type", dt, B, T_R)
+    g = torch.Generator().manual_seed(17)
+    nb = 2
+    Phi = (torch.rand(nb, T_R, 128, generator=g) + 0.5).to(dt)
+    U = torch.randn(nb, B, 128, 129, generator=g)
+    Y = K.query(Phi.to(DEV), U.to(DEV))
+    ref = O.query_by_type(Phi.double(), U.double(), SimpleNamespace(B=B))
+    assert _rel(Y, ref) < 2e-5
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T,d,n_P", [(4096, 3, 0), (8192, 2, 0), (2048, 3, 16), (32768, 3, 0),
                                      (32768, 2, 0), (32768, 2, 16)])
 def test_pool_streaming_head_dim_128(dt, T, d, n_P):
