@@ -467,10 +467,11 @@ using LgMod = LgDiv<Q, 16 * ((Q + 15) / 16) + 16 * Q>;
 // last are dead and store nothing).  Lane j's row part at step t is built from
 // s_t = (s0 + qm t) mod Q with s0 = b0 for a sloped group (s_t = b0 - m t) and
 // s0 = qm = 0 for a vertical one; s advances by d16 over sixteen steps.  lcb + j
-// is lane j's line code (e*q + b).
-template <int Q>
+// is lane j's line code (e*q + b).  PD groups a direction: all q lines by
+// default; q / 16 leaves each direction's last q mod 16 lines to the caller.
+template <int Q, int PD = (Q + 15) / 16>
 struct LgGroup {
-  static constexpr int P = (Q + 15) / 16;
+  static constexpr int P = PD;
   static constexpr int G = (Q + 1) * P;
   int b0, s0, qm, d16, lcb, nvalid, sloped;
   __device__ __forceinline__ explicit LgGroup(int g) {
@@ -823,6 +824,63 @@ __device__ __forceinline__ float4 lr_line_sum(const char* vb, const int* ot) {
   return a;
 }
 
+// A line of its own per lane (the last q mod 16 lines of each direction): at
+// step N the entry c1 N + s_N, s advancing by qm modulo m -- sloped lines
+// c1 = kCW, s_0 = b, qm = q - slope, m = q (x1 = N, x0 = b - slope N mod q);
+// vertical ones c1 = 1, s_0 = kCW b, qm = 0 and an m no sum reaches (the
+// column x1 = b from x0 = 0).  All in bytes (times 16).  Four address
+// instructions a step against the groups' one, for lanes that would otherwise
+// idle in a direction's last group.
+struct LrLane {
+  uint32_t s16, qm16, m16, c16;
+};
+
+template <int N>
+__device__ __forceinline__ void lo_issue(float4& v, const char* pb, LrLane& ln) {
+  v = *reinterpret_cast<const float4*>(pb + (__umul24(ln.c16, (uint32_t)N) + ln.s16));
+  const uint32_t c = ln.s16 + ln.qm16;
+  ln.s16 = min(c, c - ln.m16);
+}
+
+template <int Q, int K>
+__device__ __forceinline__ void lo_issue_batch(float4 (&buf)[3][4], const char* pb, LrLane& ln) {
+  if constexpr (4 * K < Q) lo_issue<4 * K>(buf[K % 3][0], pb, ln);
+  if constexpr (4 * K + 1 < Q) lo_issue<4 * K + 1>(buf[K % 3][1], pb, ln);
+  if constexpr (4 * K + 2 < Q) lo_issue<4 * K + 2>(buf[K % 3][2], pb, ln);
+  if constexpr (4 * K + 3 < Q) lo_issue<4 * K + 3>(buf[K % 3][3], pb, ln);
+}
+
+template <int Q, int K>
+__device__ __forceinline__ void lo_pipe(float4& a, float4 (&buf)[3][4], const char* pb,
+                                        LrLane& ln) {
+  if constexpr (4 * K < Q) {
+    if constexpr (K == 0)
+      a = buf[0][0];
+    else
+      add4(a, buf[K % 3][0]);
+    if constexpr (4 * K + 1 < Q) add4(a, buf[K % 3][1]);
+    if constexpr (4 * K + 2 < Q) add4(a, buf[K % 3][2]);
+    if constexpr (4 * K + 3 < Q) add4(a, buf[K % 3][3]);
+    lr_fence(a);
+    __builtin_amdgcn_sched_barrier(0);
+    lo_issue_batch<Q, K + 3>(buf, pb, ln);
+    __builtin_amdgcn_sched_barrier(0);
+    lo_pipe<Q, K + 1>(a, buf, pb, ln);
+  }
+}
+
+template <int Q>
+__device__ __forceinline__ float4 lo_line_sum(const char* pb, LrLane ln) {
+  float4 buf[3][4];
+  float4 a;
+  lo_issue_batch<Q, 0>(buf, pb, ln);
+  lo_issue_batch<Q, 1>(buf, pb, ln);
+  lo_issue_batch<Q, 2>(buf, pb, ln);
+  __builtin_amdgcn_sched_barrier(0);
+  lo_pipe<Q, 0>(a, buf, pb, ln);
+  return a;
+}
+
 // Slot ps of the panel: ps = 64 * (wave + 16 u) + lane, x1 = ps / q, x0 = ps mod q.
 template <int Q>
 using LrSlot = LgDiv<Q, 64 * ir::kWaves * ir::kPF>;
@@ -844,9 +902,15 @@ __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
   constexpr int N0 = Q * Q;
   constexpr int kCW = Sh::kCW;
   constexpr int nlines = Q * (Q + 1);
-  constexpr int P = (Q + 15) / 16;                   // groups per direction
+  // Fewer than ten lines past a direction's last full group go to lanes of
+  // their own (LrLane) rather than a group with idle lanes.
+  constexpr int R = Q % 16;
+  constexpr bool kOwn = R > 0 && R < 10;
+  constexpr int P = kOwn ? Q / 16 : (Q + 15) / 16;   // groups per direction
   constexpr int G = (Q + 1) * P;                     // groups per item
-  constexpr int NT = (G + 3) / 4;                    // wave tasks (four groups) per item
+  constexpr int NTG = (G + 3) / 4;                   // group tasks (four groups) per item
+  constexpr int NOL = kOwn ? (Q + 1) * R : 0;        // lines of their own
+  constexpr int NT = NTG + (NOL + 63) / 64;          // wave tasks per item
   constexpr int NR = (Q + 15) / 16;                  // runs of sixteen steps
   extern __shared__ float4 smem[];
   short* line_type = reinterpret_cast<short*>(smem + Sh::kEntries);
@@ -922,7 +986,28 @@ __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
     if (HasG && live) g = *reinterpret_cast<const float4*>(Fg + b * rp + e0);
 
     for (int task = wv; task < NT; task += kWaves) {
-      const LgGroup<Q> gr(4 * task + row);           // the lane's own group (per row)
+      if (kOwn && task >= NTG) {
+        // lines of their own: lane l takes line 64 (task - NTG) + l of the
+        // (direction, k) list, line b = 16 P + k of the direction
+        const int li = 64 * (task - NTG) + lane;
+        const bool valid = li < NOL;
+        const int dir = valid ? li / R : 0;
+        const int bl = 16 * P + (valid ? li - dir * R : 0);
+        const bool sl = dir < Q;
+        LrLane ln;
+        ln.s16 = 16u * (uint32_t)(sl ? bl : kCW * bl);
+        ln.qm16 = sl ? 16u * (uint32_t)(Q - dir) : 0u;
+        ln.m16 = sl ? 16u * (uint32_t)Q : 0x80000000u;
+        ln.c16 = 16u * (uint32_t)(sl ? kCW : 1);
+        float4 a = lo_line_sum<Q>(pbase, ln);
+        const int h = valid ? line_type[sl ? (dir + 1) * Q + bl : bl] : -1;
+        if (live && h >= 0) {
+          if (HasG) add4(a, g);
+          *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + (uint32_t)h * ld4) = a;
+        }
+        continue;
+      }
+      const LgGroup<Q, P> gr(4 * task + row);        // the lane's own group (per row)
       const bool valid = j < gr.nvalid;
       const int bl = gr.b0 + j;
       const int col = valid ? bl : (bl >= 16 ? bl - 16 : 0);

@@ -209,9 +209,9 @@ def _wave_staging(q):
     return panel
 
 
-def _group(q, g):
-    """LgGroup<q>(g): (b0, s0, qm, d16, lcb, nvalid, sloped)."""
-    P = (q + 15) // 16
+def _group(q, g, P=None):
+    """LgGroup<q, P>(g): (b0, s0, qm, d16, lcb, nvalid, sloped)."""
+    P = (q + 15) // 16 if P is None else P
     G = (q + 1) * P
     d = g // P
     b0 = (g - d * P) * 16
@@ -363,19 +363,46 @@ def _row_staging(q):
     return panel
 
 
+def _row_plan(q):
+    """(P, G, NTG, R, NOL) of incidence_row_kernel<q>: groups a direction, groups,
+    group tasks, and, when fewer than ten lines follow a direction's last full
+    group, those R lines a direction taken one a lane (NOL of them)."""
+    R = q % 16
+    own = 0 < R < 10
+    P = q // 16 if own else (q + 15) // 16
+    G = (q + 1) * P
+    return P, G, (G + 3) // 4, R, ((q + 1) * R if own else 0)
+
+
 def _row_reads(q):
     """Yield (group, lane j, step, entry, line code) for every read of the
-    row-group kernel: row k of wave task n takes group 4 n + k."""
+    row-group kernel: row k of group task n takes group 4 n + k; the lines of
+    their own are yielded as group ("own", line index), lane 0."""
     cw, _, _ = _row_shape(q)
-    P = (q + 15) // 16
-    G = (q + 1) * P
-    NT = (G + 3) // 4
+    P, G, NTG, R, NOL = _row_plan(q)
     NR = (q + 15) // 16
-    M, S = _lgdiv(q, 16 * P + 16 * q)
-    for task in range(NT):
+    M, S = _lgdiv(q, 16 * ((q + 15) // 16) + 16 * q)
+    for li in range(((NOL + 63) // 64) * 64):
+        # LrLane: entry c1 N + s_N, s advancing by qm modulo m (32-bit unsigned)
+        valid = li < NOL
+        d = li // R if valid else 0
+        b = 16 * P + (li - d * R if valid else 0)
+        sl = d < q
+        s16 = 16 * (b if sl else cw * b)
+        qm16 = 16 * (q - d) if sl else 0
+        m16 = 16 * q if sl else 0x80000000
+        c16 = 16 * (cw if sl else 1)
+        code = ((d + 1) * q + b if sl else b) if valid else None
+        for t in range(q):
+            addr = c16 * t + s16
+            assert addr % 16 == 0 and c16 * t < (1 << 24)
+            yield ("own", li), 0, t, addr // 16, code
+            c = (s16 + qm16) % _U32
+            s16 = min(c, (c - m16) % _U32)
+    for task in range(NTG):
         for row in range(4):
             grp = 4 * task + row
-            b0, s0, qm, d16, lcb, nvalid, sloped = _group(q, grp)
+            b0, s0, qm, d16, lcb, nvalid, sloped = _group(q, grp, P)
             ot = {}
             for l in range(16):
                 x = s0 + qm * l
@@ -408,15 +435,22 @@ def test_row_group_incidence_reads_each_line_once_in_bounds(q):
     assert lds <= 160 * 1024 and q * q <= _KPF * _KTHREADS
     panel = _row_staging(q)
     assert len(panel) == q * (q + 15) and max(panel) < entries
-    P = (q + 15) // 16
-    G = (q + 1) * P
+    P, G, NTG, R, NOL = _row_plan(q)
     got, codes, phases = {}, {}, {}
     for grp, j, t, e, lc in _row_reads(q):
         assert 0 <= e < entries and e in panel
         got.setdefault((grp, j), []).append(panel[e])
         codes[grp, j] = lc
-        phases.setdefault((grp, t), set()).add(e % 16)
-    assert all(len(v) == 16 for v in phases.values())   # one bank phase a lane
+        if not isinstance(grp, tuple):
+            phases.setdefault((grp, t), set()).add(e % 16)
+    assert all(len(v) == 16 for v in phases.values())   # one bank phase a group row
+
+    def want(dirn, b):
+        if dirn < q:
+            return sorted(((b - dirn * t) % q) * q + t for t in range(q)), (dirn + 1) * q + b
+        return sorted(x0 * q + b for x0 in range(q)), b
+
+    stored = {}
     for grp in range(G):
         dirn, part = divmod(grp, P)
         for j in range(16):
@@ -424,10 +458,16 @@ def test_row_group_incidence_reads_each_line_once_in_bounds(q):
             if b >= q:
                 assert codes[grp, j] is None
                 continue
-            if dirn < q:
-                want = sorted(((b - dirn * t) % q) * q + t for t in range(q))
-                assert codes[grp, j] == (dirn + 1) * q + b
-            else:
-                want = sorted(x0 * q + b for x0 in range(q))
-                assert codes[grp, j] == b
-            assert sorted(got[grp, j]) == want
+            pts, code = want(dirn, b)
+            assert codes[grp, j] == code and sorted(got[grp, j]) == pts
+            stored[code] = stored.get(code, 0) + 1
+    for li in range(((NOL + 63) // 64) * 64):
+        if li >= NOL:
+            assert codes[("own", li), 0] is None
+            continue
+        dirn, k = divmod(li, R)
+        pts, code = want(dirn, 16 * P + k)
+        assert codes[("own", li), 0] == code and sorted(got[("own", li), 0]) == pts
+        stored[code] = stored.get(code, 0) + 1
+    # every line of the plane stored exactly once
+    assert sorted(stored) == list(range(q * (q + 1))) and set(stored.values()) == {1}
