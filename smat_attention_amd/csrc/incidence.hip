@@ -518,6 +518,96 @@ static int64_t wave_lds_bytes(int q) {
   return (int64_t)iw::kPlanes * iw::kPlane * 16 + (((int64_t)q * (q + 1) * 2 + 15) & ~15);
 }
 
+// A line of its own per lane (the last q mod 16 lines of each direction, when
+// fewer than ten): at step N the entry c1 N + s_N (kCW entries a column), s
+// advancing by qm modulo m -- sloped lines c1 = kCW, s_0 = b, qm = q - slope,
+// m = q (x1 = N, x0 = b - slope N mod q); vertical ones c1 = 1, s_0 = kCW b,
+// qm = 0 and an m no sum reaches (the column x1 = b from x0 = 0).  All in
+// bytes (times 16).  Four address instructions a step against a group's one,
+// for lanes that would otherwise idle in a direction's last group.
+struct LrLane {
+  uint32_t s16, qm16, m16, c16;
+};
+
+// The line-group kernel's lines of their own take all four planes: two
+// addresses a step (planes 2 and 3 lie past the 16-bit read offset), four
+// 16-byte reads and sixteen adds; two steps in flight.
+typedef __attribute__((address_space(3))) const float lds_cfloat;
+typedef float lds_f4v __attribute__((ext_vector_type(4)));
+// 16 bytes at LDS address addr (16-byte aligned: one ds_read_b128)
+__device__ __forceinline__ float4 lds_at(uint32_t addr) {
+  const lds_f4v v = *(__attribute__((address_space(3))) const lds_f4v*)(size_t)addr;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+// pb: the panel's LDS address
+template <int N>
+__device__ __forceinline__ void lw_issue(float4 (&v)[4], uint32_t pb, LrLane& ln) {
+  const uint32_t a = pb + __umul24(ln.c16, (uint32_t)N) + ln.s16;
+  // planes 2 and 3 from a second base: opaque, so plane 3 stays an immediate
+  // offset from it rather than a third address
+  uint32_t a2 = a + 2 * iw::kPlaneBytes;
+  asm volatile("" : "+v"(a2));
+  v[0] = lds_at(a);
+  v[1] = lds_at(a + iw::kPlaneBytes);
+  v[2] = lds_at(a2);
+  v[3] = lds_at(a2 + iw::kPlaneBytes);
+  const uint32_t c = ln.s16 + ln.qm16;
+  ln.s16 = min(c, c - ln.m16);
+}
+
+__device__ __forceinline__ void lw_fence(float4 (&a)[4]) {
+  asm volatile("" : "+v"(a[0].x), "+v"(a[0].y), "+v"(a[0].z), "+v"(a[0].w), "+v"(a[1].x),
+               "+v"(a[1].y), "+v"(a[1].z), "+v"(a[1].w)::"memory");
+  asm volatile("" : "+v"(a[2].x), "+v"(a[2].y), "+v"(a[2].z), "+v"(a[2].w), "+v"(a[3].x),
+               "+v"(a[3].y), "+v"(a[3].z), "+v"(a[3].w)::"memory");
+}
+
+// Sum step N (in order 0 .. Q-1), then issue step N + 1 into its registers.
+template <int Q, int N>
+__device__ __forceinline__ void lw_pipe(float4 (&a)[4], float4 (&buf)[4], uint32_t pb,
+                                        LrLane& ln) {
+  if constexpr (N < Q) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if constexpr (N == 0)
+        a[p] = buf[p];
+      else
+        add4(a[p], buf[p]);
+    }
+    lw_fence(a);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (N + 1 < Q) lw_issue<N + 1>(buf, pb, ln);
+    __builtin_amdgcn_sched_barrier(0);
+    lw_pipe<Q, N + 1>(a, buf, pb, ln);
+  }
+}
+
+template <int Q>
+__device__ __forceinline__ void lw_line_sums(float4 (&a)[4], uint32_t pb, LrLane ln) {
+  float4 buf[4];
+  lw_issue<0>(buf, pb, ln);
+  __builtin_amdgcn_sched_barrier(0);
+  lw_pipe<Q, 0>(a, buf, pb, ln);
+}
+
+// The lane state of line li of the lines of their own: R of them a direction,
+// after the P full groups' 16 P lines.  Lanes past NOL walk column 0 and store
+// nothing.
+template <int Q, int P, int R, int NOL, int kCW>
+__device__ __forceinline__ LrLane own_lane(int li, int& code) {
+  const bool valid = li < NOL;
+  const int dir = valid ? li / R : 0;
+  const int bl = 16 * P + (valid ? li - dir * R : 0);
+  const bool sl = dir < Q;
+  LrLane ln;
+  ln.s16 = 16u * (uint32_t)(sl ? bl : kCW * bl);
+  ln.qm16 = sl ? 16u * (uint32_t)(Q - dir) : 0u;
+  ln.m16 = sl ? 16u * (uint32_t)Q : 0x80000000u;
+  ln.c16 = 16u * (uint32_t)(sl ? kCW : 1);
+  code = valid ? (sl ? (dir + 1) * Q + bl : bl) : -1;
+  return ln;
+}
+
 template <int Q, bool HasG>
 __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
     const float* __restrict__ F, const float* __restrict__ Fg, const int* __restrict__ code,
@@ -527,9 +617,18 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
   constexpr int q = Q;
   constexpr int N0 = Q * Q;
   constexpr int nlines = Q * (Q + 1);
-  constexpr int P = (Q + kGroup - 1) / kGroup;       // groups per direction
+  // Past 16 lines a direction, fewer than ten lines after its last full group
+  // go to lanes of their own (LrLane, all four planes) rather than a group
+  // with idle lanes; those tasks all fall in one slot k = kOwnK of every wave.
+  constexpr int R = Q % kGroup;
+  constexpr bool kOwn = Q > kGroup && R > 0 && R < 10;
+  constexpr int P = kOwn ? Q / kGroup : (Q + kGroup - 1) / kGroup;   // groups per direction
   constexpr int G = (Q + 1) * P;                     // groups per item
-  constexpr int NT = (G + 1) / 2;                    // wave tasks (two groups) per item
+  constexpr int NTG = (G + 1) / 2;                   // group tasks (two groups) per item
+  constexpr int NOL = kOwn ? (Q + 1) * R : 0;        // lines of their own
+  constexpr int NT = NTG + (NOL + 63) / 64;          // wave tasks per item
+  constexpr int kOwnK = NTG / kWaves;
+  static_assert(!kOwn || (NT - 1) / kWaves == kOwnK, "lines of their own in one task slot");
   constexpr int NR = (Q + 15) / 16;                  // runs of sixteen steps
   extern __shared__ float4 smem[];
   short* line_type = reinterpret_cast<short*>(smem + (size_t)kPlanes * kPlane);
@@ -598,9 +697,20 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
 #pragma unroll
   for (int k = 0; k < kTasks; ++k) {
     const int task = wv + kWaves * k;                // past NT: dead, never summed
+    if (kOwn && k == kOwnK && task >= NTG) {
+      // a line of its own: s_0 in tvb, qm in tot[0] (c1 and m follow from
+      // qm, zero only for vertical lines), its U row's byte offset in tsA
+      int lc;
+      const LrLane ln = own_lane<Q, P, R, NOL, kCW>(64 * (task - NTG) + lane, lc);
+      const int h = lc >= 0 ? line_type[lc] : -1;
+      tvb[k] = (int)ln.s16;
+      tot[k][0] = (int)ln.qm16;
+      tsA[k] = h >= 0 ? (uint32_t)h * ld4 : kNoLine;
+      continue;
+    }
     // The task's groups 2 task (rows 0-1) and 2 task + 1 (rows 2-3) are
     // worked out on the scalar unit; each lane then takes its own.
-    LgGroup<Q> gA(2 * task), gB(2 * task + 1);
+    LgGroup<Q, P> gA(2 * task), gB(2 * task + 1);
     gA.opaque();                                     // select the values, not their
     gB.opaque();                                     // derivation, per lane
     const int b0 = gsel ? gB.b0 : gA.b0;
@@ -666,6 +776,30 @@ __global__ __launch_bounds__(iw::kThreads, 1) void incidence_wave_kernel(
 #pragma unroll
     for (int k = 0; k < kTasks; ++k) {
       if (wv + kWaves * k >= NT) continue;
+      if (kOwn && k == kOwnK && wv + kWaves * k >= NTG) {
+        // s_0 passes through an empty asm each item: the walk depends on no
+        // load, and hoisted out of the item loop its q addresses would all
+        // stay live (and spill)
+        LrLane ln;
+        ln.s16 = (uint32_t)tvb[k];
+        ln.qm16 = (uint32_t)tot[k][0];
+        asm volatile("" : "+v"(ln.s16), "+v"(ln.qm16));
+        ln.m16 = ln.qm16 ? 16u * Q : 0x80000000u;
+        ln.c16 = ln.qm16 ? 16u * kCW : 16u;
+        float4 a[4];
+        lw_line_sums<Q>(a, (uint32_t)(size_t)(lds_cfloat*)(smem), ln);
+        if (tsA[k] != kNoLine) {
+          char* urow = const_cast<char*>(Ubase) + tsA[k];
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            if (e0 + 4 * p < rp) {                   // rp % 4 == 0: whole planes
+              if (HasG) add4(a[p], *reinterpret_cast<const float4*>(Fg + b * rp + e0 + 4 * p));
+              *reinterpret_cast<float4*>(urow + 16 * p) = a[p];
+            }
+          }
+        }
+        continue;
+      }
       float4 a0, a1;
       lg_line_sums<Q>(a0, a1, pbase + tvb[k], tot[k]);
       // Rows 0-3 hold planes (0, 1) and (2, 3) of group A, then of group B, in
@@ -824,16 +958,7 @@ __device__ __forceinline__ float4 lr_line_sum(const char* vb, const int* ot) {
   return a;
 }
 
-// A line of its own per lane (the last q mod 16 lines of each direction): at
-// step N the entry c1 N + s_N, s advancing by qm modulo m -- sloped lines
-// c1 = kCW, s_0 = b, qm = q - slope, m = q (x1 = N, x0 = b - slope N mod q);
-// vertical ones c1 = 1, s_0 = kCW b, qm = 0 and an m no sum reaches (the
-// column x1 = b from x0 = 0).  All in bytes (times 16).  Four address
-// instructions a step against the groups' one, for lanes that would otherwise
-// idle in a direction's last group.
-struct LrLane {
-  uint32_t s16, qm16, m16, c16;
-};
+// The row-group kernel's lines of their own (LrLane), one plane a lane.
 
 template <int N>
 __device__ __forceinline__ void lo_issue(float4& v, const char* pb, LrLane& ln) {
@@ -989,18 +1114,10 @@ __global__ __launch_bounds__(ir::kThreads, 1) void incidence_row_kernel(
       if (kOwn && task >= NTG) {
         // lines of their own: lane l takes line 64 (task - NTG) + l of the
         // (direction, k) list, line b = 16 P + k of the direction
-        const int li = 64 * (task - NTG) + lane;
-        const bool valid = li < NOL;
-        const int dir = valid ? li / R : 0;
-        const int bl = 16 * P + (valid ? li - dir * R : 0);
-        const bool sl = dir < Q;
-        LrLane ln;
-        ln.s16 = 16u * (uint32_t)(sl ? bl : kCW * bl);
-        ln.qm16 = sl ? 16u * (uint32_t)(Q - dir) : 0u;
-        ln.m16 = sl ? 16u * (uint32_t)Q : 0x80000000u;
-        ln.c16 = 16u * (uint32_t)(sl ? kCW : 1);
+        int lc;
+        const LrLane ln = own_lane<Q, P, R, NOL, kCW>(64 * (task - NTG) + lane, lc);
         float4 a = lo_line_sum<Q>(pbase, ln);
-        const int h = valid ? line_type[sl ? (dir + 1) * Q + bl : bl] : -1;
+        const int h = lc >= 0 ? line_type[lc] : -1;
         if (live && h >= 0) {
           if (HasG) add4(a, g);
           *reinterpret_cast<float4*>(const_cast<char*>(Ubase) + (uint32_t)h * ld4) = a;

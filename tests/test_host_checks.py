@@ -222,21 +222,59 @@ def _group(q, g, P=None):
         (min(16, q - b0) if g < G else 0), sloped
 
 
+def _wave_plan(q):
+    """(P, G, NTG, R, NOL) of incidence_wave_kernel<q>: groups a direction, groups,
+    group tasks (two groups each), and, past 16 lines a direction with fewer
+    than ten after its last full group, those R lines a direction taken one a
+    lane over all four planes (NOL of them)."""
+    R = q % 16
+    own = q > 16 and 0 < R < 10
+    P = q // 16 if own else (q + 15) // 16
+    G = (q + 1) * P
+    return P, G, (G + 1) // 2, R, ((q + 1) * R if own else 0)
+
+
+def _own_lane_reads(q, cw, P, R, NOL, plane_entries):
+    """Yield (("own", li), 0, plane, t, entry, line code) for the lines of their
+    own: own_lane's LrLane walk (entry c1 N + s_N, s advancing by qm modulo m,
+    32-bit unsigned), m and c1 rebuilt from qm (zero only for vertical lines)
+    as the kernel does; the lanes of the last task past NOL included."""
+    for li in range(((NOL + 63) // 64) * 64):
+        valid = li < NOL
+        d = li // R if valid else 0
+        b = 16 * P + (li - d * R if valid else 0)
+        sl = d < q
+        s16 = 16 * (b if sl else cw * b)
+        qm16 = 16 * (q - d) if sl else 0
+        m16 = 16 * q if qm16 else 0x80000000
+        c16 = 16 * cw if qm16 else 16
+        code = ((d + 1) * q + b if sl else b) if valid else None
+        for t in range(q):
+            addr = c16 * t + s16
+            assert addr % 16 == 0 and c16 * t < (1 << 24)
+            for plane in range(len(plane_entries)):
+                yield ("own", li), 0, plane, t, addr // 16 + plane_entries[plane], code
+            c = (s16 + qm16) % _U32
+            s16 = min(c, (c - m16) % _U32)
+
+
 def _wave_reads(q):
     """Yield (group, lane j, plane, pp, step, entry, line code) for every read the
     kernel makes, by its own arithmetic: rows 0, 1 of a wave task take group
     2 task (plane pairs (0, 1), (2, 3)), rows 2, 3 group 2 task + 1; a row's lane
     l computes ot[run] for step 16 run + l, and step t takes lane t % 16's value
-    of its own row."""
-    P = (q + 15) // 16
-    G = (q + 1) * P
-    NT = (G + 1) // 2
+    of its own row.  The lines of their own (_own_lane_reads) come first, with
+    pp = None."""
+    P, G, NTG, R, NOL = _wave_plan(q)
     NR = (q + 15) // 16
-    M, S = _lgdiv(q, 16 * P + 16 * q)
-    for task in range(NT):
+    M, S = _lgdiv(q, 16 * ((q + 15) // 16) + 16 * q)
+    planes = [k * _KPLANE for k in range(_KPLANES)]
+    for grp, j, plane, t, e, lc in _own_lane_reads(q, _KCW, P, R, NOL, planes):
+        yield grp, j, plane, None, t, e, lc
+    for task in range(NTG):
         for gsel in range(2):
             grp = 2 * task + gsel
-            b0, s0, qm, d16, lcb, nvalid, sloped = _group(q, grp)
+            b0, s0, qm, d16, lcb, nvalid, sloped = _group(q, grp, P)
             ot = {}
             for l in range(16):
                 x = s0 + qm * l
@@ -271,14 +309,23 @@ def test_line_group_incidence_reads_each_line_once_in_bounds(q):
     vertical line b the column x1 = b -- and stores under its own line code."""
     panel = _wave_staging(q)
     assert max(panel) < _KPLANES * _KPLANE
-    P = (q + 15) // 16
-    G = (q + 1) * P
+    P, G, NTG, R, NOL = _wave_plan(q)
+    # the lines of their own sit in one task slot of the waves (kOwnK)
+    NT = NTG + (NOL + 63) // 64
+    assert NOL == 0 or (NT - 1) // _KWAVES == NTG // _KWAVES
     got, codes = {}, {}
     for grp, j, plane, pp, t, e, lc in _wave_reads(q):
         assert 0 <= e < _KPLANES * _KPLANE and e in panel
         assert e // _KPLANE == plane
         got.setdefault((grp, j, plane), []).append(panel[e])
         codes[grp, j] = lc
+
+    def want(dirn, b):
+        if dirn < q:                                            # e = m + 1
+            return sorted(((b - dirn * t) % q) * q + t for t in range(q)), (dirn + 1) * q + b
+        return sorted(x0 * q + b for x0 in range(q)), b        # e = 0
+
+    stored = {}
     for grp in range(G):
         dirn, part = divmod(grp, P)
         for j in range(16):
@@ -286,14 +333,23 @@ def test_line_group_incidence_reads_each_line_once_in_bounds(q):
             if b >= q:
                 assert codes[grp, j] is None
                 continue
-            if dirn < q:
-                want = sorted(((b - dirn * t) % q) * q + t for t in range(q))
-                assert codes[grp, j] == (dirn + 1) * q + b      # e = m + 1
-            else:
-                want = sorted(x0 * q + b for x0 in range(q))
-                assert codes[grp, j] == b                       # e = 0
+            pts, code = want(dirn, b)
+            assert codes[grp, j] == code
             for plane in range(_KPLANES):
-                assert sorted(got[grp, j, plane]) == want
+                assert sorted(got[grp, j, plane]) == pts
+            stored[code] = stored.get(code, 0) + 1
+    for li in range(((NOL + 63) // 64) * 64):
+        if li >= NOL:
+            assert codes[("own", li), 0] is None
+            continue
+        dirn, k = divmod(li, R)
+        pts, code = want(dirn, 16 * P + k)
+        assert codes[("own", li), 0] == code
+        for plane in range(_KPLANES):
+            assert sorted(got[("own", li), 0, plane]) == pts
+        stored[code] = stored.get(code, 0) + 1
+    # every line of the plane stored exactly once
+    assert sorted(stored) == list(range(q * (q + 1))) and set(stored.values()) == {1}
 
 
 @pytest.mark.parametrize("q", [17, 29, 37, 41])
@@ -304,6 +360,8 @@ def test_line_group_incidence_rows_read_one_bank_phase_each(q):
     group) read at the same phases, the pattern ds_read_b128 serves at full rate."""
     rows = {}
     for grp, j, plane, pp, t, e, lc in _wave_reads(q):
+        if pp is None:                                   # lines of their own
+            continue
         rows.setdefault((grp, plane - 2 * pp, pp, t), {})[j] = e
     for (grp, half, pp, t), lanes in rows.items():
         assert sorted(e % 16 for e in lanes.values()) == list(range(16))
@@ -382,23 +440,8 @@ def _row_reads(q):
     P, G, NTG, R, NOL = _row_plan(q)
     NR = (q + 15) // 16
     M, S = _lgdiv(q, 16 * ((q + 15) // 16) + 16 * q)
-    for li in range(((NOL + 63) // 64) * 64):
-        # LrLane: entry c1 N + s_N, s advancing by qm modulo m (32-bit unsigned)
-        valid = li < NOL
-        d = li // R if valid else 0
-        b = 16 * P + (li - d * R if valid else 0)
-        sl = d < q
-        s16 = 16 * (b if sl else cw * b)
-        qm16 = 16 * (q - d) if sl else 0
-        m16 = 16 * q if sl else 0x80000000
-        c16 = 16 * (cw if sl else 1)
-        code = ((d + 1) * q + b if sl else b) if valid else None
-        for t in range(q):
-            addr = c16 * t + s16
-            assert addr % 16 == 0 and c16 * t < (1 << 24)
-            yield ("own", li), 0, t, addr // 16, code
-            c = (s16 + qm16) % _U32
-            s16 = min(c, (c - m16) % _U32)
+    for grp, j, _, t, e, lc in _own_lane_reads(q, cw, P, R, NOL, [0]):
+        yield grp, j, t, e, lc
     for task in range(NTG):
         for row in range(4):
             grp = 4 * task + row
