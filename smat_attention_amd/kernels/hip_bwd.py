@@ -406,6 +406,9 @@ def smat_attention_grad(Phi, Psi, Vb, spec, U, H, dout, *, chunk: int = 128, g=N
              Vv.stride(0), Vv.stride(1), dF.stride(0), dPsi.stride(0), dPsi.stride(1),
              dVb.stride(0), dVb.stride(1), 1, st)
     elif T_R > 0:
+        # the products below address Phi, Psi and Vb as dense rows (the
+        # feature map's Vb rows are padded to 8 elements)
+        Ph, Ps, Vv = (x.contiguous() for x in (Ph, Ps, Vv))
         Uc = U.float().contiguous()
         dU = _type_read_grad(Ph, dH, Uc, dPhi, Tp, n, T_R, B)
         # dF = C^T dU (and the global channel's sum over all types)

@@ -144,6 +144,31 @@ def test_backward_head_dim_128(dt, d, n_P, gate):
         assert e < 2e-2 and e64 < 2e-2, name
 
 
+@pytest.mark.parametrize("n_P", [0, 16])
+def test_backward_head_dim_128_padded_value_rows(n_P):
+    """Vb as the feature map stores it at head_dim 128: rows of 129 values in
+    a buffer of 136-element rows, the padding holding NaN.  Every gradient
+    equals the one of the same values in dense rows (the pool's and the global
+    channel's products must address Vb by its own row stride)."""
+    T, hd, nb = 2048, 128, 2
+    _say("backward head_dim 128 padded Vb rows", n_P)
+    spec = build_mask(T, 3, chunk=128, n_P=n_P)
+    Phi, Psi, Vb = (x.to(torch.bfloat16) for x in _feats(nb, T, hd, seed=41, k_scale=hd ** -0.5))
+    w = torch.randn(nb, T, hd, generator=torch.Generator().manual_seed(42)).to(DEV)
+    buf = torch.full((nb, T, 136), float("nan"), device=DEV, dtype=torch.bfloat16)
+    buf[..., :hd + 1] = Vb.to(DEV)
+    res = []
+    for v in (buf[..., :hd + 1], Vb.to(DEV).contiguous()):
+        xs = [Phi.to(DEV).requires_grad_(True), Psi.to(DEV).requires_grad_(True),
+              v.detach().requires_grad_(True)]
+        (A.smat_attention(*xs, spec) * w).sum().backward()
+        res.append([x.grad.float().cpu() for x in xs])
+    assert res[0][2].shape == (nb, T, hd + 1)
+    for name, a, b in zip(("dPhi", "dPsi", "dVb"), *res):
+        assert torch.isfinite(a).all(), name
+        assert torch.equal(a, b), name
+
+
 @pytest.mark.parametrize("T,d,n_P,gate", [(2048, 3, 0, False), (2048, 3, 16, True),
                                           (1024, 2, 0, True)])
 def test_parts_and_timer_under_autograd(T, d, n_P, gate):
