@@ -684,9 +684,12 @@ def _fused_ok(Q, K, V, phi, spec, C, h) -> bool:
     if C not in (64, 128) or T % 64 or spec.n % C:
         return False
     # the fused pool runs one workgroup per (sequence, profile): with fewer than
-    # 256 of them (d = 1: one profile a sequence) the unfused pool's split-K
-    # reduction is the faster path
-    if T > spec.n and spec.n > spec.n_P and nb * spec.N0 < 256:
+    # 256 of them the unfused pool's split-K reduction is the faster path --
+    # except for one profile holding every landmark token (d = 1, no global
+    # channel), whose pool the fused forward takes from the causal pass's
+    # group sums
+    one_profile = spec.N0 == 1 and spec.B == 1 and spec.n_P == 0
+    if T > spec.n and spec.n > spec.n_P and nb * spec.N0 < 256 and not one_profile:
         return False
     for t in (Q, K, V):
         if t.stride(-1) != 1 or t.stride(1) % 8 or t.stride(0) % 8 or t.data_ptr() % 16:
@@ -707,10 +710,11 @@ def smat_attention_fused(Q, K, V, phi, spec: MaskSpec, *, g=None, h=None, chunk:
     (``smat_forward_fused``), bitwise the features :func:`featurise` writes,
     so the output equals the unfused path's while Phi, Psi and Vb never reach
     memory (where a row type has more than 64 recent rows, the recent rows'
-    Phi alone is featurised for the general query kernel).  Other inputs --
-    other widths and dtypes, fewer than 256 (sequence, profile) pools (d = 1)
-    -- and inputs that require grad run :func:`featurise` then
-    :func:`smat_attention`.  Returns fp32 (nb, T, d_v).
+    Phi alone is featurised for the general query kernel; d = 1's single
+    profile is pooled from the causal pass's group sums).  Other inputs --
+    other widths and dtypes, fewer than 256 (sequence, profile) pools with
+    more than one profile or a global channel -- and inputs that require grad
+    run :func:`featurise` then :func:`smat_attention`.  Returns fp32 (nb, T, d_v).
     """
     who = "smat_attention_fused"
     _hip._on_gpu(who, Q, K, V, g, h)

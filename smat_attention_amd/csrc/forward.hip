@@ -83,7 +83,8 @@ int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v,
                          int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
                          int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
                          int64_t g_sb, const FeatArgs& fa, void* ws, int64_t ws_bytes,
-                         void* psi_buf, hipStream_t stream);
+                         void* psi_buf, float* F_out, int64_t f_sb, int phases,
+                         hipStream_t stream);
 int64_t causal_scan_workspace_bytes(int nb, int T, int C, int r, int p);
 int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void* vb,
                          const float* Y, const float* gate, float* out, int nb, int T, int n,
@@ -423,19 +424,29 @@ extern "C" int smat_forward_fused(int dtype, const void* q, const void* k, const
   const FeatArgs fa{W, h, h_sb, kind};
   int rc;
 
+  void* psi_rows = ws + L.total + fused_phi_bytes(nb, T, n, B);
+  // One profile holding every landmark token (d = 1, no global channel, the
+  // identity incidence): its pool is the sum of the causal pass's group sums
+  // over the tokens [0, n), so the prepass runs first and no pool pass is made.
+  const bool pool_from_prepass = T_R > 0 && !idx && N0 == 1 && n_P == 0 && n > 0;
   if (T_R > 0) {
     const bool profiled = n > n_P;
     // row stride of F and U
     const int64_t ld =
         idx && plane_code && profiled ? incidence_plane_ld(field_q, N0, B, rp) : rp;
-    GramItems it{};
-    it.mode = 1;
-    it.n_P = n_P;
-    it.n = n;
-    it.N0 = N0;
-    it.nsplit = 1;
-    it.per = 1 << 30;
-    {
+    if (pool_from_prepass) {
+      StageScope stage(0);
+      rc = causal_scan_run_feat(dtype, q, k, v, nullptr, g, out, nb, T, n, C, q_sb, q_st, k_sb,
+                                k_st, v_sb, v_st, (int64_t)T_R * yst, yst, o_sb, o_st, g_sb, fa,
+                                ws + L.scan, L.part - L.scan, psi_rows, F, ld, 1, st);
+    } else {
+      GramItems it{};
+      it.mode = 1;
+      it.n_P = n_P;
+      it.n = n;
+      it.N0 = N0;
+      it.nsplit = 1;
+      it.per = 1 << 30;
       StageScope stage(0);
       rc = gram_stream_launch_feat(dtype, k, v, F, Fg, it, N0 + (Fg ? 1 : 0), nb, k_sb, k_st,
                                    v_sb, v_st, (int64_t)N0 * ld, ld, rp, fa, st,
@@ -473,8 +484,8 @@ extern "C" int smat_forward_fused(int dtype, const void* q, const void* k, const
     if (rc) return rc;
   }
   StageScope stage(3);
-  void* psi_rows = ws + L.total + fused_phi_bytes(nb, T, n, B);
   return causal_scan_run_feat(dtype, q, k, v, T_R > 0 ? Y : nullptr, g, out, nb, T, n, C, q_sb,
                               q_st, k_sb, k_st, v_sb, v_st, (int64_t)T_R * yst, yst, o_sb, o_st,
-                              g_sb, fa, ws + L.scan, L.part - L.scan, psi_rows, st);
+                              g_sb, fa, ws + L.scan, L.part - L.scan, psi_rows, nullptr, 0,
+                              pool_from_prepass ? 2 : 3, st);
 }

@@ -554,18 +554,44 @@ int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb,
   return SMAT_EINVAL;
 }
 
+// F[b] = sum of the group sums G[b][g], g < ng0 (the tokens [0, n)), in
+// group order; float4 e of the r*p floats per thread.
+__global__ __launch_bounds__(256) void group_sum_kernel(const float* __restrict__ G,
+                                                        float* __restrict__ F, int ng0,
+                                                        int64_t rp4, int64_t g_sb,
+                                                        int64_t f_sb) {
+  const int64_t b = blockIdx.y;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= rp4) return;
+  const float4* Gb = reinterpret_cast<const float4*>(G + b * g_sb) + e;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int g = 0; g < ng0; ++g) {
+    const float4 x = Gb[(int64_t)g * rp4];
+    acc.x += x.x;
+    acc.y += x.y;
+    acc.z += x.z;
+    acc.w += x.w;
+  }
+  reinterpret_cast<float4*>(F + b * f_sb)[e] = acc;
+}
+
 // The streaming causal pass with the feature map computed inside the kernels:
 // q, k, v are the Q, K, V rows (r = d_qk = d_v = 128); the prepass Gram sums
 // and the scan form Psi (and Phi) tiles in LDS from the DMA'd K (and Q) rows,
 // and Vb = [V, 1] from V.  Same workspace as causal_scan_dispatch.  With
 // psi_buf (nb x T rows of 128, 16-bit) the prepass also stores the Psi tiles
-// it forms there and the scan reads them, forming only Phi.
+// it forms there and the scan reads them, forming only Phi.  phases: 1 the
+// prepass (and, with F_out, F_out[b] = the sum over the tokens [0, n) of
+// Psi^T Vb, from its group sums: one profile's pool), 2 the segment scan and
+// the streaming scan, 3 both; a call of phase 2 follows one of phase 1 with
+// the same workspace.
 int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v, const float* Y,
                          const float* gate, float* out, int nb, int T, int n, int C,
                          int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
                          int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
                          int64_t g_sb, const FeatArgs& fa, void* ws, int64_t ws_bytes,
-                         void* psi_buf, hipStream_t stream) {
+                         void* psi_buf, float* F_out, int64_t f_sb, int phases,
+                         hipStream_t stream) {
   if (nb == 0 || T == 0) return SMAT_OK;
   constexpr int r = 128, p = 129;
   const int64_t rp = (int64_t)r * p;
@@ -594,9 +620,21 @@ int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v,
   FeatArgs fp = fa;
   fp.psi_out = psi_buf;
   fp.psi_sb = (int64_t)T * 128;
-  int rc = gram_stream_launch_feat(dtype, k, v, G, nullptr, it, ng, nb, k_sb, k_st, v_sb, v_st,
-                                   (int64_t)ng * rp, rp, 0, fp, stream, "smat_forward_fused");
-  if (rc) return rc;
+  int rc = SMAT_OK;
+  if (phases & 1) {
+    rc = gram_stream_launch_feat(dtype, k, v, G, nullptr, it, ng, nb, k_sb, k_st, v_sb, v_st,
+                                 (int64_t)ng * rp, rp, 0, fp, stream, "smat_forward_fused");
+    if (rc) return rc;
+    if (F_out) {
+      const int64_t rp4 = rp / 4;
+      smat::launch(group_sum_kernel, dim3((unsigned)((rp4 + 255) / 256), (unsigned)nb),
+                   dim3(256), 0, stream, (const float*)G, F_out, it.ng0, rp4,
+                   (int64_t)ng * rp, f_sb);
+      rc = launch_status("smat_forward_fused");
+      if (rc) return rc;
+    }
+  }
+  if (!(phases & 2)) return SMAT_OK;
   rc = segment_scan_dispatch(G, Sg, nb, ng, it.ng0, rp, stream);
   if (rc) return rc;
   ScanArgs a{};

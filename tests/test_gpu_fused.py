@@ -164,6 +164,22 @@ def test_fused_forward_long_prefill_T524288():
     assert torch.isfinite(fused).all() and e < 1e-5
 
 
+@pytest.mark.parametrize("T,nb,gates", [(4096, 2, False), (8192, 3, True), (131072, 8, False)])
+def test_fused_forward_d1_pools_from_the_causal_pass(T, nb, gates):
+    """d = 1 (one profile holding every landmark token, the identity incidence):
+    the fused forward takes the profile's pool from the causal pass's group
+    sums over the tokens [0, n) instead of a pool pass; against featurise +
+    smat_attention (1e-5 of the largest entry; the pool sums in another order)."""
+    spec = build_mask(T, 1, chunk=128)
+    assert (spec.N0, spec.B, spec.n_P) == (1, 1, 0)
+    _say(f"fused forward d=1 T={T} nb={nb} gates={gates}")
+    Q, K, V, h, g = _inputs(nb, T, seed=11, gates=gates)
+    fused, unfused = _run_both(spec, Q, K, V, h, g)
+    e = _rel(fused, unfused)
+    _say(f"  vs featurise + smat_attention: {e:.2e}")
+    assert torch.isfinite(fused).all() and e < 1e-5
+
+
 def test_fused_forward_falls_back_outside_its_shape_and_under_grad():
     """head_dim 64 (the d=2 single-GPU configuration's width) is not a fused
     shape: smat_attention_fused runs featurise then smat_attention, bitwise the
@@ -178,12 +194,13 @@ def test_fused_forward_falls_back_outside_its_shape_and_under_grad():
     a = A.smat_attention_fused(Q, K, V, phi, spec)
     b = A.smat_attention(*A.featurise(Q, K, V, phi), spec)
     assert torch.equal(a, b)
-    # d = 1: one profile a sequence, the unfused pool's split-K path
-    spec1 = build_mask(4096, 1, chunk=128)
-    Q1, K1, V1, _, _ = _inputs(2, 4096, seed=3)
+    # d = 2 with a global channel and few (sequence, profile) items: the
+    # unfused pool's split-K path
+    spec1 = build_mask(2048, 2, chunk=128, n_P=16)
+    Q1, K1, V1, _, _ = _inputs(1, 2048, seed=3)
     Q1, K1, V1 = Q1.to(DEV), K1.to(DEV), V1.to(DEV)
     phi1 = A.FeatureMap(O.phi_weight(128, 128, dtype=BF, seed=0).to(DEV), "elu1")
-    assert not A._fused_ok(Q1, K1, V1, phi1, spec1, 128, None)
+    assert spec1.N0 < 256 and not A._fused_ok(Q1, K1, V1, phi1, spec1, 128, None)
     assert torch.equal(A.smat_attention_fused(Q1, K1, V1, phi1, spec1),
                        A.smat_attention(*A.featurise(Q1, K1, V1, phi1), spec1))
     Q2, K2, V2, _, _ = _inputs(2, T, seed=9)
