@@ -91,7 +91,8 @@ int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void
                          int C, int r, int p, int64_t q_sb, int64_t q_st, int64_t k_sb,
                          int64_t k_st, int64_t v_sb, int64_t v_st, int64_t y_sb, int64_t y_st,
                          int64_t o_sb, int64_t o_st, int64_t g_sb, int write_H, void* ws,
-                         int64_t ws_bytes, hipStream_t stream);
+                         int64_t ws_bytes, hipStream_t stream, float* F_out = nullptr,
+                         int64_t f_sb = 0, int phases = 3);
 
 // Workspace carve-up, each region 256-byte aligned.  The fused causal pass
 // (chunk <= 128, no H requested) needs only its group states; the staged one
@@ -238,6 +239,12 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
   const int64_t yst = y_stride(p);
   int rc;
 
+  // One profile holding every landmark token (d = 1, no global channel, the
+  // identity incidence): its pool is the sum of the causal pass's group sums
+  // over the tokens [0, n), so the causal pass's summaries run first and no
+  // pool pass is made.
+  const bool pool_from_prepass = L.fused && T_R > 0 && !idx && N0 == 1 && n_P == 0 && n > 0;
+
   // ---- long range: S^T, then C, then R ---------------------------------
   if (T_R > 0) {
     // With no profiled landmark columns (n == n_P) every U_h is the global
@@ -248,8 +255,13 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     const int64_t ld = idx && plane_code && profiled ? incidence_plane_ld(q, N0, B, rp) : rp;
     {
       StageScope stage(0);
-      rc = pool_dispatch(dtype, psi, vb, F, Fg, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st,
-                         part, part_bytes, st, ld);
+      if (pool_from_prepass)
+        rc = causal_scan_dispatch(dtype, phi, psi, vb, nullptr, g, out, nb, T, n, C, r, p, q_sb,
+                                  q_st, k_sb, k_st, v_sb, v_st, (int64_t)T_R * yst, yst, o_sb,
+                                  o_st, g_sb, 0, ws + L.scan, L.part - L.scan, st, F, ld, 1);
+      else
+        rc = pool_dispatch(dtype, psi, vb, F, Fg, nb, n_P, n, N0, r, p, k_sb, k_st, v_sb, v_st,
+                           part, part_bytes, st, ld);
     }
     if (rc) return rc;
     const float* Uq = U;
@@ -278,7 +290,8 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
     // one kernel: segmented scan, + Y on recent rows, normalise, gate
     return causal_scan_dispatch(dtype, phi, psi, vb, T_R > 0 ? Y : nullptr, g, out, nb, T, n, C,
                                 r, p, q_sb, q_st, k_sb, k_st, v_sb, v_st, (int64_t)T_R * yst, yst,
-                                o_sb, o_st, g_sb, 0, ws + L.scan, L.part - L.scan, st);
+                                o_sb, o_st, g_sb, 0, ws + L.scan, L.part - L.scan, st, nullptr,
+                                0, pool_from_prepass ? 2 : 3);
   }
   // staged: chunk summaries, segmented scan, chunk-local pass into H, normalise
   float* D = (float*)(ws + L.D);

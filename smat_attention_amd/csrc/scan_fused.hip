@@ -468,11 +468,33 @@ static int scan_group_chunks(int nb, int nc) {
   return K;
 }
 
+// F[b] = sum of the group sums G[b][g], g < ng0 (the tokens [0, n)), in
+// group order; float4 e of the r*p floats per thread.
+__global__ __launch_bounds__(256) void group_sum_kernel(const float* __restrict__ G,
+                                                        float* __restrict__ F, int ng0,
+                                                        int64_t rp4, int64_t g_sb,
+                                                        int64_t f_sb) {
+  const int64_t b = blockIdx.y;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= rp4) return;
+  const float4* Gb = reinterpret_cast<const float4*>(G + b * g_sb) + e;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int g = 0; g < ng0; ++g) {
+    const float4 x = Gb[(int64_t)g * rp4];
+    acc.x += x.x;
+    acc.y += x.y;
+    acc.z += x.z;
+    acc.w += x.w;
+  }
+  reinterpret_cast<float4*>(F + b * f_sb)[e] = acc;
+}
+
 int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb, const float* Y,
                     const float* gate, float* out, int nb, int T, int n, int C, int K, int r,
                     int p, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
                     int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
-                    int64_t g_sb, int write_H, void* ws, hipStream_t stream);
+                    int64_t g_sb, int write_H, void* ws, float* F_out, int64_t f_sb,
+                    int phases, hipStream_t stream);
 
 int64_t causal_scan_workspace_bytes(int nb, int T, int C, int r, int p) {
   const int nc = (T + C - 1) / C;
@@ -486,7 +508,8 @@ int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void
                          int C, int r, int p, int64_t q_sb, int64_t q_st, int64_t k_sb,
                          int64_t k_st, int64_t v_sb, int64_t v_st, int64_t y_sb, int64_t y_st,
                          int64_t o_sb, int64_t o_st, int64_t g_sb, int write_H, void* ws,
-                         int64_t ws_bytes, hipStream_t stream) {
+                         int64_t ws_bytes, hipStream_t stream, float* F_out, int64_t f_sb,
+                         int phases) {
   if (nb == 0 || T == 0) return SMAT_OK;
   const int nc = (T + C - 1) / C;
   const int K = scan_group_chunks(nb, nc);
@@ -498,7 +521,7 @@ int causal_scan_dispatch(int dtype, const void* phi, const void* psi, const void
   }
   return causal_scan_run(dtype, phi, psi, vb, Y, gate, out, nb, T, n, C, K, r, p, q_sb, q_st,
                          k_sb, k_st, v_sb, v_st, y_sb, y_st, o_sb, o_st, g_sb, write_H, ws,
-                         stream);
+                         F_out, f_sb, phases, stream);
 }
 
 // The causal pass with groups of K chunks; ws holds 2 * al256(nb * ng * r * p
@@ -507,15 +530,34 @@ int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb,
                     const float* gate, float* out, int nb, int T, int n, int C, int K, int r,
                     int p, int64_t q_sb, int64_t q_st, int64_t k_sb, int64_t k_st, int64_t v_sb,
                     int64_t v_st, int64_t y_sb, int64_t y_st, int64_t o_sb, int64_t o_st,
-                    int64_t g_sb, int write_H, void* ws, hipStream_t stream) {
+                    int64_t g_sb, int write_H, void* ws, float* F_out, int64_t f_sb,
+                    int phases, hipStream_t stream) {
   const int nc = (T + C - 1) / C;
   const int ng_max = (nc + K - 1) / K + 1;
   float* G = (float*)ws;
   float* Sg = (float*)((char*)ws + (((int64_t)nb * ng_max * r * p * 4 + 255) & ~(int64_t)255));
-  int ng = 0, ng0 = 0;
-  int rc = chunk_states_dispatch(dtype, psi, vb, G, nb, T, C, K, n, r, p, k_sb, k_st, v_sb, v_st,
-                                 nullptr, 0, stream, &ng, &ng0);
-  if (rc) return rc;
+  // the group layout chunk_states_dispatch uses: groups of K chunks over
+  // [0, n), then over [n, T)
+  const int ng0 = (n / C + K - 1) / K;
+  const int ng = ng0 + (nc - n / C + K - 1) / K;
+  const int64_t rp = (int64_t)r * p;
+  int rc = SMAT_OK;
+  if (phases & 1) {
+    int ng_d = 0, ng0_d = 0;
+    rc = chunk_states_dispatch(dtype, psi, vb, G, nb, T, C, K, n, r, p, k_sb, k_st, v_sb, v_st,
+                               nullptr, 0, stream, &ng_d, &ng0_d);
+    if (rc) return rc;
+    SMAT_REQUIRE(ng_d == ng && ng0_d == ng0, SMAT_EINVAL,
+                 "smat_causal_scan: group layout %d/%d, expected %d/%d", ng_d, ng0_d, ng, ng0);
+    if (F_out) {
+      smat::launch(group_sum_kernel, dim3((unsigned)((rp / 4 + 255) / 256), (unsigned)nb),
+                   dim3(256), 0, stream, (const float*)G, F_out, ng0, rp / 4, (int64_t)ng * rp,
+                   f_sb);
+      rc = launch_status("smat_forward");
+      if (rc) return rc;
+    }
+  }
+  if (!(phases & 2)) return SMAT_OK;
   rc = segment_scan_dispatch(G, Sg, nb, ng, ng0, (int64_t)r * p, stream);
   if (rc) return rc;
   ScanArgs a{};
@@ -552,27 +594,6 @@ int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb,
   }
   set_error("smat_causal_scan: unknown dtype %d", dtype);
   return SMAT_EINVAL;
-}
-
-// F[b] = sum of the group sums G[b][g], g < ng0 (the tokens [0, n)), in
-// group order; float4 e of the r*p floats per thread.
-__global__ __launch_bounds__(256) void group_sum_kernel(const float* __restrict__ G,
-                                                        float* __restrict__ F, int ng0,
-                                                        int64_t rp4, int64_t g_sb,
-                                                        int64_t f_sb) {
-  const int64_t b = blockIdx.y;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= rp4) return;
-  const float4* Gb = reinterpret_cast<const float4*>(G + b * g_sb) + e;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int g = 0; g < ng0; ++g) {
-    const float4 x = Gb[(int64_t)g * rp4];
-    acc.x += x.x;
-    acc.y += x.y;
-    acc.z += x.z;
-    acc.w += x.w;
-  }
-  reinterpret_cast<float4*>(F + b * f_sb)[e] = acc;
 }
 
 // The streaming causal pass with the feature map computed inside the kernels:
@@ -762,7 +783,7 @@ extern "C" int smat_causal_scan_noalloc(int dtype, const void* phi, const void* 
   if (rc) return rc;
   return causal_scan_run(dtype, phi, psi, vb, Y, gate, out, nb, T, n, C, K, r, p, q_sb, q_st,
                          k_sb, k_st, v_sb, v_st, y_sb, y_st, o_sb, o_st, g_sb, write_H, ws,
-                         (hipStream_t)stream);
+                         nullptr, 0, 3, (hipStream_t)stream);
 }
 
 extern "C" int64_t smat_causal_scan_workspace_bytes(int nb, int T, int C, int r, int p) {
@@ -793,5 +814,5 @@ extern "C" int smat_causal_scan(int dtype, const void* phi, const void* psi, con
                "smat_causal_scan: workspace must be 256-byte aligned");
   return causal_scan_dispatch(dtype, phi, psi, vb, Y, gate, out, nb, T, n, C, r, p, q_sb, q_st,
                               k_sb, k_st, v_sb, v_st, y_sb, y_st, o_sb, o_st, g_sb, write_H,
-                              workspace, workspace_bytes, (hipStream_t)stream);
+                              workspace, workspace_bytes, (hipStream_t)stream, nullptr, 0, 3);
 }

@@ -560,8 +560,8 @@ def test_forward_long_prefill_d3_bf16_T524288():
 @pytest.mark.parametrize("T,heads", [(32768, 2), (131072, 1)])
 def test_forward_dense_control_d1_bf16(T, heads):
     """The d = 1 control of the long prefill (B=1, H=8, head_dim=128, bf16, k
-    scaled 1/sqrt(128)): M^(1) = L_T, one profile (N0 = 1: the split-K pool)
-    and one row type (the query reads one U for all T/2 recent rows).  The
+    scaled 1/sqrt(128)): M^(1) = L_T, one profile (N0 = 1: its pool is the
+    sum of the causal pass's group summaries over [0, n)) and one row type (the query reads one U for all T/2 recent rows).  The
     first heads against the oracle; all heads against the plain causal linear
     attention on the GPU (one unbroken scan, no pool, incidence or query)."""
     _say(f"forward T={T} d=1 nb=8 hd=128 bf16")
