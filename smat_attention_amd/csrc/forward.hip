@@ -243,7 +243,9 @@ extern "C" int smat_forward(int dtype, const void* phi, const void* psi, const v
   // identity incidence): its pool is the sum of the causal pass's group sums
   // over the tokens [0, n), so the causal pass's summaries run first and no
   // pool pass is made.
-  const bool pool_from_prepass = L.fused && T_R > 0 && !idx && N0 == 1 && n_P == 0 && n > 0;
+  // (the group sums are added as float4, so r*p is a multiple of 4)
+  const bool pool_from_prepass =
+      L.fused && T_R > 0 && !idx && N0 == 1 && n_P == 0 && n > 0 && rp % 4 == 0;
 
   // ---- long range: S^T, then C, then R ---------------------------------
   if (T_R > 0) {

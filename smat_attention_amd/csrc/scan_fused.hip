@@ -468,25 +468,43 @@ static int scan_group_chunks(int nb, int nc) {
   return K;
 }
 
-// F[b] = sum of the group sums G[b][g], g < ng0 (the tokens [0, n)), in
-// group order; float4 e of the r*p floats per thread.
+// F[b] = sum of the group sums G[b][g], g < ng0 (the tokens [0, n)).  A
+// block takes 64 float4 columns of the r*p floats; its four waves sum every
+// fourth group (each wave's loads independent of one another), then wave 0
+// adds the other three partial sums in wave order.
 __global__ __launch_bounds__(256) void group_sum_kernel(const float* __restrict__ G,
                                                         float* __restrict__ F, int ng0,
                                                         int64_t rp4, int64_t g_sb,
                                                         int64_t f_sb) {
+  __shared__ float4 part[3][64];
   const int64_t b = blockIdx.y;
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= rp4) return;
-  const float4* Gb = reinterpret_cast<const float4*>(G + b * g_sb) + e;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t e = (int64_t)blockIdx.x * 64 + lane;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int g = 0; g < ng0; ++g) {
-    const float4 x = Gb[(int64_t)g * rp4];
-    acc.x += x.x;
-    acc.y += x.y;
-    acc.z += x.z;
-    acc.w += x.w;
+  if (e < rp4) {
+    const float4* Gb = reinterpret_cast<const float4*>(G + b * g_sb) + e;
+#pragma unroll 4
+    for (int g = w; g < ng0; g += 4) {
+      const float4 x = Gb[(int64_t)g * rp4];
+      acc.x += x.x;
+      acc.y += x.y;
+      acc.z += x.z;
+      acc.w += x.w;
+    }
   }
-  reinterpret_cast<float4*>(F + b * f_sb)[e] = acc;
+  if (w > 0) part[w - 1][lane] = acc;
+  __syncthreads();
+  if (w == 0 && e < rp4) {
+    for (int k = 0; k < 3; ++k) {
+      const float4 x = part[k][lane];
+      acc.x += x.x;
+      acc.y += x.y;
+      acc.z += x.z;
+      acc.w += x.w;
+    }
+    reinterpret_cast<float4*>(F + b * f_sb)[e] = acc;
+  }
 }
 
 int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb, const float* Y,
@@ -550,7 +568,9 @@ int causal_scan_run(int dtype, const void* phi, const void* psi, const void* vb,
     SMAT_REQUIRE(ng_d == ng && ng0_d == ng0, SMAT_EINVAL,
                  "smat_causal_scan: group layout %d/%d, expected %d/%d", ng_d, ng0_d, ng, ng0);
     if (F_out) {
-      smat::launch(group_sum_kernel, dim3((unsigned)((rp / 4 + 255) / 256), (unsigned)nb),
+      SMAT_REQUIRE(rp % 4 == 0 && f_sb % 4 == 0, SMAT_EINVAL,
+                   "smat_forward: group sums need r*p and the row stride of F a multiple of 4");
+      smat::launch(group_sum_kernel, dim3((unsigned)((rp / 4 + 63) / 64), (unsigned)nb),
                    dim3(256), 0, stream, (const float*)G, F_out, ng0, rp / 4, (int64_t)ng * rp,
                    f_sb);
       rc = launch_status("smat_forward");
@@ -648,7 +668,7 @@ int causal_scan_run_feat(int dtype, const void* q, const void* k, const void* v,
     if (rc) return rc;
     if (F_out) {
       const int64_t rp4 = rp / 4;
-      smat::launch(group_sum_kernel, dim3((unsigned)((rp4 + 255) / 256), (unsigned)nb),
+      smat::launch(group_sum_kernel, dim3((unsigned)((rp4 + 63) / 64), (unsigned)nb),
                    dim3(256), 0, stream, (const float*)G, F_out, it.ng0, rp4,
                    (int64_t)ng * rp, f_sb);
       rc = launch_status("smat_forward_fused");
